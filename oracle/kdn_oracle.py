@@ -1,0 +1,421 @@
+"""CPU restatement of the Kalman Delta Network recurrences (TEST INFRASTRUCTURE ONLY).
+
+This module is the parity checker for the HIP implementation in
+``kalman-delta-networks_amd``.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it; the product path never does.
+
+Everything here is plain PyTorch on the CPU, computed in fp64 when any input is
+fp64 and in fp32 otherwise, and differentiable with torch autograd (the HIP
+backward is checked against autograd of these functions).
+
+What each function restates (reference = ngocbh/kalman-delta-networks):
+
+* ``iso_gain_tokenwise``     -- lit_gpt/kdn_ops/iso_kdn_naive.py:200-251
+* ``diag_gain_tokenwise``    -- lit_gpt/kdn_ops/diag_kdn_naive.py:217-276
+* ``memory_tokenwise``       -- iso_kdn_naive.py:308-332, diag_kdn_naive.py:479-500
+* ``iso_recurrent``          -- iso_kdn_naive.py:376-440
+* ``diag_recurrent``         -- diag_kdn_naive.py:503-567
+* ``iso_gain_mobius`` / ``diag_gain_mobius`` -- the Mobius chunk forms of
+  iso_kdn_naive.py:590-634 and diag_kdn_naive.py:285-369 (second, independent form)
+* ``memory_chunked_wy``      -- the WY chunk form of iso_kdn_naive.py:449-533 and
+  diag_kdn_naive.py:570-655 (second, independent form)
+* ``iso_gate_frontend``      -- iso_kdn_chunk.py:787-813 (gate/a/omega/r/mu maps)
+* ``diag_frontend``          -- diag_kdn_chunk.py:1885-1905 (alpha clamp, omega, r, mu)
+* ``diag_normalize``         -- diag_kdn_chunk.py:194-232 (x / max(||x||, 1e-12))
+* ``l2norm_fla``             -- FLA l2norm_fwd used at iso_kdn_chunk.py:2203-2204
+  (flash-linear-attention @ 4b02d15d; x * rsqrt(sum x^2 + 1e-6)).  FLA is not
+  vendored in the reference, so this convention is PARITY UNPINNED.
+* ``iso_mixer`` / ``diag_mixer`` -- the composition order of iso_kdn.py:277-304 and
+  diag_kdn.py:315-345 (frontend -> gain -> memory scan).
+
+How each is pinned (see tests/test_oracle_*.py):
+  golden vectors written from the reference's own oracle files
+  (tests/golden/make_golden.py); tokenwise vs Mobius/WY chunk forms (independent
+  decompositions); closed forms (T=1, alpha=1 plain delta rule, kappa=0 pure decay,
+  scalar Kalman filter for K=1); gradcheck in fp64.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+LOG2E = 1.4426950408889634
+
+
+def _dtype(*xs) -> torch.dtype:
+    return torch.float64 if any(isinstance(x, torch.Tensor) and x.dtype == torch.float64 for x in xs) else torch.float32
+
+
+def _bcast_precision_iso(p, B: int, H: int, dtype) -> torch.Tensor:
+    if not isinstance(p, torch.Tensor):
+        return torch.full((B, H), float(p), dtype=dtype)
+    p = p.to(dtype)
+    if p.ndim == 0:
+        return p.expand(B, H)
+    if p.shape == (H,):
+        return p.view(1, H).expand(B, H)
+    if p.shape == (B, H):
+        return p
+    raise ValueError(f"initial_precision must be scalar, [H] or [B,H]; got {tuple(p.shape)}")
+
+
+def _bcast_precision_diag(p, B: int, H: int, K: int, dtype) -> torch.Tensor:
+    if not isinstance(p, torch.Tensor):
+        return torch.full((B, H, K), float(p), dtype=dtype)
+    p = p.to(dtype)
+    if p.ndim == 0:
+        return p.expand(B, H, K)
+    if p.shape == (H,):
+        return p.view(1, H, 1).expand(B, H, K)
+    if p.shape == (B, H):
+        return p.view(B, H, 1).expand(B, H, K)
+    if p.shape == (B, H, K):
+        return p
+    raise ValueError(f"initial_precision must be scalar, [H], [B,H] or [B,H,K]; got {tuple(p.shape)}")
+
+
+def _info_scale(s, H: int, K: int, dtype) -> torch.Tensor:
+    if s is None:
+        return torch.full((H,), float(K), dtype=dtype)
+    if isinstance(s, torch.Tensor):
+        return s.to(dtype).expand(H) if s.ndim == 0 else s.to(dtype)
+    return torch.full((H,), float(s), dtype=dtype)
+
+
+# ----------------------------------------------------------------------------
+# Uncertainty (gain) recurrences, tokenwise.
+# ----------------------------------------------------------------------------
+
+def iso_gain_tokenwise(k, alpha, omega, r, *, info_scale=None, initial_precision=1.0,
+                       output_final_state=False):
+    """Scalar-precision Kalman gain, one token at a time (iso_kdn_naive.py:200-251).
+
+    a_t = mean_i alpha_ti^2; z_t = a_t / c_{t-1} + omega_t;
+    beta_t = z_t / (r_t + z_t |k_t|^2); c_t = 1/z_t + s |k_t|^2 / (K r_t).
+    """
+    dt = _dtype(k, alpha, omega, r, initial_precision, info_scale)
+    B, T, H, K = k.shape
+    k, alpha, omega, r = (x.to(dt) for x in (k, alpha, omega, r))
+    c = _bcast_precision_iso(initial_precision, B, H, dt)
+    s = _info_scale(info_scale, H, K, dt).view(1, H) / K
+    contraction = alpha.square().mean(-1)
+    knorm2 = k.square().sum(-1)
+    betas = []
+    for t in range(T):
+        z = contraction[:, t] / c + omega[:, t]
+        betas.append(z / (r[:, t] + z * knorm2[:, t]))
+        c = 1.0 / z + s * knorm2[:, t] / r[:, t]
+    beta = torch.stack(betas, 1) if T else k.sum(-1) * 0
+    return beta, (c if output_final_state else None)
+
+
+def diag_gain_tokenwise(k, alpha, omega, r, *, info_scale=None, initial_precision=1.0,
+                        output_final_state=False):
+    """Per-channel covariance Kalman gain (diag_kdn_naive.py:217-276).
+
+    p_hat = alpha^2 p + omega; kappa = p_hat k / (r + sum_i p_hat_i k_i^2);
+    p = p_hat / (1 + s k^2 / r * p_hat)   (no division by K here).
+    """
+    dt = _dtype(k, alpha, omega, r, initial_precision, info_scale)
+    B, T, H, K = k.shape
+    k, alpha, omega, r = (x.to(dt) for x in (k, alpha, omega, r))
+    p = 1.0 / _bcast_precision_diag(initial_precision, B, H, K, dt)
+    s = _info_scale(info_scale, H, K, dt).view(1, H, 1)
+    gains = []
+    for t in range(T):
+        ph = alpha[:, t].square() * p + omega[:, t]
+        kt = k[:, t]
+        den = r[:, t, :, None] + (ph * kt.square()).sum(-1, keepdim=True)
+        gains.append(ph * kt / den)
+        p = ph / (1.0 + s * kt.square() / r[:, t, :, None] * ph)
+    kappa = torch.stack(gains, 1) if T else k * 0
+    return kappa, ((1.0 / p) if output_final_state else None)
+
+
+# ----------------------------------------------------------------------------
+# Uncertainty recurrences as chunked Mobius-map compositions (second form).
+# ----------------------------------------------------------------------------
+
+def _mobius(m, p):
+    return (m[..., 0, 0] * p + m[..., 0, 1]) / (m[..., 1, 0] * p + m[..., 1, 1])
+
+
+def iso_gain_mobius(k, alpha, omega, r, *, info_scale=None, initial_precision=1.0,
+                    chunk_size=64, output_final_state=False):
+    """Covariance p = 1/c advanced by 2x2 projective maps composed per chunk.
+
+    Token map acting on p: p' = (r a p + r w) / (s' a p + r + s' w) with
+    s' = s |k|^2 / K, i.e. [[r a, r w], [s' a, r + s' w]] (iso_kdn_naive.py:608-632).
+    """
+    dt = _dtype(k, alpha, omega, r, initial_precision, info_scale)
+    B, T, H, K = k.shape
+    k, alpha, omega, r = (x.to(dt) for x in (k, alpha, omega, r))
+    p0 = 1.0 / _bcast_precision_iso(initial_precision, B, H, dt)
+    s = _info_scale(info_scale, H, K, dt).view(1, H) / K
+    a = alpha.square().mean(-1)
+    n2 = k.square().sum(-1)
+    out = []
+    for c0 in range(0, T, chunk_size):
+        m = torch.eye(2, dtype=dt).expand(B, H, 2, 2)
+        for t in range(c0, min(T, c0 + chunk_size)):
+            p = _mobius(m, p0)
+            z = a[:, t] * p + omega[:, t]
+            out.append(z / (r[:, t] + z * n2[:, t]))
+            sw = s * n2[:, t]
+            tm = torch.stack((torch.stack((r[:, t] * a[:, t], r[:, t] * omega[:, t]), -1),
+                              torch.stack((sw * a[:, t], r[:, t] + sw * omega[:, t]), -1)), -2)
+            m = tm @ m
+            m = m / m.abs().amax((-2, -1), keepdim=True)
+        p0 = _mobius(m, p0)
+    beta = torch.stack(out, 1) if T else k.sum(-1) * 0
+    return beta, ((1.0 / p0) if output_final_state else None)
+
+
+def diag_gain_mobius(k, alpha, omega, r, *, info_scale=None, initial_precision=1.0,
+                     chunk_size=32, output_final_state=False):
+    """Per-channel map [[a^2, w], [u a^2, 1 + u w]], u = s k^2 / r (diag_kdn_naive.py:338-360)."""
+    dt = _dtype(k, alpha, omega, r, initial_precision, info_scale)
+    B, T, H, K = k.shape
+    k, alpha, omega, r = (x.to(dt) for x in (k, alpha, omega, r))
+    p0 = 1.0 / _bcast_precision_diag(initial_precision, B, H, K, dt)
+    s = _info_scale(info_scale, H, K, dt).view(1, H, 1)
+    out = []
+    for c0 in range(0, T, chunk_size):
+        m = torch.eye(2, dtype=dt).expand(B, H, K, 2, 2)
+        for t in range(c0, min(T, c0 + chunk_size)):
+            p = _mobius(m, p0)
+            a2 = alpha[:, t].square()
+            ph = a2 * p + omega[:, t]
+            kt = k[:, t]
+            den = r[:, t, :, None] + (ph * kt.square()).sum(-1, keepdim=True)
+            out.append(ph * kt / den)
+            u = s * kt.square() / r[:, t, :, None]
+            tm = torch.stack((torch.stack((a2, omega[:, t]), -1),
+                              torch.stack((u * a2, 1.0 + u * omega[:, t]), -1)), -2)
+            m = tm @ m
+            m = m / m.abs().amax((-2, -1), keepdim=True)
+        p0 = _mobius(m, p0)
+    kappa = torch.stack(out, 1) if T else k * 0
+    return kappa, ((1.0 / p0) if output_final_state else None)
+
+
+# ----------------------------------------------------------------------------
+# Memory recurrence (shared by both variants; kappa = beta k for iso).
+# ----------------------------------------------------------------------------
+
+def memory_tokenwise(q, k, v, alpha, kappa, *, scale, initial_state=None):
+    """S_hat = alpha (.) S; delta = v - k^T S_hat; S = S_hat + kappa delta^T; o = scale q^T S.
+
+    (iso_kdn_naive.py:308-332, diag_kdn_naive.py:479-500.)  Shapes: q,k,alpha,kappa
+    [B,T,H,K], v [B,T,H,V]; returns o [B,T,H,V] and S [B,H,K,V].
+    """
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    S = torch.zeros(B, H, K, V, dtype=q.dtype) if initial_state is None else initial_state.to(q.dtype)
+    outs = []
+    for t in range(T):
+        Sh = alpha[:, t, :, :, None] * S
+        delta = v[:, t] - torch.einsum("bhk,bhkv->bhv", k[:, t], Sh)
+        S = Sh + kappa[:, t, :, :, None] * delta[:, :, None, :]
+        outs.append(scale * torch.einsum("bhk,bhkv->bhv", q[:, t], S))
+    o = torch.stack(outs, 1) if T else v * 0
+    return o, S
+
+
+def memory_chunked_wy(q, k, v, alpha, kappa, *, scale, initial_state=None, chunk_size=64):
+    """Chunked WY form of the same recurrence (second, independent decomposition).
+
+    Within a chunk with G = cumsum(log alpha):
+      N[c,s] = sum_i k_ci exp(G_ci - G_si) kappa_si (s < c);  A = (I + N)^-1
+      U = A V, W = A (K e^G), D = U - W S
+      O = scale (Q e^G) S + scale tril(Q Gamma kappa^T) D
+      S' = e^{G_last} S + (e^{G_last - G} kappa)^T D
+    (iso_kdn_naive.py:449-533, diag_kdn_naive.py:570-655.)
+    """
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    S = torch.zeros(B, H, K, V, dtype=q.dtype) if initial_state is None else initial_state.to(q.dtype)
+    outs = []
+    for c0 in range(0, T, chunk_size):
+        c1 = min(T, c0 + chunk_size)
+        L = c1 - c0
+        qc = q[:, c0:c1].transpose(1, 2)
+        kc = k[:, c0:c1].transpose(1, 2)
+        vc = v[:, c0:c1].transpose(1, 2)
+        kap = kappa[:, c0:c1].transpose(1, 2)
+        G = alpha[:, c0:c1].log().transpose(1, 2).cumsum(2)
+        diff = G[:, :, :, None, :] - G[:, :, None, :, :]            # [B,H,c,s,K]
+        low = torch.tril(torch.ones(L, L, dtype=torch.bool), -1)
+        lowd = torch.tril(torch.ones(L, L, dtype=torch.bool), 0)
+        E = torch.where(lowd[:, :, None], diff, torch.zeros((), dtype=q.dtype)).exp()
+        N = torch.einsum("bhck,bhcsk,bhsk->bhcs", kc, E, kap) * low
+        Mq = torch.einsum("bhck,bhcsk,bhsk->bhcs", qc, E, kap) * lowd
+        I = torch.eye(L, dtype=q.dtype)
+        U = torch.linalg.solve_triangular(I + N, vc, upper=False, unitriangular=True)
+        W = torch.linalg.solve_triangular(I + N, kc * G.exp(), upper=False, unitriangular=True)
+        D = U - W @ S
+        outs.append((scale * ((qc * G.exp()) @ S + Mq @ D)).transpose(1, 2))
+        Gl = G[:, :, -1:, :]
+        S = Gl[:, :, 0, :, None].exp() * S + ((Gl - G).exp() * kap).transpose(-1, -2) @ D
+    o = torch.cat(outs, 1) if T else v * 0
+    return o, S
+
+
+def iso_recurrent(q, k, v, alpha, omega, r, *, info_scale=None, scale=None, initial_state=None,
+                  initial_precision=1.0, output_final_state=False, chunked=False, chunk_size=64):
+    """Full iso recurrence (iso_kdn_naive.py:376-440); q,k used exactly as given."""
+    dt = _dtype(q, k, v, alpha, omega, r, initial_state, initial_precision, info_scale)
+    q, k, v, alpha, omega, r = (x.to(dt) for x in (q, k, v, alpha, omega, r))
+    K = q.shape[-1]
+    scale = K ** -0.5 if scale is None else float(scale)
+    gain = iso_gain_mobius if chunked else iso_gain_tokenwise
+    kw = dict(chunk_size=chunk_size) if chunked else {}
+    beta, prec = gain(k, alpha, omega, r, info_scale=info_scale, initial_precision=initial_precision,
+                      output_final_state=True, **kw)
+    mem = memory_chunked_wy if chunked else memory_tokenwise
+    o, S = mem(q, k, v, alpha, beta[..., None] * k, scale=scale, initial_state=initial_state, **kw)
+    return o, ((S, prec) if output_final_state else None)
+
+
+def diag_recurrent(q, k, v, alpha, omega, r, *, info_scale=None, scale=None, initial_state=None,
+                   initial_precision=1.0, output_final_state=False, chunked=False, chunk_size=32):
+    """Full diag recurrence (diag_kdn_naive.py:503-567); q,k used exactly as given."""
+    dt = _dtype(q, k, v, alpha, omega, r, initial_state, initial_precision, info_scale)
+    q, k, v, alpha, omega, r = (x.to(dt) for x in (q, k, v, alpha, omega, r))
+    K = q.shape[-1]
+    scale = K ** -0.5 if scale is None else float(scale)
+    gain = diag_gain_mobius if chunked else diag_gain_tokenwise
+    kw = dict(chunk_size=chunk_size) if chunked else {}
+    kappa, prec = gain(k, alpha, omega, r, info_scale=info_scale, initial_precision=initial_precision,
+                       output_final_state=True, **kw)
+    mem = memory_chunked_wy if chunked else memory_tokenwise
+    o, S = mem(q, k, v, alpha, kappa, scale=scale, initial_state=initial_state, **kw)
+    return o, ((S, prec) if output_final_state else None)
+
+
+# ----------------------------------------------------------------------------
+# Production frontends (elementwise maps restated from the kernel sources).
+# ----------------------------------------------------------------------------
+
+def softplus(x):
+    """torch softplus (threshold 20), the convention used throughout."""
+    return F.softplus(x)
+
+
+def l2norm_fla(x, eps: float = 1e-6):
+    """x * rsqrt(sum x^2 + eps) over the last dim (FLA l2norm_fwd; parity unpinned)."""
+    return x * torch.rsqrt(x.square().sum(-1, keepdim=True) + eps)
+
+
+def diag_normalize(x):
+    """x / max(||x||_2, 1e-12) over the last dim (diag_kdn_chunk.py:194-232)."""
+    return x / x.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+
+
+def chunk_local_prefix(x, chunk: int):
+    """Inclusive cumulative sum over time that restarts every ``chunk`` tokens ([B,T,...])."""
+    T = x.shape[1]
+    parts = [x[:, c0:c0 + chunk].cumsum(1) for c0 in range(0, T, chunk)]
+    return torch.cat(parts, 1) if parts else x
+
+
+def iso_gate_frontend(g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu_param,
+                      omega_min=0.0, r_min=0.01, chunk=64):
+    """iso_kdn_chunk.py:787-813.
+
+    g = -exp(A_log) softplus(g_raw + dt_bias) (per channel, natural log of alpha);
+    g_cumsum = chunk-local inclusive prefix of g times log2(e);
+    a = mean_K exp(2 g); omega = omega_min + softplus(raw + b); r = r_min + softplus(raw + b);
+    mu = 0.1 + softplus(mu_param).  Returns (g_log, g_cumsum_base2, a, omega, r, mu).
+    """
+    B, T, H, K = g_raw.shape
+    x = g_raw.float() + dt_bias.float().view(H, K)
+    g = -A_log.float().exp().view(H, 1) * softplus(x)
+    gc = chunk_local_prefix(g, chunk) * LOG2E
+    a = (2.0 * g).exp().mean(-1)
+    orr = omega_r_raw.float()
+    omega = omega_min + softplus(orr[..., :H] + omega_bias.float())
+    r = r_min + softplus(orr[..., H:] + r_bias.float())
+    mu = 0.1 + softplus(mu_param.float())
+    return g, gc, a, omega, r, mu
+
+
+def diag_frontend(retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, chunk=32):
+    """diag_kdn_chunk.py:1885-1905.
+
+    alpha = exp(-exp(A_log) softplus(f + dt_bias)); the memory path uses
+    l = log(max(alpha, 1e-6)) and its chunk-local base-2 prefix; omega = softplus(z);
+    r = 0.01 + softplus(y); mu = 0.1 + softplus(mu_param).
+    Returns (l_mem, g_cumsum_base2, alpha, omega, r, mu).
+    """
+    B, T, H, K = retention_raw.shape
+    x = retention_raw.float() + dt_bias.float().view(H, K)
+    ell = -A_log.float().exp().view(H, 1) * softplus(x)
+    alpha = ell.exp()
+    l_mem = alpha.clamp_min(1e-6).log()
+    gc = chunk_local_prefix(l_mem, chunk) * LOG2E
+    omega = softplus(omega_raw.float())
+    r = 0.01 + softplus(r_raw.float())
+    mu = 0.1 + softplus(mu_param.float())
+    return l_mem, gc, alpha, omega, r, mu
+
+
+# ----------------------------------------------------------------------------
+# Composed mixers at the kdn_ops boundary (frontend -> gain -> memory), fp32 CPU.
+# ----------------------------------------------------------------------------
+
+def iso_mixer(q_raw, k_raw, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu_param,
+              *, omega_min=0.0, r_min=0.01, info_scale=None, scale=None, chunked=False):
+    """iso_kdn.py:277-304: gate frontend, scalar gain on unit keys, KDA memory scan.
+
+    The production gain consumes (a, omega, r, mu) only and assumes |k| = 1
+    (iso_kdn_chunk.py:1586-1594); the memory scan L2-normalises q and k inside
+    (iso_kdn_chunk.py:2203-2204) and uses alpha = exp(g) per channel.
+    """
+    K = q_raw.shape[-1]
+    g, _gc, a, omega, r, mu = iso_gate_frontend(g_raw, omega_r_raw, omega_bias, r_bias, A_log,
+                                                dt_bias, mu_param, omega_min, r_min)
+    qn = l2norm_fla(q_raw.float())
+    kn = l2norm_fla(k_raw.float())
+    alpha = g.exp()
+    # Gain on the production scalars: beta = z / (r + z) with unit-norm keys.
+    B, T, H, _ = q_raw.shape
+    s = (float(K) if info_scale is None else float(info_scale)) / K
+    p = (1.0 / mu).view(1, H).expand(B, H)
+    betas = []
+    for t in range(T):
+        z = a[:, t] * p + omega[:, t]
+        betas.append(z / (r[:, t] + z))
+        p = r[:, t] * z / (r[:, t] + s * z)
+    beta = torch.stack(betas, 1)
+    sc = K ** -0.5 if scale is None else scale
+    mem = memory_chunked_wy if chunked else memory_tokenwise
+    o, _ = mem(qn, kn, v.float(), alpha, beta[..., None] * kn, scale=sc)
+    return o
+
+
+def diag_mixer(q_raw, k_raw, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param,
+               *, scale=None, chunked=False, initial_state=None, initial_precision=None,
+               output_final_state=False):
+    """diag_kdn.py:315-345: normalise, frontend, vector gain, memory scan (fp32 output).
+
+    The memory path consumes alpha clamped at 1e-6 (through g_cumsum) while the
+    gain consumes the unclamped alpha (diag_kdn_chunk.py:1887-1898).
+    """
+    K = q_raw.shape[-1]
+    qn = diag_normalize(q_raw.float())
+    kn = diag_normalize(k_raw.float())
+    l_mem, _gc, alpha, omega, r, mu = diag_frontend(retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param)
+    prec = mu if initial_precision is None else initial_precision
+    gain = diag_gain_mobius if chunked else diag_gain_tokenwise
+    kappa, fprec = gain(kn, alpha, omega, r, info_scale=float(K), initial_precision=prec,
+                        output_final_state=True)
+    sc = K ** -0.5 if scale is None else scale
+    mem = memory_chunked_wy if chunked else memory_tokenwise
+    o, S = mem(qn, kn, v.float(), l_mem.exp(), kappa, scale=sc, initial_state=initial_state)
+    if output_final_state:
+        return o, (S, fprec)
+    return o
