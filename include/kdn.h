@@ -1,0 +1,140 @@
+/*
+ * kdn.h -- C ABI of the MI355X (gfx950) Kalman Delta Network scan library (libkdn_hip.so).
+ *
+ * Every entry point takes raw device pointers, plain sizes, and the hipStream_t to launch
+ * on; it allocates nothing (the caller passes outputs and workspaces, sized by the
+ * *_size() queries) and returns 0 on success, KDN_ERR_ARG (-1) on a rejected argument,
+ * or a positive hipError_t value from the launch.  Tensors are dense row-major:
+ *   [B,T,H,D]  token-major with heads interleaved (the reference layout),
+ *   bf16 arguments are raw uint16_t bit patterns.
+ * Dtype flags (*_bf16) select bf16 (1) or fp32 (0) for arguments typed void*.
+ * g_cumsum is the base-2, chunk-local inclusive prefix of the per-channel log-gate; its
+ * chunk length is kdn_mem_chunk_size() (64) for both variants, and it has exactly one
+ * consumer (the memory scan), whose backward returns the gate cotangent in natural-log
+ * coordinates, not reverse-summed (the frontends' backward performs that sum).
+ *
+ * The interface each entry point replaces is cited as reference-file:line
+ * (ngocbh/kalman-delta-networks, lit_gpt/kdn_ops/).
+ */
+#ifndef KDN_H_
+#define KDN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDN_ERR_ARG_VALUE (-1)
+
+/* ---------------------------------------------------------------- iso frontend */
+/* _iso_kdn_gate_precumsum_fwd (iso_kdn_chunk.py:1059-1113, kernel :739-813).
+ * g_raw [B,T,H,K]; omega_r_raw [B,T,2H] with strides (orr_stride_b, orr_stride_t, 1).
+ * Outputs g_cumsum [B,T,H,K] f32, a/omega/r [B,T,H] f32, mu [H] f32. */
+int kdn_iso_gate_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                     int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                     const float* dt_bias, const float* mu_param, float omega_min, float r_min, int B, int T, int H,
+                     int K, int chunk, float* g_cumsum, float* a, float* omega, float* r, float* mu,
+                     hipStream_t stream);
+size_t kdn_iso_gate_bwd_workspace_size(int B, int T, int H, int K, int chunk);
+/* _iso_kdn_gate_precumsum_bwd (iso_kdn_chunk.py:1116-1314, kernel :816-1009).  Any cotangent
+ * may be NULL (zero); any output may be NULL (not computed).  domega_r_raw is [B,T,2H] dense. */
+int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                     int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                     const float* dt_bias, const float* mu_param, const float* dg_pre, const float* da,
+                     const float* domega, const float* dr, const float* dmu, int B, int T, int H, int K, int chunk,
+                     void* dg_raw, void* domega_r_raw, float* dA_log, float* ddt_bias, float* domega_bias,
+                     float* dr_bias, float* dmu_param, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------- iso gain */
+/* _iso_kdn_gain_forward (iso_kdn_chunk.py:1598-1664): beta [B,T,H]; p_prev (nullable) saves
+ * the incoming covariance per token for the backward; final_precision [B,H] (nullable). */
+int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision, int B, int T,
+                     int H, float posterior_scale, float* beta, float* p_prev, float* final_precision,
+                     hipStream_t stream);
+/* _iso_kdn_gain_backward (iso_kdn_chunk.py:1817-1893); d_initial_precision [H] is summed over B
+ * in a fixed order (deterministic). */
+int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const float* initial_precision,
+                     const float* dbeta, const float* p_prev, int B, int T, int H, float posterior_scale, float* da,
+                     float* domega, float* dr, float* d_initial_precision, hipStream_t stream);
+
+/* ---------------------------------------------------------------- row norms */
+/* FLA l2norm_fwd / l2norm_bwd used inside _ChunkKDAPrecumsumFunction (iso_kdn_chunk.py:2203-2204,
+ * 2229-2230): y = x * rsqrt(sum x^2 + eps), rstd [rows]. */
+int kdn_l2norm_fwd(const void* x, int x_bf16, int64_t rows, int K, float eps, void* y, int y_bf16, float* rstd,
+                   hipStream_t stream);
+int kdn_l2norm_bwd(const void* x, int x_bf16, const float* rstd, const void* dy, int dy_bf16, int64_t rows, int K,
+                   void* dx, hipStream_t stream);
+/* _frozen_norm_launch_diag_norm_boundary_forward / _diag_kdn_norm_backward
+ * (diag_kdn_chunk.py:358-368, 2079-2159): y = x / max(||x||, 1e-12); q_memory bf16, k_gain f32,
+ * k_memory bf16, norms f32 [rows].  Backward sums the k_gain and k_memory cotangents. */
+int kdn_diag_norm_fwd(const void* q_raw, const void* k_raw, int x_bf16, int64_t rows, int K, uint16_t* q_memory,
+                      float* k_gain, uint16_t* k_memory, float* q_norm, float* k_norm, hipStream_t stream);
+int kdn_diag_norm_bwd(const void* q_raw, const void* k_raw, int x_bf16, const float* q_norm, const float* k_norm,
+                      const uint16_t* d_q_memory, const float* d_k_gain, const uint16_t* d_k_memory, int64_t rows,
+                      int K, void* dq_raw, void* dk_raw, hipStream_t stream);
+
+/* ---------------------------------------------------------------- diag frontend */
+/* _diag_kdn_frontend_forward (diag_kdn_chunk.py:2218-2262, kernel :1866-1905). */
+int kdn_diag_frontend_fwd(const uint16_t* retention_raw, const uint16_t* omega_raw, const uint16_t* r_raw,
+                          const float* A_log, const float* dt_bias, const float* mu_param, int B, int T, int H, int K,
+                          int chunk, float* g_cumsum, float* alpha, float* omega, float* r, float* mu,
+                          hipStream_t stream);
+size_t kdn_diag_frontend_bwd_workspace_size(int B, int T, int H, int K, int chunk);
+/* _diag_kdn_frontend_backward (diag_kdn_chunk.py:2265-2423, kernels :1907-2016). */
+int kdn_diag_frontend_bwd(const uint16_t* retention_raw, const uint16_t* omega_raw, const uint16_t* r_raw,
+                          const float* A_log, const float* dt_bias, const float* mu_param, const float* alpha,
+                          const float* d_g_cumsum, const float* d_alpha, const float* d_omega, const float* d_r,
+                          const float* d_mu, int B, int T, int H, int K, int chunk, uint16_t* d_retention_raw,
+                          uint16_t* d_omega_raw, uint16_t* d_r_raw, float* dA_log, float* ddt_bias,
+                          float* d_mu_param, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------- diag gain */
+size_t kdn_diag_gain_workspace_size(int B, int T, int H, int K);
+/* _diag_kdn_gain_forward (diag_kdn_chunk.py:2499-2565, kernels :373-494).  initial_precision is
+ * [H] (prec_mode 0) or [B,H,K] (prec_mode 1, state continuation).  p_prev [B,T,H,K] and
+ * D [B,T,H] (nullable) are saved for the backward; final_precision [B,H,K] nullable. */
+int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, const float* r,
+                      const float* initial_precision, int prec_mode, int B, int T, int H, int K, float info_scale,
+                      float* kappa, float* p_prev, float* D, float* final_precision, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+/* _diag_kdn_gain_backward (diag_kdn_chunk.py:2569-2683, kernels :496-700) with the fused
+ * softplus VJPs of omega_raw and r_raw.  G_scratch is [B,T,H] f32.  d_final_precision
+ * (nullable) is the cotangent of final_precision. */
+int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, const float* r,
+                      const float* initial_precision, int prec_mode, const float* dkappa, const float* p_prev,
+                      const float* D, const float* final_precision, const float* d_final_precision,
+                      const uint16_t* omega_raw, const uint16_t* r_raw, int B, int T, int H, int K, float info_scale,
+                      float* dk, float* dalpha, uint16_t* domega_raw, uint16_t* dr_raw, float* d_initial_precision,
+                      float* G_scratch, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------- memory scan */
+int kdn_mem_chunk_size(void);
+size_t kdn_mem_saved_size(int B, int T, int H, int K, int V);
+size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
+/* Forward of the chunked memory scan: replaces _chunk_kda_fwd_precum (iso_kdn_chunk.py:2037-2086,
+ * iso=1, kappa_or_beta = beta [B,T,H]) and _diag_kdn_memory_forward (diag_kdn_chunk.py:3224-3244,
+ * iso=0, kappa_or_beta = kappa [B,T,H,K] f32).  q, k (normalised), v are bf16; o is bf16 or f32.
+ * initial_state / final_state [B,H,K,V] f32 are nullable (state carry; the reference oracle's
+ * initial_memory / output_final_state, iso_kdn_naive.py:376-440).  `saved` receives the
+ * intermediates the backward consumes (kdn_mem_saved_size bytes). */
+int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
+                const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
+                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, hipStream_t stream);
+/* Backward: replaces _chunk_kda_bwd_precum (iso_kdn_chunk.py:2089-2187) and
+ * _DiagKdnMemoryFunction.backward (diag_kdn_chunk.py:3258-3312).  dq, dk, dv bf16; dkappa
+ * [B,T,H,K] f32 (diag) or dbeta [B,T,H] f32 (iso); dg [B,T,H,K] f32 in natural-log coordinates,
+ * not reverse-summed.  d_final_state / d_initial_state nullable. */
+int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const float* g_cumsum,
+                int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
+                const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
+                size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
+                float* dg, float* d_initial_state, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDN_H_ */

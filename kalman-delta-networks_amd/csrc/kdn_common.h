@@ -1,0 +1,58 @@
+// Shared device helpers for the KDN HIP kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define KDN_LN2 0.6931471805599453f
+#define KDN_LOG2E 1.4426950408889634f
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 <-> fp32 ----------------------------------------------------------
+__device__ __forceinline__ float bf2f(bf16_t u) { return __uint_as_float(((uint32_t)u) << 16); }
+__device__ __forceinline__ bf16_t f2bf(float x) {  // round to nearest even, NaN kept quiet
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i);
+template <> __device__ __forceinline__ float ld<float>(const float* p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ld<bf16_t>(const bf16_t* p, int64_t i) { return bf2f(p[i]); }
+template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float x);
+template <> __device__ __forceinline__ void st<float>(float* p, int64_t i, float x) { p[i] = x; }
+template <> __device__ __forceinline__ void st<bf16_t>(bf16_t* p, int64_t i, float x) { p[i] = f2bf(x); }
+
+// ---- activations ---------------------------------------------------------------
+// softplus with torch's default threshold (x > 20 -> x).
+__device__ __forceinline__ float softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+
+// ---- wave64 reductions -----------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Block-wide sum for blockDim.x <= 1024; `scratch` holds >= 16 floats. Result valid in all threads.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += scratch[i];
+  return t;
+}
+
+// Error codes returned by the C ABI besides hipError_t values.
+#define KDN_ERR_ARG (-1)
+#define KDN_CHECK_LAUNCH()                       \
+  do {                                           \
+    hipError_t e_ = hipGetLastError();           \
+    if (e_ != hipSuccess) return (int)e_;        \
+  } while (0)

@@ -1,0 +1,559 @@
+// Elementwise frontends of the KDN scan: iso gate, diag retention/noise frontend,
+// q/k row normalisations.  HBM-bound; one workgroup per (batch, chunk, head) tile.
+//
+// Reference behaviour restated (ngocbh/kalman-delta-networks):
+//   iso gate      lit_gpt/kdn_ops/iso_kdn_chunk.py:739-1009
+//   diag frontend lit_gpt/kdn_ops/diag_kdn_chunk.py:1866-2016
+//   diag norm     lit_gpt/kdn_ops/diag_kdn_chunk.py:193-353
+//   FLA l2norm    iso_kdn_chunk.py:2203-2204,2229-2230 (x * rsqrt(sum x^2 + eps))
+#include "kdn_common.h"
+#include "../../include/kdn.h"
+
+namespace {
+
+constexpr int kMaxChunk = 64;
+
+// ---------------------------------------------------------------------------
+// iso gate forward.  grid (B*NT, H), block 256 (thread = key channel).
+// ---------------------------------------------------------------------------
+template <typename TG, typename TO>
+__global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
+    const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
+    const float* __restrict__ omega_bias, const float* __restrict__ r_bias, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ mu_param, float omega_min, float r_min,
+    int T, int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ a_out,
+    float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out) {
+  __shared__ float s_e2[kMaxChunk][257];
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const float rate = expf(A_log[h]);
+  if (i < K) {
+    const float bias = dt_bias[h * K + i];
+    float acc = 0.f;
+    for (int t = 0; t < L; ++t) {
+      const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i;
+      const float g = -rate * softplusf(ld(g_raw, off) + bias);
+      acc += g;
+      g_cumsum[off] = acc * KDN_LOG2E;
+      s_e2[t][i] = expf(2.f * g);
+    }
+  }
+  __syncthreads();
+  if (i < L) {
+    float s = 0.f;
+    for (int j = 0; j < K; ++j) s += s_e2[i][j];
+    const int64_t o = ((int64_t)b * T + t0 + i) * H + h;
+    a_out[o] = s / (float)K;
+    const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + i) * orr_st + h;
+    omega_out[o] = omega_min + softplusf(ld(orr, ro) + omega_bias[h]);
+    r_out[o] = r_min + softplusf(ld(orr, ro + H) + r_bias[h]);
+  }
+  if (blockIdx.x == 0 && i == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
+}
+
+// iso gate backward.  Writes per-tile partial sums; reduce_partials_kernel finishes them.
+template <typename TG, typename TO>
+__global__ __launch_bounds__(256) void iso_gate_bwd_kernel(
+    const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
+    const float* __restrict__ omega_bias, const float* __restrict__ r_bias, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ dg_pre, const float* __restrict__ da,
+    const float* __restrict__ domega, const float* __restrict__ dr, int T, int H, int K, int chunk, int NT,
+    TG* __restrict__ dg_raw, TO* __restrict__ dorr, float* __restrict__ part_A, float* __restrict__ part_dt,
+    float* __restrict__ part_bias) {
+  __shared__ float red[16];
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const int p = blockIdx.x;  // partial index (b, nt)
+  const float rate = expf(A_log[h]);
+  float dA_term = 0.f;
+  if (i < K) {
+    const float bias = dt_bias[h * K + i];
+    float acc = 0.f, ddt = 0.f;
+    for (int t = L - 1; t >= 0; --t) {
+      const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i;
+      const float x = ld(g_raw, off) + bias;
+      const float g = -rate * softplusf(x);
+      float dgl = 0.f;
+      if (dg_pre) { acc += dg_pre[off]; dgl = acc; }
+      if (da) dgl += da[((int64_t)b * T + t0 + t) * H + h] * (2.f / (float)K) * expf(2.f * g);
+      const float dgr = dgl * (-rate) * sigmoidf(x);
+      if (dg_raw) st(dg_raw, off, dgr);
+      dA_term += dgl * g;
+      ddt += dgr;
+    }
+    if (part_dt) part_dt[((int64_t)p * H + h) * K + i] = ddt;
+  }
+  float dob = 0.f, drb = 0.f;
+  if (i < L) {
+    const int64_t o = ((int64_t)b * T + t0 + i) * H + h;
+    const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + i) * orr_st + h;
+    if (domega) dob = domega[o] * sigmoidf(ld(orr, ro) + omega_bias[h]);
+    if (dr) drb = dr[o] * sigmoidf(ld(orr, ro + H) + r_bias[h]);
+    if (dorr) {
+      const int64_t wo = ((int64_t)b * T + t0 + i) * (2 * H) + h;
+      st(dorr, wo, dob);
+      st(dorr, wo + H, drb);
+    }
+  }
+  const float sA = block_sum(dA_term, red);
+  if (part_A && i == 0) part_A[(int64_t)p * H + h] = sA;
+  const float sO = block_sum(dob, red);
+  const float sR = block_sum(drb, red);
+  if (part_bias && i == 0) {
+    part_bias[(int64_t)p * 2 * H + h] = sO;
+    part_bias[(int64_t)p * 2 * H + H + h] = sR;
+  }
+}
+
+// out[j] = sum_p part[p * stride + j] for j < n, deterministic order.  grid ceil(n/256).
+__global__ void reduce_partials_kernel(const float* __restrict__ part, int NP, int64_t stride, int n,
+                                       float* __restrict__ out) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  float s = 0.f;
+  for (int p = 0; p < NP; ++p) s += part[(int64_t)p * stride + j];
+  out[j] = s;
+}
+
+__global__ void mu_fwd_kernel(const float* __restrict__ mu_param, int H, float* __restrict__ mu) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h < H) mu[h] = 0.1f + softplusf(mu_param[h]);
+}
+
+template <typename T>
+__global__ void fill_zero_kernel(T* __restrict__ p, int64_t n) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j < n) p[j] = (T)0;
+}
+
+// dmu_param = dmu * sigmoid(mu_param)
+__global__ void mu_vjp_kernel(const float* __restrict__ mu_param, const float* __restrict__ dmu, int H,
+                              float* __restrict__ dmu_param) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h < H) dmu_param[h] = dmu ? dmu[h] * sigmoidf(mu_param[h]) : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// Row normalisations.  One wave per row, K <= 256 (4 elements per lane).
+// ---------------------------------------------------------------------------
+template <typename TX, typename TY>
+__global__ __launch_bounds__(256) void l2norm_fwd_kernel(const TX* __restrict__ x, int64_t rows, int K, float eps,
+                                                         TY* __restrict__ y, float* __restrict__ rstd) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = c < K ? ld(x, row * K + c) : 0.f;
+    ss += v[j] * v[j];
+  }
+  ss = wave_sum(ss);
+  const float rs = 1.f / sqrtf(ss + eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    if (c < K) st(y, row * K + c, v[j] * rs);
+  }
+  if (lane == 0) rstd[row] = rs;
+}
+
+template <typename TX, typename TD>
+__global__ __launch_bounds__(256) void l2norm_bwd_kernel(const TX* __restrict__ x, const float* __restrict__ rstd,
+                                                         const TD* __restrict__ dy, int64_t rows, int K,
+                                                         TX* __restrict__ dx) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float rs = rstd[row];
+  float yv[4], gv[4];
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    yv[j] = c < K ? ld(x, row * K + c) * rs : 0.f;
+    gv[j] = c < K ? ld(dy, row * K + c) : 0.f;
+    dot += yv[j] * gv[j];
+  }
+  dot = wave_sum(dot);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    if (c < K) st(dx, row * K + c, rs * (gv[j] - yv[j] * dot));
+  }
+}
+
+// diag normalisation: y = x / max(||x||, 1e-12).  Emits q bf16, k fp32 (gain), k bf16 (memory).
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_norm_fwd_kernel(const TX* __restrict__ q, const TX* __restrict__ k,
+                                                            int64_t rows, int K, bf16_t* __restrict__ q_mem,
+                                                            float* __restrict__ k_gain, bf16_t* __restrict__ k_mem,
+                                                            float* __restrict__ q_norm, float* __restrict__ k_norm) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float qv[4], kv[4], sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    qv[j] = c < K ? ld(q, row * K + c) : 0.f;
+    kv[j] = c < K ? ld(k, row * K + c) : 0.f;
+    sq += qv[j] * qv[j];
+    sk += kv[j] * kv[j];
+  }
+  const float nq = sqrtf(wave_sum(sq)), nk = sqrtf(wave_sum(sk));
+  const float dq = fmaxf(nq, 1e-12f), dk = fmaxf(nk, 1e-12f);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    if (c < K) {
+      q_mem[row * K + c] = f2bf(qv[j] / dq);
+      const float kn = kv[j] / dk;
+      k_gain[row * K + c] = kn;
+      k_mem[row * K + c] = f2bf(kn);
+    }
+  }
+  if (lane == 0) {
+    q_norm[row] = nq;
+    k_norm[row] = nk;
+  }
+}
+
+// Row VJP of y = x / max(||x||, eps): n > eps: (dy - y (y.dy)) / n; else dy / eps.
+template <typename TX>
+__device__ __forceinline__ void norm_row_vjp(const TX* x, float n, const float* g, int64_t row, int K, int lane,
+                                             TX* dx) {
+  const float d = fmaxf(n, 1e-12f);
+  float yv[4], dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    yv[j] = c < K ? ld(x, row * K + c) / d : 0.f;
+    dot += yv[j] * g[j];
+  }
+  dot = wave_sum(dot);
+  const bool clamped = !(n > 1e-12f);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane + 64 * j;
+    if (c < K) st(dx, row * K + c, clamped ? g[j] / d : (g[j] - yv[j] * dot) / d);
+  }
+}
+
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_norm_bwd_kernel(
+    const TX* __restrict__ q, const TX* __restrict__ k, const float* __restrict__ q_norm,
+    const float* __restrict__ k_norm, const bf16_t* __restrict__ dq_mem, const float* __restrict__ dk_gain,
+    const bf16_t* __restrict__ dk_mem, int64_t rows, int K, TX* __restrict__ dq, TX* __restrict__ dk) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float g[4];
+  if (dq) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + 64 * j;
+      g[j] = (c < K && dq_mem) ? bf2f(dq_mem[row * K + c]) : 0.f;
+    }
+    norm_row_vjp(q, q_norm[row], g, row, K, lane, dq);
+  }
+  if (dk) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + 64 * j;
+      float s = 0.f;
+      if (c < K) {
+        if (dk_gain) s += dk_gain[row * K + c];
+        if (dk_mem) s += bf2f(dk_mem[row * K + c]);
+      }
+      g[j] = s;
+    }
+    norm_row_vjp(k, k_norm[row], g, row, K, lane, dk);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// diag frontend.  grid (B*NT, H), block 256 (thread = key channel).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void diag_frontend_fwd_kernel(
+    const bf16_t* __restrict__ f_raw, const bf16_t* __restrict__ z_raw, const bf16_t* __restrict__ y_raw,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* __restrict__ mu_param, int T,
+    int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ alpha,
+    float* __restrict__ omega, float* __restrict__ r, float* __restrict__ mu) {
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const float rate = expf(A_log[h]);
+  const float floor_log = logf(1e-6f);
+  if (i < K) {
+    const float bias = dt_bias[h * K + i];
+    float acc = 0.f;
+    for (int t = 0; t < L; ++t) {
+      const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i;
+      const float ell = -rate * softplusf(bf2f(f_raw[off]) + bias);
+      const float al = expf(ell);
+      // memory path clamps alpha at 1e-6 (NaN propagates)
+      const float ell_mem = (al >= 1e-6f || al != al) ? ell : floor_log;
+      acc += ell_mem;
+      g_cumsum[off] = acc * KDN_LOG2E;
+      alpha[off] = al;
+      omega[off] = softplusf(bf2f(z_raw[off]));
+    }
+  }
+  if (i < L) {
+    const int64_t o = ((int64_t)b * T + t0 + i) * H + h;
+    r[o] = 0.01f + softplusf(bf2f(y_raw[o]));
+  }
+  if (blockIdx.x == 0 && i == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
+}
+
+__global__ __launch_bounds__(256) void diag_frontend_bwd_kernel(
+    const bf16_t* __restrict__ f_raw, const float* __restrict__ A_log, const float* __restrict__ dt_bias,
+    const float* __restrict__ alpha, const float* __restrict__ dG, const float* __restrict__ dalpha, int T, int H,
+    int K, int chunk, int NT, bf16_t* __restrict__ df_raw, float* __restrict__ part_A,
+    float* __restrict__ part_dt) {
+  __shared__ float red[16];
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const int p = blockIdx.x;
+  const float rate = expf(A_log[h]);
+  float dA_term = 0.f;
+  if (i < K) {
+    const float bias = dt_bias[h * K + i];
+    float acc = 0.f, ddt = 0.f;
+    for (int t = L - 1; t >= 0; --t) {
+      const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i;
+      const float x = bf2f(f_raw[off]) + bias;
+      const float ell = -rate * softplusf(x);
+      const float al = alpha[off];
+      float dell = 0.f;
+      if (dG) {
+        acc += dG[off];
+        if (al >= 1e-6f) dell = acc;
+      }
+      if (dalpha) dell += dalpha[off] * al;
+      const float df = dell * (-rate) * sigmoidf(x);
+      if (df_raw) df_raw[off] = f2bf(df);
+      dA_term += dell * ell;
+      ddt += df;
+    }
+    if (part_dt) part_dt[((int64_t)p * H + h) * K + i] = ddt;
+  }
+  const float sA = block_sum(dA_term, red);
+  if (part_A && i == 0) part_A[(int64_t)p * H + h] = sA;
+}
+
+// d raw = d * sigmoid(raw) for the (optional) omega / r cotangents reaching the frontend.
+__global__ void sigmoid_vjp_kernel(const bf16_t* __restrict__ raw, const float* __restrict__ d, int64_t n,
+                                   bf16_t* __restrict__ out) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j < n) out[j] = f2bf(d[j] * sigmoidf(bf2f(raw[j])));
+}
+
+inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+extern "C" {
+
+size_t kdn_iso_gate_bwd_workspace_size(int B, int T, int H, int K, int chunk) {
+  const int64_t NP = (int64_t)B * cdiv(T, chunk);
+  return (size_t)(NP * H + NP * H * K + NP * 2 * H) * sizeof(float);
+}
+
+int kdn_iso_gate_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                     int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                     const float* dt_bias, const float* mu_param, float omega_min, float r_min, int B, int T, int H,
+                     int K, int chunk, float* g_cumsum, float* a, float* omega, float* r, float* mu,
+                     hipStream_t stream) {
+  if (K <= 0 || K > 256 || chunk <= 0 || chunk > kMaxChunk || B < 0 || T < 0 || H <= 0) return KDN_ERR_ARG;
+  if (B == 0 || T == 0) {
+    hipLaunchKernelGGL(mu_fwd_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, mu_param, H, mu);
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
+  const int NT = cdiv(T, chunk);
+  dim3 grid(B * NT, H);
+#define KDN_GATE_FWD(TG, TO)                                                                                     \
+  hipLaunchKernelGGL((iso_gate_fwd_kernel<TG, TO>), grid, dim3(256), 0, stream, (const TG*)g_raw,               \
+                     (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
+                     mu_param, omega_min, r_min, T, H, K, chunk, NT, g_cumsum, a, omega, r, mu)
+  if (g_raw_bf16 && orr_bf16) KDN_GATE_FWD(bf16_t, bf16_t);
+  else if (g_raw_bf16) KDN_GATE_FWD(bf16_t, float);
+  else if (orr_bf16) KDN_GATE_FWD(float, bf16_t);
+  else KDN_GATE_FWD(float, float);
+#undef KDN_GATE_FWD
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                     int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                     const float* dt_bias, const float* mu_param, const float* dg_pre, const float* da,
+                     const float* domega, const float* dr, const float* dmu, int B, int T, int H, int K, int chunk,
+                     void* dg_raw, void* domega_r_raw, float* dA_log, float* ddt_bias, float* domega_bias,
+                     float* dr_bias, float* dmu_param, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  if (K <= 0 || K > 256 || chunk <= 0 || chunk > kMaxChunk || B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
+  if (workspace_bytes < kdn_iso_gate_bwd_workspace_size(B, T, H, K, chunk)) return KDN_ERR_ARG;
+  const int NT = cdiv(T, chunk);
+  const int NP = B * NT;
+  float* part_A = (float*)workspace;
+  float* part_dt = part_A + (int64_t)NP * H;
+  float* part_bias = part_dt + (int64_t)NP * H * K;
+  dim3 grid(NP, H);
+#define KDN_GATE_BWD(TG, TO)                                                                                     \
+  hipLaunchKernelGGL((iso_gate_bwd_kernel<TG, TO>), grid, dim3(256), 0, stream, (const TG*)g_raw,               \
+                     (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
+                     dg_pre, da, domega, dr, T, H, K, chunk, NT, (TG*)dg_raw, (TO*)domega_r_raw,                 \
+                     dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr,                                    \
+                     (domega_bias || dr_bias) ? part_bias : nullptr)
+  if (g_raw_bf16 && orr_bf16) KDN_GATE_BWD(bf16_t, bf16_t);
+  else if (g_raw_bf16) KDN_GATE_BWD(bf16_t, float);
+  else if (orr_bf16) KDN_GATE_BWD(float, bf16_t);
+  else KDN_GATE_BWD(float, float);
+#undef KDN_GATE_BWD
+  KDN_CHECK_LAUNCH();
+  if (dA_log)
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H, dA_log);
+  if (ddt_bias)
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H * K, 256)), dim3(256), 0, stream, part_dt, NP,
+                       (int64_t)H * K, H * K, ddt_bias);
+  // part_bias rows are [omega(H) | r(H)]
+  if (domega_bias)
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_bias, NP,
+                       (int64_t)2 * H, H, domega_bias);
+  if (dr_bias)
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_bias + H, NP,
+                       (int64_t)2 * H, H, dr_bias);
+  if (dmu_param) hipLaunchKernelGGL(mu_vjp_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, mu_param, dmu, H, dmu_param);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_l2norm_fwd(const void* x, int x_bf16, int64_t rows, int K, float eps, void* y, int y_bf16, float* rstd,
+                   hipStream_t stream) {
+  if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
+  if (rows == 0) return 0;
+  dim3 grid(cdiv(rows, 4));
+  if (x_bf16 && y_bf16)
+    hipLaunchKernelGGL((l2norm_fwd_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)x, rows, K, eps, (bf16_t*)y, rstd);
+  else if (x_bf16)
+    hipLaunchKernelGGL((l2norm_fwd_kernel<bf16_t, float>), grid, dim3(256), 0, stream, (const bf16_t*)x, rows, K, eps, (float*)y, rstd);
+  else if (y_bf16)
+    hipLaunchKernelGGL((l2norm_fwd_kernel<float, bf16_t>), grid, dim3(256), 0, stream, (const float*)x, rows, K, eps, (bf16_t*)y, rstd);
+  else
+    hipLaunchKernelGGL((l2norm_fwd_kernel<float, float>), grid, dim3(256), 0, stream, (const float*)x, rows, K, eps, (float*)y, rstd);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_l2norm_bwd(const void* x, int x_bf16, const float* rstd, const void* dy, int dy_bf16, int64_t rows, int K,
+                   void* dx, hipStream_t stream) {
+  if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
+  if (rows == 0) return 0;
+  dim3 grid(cdiv(rows, 4));
+  if (x_bf16 && dy_bf16)
+    hipLaunchKernelGGL((l2norm_bwd_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)x, rstd, (const bf16_t*)dy, rows, K, (bf16_t*)dx);
+  else if (x_bf16)
+    hipLaunchKernelGGL((l2norm_bwd_kernel<bf16_t, float>), grid, dim3(256), 0, stream, (const bf16_t*)x, rstd, (const float*)dy, rows, K, (bf16_t*)dx);
+  else if (dy_bf16)
+    hipLaunchKernelGGL((l2norm_bwd_kernel<float, bf16_t>), grid, dim3(256), 0, stream, (const float*)x, rstd, (const bf16_t*)dy, rows, K, (float*)dx);
+  else
+    hipLaunchKernelGGL((l2norm_bwd_kernel<float, float>), grid, dim3(256), 0, stream, (const float*)x, rstd, (const float*)dy, rows, K, (float*)dx);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_diag_norm_fwd(const void* q_raw, const void* k_raw, int x_bf16, int64_t rows, int K, uint16_t* q_memory,
+                      float* k_gain, uint16_t* k_memory, float* q_norm, float* k_norm, hipStream_t stream) {
+  if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
+  if (rows == 0) return 0;
+  dim3 grid(cdiv(rows, 4));
+  if (x_bf16)
+    hipLaunchKernelGGL((diag_norm_fwd_kernel<bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)q_raw, (const bf16_t*)k_raw, rows, K, q_memory, k_gain, k_memory, q_norm, k_norm);
+  else
+    hipLaunchKernelGGL((diag_norm_fwd_kernel<float>), grid, dim3(256), 0, stream, (const float*)q_raw, (const float*)k_raw, rows, K, q_memory, k_gain, k_memory, q_norm, k_norm);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_diag_norm_bwd(const void* q_raw, const void* k_raw, int x_bf16, const float* q_norm, const float* k_norm,
+                      const uint16_t* d_q_memory, const float* d_k_gain, const uint16_t* d_k_memory, int64_t rows,
+                      int K, void* dq_raw, void* dk_raw, hipStream_t stream) {
+  if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
+  if (rows == 0) return 0;
+  dim3 grid(cdiv(rows, 4));
+  if (x_bf16)
+    hipLaunchKernelGGL((diag_norm_bwd_kernel<bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)q_raw, (const bf16_t*)k_raw, q_norm, k_norm, d_q_memory, d_k_gain, d_k_memory, rows, K, (bf16_t*)dq_raw, (bf16_t*)dk_raw);
+  else
+    hipLaunchKernelGGL((diag_norm_bwd_kernel<float>), grid, dim3(256), 0, stream, (const float*)q_raw, (const float*)k_raw, q_norm, k_norm, d_q_memory, d_k_gain, d_k_memory, rows, K, (float*)dq_raw, (float*)dk_raw);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_diag_frontend_fwd(const uint16_t* retention_raw, const uint16_t* omega_raw, const uint16_t* r_raw,
+                          const float* A_log, const float* dt_bias, const float* mu_param, int B, int T, int H, int K,
+                          int chunk, float* g_cumsum, float* alpha, float* omega, float* r, float* mu,
+                          hipStream_t stream) {
+  if (K <= 0 || K > 256 || chunk <= 0 || B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
+  const int NT = cdiv(T, chunk);
+  hipLaunchKernelGGL(diag_frontend_fwd_kernel, dim3(B * NT, H), dim3(256), 0, stream, retention_raw, omega_raw, r_raw,
+                     A_log, dt_bias, mu_param, T, H, K, chunk, NT, g_cumsum, alpha, omega, r, mu);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+size_t kdn_diag_frontend_bwd_workspace_size(int B, int T, int H, int K, int chunk) {
+  const int64_t NP = (int64_t)B * cdiv(T, chunk);
+  return (size_t)(NP * H + NP * H * K) * sizeof(float);
+}
+
+int kdn_diag_frontend_bwd(const uint16_t* retention_raw, const uint16_t* omega_raw, const uint16_t* r_raw,
+                          const float* A_log, const float* dt_bias, const float* mu_param, const float* alpha,
+                          const float* d_g_cumsum, const float* d_alpha, const float* d_omega, const float* d_r,
+                          const float* d_mu, int B, int T, int H, int K, int chunk, uint16_t* d_retention_raw,
+                          uint16_t* d_omega_raw, uint16_t* d_r_raw, float* dA_log, float* ddt_bias,
+                          float* d_mu_param, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (K <= 0 || K > 256 || chunk <= 0 || B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
+  if (workspace_bytes < kdn_diag_frontend_bwd_workspace_size(B, T, H, K, chunk)) return KDN_ERR_ARG;
+  const int NT = cdiv(T, chunk);
+  const int NP = B * NT;
+  float* part_A = (float*)workspace;
+  float* part_dt = part_A + (int64_t)NP * H;
+  const bool has_decay = d_g_cumsum || d_alpha;
+  if (has_decay && (d_retention_raw || dA_log || ddt_bias)) {
+    hipLaunchKernelGGL(diag_frontend_bwd_kernel, dim3(NP, H), dim3(256), 0, stream, retention_raw, A_log, dt_bias,
+                       alpha, d_g_cumsum, d_alpha, T, H, K, chunk, NT, d_retention_raw, dA_log ? part_A : nullptr,
+                       ddt_bias ? part_dt : nullptr);
+    KDN_CHECK_LAUNCH();
+    if (dA_log)
+      hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H,
+                         dA_log);
+    if (ddt_bias)
+      hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H * K, 256)), dim3(256), 0, stream, part_dt, NP,
+                         (int64_t)H * K, H * K, ddt_bias);
+  } else {
+    const int64_t n = (int64_t)B * T * H * K;
+    if (d_retention_raw) hipLaunchKernelGGL(fill_zero_kernel<uint16_t>, dim3(cdiv(n, 256)), dim3(256), 0, stream, d_retention_raw, n);
+    if (dA_log) hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(cdiv(H, 256)), dim3(256), 0, stream, dA_log, (int64_t)H);
+    if (ddt_bias) hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(cdiv((int64_t)H * K, 256)), dim3(256), 0, stream, ddt_bias, (int64_t)H * K);
+  }
+  if (d_omega_raw && d_omega) {
+    const int64_t n = (int64_t)B * T * H * K;
+    hipLaunchKernelGGL(sigmoid_vjp_kernel, dim3(cdiv(n, 256)), dim3(256), 0, stream, omega_raw, d_omega, n, d_omega_raw);
+  }
+  if (d_r_raw && d_r) {
+    const int64_t n = (int64_t)B * T * H;
+    hipLaunchKernelGGL(sigmoid_vjp_kernel, dim3(cdiv(n, 256)), dim3(256), 0, stream, r_raw, d_r, n, d_r_raw);
+  }
+  if (d_mu_param) hipLaunchKernelGGL(mu_vjp_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, mu_param, d_mu, H, d_mu_param);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // extern "C"

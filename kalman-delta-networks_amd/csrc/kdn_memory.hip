@@ -1,0 +1,1071 @@
+// Chunked KDN memory scan (shared by iso_kdn and diag_kdn), forward and backward.
+//
+// Recurrence per (b, h):  S_hat = diag(alpha_t) S;  delta = v_t - k_t^T S_hat;
+//                         S = S_hat + kappa_t delta^T;  o_t = scale q_t^T S
+// (iso: kappa_t = beta_t k_t).  Reference: lit_gpt/kdn_ops/iso_kdn_naive.py:449-533 and
+// diag_kdn_naive.py:570-655 (chunk form), diag_kdn_chunk.py:720-1861 (production kernels).
+//
+// Chunk of C = 64 tokens, g = natural-log chunk-local cumulative gate (g_cumsum * ln 2);
+// the returned dg is the cotangent in these natural-log coordinates (not reverse-summed):
+//   N[c,s] = sum_i k_ci kappa_si e^{g_ci - g_si}   (s < c)       (write interactions)
+//   M[c,s] = scale sum_i q_ci kappa_si e^{g_ci - g_si}   (s <= c) (readout interactions)
+//   U = (I+N)^-1 V,  W = (I+N)^-1 (K e^g),  Kf = kappa e^{g_last - g},  Qg = scale Q e^g
+//   delta = U - W S_0,  O = Qg S_0 + M delta,  S_C = e^{g_last} S_0 + Kf^T delta
+//
+// Kernels (grid = one workgroup per chunk unless noted, 256 threads = 4 waves):
+//   intra_fwd    N/M (MFMA, anchored), forward substitution for U, W; Kf, Qg
+//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h); S slice in VGPRs
+//   output_fwd   O = Qg h + M delta
+//   state_bwd    serial reverse: d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
+//   bwd_hgrad    dQg = dO h^T, dW = -d delta h^T, dKf = delta dh^T, dM = dO delta^T, g_last terms
+//   bwd_solve    dV = (I+N)^-T d delta, dKg = (I+N)^-T dW, dN = -(dV U^T + dKg W^T)
+//   bwd_contrib  dq, dk, dkappa (or dbeta), dg from dN, dM and the elementwise factors
+//
+// g is kept in the base-2 units of g_cumsum, so e^{g_c - g_s} = exp2(G_c - G_s).
+// Decay factors (c >= s) are split at the start a of the row block (16 tokens):
+// exp2(G_c - G_a) exp2(G_a - G_s).  Off-diagonal blocks have both factors <= 1 for
+// non-increasing G.  Diagonal blocks use the split only when the block's decay span
+// is <= 86 (base 2, no overflow); otherwise an exact per-element path runs.
+// Products use fp32 MFMA (v_mfma_f32_16x16x4_f32), fp32 accumulate.
+#include "kdn_common.h"
+#include "../../include/kdn.h"
+
+namespace {
+
+constexpr int C = 64;        // chunk length
+constexpr int NS = C + 4;    // LDS row stride of C x C tiles
+constexpr float kSpanMax = 86.f;  // base-2 units: 2^86 ~ 8e25 leaves headroom below FLT_MAX
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ int64_t bthk(int b, int t, int h, int i, int T, int H, int D) {
+  return (((int64_t)b * T + t) * H + h) * D + i;
+}
+// [B,H,T,D] row offset for (bh, t)
+__device__ __forceinline__ int64_t bht(int bh, int t, int T, int D) { return ((int64_t)bh * T + t) * D; }
+
+// ---------------------------------------------------------------------------
+// Chunk staging: k, kappa, g (natural) and optionally q into LDS as fp32 [C][K+4].
+// Rows >= L are zero; g rows >= L repeat row L-1.  Also the per-block decay spans.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lds_f(const float* p, int i) { return p[i]; }
+__device__ __forceinline__ float lds_f(const bf16_t* p, int i) { return bf2f(p[i]); }
+__device__ __forceinline__ void lds_put(float* p, int i, float x) { p[i] = x; }
+__device__ __forceinline__ void lds_put(bf16_t* p, int i, float x) { p[i] = f2bf(x); }  // exact for bf16 inputs
+
+template <int K, bool ISO, typename TQK>
+__device__ void stage_chunk(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+                            const float* __restrict__ gc, int b, int h, int T, int H, int t0, int L, TQK* sQ,
+                            TQK* sK, float* sA, float* sG, float* sSpan) {
+  constexpr int KP = K + 4;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < C * K; e += 256) {
+    const int c = e / K, i = e - c * K;
+    float kv = 0.f, qv = 0.f, av = 0.f, gv = 0.f;
+    if (c < L) {
+      const int64_t o = bthk(b, t0 + c, h, i, T, H, K);
+      kv = bf2f(k[o]);
+      if (sQ) qv = bf2f(q[o]);
+      gv = gc[o];  // base-2 chunk-local prefix; all decays below are exp2 of differences
+      av = ISO ? kap[((int64_t)b * T + t0 + c) * H + h] * kv : kap[o];
+    }
+    lds_put(sK, c * KP + i, kv);
+    if (sQ) lds_put(sQ, c * KP + i, qv);
+    sA[c * KP + i] = av;
+    sG[c * KP + i] = gv;
+  }
+  __syncthreads();
+  if (L < C) {
+    for (int e = tid; e < (C - L) * K; e += 256) {
+      const int c = L + e / K, i = e % K;
+      sG[c * KP + i] = sG[(L - 1) * KP + i];
+    }
+    __syncthreads();
+  }
+  // span of block w (= wave w): max_i,r |g[16w][i] - g[16w + r][i]|
+  {
+    const int w = tid >> 6, lane = tid & 63;
+    float m = 0.f;
+    for (int i = lane; i < K; i += 64) {
+      const float ga = sG[(16 * w) * KP + i];
+      for (int r = 1; r < 16; ++r) m = fmaxf(m, fabsf(ga - sG[(16 * w + r) * KP + i]));
+    }
+    m = wave_max(m);
+    if (lane == 0) sSpan[w] = m;
+  }
+  __syncthreads();
+}
+
+// Lower 16x16 tile list (I, J), J <= I, in an order that balances the 4 waves.
+__device__ __forceinline__ void lower_tile(int t, int& I, int& J) {
+  // 0:(0,0) 1:(1,1) 2:(2,2) 3:(3,3) 4:(1,0) 5:(2,1) 6:(3,2) 7:(2,0) 8:(3,1) 9:(3,0), 2-bit packed
+  I = (0xfb9e4u >> (2 * t)) & 3;
+  J = (0x124e4u >> (2 * t)) & 3;
+}
+
+// Build N (strictly lower, into sN [C][NS], or its transpose) and optionally M (lower incl.
+// diagonal, scaled, written to global gM [C][C], zeros above the diagonal).
+template <int K, bool WITH_M, bool N_TRANSPOSED>
+__device__ void build_NM(const float* sQ, const float* sK, const float* sA, const float* sG, const float* sSpan,
+                         float scale, float* sN, float* __restrict__ gM) {
+  constexpr int KP = K + 4;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // upper tiles -> zero
+  for (int e = tid; e < 6 * 256; e += 256) {
+    const int ut = e >> 8, r = (e >> 4) & 15, cc = e & 15;
+    // upper tiles (0,1) (0,2) (0,3) (1,2) (1,3) (2,3), 2-bit packed
+    const int c = 16 * ((0x940u >> (2 * ut)) & 3) + r, s = 16 * ((0xfb9u >> (2 * ut)) & 3) + cc;
+    sN[N_TRANSPOSED ? s * NS + c : c * NS + s] = 0.f;
+    if (WITH_M) gM[c * C + s] = 0.f;
+  }
+  for (int t = w; t < 10; t += 4) {
+    int I, J;
+    lower_tile(t, I, J);
+    const int a = 16 * I;
+    const bool diag = I == J;
+    const bool fast = !diag || sSpan[I] <= kSpanMax;
+    f32x4 accN = zero4(), accM = zero4();
+    if (fast) {
+      const int cA = a + (lane & 15), sB = 16 * J + (lane & 15);
+#pragma unroll 4
+      for (int st = 0; st < K / 4; ++st) {
+        const int i = 4 * st + (lane >> 4);
+        const float ga = sG[a * KP + i];
+        const float el = exp2f(sG[cA * KP + i] - ga);
+        const float br = sA[sB * KP + i] * exp2f(ga - sG[sB * KP + i]);
+        accN = mfma4(sK[cA * KP + i] * el, br, accN);
+        if (WITH_M) accM = mfma4(sQ[cA * KP + i] * el, br, accM);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = a + 4 * (lane >> 4) + j, s = 16 * J + (lane & 15);
+      float nv = accN[j], mv = accM[j];
+      if (!fast) {
+        nv = 0.f;
+        mv = 0.f;
+        if (s <= c) {
+          for (int i = 0; i < K; ++i) {
+            const float tv = sA[s * KP + i] * exp2f(sG[c * KP + i] - sG[s * KP + i]);
+            nv += sK[c * KP + i] * tv;
+            if (WITH_M) mv += sQ[c * KP + i] * tv;
+          }
+        }
+      }
+      if (diag) {
+        if (s >= c) nv = 0.f;
+        if (s > c) mv = 0.f;
+      }
+      sN[N_TRANSPOSED ? s * NS + c : c * NS + s] = nv;
+      if (WITH_M) gM[c * C + s] = mv * scale;
+    }
+  }
+}
+
+// ===========================================================================
+// Forward intra-chunk kernel.
+// ===========================================================================
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_intra_fwd_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
+    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
+    float* __restrict__ Mg) {
+  constexpr int KP = K + 4;
+  constexpr int XP = V + K + 4;
+  // sQ | sA are dead after Kf / Qg are written and are then reused for the solve's sX [C][XP]
+  constexpr int OFF2 = (2 * C * KP > C * XP) ? 2 * C * KP : C * XP;
+  __shared__ float sBuf[OFF2 + 2 * C * KP];
+  __shared__ __attribute__((aligned(16))) float sN[C * NS];  // transposed: sN[s * NS + c] = N[c][s]
+  __shared__ float sSpan[4];
+  float* sQ = sBuf;
+  float* sA = sBuf + C * KP;
+  float* sK = sBuf + OFF2;
+  float* sG = sBuf + OFF2 + C * KP;
+  float* sX = sBuf;
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x;
+  stage_chunk<K, ISO, float>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
+  build_NM<K, true, true>(sQ, sK, sA, sG, sSpan, scale, sN, Mg + ((int64_t)bh * NT + n) * C * C);
+  // Kf = kappa e^{g_last - g};  Qg = scale q e^g
+  if (tid < 2 * K) {
+    const int i = tid % K;
+    const bool isKf = tid < K;
+    const float gl = sG[(L - 1) * KP + i];
+    for (int c = 0; c < L; ++c) {
+      const int64_t o = bht(bh, t0 + c, T, K) + i;
+      if (isKf) Kf[o] = sA[c * KP + i] * exp2f(gl - sG[c * KP + i]);
+      else Qg[o] = scale * sQ[c * KP + i] * exp2f(sG[c * KP + i]);
+    }
+  }
+  __syncthreads();
+  // forward substitution (I+N) X = [V | K e^g], thread = column; 16-row blocks
+  if (tid < V + K) {
+    const int j = tid;
+    const bool isV = j < V;
+    const int col = isV ? j : j - V;
+    float* dst = isV ? U : W;
+    const int D = isV ? V : K;
+#pragma unroll 1
+    for (int I = 0; I < 4; ++I) {
+      float acc[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 16 * I + r;
+        float x = 0.f;
+        if (c < L) x = isV ? bf2f(v[bthk(b, t0 + c, h, col, T, H, V)]) : sK[c * KP + col] * exp2f(sG[c * KP + col]);
+        acc[r] = x;
+      }
+#pragma unroll 1
+      for (int s = 0; s < 16 * I; ++s) {
+        const float xs = sX[s * XP + j];
+        const float4* nrow = reinterpret_cast<const float4*>(sN + s * NS + 16 * I);
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 nv = nrow[r4];
+          acc[4 * r4 + 0] -= nv.x * xs;
+          acc[4 * r4 + 1] -= nv.y * xs;
+          acc[4 * r4 + 2] -= nv.z * xs;
+          acc[4 * r4 + 3] -= nv.w * xs;
+        }
+      }
+#pragma unroll
+      for (int r = 1; r < 16; ++r) {
+#pragma unroll
+        for (int r2 = 0; r2 < r; ++r2) acc[r] -= sN[(16 * I + r2) * NS + 16 * I + r] * acc[r2];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 16 * I + r;
+        sX[c * XP + j] = acc[r];
+        if (c < L) dst[bht(bh, t0 + c, T, D) + col] = acc[r];
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// Forward state pass.  grid (V / BV, B*H); S slice [K][BV] kept in MFMA accumulators.
+// ===========================================================================
+template <int K, int V, int BV>
+__global__ __launch_bounds__(256) void mem_state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
+                                                            const float* __restrict__ Kf, const float* __restrict__ gc,
+                                                            const float* __restrict__ h0, int T, int H, int NT,
+                                                            float* __restrict__ hbuf, float* __restrict__ Dl,
+                                                            float* __restrict__ ht) {
+  constexpr int KP = K + 4, BP = BV + 4;
+  constexpr int NST = (K / 16) * (BV / 16);  // S tiles
+  constexpr int STW = NST / 4;               // S tiles per wave
+  constexpr int NDT = (C / 16) * (BV / 16);  // delta tiles
+  constexpr int DTW = NDT / 4;
+  static_assert(NST % 4 == 0 && NDT % 4 == 0, "tile split");
+  __shared__ float sW[C * KP], sKf[C * KP], sS[K * BP], sD[C * BP], sE[K];
+  const int vs = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, v0 = vs * BV;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  f32x4 S[STW];
+  // initial state
+#pragma unroll
+  for (int u = 0; u < STW; ++u) {
+    const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+      const float x = h0 ? h0[((int64_t)bh * K + i) * V + v0 + vv] : 0.f;
+      S[u][j] = x;
+      sS[i * BP + vv] = x;
+    }
+  }
+  for (int n = 0; n < NT; ++n) {
+    const int t0 = n * C, L = min(C, T - t0);
+    // stage W, Kf, e^{g_last}
+    for (int e = tid; e < C * K; e += 256) {
+      const int c = e / K, i = e - c * K;
+      float wv = 0.f, kv = 0.f;
+      if (c < L) {
+        const int64_t o = bht(bh, t0 + c, T, K) + i;
+        wv = W[o];
+        kv = Kf[o];
+      }
+      sW[c * KP + i] = wv;
+      sKf[c * KP + i] = kv;
+    }
+    if (tid < K) sE[tid] = exp2f(gc[bthk(b, t0 + L - 1, h, tid, T, H, K)]);
+    // h_n = S (S is already in sS from the previous step)
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+        hbuf[(((int64_t)bh * NT + n) * K + i) * V + v0 + vv] = S[u][j];
+      }
+    }
+    __syncthreads();
+    // delta = U - W S
+#pragma unroll
+    for (int u = 0; u < DTW; ++u) {
+      const int tile = w * DTW + u, cb = tile / (BV / 16), vb = tile % (BV / 16);
+      f32x4 acc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 16 * cb + 4 * (lane >> 4) + j;
+        acc[j] = c < L ? U[bht(bh, t0 + c, T, V) + v0 + 16 * vb + (lane & 15)] : 0.f;
+      }
+      const int cA = 16 * cb + (lane & 15), vB = 16 * vb + (lane & 15);
+#pragma unroll 8
+      for (int st = 0; st < K / 4; ++st) {
+        const int i = 4 * st + (lane >> 4);
+        acc = mfma4(-sW[cA * KP + i], sS[i * BP + vB], acc);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 16 * cb + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+        sD[c * BP + vv] = acc[j];
+        if (c < L) Dl[bht(bh, t0 + c, T, V) + v0 + vv] = acc[j];
+      }
+    }
+    __syncthreads();
+    // S = e ⊙ S + Kf^T delta
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+      f32x4 acc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = sE[16 * ib + 4 * (lane >> 4) + j] * S[u][j];
+      const int iA = 16 * ib + (lane & 15), vB = 16 * vb + (lane & 15);
+#pragma unroll 4
+      for (int st = 0; st < C / 4; ++st) {
+        const int c = 4 * st + (lane >> 4);
+        acc = mfma4(sKf[c * KP + iA], sD[c * BP + vB], acc);
+      }
+      S[u] = acc;
+    }
+    __syncthreads();  // everyone done reading sS / sD / sW / sKf
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sS[(16 * ib + 4 * (lane >> 4) + j) * BP + 16 * vb + (lane & 15)] = S[u][j];
+    }
+  }
+  if (ht) {
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+        ht[((int64_t)bh * K + i) * V + v0 + vv] = S[u][j];
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// Forward readout: O = Qg h + M delta.  grid (NT, B*H).
+// ===========================================================================
+template <int K, int V, typename TO>
+__global__ __launch_bounds__(256) void mem_output_fwd_kernel(const float* __restrict__ Qg, const float* __restrict__ hbuf,
+                                                             const float* __restrict__ Mg, const float* __restrict__ Dl,
+                                                             int T, int H, int NT, TO* __restrict__ o) {
+  constexpr int KP = K + 4, VP = V + 4;
+  __shared__ float sQg[C * KP], sH[K * VP], sM[C * NS], sD[C * VP];
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int e = tid; e < C * K; e += 256) {
+    const int c = e / K, i = e - c * K;
+    sQg[c * KP + i] = c < L ? Qg[bht(bh, t0 + c, T, K) + i] : 0.f;
+  }
+  const float* hn = hbuf + ((int64_t)bh * NT + n) * K * V;
+  for (int e = tid; e < K * V; e += 256) sH[(e / V) * VP + e % V] = hn[e];
+  const float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
+  for (int e = tid; e < C * C; e += 256) sM[(e / C) * NS + e % C] = Mn[e];
+  for (int e = tid; e < C * V; e += 256) {
+    const int c = e / V, vv = e - c * V;
+    sD[c * VP + vv] = c < L ? Dl[bht(bh, t0 + c, T, V) + vv] : 0.f;
+  }
+  __syncthreads();
+  constexpr int NTL = (C / 16) * (V / 16);
+  for (int tile = w; tile < NTL; tile += 4) {
+    const int cb = tile / (V / 16), vb = tile % (V / 16);
+    f32x4 acc = zero4();
+    const int cA = 16 * cb + (lane & 15), vB = 16 * vb + (lane & 15);
+#pragma unroll 8
+    for (int st = 0; st < K / 4; ++st) {
+      const int i = 4 * st + (lane >> 4);
+      acc = mfma4(sQg[cA * KP + i], sH[i * VP + vB], acc);
+    }
+    for (int st = 0; st < 4 * (cb + 1); ++st) {
+      const int s = 4 * st + (lane >> 4);
+      acc = mfma4(sM[cA * NS + s], sD[s * VP + vB], acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 16 * cb + 4 * (lane >> 4) + j;
+      if (c < L) st(o, bthk(b, t0 + c, h, vB, T, H, V), acc[j]);
+    }
+  }
+}
+
+// ===========================================================================
+// Backward state pass (reverse).  grid (V / BV, B*H).
+// ===========================================================================
+template <int K, int V, int BV, typename TDO>
+__global__ __launch_bounds__(256) void mem_state_bwd_kernel(
+    const float* __restrict__ Mg, const float* __restrict__ Kf, const float* __restrict__ Qg,
+    const float* __restrict__ W, const float* __restrict__ gc, const TDO* __restrict__ dO,
+    const float* __restrict__ dht, int T, int H, int NT, float* __restrict__ dhbuf, float* __restrict__ dDl,
+    float* __restrict__ dh0) {
+  constexpr int KP = K + 4, BP = BV + 4;
+  constexpr int NST = (K / 16) * (BV / 16), STW = NST / 4;
+  constexpr int NDT = (C / 16) * (BV / 16), DTW = NDT / 4;
+  __shared__ float sKf[C * KP], sQg[C * KP], sW[C * KP], sM[C * NS];
+  __shared__ float sdO[C * BP], sdS[K * BP], sdD[C * BP], sE[K];
+  const int vs = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, v0 = vs * BV;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  f32x4 dS[STW];
+#pragma unroll
+  for (int u = 0; u < STW; ++u) {
+    const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+      const float x = dht ? dht[((int64_t)bh * K + i) * V + v0 + vv] : 0.f;
+      dS[u][j] = x;
+      sdS[i * BP + vv] = x;
+    }
+  }
+  for (int n = NT - 1; n >= 0; --n) {
+    const int t0 = n * C, L = min(C, T - t0);
+    for (int e = tid; e < C * K; e += 256) {
+      const int c = e / K, i = e - c * K;
+      float a = 0.f, qv = 0.f, wv = 0.f;
+      if (c < L) {
+        const int64_t o = bht(bh, t0 + c, T, K) + i;
+        a = Kf[o];
+        qv = Qg[o];
+        wv = W[o];
+      }
+      sKf[c * KP + i] = a;
+      sQg[c * KP + i] = qv;
+      sW[c * KP + i] = wv;
+    }
+    const float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
+    for (int e = tid; e < C * C; e += 256) sM[(e / C) * NS + e % C] = Mn[e];
+    for (int e = tid; e < C * BV; e += 256) {
+      const int c = e / BV, vv = e - c * BV;
+      sdO[c * BP + vv] = c < L ? ld(dO, bthk(b, t0 + c, h, v0 + vv, T, H, V)) : 0.f;
+    }
+    if (tid < K) sE[tid] = exp2f(gc[bthk(b, t0 + L - 1, h, tid, T, H, K)]);
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+        dhbuf[(((int64_t)bh * NT + n) * K + i) * V + v0 + vv] = dS[u][j];
+      }
+    }
+    __syncthreads();
+    // d delta = M^T dO + Kf dS
+#pragma unroll
+    for (int u = 0; u < DTW; ++u) {
+      const int tile = w * DTW + u, cb = tile / (BV / 16), vb = tile % (BV / 16);
+      f32x4 acc = zero4();
+      const int cA = 16 * cb + (lane & 15), vB = 16 * vb + (lane & 15);
+      for (int st = 4 * cb; st < C / 4; ++st) {  // M[c', c] nonzero only for c' >= c
+        const int cp = 4 * st + (lane >> 4);
+        acc = mfma4(sM[cp * NS + cA], sdO[cp * BP + vB], acc);
+      }
+#pragma unroll 8
+      for (int st = 0; st < K / 4; ++st) {
+        const int i = 4 * st + (lane >> 4);
+        acc = mfma4(sKf[cA * KP + i], sdS[i * BP + vB], acc);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 16 * cb + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+        sdD[c * BP + vv] = acc[j];
+        if (c < L) dDl[bht(bh, t0 + c, T, V) + v0 + vv] = acc[j];
+      }
+    }
+    __syncthreads();
+    // dS <- e dS + Qg^T dO - W^T d delta
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+      f32x4 acc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = sE[16 * ib + 4 * (lane >> 4) + j] * dS[u][j];
+      const int iA = 16 * ib + (lane & 15), vB = 16 * vb + (lane & 15);
+#pragma unroll 4
+      for (int st = 0; st < C / 4; ++st) {
+        const int c = 4 * st + (lane >> 4);
+        acc = mfma4(sQg[c * KP + iA], sdO[c * BP + vB], acc);
+        acc = mfma4(-sW[c * KP + iA], sdD[c * BP + vB], acc);
+      }
+      dS[u] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sdS[(16 * ib + 4 * (lane >> 4) + j) * BP + 16 * vb + (lane & 15)] = dS[u][j];
+    }
+  }
+  if (dh0) {
+#pragma unroll
+    for (int u = 0; u < STW; ++u) {
+      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
+        dh0[((int64_t)bh * K + i) * V + v0 + vv] = dS[u][j];
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// Backward: products with the chunk's entry state h and exit-state gradient dh.
+// ===========================================================================
+template <int K, int V, typename TDO>
+__global__ __launch_bounds__(256) void mem_bwd_hgrad_kernel(
+    const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
+    const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ gc, int T, int H, int NT,
+    float* __restrict__ dQg, float* __restrict__ dW, float* __restrict__ dKf, float* __restrict__ dMg,
+    float* __restrict__ dgl) {
+  constexpr int VP = V + 4;
+  __shared__ float sH[K * VP], sX[C * VP], sY[C * VP];
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const float* hn = hbuf + ((int64_t)bh * NT + n) * K * V;
+  const float* dhn = dhbuf + ((int64_t)bh * NT + n) * K * V;
+  // phase 1: sH = h, sX = dO, sY = d delta
+  for (int e = tid; e < K * V; e += 256) sH[(e / V) * VP + e % V] = hn[e];
+  for (int e = tid; e < C * V; e += 256) {
+    const int c = e / V, vv = e - c * V;
+    const bool ok = c < L;
+    sX[c * VP + vv] = ok ? ld(dO, bthk(b, t0 + c, h, vv, T, H, V)) : 0.f;
+    sY[c * VP + vv] = ok ? dDl[bht(bh, t0 + c, T, V) + vv] : 0.f;
+  }
+  __syncthreads();
+  constexpr int NTL = (C / 16) * (K / 16);
+  for (int tile = w; tile < 2 * NTL; tile += 4) {
+    const bool second = tile >= NTL;
+    const int tt = second ? tile - NTL : tile;
+    const int cb = tt / (K / 16), ib = tt % (K / 16);
+    const float* sA_ = second ? sY : sX;
+    f32x4 acc = zero4();
+    const int cA = 16 * cb + (lane & 15), iB = 16 * ib + (lane & 15);
+#pragma unroll 8
+    for (int st = 0; st < V / 4; ++st) {
+      const int vv = 4 * st + (lane >> 4);
+      acc = mfma4(sA_[cA * VP + vv], sH[iB * VP + vv], acc);
+    }
+    float* dst = second ? dW : dQg;
+    const float sg = second ? -1.f : 1.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 16 * cb + 4 * (lane >> 4) + j;
+      if (c < L) dst[bht(bh, t0 + c, T, K) + iB] = sg * acc[j];
+    }
+  }
+  __syncthreads();
+  // phase 2: sH = dh, sY = delta (sX keeps dO)
+  for (int e = tid; e < K * V; e += 256) sH[(e / V) * VP + e % V] = dhn[e];
+  for (int e = tid; e < C * V; e += 256) {
+    const int c = e / V, vv = e - c * V;
+    sY[c * VP + vv] = c < L ? Dl[bht(bh, t0 + c, T, V) + vv] : 0.f;
+  }
+  __syncthreads();
+  // dKf = delta dh^T  (C x K)
+  for (int tile = w; tile < NTL; tile += 4) {
+    const int cb = tile / (K / 16), ib = tile % (K / 16);
+    f32x4 acc = zero4();
+    const int cA = 16 * cb + (lane & 15), iB = 16 * ib + (lane & 15);
+#pragma unroll 8
+    for (int st = 0; st < V / 4; ++st) {
+      const int vv = 4 * st + (lane >> 4);
+      acc = mfma4(sY[cA * VP + vv], sH[iB * VP + vv], acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 16 * cb + 4 * (lane >> 4) + j;
+      if (c < L) dKf[bht(bh, t0 + c, T, K) + iB] = acc[j];
+    }
+  }
+  // dM = dO delta^T (lower incl. diagonal), zeros above
+  float* dMn = dMg + ((int64_t)bh * NT + n) * C * C;
+  for (int tile = w; tile < 16; tile += 4) {
+    const int I = tile >> 2, J = tile & 3;
+    f32x4 acc = zero4();
+    if (J <= I) {
+      const int cA = 16 * I + (lane & 15), sB = 16 * J + (lane & 15);
+#pragma unroll 8
+      for (int st = 0; st < V / 4; ++st) {
+        const int vv = 4 * st + (lane >> 4);
+        acc = mfma4(sX[cA * VP + vv], sY[sB * VP + vv], acc);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 16 * I + 4 * (lane >> 4) + j, s = 16 * J + (lane & 15);
+      dMn[c * C + s] = (s <= c) ? acc[j] : 0.f;
+    }
+  }
+  // g_last term: e^{g_last,i} sum_v h[i][v] dh[i][v]
+  if (tid < K) {
+    const int i = tid;
+    float sacc = 0.f;
+    for (int vv = 0; vv < V; ++vv) sacc += hn[(int64_t)i * V + vv] * sH[i * VP + vv];
+    dgl[((int64_t)bh * NT + n) * K + i] = sacc * exp2f(gc[bthk(b, t0 + L - 1, h, i, T, H, K)]);
+  }
+}
+
+// ===========================================================================
+// Backward: transposed triangular solves and dN.
+// ===========================================================================
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_bwd_solve_kernel(
+    const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
+    const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
+    const float* __restrict__ W, int T, int H, int NT, bf16_t* __restrict__ dv, float* __restrict__ dKg,
+    float* __restrict__ dNg) {
+  constexpr int KP = K + 4;
+  constexpr int XP = V + K + 4;
+  // phase 1: sK | sA | sG (3 x C x KP); phase 2 (after the solve) reuses it as sX | sUW (2 x C x XP)
+  constexpr int P1 = 3 * C * KP, P2 = 2 * C * XP;
+  constexpr int R1 = P1 > P2 ? P1 : P2;
+  __shared__ float sBuf[R1];
+  __shared__ __attribute__((aligned(16))) float sN[C * NS];
+  __shared__ float sSpan[4];
+  float* sK = sBuf;
+  float* sA = sBuf + C * KP;
+  float* sG = sBuf + 2 * C * KP;
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  stage_chunk<K, ISO, float>(nullptr, k, kap, gc, b, h, T, H, t0, L, (float*)nullptr, sK, sA, sG, sSpan);
+  build_NM<K, false, false>(nullptr, sK, sA, sG, sSpan, 0.f, sN, nullptr);
+  __syncthreads();  // sK / sA / sG are dead from here on; sX reuses their space
+  float* sX = sBuf;
+  float* sUW = sBuf + C * XP;
+  // back substitution (I+N)^T X = [d delta | dW], thread = column; 16-row blocks, last first
+  if (tid < V + K) {
+    const int j = tid;
+    const bool isV = j < V;
+    const int col = isV ? j : j - V;
+#pragma unroll 1
+    for (int I = 3; I >= 0; --I) {
+      float acc[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 16 * I + r;
+        float x = 0.f;
+        if (c < L) x = isV ? dDl[bht(bh, t0 + c, T, V) + col] : dWg[bht(bh, t0 + c, T, K) + col];
+        acc[r] = x;
+      }
+#pragma unroll 1
+      for (int s = 16 * (I + 1); s < C; ++s) {
+        const float xs = sX[s * XP + j];
+        const float4* nrow = reinterpret_cast<const float4*>(sN + s * NS + 16 * I);
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 nv = nrow[r4];
+          acc[4 * r4 + 0] -= nv.x * xs;
+          acc[4 * r4 + 1] -= nv.y * xs;
+          acc[4 * r4 + 2] -= nv.z * xs;
+          acc[4 * r4 + 3] -= nv.w * xs;
+        }
+      }
+#pragma unroll
+      for (int r = 14; r >= 0; --r) {
+#pragma unroll
+        for (int r2 = r + 1; r2 < 16; ++r2) acc[r] -= sN[(16 * I + r2) * NS + 16 * I + r] * acc[r2];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 16 * I + r;
+        sX[c * XP + j] = acc[r];
+        if (c < L) {
+          if (isV) dv[bthk(b, t0 + c, h, col, T, H, V)] = f2bf(acc[r]);
+          else dKg[bht(bh, t0 + c, T, K) + col] = acc[r];
+        }
+      }
+    }
+  }
+  // stage [U | W] rows for dN
+  for (int e = tid; e < C * (V + K); e += 256) {
+    const int c = e / (V + K), jj = e - c * (V + K);
+    float xv = 0.f;
+    if (c < L) xv = jj < V ? U[bht(bh, t0 + c, T, V) + jj] : W[bht(bh, t0 + c, T, K) + jj - V];
+    sUW[c * XP + jj] = xv;
+  }
+  __syncthreads();
+  // dN = -(X [U|W]^T), strictly lower
+  float* dNn = dNg + ((int64_t)bh * NT + n) * C * C;
+  for (int tile = w; tile < 16; tile += 4) {
+    const int I = tile >> 2, J = tile & 3;
+    f32x4 acc = zero4();
+    if (J <= I) {
+      const int cA = 16 * I + (lane & 15), sB = 16 * J + (lane & 15);
+#pragma unroll 8
+      for (int st = 0; st < (V + K) / 4; ++st) {
+        const int jj = 4 * st + (lane >> 4);
+        acc = mfma4(sX[cA * XP + jj], sUW[sB * XP + jj], acc);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int c = 16 * I + 4 * (lane >> 4) + jj, s = 16 * J + (lane & 15);
+      dNn[c * C + s] = (s < c) ? -acc[jj] : 0.f;
+    }
+  }
+}
+
+// ===========================================================================
+// Backward: gradients of q, k, kappa (beta) and g from dN, dM and elementwise factors.
+// Output tile (row block I, 16 channels); lane holds rows 16I + 4(lane/16) + j.
+// ===========================================================================
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
+    const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
+    const float* __restrict__ dgl, int T, int H, int NT, float scale, bf16_t* __restrict__ dq,
+    bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg) {
+  constexpr int KP = K + 4;
+  constexpr int NCT = K / 16;  // channel tiles
+  __shared__ bf16_t sQ[C * KP], sK[C * KP];  // bf16 inputs are exact in bf16
+  __shared__ float sA[C * KP], sG[C * KP];
+  __shared__ float sDN[C * NS], sDM[C * NS];
+  __shared__ float sSpan[4];
+  __shared__ float sColPart[4 * K];     // per row block partial of sum_c dKf kappa e^{g_last - g}
+  __shared__ float sDgLast[K];          // dg of row L-1 before the g_last terms
+  __shared__ float sBetaPart[C * NCT];  // iso: per (row, channel tile) partial of sum_i dkappa k
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  stage_chunk<K, ISO, bf16_t>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
+  {
+    const float* dNn = dNg + ((int64_t)bh * NT + n) * C * C;
+    const float* dMn = dMg + ((int64_t)bh * NT + n) * C * C;
+    for (int e = tid; e < C * C; e += 256) {
+      sDN[(e / C) * NS + e % C] = dNn[e];
+      sDM[(e / C) * NS + e % C] = dMn[e];
+    }
+  }
+  for (int e = tid; e < 4 * K; e += 256) sColPart[e] = 0.f;
+  __syncthreads();
+  const int rowL = L - 1;
+  for (int tile = w; tile < 4 * NCT; tile += 4) {
+    const int I = tile / NCT, ct = tile % NCT;
+    const int a = 16 * I;
+    const bool fast = sSpan[I] <= kSpanMax;
+    const int ich = 16 * ct + (lane & 15);  // this lane's output channel
+    // ---- row-oriented: dk_N and dq_M (unscaled), anchor a ----
+    f32x4 accK = zero4(), accQ = zero4();
+    {
+      const int cA = a + (lane & 15);
+      const int nJ = fast ? I + 1 : I;
+      for (int J = 0; J < nJ; ++J) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int s = 16 * J + 4 * st + (lane >> 4);
+          const float br = sA[s * KP + ich] * exp2f(sG[a * KP + ich] - sG[s * KP + ich]);
+          accK = mfma4(sDN[cA * NS + s], br, accK);
+          accQ = mfma4(sDM[cA * NS + s], br, accQ);
+        }
+      }
+    }
+    // ---- column-oriented: dkappa_N, dkappa_M ----
+    f32x4 accK2 = zero4(), accQ2 = zero4(), accK2d = zero4(), accQ2d = zero4();
+    {
+      const int sA_ = a + (lane & 15);  // output row (as source index s)
+      if (I < 3) {
+        const int bnc = 16 * (I + 1);
+        for (int Ip = I + 1; Ip < 4; ++Ip) {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            const int c = 16 * Ip + 4 * st + (lane >> 4);
+            const float f = exp2f(sG[c * KP + ich] - sG[bnc * KP + ich]);
+            accK2 = mfma4(sDN[c * NS + sA_], lds_f(sK, c * KP + ich) * f, accK2);
+            accQ2 = mfma4(sDM[c * NS + sA_], lds_f(sQ, c * KP + ich) * f, accQ2);
+          }
+        }
+      }
+      if (fast) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int c = a + 4 * st + (lane >> 4);
+          const float f = exp2f(sG[c * KP + ich] - sG[a * KP + ich]);
+          accK2d = mfma4(sDN[c * NS + sA_], lds_f(sK, c * KP + ich) * f, accK2d);
+          accQ2d = mfma4(sDM[c * NS + sA_], lds_f(sQ, c * KP + ich) * f, accQ2d);
+        }
+      }
+    }
+    // ---- assemble ----
+    const int bnc = I < 3 ? 16 * (I + 1) : a;
+    const float ga = sG[a * KP + ich], gb = sG[bnc * KP + ich], glast = sG[rowL * KP + ich];
+    float colpart = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = a + 4 * (lane >> 4) + j;
+      const float gcv = sG[c * KP + ich];
+      const float kc = lds_f(sK, c * KP + ich), qc = lds_f(sQ, c * KP + ich), ac = sA[c * KP + ich];
+      float dkN, dqM, dkapN, dkapM;
+      if (fast) {
+        const float el = exp2f(gcv - ga);
+        dkN = accK[j] * el;
+        dqM = accQ[j] * el;
+        const float er = exp2f(ga - gcv);
+        dkapN = accK2[j] * exp2f(gb - gcv) + accK2d[j] * er;
+        dkapM = accQ2[j] * exp2f(gb - gcv) + accQ2d[j] * er;
+      } else {
+        const float el = exp2f(gcv - ga);
+        dkN = accK[j] * el;
+        dqM = accQ[j] * el;
+        dkapN = I < 3 ? accK2[j] * exp2f(gb - gcv) : 0.f;
+        dkapM = I < 3 ? accQ2[j] * exp2f(gb - gcv) : 0.f;
+        // exact diagonal block
+        for (int s = a; s < a + 16; ++s) {
+          const float gs = sG[s * KP + ich];
+          if (s <= c) {
+            const float e = exp2f(gcv - gs) * sA[s * KP + ich];
+            if (s < c) dkN += sDN[c * NS + s] * e;
+            dqM += sDM[c * NS + s] * e;
+          }
+          if (s >= c) {
+            const float e = exp2f(gs - gcv);
+            if (s > c) dkapN += sDN[s * NS + c] * lds_f(sK, s * KP + ich) * e;
+            dkapM += sDM[s * NS + c] * lds_f(sQ, s * KP + ich) * e;
+          }
+        }
+      }
+      dqM *= scale;
+      dkapM *= scale;
+      float dkv = dkN, dqv = dqM, dav = dkapN + dkapM, dgv = 0.f;
+      if (c < L) {
+        const int64_t o = bht(bh, t0 + c, T, K) + ich;
+        const float ec = exp2f(gcv);
+        const float f = exp2f(glast - gcv);
+        const float dkg = dKg[o], dqg = dQg[o], dkf = dKf[o];
+        dkv += dkg * ec;
+        dqv += scale * dqg * ec;
+        dav += dkf * f;
+        dgv = dkg * kc * ec + dqg * scale * qc * ec - dkf * ac * f;
+        colpart += dkf * ac * f;
+        dgv += kc * dkN - ac * dkapN + qc * dqM - ac * dkapM;
+      }
+      if (c < L) {
+        if (ISO) {
+          // kappa = beta k:  dk += beta dkappa;  dbeta = sum_i dkappa_i k_i (reduced below).
+          // Lanes sharing (lane >> 4) hold the same row, so the 16-lane reduction stays in one branch.
+          const float bc = kap[((int64_t)b * T + t0 + c) * H + h];
+          dkv += bc * dav;
+          float part = dav * kc;
+          // reduce over the 16 channels of this tile (lanes sharing lane>>4)
+#pragma unroll
+          for (int o2 = 1; o2 < 16; o2 <<= 1) part += __shfl_xor(part, o2, 64);
+          if ((lane & 15) == 0) sBetaPart[c * NCT + ct] = part;
+        } else {
+          dkap[bthk(b, t0 + c, h, ich, T, H, K)] = dav;
+        }
+        dq[bthk(b, t0 + c, h, ich, T, H, K)] = f2bf(dqv);
+        dk[bthk(b, t0 + c, h, ich, T, H, K)] = f2bf(dkv);
+        if (c == rowL) sDgLast[ich] = dgv;
+        else dg[bthk(b, t0 + c, h, ich, T, H, K)] = dgv;
+      }
+    }
+    // column partial of the g_last term over this lane's 4 rows, then over the 4 row groups
+    colpart += __shfl_xor(colpart, 16, 64);
+    colpart += __shfl_xor(colpart, 32, 64);
+    if (lane < 16) sColPart[I * K + ich] = colpart;
+  }
+  __syncthreads();
+  if (tid < K) {
+    const int i = tid;
+    const float extra = dgl[((int64_t)bh * NT + n) * K + i] + sColPart[i] + sColPart[K + i] + sColPart[2 * K + i] +
+                        sColPart[3 * K + i];
+    dg[bthk(b, t0 + rowL, h, i, T, H, K)] = sDgLast[i] + extra;
+  }
+  if (ISO && tid < L) {
+    float s = 0.f;
+    for (int ct = 0; ct < NCT; ++ct) s += sBetaPart[tid * NCT + ct];
+    dbeta[((int64_t)b * T + t0 + tid) * H + h] = s;
+  }
+}
+
+inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// saved-buffer layout (floats), TT = B*H*T, NB = B*H*NT
+struct MemLayout {
+  int64_t U, W, Kf, Qg, M, h, D, total;
+  MemLayout(int B, int T, int H, int K, int V) {
+    const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
+    U = 0;
+    W = U + TT * V;
+    Kf = W + TT * K;
+    Qg = Kf + TT * K;
+    M = Qg + TT * K;
+    h = M + NB * C * C;
+    D = h + NB * K * V;
+    total = D + TT * V;
+  }
+};
+struct BwdLayout {
+  int64_t dh, dD, dQg, dW, dKf, dM, dgl, dKg, dN, total;
+  BwdLayout(int B, int T, int H, int K, int V) {
+    const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
+    dh = 0;
+    dD = dh + NB * K * V;
+    dQg = dD + TT * V;
+    dW = dQg + TT * K;
+    dKf = dW + TT * K;
+    dM = dKf + TT * K;
+    dgl = dM + NB * C * C;
+    dKg = dgl + NB * K;
+    dN = dKg + TT * K;
+    total = dN + NB * C * C;
+  }
+};
+
+constexpr int kBV = 32;
+
+template <int K, int V>
+int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const bf16_t* v, const float* gc, int B,
+                 int T, int H, float scale, const float* h0, float* saved, float* ht, void* o, int o_bf16,
+                 hipStream_t stream) {
+  const int NT = cdiv(T, C);
+  MemLayout lay(B, T, H, K, V);
+  float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg, *M = saved + lay.M,
+        *hb = saved + lay.h, *D = saved + lay.D;
+  dim3 gchunk(NT, B * H);
+  if (iso)
+    hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H, NT,
+                       scale, U, W, Kf, Qg, M);
+  else
+    hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H, NT,
+                       scale, U, W, Kf, Qg, M);
+  KDN_CHECK_LAUNCH();
+  hipLaunchKernelGGL((mem_state_fwd_kernel<K, V, kBV>), dim3(V / kBV, B * H), dim3(256), 0, stream, U, W, Kf, gc, h0,
+                     T, H, NT, hb, D, ht);
+  KDN_CHECK_LAUNCH();
+  if (o_bf16)
+    hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, bf16_t>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
+                       (bf16_t*)o);
+  else
+    hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, float>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
+                       (float*)o);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+template <int K, int V, typename TDO>
+int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const float* gc, int B, int T, int H,
+                 float scale, const TDO* dO, const float* dht, const float* saved, float* work, bf16_t* dq,
+                 bf16_t* dk, float* dkap, float* dbeta, bf16_t* dv, float* dg, float* dh0, hipStream_t stream) {
+  const int NT = cdiv(T, C);
+  MemLayout lay(B, T, H, K, V);
+  BwdLayout bl(B, T, H, K, V);
+  const float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg,
+              *M = saved + lay.M, *hb = saved + lay.h, *D = saved + lay.D;
+  float *dh = work + bl.dh, *dD = work + bl.dD, *dQg = work + bl.dQg, *dW = work + bl.dW, *dKf = work + bl.dKf,
+        *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
+  dim3 gchunk(NT, B * H);
+  hipLaunchKernelGGL((mem_state_bwd_kernel<K, V, kBV, TDO>), dim3(V / kBV, B * H), dim3(256), 0, stream, M, Kf, Qg, W,
+                     gc, dO, dht, T, H, NT, dh, dD, dh0);
+  KDN_CHECK_LAUNCH();
+  hipLaunchKernelGGL((mem_bwd_hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H, NT,
+                     dQg, dW, dKf, dM, dgl);
+  KDN_CHECK_LAUNCH();
+  if (iso) {
+    hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, true>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W, T,
+                       H, NT, dv, dKg, dN);
+    KDN_CHECK_LAUNCH();
+    hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM, dQg,
+                       dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+  } else {
+    hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, false>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W, T,
+                       H, NT, dv, dKg, dN);
+    KDN_CHECK_LAUNCH();
+    hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM,
+                       dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+  }
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kdn_mem_chunk_size(void) { return C; }
+
+size_t kdn_mem_saved_size(int B, int T, int H, int K, int V) {
+  return (size_t)MemLayout(B, T, H, K, V).total * sizeof(float);
+}
+
+size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V) {
+  return (size_t)BwdLayout(B, T, H, K, V).total * sizeof(float);
+}
+
+int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
+                const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
+                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, hipStream_t stream) {
+  if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
+  if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
+  if (saved_bytes < kdn_mem_saved_size(B, T, H, K, V)) return KDN_ERR_ARG;
+  float* sv = (float*)saved;
+#define KDN_MEM_FWD(KK, VV) \
+  return mem_fwd_impl<KK, VV>(q, k, kappa_or_beta, iso, v, g_cumsum, B, T, H, scale, initial_state, sv, final_state, o, o_bf16, stream)
+  if (K == 128 && V == 128) KDN_MEM_FWD(128, 128);
+  if (K == 64 && V == 64) KDN_MEM_FWD(64, 64);
+  if (K == 128 && V == 64) KDN_MEM_FWD(128, 64);
+  KDN_MEM_FWD(64, 128);
+#undef KDN_MEM_FWD
+}
+
+int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const float* g_cumsum,
+                int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
+                const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
+                size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
+                float* dg, float* d_initial_state, hipStream_t stream) {
+  if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
+  if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
+  if (saved_bytes < kdn_mem_saved_size(B, T, H, K, V)) return KDN_ERR_ARG;
+  if (workspace_bytes < kdn_mem_bwd_workspace_size(B, T, H, K, V)) return KDN_ERR_ARG;
+  if (iso ? dbeta == nullptr : dkappa == nullptr) return KDN_ERR_ARG;
+  const float* sv = (const float*)saved;
+  float* wk = (float*)workspace;
+#define KDN_MEM_BWD(KK, VV)                                                                                          \
+  do {                                                                                                               \
+    if (do_bf16)                                                                                                     \
+      return mem_bwd_impl<KK, VV, bf16_t>(q, k, kappa_or_beta, iso, g_cumsum, B, T, H, scale, (const bf16_t*)d_o,   \
+                                          d_final_state, sv, wk, dq, dk, dkappa, dbeta, dv, dg, d_initial_state,     \
+                                          stream);                                                                   \
+    return mem_bwd_impl<KK, VV, float>(q, k, kappa_or_beta, iso, g_cumsum, B, T, H, scale, (const float*)d_o,       \
+                                       d_final_state, sv, wk, dq, dk, dkappa, dbeta, dv, dg, d_initial_state,        \
+                                       stream);                                                                      \
+  } while (0)
+  if (K == 128 && V == 128) KDN_MEM_BWD(128, 128);
+  if (K == 64 && V == 64) KDN_MEM_BWD(64, 64);
+  if (K == 128 && V == 64) KDN_MEM_BWD(128, 64);
+  KDN_MEM_BWD(64, 128);
+#undef KDN_MEM_BWD
+}
+
+}  // extern "C"

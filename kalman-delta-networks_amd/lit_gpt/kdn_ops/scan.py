@@ -1,0 +1,37 @@
+"""The KDN mixer scan: the kdn_ops calls of one layer, composed as the reference layers do.
+
+``iso_kdn_scan`` follows lit_gpt/iso_kdn.py:277-304 (gate frontend -> scalar gain ->
+chunked memory scan with in-op q/k normalisation); ``diag_kdn_scan`` follows
+lit_gpt/diag_kdn.py:315-345 (q/k normalisation -> frontend -> vector gain -> memory scan,
+output materialised at v's dtype).  Projections, short convolutions and the gated output
+norm of the layers are not part of the scan.
+"""
+from __future__ import annotations
+
+import torch
+
+from .diag_kdn_chunk import _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain, _diag_kdn_normalize, chunk_kalman
+from .iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
+
+
+def iso_kdn_scan(q, k, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param,
+                 *, omega_min: float = 0.0, r_min: float = 0.01, info_scale: float | None = None):
+    """q, k, v, g_raw [B,T,H,d]; omega_r_raw [B,T,2H]; dt_bias [H*K]; returns o [B,T,H,V]."""
+    K = q.shape[-1]
+    g_cumsum, a, omega, r, mu = _iso_kdn_gate_precumsum_paired(
+        g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param, omega_min, r_min)
+    beta = iso_kdn_gain(a, omega, r, mu, head_dim=K, out_dtype=torch.float32,
+                        info_scale=float(K) if info_scale is None else info_scale)
+    return _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=beta)
+
+
+def diag_kdn_scan(q, k, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param):
+    """q, k, v, retention_raw, omega_raw [B,T,H,d] bf16; r_raw [B,T,H]; dt_bias [H,K];
+    returns o [B,T,H,V] in v's dtype."""
+    K = q.shape[-1]
+    q_memory, k_gain, k_memory = _diag_kdn_normalize(q, k)
+    g_cumsum, alpha, omega, r, mu = _diag_kdn_frontend_precumsum_paired(
+        retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param)
+    kappa = _diag_kdn_gain(k_gain, alpha, omega, r, mu, omega_raw, r_raw)
+    out = chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, float(K ** -0.5))
+    return out.to(v.dtype)

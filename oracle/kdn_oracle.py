@@ -305,6 +305,11 @@ def softplus(x):
     return F.softplus(x)
 
 
+def _w(x):
+    """Working precision: fp64 stays fp64, anything else computes in fp32."""
+    return x if x.dtype == torch.float64 else x.float()
+
+
 def l2norm_fla(x, eps: float = 1e-6):
     """x * rsqrt(sum x^2 + eps) over the last dim (FLA l2norm_fwd; parity unpinned)."""
     return x * torch.rsqrt(x.square().sum(-1, keepdim=True) + eps)
@@ -332,14 +337,14 @@ def iso_gate_frontend(g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu
     mu = 0.1 + softplus(mu_param).  Returns (g_log, g_cumsum_base2, a, omega, r, mu).
     """
     B, T, H, K = g_raw.shape
-    x = g_raw.float() + dt_bias.float().view(H, K)
-    g = -A_log.float().exp().view(H, 1) * softplus(x)
+    x = _w(g_raw) + _w(dt_bias).view(H, K)
+    g = -_w(A_log).exp().view(H, 1) * softplus(x)
     gc = chunk_local_prefix(g, chunk) * LOG2E
     a = (2.0 * g).exp().mean(-1)
-    orr = omega_r_raw.float()
-    omega = omega_min + softplus(orr[..., :H] + omega_bias.float())
-    r = r_min + softplus(orr[..., H:] + r_bias.float())
-    mu = 0.1 + softplus(mu_param.float())
+    orr = _w(omega_r_raw)
+    omega = omega_min + softplus(orr[..., :H] + _w(omega_bias))
+    r = r_min + softplus(orr[..., H:] + _w(r_bias))
+    mu = 0.1 + softplus(_w(mu_param))
     return g, gc, a, omega, r, mu
 
 
@@ -352,14 +357,15 @@ def diag_frontend(retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, chu
     Returns (l_mem, g_cumsum_base2, alpha, omega, r, mu).
     """
     B, T, H, K = retention_raw.shape
-    x = retention_raw.float() + dt_bias.float().view(H, K)
-    ell = -A_log.float().exp().view(H, 1) * softplus(x)
+    x = _w(retention_raw) + _w(dt_bias).view(H, K)
+    ell = -_w(A_log).exp().view(H, 1) * softplus(x)
     alpha = ell.exp()
-    l_mem = alpha.clamp_min(1e-6).log()
+    # memory path: log(max(alpha, 1e-6)), i.e. ell itself unless alpha is below the floor
+    l_mem = torch.where(alpha >= 1e-6, ell, torch.full_like(ell, math.log(1e-6)))
     gc = chunk_local_prefix(l_mem, chunk) * LOG2E
-    omega = softplus(omega_raw.float())
-    r = 0.01 + softplus(r_raw.float())
-    mu = 0.1 + softplus(mu_param.float())
+    omega = softplus(_w(omega_raw))
+    r = 0.01 + softplus(_w(r_raw))
+    mu = 0.1 + softplus(_w(mu_param))
     return l_mem, gc, alpha, omega, r, mu
 
 
@@ -378,8 +384,8 @@ def iso_mixer(q_raw, k_raw, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt
     K = q_raw.shape[-1]
     g, _gc, a, omega, r, mu = iso_gate_frontend(g_raw, omega_r_raw, omega_bias, r_bias, A_log,
                                                 dt_bias, mu_param, omega_min, r_min)
-    qn = l2norm_fla(q_raw.float())
-    kn = l2norm_fla(k_raw.float())
+    qn = l2norm_fla(_w(q_raw))
+    kn = l2norm_fla(_w(k_raw))
     alpha = g.exp()
     # Gain on the production scalars: beta = z / (r + z) with unit-norm keys.
     B, T, H, _ = q_raw.shape
@@ -393,7 +399,7 @@ def iso_mixer(q_raw, k_raw, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt
     beta = torch.stack(betas, 1)
     sc = K ** -0.5 if scale is None else scale
     mem = memory_chunked_wy if chunked else memory_tokenwise
-    o, _ = mem(qn, kn, v.float(), alpha, beta[..., None] * kn, scale=sc)
+    o, _ = mem(qn, kn, _w(v), alpha, beta[..., None] * kn, scale=sc)
     return o
 
 
@@ -406,8 +412,8 @@ def diag_mixer(q_raw, k_raw, v, retention_raw, omega_raw, r_raw, A_log, dt_bias,
     gain consumes the unclamped alpha (diag_kdn_chunk.py:1887-1898).
     """
     K = q_raw.shape[-1]
-    qn = diag_normalize(q_raw.float())
-    kn = diag_normalize(k_raw.float())
+    qn = diag_normalize(_w(q_raw))
+    kn = diag_normalize(_w(k_raw))
     l_mem, _gc, alpha, omega, r, mu = diag_frontend(retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param)
     prec = mu if initial_precision is None else initial_precision
     gain = diag_gain_mobius if chunked else diag_gain_tokenwise
@@ -415,7 +421,7 @@ def diag_mixer(q_raw, k_raw, v, retention_raw, omega_raw, r_raw, A_log, dt_bias,
                         output_final_state=True)
     sc = K ** -0.5 if scale is None else scale
     mem = memory_chunked_wy if chunked else memory_tokenwise
-    o, S = mem(qn, kn, v.float(), l_mem.exp(), kappa, scale=sc, initial_state=initial_state)
+    o, S = mem(qn, kn, _w(v), l_mem.exp(), kappa, scale=sc, initial_state=initial_state)
     if output_final_state:
         return o, (S, fprec)
     return o

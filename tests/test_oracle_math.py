@@ -135,11 +135,11 @@ def test_iso_gate_frontend_special_points():
     g, gc, a, omega, r, mu = ko.iso_gate_frontend(
         g_raw, orr, torch.zeros(H), torch.zeros(H), torch.zeros(H), torch.zeros(H * K),
         torch.zeros(H), omega_min=0.25, r_min=0.01)
-    torch.testing.assert_close(g, -x.float(), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(g, -x, rtol=1e-6, atol=1e-6)
     # chunk restart at t = 64: the prefix at the first token of a chunk is that token's gate
     torch.testing.assert_close(gc[:, 64] * math.log(2), g[:, 64], rtol=1e-6, atol=1e-6)
     torch.testing.assert_close((gc[:, 1:64] - gc[:, :63]) * math.log(2), g[:, 1:64], rtol=1e-5, atol=1e-5)
-    torch.testing.assert_close(a, torch.exp(-2 * x.float()).mean(-1), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(a, torch.exp(-2 * x).mean(-1), rtol=1e-6, atol=1e-6)
     torch.testing.assert_close(omega, torch.full_like(omega, 0.25 + math.log(2)))
     torch.testing.assert_close(r, torch.full_like(r, 0.01 + math.log(2)))
     torch.testing.assert_close(mu, torch.full_like(mu, 0.1 + math.log(2)))
