@@ -1,0 +1,197 @@
+#!/usr/bin/env python
+"""Benchmark of the KDN mixer scan on one MI355X (BASELINE.json metric).
+
+A step is one forward + backward of the KDN mixer scan of one layer (gate/frontend ->
+Kalman gain -> chunked memory scan, gradients for every input and parameter) at
+B=4, H=18, T=4096, d_k=d_v=128, bf16 inputs with fp32 state, on synthetic data resident
+in HBM.  The headline line is iso_kdn; the diag_kdn figure (config 2)
+is reported alongside under "also".  Kernels are timed with HIP events recorded on their
+launch stream inside the timed region; the dominant kernel's roofline is reported against
+MI355X peaks.  The CPU baseline times the oracle's tokenwise recurrence (fp32, autograd)
+on a bounded sample of (b, h) slices on the host cores.
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--variant iso|diag] [--cpu-slices 8]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "kalman-delta-networks_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "KDN mixer fwd+bwd tokens/s at B4 H18 T4096 d128 bf16; % MFMA/HBM peak"
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # dense fp32 (the scan's MFMA path computes in fp32)
+C = 64
+
+
+def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
+    """Algorithmic HBM bytes and FLOPs per launch of each kernel (inputs read once, outputs
+    written once, no recompute).  N = B*T*H token-heads; per-token-head figures times N."""
+    N = B * T * H
+    kap_in = 4 * K if variant == "diag" else 4           # kappa fp32 [K] or beta fp32
+    dkap_out = 4 * K if variant == "diag" else 4
+    do_b = 4 * V if variant == "diag" else 2 * V         # diag output cotangent is fp32
+    h_b = 4 * K * V / C                                   # one fp32 state per chunk
+    mm = C * C / C * 4                                    # one fp32 C x C matrix per chunk
+    per = {
+        # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M
+        "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + mm,
+                          2 * (C * K + C * (V + K) / 2)),
+        # U, W, Kf, g_last -> h, delta
+        "mem_state_fwd": (4 * V + 8 * K + h_b + 4 * V, 2 * 2 * K * V),
+        # Qg, h, M, delta -> o
+        "mem_output_fwd": (4 * K + h_b + mm + 4 * V + (2 if variant == "iso" else 4) * V,
+                           2 * (K * V + C * V / 2)),
+        # M, Kf, Qg, W, dO -> dh, d delta
+        "mem_state_bwd": (mm + 12 * K + do_b + h_b + 4 * V, 2 * (C * V / 2 + 3 * K * V)),
+        # h, dh, delta, d delta, dO -> dQg, dW, dKf, dM
+        "mem_bwd_hgrad": (2 * h_b + 8 * V + do_b + 12 * K + mm, 2 * (3 * K * V + C * V / 2)),
+        # k, kappa, g, d delta, dW, U, W -> dv, dKg, dN
+        "mem_bwd_solve": (2 * K + kap_in + 4 * K + 4 * V + 4 * K + 4 * V + 4 * K + 2 * V + 4 * K + mm,
+                          2 * (C * K / 2 + C * (V + K) / 2 + C * (V + K) / 2)),
+        # q, k, kappa, g, dN, dM, dQg, dKg, dKf -> dq, dk, dkappa, dg
+        "mem_bwd_contrib": (4 * K + kap_in + 4 * K + 2 * mm + 12 * K + 4 * K + dkap_out + 4 * K,
+                            2 * 2 * (C * K)),
+    }
+    return {k: (b * N, f * N) for k, (b, f) in per.items()}
+
+
+def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K: int):
+    import torch
+
+    from lit_gpt.kdn_ops import _lib
+    from lit_gpt.kdn_ops.scan import diag_kdn_scan, iso_kdn_scan
+    from lit_gpt.kdn_ops.synthetic import GRAD_KEYS, make_inputs
+
+    dev = torch.device("cuda:0")
+    inputs, do = make_inputs(variant, B, T, H, K, seed=0, device=dev)
+    leaves = {k: x.requires_grad_(True) for k, x in inputs.items()}
+    keys = [k for k in GRAD_KEYS[variant]]
+    fn = iso_kdn_scan if variant == "iso" else diag_kdn_scan
+
+    def step():
+        o = fn(**leaves)
+        grads = torch.autograd.grad(o, [leaves[k] for k in keys], grad_outputs=do)
+        return grads
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with _lib.KernelTimer() as timer:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / steps
+    kernel_ms = {tag: timer.mean_ms(tag) for tag in timer.tags()}
+    counts = kernel_counts(variant, B, T, H, K, K)
+    per_kernel = {}
+    for tag, (nbytes, flops) in counts.items():
+        t = kernel_ms.get(tag, float("nan")) * 1e-3
+        t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+        t_mfma = flops / (FP32_PEAK_TFLOPS * 1e12)
+        bound = "hbm" if t_hbm >= t_mfma else "mfma"
+        if bound == "hbm":
+            achieved, peak, unit = nbytes / t / 1e9, HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved, peak, unit = flops / t / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
+        per_kernel[tag] = dict(ms=round(t * 1e3, 4), bound=bound, achieved=round(achieved, 2), peak=peak,
+                               unit=unit, frac=round(achieved / peak, 4), alg_bytes=int(nbytes), alg_flops=int(flops))
+    dominant = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
+    return dict(ms_per_step=ms, tokens_per_s=B * T / (ms * 1e-3), kernels=per_kernel, dominant=dominant)
+
+
+def cpu_baseline(variant: str, slices: int, T: int, K: int, B: int, H: int):
+    """Oracle tokenwise recurrence (fp32, torch autograd) fwd+bwd on `slices` (b, h) slices."""
+    import torch
+
+    from lit_gpt.kdn_ops.synthetic import GRAD_KEYS, make_inputs
+    from oracle import kdn_oracle as ko
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    names = {"q": "q_raw", "k": "k_raw", "initial_precision_param": "mu_param"}
+    mixer = ko.iso_mixer if variant == "iso" else ko.diag_mixer
+    t_total = 0.0
+    for s in range(slices):
+        inputs, do = make_inputs(variant, 1, T, 1, K, seed=100 + s, device="cpu", dtype=torch.float32)
+        leaves = {k: x.requires_grad_(True) for k, x in inputs.items()}
+        t0 = time.perf_counter()
+        o = mixer(**{names.get(k, k): x for k, x in leaves.items()})
+        torch.autograd.grad(o, [leaves[k] for k in GRAD_KEYS[variant]], grad_outputs=do)
+        t_total += time.perf_counter() - t0
+    per_slice = t_total / slices
+    tokens_per_s = B * T / (per_slice * B * H)
+    return dict(value=round(tokens_per_s, 2), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{slices} of {B * H} (b,h) slices at T={T}, d={K}: oracle tokenwise fp32 fwd+bwd "
+                       f"(autograd), {per_slice:.2f} s/slice, extrapolated to the {B}x{H} job")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--variant", choices=("iso", "diag"), default="iso")
+    ap.add_argument("--cpu-slices", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--B", type=int, default=4)
+    ap.add_argument("--T", type=int, default=4096)
+    ap.add_argument("--H", type=int, default=18)
+    ap.add_argument("--d", type=int, default=128)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build runs the KDN scan on a single GPU "
+              "(every (b, h) stream is independent; multi-GPU sharding is not part of this build). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    B, T, H, K = args.B, args.T, args.H, args.d
+    main_v = args.variant
+    other = "diag" if main_v == "iso" else "iso"
+    res = run_variant(main_v, args.steps, args.warmup, B, T, H, K)
+    res_other = run_variant(other, args.steps, args.warmup, B, T, H, K)
+    dom = res["kernels"][res["dominant"]]
+    line = {
+        "metric": METRIC,
+        "value": round(res["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": f"{main_v}_kdn mixer scan fwd+bwd (frontend+gain+chunked memory, all input grads)",
+                   "B": B, "T": T, "H": H, "d_k": K, "d_v": K, "chunk": C, "inputs": "bf16",
+                   "state": "fp32", "parallelism": "single GPU"},
+        "roofline": {"kernel": res["dominant"], "bound": dom["bound"], "achieved": dom["achieved"],
+                     "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"], "traffic": None},
+        "kernels": res["kernels"],
+        "also": {f"{other}_kdn": {"value": round(res_other["tokens_per_s"], 1), "unit": "tokens/s",
+                                  "ms_per_step": round(res_other["ms_per_step"], 4),
+                                  "dominant": res_other["dominant"],
+                                  "kernels": res_other["kernels"]}},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(main_v, args.cpu_slices, T, K, B, H)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -119,19 +119,24 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
  * iso=0, kappa_or_beta = kappa [B,T,H,K] f32).  q, k (normalised), v are bf16; o is bf16 or f32.
  * initial_state / final_state [B,H,K,V] f32 are nullable (state carry; the reference oracle's
  * initial_memory / output_final_state, iso_kdn_naive.py:376-440).  `saved` receives the
- * intermediates the backward consumes (kdn_mem_saved_size bytes). */
+ * intermediates the backward consumes (kdn_mem_saved_size bytes).  `stages` selects kernels
+ * (bit 0 intra-chunk WY build, bit 1 state pass, bit 2 readout; -1 = all) so that a caller can
+ * launch and time them one at a time; the stages must run in this order. */
 int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
                 const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
-                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, hipStream_t stream);
+                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, int stages,
+                hipStream_t stream);
 /* Backward: replaces _chunk_kda_bwd_precum (iso_kdn_chunk.py:2089-2187) and
  * _DiagKdnMemoryFunction.backward (diag_kdn_chunk.py:3258-3312).  dq, dk, dv bf16; dkappa
  * [B,T,H,K] f32 (diag) or dbeta [B,T,H] f32 (iso); dg [B,T,H,K] f32 in natural-log coordinates,
- * not reverse-summed.  d_final_state / d_initial_state nullable. */
+ * not reverse-summed.  d_final_state / d_initial_state nullable.  `stages`: bit 0 reverse state
+ * pass, bit 1 state-gradient products, bit 2 transposed solves, bit 3 q/k/kappa/gate gradients
+ * (-1 = all, in this order). */
 int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const float* g_cumsum,
                 int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
-                float* dg, float* d_initial_state, hipStream_t stream);
+                float* dg, float* d_initial_state, int stages, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -948,36 +948,43 @@ constexpr int kBV = 32;
 template <int K, int V>
 int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const bf16_t* v, const float* gc, int B,
                  int T, int H, float scale, const float* h0, float* saved, float* ht, void* o, int o_bf16,
-                 hipStream_t stream) {
+                 int stages, hipStream_t stream) {
   const int NT = cdiv(T, C);
   MemLayout lay(B, T, H, K, V);
   float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg, *M = saved + lay.M,
         *hb = saved + lay.h, *D = saved + lay.D;
   dim3 gchunk(NT, B * H);
-  if (iso)
-    hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H, NT,
-                       scale, U, W, Kf, Qg, M);
-  else
-    hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H, NT,
-                       scale, U, W, Kf, Qg, M);
-  KDN_CHECK_LAUNCH();
-  hipLaunchKernelGGL((mem_state_fwd_kernel<K, V, kBV>), dim3(V / kBV, B * H), dim3(256), 0, stream, U, W, Kf, gc, h0,
-                     T, H, NT, hb, D, ht);
-  KDN_CHECK_LAUNCH();
-  if (o_bf16)
-    hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, bf16_t>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
-                       (bf16_t*)o);
-  else
-    hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, float>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
-                       (float*)o);
-  KDN_CHECK_LAUNCH();
+  if (stages & 1) {
+    if (iso)
+      hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H, NT,
+                         scale, U, W, Kf, Qg, M);
+    else
+      hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H,
+                         NT, scale, U, W, Kf, Qg, M);
+    KDN_CHECK_LAUNCH();
+  }
+  if (stages & 2) {
+    hipLaunchKernelGGL((mem_state_fwd_kernel<K, V, kBV>), dim3(V / kBV, B * H), dim3(256), 0, stream, U, W, Kf, gc,
+                       h0, T, H, NT, hb, D, ht);
+    KDN_CHECK_LAUNCH();
+  }
+  if (stages & 4) {
+    if (o_bf16)
+      hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, bf16_t>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
+                         (bf16_t*)o);
+    else
+      hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, float>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
+                         (float*)o);
+    KDN_CHECK_LAUNCH();
+  }
   return 0;
 }
 
 template <int K, int V, typename TDO>
 int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const float* gc, int B, int T, int H,
                  float scale, const TDO* dO, const float* dht, const float* saved, float* work, bf16_t* dq,
-                 bf16_t* dk, float* dkap, float* dbeta, bf16_t* dv, float* dg, float* dh0, hipStream_t stream) {
+                 bf16_t* dk, float* dkap, float* dbeta, bf16_t* dv, float* dg, float* dh0, int stages,
+                 hipStream_t stream) {
   const int NT = cdiv(T, C);
   MemLayout lay(B, T, H, K, V);
   BwdLayout bl(B, T, H, K, V);
@@ -986,26 +993,34 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   float *dh = work + bl.dh, *dD = work + bl.dD, *dQg = work + bl.dQg, *dW = work + bl.dW, *dKf = work + bl.dKf,
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
-  hipLaunchKernelGGL((mem_state_bwd_kernel<K, V, kBV, TDO>), dim3(V / kBV, B * H), dim3(256), 0, stream, M, Kf, Qg, W,
-                     gc, dO, dht, T, H, NT, dh, dD, dh0);
-  KDN_CHECK_LAUNCH();
-  hipLaunchKernelGGL((mem_bwd_hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H, NT,
-                     dQg, dW, dKf, dM, dgl);
-  KDN_CHECK_LAUNCH();
-  if (iso) {
-    hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, true>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W, T,
-                       H, NT, dv, dKg, dN);
+  if (stages & 1) {
+    hipLaunchKernelGGL((mem_state_bwd_kernel<K, V, kBV, TDO>), dim3(V / kBV, B * H), dim3(256), 0, stream, M, Kf, Qg,
+                       W, gc, dO, dht, T, H, NT, dh, dD, dh0);
     KDN_CHECK_LAUNCH();
-    hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM, dQg,
-                       dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
-  } else {
-    hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, false>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W, T,
-                       H, NT, dv, dKg, dN);
-    KDN_CHECK_LAUNCH();
-    hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM,
-                       dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
   }
-  KDN_CHECK_LAUNCH();
+  if (stages & 2) {
+    hipLaunchKernelGGL((mem_bwd_hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H,
+                       NT, dQg, dW, dKf, dM, dgl);
+    KDN_CHECK_LAUNCH();
+  }
+  if (stages & 4) {
+    if (iso)
+      hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, true>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W,
+                         T, H, NT, dv, dKg, dN);
+    else
+      hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, false>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W,
+                         T, H, NT, dv, dKg, dN);
+    KDN_CHECK_LAUNCH();
+  }
+  if (stages & 8) {
+    if (iso)
+      hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM,
+                         dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+    else
+      hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM,
+                         dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+    KDN_CHECK_LAUNCH();
+  }
   return 0;
 }
 
@@ -1025,13 +1040,15 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V) {
 
 int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
                 const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
-                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, hipStream_t stream) {
+                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, int stages,
+                hipStream_t stream) {
   if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
   if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
   if (saved_bytes < kdn_mem_saved_size(B, T, H, K, V)) return KDN_ERR_ARG;
   float* sv = (float*)saved;
 #define KDN_MEM_FWD(KK, VV) \
-  return mem_fwd_impl<KK, VV>(q, k, kappa_or_beta, iso, v, g_cumsum, B, T, H, scale, initial_state, sv, final_state, o, o_bf16, stream)
+  return mem_fwd_impl<KK, VV>(q, k, kappa_or_beta, iso, v, g_cumsum, B, T, H, scale, initial_state, sv, final_state, o, \
+                              o_bf16, stages, stream)
   if (K == 128 && V == 128) KDN_MEM_FWD(128, 128);
   if (K == 64 && V == 64) KDN_MEM_FWD(64, 64);
   if (K == 128 && V == 64) KDN_MEM_FWD(128, 64);
@@ -1043,7 +1060,7 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
                 int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
-                float* dg, float* d_initial_state, hipStream_t stream) {
+                float* dg, float* d_initial_state, int stages, hipStream_t stream) {
   if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
   if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
   if (saved_bytes < kdn_mem_saved_size(B, T, H, K, V)) return KDN_ERR_ARG;
@@ -1056,10 +1073,10 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
     if (do_bf16)                                                                                                     \
       return mem_bwd_impl<KK, VV, bf16_t>(q, k, kappa_or_beta, iso, g_cumsum, B, T, H, scale, (const bf16_t*)d_o,   \
                                           d_final_state, sv, wk, dq, dk, dkappa, dbeta, dv, dg, d_initial_state,     \
-                                          stream);                                                                   \
+                                          stages, stream);                                                                   \
     return mem_bwd_impl<KK, VV, float>(q, k, kappa_or_beta, iso, g_cumsum, B, T, H, scale, (const float*)d_o,       \
                                        d_final_state, sv, wk, dq, dk, dkappa, dbeta, dv, dg, d_initial_state,        \
-                                       stream);                                                                      \
+                                       stages, stream);                                                                      \
   } while (0)
   if (K == 128 && V == 128) KDN_MEM_BWD(128, 128);
   if (K == 64 && V == 64) KDN_MEM_BWD(64, 64);

@@ -34,8 +34,8 @@ _SIGS = {
     "kdn_mem_chunk_size": "",
     "kdn_mem_saved_size": "iiiii",
     "kdn_mem_bwd_workspace_size": "iiiii",
-    "kdn_mem_fwd": "pppippiiiiifppzppis",
-    "kdn_mem_bwd": "pppipiiiiifpippzpzppppppps",
+    "kdn_mem_fwd": "pppippiiiiifppzppiis",
+    "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppis",
 }
 _SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_diag_frontend_bwd_workspace_size",
              "kdn_diag_gain_workspace_size", "kdn_mem_saved_size", "kdn_mem_bwd_workspace_size"}
@@ -81,9 +81,49 @@ def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def call(name: str, *args):
+class KernelTimer:
+    """Records HIP events on the launching stream around every tagged C call while active.
+
+    Used by the benchmark to time individual kernels inside the timed region."""
+
+    def __init__(self):
+        self.events: dict[str, list] = {}
+
+    def __enter__(self):
+        global _timer
+        _timer = self
+        return self
+
+    def __exit__(self, *exc):
+        global _timer
+        _timer = None
+        return False
+
+    def mean_ms(self, tag: str) -> float:
+        pairs = self.events.get(tag, [])
+        if not pairs:
+            return float("nan")
+        torch.cuda.synchronize()
+        return sum(s.elapsed_time(e) for s, e in pairs) / len(pairs)
+
+    def tags(self):
+        return tuple(self.events)
+
+
+_timer: KernelTimer | None = None
+
+
+def call(name: str, *args, tag: str | None = None):
     lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = getattr(lib, name)
+    if _timer is not None and tag is not None:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        rc = fn(*args)
+        end.record()
+        _timer.events.setdefault(tag, []).append((start, end))
+    else:
+        rc = fn(*args)
     if rc != 0:
         raise RuntimeError(f"{name} failed with code {rc}"
                            + (" (invalid argument)" if rc == -1 else " (HIP error)"))

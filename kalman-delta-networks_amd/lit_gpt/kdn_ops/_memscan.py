@@ -1,0 +1,60 @@
+"""Stage-by-stage launch of the chunked memory scan (kdn_mem_fwd / kdn_mem_bwd).
+
+Each stage is one kernel; launching them separately lets KernelTimer attribute time to
+kernels.  Shared by the iso (kappa = beta k) and diag (explicit kappa) operators.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+FWD_STAGES = ((1, "mem_intra_fwd"), (2, "mem_state_fwd"), (4, "mem_output_fwd"))
+BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_hgrad"), (4, "mem_bwd_solve"), (8, "mem_bwd_contrib"))
+
+
+def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
+            output_final_state=False, out_dtype=torch.float32):
+    """q, k, v bf16 [B,T,H,*]; kappa [B,T,H,K] f32 (diag) or beta [B,T,H] f32 (iso).
+    Returns (o, saved, final_state or None)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dev = q.device
+    saved = torch.empty((_lib.size("kdn_mem_saved_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
+    o = torch.empty((B, T, H, V), device=dev, dtype=out_dtype)
+    ht = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if output_final_state else None
+    h0 = initial_state.float().contiguous() if initial_state is not None else None
+    stream = _lib.stream_of(q)
+    for bit, tag in FWD_STAGES:
+        _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(v),
+                  _lib.ptr(g_cumsum), B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(),
+                  _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), bit, stream, tag=tag)
+    return o, saved, ht
+
+
+def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do, *, d_final_state=None,
+            need_initial_state_grad=False):
+    """Returns (dq bf16, dk bf16, dv bf16, dkappa f32 [B,T,H,K] or dbeta f32 [B,T,H],
+    dg f32 natural-log not reverse-summed, d_initial_state or None)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dev = q.device
+    ws = torch.empty((_lib.size("kdn_mem_bwd_workspace_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
+    dq = torch.empty((B, T, H, K), device=dev, dtype=torch.bfloat16)
+    dk = torch.empty_like(dq)
+    dv = torch.empty((B, T, H, V), device=dev, dtype=torch.bfloat16)
+    dkap = torch.empty((B, T, H) if iso else (B, T, H, K), device=dev, dtype=torch.float32)
+    dg = torch.empty((B, T, H, K), device=dev, dtype=torch.float32)
+    dh0 = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if need_initial_state_grad else None
+    dht = d_final_state.float().contiguous() if d_final_state is not None else None
+    if do.dtype not in (torch.bfloat16, torch.float32):
+        do = do.float()
+    do = do.contiguous()
+    stream = _lib.stream_of(q)
+    for bit, tag in BWD_STAGES:
+        _lib.call("kdn_mem_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(g_cumsum),
+                  B, T, H, K, V, float(scale), _lib.ptr(do), _lib.is_bf16(do), _lib.ptr(dht), _lib.ptr(saved),
+                  saved.numel(), _lib.ptr(ws), ws.numel(), _lib.ptr(dq), _lib.ptr(dk),
+                  None if iso else _lib.ptr(dkap), _lib.ptr(dkap) if iso else None, _lib.ptr(dv), _lib.ptr(dg),
+                  _lib.ptr(dh0), bit, stream, tag=tag)
+    return dq, dk, dv, dkap, dg, dh0

@@ -26,7 +26,7 @@ import math
 import torch
 from torch.autograd.function import once_differentiable
 
-from . import _lib
+from . import _lib, _memscan
 
 _DIAG_KDN_MEMORY_CHUNK_SIZE = 64
 _DIAG_KDN_VECTOR_DTYPE = torch.bfloat16
@@ -349,17 +349,9 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, kappa, v, g_cumsum, scale, initial_state, output_final_state):
-        B, T, H, K = q.shape
-        V = v.shape[-1]
-        dev = q.device
-        saved = torch.empty((_lib.size("kdn_mem_saved_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
-        o = torch.empty((B, T, H, V), device=dev, dtype=torch.float32)
-        ht = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if output_final_state else None
-        h0 = initial_state.float().contiguous() if initial_state is not None else None
-        with torch.cuda.device(dev):
-            _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa), 0, _lib.ptr(v), _lib.ptr(g_cumsum),
-                      B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(), _lib.ptr(ht),
-                      _lib.ptr(o), 0, _lib.stream_of(q))
+        with torch.cuda.device(q.device):
+            o, saved, ht = _memscan.mem_fwd(q, k, kappa, False, v, g_cumsum, scale, initial_state=initial_state,
+                                            output_final_state=output_final_state, out_dtype=torch.float32)
         ctx.save_for_backward(q, k, kappa, v, g_cumsum, saved)
         ctx.scale = scale
         ctx.has_h0 = initial_state is not None
@@ -378,20 +370,11 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
         V = v.shape[-1]
         dev = q.device
         do = torch.zeros((B, T, H, V), device=dev, dtype=torch.float32) if do is None else do.float().contiguous()
-        dht = d_final_state.float().contiguous() if d_final_state is not None else None
-        ws = torch.empty((_lib.size("kdn_mem_bwd_workspace_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
-        dq = torch.empty((B, T, H, K), device=dev, dtype=torch.bfloat16)
-        dk = torch.empty_like(dq)
-        dv = torch.empty((B, T, H, V), device=dev, dtype=torch.bfloat16)
-        dkappa = torch.empty((B, T, H, K), device=dev, dtype=torch.float32)
-        dg = torch.empty((B, T, H, K), device=dev, dtype=torch.float32)
         need_h0 = ctx.has_h0 and ctx.needs_input_grad[6]
-        dh0 = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if need_h0 else None
         with torch.cuda.device(dev):
-            _lib.call("kdn_mem_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa), 0, _lib.ptr(g_cumsum), B, T, H, K, V,
-                      float(ctx.scale), _lib.ptr(do), 0, _lib.ptr(dht), _lib.ptr(saved), saved.numel(), _lib.ptr(ws),
-                      ws.numel(), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dkappa), None, _lib.ptr(dv), _lib.ptr(dg),
-                      _lib.ptr(dh0), _lib.stream_of(q))
+            dq, dk, dv, dkappa, dg, dh0 = _memscan.mem_bwd(q, k, kappa, False, v, g_cumsum, saved, ctx.scale, do,
+                                                          d_final_state=d_final_state,
+                                                          need_initial_state_grad=need_h0)
         return dq, dk, dkappa, dv, dg, None, dh0, None
 
 

@@ -19,7 +19,7 @@ from numbers import Real
 
 import torch
 
-from . import _lib
+from . import _lib, _memscan
 
 ISO_GATE_CHUNK_SIZE = 64
 KDA_CHUNK_SIZE = 64
@@ -322,42 +322,16 @@ def _l2norm_bwd(x, rstd, dy):
 
 def _chunk_kda_fwd_precum(q, k, v, g_cumsum, beta, scale, *, initial_state=None, output_final_state=False,
                           out_dtype=torch.bfloat16):
-    """Memory scan forward on normalised bf16 q, k (reference :2037-2086)."""
-    B, T, H, K = q.shape
-    V = v.shape[-1]
-    dev = q.device
-    saved = torch.empty((_lib.size("kdn_mem_saved_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
-    o = torch.empty((B, T, H, V), device=dev, dtype=out_dtype)
-    ht = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if output_final_state else None
-    h0 = initial_state.float().contiguous() if initial_state is not None else None
-    _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(beta), 1, _lib.ptr(v), _lib.ptr(g_cumsum),
-              B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(), _lib.ptr(ht),
-              _lib.ptr(o), _lib.is_bf16(o), _lib.stream_of(q))
-    return o, saved, ht
+    """Memory scan forward on normalised bf16 q, k (reference :2037-2086); kappa = beta k."""
+    return _memscan.mem_fwd(q, k, beta, True, v, g_cumsum, scale, initial_state=initial_state,
+                            output_final_state=output_final_state, out_dtype=out_dtype)
 
 
 def _chunk_kda_bwd_precum(q, k, v, g_cumsum, beta, saved, scale, do, *, d_final_state=None,
                           need_initial_state_grad=False):
     """Memory scan backward (reference :2089-2187): natural-log dg, no reverse cumsum."""
-    B, T, H, K = q.shape
-    V = v.shape[-1]
-    dev = q.device
-    ws = torch.empty((_lib.size("kdn_mem_bwd_workspace_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
-    dq = torch.empty((B, T, H, K), device=dev, dtype=torch.bfloat16)
-    dk = torch.empty_like(dq)
-    dv = torch.empty((B, T, H, V), device=dev, dtype=torch.bfloat16)
-    db = torch.empty((B, T, H), device=dev, dtype=torch.float32)
-    dg = torch.empty((B, T, H, K), device=dev, dtype=torch.float32)
-    dh0 = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if need_initial_state_grad else None
-    dht = d_final_state.float().contiguous() if d_final_state is not None else None
-    if do.dtype not in (torch.bfloat16, torch.float32):
-        do = do.float()
-    do = do.contiguous()
-    _lib.call("kdn_mem_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(beta), 1, _lib.ptr(g_cumsum), B, T, H, K, V,
-              float(scale), _lib.ptr(do), _lib.is_bf16(do), _lib.ptr(dht), _lib.ptr(saved), saved.numel(),
-              _lib.ptr(ws), ws.numel(), _lib.ptr(dq), _lib.ptr(dk), None, _lib.ptr(db), _lib.ptr(dv),
-              _lib.ptr(dg), _lib.ptr(dh0), _lib.stream_of(q))
-    return dq, dk, dv, db, dg, dh0
+    return _memscan.mem_bwd(q, k, beta, True, v, g_cumsum, saved, scale, do, d_final_state=d_final_state,
+                            need_initial_state_grad=need_initial_state_grad)
 
 
 class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
