@@ -14,9 +14,9 @@
 //
 // Kernels (grid = one workgroup per chunk unless noted, 256 threads = 4 waves):
 //   intra_fwd    N/M (MFMA, anchored), forward substitution for U, W; Kf, Qg
-//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h); S slice in VGPRs
+//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h) (kdn_state.h)
 //   output_fwd   O = Qg h + M delta
-//   state_bwd    serial reverse: d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
+//   state_bwd    serial reverse (kdn_state.h): d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
 //   bwd_hgrad    dQg = dO h^T, dW = -d delta h^T, dKf = delta dh^T, dM = dO delta^T, g_last terms
 //   bwd_solve    dV = (I+N)^-T d delta, dKg = (I+N)^-T dW, dN = -(dV U^T + dKg W^T)
 //   bwd_contrib  dq, dk, dkappa (or dbeta), dg from dN, dM and the elementwise factors
@@ -28,6 +28,7 @@
 // is <= 86 (base 2, no overflow); otherwise an exact per-element path runs.
 // Products use fp32 MFMA (v_mfma_f32_16x16x4_f32), fp32 accumulate.
 #include "kdn_common.h"
+#include "kdn_state.h"
 #include "../../include/kdn.h"
 
 namespace {
@@ -58,38 +59,90 @@ __device__ __forceinline__ int64_t bht(int bh, int t, int T, int D) { return ((i
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float lds_f(const float* p, int i) { return p[i]; }
 __device__ __forceinline__ float lds_f(const bf16_t* p, int i) { return bf2f(p[i]); }
-__device__ __forceinline__ void lds_put(float* p, int i, float x) { p[i] = x; }
-__device__ __forceinline__ void lds_put(bf16_t* p, int i, float x) { p[i] = f2bf(x); }  // exact for bf16 inputs
+
+// Copy a [ROWS x D] fp32 tile (row r at src + r * stride; rows >= L read as zero) into LDS
+// dst[r * DP + col] with 16-byte loads, all issued before any store.
+template <int ROWS, int D, int DP>
+__device__ __forceinline__ void stage_f32(const float* __restrict__ src, int64_t stride, int L, float* dst) {
+  constexpr int D4 = D / 4, N4 = ROWS * D4, PER = (N4 + 255) / 256;
+  static_assert(DP % 4 == 0, "16-byte aligned LDS rows");
+  float4 v[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + 256 * u, r = e / D4, c4 = e % D4;
+    v[u] = (e < N4 && r < L) ? *reinterpret_cast<const float4*>(src + r * stride + 4 * c4) : float4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + 256 * u, r = e / D4, c4 = e % D4;
+    if (e < N4) *reinterpret_cast<float4*>(dst + r * DP + 4 * c4) = v[u];
+  }
+}
+
+// Copy a [ROWS x D] bf16 tile into LDS as fp32 (DP % 4 == 0) or as bf16 (DP % 8 == 0).
+template <int ROWS, int D, int DP, typename TD>
+__device__ __forceinline__ void stage_bf16(const bf16_t* __restrict__ src, int64_t stride, int L, TD* dst) {
+  constexpr int D8 = D / 8, N8 = ROWS * D8, PER = (N8 + 255) / 256;
+  uint4 v[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + 256 * u, r = e / D8, c8 = e % D8;
+    v[u] = (e < N8 && r < L) ? *reinterpret_cast<const uint4*>(src + r * stride + 8 * c8) : uint4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + 256 * u, r = e / D8, c8 = e % D8;
+    if (e >= N8) continue;
+    if constexpr (sizeof(TD) == 2) {
+      static_assert(DP % 8 == 0, "16-byte aligned LDS rows");
+      *reinterpret_cast<uint4*>(dst + r * DP + 8 * c8) = v[u];
+    } else {
+      static_assert(DP % 4 == 0, "16-byte aligned LDS rows");
+      const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      float f[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f[2 * q] = __uint_as_float(w4[q] << 16);
+        f[2 * q + 1] = __uint_as_float(w4[q] & 0xffff0000u);
+      }
+      *reinterpret_cast<float4*>(dst + r * DP + 8 * c8) = float4{f[0], f[1], f[2], f[3]};
+      *reinterpret_cast<float4*>(dst + r * DP + 8 * c8 + 4) = float4{f[4], f[5], f[6], f[7]};
+    }
+  }
+}
+
+// LDS row stride of the staged q / k arrays: K + 4 floats or K + 8 bf16 (16-byte rows).
+template <int K, typename TQK>
+struct QKStride {
+  static constexpr int value = sizeof(TQK) == 2 ? K + 8 : K + 4;
+};
 
 template <int K, bool ISO, typename TQK>
 __device__ void stage_chunk(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
                             const float* __restrict__ gc, int b, int h, int T, int H, int t0, int L, TQK* sQ,
                             TQK* sK, float* sA, float* sG, float* sSpan) {
   constexpr int KP = K + 4;
+  constexpr int KQ = QKStride<K, TQK>::value;
   const int tid = threadIdx.x;
-  for (int e = tid; e < C * K; e += 256) {
-    const int c = e / K, i = e - c * K;
-    float kv = 0.f, qv = 0.f, av = 0.f, gv = 0.f;
-    if (c < L) {
-      const int64_t o = bthk(b, t0 + c, h, i, T, H, K);
-      kv = bf2f(k[o]);
-      if (sQ) qv = bf2f(q[o]);
-      gv = gc[o];  // base-2 chunk-local prefix; all decays below are exp2 of differences
-      av = ISO ? kap[((int64_t)b * T + t0 + c) * H + h] * kv : kap[o];
-    }
-    lds_put(sK, c * KP + i, kv);
-    if (sQ) lds_put(sQ, c * KP + i, qv);
-    sA[c * KP + i] = av;
-    sG[c * KP + i] = gv;
-  }
+  const int64_t base = (((int64_t)b * T + t0) * H + h) * K, stride = (int64_t)H * K;
+  stage_f32<C, K, KP>(gc + base, stride, L, sG);  // base-2 chunk-local prefix
+  if (!ISO) stage_f32<C, K, KP>(kap + base, stride, L, sA);
+  stage_bf16<C, K, KQ>(k + base, stride, L, sK);
+  if (sQ) stage_bf16<C, K, KQ>(q + base, stride, L, sQ);
   __syncthreads();
-  if (L < C) {
+  if (ISO) {  // kappa = beta k
+    for (int e = tid; e < C * K; e += 256) {
+      const int c = e / K, i = e - c * K;
+      sA[c * KP + i] = c < L ? kap[((int64_t)b * T + t0 + c) * H + h] * lds_f(sK, c * KQ + i) : 0.f;
+    }
+  }
+  if (L < C) {  // g rows past the end repeat the last token's prefix
     for (int e = tid; e < (C - L) * K; e += 256) {
       const int c = L + e / K, i = e % K;
       sG[c * KP + i] = sG[(L - 1) * KP + i];
     }
-    __syncthreads();
   }
+  __syncthreads();
   // span of block w (= wave w): max_i,r |g[16w][i] - g[16w + r][i]|
   {
     const int w = tid >> 6, lane = tid & 63;
@@ -183,7 +236,7 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_kernel(
   constexpr int XP = V + K + 4;
   // sQ | sA are dead after Kf / Qg are written and are then reused for the solve's sX [C][XP]
   constexpr int OFF2 = (2 * C * KP > C * XP) ? 2 * C * KP : C * XP;
-  __shared__ float sBuf[OFF2 + 2 * C * KP];
+  __shared__ __attribute__((aligned(16))) float sBuf[OFF2 + 2 * C * KP];
   __shared__ __attribute__((aligned(16))) float sN[C * NS];  // transposed: sN[s * NS + c] = N[c][s]
   __shared__ float sSpan[4];
   float* sQ = sBuf;
@@ -254,123 +307,6 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_kernel(
 }
 
 // ===========================================================================
-// Forward state pass.  grid (V / BV, B*H); S slice [K][BV] kept in MFMA accumulators.
-// ===========================================================================
-template <int K, int V, int BV>
-__global__ __launch_bounds__(256) void mem_state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
-                                                            const float* __restrict__ Kf, const float* __restrict__ gc,
-                                                            const float* __restrict__ h0, int T, int H, int NT,
-                                                            float* __restrict__ hbuf, float* __restrict__ Dl,
-                                                            float* __restrict__ ht) {
-  constexpr int KP = K + 4, BP = BV + 4;
-  constexpr int NST = (K / 16) * (BV / 16);  // S tiles
-  constexpr int STW = NST / 4;               // S tiles per wave
-  constexpr int NDT = (C / 16) * (BV / 16);  // delta tiles
-  constexpr int DTW = NDT / 4;
-  static_assert(NST % 4 == 0 && NDT % 4 == 0, "tile split");
-  __shared__ float sW[C * KP], sKf[C * KP], sS[K * BP], sD[C * BP], sE[K];
-  const int vs = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, v0 = vs * BV;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  f32x4 S[STW];
-  // initial state
-#pragma unroll
-  for (int u = 0; u < STW; ++u) {
-    const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-      const float x = h0 ? h0[((int64_t)bh * K + i) * V + v0 + vv] : 0.f;
-      S[u][j] = x;
-      sS[i * BP + vv] = x;
-    }
-  }
-  for (int n = 0; n < NT; ++n) {
-    const int t0 = n * C, L = min(C, T - t0);
-    // stage W, Kf, e^{g_last}
-    for (int e = tid; e < C * K; e += 256) {
-      const int c = e / K, i = e - c * K;
-      float wv = 0.f, kv = 0.f;
-      if (c < L) {
-        const int64_t o = bht(bh, t0 + c, T, K) + i;
-        wv = W[o];
-        kv = Kf[o];
-      }
-      sW[c * KP + i] = wv;
-      sKf[c * KP + i] = kv;
-    }
-    if (tid < K) sE[tid] = exp2f(gc[bthk(b, t0 + L - 1, h, tid, T, H, K)]);
-    // h_n = S (S is already in sS from the previous step)
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-        hbuf[(((int64_t)bh * NT + n) * K + i) * V + v0 + vv] = S[u][j];
-      }
-    }
-    __syncthreads();
-    // delta = U - W S
-#pragma unroll
-    for (int u = 0; u < DTW; ++u) {
-      const int tile = w * DTW + u, cb = tile / (BV / 16), vb = tile % (BV / 16);
-      f32x4 acc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = 16 * cb + 4 * (lane >> 4) + j;
-        acc[j] = c < L ? U[bht(bh, t0 + c, T, V) + v0 + 16 * vb + (lane & 15)] : 0.f;
-      }
-      const int cA = 16 * cb + (lane & 15), vB = 16 * vb + (lane & 15);
-#pragma unroll 8
-      for (int st = 0; st < K / 4; ++st) {
-        const int i = 4 * st + (lane >> 4);
-        acc = mfma4(-sW[cA * KP + i], sS[i * BP + vB], acc);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = 16 * cb + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-        sD[c * BP + vv] = acc[j];
-        if (c < L) Dl[bht(bh, t0 + c, T, V) + v0 + vv] = acc[j];
-      }
-    }
-    __syncthreads();
-    // S = e ⊙ S + Kf^T delta
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-      f32x4 acc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = sE[16 * ib + 4 * (lane >> 4) + j] * S[u][j];
-      const int iA = 16 * ib + (lane & 15), vB = 16 * vb + (lane & 15);
-#pragma unroll 4
-      for (int st = 0; st < C / 4; ++st) {
-        const int c = 4 * st + (lane >> 4);
-        acc = mfma4(sKf[c * KP + iA], sD[c * BP + vB], acc);
-      }
-      S[u] = acc;
-    }
-    __syncthreads();  // everyone done reading sS / sD / sW / sKf
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sS[(16 * ib + 4 * (lane >> 4) + j) * BP + 16 * vb + (lane & 15)] = S[u][j];
-    }
-  }
-  if (ht) {
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-        ht[((int64_t)bh * K + i) * V + v0 + vv] = S[u][j];
-      }
-    }
-  }
-}
-
-// ===========================================================================
 // Forward readout: O = Qg h + M delta.  grid (NT, B*H).
 // ===========================================================================
 template <int K, int V, typename TO>
@@ -378,22 +314,14 @@ __global__ __launch_bounds__(256) void mem_output_fwd_kernel(const float* __rest
                                                              const float* __restrict__ Mg, const float* __restrict__ Dl,
                                                              int T, int H, int NT, TO* __restrict__ o) {
   constexpr int KP = K + 4, VP = V + 4;
-  __shared__ float sQg[C * KP], sH[K * VP], sM[C * NS], sD[C * VP];
+  __shared__ __attribute__((aligned(16))) float sQg[C * KP], sH[K * VP], sM[C * NS], sD[C * VP];
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int e = tid; e < C * K; e += 256) {
-    const int c = e / K, i = e - c * K;
-    sQg[c * KP + i] = c < L ? Qg[bht(bh, t0 + c, T, K) + i] : 0.f;
-  }
-  const float* hn = hbuf + ((int64_t)bh * NT + n) * K * V;
-  for (int e = tid; e < K * V; e += 256) sH[(e / V) * VP + e % V] = hn[e];
-  const float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
-  for (int e = tid; e < C * C; e += 256) sM[(e / C) * NS + e % C] = Mn[e];
-  for (int e = tid; e < C * V; e += 256) {
-    const int c = e / V, vv = e - c * V;
-    sD[c * VP + vv] = c < L ? Dl[bht(bh, t0 + c, T, V) + vv] : 0.f;
-  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  stage_f32<C, K, KP>(Qg + bht(bh, t0, T, K), K, L, sQg);
+  stage_f32<K, V, VP>(hbuf + ((int64_t)bh * NT + n) * K * V, V, K, sH);
+  stage_f32<C, C, NS>(Mg + ((int64_t)bh * NT + n) * C * C, C, C, sM);
+  stage_f32<C, V, VP>(Dl + bht(bh, t0, T, V), V, L, sD);
   __syncthreads();
   constexpr int NTL = (C / 16) * (V / 16);
   for (int tile = w; tile < NTL; tile += 4) {
@@ -418,126 +346,6 @@ __global__ __launch_bounds__(256) void mem_output_fwd_kernel(const float* __rest
 }
 
 // ===========================================================================
-// Backward state pass (reverse).  grid (V / BV, B*H).
-// ===========================================================================
-template <int K, int V, int BV, typename TDO>
-__global__ __launch_bounds__(256) void mem_state_bwd_kernel(
-    const float* __restrict__ Mg, const float* __restrict__ Kf, const float* __restrict__ Qg,
-    const float* __restrict__ W, const float* __restrict__ gc, const TDO* __restrict__ dO,
-    const float* __restrict__ dht, int T, int H, int NT, float* __restrict__ dhbuf, float* __restrict__ dDl,
-    float* __restrict__ dh0) {
-  constexpr int KP = K + 4, BP = BV + 4;
-  constexpr int NST = (K / 16) * (BV / 16), STW = NST / 4;
-  constexpr int NDT = (C / 16) * (BV / 16), DTW = NDT / 4;
-  __shared__ float sKf[C * KP], sQg[C * KP], sW[C * KP], sM[C * NS];
-  __shared__ float sdO[C * BP], sdS[K * BP], sdD[C * BP], sE[K];
-  const int vs = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, v0 = vs * BV;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  f32x4 dS[STW];
-#pragma unroll
-  for (int u = 0; u < STW; ++u) {
-    const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-      const float x = dht ? dht[((int64_t)bh * K + i) * V + v0 + vv] : 0.f;
-      dS[u][j] = x;
-      sdS[i * BP + vv] = x;
-    }
-  }
-  for (int n = NT - 1; n >= 0; --n) {
-    const int t0 = n * C, L = min(C, T - t0);
-    for (int e = tid; e < C * K; e += 256) {
-      const int c = e / K, i = e - c * K;
-      float a = 0.f, qv = 0.f, wv = 0.f;
-      if (c < L) {
-        const int64_t o = bht(bh, t0 + c, T, K) + i;
-        a = Kf[o];
-        qv = Qg[o];
-        wv = W[o];
-      }
-      sKf[c * KP + i] = a;
-      sQg[c * KP + i] = qv;
-      sW[c * KP + i] = wv;
-    }
-    const float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
-    for (int e = tid; e < C * C; e += 256) sM[(e / C) * NS + e % C] = Mn[e];
-    for (int e = tid; e < C * BV; e += 256) {
-      const int c = e / BV, vv = e - c * BV;
-      sdO[c * BP + vv] = c < L ? ld(dO, bthk(b, t0 + c, h, v0 + vv, T, H, V)) : 0.f;
-    }
-    if (tid < K) sE[tid] = exp2f(gc[bthk(b, t0 + L - 1, h, tid, T, H, K)]);
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-        dhbuf[(((int64_t)bh * NT + n) * K + i) * V + v0 + vv] = dS[u][j];
-      }
-    }
-    __syncthreads();
-    // d delta = M^T dO + Kf dS
-#pragma unroll
-    for (int u = 0; u < DTW; ++u) {
-      const int tile = w * DTW + u, cb = tile / (BV / 16), vb = tile % (BV / 16);
-      f32x4 acc = zero4();
-      const int cA = 16 * cb + (lane & 15), vB = 16 * vb + (lane & 15);
-      for (int st = 4 * cb; st < C / 4; ++st) {  // M[c', c] nonzero only for c' >= c
-        const int cp = 4 * st + (lane >> 4);
-        acc = mfma4(sM[cp * NS + cA], sdO[cp * BP + vB], acc);
-      }
-#pragma unroll 8
-      for (int st = 0; st < K / 4; ++st) {
-        const int i = 4 * st + (lane >> 4);
-        acc = mfma4(sKf[cA * KP + i], sdS[i * BP + vB], acc);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = 16 * cb + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-        sdD[c * BP + vv] = acc[j];
-        if (c < L) dDl[bht(bh, t0 + c, T, V) + v0 + vv] = acc[j];
-      }
-    }
-    __syncthreads();
-    // dS <- e dS + Qg^T dO - W^T d delta
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-      f32x4 acc;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = sE[16 * ib + 4 * (lane >> 4) + j] * dS[u][j];
-      const int iA = 16 * ib + (lane & 15), vB = 16 * vb + (lane & 15);
-#pragma unroll 4
-      for (int st = 0; st < C / 4; ++st) {
-        const int c = 4 * st + (lane >> 4);
-        acc = mfma4(sQg[c * KP + iA], sdO[c * BP + vB], acc);
-        acc = mfma4(-sW[c * KP + iA], sdD[c * BP + vB], acc);
-      }
-      dS[u] = acc;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sdS[(16 * ib + 4 * (lane >> 4) + j) * BP + 16 * vb + (lane & 15)] = dS[u][j];
-    }
-  }
-  if (dh0) {
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / (BV / 16), vb = tile % (BV / 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 16 * ib + 4 * (lane >> 4) + j, vv = 16 * vb + (lane & 15);
-        dh0[((int64_t)bh * K + i) * V + v0 + vv] = dS[u][j];
-      }
-    }
-  }
-}
-
-// ===========================================================================
 // Backward: products with the chunk's entry state h and exit-state gradient dh.
 // ===========================================================================
 template <int K, int V, typename TDO>
@@ -547,20 +355,19 @@ __global__ __launch_bounds__(256) void mem_bwd_hgrad_kernel(
     float* __restrict__ dQg, float* __restrict__ dW, float* __restrict__ dKf, float* __restrict__ dMg,
     float* __restrict__ dgl) {
   constexpr int VP = V + 4;
-  __shared__ float sH[K * VP], sX[C * VP], sY[C * VP];
+  __shared__ __attribute__((aligned(16))) float sH[K * VP], sX[C * VP], sY[C * VP];
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const float* hn = hbuf + ((int64_t)bh * NT + n) * K * V;
   const float* dhn = dhbuf + ((int64_t)bh * NT + n) * K * V;
   // phase 1: sH = h, sX = dO, sY = d delta
-  for (int e = tid; e < K * V; e += 256) sH[(e / V) * VP + e % V] = hn[e];
-  for (int e = tid; e < C * V; e += 256) {
-    const int c = e / V, vv = e - c * V;
-    const bool ok = c < L;
-    sX[c * VP + vv] = ok ? ld(dO, bthk(b, t0 + c, h, vv, T, H, V)) : 0.f;
-    sY[c * VP + vv] = ok ? dDl[bht(bh, t0 + c, T, V) + vv] : 0.f;
-  }
+  stage_f32<K, V, VP>(hn, V, K, sH);
+  if constexpr (sizeof(TDO) == 2)
+    stage_bf16<C, V, VP>(reinterpret_cast<const bf16_t*>(dO) + bthk(b, t0, h, 0, T, H, V), (int64_t)H * V, L, sX);
+  else
+    stage_f32<C, V, VP>(reinterpret_cast<const float*>(dO) + bthk(b, t0, h, 0, T, H, V), (int64_t)H * V, L, sX);
+  stage_f32<C, V, VP>(dDl + bht(bh, t0, T, V), V, L, sY);
   __syncthreads();
   constexpr int NTL = (C / 16) * (K / 16);
   for (int tile = w; tile < 2 * NTL; tile += 4) {
@@ -585,11 +392,8 @@ __global__ __launch_bounds__(256) void mem_bwd_hgrad_kernel(
   }
   __syncthreads();
   // phase 2: sH = dh, sY = delta (sX keeps dO)
-  for (int e = tid; e < K * V; e += 256) sH[(e / V) * VP + e % V] = dhn[e];
-  for (int e = tid; e < C * V; e += 256) {
-    const int c = e / V, vv = e - c * V;
-    sY[c * VP + vv] = c < L ? Dl[bht(bh, t0 + c, T, V) + vv] : 0.f;
-  }
+  stage_f32<K, V, VP>(dhn, V, K, sH);
+  stage_f32<C, V, VP>(Dl + bht(bh, t0, T, V), V, L, sY);
   __syncthreads();
   // dKf = delta dh^T  (C x K)
   for (int tile = w; tile < NTL; tile += 4) {
@@ -649,7 +453,7 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_kernel(
   // phase 1: sK | sA | sG (3 x C x KP); phase 2 (after the solve) reuses it as sX | sUW (2 x C x XP)
   constexpr int P1 = 3 * C * KP, P2 = 2 * C * XP;
   constexpr int R1 = P1 > P2 ? P1 : P2;
-  __shared__ float sBuf[R1];
+  __shared__ __attribute__((aligned(16))) float sBuf[R1];
   __shared__ __attribute__((aligned(16))) float sN[C * NS];
   __shared__ float sSpan[4];
   float* sK = sBuf;
@@ -708,12 +512,8 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_kernel(
     }
   }
   // stage [U | W] rows for dN
-  for (int e = tid; e < C * (V + K); e += 256) {
-    const int c = e / (V + K), jj = e - c * (V + K);
-    float xv = 0.f;
-    if (c < L) xv = jj < V ? U[bht(bh, t0 + c, T, V) + jj] : W[bht(bh, t0 + c, T, K) + jj - V];
-    sUW[c * XP + jj] = xv;
-  }
+  stage_f32<C, V, XP>(U + bht(bh, t0, T, V), V, L, sUW);
+  stage_f32<C, K, XP>(W + bht(bh, t0, T, K), K, L, sUW + V);
   __syncthreads();
   // dN = -(X [U|W]^T), strictly lower
   float* dNn = dNg + ((int64_t)bh * NT + n) * C * C;
@@ -749,9 +549,10 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
     bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg) {
   constexpr int KP = K + 4;
   constexpr int NCT = K / 16;  // channel tiles
-  __shared__ bf16_t sQ[C * KP], sK[C * KP];  // bf16 inputs are exact in bf16
-  __shared__ float sA[C * KP], sG[C * KP];
-  __shared__ float sDN[C * NS], sDM[C * NS];
+  constexpr int KQ = QKStride<K, bf16_t>::value;
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[C * KQ], sK[C * KQ];  // bf16 inputs are exact in bf16
+  __shared__ __attribute__((aligned(16))) float sA[C * KP], sG[C * KP];
+  __shared__ __attribute__((aligned(16))) float sDN[C * NS], sDM[C * NS];
   __shared__ float sSpan[4];
   __shared__ float sColPart[4 * K];     // per row block partial of sum_c dKf kappa e^{g_last - g}
   __shared__ float sDgLast[K];          // dg of row L-1 before the g_last terms
@@ -760,14 +561,8 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   stage_chunk<K, ISO, bf16_t>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
-  {
-    const float* dNn = dNg + ((int64_t)bh * NT + n) * C * C;
-    const float* dMn = dMg + ((int64_t)bh * NT + n) * C * C;
-    for (int e = tid; e < C * C; e += 256) {
-      sDN[(e / C) * NS + e % C] = dNn[e];
-      sDM[(e / C) * NS + e % C] = dMn[e];
-    }
-  }
+  stage_f32<C, C, NS>(dNg + ((int64_t)bh * NT + n) * C * C, C, C, sDN);
+  stage_f32<C, C, NS>(dMg + ((int64_t)bh * NT + n) * C * C, C, C, sDM);
   for (int e = tid; e < 4 * K; e += 256) sColPart[e] = 0.f;
   __syncthreads();
   const int rowL = L - 1;
@@ -802,8 +597,8 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
           for (int st = 0; st < 4; ++st) {
             const int c = 16 * Ip + 4 * st + (lane >> 4);
             const float f = exp2f(sG[c * KP + ich] - sG[bnc * KP + ich]);
-            accK2 = mfma4(sDN[c * NS + sA_], lds_f(sK, c * KP + ich) * f, accK2);
-            accQ2 = mfma4(sDM[c * NS + sA_], lds_f(sQ, c * KP + ich) * f, accQ2);
+            accK2 = mfma4(sDN[c * NS + sA_], lds_f(sK, c * KQ + ich) * f, accK2);
+            accQ2 = mfma4(sDM[c * NS + sA_], lds_f(sQ, c * KQ + ich) * f, accQ2);
           }
         }
       }
@@ -812,8 +607,8 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
         for (int st = 0; st < 4; ++st) {
           const int c = a + 4 * st + (lane >> 4);
           const float f = exp2f(sG[c * KP + ich] - sG[a * KP + ich]);
-          accK2d = mfma4(sDN[c * NS + sA_], lds_f(sK, c * KP + ich) * f, accK2d);
-          accQ2d = mfma4(sDM[c * NS + sA_], lds_f(sQ, c * KP + ich) * f, accQ2d);
+          accK2d = mfma4(sDN[c * NS + sA_], lds_f(sK, c * KQ + ich) * f, accK2d);
+          accQ2d = mfma4(sDM[c * NS + sA_], lds_f(sQ, c * KQ + ich) * f, accQ2d);
         }
       }
     }
@@ -825,7 +620,7 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
     for (int j = 0; j < 4; ++j) {
       const int c = a + 4 * (lane >> 4) + j;
       const float gcv = sG[c * KP + ich];
-      const float kc = lds_f(sK, c * KP + ich), qc = lds_f(sQ, c * KP + ich), ac = sA[c * KP + ich];
+      const float kc = lds_f(sK, c * KQ + ich), qc = lds_f(sQ, c * KQ + ich), ac = sA[c * KP + ich];
       float dkN, dqM, dkapN, dkapM;
       if (fast) {
         const float el = exp2f(gcv - ga);
@@ -850,8 +645,8 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
           }
           if (s >= c) {
             const float e = exp2f(gs - gcv);
-            if (s > c) dkapN += sDN[s * NS + c] * lds_f(sK, s * KP + ich) * e;
-            dkapM += sDM[s * NS + c] * lds_f(sQ, s * KP + ich) * e;
+            if (s > c) dkapN += sDN[s * NS + c] * lds_f(sK, s * KQ + ich) * e;
+            dkapM += sDM[s * NS + c] * lds_f(sQ, s * KQ + ich) * e;
           }
         }
       }
@@ -943,7 +738,7 @@ struct BwdLayout {
   }
 };
 
-constexpr int kBV = 32;
+constexpr int kBV = 16;  // V columns per state-pass workgroup
 
 template <int K, int V>
 int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const bf16_t* v, const float* gc, int B,
@@ -964,8 +759,8 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     KDN_CHECK_LAUNCH();
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((mem_state_fwd_kernel<K, V, kBV>), dim3(V / kBV, B * H), dim3(256), 0, stream, U, W, Kf, gc,
-                       h0, T, H, NT, hb, D, ht);
+    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, kBV>), dim3(B * H * (V / kBV)), dim3(256), 0, stream, U,
+                       W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 4) {
@@ -994,8 +789,8 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
   if (stages & 1) {
-    hipLaunchKernelGGL((mem_state_bwd_kernel<K, V, kBV, TDO>), dim3(V / kBV, B * H), dim3(256), 0, stream, M, Kf, Qg,
-                       W, gc, dO, dht, T, H, NT, dh, dD, dh0);
+    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, kBV, TDO>), dim3(B * H * (V / kBV)), dim3(256), 0, stream,
+                       M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H, dh, dD, dh0);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 2) {
