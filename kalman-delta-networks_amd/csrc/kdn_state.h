@@ -108,15 +108,14 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     const int t0 = n * C, L = min(C, T - t0);
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u, c = e4 / K4, i4 = e4 % K4;
-      if (c < L) {
-        const int64_t o = row_bht(bh, t0 + c, T, K) + 4 * i4;
-        pW[u] = *reinterpret_cast<const float4*>(W + o);
-        pK[u] = *reinterpret_cast<const float4*>(Kf + o);
-      } else {
-        pW[u] = float4{0.f, 0.f, 0.f, 0.f};
-        pK[u] = float4{0.f, 0.f, 0.f, 0.f};
-      }
+      const int e4 = tid + 256 * u;
+      // W is staged row-major: consecutive lanes walk a row.  Kf is staged transposed:
+      // consecutive lanes walk a column, so the transposed LDS stores are contiguous.
+      const int cw = e4 / K4, iw = e4 % K4, ck = e4 % C, ik = e4 / C;
+      pW[u] = cw < L ? *reinterpret_cast<const float4*>(W + row_bht(bh, t0 + cw, T, K) + 4 * iw)
+                     : float4{0.f, 0.f, 0.f, 0.f};
+      pK[u] = ck < L ? *reinterpret_cast<const float4*>(Kf + row_bht(bh, t0 + ck, T, K) + 4 * ik)
+                     : float4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int u = 0; u < DTW; ++u) {
@@ -148,9 +147,9 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     // stage this chunk's operands
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u, c = e4 / K4, i4 = e4 % K4;
-      put4_rowmajor(sWh, sWl, c * KH + 4 * i4, pW[u]);
-      put4_transposed(sKh, sKl, 4 * i4, CH, c, pK[u]);
+      const int e4 = tid + 256 * u;
+      put4_rowmajor(sWh, sWl, (e4 / K4) * KH + 4 * (e4 % K4), pW[u]);
+      put4_transposed(sKh, sKl, 4 * (e4 / C), CH, e4 % C, pK[u]);
     }
     if (tid < K) sE[tid] = exp2f(pG);
     float cU[DTW][4];
@@ -280,19 +279,21 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
     const int t0 = n * C, L = min(C, T - t0);
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u, c = e4 / K4, i4 = e4 % K4;
-      if (c < L) {
-        const int64_t o = row_bht(bh, t0 + c, T, K) + 4 * i4;
-        pK[u] = *reinterpret_cast<const float4*>(Kf + o);
-        pQ[u] = *reinterpret_cast<const float4*>(Qg + o);
-        pW[u] = *reinterpret_cast<const float4*>(W + o);
-      } else {
-        pK[u] = pQ[u] = pW[u] = float4{0.f, 0.f, 0.f, 0.f};
-      }
+      const int e4 = tid + 256 * u;
+      // Kf is staged row-major (lanes walk a row); Qg and W transposed (lanes walk a column).
+      const int cr = e4 / K4, ir = e4 % K4, cc = e4 % C, ic = e4 / C;
+      const float4 z = float4{0.f, 0.f, 0.f, 0.f};
+      pK[u] = cr < L ? *reinterpret_cast<const float4*>(Kf + row_bht(bh, t0 + cr, T, K) + 4 * ir) : z;
+      const int64_t oc = row_bht(bh, t0 + cc, T, K) + 4 * ic;
+      pQ[u] = cc < L ? *reinterpret_cast<const float4*>(Qg + oc) : z;
+      pW[u] = cc < L ? *reinterpret_cast<const float4*>(W + oc) : z;
     }
     const float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
 #pragma unroll
-    for (int u = 0; u < PM; ++u) pM[u] = *reinterpret_cast<const float4*>(Mn + 4 * (tid + 256 * u));
+    for (int u = 0; u < PM; ++u) {  // M[cp][4 c4 .. 4 c4 + 3], lanes walk cp
+      const int e4 = tid + 256 * u, cp = e4 % C, c4 = e4 / C;
+      pM[u] = *reinterpret_cast<const float4*>(Mn + cp * C + 4 * c4);
+    }
 #pragma unroll
     for (int u = 0; u < PO; ++u) {
       const int e = tid + 256 * u, c = e / BV, vv = e % BV;
@@ -318,15 +319,15 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
     const int t0 = n * C, L = min(C, T - t0);
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u, c = e4 / K4, i4 = e4 % K4;
-      put4_rowmajor(sKh, sKl, c * KH + 4 * i4, pK[u]);
-      put4_transposed(sQh, sQl, 4 * i4, CH, c, pQ[u]);
-      put4_transposed(sWh, sWl, 4 * i4, CH, c, pW[u]);
+      const int e4 = tid + 256 * u;
+      put4_rowmajor(sKh, sKl, (e4 / K4) * KH + 4 * (e4 % K4), pK[u]);
+      put4_transposed(sQh, sQl, 4 * (e4 / C), CH, e4 % C, pQ[u]);
+      put4_transposed(sWh, sWl, 4 * (e4 / C), CH, e4 % C, pW[u]);
     }
 #pragma unroll
     for (int u = 0; u < PM; ++u) {
-      const int e4 = tid + 256 * u, cp = e4 / (C / 4), c4 = e4 % (C / 4);  // M[cp][4c4 .. 4c4+3]
-      put4_transposed(sMh, sMl, 4 * c4, CH, cp, pM[u]);                    // M^T [c][cp]
+      const int e4 = tid + 256 * u;
+      put4_transposed(sMh, sMl, 4 * (e4 / C), CH, e4 % C, pM[u]);  // M^T [c][cp]
     }
 #pragma unroll
     for (int u = 0; u < PO; ++u) {
