@@ -25,6 +25,34 @@ template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float 
 template <> __device__ __forceinline__ void st<float>(float* p, int64_t i, float x) { p[i] = x; }
 template <> __device__ __forceinline__ void st<bf16_t>(bf16_t* p, int64_t i, float x) { p[i] = f2bf(x); }
 
+// ---- buffer-descriptor memory access ----------------------------------------------
+// A raw buffer descriptor over [base, base + bytes) (gfx9 dword3: 32-bit data format).
+// Loads at or past `bytes` return 0 and stores there are dropped, which replaces
+// per-element bounds branches; offsets are 32-bit bytes.  `base` must be wave-uniform.
+typedef __amdgpu_buffer_rsrc_t bufrsrc;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bufrsrc make_buf(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buf_ld(bufrsrc r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ float4 buf_ld4(bufrsrc r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+}
+__device__ __forceinline__ float buf_ld_bf16(bufrsrc r, uint32_t off) {
+  return bf2f(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+template <typename T> __device__ __forceinline__ float buf_ldt(bufrsrc r, uint32_t elem);
+template <> __device__ __forceinline__ float buf_ldt<float>(bufrsrc r, uint32_t elem) { return buf_ld(r, elem * 4); }
+template <> __device__ __forceinline__ float buf_ldt<bf16_t>(bufrsrc r, uint32_t elem) {
+  return buf_ld_bf16(r, elem * 2);
+}
+__device__ __forceinline__ void buf_st(bufrsrc r, uint32_t off, float x) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, 0);
+}
+
 // ---- activations ---------------------------------------------------------------
 // softplus with torch's default threshold (x > 20 -> x).
 __device__ __forceinline__ float softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }

@@ -738,7 +738,6 @@ struct BwdLayout {
   }
 };
 
-constexpr int kBV = 16;  // V columns per state-pass workgroup
 
 template <int K, int V>
 int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const bf16_t* v, const float* gc, int B,
@@ -759,7 +758,7 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     KDN_CHECK_LAUNCH();
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, kBV>), dim3(B * H * (V / kBV)), dim3(256), 0, stream, U,
+    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), dim3(B * H * (V / kdn_state::WG_COLS)), dim3(256), 0, stream, U,
                        W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht);
     KDN_CHECK_LAUNCH();
   }
@@ -789,7 +788,7 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
   if (stages & 1) {
-    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, kBV, TDO>), dim3(B * H * (V / kBV)), dim3(256), 0, stream,
+    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO>), dim3(B * H * (V / kdn_state::WG_COLS)), dim3(256), 0, stream,
                        M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H, dh, dD, dh0);
     KDN_CHECK_LAUNCH();
   }

@@ -1,42 +1,100 @@
 // Serial chunk-state passes of the KDN memory scan (forward and reverse).
 //
-// One workgroup per (b, h, V-slice of BV columns); the workgroups of one (b, h) are placed
-// on one XCD so the chunk operands they all read (W, Kf, Qg, M) are shared through that
-// XCD's L2.  The state slice lives in MFMA accumulators; per chunk the next chunk's
-// operands are prefetched into registers (16-byte loads) while the current chunk computes.
-// Products use bf16x3 split MFMA (v_mfma_f32_16x16x32_bf16 on hi*hi + hi*lo + lo*hi of
-// x = hi + lo), which keeps the fp32 state to ~2^-16 relative per product.  LDS operand
-// tiles are stored so that every MFMA fragment is one 16-byte read: A tiles [row][k],
-// B tiles transposed [col][k].
+//   forward  (per chunk n):  h_n = S;  delta = U - W S;  S = e^{g_last} S + Kf^T delta
+//   backward (reverse):      dh_n = dS;  d delta = M^T dO + Kf dS;
+//                            dS <- e^{g_last} dS + Qg^T dO - W^T d delta
 //
-//   forward  (per chunk): h_n = S;  delta = U - W S;  S = e^{g_last} S + Kf^T delta
-//   backward (reverse):   dh_n = dS;  d delta = M^T dO + Kf dS;
-//                         dS <- e^{g_last} dS + Qg^T dO - W^T d delta
+// Work split.  One workgroup (4 waves) per (b, h, 64-column slice of V); each wave owns 16
+// state columns and keeps them for the whole sequence as K/16 MFMA accumulator tiles.  The
+// workgroups of one (b, h) are placed on one XCD so the chunk operands they both read are
+// shared through that XCD's L2.
+//
+// Precision.  Products use bf16x3 split MFMA (v_mfma_f32_16x16x32_bf16 on hi*hi + hi*lo +
+// lo*hi of x = hi + lo, both halves rounded to nearest even), ~2^-16 relative per product with
+// fp32 accumulation.  A bf16 output cotangent is exact in one half, so its products take two.
+//
+// Operand flow.
+//  * B operands are the recurrent state and the chunk's delta, taken straight from the
+//    accumulators.  The D layout of a 16x16 MFMA tile gives lane l the rows 4(l/16)+j of
+//    column l%16, so two stacked row tiles supply the 8 k-values a 16x16x32 B fragment needs
+//    once the k index is permuted inside each 32-block: slot s of lane group g = l/16 holds
+//    k = 4g + s (s < 4) or 16 + 4g + (s - 4) (s >= 4).  The A fragments use the same order.
+//  * A operands (chunk matrices shared by the 4 waves) are split to bf16 hi/lo once per
+//    workgroup and stored in LDS in fragment order: a 16 x 32 tile is 64 lanes x 8 bf16 of hi
+//    followed by the same for lo, so a fragment is one contiguous 16-byte read per lane.
+//  * Each chunk update has two phases with an LDS buffer each.  While a phase multiplies out
+//    of its buffer, the threads split the other phase's next operands (loaded into registers
+//    one phase earlier) into the other buffer: two barriers per chunk, loads one phase ahead.
 #pragma once
 #include "kdn_common.h"
 
 namespace kdn_state {
 
 constexpr int C = 64;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int WG_COLS = 64;  // V columns per workgroup: 4 waves x 16
+constexpr int TILE = 1024;   // bf16 elements of one 16 x 32 A tile (hi 512, lo 512)
 
-__device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                  0, 0);
 }
 // a*b with a = ah + al, b = bh + bl, dropping al*bl
 __device__ __forceinline__ f32x4 mma3(uint4 ah, uint4 al, uint4 bh, uint4 bl, f32x4 c) {
-  c = mfma_bf16(ah, bh, c);
-  c = mfma_bf16(ah, bl, c);
-  c = mfma_bf16(al, bh, c);
+  c = mfma(ah, bh, c);
+  c = mfma(ah, bl, c);
+  c = mfma(al, bh, c);
   return c;
 }
-__device__ __forceinline__ void split(float x, bf16_t& hi, bf16_t& lo) {
-  hi = f2bf(x);
-  lo = f2bf(x - bf2f(hi));
+// a*b with b exact in bf16
+__device__ __forceinline__ f32x4 mma2(uint4 ah, uint4 al, uint4 b, f32x4 c) {
+  c = mfma(ah, b, c);
+  c = mfma(al, b, c);
+  return c;
 }
-__device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Two floats -> packed bf16 (RNE), element 0 in the low half.
+__device__ __forceinline__ uint32_t pk2(float a, float b) {
+  bf16x2v v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pk2(a, b);
+  lo = pk2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+// hi/lo B fragment from two stacked D-layout tiles (k rows [0,16) and [16,32) of a block).
+__device__ __forceinline__ void bfrag(f32x4 t0, f32x4 t1, uint4& hi, uint4& lo) {
+  split2(t0[0], t0[1], hi.x, lo.x);
+  split2(t0[2], t0[3], hi.y, lo.y);
+  split2(t1[0], t1[1], hi.z, lo.z);
+  split2(t1[2], t1[3], hi.w, lo.w);
+}
+
+// Staging unit u of an A operand with contraction length KD: 4 consecutive k-slots of one lane
+// of one tile.  Consecutive u are consecutive lanes, so a wave's LDS stores are contiguous.
+struct Unit {
+  int row, k0, off;
+};
+template <int KD>
+__device__ __forceinline__ Unit unit(int u) {
+  constexpr int KB = KD / 32;
+  const int tile = u >> 7, half = (u >> 6) & 1, L = u & 63;
+  return Unit{16 * (tile / KB) + (L & 15), 32 * (tile % KB) + 16 * half + 4 * (L >> 4), tile * TILE + L * 8 + 4 * half};
+}
+__device__ __forceinline__ void put_unit(bf16_t* buf, int off, float a, float b, float c, float d) {
+  uint32_t h0, l0, h1, l1;
+  split2(a, b, h0, l0);
+  split2(c, d, h1, l1);
+  *reinterpret_cast<uint2*>(buf + off) = uint2{h0, h1};
+  *reinterpret_cast<uint2*>(buf + off + 512) = uint2{l0, l1};
+}
+__device__ __forceinline__ void afrag(const bf16_t* buf, int tile, int lane, uint4& hi, uint4& lo) {
+  hi = *reinterpret_cast<const uint4*>(buf + tile * TILE + lane * 8);
+  lo = *reinterpret_cast<const uint4*>(buf + tile * TILE + 512 + lane * 8);
+}
 
 // Block -> (bh, V-slice): the NV slices of one (b, h) go to one XCD (dispatch is round-robin
 // over the 8 XCDs), when B*H is a multiple of 8.
@@ -56,379 +114,332 @@ __device__ __forceinline__ int64_t row_bthk(int b, int t, int h, int T, int H, i
   return (((int64_t)b * T + t) * H + h) * D;
 }
 
-// Store 4 consecutive values (one float4) split into hi/lo at p_hi[o..o+3], p_lo[o..o+3].
-__device__ __forceinline__ void put4_rowmajor(bf16_t* hi, bf16_t* lo, int o, float4 x) {
-  bf16_t h0, h1, h2, h3, l0, l1, l2, l3;
-  split(x.x, h0, l0);
-  split(x.y, h1, l1);
-  split(x.z, h2, l2);
-  split(x.w, h3, l3);
-  *reinterpret_cast<uint2*>(hi + o) = uint2{(uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2 | ((uint32_t)h3 << 16)};
-  *reinterpret_cast<uint2*>(lo + o) = uint2{(uint32_t)l0 | ((uint32_t)l1 << 16), (uint32_t)l2 | ((uint32_t)l3 << 16)};
-}
-// Store the 4 values of a float4 (consecutive in k) into a transposed tile: p[(k0+q)*ld + r].
-__device__ __forceinline__ void put4_transposed(bf16_t* hi, bf16_t* lo, int k0, int ld, int r, float4 x) {
-  split(x.x, hi[(k0 + 0) * ld + r], lo[(k0 + 0) * ld + r]);
-  split(x.y, hi[(k0 + 1) * ld + r], lo[(k0 + 1) * ld + r]);
-  split(x.z, hi[(k0 + 2) * ld + r], lo[(k0 + 2) * ld + r]);
-  split(x.w, hi[(k0 + 3) * ld + r], lo[(k0 + 3) * ld + r]);
-}
-
 // ===========================================================================
-// Forward state pass.  grid (B*H*V/BV), block 256.
+// Forward state pass.  grid (B*H*V/64), block 256.  LDS 64.5 KB.
 // ===========================================================================
-template <int K, int V, int BV>
+template <int K, int V>
 __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
                                                         const float* __restrict__ Kf, const float* __restrict__ gc,
                                                         const float* __restrict__ h0, int T, int H, int NT, int BH,
                                                         float* __restrict__ hbuf, float* __restrict__ Dl,
                                                         float* __restrict__ ht) {
-  constexpr int NV = V / BV;
-  constexpr int KH = K + 8, CH = C + 8;
-  constexpr int NVB = BV / 16;
-  constexpr int STW = (K / 16) * NVB / 4;  // state tiles per wave
-  constexpr int DTW = (C / 16) * NVB / 4;  // delta tiles per wave
-  constexpr int K4 = K / 4;
-  constexpr int PW = C * K4 / 256;  // float4 per thread of one C x K operand
-  static_assert((K / 16) * NVB % 4 == 0 && (C / 16) * NVB % 4 == 0, "tile split over 4 waves");
-  __shared__ __attribute__((aligned(16))) bf16_t sWh[C * KH], sWl[C * KH];  // W [c][i]
-  __shared__ __attribute__((aligned(16))) bf16_t sKh[K * CH], sKl[K * CH];  // Kf^T [i][c]
-  __shared__ __attribute__((aligned(16))) bf16_t sSh[BV * KH], sSl[BV * KH];  // S^T [v][i]
-  __shared__ __attribute__((aligned(16))) bf16_t sDh[BV * CH], sDl[BV * CH];  // delta^T [v][c]
-  __shared__ float sE[K];
+  constexpr int NV = V / WG_COLS;
+  constexpr int KB = K / 32;           // k-blocks of a contraction over K
+  constexpr int ST = K / 16;           // state row tiles per wave
+  constexpr int UN = C * K / 4 / 256;  // staging units per thread of a C x K operand
+  __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
+  __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
+  __shared__ __attribute__((aligned(16))) float sE[K];
   int bh, vs;
   xcd_map(blockIdx.x, NV, BH, bh, vs);
-  const int b = bh / H, h = bh % H, v0 = vs * BV;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
+  const int col = vs * WG_COLS + 16 * w + (lane & 15);  // this lane's state column
 
-  float4 pW[PW], pK[PW];
-  float pU[DTW][4];
-  float pG = 0.f;
-  auto prefetch = [&](int n) {
+  float4 rW[UN];
+  float rK[UN][4], rU[4][4], rE = 0.f;
+  auto load_W = [&](int n) {
     const int t0 = n * C, L = min(C, T - t0);
+    const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);  // rows past L read 0
 #pragma unroll
-    for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u;
-      // W is staged row-major: consecutive lanes walk a row.  Kf is staged transposed:
-      // consecutive lanes walk a column, so the transposed LDS stores are contiguous.
-      const int cw = e4 / K4, iw = e4 % K4, ck = e4 % C, ik = e4 / C;
-      pW[u] = cw < L ? *reinterpret_cast<const float4*>(W + row_bht(bh, t0 + cw, T, K) + 4 * iw)
-                     : float4{0.f, 0.f, 0.f, 0.f};
-      pK[u] = ck < L ? *reinterpret_cast<const float4*>(Kf + row_bht(bh, t0 + ck, T, K) + 4 * ik)
-                     : float4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < UN; ++u) {
+      const Unit x = unit<K>(tid + 256 * u);
+      rW[u] = buf_ld4(rw, (x.row * K + x.k0) * 4);
+    }
+  };
+  auto load_K = [&](int n) {  // Kf^T (rows i, k = c), U rows of this lane, e^{g_last}
+    const int t0 = n * C, L = min(C, T - t0);
+    const bufrsrc rk = make_buf(Kf + row_bht(bh, t0, T, K), L * K * 4);
+    const bufrsrc ru = make_buf(U + row_bht(bh, t0, T, V), L * V * 4);
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const Unit x = unit<C>(tid + 256 * u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rK[u][j] = buf_ld(rk, ((x.k0 + j) * K + x.row) * 4);
     }
 #pragma unroll
-    for (int u = 0; u < DTW; ++u) {
-      const int tile = w * DTW + u, cb = tile / NVB, vb = tile % NVB;
+    for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = 16 * cb + 4 * q4 + j;
-        pU[u][j] = c < L ? U[row_bht(bh, t0 + c, T, V) + v0 + 16 * vb + r16] : 0.f;
-      }
-    }
-    if (tid < K) pG = gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid];
+      for (int j = 0; j < 4; ++j) rU[cb][j] = buf_ld(ru, ((16 * cb + 4 * g4 + j) * V + col) * 4);
+    if (tid < K) rE = exp2f(gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid]);
+  };
+  auto stage_W = [&]() {
+#pragma unroll
+    for (int u = 0; u < UN; ++u) put_unit(sW, unit<K>(tid + 256 * u).off, rW[u].x, rW[u].y, rW[u].z, rW[u].w);
+  };
+  auto stage_K = [&]() {
+#pragma unroll
+    for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + 256 * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
+    if (tid < K) sE[tid] = rE;
   };
 
-  f32x4 S[STW];
+  f32x4 S[ST];
 #pragma unroll
-  for (int u = 0; u < STW; ++u) {
-    const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
+  for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 16 * ib + 4 * q4 + j, vv = 16 * vb + r16;
-      const float x = h0 ? h0[((int64_t)bh * K + i) * V + v0 + vv] : 0.f;
-      S[u][j] = x;
-      split(x, sSh[vv * KH + i], sSl[vv * KH + i]);
-    }
-  }
-  prefetch(0);
+    for (int j = 0; j < 4; ++j) S[ib][j] = h0 ? h0[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] : 0.f;
+
+  load_W(0);
+  stage_W();
+  load_K(0);
+  __syncthreads();
   for (int n = 0; n < NT; ++n) {
     const int t0 = n * C, L = min(C, T - t0);
-    // stage this chunk's operands
-#pragma unroll
-    for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u;
-      put4_rowmajor(sWh, sWl, (e4 / K4) * KH + 4 * (e4 % K4), pW[u]);
-      put4_transposed(sKh, sKl, 4 * (e4 / C), CH, e4 % C, pK[u]);
-    }
-    if (tid < K) sE[tid] = exp2f(pG);
-    float cU[DTW][4];
-#pragma unroll
-    for (int u = 0; u < DTW; ++u)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) cU[u][j] = pU[u][j];
-    __syncthreads();
-    if (n + 1 < NT) prefetch(n + 1);
-    // h_n = S
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        hbuf[(((int64_t)bh * NT + n) * K + 16 * ib + 4 * q4 + j) * V + v0 + 16 * vb + r16] = S[u][j];
-    }
-    // delta = U - W S
     {
-      f32x4 acc[DTW];
+      const bufrsrc rh = make_buf(hbuf + ((int64_t)bh * NT + n) * K * V, K * V * 4);
 #pragma unroll
-      for (int u = 0; u < DTW; ++u) acc[u] = zero4();
+      for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-      for (int kk = 0; kk < K / 32; ++kk) {
-        const int ko = 32 * kk + 8 * q4;
+        for (int j = 0; j < 4; ++j) buf_st(rh, ((16 * ib + 4 * g4 + j) * V + col) * 4, S[ib][j]);
+    }
+
+    // ---- phase 1: delta = U - W S   (reads sW; fills sK with chunk n; loads W of chunk n+1)
+    stage_K();
+    float cU[4][4];
 #pragma unroll
-        for (int u = 0; u < DTW; ++u) {
-          const int tile = w * DTW + u, cb = tile / NVB, vb = tile % NVB;
-          const int ra = (16 * cb + r16) * KH + ko, rb = (16 * vb + r16) * KH + ko;
-          acc[u] = mma3(ld16(sWh + ra), ld16(sWl + ra), ld16(sSh + rb), ld16(sSl + rb), acc[u]);
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cU[cb][j] = rU[cb][j];
+    if (n + 1 < NT) load_W(n + 1);
+    f32x4 D[4];
+    {
+      uint4 bh_[KB], bl_[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) bfrag(S[2 * kb], S[2 * kb + 1], bh_[kb], bl_[kb]);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) D[cb] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          uint4 ah, al;
+          afrag(sW, cb * KB + kb, lane, ah, al);
+          D[cb] = mma3(ah, al, bh_[kb], bl_[kb], D[cb]);
         }
-      }
+      const bufrsrc rd = make_buf(Dl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
 #pragma unroll
-      for (int u = 0; u < DTW; ++u) {
-        const int tile = w * DTW + u, cb = tile / NVB, vb = tile % NVB;
+      for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int c = 16 * cb + 4 * q4 + j, vv = 16 * vb + r16;
-          const float d = cU[u][j] - acc[u][j];
-          if (c < L) Dl[row_bht(bh, t0 + c, T, V) + v0 + vv] = d;
-          split(d, sDh[vv * CH + c], sDl[vv * CH + c]);
+          const float d = cU[cb][j] - D[cb][j];
+          D[cb][j] = d;
+          buf_st(rd, ((16 * cb + 4 * g4 + j) * V + col) * 4, d);
         }
-      }
     }
     __syncthreads();
-    // S = e ⊙ S + Kf^T delta
+
+    // ---- phase 2: S = e S + Kf^T delta   (reads sK; fills sW with chunk n+1; loads Kf, U, e of n+1)
+    if (n + 1 < NT) {
+      stage_W();
+      load_K(n + 1);
+    }
     {
-      f32x4 acc[STW];
+      uint4 dh_[2], dl_[2];
+      bfrag(D[0], D[1], dh_[0], dl_[0]);
+      bfrag(D[2], D[3], dh_[1], dl_[1]);
 #pragma unroll
-      for (int u = 0; u < STW; ++u) {
-        const int tile = w * STW + u, ib = tile / NVB;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[u][j] = sE[16 * ib + 4 * q4 + j] * S[u][j];
+      for (int ib = 0; ib < ST; ++ib) {
+        const float4 e = *reinterpret_cast<const float4*>(sE + 16 * ib + 4 * g4);
+        S[ib] = f32x4{e.x * S[ib][0], e.y * S[ib][1], e.z * S[ib][2], e.w * S[ib][3]};
       }
 #pragma unroll
-      for (int kk = 0; kk < C / 32; ++kk) {
-        const int ko = 32 * kk + 8 * q4;
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int u = 0; u < STW; ++u) {
-          const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
-          const int ra = (16 * ib + r16) * CH + ko, rb = (16 * vb + r16) * CH + ko;
-          acc[u] = mma3(ld16(sKh + ra), ld16(sKl + ra), ld16(sDh + rb), ld16(sDl + rb), acc[u]);
+        for (int ib = 0; ib < ST; ++ib) {
+          uint4 ah, al;
+          afrag(sK, ib * 2 + kb, lane, ah, al);
+          S[ib] = mma3(ah, al, dh_[kb], dl_[kb], S[ib]);
         }
-      }
-#pragma unroll
-      for (int u = 0; u < STW; ++u) S[u] = acc[u];
     }
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = 16 * ib + 4 * q4 + j, vv = 16 * vb + r16;
-        split(S[u][j], sSh[vv * KH + i], sSl[vv * KH + i]);
-      }
-    }
   }
   if (ht) {
 #pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
+    for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        ht[((int64_t)bh * K + 16 * ib + 4 * q4 + j) * V + v0 + 16 * vb + r16] = S[u][j];
-    }
+      for (int j = 0; j < 4; ++j) ht[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] = S[ib][j];
   }
 }
 
 // ===========================================================================
-// Reverse state pass.  grid (B*H*V/BV), block 256.
+// Reverse state pass.  grid (B*H*V/64), block 256.  LDS 112.5 KB.
 // ===========================================================================
-template <int K, int V, int BV, typename TDO>
+template <int K, int V, typename TDO>
 __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict__ Mg, const float* __restrict__ Kf,
                                                         const float* __restrict__ Qg, const float* __restrict__ W,
                                                         const float* __restrict__ gc, const TDO* __restrict__ dO,
                                                         const float* __restrict__ dht, int T, int H, int NT, int BH,
                                                         float* __restrict__ dhbuf, float* __restrict__ dDl,
                                                         float* __restrict__ dh0) {
-  constexpr int NV = V / BV;
-  constexpr int KH = K + 8, CH = C + 8;
-  constexpr int NVB = BV / 16;
-  constexpr int STW = (K / 16) * NVB / 4;
-  constexpr int DTW = (C / 16) * NVB / 4;
-  constexpr int K4 = K / 4;
-  constexpr int PW = C * K4 / 256;
-  constexpr int PM = C * C / 4 / 256;         // float4 per thread of M
-  constexpr int PO = C * BV / 256;            // dO values per thread
-  static_assert(PO >= 1 && C * BV % 256 == 0, "dO staging");
-  __shared__ __attribute__((aligned(16))) bf16_t sKh[C * KH], sKl[C * KH];   // Kf [c][i]
-  __shared__ __attribute__((aligned(16))) bf16_t sQh[K * CH], sQl[K * CH];   // Qg^T [i][c]
-  __shared__ __attribute__((aligned(16))) bf16_t sWh[K * CH], sWl[K * CH];   // W^T [i][c]
-  __shared__ __attribute__((aligned(16))) bf16_t sMh[C * CH], sMl[C * CH];   // M^T [c][c']
-  __shared__ __attribute__((aligned(16))) bf16_t sOh[BV * CH], sOl[BV * CH]; // dO^T [v][c]
-  __shared__ __attribute__((aligned(16))) bf16_t sSh[BV * KH], sSl[BV * KH]; // dS^T [v][i]
-  __shared__ __attribute__((aligned(16))) bf16_t sDh[BV * CH], sDl[BV * CH]; // d delta^T [v][c]
-  __shared__ float sE[K];
+  constexpr int NV = V / WG_COLS;
+  constexpr int KB = K / 32;
+  constexpr int ST = K / 16;
+  constexpr int UN = C * K / 4 / 256;  // staging units per thread of a C x K operand
+  constexpr int UM = C * C / 4 / 256;  // ... of M^T
+  constexpr bool DO_BF16 = sizeof(TDO) == 2;
+  // phase 1: M^T (rows c', k = c) and Kf (rows c, k = i);  phase 2: Qg^T, W^T (rows i, k = c)
+  __shared__ __attribute__((aligned(16))) bf16_t sM[(C / 16) * (C / 32) * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sKn[(C / 16) * KB * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[(K / 16) * (C / 32) * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sWt[(K / 16) * (C / 32) * TILE];
+  __shared__ __attribute__((aligned(16))) float sE[K];
   int bh, vs;
   xcd_map(blockIdx.x, NV, BH, bh, vs);
-  const int b = bh / H, h = bh % H, v0 = vs * BV;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, q4 = lane >> 4;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
+  const int col = vs * WG_COLS + 16 * w + (lane & 15);
 
-  float4 pK[PW], pQ[PW], pW[PW], pM[PM];
-  float pO[PO];
-  float pG = 0.f;
-  auto prefetch = [&](int n) {
+  float rM[UM][4], rQ[UN][4], rWt[UN][4], rO[4][4], rE = 0.f;
+  float4 rKn[UN];
+  auto load_p1 = [&](int n) {  // M^T and Kf of chunk n
     const int t0 = n * C, L = min(C, T - t0);
+    const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][c'] row-major
+    const bufrsrc rk = make_buf(Kf + row_bht(bh, t0, T, K), L * K * 4);
 #pragma unroll
-    for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u;
-      // Kf is staged row-major (lanes walk a row); Qg and W transposed (lanes walk a column).
-      const int cr = e4 / K4, ir = e4 % K4, cc = e4 % C, ic = e4 / C;
-      const float4 z = float4{0.f, 0.f, 0.f, 0.f};
-      pK[u] = cr < L ? *reinterpret_cast<const float4*>(Kf + row_bht(bh, t0 + cr, T, K) + 4 * ir) : z;
-      const int64_t oc = row_bht(bh, t0 + cc, T, K) + 4 * ic;
-      pQ[u] = cc < L ? *reinterpret_cast<const float4*>(Qg + oc) : z;
-      pW[u] = cc < L ? *reinterpret_cast<const float4*>(W + oc) : z;
-    }
-    const float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
+    for (int u = 0; u < UM; ++u) {
+      const Unit x = unit<C>(tid + 256 * u);  // row = c' (the d delta index), k = c
 #pragma unroll
-    for (int u = 0; u < PM; ++u) {  // M[cp][4 c4 .. 4 c4 + 3], lanes walk cp
-      const int e4 = tid + 256 * u, cp = e4 % C, c4 = e4 / C;
-      pM[u] = *reinterpret_cast<const float4*>(Mn + cp * C + 4 * c4);
+      for (int j = 0; j < 4; ++j) rM[u][j] = buf_ld(rm, ((x.k0 + j) * C + x.row) * 4);
     }
 #pragma unroll
-    for (int u = 0; u < PO; ++u) {
-      const int e = tid + 256 * u, c = e / BV, vv = e % BV;
-      pO[u] = c < L ? ld(dO, row_bthk(b, t0 + c, h, T, H, V) + v0 + vv) : 0.f;
+    for (int u = 0; u < UN; ++u) {
+      const Unit x = unit<K>(tid + 256 * u);
+      rKn[u] = buf_ld4(rk, (x.row * K + x.k0) * 4);
     }
-    if (tid < K) pG = gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid];
   };
-
-  f32x4 dS[STW];
-#pragma unroll
-  for (int u = 0; u < STW; ++u) {
-    const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 16 * ib + 4 * q4 + j, vv = 16 * vb + r16;
-      const float x = dht ? dht[((int64_t)bh * K + i) * V + v0 + vv] : 0.f;
-      dS[u][j] = x;
-      split(x, sSh[vv * KH + i], sSl[vv * KH + i]);
-    }
-  }
-  prefetch(NT - 1);
-  for (int n = NT - 1; n >= 0; --n) {
+  auto load_p2 = [&](int n) {  // Qg^T, W^T, dO rows of this lane, e^{g_last} of chunk n
     const int t0 = n * C, L = min(C, T - t0);
+    const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
+    const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);
+    // dO rows are H*V apart; the descriptor ends right after row L-1's head h
+    const bufrsrc ro = make_buf(dO + row_bthk(b, t0, h, T, H, V), ((L - 1) * H + 1) * V * sizeof(TDO));
 #pragma unroll
-    for (int u = 0; u < PW; ++u) {
-      const int e4 = tid + 256 * u;
-      put4_rowmajor(sKh, sKl, (e4 / K4) * KH + 4 * (e4 % K4), pK[u]);
-      put4_transposed(sQh, sQl, 4 * (e4 / C), CH, e4 % C, pQ[u]);
-      put4_transposed(sWh, sWl, 4 * (e4 / C), CH, e4 % C, pW[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < PM; ++u) {
-      const int e4 = tid + 256 * u;
-      put4_transposed(sMh, sMl, 4 * (e4 / C), CH, e4 % C, pM[u]);  // M^T [c][cp]
-    }
-#pragma unroll
-    for (int u = 0; u < PO; ++u) {
-      const int e = tid + 256 * u, c = e / BV, vv = e % BV;
-      split(pO[u], sOh[vv * CH + c], sOl[vv * CH + c]);
-    }
-    if (tid < K) sE[tid] = exp2f(pG);
-    __syncthreads();
-    if (n > 0) prefetch(n - 1);
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        dhbuf[(((int64_t)bh * NT + n) * K + 16 * ib + 4 * q4 + j) * V + v0 + 16 * vb + r16] = dS[u][j];
-    }
-    // d delta = M^T dO + Kf dS
-    {
-      f32x4 acc[DTW];
-#pragma unroll
-      for (int u = 0; u < DTW; ++u) acc[u] = zero4();
-#pragma unroll
-      for (int kk = 0; kk < C / 32; ++kk) {
-        const int ko = 32 * kk + 8 * q4;
-#pragma unroll
-        for (int u = 0; u < DTW; ++u) {
-          const int tile = w * DTW + u, cb = tile / NVB, vb = tile % NVB;
-          if (32 * kk + 32 > 16 * cb) {  // M^T[c][c'] = 0 for c' < c
-            const int ra = (16 * cb + r16) * CH + ko, rb = (16 * vb + r16) * CH + ko;
-            acc[u] = mma3(ld16(sMh + ra), ld16(sMl + ra), ld16(sOh + rb), ld16(sOl + rb), acc[u]);
-          }
-        }
-      }
-#pragma unroll
-      for (int kk = 0; kk < K / 32; ++kk) {
-        const int ko = 32 * kk + 8 * q4;
-#pragma unroll
-        for (int u = 0; u < DTW; ++u) {
-          const int tile = w * DTW + u, cb = tile / NVB, vb = tile % NVB;
-          const int ra = (16 * cb + r16) * KH + ko, rb = (16 * vb + r16) * KH + ko;
-          acc[u] = mma3(ld16(sKh + ra), ld16(sKl + ra), ld16(sSh + rb), ld16(sSl + rb), acc[u]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < DTW; ++u) {
-        const int tile = w * DTW + u, cb = tile / NVB, vb = tile % NVB;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int c = 16 * cb + 4 * q4 + j, vv = 16 * vb + r16;
-          const float d = acc[u][j];
-          if (c < L) dDl[row_bht(bh, t0 + c, T, V) + v0 + vv] = d;
-          split(d, sDh[vv * CH + c], sDl[vv * CH + c]);
-        }
-      }
-    }
-    __syncthreads();
-    // dS <- e dS + Qg^T dO - W^T d delta
-    {
-      f32x4 accP[STW], accW[STW];
-#pragma unroll
-      for (int u = 0; u < STW; ++u) {
-        const int tile = w * STW + u, ib = tile / NVB;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) accP[u][j] = sE[16 * ib + 4 * q4 + j] * dS[u][j];
-        accW[u] = zero4();
-      }
-#pragma unroll
-      for (int kk = 0; kk < C / 32; ++kk) {
-        const int ko = 32 * kk + 8 * q4;
-#pragma unroll
-        for (int u = 0; u < STW; ++u) {
-          const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
-          const int ra = (16 * ib + r16) * CH + ko, rb = (16 * vb + r16) * CH + ko;
-          accP[u] = mma3(ld16(sQh + ra), ld16(sQl + ra), ld16(sOh + rb), ld16(sOl + rb), accP[u]);
-          accW[u] = mma3(ld16(sWh + ra), ld16(sWl + ra), ld16(sDh + rb), ld16(sDl + rb), accW[u]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < STW; ++u)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dS[u][j] = accP[u][j] - accW[u][j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
+    for (int u = 0; u < UN; ++u) {
+      const Unit x = unit<C>(tid + 256 * u);  // row = i, k = c
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = 16 * ib + 4 * q4 + j, vv = 16 * vb + r16;
-        split(dS[u][j], sSh[vv * KH + i], sSl[vv * KH + i]);
+        const uint32_t o = ((x.k0 + j) * K + x.row) * 4;
+        rQ[u][j] = buf_ld(rq, o);
+        rWt[u][j] = buf_ld(rw, o);
       }
     }
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rO[cb][j] = buf_ldt<TDO>(ro, (16 * cb + 4 * g4 + j) * H * V + col);
+    if (tid < K) rE = exp2f(gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid]);
+  };
+  auto stage_p1 = [&]() {
+#pragma unroll
+    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + 256 * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
+#pragma unroll
+    for (int u = 0; u < UN; ++u)
+      put_unit(sKn, unit<K>(tid + 256 * u).off, rKn[u].x, rKn[u].y, rKn[u].z, rKn[u].w);
+  };
+  auto stage_p2 = [&]() {
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int off = unit<C>(tid + 256 * u).off;
+      put_unit(sQ, off, rQ[u][0], rQ[u][1], rQ[u][2], rQ[u][3]);
+      put_unit(sWt, off, rWt[u][0], rWt[u][1], rWt[u][2], rWt[u][3]);
+    }
+    if (tid < K) sE[tid] = rE;
+  };
+
+  f32x4 dS[ST];
+#pragma unroll
+  for (int ib = 0; ib < ST; ++ib)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dS[ib][j] = dht ? dht[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] : 0.f;
+
+  load_p1(NT - 1);
+  stage_p1();
+  load_p2(NT - 1);
+  __syncthreads();
+  for (int n = NT - 1; n >= 0; --n) {
+    const int t0 = n * C, L = min(C, T - t0);
+    {
+      const bufrsrc rh = make_buf(dhbuf + ((int64_t)bh * NT + n) * K * V, K * V * 4);
+#pragma unroll
+      for (int ib = 0; ib < ST; ++ib)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) buf_st(rh, ((16 * ib + 4 * g4 + j) * V + col) * 4, dS[ib][j]);
+    }
+
+    // dO of this chunk as B fragments (k = c), kept for both phases; a bf16 dO has ol = 0
+    uint4 oh[2], ol[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      bfrag(f32x4{rO[2 * kb][0], rO[2 * kb][1], rO[2 * kb][2], rO[2 * kb][3]},
+            f32x4{rO[2 * kb + 1][0], rO[2 * kb + 1][1], rO[2 * kb + 1][2], rO[2 * kb + 1][3]}, oh[kb], ol[kb]);
+
+    // ---- phase 1: d delta = M^T dO + Kf dS   (reads sM, sKn; fills sQ, sWt with chunk n)
+    stage_p2();
+    if (n > 0) load_p1(n - 1);
+    f32x4 dD[4];
+    {
+      uint4 bh_[KB], bl_[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) bfrag(dS[2 * kb], dS[2 * kb + 1], bh_[kb], bl_[kb]);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) dD[cb] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          if (kb == 0 && cb >= 2) continue;  // M^T[c'][c] = M[c][c'] = 0 for c < c'
+          uint4 ah, al;
+          afrag(sM, cb * 2 + kb, lane, ah, al);
+          dD[cb] = DO_BF16 ? mma2(ah, al, oh[kb], dD[cb]) : mma3(ah, al, oh[kb], ol[kb], dD[cb]);
+        }
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          uint4 ah, al;
+          afrag(sKn, cb * KB + kb, lane, ah, al);
+          dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
+        }
+      const bufrsrc rd = make_buf(dDl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) buf_st(rd, ((16 * cb + 4 * g4 + j) * V + col) * 4, dD[cb][j]);
+    }
+    __syncthreads();
+
+    // ---- phase 2: dS <- e dS + Qg^T dO - W^T d delta   (reads sQ, sWt; fills sM, sKn with n-1)
+    if (n > 0) {
+      stage_p1();
+      load_p2(n - 1);
+    }
+    {
+      uint4 dh_[2], dl_[2];
+      bfrag(-dD[0], -dD[1], dh_[0], dl_[0]);
+      bfrag(-dD[2], -dD[3], dh_[1], dl_[1]);
+#pragma unroll
+      for (int ib = 0; ib < ST; ++ib) {
+        const float4 e = *reinterpret_cast<const float4*>(sE + 16 * ib + 4 * g4);
+        dS[ib] = f32x4{e.x * dS[ib][0], e.y * dS[ib][1], e.z * dS[ib][2], e.w * dS[ib][3]};
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int ib = 0; ib < ST; ++ib) {
+          uint4 ah, al;
+          afrag(sQ, ib * 2 + kb, lane, ah, al);
+          dS[ib] = DO_BF16 ? mma2(ah, al, oh[kb], dS[ib]) : mma3(ah, al, oh[kb], ol[kb], dS[ib]);
+          afrag(sWt, ib * 2 + kb, lane, ah, al);
+          dS[ib] = mma3(ah, al, dh_[kb], dl_[kb], dS[ib]);
+        }
+    }
+    __syncthreads();
   }
   if (dh0) {
 #pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int tile = w * STW + u, ib = tile / NVB, vb = tile % NVB;
+    for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        dh0[((int64_t)bh * K + 16 * ib + 4 * q4 + j) * V + v0 + 16 * vb + r16] = dS[u][j];
-    }
+      for (int j = 0; j < 4; ++j) dh0[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] = dS[ib][j];
   }
 }
 
