@@ -28,8 +28,20 @@ for _p in (ROOT, PKG):
 
 METRIC = "KDN mixer fwd+bwd tokens/s at B4 H18 T4096 d128 bf16; % MFMA/HBM peak"
 HBM_PEAK_GBS = 8000.0
-FP32_PEAK_TFLOPS = 157.3  # dense fp32 (the scan's MFMA path computes in fp32)
+FP32_PEAK_TFLOPS = 157.3   # dense fp32 MFMA (v_mfma_f32_16x16x4_f32)
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 C = 64
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
+
+# MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
+# MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
+MFMA_PATH = {"mem_intra_fwd": "f32", "mem_state_fwd": "bf16x3", "mem_output_fwd": "f32",
+             "mem_state_bwd": "bf16x3", "mem_bwd_hgrad": "f32", "mem_bwd_solve": "f32",
+             "mem_bwd_contrib": "f32"}
+
+
+def mfma_peak(tag: str) -> float:
+    return FP32_PEAK_TFLOPS if MFMA_PATH.get(tag, "f32") == "f32" else BF16_PEAK_TFLOPS / 3.0
 
 
 def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
@@ -98,14 +110,15 @@ def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K
     for tag, (nbytes, flops) in counts.items():
         t = kernel_ms.get(tag, float("nan")) * 1e-3
         t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
-        t_mfma = flops / (FP32_PEAK_TFLOPS * 1e12)
+        t_mfma = flops / (mfma_peak(tag) * 1e12)
         bound = "hbm" if t_hbm >= t_mfma else "mfma"
         if bound == "hbm":
             achieved, peak, unit = nbytes / t / 1e9, HBM_PEAK_GBS, "GB/s"
         else:
-            achieved, peak, unit = flops / t / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
+            achieved, peak, unit = flops / t / 1e12, round(mfma_peak(tag), 1), "TFLOP/s"
         per_kernel[tag] = dict(ms=round(t * 1e3, 4), bound=bound, achieved=round(achieved, 2), peak=peak,
-                               unit=unit, frac=round(achieved / peak, 4), alg_bytes=int(nbytes), alg_flops=int(flops))
+                               unit=unit, frac=round(achieved / peak, 4), mfma=MFMA_PATH.get(tag, "f32"),
+                               alg_bytes=int(nbytes), alg_flops=int(flops))
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
     return dict(ms_per_step=ms, tokens_per_s=B * T / (ms * 1e-3), kernels=per_kernel, dominant=dominant)
 
@@ -135,6 +148,31 @@ def cpu_baseline(variant: str, slices: int, T: int, K: int, B: int, H: int):
                        f"(autograd), {per_slice:.2f} s/slice, extrapolated to the {B}x{H} job")
 
 
+def measured_traffic(kernel: str, config: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    if rec.get("config") != config or not k:
+        return None
+    return int(k["fetch_bytes"] + k["write_bytes"])
+
+
+def calib_copy(mib: int):
+    """A plain device copy of known size, for calibrating FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    x = torch.ones(mib * (1 << 20) // 4, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +181,8 @@ def main():
     ap.add_argument("--variant", choices=("iso", "diag"), default="iso")
     ap.add_argument("--cpu-slices", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain copy of MIB MiB (PMC byte-counter calibration)")
     ap.add_argument("--B", type=int, default=4)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--H", type=int, default=18)
@@ -164,6 +204,8 @@ def main():
     res = run_variant(main_v, args.steps, args.warmup, B, T, H, K)
     res_other = run_variant(other, args.steps, args.warmup, B, T, H, K)
     dom = res["kernels"][res["dominant"]]
+    cfg_key = f"{main_v} B{B} T{T} H{H} d{K}"
+    traffic = measured_traffic(res["dominant"], cfg_key)
     line = {
         "metric": METRIC,
         "value": round(res["tokens_per_s"], 1),
@@ -181,13 +223,16 @@ def main():
                    "B": B, "T": T, "H": H, "d_k": K, "d_v": K, "chunk": C, "inputs": "bf16",
                    "state": "fp32", "parallelism": "single GPU"},
         "roofline": {"kernel": res["dominant"], "bound": dom["bound"], "achieved": dom["achieved"],
-                     "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"], "traffic": None},
+                     "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,
+                     "traffic_source": (os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None)},
         "kernels": res["kernels"],
         "also": {f"{other}_kdn": {"value": round(res_other["tokens_per_s"], 1), "unit": "tokens/s",
                                   "ms_per_step": round(res_other["ms_per_step"], 4),
                                   "dominant": res_other["dominant"],
                                   "kernels": res_other["kernels"]}},
     }
+    if args.calib_copy:
+        calib_copy(args.calib_copy)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(main_v, args.cpu_slices, T, K, B, H)
     print(json.dumps(line), flush=True)
