@@ -25,13 +25,27 @@ def iso_kdn_scan(q, k, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias
     return _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=beta)
 
 
-def diag_kdn_scan(q, k, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param):
+def diag_kdn_scan(q, k, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param,
+                  *, initial_state=None, initial_precision=None, output_final_state: bool = False):
     """q, k, v, retention_raw, omega_raw [B,T,H,d] bf16; r_raw [B,T,H]; dt_bias [H,K];
-    returns o [B,T,H,V] in v's dtype."""
+    returns o [B,T,H,V] in v's dtype.
+
+    Long-context continuation (the reference oracle's initial_memory / initial_precision,
+    diag_kdn_naive.py:503-516): ``initial_state`` [B,H,K,V] fp32 seeds the memory,
+    ``initial_precision`` [B,H,K] fp32 replaces the learned [H] prior, and with
+    ``output_final_state`` the call returns ``(o, (final_state, final_precision))``."""
     K = q.shape[-1]
     q_memory, k_gain, k_memory = _diag_kdn_normalize(q, k)
     g_cumsum, alpha, omega, r, mu = _diag_kdn_frontend_precumsum_paired(
         retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param)
-    kappa = _diag_kdn_gain(k_gain, alpha, omega, r, mu, omega_raw, r_raw)
-    out = chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, float(K ** -0.5))
+    prec = mu if initial_precision is None else initial_precision
+    scale = float(K ** -0.5)
+    if output_final_state:
+        kappa, final_precision = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw,
+                                                output_final_state=True)
+        out, final_state = chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state=initial_state,
+                                        output_final_state=True)
+        return out.to(v.dtype), (final_state, final_precision)
+    kappa = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw)
+    out = chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state=initial_state)
     return out.to(v.dtype)
