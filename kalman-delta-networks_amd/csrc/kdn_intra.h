@@ -1,0 +1,284 @@
+// Forward intra-chunk kernel of the KDN memory scan, MFMA formulation.
+//
+// Per chunk (C = 64 tokens) with G the base-2 chunk-local prefix of the log gate and the
+// chunk's first row as the decay anchor (G_c - G_0 <= 0, G_0 - G_s >= 0):
+//   Lk = k 2^{G - G_0},  Lq = scale q 2^{G - G_0},  R = kappa 2^{G_0 - G}
+//   N = strict_lower(Lk R^T),  M = lower(Lq R^T)                   (bf16x3 MFMA, K-contraction)
+//   A = (I + N)^{-1}:  16x16 diagonal blocks by substitution, off-diagonal blocks level by level
+//                      A_IJ = -A_II sum_{J<=P<I} N_IP A_PJ           (fp32 MFMA)
+//   U = A V,  W = A (k 2^G),  Kf = kappa 2^{G_last - G},  Qg = scale q 2^G
+// A is saved for the backward.  R <= 2^span where span = max_i (G_0 - G_{L-1})_i; chunks with
+// span > kAnchorSpanMax are flagged (flags[chunk] = 1) and left to the exact per-block kernel,
+// which runs after this one over the flagged chunks only.
+//
+// Layout of work: wave w owns row block I = w (16 rows) for the N / M build, computing its own
+// Lk / Lq fragments in registers and publishing its R fragments to LDS; the U / W products
+// are split over the waves by output column tile.  LDS ~49 KB: three workgroups per CU.
+#pragma once
+#include "kdn_common.h"
+#include "kdn_state.h"
+
+namespace kdn_intra {
+
+using kdn_state::afrag;
+using kdn_state::bfrag;
+using kdn_state::C;
+using kdn_state::mma2;
+using kdn_state::mma3;
+using kdn_state::split2;
+using kdn_state::TILE;
+using kdn_state::zero4;
+
+constexpr float kAnchorSpanMax = 100.f;  // base 2: R <= 2^100 stays far inside fp32
+constexpr int AP = C + 1;                // LDS row stride of the fp32 N and A tiles
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// 8 bf16 (raw bits in a uint4) -> 8 floats
+__device__ __forceinline__ void unpack8(u32x4 v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    f[2 * p] = __uint_as_float(w[p] << 16);
+    f[2 * p + 1] = __uint_as_float(w[p] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& lo) {
+  split2(x[0], x[1], hi.x, lo.x);
+  split2(x[2], x[3], hi.y, lo.y);
+  split2(x[4], x[5], hi.z, lo.z);
+  split2(x[6], x[7], hi.w, lo.w);
+}
+__device__ __forceinline__ void ld8(bufrsrc r, uint32_t off, float* f) {
+  const float4 a = buf_ld4(r, off), b = buf_ld4(r, off + 16);
+  f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+}
+__device__ __forceinline__ void st8(bufrsrc r, uint32_t off, const float* f) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                                               __float_as_uint(f[3])},
+                                         r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]),
+                                               __float_as_uint(f[7])},
+                                         r, off + 16, 0, 0);
+}
+
+// grid (NT, B*H), block 256.
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
+    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags) {
+  constexpr int KB = K / 32;
+  // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
+  constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char sRA[RBYTES > ABYTES ? RBYTES : ABYTES];
+  __shared__ __attribute__((aligned(16))) float sN[C * AP];  // N [c][s]
+  bf16_t* sR = reinterpret_cast<bf16_t*>(sRA);
+  float* sA = reinterpret_cast<float*>(sRA);
+  __shared__ float sSpan[4];
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+
+  // [B,T,H,D] inputs: row c of this chunk at ((b*T + t0 + c)*H + h)*D
+  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);  // descriptor covers rows 0..L-1 of this head
+  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rv = make_buf(v + in_row0 * V, rows_in * V * 2);
+  // [B*H, T, D] outputs
+  const bufrsrc rKf = make_buf(Kf + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rQg = make_buf(Qg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
+  float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
+  float* An = Ag + ((int64_t)bh * NT + n) * C * C;
+
+  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels
+  const int c = 16 * w + r16;
+  const uint32_t crow = (uint32_t)(c * H);
+  uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
+  float span = 0.f;
+  const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int i0 = 32 * kb + 8 * g4;
+    float gcv[8], g0[8], gl[8], kv[8], qv[8], av[8];
+    ld8(rG, (crow * K + i0) * 4, gcv);
+    ld8(rG, i0 * 4, g0);
+    ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
+    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
+    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
+    if (ISO) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) av[j] = beta * kv[j];
+    } else {
+      ld8(rkap, (crow * K + i0) * 4, av);
+    }
+    float lk[8], lq[8], rr[8], kf[8], qg[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = exp2f(gcv[j] - g0[j]);
+      lk[j] = kv[j] * e;
+      lq[j] = scale * qv[j] * e;
+      rr[j] = av[j] * exp2f(g0[j] - gcv[j]);
+      kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
+      qg[j] = scale * qv[j] * exp2f(gcv[j]);
+      span = fmaxf(span, g0[j] - gl[j]);
+    }
+    split8(lk, lkh[kb], lkl[kb]);
+    split8(lq, lqh[kb], lql[kb]);
+    uint4 rh, rl;
+    split8(rr, rh, rl);
+    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + lane * 8) = rh;
+    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + 512 + lane * 8) = rl;
+    st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
+    st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
+  if (lane == 0) sSpan[w] = span;
+  __syncthreads();
+  const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
+  if (!(cspan <= kAnchorSpanMax)) {  // the exact kernel takes this chunk
+    if (tid == 0) flags[(int64_t)bh * NT + n] = 1;
+    return;
+  }
+  if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
+
+  // ---- 2. N and M tiles of row block I = w
+  const bufrsrc rM = make_buf(Mn, C * C * 4);
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    const int s = 16 * J + r16;
+    if (J <= w) {
+      f32x4 aN = zero4(), aM = zero4();
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        uint4 rh, rl;
+        afrag(sR, J * KB + kb, lane, rh, rl);
+        aN = mma3(lkh[kb], lkl[kb], rh, rl, aN);
+        aM = mma3(lqh[kb], lql[kb], rh, rl, aM);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = 16 * w + 4 * g4 + j;
+        sN[cc * AP + s] = (J < w || s < cc) ? aN[j] : 0.f;
+        buf_st(rM, (cc * C + s) * 4, (J < w || s <= cc) ? aM[j] : 0.f);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * w + 4 * g4 + j) * C + s) * 4, 0.f);
+    }
+  }
+  __syncthreads();
+
+  // ---- 3. diagonal blocks of A: X_I = (I + N_II)^{-1}, lane j < 16 of wave I owns column j
+  if (lane < 16) {
+    const int base = 16 * w, j = lane;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = r == j ? 1.f : 0.f;
+#pragma unroll
+    for (int r = 1; r < 16; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int m = 0; m < r; ++m) acc -= sN[(base + r) * AP + base + m] * x[m];
+      if (r > j) x[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sA[(base + r) * AP + base + j] = x[r];
+  }
+  // blocks above the diagonal are zero
+  for (int e = lane; e < 256 * (3 - w); e += 64) {
+    const int J = w + 1 + (e >> 8), rr = (e >> 4) & 15, cc = e & 15;
+    sA[(16 * w + rr) * AP + 16 * J + cc] = 0.f;
+  }
+  __syncthreads();
+
+  // ---- 4. off-diagonal blocks, one block-row level at a time: wave J makes A_IJ
+#pragma unroll
+  for (int I = 1; I < 4; ++I) {
+    if (w < I) {
+      const int J = w;
+      f32x4 t = zero4();
+      for (int P = J; P < I; ++P) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+          t = mfma_f32(sN[(16 * I + r16) * AP + 16 * P + 4 * st + g4], sA[(16 * P + 4 * st + g4) * AP + 16 * J + r16],
+                       t);
+      }
+      // A_IJ = -X_I T; the k index of step st is 4 g4 + st, so T comes straight from the D layout
+      f32x4 o = zero4();
+#pragma unroll
+      for (int st = 0; st < 4; ++st) o = mfma_f32(sA[(16 * I + r16) * AP + 16 * I + 4 * g4 + st], t[st], o);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sA[(16 * I + 4 * g4 + j) * AP + 16 * J + r16] = -o[j];
+    }
+    __syncthreads();
+  }
+
+  // ---- 5. save A for the backward
+  {
+    const bufrsrc rA = make_buf(An, C * C * 4);
+#pragma unroll
+    for (int u = 0; u < C * C / 256; ++u) {
+      const int e = tid + 256 * u;
+      buf_st(rA, e * 4, sA[(e / C) * AP + (e % C)]);
+    }
+  }
+
+  // ---- 6. U = A V, W = A (k 2^G) over output column tiles t (V/16 of U, then K/16 of W)
+  // A fragments in the permuted k order of the accumulator-layout B operands:
+  // slots 0-3 <- s = 32 kb + 4 g4 + (0..3), slots 4-7 <- s = 32 kb + 16 + 4 g4 + (0..3)
+  uint4 ah[4][2], al[4][2];
+#pragma unroll
+  for (int I = 0; I < 4; ++I)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if (kb == 1 && I < 2) continue;
+      const float* row = sA + (16 * I + r16) * AP + 32 * kb + 4 * g4;
+      const float x[8] = {row[0], row[1], row[2], row[3], row[16], row[17], row[18], row[19]};
+      split8(x, ah[I][kb], al[I][kb]);
+    }
+  constexpr int NCT = (V + K) / 16;
+  for (int t = w; t < NCT; t += 4) {
+    const bool isU = t < V / 16;
+    const int col = 16 * (isU ? t : t - V / 16) + r16;
+    uint4 bh_[2], bl_[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float x[8];
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl) {
+        const int s = 32 * kb + (sl < 4 ? 4 * g4 + sl : 16 + 4 * g4 + sl - 4);
+        const uint32_t srow = (uint32_t)(s * H);
+        if (isU) {
+          x[sl] = buf_ld_bf16(rv, (srow * V + col) * 2);
+        } else {
+          const float kk = buf_ld_bf16(rk, (srow * K + col) * 2);
+          x[sl] = kk * exp2f(buf_ld(rG, (srow * K + col) * 4));
+        }
+      }
+      split8(x, bh_[kb], bl_[kb]);  // exact for V (lo = 0)
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      f32x4 acc = zero4();
+      acc = isU ? mma2(ah[I][0], al[I][0], bh_[0], acc) : mma3(ah[I][0], al[I][0], bh_[0], bl_[0], acc);
+      if (I >= 2) acc = isU ? mma2(ah[I][1], al[I][1], bh_[1], acc) : mma3(ah[I][1], al[I][1], bh_[1], bl_[1], acc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = 16 * I + 4 * g4 + j;
+        if (isU) buf_st(rU, (cc * V + col) * 4, acc[j]);
+        else buf_st(rW, (cc * K + col) * 4, acc[j]);
+      }
+    }
+  }
+}
+
+}  // namespace kdn_intra

@@ -29,6 +29,7 @@
 // Products use fp32 MFMA (v_mfma_f32_16x16x4_f32), fp32 accumulate.
 #include "kdn_common.h"
 #include "kdn_state.h"
+#include "kdn_intra.h"
 #include "../../include/kdn.h"
 
 namespace {
@@ -226,12 +227,15 @@ __device__ void build_NM(const float* sQ, const float* sK, const float* sA, cons
 // ===========================================================================
 // Forward intra-chunk kernel.
 // ===========================================================================
+// Exact path for one chunk (per-block decay anchors, per-element diagonal blocks when a
+// block's span exceeds kSpanMax, scalar forward substitution).  Runs only for the chunks the
+// MFMA kernel (kdn_intra.h) flags as outside its single-anchor range.
 template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256) void mem_intra_fwd_kernel(
+__device__ void intra_fwd_exact_chunk(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg) {
+    float* __restrict__ Mg, float* __restrict__ Ag, int n, int bh) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // sQ | sA are dead after Kf / Qg are written and are then reused for the solve's sX [C][XP]
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_kernel(
   float* sK = sBuf + OFF2;
   float* sG = sBuf + OFF2 + C * KP;
   float* sX = sBuf;
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x;
   stage_chunk<K, ISO, float>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
@@ -303,6 +307,20 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_kernel(
         if (c < L) dst[bht(bh, t0 + c, T, D) + col] = acc[r];
       }
     }
+  }
+}
+
+// Grid-stride pass over the chunks the MFMA kernel flagged (flags[chunk] != 0).
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, int NB, float scale,
+    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
+    float* __restrict__ Mg, float* __restrict__ Ag, const int* __restrict__ flags) {
+  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
+    if (flags[lin] == 0) continue;
+    __syncthreads();  // LDS of the previous chunk is dead
+    intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, lin % NT, lin / NT);
   }
 }
 
@@ -708,7 +726,7 @@ inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 // saved-buffer layout (floats), TT = B*H*T, NB = B*H*NT
 struct MemLayout {
-  int64_t U, W, Kf, Qg, M, h, D, total;
+  int64_t U, W, Kf, Qg, M, A, h, D, flags, total;
   MemLayout(int B, int T, int H, int K, int V) {
     const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
     U = 0;
@@ -716,9 +734,11 @@ struct MemLayout {
     Kf = W + TT * K;
     Qg = Kf + TT * K;
     M = Qg + TT * K;
-    h = M + NB * C * C;
+    A = M + NB * C * C;
+    h = A + NB * C * C;
     D = h + NB * K * V;
-    total = D + TT * V;
+    flags = D + TT * V;  // NB ints: chunk taken by the exact intra-chunk path
+    total = flags + NB;
   }
 };
 struct BwdLayout {
@@ -746,15 +766,22 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   const int NT = cdiv(T, C);
   MemLayout lay(B, T, H, K, V);
   float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg, *M = saved + lay.M,
-        *hb = saved + lay.h, *D = saved + lay.D;
+        *A = saved + lay.A, *hb = saved + lay.h, *D = saved + lay.D;
+  int* flags = reinterpret_cast<int*>(saved + lay.flags);
   dim3 gchunk(NT, B * H);
   if (stages & 1) {
-    if (iso)
-      hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H, NT,
-                         scale, U, W, Kf, Qg, M);
-    else
-      hipLaunchKernelGGL((mem_intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T, H,
-                         NT, scale, U, W, Kf, Qg, M);
+    const int NB = B * H * NT, gx = min(NB, 512);
+    if (iso) {
+      hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T,
+                         H, NT, scale, U, W, Kf, Qg, M, A, flags);
+      hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
+                         T, H, NT, NB, scale, U, W, Kf, Qg, M, A, flags);
+    } else {
+      hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc,
+                         T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
+      hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
+                         T, H, NT, NB, scale, U, W, Kf, Qg, M, A, flags);
+    }
     KDN_CHECK_LAUNCH();
   }
   if (stages & 2) {

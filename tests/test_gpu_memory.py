@@ -142,3 +142,26 @@ def test_memory_scan_extreme_decay_exact_path(variant):
     _check("dv", dv, g_ref[2], TOL_BF16)
     _check("dgate", dell, g_ref[3], TOL_F32 * 5)
     _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+
+
+@pytest.mark.parametrize("variant", ["iso", "diag"])
+def test_memory_scan_mixed_anchor_and_exact_chunks(variant):
+    """One chunk (tokens 64..127) decays by ~e^-8 per token, so its decay span leaves the
+    single-anchor range and that chunk alone takes the exact intra-chunk path, while the
+    chunks before and after it take the MFMA path in the same launch."""
+    dev = gpu_or_skip()
+    B, T, H, K, V = 1, 200, 2, 128, 128
+    log(f"case memory mixed anchor/exact chunks {variant}")
+    iso = variant == "iso"
+    q, k, v, ell, kap, do = memory_inputs(31, B, T, H, K, V, diag=not iso)
+    g = torch.Generator().manual_seed(32)
+    ell[:, 64:128] = (-8.0 + 2.0 * torch.randn(B, 64, H, K, generator=g)).clamp(max=0.0)
+    scale = K ** -0.5
+    o_ref, _, g_ref = _oracle(q, k, v, ell, kap, do, iso=iso, scale=scale)
+    o, _, dq, dkk, dv, dell, dkap, _ = _gpu(q, k, v, ell, kap, do, iso=iso, scale=scale, dev=dev)
+    _check("o", o, o_ref, TOL_F32)
+    _check("dq", dq, g_ref[0], TOL_BF16)
+    _check("dk", dkk, g_ref[1], TOL_BF16)
+    _check("dv", dv, g_ref[2], TOL_BF16)
+    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
+    _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
