@@ -1,0 +1,177 @@
+// Chunk-parallel backward kernels of the KDN memory scan on bf16x3 MFMA.
+//
+// State-gradient products (per chunk, h = state entering the chunk, dh = gradient of the
+// state leaving it, delta / d delta = the chunk's delta and its gradient):
+//   dQg = dO h^T,  dW = -d delta h^T,  dKf = delta dh^T,  dM = lower(dO delta^T),
+//   dgl_i = 2^{G_last,i} sum_v h_iv dh_iv
+// Every product contracts over V, which is the contiguous index of all five operands, so each
+// lane loads its MFMA fragments (8 consecutive v) straight from global memory; no LDS.  Wave w
+// owns the K-row tiles w, w+4 of h and dh (kept as split registers for the whole chunk) and
+// streams the chunk rows of dO, delta and d delta, which the four waves share through L1/L2.
+#pragma once
+#include "kdn_common.h"
+#include "kdn_intra.h"
+#include "kdn_state.h"
+
+namespace kdn_bwd {
+
+using kdn_intra::ld8;
+using kdn_intra::split8;
+using kdn_intra::unpack8;
+using kdn_state::C;
+using kdn_state::mfma;
+using kdn_state::mma3;
+using kdn_state::zero4;
+
+// a*b with a exact in bf16 (A operand) and b = bh + bl split (B operand)
+__device__ __forceinline__ f32x4 mma2b(uint4 a, uint4 bh, uint4 bl, f32x4 c) {
+  c = mfma(a, bh, c);
+  c = mfma(a, bl, c);
+  return c;
+}
+
+// Lower 16x16 tiles (I, J), J <= I, 2-bit packed: 0:(0,0) 1:(1,1) 2:(2,2) 3:(3,3) 4:(1,0)
+// 5:(2,1) 6:(3,2) 7:(2,0) 8:(3,1) 9:(3,0); upper tiles (0,1) (0,2) (0,3) (1,2) (1,3) (2,3).
+__device__ __forceinline__ void lower_tile(int t, int& I, int& J) {
+  I = (0xfb9e4u >> (2 * t)) & 3;
+  J = (0x124e4u >> (2 * t)) & 3;
+}
+__device__ __forceinline__ void upper_tile(int t, int& I, int& J) {
+  I = (0x940u >> (2 * t)) & 3;
+  J = (0xfb9u >> (2 * t)) & 3;
+}
+
+// A fragment (row r, 8 consecutive v from v0) of a [rows][V] operand; bf16 input is exact (lo = 0).
+template <typename T>
+__device__ __forceinline__ void row_frag(bufrsrc r, uint32_t elem, uint4& hi, uint4& lo);
+template <>
+__device__ __forceinline__ void row_frag<float>(bufrsrc r, uint32_t elem, uint4& hi, uint4& lo) {
+  float x[8];
+  ld8(r, elem * 4, x);
+  split8(x, hi, lo);
+}
+template <>
+__device__ __forceinline__ void row_frag<bf16_t>(bufrsrc r, uint32_t elem, uint4& hi, uint4& lo) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, elem * 2, 0, 0);
+  hi = uint4{v.x, v.y, v.z, v.w};
+  lo = uint4{0u, 0u, 0u, 0u};
+}
+
+// grid (NT, B*H), block 256.
+template <int K, int V, typename TDO>
+__global__ __launch_bounds__(256, 2) void hgrad_kernel(const float* __restrict__ hbuf, const float* __restrict__ dhbuf,
+                                                       const float* __restrict__ Dl, const float* __restrict__ dDl,
+                                                       const TDO* __restrict__ dO, const float* __restrict__ gc,
+                                                       int T, int H, int NT, float* __restrict__ dQg,
+                                                       float* __restrict__ dW, float* __restrict__ dKf,
+                                                       float* __restrict__ dMg, float* __restrict__ dgl) {
+  constexpr bool DO_BF16 = sizeof(TDO) == 2;
+  constexpr int VB = V / 32;          // k-blocks of the V contraction
+  constexpr int NIT = K / 16;         // K-row tiles of h / dh
+  constexpr int ITW = (NIT + 3) / 4;  // per wave
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+
+  const int64_t chunk = (int64_t)bh * NT + n;
+  const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
+  const bufrsrc rdh = make_buf(dhbuf + chunk * K * V, K * V * 4);
+  const bufrsrc rD = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const bufrsrc rdD = make_buf(dDl + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const bufrsrc rO = make_buf(dO + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * sizeof(TDO));
+  const bufrsrc rQ = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rW = make_buf(dW + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rM = make_buf(dMg + chunk * C * C, C * C * 4);
+
+  // ---- h and dh rows of this wave's tiles as B fragments (col i, k = v), and the g_last dot
+  uint4 hh[ITW][VB], hl[ITW][VB], dhh[ITW][VB], dhl[ITW][VB];
+#pragma unroll
+  for (int u = 0; u < ITW; ++u) {
+    const int it = w + 4 * u;
+    if (it >= NIT) break;
+    const int i = 16 * it + r16;
+    float dot = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) {
+      const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
+      float x[8], y[8];
+      ld8(rh, e * 4, x);
+      ld8(rdh, e * 4, y);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dot += x[j] * y[j];
+      split8(x, hh[u][kb], hl[u][kb]);
+      split8(y, dhh[u][kb], dhl[u][kb]);
+    }
+    dot += __shfl_xor(dot, 16, 64);
+    dot += __shfl_xor(dot, 32, 64);
+    if (g4 == 0) dgl[chunk * K + i] = dot * exp2f(gc[(((int64_t)b * T + t0 + L - 1) * H + h) * K + i]);
+  }
+
+  // ---- dQg, dW, dKf: row block cb x this wave's K tiles
+#pragma unroll 1
+  for (int cb = 0; cb < 4; ++cb) {
+    f32x4 aQ[ITW], aW[ITW], aK[ITW];
+#pragma unroll
+    for (int u = 0; u < ITW; ++u) aQ[u] = aW[u] = aK[u] = zero4();
+    const uint32_t crow = (uint32_t)(16 * cb + r16);
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) {
+      const uint32_t v0 = 32 * kb + 8 * g4;
+      uint4 oh, ol, ddh, ddl, dh_, dl_;
+      row_frag<TDO>(rO, crow * H * V + v0, oh, ol);
+      row_frag<float>(rdD, crow * V + v0, ddh, ddl);
+      row_frag<float>(rD, crow * V + v0, dh_, dl_);
+#pragma unroll
+      for (int u = 0; u < ITW; ++u) {
+        if (w + 4 * u >= NIT) break;
+        aQ[u] = DO_BF16 ? mma2b(oh, hh[u][kb], hl[u][kb], aQ[u]) : mma3(oh, ol, hh[u][kb], hl[u][kb], aQ[u]);
+        aW[u] = mma3(ddh, ddl, hh[u][kb], hl[u][kb], aW[u]);
+        aK[u] = mma3(dh_, dl_, dhh[u][kb], dhl[u][kb], aK[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < ITW; ++u) {
+      const int it = w + 4 * u;
+      if (it >= NIT) break;
+      const int i = 16 * it + r16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t o = ((16 * cb + 4 * g4 + j) * K + i) * 4;
+        buf_st(rQ, o, aQ[u][j]);
+        buf_st(rW, o, -aW[u][j]);
+        buf_st(rKf, o, aK[u][j]);
+      }
+    }
+  }
+
+  // ---- dM = lower(dO delta^T): lower tiles w, w+4, w+8; upper tiles are zero
+#pragma unroll 1
+  for (int t = w; t < 10; t += 4) {
+    int I, J;
+    lower_tile(t, I, J);
+    f32x4 acc = zero4();
+    const uint32_t crow = (uint32_t)(16 * I + r16), srow = (uint32_t)(16 * J + r16);
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) {
+      const uint32_t v0 = 32 * kb + 8 * g4;
+      uint4 oh, ol, dh_, dl_;
+      row_frag<TDO>(rO, crow * H * V + v0, oh, ol);
+      row_frag<float>(rD, srow * V + v0, dh_, dl_);
+      acc = DO_BF16 ? mma2b(oh, dh_, dl_, acc) : mma3(oh, ol, dh_, dl_, acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 16 * I + 4 * g4 + j, s = 16 * J + r16;
+      buf_st(rM, (c * C + s) * 4, s <= c ? acc[j] : 0.f);
+    }
+  }
+  for (int t = w; t < 6; t += 4) {
+    int I, J;
+    upper_tile(t, I, J);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * I + 4 * g4 + j) * C + 16 * J + r16) * 4, 0.f);
+  }
+}
+
+}  // namespace kdn_bwd

@@ -30,6 +30,7 @@
 #include "kdn_common.h"
 #include "kdn_state.h"
 #include "kdn_intra.h"
+#include "kdn_bwd.h"
 #include "../../include/kdn.h"
 
 namespace {
@@ -820,7 +821,7 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     KDN_CHECK_LAUNCH();
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((mem_bwd_hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H,
+    hipLaunchKernelGGL((kdn_bwd::hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H,
                        NT, dQg, dW, dKf, dM, dgl);
     KDN_CHECK_LAUNCH();
   }
