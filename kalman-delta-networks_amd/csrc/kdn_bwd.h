@@ -174,4 +174,138 @@ __global__ __launch_bounds__(256, 2) void hgrad_kernel(const float* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Transposed solves with the saved inverse (At[s][c] = A[c][s], A = (I + N)^{-1}) and dN:
+//   dV^T = d delta^T A,  dKg^T = dW^T A          (contraction over chunk rows c >= s)
+//   dN = -strict_lower(dV U^T + dKg W^T)
+// Column blocks of 32 (V/32 of d delta, then K/32 of dW) go to the waves round-robin.  A block's
+// dV^T (dKg^T) tiles stay in the accumulator layout, which is the B operand (k = column, permuted
+// order) of the block's share of dN^T; the four per-wave shares are summed through LDS.
+// Chunks flagged by the forward (outside the single-anchor range) are left to the exact kernel.
+// grid (NT, B*H), block 256.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ int lower_tile_index(int I, int J) {
+  const int d = I - J;
+  return d == 0 ? I : d == 1 ? 4 + J : d == 2 ? 7 + J : 9;
+}
+
+template <int K, int V>
+__global__ __launch_bounds__(256, 2) void solve_kernel(const float* __restrict__ At, const float* __restrict__ dDl,
+                                                       const float* __restrict__ dWg, const float* __restrict__ U,
+                                                       const float* __restrict__ W, const int* __restrict__ flags,
+                                                       int T, int H, int NT, bf16_t* __restrict__ dv,
+                                                       float* __restrict__ dKg, float* __restrict__ dNg) {
+  constexpr int NBLK = (V + K) / 32;
+  constexpr int AP4 = C + 4;  // LDS row stride of A^T (16-byte rows)
+  __shared__ __attribute__((aligned(16))) float sAt[C * AP4];
+  __shared__ __attribute__((aligned(16))) float sP[4 * 10 * 256];  // per-wave partial dN^T tiles
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int64_t chunk = (int64_t)bh * NT + n;
+  if (flags[chunk]) return;
+
+  {
+    const bufrsrc rA = make_buf(At + chunk * C * C, C * C * 4);
+#pragma unroll
+    for (int u = 0; u < C * C / 4 / 256; ++u) {
+      const int e4 = tid + 256 * u, sr = e4 / (C / 4), c4 = e4 % (C / 4);
+      *reinterpret_cast<float4*>(sAt + sr * AP4 + 4 * c4) = buf_ld4(rA, (sr * C + 4 * c4) * 4);
+    }
+  }
+  __syncthreads();
+
+  const bufrsrc rdv = make_buf(dv + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * 2);
+  const bufrsrc rdKg = make_buf(dKg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  f32x4 part[10];
+#pragma unroll
+  for (int t = 0; t < 10; ++t) part[t] = zero4();
+
+#pragma unroll 1
+  for (int blk = w; blk < NBLK; blk += 4) {
+    const bool isV = blk < V / 32;
+    const int col0 = 32 * (isV ? blk : blk - V / 32), D = isV ? V : K;
+    const bufrsrc rX = make_buf((isV ? dDl : dWg) + ((int64_t)bh * T + t0) * D, L * D * 4);
+    const bufrsrc rY = make_buf((isV ? U : W) + ((int64_t)bh * T + t0) * D, L * D * 4);
+    // ---- Y = X^T A for the block's two column tiles and the four time blocks
+    f32x4 Y[2][4];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int J = 0; J < 4; ++J) Y[ct][J] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      uint4 xh[2], xl[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        float xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[j] = buf_ld(rX, ((32 * kb + 8 * g4 + j) * D + col0 + 16 * ct + r16) * 4);
+        split8(xv, xh[ct], xl[ct]);
+      }
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        if (J > 2 * kb + 1) continue;  // A[c][s] = 0 for c < s
+        const float* row = sAt + (16 * J + r16) * AP4 + 32 * kb + 8 * g4;
+        const float4 a0 = *reinterpret_cast<const float4*>(row), a1 = *reinterpret_cast<const float4*>(row + 4);
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        uint4 ah, al;
+        split8(av, ah, al);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) Y[ct][J] = mma3(xh[ct], xl[ct], ah, al, Y[ct][J]);
+      }
+    }
+    // ---- outputs: dv (bf16 [B,T,H,V]) or dKg (fp32 [B*H,T,K]); Y rows = columns, Y cols = time
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        const uint32_t tr = (uint32_t)(16 * J + r16), x0 = (uint32_t)(col0 + 16 * ct + 4 * g4);
+        const f32x4 y = Y[ct][J];
+        if (isV) {
+          const uint32_t lo = (uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16);
+          const uint32_t hi = (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16);
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rdv, ((tr * H) * V + x0) * 2, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])}, rdKg,
+              (tr * K + x0) * 4, 0, 0);
+        }
+      }
+    // ---- this block's share of dN^T[s][c] = sum_x (U|W)[s][x] Y[x][c]: A = U|W rows (k = x, permuted), B = Y
+    uint4 uh[4], ul[4], yh[4], yl[4];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      const uint32_t sr = (uint32_t)(16 * J + r16);
+      const float4 a0 = buf_ld4(rY, (sr * D + col0 + 4 * g4) * 4), a1 = buf_ld4(rY, (sr * D + col0 + 16 + 4 * g4) * 4);
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      split8(av, uh[J], ul[J]);
+      kdn_state::bfrag(Y[0][J], Y[1][J], yh[J], yl[J]);
+    }
+#pragma unroll
+    for (int t = 0; t < 10; ++t) {
+      int I, J;
+      lower_tile(t, I, J);  // dN tile (c-block I, s-block J) = dN^T tile (rows s-block J, cols c-block I)
+      part[t] = mma3(uh[J], ul[J], yh[I], yl[I], part[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 10; ++t)
+    *reinterpret_cast<f32x4*>(sP + ((w * 10 + t) * 64 + lane) * 4) = part[t];
+  __syncthreads();
+  // dN[c][s] = -sum over waves, strictly lower; zeros elsewhere
+  const bufrsrc rN = make_buf(dNg + chunk * C * C, C * C * 4);
+#pragma unroll 4
+  for (int u = 0; u < C * C / 256; ++u) {
+    const int e = tid + 256 * u, c = e / C, sc = e % C;
+    float val = 0.f;
+    if (sc < c) {
+      const int t = lower_tile_index(c >> 4, sc >> 4), ln = (c & 15) + 16 * ((sc & 15) >> 2), j = sc & 3;
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) val -= sP[((ww * 10 + t) * 64 + ln) * 4 + j];
+    }
+    buf_st(rN, e * 4, val);
+  }
+}
+
 }  // namespace kdn_bwd

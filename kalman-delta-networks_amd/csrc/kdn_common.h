@@ -31,6 +31,7 @@ template <> __device__ __forceinline__ void st<bf16_t>(bf16_t* p, int64_t i, flo
 // per-element bounds branches; offsets are 32-bit bytes.  `base` must be wave-uniform.
 typedef __amdgpu_buffer_rsrc_t bufrsrc;
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ bufrsrc make_buf(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

@@ -7,7 +7,7 @@
 //   A = (I + N)^{-1}:  16x16 diagonal blocks by substitution, off-diagonal blocks level by level
 //                      A_IJ = -A_II sum_{J<=P<I} N_IP A_PJ           (fp32 MFMA)
 //   U = A V,  W = A (k 2^G),  Kf = kappa 2^{G_last - G},  Qg = scale q 2^G
-// A is saved for the backward.  R <= 2^span where span = max_i (G_0 - G_{L-1})_i; chunks with
+// A^T is saved for the backward.  R <= 2^span where span = max_i (G_0 - G_{L-1})_i; chunks with
 // span > kAnchorSpanMax are flagged (flags[chunk] = 1) and left to the exact per-block kernel,
 // which runs after this one over the flagged chunks only.
 //
@@ -222,13 +222,13 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     __syncthreads();
   }
 
-  // ---- 5. save A for the backward
+  // ---- 5. save A^T ([s][c], the orientation the backward contracts over) for the backward
   {
     const bufrsrc rA = make_buf(An, C * C * 4);
 #pragma unroll
     for (int u = 0; u < C * C / 256; ++u) {
       const int e = tid + 256 * u;
-      buf_st(rA, e * 4, sA[(e / C) * AP + (e % C)]);
+      buf_st(rA, e * 4, sA[(e % C) * AP + (e / C)]);
     }
   }
 

@@ -461,12 +461,14 @@ __global__ __launch_bounds__(256) void mem_bwd_hgrad_kernel(
 // ===========================================================================
 // Backward: transposed triangular solves and dN.
 // ===========================================================================
+// Exact path for one chunk (rebuilds N with per-block anchors, scalar back substitution); runs
+// only for the chunks the forward flagged as outside the single-anchor range.
 template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256) void mem_bwd_solve_kernel(
+__device__ void bwd_solve_exact_chunk(
     const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, bf16_t* __restrict__ dv, float* __restrict__ dKg,
-    float* __restrict__ dNg) {
+    float* __restrict__ dNg, int n, int bh) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // phase 1: sK | sA | sG (3 x C x KP); phase 2 (after the solve) reuses it as sX | sUW (2 x C x XP)
@@ -478,7 +480,7 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_kernel(
   float* sK = sBuf;
   float* sA = sBuf + C * KP;
   float* sG = sBuf + 2 * C * KP;
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   stage_chunk<K, ISO, float>(nullptr, k, kap, gc, b, h, T, H, t0, L, (float*)nullptr, sK, sA, sG, sSpan);
@@ -552,6 +554,19 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_kernel(
       const int c = 16 * I + 4 * (lane >> 4) + jj, s = 16 * J + (lane & 15);
       dNn[c * C + s] = (s < c) ? -acc[jj] : 0.f;
     }
+  }
+}
+
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_bwd_solve_exact_kernel(
+    const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
+    const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
+    const float* __restrict__ W, int T, int H, int NT, int NB, const int* __restrict__ flags, bf16_t* __restrict__ dv,
+    float* __restrict__ dKg, float* __restrict__ dNg) {
+  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
+    if (flags[lin] == 0) continue;
+    __syncthreads();
+    bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, lin % NT, lin / NT);
   }
 }
 
@@ -811,7 +826,8 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   MemLayout lay(B, T, H, K, V);
   BwdLayout bl(B, T, H, K, V);
   const float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg,
-              *M = saved + lay.M, *hb = saved + lay.h, *D = saved + lay.D;
+              *M = saved + lay.M, *A = saved + lay.A, *hb = saved + lay.h, *D = saved + lay.D;
+  const int* flags = reinterpret_cast<const int*>(saved + lay.flags);
   float *dh = work + bl.dh, *dD = work + bl.dD, *dQg = work + bl.dQg, *dW = work + bl.dW, *dKf = work + bl.dKf,
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
@@ -826,12 +842,15 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     KDN_CHECK_LAUNCH();
   }
   if (stages & 4) {
+    const int NB = B * H * NT, gx = min(NB, 512);
+    hipLaunchKernelGGL((kdn_bwd::solve_kernel<K, V>), gchunk, dim3(256), 0, stream, A, dD, dW, U, W, flags, T, H, NT, dv,
+                       dKg, dN);
     if (iso)
-      hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, true>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W,
-                         T, H, NT, dv, dKg, dN);
+      hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD, dW,
+                         U, W, T, H, NT, NB, flags, dv, dKg, dN);
     else
-      hipLaunchKernelGGL((mem_bwd_solve_kernel<K, V, false>), gchunk, dim3(256), 0, stream, k, kap, gc, dD, dW, U, W,
-                         T, H, NT, dv, dKg, dN);
+      hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD,
+                         dW, U, W, T, H, NT, NB, flags, dv, dKg, dN);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 8) {
