@@ -22,6 +22,8 @@ using kdn_state::C;
 using kdn_state::mfma;
 using kdn_state::mma3;
 using kdn_state::zero4;
+using kdn_state::afrag;
+using kdn_state::TILE;
 
 // a*b with a exact in bf16 (A operand) and b = bh + bl split (B operand)
 __device__ __forceinline__ f32x4 mma2b(uint4 a, uint4 bh, uint4 bl, f32x4 c) {
@@ -305,6 +307,187 @@ __global__ __launch_bounds__(256, 2) void solve_kernel(const float* __restrict__
       for (int ww = 0; ww < 4; ++ww) val -= sP[((ww * 10 + t) * 64 + ln) * 4 + j];
     }
     buf_st(rN, e * 4, val);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Gradients of q, k, kappa (iso: beta) and the gate, from dN, dM and the elementwise factors.
+// With the forward's row-0 anchor, per element (c, i):
+//   e0 = 2^{G_c - G_0}, Lk = k e0, Lq = q e0, R = kappa / e0, eg = 2^{G_c}, f = 2^{G_last - G_c}
+//   dLk = dN R,  dLq = scale dM R,  dR = dN^T Lk + scale dM^T Lq          (bf16x3 MFMA)
+//   dk = dLk e0 + dKg eg,  dq = dLq e0 + scale dQg eg,  dkappa = dR / e0 + dKf f
+//   dg = Lk dLk + Lq dLq - R dR + k eg dKg + scale q eg dQg - kappa f dKf  (natural-log coordinates)
+//   dg[last row] += sum_c kappa f dKf + dgl;   iso: dbeta = sum_i dkappa k, dk += beta dkappa
+// The anchor terms cancel exactly (N and M do not depend on the anchor) and are omitted.
+// Wave w owns the channel tiles w, w+4 and holds the factors at its accumulator positions
+// (rows = chunk rows, column = channel), which are also the permuted-k B operands of the
+// time contractions; dN, dM, dN^T, dM^T are split once per workgroup into LDS fragments.
+// grid (NT, B*H), block 256.  Chunks flagged by the forward go to the exact kernel.
+// ---------------------------------------------------------------------------------------------
+template <int K, bool ISO>
+__global__ __launch_bounds__(256, 2) void contrib_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
+    const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
+    const float* __restrict__ dgl, const int* __restrict__ flags, int T, int H, int NT, float scale,
+    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
+    float* __restrict__ dg) {
+  constexpr int NIT = K / 16;
+  constexpr int ITW = (NIT + 3) / 4;
+  constexpr int FR = 8 * TILE;  // one 64 x 64 operand as (4 row tiles x 2 k-blocks) fragments
+  __shared__ __attribute__((aligned(16))) bf16_t sF[4 * FR];  // dN rows, dM rows, dN^T rows, dM^T rows
+  __shared__ float sBeta[4 * C];
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int64_t chunk = (int64_t)bh * NT + n;
+  if (flags[chunk]) return;
+
+  // ---- stage dN, dM (rows c, k = s) and their transposes (rows s, k = c) as split fragments in
+  // the permuted k order: slot 4h + j of lane group g <-> k = 32 kb + 16 h + 4 g + j
+  {
+    const bufrsrc rN = make_buf(dNg + chunk * C * C, C * C * 4), rM = make_buf(dMg + chunk * C * C, C * C * 4);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // unit: (row, kb, h, g) -> 4 consecutive slots of one lane
+      const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
+      const int k0 = 32 * kb + 16 * hh + 4 * gg;
+      const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
+      float x[4], y[4], xt[4], yt[4];
+      const float4 a = buf_ld4(rN, (row * C + k0) * 4), bq = buf_ld4(rM, (row * C + k0) * 4);
+      x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w;
+      y[0] = bq.x, y[1] = bq.y, y[2] = bq.z, y[3] = bq.w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xt[j] = buf_ld(rN, ((k0 + j) * C + row) * 4);
+        yt[j] = buf_ld(rM, ((k0 + j) * C + row) * 4);
+      }
+      kdn_state::put_unit(sF, off, x[0], x[1], x[2], x[3]);
+      kdn_state::put_unit(sF + FR, off, y[0], y[1], y[2], y[3]);
+      kdn_state::put_unit(sF + 2 * FR, off, xt[0], xt[1], xt[2], xt[3]);
+      kdn_state::put_unit(sF + 3 * FR, off, yt[0], yt[1], yt[2], yt[3]);
+    }
+  }
+  __syncthreads();
+
+  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
+  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rdkap = ISO ? make_buf(dkap, 0) : make_buf(dkap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rdg = make_buf(dg + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rdQg = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rdKg = make_buf(dKg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rdKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
+  float bpart[16];
+#pragma unroll
+  for (int p = 0; p < 16; ++p) bpart[p] = 0.f;
+
+#pragma unroll 1
+  for (int u = 0; u < ITW; ++u) {
+    const int it = w + 4 * u;
+    if (it >= NIT) break;
+    const int i = 16 * it + r16;
+    const float g0 = buf_ld(rG, i * 4), gl = buf_ld(rG, ((uint32_t)((L - 1) * H) * K + i) * 4);
+    // factors at this lane's positions: rows c = 16 tl + 4 g4 + j
+    f32x4 Lk[4], Lq[4], Rv[4];
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t crow = (uint32_t)((16 * tl + 4 * g4 + j) * H);
+        const float kv = buf_ld_bf16(rk, (crow * K + i) * 2), qv = buf_ld_bf16(rq, (crow * K + i) * 2);
+        const float av = ISO ? buf_ld(rkap, crow * 4) * kv : buf_ld(rkap, (crow * K + i) * 4);
+        const float e0 = exp2f(buf_ld(rG, (crow * K + i) * 4) - g0);
+        Lk[tl][j] = kv * e0;
+        Lq[tl][j] = scale * qv * e0;
+        Rv[tl][j] = av * exp2f(g0 - buf_ld(rG, (crow * K + i) * 4));
+      }
+    uint4 Rh[2], Rl[2], Kh[2], Kl[2], Qh[2], Ql[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      kdn_state::bfrag(Rv[2 * kb], Rv[2 * kb + 1], Rh[kb], Rl[kb]);
+      kdn_state::bfrag(Lk[2 * kb], Lk[2 * kb + 1], Kh[kb], Kl[kb]);
+      kdn_state::bfrag(Lq[2 * kb], Lq[2 * kb + 1], Qh[kb], Ql[kb]);
+    }
+    // ---- time contractions
+    f32x4 dLk[4], dLq[4], dR[4];
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      dLk[tl] = dLq[tl] = dR[tl] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        uint4 ah, al;
+        if (kb <= tl / 2) {  // dN, dM rows c: nonzero for s <= c
+          afrag(sF, tl * 2 + kb, lane, ah, al);
+          dLk[tl] = mma3(ah, al, Rh[kb], Rl[kb], dLk[tl]);
+          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
+          dLq[tl] = mma3(ah, al, Rh[kb], Rl[kb], dLq[tl]);
+        }
+        if (2 * kb + 1 >= tl) {  // dN^T, dM^T rows s: nonzero for c >= s
+          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
+          dR[tl] = mma3(ah, al, Kh[kb], Kl[kb], dR[tl]);
+          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
+          dR[tl] = mma3(ah, al, Qh[kb], Ql[kb], dR[tl]);
+        }
+      }
+    }
+    // ---- assemble
+    float colpart = 0.f, dg_last = 0.f;
+    int last_slot = -1;
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 16 * tl + 4 * g4 + j;
+        const uint32_t crow = (uint32_t)(c * H), o = crow * K + i, ol = (uint32_t)c * K + i;
+        const float kv = buf_ld_bf16(rk, o * 2), qv = buf_ld_bf16(rq, o * 2);
+        const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+        const float av = ISO ? beta * kv : buf_ld(rkap, o * 4);
+        const float Gc = buf_ld(rG, o * 4);
+        const float e0 = exp2f(Gc - g0), eg = exp2f(Gc), f = exp2f(gl - Gc);
+        const float dkg = buf_ld(rdKg, ol * 4), dqg = buf_ld(rdQg, ol * 4), dkf = buf_ld(rdKf, ol * 4);
+        const float lk = Lk[tl][j], lq = qv * e0, rv = Rv[tl][j];  // Lq unscaled (registers hold scale Lq)
+        const float a_lk = dLk[tl][j], a_lq = dLq[tl][j] * scale, a_r = dR[tl][j];
+        float dkv = a_lk * e0 + dkg * eg;
+        const float dqv = a_lq * e0 + scale * dqg * eg;
+        const float dav = (e0 > 0.f ? a_r / e0 : 0.f) + dkf * f;
+        float dgv = lk * a_lk + lq * a_lq - rv * a_r + kv * eg * dkg + scale * qv * eg * dqg - av * f * dkf;
+        if (c < L) colpart += av * f * dkf;
+        if (ISO) {
+          dkv += beta * dav;
+          bpart[4 * tl + j] += dav * kv;
+        } else {
+          buf_st(rdkap, o * 4, dav);
+        }
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(dqv), rdq, o * 2, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(dkv), rdk, o * 2, 0, 0);
+        if (c == L - 1) {
+          dg_last = dgv;
+          last_slot = 4 * tl + j;
+        } else {
+          buf_st(rdg, o * 4, dgv);
+        }
+      }
+    colpart += __shfl_xor(colpart, 16, 64);
+    colpart += __shfl_xor(colpart, 32, 64);
+    if (last_slot >= 0)
+      buf_st(rdg, ((uint32_t)((L - 1) * H) * K + i) * 4, dg_last + colpart + dgl[chunk * K + i]);
+  }
+  if (ISO) {  // dbeta[c] = sum_i dkappa k: over the 16 channels of a tile, this wave's tiles, then the waves
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      float v = bpart[p];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+      if (r16 == 0) sBeta[w * C + 16 * (p >> 2) + 4 * g4 + (p & 3)] = v;
+    }
+    __syncthreads();
+    if (tid < L) dbeta[((int64_t)b * T + t0 + tid) * H + h] = sBeta[tid] + sBeta[C + tid] + sBeta[2 * C + tid] +
+                                                               sBeta[3 * C + tid];
   }
 }
 

@@ -571,16 +571,19 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_exact_kernel(
 }
 
 // ===========================================================================
-// Backward: gradients of q, k, kappa (beta) and g from dN, dM and elementwise factors.
-// Output tile (row block I, 16 channels); lane holds rows 16I + 4(lane/16) + j.
+// Backward, exact path for one chunk: gradients of q, k, kappa (beta) and g from dN, dM and
+// the elementwise factors with per-block anchors and per-element diagonal blocks; runs only
+// for the chunks the forward flagged.  Output tile (row block I, 16 channels); lane holds
+// rows 16I + 4(lane/16) + j.
 // ===========================================================================
 template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
+__device__ void bwd_contrib_exact_chunk(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
     const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
     const float* __restrict__ dgl, int T, int H, int NT, float scale, bf16_t* __restrict__ dq,
-    bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg) {
+    bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, int n,
+    int bh) {
   constexpr int KP = K + 4;
   constexpr int NCT = K / 16;  // channel tiles
   constexpr int KQ = QKStride<K, bf16_t>::value;
@@ -591,7 +594,7 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
   __shared__ float sColPart[4 * K];     // per row block partial of sum_c dKf kappa e^{g_last - g}
   __shared__ float sDgLast[K];          // dg of row L-1 before the g_last terms
   __shared__ float sBetaPart[C * NCT];  // iso: per (row, channel tile) partial of sum_i dkappa k
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   stage_chunk<K, ISO, bf16_t>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
@@ -738,6 +741,22 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_kernel(
   }
 }
 
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
+    const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
+    const float* __restrict__ dgl, int T, int H, int NT, int NB, const int* __restrict__ flags, float scale,
+    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
+    float* __restrict__ dg) {
+  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
+    if (flags[lin] == 0) continue;
+    __syncthreads();
+    bwd_contrib_exact_chunk<K, V, ISO>(q, k, kap, gc, dNg, dMg, dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap,
+                                       dbeta, dg, lin % NT, lin / NT);
+  }
+}
+
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 // saved-buffer layout (floats), TT = B*H*T, NB = B*H*NT
@@ -854,12 +873,18 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     KDN_CHECK_LAUNCH();
   }
   if (stages & 8) {
-    if (iso)
-      hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM,
-                         dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
-    else
-      hipLaunchKernelGGL((mem_bwd_contrib_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM,
-                         dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+    const int NB = B * H * NT, gx = min(NB, 512);
+    if (iso) {
+      hipLaunchKernelGGL((kdn_bwd::contrib_kernel<K, true>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM, dQg,
+                         dKg, dKf, dgl, flags, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+      hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc, dN,
+                         dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
+    } else {
+      hipLaunchKernelGGL((kdn_bwd::contrib_kernel<K, false>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM, dQg,
+                         dKg, dKf, dgl, flags, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+      hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc,
+                         dN, dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
+    }
     KDN_CHECK_LAUNCH();
   }
   return 0;
