@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void solve_kernel(const float* __restrict__
 // grid (NT, B*H), block 256.  Chunks flagged by the forward go to the exact kernel.
 // ---------------------------------------------------------------------------------------------
 template <int K, bool ISO>
-__global__ __launch_bounds__(256, 2) void contrib_kernel(
+__global__ __launch_bounds__(256, 1) void contrib_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
     const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
@@ -391,27 +391,37 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
     const int it = w + 4 * u;
     if (it >= NIT) break;
     const int i = 16 * it + r16;
+    // ---- loads in two batches (factor inputs, then gradient inputs) so the wave waits for memory
+    // twice per channel tile instead of once per row; rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j
+    float kv[16], qv[16], av[16], Gv[16], dkg[16], dqg[16], dkf[16];
     const float g0 = buf_ld(rG, i * 4), gl = buf_ld(rG, ((uint32_t)((L - 1) * H) * K + i) * 4);
-    // factors at this lane's positions: rows c = 16 tl + 4 g4 + j
-    f32x4 Lk[4], Lq[4], Rv[4];
 #pragma unroll
-    for (int tl = 0; tl < 4; ++tl)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t crow = (uint32_t)((16 * tl + 4 * g4 + j) * H);
-        const float kv = buf_ld_bf16(rk, (crow * K + i) * 2), qv = buf_ld_bf16(rq, (crow * K + i) * 2);
-        const float av = ISO ? buf_ld(rkap, crow * 4) * kv : buf_ld(rkap, (crow * K + i) * 4);
-        const float e0 = exp2f(buf_ld(rG, (crow * K + i) * 4) - g0);
-        Lk[tl][j] = kv * e0;
-        Lq[tl][j] = scale * qv * e0;
-        Rv[tl][j] = av * exp2f(g0 - buf_ld(rG, (crow * K + i) * 4));
-      }
+    for (int p = 0; p < 16; ++p) {
+      const int c = 16 * (p >> 2) + 4 * g4 + (p & 3);
+      const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
+      kv[p] = buf_ld_bf16(rk, o * 2);
+      qv[p] = buf_ld_bf16(rq, o * 2);
+      av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);  // iso: beta of the row
+      Gv[p] = buf_ld(rG, o * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the batch together
+    // factors at this lane's positions, as permuted-k B fragments per 32-row block
     uint4 Rh[2], Rl[2], Kh[2], Kl[2], Qh[2], Ql[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      kdn_state::bfrag(Rv[2 * kb], Rv[2 * kb + 1], Rh[kb], Rl[kb]);
-      kdn_state::bfrag(Lk[2 * kb], Lk[2 * kb + 1], Kh[kb], Kl[kb]);
-      kdn_state::bfrag(Lq[2 * kb], Lq[2 * kb + 1], Qh[kb], Ql[kb]);
+      float lk[8], lq[8], rv[8];
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl) {
+        const int p = 8 * kb + sl;  // tiles 2kb (slots 0-3) and 2kb+1 (slots 4-7)
+        const float kap_p = ISO ? av[p] * kv[p] : av[p];
+        const float e0 = exp2f(Gv[p] - g0);
+        lk[sl] = kv[p] * e0;
+        lq[sl] = scale * qv[p] * e0;
+        rv[sl] = kap_p * exp2f(g0 - Gv[p]);
+      }
+      split8(rv, Rh[kb], Rl[kb]);
+      split8(lk, Kh[kb], Kl[kb]);
+      split8(lq, Qh[kb], Ql[kb]);
     }
     // ---- time contractions
     f32x4 dLk[4], dLq[4], dR[4];
@@ -435,47 +445,53 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
         }
       }
     }
+    // ---- second batch: the elementwise gradient inputs
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t ol = (uint32_t)(16 * (p >> 2) + 4 * g4 + (p & 3)) * K + i;
+      dkg[p] = buf_ld(rdKg, ol * 4);
+      dqg[p] = buf_ld(rdQg, ol * 4);
+      dkf[p] = buf_ld(rdKf, ol * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // ---- assemble
     float colpart = 0.f, dg_last = 0.f;
-    int last_slot = -1;
+    bool has_last = false;
 #pragma unroll
-    for (int tl = 0; tl < 4; ++tl)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = 16 * tl + 4 * g4 + j;
-        const uint32_t crow = (uint32_t)(c * H), o = crow * K + i, ol = (uint32_t)c * K + i;
-        const float kv = buf_ld_bf16(rk, o * 2), qv = buf_ld_bf16(rq, o * 2);
-        const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
-        const float av = ISO ? beta * kv : buf_ld(rkap, o * 4);
-        const float Gc = buf_ld(rG, o * 4);
-        const float e0 = exp2f(Gc - g0), eg = exp2f(Gc), f = exp2f(gl - Gc);
-        const float dkg = buf_ld(rdKg, ol * 4), dqg = buf_ld(rdQg, ol * 4), dkf = buf_ld(rdKf, ol * 4);
-        const float lk = Lk[tl][j], lq = qv * e0, rv = Rv[tl][j];  // Lq unscaled (registers hold scale Lq)
-        const float a_lk = dLk[tl][j], a_lq = dLq[tl][j] * scale, a_r = dR[tl][j];
-        float dkv = a_lk * e0 + dkg * eg;
-        const float dqv = a_lq * e0 + scale * dqg * eg;
-        const float dav = (e0 > 0.f ? a_r / e0 : 0.f) + dkf * f;
-        float dgv = lk * a_lk + lq * a_lq - rv * a_r + kv * eg * dkg + scale * qv * eg * dqg - av * f * dkf;
-        if (c < L) colpart += av * f * dkf;
-        if (ISO) {
-          dkv += beta * dav;
-          bpart[4 * tl + j] += dav * kv;
-        } else {
-          buf_st(rdkap, o * 4, dav);
-        }
-        __builtin_amdgcn_raw_buffer_store_b16(f2bf(dqv), rdq, o * 2, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b16(f2bf(dkv), rdk, o * 2, 0, 0);
-        if (c == L - 1) {
-          dg_last = dgv;
-          last_slot = 4 * tl + j;
-        } else {
-          buf_st(rdg, o * 4, dgv);
-        }
+    for (int p = 0; p < 16; ++p) {
+      const int tl = p >> 2, j = p & 3;
+      const int c = 16 * tl + 4 * g4 + j;
+      const uint32_t o = (uint32_t)(c * H) * K + i;
+      const float beta = ISO ? av[p] : 0.f;
+      const float kap_p = ISO ? beta * kv[p] : av[p];
+      const float er = exp2f(g0 - Gv[p]), e0 = exp2f(Gv[p] - g0), eg = exp2f(Gv[p]), f = exp2f(gl - Gv[p]);
+      const float a_lk = dLk[tl][j], a_lq = dLq[tl][j] * scale, a_r = dR[tl][j];
+      float dkv = a_lk * e0 + dkg[p] * eg;
+      const float dqv = a_lq * e0 + scale * dqg[p] * eg;
+      const float dav = a_r * er + dkf[p] * f;
+      // Lk = k e0, Lq (unscaled) = q e0, R = kappa er
+      const float dgv = kv[p] * e0 * a_lk + qv[p] * e0 * a_lq - kap_p * er * a_r + kv[p] * eg * dkg[p] +
+                        scale * qv[p] * eg * dqg[p] - kap_p * f * dkf[p];
+      if (c < L) colpart += kap_p * f * dkf[p];
+      if (ISO) {
+        dkv += beta * dav;
+        bpart[p] += dav * kv[p];
+      } else {
+        buf_st(rdkap, o * 4, dav);
       }
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dqv), rdq, o * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dkv), rdk, o * 2, 0, 0);
+      if (c == L - 1) {
+        dg_last = dgv;
+        has_last = true;
+      } else {
+        buf_st(rdg, o * 4, dgv);
+      }
+    }
     colpart += __shfl_xor(colpart, 16, 64);
     colpart += __shfl_xor(colpart, 32, 64);
-    if (last_slot >= 0)
-      buf_st(rdg, ((uint32_t)((L - 1) * H) * K + i) * 4, dg_last + colpart + dgl[chunk * K + i]);
+    if (has_last) buf_st(rdg, ((uint32_t)((L - 1) * H) * K + i) * 4, dg_last + colpart + dgl[chunk * K + i]);
   }
   if (ISO) {  // dbeta[c] = sum_i dkappa k: over the 16 channels of a tile, this wave's tiles, then the waves
 #pragma unroll
