@@ -55,9 +55,15 @@ __device__ __forceinline__ void buf_st(bufrsrc r, uint32_t off, float x) {
 }
 
 // ---- activations ---------------------------------------------------------------
-// softplus with torch's default threshold (x > 20 -> x).
-__device__ __forceinline__ float softplusf(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float sigmoidf(float x) { return 1.f / (1.f + expf(-x)); }
+// softplus with torch's default threshold (x > 20 -> x), on the hardware exp/log
+// (v_exp_f32 / v_log_f32, a few ulp); log1p(y) = y (1 - y/2) below y = 1e-3 keeps small
+// values accurate to ~y^3/3.
+__device__ __forceinline__ float softplusf(float x) {
+  if (x > 20.f) return x;
+  const float y = __expf(x);
+  return y < 1e-3f ? y * (1.f - 0.5f * y) : __logf(1.f + y);
+}
+__device__ __forceinline__ float sigmoidf(float x) { return __frcp_rn(1.f + __expf(-x)); }
 
 // ---- wave64 reductions -----------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

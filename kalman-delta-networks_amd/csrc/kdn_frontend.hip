@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
   __shared__ float s_e2[kMaxChunk][257];
   const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const float rate = expf(A_log[h]);
+  const float rate = __expf(A_log[h]);
   if (i < K) {
     const float bias = dt_bias[h * K + i];
     float acc = 0.f;
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
       const float g = -rate * softplusf(ld(g_raw, off) + bias);
       acc += g;
       g_cumsum[off] = acc * KDN_LOG2E;
-      s_e2[t][i] = expf(2.f * g);
+      s_e2[t][i] = __expf(2.f * g);
     }
   }
   __syncthreads();
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_kernel(
   const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const int p = blockIdx.x;  // partial index (b, nt)
-  const float rate = expf(A_log[h]);
+  const float rate = __expf(A_log[h]);
   float dA_term = 0.f;
   if (i < K) {
     const float bias = dt_bias[h * K + i];
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_kernel(
       const float g = -rate * softplusf(x);
       float dgl = 0.f;
       if (dg_pre) { acc += dg_pre[off]; dgl = acc; }
-      if (da) dgl += da[((int64_t)b * T + t0 + t) * H + h] * (2.f / (float)K) * expf(2.f * g);
+      if (da) dgl += da[((int64_t)b * T + t0 + t) * H + h] * (2.f / (float)K) * __expf(2.f * g);
       const float dgr = dgl * (-rate) * sigmoidf(x);
       if (dg_raw) st(dg_raw, off, dgr);
       dA_term += dgl * g;
@@ -103,6 +103,231 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_kernel(
     part_bias[(int64_t)p * 2 * H + h] = sO;
     part_bias[(int64_t)p * 2 * H + H + h] = sR;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Vectorised iso gate (K % 8 == 0): thread = 8 consecutive channels x TPG tokens of the chunk.
+// tid = tg * CG + cg (CG = K/8 channel groups, TG = 256/CG token groups).  The chunk-local
+// prefix (forward) / suffix (backward) over token groups goes through LDS group totals.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* f);
+template <>
+__device__ __forceinline__ void load8<bf16_t>(const bf16_t* p, float* f) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = __uint_as_float(w[q] << 16);
+    f[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* f) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* f);
+template <>
+__device__ __forceinline__ void store8<bf16_t>(bf16_t* p, const float* f) {
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) w[q] = (uint32_t)f2bf(f[2 * q]) | ((uint32_t)f2bf(f[2 * q + 1]) << 16);
+  *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+}
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float* f) {
+  reinterpret_cast<float4*>(p)[0] = float4{f[0], f[1], f[2], f[3]};
+  reinterpret_cast<float4*>(p)[1] = float4{f[4], f[5], f[6], f[7]};
+}
+
+// grid (B*NT, H), block 256.
+template <typename TG, typename TO>
+__global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
+    const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
+    const float* __restrict__ omega_bias, const float* __restrict__ r_bias, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ mu_param, float omega_min, float r_min,
+    int T, int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ a_out,
+    float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out) {
+  __shared__ float s_tot[256 * 8];  // [tg][K] group totals (TG * K = 2048)
+  const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const float rate = __expf(A_log[h]);
+  float bias[8];
+  load8<float>(dt_bias + h * K + i0, bias);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float pre[4][8];  // local inclusive prefix per token (TPG <= 4 when K >= 64 and chunk <= 64)
+  float e2[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tg * TPG + u;
+    e2[u] = 0.f;
+    if (u < TPG && t < L) {
+      float x[8];
+      load8<TG>(g_raw + (((int64_t)b * T + t0 + t) * H + h) * K + i0, x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float g = -rate * softplusf(x[j] + bias[j]);
+        acc[j] += g;
+        pre[u][j] = acc[j];
+        e2[u] += __expf(2.f * g);
+      }
+    }
+  }
+  if (tg < TGN) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = acc[j];
+  }
+  __syncthreads();
+  float off[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < tg; ++q)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] += s_tot[q * K + i0 + j];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tg * TPG + u;
+    if (u < TPG && t < L) {
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (off[j] + pre[u][j]) * KDN_LOG2E;
+      store8<float>(g_cumsum + (((int64_t)b * T + t0 + t) * H + h) * K + i0, y);
+    }
+    // a = mean over channels of e^{2g}: reduce over the CG consecutive lanes of this token group
+    float s = e2[u];
+    for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
+    if (cg == 0 && u < TPG && t < L) {
+      const int64_t o = ((int64_t)b * T + t0 + t) * H + h;
+      a_out[o] = s / (float)K;
+      const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
+      omega_out[o] = omega_min + softplusf(ld(orr, ro) + omega_bias[h]);
+      r_out[o] = r_min + softplusf(ld(orr, ro + H) + r_bias[h]);
+    }
+  }
+  if (blockIdx.x == 0 && tid == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
+}
+
+// grid (B*NT, H), block 256.  Per-block partials as in iso_gate_bwd_kernel.
+template <typename TG, typename TO>
+__global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
+    const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
+    const float* __restrict__ omega_bias, const float* __restrict__ r_bias, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ dg_pre, const float* __restrict__ da,
+    const float* __restrict__ domega, const float* __restrict__ dr, int T, int H, int K, int chunk, int NT,
+    TG* __restrict__ dg_raw, TO* __restrict__ dorr, float* __restrict__ part_A, float* __restrict__ part_dt,
+    float* __restrict__ part_bias) {
+  __shared__ float s_tot[256 * 8];
+  __shared__ float red[16];
+  const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const int p = blockIdx.x;
+  const float rate = __expf(A_log[h]);
+  float bias[8];
+  load8<float>(dt_bias + h * K + i0, bias);
+  // local suffix sums of dg_pre over this thread's tokens (last token first)
+  float dgp[4][8], acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 3; u >= 0; --u) {
+    const int t = tg * TPG + u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dgp[u][j] = 0.f;
+    if (dg_pre && u < TPG && t < L) {
+      float d[8];
+      load8<float>(dg_pre + (((int64_t)b * T + t0 + t) * H + h) * K + i0, d);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc[j] += d[j];
+        dgp[u][j] = acc[j];
+      }
+    }
+  }
+  if (tg < TGN) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = acc[j];
+  }
+  __syncthreads();
+  float off[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int q = tg + 1; q < TGN; ++q)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) off[j] += s_tot[q * K + i0 + j];
+  __syncthreads();  // s_tot is reused for the per-channel ddt partials below
+  float ddt[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, dA_term = 0.f, dob = 0.f, drb = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tg * TPG + u;
+    if (u < TPG && t < L) {
+      const int64_t row = ((int64_t)b * T + t0 + t) * H + h;
+      float x[8], dgr[8];
+      load8<TG>(g_raw + row * K + i0, x);
+      const float dav = da ? da[row] * (2.f / (float)K) : 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xb = x[j] + bias[j];
+        const float g = -rate * softplusf(xb);
+        float dgl = dg_pre ? off[j] + dgp[u][j] : 0.f;
+        if (da) dgl += dav * __expf(2.f * g);
+        dgr[j] = dgl * (-rate) * sigmoidf(xb);
+        dA_term += dgl * g;
+        ddt[j] += dgr[j];
+      }
+      if (dg_raw) store8<TG>(dg_raw + row * K + i0, dgr);
+      if (cg == 0) {
+        const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
+        const float ob = domega ? domega[row] * sigmoidf(ld(orr, ro) + omega_bias[h]) : 0.f;
+        const float rb = dr ? dr[row] * sigmoidf(ld(orr, ro + H) + r_bias[h]) : 0.f;
+        dob += ob;
+        drb += rb;
+        if (dorr) {
+          const int64_t wo = ((int64_t)b * T + t0 + t) * (2 * H) + h;
+          st(dorr, wo, ob);
+          st(dorr, wo + H, rb);
+        }
+      }
+    }
+  }
+  // per-channel ddt partial: sum over token groups
+  if (tg < TGN) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = ddt[j];
+  }
+  __syncthreads();
+  if (part_dt && tid < K) {
+    float sdt = 0.f;
+    for (int q = 0; q < TGN; ++q) sdt += s_tot[q * K + tid];
+    part_dt[((int64_t)p * H + h) * K + tid] = sdt;
+  }
+  const float sA = block_sum(dA_term, red);
+  if (part_A && tid == 0) part_A[(int64_t)p * H + h] = sA;
+  const float sO = block_sum(dob, red);
+  const float sR = block_sum(drb, red);
+  if (part_bias && tid == 0) {
+    part_bias[(int64_t)p * 2 * H + h] = sO;
+    part_bias[(int64_t)p * 2 * H + H + h] = sR;
+  }
+}
+
+// out[j] = sum_p part[p * stride + j] for j < n, deterministic order: block = 64 outputs x 4
+// partial stripes (each 8-way unrolled over p), stripes combined in order.  grid ceil(n/64).
+__global__ __launch_bounds__(256) void reduce_partials_vec_kernel(const float* __restrict__ part, int NP,
+                                                                  int64_t stride, int n, float* __restrict__ out) {
+  __shared__ float s[4][64];
+  const int jj = threadIdx.x & 63, st4 = threadIdx.x >> 6, j = blockIdx.x * 64 + jj;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (j < n) {
+    int pp = st4;
+    for (; pp + 28 < NP; pp += 32) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += part[(int64_t)(pp + 4 * q) * stride + j];
+    }
+    for (; pp < NP; pp += 4) acc[0] += part[(int64_t)pp * stride + j];
+  }
+  s[st4][jj] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  __syncthreads();
+  if (st4 == 0 && j < n) out[j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
 }
 
 // out[j] = sum_p part[p * stride + j] for j < n, deterministic order.  grid ceil(n/256).
@@ -183,6 +408,56 @@ __global__ __launch_bounds__(256) void l2norm_bwd_kernel(const TX* __restrict__ 
     const int c = lane + 64 * j;
     if (c < K) st(dx, row * K + c, rs * (gv[j] - yv[j] * dot));
   }
+}
+
+// Vectorised row kernels: LPR = K/8 lanes per row, each lane 8 consecutive elements.
+template <typename TX, typename TY>
+__global__ __launch_bounds__(256) void l2norm_fwd_vec_kernel(const TX* __restrict__ x, int64_t rows, int K, float eps,
+                                                             TY* __restrict__ y, float* __restrict__ rstd) {
+  const int LPR = K / 8, RPB = 256 / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  float v[8];
+  float ss = 0.f;
+  if (row < rows) {
+    load8<TX>(x + row * K + 8 * sub, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+  }
+  for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
+  if (row >= rows) return;
+  const float rs = 1.f / sqrtf(ss + eps);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] *= rs;
+  store8<TY>(y + row * K + 8 * sub, v);
+  if (sub == 0) rstd[row] = rs;
+}
+
+template <typename TX, typename TD>
+__global__ __launch_bounds__(256) void l2norm_bwd_vec_kernel(const TX* __restrict__ x, const float* __restrict__ rstd,
+                                                             const TD* __restrict__ dy, int64_t rows, int K,
+                                                             TX* __restrict__ dx) {
+  const int LPR = K / 8, RPB = 256 / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  float yv[8], gv[8];
+  float dot = 0.f, rs = 0.f;
+  if (row < rows) {
+    rs = rstd[row];
+    load8<TX>(x + row * K + 8 * sub, yv);
+    load8<TD>(dy + row * K + 8 * sub, gv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      yv[j] *= rs;
+      dot += yv[j] * gv[j];
+    }
+  }
+  for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
+  if (row >= rows) return;
+  float d[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) d[j] = rs * (gv[j] - yv[j] * dot);
+  store8<TX>(dx + row * K + 8 * sub, d);
 }
 
 // diag normalisation: y = x / max(||x||, 1e-12).  Emits q bf16, k fp32 (gain), k bf16 (memory).
@@ -284,7 +559,7 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_kernel(
     float* __restrict__ omega, float* __restrict__ r, float* __restrict__ mu) {
   const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const float rate = expf(A_log[h]);
+  const float rate = __expf(A_log[h]);
   const float floor_log = logf(1e-6f);
   if (i < K) {
     const float bias = dt_bias[h * K + i];
@@ -317,7 +592,7 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_kernel(
   const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const int p = blockIdx.x;
-  const float rate = expf(A_log[h]);
+  const float rate = __expf(A_log[h]);
   float dA_term = 0.f;
   if (i < K) {
     const float bias = dt_bias[h * K + i];
@@ -355,6 +630,16 @@ inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 }  // namespace
 
+// The vectorised gate kernels need 8-channel groups that tile 256 threads, at most 4 tokens per
+// thread, and 16-byte aligned rows.
+inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool gate_vec_ok(int K, int chunk) {
+  if (K % 8 != 0 || 256 % (K / 8) != 0) return false;
+  return chunk <= 4 * (256 / (K / 8));
+}
+// Row kernels: K/8 lanes per row, 8 elements per lane (K/8 a power of two dividing 64).
+inline bool row_vec_ok(int K) { return K % 8 == 0 && K <= 512 && 64 % (K / 8) == 0; }
+
 // ============================================================================
 // C ABI
 // ============================================================================
@@ -378,8 +663,10 @@ int kdn_iso_gate_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   }
   const int NT = cdiv(T, chunk);
   dim3 grid(B * NT, H);
+  const bool vec = gate_vec_ok(K, chunk) && aligned16(g_raw) && aligned16(g_cumsum) && aligned16(dt_bias);
 #define KDN_GATE_FWD(TG, TO)                                                                                     \
-  hipLaunchKernelGGL((iso_gate_fwd_kernel<TG, TO>), grid, dim3(256), 0, stream, (const TG*)g_raw,               \
+  hipLaunchKernelGGL((vec ? iso_gate_fwd_vec_kernel<TG, TO> : iso_gate_fwd_kernel<TG, TO>), grid, dim3(256), 0,  \
+                     stream, (const TG*)g_raw,                                                                    \
                      (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
                      mu_param, omega_min, r_min, T, H, K, chunk, NT, g_cumsum, a, omega, r, mu)
   if (g_raw_bf16 && orr_bf16) KDN_GATE_FWD(bf16_t, bf16_t);
@@ -406,8 +693,11 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   float* part_dt = part_A + (int64_t)NP * H;
   float* part_bias = part_dt + (int64_t)NP * H * K;
   dim3 grid(NP, H);
+  const bool vec = gate_vec_ok(K, chunk) && aligned16(g_raw) && aligned16(dg_pre) && aligned16(dg_raw) &&
+                   aligned16(dt_bias);
 #define KDN_GATE_BWD(TG, TO)                                                                                     \
-  hipLaunchKernelGGL((iso_gate_bwd_kernel<TG, TO>), grid, dim3(256), 0, stream, (const TG*)g_raw,               \
+  hipLaunchKernelGGL((vec ? iso_gate_bwd_vec_kernel<TG, TO> : iso_gate_bwd_kernel<TG, TO>), grid, dim3(256), 0,  \
+                     stream, (const TG*)g_raw,                                                                    \
                      (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
                      dg_pre, da, domega, dr, T, H, K, chunk, NT, (TG*)dg_raw, (TO*)domega_r_raw,                 \
                      dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr,                                    \
@@ -419,16 +709,16 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
 #undef KDN_GATE_BWD
   KDN_CHECK_LAUNCH();
   if (dA_log)
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H, dA_log);
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H, dA_log);
   if (ddt_bias)
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H * K, 256)), dim3(256), 0, stream, part_dt, NP,
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H * K, 64)), dim3(256), 0, stream, part_dt, NP,
                        (int64_t)H * K, H * K, ddt_bias);
   // part_bias rows are [omega(H) | r(H)]
   if (domega_bias)
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_bias, NP,
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_bias, NP,
                        (int64_t)2 * H, H, domega_bias);
   if (dr_bias)
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_bias + H, NP,
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_bias + H, NP,
                        (int64_t)2 * H, H, dr_bias);
   if (dmu_param) hipLaunchKernelGGL(mu_vjp_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, mu_param, dmu, H, dmu_param);
   KDN_CHECK_LAUNCH();
@@ -439,6 +729,19 @@ int kdn_l2norm_fwd(const void* x, int x_bf16, int64_t rows, int K, float eps, vo
                    hipStream_t stream) {
   if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
   if (rows == 0) return 0;
+  if (row_vec_ok(K) && aligned16(x) && aligned16(y)) {
+    dim3 gv(cdiv(rows, 256 / (K / 8)));
+#define KDN_L2F(TX, TY)                                                                                            \
+  hipLaunchKernelGGL((l2norm_fwd_vec_kernel<TX, TY>), gv, dim3(256), 0, stream, (const TX*)x, rows, K, eps, (TY*)y, \
+                     rstd)
+    if (x_bf16 && y_bf16) KDN_L2F(bf16_t, bf16_t);
+    else if (x_bf16) KDN_L2F(bf16_t, float);
+    else if (y_bf16) KDN_L2F(float, bf16_t);
+    else KDN_L2F(float, float);
+#undef KDN_L2F
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
   dim3 grid(cdiv(rows, 4));
   if (x_bf16 && y_bf16)
     hipLaunchKernelGGL((l2norm_fwd_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)x, rows, K, eps, (bf16_t*)y, rstd);
@@ -456,6 +759,19 @@ int kdn_l2norm_bwd(const void* x, int x_bf16, const float* rstd, const void* dy,
                    void* dx, hipStream_t stream) {
   if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
   if (rows == 0) return 0;
+  if (row_vec_ok(K) && aligned16(x) && aligned16(dy) && aligned16(dx)) {
+    dim3 gv(cdiv(rows, 256 / (K / 8)));
+#define KDN_L2B(TX, TD)                                                                                           \
+  hipLaunchKernelGGL((l2norm_bwd_vec_kernel<TX, TD>), gv, dim3(256), 0, stream, (const TX*)x, rstd, (const TD*)dy, \
+                     rows, K, (TX*)dx)
+    if (x_bf16 && dy_bf16) KDN_L2B(bf16_t, bf16_t);
+    else if (x_bf16) KDN_L2B(bf16_t, float);
+    else if (dy_bf16) KDN_L2B(float, bf16_t);
+    else KDN_L2B(float, float);
+#undef KDN_L2B
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
   dim3 grid(cdiv(rows, 4));
   if (x_bf16 && dy_bf16)
     hipLaunchKernelGGL((l2norm_bwd_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)x, rstd, (const bf16_t*)dy, rows, K, (bf16_t*)dx);
@@ -532,10 +848,10 @@ int kdn_diag_frontend_bwd(const uint16_t* retention_raw, const uint16_t* omega_r
                        ddt_bias ? part_dt : nullptr);
     KDN_CHECK_LAUNCH();
     if (dA_log)
-      hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H,
+      hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H,
                          dA_log);
     if (ddt_bias)
-      hipLaunchKernelGGL(reduce_partials_kernel, dim3(cdiv(H * K, 256)), dim3(256), 0, stream, part_dt, NP,
+      hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H * K, 64)), dim3(256), 0, stream, part_dt, NP,
                          (int64_t)H * K, H * K, ddt_bias);
   } else {
     const int64_t n = (int64_t)B * T * H * K;
