@@ -39,83 +39,129 @@ __device__ __forceinline__ Map2 shfl_up_map(const Map2& m, int d) {
 }
 
 // ----------------------------------------------------------------------------
-// iso gain forward.  grid (H), block 64 * nw; wave w handles b = w, w + nw, ...
+// iso gain, block per head: the block's 256-thread groups take batch rows b = g, g + GB, ...;
+// thread j of a group owns tokens [j S, (j+1) S), S = ceil(T / 256).  Segment maps are
+// combined by a wave shuffle scan and an LDS scan over the group's 4 waves, then replayed.
 // ----------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void iso_gain_fwd_kernel(const float* __restrict__ a, const float* __restrict__ omega,
-                                                            const float* __restrict__ r, const float* __restrict__ mu,
-                                                            int B, int T, int H, float s, int unit_scale,
-                                                            float* __restrict__ beta, float* __restrict__ p_prev,
-                                                            float* __restrict__ final_precision) {
-  const int h = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int L = (T + 63) / 64;
-  const int t0 = min(lane * L, T), t1 = min(t0 + L, T);
-  const float p0 = 1.f / mu[h];
-  for (int b = w; b < B; b += nw) {
-    const int64_t base = (int64_t)b * T * H + h;
-    Map2 M{1.f, 0.f, 0.f, 1.f};
-    for (int t = t0; t < t1; ++t) {
-      const int64_t o = base + (int64_t)t * H;
-      const float at = a[o], wt = omega[o], rt = r[o];
-      M = map_mul(Map2{rt * at, rt * wt, s * at, rt + s * wt}, M);
-    }
-    // inclusive scan over lanes: M_j <- M_j * M_{j-d}
+constexpr int kIsoGroup = 256;
+constexpr int kIsoBatch = 16;  // tokens loaded per batch in the segment loops
+
+__device__ __forceinline__ Map2 map_identity() { return Map2{1.f, 0.f, 0.f, 1.f}; }
+
+// Exclusive scan of segment maps over the 256 threads of group g (later maps applied after).
+__device__ __forceinline__ Map2 group_exclusive_map(Map2 M, Map2* sW, int g, int lane, int w) {
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const Map2 prev = shfl_up_map(M, d);
-      if (lane >= d) M = map_mul(M, prev);
+  for (int d = 1; d < 64; d <<= 1) {
+    const Map2 prev = shfl_up_map(M, d);
+    if (lane >= d) M = map_mul(M, prev);
+  }
+  if (lane == 63) sW[4 * g + w] = M;
+  __syncthreads();
+  Map2 P = map_identity();
+  for (int q = 0; q < w; ++q) P = map_mul(sW[4 * g + q], P);
+  Map2 E = shfl_up_map(M, 1);
+  if (lane == 0) E = map_identity();
+  return map_mul(E, P);
+}
+
+// grid (H), block 256 * GB.
+__global__ __launch_bounds__(1024) void iso_gain_fwd_grp_kernel(const float* __restrict__ a,
+                                                                const float* __restrict__ omega,
+                                                                const float* __restrict__ r,
+                                                                const float* __restrict__ mu, int B, int T, int H,
+                                                                float s, int unit_scale, float* __restrict__ beta,
+                                                                float* __restrict__ p_prev,
+                                                                float* __restrict__ final_precision) {
+  __shared__ Map2 sW[16];
+  const int h = blockIdx.x, GB = blockDim.x / kIsoGroup, g = threadIdx.x / kIsoGroup;
+  const int j = threadIdx.x % kIsoGroup, lane = j & 63, w = j >> 6;
+  const int S = (T + kIsoGroup - 1) / kIsoGroup;
+  const int t0 = min(j * S, T), t1 = min(t0 + S, T);
+  const float p0 = 1.f / mu[h];
+  for (int b0 = 0; b0 < B; b0 += GB) {
+    const int b = b0 + g;
+    const bool act = b < B;
+    const int64_t base = (int64_t)(act ? b : 0) * T * H + h;
+    Map2 M = map_identity();
+    if (act) {
+      for (int tb = t0; tb < t1; tb += kIsoBatch) {
+        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch];
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          const int64_t o = base + (int64_t)min(tb + u, t1 - 1) * H;
+          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o];
+        }
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u)
+          if (tb + u < t1) M = map_mul(Map2{rt[u] * at[u], rt[u] * wt[u], s * at[u], rt[u] + s * wt[u]}, M);
+      }
     }
-    Map2 E = shfl_up_map(M, 1);
-    if (lane == 0) E = Map2{1.f, 0.f, 0.f, 1.f};
+    const Map2 E = group_exclusive_map(M, sW, g, lane, w);
     float p = mobius(E, p0);
-    for (int t = t0; t < t1; ++t) {
-      const int64_t o = base + (int64_t)t * H;
-      const float at = a[o], wt = omega[o], rt = r[o];
-      if (p_prev) p_prev[o] = p;
-      const float z = at * p + wt;
-      const float g = z / (rt + z);
-      beta[o] = g;
-      p = unit_scale ? rt * g : rt * z / (rt + s * z);
+    if (act) {
+      for (int tb = t0; tb < t1; tb += kIsoBatch) {
+        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch];
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          const int64_t o = base + (int64_t)min(tb + u, t1 - 1) * H;
+          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o];
+        }
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          if (tb + u >= t1) break;
+          const int64_t o = base + (int64_t)(tb + u) * H;
+          if (p_prev) p_prev[o] = p;
+          const float z = at[u] * p + wt[u];
+          const float gg = z / (rt[u] + z);
+          beta[o] = gg;
+          p = unit_scale ? rt[u] * gg : rt[u] * z / (rt[u] + s * z);
+        }
+      }
+      if (final_precision && t0 < T && t1 == T) final_precision[(int64_t)b * H + h] = 1.f / p;
     }
-    if (final_precision) {
-      // the last non-empty segment holds p_T
-      const int last = (T - 1) / L;
-      if (lane == last) final_precision[(int64_t)b * H + h] = 1.f / p;
-    }
+    __syncthreads();  // sW is reused by the next batch rows
   }
 }
 
-// ----------------------------------------------------------------------------
-// iso gain backward.  Same launch shape; the dmu reduction over b is in-block.
-// lambda_{t-1} = A_t lambda_t + B_t,  A_t = a r^2/(r+sz)^2,  B_t = a dbeta r/(r+z)^2.
-// ----------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void iso_gain_bwd_kernel(const float* __restrict__ a, const float* __restrict__ omega,
-                                                            const float* __restrict__ r, const float* __restrict__ mu,
-                                                            const float* __restrict__ dbeta,
-                                                            const float* __restrict__ p_prev, int B, int T, int H,
-                                                            float s, int unit_scale, float* __restrict__ da,
-                                                            float* __restrict__ domega, float* __restrict__ dr,
-                                                            float* __restrict__ dmu) {
-  __shared__ float red[16];
-  const int h = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int L = (T + 63) / 64;
-  const int t0 = min(lane * L, T), t1 = min(t0 + L, T);
+// grid (H), block 256 * GB.  lambda_{t-1} = A_t lambda_t + B_t (reverse), lambda_T = 0.
+__global__ __launch_bounds__(1024) void iso_gain_bwd_grp_kernel(
+    const float* __restrict__ a, const float* __restrict__ omega, const float* __restrict__ r,
+    const float* __restrict__ mu, const float* __restrict__ dbeta, const float* __restrict__ p_prev, int B, int T,
+    int H, float s, int unit_scale, float* __restrict__ da, float* __restrict__ domega, float* __restrict__ dr,
+    float* __restrict__ dmu) {
+  __shared__ float sA[16], sB[16], sMu[4];
+  const int h = blockIdx.x, GB = blockDim.x / kIsoGroup, g = threadIdx.x / kIsoGroup;
+  const int j = threadIdx.x % kIsoGroup, lane = j & 63, w = j >> 6;
+  const int S = (T + kIsoGroup - 1) / kIsoGroup;
+  const int t0 = min(j * S, T), t1 = min(t0 + S, T);
   const float muh = mu[h];
   float dmu_acc = 0.f;
-  for (int b = w; b < B; b += nw) {
-    const int64_t base = (int64_t)b * T * H + h;
+  for (int b0 = 0; b0 < B; b0 += GB) {
+    const int b = b0 + g;
+    const bool act = b < B;
+    const int64_t base = (int64_t)(act ? b : 0) * T * H + h;
     float Aseg = 1.f, Bseg = 0.f;
-    for (int t = t1 - 1; t >= t0; --t) {
-      const int64_t o = base + (int64_t)t * H;
-      const float at = a[o], wt = omega[o], rt = r[o], dl = dbeta[o], pp = p_prev[o];
-      const float z = at * pp + wt;
-      const float ig = 1.f / (rt + z);
-      const float ip = 1.f / (rt + s * z);
-      const float At = at * rt * rt * ip * ip;
-      const float Bt = at * dl * rt * ig * ig;
-      Bseg = At * Bseg + Bt;
-      Aseg = At * Aseg;
+    if (act) {
+      for (int te = t1; te > t0; te -= kIsoBatch) {  // tokens te-1 down to te-kIsoBatch
+        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch], dl[kIsoBatch], pp[kIsoBatch];
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          const int64_t o = base + (int64_t)max(te - 1 - u, t0) * H;
+          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o], dl[u] = dbeta[o], pp[u] = p_prev[o];
+        }
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          if (te - 1 - u < t0) break;
+          const float z = at[u] * pp[u] + wt[u];
+          const float ig = 1.f / (rt[u] + z), ip = 1.f / (rt[u] + s * z);
+          const float At = at[u] * rt[u] * rt[u] * ip * ip;
+          const float Bt = at[u] * dl[u] * rt[u] * ig * ig;
+          Bseg = At * Bseg + Bt;
+          Aseg = At * Aseg;
+        }
+      }
     }
-    // inclusive suffix scan: S_j <- S_j o S_{j+d}
+    // exclusive suffix scan over the group: lambda after this thread's segment
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const float An = __shfl_down(Aseg, d, 64), Bn = __shfl_down(Bseg, d, 64);
@@ -124,36 +170,59 @@ __global__ __launch_bounds__(1024) void iso_gain_bwd_kernel(const float* __restr
         Aseg = Aseg * An;
       }
     }
-    float Ae = __shfl_down(Aseg, 1, 64), Be = __shfl_down(Bseg, 1, 64);
-    if (lane == 63) { Ae = 1.f; Be = 0.f; }
-    float lam = Be;  // lambda after this lane's segment (lambda_end = 0)
-    (void)Ae;
-    for (int t = t1 - 1; t >= t0; --t) {
-      const int64_t o = base + (int64_t)t * H;
-      const float at = a[o], wt = omega[o], rt = r[o], dl = dbeta[o], pp = p_prev[o];
-      const float z = at * pp + wt;
-      const float ig = 1.f / (rt + z);
-      const float ig2 = ig * ig;
-      float zbar, drt;
-      if (unit_scale) {
-        zbar = (dl + rt * lam) * rt * ig2;
-        drt = z * (lam * z - dl) * ig2;
-      } else {
-        const float ip = 1.f / (rt + s * z);
-        const float ip2 = ip * ip;
-        zbar = dl * rt * ig2 + lam * rt * rt * ip2;
-        drt = -dl * z * ig2 + lam * s * z * z * ip2;
-      }
-      da[o] = zbar * pp;
-      domega[o] = zbar;
-      dr[o] = drt;
-      lam = at * zbar;
+    if (lane == 0) {
+      sA[4 * g + w] = Aseg;
+      sB[4 * g + w] = Bseg;
     }
-    if (lane == 0) dmu_acc += -lam / (muh * muh);
+    __syncthreads();
+    float lam = 0.f;  // lambda entering the later waves' segments, applied from the last wave back
+    for (int q = 3; q > w; --q) lam = sA[4 * g + q] * lam + sB[4 * g + q];
+    {
+      const float An = __shfl_down(Aseg, 1, 64), Bn = __shfl_down(Bseg, 1, 64);
+      if (lane < 63) lam = An * lam + Bn;
+    }
+    if (act) {
+      for (int te = t1; te > t0; te -= kIsoBatch) {
+        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch], dl[kIsoBatch], pp[kIsoBatch];
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          const int64_t o = base + (int64_t)max(te - 1 - u, t0) * H;
+          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o], dl[u] = dbeta[o], pp[u] = p_prev[o];
+        }
+#pragma unroll
+        for (int u = 0; u < kIsoBatch; ++u) {
+          if (te - 1 - u < t0) break;
+          const int64_t o = base + (int64_t)(te - 1 - u) * H;
+          const float z = at[u] * pp[u] + wt[u];
+          const float ig = 1.f / (rt[u] + z);
+          const float ig2 = ig * ig;
+          float zbar, drt;
+          if (unit_scale) {
+            zbar = (dl[u] + rt[u] * lam) * rt[u] * ig2;
+            drt = z * (lam * z - dl[u]) * ig2;
+          } else {
+            const float ip = 1.f / (rt[u] + s * z);
+            const float ip2 = ip * ip;
+            zbar = dl[u] * rt[u] * ig2 + lam * rt[u] * rt[u] * ip2;
+            drt = -dl[u] * z * ig2 + lam * s * z * z * ip2;
+          }
+          da[o] = zbar * pp[u];
+          domega[o] = zbar;
+          dr[o] = drt;
+          lam = at[u] * zbar;
+        }
+      }
+      if (j == 0) dmu_acc += -lam / (muh * muh);
+    }
+    __syncthreads();  // sA / sB are reused by the next batch rows
   }
-  // deterministic reduction of the per-wave contributions (held by lane 0 of each wave)
-  const float tot = block_sum(lane == 0 ? dmu_acc : 0.f, red);
-  if (threadIdx.x == 0 && dmu) dmu[h] = tot;
+  if (j == 0) sMu[g] = dmu_acc;
+  __syncthreads();
+  if (threadIdx.x == 0 && dmu) {
+    float tot = 0.f;
+    for (int q = 0; q < GB; ++q) tot += sMu[q];
+    dmu[h] = tot;
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -391,9 +460,10 @@ int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const f
                      hipStream_t stream) {
   if (B < 0 || T < 0 || H <= 0 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
-  const int nw = B < 16 ? B : 16;
-  hipLaunchKernelGGL(iso_gain_fwd_kernel, dim3(H), dim3(64 * nw), 0, stream, a, omega, r, initial_precision, B, T, H,
-                     posterior_scale, posterior_scale == 1.f ? 1 : 0, beta, p_prev, final_precision);
+  const int GB = B < 4 ? B : 4;
+  hipLaunchKernelGGL(iso_gain_fwd_grp_kernel, dim3(H), dim3(kIsoGroup * GB), 0, stream, a, omega, r,
+                     initial_precision, B, T, H, posterior_scale, posterior_scale == 1.f ? 1 : 0, beta, p_prev,
+                     final_precision);
   KDN_CHECK_LAUNCH();
   return 0;
 }
@@ -403,10 +473,10 @@ int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const f
                      float* domega, float* dr, float* d_initial_precision, hipStream_t stream) {
   if (B < 0 || T < 0 || H <= 0 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
-  const int nw = B < 16 ? B : 16;
-  hipLaunchKernelGGL(iso_gain_bwd_kernel, dim3(H), dim3(64 * nw), 0, stream, a, omega, r, initial_precision, dbeta,
-                     p_prev, B, T, H, posterior_scale, posterior_scale == 1.f ? 1 : 0, da, domega, dr,
-                     d_initial_precision);
+  const int GB = B < 4 ? B : 4;
+  hipLaunchKernelGGL(iso_gain_bwd_grp_kernel, dim3(H), dim3(kIsoGroup * GB), 0, stream, a, omega, r,
+                     initial_precision, dbeta, p_prev, B, T, H, posterior_scale, posterior_scale == 1.f ? 1 : 0, da,
+                     domega, dr, d_initial_precision);
   KDN_CHECK_LAUNCH();
   return 0;
 }
