@@ -35,9 +35,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
 
 # MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
 # MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
-MFMA_PATH = {"mem_intra_fwd": "f32", "mem_state_fwd": "bf16x3", "mem_output_fwd": "f32",
-             "mem_state_bwd": "bf16x3", "mem_bwd_hgrad": "f32", "mem_bwd_solve": "f32",
-             "mem_bwd_contrib": "f32"}
+MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_fwd": "bf16x3",
+             "mem_state_bwd": "bf16x3", "mem_bwd_hgrad": "bf16x3", "mem_bwd_solve": "bf16x3",
+             "mem_bwd_contrib": "bf16x3"}
 
 
 def mfma_peak(tag: str) -> float:
@@ -54,21 +54,19 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
     h_b = 4 * K * V / C                                   # one fp32 state per chunk
     mm = C * C / C * 4                                    # one fp32 C x C matrix per chunk
     per = {
-        # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M
-        "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + mm,
+        # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M, A^T (the inverse, saved)
+        "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + 2 * mm,
                           2 * (C * K + C * (V + K) / 2)),
-        # U, W, Kf, g_last -> h, delta
-        "mem_state_fwd": (4 * V + 8 * K + h_b + 4 * V, 2 * 2 * K * V),
-        # Qg, h, M, delta -> o
-        "mem_output_fwd": (4 * K + h_b + mm + 4 * V + (2 if variant == "iso" else 4) * V,
-                           2 * (K * V + C * V / 2)),
+        # U, W, Kf, Qg, M, g_last -> h, delta, o  (readout fused into the state pass)
+        "mem_state_fwd": (4 * V + 8 * K + h_b + 4 * V + 4 * K + mm + (2 if variant == "iso" else 4) * V,
+                          2 * 2 * K * V + 2 * (K * V + C * V / 2)),
         # M, Kf, Qg, W, dO -> dh, d delta
         "mem_state_bwd": (mm + 12 * K + do_b + h_b + 4 * V, 2 * (C * V / 2 + 3 * K * V)),
         # h, dh, delta, d delta, dO -> dQg, dW, dKf, dM
         "mem_bwd_hgrad": (2 * h_b + 8 * V + do_b + 12 * K + mm, 2 * (3 * K * V + C * V / 2)),
-        # k, kappa, g, d delta, dW, U, W -> dv, dKg, dN
-        "mem_bwd_solve": (2 * K + kap_in + 4 * K + 4 * V + 4 * K + 4 * V + 4 * K + 2 * V + 4 * K + mm,
-                          2 * (C * K / 2 + C * (V + K) / 2 + C * (V + K) / 2)),
+        # A^T, d delta, dW, U, W -> dv, dKg, dN
+        "mem_bwd_solve": (mm + 4 * V + 4 * K + 4 * V + 4 * K + 2 * V + 4 * K + mm,
+                          2 * (C * (V + K) / 2 + C * (V + K) / 2)),
         # q, k, kappa, g, dN, dM, dQg, dKg, dKf -> dq, dk, dkappa, dg
         "mem_bwd_contrib": (4 * K + kap_in + 4 * K + 2 * mm + 12 * K + 4 * K + dkap_out + 4 * K,
                             2 * 2 * (C * K)),

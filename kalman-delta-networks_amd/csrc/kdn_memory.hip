@@ -14,8 +14,8 @@
 //
 // Kernels (grid = one workgroup per chunk unless noted, 256 threads = 4 waves):
 //   intra_fwd    N/M (MFMA, anchored), forward substitution for U, W; Kf, Qg
-//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h) (kdn_state.h)
-//   output_fwd   O = Qg h + M delta
+//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h), with the readout
+//                O = Qg h + M delta fused in (kdn_state.h)
 //   state_bwd    serial reverse (kdn_state.h): d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
 //   bwd_hgrad    dQg = dO h^T, dW = -d delta h^T, dKf = delta dh^T, dM = dO delta^T, g_last terms
 //   bwd_solve    dV = (I+N)^-T d delta, dKg = (I+N)^-T dW, dN = -(dV U^T + dKg W^T)
@@ -322,45 +322,6 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
     if (flags[lin] == 0) continue;
     __syncthreads();  // LDS of the previous chunk is dead
     intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, lin % NT, lin / NT);
-  }
-}
-
-// ===========================================================================
-// Forward readout: O = Qg h + M delta.  grid (NT, B*H).
-// ===========================================================================
-template <int K, int V, typename TO>
-__global__ __launch_bounds__(256) void mem_output_fwd_kernel(const float* __restrict__ Qg, const float* __restrict__ hbuf,
-                                                             const float* __restrict__ Mg, const float* __restrict__ Dl,
-                                                             int T, int H, int NT, TO* __restrict__ o) {
-  constexpr int KP = K + 4, VP = V + 4;
-  __shared__ __attribute__((aligned(16))) float sQg[C * KP], sH[K * VP], sM[C * NS], sD[C * VP];
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  stage_f32<C, K, KP>(Qg + bht(bh, t0, T, K), K, L, sQg);
-  stage_f32<K, V, VP>(hbuf + ((int64_t)bh * NT + n) * K * V, V, K, sH);
-  stage_f32<C, C, NS>(Mg + ((int64_t)bh * NT + n) * C * C, C, C, sM);
-  stage_f32<C, V, VP>(Dl + bht(bh, t0, T, V), V, L, sD);
-  __syncthreads();
-  constexpr int NTL = (C / 16) * (V / 16);
-  for (int tile = w; tile < NTL; tile += 4) {
-    const int cb = tile / (V / 16), vb = tile % (V / 16);
-    f32x4 acc = zero4();
-    const int cA = 16 * cb + (lane & 15), vB = 16 * vb + (lane & 15);
-#pragma unroll 8
-    for (int st = 0; st < K / 4; ++st) {
-      const int i = 4 * st + (lane >> 4);
-      acc = mfma4(sQg[cA * KP + i], sH[i * VP + vB], acc);
-    }
-    for (int st = 0; st < 4 * (cb + 1); ++st) {
-      const int s = 4 * st + (lane >> 4);
-      acc = mfma4(sM[cA * NS + s], sD[s * VP + vB], acc);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = 16 * cb + 4 * (lane >> 4) + j;
-      if (c < L) st(o, bthk(b, t0 + c, h, vB, T, H, V), acc[j]);
-    }
   }
 }
 
@@ -819,18 +780,14 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     }
     KDN_CHECK_LAUNCH();
   }
-  if (stages & 2) {
-    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), dim3(B * H * (V / kdn_state::WG_COLS)), dim3(256), 0, stream, U,
-                       W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht);
-    KDN_CHECK_LAUNCH();
-  }
-  if (stages & 4) {
+  if (stages & 2) {  // state pass with the fused readout
+    const dim3 gs(B * H * (V / kdn_state::WG_COLS));
     if (o_bf16)
-      hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, bf16_t>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
-                         (bf16_t*)o);
+      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t>), gs, dim3(256), 0, stream, U, W, Kf, Qg, M, gc,
+                         h0, T, H, NT, B * H, hb, D, ht, (bf16_t*)o);
     else
-      hipLaunchKernelGGL((mem_output_fwd_kernel<K, V, float>), gchunk, dim3(256), 0, stream, Qg, hb, M, D, T, H, NT,
-                         (float*)o);
+      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float>), gs, dim3(256), 0, stream, U, W, Kf, Qg, M, gc,
+                         h0, T, H, NT, B * H, hb, D, ht, (float*)o);
     KDN_CHECK_LAUNCH();
   }
   return 0;

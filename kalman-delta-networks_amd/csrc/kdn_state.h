@@ -1,6 +1,7 @@
 // Serial chunk-state passes of the KDN memory scan (forward and reverse).
 //
-//   forward  (per chunk n):  h_n = S;  delta = U - W S;  S = e^{g_last} S + Kf^T delta
+//   forward  (per chunk n):  h_n = S;  delta = U - W S;  O = Qg S + M delta;
+//                            S = e^{g_last} S + Kf^T delta
 //   backward (reverse):      dh_n = dS;  d delta = M^T dO + Kf dS;
 //                            dS <- e^{g_last} dS + Qg^T dO - W^T d delta
 //
@@ -115,20 +116,24 @@ __device__ __forceinline__ int64_t row_bthk(int b, int t, int h, int T, int H, i
 }
 
 // ===========================================================================
-// Forward state pass.  grid (B*H*V/64), block 256.  LDS 64.5 KB.
+// Forward state pass with the fused readout.  grid (B*H*V/64), block 256.  LDS 96.5 KB.
 // ===========================================================================
-template <int K, int V>
+template <int K, int V, typename TO>
 __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
-                                                        const float* __restrict__ Kf, const float* __restrict__ gc,
+                                                        const float* __restrict__ Kf, const float* __restrict__ Qg,
+                                                        const float* __restrict__ Mg, const float* __restrict__ gc,
                                                         const float* __restrict__ h0, int T, int H, int NT, int BH,
                                                         float* __restrict__ hbuf, float* __restrict__ Dl,
-                                                        float* __restrict__ ht) {
+                                                        float* __restrict__ ht, TO* __restrict__ out) {
   constexpr int NV = V / WG_COLS;
   constexpr int KB = K / 32;           // k-blocks of a contraction over K
   constexpr int ST = K / 16;           // state row tiles per wave
   constexpr int UN = C * K / 4 / 256;  // staging units per thread of a C x K operand
+  constexpr int UM = C * C / 4 / 256;  // ... of M
   __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[(C / 16) * KB * TILE];        // Qg: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
+  __shared__ __attribute__((aligned(16))) bf16_t sM[(C / 16) * (C / 32) * TILE];  // M: rows c, k = s
   __shared__ __attribute__((aligned(16))) float sE[K];
   int bh, vs;
   xcd_map(blockIdx.x, NV, BH, bh, vs);
@@ -136,15 +141,17 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
   const int col = vs * WG_COLS + 16 * w + (lane & 15);  // this lane's state column
 
-  float4 rW[UN];
-  float rK[UN][4], rU[4][4], rE = 0.f;
-  auto load_W = [&](int n) {
+  float4 rW[UN], rQ[UN];
+  float rK[UN][4], rM[UM][4], rU[4][4], rE = 0.f;
+  auto load_W = [&](int n) {  // W and Qg (rows c, k = i)
     const int t0 = n * C, L = min(C, T - t0);
     const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);  // rows past L read 0
+    const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const Unit x = unit<K>(tid + 256 * u);
       rW[u] = buf_ld4(rw, (x.row * K + x.k0) * 4);
+      rQ[u] = buf_ld4(rq, (x.row * K + x.k0) * 4);
     }
   };
   auto load_K = [&](int n) {  // Kf^T (rows i, k = c), U rows of this lane, e^{g_last}
@@ -162,14 +169,27 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
 #pragma unroll
       for (int j = 0; j < 4; ++j) rU[cb][j] = buf_ld(ru, ((16 * cb + 4 * g4 + j) * V + col) * 4);
     if (tid < K) rE = exp2f(gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid]);
+    const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][s] row-major
+#pragma unroll
+    for (int u = 0; u < UM; ++u) {
+      const Unit x = unit<C>(tid + 256 * u);
+      const float4 m = buf_ld4(rm, (x.row * C + x.k0) * 4);
+      rM[u][0] = m.x, rM[u][1] = m.y, rM[u][2] = m.z, rM[u][3] = m.w;
+    }
   };
   auto stage_W = [&]() {
 #pragma unroll
-    for (int u = 0; u < UN; ++u) put_unit(sW, unit<K>(tid + 256 * u).off, rW[u].x, rW[u].y, rW[u].z, rW[u].w);
+    for (int u = 0; u < UN; ++u) {
+      const int off = unit<K>(tid + 256 * u).off;
+      put_unit(sW, off, rW[u].x, rW[u].y, rW[u].z, rW[u].w);
+      put_unit(sQ, off, rQ[u].x, rQ[u].y, rQ[u].z, rQ[u].w);
+    }
   };
   auto stage_K = [&]() {
 #pragma unroll
     for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + 256 * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
+#pragma unroll
+    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + 256 * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
     if (tid < K) sE[tid] = rE;
   };
 
@@ -201,13 +221,13 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
 #pragma unroll
       for (int j = 0; j < 4; ++j) cU[cb][j] = rU[cb][j];
     if (n + 1 < NT) load_W(n + 1);
-    f32x4 D[4];
+    f32x4 D[4], O[4];
     {
       uint4 bh_[KB], bl_[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) bfrag(S[2 * kb], S[2 * kb + 1], bh_[kb], bl_[kb]);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) D[cb] = zero4();
+      for (int cb = 0; cb < 4; ++cb) D[cb] = O[cb] = zero4();
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -215,6 +235,8 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
           uint4 ah, al;
           afrag(sW, cb * KB + kb, lane, ah, al);
           D[cb] = mma3(ah, al, bh_[kb], bl_[kb], D[cb]);
+          afrag(sQ, cb * KB + kb, lane, ah, al);
+          O[cb] = mma3(ah, al, bh_[kb], bl_[kb], O[cb]);
         }
       const bufrsrc rd = make_buf(Dl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
 #pragma unroll
@@ -249,6 +271,27 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
           uint4 ah, al;
           afrag(sK, ib * 2 + kb, lane, ah, al);
           S[ib] = mma3(ah, al, dh_[kb], dl_[kb], S[ib]);
+        }
+      // readout O = Qg h + M delta  (M[c][s] = 0 for s > c)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          if (kb == 1 && cb < 2) continue;
+          uint4 ah, al;
+          afrag(sM, cb * 2 + kb, lane, ah, al);
+          O[cb] = mma3(ah, al, dh_[kb], dl_[kb], O[cb]);
+        }
+      const bufrsrc ro = make_buf(out + row_bthk(b, t0, h, T, H, V), ((L - 1) * H + 1) * V * sizeof(TO));
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t e = (uint32_t)((16 * cb + 4 * g4 + j) * H) * V + col;
+          if constexpr (sizeof(TO) == 2)
+            __builtin_amdgcn_raw_buffer_store_b16(f2bf(O[cb][j]), ro, e * 2, 0, 0);
+          else
+            buf_st(ro, e * 4, O[cb][j]);
         }
     }
     __syncthreads();
