@@ -49,16 +49,19 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
                      float* dr_bias, float* dmu_param, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- iso gain */
+/* Workspace of kdn_iso_gain_fwd / kdn_iso_gain_bwd (per-chunk maps and carries). */
+size_t kdn_iso_gain_workspace_size(int B, int T, int H);
 /* _iso_kdn_gain_forward (iso_kdn_chunk.py:1598-1664): beta [B,T,H]; p_prev (nullable) saves
- * the incoming covariance per token for the backward; final_precision [B,H] (nullable). */
+ * the incoming covariance per token for the backward; final_precision [B,H] (nullable).  H <= 96. */
 int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision, int B, int T,
                      int H, float posterior_scale, float* beta, float* p_prev, float* final_precision,
-                     hipStream_t stream);
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* _iso_kdn_gain_backward (iso_kdn_chunk.py:1817-1893); d_initial_precision [H] is summed over B
  * in a fixed order (deterministic). */
 int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const float* initial_precision,
                      const float* dbeta, const float* p_prev, int B, int T, int H, float posterior_scale, float* da,
-                     float* domega, float* dr, float* d_initial_precision, hipStream_t stream);
+                     float* domega, float* dr, float* d_initial_precision, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
 
 /* ---------------------------------------------------------------- row norms */
 /* FLA l2norm_fwd / l2norm_bwd used inside _ChunkKDAPrecumsumFunction (iso_kdn_chunk.py:2203-2204,

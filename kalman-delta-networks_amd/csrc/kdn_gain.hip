@@ -39,190 +39,273 @@ __device__ __forceinline__ Map2 shfl_up_map(const Map2& m, int d) {
 }
 
 // ----------------------------------------------------------------------------
-// iso gain, block per head: the block's 256-thread groups take batch rows b = g, g + GB, ...;
-// thread j of a group owns tokens [j S, (j+1) S), S = ceil(T / 256).  Segment maps are
-// combined by a wave shuffle scan and an LDS scan over the group's 4 waves, then replayed.
+// iso gain: chunked map / carry / emit over 64-token chunks.  a, omega, r, beta, p_prev are
+// [B,T,H] (heads interleaved), so the map and emit kernels stage a chunk's contiguous
+// [64][H] tile in LDS; four threads per head compose or replay 16 tokens each.  The carry
+// kernel scans one (b, h) stream's chunk maps with a wave (64 chunks per step).
+//   forward map of a token:  p -> (r a p + r w) / (s a p + r + s w)       (p' = r z / (r + s z))
+//   backward (reverse):      lambda_{t-1} = A_t lambda_t + B_t,
+//                            A_t = a r^2 / (r + s z)^2,  B_t = a dbeta r / (r + z)^2
+// Workspace: maps [B*H][NC] x 4 floats, then per-chunk carries [B*H][NC].
 // ----------------------------------------------------------------------------
-constexpr int kIsoGroup = 256;
-constexpr int kIsoBatch = 16;  // tokens loaded per batch in the segment loops
+constexpr int kIsoChunk = 64;
+constexpr int kIsoSub = 4;  // threads per head in a chunk (16 tokens each)
 
 __device__ __forceinline__ Map2 map_identity() { return Map2{1.f, 0.f, 0.f, 1.f}; }
+__device__ __forceinline__ Map2 token_map(float at, float wt, float rt, float s) {
+  return Map2{rt * at, rt * wt, s * at, rt + s * wt};
+}
 
-// Exclusive scan of segment maps over the 256 threads of group g (later maps applied after).
-__device__ __forceinline__ Map2 group_exclusive_map(Map2 M, Map2* sW, int g, int lane, int w) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const Map2 prev = shfl_up_map(M, d);
-    if (lane >= d) M = map_mul(M, prev);
-  }
-  if (lane == 63) sW[4 * g + w] = M;
+// Stage rows [t0, t0 + L) of a [B,T,H] array into LDS tile[t][h] (coalesced).
+__device__ __forceinline__ void stage_bth(const float* __restrict__ x, int b, int T, int H, int t0, int L,
+                                          float* tile) {
+  const int64_t base = ((int64_t)b * T + t0) * H;
+  for (int e = threadIdx.x; e < L * H; e += blockDim.x) tile[e] = x[base + e];
+}
+__device__ __forceinline__ void store_bth(float* __restrict__ x, int b, int T, int H, int t0, int L,
+                                          const float* tile) {
+  const int64_t base = ((int64_t)b * T + t0) * H;
+  for (int e = threadIdx.x; e < L * H; e += blockDim.x) x[base + e] = tile[e];
+}
+
+// grid (NC, B), block 256, dynamic LDS 3 * 64 * H floats + 4 * H maps.
+__global__ __launch_bounds__(256) void iso_gain_map_kernel(const float* __restrict__ a, const float* __restrict__ omega,
+                                                           const float* __restrict__ r, int T, int H, int NC, float s,
+                                                           float4* __restrict__ maps) {
+  extern __shared__ float sm[];
+  float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H;
+  Map2* sub = reinterpret_cast<Map2*>(sm + 3 * kIsoChunk * H);
+  const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
+  stage_bth(a, b, T, H, t0, L, sa);
+  stage_bth(omega, b, T, H, t0, L, sw);
+  stage_bth(r, b, T, H, t0, L, sr);
   __syncthreads();
-  Map2 P = map_identity();
-  for (int q = 0; q < w; ++q) P = map_mul(sW[4 * g + q], P);
-  Map2 E = shfl_up_map(M, 1);
-  if (lane == 0) E = map_identity();
-  return map_mul(E, P);
-}
-
-// grid (H), block 256 * GB.
-__global__ __launch_bounds__(1024) void iso_gain_fwd_grp_kernel(const float* __restrict__ a,
-                                                                const float* __restrict__ omega,
-                                                                const float* __restrict__ r,
-                                                                const float* __restrict__ mu, int B, int T, int H,
-                                                                float s, int unit_scale, float* __restrict__ beta,
-                                                                float* __restrict__ p_prev,
-                                                                float* __restrict__ final_precision) {
-  __shared__ Map2 sW[16];
-  const int h = blockIdx.x, GB = blockDim.x / kIsoGroup, g = threadIdx.x / kIsoGroup;
-  const int j = threadIdx.x % kIsoGroup, lane = j & 63, w = j >> 6;
-  const int S = (T + kIsoGroup - 1) / kIsoGroup;
-  const int t0 = min(j * S, T), t1 = min(t0 + S, T);
-  const float p0 = 1.f / mu[h];
-  for (int b0 = 0; b0 < B; b0 += GB) {
-    const int b = b0 + g;
-    const bool act = b < B;
-    const int64_t base = (int64_t)(act ? b : 0) * T * H + h;
+  constexpr int SL = kIsoChunk / kIsoSub;
+  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
+    const int h = hq / kIsoSub, q = hq % kIsoSub;
     Map2 M = map_identity();
-    if (act) {
-      for (int tb = t0; tb < t1; tb += kIsoBatch) {
-        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch];
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          const int64_t o = base + (int64_t)min(tb + u, t1 - 1) * H;
-          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o];
-        }
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u)
-          if (tb + u < t1) M = map_mul(Map2{rt[u] * at[u], rt[u] * wt[u], s * at[u], rt[u] + s * wt[u]}, M);
-      }
-    }
-    const Map2 E = group_exclusive_map(M, sW, g, lane, w);
-    float p = mobius(E, p0);
-    if (act) {
-      for (int tb = t0; tb < t1; tb += kIsoBatch) {
-        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch];
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          const int64_t o = base + (int64_t)min(tb + u, t1 - 1) * H;
-          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o];
-        }
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          if (tb + u >= t1) break;
-          const int64_t o = base + (int64_t)(tb + u) * H;
-          if (p_prev) p_prev[o] = p;
-          const float z = at[u] * p + wt[u];
-          const float gg = z / (rt[u] + z);
-          beta[o] = gg;
-          p = unit_scale ? rt[u] * gg : rt[u] * z / (rt[u] + s * z);
-        }
-      }
-      if (final_precision && t0 < T && t1 == T) final_precision[(int64_t)b * H + h] = 1.f / p;
-    }
-    __syncthreads();  // sW is reused by the next batch rows
+    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
+    sub[hq] = M;
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    Map2 M = sub[kIsoSub * h];
+    for (int q = 1; q < kIsoSub; ++q) M = map_mul(sub[kIsoSub * h + q], M);
+    maps[((int64_t)b * H + h) * NC + n] = float4{M.m0, M.m1, M.m2, M.m3};
   }
 }
 
-// grid (H), block 256 * GB.  lambda_{t-1} = A_t lambda_t + B_t (reverse), lambda_T = 0.
-__global__ __launch_bounds__(1024) void iso_gain_bwd_grp_kernel(
-    const float* __restrict__ a, const float* __restrict__ omega, const float* __restrict__ r,
-    const float* __restrict__ mu, const float* __restrict__ dbeta, const float* __restrict__ p_prev, int B, int T,
-    int H, float s, int unit_scale, float* __restrict__ da, float* __restrict__ domega, float* __restrict__ dr,
-    float* __restrict__ dmu) {
-  __shared__ float sA[16], sB[16], sMu[4];
-  const int h = blockIdx.x, GB = blockDim.x / kIsoGroup, g = threadIdx.x / kIsoGroup;
-  const int j = threadIdx.x % kIsoGroup, lane = j & 63, w = j >> 6;
-  const int S = (T + kIsoGroup - 1) / kIsoGroup;
-  const int t0 = min(j * S, T), t1 = min(t0 + S, T);
-  const float muh = mu[h];
-  float dmu_acc = 0.f;
-  for (int b0 = 0; b0 < B; b0 += GB) {
-    const int b = b0 + g;
-    const bool act = b < B;
-    const int64_t base = (int64_t)(act ? b : 0) * T * H + h;
-    float Aseg = 1.f, Bseg = 0.f;
-    if (act) {
-      for (int te = t1; te > t0; te -= kIsoBatch) {  // tokens te-1 down to te-kIsoBatch
-        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch], dl[kIsoBatch], pp[kIsoBatch];
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          const int64_t o = base + (int64_t)max(te - 1 - u, t0) * H;
-          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o], dl[u] = dbeta[o], pp[u] = p_prev[o];
-        }
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          if (te - 1 - u < t0) break;
-          const float z = at[u] * pp[u] + wt[u];
-          const float ig = 1.f / (rt[u] + z), ip = 1.f / (rt[u] + s * z);
-          const float At = at[u] * rt[u] * rt[u] * ip * ip;
-          const float Bt = at[u] * dl[u] * rt[u] * ig * ig;
-          Bseg = At * Bseg + Bt;
-          Aseg = At * Aseg;
-        }
-      }
+// grid (B*H), block 64: p at each chunk start (carry) and the final precision.
+__global__ __launch_bounds__(64) void iso_gain_carry_kernel(const float4* __restrict__ maps,
+                                                            const float* __restrict__ mu, int H, int NC,
+                                                            float* __restrict__ carry,
+                                                            float* __restrict__ final_precision) {
+  const int bh = blockIdx.x, h = bh % H, lane = threadIdx.x;
+  float p = 1.f / mu[h];
+  for (int c0 = 0; c0 < NC; c0 += 64) {
+    const int c = c0 + lane;
+    Map2 M = map_identity();
+    if (c < NC) {
+      const float4 m = maps[(int64_t)bh * NC + c];
+      M = Map2{m.x, m.y, m.z, m.w};
     }
-    // exclusive suffix scan over the group: lambda after this thread's segment
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-      const float An = __shfl_down(Aseg, d, 64), Bn = __shfl_down(Bseg, d, 64);
-      if (lane + d < 64) {
-        Bseg = Aseg * Bn + Bseg;
-        Aseg = Aseg * An;
-      }
+      const Map2 prev = shfl_up_map(M, d);
+      if (lane >= d) M = map_mul(M, prev);
     }
-    if (lane == 0) {
-      sA[4 * g + w] = Aseg;
-      sB[4 * g + w] = Bseg;
-    }
-    __syncthreads();
-    float lam = 0.f;  // lambda entering the later waves' segments, applied from the last wave back
-    for (int q = 3; q > w; --q) lam = sA[4 * g + q] * lam + sB[4 * g + q];
-    {
-      const float An = __shfl_down(Aseg, 1, 64), Bn = __shfl_down(Bseg, 1, 64);
-      if (lane < 63) lam = An * lam + Bn;
-    }
-    if (act) {
-      for (int te = t1; te > t0; te -= kIsoBatch) {
-        float at[kIsoBatch], wt[kIsoBatch], rt[kIsoBatch], dl[kIsoBatch], pp[kIsoBatch];
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          const int64_t o = base + (int64_t)max(te - 1 - u, t0) * H;
-          at[u] = a[o], wt[u] = omega[o], rt[u] = r[o], dl[u] = dbeta[o], pp[u] = p_prev[o];
-        }
-#pragma unroll
-        for (int u = 0; u < kIsoBatch; ++u) {
-          if (te - 1 - u < t0) break;
-          const int64_t o = base + (int64_t)(te - 1 - u) * H;
-          const float z = at[u] * pp[u] + wt[u];
-          const float ig = 1.f / (rt[u] + z);
-          const float ig2 = ig * ig;
-          float zbar, drt;
-          if (unit_scale) {
-            zbar = (dl[u] + rt[u] * lam) * rt[u] * ig2;
-            drt = z * (lam * z - dl[u]) * ig2;
-          } else {
-            const float ip = 1.f / (rt[u] + s * z);
-            const float ip2 = ip * ip;
-            zbar = dl[u] * rt[u] * ig2 + lam * rt[u] * rt[u] * ip2;
-            drt = -dl[u] * z * ig2 + lam * s * z * z * ip2;
-          }
-          da[o] = zbar * pp[u];
-          domega[o] = zbar;
-          dr[o] = drt;
-          lam = at[u] * zbar;
-        }
-      }
-      if (j == 0) dmu_acc += -lam / (muh * muh);
-    }
-    __syncthreads();  // sA / sB are reused by the next batch rows
+    Map2 E = shfl_up_map(M, 1);
+    if (lane == 0) E = map_identity();
+    if (c < NC) carry[(int64_t)bh * NC + c] = mobius(E, p);
+    const Map2 tot{__shfl(M.m0, 63, 64), __shfl(M.m1, 63, 64), __shfl(M.m2, 63, 64), __shfl(M.m3, 63, 64)};
+    p = mobius(tot, p);
   }
-  if (j == 0) sMu[g] = dmu_acc;
+  if (final_precision && lane == 0) final_precision[bh] = 1.f / p;
+}
+
+// grid (NC, B), block 256, dynamic LDS 5 * 64 * H floats + 4 * H maps.
+__global__ __launch_bounds__(256) void iso_gain_emit_kernel(const float* __restrict__ a, const float* __restrict__ omega,
+                                                            const float* __restrict__ r, int B, int T, int H, int NC,
+                                                            float s, int unit_scale, const float* __restrict__ carry,
+                                                            float* __restrict__ beta, float* __restrict__ p_prev) {
+  extern __shared__ float sm[];
+  float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H, *sbeta = sm + 3 * kIsoChunk * H,
+        *spp = sm + 4 * kIsoChunk * H;
+  Map2* sub = reinterpret_cast<Map2*>(sm + 5 * kIsoChunk * H);
+  const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
+  stage_bth(a, b, T, H, t0, L, sa);
+  stage_bth(omega, b, T, H, t0, L, sw);
+  stage_bth(r, b, T, H, t0, L, sr);
+  __syncthreads();
+  constexpr int SL = kIsoChunk / kIsoSub;
+  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
+    const int h = hq / kIsoSub, q = hq % kIsoSub;
+    Map2 M = map_identity();
+    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
+    sub[hq] = M;
+  }
+  __syncthreads();
+  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
+    const int h = hq / kIsoSub, q = hq % kIsoSub;
+    Map2 E = map_identity();
+    for (int q2 = 0; q2 < q; ++q2) E = map_mul(sub[kIsoSub * h + q2], E);
+    float p = mobius(E, carry[((int64_t)b * H + h) * NC + n]);
+    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) {
+      const float at = sa[t * H + h], wt = sw[t * H + h], rt = sr[t * H + h];
+      spp[t * H + h] = p;
+      const float z = at * p + wt;
+      const float g = z / (rt + z);
+      sbeta[t * H + h] = g;
+      p = unit_scale ? rt * g : rt * z / (rt + s * z);
+    }
+  }
+  __syncthreads();
+  store_bth(beta, b, T, H, t0, L, sbeta);
+  if (p_prev) store_bth(p_prev, b, T, H, t0, L, spp);
+}
+
+// Affine maps x -> A x + B of the reverse recurrence; compose(f, g) = f o g (g applied first).
+__device__ __forceinline__ float2 aff_compose(float2 f, float2 g) { return float2{f.x * g.x, f.x * g.y + f.y}; }
+__device__ __forceinline__ float2 token_aff(float at, float wt, float rt, float dl, float pp, float s) {
+  const float z = at * pp + wt;
+  const float ig = 1.f / (rt + z), ip = 1.f / (rt + s * z);
+  return float2{at * rt * rt * ip * ip, at * dl * rt * ig * ig};
+}
+
+// grid (NC, B), block 256, dynamic LDS 5 * 64 * H floats + 2 * 4 * H.
+__global__ __launch_bounds__(256) void iso_gain_bwd_map_kernel(const float* __restrict__ a,
+                                                               const float* __restrict__ omega,
+                                                               const float* __restrict__ r,
+                                                               const float* __restrict__ dbeta,
+                                                               const float* __restrict__ p_prev, int T, int H, int NC,
+                                                               float s, float2* __restrict__ maps) {
+  extern __shared__ float sm[];
+  float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H, *sd = sm + 3 * kIsoChunk * H,
+        *sp = sm + 4 * kIsoChunk * H;
+  float2* sub = reinterpret_cast<float2*>(sm + 5 * kIsoChunk * H);
+  const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
+  stage_bth(a, b, T, H, t0, L, sa);
+  stage_bth(omega, b, T, H, t0, L, sw);
+  stage_bth(r, b, T, H, t0, L, sr);
+  stage_bth(dbeta, b, T, H, t0, L, sd);
+  stage_bth(p_prev, b, T, H, t0, L, sp);
+  __syncthreads();
+  constexpr int SL = kIsoChunk / kIsoSub;
+  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
+    const int h = hq / kIsoSub, q = hq % kIsoSub;
+    float2 F{1.f, 0.f};  // lambda before the sub-segment from lambda after it
+    for (int t = min(L, (q + 1) * SL) - 1; t >= q * SL; --t) {
+      const int e = t * H + h;
+      F = aff_compose(token_aff(sa[e], sw[e], sr[e], sd[e], sp[e], s), F);  // earlier token applied after
+    }
+    sub[hq] = F;
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    float2 F = sub[kIsoSub * h + kIsoSub - 1];
+    for (int q = kIsoSub - 2; q >= 0; --q) F = aff_compose(sub[kIsoSub * h + q], F);
+    maps[((int64_t)b * H + h) * NC + n] = F;
+  }
+}
+
+// grid (H), block 64 * GB (GB = min(B, 16)): wave g scans batch rows b = g, g + GB, ... from the
+// last chunk back; lambda after each chunk goes to `carry`, and d mu = -sum_b lambda_0 / mu^2.
+__global__ __launch_bounds__(1024) void iso_gain_bwd_carry_kernel(const float2* __restrict__ maps,
+                                                                  const float* __restrict__ mu, int B, int H, int NC,
+                                                                  float* __restrict__ carry, float* __restrict__ dmu) {
+  __shared__ float sMu[16];
+  const int h = blockIdx.x, lane = threadIdx.x & 63, g = threadIdx.x >> 6, GB = blockDim.x >> 6;
+  float dmu_acc = 0.f;
+  for (int b = g; b < B; b += GB) {
+    const int64_t bh = (int64_t)b * H + h;
+    float lam = 0.f;  // lambda after the last chunk
+    for (int c1 = NC; c1 > 0; c1 -= 64) {
+      const int c = c1 - 1 - lane;  // lane 0 = latest chunk of this group
+      float2 F{1.f, 0.f};
+      if (c >= 0) F = maps[bh * NC + c];
+      // inclusive scan over lanes: lane j composes chunks c1-1 ... c1-1-j (latest applied first)
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float Ap = __shfl_up(F.x, d, 64), Bp = __shfl_up(F.y, d, 64);
+        if (lane >= d) F = aff_compose(F, float2{Ap, Bp});
+      }
+      float Ae = __shfl_up(F.x, 1, 64), Be = __shfl_up(F.y, 1, 64);
+      if (lane == 0) Ae = 1.f, Be = 0.f;
+      if (c >= 0) carry[bh * NC + c] = Ae * lam + Be;  // lambda after chunk c
+      lam = __shfl(F.x, 63, 64) * lam + __shfl(F.y, 63, 64);
+    }
+    if (lane == 0) dmu_acc += -lam / (mu[h] * mu[h]);
+  }
+  if (lane == 0) sMu[g] = dmu_acc;
   __syncthreads();
   if (threadIdx.x == 0 && dmu) {
     float tot = 0.f;
     for (int q = 0; q < GB; ++q) tot += sMu[q];
     dmu[h] = tot;
   }
+}
+
+// grid (NC, B), block 256, dynamic LDS 8 * 64 * H floats + 2 * 4 * H.
+__global__ __launch_bounds__(256) void iso_gain_bwd_emit_kernel(
+    const float* __restrict__ a, const float* __restrict__ omega, const float* __restrict__ r,
+    const float* __restrict__ dbeta, const float* __restrict__ p_prev, int T, int H, int NC, float s, int unit_scale,
+    const float* __restrict__ carry, float* __restrict__ da, float* __restrict__ domega, float* __restrict__ dr) {
+  extern __shared__ float sm[];
+  float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H, *sd = sm + 3 * kIsoChunk * H,
+        *sp = sm + 4 * kIsoChunk * H, *oa = sm + 5 * kIsoChunk * H, *ow = sm + 6 * kIsoChunk * H,
+        *orr = sm + 7 * kIsoChunk * H;
+  float2* sub = reinterpret_cast<float2*>(sm + 8 * kIsoChunk * H);
+  const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
+  stage_bth(a, b, T, H, t0, L, sa);
+  stage_bth(omega, b, T, H, t0, L, sw);
+  stage_bth(r, b, T, H, t0, L, sr);
+  stage_bth(dbeta, b, T, H, t0, L, sd);
+  stage_bth(p_prev, b, T, H, t0, L, sp);
+  __syncthreads();
+  constexpr int SL = kIsoChunk / kIsoSub;
+  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
+    const int h = hq / kIsoSub, q = hq % kIsoSub;
+    float2 F{1.f, 0.f};
+    for (int t = min(L, (q + 1) * SL) - 1; t >= q * SL; --t) {
+      const int e = t * H + h;
+      F = aff_compose(token_aff(sa[e], sw[e], sr[e], sd[e], sp[e], s), F);  // earlier token applied after
+    }
+    sub[hq] = F;
+  }
+  __syncthreads();
+  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
+    const int h = hq / kIsoSub, q = hq % kIsoSub;
+    float lam = carry[((int64_t)b * H + h) * NC + n];  // lambda after the chunk
+    for (int q2 = kIsoSub - 1; q2 > q; --q2) {
+      const float2 F = sub[kIsoSub * h + q2];
+      lam = F.x * lam + F.y;
+    }
+    for (int t = min(L, (q + 1) * SL) - 1; t >= q * SL; --t) {
+      const int e = t * H + h;
+      const float at = sa[e], wt = sw[e], rt = sr[e], dl = sd[e], pp = sp[e];
+      const float z = at * pp + wt;
+      const float ig = 1.f / (rt + z);
+      const float ig2 = ig * ig;
+      float zbar, drt;
+      if (unit_scale) {
+        zbar = (dl + rt * lam) * rt * ig2;
+        drt = z * (lam * z - dl) * ig2;
+      } else {
+        const float ip = 1.f / (rt + s * z);
+        const float ip2 = ip * ip;
+        zbar = dl * rt * ig2 + lam * rt * rt * ip2;
+        drt = -dl * z * ig2 + lam * s * z * z * ip2;
+      }
+      oa[e] = zbar * pp;
+      ow[e] = zbar;
+      orr[e] = drt;
+      lam = at * zbar;
+    }
+  }
+  __syncthreads();
+  store_bth(da, b, T, H, t0, L, oa);
+  store_bth(domega, b, T, H, t0, L, ow);
+  store_bth(dr, b, T, H, t0, L, orr);
 }
 
 // ----------------------------------------------------------------------------
@@ -455,28 +538,53 @@ inline int gain_block(int K) { return ((K + 63) / 64) * 64; }
 
 extern "C" {
 
+size_t kdn_iso_gain_workspace_size(int B, int T, int H) {
+  const int64_t NC = cdiv(T, kIsoChunk);
+  return (size_t)((int64_t)B * H * NC * 5) * sizeof(float);
+}
+
 int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision, int B, int T,
                      int H, float posterior_scale, float* beta, float* p_prev, float* final_precision,
-                     hipStream_t stream) {
-  if (B < 0 || T < 0 || H <= 0 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
-  const int GB = B < 4 ? B : 4;
-  hipLaunchKernelGGL(iso_gain_fwd_grp_kernel, dim3(H), dim3(kIsoGroup * GB), 0, stream, a, omega, r,
-                     initial_precision, B, T, H, posterior_scale, posterior_scale == 1.f ? 1 : 0, beta, p_prev,
+  if (workspace_bytes < kdn_iso_gain_workspace_size(B, T, H)) return KDN_ERR_ARG;
+  const int NC = cdiv(T, kIsoChunk);
+  float4* maps = (float4*)workspace;
+  float* carry = (float*)(maps + (int64_t)B * H * NC);
+  const int unit = posterior_scale == 1.f ? 1 : 0;
+  const size_t lds_map = (size_t)(3 * kIsoChunk * H + 4 * kIsoSub * H) * sizeof(float);
+  const size_t lds_emit = (size_t)(5 * kIsoChunk * H + 4 * kIsoSub * H) * sizeof(float);
+  hipLaunchKernelGGL(iso_gain_map_kernel, dim3(NC, B), dim3(256), lds_map, stream, a, omega, r, T, H, NC,
+                     posterior_scale, maps);
+  hipLaunchKernelGGL(iso_gain_carry_kernel, dim3(B * H), dim3(64), 0, stream, maps, initial_precision, H, NC, carry,
                      final_precision);
+  hipLaunchKernelGGL(iso_gain_emit_kernel, dim3(NC, B), dim3(256), lds_emit, stream, a, omega, r, B, T, H, NC,
+                     posterior_scale, unit, carry, beta, p_prev);
   KDN_CHECK_LAUNCH();
   return 0;
 }
 
 int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const float* initial_precision,
                      const float* dbeta, const float* p_prev, int B, int T, int H, float posterior_scale, float* da,
-                     float* domega, float* dr, float* d_initial_precision, hipStream_t stream) {
-  if (B < 0 || T < 0 || H <= 0 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
+                     float* domega, float* dr, float* d_initial_precision, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
-  const int GB = B < 4 ? B : 4;
-  hipLaunchKernelGGL(iso_gain_bwd_grp_kernel, dim3(H), dim3(kIsoGroup * GB), 0, stream, a, omega, r,
-                     initial_precision, dbeta, p_prev, B, T, H, posterior_scale, posterior_scale == 1.f ? 1 : 0, da,
-                     domega, dr, d_initial_precision);
+  if (workspace_bytes < kdn_iso_gain_workspace_size(B, T, H)) return KDN_ERR_ARG;
+  const int NC = cdiv(T, kIsoChunk);
+  float2* maps = (float2*)workspace;
+  float* carry = (float*)(maps + (int64_t)B * H * NC);
+  const int unit = posterior_scale == 1.f ? 1 : 0;
+  const size_t lds_map = (size_t)(5 * kIsoChunk * H + 2 * kIsoSub * H) * sizeof(float);
+  const size_t lds_emit = (size_t)(8 * kIsoChunk * H + 2 * kIsoSub * H) * sizeof(float);
+  const int GB = B < 16 ? B : 16;
+  hipLaunchKernelGGL(iso_gain_bwd_map_kernel, dim3(NC, B), dim3(256), lds_map, stream, a, omega, r, dbeta, p_prev, T,
+                     H, NC, posterior_scale, maps);
+  hipLaunchKernelGGL(iso_gain_bwd_carry_kernel, dim3(H), dim3(64 * GB), 0, stream, maps, initial_precision, B, H, NC,
+                     carry, d_initial_precision);
+  hipLaunchKernelGGL(iso_gain_bwd_emit_kernel, dim3(NC, B), dim3(256), lds_emit, stream, a, omega, r, dbeta, p_prev, T,
+                     H, NC, posterior_scale, unit, carry, da, domega, dr);
   KDN_CHECK_LAUNCH();
   return 0;
 }

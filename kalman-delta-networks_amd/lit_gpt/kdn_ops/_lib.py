@@ -19,8 +19,9 @@ _SIGS = {
     "kdn_iso_gate_fwd": "pipillpppppffiiiiippppps",
     "kdn_iso_gate_bwd_workspace_size": "iiiii",
     "kdn_iso_gate_bwd": "pipillppppppppppiiiiippppppppzs",
-    "kdn_iso_gain_fwd": "ppppiiifppps",
-    "kdn_iso_gain_bwd": "ppppppiiifpppps",
+    "kdn_iso_gain_workspace_size": "iii",
+    "kdn_iso_gain_fwd": "ppppiiifppppzs",
+    "kdn_iso_gain_bwd": "ppppppiiifpppppzs",
     "kdn_l2norm_fwd": "pilifpips",
     "kdn_l2norm_bwd": "pippilips",
     "kdn_diag_norm_fwd": "ppilippppps",
@@ -37,7 +38,7 @@ _SIGS = {
     "kdn_mem_fwd": "pppippiiiiifppzppiis",
     "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppis",
 }
-_SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_diag_frontend_bwd_workspace_size",
+_SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_iso_gain_workspace_size", "kdn_diag_frontend_bwd_workspace_size",
              "kdn_diag_gain_workspace_size", "kdn_mem_saved_size", "kdn_mem_bwd_workspace_size"}
 _CT = {"p": ctypes.c_void_p, "i": ctypes.c_int, "l": ctypes.c_int64, "f": ctypes.c_float,
        "z": ctypes.c_size_t, "s": ctypes.c_void_p}

@@ -210,10 +210,12 @@ def _iso_kdn_gain_forward(a, omega, r, initial_precision, *, out_dtype, save_sta
     gain = torch.empty((B, T, H), dtype=torch.float32, device=device)
     p_prev = torch.empty((B, T, H), dtype=torch.float32, device=device) if save_state else None
     if T > 0 and B > 0:
+        ws_bytes = _lib.size("kdn_iso_gain_workspace_size", B, T, H)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
         with torch.cuda.device(device):
             _lib.call("kdn_iso_gain_fwd", _lib.ptr(a), _lib.ptr(omega), _lib.ptr(r),
                       _lib.ptr(initial_precision), B, T, H, float(posterior_scale), _lib.ptr(gain),
-                      _lib.ptr(p_prev), None, _lib.stream_of(a))
+                      _lib.ptr(p_prev), None, _lib.ptr(ws), ws_bytes, _lib.stream_of(a))
     return (gain if out_dtype == torch.float32 else gain.to(out_dtype)), p_prev
 
 
@@ -226,10 +228,12 @@ def _iso_kdn_gain_backward(a, omega, r, initial_precision, dgain, p_prev, *, pos
     dr = torch.empty_like(r)
     dmu = torch.zeros((H,), dtype=torch.float32, device=device)
     if T > 0 and B > 0:
+        ws_bytes = _lib.size("kdn_iso_gain_workspace_size", B, T, H)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
         with torch.cuda.device(device):
             _lib.call("kdn_iso_gain_bwd", _lib.ptr(a), _lib.ptr(omega), _lib.ptr(r), _lib.ptr(initial_precision),
                       _lib.ptr(dgain), _lib.ptr(p_prev), B, T, H, float(posterior_scale), _lib.ptr(da),
-                      _lib.ptr(domega), _lib.ptr(dr), _lib.ptr(dmu), _lib.stream_of(a))
+                      _lib.ptr(domega), _lib.ptr(dr), _lib.ptr(dmu), _lib.ptr(ws), ws_bytes, _lib.stream_of(a))
     return da, domega, dr, dmu.to(initial_precision.dtype)
 
 

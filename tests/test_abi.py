@@ -31,3 +31,22 @@ def test_library_is_current_and_exports_all_symbols():
         assert hasattr(lib, name), name
     assert lib.kdn_mem_chunk_size() == 64
     assert _lib.size("kdn_mem_saved_size", 1, 64, 1, 64, 64) > 0
+
+
+def test_integration_stub_matches_header():
+    """The ctypes stub shown to reference-side maintainers declares every entry point with the
+    header's argument and return types."""
+    import re
+
+    from _header_sigs import header_signatures
+    sigs = header_signatures()
+    doc = (pathlib.Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    blk = doc[doc.index("_sig = {"):doc.index("for _n, (_a, _r)")]
+    code = {"P": "p", "I": "i", "L": "l", "F": "f", "Z": "z", "S": "s"}
+    stub = {}
+    for name, args, ret in re.findall(r'"(kdn_\w+)": \(\[([^\]]*)\], (\w)\)', blk, re.S):
+        stub[name] = ({"I": "int", "Z": "size_t"}[ret],
+                      "".join(code[a.strip()] for a in args.replace("\n", " ").split(",") if a.strip()))
+    assert set(stub) == set(sigs), set(stub) ^ set(sigs)
+    for name, sig in sigs.items():
+        assert stub[name] == tuple(sig), name
