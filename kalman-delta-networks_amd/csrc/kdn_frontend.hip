@@ -619,6 +619,238 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_kernel(
   if (part_A && i == 0) part_A[(int64_t)p * H + h] = sA;
 }
 
+// ---------------------------------------------------------------------------
+// Vectorised diag frontend (same thread layout as the vectorised iso gate).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void diag_frontend_fwd_vec_kernel(
+    const bf16_t* __restrict__ f_raw, const bf16_t* __restrict__ z_raw, const bf16_t* __restrict__ y_raw,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* __restrict__ mu_param, int T,
+    int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ alpha,
+    float* __restrict__ omega, float* __restrict__ r, float* __restrict__ mu) {
+  __shared__ float s_tot[256 * 8];
+  const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const float rate = __expf(A_log[h]);
+  const float floor_log = -13.815510557964274f;  // log(1e-6)
+  float bias[8];
+  load8<float>(dt_bias + h * K + i0, bias);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float pre[4][8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tg * TPG + u;
+    if (u < TPG && t < L) {
+      const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i0;
+      float x[8], zr[8], al[8], om[8];
+      load8<bf16_t>(f_raw + off, x);
+      load8<bf16_t>(z_raw + off, zr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ell = -rate * softplusf(x[j] + bias[j]);
+        al[j] = __expf(ell);
+        // memory path clamps alpha at 1e-6 (NaN propagates)
+        acc[j] += (al[j] >= 1e-6f || al[j] != al[j]) ? ell : floor_log;
+        pre[u][j] = acc[j];
+        om[j] = softplusf(zr[j]);
+      }
+      store8<float>(alpha + off, al);
+      store8<float>(omega + off, om);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = acc[j];
+  __syncthreads();
+  float offs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < tg; ++q)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) offs[j] += s_tot[q * K + i0 + j];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tg * TPG + u;
+    if (u < TPG && t < L) {
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (offs[j] + pre[u][j]) * KDN_LOG2E;
+      store8<float>(g_cumsum + (((int64_t)b * T + t0 + t) * H + h) * K + i0, y);
+    }
+  }
+  if (tid < L) {
+    const int64_t o = ((int64_t)b * T + t0 + tid) * H + h;
+    r[o] = 0.01f + softplusf(bf2f(y_raw[o]));
+  }
+  if (blockIdx.x == 0 && tid == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
+}
+
+__global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
+    const bf16_t* __restrict__ f_raw, const float* __restrict__ A_log, const float* __restrict__ dt_bias,
+    const float* __restrict__ alpha, const float* __restrict__ dG, const float* __restrict__ dalpha, int T, int H,
+    int K, int chunk, int NT, bf16_t* __restrict__ df_raw, float* __restrict__ part_A,
+    float* __restrict__ part_dt) {
+  __shared__ float s_tot[256 * 8];
+  __shared__ float red[16];
+  const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
+  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
+  const int t0 = nt * chunk, L = min(chunk, T - t0);
+  const int p = blockIdx.x;
+  const float rate = __expf(A_log[h]);
+  float bias[8];
+  load8<float>(dt_bias + h * K + i0, bias);
+  // local suffix sums of dG over this thread's tokens
+  float dgs[4][8], acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 3; u >= 0; --u) {
+    const int t = tg * TPG + u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dgs[u][j] = 0.f;
+    if (dG && u < TPG && t < L) {
+      float d[8];
+      load8<float>(dG + (((int64_t)b * T + t0 + t) * H + h) * K + i0, d);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc[j] += d[j];
+        dgs[u][j] = acc[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = acc[j];
+  __syncthreads();
+  float offs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int q = tg + 1; q < TGN; ++q)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) offs[j] += s_tot[q * K + i0 + j];
+  __syncthreads();
+  float ddt[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, dA_term = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = tg * TPG + u;
+    if (u < TPG && t < L) {
+      const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i0;
+      float x[8], al[8], da[8], df[8];
+      load8<bf16_t>(f_raw + off, x);
+      load8<float>(alpha + off, al);
+      if (dalpha) load8<float>(dalpha + off, da);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xb = x[j] + bias[j];
+        const float ell = -rate * softplusf(xb);
+        float dell = (dG && al[j] >= 1e-6f) ? offs[j] + dgs[u][j] : 0.f;
+        if (dalpha) dell += da[j] * al[j];
+        df[j] = dell * (-rate) * sigmoidf(xb);
+        dA_term += dell * ell;
+        ddt[j] += df[j];
+      }
+      if (df_raw) store8<bf16_t>(df_raw + off, df);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = ddt[j];
+  __syncthreads();
+  if (part_dt && tid < K) {
+    float sdt = 0.f;
+    for (int q = 0; q < TGN; ++q) sdt += s_tot[q * K + tid];
+    part_dt[((int64_t)p * H + h) * K + tid] = sdt;
+  }
+  const float sA = block_sum(dA_term, red);
+  if (part_A && tid == 0) part_A[(int64_t)p * H + h] = sA;
+}
+
+// Vectorised diag normalisation rows (K/8 lanes per row, 8 elements per lane).
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_norm_fwd_vec_kernel(const TX* __restrict__ q, const TX* __restrict__ k,
+                                                                int64_t rows, int K, bf16_t* __restrict__ q_mem,
+                                                                float* __restrict__ k_gain, bf16_t* __restrict__ k_mem,
+                                                                float* __restrict__ q_norm,
+                                                                float* __restrict__ k_norm) {
+  const int LPR = K / 8, RPB = 256 / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  float qv[8], kv[8], sq = 0.f, sk = 0.f;
+  if (row < rows) {
+    load8<TX>(q + row * K + 8 * sub, qv);
+    load8<TX>(k + row * K + 8 * sub, kv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sq += qv[j] * qv[j];
+      sk += kv[j] * kv[j];
+    }
+  }
+  for (int o = 1; o < LPR; o <<= 1) {
+    sq += __shfl_xor(sq, o, 64);
+    sk += __shfl_xor(sk, o, 64);
+  }
+  if (row >= rows) return;
+  const float nq = sqrtf(sq), nk = sqrtf(sk);
+  const float iq = 1.f / fmaxf(nq, 1e-12f), ik = 1.f / fmaxf(nk, 1e-12f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    qv[j] *= iq;
+    kv[j] *= ik;
+  }
+  store8<bf16_t>(q_mem + row * K + 8 * sub, qv);
+  store8<float>(k_gain + row * K + 8 * sub, kv);
+  store8<bf16_t>(k_mem + row * K + 8 * sub, kv);
+  if (sub == 0) {
+    q_norm[row] = nq;
+    k_norm[row] = nk;
+  }
+}
+
+// Row VJP of y = x / max(||x||, eps) on 8 elements per lane, LPR lanes per row.
+template <typename TX>
+__device__ __forceinline__ void norm_row_vjp8(const TX* x, float n, const float* g, int LPR, bool valid, float* dx) {
+  const float d = fmaxf(n, 1e-12f), id = 1.f / d;
+  float yv[8], dot = 0.f;
+  if (valid) {
+    load8<TX>(x, yv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      yv[j] *= id;
+      dot += yv[j] * g[j];
+    }
+  }
+  for (int o = 1; o < LPR; o <<= 1) dot += __shfl_xor(dot, o, 64);
+  const bool clamped = !(n > 1e-12f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dx[j] = clamped ? g[j] * id : (g[j] - yv[j] * dot) * id;
+}
+
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_norm_bwd_vec_kernel(
+    const TX* __restrict__ q, const TX* __restrict__ k, const float* __restrict__ q_norm,
+    const float* __restrict__ k_norm, const bf16_t* __restrict__ dq_mem, const float* __restrict__ dk_gain,
+    const bf16_t* __restrict__ dk_mem, int64_t rows, int K, TX* __restrict__ dq, TX* __restrict__ dk) {
+  const int LPR = K / 8, RPB = 256 / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  const bool valid = row < rows;
+  const int64_t e = (valid ? row : 0) * K + 8 * sub;
+  float g[8], out[8];
+  if (dq) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) g[j] = 0.f;
+    if (valid && dq_mem) load8<bf16_t>(dq_mem + e, g);
+    norm_row_vjp8<TX>(q + e, valid ? q_norm[row] : 1.f, g, LPR, valid, out);
+    if (valid) store8<TX>(dq + e, out);
+  }
+  if (dk) {
+    float g2[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) g[j] = 0.f;
+    if (valid && dk_gain) load8<float>(dk_gain + e, g);
+    if (valid && dk_mem) {
+      load8<bf16_t>(dk_mem + e, g2);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) g[j] += g2[j];
+    }
+    norm_row_vjp8<TX>(k + e, valid ? k_norm[row] : 1.f, g, LPR, valid, out);
+    if (valid) store8<TX>(dk + e, out);
+  }
+}
+
 // d raw = d * sigmoid(raw) for the (optional) omega / r cotangents reaching the frontend.
 __global__ void sigmoid_vjp_kernel(const bf16_t* __restrict__ raw, const float* __restrict__ d, int64_t n,
                                    bf16_t* __restrict__ out) {
@@ -789,6 +1021,18 @@ int kdn_diag_norm_fwd(const void* q_raw, const void* k_raw, int x_bf16, int64_t 
                       float* k_gain, uint16_t* k_memory, float* q_norm, float* k_norm, hipStream_t stream) {
   if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
   if (rows == 0) return 0;
+  if (row_vec_ok(K) && aligned16(q_raw) && aligned16(k_raw) && aligned16(q_memory) && aligned16(k_gain) &&
+      aligned16(k_memory)) {
+    dim3 gv(cdiv(rows, 256 / (K / 8)));
+    if (x_bf16)
+      hipLaunchKernelGGL((diag_norm_fwd_vec_kernel<bf16_t>), gv, dim3(256), 0, stream, (const bf16_t*)q_raw,
+                         (const bf16_t*)k_raw, rows, K, q_memory, k_gain, k_memory, q_norm, k_norm);
+    else
+      hipLaunchKernelGGL((diag_norm_fwd_vec_kernel<float>), gv, dim3(256), 0, stream, (const float*)q_raw,
+                         (const float*)k_raw, rows, K, q_memory, k_gain, k_memory, q_norm, k_norm);
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
   dim3 grid(cdiv(rows, 4));
   if (x_bf16)
     hipLaunchKernelGGL((diag_norm_fwd_kernel<bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)q_raw, (const bf16_t*)k_raw, rows, K, q_memory, k_gain, k_memory, q_norm, k_norm);
@@ -803,6 +1047,20 @@ int kdn_diag_norm_bwd(const void* q_raw, const void* k_raw, int x_bf16, const fl
                       int K, void* dq_raw, void* dk_raw, hipStream_t stream) {
   if (K <= 0 || K > 256 || rows < 0) return KDN_ERR_ARG;
   if (rows == 0) return 0;
+  if (row_vec_ok(K) && aligned16(q_raw) && aligned16(k_raw) && aligned16(d_q_memory) && aligned16(d_k_gain) &&
+      aligned16(d_k_memory) && aligned16(dq_raw) && aligned16(dk_raw)) {
+    dim3 gv(cdiv(rows, 256 / (K / 8)));
+    if (x_bf16)
+      hipLaunchKernelGGL((diag_norm_bwd_vec_kernel<bf16_t>), gv, dim3(256), 0, stream, (const bf16_t*)q_raw,
+                         (const bf16_t*)k_raw, q_norm, k_norm, d_q_memory, d_k_gain, d_k_memory, rows, K,
+                         (bf16_t*)dq_raw, (bf16_t*)dk_raw);
+    else
+      hipLaunchKernelGGL((diag_norm_bwd_vec_kernel<float>), gv, dim3(256), 0, stream, (const float*)q_raw,
+                         (const float*)k_raw, q_norm, k_norm, d_q_memory, d_k_gain, d_k_memory, rows, K,
+                         (float*)dq_raw, (float*)dk_raw);
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
   dim3 grid(cdiv(rows, 4));
   if (x_bf16)
     hipLaunchKernelGGL((diag_norm_bwd_kernel<bf16_t>), grid, dim3(256), 0, stream, (const bf16_t*)q_raw, (const bf16_t*)k_raw, q_norm, k_norm, d_q_memory, d_k_gain, d_k_memory, rows, K, (bf16_t*)dq_raw, (bf16_t*)dk_raw);
@@ -818,8 +1076,11 @@ int kdn_diag_frontend_fwd(const uint16_t* retention_raw, const uint16_t* omega_r
                           hipStream_t stream) {
   if (K <= 0 || K > 256 || chunk <= 0 || B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
   const int NT = cdiv(T, chunk);
-  hipLaunchKernelGGL(diag_frontend_fwd_kernel, dim3(B * NT, H), dim3(256), 0, stream, retention_raw, omega_raw, r_raw,
-                     A_log, dt_bias, mu_param, T, H, K, chunk, NT, g_cumsum, alpha, omega, r, mu);
+  const bool vec = gate_vec_ok(K, chunk) && aligned16(retention_raw) && aligned16(omega_raw) && aligned16(dt_bias) &&
+                   aligned16(g_cumsum) && aligned16(alpha) && aligned16(omega);
+  hipLaunchKernelGGL(vec ? diag_frontend_fwd_vec_kernel : diag_frontend_fwd_kernel, dim3(B * NT, H), dim3(256), 0,
+                     stream, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, T, H, K, chunk, NT, g_cumsum,
+                     alpha, omega, r, mu);
   KDN_CHECK_LAUNCH();
   return 0;
 }
@@ -843,9 +1104,11 @@ int kdn_diag_frontend_bwd(const uint16_t* retention_raw, const uint16_t* omega_r
   float* part_dt = part_A + (int64_t)NP * H;
   const bool has_decay = d_g_cumsum || d_alpha;
   if (has_decay && (d_retention_raw || dA_log || ddt_bias)) {
-    hipLaunchKernelGGL(diag_frontend_bwd_kernel, dim3(NP, H), dim3(256), 0, stream, retention_raw, A_log, dt_bias,
-                       alpha, d_g_cumsum, d_alpha, T, H, K, chunk, NT, d_retention_raw, dA_log ? part_A : nullptr,
-                       ddt_bias ? part_dt : nullptr);
+    const bool vec = gate_vec_ok(K, chunk) && aligned16(retention_raw) && aligned16(dt_bias) && aligned16(alpha) &&
+                     aligned16(d_g_cumsum) && aligned16(d_alpha) && aligned16(d_retention_raw);
+    hipLaunchKernelGGL(vec ? diag_frontend_bwd_vec_kernel : diag_frontend_bwd_kernel, dim3(NP, H), dim3(256), 0,
+                       stream, retention_raw, A_log, dt_bias, alpha, d_g_cumsum, d_alpha, T, H, K, chunk, NT,
+                       d_retention_raw, dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr);
     KDN_CHECK_LAUNCH();
     if (dA_log)
       hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H,

@@ -522,6 +522,276 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_emit_kernel(
   }
 }
 
+// ----------------------------------------------------------------------------
+// Vectorised diag gain (K % 8 == 0, K/8 | 64): a thread owns 8 consecutive channels of one
+// (b, h, chunk) tile; TPT = K/8 threads per tile, tiles ordered with h fastest.  Loads and
+// stores are 16-byte vectors; the per-token cross-channel sums are shuffles over the tile's
+// TPT lanes.  Same workspace layouts as the per-channel kernels above.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void ld8f(const float* p, float* f) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+}
+__device__ __forceinline__ void st8f(float* p, const float* f) {
+  reinterpret_cast<float4*>(p)[0] = float4{f[0], f[1], f[2], f[3]};
+  reinterpret_cast<float4*>(p)[1] = float4{f[4], f[5], f[6], f[7]};
+}
+__device__ __forceinline__ float tile_sum(float x, int tpt) {
+  for (int o = 1; o < tpt; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+struct GainTile {
+  int b, h, nt, i0, sub, t0, t1;
+  bool ok;
+};
+__device__ __forceinline__ GainTile gain_tile(int B, int T, int H, int K, int NT) {
+  const int tpt = K / 8, tpb = 256 / tpt;
+  const int64_t gt = (int64_t)blockIdx.x * tpb + threadIdx.x / tpt;
+  GainTile g;
+  g.ok = gt < (int64_t)B * NT * H;
+  const int64_t gg = g.ok ? gt : 0;
+  g.h = (int)(gg % H);
+  const int64_t bn = gg / H;
+  g.nt = (int)(bn % NT);
+  g.b = (int)(bn / NT);
+  g.sub = threadIdx.x % tpt;
+  g.i0 = 8 * g.sub;
+  g.t0 = g.nt * kGainChunk;
+  g.t1 = min(g.t0 + kGainChunk, T);
+  return g;
+}
+
+__global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __restrict__ k, const float* __restrict__ alpha,
+                                                              const float* __restrict__ omega, const float* __restrict__ r,
+                                                              int B, int T, int H, int K, int NT, float s,
+                                                              float* __restrict__ maps) {
+  const GainTile g = gain_tile(B, T, H, K, NT);
+  if (!g.ok) return;
+  Map2 M[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) M[j] = Map2{1.f, 0.f, 0.f, 1.f};
+  for (int t = g.t0; t < g.t1; ++t) {
+    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
+    float kt[8], al[8], wt[8];
+    ld8f(k + row * K + g.i0, kt);
+    ld8f(alpha + row * K + g.i0, al);
+    ld8f(omega + row * K + g.i0, wt);
+    const float ir = 1.f / r[row];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a2 = al[j] * al[j], u = s * kt[j] * kt[j] * ir;
+      M[j] = map_mul(Map2{a2, wt[j], u * a2, 1.f + u * wt[j]}, M[j]);
+    }
+  }
+  float4* dst = reinterpret_cast<float4*>(maps + ((((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0) * 4);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dst[j] = float4{M[j].m0, M[j].m1, M[j].m2, M[j].m3};
+}
+
+// grid (B*H), block K: per channel, maps of 8 chunks loaded at a time.
+__global__ __launch_bounds__(256) void diag_gain_carry_v_kernel(const float4* __restrict__ maps,
+                                                                const float* __restrict__ prec0, int prec_mode, int H,
+                                                                int K, int NT, float* __restrict__ carry,
+                                                                float* __restrict__ final_prec) {
+  const int bh = blockIdx.x, b = bh / H, h = bh % H, i = threadIdx.x;
+  if (i >= K) return;
+  float p = 1.f / (prec_mode == 0 ? prec0[h] : prec0[((int64_t)b * H + h) * K + i]);
+  const int64_t cb = (int64_t)bh * NT;
+  for (int n0 = 0; n0 < NT; n0 += 8) {
+    float4 m[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m[u] = maps[(cb + min(n0 + u, NT - 1)) * K + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (n0 + u >= NT) break;
+      carry[(cb + n0 + u) * K + i] = p;
+      p = (m[u].x * p + m[u].y) / (m[u].z * p + m[u].w);
+    }
+  }
+  if (final_prec) final_prec[((int64_t)b * H + h) * K + i] = 1.f / p;
+}
+
+__global__ __launch_bounds__(256) void diag_gain_emit_v_kernel(const float* __restrict__ k, const float* __restrict__ alpha,
+                                                               const float* __restrict__ omega,
+                                                               const float* __restrict__ r,
+                                                               const float* __restrict__ carry, int B, int T, int H,
+                                                               int K, int NT, float s, float* __restrict__ kappa,
+                                                               float* __restrict__ p_prev, float* __restrict__ Dsave) {
+  const GainTile g = gain_tile(B, T, H, K, NT);
+  if (!g.ok) return;
+  const int tpt = K / 8;
+  float p[8];
+  ld8f(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, p);
+  for (int t = g.t0; t < g.t1; ++t) {
+    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
+    float kt[8], al[8], wt[8], pp[8], num[8];
+    ld8f(k + row * K + g.i0, kt);
+    ld8f(alpha + row * K + g.i0, al);
+    ld8f(omega + row * K + g.i0, wt);
+    const float rt = r[row], ir = 1.f / rt;
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float ph = al[j] * al[j] * p[j] + wt[j];
+      pp[j] = p[j];
+      num[j] = ph * kt[j];
+      sq += num[j] * kt[j];
+      p[j] = ph / (1.f + s * kt[j] * kt[j] * ir * ph);
+    }
+    if (p_prev) st8f(p_prev + row * K + g.i0, pp);
+    const float D = rt + tile_sum(sq, tpt), iD = 1.f / D;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) num[j] *= iD;
+    st8f(kappa + row * K + g.i0, num);
+    if (Dsave && g.sub == 0) Dsave[row] = D;
+  }
+}
+
+__global__ __launch_bounds__(256) void diag_gain_bwd_map_v_kernel(
+    const float* __restrict__ k, const float* __restrict__ alpha, const float* __restrict__ omega,
+    const float* __restrict__ r, const float* __restrict__ dkappa, const float* __restrict__ p_prev,
+    const float* __restrict__ Dsave, int B, int T, int H, int K, int NT, float s, float* __restrict__ ab,
+    float* __restrict__ Gsave) {
+  const GainTile g = gain_tile(B, T, H, K, NT);
+  if (!g.ok) return;
+  const int tpt = K / 8;
+  float Aacc[8], Bacc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f;
+  for (int t = g.t1 - 1; t >= g.t0; --t) {
+    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
+    float kt[8], al[8], wt[8], pv[8], dk_[8], ph[8];
+    ld8f(k + row * K + g.i0, kt);
+    ld8f(alpha + row * K + g.i0, al);
+    ld8f(omega + row * K + g.i0, wt);
+    ld8f(p_prev + row * K + g.i0, pv);
+    ld8f(dkappa + row * K + g.i0, dk_);
+    const float D = Dsave[row], iD = 1.f / D, ir = 1.f / r[row];
+    float gp = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ph[j] = al[j] * al[j] * pv[j] + wt[j];
+      gp += dk_[j] * ph[j] * kt[j];
+    }
+    const float G = tile_sum(gp, tpt) * iD;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a2 = al[j] * al[j];
+      const float hh = 1.f + s * kt[j] * kt[j] * ir * ph[j];
+      const float pbar = dk_[j] * kt[j] * iD - kt[j] * kt[j] * G * iD;
+      const float At = a2 / (hh * hh);
+      Bacc[j] = At * Bacc[j] + a2 * pbar;
+      Aacc[j] = At * Aacc[j];
+    }
+    if (Gsave && g.sub == 0) Gsave[row] = G;
+  }
+  float4* dst = reinterpret_cast<float4*>(ab + ((((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0) * 2);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) dst[q] = float4{Aacc[2 * q], Bacc[2 * q], Aacc[2 * q + 1], Bacc[2 * q + 1]};
+}
+
+__global__ __launch_bounds__(256) void diag_gain_bwd_carry_v_kernel(const float2* __restrict__ ab,
+                                                                    const float* __restrict__ d_final_prec,
+                                                                    const float* __restrict__ final_prec, int H,
+                                                                    int K, int NT, float* __restrict__ carry) {
+  const int bh = blockIdx.x, i = threadIdx.x;
+  if (i >= K) return;
+  float lam = 0.f;
+  if (d_final_prec) {
+    const float c = final_prec[(int64_t)bh * K + i];
+    lam = -d_final_prec[(int64_t)bh * K + i] * c * c;
+  }
+  const int64_t cb = (int64_t)bh * NT;
+  for (int n1 = NT - 1; n1 >= 0; n1 -= 8) {
+    float2 m[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m[u] = ab[(cb + max(n1 - u, 0)) * K + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (n1 - u < 0) break;
+      carry[(cb + n1 - u) * K + i] = lam;
+      lam = m[u].x * lam + m[u].y;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void diag_gain_bwd_emit_v_kernel(
+    const float* __restrict__ k, const float* __restrict__ alpha, const float* __restrict__ omega,
+    const float* __restrict__ r, const float* __restrict__ dkappa, const float* __restrict__ p_prev,
+    const float* __restrict__ Dsave, const float* __restrict__ Gsave, const float* __restrict__ carry,
+    const bf16_t* __restrict__ omega_raw, const bf16_t* __restrict__ r_raw, const float* __restrict__ prec0,
+    int prec_mode, int B, int T, int H, int K, int NT, float s, float* __restrict__ dk, float* __restrict__ dalpha,
+    bf16_t* __restrict__ domega_raw, bf16_t* __restrict__ dr_raw, float* __restrict__ dprec_part) {
+  const GainTile g = gain_tile(B, T, H, K, NT);
+  if (!g.ok) return;
+  const int tpt = K / 8;
+  float lam[8];
+  ld8f(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, lam);
+  for (int t = g.t1 - 1; t >= g.t0; --t) {
+    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
+    float kt[8], al[8], wt[8], pv[8], dk_[8], oraw[8], dko[8], dao[8], dwo[8];
+    ld8f(k + row * K + g.i0, kt);
+    ld8f(alpha + row * K + g.i0, al);
+    ld8f(omega + row * K + g.i0, wt);
+    ld8f(p_prev + row * K + g.i0, pv);
+    ld8f(dkappa + row * K + g.i0, dk_);
+    {
+      const uint4 w = *reinterpret_cast<const uint4*>(omega_raw + row * K + g.i0);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        oraw[2 * q] = __uint_as_float(ww[q] << 16);
+        oraw[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
+      }
+    }
+    const float D = Dsave[row], G = Gsave[row], rt = r[row], iD = 1.f / D, ir = 1.f / rt;
+    float urr = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a2 = al[j] * al[j];
+      const float ph = a2 * pv[j] + wt[j];
+      const float u = s * kt[j] * kt[j] * ir;
+      const float hh = 1.f + u * ph, ihh = 1.f / hh;
+      const float pnext = ph * ihh;
+      const float pbar = dk_[j] * kt[j] * iD - kt[j] * kt[j] * G * iD + lam[j] * ihh * ihh;
+      const float ubar = -lam[j] * pnext * pnext;
+      dko[j] = dk_[j] * ph * iD - 2.f * ph * kt[j] * G * iD + ubar * (2.f * s * kt[j] * ir);
+      dao[j] = 2.f * al[j] * pv[j] * pbar;
+      dwo[j] = pbar * sigmoidf(oraw[j]);
+      urr += ubar * (-s * kt[j] * kt[j] * ir * ir);
+      lam[j] = a2 * pbar;
+    }
+    st8f(dk + row * K + g.i0, dko);
+    st8f(dalpha + row * K + g.i0, dao);
+    {
+      uint32_t ww[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ww[q] = (uint32_t)f2bf(dwo[2 * q]) | ((uint32_t)f2bf(dwo[2 * q + 1]) << 16);
+      *reinterpret_cast<uint4*>(domega_raw + row * K + g.i0) = uint4{ww[0], ww[1], ww[2], ww[3]};
+    }
+    const float utot = tile_sum(urr, tpt);
+    if (g.sub == 0) dr_raw[row] = f2bf((-G * iD + utot) * sigmoidf(bf2f(r_raw[row])));
+  }
+  if (g.nt == 0 && dprec_part) {
+    // lam holds dL/dp_{-1}; p_{-1} = 1/c  ->  dL/dc = -lam p^2
+    float c8[8], part = 0.f;
+    if (prec_mode == 1) ld8f(prec0 + ((int64_t)g.b * H + g.h) * K + g.i0, c8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float c = prec_mode == 0 ? prec0[g.h] : c8[j];
+      const float p0 = 1.f / c;
+      c8[j] = -lam[j] * p0 * p0;
+      part += c8[j];
+    }
+    if (prec_mode == 1) {
+      st8f(dprec_part + ((int64_t)g.b * H + g.h) * K + g.i0, c8);
+    } else {
+      part = tile_sum(part, tpt);
+      if (g.sub == 0) dprec_part[(int64_t)g.b * H + g.h] = part;
+    }
+  }
+}
+
 // dprec[h] = sum_b part[b, h]
 __global__ void sum_over_batch_kernel(const float* __restrict__ part, int B, int H, float* __restrict__ out) {
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
@@ -533,6 +803,8 @@ __global__ void sum_over_batch_kernel(const float* __restrict__ part, int B, int
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 inline int gain_block(int K) { return ((K + 63) / 64) * 64; }
+inline bool gain_vec_ok(int K) { return K % 8 == 0 && 64 % (K / 8) == 0; }
+inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
@@ -605,6 +877,18 @@ int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, co
   float* maps = (float*)workspace;
   float* carry = maps + (int64_t)B * H * NT * K * 4;
   const int bs = gain_block(K);
+  if (gain_vec_ok(K) && aligned16(k) && aligned16(alpha) && aligned16(omega) && aligned16(kappa) &&
+      aligned16(p_prev) && (prec_mode == 0 || aligned16(initial_precision))) {
+    const int tiles = B * H * NT, tpb = 256 / (K / 8);
+    hipLaunchKernelGGL(diag_gain_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r, B, T,
+                       H, K, NT, info_scale, maps);
+    hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)maps,
+                       initial_precision, prec_mode, H, K, NT, carry, final_precision);
+    hipLaunchKernelGGL(diag_gain_emit_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
+                       carry, B, T, H, K, NT, info_scale, kappa, p_prev, D);
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
   hipLaunchKernelGGL(diag_gain_map_kernel, dim3(NT, B * H), dim3(bs), 0, stream, k, alpha, omega, r, T, H, K, NT,
                      info_scale, maps);
   hipLaunchKernelGGL(diag_gain_carry_kernel, dim3(B * H), dim3(bs), 0, stream, maps, initial_precision, prec_mode, H, K,
@@ -629,14 +913,27 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
   float* carry = ab + (int64_t)B * H * NT * K * 4;   // [B,H,NT,K]
   float* dpart = carry + (int64_t)B * H * NT * K;    // [B,H] or [B,H,K]
   const int bs = gain_block(K);
-  hipLaunchKernelGGL(diag_gain_bwd_map_kernel, dim3(NT, B * H), dim3(bs), 0, stream, k, alpha, omega, r, dkappa, p_prev,
-                     D, T, H, K, NT, info_scale, ab, G_scratch);
-  hipLaunchKernelGGL(diag_gain_bwd_carry_kernel, dim3(B * H), dim3(bs), 0, stream, ab, d_final_precision,
-                     final_precision, H, K, NT, carry);
   float* dpart_out = d_initial_precision ? (prec_mode == 1 ? d_initial_precision : dpart) : nullptr;
-  hipLaunchKernelGGL(diag_gain_bwd_emit_kernel, dim3(NT, B * H), dim3(bs), 0, stream, k, alpha, omega, r, dkappa,
-                     p_prev, D, G_scratch, carry, omega_raw, r_raw, initial_precision, prec_mode, T, H, K, NT,
-                     info_scale, dk, dalpha, domega_raw, dr_raw, dpart_out);
+  if (gain_vec_ok(K) && aligned16(k) && aligned16(alpha) && aligned16(omega) && aligned16(dkappa) &&
+      aligned16(p_prev) && aligned16(omega_raw) && aligned16(dk) && aligned16(dalpha) && aligned16(domega_raw) &&
+      (prec_mode == 0 || (aligned16(initial_precision) && aligned16(dpart_out)))) {
+    const int tiles = B * H * NT, tpb = 256 / (K / 8);
+    hipLaunchKernelGGL(diag_gain_bwd_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
+                       dkappa, p_prev, D, B, T, H, K, NT, info_scale, ab, G_scratch);
+    hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)ab,
+                       d_final_precision, final_precision, H, K, NT, carry);
+    hipLaunchKernelGGL(diag_gain_bwd_emit_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
+                       dkappa, p_prev, D, G_scratch, carry, omega_raw, r_raw, initial_precision, prec_mode, B, T, H, K,
+                       NT, info_scale, dk, dalpha, domega_raw, dr_raw, dpart_out);
+  } else {
+    hipLaunchKernelGGL(diag_gain_bwd_map_kernel, dim3(NT, B * H), dim3(bs), 0, stream, k, alpha, omega, r, dkappa,
+                       p_prev, D, T, H, K, NT, info_scale, ab, G_scratch);
+    hipLaunchKernelGGL(diag_gain_bwd_carry_kernel, dim3(B * H), dim3(bs), 0, stream, ab, d_final_precision,
+                       final_precision, H, K, NT, carry);
+    hipLaunchKernelGGL(diag_gain_bwd_emit_kernel, dim3(NT, B * H), dim3(bs), 0, stream, k, alpha, omega, r, dkappa,
+                       p_prev, D, G_scratch, carry, omega_raw, r_raw, initial_precision, prec_mode, T, H, K, NT,
+                       info_scale, dk, dalpha, domega_raw, dr_raw, dpart_out);
+  }
   if (d_initial_precision && prec_mode == 0)
     hipLaunchKernelGGL(sum_over_batch_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, dpart, B, H,
                        d_initial_precision);
