@@ -540,6 +540,10 @@ __device__ __forceinline__ float tile_sum(float x, int tpt) {
   for (int o = 1; o < tpt; o <<= 1) x += __shfl_xor(x, o, 64);
   return x;
 }
+// Vectorised path: one tile = (b, h, 16-token chunk) x K channels, K/8 threads per tile, 8 channels
+// per thread.  Short chunks give B*H*T/16 * K/8 threads (enough waves to cover load latency on
+// every CU); each thread issues the loads of NB tokens before it computes on them.
+constexpr int kVecChunk = 16;
 struct GainTile {
   int b, h, nt, i0, sub, t0, t1;
   bool ok;
@@ -556,31 +560,43 @@ __device__ __forceinline__ GainTile gain_tile(int B, int T, int H, int K, int NT
   g.b = (int)(bn / NT);
   g.sub = threadIdx.x % tpt;
   g.i0 = 8 * g.sub;
-  g.t0 = g.nt * kGainChunk;
-  g.t1 = min(g.t0 + kGainChunk, T);
+  g.t0 = g.nt * kVecChunk;
+  g.t1 = min(g.t0 + kVecChunk, T);
   return g;
+}
+__device__ __forceinline__ int64_t gain_row(const GainTile& g, int T, int H, int t) {
+  return ((int64_t)g.b * T + t) * H + g.h;
 }
 
 __global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __restrict__ k, const float* __restrict__ alpha,
                                                               const float* __restrict__ omega, const float* __restrict__ r,
                                                               int B, int T, int H, int K, int NT, float s,
                                                               float* __restrict__ maps) {
+  constexpr int NB = 4;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
   Map2 M[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) M[j] = Map2{1.f, 0.f, 0.f, 1.f};
-  for (int t = g.t0; t < g.t1; ++t) {
-    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
-    float kt[8], al[8], wt[8];
-    ld8f(k + row * K + g.i0, kt);
-    ld8f(alpha + row * K + g.i0, al);
-    ld8f(omega + row * K + g.i0, wt);
-    const float ir = 1.f / r[row];
+  for (int t = g.t0; t < g.t1; t += NB) {
+    float kt[NB][8], al[NB][8], wt[NB][8], ir[NB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float a2 = al[j] * al[j], u = s * kt[j] * kt[j] * ir;
-      M[j] = map_mul(Map2{a2, wt[j], u * a2, 1.f + u * wt[j]}, M[j]);
+    for (int u = 0; u < NB; ++u) {
+      const int64_t row = gain_row(g, T, H, min(t + u, g.t1 - 1));
+      ld8f(k + row * K + g.i0, kt[u]);
+      ld8f(alpha + row * K + g.i0, al[u]);
+      ld8f(omega + row * K + g.i0, wt[u]);
+      ir[u] = r[row];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (t + u >= g.t1) break;
+      const float iru = 1.f / ir[u];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a2 = al[u][j] * al[u][j], uu = s * kt[u][j] * kt[u][j] * iru;
+        M[j] = map_mul(Map2{a2, wt[u][j], uu * a2, 1.f + uu * wt[u][j]}, M[j]);
+      }
     }
   }
   float4* dst = reinterpret_cast<float4*>(maps + ((((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0) * 4);
@@ -588,7 +604,8 @@ __global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __res
   for (int j = 0; j < 8; ++j) dst[j] = float4{M[j].m0, M[j].m1, M[j].m2, M[j].m3};
 }
 
-// grid (B*H), block K: per channel, maps of 8 chunks loaded at a time.
+// grid (B*H), block K: per channel, the chunk maps in groups of 8 with the next group's loads in
+// flight while the current group is applied.
 __global__ __launch_bounds__(256) void diag_gain_carry_v_kernel(const float4* __restrict__ maps,
                                                                 const float* __restrict__ prec0, int prec_mode, int H,
                                                                 int K, int NT, float* __restrict__ carry,
@@ -597,16 +614,20 @@ __global__ __launch_bounds__(256) void diag_gain_carry_v_kernel(const float4* __
   if (i >= K) return;
   float p = 1.f / (prec_mode == 0 ? prec0[h] : prec0[((int64_t)b * H + h) * K + i]);
   const int64_t cb = (int64_t)bh * NT;
-  for (int n0 = 0; n0 < NT; n0 += 8) {
-    float4 m[8];
+  float4 cur[8], nxt[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) m[u] = maps[(cb + min(n0 + u, NT - 1)) * K + i];
+  for (int u = 0; u < 8; ++u) cur[u] = maps[(cb + min(u, NT - 1)) * K + i];
+  for (int n0 = 0; n0 < NT; n0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) nxt[u] = maps[(cb + min(n0 + 8 + u, NT - 1)) * K + i];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (n0 + u >= NT) break;
       carry[(cb + n0 + u) * K + i] = p;
-      p = (m[u].x * p + m[u].y) / (m[u].z * p + m[u].w);
+      p = (cur[u].x * p + cur[u].y) / (cur[u].z * p + cur[u].w);
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
   }
   if (final_prec) final_prec[((int64_t)b * H + h) * K + i] = 1.f / p;
 }
@@ -617,33 +638,42 @@ __global__ __launch_bounds__(256) void diag_gain_emit_v_kernel(const float* __re
                                                                const float* __restrict__ carry, int B, int T, int H,
                                                                int K, int NT, float s, float* __restrict__ kappa,
                                                                float* __restrict__ p_prev, float* __restrict__ Dsave) {
+  constexpr int NB = 4;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
   const int tpt = K / 8;
   float p[8];
   ld8f(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, p);
-  for (int t = g.t0; t < g.t1; ++t) {
-    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
-    float kt[8], al[8], wt[8], pp[8], num[8];
-    ld8f(k + row * K + g.i0, kt);
-    ld8f(alpha + row * K + g.i0, al);
-    ld8f(omega + row * K + g.i0, wt);
-    const float rt = r[row], ir = 1.f / rt;
-    float sq = 0.f;
+  for (int t = g.t0; t < g.t1; t += NB) {
+    float kt[NB][8], al[NB][8], wt[NB][8], rt[NB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float ph = al[j] * al[j] * p[j] + wt[j];
-      pp[j] = p[j];
-      num[j] = ph * kt[j];
-      sq += num[j] * kt[j];
-      p[j] = ph / (1.f + s * kt[j] * kt[j] * ir * ph);
+    for (int u = 0; u < NB; ++u) {
+      const int64_t row = gain_row(g, T, H, min(t + u, g.t1 - 1));
+      ld8f(k + row * K + g.i0, kt[u]);
+      ld8f(alpha + row * K + g.i0, al[u]);
+      ld8f(omega + row * K + g.i0, wt[u]);
+      rt[u] = r[row];
     }
-    if (p_prev) st8f(p_prev + row * K + g.i0, pp);
-    const float D = rt + tile_sum(sq, tpt), iD = 1.f / D;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) num[j] *= iD;
-    st8f(kappa + row * K + g.i0, num);
-    if (Dsave && g.sub == 0) Dsave[row] = D;
+    for (int u = 0; u < NB; ++u) {
+      if (t + u >= g.t1) break;
+      const int64_t row = gain_row(g, T, H, t + u);
+      const float ir = 1.f / rt[u];
+      float num[8], sq = 0.f;
+      if (p_prev) st8f(p_prev + row * K + g.i0, p);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ph = al[u][j] * al[u][j] * p[j] + wt[u][j];
+        num[j] = ph * kt[u][j];
+        sq += num[j] * kt[u][j];
+        p[j] = ph / (1.f + s * kt[u][j] * kt[u][j] * ir * ph);
+      }
+      const float D = rt[u] + tile_sum(sq, tpt), iD = 1.f / D;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) num[j] *= iD;
+      st8f(kappa + row * K + g.i0, num);
+      if (Dsave && g.sub == 0) Dsave[row] = D;
+    }
   }
 }
 
@@ -652,38 +682,48 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_map_v_kernel(
     const float* __restrict__ r, const float* __restrict__ dkappa, const float* __restrict__ p_prev,
     const float* __restrict__ Dsave, int B, int T, int H, int K, int NT, float s, float* __restrict__ ab,
     float* __restrict__ Gsave) {
+  constexpr int NB = 2;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
   const int tpt = K / 8;
   float Aacc[8], Bacc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f;
-  for (int t = g.t1 - 1; t >= g.t0; --t) {
-    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
-    float kt[8], al[8], wt[8], pv[8], dk_[8], ph[8];
-    ld8f(k + row * K + g.i0, kt);
-    ld8f(alpha + row * K + g.i0, al);
-    ld8f(omega + row * K + g.i0, wt);
-    ld8f(p_prev + row * K + g.i0, pv);
-    ld8f(dkappa + row * K + g.i0, dk_);
-    const float D = Dsave[row], iD = 1.f / D, ir = 1.f / r[row];
-    float gp = 0.f;
+  for (int t = g.t1 - 1; t >= g.t0; t -= NB) {
+    float kt[NB][8], al[NB][8], wt[NB][8], pv[NB][8], dk_[NB][8], Dv[NB], rv[NB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      ph[j] = al[j] * al[j] * pv[j] + wt[j];
-      gp += dk_[j] * ph[j] * kt[j];
+    for (int u = 0; u < NB; ++u) {
+      const int64_t row = gain_row(g, T, H, max(t - u, g.t0));
+      ld8f(k + row * K + g.i0, kt[u]);
+      ld8f(alpha + row * K + g.i0, al[u]);
+      ld8f(omega + row * K + g.i0, wt[u]);
+      ld8f(p_prev + row * K + g.i0, pv[u]);
+      ld8f(dkappa + row * K + g.i0, dk_[u]);
+      Dv[u] = Dsave[row];
+      rv[u] = r[row];
     }
-    const float G = tile_sum(gp, tpt) * iD;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float a2 = al[j] * al[j];
-      const float hh = 1.f + s * kt[j] * kt[j] * ir * ph[j];
-      const float pbar = dk_[j] * kt[j] * iD - kt[j] * kt[j] * G * iD;
-      const float At = a2 / (hh * hh);
-      Bacc[j] = At * Bacc[j] + a2 * pbar;
-      Aacc[j] = At * Aacc[j];
+    for (int u = 0; u < NB; ++u) {
+      if (t - u < g.t0) break;
+      const float iD = 1.f / Dv[u], ir = 1.f / rv[u];
+      float ph[8], gp = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ph[j] = al[u][j] * al[u][j] * pv[u][j] + wt[u][j];
+        gp += dk_[u][j] * ph[j] * kt[u][j];
+      }
+      const float G = tile_sum(gp, tpt) * iD;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float a2 = al[u][j] * al[u][j];
+        const float hh = 1.f + s * kt[u][j] * kt[u][j] * ir * ph[j];
+        const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD;
+        const float At = a2 / (hh * hh);
+        Bacc[j] = At * Bacc[j] + a2 * pbar;
+        Aacc[j] = At * Aacc[j];
+      }
+      if (Gsave && g.sub == 0) Gsave[gain_row(g, T, H, t - u)] = G;
     }
-    if (Gsave && g.sub == 0) Gsave[row] = G;
   }
   float4* dst = reinterpret_cast<float4*>(ab + ((((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0) * 2);
 #pragma unroll
@@ -702,16 +742,20 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_carry_v_kernel(const float2
     lam = -d_final_prec[(int64_t)bh * K + i] * c * c;
   }
   const int64_t cb = (int64_t)bh * NT;
-  for (int n1 = NT - 1; n1 >= 0; n1 -= 8) {
-    float2 m[8];
+  float2 cur[8], nxt[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) m[u] = ab[(cb + max(n1 - u, 0)) * K + i];
+  for (int u = 0; u < 8; ++u) cur[u] = ab[(cb + max(NT - 1 - u, 0)) * K + i];
+  for (int n1 = NT - 1; n1 >= 0; n1 -= 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) nxt[u] = ab[(cb + max(n1 - 8 - u, 0)) * K + i];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (n1 - u < 0) break;
       carry[(cb + n1 - u) * K + i] = lam;
-      lam = m[u].x * lam + m[u].y;
+      lam = cur[u].x * lam + cur[u].y;
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
   }
 }
 
@@ -722,55 +766,67 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_emit_v_kernel(
     const bf16_t* __restrict__ omega_raw, const bf16_t* __restrict__ r_raw, const float* __restrict__ prec0,
     int prec_mode, int B, int T, int H, int K, int NT, float s, float* __restrict__ dk, float* __restrict__ dalpha,
     bf16_t* __restrict__ domega_raw, bf16_t* __restrict__ dr_raw, float* __restrict__ dprec_part) {
+  constexpr int NB = 2;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
   const int tpt = K / 8;
   float lam[8];
   ld8f(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, lam);
-  for (int t = g.t1 - 1; t >= g.t0; --t) {
-    const int64_t row = ((int64_t)g.b * T + t) * H + g.h;
-    float kt[8], al[8], wt[8], pv[8], dk_[8], oraw[8], dko[8], dao[8], dwo[8];
-    ld8f(k + row * K + g.i0, kt);
-    ld8f(alpha + row * K + g.i0, al);
-    ld8f(omega + row * K + g.i0, wt);
-    ld8f(p_prev + row * K + g.i0, pv);
-    ld8f(dkappa + row * K + g.i0, dk_);
-    {
-      const uint4 w = *reinterpret_cast<const uint4*>(omega_raw + row * K + g.i0);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  for (int t = g.t1 - 1; t >= g.t0; t -= NB) {
+    float kt[NB][8], al[NB][8], wt[NB][8], pv[NB][8], dk_[NB][8], Dv[NB], Gv[NB], rv[NB];
+    uint4 ow[NB];
+    bf16_t rr[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t row = gain_row(g, T, H, max(t - u, g.t0));
+      ld8f(k + row * K + g.i0, kt[u]);
+      ld8f(alpha + row * K + g.i0, al[u]);
+      ld8f(omega + row * K + g.i0, wt[u]);
+      ld8f(p_prev + row * K + g.i0, pv[u]);
+      ld8f(dkappa + row * K + g.i0, dk_[u]);
+      ow[u] = *reinterpret_cast<const uint4*>(omega_raw + row * K + g.i0);
+      Dv[u] = Dsave[row];
+      Gv[u] = Gsave[row];
+      rv[u] = r[row];
+      rr[u] = r_raw[row];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (t - u < g.t0) break;
+      const int64_t row = gain_row(g, T, H, t - u);
+      float oraw[8], dko[8], dao[8], dwo[8];
+      const uint32_t ww[4] = {ow[u].x, ow[u].y, ow[u].z, ow[u].w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         oraw[2 * q] = __uint_as_float(ww[q] << 16);
         oraw[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
       }
-    }
-    const float D = Dsave[row], G = Gsave[row], rt = r[row], iD = 1.f / D, ir = 1.f / rt;
-    float urr = 0.f;
+      const float G = Gv[u], iD = 1.f / Dv[u], ir = 1.f / rv[u];
+      float urr = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float a2 = al[j] * al[j];
-      const float ph = a2 * pv[j] + wt[j];
-      const float u = s * kt[j] * kt[j] * ir;
-      const float hh = 1.f + u * ph, ihh = 1.f / hh;
-      const float pnext = ph * ihh;
-      const float pbar = dk_[j] * kt[j] * iD - kt[j] * kt[j] * G * iD + lam[j] * ihh * ihh;
-      const float ubar = -lam[j] * pnext * pnext;
-      dko[j] = dk_[j] * ph * iD - 2.f * ph * kt[j] * G * iD + ubar * (2.f * s * kt[j] * ir);
-      dao[j] = 2.f * al[j] * pv[j] * pbar;
-      dwo[j] = pbar * sigmoidf(oraw[j]);
-      urr += ubar * (-s * kt[j] * kt[j] * ir * ir);
-      lam[j] = a2 * pbar;
-    }
-    st8f(dk + row * K + g.i0, dko);
-    st8f(dalpha + row * K + g.i0, dao);
-    {
-      uint32_t ww[4];
+      for (int j = 0; j < 8; ++j) {
+        const float a2 = al[u][j] * al[u][j];
+        const float ph = a2 * pv[u][j] + wt[u][j];
+        const float uu = s * kt[u][j] * kt[u][j] * ir;
+        const float hh = 1.f + uu * ph, ihh = 1.f / hh;
+        const float pnext = ph * ihh;
+        const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD + lam[j] * ihh * ihh;
+        const float ubar = -lam[j] * pnext * pnext;
+        dko[j] = dk_[u][j] * ph * iD - 2.f * ph * kt[u][j] * G * iD + ubar * (2.f * s * kt[u][j] * ir);
+        dao[j] = 2.f * al[u][j] * pv[u][j] * pbar;
+        dwo[j] = pbar * sigmoidf(oraw[j]);
+        urr += ubar * (-s * kt[u][j] * kt[u][j] * ir * ir);
+        lam[j] = a2 * pbar;
+      }
+      st8f(dk + row * K + g.i0, dko);
+      st8f(dalpha + row * K + g.i0, dao);
+      uint32_t wo[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ww[q] = (uint32_t)f2bf(dwo[2 * q]) | ((uint32_t)f2bf(dwo[2 * q + 1]) << 16);
-      *reinterpret_cast<uint4*>(domega_raw + row * K + g.i0) = uint4{ww[0], ww[1], ww[2], ww[3]};
+      for (int q = 0; q < 4; ++q) wo[q] = (uint32_t)f2bf(dwo[2 * q]) | ((uint32_t)f2bf(dwo[2 * q + 1]) << 16);
+      *reinterpret_cast<uint4*>(domega_raw + row * K + g.i0) = uint4{wo[0], wo[1], wo[2], wo[3]};
+      const float utot = tile_sum(urr, tpt);
+      if (g.sub == 0) dr_raw[row] = f2bf((-G * iD + utot) * sigmoidf(bf2f(rr[u])));
     }
-    const float utot = tile_sum(urr, tpt);
-    if (g.sub == 0) dr_raw[row] = f2bf((-G * iD + utot) * sigmoidf(bf2f(r_raw[row])));
   }
   if (g.nt == 0 && dprec_part) {
     // lam holds dL/dp_{-1}; p_{-1} = 1/c  ->  dL/dc = -lam p^2
@@ -862,7 +918,7 @@ int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const f
 }
 
 size_t kdn_diag_gain_workspace_size(int B, int T, int H, int K) {
-  const int64_t NT = cdiv(T, kGainChunk);
+  const int64_t NT = cdiv(T, kVecChunk);  // covers both chunkings (kVecChunk <= kGainChunk)
   // maps (4) + carry (1) per (b, h, chunk, channel), plus [B,H,K] precision partials
   return (size_t)((int64_t)B * H * NT * K * 5 + (int64_t)B * H * K) * sizeof(float);
 }
@@ -879,13 +935,14 @@ int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, co
   const int bs = gain_block(K);
   if (gain_vec_ok(K) && aligned16(k) && aligned16(alpha) && aligned16(omega) && aligned16(kappa) &&
       aligned16(p_prev) && (prec_mode == 0 || aligned16(initial_precision))) {
-    const int tiles = B * H * NT, tpb = 256 / (K / 8);
+    const int NV = cdiv(T, kVecChunk), tiles = B * H * NV, tpb = 256 / (K / 8);
+    float* carry_v = maps + (int64_t)B * H * NV * K * 4;
     hipLaunchKernelGGL(diag_gain_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r, B, T,
-                       H, K, NT, info_scale, maps);
+                       H, K, NV, info_scale, maps);
     hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)maps,
-                       initial_precision, prec_mode, H, K, NT, carry, final_precision);
+                       initial_precision, prec_mode, H, K, NV, carry_v, final_precision);
     hipLaunchKernelGGL(diag_gain_emit_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
-                       carry, B, T, H, K, NT, info_scale, kappa, p_prev, D);
+                       carry_v, B, T, H, K, NV, info_scale, kappa, p_prev, D);
     KDN_CHECK_LAUNCH();
     return 0;
   }
@@ -917,14 +974,18 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
   if (gain_vec_ok(K) && aligned16(k) && aligned16(alpha) && aligned16(omega) && aligned16(dkappa) &&
       aligned16(p_prev) && aligned16(omega_raw) && aligned16(dk) && aligned16(dalpha) && aligned16(domega_raw) &&
       (prec_mode == 0 || (aligned16(initial_precision) && aligned16(dpart_out)))) {
-    const int tiles = B * H * NT, tpb = 256 / (K / 8);
+    const int NV = cdiv(T, kVecChunk), tiles = B * H * NV, tpb = 256 / (K / 8);
+    float* carry_v = ab + (int64_t)B * H * NV * K * 4;
+    float* dpart_v = carry_v + (int64_t)B * H * NV * K;
+    float* dpart_out_v = d_initial_precision ? (prec_mode == 1 ? d_initial_precision : dpart_v) : nullptr;
+    dpart = dpart_v;
     hipLaunchKernelGGL(diag_gain_bwd_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
-                       dkappa, p_prev, D, B, T, H, K, NT, info_scale, ab, G_scratch);
+                       dkappa, p_prev, D, B, T, H, K, NV, info_scale, ab, G_scratch);
     hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)ab,
-                       d_final_precision, final_precision, H, K, NT, carry);
+                       d_final_precision, final_precision, H, K, NV, carry_v);
     hipLaunchKernelGGL(diag_gain_bwd_emit_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
-                       dkappa, p_prev, D, G_scratch, carry, omega_raw, r_raw, initial_precision, prec_mode, B, T, H, K,
-                       NT, info_scale, dk, dalpha, domega_raw, dr_raw, dpart_out);
+                       dkappa, p_prev, D, G_scratch, carry_v, omega_raw, r_raw, initial_precision, prec_mode, B, T, H,
+                       K, NV, info_scale, dk, dalpha, domega_raw, dr_raw, dpart_out_v);
   } else {
     hipLaunchKernelGGL(diag_gain_bwd_map_kernel, dim3(NT, B * H), dim3(bs), 0, stream, k, alpha, omega, r, dkappa,
                        p_prev, D, T, H, K, NT, info_scale, ab, G_scratch);
