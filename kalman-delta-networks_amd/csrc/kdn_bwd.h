@@ -394,17 +394,20 @@ __global__ __launch_bounds__(256, 1) void contrib_kernel(
     // ---- loads in two batches (factor inputs, then gradient inputs) so the wave waits for memory
     // twice per channel tile instead of once per row; rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j
     float kv[16], qv[16], av[16], Gv[16], dkg[16], dqg[16], dkf[16];
+    uint16_t kraw[16], qraw[16];
     const float g0 = buf_ld(rG, i * 4), gl = buf_ld(rG, ((uint32_t)((L - 1) * H) * K + i) * 4);
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
       const int c = 16 * (p >> 2) + 4 * g4 + (p & 3);
       const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
-      kv[p] = buf_ld_bf16(rk, o * 2);
-      qv[p] = buf_ld_bf16(rq, o * 2);
+      kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
+      qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
       av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);  // iso: beta of the row
       Gv[p] = buf_ld(rG, o * 4);
     }
-    __builtin_amdgcn_sched_barrier(0);  // keep the batch together
+    __builtin_amdgcn_sched_barrier(0);  // keep the batch together (raw bf16 held until every load is out)
+#pragma unroll
+    for (int p = 0; p < 16; ++p) kv[p] = bf2f(kraw[p]), qv[p] = bf2f(qraw[p]);
     // factors at this lane's positions, as permuted-k B fragments per 32-row block
     uint4 Rh[2], Rl[2], Kh[2], Kl[2], Qh[2], Ql[2];
 #pragma unroll

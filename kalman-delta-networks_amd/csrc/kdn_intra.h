@@ -15,6 +15,7 @@
 // Lk / Lq fragments in registers and publishing its R fragments to LDS; the U / W products
 // are split over the waves by output column tile.  LDS ~49 KB: three workgroups per CU.
 #pragma once
+#include <type_traits>
 #include "kdn_common.h"
 #include "kdn_state.h"
 
@@ -245,24 +246,34 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
       const float x[8] = {row[0], row[1], row[2], row[3], row[16], row[17], row[18], row[19]};
       split8(x, ah[I][kb], al[I][kb]);
     }
-  constexpr int NCT = (V + K) / 16;
-  for (int t = w; t < NCT; t += 4) {
-    const bool isU = t < V / 16;
-    const int col = 16 * (isU ? t : t - V / 16) + r16;
+  // U = A V (column tiles of V, exact bf16 B operand) and W = A Kg (Kg = k 2^G, split): each tile's
+  // 16 loads go out together, separate loops keep the tile kind uniform at compile time.
+  auto tile = [&](auto is_u, int t) {
+    constexpr bool isU = decltype(is_u)::value;
+    const int col = 16 * t + r16;
+    uint16_t raw[16];
+    float gv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int kb = q >> 3, sl = q & 7;
+      const int s = 32 * kb + (sl < 4 ? 4 * g4 + sl : 16 + 4 * g4 + sl - 4);
+      const uint32_t srow = (uint32_t)(s * H);
+      if constexpr (isU) {
+        raw[q] = __builtin_amdgcn_raw_buffer_load_b16(rv, (srow * V + col) * 2, 0, 0);
+      } else {
+        raw[q] = __builtin_amdgcn_raw_buffer_load_b16(rk, (srow * K + col) * 2, 0, 0);
+        gv[q] = buf_ld(rG, (srow * K + col) * 4);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     uint4 bh_[2], bl_[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       float x[8];
 #pragma unroll
       for (int sl = 0; sl < 8; ++sl) {
-        const int s = 32 * kb + (sl < 4 ? 4 * g4 + sl : 16 + 4 * g4 + sl - 4);
-        const uint32_t srow = (uint32_t)(s * H);
-        if (isU) {
-          x[sl] = buf_ld_bf16(rv, (srow * V + col) * 2);
-        } else {
-          const float kk = buf_ld_bf16(rk, (srow * K + col) * 2);
-          x[sl] = kk * exp2f(buf_ld(rG, (srow * K + col) * 4));
-        }
+        const int q = 8 * kb + sl;
+        x[sl] = isU ? bf2f(raw[q]) : bf2f(raw[q]) * exp2f(gv[q]);
       }
       split8(x, bh_[kb], bl_[kb]);  // exact for V (lo = 0)
     }
@@ -274,11 +285,13 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int cc = 16 * I + 4 * g4 + j;
-        if (isU) buf_st(rU, (cc * V + col) * 4, acc[j]);
+        if constexpr (isU) buf_st(rU, (cc * V + col) * 4, acc[j]);
         else buf_st(rW, (cc * K + col) * 4, acc[j]);
       }
     }
-  }
+  };
+  for (int t = w; t < V / 16; t += 4) tile(std::true_type{}, t);
+  for (int t = w; t < K / 16; t += 4) tile(std::false_type{}, t);
 }
 
 }  // namespace kdn_intra

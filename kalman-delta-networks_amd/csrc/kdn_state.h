@@ -168,7 +168,10 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) rU[cb][j] = buf_ld(ru, ((16 * cb + 4 * g4 + j) * V + col) * 4);
-    if (tid < K) rE = exp2f(gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid]);
+    {  // raw g_last of the chunk; the exponential is taken when staging, so no wait sits here
+      const bufrsrc rg = make_buf(gc + row_bthk(b, t0 + L - 1, h, T, H, K), K * 4);  // lanes >= K read 0
+      rE = buf_ld(rg, tid * 4);
+    }
     const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][s] row-major
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
@@ -190,7 +193,7 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + 256 * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
 #pragma unroll
     for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + 256 * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
-    if (tid < K) sE[tid] = rE;
+    if (tid < K) sE[tid] = exp2f(rE);
   };
 
   f32x4 S[ST];
@@ -370,7 +373,10 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) rO[cb][j] = buf_ldt<TDO>(ro, (16 * cb + 4 * g4 + j) * H * V + col);
-    if (tid < K) rE = exp2f(gc[row_bthk(b, t0 + L - 1, h, T, H, K) + tid]);
+    {  // raw g_last of the chunk; the exponential is taken when staging, so no wait sits here
+      const bufrsrc rg = make_buf(gc + row_bthk(b, t0 + L - 1, h, T, H, K), K * 4);  // lanes >= K read 0
+      rE = buf_ld(rg, tid * 4);
+    }
   };
   auto stage_p1 = [&]() {
 #pragma unroll
@@ -386,7 +392,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
       put_unit(sQ, off, rQ[u][0], rQ[u][1], rQ[u][2], rQ[u][3]);
       put_unit(sWt, off, rWt[u][0], rWt[u][1], rWt[u][2], rWt[u][3]);
     }
-    if (tid < K) sE[tid] = rE;
+    if (tid < K) sE[tid] = exp2f(rE);
   };
 
   f32x4 dS[ST];
