@@ -97,6 +97,19 @@ __device__ __forceinline__ void afrag(const bf16_t* buf, int tile, int lane, uin
   lo = *reinterpret_cast<const uint4*>(buf + tile * TILE + 512 + lane * 8);
 }
 
+// A sequence of NS fragment-read + MFMA steps with the reads issued LA steps ahead, so the
+// LDS latency of step s+LA overlaps the MFMAs of step s.  rd(s, hi, lo) reads step s's A
+// fragment; mm(s, hi, lo) issues its MFMAs.  Both are fully unrolled (s is a constant).
+template <int NS, int LA, typename Rd, typename Mm>
+__device__ __forceinline__ void mfma_pipe(Rd rd, Mm mm) {
+  uint4 fh[NS], fl[NS];
+#pragma unroll
+  for (int s = 0; s < NS + LA; ++s) {
+    if (s < NS) rd(s, fh[s], fl[s]);
+    if (s >= LA) mm(s - LA, fh[s - LA], fl[s - LA]);
+  }
+}
+
 // Block -> (bh, V-slice): the NV slices of one (b, h) go to one XCD (dispatch is round-robin
 // over the 8 XCDs), when B*H is a multiple of 8.
 __device__ __forceinline__ void xcd_map(int lin, int NV, int BH, int& bh, int& vs) {
@@ -231,16 +244,14 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
       for (int kb = 0; kb < KB; ++kb) bfrag(S[2 * kb], S[2 * kb + 1], bh_[kb], bl_[kb]);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) D[cb] = O[cb] = zero4();
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          uint4 ah, al;
-          afrag(sW, cb * KB + kb, lane, ah, al);
-          D[cb] = mma3(ah, al, bh_[kb], bl_[kb], D[cb]);
-          afrag(sQ, cb * KB + kb, lane, ah, al);
-          O[cb] = mma3(ah, al, bh_[kb], bl_[kb], O[cb]);
-        }
+      // step s: kb = s / 8, cb = (s / 2) % 4, operand W (even s) or Qg (odd s)
+      mfma_pipe<8 * KB, 4>(
+          [&](int st, uint4& ah, uint4& al) { afrag((st & 1) ? sQ : sW, ((st >> 1) & 3) * KB + (st >> 3), lane, ah, al); },
+          [&](int st, const uint4& ah, const uint4& al) {
+            const int kb = st >> 3, cb = (st >> 1) & 3;
+            if (st & 1) O[cb] = mma3(ah, al, bh_[kb], bl_[kb], O[cb]);
+            else D[cb] = mma3(ah, al, bh_[kb], bl_[kb], D[cb]);
+          });
       const bufrsrc rd = make_buf(Dl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
@@ -267,24 +278,26 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
         const float4 e = *reinterpret_cast<const float4*>(sE + 16 * ib + 4 * g4);
         S[ib] = f32x4{e.x * S[ib][0], e.y * S[ib][1], e.z * S[ib][2], e.w * S[ib][3]};
       }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ib = 0; ib < ST; ++ib) {
-          uint4 ah, al;
-          afrag(sK, ib * 2 + kb, lane, ah, al);
-          S[ib] = mma3(ah, al, dh_[kb], dl_[kb], S[ib]);
-        }
-      // readout O = Qg h + M delta  (M[c][s] = 0 for s > c)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          if (kb == 1 && cb < 2) continue;
-          uint4 ah, al;
-          afrag(sM, cb * 2 + kb, lane, ah, al);
-          O[cb] = mma3(ah, al, dh_[kb], dl_[kb], O[cb]);
-        }
+      // steps 0 .. 2 ST-1: S[ib] += Kf^T delta (kb = s / ST, ib = s % ST); then the readout
+      // O = Qg h + M delta over the nonzero M tiles (cb, kb): (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
+      mfma_pipe<2 * ST + 6, 4>(
+          [&](int st, uint4& ah, uint4& al) {
+            if (st < 2 * ST) {
+              afrag(sK, (st % ST) * 2 + st / ST, lane, ah, al);
+            } else {
+              const int m = st - 2 * ST, cb = m < 4 ? m : m - 2, kb = m < 4 ? 0 : 1;
+              afrag(sM, cb * 2 + kb, lane, ah, al);
+            }
+          },
+          [&](int st, const uint4& ah, const uint4& al) {
+            if (st < 2 * ST) {
+              const int ib = st % ST, kb = st / ST;
+              S[ib] = mma3(ah, al, dh_[kb], dl_[kb], S[ib]);
+            } else {
+              const int m = st - 2 * ST, cb = m < 4 ? m : m - 2, kb = m < 4 ? 0 : 1;
+              O[cb] = mma3(ah, al, dh_[kb], dl_[kb], O[cb]);
+            }
+          });
       const bufrsrc ro = make_buf(out + row_bthk(b, t0, h, T, H, V), ((L - 1) * H + 1) * V * sizeof(TO));
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
@@ -432,23 +445,27 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
       for (int kb = 0; kb < KB; ++kb) bfrag(dS[2 * kb], dS[2 * kb + 1], bh_[kb], bl_[kb]);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) dD[cb] = zero4();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          if (kb == 0 && cb >= 2) continue;  // M^T[c'][c] = M[c][c'] = 0 for c < c'
-          uint4 ah, al;
-          afrag(sM, cb * 2 + kb, lane, ah, al);
-          dD[cb] = DO_BF16 ? mma2(ah, al, oh[kb], dD[cb]) : mma3(ah, al, oh[kb], ol[kb], dD[cb]);
-        }
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          uint4 ah, al;
-          afrag(sKn, cb * KB + kb, lane, ah, al);
-          dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
-        }
+      // steps 0..5: M^T dO over the nonzero tiles (cb, kb): (0,0) (1,0) (0,1) (1,1) (2,1) (3,1)
+      // (M^T[c'][c] = M[c][c'] = 0 for c < c'); then Kf dS (kb = m / 4, cb = m % 4)
+      mfma_pipe<6 + 4 * KB, 4>(
+          [&](int st, uint4& ah, uint4& al) {
+            if (st < 6) {
+              const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
+              afrag(sM, cb * 2 + kb, lane, ah, al);
+            } else {
+              const int m = st - 6;
+              afrag(sKn, (m & 3) * KB + (m >> 2), lane, ah, al);
+            }
+          },
+          [&](int st, const uint4& ah, const uint4& al) {
+            if (st < 6) {
+              const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
+              dD[cb] = DO_BF16 ? mma2(ah, al, oh[kb], dD[cb]) : mma3(ah, al, oh[kb], ol[kb], dD[cb]);
+            } else {
+              const int m = st - 6, cb = m & 3, kb = m >> 2;
+              dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
+            }
+          });
       const bufrsrc rd = make_buf(dDl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
@@ -471,16 +488,16 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
         const float4 e = *reinterpret_cast<const float4*>(sE + 16 * ib + 4 * g4);
         dS[ib] = f32x4{e.x * dS[ib][0], e.y * dS[ib][1], e.z * dS[ib][2], e.w * dS[ib][3]};
       }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ib = 0; ib < ST; ++ib) {
-          uint4 ah, al;
-          afrag(sQ, ib * 2 + kb, lane, ah, al);
-          dS[ib] = DO_BF16 ? mma2(ah, al, oh[kb], dS[ib]) : mma3(ah, al, oh[kb], ol[kb], dS[ib]);
-          afrag(sWt, ib * 2 + kb, lane, ah, al);
-          dS[ib] = mma3(ah, al, dh_[kb], dl_[kb], dS[ib]);
-        }
+      // step s: kb = s / (2 ST), ib = (s / 2) % ST, operand Qg^T (even s, B = dO) or W^T (odd s)
+      mfma_pipe<4 * ST, 4>(
+          [&](int st, uint4& ah, uint4& al) {
+            afrag((st & 1) ? sWt : sQ, ((st >> 1) % ST) * 2 + st / (2 * ST), lane, ah, al);
+          },
+          [&](int st, const uint4& ah, const uint4& al) {
+            const int kb = st / (2 * ST), ib = (st >> 1) % ST;
+            if (st & 1) dS[ib] = mma3(ah, al, dh_[kb], dl_[kb], dS[ib]);
+            else dS[ib] = DO_BF16 ? mma2(ah, al, oh[kb], dS[ib]) : mma3(ah, al, oh[kb], ol[kb], dS[ib]);
+          });
     }
     __syncthreads();
   }
