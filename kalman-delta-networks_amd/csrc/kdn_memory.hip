@@ -781,12 +781,12 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     KDN_CHECK_LAUNCH();
   }
   if (stages & 2) {  // state pass with the fused readout
-    const dim3 gs(B * H * (V / kdn_state::WG_COLS));
+    const dim3 gs(B * H * (V / kdn_state::state_cols(V))), bs(kdn_state::state_threads(V));
     if (o_bf16)
-      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t>), gs, dim3(256), 0, stream, U, W, Kf, Qg, M, gc,
+      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t>), gs, bs, 0, stream, U, W, Kf, Qg, M, gc,
                          h0, T, H, NT, B * H, hb, D, ht, (bf16_t*)o);
     else
-      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float>), gs, dim3(256), 0, stream, U, W, Kf, Qg, M, gc,
+      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float>), gs, bs, 0, stream, U, W, Kf, Qg, M, gc,
                          h0, T, H, NT, B * H, hb, D, ht, (float*)o);
     KDN_CHECK_LAUNCH();
   }
@@ -808,7 +808,8 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
   if (stages & 1) {
-    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO>), dim3(B * H * (V / kdn_state::WG_COLS)), dim3(256), 0, stream,
+    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO>), dim3(B * H * (V / kdn_state::state_cols(V))),
+                       dim3(kdn_state::state_threads(V)), 0, stream,
                        M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H, dh, dD, dh0);
     KDN_CHECK_LAUNCH();
   }

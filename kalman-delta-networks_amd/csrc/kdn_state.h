@@ -5,8 +5,8 @@
 //   backward (reverse):      dh_n = dS;  d delta = M^T dO + Kf dS;
 //                            dS <- e^{g_last} dS + Qg^T dO - W^T d delta
 //
-// Work split.  One workgroup (4 waves) per (b, h, 64-column slice of V); each wave owns 16
-// state columns and keeps them for the whole sequence as K/16 MFMA accumulator tiles.  The
+// Work split.  One workgroup per (b, h, 64-column slice of V), one wave per 16 state columns;
+// each wave keeps its columns for the whole sequence as K/16 MFMA accumulator tiles.  The
 // workgroups of one (b, h) are placed on one XCD so the chunk operands they both read are
 // shared through that XCD's L2.
 //
@@ -27,12 +27,17 @@
 //    of its buffer, the threads split the other phase's next operands (loaded into registers
 //    one phase earlier) into the other buffer: two barriers per chunk, loads one phase ahead.
 #pragma once
+#include <type_traits>
 #include "kdn_common.h"
 
 namespace kdn_state {
 
 constexpr int C = 64;
-constexpr int WG_COLS = 64;  // V columns per workgroup: 4 waves x 16
+// V columns per workgroup (16 per wave).  64 columns (4 waves) keeps twice as many CUs busy as
+// one 128-column workgroup per (b, h), which measures faster: the pass is bound by each CU's
+// chunk-operand throughput, not by the duplicated operand splitting.
+__host__ __device__ constexpr int state_cols(int V) { return V < 64 ? V : 64; }
+__host__ __device__ constexpr int state_threads(int V) { return 4 * state_cols(V); }
 constexpr int TILE = 1024;   // bf16 elements of one 16 x 32 A tile (hi 512, lo 512)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -97,6 +102,18 @@ __device__ __forceinline__ void afrag(const bf16_t* buf, int tile, int lane, uin
   lo = *reinterpret_cast<const uint4*>(buf + tile * TILE + 512 + lane * 8);
 }
 
+// Stores of one lane's 4 D-layout values (rows r0 + j of a column) with one voffset: the row
+// block goes into the descriptor base (rows past the end stay range-checked) and the row j
+// into the instruction's immediate offset, so no per-element address registers are kept.
+__device__ __forceinline__ void st_rows4(bufrsrc r, uint32_t vbase, uint32_t row_bytes, const f32x4& x) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x[j]), r, vbase + j * row_bytes, 0, 0);
+}
+// Descriptor over rows [r0, L) of a row-major [rows][D] fp32 block at p (row stride D).
+__device__ __forceinline__ bufrsrc rows_from(const float* p, int r0, int L, int D) {
+  return make_buf(p + (int64_t)r0 * D, (uint32_t)(L > r0 ? (L - r0) * D * 4 : 0));
+}
+
 // A sequence of NS fragment-read + MFMA steps with the reads issued LA steps ahead, so the
 // LDS latency of step s+LA overlaps the MFMAs of step s.  rd(s, hi, lo) reads step s's A
 // fragment; mm(s, hi, lo) issues its MFMAs.  Both are fully unrolled (s is a constant).
@@ -129,20 +146,21 @@ __device__ __forceinline__ int64_t row_bthk(int b, int t, int h, int T, int H, i
 }
 
 // ===========================================================================
-// Forward state pass with the fused readout.  grid (B*H*V/64), block 256.  LDS 96.5 KB.
+// Forward state pass with the fused readout.  grid (B*H*V/COLS), block 4 COLS.  LDS 96.5 KB.
 // ===========================================================================
 template <int K, int V, typename TO>
-__global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
+__global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
                                                         const float* __restrict__ Kf, const float* __restrict__ Qg,
                                                         const float* __restrict__ Mg, const float* __restrict__ gc,
                                                         const float* __restrict__ h0, int T, int H, int NT, int BH,
                                                         float* __restrict__ hbuf, float* __restrict__ Dl,
                                                         float* __restrict__ ht, TO* __restrict__ out) {
-  constexpr int NV = V / WG_COLS;
+  constexpr int COLS = state_cols(V), NTHR = state_threads(V), NV = V / COLS;
   constexpr int KB = K / 32;           // k-blocks of a contraction over K
   constexpr int ST = K / 16;           // state row tiles per wave
-  constexpr int UN = C * K / 4 / 256;  // staging units per thread of a C x K operand
-  constexpr int UM = C * C / 4 / 256;  // ... of M
+  static_assert((C * K / 4) % NTHR == 0 && (C * C / 4) % NTHR == 0, "staging units per thread");
+  constexpr int UN = C * K / 4 / NTHR;  // staging units per thread of a C x K operand
+  constexpr int UM = C * C / 4 / NTHR;  // ... of M
   __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sQ[(C / 16) * KB * TILE];        // Qg: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
@@ -152,7 +170,7 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
   xcd_map(blockIdx.x, NV, BH, bh, vs);
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
-  const int col = vs * WG_COLS + 16 * w + (lane & 15);  // this lane's state column
+  const int col = vs * COLS + 16 * w + (lane & 15);  // this lane's state column
 
   float4 rW[UN], rQ[UN];
   float rK[UN][4], rM[UM][4], rU[4][4], rE = 0.f;
@@ -162,7 +180,7 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const Unit x = unit<K>(tid + 256 * u);
+      const Unit x = unit<K>(tid + NTHR * u);
       rW[u] = buf_ld4(rw, (x.row * K + x.k0) * 4);
       rQ[u] = buf_ld4(rq, (x.row * K + x.k0) * 4);
     }
@@ -173,7 +191,7 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     const bufrsrc ru = make_buf(U + row_bht(bh, t0, T, V), L * V * 4);
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const Unit x = unit<C>(tid + 256 * u);
+      const Unit x = unit<C>(tid + NTHR * u);
 #pragma unroll
       for (int j = 0; j < 4; ++j) rK[u][j] = buf_ld(rk, ((x.k0 + j) * K + x.row) * 4);
     }
@@ -188,7 +206,7 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
     const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][s] row-major
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
-      const Unit x = unit<C>(tid + 256 * u);
+      const Unit x = unit<C>(tid + NTHR * u);
       const float4 m = buf_ld4(rm, (x.row * C + x.k0) * 4);
       rM[u][0] = m.x, rM[u][1] = m.y, rM[u][2] = m.z, rM[u][3] = m.w;
     }
@@ -196,16 +214,16 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
   auto stage_W = [&]() {
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int off = unit<K>(tid + 256 * u).off;
+      const int off = unit<K>(tid + NTHR * u).off;
       put_unit(sW, off, rW[u].x, rW[u].y, rW[u].z, rW[u].w);
       put_unit(sQ, off, rQ[u].x, rQ[u].y, rQ[u].z, rQ[u].w);
     }
   };
   auto stage_K = [&]() {
 #pragma unroll
-    for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + 256 * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
+    for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + NTHR * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
 #pragma unroll
-    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + 256 * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
+    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + NTHR * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
     if (tid < K) sE[tid] = exp2f(rE);
   };
 
@@ -222,11 +240,9 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
   for (int n = 0; n < NT; ++n) {
     const int t0 = n * C, L = min(C, T - t0);
     {
-      const bufrsrc rh = make_buf(hbuf + ((int64_t)bh * NT + n) * K * V, K * V * 4);
+      const float* hb = hbuf + ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
-      for (int ib = 0; ib < ST; ++ib)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) buf_st(rh, ((16 * ib + 4 * g4 + j) * V + col) * 4, S[ib][j]);
+      for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, S[ib]);
     }
 
     // ---- phase 1: delta = U - W S   (reads sW; fills sK with chunk n; loads W of chunk n+1)
@@ -245,22 +261,20 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) D[cb] = O[cb] = zero4();
       // step s: kb = s / 8, cb = (s / 2) % 4, operand W (even s) or Qg (odd s)
-      mfma_pipe<8 * KB, 4>(
+      mfma_pipe<8 * KB, 2>(
           [&](int st, uint4& ah, uint4& al) { afrag((st & 1) ? sQ : sW, ((st >> 1) & 3) * KB + (st >> 3), lane, ah, al); },
           [&](int st, const uint4& ah, const uint4& al) {
             const int kb = st >> 3, cb = (st >> 1) & 3;
             if (st & 1) O[cb] = mma3(ah, al, bh_[kb], bl_[kb], O[cb]);
             else D[cb] = mma3(ah, al, bh_[kb], bl_[kb], D[cb]);
           });
-      const bufrsrc rd = make_buf(Dl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
+      const float* dl = Dl + row_bht(bh, t0, T, V);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
+      for (int cb = 0; cb < 4; ++cb) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float d = cU[cb][j] - D[cb][j];
-          D[cb][j] = d;
-          buf_st(rd, ((16 * cb + 4 * g4 + j) * V + col) * 4, d);
-        }
+        for (int j = 0; j < 4; ++j) D[cb][j] = cU[cb][j] - D[cb][j];
+        st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, D[cb]);  // rows past L dropped
+      }
     }
     __syncthreads();
 
@@ -280,7 +294,7 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
       }
       // steps 0 .. 2 ST-1: S[ib] += Kf^T delta (kb = s / ST, ib = s % ST); then the readout
       // O = Qg h + M delta over the nonzero M tiles (cb, kb): (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
-      mfma_pipe<2 * ST + 6, 4>(
+      mfma_pipe<2 * ST + 6, 2>(
           [&](int st, uint4& ah, uint4& al) {
             if (st < 2 * ST) {
               afrag(sK, (st % ST) * 2 + st / ST, lane, ah, al);
@@ -298,17 +312,21 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
               O[cb] = mma3(ah, al, dh_[kb], dl_[kb], O[cb]);
             }
           });
-      const bufrsrc ro = make_buf(out + row_bthk(b, t0, h, T, H, V), ((L - 1) * H + 1) * V * sizeof(TO));
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
+      for (int cb = 0; cb < 4; ++cb) {
+        // rows 16 cb .. of this chunk, H*V apart; the descriptor ends right after row L-1's head h
+        const int r0 = 16 * cb;
+        const bufrsrc ro = make_buf(out + row_bthk(b, t0 + r0, h, T, H, V),
+                                    L > r0 ? ((L - 1 - r0) * H + 1) * V * (uint32_t)sizeof(TO) : 0u);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t e = (uint32_t)((16 * cb + 4 * g4 + j) * H) * V + col;
+          const uint32_t e = (uint32_t)((4 * g4 + j) * H) * V + col;
           if constexpr (sizeof(TO) == 2)
             __builtin_amdgcn_raw_buffer_store_b16(f2bf(O[cb][j]), ro, e * 2, 0, 0);
           else
             buf_st(ro, e * 4, O[cb][j]);
         }
+      }
     }
     __syncthreads();
   }
@@ -321,20 +339,21 @@ __global__ __launch_bounds__(256) void state_fwd_kernel(const float* __restrict_
 }
 
 // ===========================================================================
-// Reverse state pass.  grid (B*H*V/64), block 256.  LDS 112.5 KB.
+// Reverse state pass.  grid (B*H*V/COLS), block 4 COLS.  LDS 112.5 KB.
 // ===========================================================================
 template <int K, int V, typename TDO>
-__global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict__ Mg, const float* __restrict__ Kf,
+__global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float* __restrict__ Mg, const float* __restrict__ Kf,
                                                         const float* __restrict__ Qg, const float* __restrict__ W,
                                                         const float* __restrict__ gc, const TDO* __restrict__ dO,
                                                         const float* __restrict__ dht, int T, int H, int NT, int BH,
                                                         float* __restrict__ dhbuf, float* __restrict__ dDl,
                                                         float* __restrict__ dh0) {
-  constexpr int NV = V / WG_COLS;
+  constexpr int COLS = state_cols(V), NTHR = state_threads(V), NV = V / COLS;
   constexpr int KB = K / 32;
   constexpr int ST = K / 16;
-  constexpr int UN = C * K / 4 / 256;  // staging units per thread of a C x K operand
-  constexpr int UM = C * C / 4 / 256;  // ... of M^T
+  static_assert((C * K / 4) % NTHR == 0 && (C * C / 4) % NTHR == 0, "staging units per thread");
+  constexpr int UN = C * K / 4 / NTHR;  // staging units per thread of a C x K operand
+  constexpr int UM = C * C / 4 / NTHR;  // ... of M^T
   constexpr bool DO_BF16 = sizeof(TDO) == 2;
   // phase 1: M^T (rows c', k = c) and Kf (rows c, k = i);  phase 2: Qg^T, W^T (rows i, k = c)
   __shared__ __attribute__((aligned(16))) bf16_t sM[(C / 16) * (C / 32) * TILE];
@@ -346,9 +365,17 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
   xcd_map(blockIdx.x, NV, BH, bh, vs);
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
-  const int col = vs * WG_COLS + 16 * w + (lane & 15);
+  const int col = vs * COLS + 16 * w + (lane & 15);
 
-  float rM[UM][4], rQ[UN][4], rWt[UN][4], rO[4][4], rE = 0.f;
+  float rM[UM][4], rQ[UN][4], rWt[UN][4], rE = 0.f;
+  // dO as loaded (raw bf16 bits or fp32), widened only where the fragments are built, so the
+  // loads of a chunk are all issued before any of them is waited for
+  using RawO = std::conditional_t<DO_BF16, uint16_t, float>;
+  RawO rO[4][4];
+  auto widen = [](RawO x) -> float {
+    if constexpr (DO_BF16) return bf2f(x);
+    else return x;
+  };
   float4 rKn[UN];
   auto load_p1 = [&](int n) {  // M^T and Kf of chunk n
     const int t0 = n * C, L = min(C, T - t0);
@@ -356,13 +383,13 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
     const bufrsrc rk = make_buf(Kf + row_bht(bh, t0, T, K), L * K * 4);
 #pragma unroll
     for (int u = 0; u < UM; ++u) {
-      const Unit x = unit<C>(tid + 256 * u);  // row = c' (the d delta index), k = c
+      const Unit x = unit<C>(tid + NTHR * u);  // row = c' (the d delta index), k = c
 #pragma unroll
       for (int j = 0; j < 4; ++j) rM[u][j] = buf_ld(rm, ((x.k0 + j) * C + x.row) * 4);
     }
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const Unit x = unit<K>(tid + 256 * u);
+      const Unit x = unit<K>(tid + NTHR * u);
       rKn[u] = buf_ld4(rk, (x.row * K + x.k0) * 4);
     }
   };
@@ -370,11 +397,10 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
     const int t0 = n * C, L = min(C, T - t0);
     const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
     const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);
-    // dO rows are H*V apart; the descriptor ends right after row L-1's head h
-    const bufrsrc ro = make_buf(dO + row_bthk(b, t0, h, T, H, V), ((L - 1) * H + 1) * V * sizeof(TDO));
+
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const Unit x = unit<C>(tid + 256 * u);  // row = i, k = c
+      const Unit x = unit<C>(tid + NTHR * u);  // row = i, k = c
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t o = ((x.k0 + j) * K + x.row) * 4;
@@ -383,9 +409,18 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
       }
     }
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < 4; ++cb) {
+      // dO rows 16 cb .. are H*V apart; the descriptor ends right after row L-1's head h
+      const int r0 = 16 * cb;
+      const bufrsrc ro = make_buf(dO + row_bthk(b, t0 + r0, h, T, H, V),
+                                  L > r0 ? ((L - 1 - r0) * H + 1) * V * (uint32_t)sizeof(TDO) : 0u);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) rO[cb][j] = buf_ldt<TDO>(ro, (16 * cb + 4 * g4 + j) * H * V + col);
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t e = (uint32_t)((4 * g4 + j) * H * V + col);
+        if constexpr (DO_BF16) rO[cb][j] = __builtin_amdgcn_raw_buffer_load_b16(ro, e * 2, 0, 0);
+        else rO[cb][j] = buf_ld(ro, e * 4);
+      }
+    }
     {  // raw g_last of the chunk; the exponential is taken when staging, so no wait sits here
       const bufrsrc rg = make_buf(gc + row_bthk(b, t0 + L - 1, h, T, H, K), K * 4);  // lanes >= K read 0
       rE = buf_ld(rg, tid * 4);
@@ -393,15 +428,15 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
   };
   auto stage_p1 = [&]() {
 #pragma unroll
-    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + 256 * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
+    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + NTHR * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
 #pragma unroll
     for (int u = 0; u < UN; ++u)
-      put_unit(sKn, unit<K>(tid + 256 * u).off, rKn[u].x, rKn[u].y, rKn[u].z, rKn[u].w);
+      put_unit(sKn, unit<K>(tid + NTHR * u).off, rKn[u].x, rKn[u].y, rKn[u].z, rKn[u].w);
   };
   auto stage_p2 = [&]() {
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int off = unit<C>(tid + 256 * u).off;
+      const int off = unit<C>(tid + NTHR * u).off;
       put_unit(sQ, off, rQ[u][0], rQ[u][1], rQ[u][2], rQ[u][3]);
       put_unit(sWt, off, rWt[u][0], rWt[u][1], rWt[u][2], rWt[u][3]);
     }
@@ -421,19 +456,19 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
   for (int n = NT - 1; n >= 0; --n) {
     const int t0 = n * C, L = min(C, T - t0);
     {
-      const bufrsrc rh = make_buf(dhbuf + ((int64_t)bh * NT + n) * K * V, K * V * 4);
+      const float* hb = dhbuf + ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
-      for (int ib = 0; ib < ST; ++ib)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) buf_st(rh, ((16 * ib + 4 * g4 + j) * V + col) * 4, dS[ib][j]);
+      for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, dS[ib]);
     }
 
     // dO of this chunk as B fragments (k = c), kept for both phases; a bf16 dO has ol = 0
     uint4 oh[2], ol[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
-      bfrag(f32x4{rO[2 * kb][0], rO[2 * kb][1], rO[2 * kb][2], rO[2 * kb][3]},
-            f32x4{rO[2 * kb + 1][0], rO[2 * kb + 1][1], rO[2 * kb + 1][2], rO[2 * kb + 1][3]}, oh[kb], ol[kb]);
+      bfrag(f32x4{widen(rO[2 * kb][0]), widen(rO[2 * kb][1]), widen(rO[2 * kb][2]), widen(rO[2 * kb][3])},
+            f32x4{widen(rO[2 * kb + 1][0]), widen(rO[2 * kb + 1][1]), widen(rO[2 * kb + 1][2]),
+                  widen(rO[2 * kb + 1][3])},
+            oh[kb], ol[kb]);
 
     // ---- phase 1: d delta = M^T dO + Kf dS   (reads sM, sKn; fills sQ, sWt with chunk n)
     stage_p2();
@@ -447,7 +482,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
       for (int cb = 0; cb < 4; ++cb) dD[cb] = zero4();
       // steps 0..5: M^T dO over the nonzero tiles (cb, kb): (0,0) (1,0) (0,1) (1,1) (2,1) (3,1)
       // (M^T[c'][c] = M[c][c'] = 0 for c < c'); then Kf dS (kb = m / 4, cb = m % 4)
-      mfma_pipe<6 + 4 * KB, 4>(
+      mfma_pipe<6 + 4 * KB, 2>(
           [&](int st, uint4& ah, uint4& al) {
             if (st < 6) {
               const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
@@ -466,11 +501,10 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
               dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
             }
           });
-      const bufrsrc rd = make_buf(dDl + row_bht(bh, t0, T, V), L * V * 4);  // rows past L dropped
+      const float* dl = dDl + row_bht(bh, t0, T, V);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) buf_st(rd, ((16 * cb + 4 * g4 + j) * V + col) * 4, dD[cb][j]);
+        st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, dD[cb]);  // rows past L dropped
     }
     __syncthreads();
 
@@ -489,7 +523,7 @@ __global__ __launch_bounds__(256) void state_bwd_kernel(const float* __restrict_
         dS[ib] = f32x4{e.x * dS[ib][0], e.y * dS[ib][1], e.z * dS[ib][2], e.w * dS[ib][3]};
       }
       // step s: kb = s / (2 ST), ib = (s / 2) % ST, operand Qg^T (even s, B = dO) or W^T (odd s)
-      mfma_pipe<4 * ST, 4>(
+      mfma_pipe<4 * ST, 2>(
           [&](int st, uint4& ah, uint4& al) {
             afrag((st & 1) ? sWt : sQ, ((st >> 1) % ST) * 2 + st / (2 * ST), lane, ah, al);
           },
