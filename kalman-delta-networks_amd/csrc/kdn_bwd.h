@@ -4,10 +4,8 @@
 // state leaving it, delta / d delta = the chunk's delta and its gradient):
 //   dQg = dO h^T,  dW = -d delta h^T,  dKf = delta dh^T,  dM = lower(dO delta^T),
 //   dgl_i = 2^{G_last,i} sum_v h_iv dh_iv
-// Every product contracts over V, which is the contiguous index of all five operands, so each
-// lane loads its MFMA fragments (8 consecutive v) straight from global memory; no LDS.  Wave w
-// owns the K-row tiles w, w+4 of h and dh (kept as split registers for the whole chunk) and
-// streams the chunk rows of dO, delta and d delta, which the four waves share through L1/L2.
+// Every product contracts over V, the contiguous index of all five operands, so MFMA fragments
+// are 8 consecutive v of one row.
 #pragma once
 #include "kdn_common.h"
 #include "kdn_intra.h"
@@ -59,7 +57,14 @@ __device__ __forceinline__ void row_frag<bf16_t>(bufrsrc r, uint32_t elem, uint4
   lo = uint4{0u, 0u, 0u, 0u};
 }
 
-// grid (NT, B*H), block 256.
+// grid (NT, B*H), block 256, two workgroups per CU (LDS 64 KB).
+//
+// The chunk rows of dO, d delta and delta are staged once per workgroup, 16 rows at a time, as
+// split fragments in LDS (double-buffered; delta's blocks are kept for the dM tiles), so each
+// row is loaded and split once instead of once per wave.  Each wave keeps its K-row tiles of h
+// and dh as split A fragments and computes the transposed products
+//   dQg^T = h dO^T,  dW^T = -h d delta^T,  dKf^T = dh delta^T,  dM^T = delta dO^T (lower part)
+// whose D tiles give each lane 4 consecutive K (or s) entries of one chunk row: 16-byte stores.
 template <int K, int V, typename TDO>
 __global__ __launch_bounds__(256, 2) void hgrad_kernel(const float* __restrict__ hbuf, const float* __restrict__ dhbuf,
                                                        const float* __restrict__ Dl, const float* __restrict__ dDl,
@@ -71,9 +76,15 @@ __global__ __launch_bounds__(256, 2) void hgrad_kernel(const float* __restrict__
   constexpr int VB = V / 32;          // k-blocks of the V contraction
   constexpr int NIT = K / 16;         // K-row tiles of h / dh
   constexpr int ITW = (NIT + 3) / 4;  // per wave
+  constexpr int RB = VB * TILE;       // one 16-row block of a [rows][V] operand as fragments
+  constexpr int NST = 2 * V;          // staging threads: 8 consecutive v of one row each
+  static_assert(NST <= 256, "one staging slice per thread");
+  __shared__ __attribute__((aligned(16))) bf16_t sO[2][RB];       // dO rows of the current / next block
+  __shared__ __attribute__((aligned(16))) bf16_t sdD[2][RB];      // d delta rows
+  __shared__ __attribute__((aligned(16))) bf16_t sD[C / 16][RB];  // delta rows, all blocks
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
 
   const int64_t chunk = (int64_t)bh * NT + n;
   const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
@@ -86,93 +97,144 @@ __global__ __launch_bounds__(256, 2) void hgrad_kernel(const float* __restrict__
   const bufrsrc rKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
   const bufrsrc rM = make_buf(dMg + chunk * C * C, C * C * 4);
 
-  // ---- h and dh rows of this wave's tiles as B fragments (col i, k = v), and the g_last dot
-  uint4 hh[ITW][VB], hl[ITW][VB], dhh[ITW][VB], dhl[ITW][VB];
-#pragma unroll
-  for (int u = 0; u < ITW; ++u) {
-    const int it = w + 4 * u;
-    if (it >= NIT) break;
-    const int i = 16 * it + r16;
-    float dot = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < VB; ++kb) {
-      const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
-      float x[8], y[8];
-      ld8(rh, e * 4, x);
-      ld8(rdh, e * 4, y);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) dot += x[j] * y[j];
-      split8(x, hh[u][kb], hl[u][kb]);
-      split8(y, dhh[u][kb], dhl[u][kb]);
+  // ---- staging slice: row sr of a 16-row block, v = sv0 .. sv0 + 7, fragment slot so
+  const int skb = tid >> 6, sl = tid & 63, sr = sl & 15, sv0 = 32 * skb + 8 * (sl >> 4), so = skb * TILE + sl * 8;
+  const bool stager = tid < NST;
+  u32x4 oraw[DO_BF16 ? 1 : 2];
+  float4 ddraw[2], draw[2];
+  auto load_block = [&](int blk) {
+    const uint32_t c = (uint32_t)(16 * blk + sr);
+    if constexpr (DO_BF16) {
+      oraw[0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + sv0) * 2, 0, 0);
+    } else {
+      oraw[0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + sv0) * 4, 0, 0);
+      oraw[1] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + sv0) * 4 + 16, 0, 0);
     }
-    dot += __shfl_xor(dot, 16, 64);
-    dot += __shfl_xor(dot, 32, 64);
-    if (g4 == 0) dgl[chunk * K + i] = dot * exp2f(gc[(((int64_t)b * T + t0 + L - 1) * H + h) * K + i]);
-  }
+    ddraw[0] = buf_ld4(rdD, (c * V + sv0) * 4);
+    ddraw[1] = buf_ld4(rdD, (c * V + sv0) * 4 + 16);
+    draw[0] = buf_ld4(rD, (c * V + sv0) * 4);
+    draw[1] = buf_ld4(rD, (c * V + sv0) * 4 + 16);
+  };
+  auto put8 = [&](bf16_t* dst, const float4& x0, const float4& x1) {
+    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    uint4 hi, lo;
+    split8(x, hi, lo);
+    *reinterpret_cast<uint4*>(dst + so) = hi;
+    *reinterpret_cast<uint4*>(dst + so + 512) = lo;
+  };
+  auto stage_block = [&](int blk) {
+    const int p = blk & 1;
+    if constexpr (DO_BF16) {
+      *reinterpret_cast<uint4*>(sO[p] + so) = uint4{oraw[0].x, oraw[0].y, oraw[0].z, oraw[0].w};  // exact, lo = 0
+    } else {
+      put8(sO[p], __builtin_bit_cast(float4, oraw[0]), __builtin_bit_cast(float4, oraw[1]));
+    }
+    put8(sdD[p], ddraw[0], ddraw[1]);
+    put8(sD[blk], draw[0], draw[1]);
+  };
 
-  // ---- dQg, dW, dKf: row block cb x this wave's K tiles
-#pragma unroll 1
-  for (int cb = 0; cb < 4; ++cb) {
-    f32x4 aQ[ITW], aW[ITW], aK[ITW];
-#pragma unroll
-    for (int u = 0; u < ITW; ++u) aQ[u] = aW[u] = aK[u] = zero4();
-    const uint32_t crow = (uint32_t)(16 * cb + r16);
-#pragma unroll
-    for (int kb = 0; kb < VB; ++kb) {
-      const uint32_t v0 = 32 * kb + 8 * g4;
-      uint4 oh, ol, ddh, ddl, dh_, dl_;
-      row_frag<TDO>(rO, crow * H * V + v0, oh, ol);
-      row_frag<float>(rdD, crow * V + v0, ddh, ddl);
-      row_frag<float>(rD, crow * V + v0, dh_, dl_);
-#pragma unroll
-      for (int u = 0; u < ITW; ++u) {
-        if (w + 4 * u >= NIT) break;
-        aQ[u] = DO_BF16 ? mma2b(oh, hh[u][kb], hl[u][kb], aQ[u]) : mma3(oh, ol, hh[u][kb], hl[u][kb], aQ[u]);
-        aW[u] = mma3(ddh, ddl, hh[u][kb], hl[u][kb], aW[u]);
-        aK[u] = mma3(dh_, dl_, dhh[u][kb], dhl[u][kb], aK[u]);
-      }
-    }
+  if (stager) load_block(0);
+
+  // ---- h and dh rows of this wave's tiles as split A fragments (row i, k = v), and the g_last dot
+  uint4 hh[ITW][VB], hl[ITW][VB], dhh[ITW][VB], dhl[ITW][VB];
+  {
+    const bufrsrc rg = make_buf(gc + (((int64_t)b * T + t0 + L - 1) * H + h) * K, K * 4);
 #pragma unroll
     for (int u = 0; u < ITW; ++u) {
       const int it = w + 4 * u;
       if (it >= NIT) break;
       const int i = 16 * it + r16;
+      const float gl = buf_ld(rg, i * 4);
+      float dot = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t o = ((16 * cb + 4 * g4 + j) * K + i) * 4;
-        buf_st(rQ, o, aQ[u][j]);
-        buf_st(rW, o, -aW[u][j]);
-        buf_st(rKf, o, aK[u][j]);
+      for (int kb = 0; kb < VB; ++kb) {
+        const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
+        float x[8], y[8];
+        ld8(rh, e * 4, x);
+        ld8(rdh, e * 4, y);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot += x[j] * y[j];
+        split8(x, hh[u][kb], hl[u][kb]);
+        split8(y, dhh[u][kb], dhl[u][kb]);
       }
+      dot += __shfl_xor(dot, 16, 64);
+      dot += __shfl_xor(dot, 32, 64);
+      if (g4 == 0) dgl[chunk * K + i] = dot * exp2f(gl);
     }
   }
+  if (stager) {
+    stage_block(0);
+    load_block(1);
+  }
+  __syncthreads();
 
-  // ---- dM = lower(dO delta^T): lower tiles w, w+4, w+8; upper tiles are zero
 #pragma unroll 1
-  for (int t = w; t < 10; t += 4) {
-    int I, J;
-    lower_tile(t, I, J);
-    f32x4 acc = zero4();
-    const uint32_t crow = (uint32_t)(16 * I + r16), srow = (uint32_t)(16 * J + r16);
+  for (int cb = 0; cb < C / 16; ++cb) {
+    const int p = cb & 1;
+    // ---- dQg^T, dW^T, dKf^T for this block's 16 chunk rows x this wave's K tiles
+    f32x4 aQ[ITW], aW[ITW], aK[ITW];
+#pragma unroll
+    for (int u = 0; u < ITW; ++u) aQ[u] = aW[u] = aK[u] = zero4();
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb) {
-      const uint32_t v0 = 32 * kb + 8 * g4;
-      uint4 oh, ol, dh_, dl_;
-      row_frag<TDO>(rO, crow * H * V + v0, oh, ol);
-      row_frag<float>(rD, srow * V + v0, dh_, dl_);
-      acc = DO_BF16 ? mma2b(oh, dh_, dl_, acc) : mma3(oh, ol, dh_, dl_, acc);
-    }
+      uint4 oh, ol, ddh, ddl, dh_, dl_;
+      oh = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + lane * 8);
+      if constexpr (!DO_BF16) ol = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + 512 + lane * 8);
+      afrag(sdD[p], kb, lane, ddh, ddl);
+      afrag(sD[cb], kb, lane, dh_, dl_);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = 16 * I + 4 * g4 + j, s = 16 * J + r16;
-      buf_st(rM, (c * C + s) * 4, s <= c ? acc[j] : 0.f);
+      for (int u = 0; u < ITW; ++u) {
+        if (w + 4 * u >= NIT) break;
+        if constexpr (DO_BF16) aQ[u] = kdn_state::mma2(hh[u][kb], hl[u][kb], oh, aQ[u]);
+        else aQ[u] = mma3(hh[u][kb], hl[u][kb], oh, ol, aQ[u]);
+        aW[u] = mma3(hh[u][kb], hl[u][kb], ddh, ddl, aW[u]);
+        aK[u] = mma3(dhh[u][kb], dhl[u][kb], dh_, dl_, aK[u]);
+      }
     }
-  }
-  for (int t = w; t < 6; t += 4) {
-    int I, J;
-    upper_tile(t, I, J);
+    {
+      const uint32_t c = (uint32_t)(16 * cb + r16);  // rows past L are dropped by the descriptors
 #pragma unroll
-    for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * I + 4 * g4 + j) * C + 16 * J + r16) * 4, 0.f);
+      for (int u = 0; u < ITW; ++u) {
+        const int it = w + 4 * u;
+        if (it >= NIT) break;
+        const uint32_t o = (c * K + 16 * it + 4 * g4) * 4;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, aQ[u]), rQ, o, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, -aW[u]), rW, o, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, aK[u]), rKf, o, 0, 0);
+      }
+    }
+    // ---- dM rows of this block: tile (cb, J) = lower(dO delta^T), zero above the diagonal;
+    // tile J goes to wave (J + cb) % 4
+#pragma unroll
+    for (int J = 0; J < C / 16; ++J) {
+      if (((J + cb) & 3) != w) continue;
+      const uint32_t c = (uint32_t)(16 * cb + r16), s0 = (uint32_t)(16 * J + 4 * g4);
+      f32x4 acc = zero4();
+      if (J <= cb) {
+#pragma unroll
+        for (int kb = 0; kb < VB; ++kb) {
+          uint4 oh, ol, xh, xl;
+          oh = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + lane * 8);
+          afrag(sD[J], kb, lane, xh, xl);
+          if constexpr (DO_BF16) {
+            acc = kdn_state::mma2(xh, xl, oh, acc);
+          } else {
+            ol = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + 512 + lane * 8);
+            acc = mma3(xh, xl, oh, ol, acc);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (s0 + j > c) acc[j] = 0.f;
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), rM, (c * C + s0) * 4, 0, 0);
+    }
+    // ---- next block into the other buffer, and the loads of the one after
+    if (cb + 1 < C / 16 && stager) {
+      stage_block(cb + 1);
+      if (cb + 2 < C / 16) load_block(cb + 2);
+    }
+    __syncthreads();
   }
 }
 
