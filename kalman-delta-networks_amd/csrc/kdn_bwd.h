@@ -381,13 +381,15 @@ __global__ __launch_bounds__(256, 2) void solve_kernel(const float* __restrict__
 //   dg = Lk dLk + Lq dLq - R dR + k eg dKg + scale q eg dQg - kappa f dKf  (natural-log coordinates)
 //   dg[last row] += sum_c kappa f dKf + dgl;   iso: dbeta = sum_i dkappa k, dk += beta dkappa
 // The anchor terms cancel exactly (N and M do not depend on the anchor) and are omitted.
-// Wave w owns the channel tiles w, w+4 and holds the factors at its accumulator positions
-// (rows = chunk rows, column = channel), which are also the permuted-k B operands of the
-// time contractions; dN, dM, dN^T, dM^T are split once per workgroup into LDS fragments.
+// Wave w owns the channel tiles w, w+4.  The factors R, Lk, Lq are built per lane for one
+// channel and 16 chunk rows (the permuted-k fragment order) and enter the time contractions as
+// the A operand, with dN, dM, dN^T, dM^T (split once per workgroup into LDS fragments) as B:
+// the transposed D tiles give each lane 4 consecutive channels of one chunk row, so the
+// elementwise inputs and outputs move as 16-byte (fp32) and 8-byte (bf16) vectors.
 // grid (NT, B*H), block 256.  Chunks flagged by the forward go to the exact kernel.
 // ---------------------------------------------------------------------------------------------
 template <int K, bool ISO>
-__global__ __launch_bounds__(256, 1) void contrib_kernel(
+__global__ __launch_bounds__(256, 2) void contrib_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
     const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
@@ -444,20 +446,19 @@ __global__ __launch_bounds__(256, 1) void contrib_kernel(
   const bufrsrc rdQg = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
   const bufrsrc rdKg = make_buf(dKg + ((int64_t)bh * T + t0) * K, L * K * 4);
   const bufrsrc rdKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
-  float bpart[16];
+  float bpart[4];  // iso: dbeta partials of rows 16 tl + r16
 #pragma unroll
-  for (int p = 0; p < 16; ++p) bpart[p] = 0.f;
+  for (int p = 0; p < 4; ++p) bpart[p] = 0.f;
 
 #pragma unroll 1
   for (int u = 0; u < ITW; ++u) {
     const int it = w + 4 * u;
     if (it >= NIT) break;
     const int i = 16 * it + r16;
-    // ---- loads in two batches (factor inputs, then gradient inputs) so the wave waits for memory
-    // twice per channel tile instead of once per row; rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j
-    float kv[16], qv[16], av[16], Gv[16], dkg[16], dqg[16], dkf[16];
+    // ---- factor loads, one channel per lane: rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j
+    float av[16], Gv[16];
     uint16_t kraw[16], qraw[16];
-    const float g0 = buf_ld(rG, i * 4), gl = buf_ld(rG, ((uint32_t)((L - 1) * H) * K + i) * 4);
+    const float g0 = buf_ld(rG, i * 4);
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
       const int c = 16 * (p >> 2) + 4 * g4 + (p & 3);
@@ -468,9 +469,7 @@ __global__ __launch_bounds__(256, 1) void contrib_kernel(
       Gv[p] = buf_ld(rG, o * 4);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the batch together (raw bf16 held until every load is out)
-#pragma unroll
-    for (int p = 0; p < 16; ++p) kv[p] = bf2f(kraw[p]), qv[p] = bf2f(qraw[p]);
-    // factors at this lane's positions, as permuted-k B fragments per 32-row block
+    // factors as permuted-k fragments per 32-row block (k = chunk row, lane column = channel i)
     uint4 Rh[2], Rl[2], Kh[2], Kl[2], Qh[2], Ql[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -478,17 +477,41 @@ __global__ __launch_bounds__(256, 1) void contrib_kernel(
 #pragma unroll
       for (int sl = 0; sl < 8; ++sl) {
         const int p = 8 * kb + sl;  // tiles 2kb (slots 0-3) and 2kb+1 (slots 4-7)
-        const float kap_p = ISO ? av[p] * kv[p] : av[p];
+        const float kvp = bf2f(kraw[p]), qvp = bf2f(qraw[p]);
+        const float kap_p = ISO ? av[p] * kvp : av[p];
         const float e0 = exp2f(Gv[p] - g0);
-        lk[sl] = kv[p] * e0;
-        lq[sl] = scale * qv[p] * e0;
+        lk[sl] = kvp * e0;
+        lq[sl] = scale * qvp * e0;
         rv[sl] = kap_p * exp2f(g0 - Gv[p]);
       }
       split8(rv, Rh[kb], Rl[kb]);
       split8(lk, Kh[kb], Kl[kb]);
       split8(lq, Qh[kb], Ql[kb]);
     }
-    // ---- time contractions
+    // ---- elementwise inputs at the transposed tile positions: row c = 16 tl + r16, channels
+    // i0 .. i0+3 (16-byte / 8-byte loads), issued before the contractions
+    const int i0 = 16 * it + 4 * g4;
+    const float4 g0v = buf_ld4(rG, i0 * 4), glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
+    u32x2 kq4[4], qq4[4];
+    float4 kap4[4], G4[4], dkg4[4], dqg4[4], dkf4[4];
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0, ol = c * K + i0;
+      kq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rk, o * 2, 0, 0);
+      qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
+      if (ISO) {
+        const float be = buf_ld(rkap, c * H * 4);
+        kap4[tl] = float4{be, be, be, be};
+      } else {
+        kap4[tl] = buf_ld4(rkap, o * 4);
+      }
+      G4[tl] = buf_ld4(rG, o * 4);
+      dkg4[tl] = buf_ld4(rdKg, ol * 4);
+      dqg4[tl] = buf_ld4(rdQg, ol * 4);
+      dkf4[tl] = buf_ld4(rdKf, ol * 4);
+    }
+    // ---- time contractions, transposed (factor fragments as A, dN/dM fragments as B): the D
+    // tile of row block tl gives lane (row 16 tl + r16) the channels i0 .. i0+3
     f32x4 dLk[4], dLq[4], dR[4];
 #pragma unroll
     for (int tl = 0; tl < 4; ++tl) {
@@ -498,73 +521,101 @@ __global__ __launch_bounds__(256, 1) void contrib_kernel(
         uint4 ah, al;
         if (kb <= tl / 2) {  // dN, dM rows c: nonzero for s <= c
           afrag(sF, tl * 2 + kb, lane, ah, al);
-          dLk[tl] = mma3(ah, al, Rh[kb], Rl[kb], dLk[tl]);
+          dLk[tl] = mma3(Rh[kb], Rl[kb], ah, al, dLk[tl]);
           afrag(sF + FR, tl * 2 + kb, lane, ah, al);
-          dLq[tl] = mma3(ah, al, Rh[kb], Rl[kb], dLq[tl]);
+          dLq[tl] = mma3(Rh[kb], Rl[kb], ah, al, dLq[tl]);
         }
         if (2 * kb + 1 >= tl) {  // dN^T, dM^T rows s: nonzero for c >= s
           afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
-          dR[tl] = mma3(ah, al, Kh[kb], Kl[kb], dR[tl]);
+          dR[tl] = mma3(Kh[kb], Kl[kb], ah, al, dR[tl]);
           afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
-          dR[tl] = mma3(ah, al, Qh[kb], Ql[kb], dR[tl]);
+          dR[tl] = mma3(Qh[kb], Ql[kb], ah, al, dR[tl]);
         }
       }
     }
-    // ---- second batch: the elementwise gradient inputs
-    __builtin_amdgcn_sched_barrier(0);
+    // ---- assemble.  Per channel 2^{-G_0}, 2^{G_0}, 2^{G_last}; per element one exponential
+    // eg = 2^{G_c} and its reciprocal: e0 = eg 2^{-G_0}, er = 2^{G_0} / eg, f = 2^{G_last} / eg.
+    float E0[4], Ez[4], El[4];
+    {
+      const float gz[4] = {g0v.x, g0v.y, g0v.z, g0v.w}, gla[4] = {glv.x, glv.y, glv.z, glv.w};
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const uint32_t ol = (uint32_t)(16 * (p >> 2) + 4 * g4 + (p & 3)) * K + i;
-      dkg[p] = buf_ld(rdKg, ol * 4);
-      dqg[p] = buf_ld(rdQg, ol * 4);
-      dkf[p] = buf_ld(rdKf, ol * 4);
+      for (int j = 0; j < 4; ++j) E0[j] = exp2f(-gz[j]), Ez[j] = exp2f(gz[j]), El[j] = exp2f(gla[j]);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // ---- assemble
-    float colpart = 0.f, dg_last = 0.f;
+    float colpart[4] = {0.f, 0.f, 0.f, 0.f};
+    float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
     bool has_last = false;
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const int tl = p >> 2, j = p & 3;
-      const int c = 16 * tl + 4 * g4 + j;
-      const uint32_t o = (uint32_t)(c * H) * K + i;
-      const float beta = ISO ? av[p] : 0.f;
-      const float kap_p = ISO ? beta * kv[p] : av[p];
-      const float er = exp2f(g0 - Gv[p]), e0 = exp2f(Gv[p] - g0), eg = exp2f(Gv[p]), f = exp2f(gl - Gv[p]);
-      const float a_lk = dLk[tl][j], a_lq = dLq[tl][j] * scale, a_r = dR[tl][j];
-      float dkv = a_lk * e0 + dkg[p] * eg;
-      const float dqv = a_lq * e0 + scale * dqg[p] * eg;
-      const float dav = a_r * er + dkf[p] * f;
-      // Lk = k e0, Lq (unscaled) = q e0, R = kappa er
-      const float dgv = kv[p] * e0 * a_lk + qv[p] * e0 * a_lq - kap_p * er * a_r + kv[p] * eg * dkg[p] +
-                        scale * qv[p] * eg * dqg[p] - kap_p * f * dkf[p];
-      if (c < L) colpart += kap_p * f * dkf[p];
-      if (ISO) {
-        dkv += beta * dav;
-        bpart[p] += dav * kv[p];
-      } else {
-        buf_st(rdkap, o * 4, dav);
+    for (int tl = 0; tl < 4; ++tl) {
+      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
+      const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
+                            __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
+      const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
+                            __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
+      const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
+      const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
+
+      const float dkgv[4] = {dkg4[tl].x, dkg4[tl].y, dkg4[tl].z, dkg4[tl].w};
+      const float dqgv[4] = {dqg4[tl].x, dqg4[tl].y, dqg4[tl].z, dqg4[tl].w};
+      const float dkfv[4] = {dkf4[tl].x, dkf4[tl].y, dkf4[tl].z, dkf4[tl].w};
+      float dkv[4], dqv[4], dav[4], dgv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float beta = ISO ? a4[j] : 0.f;
+        const float kap_p = ISO ? beta * kv4[j] : a4[j];
+        const float eg = exp2f(gv[j]), ig = __frcp_rn(eg);
+        const float e0 = eg * E0[j], er = ig * Ez[j], f = ig * El[j];
+        const float a_lk = dLk[tl][j], a_lq = dLq[tl][j] * scale, a_r = dR[tl][j];
+        dkv[j] = a_lk * e0 + dkgv[j] * eg;
+        dqv[j] = a_lq * e0 + scale * dqgv[j] * eg;
+        dav[j] = a_r * er + dkfv[j] * f;
+        // Lk = k e0, Lq (unscaled) = q e0, R = kappa er
+        dgv[j] = kv4[j] * e0 * a_lk + qv4[j] * e0 * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv[j] +
+                 scale * qv4[j] * eg * dqgv[j] - kap_p * f * dkfv[j];
+        if ((int)c < L) colpart[j] += kap_p * f * dkfv[j];
+        if (ISO) {
+          dkv[j] += beta * dav[j];
+          bpart[tl] += dav[j] * kv4[j];
+        }
       }
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dqv), rdq, o * 2, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16(f2bf(dkv), rdk, o * 2, 0, 0);
-      if (c == L - 1) {
-        dg_last = dgv;
+      if (!ISO)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(dav[0]), __float_as_uint(dav[1]), __float_as_uint(dav[2]), __float_as_uint(dav[3])},
+            rdkap, o * 4, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16), (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
+          rdq, o * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16), (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
+          rdk, o * 2, 0, 0);
+      if ((int)c == L - 1) {
+        dg_last = float4{dgv[0], dgv[1], dgv[2], dgv[3]};
         has_last = true;
       } else {
-        buf_st(rdg, o * 4, dgv);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(dgv[0]), __float_as_uint(dgv[1]), __float_as_uint(dgv[2]), __float_as_uint(dgv[3])},
+            rdg, o * 4, 0, 0);
       }
     }
-    colpart += __shfl_xor(colpart, 16, 64);
-    colpart += __shfl_xor(colpart, 32, 64);
-    if (has_last) buf_st(rdg, ((uint32_t)((L - 1) * H) * K + i) * 4, dg_last + colpart + dgl[chunk * K + i]);
+    // column sums over the chunk rows: the 16 lanes of a channel group hold rows r16 of each block
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) colpart[j] += __shfl_xor(colpart[j], m, 64);
+    if (has_last) {
+      const float4 gl4 = *reinterpret_cast<const float4*>(dgl + chunk * K + i0);
+      const float4 v = float4{dg_last.x + colpart[0] + gl4.x, dg_last.y + colpart[1] + gl4.y,
+                              dg_last.z + colpart[2] + gl4.z, dg_last.w + colpart[3] + gl4.w};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rdg,
+                                             ((uint32_t)((L - 1) * H) * K + i0) * 4, 0, 0);
+    }
   }
-  if (ISO) {  // dbeta[c] = sum_i dkappa k: over the 16 channels of a tile, this wave's tiles, then the waves
+  if (ISO) {  // dbeta[c] = sum_i dkappa k: over the 4 lane groups (channels), then the waves
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      float v = bpart[p];
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-      if (r16 == 0) sBeta[w * C + 16 * (p >> 2) + 4 * g4 + (p & 3)] = v;
+    for (int tl = 0; tl < 4; ++tl) {
+      float v = bpart[tl];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (g4 == 0) sBeta[w * C + 16 * tl + r16] = v;
     }
     __syncthreads();
     if (tid < L) dbeta[((int64_t)b * T + t0 + tid) * H + h] = sBeta[tid] + sBeta[C + tid] + sBeta[2 * C + tid] +
