@@ -416,19 +416,23 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
       const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
       const int k0 = 32 * kb + 16 * hh + 4 * gg;
       const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
-      float x[4], y[4], xt[4], yt[4];
       const float4 a = buf_ld4(rN, (row * C + k0) * 4), bq = buf_ld4(rM, (row * C + k0) * 4);
-      x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w;
-      y[0] = bq.x, y[1] = bq.y, y[2] = bq.z, y[3] = bq.w;
+      kdn_state::put_unit(sF, off, a.x, a.y, a.z, a.w);
+      kdn_state::put_unit(sF + FR, off, bq.x, bq.y, bq.z, bq.w);
+      // the same values as the transposed operands: element (row s = k0 + j, k = row) of dN^T, dM^T,
+      // one bf16 hi and lo each (tile (s/16, row/32), lane s%16 + 16 g', slot from row%32)
+      const int rk = row & 31, tg = (rk & 15) >> 2, ts = (rk & 3) + 4 * (rk >> 4);
+      const float xv[4] = {a.x, a.y, a.z, a.w}, yv[4] = {bq.x, bq.y, bq.z, bq.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        xt[j] = buf_ld(rN, ((k0 + j) * C + row) * 4);
-        yt[j] = buf_ld(rM, ((k0 + j) * C + row) * 4);
+        const int sr = k0 + j;
+        const int toff = ((sr >> 4) * 2 + (row >> 5)) * TILE + ((sr & 15) + 16 * tg) * 8 + ts;
+        const bf16_t xhi = f2bf(xv[j]), yhi = f2bf(yv[j]);
+        sF[2 * FR + toff] = xhi;
+        sF[2 * FR + toff + 512] = f2bf(xv[j] - bf2f(xhi));
+        sF[3 * FR + toff] = yhi;
+        sF[3 * FR + toff + 512] = f2bf(yv[j] - bf2f(yhi));
       }
-      kdn_state::put_unit(sF, off, x[0], x[1], x[2], x[3]);
-      kdn_state::put_unit(sF + FR, off, y[0], y[1], y[2], y[3]);
-      kdn_state::put_unit(sF + 2 * FR, off, xt[0], xt[1], xt[2], xt[3]);
-      kdn_state::put_unit(sF + 3 * FR, off, yt[0], yt[1], yt[2], yt[3]);
     }
   }
   __syncthreads();
