@@ -158,6 +158,17 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
+  // every load of this thread's tokens goes out first (rows clamped to the chunk; the clamped
+  // duplicates are never used), so the thread waits for memory once
+  float xr[4][8], oraw[4], rraw[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = min(tg * TPG + u, L - 1);
+    load8<TG>(g_raw + (((int64_t)b * T + t0 + t) * H + h) * K + i0, xr[u]);
+    const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
+    oraw[u] = ld(orr, ro);
+    rraw[u] = ld(orr, ro + H);
+  }
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float pre[4][8];  // local inclusive prefix per token (TPG <= 4 when K >= 64 and chunk <= 64)
   float e2[4];
@@ -166,11 +177,9 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     const int t = tg * TPG + u;
     e2[u] = 0.f;
     if (u < TPG && t < L) {
-      float x[8];
-      load8<TG>(g_raw + (((int64_t)b * T + t0 + t) * H + h) * K + i0, x);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float g = -rate * softplusf(x[j] + bias[j]);
+        const float g = -rate * softplusf(xr[u][j] + bias[j]);
         acc[j] += g;
         pre[u][j] = acc[j];
         e2[u] += __expf(2.f * g);
@@ -201,9 +210,8 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     if (cg == 0 && u < TPG && t < L) {
       const int64_t o = ((int64_t)b * T + t0 + t) * H + h;
       a_out[o] = s / (float)K;
-      const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
-      omega_out[o] = omega_min + softplusf(ld(orr, ro) + omega_bias[h]);
-      r_out[o] = r_min + softplusf(ld(orr, ro + H) + r_bias[h]);
+      omega_out[o] = omega_min + softplusf(oraw[u] + omega_bias[h]);
+      r_out[o] = r_min + softplusf(rraw[u] + r_bias[h]);
     }
   }
   if (blockIdx.x == 0 && tid == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
@@ -228,6 +236,22 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
+  // every load of this thread's tokens goes out first (rows clamped to the chunk; the clamped
+  // duplicates are never used), so the thread waits for memory once
+  float dgr_in[4][8], xr[4][8], dav[4], dov[4], drv[4], oraw[4], rraw[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = min(tg * TPG + u, L - 1);
+    const int64_t row = ((int64_t)b * T + t0 + t) * H + h;
+    if (dg_pre) load8<float>(dg_pre + row * K + i0, dgr_in[u]);
+    load8<TG>(g_raw + row * K + i0, xr[u]);
+    dav[u] = da ? da[row] : 0.f;
+    dov[u] = domega ? domega[row] : 0.f;
+    drv[u] = dr ? dr[row] : 0.f;
+    const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
+    oraw[u] = ld(orr, ro);
+    rraw[u] = ld(orr, ro + H);
+  }
   // local suffix sums of dg_pre over this thread's tokens (last token first)
   float dgp[4][8], acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -236,11 +260,9 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) dgp[u][j] = 0.f;
     if (dg_pre && u < TPG && t < L) {
-      float d[8];
-      load8<float>(dg_pre + (((int64_t)b * T + t0 + t) * H + h) * K + i0, d);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        acc[j] += d[j];
+        acc[j] += dgr_in[u][j];
         dgp[u][j] = acc[j];
       }
     }
@@ -261,24 +283,22 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     const int t = tg * TPG + u;
     if (u < TPG && t < L) {
       const int64_t row = ((int64_t)b * T + t0 + t) * H + h;
-      float x[8], dgr[8];
-      load8<TG>(g_raw + row * K + i0, x);
-      const float dav = da ? da[row] * (2.f / (float)K) : 0.f;
+      float dgr[8];
+      const float dau = dav[u] * (2.f / (float)K);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float xb = x[j] + bias[j];
+        const float xb = xr[u][j] + bias[j];
         const float g = -rate * softplusf(xb);
         float dgl = dg_pre ? off[j] + dgp[u][j] : 0.f;
-        if (da) dgl += dav * __expf(2.f * g);
+        if (da) dgl += dau * __expf(2.f * g);
         dgr[j] = dgl * (-rate) * sigmoidf(xb);
         dA_term += dgl * g;
         ddt[j] += dgr[j];
       }
       if (dg_raw) store8<TG>(dg_raw + row * K + i0, dgr);
       if (cg == 0) {
-        const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
-        const float ob = domega ? domega[row] * sigmoidf(ld(orr, ro) + omega_bias[h]) : 0.f;
-        const float rb = dr ? dr[row] * sigmoidf(ld(orr, ro + H) + r_bias[h]) : 0.f;
+        const float ob = domega ? dov[u] * sigmoidf(oraw[u] + omega_bias[h]) : 0.f;
+        const float rb = dr ? drv[u] * sigmoidf(rraw[u] + r_bias[h]) : 0.f;
         dob += ob;
         drb += rb;
         if (dorr) {
@@ -636,6 +656,15 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_vec_kernel(
   const float floor_log = -13.815510557964274f;  // log(1e-6)
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
+  // the loads of all this thread's tokens go out first (rows clamped to the chunk)
+  float xr[4][8], zrr[4][8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t off = (((int64_t)b * T + t0 + min(tg * TPG + u, L - 1)) * H + h) * K + i0;
+    load8<bf16_t>(f_raw + off, xr[u]);
+    load8<bf16_t>(z_raw + off, zrr[u]);
+  }
+  const float yv = tid < L ? bf2f(y_raw[((int64_t)b * T + t0 + tid) * H + h]) : 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float pre[4][8];
 #pragma unroll
@@ -643,9 +672,9 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_vec_kernel(
     const int t = tg * TPG + u;
     if (u < TPG && t < L) {
       const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i0;
-      float x[8], zr[8], al[8], om[8];
-      load8<bf16_t>(f_raw + off, x);
-      load8<bf16_t>(z_raw + off, zr);
+      float al[8], om[8];
+      const float* x = xr[u];
+      const float* zr = zrr[u];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float ell = -rate * softplusf(x[j] + bias[j]);
@@ -676,10 +705,7 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_vec_kernel(
       store8<float>(g_cumsum + (((int64_t)b * T + t0 + t) * H + h) * K + i0, y);
     }
   }
-  if (tid < L) {
-    const int64_t o = ((int64_t)b * T + t0 + tid) * H + h;
-    r[o] = 0.01f + softplusf(bf2f(y_raw[o]));
-  }
+  if (tid < L) r[((int64_t)b * T + t0 + tid) * H + h] = 0.01f + softplusf(yv);
   if (blockIdx.x == 0 && tid == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
 }
 
@@ -698,6 +724,16 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
+  // the loads of all this thread's tokens go out first (rows clamped to the chunk)
+  float dGr[4][8], xr[4][8], alr[4][8], dar[4][8];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t off = (((int64_t)b * T + t0 + min(tg * TPG + u, L - 1)) * H + h) * K + i0;
+    if (dG) load8<float>(dG + off, dGr[u]);
+    load8<bf16_t>(f_raw + off, xr[u]);
+    load8<float>(alpha + off, alr[u]);
+    if (dalpha) load8<float>(dalpha + off, dar[u]);
+  }
   // local suffix sums of dG over this thread's tokens
   float dgs[4][8], acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -706,11 +742,9 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) dgs[u][j] = 0.f;
     if (dG && u < TPG && t < L) {
-      float d[8];
-      load8<float>(dG + (((int64_t)b * T + t0 + t) * H + h) * K + i0, d);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        acc[j] += d[j];
+        acc[j] += dGr[u][j];
         dgs[u][j] = acc[j];
       }
     }
@@ -729,10 +763,10 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
     const int t = tg * TPG + u;
     if (u < TPG && t < L) {
       const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i0;
-      float x[8], al[8], da[8], df[8];
-      load8<bf16_t>(f_raw + off, x);
-      load8<float>(alpha + off, al);
-      if (dalpha) load8<float>(dalpha + off, da);
+      float df[8];
+      const float* x = xr[u];
+      const float* al = alr[u];
+      const float* da = dar[u];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float xb = x[j] + bias[j];

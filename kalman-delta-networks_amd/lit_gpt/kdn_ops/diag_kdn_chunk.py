@@ -345,13 +345,17 @@ def _validate_diag_kdn_memory_inputs(q, k, kappa, v, g_cumsum, scale):
 
 
 class _DiagKdnMemoryFunction(torch.autograd.Function):
-    """Reference diag_kdn_chunk.py:3247-3312 (fp32 output; fp32 output cotangent)."""
+    """Reference diag_kdn_chunk.py:3247-3312 (fp32 output; fp32 output cotangent).
+
+    ``out_dtype`` bf16 is the layer composition's ``chunk_kalman(...).to(v.dtype)``
+    (diag_kdn.py:342-345) done in the kernel: the fp32 accumulator is rounded to bf16 at the
+    store, and the bf16 cotangent is the cast's exact upcast, so results are identical."""
 
     @staticmethod
-    def forward(ctx, q, k, kappa, v, g_cumsum, scale, initial_state, output_final_state):
+    def forward(ctx, q, k, kappa, v, g_cumsum, scale, initial_state, output_final_state, out_dtype=torch.float32):
         with torch.cuda.device(q.device):
             o, saved, ht = _memscan.mem_fwd(q, k, kappa, False, v, g_cumsum, scale, initial_state=initial_state,
-                                            output_final_state=output_final_state, out_dtype=torch.float32)
+                                            output_final_state=output_final_state, out_dtype=out_dtype)
         ctx.save_for_backward(q, k, kappa, v, g_cumsum, saved)
         ctx.scale = scale
         ctx.has_h0 = initial_state is not None
@@ -365,17 +369,22 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
     def backward(ctx, do, d_final_state=None):
         q, k, kappa, v, g_cumsum, saved = ctx.saved_tensors
         if do is None and d_final_state is None:
-            return None, None, None, None, None, None, None, None
+            return None, None, None, None, None, None, None, None, None
         B, T, H, K = q.shape
         V = v.shape[-1]
         dev = q.device
-        do = torch.zeros((B, T, H, V), device=dev, dtype=torch.float32) if do is None else do.float().contiguous()
+        if do is None:
+            do = torch.zeros((B, T, H, V), device=dev, dtype=torch.float32)
+        elif do.dtype not in (torch.bfloat16, torch.float32):
+            do = do.float().contiguous()
+        else:
+            do = do.contiguous()
         need_h0 = ctx.has_h0 and ctx.needs_input_grad[6]
         with torch.cuda.device(dev):
             dq, dk, dv, dkappa, dg, dh0 = _memscan.mem_bwd(q, k, kappa, False, v, g_cumsum, saved, ctx.scale, do,
                                                           d_final_state=d_final_state,
                                                           need_initial_state_grad=need_h0)
-        return dq, dk, dkappa, dv, dg, None, dh0, None
+        return dq, dk, dkappa, dv, dg, None, dh0, None, None
 
 
 def chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, scale, *, initial_state=None, output_final_state=False):
@@ -392,6 +401,22 @@ def chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, scale, *, initial_state
             raise ValueError("initial_state must be on the same device as q")
     return _DiagKdnMemoryFunction.apply(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state,
                                         bool(output_final_state))
+
+
+def _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale, *, initial_state=None,
+                     output_final_state=False, out_dtype=torch.bfloat16):
+    """``chunk_kalman(...)`` followed by ``.to(out_dtype)``, with the cast done at the kernel's store
+    (the layer composition of diag_kdn.py:342-345); same validation and results."""
+    B, T, H, K = _validate_diag_kdn_memory_inputs(q_memory, k_memory, kappa, v, g_cumsum, scale)
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("out_dtype must be torch.bfloat16 or torch.float32")
+    if initial_state is not None:
+        if initial_state.shape != (B, H, K, v.shape[-1]) or not initial_state.is_cuda:
+            raise ValueError(f"initial_state must be a GPU tensor of shape {(B, H, K, v.shape[-1])}")
+        if initial_state.device != q_memory.device:
+            raise ValueError("initial_state must be on the same device as q")
+    return _DiagKdnMemoryFunction.apply(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state,
+                                        bool(output_final_state), out_dtype)
 
 
 __all__ = ("chunk_kalman", "_diag_kdn_normalize", "_diag_kdn_frontend_precumsum_paired", "_diag_kdn_gain")

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import torch
 
-from .diag_kdn_chunk import _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain, _diag_kdn_normalize, chunk_kalman
+from .diag_kdn_chunk import _chunk_kalman_as, _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain, _diag_kdn_normalize
 from .iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
 
 
@@ -43,9 +43,10 @@ def diag_kdn_scan(q, k, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, init
     if output_final_state:
         kappa, final_precision = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw,
                                                 output_final_state=True)
-        out, final_state = chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state=initial_state,
-                                        output_final_state=True)
-        return out.to(v.dtype), (final_state, final_precision)
+        out, final_state = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale,
+                                            initial_state=initial_state, output_final_state=True, out_dtype=v.dtype)
+        return out, (final_state, final_precision)
     kappa = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw)
-    out = chunk_kalman(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state=initial_state)
-    return out.to(v.dtype)
+    # chunk_kalman(...).to(v.dtype) with the cast at the kernel's store
+    return _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state=initial_state,
+                            out_dtype=v.dtype)

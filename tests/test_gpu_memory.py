@@ -165,3 +165,30 @@ def test_memory_scan_mixed_anchor_and_exact_chunks(variant):
     _check("dv", dv, g_ref[2], TOL_BF16)
     _check("dgate", dell, g_ref[3], TOL_F32 * 5)
     _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+
+
+def test_diag_bf16_output_equals_fp32_output_cast():
+    """The layer composition chunk_kalman(...).to(bf16) (reference diag_kdn.py:342-345) done at the
+    kernel's store: the bf16 output and every gradient (given the same bf16 output cotangent) are
+    bit-identical to the fp32-output op followed by the cast."""
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import diag_kdn_chunk as dk
+    B, T, H, K = 2, 200, 2, 128
+    log(f"case diag bf16-out vs fp32-out cast B={B} T={T} H={H} K={K}")
+    q, k, v, ell, kap = memory_inputs(11, B, T, H, K, K, diag=True)[:5]
+    G2 = chunk_prefix_base2(ell, CHUNK).float()
+    qg, kg, vg, Gg, kapg = (x.to(dev).contiguous() for x in (q, k, v, G2, kap.float()))
+    do = torch.randn(B, T, H, K, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16).to(dev)
+    scale = K ** -0.5
+    outs = []
+    for fused in (False, True):
+        leaves = [x.clone().requires_grad_(True) for x in (qg, kg, kapg, vg, Gg)]
+        if fused:
+            o = dk._chunk_kalman_as(*leaves, float(scale), out_dtype=torch.bfloat16)
+        else:
+            o = dk.chunk_kalman(*leaves, float(scale)).to(torch.bfloat16)
+        grads = torch.autograd.grad((o.float() * do.float()).sum(), leaves)
+        torch.cuda.synchronize()
+        outs.append([o] + list(grads))
+    for name, a, b in zip(("o", "dq", "dk", "dkappa", "dv", "dg"), outs[0], outs[1]):
+        assert a.dtype == b.dtype and torch.equal(a, b), f"{name} differs"
