@@ -24,6 +24,7 @@ namespace kdn_intra {
 using kdn_state::afrag;
 using kdn_state::bfrag;
 using kdn_state::C;
+using kdn_state::mfma;
 using kdn_state::mma2;
 using kdn_state::mma3;
 using kdn_state::split2;
@@ -32,6 +33,7 @@ using kdn_state::zero4;
 
 constexpr float kAnchorSpanMax = 100.f;  // base 2: R <= 2^100 stays far inside fp32
 constexpr int AP = C + 1;                // LDS row stride of the fp32 N and A tiles
+constexpr int XS = C + 4;                // LDS row stride of the staged [column][s] operands
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -74,10 +76,15 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   constexpr int KB = K / 32;
   // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char sRA[RBYTES > ABYTES ? RBYTES : ABYTES];
-  __shared__ __attribute__((aligned(16))) float sN[C * AP];  // N [c][s]
-  bf16_t* sR = reinterpret_cast<bf16_t*>(sRA);
-  float* sA = reinterpret_cast<float*>(sRA);
+  constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
+  // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
+  constexpr int SBYTES = RABYTES + C * AP * 4 > 128 * XS * 4 ? RABYTES + C * AP * 4 : 128 * XS * 4;
+  static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
+  __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
+  bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
+  float* sA = reinterpret_cast<float*>(sbuf);
+  float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
+  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
   __shared__ float sSpan[4];
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
@@ -227,9 +234,10 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   {
     const bufrsrc rA = make_buf(An, C * C * 4);
 #pragma unroll
-    for (int u = 0; u < C * C / 256; ++u) {
-      const int e = tid + 256 * u;
-      buf_st(rA, e * 4, sA[(e % C) * AP + (e / C)]);
+    for (int u = 0; u < C * C / 4 / 256; ++u) {
+      const int e = 4 * (tid + 256 * u), sr = e / C, c0 = e % C;  // A^T[sr][c0 .. c0+3] = A[c0 + j][sr]
+      const float4 x = float4{sA[c0 * AP + sr], sA[(c0 + 1) * AP + sr], sA[(c0 + 2) * AP + sr], sA[(c0 + 3) * AP + sr]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rA, e * 4, 0, 0);
     }
   }
 
@@ -246,51 +254,64 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
       const float x[8] = {row[0], row[1], row[2], row[3], row[16], row[17], row[18], row[19]};
       split8(x, ah[I][kb], al[I][kb]);
     }
-  // U = A V (column tiles of V, exact bf16 B operand) and W = A Kg (Kg = k 2^G, split): each tile's
-  // 16 loads go out together, separate loops keep the tile kind uniform at compile time.
+  // U = A V and W = A Kg (Kg = k 2^G) in transposed form: the operand (staged in LDS as columns
+  // [col][s], loaded coalesced as rows) is the A fragment and A's rows the B fragment, so the D
+  // tile gives each lane 4 consecutive output columns of one chunk row (16-byte stores).
+  __syncthreads();  // every wave has its A fragments; the buffer is free
+  auto stage = [&](auto is_u) {
+    constexpr bool isU = decltype(is_u)::value;
+    constexpr int D = isU ? V : K, UNITS = C * D / 8 / 256;
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      const int e = tid + 256 * u, sr = e / (D / 8), c8 = 8 * (e % (D / 8));
+      const uint32_t o = (uint32_t)(sr * H) * D + c8;
+      float x[8];
+      if constexpr (isU) {
+        unpack8(__builtin_amdgcn_raw_buffer_load_b128(rv, o * 2, 0, 0), x);
+      } else {
+        float g[8];
+        unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, o * 2, 0, 0), x);
+        ld8(rG, o * 4, g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] *= exp2f(g[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sX[(c8 + j) * XS + sr] = x[j];
+    }
+  };
   auto tile = [&](auto is_u, int t) {
     constexpr bool isU = decltype(is_u)::value;
-    const int col = 16 * t + r16;
-    uint16_t raw[16];
-    float gv[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int kb = q >> 3, sl = q & 7;
-      const int s = 32 * kb + (sl < 4 ? 4 * g4 + sl : 16 + 4 * g4 + sl - 4);
-      const uint32_t srow = (uint32_t)(s * H);
-      if constexpr (isU) {
-        raw[q] = __builtin_amdgcn_raw_buffer_load_b16(rv, (srow * V + col) * 2, 0, 0);
-      } else {
-        raw[q] = __builtin_amdgcn_raw_buffer_load_b16(rk, (srow * K + col) * 2, 0, 0);
-        gv[q] = buf_ld(rG, (srow * K + col) * 4);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 bh_[2], bl_[2];
+    constexpr int D = isU ? V : K;
+    uint4 xh[2], xl[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      float x[8];
-#pragma unroll
-      for (int sl = 0; sl < 8; ++sl) {
-        const int q = 8 * kb + sl;
-        x[sl] = isU ? bf2f(raw[q]) : bf2f(raw[q]) * exp2f(gv[q]);
-      }
-      split8(x, bh_[kb], bl_[kb]);  // exact for V (lo = 0)
+      const float* colp = sX + (16 * t + r16) * XS + 32 * kb + 4 * g4;
+      const float4 a0 = *reinterpret_cast<const float4*>(colp), a1 = *reinterpret_cast<const float4*>(colp + 16);
+      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      split8(x, xh[kb], xl[kb]);  // exact for V (lo = 0)
     }
+    const bufrsrc rO = isU ? rU : rW;
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       f32x4 acc = zero4();
-      acc = isU ? mma2(ah[I][0], al[I][0], bh_[0], acc) : mma3(ah[I][0], al[I][0], bh_[0], bl_[0], acc);
-      if (I >= 2) acc = isU ? mma2(ah[I][1], al[I][1], bh_[1], acc) : mma3(ah[I][1], al[I][1], bh_[1], bl_[1], acc);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int cc = 16 * I + 4 * g4 + j;
-        if constexpr (isU) buf_st(rU, (cc * V + col) * 4, acc[j]);
-        else buf_st(rW, (cc * K + col) * 4, acc[j]);
+      for (int kb = 0; kb < 2; ++kb) {
+        if (kb == 1 && I < 2) continue;  // A[c][s] = 0 for s > c
+        acc = mfma(xh[kb], ah[I][kb], acc);
+        acc = mfma(xh[kb], al[I][kb], acc);
+        if constexpr (!isU) acc = mfma(xl[kb], ah[I][kb], acc);
       }
+      const uint32_t row = (uint32_t)(16 * I + r16);  // rows past L are dropped by the descriptor
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), rO,
+                                             (row * D + 16 * t + 4 * g4) * 4, 0, 0);
     }
   };
+  stage(std::true_type{});
+  __syncthreads();
   for (int t = w; t < V / 16; t += 4) tile(std::true_type{}, t);
+  __syncthreads();
+  stage(std::false_type{});
+  __syncthreads();
   for (int t = w; t < K / 16; t += 4) tile(std::false_type{}, t);
 }
 
