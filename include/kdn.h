@@ -141,6 +141,43 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
                 size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
                 float* dg, float* d_initial_state, int stages, hipStream_t stream);
 
+/* ---------------------------------------------------------------- layer frontends */
+/* Depthwise causal short convolution with SiLU, fixed length, width W = 4, no bias:
+ * y[b,t,d] = silu(sum_j w[d,j] x[b,t-3+j,d]), x before t = 0 is 0, computed in f32 and rounded to
+ * x's dtype.  Replaces FLA causal_conv1d(x, weight, activation="silu") as called by
+ * lit_gpt/diag_kdn.py:75-96 and per q|k|v group by qkv_causal_conv1d (iso_kdn_chunk.py:47-478,
+ * forward kernel :56-120).  x [B,T,D] and y [B,T,D] have unit channel stride and the given batch /
+ * time strides (elements; multiples of 8, so packed q|k|v views need no copy); weight [D,W] dense.
+ * D % 8 == 0. */
+int kdn_short_conv_fwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_stride_t, const void* weight,
+                       int w_bf16, int B, int T, int D, int W, void* y, int64_t y_stride_b, int64_t y_stride_t,
+                       hipStream_t stream);
+/* Workspace of kdn_short_conv_bwd when dweight is requested: f32 partials per (b, 64-token block). */
+size_t kdn_short_conv_bwd_workspace_size(int B, int T, int D);
+/* Backward (iso_kdn_chunk.py:127-254, 379-437): g = dy * silu'(y) with the preactivation y recomputed
+ * (rounded to x's dtype when round_preactivation, as the reference's raw_y buffer is),
+ * dx[t] = sum_j w[j] g[t+3-j], dweight[d,j] = sum_{b,t} g[t] x[t-3+j] summed in a fixed order and
+ * stored in weight's dtype.  dy has x's dtype and may be NULL (zero); dx / dweight may be NULL. */
+int kdn_short_conv_bwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_stride_t, const void* weight,
+                       int w_bf16, const void* dy, int64_t dy_stride_b, int64_t dy_stride_t, int B, int T, int D,
+                       int W, int round_preactivation, void* dx, int64_t dx_stride_b, int64_t dx_stride_t,
+                       void* dweight, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Gated RMS norm over the last dimension D of dense rows:
+ * y = x rsqrt(mean(x^2) + eps) * weight * act(g), act = sigmoid (activation 0) or g sigmoid(g)
+ * (activation 1, "swish"); f32 math, y in x's dtype, rstd [rows] f32 saved (nullable).
+ * Replaces FLA FusedRMSNormGated as the layers' o_norm (lit_gpt/iso_kdn.py:192-196,305-312;
+ * lit_gpt/diag_kdn.py:216-219,346).  D % 8 == 0, D / 8 a power of two <= 64. */
+int kdn_rms_norm_gated_fwd(const void* x, int x_bf16, const void* g, int g_bf16, const void* weight, int w_bf16,
+                           int64_t rows, int D, float eps, int activation, void* y, float* rstd, hipStream_t stream);
+/* Workspace of kdn_rms_norm_gated_bwd when dweight is requested: f32 per-block partials. */
+size_t kdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int D);
+/* Backward: dx (x's dtype), dg (g's dtype), dweight (weight's dtype, summed over rows in a fixed
+ * order); dy has x's dtype; any output may be NULL. */
+int kdn_rms_norm_gated_bwd(const void* x, int x_bf16, const void* g, int g_bf16, const void* weight, int w_bf16,
+                           const float* rstd, const void* dy, int64_t rows, int D, int activation, void* dx,
+                           void* dg, void* dweight, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,18 @@ What each function restates (reference = ngocbh/kalman-delta-networks):
   vendored in the reference, so this convention is PARITY UNPINNED.
 * ``iso_mixer`` / ``diag_mixer`` -- the composition order of iso_kdn.py:277-304 and
   diag_kdn.py:315-345 (frontend -> gain -> memory scan).
+* ``short_conv_silu``        -- fixed-length causal depthwise convolution (width 4, no bias)
+  + SiLU: FLA causal_conv1d as called at diag_kdn.py:75-96 and per q|k|v group by
+  iso_kdn_chunk.py:56-120 (packed forward kernel).  Pinned against torch's conv1d
+  (``short_conv_silu_conv1d``, a library routine) and brute force; FLA's own rounding points
+  are not in the reference tree (PARITY UNPINNED beyond the f32-then-round convention).
+* ``qkv_conv_backward``      -- the reference's packed backward kernel rule,
+  iso_kdn_chunk.py:127-254 + 379-437 (preactivation recomputed into x's dtype, then
+  g = dy s (1 + y (1 - s)); dx and dw sums); pinned by autograd of ``short_conv_silu`` (exact
+  when the preactivation is not rounded).
+* ``rms_norm_gated``         -- FLA FusedRMSNormGated(activation="sigmoid"|"swish") as the
+  layers' o_norm (iso_kdn.py:192-196,305-312; diag_kdn.py:216-219,346):
+  x rsqrt(mean x^2 + eps) w act(g).  FLA is not vendored: PARITY UNPINNED beyond this formula.
 
 How each is pinned (see tests/test_oracle_*.py):
   golden vectors written from the reference's own oracle files
@@ -425,3 +437,55 @@ def diag_mixer(q_raw, k_raw, v, retention_raw, omega_raw, r_raw, A_log, dt_bias,
     if output_final_state:
         return o, (S, fprec)
     return o
+
+
+# ----------------------------------------------------------------------------
+# Layer frontends around the scan (short convolution, gated output norm).
+# ----------------------------------------------------------------------------
+
+SHORT_CONV_WIDTH = 4
+
+
+def short_conv_silu(x, weight):
+    """silu(sum_j w[d, j] x[t - 3 + j, d]) with zero history; x [B,T,D], weight [D,4]."""
+    xw, ww = _w(x), _w(weight)
+    B, T, D = xw.shape
+    W = ww.shape[1]
+    pad = torch.cat([xw.new_zeros(B, W - 1, D), xw], 1)
+    y = sum(pad[:, j:j + T] * ww[:, j] for j in range(W))
+    return F.silu(y)
+
+
+def short_conv_silu_conv1d(x, weight):
+    """The same map through torch's grouped conv1d (independent formulation)."""
+    xw, ww = _w(x), _w(weight)
+    T, D = xw.shape[1], xw.shape[2]
+    y = F.conv1d(xw.transpose(1, 2), ww[:, None, :], padding=ww.shape[1] - 1, groups=D)[..., :T]
+    return F.silu(y.transpose(1, 2))
+
+
+def qkv_conv_backward(x, weight, dy, raw_dtype=None):
+    """Gradients of one convolution group by the reference kernel's rule: the preactivation is
+    recomputed and (for ``raw_dtype`` bf16) rounded as its raw_y buffer is, then
+    g = dy * s * (1 + y (1 - s)), dx[t] = sum_j w[j] g[t + 3 - j], dw[j] = sum_{b,t} g[t] x[t - 3 + j]."""
+    xw, ww, dyw = _w(x), _w(weight), _w(dy)
+    B, T, D = xw.shape
+    W = ww.shape[1]
+    pad = torch.cat([xw.new_zeros(B, W - 1, D), xw], 1)
+    y = sum(pad[:, j:j + T] * ww[:, j] for j in range(W))
+    if raw_dtype is not None:
+        y = y.to(raw_dtype).to(y.dtype)
+    s = torch.sigmoid(y)
+    g = dyw * s * (1 + y * (1 - s))
+    gpad = torch.cat([g, g.new_zeros(B, W - 1, D)], 1)
+    dx = sum(gpad[:, W - 1 - j:W - 1 - j + T] * ww[:, j] for j in range(W))
+    dw = torch.stack([(g * pad[:, j:j + T]).sum((0, 1)) for j in range(W)], -1)
+    return dx, dw
+
+
+def rms_norm_gated(x, g, weight, eps: float = 1e-5, activation: str = "sigmoid"):
+    """x * rsqrt(mean(x^2) + eps) * weight * act(g) over the last dim; act = sigmoid or swish."""
+    xw, gw, ww = _w(x), _w(g), _w(weight)
+    n = xw * torch.rsqrt(xw.square().mean(-1, keepdim=True) + eps)
+    a = torch.sigmoid(gw) if activation == "sigmoid" else gw * torch.sigmoid(gw)
+    return n * ww * a
