@@ -121,6 +121,52 @@ def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K
     return dict(ms_per_step=ms, tokens_per_s=B * T / (ms * 1e-3), kernels=per_kernel, dominant=dominant)
 
 
+def run_layer_frontends(steps: int, warmup: int, B: int, T: int, H: int, K: int):
+    """Layer frontends around the scan at the same shape: the packed q|k|v short convolution
+    (x [B,T,3HK] bf16) and the gated output norm (o, gate [B,T,H,K] bf16), fwd+bwd, timed per
+    kernel launch; HBM-bound, priced at their minimum bytes."""
+    import torch
+
+    from lit_gpt.kdn_ops import _lib
+    from lit_gpt.kdn_ops.gated_norm import FusedRMSNormGated
+    from lit_gpt.kdn_ops.short_conv import qkv_causal_conv1d
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(1)
+    D = H * K
+    x = torch.randn(B, T, 3 * D, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    w = (0.5 * torch.randn(3 * D, 4, generator=g)).to(torch.bfloat16).to(dev).requires_grad_(True)
+    dqkv = [torch.randn(B, T, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+    o = torch.randn(B, T, H, K, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    gate = torch.randn(B, T, H, K, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    do = torch.randn(B, T, H, K, generator=g).to(torch.bfloat16).to(dev)
+    norm = FusedRMSNormGated(K, activation="sigmoid", eps=1e-5).to(dev)
+
+    def step():
+        outs = qkv_causal_conv1d(x, w)
+        torch.autograd.grad(outs, (x, w), dqkv)
+        y = norm(o, gate)
+        torch.autograd.grad(y, (o, gate, norm.weight), do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with _lib.KernelTimer() as timer:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    N = B * T * D
+    nbytes = {"short_conv_fwd": 2 * N * 2, "short_conv_bwd": 3 * N * 2,  # per q|k|v group launch
+              "rms_norm_gated_fwd": 3 * N * 2 + B * T * H * 4, "rms_norm_gated_bwd": 5 * N * 2 + B * T * H * 4}
+    out = {}
+    for tag, nb in nbytes.items():
+        t = timer.mean_ms(tag) * 1e-3
+        achieved = nb / t / 1e9
+        out[tag] = dict(ms=round(t * 1e3, 4), bound="hbm", achieved=round(achieved, 2), peak=HBM_PEAK_GBS,
+                        unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), alg_bytes=int(nb))
+    return out
+
+
 def cpu_baseline(variant: str, slices: int, T: int, K: int, B: int, H: int):
     """Oracle tokenwise recurrence (fp32, torch autograd) fwd+bwd on `slices` (b, h) slices."""
     import torch
@@ -227,7 +273,10 @@ def main():
         "also": {f"{other}_kdn": {"value": round(res_other["tokens_per_s"], 1), "unit": "tokens/s",
                                   "ms_per_step": round(res_other["ms_per_step"], 4),
                                   "dominant": res_other["dominant"],
-                                  "kernels": res_other["kernels"]}},
+                                  "kernels": res_other["kernels"]},
+                 "layer_frontends": {"workload": "packed q|k|v short conv + SiLU and sigmoid-gated RMS norm, "
+                                                 "fwd+bwd, bf16, same B/T/H/d",
+                                     "kernels": run_layer_frontends(args.steps, args.warmup, B, T, H, K)}},
     }
     if args.calib_copy:
         calib_copy(args.calib_copy)

@@ -13,6 +13,8 @@
 //   gated norm    FLA FusedRMSNormGated(D, activation="sigmoid", eps) as lit_gpt/iso_kdn.py:192-196,
 //                 305-312 and lit_gpt/diag_kdn.py:216-219,346:
 //                 y = x rsqrt(mean x^2 + eps) * w * act(g), act = sigmoid (or swish: g sigmoid(g))
+#include <algorithm>
+
 #include "kdn_common.h"
 #include "../../include/kdn.h"
 
@@ -69,6 +71,27 @@ __device__ __forceinline__ void st1(T* p, float x) {
   if constexpr (sizeof(T) == 2) *p = f2bf(x);
   else *p = x;
 }
+// weights of 8 consecutive channels x kConvW taps (row-major [D][W]): 32 contiguous elements
+template <typename TW>
+__device__ __forceinline__ void ld_taps(const TW* p, float (&wt)[8][kConvW]) {
+  float f[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) ld8v(p + 8 * q, f + 8 * q);
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int j = 0; j < kConvW; ++j) wt[c][j] = f[c * kConvW + j];
+}
+// 8 channels of row t, or zeros outside [0, T): the load is unconditional (row clamped), so the
+// compiler issues every row's load before the first use
+template <typename TX>
+__device__ __forceinline__ void ld_row(const TX* base, int64_t st, int t, int T, float* f) {
+  const int tc = t < 0 ? 0 : (t >= T ? T - 1 : t);
+  ld8v(base + (int64_t)tc * st, f);
+  const bool ok = t >= 0 && t < T;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) f[c] = ok ? f[c] : 0.f;
+}
 __device__ __forceinline__ float silu_grad(float y) {  // d/dy [y sigmoid(y)]
   const float s = sigmoidf(y);
   return s * (1.f + y * (1.f - s));
@@ -88,22 +111,11 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(const TX* __restric
   const int cg = (int)(gid % CG), run = (int)((gid / CG) % NR), b = (int)(gid / ((int64_t)CG * NR));
   const int d0 = 8 * cg, t0 = run * kConvRun;
   float wt[8][kConvW];
-#pragma unroll
-  for (int c = 0; c < 8; ++c)
-#pragma unroll
-    for (int j = 0; j < kConvW; ++j) wt[c][j] = ld1(w + (int64_t)(d0 + c) * kConvW + j);
+  ld_taps(w + (int64_t)d0 * kConvW, wt);
   constexpr int NX = kConvRun + kConvW - 1;
   float xr[NX][8];
 #pragma unroll
-  for (int r = 0; r < NX; ++r) {
-    const int t = t0 - (kConvW - 1) + r;
-    if (t >= 0 && t < T) {
-      ld8v(x + (int64_t)b * xsb + (int64_t)t * xst + d0, xr[r]);
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) xr[r][c] = 0.f;
-    }
-  }
+  for (int r = 0; r < NX; ++r) ld_row(x + (int64_t)b * xsb + d0, xst, t0 - (kConvW - 1) + r, T, xr[r]);
 #pragma unroll
   for (int u = 0; u < kConvRun; ++u) {
     const int t = t0 + u;
@@ -121,50 +133,47 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(const TX* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Short convolution backward.  Thread = (b, 64-token block, 8-channel group); it walks the block
-// in 8-token runs.  g_t = dy_t silu'(y_t) with y the recomputed preactivation (rounded to x's
-// dtype when round_y, as the reference's raw_y buffer is), dx_t = sum_j w_j g_{t+3-j},
-// dw_j partial = sum_t g_t x_{t-3+j} over the block's tokens -> part[b * NB + blk][d][j].
+// Short convolution backward.  Block = 32 channel groups x 8 runs of 8 tokens (one 64-token
+// block of 256 channels); thread = (run, channel group), all its loads issued at once.
+// g_t = dy_t silu'(y_t) with y the recomputed preactivation (rounded to x's dtype when round_y,
+// as the reference's raw_y buffer is), dx_t = sum_j w_j g_{t+3-j}, and the dw_j partial
+// sum_t g_t x_{t-3+j} over the 64 tokens, reduced over the runs in LDS in a fixed order
+// -> part[b * NB + blk][d][j].
 // ---------------------------------------------------------------------------
+constexpr int kConvCG = 32;  // channel groups per backward block
 template <typename TX, typename TW>
 __global__ __launch_bounds__(256) void short_conv_bwd_kernel(const TX* __restrict__ x, int64_t xsb, int64_t xst,
                                                              const TW* __restrict__ w, const TX* __restrict__ dy,
                                                              int64_t dsb, int64_t dst, int B, int T, int D,
                                                              int round_y, TX* __restrict__ dx, int64_t gsb,
                                                              int64_t gst, float* __restrict__ part) {
-  const int CG = D / 8, NB = (T + kConvBlockT - 1) / kConvBlockT;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)B * NB * CG) return;
-  const int cg = (int)(gid % CG), blk = (int)((gid / CG) % NB), b = (int)(gid / ((int64_t)CG * NB));
-  const int d0 = 8 * cg;
-  float wt[8][kConvW], dw[8][kConvW];
+  __shared__ float s_dw[kConvBlockT / kConvRun][kConvCG * 8 * kConvW];
+  const int CG = D / 8, NB = (T + kConvBlockT - 1) / kConvBlockT, NCB = (CG + kConvCG - 1) / kConvCG;
+  const int cb = blockIdx.x % NCB, blk = (blockIdx.x / NCB) % NB, b = blockIdx.x / (NCB * NB);
+  const int lc = threadIdx.x % kConvCG, run = threadIdx.x / kConvCG;
+  const int cg = cb * kConvCG + lc, d0 = 8 * cg, t0 = blk * kConvBlockT + run * kConvRun;
+  const bool active = cg < CG && t0 < T;
+  float dw[8][kConvW];
 #pragma unroll
   for (int c = 0; c < 8; ++c)
 #pragma unroll
-    for (int j = 0; j < kConvW; ++j) wt[c][j] = ld1(w + (int64_t)(d0 + c) * kConvW + j), dw[c][j] = 0.f;
-  constexpr int NX = kConvRun + 2 * (kConvW - 1);  // x rows t0-3 .. t0+run+2
-  constexpr int NG = kConvRun + kConvW - 1;        // g at t0 .. t0+run+2
-  for (int t0 = blk * kConvBlockT; t0 < min((blk + 1) * kConvBlockT, T); t0 += kConvRun) {
+    for (int j = 0; j < kConvW; ++j) dw[c][j] = 0.f;
+  if (active) {
+    float wt[8][kConvW];
+    ld_taps(w + (int64_t)d0 * kConvW, wt);
+    constexpr int NX = kConvRun + 2 * (kConvW - 1);  // x rows t0-3 .. t0+run+2
+    constexpr int NG = kConvRun + kConvW - 1;        // g at t0 .. t0+run+2
     float xr[NX][8], dyr[NG][8];
 #pragma unroll
-    for (int r = 0; r < NX; ++r) {
-      const int t = t0 - (kConvW - 1) + r;
-      if (t >= 0 && t < T) {
-        ld8v(x + (int64_t)b * xsb + (int64_t)t * xst + d0, xr[r]);
-      } else {
+    for (int r = 0; r < NX; ++r) ld_row(x + (int64_t)b * xsb + d0, xst, t0 - (kConvW - 1) + r, T, xr[r]);
+    if (dy) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) xr[r][c] = 0.f;
-      }
-    }
+      for (int r = 0; r < NG; ++r) ld_row(dy + (int64_t)b * dsb + d0, dst, t0 + r, T, dyr[r]);
+    } else {
 #pragma unroll
-    for (int r = 0; r < NG; ++r) {
-      const int t = t0 + r;
-      if (dy && t < T) {
-        ld8v(dy + (int64_t)b * dsb + (int64_t)t * dst + d0, dyr[r]);
-      } else {
+      for (int r = 0; r < NG; ++r)
 #pragma unroll
         for (int c = 0; c < 8; ++c) dyr[r][c] = 0.f;
-      }
     }
     float gr[NG][8];
 #pragma unroll
@@ -195,28 +204,45 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(const TX* __restric
     }
   }
   if (!part) return;
-  float* pp = part + ((int64_t)b * NB + blk) * D * kConvW + (int64_t)d0 * kConvW;
+  // [run][tap][channel-in-group][group]: consecutive lanes (groups) hit consecutive banks
 #pragma unroll
   for (int c = 0; c < 8; ++c)
-    reinterpret_cast<float4*>(pp)[c] = float4{dw[c][0], dw[c][1], dw[c][2], dw[c][3]};
+#pragma unroll
+    for (int j = 0; j < kConvW; ++j) s_dw[run][(j * 8 + c) * kConvCG + lc] = dw[c][j];
+  __syncthreads();
+  // this block's 256 channels x 4 taps, summed over the 8 runs in order
+  for (int e = threadIdx.x; e < kConvCG * 8 * kConvW; e += 256) {
+    const int q = e / kConvW, j = e % kConvW;  // q = local channel (group-major), j = tap
+    const int lg = q / 8, c = q % 8, d = cb * kConvCG * 8 + q;
+    if (d >= D) continue;
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < kConvBlockT / kConvRun; ++r) acc += s_dw[r][(j * 8 + c) * kConvCG + lg];
+    part[((int64_t)b * NB + blk) * D * kConvW + (int64_t)d * kConvW + j] = acc;
+  }
 }
 
-// out[j] = sum_p part[p * n + j], fixed order (4 stripes of p, combined in order).  grid ceil(n/64).
+// out[j] = sum_p part[p * n + j] in a fixed order: block = 16 columns x 16 stripes of p, the
+// stripes combined by a fixed LDS tree.  grid ceil(n/16).
 template <typename TO>
 __global__ __launch_bounds__(256) void sum_partials_kernel(const float* __restrict__ part, int NP, int64_t n,
                                                            TO* __restrict__ out) {
-  __shared__ float s[4][64];
-  const int jj = threadIdx.x & 63, st4 = threadIdx.x >> 6;
-  const int64_t j = (int64_t)blockIdx.x * 64 + jj;
+  __shared__ float s[16][17];
+  const int jj = threadIdx.x & 15, st = threadIdx.x >> 4;
+  const int64_t j = (int64_t)blockIdx.x * 16 + jj;
   float a0 = 0.f, a1 = 0.f;
   if (j < n) {
-    int p = st4;
-    for (; p + 4 < NP; p += 8) a0 += part[(int64_t)p * n + j], a1 += part[(int64_t)(p + 4) * n + j];
-    for (; p < NP; p += 4) a0 += part[(int64_t)p * n + j];
+    int p = st;
+    for (; p + 16 < NP; p += 32) a0 += part[(int64_t)p * n + j], a1 += part[(int64_t)(p + 16) * n + j];
+    for (; p < NP; p += 16) a0 += part[(int64_t)p * n + j];
   }
-  s[st4][jj] = a0 + a1;
+  s[st][jj] = a0 + a1;
   __syncthreads();
-  if (st4 == 0 && j < n) st1(out + j, (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]));
+  for (int h = 8; h > 0; h >>= 1) {
+    if (st < h) s[st][jj] += s[st + h][jj];
+    __syncthreads();
+  }
+  if (st == 0 && j < n) st1(out + j, s[0][jj]);
 }
 
 // ---------------------------------------------------------------------------
@@ -247,8 +273,9 @@ __global__ __launch_bounds__(256) void rms_gated_fwd_kernel(const TX* __restrict
   const int64_t rr = ok ? row : 0;
   ld8v(x + rr * D + d0, xv);
   ld8v(g + rr * D + d0, gv);
+  ld8v(w + d0, wv);
 #pragma unroll
-  for (int c = 0; c < 8; ++c) wv[c] = ld1(w + d0 + c), ss += xv[c] * xv[c];
+  for (int c = 0; c < 8; ++c) ss += xv[c] * xv[c];
   ss = row_sum(ss, LPR);
   const float rs = rsqrtf(ss / (float)D + eps);
   float o[8];
@@ -259,6 +286,9 @@ __global__ __launch_bounds__(256) void rms_gated_fwd_kernel(const TX* __restrict
   if (sub == 0 && rstd) rstd[row] = rs;
 }
 
+// Backward: grid-stride over row groups with a fixed grid; each thread accumulates its 8
+// channels' dweight over its rows, then the block sums its row slots in order -> part[block][D].
+constexpr int kRmsBwdBlocks = 1024;
 template <typename TX, typename TG, typename TW>
 __global__ __launch_bounds__(256) void rms_gated_bwd_kernel(const TX* __restrict__ x, const TG* __restrict__ g,
                                                             const TW* __restrict__ w, const float* __restrict__ rstd,
@@ -268,46 +298,49 @@ __global__ __launch_bounds__(256) void rms_gated_bwd_kernel(const TX* __restrict
   __shared__ float s_dw[256 * 8];
   const int LPR = D / 8, RPB = 256 / LPR;
   const int r_in = threadIdx.x / LPR;
-  const int64_t row = (int64_t)blockIdx.x * RPB + r_in;
   const int sub = threadIdx.x % LPR, d0 = 8 * sub;
-  const bool ok = row < rows;
-  const int64_t rr = ok ? row : 0;
-  float xv[8], gv[8], dyv[8], wv[8];
-  ld8v(x + rr * D + d0, xv);
-  ld8v(g + rr * D + d0, gv);
-  ld8v(dy + rr * D + d0, dyv);
-  const float rs = rstd[rr];
-  float dn[8], n[8], dot = 0.f, dwv[8];
+  float wv[8], dwv[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    wv[c] = ld1(w + d0 + c);
-    n[c] = xv[c] * rs;
-    const float a = gate_act(gv[c], act);
-    dn[c] = dyv[c] * wv[c] * a;
-    dot += dn[c] * n[c];
-    dwv[c] = ok ? dyv[c] * n[c] * a : 0.f;
-  }
-  dot = row_sum(dot, LPR) / (float)D;
-  if (ok) {
-    float o[8], og[8];
+  for (int c = 0; c < 8; ++c) dwv[c] = 0.f;
+  ld8v(w + d0, wv);
+  for (int64_t base = (int64_t)blockIdx.x * RPB; base < rows; base += (int64_t)gridDim.x * RPB) {
+    const int64_t row = base + r_in;
+    const bool ok = row < rows;
+    const int64_t rr = ok ? row : 0;
+    float xv[8], gv[8], dyv[8];
+    ld8v(x + rr * D + d0, xv);
+    ld8v(g + rr * D + d0, gv);
+    ld8v(dy + rr * D + d0, dyv);
+    const float rs = rstd[rr];
+    float dn[8], n[8], av[8], dot = 0.f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      o[c] = rs * (dn[c] - n[c] * dot);
-      og[c] = dyv[c] * n[c] * wv[c] * gate_grad(gv[c], act);
+      n[c] = xv[c] * rs;
+      av[c] = gate_act(gv[c], act);
+      dn[c] = dyv[c] * wv[c] * av[c];
+      dot += dn[c] * n[c];
     }
-    if (dx) st8v(dx + row * D + d0, o);
-    if (dg) st8v(dg + row * D + d0, og);
+    dot = row_sum(dot, LPR) / (float)D;
+    if (ok) {
+      float o[8], og[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        o[c] = rs * (dn[c] - n[c] * dot);
+        og[c] = dyv[c] * n[c] * wv[c] * gate_grad(gv[c], act);
+        dwv[c] += dyv[c] * n[c] * av[c];
+      }
+      if (dx) st8v(dx + row * D + d0, o);
+      if (dg) st8v(dg + row * D + d0, og);
+    }
   }
-  // per-block dweight partial: sum over the block's rows, fixed order
+  if (!part) return;
 #pragma unroll
   for (int c = 0; c < 8; ++c) s_dw[r_in * D + d0 + c] = dwv[c];
   __syncthreads();
-  if (part) {
-    for (int d = threadIdx.x; d < D; d += 256) {
-      float s = 0.f;
-      for (int q = 0; q < RPB; ++q) s += s_dw[q * D + d];
-      part[(int64_t)blockIdx.x * D + d] = s;
-    }
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float s = 0.f;
+    for (int q = 0; q < RPB; ++q) s += s_dw[q * D + d];
+    part[(int64_t)blockIdx.x * D + d] = s;
   }
 }
 
@@ -322,7 +355,7 @@ int kdn_short_conv_fwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_
                        int w_bf16, int B, int T, int D, int W, void* y, int64_t y_stride_b, int64_t y_stride_t,
                        hipStream_t stream) {
   if (B < 0 || T < 0 || D <= 0 || W != kConvW || D % 8 != 0 || !x || !weight || !y) return KDN_ERR_ARG;
-  if (!al16(x) || !al16(y) || x_stride_t % 8 != 0 || x_stride_b % 8 != 0 || y_stride_t % 8 != 0 ||
+  if (!al16(x) || !al16(y) || !al16(weight) || x_stride_t % 8 != 0 || x_stride_b % 8 != 0 || y_stride_t % 8 != 0 ||
       y_stride_b % 8 != 0)
     return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
@@ -351,16 +384,15 @@ int kdn_short_conv_bwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_
                        int W, int round_preactivation, void* dx, int64_t dx_stride_b, int64_t dx_stride_t,
                        void* dweight, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (B < 0 || T < 0 || D <= 0 || W != kConvW || D % 8 != 0 || !x || !weight) return KDN_ERR_ARG;
-  if (!al16(x) || (dy && !al16(dy)) || (dx && !al16(dx)) || x_stride_t % 8 || x_stride_b % 8 ||
+  if (!al16(x) || !al16(weight) || (dy && !al16(dy)) || (dx && !al16(dx)) || x_stride_t % 8 || x_stride_b % 8 ||
       (dy && (dy_stride_t % 8 || dy_stride_b % 8)) || (dx && (dx_stride_t % 8 || dx_stride_b % 8)))
     return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
   if (dweight && (!workspace || workspace_bytes < kdn_short_conv_bwd_workspace_size(B, T, D) ||
                   !al16(workspace)))
     return KDN_ERR_ARG;
-  const int NB = (T + kConvBlockT - 1) / kConvBlockT;
-  const int64_t threads = (int64_t)B * NB * (D / 8);
-  const dim3 grid((unsigned)((threads + 255) / 256));
+  const int NB = (T + kConvBlockT - 1) / kConvBlockT, NCB = (D / 8 + kConvCG - 1) / kConvCG;
+  const dim3 grid((unsigned)((int64_t)B * NB * NCB));
   float* part = dweight ? (float*)workspace : nullptr;
   if (!dweight && !dx) return 0;
 #define KDN_CONV_BWD(TX, TW)                                                                                       \
@@ -375,7 +407,7 @@ int kdn_short_conv_bwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_
   KDN_CHECK_LAUNCH();
   if (dweight) {
     const int64_t n = (int64_t)D * kConvW;
-    const dim3 rg((unsigned)((n + 63) / 64));
+    const dim3 rg((unsigned)((n + 15) / 16));
     if (w_bf16)
       hipLaunchKernelGGL((sum_partials_kernel<bf16_t>), rg, dim3(256), 0, stream, part, B * NB, n, (bf16_t*)dweight);
     else
@@ -392,7 +424,7 @@ int kdn_rms_norm_gated_fwd(const void* x, int x_bf16, const void* g, int g_bf16,
                            int64_t rows, int D, float eps, int activation, void* y, float* rstd,
                            hipStream_t stream) {
   if (rows < 0 || D <= 0 || !rms_shape_ok(D) || (activation != 0 && activation != 1) || !(eps >= 0.f)) return KDN_ERR_ARG;
-  if (!x || !g || !weight || !y || !al16(x) || !al16(g) || !al16(y)) return KDN_ERR_ARG;
+  if (!x || !g || !weight || !y || !al16(x) || !al16(g) || !al16(y) || !al16(weight)) return KDN_ERR_ARG;
   if (rows == 0) return 0;
   const int RPB = 256 / (D / 8);
   const dim3 grid((unsigned)((rows + RPB - 1) / RPB));
@@ -414,20 +446,21 @@ int kdn_rms_norm_gated_fwd(const void* x, int x_bf16, const void* g, int g_bf16,
 size_t kdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int D) {
   if (rows <= 0 || D <= 0 || !rms_shape_ok(D)) return 0;
   const int RPB = 256 / (D / 8);
-  return (size_t)(((rows + RPB - 1) / RPB) * D) * sizeof(float);
+  const int64_t nblk = std::min<int64_t>((rows + RPB - 1) / RPB, kRmsBwdBlocks);
+  return (size_t)(nblk * D) * sizeof(float);
 }
 
 int kdn_rms_norm_gated_bwd(const void* x, int x_bf16, const void* g, int g_bf16, const void* weight, int w_bf16,
                            const float* rstd, const void* dy, int64_t rows, int D, int activation, void* dx,
                            void* dg, void* dweight, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (rows < 0 || D <= 0 || !rms_shape_ok(D) || (activation != 0 && activation != 1)) return KDN_ERR_ARG;
-  if (!x || !g || !weight || !rstd || !dy || !al16(x) || !al16(g) || !al16(dy) || (dx && !al16(dx)) ||
+  if (!x || !g || !weight || !rstd || !dy || !al16(x) || !al16(g) || !al16(dy) || !al16(weight) || (dx && !al16(dx)) ||
       (dg && !al16(dg)))
     return KDN_ERR_ARG;
   if (rows == 0) return 0;
   if (dweight && (!workspace || workspace_bytes < kdn_rms_norm_gated_bwd_workspace_size(rows, D))) return KDN_ERR_ARG;
   const int RPB = 256 / (D / 8);
-  const int NBLK = (int)((rows + RPB - 1) / RPB);
+  const int NBLK = (int)std::min<int64_t>((rows + RPB - 1) / RPB, kRmsBwdBlocks);
   float* part = dweight ? (float*)workspace : nullptr;
 #define KDN_RMS_BWD(TX, TG, TW)                                                                                     \
   hipLaunchKernelGGL((rms_gated_bwd_kernel<TX, TG, TW>), dim3(NBLK), dim3(256), 0, stream, (const TX*)x,           \
@@ -443,7 +476,7 @@ int kdn_rms_norm_gated_bwd(const void* x, int x_bf16, const void* g, int g_bf16,
 #undef KDN_RMS_BWD
   KDN_CHECK_LAUNCH();
   if (dweight) {
-    const dim3 rg((unsigned)((D + 63) / 64));
+    const dim3 rg((unsigned)((D + 15) / 16));
     if (w_bf16)
       hipLaunchKernelGGL((sum_partials_kernel<bf16_t>), rg, dim3(256), 0, stream, part, NBLK, (int64_t)D, (bf16_t*)dweight);
     else
