@@ -6,11 +6,12 @@ Drop-in for the hot-path entry points of the reference module
 * ``_iso_kdn_gate_precumsum_paired``  (reference :1395-1436)
 * ``iso_kdn_gain``                    (reference :1965-2031)
 * ``_chunk_kda_precumsum_paired``     (reference :2241-2285)
+* ``qkv_causal_conv1d``               (reference :468-478; implemented in ``short_conv.py``)
 
 with the same argument order, dtypes, return tuples, autograd.Function structure and
 Python-side errors.  All arithmetic runs in the HIP library (``libkdn_hip.so``); there is
-no PyTorch or CPU fallback.  The layer frontend helpers of the reference module (packed
-projections, QKV short convolution) are outside this package's scope.
+no PyTorch or CPU fallback.  The packed projections of the reference module (plain GEMMs,
+iso_kdn_chunk.py:480-729) are not part of this package.
 """
 from __future__ import annotations
 
@@ -20,6 +21,7 @@ from numbers import Real
 import torch
 
 from . import _lib, _memscan
+from .short_conv import qkv_causal_conv1d  # the reference module also defines it (:468-478)
 
 ISO_GATE_CHUNK_SIZE = 64
 KDA_CHUNK_SIZE = 64
@@ -406,4 +408,4 @@ def _chunk_kda_precumsum_paired(q, k, v, g_cumsum, beta, scale=None):
                                             g_cumsum.contiguous(), beta.float().contiguous(), scale)
 
 
-__all__ = ("_chunk_kda_precumsum_paired", "_iso_kdn_gate_precumsum_paired", "iso_kdn_gain")
+__all__ = ("_chunk_kda_precumsum_paired", "_iso_kdn_gate_precumsum_paired", "iso_kdn_gain", "qkv_causal_conv1d")
