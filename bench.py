@@ -167,6 +167,94 @@ def run_layer_frontends(steps: int, warmup: int, B: int, T: int, H: int, K: int)
     return out
 
 
+def run_config4(name: str, steps: int, warmup: int, B: int, T: int):
+    """The whole random-init config-4 model (``name``, mamba init) on synthetic token ids.
+
+    * forward (the config-4 workload): bf16 weights, eval mode, no autograd; logits over the
+      padded vocabulary.  The KDN-mixer share is one mixer layer's forward at the same shape,
+      timed alone, times the layer count, over the model's forward time.
+    * training step (reported beside it): fp32 master weights, forward under CUDA bf16 autocast,
+      cross-entropy, backward, fused AdamW; mixer share from one mixer layer's fwd+bwd alone.
+    """
+    import torch
+    import torch.nn.functional as F
+
+    from lit_gpt.model import GPT
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = GPT.from_name(name)
+    model.init_weights()
+    cfg = model.config
+    V = cfg.padded_vocab_size
+    idx = torch.randint(0, cfg.vocab_size, (B, T + 1), device=dev)
+    x = torch.randn(B, T, cfg.n_embd, device=dev, requires_grad=True)
+    dy = torch.randn(B, T, cfg.n_embd, device=dev, dtype=torch.bfloat16)
+    mixer = model.transformer.h[0].attn
+
+    def timed(fn, n, w):
+        for _ in range(w):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(n):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / n
+
+    # training step
+    model.train()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.1, fused=True)
+
+    def train_step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = model(idx[:, :-1])
+        loss = F.cross_entropy(logits.float().view(-1, V), idx[:, 1:].reshape(-1))
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+
+    def mixer_fwd_bwd():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = mixer(x)[0]
+        torch.autograd.grad(out, [x] + list(mixer.parameters()), dy)
+
+    train_ms = timed(train_step, steps, warmup)
+    mixer_train_ms = timed(mixer_fwd_bwd, steps, warmup)
+    del opt
+    torch.cuda.empty_cache()
+
+    # forward (config 4)
+    model = model.to(torch.bfloat16).eval()
+    xb = x.detach().to(torch.bfloat16)
+
+    @torch.no_grad()
+    def forward():
+        model(idx[:, :-1])
+
+    @torch.no_grad()
+    def mixer_fwd():
+        mixer(xb)
+
+    fwd_ms = timed(forward, steps, warmup)
+    mixer_fwd_ms = timed(mixer_fwd, steps, warmup)
+    del model
+    torch.cuda.empty_cache()
+    L = cfg.n_layer
+    return {"workload": f"{name} forward, random init (mamba), bf16 weights, synthetic token ids, logits over "
+                        f"{V}; training step beside it",
+            "B": B, "T": T, "n_layer": L, "value": round(B * T / (fwd_ms * 1e-3), 1), "unit": "tokens/s",
+            "ms_per_forward": round(fwd_ms, 3), "mixer_layer_fwd_ms": round(mixer_fwd_ms, 3),
+            "mixer_share": round(L * mixer_fwd_ms / fwd_ms, 4),
+            "train_step": {"what": "fwd (bf16 autocast, fp32 master weights) + cross-entropy + bwd + fused AdamW",
+                           "value": round(B * T / (train_ms * 1e-3), 1), "unit": "tokens/s",
+                           "ms_per_step": round(train_ms, 3), "mixer_layer_fwd_bwd_ms": round(mixer_train_ms, 3),
+                           "mixer_share": round(L * mixer_train_ms / train_ms, 4)}}
+
+
 def cpu_baseline(variant: str, slices: int, T: int, K: int, B: int, H: int):
     """Oracle tokenwise recurrence (fp32, torch autograd) fwd+bwd on `slices` (b, h) slices."""
     import torch
@@ -225,6 +313,7 @@ def main():
     ap.add_argument("--variant", choices=("iso", "diag"), default="iso")
     ap.add_argument("--cpu-slices", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-config4", action="store_true", help="skip the whole-model (config 4) training step")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain copy of MIB MiB (PMC byte-counter calibration)")
     ap.add_argument("--B", type=int, default=4)
@@ -278,6 +367,8 @@ def main():
                                                  "fwd+bwd, bf16, same B/T/H/d",
                                      "kernels": run_layer_frontends(args.steps, args.warmup, B, T, H, K)}},
     }
+    if not args.no_config4:
+        line["also"]["config4"] = run_config4(f"{main_v}_kdn_1.3B", min(args.steps, 10), args.warmup, 1, T)
     if args.calib_copy:
         calib_copy(args.calib_copy)
     if not args.no_cpu:

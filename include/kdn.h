@@ -163,6 +163,18 @@ int kdn_short_conv_bwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_
                        int W, int round_preactivation, void* dx, int64_t dx_stride_b, int64_t dx_stride_t,
                        void* dweight, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* RMS norm over wide dense rows (the model's block norm FusedRMSNorm, reference
+ * lit_gpt/rmsnorm.py:1182-1216, no residual / dropout): y = x rsqrt(mean(x^2) + eps) * weight, f32 math,
+ * y in x's dtype, rstd [rows] f32 (nullable).  D % 8 == 0, D <= 8192. */
+int kdn_rms_norm_fwd(const void* x, int x_bf16, const void* weight, int w_bf16, int64_t rows, int D, float eps,
+                     void* y, float* rstd, hipStream_t stream);
+/* Workspace of kdn_rms_norm_bwd when dweight is requested (f32 partials). */
+size_t kdn_rms_norm_bwd_workspace_size(int64_t rows, int D);
+/* Backward: dx (x's dtype), dweight (weight's dtype, fixed-order sum); dy has x's dtype. */
+int kdn_rms_norm_bwd(const void* x, int x_bf16, const void* weight, int w_bf16, const float* rstd, const void* dy,
+                     int64_t rows, int D, void* dx, void* dweight, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
+
 /* Gated RMS norm over the last dimension D of dense rows:
  * y = x rsqrt(mean(x^2) + eps) * weight * act(g), act = sigmoid (activation 0) or g sigmoid(g)
  * (activation 1, "swish"); f32 math, y in x's dtype, rstd [rows] f32 saved (nullable).

@@ -344,6 +344,101 @@ __global__ __launch_bounds__(256) void rms_gated_bwd_kernel(const TX* __restrict
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block RMS norm over wide rows (the model's FusedRMSNorm, D = n_embd): one workgroup per row,
+// 8 elements per thread per pass, block sum through LDS.  y = x rsqrt(mean x^2 + eps) * w.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <typename TX, typename TW>
+__global__ __launch_bounds__(256) void rms_row_fwd_kernel(const TX* __restrict__ x, const TW* __restrict__ w, int D,
+                                                          float eps, TX* __restrict__ y, float* __restrict__ rstd) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const TX* xr = x + row * D;
+  float ss = 0.f;
+  for (int d0 = 8 * threadIdx.x; d0 < D; d0 += 8 * 256) {
+    float v[8];
+    ld8v(xr + d0, v);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss += v[c] * v[c];
+  }
+  const float rs = rsqrtf(block_sum256(ss, red) / (float)D + eps);
+  for (int d0 = 8 * threadIdx.x; d0 < D; d0 += 8 * 256) {
+    float v[8], wv[8];
+    ld8v(xr + d0, v);
+    ld8v(w + d0, wv);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = v[c] * rs * wv[c];
+    st8v(y + row * D + d0, v);
+  }
+  if (threadIdx.x == 0 && rstd) rstd[row] = rs;
+}
+
+// backward: dx = rstd (dy w - n mean(dy w n)), n = x rstd; dweight partial per workgroup
+// (one row) accumulated over a fixed stride of rows: part[blockIdx.x][D]
+template <typename TX, typename TW>
+__global__ __launch_bounds__(256) void rms_row_bwd_kernel(const TX* __restrict__ x, const TW* __restrict__ w,
+                                                          const float* __restrict__ rstd, const TX* __restrict__ dy,
+                                                          int64_t rows, int D, TX* __restrict__ dx,
+                                                          float* __restrict__ part) {
+  __shared__ float red[4];
+  constexpr int MAXG = 4;  // up to 4 passes of 2048 elements per thread-slot: D <= 8192
+  float dwv[MAXG][8];
+#pragma unroll
+  for (int q = 0; q < MAXG; ++q)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) dwv[q][c] = 0.f;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float rs = rstd[row];
+    float dot = 0.f;
+#pragma unroll
+    for (int q = 0; q < MAXG; ++q) {
+      const int d0 = 8 * threadIdx.x + 2048 * q;
+      if (d0 >= D) break;
+      float xv[8], dv[8], wv[8];
+      ld8v(x + row * D + d0, xv);
+      ld8v(dy + row * D + d0, dv);
+      ld8v(w + d0, wv);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float n = xv[c] * rs;
+        dot += dv[c] * wv[c] * n;
+        dwv[q][c] += dv[c] * n;
+      }
+    }
+    dot = block_sum256(dot, red) / (float)D;
+    if (dx) {
+#pragma unroll
+      for (int q = 0; q < MAXG; ++q) {
+        const int d0 = 8 * threadIdx.x + 2048 * q;
+        if (d0 >= D) break;
+        float xv[8], dv[8], wv[8], o[8];
+        ld8v(x + row * D + d0, xv);
+        ld8v(dy + row * D + d0, dv);
+        ld8v(w + d0, wv);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o[c] = rs * (dv[c] * wv[c] - xv[c] * rs * dot);
+        st8v(dx + row * D + d0, o);
+      }
+    }
+  }
+  if (!part) return;
+#pragma unroll
+  for (int q = 0; q < MAXG; ++q) {
+    const int d0 = 8 * threadIdx.x + 2048 * q;
+    if (d0 >= D) break;
+    st8v(part + (int64_t)blockIdx.x * D + d0, dwv[q]);
+  }
+}
+constexpr int kRmsRowBwdBlocks = 512;
+
 bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -419,6 +514,57 @@ int kdn_short_conv_bwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_
 
 // ---------------------------------------------------------------------------------- gated norm
 static bool rms_shape_ok(int D) { return D % 8 == 0 && D / 8 <= 64 && (D / 8 & (D / 8 - 1)) == 0; }
+
+// ---------------------------------------------------------------------------------- block RMS norm
+int kdn_rms_norm_fwd(const void* x, int x_bf16, const void* weight, int w_bf16, int64_t rows, int D, float eps,
+                     void* y, float* rstd, hipStream_t stream) {
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 8192 || !(eps >= 0.f)) return KDN_ERR_ARG;
+  if (!x || !weight || !y || !al16(x) || !al16(weight) || !al16(y)) return KDN_ERR_ARG;
+  if (rows == 0) return 0;
+  const dim3 grid((unsigned)rows);
+#define KDN_ROW_FWD(TX, TW)                                                                                        \
+  hipLaunchKernelGGL((rms_row_fwd_kernel<TX, TW>), grid, dim3(256), 0, stream, (const TX*)x, (const TW*)weight, D, \
+                     eps, (TX*)y, rstd)
+  if (x_bf16) { if (w_bf16) KDN_ROW_FWD(bf16_t, bf16_t); else KDN_ROW_FWD(bf16_t, float); }
+  else { if (w_bf16) KDN_ROW_FWD(float, bf16_t); else KDN_ROW_FWD(float, float); }
+#undef KDN_ROW_FWD
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+size_t kdn_rms_norm_bwd_workspace_size(int64_t rows, int D) {
+  if (rows <= 0 || D <= 0) return 0;
+  return (size_t)(std::min<int64_t>(rows, kRmsRowBwdBlocks) * D) * sizeof(float);
+}
+
+int kdn_rms_norm_bwd(const void* x, int x_bf16, const void* weight, int w_bf16, const float* rstd, const void* dy,
+                     int64_t rows, int D, void* dx, void* dweight, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 8192) return KDN_ERR_ARG;
+  if (!x || !weight || !rstd || !dy || !al16(x) || !al16(weight) || !al16(dy) || (dx && !al16(dx)))
+    return KDN_ERR_ARG;
+  if (rows == 0) return 0;
+  if (dweight && (!workspace || workspace_bytes < kdn_rms_norm_bwd_workspace_size(rows, D) || !al16(workspace)))
+    return KDN_ERR_ARG;
+  const int NBLK = (int)std::min<int64_t>(rows, kRmsRowBwdBlocks);
+  float* part = dweight ? (float*)workspace : nullptr;
+#define KDN_ROW_BWD(TX, TW)                                                                                       \
+  hipLaunchKernelGGL((rms_row_bwd_kernel<TX, TW>), dim3(NBLK), dim3(256), 0, stream, (const TX*)x,               \
+                     (const TW*)weight, rstd, (const TX*)dy, rows, D, (TX*)dx, part)
+  if (x_bf16) { if (w_bf16) KDN_ROW_BWD(bf16_t, bf16_t); else KDN_ROW_BWD(bf16_t, float); }
+  else { if (w_bf16) KDN_ROW_BWD(float, bf16_t); else KDN_ROW_BWD(float, float); }
+#undef KDN_ROW_BWD
+  KDN_CHECK_LAUNCH();
+  if (dweight) {
+    const dim3 rg((unsigned)((D + 15) / 16));
+    if (w_bf16)
+      hipLaunchKernelGGL((sum_partials_kernel<bf16_t>), rg, dim3(256), 0, stream, part, NBLK, (int64_t)D, (bf16_t*)dweight);
+    else
+      hipLaunchKernelGGL((sum_partials_kernel<float>), rg, dim3(256), 0, stream, part, NBLK, (int64_t)D, (float*)dweight);
+    KDN_CHECK_LAUNCH();
+  }
+  return 0;
+}
 
 int kdn_rms_norm_gated_fwd(const void* x, int x_bf16, const void* g, int g_bf16, const void* weight, int w_bf16,
                            int64_t rows, int D, float eps, int activation, void* y, float* rstd,

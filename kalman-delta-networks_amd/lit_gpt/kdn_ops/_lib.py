@@ -40,13 +40,17 @@ _SIGS = {
     "kdn_short_conv_fwd": "pillpiiiiiplls",
     "kdn_short_conv_bwd_workspace_size": "iii",
     "kdn_short_conv_bwd": "pillpiplliiiiipllppzs",
+    "kdn_rms_norm_fwd": "pipilifpps",
+    "kdn_rms_norm_bwd_workspace_size": "li",
+    "kdn_rms_norm_bwd": "pipipplipppzs",
     "kdn_rms_norm_gated_fwd": "pipipilifipps",
     "kdn_rms_norm_gated_bwd_workspace_size": "li",
     "kdn_rms_norm_gated_bwd": "pipipippliippppzs",
 }
 _SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_iso_gain_workspace_size", "kdn_diag_frontend_bwd_workspace_size",
              "kdn_diag_gain_workspace_size", "kdn_mem_saved_size", "kdn_mem_bwd_workspace_size",
-             "kdn_short_conv_bwd_workspace_size", "kdn_rms_norm_gated_bwd_workspace_size"}
+             "kdn_short_conv_bwd_workspace_size", "kdn_rms_norm_gated_bwd_workspace_size",
+             "kdn_rms_norm_bwd_workspace_size"}
 _CT = {"p": ctypes.c_void_p, "i": ctypes.c_int, "l": ctypes.c_int64, "f": ctypes.c_float,
        "z": ctypes.c_size_t, "s": ctypes.c_void_p}
 

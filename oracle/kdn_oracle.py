@@ -39,6 +39,17 @@ What each function restates (reference = ngocbh/kalman-delta-networks):
 * ``rms_norm_gated``         -- FLA FusedRMSNormGated(activation="sigmoid"|"swish") as the
   layers' o_norm (iso_kdn.py:192-196,305-312; diag_kdn.py:216-219,346):
   x rsqrt(mean x^2 + eps) w act(g).  FLA is not vendored: PARITY UNPINNED beyond this formula.
+* ``rms_norm``               -- the model's FusedRMSNorm (rmsnorm.py:1141-1216, LayerNormFn with
+  is_rms_norm, no residual): pinned against torch's F.rms_norm (a library routine).
+* ``linear`` / ``amp_round`` / ``swiglu`` -- F.linear and SwiGLU (model.py:452-464), with the bf16
+  rounding points of CUDA bf16 autocast when ``amp``; swiglu pinned by a closed form.
+* ``iso_layer`` / ``diag_layer`` -- the layer compositions of iso_kdn.py:262-314 and
+  diag_kdn.py:259-357 (projection slices, convolutions, mixer, gated norm, output projection);
+  ``gpt_forward`` -- GPT/Block of model.py:95-162,217-298.  Pinned by the reference's own
+  parameter totals (the modules' shapes), closed-form reductions (zero output projections make
+  every block the identity plus its MLP; zero MLP and mixer outputs leave
+  lm_head(ln_f(wte[idx]))), and the mixer composition's own pins above.  Which projection slice
+  feeds which operand is a restatement of the layer files: PARTIALLY PINNED.
 
 How each is pinned (see tests/test_oracle_*.py):
   golden vectors written from the reference's own oracle files
@@ -489,3 +500,103 @@ def rms_norm_gated(x, g, weight, eps: float = 1e-5, activation: str = "sigmoid")
     n = xw * torch.rsqrt(xw.square().mean(-1, keepdim=True) + eps)
     a = torch.sigmoid(gw) if activation == "sigmoid" else gw * torch.sigmoid(gw)
     return n * ww * a
+
+
+# ----------------------------------------------------------------------------
+# The config-4 block stack: layers, block, GPT (compositions of the above).
+# ----------------------------------------------------------------------------
+
+def rms_norm(x, weight, eps: float = 1e-5):
+    """FusedRMSNorm without residual/dropout (rmsnorm.py:1141-1216): x rsqrt(mean x^2 + eps) w."""
+    xw = _w(x)
+    return xw * torch.rsqrt(xw.square().mean(-1, keepdim=True) + eps) * _w(weight)
+
+
+def amp_round(x, amp: bool):
+    """Round to bf16 where CUDA bf16 autocast stores a bf16 tensor (identity otherwise)."""
+    return x.to(torch.bfloat16).to(x.dtype) if amp else x
+
+
+def linear(x, weight, bias=None, amp: bool = False):
+    """F.linear; under bf16 autocast its operands and its result are bf16 (f32 accumulation)."""
+    x, weight = amp_round(x, amp), amp_round(_w(weight), amp)
+    y = x @ weight.transpose(0, 1)
+    if bias is not None:
+        y = y + amp_round(_w(bias), amp)
+    return amp_round(y, amp)
+
+
+def swiglu(x, w1, w2, w3, amp: bool = False):
+    """model.py:452-464: w3(silu(w1 x) * w2 x)."""
+    a, b = linear(x, w1, amp=amp), linear(x, w2, amp=amp)
+    return linear(amp_round(amp_round(F.silu(a), amp) * b, amp), w3, amp=amp)
+
+
+def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp=False):
+    """IsotropicKalmanDeltaNetwork.forward (iso_kdn.py:262-314) on a state dict ``p`` of the
+    layer (reference parameter names): packed q|k|v projection + per-group SiLU short
+    convolution; [f0 | omega | r] packed projection, f_proj[1] on the f0 slice; iso_mixer;
+    sigmoid-gated RMS norm against g_proj(x); o_proj."""
+    H = p["A_log"].shape[0]
+    Dm = p["qkv_pack.projection_weight"].shape[0] // 3
+    K = Dm // H
+    B, T, _ = x.shape
+    qkv = linear(x, p["qkv_pack.projection_weight"], amp=amp)
+    cw = p["qkv_pack.convolution_weight"]
+    q, k, v = (amp_round(short_conv_silu(qkv[..., i * Dm:(i + 1) * Dm], cw[i * Dm:(i + 1) * Dm]), amp)
+               for i in range(3))
+    packed = linear(x, p["f_omega_r_proj.weight"], amp=amp)
+    f_hidden, omega_r_raw = packed[..., :K], packed[..., K:]
+    g_raw = linear(f_hidden, p["f_proj.1.weight"], amp=amp)
+    o = iso_mixer(q.view(B, T, H, K), k.view(B, T, H, K), v.view(B, T, H, K), g_raw.view(B, T, H, K),
+                  omega_r_raw, p["omega_proj.bias"], p["r_proj.bias"], p["A_log"], p["dt_bias"],
+                  p["initial_precision_param"], omega_min=omega_min, r_min=r_min, info_scale=info_scale)
+    o = amp_round(o, amp)
+    gate = linear(linear(x, p["g_proj.0.weight"], amp=amp), p["g_proj.1.weight"], p["g_proj.1.bias"], amp=amp)
+    y = amp_round(rms_norm_gated(o, gate.view(B, T, H, K), p["o_norm.weight"], eps, "sigmoid"), amp)
+    return linear(y.reshape(B, T, Dm), p["o_proj.weight"], amp=amp)
+
+
+def diag_layer(p, x, *, eps=1e-5, amp=False):
+    """DiagonalKalmanDeltaNetwork.forward (diag_kdn.py:259-357) on a state dict ``p`` of the layer:
+    q/k/v projections + SiLU short convolutions, f_proj / omega_proj two-layer projections,
+    r_proj, diag_mixer (its f32 output stored at v's dtype), gated RMS norm, o_proj."""
+    H = p["A_log"].shape[0]
+    Dm = p["q_proj.weight"].shape[0]
+    K = Dm // H
+    B, T, _ = x.shape
+
+    def conv(name):
+        y = short_conv_silu(linear(x, p[f"{name}_proj.weight"], amp=amp), p[f"{name}_conv1d.weight"][:, 0, :])
+        return amp_round(y, amp).view(B, T, H, K)
+
+    q, k, v = conv("q"), conv("k"), conv("v")
+    retention_raw = linear(linear(x, p["f_proj.0.weight"], amp=amp), p["f_proj.1.weight"], amp=amp)
+    omega_raw = linear(linear(x, p["omega_proj.0.weight"], amp=amp), p["omega_proj.1.weight"],
+                       p["omega_proj.1.bias"], amp=amp)
+    r_raw = linear(x, p["r_proj.weight"], p["r_proj.bias"], amp=amp)
+    o = diag_mixer(q, k, v, retention_raw.view(B, T, H, K), omega_raw.view(B, T, H, K), r_raw, p["A_log"],
+                   p["dt_bias"], p["initial_precision_param"])
+    o = amp_round(o, amp)
+    gate = linear(linear(x, p["g_proj.0.weight"], amp=amp), p["g_proj.1.weight"], p["g_proj.1.bias"], amp=amp)
+    y = amp_round(rms_norm_gated(o, gate.view(B, T, H, K), p["o_norm.weight"], eps, "sigmoid"), amp)
+    return linear(y.reshape(B, T, Dm), p["o_proj.weight"], amp=amp)
+
+
+def _sub(p, prefix):
+    return {k[len(prefix):]: v for k, v in p.items() if k.startswith(prefix)}
+
+
+def gpt_forward(p, idx, *, n_layer, mixer_type, eps=1e-5, amp=False, **mixer_kw):
+    """GPT.forward (model.py:95-162) for KDN-only stacks with parallel_residual=False:
+    x = wte[idx]; per block x += mixer(norm_1(x)); x += swiglu(norm_2(x)); logits = lm_head(ln_f(x)).
+    The residual stream stays in the embedding's dtype (bf16 branch outputs add into f32)."""
+    layer = iso_layer if mixer_type == "iso_kdn" else diag_layer
+    x = _w(p["transformer.wte.weight"])[idx]
+    for i in range(n_layer):
+        b = _sub(p, f"transformer.h.{i}.")
+        h = layer(_sub(b, "attn."), rms_norm(x, b["norm_1.weight"], eps), eps=eps, amp=amp, **mixer_kw)
+        x = x + h
+        m = _sub(b, "mlp.swiglu.")
+        x = x + swiglu(rms_norm(x, b["norm_2.weight"], eps), m["w1.weight"], m["w2.weight"], m["w3.weight"], amp=amp)
+    return linear(rms_norm(x, p["transformer.ln_f.weight"], eps), p["lm_head.weight"], amp=amp)

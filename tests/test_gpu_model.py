@@ -1,0 +1,174 @@
+"""GPU parity of the config-4 block stack against the CPU oracle composition.
+
+* ``FusedRMSNorm`` (kdn_rms_norm_* through the C ABI): y, dx, dweight at 1e-5 (fp32) / 2e-2
+  (bf16), at the model width 2304 and a narrow width, plus bit-identical repeated weight
+  gradients (fixed-order sums).
+* Isotropic layer in fp32 eval mode against the fp64 oracle layer (``ko.iso_layer``): output and
+  every parameter / input gradient at 2e-2 (the scan stores q, k, v in bf16 on this path, as the
+  reference's does).
+* Isotropic and diagonal layers in training mode under CUDA bf16 autocast (the reference's only
+  training configuration) against the oracle with autocast's bf16 rounding points (``amp=True``):
+  output and gradients at 2e-2.
+* A two-layer GPT of each mixer under autocast: logits and the gradients of the embedding,
+  the first block's norms / mixer input projection and the head at 2e-2.
+"""
+import pytest
+import torch
+
+from gpu_util import gpu_or_skip, log, rel
+from oracle import kdn_oracle as ko
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+TOL_LAYER = 2e-2
+
+
+def _check(name, got, ref, tol):
+    r = rel(got, ref)
+    log(f"  {name}: rel err {r:.3e} (tol {tol:g})")
+    assert r <= tol, f"{name}: {r:.3e} > {tol}"
+
+
+@pytest.mark.parametrize("rows,D,dtype", [(300, 2304, torch.bfloat16), (300, 2304, torch.float32),
+                                          (1, 128, torch.float32), (4096, 128, torch.bfloat16),
+                                          (7, 8192, torch.bfloat16)])
+def test_rms_norm_matches_oracle(rows, D, dtype):
+    dev = gpu_or_skip()
+    from lit_gpt.rmsnorm import FusedRMSNorm
+    log(f"case rms norm rows={rows} D={D} {dtype}")
+    g = torch.Generator().manual_seed(rows + D)
+    x = (3.0 * torch.randn(rows, D, generator=g)).to(dtype)
+    w = 1.0 + 0.1 * torch.randn(D, generator=g)
+    dy = torch.randn(rows, D, generator=g).to(dtype)
+    xd, wd = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    y_ref = ko.rms_norm(xd, wd, 1e-5)
+    dx_ref, dw_ref = torch.autograd.grad((y_ref * dy.double()).sum(), (xd, wd))
+    norm = FusedRMSNorm(D, eps=1e-5).to(dev)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+    xg = x.to(dev).requires_grad_(True)
+    y = norm(xg)
+    assert y.dtype == dtype
+    dx, dw = torch.autograd.grad(y, (xg, norm.weight), dy.to(dev))
+    dw2 = torch.autograd.grad(norm(xg), norm.weight, dy.to(dev))[0]
+    torch.cuda.synchronize()
+    tol = TOL[dtype]
+    _check("y", y, y_ref, tol)
+    _check("dx", dx, dx_ref, tol)
+    _check("dweight", dw, dw_ref, tol)
+    assert torch.equal(dw, dw2)
+
+
+def _layer(variant, dev, seed):
+    torch.manual_seed(seed)
+    if variant == "iso":
+        from lit_gpt.iso_kdn import IsotropicKalmanDeltaNetwork as L
+    else:
+        from lit_gpt.diag_kdn import DiagonalKalmanDeltaNetwork as L
+    layer = L(hidden_size=128, head_dim=64, num_heads=2)
+    with torch.no_grad():
+        # move off the zero / one initial values so every parameter's gradient is exercised
+        for name, p in layer.named_parameters():
+            if "omega_proj.1" in name or "o_norm" in name:
+                p.add_(0.05 * torch.randn_like(p))
+    return layer.to(dev)
+
+
+def _oracle_params(layer):
+    return {k: v.detach().cpu().double().requires_grad_(True) for k, v in layer.state_dict().items()}
+
+
+def _compare_layer(layer, p_ref, x, xg, out, out_ref, dy):
+    _check("output", out, out_ref, TOL_LAYER)
+    names = list(p_ref)
+    grads_ref = torch.autograd.grad((out_ref * dy.double()).sum(), [x] + [p_ref[n] for n in names],
+                                    allow_unused=True)
+    params = dict(layer.named_parameters())
+    grads = torch.autograd.grad(out, [xg] + [params[n] for n in names], dy.to(out.device).to(out.dtype),
+                                allow_unused=True)
+    torch.cuda.synchronize()
+    _check("d hidden", grads[0], grads_ref[0], TOL_LAYER)
+    for n, gg, gr in zip(names, grads[1:], grads_ref[1:]):
+        assert gg is not None and gr is not None, n
+        _check(f"d {n}", gg, gr, TOL_LAYER)
+
+
+def test_iso_layer_fp32_eval_matches_oracle():
+    dev = gpu_or_skip()
+    B, T = 2, 130
+    log(f"case iso layer fp32 eval B={B} T={T} H=2 K=64")
+    layer = _layer("iso", dev, 0).eval()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(B, T, 128, generator=g)
+    dy = torch.randn(B, T, 128, generator=g).bfloat16().float()  # exact in bf16 and fp32
+    p_ref = _oracle_params(layer)
+    xd = x.double().requires_grad_(True)
+    out_ref = ko.iso_layer(p_ref, xd, info_scale=64.0)
+    xg = x.to(dev).requires_grad_(True)
+    out, _, _ = layer(xg)
+    assert out.dtype == torch.float32
+    _compare_layer(layer, p_ref, xd, xg, out, out_ref, dy)
+
+
+@pytest.mark.parametrize("variant", ["iso", "diag"])
+def test_layer_bf16_autocast_training_matches_oracle(variant):
+    dev = gpu_or_skip()
+    B, T = 2, 130
+    log(f"case {variant} layer autocast training B={B} T={T} H=2 K=64")
+    layer = _layer(variant, dev, 1).train()
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(B, T, 128, generator=g)
+    dy = torch.randn(B, T, 128, generator=g).bfloat16().float()  # exact in bf16 and fp32
+    p_ref = _oracle_params(layer)
+    xd = x.double().requires_grad_(True)
+    if variant == "iso":
+        out_ref = ko.iso_layer(p_ref, xd, info_scale=64.0, amp=True)
+    else:
+        out_ref = ko.diag_layer(p_ref, xd, amp=True)
+    xg = x.to(dev).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out, _, _ = layer(xg)
+    assert out.dtype == torch.bfloat16
+    _compare_layer(layer, p_ref, xd, xg, out, out_ref, dy)
+
+
+def test_layer_training_requires_bf16_autocast():
+    dev = gpu_or_skip()
+    layer = _layer("iso", dev, 2).train()
+    with pytest.raises(TypeError, match="autocast"):
+        layer(torch.zeros(1, 8, 128, device=dev))
+
+
+@pytest.mark.parametrize("mixer_type", ["iso_kdn", "diag_kdn"])
+def test_gpt_bf16_autocast_matches_oracle(mixer_type):
+    dev = gpu_or_skip()
+    from lit_gpt.config import Config
+    from lit_gpt.model import GPT
+    B, T = 1, 100
+    log(f"case GPT {mixer_type} 2 layers autocast B={B} T={T}")
+    cfg = Config(name="tiny", block_size=256, vocab_size=200, padding_multiple=64, gdn2_per_layer=1,
+                 mixer_type=mixer_type, n_layer=2, n_head=2, n_embd=128, rotary_percentage=1.0,
+                 parallel_residual=False, bias=False, _norm_class="FusedRMSNorm", norm_eps=1e-5,
+                 _mlp_class="LLaMAMLP", intermediate_size=96, mamba_init=True, kdn_info_scale=64.0)
+    torch.manual_seed(3)
+    model = GPT(cfg)
+    model.init_weights()
+    model = model.to(dev).train()
+    g = torch.Generator().manual_seed(13)
+    idx = torch.randint(0, 200, (B, T), generator=g)
+    dl = torch.randn(B, T, cfg.padded_vocab_size, generator=g).bfloat16().float()
+    p_ref = {k: v.detach().cpu().double().requires_grad_(True) for k, v in model.state_dict().items()}
+    kw = {"info_scale": 64.0} if mixer_type == "iso_kdn" else {}
+    logits_ref = ko.gpt_forward(p_ref, idx, n_layer=2, mixer_type=mixer_type, amp=True, **kw)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        logits = model(idx.to(dev))
+    _check("logits", logits, logits_ref, TOL_LAYER)
+    first = "transformer.h.0.attn." + ("qkv_pack.projection_weight" if mixer_type == "iso_kdn" else "q_proj.weight")
+    names = ["transformer.wte.weight", "transformer.h.0.norm_1.weight", "transformer.h.0.norm_2.weight", first,
+             "transformer.h.1.attn.A_log", "transformer.ln_f.weight", "lm_head.weight"]
+    params = dict(model.named_parameters())
+    grads_ref = torch.autograd.grad((logits_ref * dl.double()).sum(), [p_ref[n] for n in names])
+    grads = torch.autograd.grad(logits, [params[n] for n in names], dl.to(dev).to(logits.dtype))
+    torch.cuda.synchronize()
+    for n, gg, gr in zip(names, grads, grads_ref):
+        _check(f"d {n}", gg, gr, TOL_LAYER)
