@@ -313,7 +313,9 @@ def main():
     ap.add_argument("--variant", choices=("iso", "diag"), default="iso")
     ap.add_argument("--cpu-slices", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-config4", action="store_true", help="skip the whole-model (config 4) training step")
+    ap.add_argument("--no-config4", action="store_true", help="skip the whole-model (config 4) measurement")
+    ap.add_argument("--config4-only", action="store_true",
+                    help="measure only the whole model (config 4) and print its line (for profiling)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain copy of MIB MiB (PMC byte-counter calibration)")
     ap.add_argument("--B", type=int, default=4)
@@ -333,6 +335,10 @@ def main():
         sys.exit(1)
     B, T, H, K = args.B, args.T, args.H, args.d
     main_v = args.variant
+    if args.config4_only:
+        line = run_config4(f"{main_v}_kdn_1.3B", args.steps, args.warmup, 1, T)
+        print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B forward tokens/s (config 4)")), flush=True)
+        return
     other = "diag" if main_v == "iso" else "iso"
     res = run_variant(main_v, args.steps, args.warmup, B, T, H, K)
     res_other = run_variant(other, args.steps, args.warmup, B, T, H, K)

@@ -374,18 +374,21 @@ __global__ __launch_bounds__(256, 2) void solve_kernel(const float* __restrict__
 
 // ---------------------------------------------------------------------------------------------
 // Gradients of q, k, kappa (iso: beta) and the gate, from dN, dM and the elementwise factors.
-// With the forward's row-0 anchor, per element (c, i):
-//   e0 = 2^{G_c - G_0}, Lk = k e0, Lq = q e0, R = kappa / e0, eg = 2^{G_c}, f = 2^{G_last - G_c}
+// Each output row block tl uses the forward's anchor of that block, m = (G_{16tl} + G_{16tl+15})/2
+// per channel (rows clamped to the chunk), for every factor it contracts with, so each factor is
+// <= 2^{span/2} on the diagonal block and <= 1 off it.  Per element (c, i) of block tl:
+//   e = 2^{G_c - m}, Lk = k e, Lq = q e, R = kappa / e, eg = 2^{G_c}, f = 2^{G_last - G_c}
 //   dLk = dN R,  dLq = scale dM R,  dR = dN^T Lk + scale dM^T Lq          (bf16x3 MFMA)
-//   dk = dLk e0 + dKg eg,  dq = dLq e0 + scale dQg eg,  dkappa = dR / e0 + dKf f
+//   dk = dLk e + dKg eg,  dq = dLq e + scale dQg eg,  dkappa = dR / e + dKf f
 //   dg = Lk dLk + Lq dLq - R dR + k eg dKg + scale q eg dQg - kappa f dKf  (natural-log coordinates)
 //   dg[last row] += sum_c kappa f dKf + dgl;   iso: dbeta = sum_i dkappa k, dk += beta dkappa
-// The anchor terms cancel exactly (N and M do not depend on the anchor) and are omitted.
+// The anchor terms cancel exactly (N and M do not depend on the anchors) and are omitted.
 // Wave w owns the channel tiles w, w+4.  The factors R, Lk, Lq are built per lane for one
-// channel and 16 chunk rows (the permuted-k fragment order) and enter the time contractions as
-// the A operand, with dN, dM, dN^T, dM^T (split once per workgroup into LDS fragments) as B:
-// the transposed D tiles give each lane 4 consecutive channels of one chunk row, so the
-// elementwise inputs and outputs move as 16-byte (fp32) and 8-byte (bf16) vectors.
+// channel and 16 chunk rows (the permuted-k fragment order), rows outside the contraction's
+// nonzero range zeroed, and enter the time contractions as the A operand, with dN, dM, dN^T,
+// dM^T (split once per workgroup into LDS fragments) as B: the transposed D tiles give each lane
+// 4 consecutive channels of one chunk row, so the elementwise inputs and outputs move as 16-byte
+// (fp32) and 8-byte (bf16) vectors.
 // grid (NT, B*H), block 256.  Chunks flagged by the forward go to the exact kernel.
 // ---------------------------------------------------------------------------------------------
 template <int K, bool ISO>
@@ -459,48 +462,47 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
     const int it = w + 4 * u;
     if (it >= NIT) break;
     const int i = 16 * it + r16;
-    // ---- factor loads, one channel per lane: rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j
+    // the row offsets below are recomputed per iteration rather than held across the loop
+    int lg4 = g4, lr16 = r16;
+    asm volatile("" : "+v"(lg4), "+v"(lr16));
+    // ---- factor loads, one channel per lane: rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j; the gate
+    // of rows past L repeats row L-1 (their k, q, kappa read zero)
     float av[16], Gv[16];
     uint16_t kraw[16], qraw[16];
-    const float g0 = buf_ld(rG, i * 4);
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
-      const int c = 16 * (p >> 2) + 4 * g4 + (p & 3);
+      const int c = 16 * (p >> 2) + 4 * lg4 + (p & 3);
       const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
       kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
       qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
       av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);  // iso: beta of the row
-      Gv[p] = buf_ld(rG, o * 4);
+      Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the batch together (raw bf16 held until every load is out)
-    // factors as permuted-k fragments per 32-row block (k = chunk row, lane column = channel i)
-    uint4 Rh[2], Rl[2], Kh[2], Kl[2], Qh[2], Ql[2];
+    // block anchors of channel i: rows 16J and 16J + 15 (clamped) are slot 4J of lane group 0 and
+    // slot 4J + 3 of lane group 3
+    float mA[4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      float lk[8], lq[8], rv[8];
+    for (int J = 0; J < 4; ++J) mA[J] = 0.5f * (__shfl(Gv[4 * J], r16, 64) + __shfl(Gv[4 * J + 3], 48 + r16, 64));
+    // factors of each slot anchored at its own block J = p / 4 (<= 2^{span_J / 2}); another block's
+    // anchor is one per-lane scale 2^{m_tl - m_J} (R side, J <= tl) or 2^{m_J - m_tl} (k side, J >= tl)
+    float Rown[16], Kown[16], Qown[16];
 #pragma unroll
-      for (int sl = 0; sl < 8; ++sl) {
-        const int p = 8 * kb + sl;  // tiles 2kb (slots 0-3) and 2kb+1 (slots 4-7)
-        const float kvp = bf2f(kraw[p]), qvp = bf2f(qraw[p]);
-        const float kap_p = ISO ? av[p] * kvp : av[p];
-        const float e0 = exp2f(Gv[p] - g0);
-        lk[sl] = kvp * e0;
-        lq[sl] = scale * qvp * e0;
-        rv[sl] = kap_p * exp2f(g0 - Gv[p]);
-      }
-      split8(rv, Rh[kb], Rl[kb]);
-      split8(lk, Kh[kb], Kl[kb]);
-      split8(lq, Qh[kb], Ql[kb]);
+    for (int p = 0; p < 16; ++p) {
+      const float kvp = bf2f(kraw[p]), e = exp2f(Gv[p] - mA[p >> 2]);
+      Kown[p] = kvp * e;
+      Qown[p] = scale * bf2f(qraw[p]) * e;
+      Rown[p] = (ISO ? av[p] * kvp : av[p]) * __frcp_rn(e);
     }
     // ---- elementwise inputs at the transposed tile positions: row c = 16 tl + r16, channels
     // i0 .. i0+3 (16-byte / 8-byte loads), issued before the contractions
     const int i0 = 16 * it + 4 * g4;
-    const float4 g0v = buf_ld4(rG, i0 * 4), glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
+    const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
     u32x2 kq4[4], qq4[4];
     float4 kap4[4], G4[4], dkg4[4], dqg4[4], dkf4[4];
 #pragma unroll
     for (int tl = 0; tl < 4; ++tl) {
-      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0, ol = c * K + i0;
+      const uint32_t c = (uint32_t)(16 * tl + lr16), o = c * H * K + i0, ol = c * K + i0;
       kq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rk, o * 2, 0, 0);
       qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
       if (ISO) {
@@ -509,47 +511,56 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
       } else {
         kap4[tl] = buf_ld4(rkap, o * 4);
       }
-      G4[tl] = buf_ld4(rG, o * 4);
+      G4[tl] = buf_ld4(rG, ((uint32_t)(min(16 * tl + lr16, L - 1) * H) * K + i0) * 4);
       dkg4[tl] = buf_ld4(rdKg, ol * 4);
       dqg4[tl] = buf_ld4(rdQg, ol * 4);
       dkf4[tl] = buf_ld4(rdKf, ol * 4);
     }
-    // ---- time contractions, transposed (factor fragments as A, dN/dM fragments as B): the D
-    // tile of row block tl gives lane (row 16 tl + r16) the channels i0 .. i0+3
-    f32x4 dLk[4], dLq[4], dR[4];
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      dLk[tl] = dLq[tl] = dR[tl] = zero4();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        uint4 ah, al;
-        if (kb <= tl / 2) {  // dN, dM rows c: nonzero for s <= c
-          afrag(sF, tl * 2 + kb, lane, ah, al);
-          dLk[tl] = mma3(Rh[kb], Rl[kb], ah, al, dLk[tl]);
-          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
-          dLq[tl] = mma3(Rh[kb], Rl[kb], ah, al, dLq[tl]);
-        }
-        if (2 * kb + 1 >= tl) {  // dN^T, dM^T rows s: nonzero for c >= s
-          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
-          dR[tl] = mma3(Kh[kb], Kl[kb], ah, al, dR[tl]);
-          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
-          dR[tl] = mma3(Qh[kb], Ql[kb], ah, al, dR[tl]);
-        }
-      }
-    }
-    // ---- assemble.  Per channel 2^{-G_0}, 2^{G_0}, 2^{G_last}; per element one exponential
-    // eg = 2^{G_c} and its reciprocal: e0 = eg 2^{-G_0}, er = 2^{G_0} / eg, f = 2^{G_last} / eg.
-    float E0[4], Ez[4], El[4];
-    {
-      const float gz[4] = {g0v.x, g0v.y, g0v.z, g0v.w}, gla[4] = {glv.x, glv.y, glv.z, glv.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) E0[j] = exp2f(-gz[j]), Ez[j] = exp2f(gz[j]), El[j] = exp2f(gla[j]);
-    }
     float colpart[4] = {0.f, 0.f, 0.f, 0.f};
     float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
     bool has_last = false;
+    const float gla[4] = {glv.x, glv.y, glv.z, glv.w};
 #pragma unroll
     for (int tl = 0; tl < 4; ++tl) {
+      // ---- time contractions of row block tl, transposed (factor fragments anchored at block tl as
+      // A, dN/dM fragments as B): the D tile gives lane (row 16 tl + r16) the channels i0 .. i0+3
+      f32x4 dLk = zero4(), dLq = zero4(), dR = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        uint4 ah, al;
+        if (kb <= tl / 2) {  // dN, dM rows c: nonzero for s <= c; R of rows in blocks <= tl
+          const float s0 = 2 * kb <= tl ? exp2f(mA[tl] - mA[2 * kb]) : 0.f;
+          const float s1 = 2 * kb + 1 <= tl ? exp2f(mA[tl] - mA[2 * kb + 1]) : 0.f;
+          float rv[8];
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) rv[sl] = Rown[8 * kb + sl] * (sl < 4 ? s0 : s1);
+          uint4 Rh, Rl;
+          split8(rv, Rh, Rl);
+          afrag(sF, tl * 2 + kb, lane, ah, al);
+          dLk = mma3(Rh, Rl, ah, al, dLk);
+          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
+          dLq = mma3(Rh, Rl, ah, al, dLq);
+        }
+        if (2 * kb + 1 >= tl) {  // dN^T, dM^T rows s: nonzero for c >= s; Lk, Lq of rows in blocks >= tl
+          const float t0 = 2 * kb >= tl ? exp2f(mA[2 * kb] - mA[tl]) : 0.f;
+          const float t1 = 2 * kb + 1 >= tl ? exp2f(mA[2 * kb + 1] - mA[tl]) : 0.f;
+          float lk[8], lq[8];
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) {
+            const float t = sl < 4 ? t0 : t1;
+            lk[sl] = Kown[8 * kb + sl] * t;
+            lq[sl] = Qown[8 * kb + sl] * t;
+          }
+          uint4 Kh, Kl, Qh, Ql;
+          split8(lk, Kh, Kl);
+          split8(lq, Qh, Ql);
+          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
+          dR = mma3(Kh, Kl, ah, al, dR);
+          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
+          dR = mma3(Qh, Ql, ah, al, dR);
+        }
+      }
+      // ---- assemble row block tl
       const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
       const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
                             __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
@@ -557,7 +568,9 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
                             __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
       const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
       const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
-
+      // anchors of channels i0 .. i0+3 = 16 it + 4 g4 + j, held by lanes 4 g4 + j
+      const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
+                           __shfl(mA[tl], 4 * g4 + 3, 64)};
       const float dkgv[4] = {dkg4[tl].x, dkg4[tl].y, dkg4[tl].z, dkg4[tl].w};
       const float dqgv[4] = {dqg4[tl].x, dqg4[tl].y, dqg4[tl].z, dqg4[tl].w};
       const float dkfv[4] = {dkf4[tl].x, dkf4[tl].y, dkf4[tl].z, dkf4[tl].w};
@@ -566,14 +579,14 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
       for (int j = 0; j < 4; ++j) {
         const float beta = ISO ? a4[j] : 0.f;
         const float kap_p = ISO ? beta * kv4[j] : a4[j];
-        const float eg = exp2f(gv[j]), ig = __frcp_rn(eg);
-        const float e0 = eg * E0[j], er = ig * Ez[j], f = ig * El[j];
-        const float a_lk = dLk[tl][j], a_lq = dLq[tl][j] * scale, a_r = dR[tl][j];
-        dkv[j] = a_lk * e0 + dkgv[j] * eg;
-        dqv[j] = a_lq * e0 + scale * dqgv[j] * eg;
+        const float e = exp2f(gv[j] - mz[j]), er = __frcp_rn(e);
+        const float eg = exp2f(gv[j]), f = exp2f(gla[j] - gv[j]);
+        const float a_lk = dLk[j], a_lq = dLq[j] * scale, a_r = dR[j];
+        dkv[j] = a_lk * e + dkgv[j] * eg;
+        dqv[j] = a_lq * e + scale * dqgv[j] * eg;
         dav[j] = a_r * er + dkfv[j] * f;
-        // Lk = k e0, Lq (unscaled) = q e0, R = kappa er
-        dgv[j] = kv4[j] * e0 * a_lk + qv4[j] * e0 * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv[j] +
+        // Lk = k e, Lq (unscaled) = q e, R = kappa er
+        dgv[j] = kv4[j] * e * a_lk + qv4[j] * e * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv[j] +
                  scale * qv4[j] * eg * dqgv[j] - kap_p * f * dkfv[j];
         if ((int)c < L) colpart[j] += kap_p * f * dkfv[j];
         if (ISO) {

@@ -1,19 +1,25 @@
 // Forward intra-chunk kernel of the KDN memory scan, MFMA formulation.
 //
-// Per chunk (C = 64 tokens) with G the base-2 chunk-local prefix of the log gate and the
-// chunk's first row as the decay anchor (G_c - G_0 <= 0, G_0 - G_s >= 0):
-//   Lk = k 2^{G - G_0},  Lq = scale q 2^{G - G_0},  R = kappa 2^{G_0 - G}
-//   N = strict_lower(Lk R^T),  M = lower(Lq R^T)                   (bf16x3 MFMA, K-contraction)
+// Per chunk (C = 64 tokens) with G the base-2 chunk-local prefix of the log gate, split into
+// four row blocks of 16 tokens.  Block J has the per-channel anchor m_J = (G_{16J} + G_{16J+15})/2
+// (rows clamped to the chunk), so within the block |G - m_J| <= span_J / 2.  For c >= s with s in
+// block J and c in block I >= J, 2^{G_c - G_s} = (k-side 2^{G_c - m_J}) (kappa-side 2^{m_J - G_s}),
+// where the k side is <= 1 off the diagonal block and both sides are <= 2^{span_J / 2} on it:
+//   R_J = kappa 2^{m_J - G}         (rows of block J, published per block)
+//   Lk_IJ = k 2^{G - m_I} 2^{m_I - m_J},  Lq_IJ = scale q 2^{G - m_I} 2^{m_I - m_J}   (rows of block I)
+//   N_IJ = Lk_IJ R_J^T (strictly lower),  M_IJ = Lq_IJ R_J^T (lower)   (bf16x3 MFMA, K-contraction)
 //   A = (I + N)^{-1}:  16x16 diagonal blocks by substitution, off-diagonal blocks level by level
 //                      A_IJ = -A_II sum_{J<=P<I} N_IP A_PJ           (fp32 MFMA)
 //   U = A V,  W = A (k 2^G),  Kf = kappa 2^{G_last - G},  Qg = scale q 2^G
-// A^T is saved for the backward.  R <= 2^span where span = max_i (G_0 - G_{L-1})_i; chunks with
-// span > kAnchorSpanMax are flagged (flags[chunk] = 1) and left to the exact per-block kernel,
-// which runs after this one over the flagged chunks only.
+// A^T is saved for the backward.  A chunk with a 16-token block whose span exceeds
+// kBlockSpanMax (the masked upper-triangle products of a diagonal block reach 2^span) is flagged
+// (flags[chunk] = 1) and left to the exact per-block kernel, which runs after this one over the
+// flagged chunks only.
 //
-// Layout of work: wave w owns row block I = w (16 rows) for the N / M build, computing its own
-// Lk / Lq fragments in registers and publishing its R fragments to LDS; the U / W products
-// are split over the waves by output column tile.  LDS ~49 KB: three workgroups per CU.
+// Layout of work: wave w owns row block I = w (16 rows) for the N / M build, keeping its k / q
+// factors in registers and publishing its R fragments and anchors to LDS; the U / W products
+// are split over the waves by output column tile.  LDS ~51 KB, up to 256 VGPRs: two workgroups per CU
+// (the kernel streams from HBM; a third workgroup measured no faster).
 #pragma once
 #include <type_traits>
 #include "kdn_common.h"
@@ -31,7 +37,7 @@ using kdn_state::split2;
 using kdn_state::TILE;
 using kdn_state::zero4;
 
-constexpr float kAnchorSpanMax = 100.f;  // base 2: R <= 2^100 stays far inside fp32
+constexpr float kBlockSpanMax = 120.f;  // base 2, per 16-token block: every product stays below 2^120
 constexpr int AP = C + 1;                // LDS row stride of the fp32 N and A tiles
 constexpr int XS = C + 4;                // LDS row stride of the staged [column][s] operands
 
@@ -53,6 +59,17 @@ __device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& lo) {
   split2(x[4], x[5], hi.z, lo.z);
   split2(x[6], x[7], hi.w, lo.w);
 }
+// (hi + lo) * f, re-split: the split pair holds the value to 2^-17 relative
+__device__ __forceinline__ void rescale8(const uint4& hi, const uint4& lo, const float* f, uint4& oh, uint4& ol) {
+  const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w}, l[4] = {lo.x, lo.y, lo.z, lo.w};
+  float x[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    x[2 * p] = (__uint_as_float(h[p] << 16) + __uint_as_float(l[p] << 16)) * f[2 * p];
+    x[2 * p + 1] = (__uint_as_float(h[p] & 0xffff0000u) + __uint_as_float(l[p] & 0xffff0000u)) * f[2 * p + 1];
+  }
+  split8(x, oh, ol);
+}
 __device__ __forceinline__ void ld8(bufrsrc r, uint32_t off, float* f) {
   const float4 a = buf_ld4(r, off), b = buf_ld4(r, off + 16);
   f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
@@ -68,7 +85,7 @@ __device__ __forceinline__ void st8(bufrsrc r, uint32_t off, const float* f) {
 
 // grid (NT, B*H), block 256.
 template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
+__global__ __launch_bounds__(256, 2) void intra_fwd_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
@@ -86,6 +103,7 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
   float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
   __shared__ float sSpan[4];
+  __shared__ __attribute__((aligned(16))) float sMid[4 * K];  // block anchors m_J per channel
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
@@ -106,18 +124,18 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
   float* An = Ag + ((int64_t)bh * NT + n) * C * C;
 
-  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels
+  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels.
+  // Rows past L read zero k, q, kappa and repeat the gate of row L-1, so every factor is bounded.
   const int c = 16 * w + r16;
-  const uint32_t crow = (uint32_t)(c * H);
-  uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
+  const uint32_t crow = (uint32_t)(c * H), grow = (uint32_t)(min(c, L - 1) * H);
+  uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];  // k 2^{G - m_I}, scale q 2^{G - m_I} as split fragments
   float span = 0.f;
   const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int i0 = 32 * kb + 8 * g4;
-    float gcv[8], g0[8], gl[8], kv[8], qv[8], av[8];
-    ld8(rG, (crow * K + i0) * 4, gcv);
-    ld8(rG, i0 * 4, g0);
+    float gcv[8], gl[8], kv[8], qv[8], av[8];
+    ld8(rG, (grow * K + i0) * 4, gcv);
     ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
     unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
     unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
@@ -127,16 +145,19 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     } else {
       ld8(rkap, (crow * K + i0) * 4, av);
     }
-    float lk[8], lq[8], rr[8], kf[8], qg[8];
+    float mid[8], lk[8], lq[8], rr[8], kf[8], qg[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float e = exp2f(gcv[j] - g0[j]);
+      // the block's first and last rows (clamped) are lanes 16 g4 and 16 g4 + 15 of this wave
+      const float ga = __shfl(gcv[j], 16 * g4, 64), gb = __shfl(gcv[j], 16 * g4 + 15, 64);
+      mid[j] = 0.5f * (ga + gb);
+      const float e = exp2f(gcv[j] - mid[j]);
       lk[j] = kv[j] * e;
       lq[j] = scale * qv[j] * e;
-      rr[j] = av[j] * exp2f(g0[j] - gcv[j]);
+      rr[j] = av[j] * exp2f(mid[j] - gcv[j]);
       kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
       qg[j] = scale * qv[j] * exp2f(gcv[j]);
-      span = fmaxf(span, g0[j] - gl[j]);
+      span = fmaxf(span, ga - gb);
     }
     split8(lk, lkh[kb], lkl[kb]);
     split8(lq, lqh[kb], lql[kb]);
@@ -144,27 +165,36 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     split8(rr, rh, rl);
     *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + lane * 8) = rh;
     *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + 512 + lane * 8) = rl;
+    if (r16 == 0) {
+      *reinterpret_cast<float4*>(sMid + w * K + i0) = float4{mid[0], mid[1], mid[2], mid[3]};
+      *reinterpret_cast<float4*>(sMid + w * K + i0 + 4) = float4{mid[4], mid[5], mid[6], mid[7]};
+    }
     st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
     st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
+    __builtin_amdgcn_sched_barrier(0);  // one k-block at a time
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
   if (lane == 0) sSpan[w] = span;
   __syncthreads();
   const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
-  if (!(cspan <= kAnchorSpanMax)) {  // the exact kernel takes this chunk
+  if (!(cspan <= kBlockSpanMax)) {  // the exact kernel takes this chunk
     if (tid == 0) flags[(int64_t)bh * NT + n] = 1;
     return;
   }
   if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
 
-  // ---- 2. N and M tiles of row block I = w
+  // ---- 2. N and M tiles of row block I = w; column block J uses the anchor m_J on both sides
+  // (the k side carries 2^{m_I - m_J} <= 1, exactly 1 for J = I)
   const bufrsrc rM = make_buf(Mn, C * C * 4);
+  for (int J = w + 1; J < 4; ++J)
 #pragma unroll
-  for (int J = 0; J < 4; ++J) {
+    for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * w + 4 * g4 + j) * C + 16 * J + r16) * 4, 0.f);
+#pragma unroll 1
+  for (int J = 0; J <= w; ++J) {
     const int s = 16 * J + r16;
-    if (J <= w) {
-      f32x4 aN = zero4(), aM = zero4();
+    f32x4 aN = zero4(), aM = zero4();
+    if (J == w) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         uint4 rh, rl;
@@ -172,15 +202,30 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
         aN = mma3(lkh[kb], lkl[kb], rh, rl, aN);
         aM = mma3(lqh[kb], lql[kb], rh, rl, aM);
       }
+    } else {  // the k side times 2^{m_I - m_J} <= 1, re-split
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int cc = 16 * w + 4 * g4 + j;
-        sN[cc * AP + s] = (J < w || s < cc) ? aN[j] : 0.f;
-        buf_st(rM, (cc * C + s) * 4, (J < w || s <= cc) ? aM[j] : 0.f);
+      for (int kb = 0; kb < KB; ++kb) {
+        const int i0 = 32 * kb + 8 * g4;
+        const float4 m0 = *reinterpret_cast<const float4*>(sMid + w * K + i0);
+        const float4 m1 = *reinterpret_cast<const float4*>(sMid + w * K + i0 + 4);
+        const float4 p0 = *reinterpret_cast<const float4*>(sMid + J * K + i0);
+        const float4 p1 = *reinterpret_cast<const float4*>(sMid + J * K + i0 + 4);
+        const float f[8] = {exp2f(m0.x - p0.x), exp2f(m0.y - p0.y), exp2f(m0.z - p0.z), exp2f(m0.w - p0.w),
+                            exp2f(m1.x - p1.x), exp2f(m1.y - p1.y), exp2f(m1.z - p1.z), exp2f(m1.w - p1.w)};
+        uint4 xh, xl, rh, rl;
+        afrag(sR, J * KB + kb, lane, rh, rl);
+        rescale8(lkh[kb], lkl[kb], f, xh, xl);
+        aN = mma3(xh, xl, rh, rl, aN);
+        rescale8(lqh[kb], lql[kb], f, xh, xl);
+        aM = mma3(xh, xl, rh, rl, aM);
+        __builtin_amdgcn_sched_barrier(0);  // one k-block at a time
       }
-    } else {
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * w + 4 * g4 + j) * C + s) * 4, 0.f);
+    for (int j = 0; j < 4; ++j) {
+      const int cc = 16 * w + 4 * g4 + j;
+      sN[cc * AP + s] = (J < w || s < cc) ? aN[j] : 0.f;
+      buf_st(rM, (cc * C + s) * 4, (J < w || s <= cc) ? aM[j] : 0.f);
     }
   }
   __syncthreads();

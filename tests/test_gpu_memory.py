@@ -167,6 +167,29 @@ def test_memory_scan_mixed_anchor_and_exact_chunks(variant):
     _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
 
 
+@pytest.mark.parametrize("variant", ["iso", "diag"])
+@pytest.mark.parametrize("ell_mean,ell_std", [(-1.5, 0.8), (-4.0, 0.3)])
+def test_memory_scan_large_decay_block_anchors(variant, ell_mean, ell_std):
+    """Per-token decays of e^-1.5 to e^-4 (a 64-token chunk spans ~140 to ~370 in base 2), the range
+    a randomly initialised 1.3B model produces: far outside one anchor per chunk, inside the
+    per-16-token block anchors (block spans <= ~100), so the MFMA path must match the oracle."""
+    dev = gpu_or_skip()
+    B, T, H, K, V = 1, 200, 2, 128, 128
+    log(f"case memory large decay {variant} ell~N({ell_mean},{ell_std})")
+    iso = variant == "iso"
+    q, k, v, ell, kap, do = memory_inputs(41, B, T, H, K, V, diag=not iso, ell_mean=ell_mean, ell_std=ell_std)
+    scale = K ** -0.5
+    o_ref, _, g_ref = _oracle(q, k, v, ell, kap, do, iso=iso, scale=scale)
+    o, _, dq, dkk, dv, dell, dkap, _ = _gpu(q, k, v, ell, kap, do, iso=iso, scale=scale, dev=dev)
+    assert torch.isfinite(o).all() and torch.isfinite(dell).all()
+    _check("o", o, o_ref, TOL_F32)
+    _check("dq", dq, g_ref[0], TOL_BF16)
+    _check("dk", dkk, g_ref[1], TOL_BF16)
+    _check("dv", dv, g_ref[2], TOL_BF16)
+    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
+    _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+
+
 def test_diag_bf16_output_equals_fp32_output_cast():
     """The layer composition chunk_kalman(...).to(bf16) (reference diag_kdn.py:342-345) done at the
     kernel's store: the bf16 output and every gradient (given the same bf16 output cotangent) are
