@@ -1,25 +1,29 @@
-// Forward intra-chunk kernel of the KDN memory scan, MFMA formulation.
+// Forward intra-chunk kernels of the KDN memory scan, MFMA formulation.
 //
-// Per chunk (C = 64 tokens) with G the base-2 chunk-local prefix of the log gate, split into
-// four row blocks of 16 tokens.  Block J has the per-channel anchor m_J = (G_{16J} + G_{16J+15})/2
-// (rows clamped to the chunk), so within the block |G - m_J| <= span_J / 2.  For c >= s with s in
-// block J and c in block I >= J, 2^{G_c - G_s} = (k-side 2^{G_c - m_J}) (kappa-side 2^{m_J - G_s}),
-// where the k side is <= 1 off the diagonal block and both sides are <= 2^{span_J / 2} on it:
-//   R_J = kappa 2^{m_J - G}         (rows of block J, published per block)
-//   Lk_IJ = k 2^{G - m_I} 2^{m_I - m_J},  Lq_IJ = scale q 2^{G - m_I} 2^{m_I - m_J}   (rows of block I)
-//   N_IJ = Lk_IJ R_J^T (strictly lower),  M_IJ = Lq_IJ R_J^T (lower)   (bf16x3 MFMA, K-contraction)
+// Per chunk (C = 64 tokens) with G the base-2 chunk-local prefix of the log gate:
+//   N[c,s] = sum_i k_ci kappa_si 2^{G_ci - G_si} (s < c),  M[c,s] = scale sum_i q_ci kappa_si 2^{G_ci - G_si} (s <= c)
 //   A = (I + N)^{-1}:  16x16 diagonal blocks by substitution, off-diagonal blocks level by level
 //                      A_IJ = -A_II sum_{J<=P<I} N_IP A_PJ           (fp32 MFMA)
 //   U = A V,  W = A (k 2^G),  Kf = kappa 2^{G_last - G},  Qg = scale q 2^G
-// A^T is saved for the backward.  A chunk with a 16-token block whose span exceeds
-// kBlockSpanMax (the masked upper-triangle products of a diagonal block reach 2^span) is flagged
-// (flags[chunk] = 1) and left to the exact per-block kernel, which runs after this one over the
-// flagged chunks only.
+// N and M are K-contractions of factored operands (bf16x3 MFMA); the decay 2^{G_c - G_s} is split
+// at an anchor so neither factor overflows.  A^T is saved for the backward.
+//
+// intra_fwd_kernel (every chunk): one anchor per chunk, the first row,
+//   Lk = k 2^{G - G_0},  Lq = scale q 2^{G - G_0},  R = kappa 2^{G_0 - G}  (R <= 2^span);
+//   a chunk whose span max_i (G_0 - G_{L-1})_i exceeds kAnchorSpanMax is flagged (flags = 1).
+// intra_fwd_block_kernel (the flagged chunks): one anchor per 16-token block J,
+//   m_J = (G_{16J} + G_{16J+15})/2 per channel (rows clamped), so |G - m_J| <= span_J / 2 inside
+//   the block.  For s in block J and c in block I >= J, 2^{G_c - G_s} = (2^{G_c - m_J}) (2^{m_J - G_s}):
+//   R_J = kappa 2^{m_J - G} (published per block),  Lk_IJ = k 2^{G - m_I} 2^{m_I - m_J}  (<= 1 for J < I),
+//   Lq likewise.  A chunk handled here gets flags = 0; one with a block span past kBlockSpanMax
+//   (the masked upper-triangle products of a diagonal block reach 2^span) stays flagged for the
+//   exact per-block kernel, which runs last.
+// Random-init and trained models decay fast enough (up to ~e^-4 per token and channel) that most
+// of their chunks take the block kernel; slow-decay inputs stay on the single-anchor kernel.
 //
 // Layout of work: wave w owns row block I = w (16 rows) for the N / M build, keeping its k / q
-// factors in registers and publishing its R fragments and anchors to LDS; the U / W products
-// are split over the waves by output column tile.  LDS ~51 KB, up to 256 VGPRs: two workgroups per CU
-// (the kernel streams from HBM; a third workgroup measured no faster).
+// factors in registers and publishing its R fragments (and block anchors) to LDS; the U / W
+// products are split over the waves by output column tile.
 #pragma once
 #include <type_traits>
 #include "kdn_common.h"
@@ -37,7 +41,8 @@ using kdn_state::split2;
 using kdn_state::TILE;
 using kdn_state::zero4;
 
-constexpr float kBlockSpanMax = 120.f;  // base 2, per 16-token block: every product stays below 2^120
+constexpr float kAnchorSpanMax = 100.f;  // base 2, one anchor per chunk: R <= 2^100 stays far inside fp32
+constexpr float kBlockSpanMax = 120.f;   // base 2, per 16-token block: every product stays below 2^120
 constexpr int AP = C + 1;                // LDS row stride of the fp32 N and A tiles
 constexpr int XS = C + 4;                // LDS row stride of the staged [column][s] operands
 
@@ -83,153 +88,13 @@ __device__ __forceinline__ void st8(bufrsrc r, uint32_t off, const float* f) {
                                          r, off + 16, 0, 0);
 }
 
-// grid (NT, B*H), block 256.
-template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256, 2) void intra_fwd_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
-    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
-    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags) {
-  constexpr int KB = K / 32;
-  // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
-  constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
-  constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
-  // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
-  constexpr int SBYTES = RABYTES + C * AP * 4 > 128 * XS * 4 ? RABYTES + C * AP * 4 : 128 * XS * 4;
-  static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
-  __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
-  bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
-  float* sA = reinterpret_cast<float*>(sbuf);
-  float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
-  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
-  __shared__ float sSpan[4];
-  __shared__ __attribute__((aligned(16))) float sMid[4 * K];  // block anchors m_J per channel
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-
-  // [B,T,H,D] inputs: row c of this chunk at ((b*T + t0 + c)*H + h)*D
-  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
-  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);  // descriptor covers rows 0..L-1 of this head
-  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rv = make_buf(v + in_row0 * V, rows_in * V * 2);
-  // [B*H, T, D] outputs
-  const bufrsrc rKf = make_buf(Kf + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rQg = make_buf(Qg + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
-  const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
-  float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
-  float* An = Ag + ((int64_t)bh * NT + n) * C * C;
-
-  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels.
-  // Rows past L read zero k, q, kappa and repeat the gate of row L-1, so every factor is bounded.
-  const int c = 16 * w + r16;
-  const uint32_t crow = (uint32_t)(c * H), grow = (uint32_t)(min(c, L - 1) * H);
-  uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];  // k 2^{G - m_I}, scale q 2^{G - m_I} as split fragments
-  float span = 0.f;
-  const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    const int i0 = 32 * kb + 8 * g4;
-    float gcv[8], gl[8], kv[8], qv[8], av[8];
-    ld8(rG, (grow * K + i0) * 4, gcv);
-    ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
-    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
-    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
-    if (ISO) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) av[j] = beta * kv[j];
-    } else {
-      ld8(rkap, (crow * K + i0) * 4, av);
-    }
-    float mid[8], lk[8], lq[8], rr[8], kf[8], qg[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // the block's first and last rows (clamped) are lanes 16 g4 and 16 g4 + 15 of this wave
-      const float ga = __shfl(gcv[j], 16 * g4, 64), gb = __shfl(gcv[j], 16 * g4 + 15, 64);
-      mid[j] = 0.5f * (ga + gb);
-      const float e = exp2f(gcv[j] - mid[j]);
-      lk[j] = kv[j] * e;
-      lq[j] = scale * qv[j] * e;
-      rr[j] = av[j] * exp2f(mid[j] - gcv[j]);
-      kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
-      qg[j] = scale * qv[j] * exp2f(gcv[j]);
-      span = fmaxf(span, ga - gb);
-    }
-    split8(lk, lkh[kb], lkl[kb]);
-    split8(lq, lqh[kb], lql[kb]);
-    uint4 rh, rl;
-    split8(rr, rh, rl);
-    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + lane * 8) = rh;
-    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + 512 + lane * 8) = rl;
-    if (r16 == 0) {
-      *reinterpret_cast<float4*>(sMid + w * K + i0) = float4{mid[0], mid[1], mid[2], mid[3]};
-      *reinterpret_cast<float4*>(sMid + w * K + i0 + 4) = float4{mid[4], mid[5], mid[6], mid[7]};
-    }
-    st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
-    st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
-    __builtin_amdgcn_sched_barrier(0);  // one k-block at a time
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
-  if (lane == 0) sSpan[w] = span;
-  __syncthreads();
-  const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
-  if (!(cspan <= kBlockSpanMax)) {  // the exact kernel takes this chunk
-    if (tid == 0) flags[(int64_t)bh * NT + n] = 1;
-    return;
-  }
-  if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
-
-  // ---- 2. N and M tiles of row block I = w; column block J uses the anchor m_J on both sides
-  // (the k side carries 2^{m_I - m_J} <= 1, exactly 1 for J = I)
-  const bufrsrc rM = make_buf(Mn, C * C * 4);
-  for (int J = w + 1; J < 4; ++J)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * w + 4 * g4 + j) * C + 16 * J + r16) * 4, 0.f);
-#pragma unroll 1
-  for (int J = 0; J <= w; ++J) {
-    const int s = 16 * J + r16;
-    f32x4 aN = zero4(), aM = zero4();
-    if (J == w) {
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        uint4 rh, rl;
-        afrag(sR, J * KB + kb, lane, rh, rl);
-        aN = mma3(lkh[kb], lkl[kb], rh, rl, aN);
-        aM = mma3(lqh[kb], lql[kb], rh, rl, aM);
-      }
-    } else {  // the k side times 2^{m_I - m_J} <= 1, re-split
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const int i0 = 32 * kb + 8 * g4;
-        const float4 m0 = *reinterpret_cast<const float4*>(sMid + w * K + i0);
-        const float4 m1 = *reinterpret_cast<const float4*>(sMid + w * K + i0 + 4);
-        const float4 p0 = *reinterpret_cast<const float4*>(sMid + J * K + i0);
-        const float4 p1 = *reinterpret_cast<const float4*>(sMid + J * K + i0 + 4);
-        const float f[8] = {exp2f(m0.x - p0.x), exp2f(m0.y - p0.y), exp2f(m0.z - p0.z), exp2f(m0.w - p0.w),
-                            exp2f(m1.x - p1.x), exp2f(m1.y - p1.y), exp2f(m1.z - p1.z), exp2f(m1.w - p1.w)};
-        uint4 xh, xl, rh, rl;
-        afrag(sR, J * KB + kb, lane, rh, rl);
-        rescale8(lkh[kb], lkl[kb], f, xh, xl);
-        aN = mma3(xh, xl, rh, rl, aN);
-        rescale8(lqh[kb], lql[kb], f, xh, xl);
-        aM = mma3(xh, xl, rh, rl, aM);
-        __builtin_amdgcn_sched_barrier(0);  // one k-block at a time
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int cc = 16 * w + 4 * g4 + j;
-      sN[cc * AP + s] = (J < w || s < cc) ? aN[j] : 0.f;
-      buf_st(rM, (cc * C + s) * 4, (J < w || s <= cc) ? aM[j] : 0.f);
-    }
-  }
-  __syncthreads();
-
+// Stages after the N / M build, shared by both kernels: the inverse A = (I + N)^{-1} from sN, A^T
+// saved to An, then U = A V and W = A (k 2^G) (rows past L dropped by the output descriptors).
+// The whole LDS buffer (sA / sN / sX) is free for this function's staging after the first barrier.
+template <int K, int V>
+__device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX, float* An, bufrsrc rv, bufrsrc rk,
+                                                 bufrsrc rG, bufrsrc rU, bufrsrc rW, int H, int tid) {
+  const int lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   // ---- 3. diagonal blocks of A: X_I = (I + N_II)^{-1}, lane j < 16 of wave I owns column j
   if (lane < 16) {
     const int base = 16 * w, j = lane;
@@ -358,6 +223,285 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_kernel(
   stage(std::false_type{});
   __syncthreads();
   for (int t = w; t < K / 16; t += 4) tile(std::false_type{}, t);
+}
+
+// grid (NT, B*H), block 256.
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
+    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags) {
+  constexpr int KB = K / 32;
+  // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
+  constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
+  constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
+  // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
+  constexpr int SBYTES = RABYTES + C * AP * 4 > 128 * XS * 4 ? RABYTES + C * AP * 4 : 128 * XS * 4;
+  static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
+  __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
+  bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
+  float* sA = reinterpret_cast<float*>(sbuf);
+  float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
+  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
+  __shared__ float sSpan[4];
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+
+  // [B,T,H,D] inputs: row c of this chunk at ((b*T + t0 + c)*H + h)*D
+  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);  // descriptor covers rows 0..L-1 of this head
+  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rv = make_buf(v + in_row0 * V, rows_in * V * 2);
+  // [B*H, T, D] outputs
+  const bufrsrc rKf = make_buf(Kf + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rQg = make_buf(Qg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
+  float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
+  float* An = Ag + ((int64_t)bh * NT + n) * C * C;
+
+  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels
+  const int c = 16 * w + r16;
+  const uint32_t crow = (uint32_t)(c * H);
+  uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
+  float span = 0.f;
+  const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int i0 = 32 * kb + 8 * g4;
+    float gcv[8], g0[8], gl[8], kv[8], qv[8], av[8];
+    ld8(rG, (crow * K + i0) * 4, gcv);
+    ld8(rG, i0 * 4, g0);
+    ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
+    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
+    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
+    if (ISO) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) av[j] = beta * kv[j];
+    } else {
+      ld8(rkap, (crow * K + i0) * 4, av);
+    }
+    float lk[8], lq[8], rr[8], kf[8], qg[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = exp2f(gcv[j] - g0[j]);
+      lk[j] = kv[j] * e;
+      lq[j] = scale * qv[j] * e;
+      rr[j] = av[j] * exp2f(g0[j] - gcv[j]);
+      kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
+      qg[j] = scale * qv[j] * exp2f(gcv[j]);
+      span = fmaxf(span, g0[j] - gl[j]);
+    }
+    split8(lk, lkh[kb], lkl[kb]);
+    split8(lq, lqh[kb], lql[kb]);
+    uint4 rh, rl;
+    split8(rr, rh, rl);
+    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + lane * 8) = rh;
+    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + 512 + lane * 8) = rl;
+    st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
+    st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
+  if (lane == 0) sSpan[w] = span;
+  __syncthreads();
+  const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
+  if (!(cspan <= kAnchorSpanMax)) {  // the block-anchor kernel (or, past it, the exact one) takes this chunk
+    if (tid == 0) flags[(int64_t)bh * NT + n] = 1;
+    return;
+  }
+  if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
+
+  // ---- 2. N and M tiles of row block I = w
+  const bufrsrc rM = make_buf(Mn, C * C * 4);
+#pragma unroll
+  for (int J = 0; J < 4; ++J) {
+    const int s = 16 * J + r16;
+    if (J <= w) {
+      f32x4 aN = zero4(), aM = zero4();
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        uint4 rh, rl;
+        afrag(sR, J * KB + kb, lane, rh, rl);
+        aN = mma3(lkh[kb], lkl[kb], rh, rl, aN);
+        aM = mma3(lqh[kb], lql[kb], rh, rl, aM);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = 16 * w + 4 * g4 + j;
+        sN[cc * AP + s] = (J < w || s < cc) ? aN[j] : 0.f;
+        buf_st(rM, (cc * C + s) * 4, (J < w || s <= cc) ? aM[j] : 0.f);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * w + 4 * g4 + j) * C + s) * 4, 0.f);
+    }
+  }
+  __syncthreads();
+
+  intra_solve_emit<K, V>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid);
+}
+
+// grid (NT, B*H), block 256; a workgroup whose chunk intra_fwd_kernel did not flag exits at once.
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
+    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags) {
+  constexpr int KB = K / 32;
+  // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
+  constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
+  constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
+  // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
+  constexpr int SBYTES = RABYTES + C * AP * 4 > 128 * XS * 4 ? RABYTES + C * AP * 4 : 128 * XS * 4;
+  static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
+  __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
+  bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
+  float* sA = reinterpret_cast<float*>(sbuf);
+  float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
+  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
+  __shared__ float sSpan[4];
+  __shared__ __attribute__((aligned(16))) float sMid[4 * K];  // block anchors m_J per channel
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int64_t lin = (int64_t)bh * NT + n;
+  if (flags[lin] == 0) return;  // handled by intra_fwd_kernel
+  const int t0 = n * C, L = min(C, T - t0);
+
+  // [B,T,H,D] inputs: row c of this chunk at ((b*T + t0 + c)*H + h)*D
+  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);  // descriptor covers rows 0..L-1 of this head
+  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rv = make_buf(v + in_row0 * V, rows_in * V * 2);
+  // [B*H, T, D] outputs
+  const bufrsrc rKf = make_buf(Kf + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rQg = make_buf(Qg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
+  float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
+  float* An = Ag + ((int64_t)bh * NT + n) * C * C;
+
+  // ---- 0. block anchors m_J = (G_{16J} + G_{16J+15}) / 2 per channel (rows clamped to the chunk)
+  // and the block spans; a chunk with a span past kBlockSpanMax stays for the exact kernel
+  {
+    float span = 0.f;
+#pragma unroll
+    for (int e = tid; e < 4 * K; e += 256) {
+      const int J = e / K, i = e % K;
+      const float ga = buf_ld(rG, ((uint32_t)(min(16 * J, L - 1) * H) * K + i) * 4);
+      const float gb = buf_ld(rG, ((uint32_t)(min(16 * J + 15, L - 1) * H) * K + i) * 4);
+      sMid[e] = 0.5f * (ga + gb);
+      span = fmaxf(span, ga - gb);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
+    if (lane == 0) sSpan[w] = span;
+  }
+  __syncthreads();
+  const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
+  if (!(cspan <= kBlockSpanMax)) return;  // left flagged: the exact kernel takes this chunk
+
+  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels.
+  // Rows past L read zero k, q, kappa and repeat the gate of row L-1, so every factor is bounded.
+  const int c = 16 * w + r16;
+  const uint32_t crow = (uint32_t)(c * H), grow = (uint32_t)(min(c, L - 1) * H);
+  uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];  // k 2^{G - m_I}, scale q 2^{G - m_I} as split fragments
+  const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int i0 = 32 * kb + 8 * g4;
+    float gcv[8], gl[8], kv[8], qv[8], av[8];
+    ld8(rG, (grow * K + i0) * 4, gcv);
+    ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
+    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
+    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
+    if (ISO) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) av[j] = beta * kv[j];
+    } else {
+      ld8(rkap, (crow * K + i0) * 4, av);
+    }
+    const float4 m0 = *reinterpret_cast<const float4*>(sMid + w * K + i0);
+    const float4 m1 = *reinterpret_cast<const float4*>(sMid + w * K + i0 + 4);
+    const float mid[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    float lk[8], lq[8], rr[8], kf[8], qg[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = exp2f(gcv[j] - mid[j]);
+      lk[j] = kv[j] * e;
+      lq[j] = scale * qv[j] * e;
+      rr[j] = av[j] * exp2f(mid[j] - gcv[j]);
+      kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
+      qg[j] = scale * qv[j] * exp2f(gcv[j]);
+    }
+    split8(lk, lkh[kb], lkl[kb]);
+    split8(lq, lqh[kb], lql[kb]);
+    uint4 rh, rl;
+    split8(rr, rh, rl);
+    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + lane * 8) = rh;
+    *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + 512 + lane * 8) = rl;
+    st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
+    st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
+  }
+  __syncthreads();
+
+  // ---- 2. N and M tiles of row block I = w; column block J uses the anchor m_J on both sides
+  // (the k side carries 2^{m_I - m_J} <= 1, exactly 1 for J = I)
+  const bufrsrc rM = make_buf(Mn, C * C * 4);
+  for (int J = w + 1; J < 4; ++J)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) buf_st(rM, ((16 * w + 4 * g4 + j) * C + 16 * J + r16) * 4, 0.f);
+#pragma unroll 1
+  for (int J = 0; J <= w; ++J) {
+    const int s = 16 * J + r16;
+    f32x4 aN = zero4(), aM = zero4();
+    if (J == w) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        uint4 rh, rl;
+        afrag(sR, J * KB + kb, lane, rh, rl);
+        aN = mma3(lkh[kb], lkl[kb], rh, rl, aN);
+        aM = mma3(lqh[kb], lql[kb], rh, rl, aM);
+      }
+    } else {  // the k side times 2^{m_I - m_J} <= 1, re-split
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int i0 = 32 * kb + 8 * g4;
+        const float4 m0 = *reinterpret_cast<const float4*>(sMid + w * K + i0);
+        const float4 m1 = *reinterpret_cast<const float4*>(sMid + w * K + i0 + 4);
+        const float4 p0 = *reinterpret_cast<const float4*>(sMid + J * K + i0);
+        const float4 p1 = *reinterpret_cast<const float4*>(sMid + J * K + i0 + 4);
+        const float f[8] = {exp2f(m0.x - p0.x), exp2f(m0.y - p0.y), exp2f(m0.z - p0.z), exp2f(m0.w - p0.w),
+                            exp2f(m1.x - p1.x), exp2f(m1.y - p1.y), exp2f(m1.z - p1.z), exp2f(m1.w - p1.w)};
+        uint4 xh, xl, rh, rl;
+        afrag(sR, J * KB + kb, lane, rh, rl);
+        rescale8(lkh[kb], lkl[kb], f, xh, xl);
+        aN = mma3(xh, xl, rh, rl, aN);
+        rescale8(lqh[kb], lql[kb], f, xh, xl);
+        aM = mma3(xh, xl, rh, rl, aM);
+        __builtin_amdgcn_sched_barrier(0);  // one k-block at a time
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int cc = 16 * w + 4 * g4 + j;
+      sN[cc * AP + s] = (J < w || s < cc) ? aN[j] : 0.f;
+      buf_st(rM, (cc * C + s) * 4, (J < w || s <= cc) ? aM[j] : 0.f);
+    }
+  }
+  __syncthreads();
+
+  intra_solve_emit<K, V>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid);
+  if (tid == 0) flags[lin] = 0;
 }
 
 }  // namespace kdn_intra

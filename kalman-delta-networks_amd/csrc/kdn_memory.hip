@@ -13,7 +13,8 @@
 //   delta = U - W S_0,  O = Qg S_0 + M delta,  S_C = e^{g_last} S_0 + Kf^T delta
 //
 // Kernels (grid = one workgroup per chunk unless noted, 256 threads = 4 waves):
-//   intra_fwd    N/M (MFMA, anchored), forward substitution for U, W; Kf, Qg
+//   intra_fwd    N/M (MFMA, one anchor per chunk, then one per 16-token block for the chunks
+//                that need it), forward substitution for U, W; Kf, Qg
 //   state_fwd    serial over chunks, one workgroup per (V-slice, b, h), with the readout
 //                O = Qg h + M delta fused in (kdn_state.h)
 //   state_bwd    serial reverse (kdn_state.h): d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
@@ -770,11 +771,15 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     if (iso) {
       hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T,
                          H, NT, scale, U, W, Kf, Qg, M, A, flags);
+      hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap,
+                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
       hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
                          T, H, NT, NB, scale, U, W, Kf, Qg, M, A, flags);
     } else {
       hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc,
                          T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
+      hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap,
+                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
       hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
                          T, H, NT, NB, scale, U, W, Kf, Qg, M, A, flags);
     }
