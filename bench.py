@@ -35,7 +35,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
 
 # MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
 # MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
-MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_fwd": "bf16x3",
+MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_fwd": "bf16x3", "mem_readout_fwd": "bf16x3",
              "mem_state_bwd": "bf16x3", "mem_bwd_hgrad": "bf16x3", "mem_bwd_solve": "bf16x3",
              "mem_bwd_contrib": "bf16x3"}
 
@@ -57,9 +57,11 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
         # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M, A^T (the inverse, saved)
         "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + 2 * mm,
                           2 * (C * K + C * (V + K) / 2)),
-        # U, W, Kf, Qg, M, g_last -> h, delta, o  (readout fused into the state pass)
-        "mem_state_fwd": (4 * V + 8 * K + h_b + 4 * V + 4 * K + mm + (2 if variant == "iso" else 4) * V,
-                          2 * 2 * K * V + 2 * (K * V + C * V / 2)),
+        # U, W, Kf, g_last -> h, delta  (serial chain)
+        "mem_state_fwd": (4 * V + 8 * K + 4 * K / C + h_b + 4 * V, 2 * 2 * K * V),
+        # Qg, M, h, delta -> o  (chunk-parallel readout)
+        "mem_readout_fwd": (4 * K + mm + h_b + 4 * V + (2 if variant == "iso" else 4) * V,
+                            2 * (K * V + C * V / 2)),
         # M, Kf, Qg, W, dO -> dh, d delta
         "mem_state_bwd": (mm + 12 * K + do_b + h_b + 4 * V, 2 * (C * V / 2 + 3 * K * V)),
         # h, dh, delta, d delta, dO -> dQg, dW, dKf, dM

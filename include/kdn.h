@@ -123,8 +123,8 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
  * initial_state / final_state [B,H,K,V] f32 are nullable (state carry; the reference oracle's
  * initial_memory / output_final_state, iso_kdn_naive.py:376-440).  `saved` receives the
  * intermediates the backward consumes (kdn_mem_saved_size bytes).  `stages` selects kernels
- * (bit 0 intra-chunk WY build, bit 1 state pass with the readout o; -1 = all) so that a caller
- * can launch and time them one at a time; the stages must run in this order. */
+ * (bit 0 intra-chunk WY build, bit 1 serial state pass, bit 2 readout o; -1 = all) so that a
+ * caller can launch and time them one at a time; the stages must run in this order. */
 int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
                 const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
                 void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, int stages,

@@ -15,8 +15,8 @@
 // Kernels (grid = one workgroup per chunk unless noted, 256 threads = 4 waves):
 //   intra_fwd    N/M (MFMA, one anchor per chunk, then one per 16-token block for the chunks
 //                that need it), forward substitution for U, W; Kf, Qg
-//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h), with the readout
-//                O = Qg h + M delta fused in (kdn_state.h)
+//   state_fwd    serial over chunks, one workgroup per (V-slice, b, h): h per chunk, delta
+//   readout      chunk-parallel O = Qg h + M delta (kdn_state.h)
 //   state_bwd    serial reverse (kdn_state.h): d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
 //   bwd_hgrad    dQg = dO h^T, dW = -d delta h^T, dKf = delta dh^T, dM = dO delta^T, g_last terms
 //   bwd_solve    dV = (I+N)^-T d delta, dKg = (I+N)^-T dW, dN = -(dV U^T + dKg W^T)
@@ -785,14 +785,21 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     }
     KDN_CHECK_LAUNCH();
   }
-  if (stages & 2) {  // state pass with the fused readout
+  if (stages & 2) {  // serial state pass: h per chunk, delta, final state
     const dim3 gs(B * H * (V / kdn_state::state_cols(V))), bs(kdn_state::state_threads(V));
+    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), gs, bs, 0, stream, U, W, Kf, gc, h0, T, H, NT, B * H, hb,
+                       D, ht);
+    KDN_CHECK_LAUNCH();
+  }
+  if (stages & 4) {  // chunk-parallel readout O = Qg h + M delta
+    const int NCH = NT * B * H;  // chunk-heads; with two V halves the grid is padded to pairs of 8
+    const dim3 gr(V / 64 == 2 ? 16 * cdiv(NCH, 8) : NCH);
     if (o_bf16)
-      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t>), gs, bs, 0, stream, U, W, Kf, Qg, M, gc,
-                         h0, T, H, NT, B * H, hb, D, ht, (bf16_t*)o);
+      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, bf16_t>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
+                         B * H, (bf16_t*)o);
     else
-      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float>), gs, bs, 0, stream, U, W, Kf, Qg, M, gc,
-                         h0, T, H, NT, B * H, hb, D, ht, (float*)o);
+      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, float>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
+                         B * H, (float*)o);
     KDN_CHECK_LAUNCH();
   }
   return 0;

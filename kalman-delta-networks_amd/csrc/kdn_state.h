@@ -71,6 +71,32 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
   hi = pk2(a, b);
   lo = pk2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
+// 4 x 4 transpose across a lane quad: lane r of the quad holds row r (x, y, z, w = columns 0..3)
+// on entry and column r (rows 0..3) on return.  Round t moves element (row s, column r) from lane
+// s = (r + t) % 4 with a DPP quad permutation.
+__device__ __forceinline__ float4 quad_transpose(const float4& a, int r) {
+  const float av[4] = {a.x, a.y, a.z, a.w};
+  auto pick = [&](int i) { return i == 0 ? av[0] : i == 1 ? av[1] : i == 2 ? av[2] : av[3]; };
+  float bv[4];
+  bv[0] = bv[1] = bv[2] = bv[3] = 0.f;
+  auto place = [&](int i, float y) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bv[k] = i == k ? y : bv[k];
+  };
+  place(r, pick(r));
+  // lane r reads lane (r + t) % 4, which sends its element of column r = (its lane - t) % 4
+  place((r + 1) & 3, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pick((r - 1) & 3)), 0x39, 0xf, 0xf, false)));
+  place((r + 2) & 3, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pick((r - 2) & 3)), 0x4e, 0xf, 0xf, false)));
+  place((r + 3) & 3, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pick((r - 3) & 3)), 0x93, 0xf, 0xf, false)));
+  return float4{bv[0], bv[1], bv[2], bv[3]};
+}
+// 8 floats -> split hi/lo fragment (slot j <- x[j])
+__device__ __forceinline__ void split8v(const float* x, uint4& hi, uint4& lo) {
+  split2(x[0], x[1], hi.x, lo.x);
+  split2(x[2], x[3], hi.y, lo.y);
+  split2(x[4], x[5], hi.z, lo.z);
+  split2(x[6], x[7], hi.w, lo.w);
+}
 // hi/lo B fragment from two stacked D-layout tiles (k rows [0,16) and [16,32) of a block).
 __device__ __forceinline__ void bfrag(f32x4 t0, f32x4 t1, uint4& hi, uint4& lo) {
   split2(t0[0], t0[1], hi.x, lo.x);
@@ -146,25 +172,23 @@ __device__ __forceinline__ int64_t row_bthk(int b, int t, int h, int T, int H, i
 }
 
 // ===========================================================================
-// Forward state pass with the fused readout.  grid (B*H*V/COLS), block 4 COLS.  LDS 96.5 KB.
+// Forward state pass.  grid (B*H*V/COLS), block 4 COLS.  LDS 64.5 KB.
+// The readout O = Qg h + M delta is left to readout_kernel: it is off the serial chain, and its
+// operands (Qg, M) would double the chunk operands staged on the chain's critical path.
 // ===========================================================================
-template <int K, int V, typename TO>
+template <int K, int V>
 __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
-                                                        const float* __restrict__ Kf, const float* __restrict__ Qg,
-                                                        const float* __restrict__ Mg, const float* __restrict__ gc,
+                                                        const float* __restrict__ Kf, const float* __restrict__ gc,
                                                         const float* __restrict__ h0, int T, int H, int NT, int BH,
                                                         float* __restrict__ hbuf, float* __restrict__ Dl,
-                                                        float* __restrict__ ht, TO* __restrict__ out) {
+                                                        float* __restrict__ ht) {
   constexpr int COLS = state_cols(V), NTHR = state_threads(V), NV = V / COLS;
   constexpr int KB = K / 32;           // k-blocks of a contraction over K
   constexpr int ST = K / 16;           // state row tiles per wave
-  static_assert((C * K / 4) % NTHR == 0 && (C * C / 4) % NTHR == 0, "staging units per thread");
+  static_assert((C * K / 4) % NTHR == 0, "staging units per thread");
   constexpr int UN = C * K / 4 / NTHR;  // staging units per thread of a C x K operand
-  constexpr int UM = C * C / 4 / NTHR;  // ... of M
   __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
-  __shared__ __attribute__((aligned(16))) bf16_t sQ[(C / 16) * KB * TILE];        // Qg: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
-  __shared__ __attribute__((aligned(16))) bf16_t sM[(C / 16) * (C / 32) * TILE];  // M: rows c, k = s
   __shared__ __attribute__((aligned(16))) float sE[K];
   int bh, vs;
   xcd_map(blockIdx.x, NV, BH, bh, vs);
@@ -172,17 +196,15 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
   const int col = vs * COLS + 16 * w + (lane & 15);  // this lane's state column
 
-  float4 rW[UN], rQ[UN];
-  float rK[UN][4], rM[UM][4], rU[4][4], rE = 0.f;
-  auto load_W = [&](int n) {  // W and Qg (rows c, k = i)
+  float4 rW[UN];
+  float rK[UN][4], rU[4][4], rE = 0.f;
+  auto load_W = [&](int n) {  // W (rows c, k = i)
     const int t0 = n * C, L = min(C, T - t0);
     const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);  // rows past L read 0
-    const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const Unit x = unit<K>(tid + NTHR * u);
       rW[u] = buf_ld4(rw, (x.row * K + x.k0) * 4);
-      rQ[u] = buf_ld4(rq, (x.row * K + x.k0) * 4);
     }
   };
   auto load_K = [&](int n) {  // Kf^T (rows i, k = c), U rows of this lane, e^{g_last}
@@ -203,27 +225,14 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
       const bufrsrc rg = make_buf(gc + row_bthk(b, t0 + L - 1, h, T, H, K), K * 4);  // lanes >= K read 0
       rE = buf_ld(rg, tid * 4);
     }
-    const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][s] row-major
-#pragma unroll
-    for (int u = 0; u < UM; ++u) {
-      const Unit x = unit<C>(tid + NTHR * u);
-      const float4 m = buf_ld4(rm, (x.row * C + x.k0) * 4);
-      rM[u][0] = m.x, rM[u][1] = m.y, rM[u][2] = m.z, rM[u][3] = m.w;
-    }
   };
   auto stage_W = [&]() {
 #pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const int off = unit<K>(tid + NTHR * u).off;
-      put_unit(sW, off, rW[u].x, rW[u].y, rW[u].z, rW[u].w);
-      put_unit(sQ, off, rQ[u].x, rQ[u].y, rQ[u].z, rQ[u].w);
-    }
+    for (int u = 0; u < UN; ++u) put_unit(sW, unit<K>(tid + NTHR * u).off, rW[u].x, rW[u].y, rW[u].z, rW[u].w);
   };
   auto stage_K = [&]() {
 #pragma unroll
     for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + NTHR * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
-#pragma unroll
-    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + NTHR * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
     if (tid < K) sE[tid] = exp2f(rE);
   };
 
@@ -253,21 +262,18 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
 #pragma unroll
       for (int j = 0; j < 4; ++j) cU[cb][j] = rU[cb][j];
     if (n + 1 < NT) load_W(n + 1);
-    f32x4 D[4], O[4];
+    f32x4 D[4];
     {
       uint4 bh_[KB], bl_[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) bfrag(S[2 * kb], S[2 * kb + 1], bh_[kb], bl_[kb]);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) D[cb] = O[cb] = zero4();
-      // step s: kb = s / 8, cb = (s / 2) % 4, operand W (even s) or Qg (odd s)
-      mfma_pipe<8 * KB, 2>(
-          [&](int st, uint4& ah, uint4& al) { afrag((st & 1) ? sQ : sW, ((st >> 1) & 3) * KB + (st >> 3), lane, ah, al); },
-          [&](int st, const uint4& ah, const uint4& al) {
-            const int kb = st >> 3, cb = (st >> 1) & 3;
-            if (st & 1) O[cb] = mma3(ah, al, bh_[kb], bl_[kb], O[cb]);
-            else D[cb] = mma3(ah, al, bh_[kb], bl_[kb], D[cb]);
-          });
+      for (int cb = 0; cb < 4; ++cb) D[cb] = zero4();
+      // step s: kb = s / 4, cb = s % 4
+      mfma_pipe<4 * KB, 2>([&](int st, uint4& ah, uint4& al) { afrag(sW, (st & 3) * KB + (st >> 2), lane, ah, al); },
+                           [&](int st, const uint4& ah, const uint4& al) {
+                             D[st & 3] = mma3(ah, al, bh_[st >> 2], bl_[st >> 2], D[st & 3]);
+                           });
       const float* dl = Dl + row_bht(bh, t0, T, V);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
@@ -292,41 +298,11 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
         const float4 e = *reinterpret_cast<const float4*>(sE + 16 * ib + 4 * g4);
         S[ib] = f32x4{e.x * S[ib][0], e.y * S[ib][1], e.z * S[ib][2], e.w * S[ib][3]};
       }
-      // steps 0 .. 2 ST-1: S[ib] += Kf^T delta (kb = s / ST, ib = s % ST); then the readout
-      // O = Qg h + M delta over the nonzero M tiles (cb, kb): (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
-      mfma_pipe<2 * ST + 6, 2>(
-          [&](int st, uint4& ah, uint4& al) {
-            if (st < 2 * ST) {
-              afrag(sK, (st % ST) * 2 + st / ST, lane, ah, al);
-            } else {
-              const int m = st - 2 * ST, cb = m < 4 ? m : m - 2, kb = m < 4 ? 0 : 1;
-              afrag(sM, cb * 2 + kb, lane, ah, al);
-            }
-          },
-          [&](int st, const uint4& ah, const uint4& al) {
-            if (st < 2 * ST) {
-              const int ib = st % ST, kb = st / ST;
-              S[ib] = mma3(ah, al, dh_[kb], dl_[kb], S[ib]);
-            } else {
-              const int m = st - 2 * ST, cb = m < 4 ? m : m - 2, kb = m < 4 ? 0 : 1;
-              O[cb] = mma3(ah, al, dh_[kb], dl_[kb], O[cb]);
-            }
-          });
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        // rows 16 cb .. of this chunk, H*V apart; the descriptor ends right after row L-1's head h
-        const int r0 = 16 * cb;
-        const bufrsrc ro = make_buf(out + row_bthk(b, t0 + r0, h, T, H, V),
-                                    L > r0 ? ((L - 1 - r0) * H + 1) * V * (uint32_t)sizeof(TO) : 0u);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t e = (uint32_t)((4 * g4 + j) * H) * V + col;
-          if constexpr (sizeof(TO) == 2)
-            __builtin_amdgcn_raw_buffer_store_b16(f2bf(O[cb][j]), ro, e * 2, 0, 0);
-          else
-            buf_st(ro, e * 4, O[cb][j]);
-        }
-      }
+      // step s: S[ib] += Kf^T delta (kb = s / ST, ib = s % ST)
+      mfma_pipe<2 * ST, 2>([&](int st, uint4& ah, uint4& al) { afrag(sK, (st % ST) * 2 + st / ST, lane, ah, al); },
+                           [&](int st, const uint4& ah, const uint4& al) {
+                             S[st % ST] = mma3(ah, al, dh_[st / ST], dl_[st / ST], S[st % ST]);
+                           });
     }
     __syncthreads();
   }
@@ -335,6 +311,126 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
     for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
       for (int j = 0; j < 4; ++j) ht[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] = S[ib][j];
+  }
+}
+
+// ===========================================================================
+// Forward readout, chunk-parallel:  O = Qg h + M delta  per chunk, from the state pass's h (the
+// state entering the chunk) and delta.  grid: one workgroup per (chunk, head, 64 columns of V), see
+// below; block 256, LDS 48 KB.
+// Computed transposed, O^T = h^T Qg^T + delta^T M^T, so each lane's D tile holds 4 consecutive
+// columns of one chunk row (8- or 16-byte stores).  h^T and delta^T (A operands, contraction over
+// the state row i / the chunk row s) are staged once per workgroup as split fragments in LDS; the
+// B operands Qg^T and M^T are rows of Qg and M, loaded straight into registers by the wave that
+// owns those 16 chunk rows.  Fragment k order is natural (slot j of lane group g <-> k = 8 g + j).
+// ===========================================================================
+template <int K, int V, typename TO>
+__global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict__ Qg, const float* __restrict__ Mg,
+                                                         const float* __restrict__ hbuf, const float* __restrict__ Dl,
+                                                         int T, int H, int NT, int BH, TO* __restrict__ out) {
+  constexpr int VC = 64;                 // columns of V per workgroup
+  constexpr int KB = K / 32, VT = VC / 16;
+  static_assert(V % VC == 0, "V is a multiple of 64");
+  __shared__ __attribute__((aligned(16))) bf16_t sH[VT * KB * TILE];  // h^T: rows v, k = i
+  __shared__ __attribute__((aligned(16))) bf16_t sD[VT * 2 * TILE];   // delta^T: rows v, k = s
+  // workgroup lin -> (chunk of a head, V half): the two halves of a chunk are lin and lin + 8, which
+  // dispatch round-robin puts on one XCD, so they share Qg and M through its L2
+  static_assert(V / VC == 2 || V / VC == 1, "one or two column halves");
+  const int lin = blockIdx.x, NH = V / VC;
+  const int ch = NH == 2 ? 8 * (lin >> 4) + (lin & 7) : lin, half = NH == 2 ? (lin >> 3) & 1 : 0;
+  if (ch >= NT * BH) return;
+  const int n = ch % NT, bh = ch / NT, v0 = VC * half, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int64_t chunk = (int64_t)bh * NT + n;
+
+  // ---- B operands of this wave's 16 chunk rows c = 16 w + r16: Qg row (k = i) and M row (k = s)
+  const uint32_t c = (uint32_t)(16 * w + r16);
+  const bufrsrc rQ = make_buf(Qg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rM = make_buf(Mg + chunk * C * C, C * C * 4);
+  float4 q4[KB][2], m4[2][2];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) q4[kb][p] = buf_ld4(rQ, (c * K + 32 * kb + 8 * g4 + 4 * p) * 4);
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) m4[kb][p] = buf_ld4(rM, (c * C + 32 * kb + 8 * g4 + 4 * p) * 4);
+
+  // ---- stage h^T and delta^T.  A wave loads 4 rows x 64 columns per instruction (lane l: row
+  // 4 rb + l % 4, columns 4 (l / 4) .. +3), transposes each 4 x 4 block across its lane quad (DPP),
+  // so a lane holds 4 consecutive rows of one column: 4 consecutive fragment slots of one lane,
+  // written as 8 bytes of hi and 8 of lo
+  {
+    const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
+    const bufrsrc rd = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);  // rows past L read 0
+    constexpr int HU = K / 16, DU = C / 16;  // 4-row blocks per wave
+    const int qr = lane & 3, vq = 4 * (lane >> 2), vc = vq + qr;  // after the transpose: column vc
+    float4 hx[HU], dx[DU];
+#pragma unroll
+    for (int u = 0; u < HU; ++u) hx[u] = buf_ld4(rh, ((4 * (w + 4 * u) + qr) * V + v0 + vq) * 4);
+#pragma unroll
+    for (int u = 0; u < DU; ++u) dx[u] = buf_ld4(rd, ((4 * (w + 4 * u) + qr) * V + v0 + vq) * 4);
+    auto put = [&](bf16_t* buf, int nkb, int r0, const float4& x) {  // rows r0 .. r0+3 of column vc
+      const float4 y = quad_transpose(x, qr);
+      const int tile = (vc >> 4) * nkb + (r0 >> 5), ln = (vc & 15) + 16 * ((r0 & 31) >> 3);
+      uint32_t h0, l0, h1, l1;
+      split2(y.x, y.y, h0, l0);
+      split2(y.z, y.w, h1, l1);
+      const int off = tile * TILE + ln * 8 + (r0 & 7);
+      *reinterpret_cast<uint2*>(buf + off) = uint2{h0, h1};
+      *reinterpret_cast<uint2*>(buf + off + 512) = uint2{l0, l1};
+    };
+#pragma unroll
+    for (int u = 0; u < HU; ++u) put(sH, KB, 4 * (w + 4 * u), hx[u]);
+#pragma unroll
+    for (int u = 0; u < DU; ++u) put(sD, 2, 4 * (w + 4 * u), dx[u]);
+  }
+  uint4 qh[KB], ql[KB], mh[2], ml[2];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const float x[8] = {q4[kb][0].x, q4[kb][0].y, q4[kb][0].z, q4[kb][0].w,
+                        q4[kb][1].x, q4[kb][1].y, q4[kb][1].z, q4[kb][1].w};
+    split8v(x, qh[kb], ql[kb]);
+  }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const float x[8] = {m4[kb][0].x, m4[kb][0].y, m4[kb][0].z, m4[kb][0].w,
+                        m4[kb][1].x, m4[kb][1].y, m4[kb][1].z, m4[kb][1].w};
+    split8v(x, mh[kb], ml[kb]);
+  }
+  __syncthreads();
+
+  // ---- O^T tiles (v tile vt, chunk rows 16 w ..): M[c][s] = 0 for s > c, so chunk-row tiles 0, 1
+  // skip the second s block
+  const int r0 = 16 * w;
+  const bufrsrc ro = make_buf(out + row_bthk(b, t0 + r0, h, T, H, V),
+                              L > r0 ? ((L - 1 - r0) * H + 1) * V * (uint32_t)sizeof(TO) : 0u);
+#pragma unroll
+  for (int vt = 0; vt < VT; ++vt) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      uint4 ah, al;
+      afrag(sH, vt * KB + kb, lane, ah, al);
+      acc = mma3(ah, al, qh[kb], ql[kb], acc);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if (kb == 1 && w < 2) continue;
+      uint4 ah, al;
+      afrag(sD, vt * 2 + kb, lane, ah, al);
+      acc = mma3(ah, al, mh[kb], ml[kb], acc);
+    }
+    const uint32_t e = (uint32_t)(r16 * H) * V + v0 + 16 * vt + 4 * g4;  // rows past L dropped
+    if constexpr (sizeof(TO) == 2) {
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(acc[0]) | ((uint32_t)f2bf(acc[1]) << 16), (uint32_t)f2bf(acc[2]) | ((uint32_t)f2bf(acc[3]) << 16)},
+          ro, e * 2, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ro, e * 4, 0, 0);
+    }
   }
 }
 

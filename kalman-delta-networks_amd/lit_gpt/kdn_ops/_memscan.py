@@ -9,7 +9,7 @@ import torch
 
 from . import _lib
 
-FWD_STAGES = ((1, "mem_intra_fwd"), (2, "mem_state_fwd"))  # the state pass writes the readout o
+FWD_STAGES = ((1, "mem_intra_fwd"), (2, "mem_state_fwd"), (4, "mem_readout_fwd"))
 BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_hgrad"), (4, "mem_bwd_solve"), (8, "mem_bwd_contrib"))
 
 
