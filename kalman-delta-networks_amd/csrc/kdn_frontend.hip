@@ -158,16 +158,21 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
+  // per-token omega / r: thread tid owns token tid (chunk <= 256; loads clamped to the chunk)
+  const int64_t sro = (int64_t)b * orr_sb + (int64_t)(t0 + min(tid, L - 1)) * orr_st + h;
+  const float or_t = ld(orr, sro), rr_t = ld(orr, sro + H);
   // every load of this thread's tokens goes out first (rows clamped to the chunk; the clamped
   // duplicates are never used), so the thread waits for memory once
-  float xr[4][8], oraw[4], rraw[4];
+  float xr[4][8];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int t = min(tg * TPG + u, L - 1);
     load8<TG>(g_raw + (((int64_t)b * T + t0 + t) * H + h) * K + i0, xr[u]);
-    const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
-    oraw[u] = ld(orr, ro);
-    rraw[u] = ld(orr, ro + H);
+  }
+  if (tid < L) {
+    const int64_t o = ((int64_t)b * T + t0 + tid) * H + h;
+    omega_out[o] = omega_min + softplusf(or_t + omega_bias[h]);
+    r_out[o] = r_min + softplusf(rr_t + r_bias[h]);
   }
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float pre[4][8];  // local inclusive prefix per token (TPG <= 4 when K >= 64 and chunk <= 64)
@@ -207,12 +212,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     // a = mean over channels of e^{2g}: reduce over the CG consecutive lanes of this token group
     float s = e2[u];
     for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
-    if (cg == 0 && u < TPG && t < L) {
-      const int64_t o = ((int64_t)b * T + t0 + t) * H + h;
-      a_out[o] = s / (float)K;
-      omega_out[o] = omega_min + softplusf(oraw[u] + omega_bias[h]);
-      r_out[o] = r_min + softplusf(rraw[u] + r_bias[h]);
-    }
+    if (cg == 0 && u < TPG && t < L) a_out[((int64_t)b * T + t0 + t) * H + h] = s / (float)K;
   }
   if (blockIdx.x == 0 && tid == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
 }
@@ -227,6 +227,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     TG* __restrict__ dg_raw, TO* __restrict__ dorr, float* __restrict__ part_A, float* __restrict__ part_dt,
     float* __restrict__ part_bias) {
   __shared__ float s_tot[256 * 8];
+  __shared__ float s_da[256];
   __shared__ float red[16];
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
   const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
@@ -236,22 +237,25 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
-  // every load of this thread's tokens goes out first (rows clamped to the chunk; the clamped
-  // duplicates are never used), so the thread waits for memory once
-  float dgr_in[4][8], xr[4][8], dav[4], dov[4], drv[4], oraw[4], rraw[4];
+  // per-token scalars: thread tid owns token tid (chunk <= 256; loads clamped to the chunk, only
+  // tid < L is used), so each is loaded once rather than by every channel group
+  const int64_t srow = ((int64_t)b * T + t0 + min(tid, L - 1)) * H + h;
+  const float da_t = da ? da[srow] : 0.f;
+  const float do_t = domega ? domega[srow] : 0.f;
+  const float dr_t = dr ? dr[srow] : 0.f;
+  const int64_t sro = (int64_t)b * orr_sb + (int64_t)(t0 + min(tid, L - 1)) * orr_st + h;
+  const float or_t = ld(orr, sro), rr_t = ld(orr, sro + H);
+  // every vector load of this thread's tokens goes out first (rows clamped to the chunk; the
+  // clamped duplicates are never used), so the thread waits for memory once
+  float dgr_in[4][8], xr[4][8];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int t = min(tg * TPG + u, L - 1);
     const int64_t row = ((int64_t)b * T + t0 + t) * H + h;
     if (dg_pre) load8<float>(dg_pre + row * K + i0, dgr_in[u]);
     load8<TG>(g_raw + row * K + i0, xr[u]);
-    dav[u] = da ? da[row] : 0.f;
-    dov[u] = domega ? domega[row] : 0.f;
-    drv[u] = dr ? dr[row] : 0.f;
-    const int64_t ro = (int64_t)b * orr_sb + (int64_t)(t0 + t) * orr_st + h;
-    oraw[u] = ld(orr, ro);
-    rraw[u] = ld(orr, ro + H);
   }
+  s_da[tid] = da_t * (2.f / (float)K);
   // local suffix sums of dg_pre over this thread's tokens (last token first)
   float dgp[4][8], acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -284,7 +288,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     if (u < TPG && t < L) {
       const int64_t row = ((int64_t)b * T + t0 + t) * H + h;
       float dgr[8];
-      const float dau = dav[u] * (2.f / (float)K);
+      const float dau = s_da[t];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float xb = xr[u][j] + bias[j];
@@ -296,17 +300,17 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
         ddt[j] += dgr[j];
       }
       if (dg_raw) store8<TG>(dg_raw + row * K + i0, dgr);
-      if (cg == 0) {
-        const float ob = domega ? dov[u] * sigmoidf(oraw[u] + omega_bias[h]) : 0.f;
-        const float rb = dr ? drv[u] * sigmoidf(rraw[u] + r_bias[h]) : 0.f;
-        dob += ob;
-        drb += rb;
-        if (dorr) {
-          const int64_t wo = ((int64_t)b * T + t0 + t) * (2 * H) + h;
-          st(dorr, wo, ob);
-          st(dorr, wo + H, rb);
-        }
-      }
+    }
+  }
+  if (tid < L) {  // the per-token omega / r terms of token tid
+    const float ob = domega ? do_t * sigmoidf(or_t + omega_bias[h]) : 0.f;
+    const float rb = dr ? dr_t * sigmoidf(rr_t + r_bias[h]) : 0.f;
+    dob = ob;
+    drb = rb;
+    if (dorr) {
+      const int64_t wo = ((int64_t)b * T + t0 + tid) * (2 * H) + h;
+      st(dorr, wo, ob);
+      st(dorr, wo + H, rb);
     }
   }
   // per-channel ddt partial: sum over token groups
@@ -899,9 +903,9 @@ inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // The vectorised gate kernels need 8-channel groups that tile 256 threads, at most 4 tokens per
 // thread, and 16-byte aligned rows.
 inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-inline bool gate_vec_ok(int K, int chunk) {
-  if (K % 8 != 0 || 256 % (K / 8) != 0) return false;
-  return chunk <= 4 * (256 / (K / 8));
+inline bool gate_vec_ok(int K, int chunk) {  // the vector kernels also give each of the chunk's
+  if (K % 8 != 0 || 256 % (K / 8) != 0) return false;  // tokens one thread: chunk <= 256
+  return chunk <= 4 * (256 / (K / 8)) && chunk <= 256;
 }
 // Row kernels: K/8 lanes per row, 8 elements per lane (K/8 a power of two dividing 64).
 inline bool row_vec_ok(int K) { return K % 8 == 0 && K <= 512 && 64 % (K / 8) == 0; }
