@@ -168,14 +168,17 @@ def test_memory_scan_mixed_anchor_and_exact_chunks(variant):
 
 
 @pytest.mark.parametrize("variant", ["iso", "diag"])
-@pytest.mark.parametrize("ell_mean,ell_std", [(-1.5, 0.8), (-4.0, 0.3)])
-def test_memory_scan_large_decay_block_anchors(variant, ell_mean, ell_std):
+@pytest.mark.parametrize("ell_mean,ell_std,shape", [(-1.5, 0.8, (1, 200, 2, 128, 128)),
+                                                    (-4.0, 0.3, (1, 200, 2, 128, 128)),
+                                                    (-2.0, 0.5, (2, 130, 2, 64, 64))])
+def test_memory_scan_large_decay_block_anchors(variant, ell_mean, ell_std, shape):
     """Per-token decays of e^-1.5 to e^-4 (a 64-token chunk spans ~140 to ~370 in base 2), the range
     a randomly initialised 1.3B model produces: far outside one anchor per chunk, inside the
-    per-16-token block anchors (block spans <= ~100), so the MFMA path must match the oracle."""
+    per-16-token block anchors (block spans <= ~100), so the MFMA block-anchor kernels must match
+    the oracle, at d = 128 and d = 64 with a partial last chunk."""
     dev = gpu_or_skip()
-    B, T, H, K, V = 1, 200, 2, 128, 128
-    log(f"case memory large decay {variant} ell~N({ell_mean},{ell_std})")
+    B, T, H, K, V = shape
+    log(f"case memory large decay {variant} ell~N({ell_mean},{ell_std}) B={B} T={T} H={H} K={K} V={V}")
     iso = variant == "iso"
     q, k, v, ell, kap, do = memory_inputs(41, B, T, H, K, V, diag=not iso, ell_mean=ell_mean, ell_std=ell_std)
     scale = K ** -0.5

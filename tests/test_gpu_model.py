@@ -61,13 +61,13 @@ def test_rms_norm_matches_oracle(rows, D, dtype):
     assert torch.equal(dw, dw2)
 
 
-def _layer(variant, dev, seed):
+def _layer(variant, dev, seed, head_dim=64):
     torch.manual_seed(seed)
     if variant == "iso":
         from lit_gpt.iso_kdn import IsotropicKalmanDeltaNetwork as L
     else:
         from lit_gpt.diag_kdn import DiagonalKalmanDeltaNetwork as L
-    layer = L(hidden_size=128, head_dim=64, num_heads=2)
+    layer = L(hidden_size=2 * head_dim, head_dim=head_dim, num_heads=2)
     with torch.no_grad():
         # move off the zero / one initial values so every parameter's gradient is exercised
         for name, p in layer.named_parameters():
@@ -112,19 +112,19 @@ def test_iso_layer_fp32_eval_matches_oracle():
     _compare_layer(layer, p_ref, xd, xg, out, out_ref, dy)
 
 
-@pytest.mark.parametrize("variant", ["iso", "diag"])
-def test_layer_bf16_autocast_training_matches_oracle(variant):
+@pytest.mark.parametrize("variant,head_dim", [("iso", 64), ("diag", 64), ("iso", 128), ("diag", 128)])
+def test_layer_bf16_autocast_training_matches_oracle(variant, head_dim):
     dev = gpu_or_skip()
-    B, T = 2, 130
-    log(f"case {variant} layer autocast training B={B} T={T} H=2 K=64")
-    layer = _layer(variant, dev, 1).train()
+    B, T, D = 2, 130, 2 * head_dim
+    log(f"case {variant} layer autocast training B={B} T={T} H=2 K={head_dim}")
+    layer = _layer(variant, dev, 1, head_dim).train()
     g = torch.Generator().manual_seed(12)
-    x = torch.randn(B, T, 128, generator=g)
-    dy = torch.randn(B, T, 128, generator=g).bfloat16().float()  # exact in bf16 and fp32
+    x = torch.randn(B, T, D, generator=g)
+    dy = torch.randn(B, T, D, generator=g).bfloat16().float()  # exact in bf16 and fp32
     p_ref = _oracle_params(layer)
     xd = x.double().requires_grad_(True)
     if variant == "iso":
-        out_ref = ko.iso_layer(p_ref, xd, info_scale=64.0, amp=True)
+        out_ref = ko.iso_layer(p_ref, xd, info_scale=float(head_dim), amp=True)
     else:
         out_ref = ko.diag_layer(p_ref, xd, amp=True)
     xg = x.to(dev).requires_grad_(True)
