@@ -72,23 +72,31 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
   lo = pk2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 // 4 x 4 transpose across a lane quad: lane r of the quad holds row r (x, y, z, w = columns 0..3)
-// on entry and column r (rows 0..3) on return.  Round t moves element (row s, column r) from lane
-// s = (r + t) % 4 with a DPP quad permutation.
-__device__ __forceinline__ float4 quad_transpose(const float4& a, int r) {
-  const float av[4] = {a.x, a.y, a.z, a.w};
-  auto pick = [&](int i) { return i == 0 ? av[0] : i == 1 ? av[1] : i == 2 ? av[2] : av[3]; };
-  float bv[4];
-  bv[0] = bv[1] = bv[2] = bv[3] = 0.f;
-  auto place = [&](int i, float y) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) bv[k] = i == k ? y : bv[k];
+// on entry and column r (rows 0..3) on return.  Two butterfly stages with DPP quad permutations:
+// swap the off-diagonal elements of the 2 x 2 blocks between lanes r and r ^ 1, then the
+// off-diagonal 2 x 2 blocks between lanes r and r ^ 2.
+__device__ __forceinline__ float4 quad_transpose(const float4& x, int r) {
+  auto dpp = [](float v, int ctrl) {
+    return __int_as_float(ctrl == 0xb1 ? __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false)
+                                       : __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
   };
-  place(r, pick(r));
-  // lane r reads lane (r + t) % 4, which sends its element of column r = (its lane - t) % 4
-  place((r + 1) & 3, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pick((r - 1) & 3)), 0x39, 0xf, 0xf, false)));
-  place((r + 2) & 3, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pick((r - 2) & 3)), 0x4e, 0xf, 0xf, false)));
-  place((r + 3) & 3, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(pick((r - 3) & 3)), 0x93, 0xf, 0xf, false)));
-  return float4{bv[0], bv[1], bv[2], bv[3]};
+  float a0 = x.x, a1 = x.y, a2 = x.z, a3 = x.w;
+  const bool odd = r & 1, hi = r & 2;
+  {  // lanes r, r ^ 1: even lanes take the partner's columns 0, 2 into slots 1, 3; odd lanes the reverse
+    const float r0 = dpp(odd ? a0 : a1, 0xb1), r1 = dpp(odd ? a2 : a3, 0xb1);
+    a0 = odd ? r0 : a0;
+    a1 = odd ? a1 : r0;
+    a2 = odd ? r1 : a2;
+    a3 = odd ? a3 : r1;
+  }
+  {  // lanes r, r ^ 2: the upper lanes take the partner's slots 2, 3 into slots 0, 1; lower the reverse
+    const float r0 = dpp(hi ? a0 : a2, 0x4e), r1 = dpp(hi ? a1 : a3, 0x4e);
+    a0 = hi ? r0 : a0;
+    a1 = hi ? r1 : a1;
+    a2 = hi ? a2 : r0;
+    a3 = hi ? a3 : r1;
+  }
+  return float4{a0, a1, a2, a3};
 }
 // 8 floats -> split hi/lo fragment (slot j <- x[j])
 __device__ __forceinline__ void split8v(const float* x, uint4& hi, uint4& lo) {
