@@ -52,14 +52,18 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
 /* Workspace of kdn_iso_gain_fwd / kdn_iso_gain_bwd (per-chunk maps and carries). */
 size_t kdn_iso_gain_workspace_size(int B, int T, int H);
 /* _iso_kdn_gain_forward (iso_kdn_chunk.py:1598-1664): beta [B,T,H]; p_prev (nullable) saves
- * the incoming covariance per token for the backward; final_precision [B,H] (nullable).  H <= 96. */
-int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision, int B, int T,
-                     int H, float posterior_scale, float* beta, float* p_prev, float* final_precision,
-                     void* workspace, size_t workspace_bytes, hipStream_t stream);
-/* _iso_kdn_gain_backward (iso_kdn_chunk.py:1817-1893); d_initial_precision [H] is summed over B
- * in a fixed order (deterministic). */
+ * the incoming covariance per token for the backward; final_precision [B,H] (nullable).  H <= 96.
+ * initial_precision is [H] (prec_mode 0, the reference's only form) or [B,H] (prec_mode 1: the
+ * final_precision of an earlier segment, for state continuation; the reference has no such mode). */
+int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision,
+                     int prec_mode, int B, int T, int H, float posterior_scale, float* beta, float* p_prev,
+                     float* final_precision, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* _iso_kdn_gain_backward (iso_kdn_chunk.py:1817-1893); d_initial_precision is [H] summed over B
+ * in a fixed order (deterministic) for prec_mode 0, [B,H] for prec_mode 1.  d_final_precision
+ * (nullable; needs final_precision from the forward) is the cotangent of final_precision. */
 int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const float* initial_precision,
-                     const float* dbeta, const float* p_prev, int B, int T, int H, float posterior_scale, float* da,
+                     int prec_mode, const float* dbeta, const float* p_prev, const float* final_precision,
+                     const float* d_final_precision, int B, int T, int H, float posterior_scale, float* da,
                      float* domega, float* dr, float* d_initial_precision, void* workspace, size_t workspace_bytes,
                      hipStream_t stream);
 
@@ -140,6 +144,18 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
                 float* dg, float* d_initial_state, int stages, hipStream_t stream);
+/* One token of the memory recurrence with a carried state (decode).  The reference has no step
+ * kernel (it refuses caching for KDN layers, model.py:104,184); this is the tokenwise recurrence
+ * of iso_kdn_naive.py:308-332 / diag_kdn_naive.py:479-500 on the scan's state layout:
+ * S = 2^g (.) S; delta = v - S^T k; S += kappa delta^T; o = scale S^T q.  q, k [B,H,K] and
+ * v [B,H,V] share a dtype (qkv_bf16: bf16, else f32); g [B,H,K] f32 is the token's base-2 log
+ * decay (kdn_mem_fwd's g_cumsum at T = 1).  iso = 1: kappa_or_beta is beta [B,H] and q, k are
+ * L2-normalised inside (x rsqrt(sum x^2 + 1e-6)), kappa = beta k_hat; iso = 0: kappa [B,H,K]
+ * f32 and q, k are used as given.  state [B,H,K,V] f32 is read and overwritten in place;
+ * o [B,H,V] (o_bf16: bf16, else f32).  K, V in {64, 128}; state 16-byte aligned. */
+int kdn_mem_step(const void* q, const void* k, const float* kappa_or_beta, int iso, const void* v, int qkv_bf16,
+                 const float* g, int B, int H, int K, int V, float scale, float* state, void* o, int o_bf16,
+                 hipStream_t stream);
 
 /* ---------------------------------------------------------------- layer frontends */
 /* Depthwise causal short convolution with SiLU, fixed length, width W = 4, no bias:

@@ -95,13 +95,15 @@ __global__ __launch_bounds__(256) void iso_gain_map_kernel(const float* __restri
   }
 }
 
-// grid (B*H), block 64: p at each chunk start (carry) and the final precision.
+// grid (B*H), block 64: p at each chunk start (carry) and the final precision.  The initial
+// precision mu is per head ([H], prec_mode 0) or per batch row and head ([B,H], prec_mode 1: the
+// final precision of an earlier segment of the same sequences).
 __global__ __launch_bounds__(64) void iso_gain_carry_kernel(const float4* __restrict__ maps,
-                                                            const float* __restrict__ mu, int H, int NC,
-                                                            float* __restrict__ carry,
+                                                            const float* __restrict__ mu, int prec_mode, int H,
+                                                            int NC, float* __restrict__ carry,
                                                             float* __restrict__ final_precision) {
   const int bh = blockIdx.x, h = bh % H, lane = threadIdx.x;
-  float p = 1.f / mu[h];
+  float p = 1.f / mu[prec_mode ? bh : h];
   for (int c0 = 0; c0 < NC; c0 += 64) {
     const int c = c0 + lane;
     Map2 M = map_identity();
@@ -209,16 +211,21 @@ __global__ __launch_bounds__(256) void iso_gain_bwd_map_kernel(const float* __re
 }
 
 // grid (H), block 64 * GB (GB = min(B, 16)): wave g scans batch rows b = g, g + GB, ... from the
-// last chunk back; lambda after each chunk goes to `carry`, and d mu = -sum_b lambda_0 / mu^2.
+// last chunk back; lambda after each chunk goes to `carry`.  lambda after the last token is the
+// cotangent of p_T: with final precision c_T = 1/p_T and its cotangent dc, lambda_T = -dc c_T^2
+// (zero without dc).  d mu = -lambda_0 / mu^2, summed over b for a per-head mu (prec_mode 0), per
+// batch row for mu [B,H] (prec_mode 1).
 __global__ __launch_bounds__(1024) void iso_gain_bwd_carry_kernel(const float2* __restrict__ maps,
-                                                                  const float* __restrict__ mu, int B, int H, int NC,
+                                                                  const float* __restrict__ mu, int prec_mode, int B,
+                                                                  int H, int NC, const float* __restrict__ fprec,
+                                                                  const float* __restrict__ dfprec,
                                                                   float* __restrict__ carry, float* __restrict__ dmu) {
   __shared__ float sMu[16];
   const int h = blockIdx.x, lane = threadIdx.x & 63, g = threadIdx.x >> 6, GB = blockDim.x >> 6;
   float dmu_acc = 0.f;
   for (int b = g; b < B; b += GB) {
     const int64_t bh = (int64_t)b * H + h;
-    float lam = 0.f;  // lambda after the last chunk
+    float lam = dfprec ? -dfprec[bh] * fprec[bh] * fprec[bh] : 0.f;  // lambda after the last token
     for (int c1 = NC; c1 > 0; c1 -= 64) {
       const int c = c1 - 1 - lane;  // lane 0 = latest chunk of this group
       float2 F{1.f, 0.f};
@@ -234,8 +241,13 @@ __global__ __launch_bounds__(1024) void iso_gain_bwd_carry_kernel(const float2* 
       if (c >= 0) carry[bh * NC + c] = Ae * lam + Be;  // lambda after chunk c
       lam = __shfl(F.x, 63, 64) * lam + __shfl(F.y, 63, 64);
     }
-    if (lane == 0) dmu_acc += -lam / (mu[h] * mu[h]);
+    if (prec_mode) {
+      if (lane == 0 && dmu) dmu[bh] = -lam / (mu[bh] * mu[bh]);
+    } else if (lane == 0) {
+      dmu_acc += -lam / (mu[h] * mu[h]);
+    }
   }
+  if (prec_mode) return;
   if (lane == 0) sMu[g] = dmu_acc;
   __syncthreads();
   if (threadIdx.x == 0 && dmu) {
@@ -871,10 +883,11 @@ size_t kdn_iso_gain_workspace_size(int B, int T, int H) {
   return (size_t)((int64_t)B * H * NC * 5) * sizeof(float);
 }
 
-int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision, int B, int T,
-                     int H, float posterior_scale, float* beta, float* p_prev, float* final_precision,
-                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
+int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision,
+                     int prec_mode, int B, int T, int H, float posterior_scale, float* beta, float* p_prev,
+                     float* final_precision, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f) || (prec_mode != 0 && prec_mode != 1))
+    return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
   if (workspace_bytes < kdn_iso_gain_workspace_size(B, T, H)) return KDN_ERR_ARG;
   const int NC = cdiv(T, kIsoChunk);
@@ -885,8 +898,8 @@ int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const f
   const size_t lds_emit = (size_t)(5 * kIsoChunk * H + 4 * kIsoSub * H) * sizeof(float);
   hipLaunchKernelGGL(iso_gain_map_kernel, dim3(NC, B), dim3(256), lds_map, stream, a, omega, r, T, H, NC,
                      posterior_scale, maps);
-  hipLaunchKernelGGL(iso_gain_carry_kernel, dim3(B * H), dim3(64), 0, stream, maps, initial_precision, H, NC, carry,
-                     final_precision);
+  hipLaunchKernelGGL(iso_gain_carry_kernel, dim3(B * H), dim3(64), 0, stream, maps, initial_precision, prec_mode, H,
+                     NC, carry, final_precision);
   hipLaunchKernelGGL(iso_gain_emit_kernel, dim3(NC, B), dim3(256), lds_emit, stream, a, omega, r, B, T, H, NC,
                      posterior_scale, unit, carry, beta, p_prev);
   KDN_CHECK_LAUNCH();
@@ -894,10 +907,13 @@ int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const f
 }
 
 int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const float* initial_precision,
-                     const float* dbeta, const float* p_prev, int B, int T, int H, float posterior_scale, float* da,
+                     int prec_mode, const float* dbeta, const float* p_prev, const float* final_precision,
+                     const float* d_final_precision, int B, int T, int H, float posterior_scale, float* da,
                      float* domega, float* dr, float* d_initial_precision, void* workspace, size_t workspace_bytes,
                      hipStream_t stream) {
-  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
+  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f) || (prec_mode != 0 && prec_mode != 1))
+    return KDN_ERR_ARG;
+  if (d_final_precision && !final_precision) return KDN_ERR_ARG;
   if (B == 0 || T == 0) return 0;
   if (workspace_bytes < kdn_iso_gain_workspace_size(B, T, H)) return KDN_ERR_ARG;
   const int NC = cdiv(T, kIsoChunk);
@@ -909,8 +925,8 @@ int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const f
   const int GB = B < 16 ? B : 16;
   hipLaunchKernelGGL(iso_gain_bwd_map_kernel, dim3(NC, B), dim3(256), lds_map, stream, a, omega, r, dbeta, p_prev, T,
                      H, NC, posterior_scale, maps);
-  hipLaunchKernelGGL(iso_gain_bwd_carry_kernel, dim3(H), dim3(64 * GB), 0, stream, maps, initial_precision, B, H, NC,
-                     carry, d_initial_precision);
+  hipLaunchKernelGGL(iso_gain_bwd_carry_kernel, dim3(H), dim3(64 * GB), 0, stream, maps, initial_precision, prec_mode,
+                     B, H, NC, final_precision, d_final_precision, carry, d_initial_precision);
   hipLaunchKernelGGL(iso_gain_bwd_emit_kernel, dim3(NC, B), dim3(256), lds_emit, stream, a, omega, r, dbeta, p_prev, T,
                      H, NC, posterior_scale, unit, carry, da, domega, dr);
   KDN_CHECK_LAUNCH();

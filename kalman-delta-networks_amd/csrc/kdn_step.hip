@@ -1,0 +1,163 @@
+// Single-token step of the KDN memory recurrence (decode with a carried state).
+//
+// The reference runs only fixed-length sequences and has no step kernel; its recurrence is the
+// tokenwise one of iso_kdn_naive.py:308-332 and diag_kdn_naive.py:479-500:
+//   S_hat = diag(e) S,  e = 2^g (g = the token's base-2 log decay, the chunked scan's g_cumsum
+//   at T = 1);  delta = v - S_hat^T k;  S = S_hat + kappa delta^T;  o = scale S^T q.
+// For the isotropic variant kappa = beta k_hat and q, k are L2-normalised here exactly as the
+// chunked scan normalises them (x * rsqrt(sum x^2 + 1e-6)); the diagonal variant takes
+// normalised q, k and an explicit kappa.  State layout is the scan's h0 / ht layout
+// [B,H,K,V] fp32, so a chunked prefill's final state feeds this kernel directly.
+//
+// One workgroup per (b, h, 32-column slice of V), 256 threads: thread t owns columns
+// 4 (t & 7) .. +3 of the slice and rows rg + 32 j (rg = t >> 3, j < K / 32), so each row's 128
+// bytes of the slice are read and written by 8 neighbouring lanes (float4 each).  The two sums
+// over K (delta and o) reduce over lane bits 3..5 with xor shuffles, then over the 4 waves in LDS.
+// HBM traffic per token is 2 K V 4 bytes of state (read + write) plus the vectors.
+#include "kdn_common.h"
+
+namespace {
+
+constexpr float kL2Eps = 1e-6f;
+
+__device__ __forceinline__ float4 f4_fma(float a, const float4& x, const float4& y) {
+  return float4{fmaf(a, x.x, y.x), fmaf(a, x.y, y.y), fmaf(a, x.z, y.z), fmaf(a, x.w, y.w)};
+}
+__device__ __forceinline__ float4 f4_scale(float a, const float4& x) { return float4{a * x.x, a * x.y, a * x.z, a * x.w}; }
+__device__ __forceinline__ float4 f4_add(const float4& x, const float4& y) {
+  return float4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
+}
+__device__ __forceinline__ float4 f4_sub(const float4& x, const float4& y) {
+  return float4{x.x - y.x, x.y - y.y, x.z - y.z, x.w - y.w};
+}
+__device__ __forceinline__ float4 f4_xor(const float4& x, int m) {
+  return float4{__shfl_xor(x.x, m, 64), __shfl_xor(x.y, m, 64), __shfl_xor(x.z, m, 64), __shfl_xor(x.w, m, 64)};
+}
+
+// Sum of x over the 32 row groups of the workgroup for this thread's 4 columns; valid in every
+// thread.  `red` is [4 waves][8 column groups] of float4; the caller separates two uses by a
+// barrier or uses two buffers.
+__device__ __forceinline__ float4 rows_sum(float4 x, float4* red) {
+  x = f4_add(x, f4_xor(x, 8));
+  x = f4_add(x, f4_xor(x, 16));
+  x = f4_add(x, f4_xor(x, 32));
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane < 8) red[w * 8 + lane] = x;
+  __syncthreads();
+  const int c = lane & 7;
+  return f4_add(f4_add(red[c], red[8 + c]), f4_add(red[16 + c], red[24 + c]));
+}
+
+template <typename T> __device__ __forceinline__ float4 ld4(const T* p);
+template <> __device__ __forceinline__ float4 ld4<float>(const float* p) { return *reinterpret_cast<const float4*>(p); }
+template <> __device__ __forceinline__ float4 ld4<bf16_t>(const bf16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return float4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                __uint_as_float(u.y & 0xffff0000u)};
+}
+template <typename T> __device__ __forceinline__ void st4(T* p, const float4& x);
+template <> __device__ __forceinline__ void st4<float>(float* p, const float4& x) { *reinterpret_cast<float4*>(p) = x; }
+template <> __device__ __forceinline__ void st4<bf16_t>(bf16_t* p, const float4& x) {
+  const uint2 u{(uint32_t)f2bf(x.x) | ((uint32_t)f2bf(x.y) << 16), (uint32_t)f2bf(x.z) | ((uint32_t)f2bf(x.w) << 16)};
+  *reinterpret_cast<uint2*>(p) = u;
+}
+
+// grid (B * H * V / 32), block 256.
+template <int K, int V, typename TI, typename TO, bool ISO>
+__global__ __launch_bounds__(256) void mem_step_kernel(const TI* __restrict__ q, const TI* __restrict__ k,
+                                                       const float* __restrict__ kappa_or_beta,
+                                                       const TI* __restrict__ v, const float* __restrict__ g,
+                                                       float scale, float* __restrict__ state, TO* __restrict__ o) {
+  constexpr int NS = V / 32, R = K / 32;
+  __shared__ float4 red[2][32];
+  const int64_t bh = blockIdx.x / NS;
+  const int slice = blockIdx.x % NS, t = threadIdx.x, lane = t & 63, c4 = t & 7, rg = t >> 3;
+  const TI* qp = q + bh * K;
+  const TI* kp = k + bh * K;
+  float qs = 1.f, ks = 1.f;
+  if (ISO) {  // every wave forms both norms itself (K <= 128: two elements per lane)
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int i = lane; i < K; i += 64) {
+      const float a = ld(qp, i), b = ld(kp, i);
+      sq = fmaf(a, a, sq);
+      sk = fmaf(b, b, sk);
+    }
+    qs = 1.f / sqrtf(wave_sum(sq) + kL2Eps);
+    ks = 1.f / sqrtf(wave_sum(sk) + kL2Eps);
+  }
+  const float beta = ISO ? kappa_or_beta[bh] : 0.f;
+  const int col = slice * 32 + 4 * c4;
+  float* sp = state + bh * K * V + col;
+  float4 S[R];
+  float kr[R], qr[R], kap[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int row = rg + 32 * j;
+    S[j] = *reinterpret_cast<const float4*>(sp + (int64_t)row * V);
+    kr[j] = ld(kp, row) * ks;
+    qr[j] = ld(qp, row) * qs;
+    kap[j] = ISO ? beta * kr[j] : kappa_or_beta[bh * K + row];
+    S[j] = f4_scale(exp2f(g[bh * K + row]), S[j]);
+  }
+  float4 acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < R; ++j) acc = f4_fma(kr[j], S[j], acc);
+  const float4 delta = f4_sub(ld4(v + bh * V + col), rows_sum(acc, red[0]));
+  acc = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    S[j] = f4_fma(kap[j], delta, S[j]);
+    *reinterpret_cast<float4*>(sp + (int64_t)(rg + 32 * j) * V) = S[j];
+    acc = f4_fma(qr[j], S[j], acc);
+  }
+  const float4 out = rows_sum(acc, red[1]);
+  if (t < 8) st4(o + bh * V + col, f4_scale(scale, out));
+}
+
+template <int K, int V, typename TI, typename TO>
+void launch_step(bool iso, const void* q, const void* k, const float* kb, const void* v, const float* g, int BH,
+                 float scale, float* state, void* o, hipStream_t stream) {
+  const dim3 grid(BH * (V / 32)), block(256);
+  if (iso)
+    hipLaunchKernelGGL((mem_step_kernel<K, V, TI, TO, true>), grid, block, 0, stream, (const TI*)q, (const TI*)k, kb,
+                       (const TI*)v, g, scale, state, (TO*)o);
+  else
+    hipLaunchKernelGGL((mem_step_kernel<K, V, TI, TO, false>), grid, block, 0, stream, (const TI*)q, (const TI*)k, kb,
+                       (const TI*)v, g, scale, state, (TO*)o);
+}
+
+template <int K, int V>
+void launch_step_kv(bool iso, const void* q, const void* k, int qkv_bf16, const float* kb, const void* v,
+                    const float* g, int BH, float scale, float* state, void* o, int o_bf16, hipStream_t stream) {
+  if (qkv_bf16 && o_bf16) launch_step<K, V, bf16_t, bf16_t>(iso, q, k, kb, v, g, BH, scale, state, o, stream);
+  else if (qkv_bf16) launch_step<K, V, bf16_t, float>(iso, q, k, kb, v, g, BH, scale, state, o, stream);
+  else if (o_bf16) launch_step<K, V, float, bf16_t>(iso, q, k, kb, v, g, BH, scale, state, o, stream);
+  else launch_step<K, V, float, float>(iso, q, k, kb, v, g, BH, scale, state, o, stream);
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int kdn_mem_step(const void* q, const void* k, const float* kappa_or_beta, int iso, const void* v, int qkv_bf16,
+                 const float* g, int B, int H, int K, int V, float scale, float* state, void* o, int o_bf16,
+                 hipStream_t stream) {
+  if (B < 0 || H <= 0 || (K != 64 && K != 128) || (V != 64 && V != 128)) return KDN_ERR_ARG;
+  if (B == 0) return 0;
+  if (!q || !k || !kappa_or_beta || !v || !g || !state || !o) return KDN_ERR_ARG;
+  // float4 state rows and 4-element vector loads / stores
+  if (!aligned(state, 16) || !aligned(v, qkv_bf16 ? 8 : 16) || !aligned(o, o_bf16 ? 8 : 16)) return KDN_ERR_ARG;
+  const int BH = B * H;
+  const bool is_iso = iso != 0;
+  if (K == 64 && V == 64) launch_step_kv<64, 64>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
+  else if (K == 64) launch_step_kv<64, 128>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
+  else if (V == 64) launch_step_kv<128, 64>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
+  else launch_step_kv<128, 128>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // extern "C"

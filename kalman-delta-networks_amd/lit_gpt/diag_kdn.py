@@ -23,6 +23,8 @@ from .kdn_ops.diag_kdn_chunk import (_chunk_kalman_as, _diag_kdn_frontend_precum
                                      _diag_kdn_normalize)
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.short_conv import causal_conv1d
+from .kdn_ops.step import kdn_memory_step
+from .kdn_state import CONV_TAIL, KDNLayerState, check_state, conv_input_with_tail
 
 _OMEGA_MIN = 0.0
 _R_MIN = 0.01
@@ -47,7 +49,7 @@ class ShortConvolution(nn.Module):
 
 
 class DiagonalKalmanDeltaNetwork(nn.Module):
-    """Fixed-length Diagonal KDN mixer (reference diag_kdn.py:101-357)."""
+    """Diagonal KDN mixer (reference diag_kdn.py:101-357), plus an optional carried state."""
 
     def __init__(self, hidden_size: int = 2304, head_dim: int = 128, num_heads: int = 18, expand_v: float = 1.0,
                  num_v_heads=None, use_short_conv: bool = True, conv_size: int = 4, conv_bias: bool = False,
@@ -104,14 +106,18 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
 
     def forward(self, hidden_states, attention_mask=None, past_key_values=None, use_cache=False,
                 output_attentions=False, **kwargs):
+        """Returns ``(output, None, state)``.  Without ``past_key_values`` / ``use_cache`` this is the
+        reference's fixed-length forward and ``state`` is None.  With them (state carry, which the
+        reference refuses): ``past_key_values`` is the ``KDNLayerState`` after the earlier tokens (None:
+        no earlier tokens) and ``use_cache=True`` returns the state after these tokens.  One token
+        without autograd runs the single-token step kernel; longer segments run the chunked scan from
+        the carried state."""
         requested = tuple(n for n, on in (("attention_mask", attention_mask is not None),
-                                          ("past_key_values", past_key_values is not None),
-                                          ("use_cache", use_cache is not False),
                                           ("output_attentions", output_attentions is not False),
                                           ("kwargs", bool(kwargs))) if on)
         if requested:
-            raise ValueError("DiagonalKalmanDeltaNetwork supports only fixed-length sequences; "
-                             f"unsupported arguments: {requested}")
+            raise ValueError("DiagonalKalmanDeltaNetwork supports only fixed-length sequences (with an optional "
+                             f"carried state); unsupported arguments: {requested}")
         if hidden_states.ndim != 3 or hidden_states.shape[-1] != self.hidden_size:
             raise ValueError(f"hidden_states must have shape [B,T,{self.hidden_size}], "
                              f"got {tuple(hidden_states.shape)}")
@@ -125,9 +131,22 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
         validate_training_dtype("Diagonal", training=self.training, hidden_dtype=hidden_states.dtype)
         B, T, _ = hidden_states.shape
         H, K, V = self.num_heads, self.head_k_dim, self.head_v_dim
-        q = self.q_conv1d(self.q_proj(hidden_states)).view(B, T, H, K)
-        k = self.k_conv1d(self.k_proj(hidden_states)).view(B, T, H, K)
-        v = self.v_conv1d(self.v_proj(hidden_states)).view(B, T, H, V)
+        stateful = past_key_values is not None or bool(use_cache)
+        state = past_key_values
+        if state is not None:
+            check_state(state, B, H, K, V, 3, (B, H, K), hidden_states.device)
+        projections = (self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states))
+        convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d)
+        if stateful:
+            tails, outs = [], []
+            for i, (x, conv) in enumerate(zip(projections, convs)):
+                xc, tail = conv_input_with_tail(x, state.conv[i] if state is not None else None)
+                outs.append(conv(xc)[:, CONV_TAIL:].contiguous())
+                tails.append(tail)
+            q, k, v = outs
+        else:
+            q, k, v = (conv(x) for x, conv in zip(projections, convs))
+        q, k, v = q.reshape(B, T, H, K), k.reshape(B, T, H, K), v.reshape(B, T, H, V)
         retention_raw = self.f_proj(hidden_states).view(B, T, H, K)
         omega_raw = self.omega_proj(hidden_states).view(B, T, H, K)
         r_raw = self.r_proj(hidden_states)
@@ -135,11 +154,30 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
         g_cumsum, alpha, omega, r, initial_precision = _diag_kdn_frontend_precumsum_paired(
             retention_raw, omega_raw, r_raw, self.A_log.float(), self.dt_bias.float().view(H, K),
             self.initial_precision_param.float())
-        kappa = _diag_kdn_gain(k_gain, alpha, omega, r, initial_precision, omega_raw, r_raw)
-        # the f32 recurrence is stored at the value dtype, as the reference's .to(v.dtype) does
-        output = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, float(K ** -0.5), out_dtype=v.dtype)
+        new_state = None
+        scale = float(K ** -0.5)
+        if not stateful:
+            kappa = _diag_kdn_gain(k_gain, alpha, omega, r, initial_precision, omega_raw, r_raw)
+            # the f32 recurrence is stored at the value dtype, as the reference's .to(v.dtype) does
+            output = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale, out_dtype=v.dtype)
+        else:
+            kappa, precision = _diag_kdn_gain(k_gain, alpha, omega, r,
+                                              state.precision if state is not None else initial_precision,
+                                              omega_raw, r_raw, output_final_state=True)
+            if T == 1 and not torch.is_grad_enabled():
+                memory = (state.memory.clone() if state is not None else
+                          torch.zeros(B, H, K, V, device=q.device, dtype=torch.float32))
+                output = kdn_memory_step(q_memory, k_memory, v, g_cumsum, state=memory, kappa=kappa, scale=scale,
+                                         out_dtype=v.dtype)
+            else:
+                output, memory = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale,
+                                                  initial_state=state.memory if state is not None else None,
+                                                  output_final_state=True, out_dtype=v.dtype)
+            if use_cache:
+                new_state = KDNLayerState(tuple(tails), memory, precision,
+                                          (state.seen_tokens if state is not None else 0) + T)
         output = self.o_norm(output, self.g_proj(hidden_states).view(B, T, H, V))
-        return self.o_proj(output.reshape(B, T, self.value_dim)), None, None
+        return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
 
 
 __all__ = ("DiagonalKalmanDeltaNetwork", "ShortConvolution")

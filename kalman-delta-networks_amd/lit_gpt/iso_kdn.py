@@ -22,6 +22,8 @@ from torch import nn
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
 from .kdn_ops.short_conv import qkv_causal_conv1d
+from .kdn_ops.step import kdn_memory_step
+from .kdn_state import CONV_TAIL, KDNLayerState, check_state, conv_input_with_tail
 
 _SUPPORTED_HEAD_DIMS = (64, 128)
 _INITIAL_PRECISION = 1.0
@@ -94,7 +96,7 @@ class _Bias(nn.Module):
 
 
 class IsotropicKalmanDeltaNetwork(nn.Module):
-    """Fixed-length Isotropic KDN mixer (reference iso_kdn.py:84-314)."""
+    """Isotropic KDN mixer (reference iso_kdn.py:84-314), plus an optional carried state."""
 
     def __init__(self, hidden_size: int = 2304, head_dim: int = 128, num_heads: int = 18, expand_v: float = 1.0,
                  num_v_heads=None, use_short_conv: bool = True, conv_size: int = 4, conv_bias: bool = False,
@@ -152,14 +154,18 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
 
     def forward(self, hidden_states, attention_mask=None, past_key_values=None, use_cache=False,
                 output_attentions=False, **kwargs):
+        """Returns ``(output, None, state)``.  Without ``past_key_values`` / ``use_cache`` this is the
+        reference's fixed-length forward and ``state`` is None.  With them (state carry, which the
+        reference refuses): ``past_key_values`` is the ``KDNLayerState`` after the earlier tokens (None:
+        no earlier tokens) and ``use_cache=True`` returns the state after these tokens.  One token
+        without autograd runs the single-token step kernel; longer segments run the chunked scan from
+        the carried state."""
         requested = tuple(n for n, on in (("attention_mask", attention_mask is not None),
-                                          ("past_key_values", past_key_values is not None),
-                                          ("use_cache", use_cache is not False),
                                           ("output_attentions", output_attentions is not False),
                                           ("kwargs", bool(kwargs))) if on)
         if requested:
-            raise ValueError("IsotropicKalmanDeltaNetwork supports only fixed-length sequences; "
-                             f"unsupported arguments: {requested}")
+            raise ValueError("IsotropicKalmanDeltaNetwork supports only fixed-length sequences (with an optional "
+                             f"carried state); unsupported arguments: {requested}")
         if hidden_states.ndim != 3 or hidden_states.shape[-1] != self.hidden_size:
             raise ValueError(f"hidden_states must have shape [B,T,{self.hidden_size}], "
                              f"got {tuple(hidden_states.shape)}")
@@ -173,22 +179,48 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         validate_training_dtype("Isotropic", training=self.training, hidden_dtype=hidden_states.dtype)
         B, T, _ = hidden_states.shape
         H, K = self.num_heads, self.head_k_dim
-        q, k, v = self.qkv_pack(hidden_states)
+        stateful = past_key_values is not None or bool(use_cache)
+        state = past_key_values
+        if state is not None:
+            check_state(state, B, H, K, self.head_v_dim, 1, (B, H), hidden_states.device)
+        if stateful:
+            x_proj, conv_tail = conv_input_with_tail(F.linear(hidden_states, self.qkv_pack.projection_weight),
+                                                     state.conv[0] if state is not None else None)
+            q, k, v = (t[:, CONV_TAIL:] for t in qkv_causal_conv1d(x_proj, self.qkv_pack.convolution_weight))
+        else:
+            q, k, v = self.qkv_pack(hidden_states)
         packed = self.f_omega_r_proj.forward_packed(hidden_states)
         f_hidden, omega_r_raw = packed.split((self.head_v_dim, 2 * H), dim=-1)
         g_raw = self.f_proj[1](f_hidden)
-        q, k = q.view(B, T, H, K), k.view(B, T, H, K)
-        v = v.view(B, T, H, self.head_v_dim)
+        q, k = q.reshape(B, T, H, K), k.reshape(B, T, H, K)
+        v = v.reshape(B, T, H, self.head_v_dim)
         g_raw = g_raw.view(B, T, H, K)
         g_cumsum, a, omega, r, initial_precision = _iso_kdn_gate_precumsum_paired(
             g_raw, omega_r_raw, self.omega_proj.bias.float(), self.r_proj.bias.float(), self.A_log.float(),
             self.dt_bias.float(), self.initial_precision_param.float(), self.omega_min, self.r_min)
-        gain = iso_kdn_gain(a, omega, r, initial_precision, head_dim=K, out_dtype=torch.float32,
-                            info_scale=self.info_scale)
-        output = _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain)
+        new_state = None
+        if not stateful:
+            gain = iso_kdn_gain(a, omega, r, initial_precision, head_dim=K, out_dtype=torch.float32,
+                                info_scale=self.info_scale)
+            output = _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain)
+        else:
+            gain, precision = iso_kdn_gain(a, omega, r, state.precision if state is not None else initial_precision,
+                                           head_dim=K, out_dtype=torch.float32, info_scale=self.info_scale,
+                                           output_final_state=True)
+            if T == 1 and not torch.is_grad_enabled():
+                memory = (state.memory.clone() if state is not None else
+                          torch.zeros(B, H, K, self.head_v_dim, device=q.device, dtype=torch.float32))
+                output = kdn_memory_step(q, k, v, g_cumsum, state=memory, beta=gain)
+            else:
+                output, memory = _chunk_kda_precumsum_paired(
+                    q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain,
+                    initial_state=state.memory if state is not None else None, output_final_state=True)
+            if use_cache:
+                new_state = KDNLayerState((conv_tail,), memory, precision,
+                                          (state.seen_tokens if state is not None else 0) + T)
         gate = self.g_proj(hidden_states).view(B, T, H, self.head_v_dim)
         output = self.o_norm(output, gate)
-        return self.o_proj(output.reshape(B, T, self.value_dim)), None, None
+        return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
 
 
 __all__ = ("IsotropicKalmanDeltaNetwork", "PackedQKV", "PackedLinear")

@@ -20,8 +20,8 @@ _SIGS = {
     "kdn_iso_gate_bwd_workspace_size": "iiiii",
     "kdn_iso_gate_bwd": "pipillppppppppppiiiiippppppppzs",
     "kdn_iso_gain_workspace_size": "iii",
-    "kdn_iso_gain_fwd": "ppppiiifppppzs",
-    "kdn_iso_gain_bwd": "ppppppiiifpppppzs",
+    "kdn_iso_gain_fwd": "ppppiiiifppppzs",
+    "kdn_iso_gain_bwd": "ppppippppiiifpppppzs",
     "kdn_l2norm_fwd": "pilifpips",
     "kdn_l2norm_bwd": "pippilips",
     "kdn_diag_norm_fwd": "ppilippppps",
@@ -37,6 +37,7 @@ _SIGS = {
     "kdn_mem_bwd_workspace_size": "iiiii",
     "kdn_mem_fwd": "pppippiiiiifppzppiis",
     "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppis",
+    "kdn_mem_step": "pppipipiiiifppis",
     "kdn_short_conv_fwd": "pillpiiiiiplls",
     "kdn_short_conv_bwd_workspace_size": "iii",
     "kdn_short_conv_bwd": "pillpiplliiiiipllppzs",

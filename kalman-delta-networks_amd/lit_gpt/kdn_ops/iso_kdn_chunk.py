@@ -206,82 +206,112 @@ def _require_same_cuda_device(a, *named_tensors):
     return device
 
 
-def _iso_kdn_gain_forward(a, omega, r, initial_precision, *, out_dtype, save_state, posterior_scale):
+def _iso_kdn_gain_forward(a, omega, r, initial_precision, *, out_dtype, save_state, posterior_scale,
+                          output_final_state=False):
+    """Returns (beta, p_prev or None, final_precision [B,H] or None).  ``initial_precision`` is
+    [H] (the reference's form) or [B,H] (continuation of an earlier segment)."""
     B, T, H = a.shape
     device = _require_same_cuda_device(a, ("omega", omega), ("r", r), ("initial_precision", initial_precision))
+    prec_mode = 0 if initial_precision.ndim == 1 else 1
     gain = torch.empty((B, T, H), dtype=torch.float32, device=device)
     p_prev = torch.empty((B, T, H), dtype=torch.float32, device=device) if save_state else None
+    fprec = None
+    if output_final_state:
+        fprec = torch.empty((B, H), dtype=torch.float32, device=device)
+        if T == 0:
+            fprec.copy_(initial_precision.float().expand(B, H))
     if T > 0 and B > 0:
         ws_bytes = _lib.size("kdn_iso_gain_workspace_size", B, T, H)
         ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
         with torch.cuda.device(device):
             _lib.call("kdn_iso_gain_fwd", _lib.ptr(a), _lib.ptr(omega), _lib.ptr(r),
-                      _lib.ptr(initial_precision), B, T, H, float(posterior_scale), _lib.ptr(gain),
-                      _lib.ptr(p_prev), None, _lib.ptr(ws), ws_bytes, _lib.stream_of(a))
-    return (gain if out_dtype == torch.float32 else gain.to(out_dtype)), p_prev
+                      _lib.ptr(initial_precision), prec_mode, B, T, H, float(posterior_scale), _lib.ptr(gain),
+                      _lib.ptr(p_prev), _lib.ptr(fprec), _lib.ptr(ws), ws_bytes, _lib.stream_of(a))
+    return (gain if out_dtype == torch.float32 else gain.to(out_dtype)), p_prev, fprec
 
 
-def _iso_kdn_gain_backward(a, omega, r, initial_precision, dgain, p_prev, *, posterior_scale):
+def _iso_kdn_gain_backward(a, omega, r, initial_precision, dgain, p_prev, *, posterior_scale,
+                           final_precision=None, d_final_precision=None):
     B, T, H = a.shape
     device = _require_same_cuda_device(a, ("omega", omega), ("r", r), ("initial_precision", initial_precision),
                                        ("dgain", dgain), ("previous_covariance", p_prev))
+    prec_mode = 0 if initial_precision.ndim == 1 else 1
     da = torch.empty_like(a)
     domega = torch.empty_like(omega)
     dr = torch.empty_like(r)
-    dmu = torch.zeros((H,), dtype=torch.float32, device=device)
+    dmu = torch.zeros(initial_precision.shape, dtype=torch.float32, device=device)
     if T > 0 and B > 0:
         ws_bytes = _lib.size("kdn_iso_gain_workspace_size", B, T, H)
         ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
+        dfp = d_final_precision.float().contiguous() if d_final_precision is not None else None
         with torch.cuda.device(device):
             _lib.call("kdn_iso_gain_bwd", _lib.ptr(a), _lib.ptr(omega), _lib.ptr(r), _lib.ptr(initial_precision),
-                      _lib.ptr(dgain), _lib.ptr(p_prev), B, T, H, float(posterior_scale), _lib.ptr(da),
-                      _lib.ptr(domega), _lib.ptr(dr), _lib.ptr(dmu), _lib.ptr(ws), ws_bytes, _lib.stream_of(a))
+                      prec_mode, _lib.ptr(dgain), _lib.ptr(p_prev), _lib.ptr(final_precision if dfp is not None
+                                                                             else None),
+                      _lib.ptr(dfp), B, T, H, float(posterior_scale), _lib.ptr(da), _lib.ptr(domega), _lib.ptr(dr),
+                      _lib.ptr(dmu), _lib.ptr(ws), ws_bytes, _lib.stream_of(a))
+    elif d_final_precision is not None and B > 0:
+        # no tokens: the final precision is the initial one
+        dfp = d_final_precision.float()
+        dmu.copy_(dfp if prec_mode else dfp.sum(0))
     return da, domega, dr, dmu.to(initial_precision.dtype)
 
 
 class _IsoKDNGainFunction(torch.autograd.Function):
-    """Reference iso_kdn_chunk.py:1896-1962."""
+    """Reference iso_kdn_chunk.py:1896-1962, plus the optional final precision output."""
 
     @staticmethod
-    def forward(ctx, a, omega, r, initial_precision, out_dtype, posterior_scale, needs_backward):
-        gain, p_prev = _iso_kdn_gain_forward(a, omega, r, initial_precision, out_dtype=out_dtype,
-                                             save_state=needs_backward, posterior_scale=posterior_scale)
+    def forward(ctx, a, omega, r, initial_precision, out_dtype, posterior_scale, needs_backward,
+                output_final_state=False):
+        gain, p_prev, fprec = _iso_kdn_gain_forward(a, omega, r, initial_precision, out_dtype=out_dtype,
+                                                    save_state=needs_backward, posterior_scale=posterior_scale,
+                                                    output_final_state=output_final_state)
         ctx.posterior_scale = posterior_scale
         ctx.has_saved_state = needs_backward
         if needs_backward:
-            ctx.save_for_backward(a, omega, r, initial_precision, p_prev)
+            ctx.save_for_backward(a, omega, r, initial_precision, p_prev, fprec)
+        if output_final_state:
+            return gain, fprec
         return gain
 
     @staticmethod
-    def backward(ctx, dgain):
-        if dgain is None:
-            return None, None, None, None, None, None, None
+    def backward(ctx, dgain, d_final_precision=None):
+        if dgain is None and d_final_precision is None:
+            return None, None, None, None, None, None, None, None
         if not ctx.has_saved_state:
             raise RuntimeError("Isotropic KDN gain backward called after a no-save forward")
-        a, omega, r, initial_precision, p_prev = ctx.saved_tensors
-        da, domega, dr, dmu = _iso_kdn_gain_backward(a, omega, r, initial_precision,
-                                                     dgain.float().contiguous(), p_prev,
-                                                     posterior_scale=ctx.posterior_scale)
+        a, omega, r, initial_precision, p_prev, fprec = ctx.saved_tensors
+        dgain = torch.zeros_like(a) if dgain is None else dgain.float().contiguous()
+        da, domega, dr, dmu = _iso_kdn_gain_backward(a, omega, r, initial_precision, dgain, p_prev,
+                                                     posterior_scale=ctx.posterior_scale, final_precision=fprec,
+                                                     d_final_precision=d_final_precision)
         needs = ctx.needs_input_grad
         return (da if needs[0] else None, domega if needs[1] else None, dr if needs[2] else None,
-                dmu if needs[3] else None, None, None, None)
+                dmu if needs[3] else None, None, None, None, None)
 
 
 @torch.compiler.disable
-def iso_kdn_gain(a, omega, r, initial_precision, *, head_dim, out_dtype=None, info_scale=None):
+def iso_kdn_gain(a, omega, r, initial_precision, *, head_dim, out_dtype=None, info_scale=None,
+                 output_final_state=False):
     """Differentiable Isotropic KDN scalar write gate beta [B,T,H] (reference :1965-2031).
 
     z = a p + omega;  beta = z / (r + z);  p' = r z / (r + s z),  s = info_scale / head_dim,
     p_0 = 1 / initial_precision.  Keys are unit-normalised on the production path, so |k|^2 = 1.
+
+    State continuation (not in the reference, which takes only [H]): ``initial_precision`` may be
+    [B,H], and ``output_final_state=True`` returns ``(beta, final_precision [B,H] fp32)`` with
+    final_precision = 1 / p_T, so a sequence split into segments gives the beta of the whole when
+    each segment starts from the previous segment's final precision.  Gradients flow through both.
     """
     if a.ndim != 3:
         raise ValueError(f"a must have shape [B,T,H], got {tuple(a.shape)}")
     if omega.shape != a.shape or r.shape != a.shape:
         raise ValueError("a, omega, and r must share shape [B,T,H]; got "
                          f"a={tuple(a.shape)}, omega={tuple(omega.shape)}, r={tuple(r.shape)}")
-    H = a.shape[-1]
-    if initial_precision.ndim != 1 or initial_precision.shape[0] != H:
-        raise ValueError(f"initial_precision must have shape [{H}], got {tuple(initial_precision.shape)}")
+    B, _, H = a.shape
+    if initial_precision.shape not in ((H,), (B, H)):
+        raise ValueError(f"initial_precision must have shape [{H}] or [{B},{H}], "
+                         f"got {tuple(initial_precision.shape)}")
     _require_same_cuda_device(a, ("omega", omega), ("r", r), ("initial_precision", initial_precision))
     if isinstance(head_dim, bool) or not isinstance(head_dim, int):
         raise TypeError(f"head_dim must be a positive int, got {type(head_dim).__name__}")
@@ -302,7 +332,7 @@ def iso_kdn_gain(a, omega, r, initial_precision, *, head_dim, out_dtype=None, in
         t.requires_grad for t in (a, omega, r, initial_precision))
     return _IsoKDNGainFunction.apply(a.float().contiguous(), omega.float().contiguous(), r.float().contiguous(),
                                      initial_precision.float().contiguous(), out_dtype, posterior_scale,
-                                     needs_backward)
+                                     needs_backward, bool(output_final_state))
 
 
 # ---------------------------------------------------------------------------
@@ -341,38 +371,50 @@ def _chunk_kda_bwd_precum(q, k, v, g_cumsum, beta, saved, scale, do, *, d_final_
 
 
 class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
-    """Reference iso_kdn_chunk.py:2190-2238: L2-normalise q, k inside; memory scan; VJPs."""
+    """Reference iso_kdn_chunk.py:2190-2238: L2-normalise q, k inside; memory scan; VJPs.  With an
+    initial state h0 [B,H,K,V] and / or the final state requested, their gradients flow too."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g_cumsum, beta, scale):
+    def forward(ctx, q, k, v, g_cumsum, beta, scale, initial_state=None, output_final_state=False):
         dev = q.device
         with torch.cuda.device(dev):
             qn, q_rstd = _l2norm_fwd(q)
             kn, k_rstd = _l2norm_fwd(k)
             vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
-            o, saved, _ = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
-                                                out_dtype=q.dtype if q.dtype == torch.float32 else torch.bfloat16)
+            o, saved, ht = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
+                                                 initial_state=initial_state, output_final_state=output_final_state,
+                                                 out_dtype=q.dtype if q.dtype == torch.float32 else torch.bfloat16)
         ctx.save_for_backward(q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved)
         ctx.scale = scale
-        return o if o.dtype == q.dtype else o.to(q.dtype)
+        ctx.h0_dtype = initial_state.dtype if initial_state is not None else None
+        o = o if o.dtype == q.dtype else o.to(q.dtype)
+        return (o, ht) if output_final_state else o
 
     @staticmethod
-    def backward(ctx, do):
+    def backward(ctx, do, dht=None):
         q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved = ctx.saved_tensors
+        need_h0 = ctx.h0_dtype is not None and ctx.needs_input_grad[6]
         with torch.cuda.device(q.device):
-            dqn, dkn, dv, db, dg, _ = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do)
+            dqn, dkn, dv, db, dg, dh0 = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do,
+                                                              d_final_state=dht, need_initial_state_grad=need_h0)
             dq = _l2norm_bwd(q, q_rstd, dqn)
             dk = _l2norm_bwd(k, k_rstd, dkn)
-        return dq, dk, dv, dg, db, None
+        dh0 = dh0.to(ctx.h0_dtype) if dh0 is not None else None
+        return dq, dk, dv, dg, db, None, dh0, None
 
 
 @torch.compiler.disable
-def _chunk_kda_precumsum_paired(q, k, v, g_cumsum, beta, scale=None):
+def _chunk_kda_precumsum_paired(q, k, v, g_cumsum, beta, scale=None, *, initial_state=None,
+                                output_final_state=False):
     """Consume the private paired cumulative gate on the fixed-length path (reference :2241-2285).
 
     ``g_cumsum`` must be the unbranched output of :func:`_iso_kdn_gate_precumsum_paired`.
     Returns o [B,T,H,V] in q's dtype; the backward returns the natural-log-coordinate gate
     cotangent expected by that producer.
+
+    State continuation (the reference's wrapper passes no state): ``initial_state`` [B,H,K,V]
+    starts the memory from an earlier segment's state, and ``output_final_state=True`` returns
+    ``(o, final_state [B,H,K,V] fp32)``.
     """
     if q.ndim != 4 or q.shape != k.shape:
         raise ValueError(f"q and k must share [B,T,H,K], got {tuple(q.shape)} and {tuple(k.shape)}")
@@ -402,10 +444,17 @@ def _chunk_kda_precumsum_paired(q, k, v, g_cumsum, beta, scale=None):
         raise ValueError("_chunk_kda_precumsum_paired is GPU-only")
     if len({x.device for x in tensors}) != 1:
         raise ValueError("all _chunk_kda_precumsum_paired tensors must be on the same GPU device")
+    if initial_state is not None:
+        if initial_state.shape != (B, H, K, v.shape[-1]) or initial_state.device != q.device:
+            raise ValueError(f"initial_state must be a tensor of shape {(B, H, K, v.shape[-1])} on {q.device}")
+        if initial_state.dtype != torch.float32:
+            raise TypeError(f"initial_state must be fp32, got {initial_state.dtype}")
     if scale is None:
         scale = K ** -0.5
     return _ChunkKDAPrecumsumFunction.apply(q.contiguous(), k.contiguous(), v.contiguous(),
-                                            g_cumsum.contiguous(), beta.float().contiguous(), scale)
+                                            g_cumsum.contiguous(), beta.float().contiguous(), scale,
+                                            initial_state.contiguous() if initial_state is not None else None,
+                                            bool(output_final_state))
 
 
 __all__ = ("_chunk_kda_precumsum_paired", "_iso_kdn_gate_precumsum_paired", "iso_kdn_gain", "qkv_causal_conv1d")

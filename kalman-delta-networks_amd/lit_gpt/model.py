@@ -6,6 +6,8 @@ whose every layer is a KDN mixer (``gdn2_per_layer=1``, ``mixer_type`` "iso_kdn"
 * ``GPT`` (model.py:27-165): ``wte`` -> blocks -> ``ln_f`` -> ``lm_head``, same module names, so
   a reference state dict loads; KV caching is rejected for KDN mixers as in the reference.  The
   rotary cache the reference builds is not consumed by KDN blocks and is not built here.
+  Beyond the reference, the layers' recurrent state can be carried between calls (``state=`` /
+  ``return_state=True``) for segmented prefill and token-by-token decoding.
 * ``Block`` (model.py:217-298): pre-norm residual ``x + mixer(norm_1(x))`` then
   ``x + mlp(norm_2(x))`` (``parallel_residual=False``).
 * ``LLaMAMLP`` / ``SwiGLU`` (model.py:415-464): w3(silu(w1 x) * w2 x).
@@ -79,16 +81,31 @@ class GPT(nn.Module):
         self.max_len = self.config.block_size
 
     def forward(self, idx: torch.Tensor, max_seq_length: Optional[int] = None,
-                input_pos: Optional[torch.Tensor] = None) -> torch.Tensor:
+                input_pos: Optional[torch.Tensor] = None, *, state: Optional[list] = None,
+                return_state: bool = False):
+        """Logits [B,T,vocab].  KV caching by position (``input_pos``) is refused as in the reference.
+
+        State carry (not in the reference): ``state`` is the list of per-layer ``KDNLayerState``
+        after the earlier tokens of these sequences (from a previous call with
+        ``return_state=True``), and ``return_state=True`` returns ``(logits, new_state)``.  Feeding
+        a sequence in segments, or one token at a time under ``torch.no_grad()``, gives the logits
+        of the whole sequence."""
         if input_pos is not None:
-            raise ValueError("KDN mixers do not support KV caching")
+            raise ValueError("KDN mixers do not support KV caching (carry the recurrent state with "
+                             "state= / return_state=True instead)")
         if max_seq_length is None:
             max_seq_length = self.config.block_size
+        if state is not None and len(state) != len(self.transformer.h):
+            raise ValueError(f"state must hold one entry per layer ({len(self.transformer.h)}), got {len(state)}")
+        stateful = return_state or state is not None
+        states = list(state) if state is not None else [None] * len(self.transformer.h)
         x = self.transformer.wte(idx)
-        for block in self.transformer.h:
-            x, *_ = block(x, None, max_seq_length)
+        for i, block in enumerate(self.transformer.h):
+            x, new = block(x, None, max_seq_length, kv_cache=states[i], use_state=stateful)
+            states[i] = new
         x = self.transformer.ln_f(x)
-        return self.lm_head(x)
+        logits = self.lm_head(x)
+        return (logits, states) if return_state else logits
 
     @classmethod
     def from_name(cls, name: str, **kwargs: Any) -> "GPT":
@@ -120,10 +137,14 @@ class Block(nn.Module):
             self.mlp = config.mlp_class(config)
         self.config = config
 
-    def forward(self, x, rope=None, max_seq_length=None, mask=None, input_pos=None, kv_cache=None):
+    def forward(self, x, rope=None, max_seq_length=None, mask=None, input_pos=None, kv_cache=None, *,
+                use_state=False):
+        """``kv_cache`` carries the mixer's ``KDNLayerState``; with ``use_state`` the second output is
+        the state after these tokens (None otherwise)."""
+        if input_pos is not None:
+            raise ValueError("KDN mixers do not support KV caching")
         n_1 = self.norm_1(x)
-        h, _, new_kv_cache = self.attn(n_1, attention_mask=mask, past_key_values=kv_cache,
-                                       use_cache=input_pos is not None)
+        h, _, new_kv_cache = self.attn(n_1, attention_mask=mask, past_key_values=kv_cache, use_cache=use_state)
         if self.config.parallel_residual:
             assert self.config.shared_attention_norm
             if self.config.mlp:

@@ -51,6 +51,28 @@ def test_tokenwise_equals_chunked(variant, T, chunk):
     torch.testing.assert_close(c1, c2, rtol=1e-10, atol=1e-10)
 
 
+@pytest.mark.parametrize("variant", ["iso", "diag"])
+def test_segments_from_carried_state_equal_whole_sequence(variant):
+    """The state-carry contract: running tokens [0, T1) and then [T1, T) from the first part's
+    final memory and precision gives the outputs and final state of [0, T) run at once."""
+    T, T1 = 23, 9
+    q, k, v, alpha, omega, r = _inputs(3, 2, T, 2, 6, 5, variant == "diag")
+    fn = ko.iso_recurrent if variant == "iso" else ko.diag_recurrent
+    kw = dict(info_scale=3.0, scale=0.7, output_final_state=True)
+    o, (S, c) = fn(q, k, v, alpha, omega, r, **kw)
+    a = (q[:, :T1], k[:, :T1], v[:, :T1], alpha[:, :T1], omega[:, :T1], r[:, :T1])
+    b = (q[:, T1:], k[:, T1:], v[:, T1:], alpha[:, T1:], omega[:, T1:], r[:, T1:])
+    o1, (S1, c1) = fn(*a, **kw)
+    assert c1.shape == ((2, 2, 6) if variant == "diag" else (2, 2))
+    o2, (S2, c2) = fn(*b, initial_state=S1, initial_precision=c1, **kw)
+    torch.testing.assert_close(torch.cat([o1, o2], 1), o, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(S2, S, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(c2, c, rtol=1e-12, atol=1e-12)
+    # one more token from the carried state is the tokenwise step (the decode kernel's contract)
+    o3, (S3, _) = fn(*(x[:, :1] for x in b), initial_state=S1, initial_precision=c1, **kw)
+    torch.testing.assert_close(o3, o2[:, :1], rtol=1e-12, atol=1e-12)
+
+
 def _kalman_by_conditioning(alpha, omega, r, k, y, x0_mean, x0_var):
     """Filtered mean/variance of x_t | y_1..t by dense Gaussian conditioning.
 

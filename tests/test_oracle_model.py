@@ -143,7 +143,7 @@ def test_model_argument_checks():
     with pytest.raises(ValueError, match="CUDA"):
         layer(x)
     with pytest.raises(ValueError, match="fixed-length"):
-        layer(x, use_cache=True)
+        layer(x, attention_mask=torch.ones(1, 4))
     with pytest.raises(ValueError, match="sequence length >= 2"):
         layer(torch.zeros(1, 1, 128))
     with pytest.raises(ValueError):
