@@ -257,6 +257,78 @@ def run_config4(name: str, steps: int, warmup: int, B: int, T: int):
                            "mixer_share": round(L * mixer_train_ms / train_ms, 4)}}
 
 
+def run_decode(name: str, steps: int, warmup: int, prompt: int = 1024):
+    """Token-by-token decoding of the random-init config-4 model (bf16 weights, eval) after a
+    ``prompt``-token prefill, eager and as a replayed HIP graph (``KDNDecoder``), at batch 1 and 32:
+    ms per decode step (one token for each of B sequences) and tokens/s = B / step time.  Beside it,
+    the single-token memory kernel ``kdn_mem_step`` alone at the model's H18 d128 and B in {1, 64}:
+    HBM-bound, algorithmic bytes = B H (2 K V 4 state read + write, q, k, v, o bf16, g f32, beta)."""
+    import torch
+
+    from lit_gpt.decode import KDNDecoder
+    from lit_gpt.kdn_ops import _lib
+    from lit_gpt.kdn_ops.step import kdn_memory_step
+    from lit_gpt.model import GPT
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = GPT.from_name(name)
+    model.init_weights()
+    model = model.to(torch.bfloat16).eval()
+    cfg = model.config
+    H, K = cfg.n_head, cfg.head_size
+
+    def timed(fn, n, w):
+        for _ in range(w):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(n):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / n
+
+    out = {"workload": f"{name} decode after a {prompt}-token prefill, bf16 weights, random init, synthetic ids",
+           "unit": "tokens/s", "model": {}}
+    for B in (1, 32):
+        idx = torch.randint(0, cfg.vocab_size, (B, prompt), device=dev)
+        row = {}
+        for use_graph in (False, True):
+            dec = KDNDecoder(model, B, use_graph=use_graph)
+            dec.prefill(idx)
+            tok = idx[:, -1].clone()
+            ms = timed(lambda: dec.step(tok), steps, warmup)
+            row["graph" if use_graph else "eager"] = {"ms_per_step": round(ms, 4), "value": round(B / (ms * 1e-3), 1)}
+            del dec
+        out["model"][f"B{B}"] = row
+    del model
+    torch.cuda.empty_cache()
+    kern = {}
+    for B in (1, 64):
+        g = torch.Generator(device=dev).manual_seed(B)
+        q = torch.randn(B, 1, H, K, device=dev, generator=g).bfloat16()
+        k = torch.randn(B, 1, H, K, device=dev, generator=g).bfloat16()
+        v = torch.randn(B, 1, H, K, device=dev, generator=g).bfloat16()
+        gc = (-0.1 * torch.rand(B, 1, H, K, device=dev, generator=g)).float()
+        beta = torch.rand(B, 1, H, device=dev, generator=g)
+        S = torch.zeros(B, H, K, K, device=dev)
+        for _ in range(warmup):
+            kdn_memory_step(q, k, v, gc, state=S, beta=beta)
+        with _lib.KernelTimer() as kt:
+            for _ in range(steps):
+                kdn_memory_step(q, k, v, gc, state=S, beta=beta)
+        ms = kt.mean_ms("mem_step")
+        alg = B * H * (2 * K * K * 4 + 3 * K * 2 + K * 4 + 4 + K * 2)
+        gbs = alg / (ms * 1e-3) / 1e9
+        kern[f"B{B}"] = {"us": round(ms * 1e3, 2), "alg_bytes": alg, "achieved_GBps": round(gbs, 1),
+                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    out["mem_step_kernel"] = kern
+    return out
+
+
 def cpu_baseline(variant: str, slices: int, T: int, K: int, B: int, H: int):
     """Oracle tokenwise recurrence (fp32, torch autograd) fwd+bwd on `slices` (b, h) slices."""
     import torch
@@ -316,6 +388,8 @@ def main():
     ap.add_argument("--cpu-slices", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-config4", action="store_true", help="skip the whole-model (config 4) measurement")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode (state-carry) measurement")
+    ap.add_argument("--decode-only", action="store_true", help="measure only decoding and print its line")
     ap.add_argument("--config4-only", action="store_true",
                     help="measure only the whole model (config 4) and print its line (for profiling)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
@@ -337,6 +411,10 @@ def main():
         sys.exit(1)
     B, T, H, K = args.B, args.T, args.H, args.d
     main_v = args.variant
+    if args.decode_only:
+        line = run_decode(f"{main_v}_kdn_1.3B", max(args.steps, 20), args.warmup)
+        print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B decode tokens/s")), flush=True)
+        return
     if args.config4_only:
         line = run_config4(f"{main_v}_kdn_1.3B", args.steps, args.warmup, 1, T)
         print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B forward tokens/s (config 4)")), flush=True)
@@ -377,6 +455,8 @@ def main():
     }
     if not args.no_config4:
         line["also"]["config4"] = run_config4(f"{main_v}_kdn_1.3B", min(args.steps, 10), args.warmup, 1, T)
+    if not args.no_decode:
+        line["also"]["decode"] = run_decode(f"{main_v}_kdn_1.3B", max(args.steps, 20), args.warmup)
     if args.calib_copy:
         calib_copy(args.calib_copy)
     if not args.no_cpu:
