@@ -14,7 +14,7 @@ namespace {
 constexpr int kMaxChunk = 64;
 
 // ---------------------------------------------------------------------------
-// iso gate forward.  grid (B*NT, H), block 256 (thread = key channel).
+// iso gate forward.  grid (H * B * NT) with the head fastest, block 256 (thread = key channel).
 // ---------------------------------------------------------------------------
 template <typename TG, typename TO>
 __global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
@@ -24,7 +24,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
     int T, int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ a_out,
     float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out) {
   __shared__ float s_e2[kMaxChunk][257];
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const float rate = __expf(A_log[h]);
   if (i < K) {
@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
     omega_out[o] = omega_min + softplusf(ld(orr, ro) + omega_bias[h]);
     r_out[o] = r_min + softplusf(ld(orr, ro + H) + r_bias[h]);
   }
-  if (blockIdx.x == 0 && i == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
+  if (blockIdx.x < H && i == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
 }
 
 // iso gate backward.  Writes per-tile partial sums; reduce_partials_kernel finishes them.
@@ -61,9 +61,9 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_kernel(
     TG* __restrict__ dg_raw, TO* __restrict__ dorr, float* __restrict__ part_A, float* __restrict__ part_dt,
     float* __restrict__ part_bias) {
   __shared__ float red[16];
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const int p = blockIdx.x;  // partial index (b, nt)
+  const int p = blockIdx.x / H;  // partial index (b, nt)
   const float rate = __expf(A_log[h]);
   float dA_term = 0.f;
   if (i < K) {
@@ -142,7 +142,7 @@ __device__ __forceinline__ void store8<float>(float* p, const float* f) {
   reinterpret_cast<float4*>(p)[1] = float4{f[4], f[5], f[6], f[7]};
 }
 
-// grid (B*NT, H), block 256.
+// grid (H * B * NT) with the head fastest, block 256.
 template <typename TG, typename TO>
 __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out) {
   __shared__ float s_tot[256 * 8];  // [tg][K] group totals (TG * K = 2048)
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const float rate = __expf(A_log[h]);
@@ -214,10 +214,10 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
     if (cg == 0 && u < TPG && t < L) a_out[((int64_t)b * T + t0 + t) * H + h] = s / (float)K;
   }
-  if (blockIdx.x == 0 && tid == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
+  if (blockIdx.x < H && tid == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
 }
 
-// grid (B*NT, H), block 256.  Per-block partials as in iso_gate_bwd_kernel.
+// grid (H * B * NT) with the head fastest, block 256.  Per-block partials as in iso_gate_bwd_kernel.
 template <typename TG, typename TO>
 __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
@@ -230,10 +230,10 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
   __shared__ float s_da[256];
   __shared__ float red[16];
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const int p = blockIdx.x;
+  const int p = blockIdx.x / H;
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
@@ -574,14 +574,14 @@ __global__ __launch_bounds__(256) void diag_norm_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// diag frontend.  grid (B*NT, H), block 256 (thread = key channel).
+// diag frontend.  grid (H * B * NT) with the head fastest, block 256 (thread = key channel).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void diag_frontend_fwd_kernel(
     const bf16_t* __restrict__ f_raw, const bf16_t* __restrict__ z_raw, const bf16_t* __restrict__ y_raw,
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, const float* __restrict__ mu_param, int T,
     int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ alpha,
     float* __restrict__ omega, float* __restrict__ r, float* __restrict__ mu) {
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const float rate = __expf(A_log[h]);
   const float floor_log = logf(1e-6f);
@@ -604,7 +604,7 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_kernel(
     const int64_t o = ((int64_t)b * T + t0 + i) * H + h;
     r[o] = 0.01f + softplusf(bf2f(y_raw[o]));
   }
-  if (blockIdx.x == 0 && i == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
+  if (blockIdx.x < H && i == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
 }
 
 __global__ __launch_bounds__(256) void diag_frontend_bwd_kernel(
@@ -613,9 +613,9 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_kernel(
     int K, int chunk, int NT, bf16_t* __restrict__ df_raw, float* __restrict__ part_A,
     float* __restrict__ part_dt) {
   __shared__ float red[16];
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, i = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, i = threadIdx.x;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const int p = blockIdx.x;
+  const int p = blockIdx.x / H;
   const float rate = __expf(A_log[h]);
   float dA_term = 0.f;
   if (i < K) {
@@ -653,7 +653,7 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_vec_kernel(
     float* __restrict__ omega, float* __restrict__ r, float* __restrict__ mu) {
   __shared__ float s_tot[256 * 8];
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const float rate = __expf(A_log[h]);
@@ -710,7 +710,7 @@ __global__ __launch_bounds__(256) void diag_frontend_fwd_vec_kernel(
     }
   }
   if (tid < L) r[((int64_t)b * T + t0 + tid) * H + h] = 0.01f + softplusf(yv);
-  if (blockIdx.x == 0 && tid == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
+  if (blockIdx.x < H && tid == 0) mu[h] = 0.1f + softplusf(mu_param[h]);
 }
 
 __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
@@ -721,10 +721,10 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
   __shared__ float s_tot[256 * 8];
   __shared__ float red[16];
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
-  const int b = blockIdx.x / NT, nt = blockIdx.x % NT, h = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const int p = blockIdx.x;
+  const int p = blockIdx.x / H;
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
@@ -932,7 +932,8 @@ int kdn_iso_gate_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
     return 0;
   }
   const int NT = cdiv(T, chunk);
-  dim3 grid(B * NT, H);
+  // head fastest: the workgroups in flight read neighbouring heads' rows of the same tokens
+  dim3 grid(H * B * NT);
   const bool vec = gate_vec_ok(K, chunk) && aligned16(g_raw) && aligned16(g_cumsum) && aligned16(dt_bias);
 #define KDN_GATE_FWD(TG, TO)                                                                                     \
   hipLaunchKernelGGL((vec ? iso_gate_fwd_vec_kernel<TG, TO> : iso_gate_fwd_kernel<TG, TO>), grid, dim3(256), 0,  \
@@ -962,7 +963,7 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   float* part_A = (float*)workspace;
   float* part_dt = part_A + (int64_t)NP * H;
   float* part_bias = part_dt + (int64_t)NP * H * K;
-  dim3 grid(NP, H);
+  dim3 grid(H * NP);  // head fastest
   const bool vec = gate_vec_ok(K, chunk) && aligned16(g_raw) && aligned16(dg_pre) && aligned16(dg_raw) &&
                    aligned16(dt_bias);
 #define KDN_GATE_BWD(TG, TO)                                                                                     \
@@ -1116,7 +1117,7 @@ int kdn_diag_frontend_fwd(const uint16_t* retention_raw, const uint16_t* omega_r
   const int NT = cdiv(T, chunk);
   const bool vec = gate_vec_ok(K, chunk) && aligned16(retention_raw) && aligned16(omega_raw) && aligned16(dt_bias) &&
                    aligned16(g_cumsum) && aligned16(alpha) && aligned16(omega);
-  hipLaunchKernelGGL(vec ? diag_frontend_fwd_vec_kernel : diag_frontend_fwd_kernel, dim3(B * NT, H), dim3(256), 0,
+  hipLaunchKernelGGL(vec ? diag_frontend_fwd_vec_kernel : diag_frontend_fwd_kernel, dim3(H * B * NT), dim3(256), 0,
                      stream, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, T, H, K, chunk, NT, g_cumsum,
                      alpha, omega, r, mu);
   KDN_CHECK_LAUNCH();
@@ -1144,7 +1145,7 @@ int kdn_diag_frontend_bwd(const uint16_t* retention_raw, const uint16_t* omega_r
   if (has_decay && (d_retention_raw || dA_log || ddt_bias)) {
     const bool vec = gate_vec_ok(K, chunk) && aligned16(retention_raw) && aligned16(dt_bias) && aligned16(alpha) &&
                      aligned16(d_g_cumsum) && aligned16(d_alpha) && aligned16(d_retention_raw);
-    hipLaunchKernelGGL(vec ? diag_frontend_bwd_vec_kernel : diag_frontend_bwd_kernel, dim3(NP, H), dim3(256), 0,
+    hipLaunchKernelGGL(vec ? diag_frontend_bwd_vec_kernel : diag_frontend_bwd_kernel, dim3(H * NP), dim3(256), 0,
                        stream, retention_raw, A_log, dt_bias, alpha, d_g_cumsum, d_alpha, T, H, K, chunk, NT,
                        d_retention_raw, dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr);
     KDN_CHECK_LAUNCH();

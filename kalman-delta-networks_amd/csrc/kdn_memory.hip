@@ -313,12 +313,22 @@ __device__ void intra_fwd_exact_chunk(
 }
 
 // Grid-stride pass over the chunks the MFMA kernel flagged (flags[chunk] != 0).
+// True in every thread when any chunk of this workgroup's grid-stride share (blockIdx.x,
+// blockIdx.x + gridDim.x, ...) is flagged.  One flag per thread, loaded in parallel, so a
+// workgroup with nothing to do exits after one load instead of one dependent load per chunk.
+__device__ __forceinline__ bool any_flagged(const int* __restrict__ flags, int NB) {
+  int any = 0;
+  for (int lin = blockIdx.x + threadIdx.x * gridDim.x; lin < NB; lin += blockDim.x * gridDim.x) any |= flags[lin];
+  return __syncthreads_or(any) != 0;
+}
+
 template <int K, int V, bool ISO>
 __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, int NB, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
     float* __restrict__ Mg, float* __restrict__ Ag, const int* __restrict__ flags) {
+  if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();  // LDS of the previous chunk is dead
@@ -525,6 +535,7 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_exact_kernel(
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, int NB, const int* __restrict__ flags, bf16_t* __restrict__ dv,
     float* __restrict__ dKg, float* __restrict__ dNg) {
+  if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
@@ -711,6 +722,7 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
     const float* __restrict__ dgl, int T, int H, int NT, int NB, const int* __restrict__ flags, float scale,
     bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
     float* __restrict__ dg) {
+  if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
