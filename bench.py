@@ -76,6 +76,45 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
     return {k: (b * N, f * N) for k, (b, f) in per.items()}
 
 
+def frontend_counts(variant: str, B: int, T: int, H: int, K: int):
+    """Algorithmic HBM bytes per call of the gate / gain / norm entry points around the memory
+    scan (inputs read once, outputs written once; no FLOP bound).  N = B*T*H token-heads,
+    E = N*K elements.  ``l2norm_*`` is one tensor per call (q and k: two calls per step)."""
+    N = B * T * H
+    E = N * K
+    if variant == "iso":
+        per = {
+            # g_raw bf16, omega|r raw bf16 -> g_cumsum f32, a, omega, r f32
+            "iso_gate_fwd": 6 * E + 16 * N,
+            # g_raw, omega|r raw, dg f32, da, domega, dr -> dg_raw bf16, d omega|r raw bf16
+            "iso_gate_bwd": 8 * E + 20 * N,
+            # a, omega, r -> beta, p_prev
+            "iso_gain_fwd": 20 * N,
+            # a, omega, r, dbeta, p_prev -> da, domega, dr
+            "iso_gain_bwd": 32 * N,
+            # x bf16 -> y bf16, rstd f32
+            "l2norm_fwd": 4 * E + 4 * N,
+            # x bf16, rstd, dy bf16 -> dx bf16
+            "l2norm_bwd": 6 * E + 4 * N,
+        }
+    else:
+        per = {
+            # q, k bf16 -> q_memory bf16, k_gain f32, k_memory bf16, two norms
+            "diag_norm_fwd": 12 * E + 8 * N,
+            # q, k, norms, d q_memory bf16, d k_gain f32, d k_memory bf16 -> dq, dk bf16
+            "diag_norm_bwd": 16 * E + 8 * N,
+            # retention, omega raw bf16, r raw bf16 -> g_cumsum, alpha, omega f32, r
+            "diag_frontend_fwd": 16 * E + 6 * N,
+            # retention raw, alpha, d g_cumsum, d alpha -> d retention raw bf16
+            "diag_frontend_bwd": 16 * E,
+            # k, alpha, omega f32, r -> kappa, p_prev f32, D
+            "diag_gain_fwd": 20 * E + 8 * N,
+            # k, alpha, omega, r, dkappa, p_prev, D, omega raw, r raw -> dk, dalpha f32, d omega raw, d r raw
+            "diag_gain_bwd": 32 * E + 12 * N,
+        }
+    return {k: (b, 0) for k, b in per.items()}
+
+
 def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K: int):
     import torch
 
@@ -97,15 +136,21 @@ def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    # the step rate is timed without per-call events; a second pass of the same steps times each
+    # entry point with HIP events on its launch stream
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / steps
     with _lib.KernelTimer() as timer:
-        t0 = time.perf_counter()
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / steps
     kernel_ms = {tag: timer.mean_ms(tag) for tag in timer.tags()}
     counts = kernel_counts(variant, B, T, H, K, K)
+    counts.update(frontend_counts(variant, B, T, H, K))
     per_kernel = {}
     for tag, (nbytes, flops) in counts.items():
         t = kernel_ms.get(tag, float("nan")) * 1e-3

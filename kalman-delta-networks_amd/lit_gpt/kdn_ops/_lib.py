@@ -127,9 +127,13 @@ _timer: KernelTimer | None = None
 
 
 def call(name: str, *args, tag: str | None = None):
+    """Call entry point ``name``; under a KernelTimer the call is timed as ``tag`` (default: the
+    entry name without its ``kdn_`` prefix)."""
     lib = load()
     fn = getattr(lib, name)
-    if _timer is not None and tag is not None:
+    if _timer is not None:
+        if tag is None:
+            tag = name[4:] if name.startswith("kdn_") else name
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         rc = fn(*args)
