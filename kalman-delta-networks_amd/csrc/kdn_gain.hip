@@ -535,25 +535,40 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_emit_kernel(
 }
 
 // ----------------------------------------------------------------------------
-// Vectorised diag gain (K % 8 == 0, K/8 | 64): a thread owns 8 consecutive channels of one
-// (b, h, chunk) tile; TPT = K/8 threads per tile, tiles ordered with h fastest.  Loads and
+// Vectorised diag gain (K % 4 == 0, K/4 | 64): a thread owns CPT = 4 consecutive channels of one
+// (b, h, chunk) tile; TPT = K/CPT threads per tile, tiles ordered with h fastest.  Loads and
 // stores are 16-byte vectors; the per-token cross-channel sums are shuffles over the tile's
-// TPT lanes.  Same workspace layouts as the per-channel kernels above.
+// TPT lanes.  Same workspace layouts as the per-channel kernels above.  Four channels per thread
+// (rather than eight) double the waves in flight: these passes wait on loads, not arithmetic.
 // ----------------------------------------------------------------------------
-__device__ __forceinline__ void ld8f(const float* p, float* f) {
-  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
-  f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w, f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+constexpr int kCPT = 4;  // channels per thread
+__device__ __forceinline__ void ldcf(const float* p, float* f) {
+#pragma unroll
+  for (int q = 0; q < kCPT / 4; ++q) {
+    const float4 a = reinterpret_cast<const float4*>(p)[q];
+    f[4 * q] = a.x, f[4 * q + 1] = a.y, f[4 * q + 2] = a.z, f[4 * q + 3] = a.w;
+  }
 }
-__device__ __forceinline__ void st8f(float* p, const float* f) {
-  reinterpret_cast<float4*>(p)[0] = float4{f[0], f[1], f[2], f[3]};
-  reinterpret_cast<float4*>(p)[1] = float4{f[4], f[5], f[6], f[7]};
+__device__ __forceinline__ void stcf(float* p, const float* f) {
+#pragma unroll
+  for (int q = 0; q < kCPT / 4; ++q) reinterpret_cast<float4*>(p)[q] = float4{f[4 * q], f[4 * q + 1], f[4 * q + 2], f[4 * q + 3]};
+}
+// kCPT bf16 values <-> floats
+__device__ __forceinline__ void ldc_bf16(const bf16_t* p, float* f) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  f[0] = __uint_as_float(v.x << 16), f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16), f[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+__device__ __forceinline__ void stc_bf16(bf16_t* p, const float* f) {
+  *reinterpret_cast<uint2*>(p) = uint2{(uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16),
+                                       (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16)};
 }
 __device__ __forceinline__ float tile_sum(float x, int tpt) {
   for (int o = 1; o < tpt; o <<= 1) x += __shfl_xor(x, o, 64);
   return x;
 }
-// Vectorised path: one tile = (b, h, 16-token chunk) x K channels, K/8 threads per tile, 8 channels
-// per thread.  Short chunks give B*H*T/16 * K/8 threads (enough waves to cover load latency on
+// Vectorised path: one tile = (b, h, 16-token chunk) x K channels, K/kCPT threads per tile, kCPT
+// channels per thread.  Short chunks give B*H*T/16 * K/8 threads (enough waves to cover load latency on
 // every CU); each thread issues the loads of NB tokens before it computes on them.
 constexpr int kVecChunk = 16;
 struct GainTile {
@@ -561,7 +576,7 @@ struct GainTile {
   bool ok;
 };
 __device__ __forceinline__ GainTile gain_tile(int B, int T, int H, int K, int NT) {
-  const int tpt = K / 8, tpb = 256 / tpt;
+  const int tpt = K / kCPT, tpb = 256 / tpt;
   const int64_t gt = (int64_t)blockIdx.x * tpb + threadIdx.x / tpt;
   GainTile g;
   g.ok = gt < (int64_t)B * NT * H;
@@ -571,7 +586,7 @@ __device__ __forceinline__ GainTile gain_tile(int B, int T, int H, int K, int NT
   g.nt = (int)(bn % NT);
   g.b = (int)(bn / NT);
   g.sub = threadIdx.x % tpt;
-  g.i0 = 8 * g.sub;
+  g.i0 = kCPT * g.sub;
   g.t0 = g.nt * kVecChunk;
   g.t1 = min(g.t0 + kVecChunk, T);
   return g;
@@ -587,17 +602,17 @@ __global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __res
   constexpr int NB = 4;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
-  Map2 M[8];
+  Map2 M[kCPT];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) M[j] = Map2{1.f, 0.f, 0.f, 1.f};
+  for (int j = 0; j < kCPT; ++j) M[j] = Map2{1.f, 0.f, 0.f, 1.f};
   for (int t = g.t0; t < g.t1; t += NB) {
-    float kt[NB][8], al[NB][8], wt[NB][8], ir[NB];
+    float kt[NB][kCPT], al[NB][kCPT], wt[NB][kCPT], ir[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int64_t row = gain_row(g, T, H, min(t + u, g.t1 - 1));
-      ld8f(k + row * K + g.i0, kt[u]);
-      ld8f(alpha + row * K + g.i0, al[u]);
-      ld8f(omega + row * K + g.i0, wt[u]);
+      ldcf(k + row * K + g.i0, kt[u]);
+      ldcf(alpha + row * K + g.i0, al[u]);
+      ldcf(omega + row * K + g.i0, wt[u]);
       ir[u] = r[row];
     }
 #pragma unroll
@@ -605,7 +620,7 @@ __global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __res
       if (t + u >= g.t1) break;
       const float iru = 1.f / ir[u];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kCPT; ++j) {
         const float a2 = al[u][j] * al[u][j], uu = s * kt[u][j] * kt[u][j] * iru;
         M[j] = map_mul(Map2{a2, wt[u][j], uu * a2, 1.f + uu * wt[u][j]}, M[j]);
       }
@@ -613,7 +628,7 @@ __global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __res
   }
   float4* dst = reinterpret_cast<float4*>(maps + ((((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0) * 4);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) dst[j] = float4{M[j].m0, M[j].m1, M[j].m2, M[j].m3};
+  for (int j = 0; j < kCPT; ++j) dst[j] = float4{M[j].m0, M[j].m1, M[j].m2, M[j].m3};
 }
 
 // grid (B*H), block K: per channel, the chunk maps in groups of 8 with the next group's loads in
@@ -653,17 +668,17 @@ __global__ __launch_bounds__(256) void diag_gain_emit_v_kernel(const float* __re
   constexpr int NB = 4;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
-  const int tpt = K / 8;
-  float p[8];
-  ld8f(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, p);
+  const int tpt = K / kCPT;
+  float p[kCPT];
+  ldcf(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, p);
   for (int t = g.t0; t < g.t1; t += NB) {
-    float kt[NB][8], al[NB][8], wt[NB][8], rt[NB];
+    float kt[NB][kCPT], al[NB][kCPT], wt[NB][kCPT], rt[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int64_t row = gain_row(g, T, H, min(t + u, g.t1 - 1));
-      ld8f(k + row * K + g.i0, kt[u]);
-      ld8f(alpha + row * K + g.i0, al[u]);
-      ld8f(omega + row * K + g.i0, wt[u]);
+      ldcf(k + row * K + g.i0, kt[u]);
+      ldcf(alpha + row * K + g.i0, al[u]);
+      ldcf(omega + row * K + g.i0, wt[u]);
       rt[u] = r[row];
     }
 #pragma unroll
@@ -671,10 +686,10 @@ __global__ __launch_bounds__(256) void diag_gain_emit_v_kernel(const float* __re
       if (t + u >= g.t1) break;
       const int64_t row = gain_row(g, T, H, t + u);
       const float ir = 1.f / rt[u];
-      float num[8], sq = 0.f;
-      if (p_prev) st8f(p_prev + row * K + g.i0, p);
+      float num[kCPT], sq = 0.f;
+      if (p_prev) stcf(p_prev + row * K + g.i0, p);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kCPT; ++j) {
         const float ph = al[u][j] * al[u][j] * p[j] + wt[u][j];
         num[j] = ph * kt[u][j];
         sq += num[j] * kt[u][j];
@@ -682,8 +697,8 @@ __global__ __launch_bounds__(256) void diag_gain_emit_v_kernel(const float* __re
       }
       const float D = rt[u] + tile_sum(sq, tpt), iD = 1.f / D;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) num[j] *= iD;
-      st8f(kappa + row * K + g.i0, num);
+      for (int j = 0; j < kCPT; ++j) num[j] *= iD;
+      stcf(kappa + row * K + g.i0, num);
       if (Dsave && g.sub == 0) Dsave[row] = D;
     }
   }
@@ -697,20 +712,20 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_map_v_kernel(
   constexpr int NB = 2;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
-  const int tpt = K / 8;
-  float Aacc[8], Bacc[8];
+  const int tpt = K / kCPT;
+  float Aacc[kCPT], Bacc[kCPT];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f;
+  for (int j = 0; j < kCPT; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f;
   for (int t = g.t1 - 1; t >= g.t0; t -= NB) {
-    float kt[NB][8], al[NB][8], wt[NB][8], pv[NB][8], dk_[NB][8], Dv[NB], rv[NB];
+    float kt[NB][kCPT], al[NB][kCPT], wt[NB][kCPT], pv[NB][kCPT], dk_[NB][kCPT], Dv[NB], rv[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int64_t row = gain_row(g, T, H, max(t - u, g.t0));
-      ld8f(k + row * K + g.i0, kt[u]);
-      ld8f(alpha + row * K + g.i0, al[u]);
-      ld8f(omega + row * K + g.i0, wt[u]);
-      ld8f(p_prev + row * K + g.i0, pv[u]);
-      ld8f(dkappa + row * K + g.i0, dk_[u]);
+      ldcf(k + row * K + g.i0, kt[u]);
+      ldcf(alpha + row * K + g.i0, al[u]);
+      ldcf(omega + row * K + g.i0, wt[u]);
+      ldcf(p_prev + row * K + g.i0, pv[u]);
+      ldcf(dkappa + row * K + g.i0, dk_[u]);
       Dv[u] = Dsave[row];
       rv[u] = r[row];
     }
@@ -718,15 +733,15 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_map_v_kernel(
     for (int u = 0; u < NB; ++u) {
       if (t - u < g.t0) break;
       const float iD = 1.f / Dv[u], ir = 1.f / rv[u];
-      float ph[8], gp = 0.f;
+      float ph[kCPT], gp = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kCPT; ++j) {
         ph[j] = al[u][j] * al[u][j] * pv[u][j] + wt[u][j];
         gp += dk_[u][j] * ph[j] * kt[u][j];
       }
       const float G = tile_sum(gp, tpt) * iD;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kCPT; ++j) {
         const float a2 = al[u][j] * al[u][j];
         const float hh = 1.f + s * kt[u][j] * kt[u][j] * ir * ph[j];
         const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD;
@@ -739,7 +754,7 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_map_v_kernel(
   }
   float4* dst = reinterpret_cast<float4*>(ab + ((((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0) * 2);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) dst[q] = float4{Aacc[2 * q], Bacc[2 * q], Aacc[2 * q + 1], Bacc[2 * q + 1]};
+  for (int q = 0; q < kCPT / 2; ++q) dst[q] = float4{Aacc[2 * q], Bacc[2 * q], Aacc[2 * q + 1], Bacc[2 * q + 1]};
 }
 
 __global__ __launch_bounds__(256) void diag_gain_bwd_carry_v_kernel(const float2* __restrict__ ab,
@@ -781,22 +796,22 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_emit_v_kernel(
   constexpr int NB = 2;
   const GainTile g = gain_tile(B, T, H, K, NT);
   if (!g.ok) return;
-  const int tpt = K / 8;
-  float lam[8];
-  ld8f(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, lam);
+  const int tpt = K / kCPT;
+  float lam[kCPT];
+  ldcf(carry + (((int64_t)g.b * H + g.h) * NT + g.nt) * K + g.i0, lam);
   for (int t = g.t1 - 1; t >= g.t0; t -= NB) {
-    float kt[NB][8], al[NB][8], wt[NB][8], pv[NB][8], dk_[NB][8], Dv[NB], Gv[NB], rv[NB];
-    uint4 ow[NB];
+    float kt[NB][kCPT], al[NB][kCPT], wt[NB][kCPT], pv[NB][kCPT], dk_[NB][kCPT], Dv[NB], Gv[NB], rv[NB];
+    float ow[NB][kCPT];
     bf16_t rr[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       const int64_t row = gain_row(g, T, H, max(t - u, g.t0));
-      ld8f(k + row * K + g.i0, kt[u]);
-      ld8f(alpha + row * K + g.i0, al[u]);
-      ld8f(omega + row * K + g.i0, wt[u]);
-      ld8f(p_prev + row * K + g.i0, pv[u]);
-      ld8f(dkappa + row * K + g.i0, dk_[u]);
-      ow[u] = *reinterpret_cast<const uint4*>(omega_raw + row * K + g.i0);
+      ldcf(k + row * K + g.i0, kt[u]);
+      ldcf(alpha + row * K + g.i0, al[u]);
+      ldcf(omega + row * K + g.i0, wt[u]);
+      ldcf(p_prev + row * K + g.i0, pv[u]);
+      ldcf(dkappa + row * K + g.i0, dk_[u]);
+      ldc_bf16(omega_raw + row * K + g.i0, ow[u]);
       Dv[u] = Dsave[row];
       Gv[u] = Gsave[row];
       rv[u] = r[row];
@@ -806,17 +821,12 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_emit_v_kernel(
     for (int u = 0; u < NB; ++u) {
       if (t - u < g.t0) break;
       const int64_t row = gain_row(g, T, H, t - u);
-      float oraw[8], dko[8], dao[8], dwo[8];
-      const uint32_t ww[4] = {ow[u].x, ow[u].y, ow[u].z, ow[u].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        oraw[2 * q] = __uint_as_float(ww[q] << 16);
-        oraw[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
-      }
+      const float* oraw = ow[u];
+      float dko[kCPT], dao[kCPT], dwo[kCPT];
       const float G = Gv[u], iD = 1.f / Dv[u], ir = 1.f / rv[u];
       float urr = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kCPT; ++j) {
         const float a2 = al[u][j] * al[u][j];
         const float ph = a2 * pv[u][j] + wt[u][j];
         const float uu = s * kt[u][j] * kt[u][j] * ir;
@@ -830,29 +840,26 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_emit_v_kernel(
         urr += ubar * (-s * kt[u][j] * kt[u][j] * ir * ir);
         lam[j] = a2 * pbar;
       }
-      st8f(dk + row * K + g.i0, dko);
-      st8f(dalpha + row * K + g.i0, dao);
-      uint32_t wo[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) wo[q] = (uint32_t)f2bf(dwo[2 * q]) | ((uint32_t)f2bf(dwo[2 * q + 1]) << 16);
-      *reinterpret_cast<uint4*>(domega_raw + row * K + g.i0) = uint4{wo[0], wo[1], wo[2], wo[3]};
+      stcf(dk + row * K + g.i0, dko);
+      stcf(dalpha + row * K + g.i0, dao);
+      stc_bf16(domega_raw + row * K + g.i0, dwo);
       const float utot = tile_sum(urr, tpt);
       if (g.sub == 0) dr_raw[row] = f2bf((-G * iD + utot) * sigmoidf(bf2f(rr[u])));
     }
   }
   if (g.nt == 0 && dprec_part) {
     // lam holds dL/dp_{-1}; p_{-1} = 1/c  ->  dL/dc = -lam p^2
-    float c8[8], part = 0.f;
-    if (prec_mode == 1) ld8f(prec0 + ((int64_t)g.b * H + g.h) * K + g.i0, c8);
+    float cN[kCPT], part = 0.f;
+    if (prec_mode == 1) ldcf(prec0 + ((int64_t)g.b * H + g.h) * K + g.i0, cN);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float c = prec_mode == 0 ? prec0[g.h] : c8[j];
+    for (int j = 0; j < kCPT; ++j) {
+      const float c = prec_mode == 0 ? prec0[g.h] : cN[j];
       const float p0 = 1.f / c;
-      c8[j] = -lam[j] * p0 * p0;
-      part += c8[j];
+      cN[j] = -lam[j] * p0 * p0;
+      part += cN[j];
     }
     if (prec_mode == 1) {
-      st8f(dprec_part + ((int64_t)g.b * H + g.h) * K + g.i0, c8);
+      stcf(dprec_part + ((int64_t)g.b * H + g.h) * K + g.i0, cN);
     } else {
       part = tile_sum(part, tpt);
       if (g.sub == 0) dprec_part[(int64_t)g.b * H + g.h] = part;
@@ -871,7 +878,7 @@ __global__ void sum_over_batch_kernel(const float* __restrict__ part, int B, int
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 inline int gain_block(int K) { return ((K + 63) / 64) * 64; }
-inline bool gain_vec_ok(int K) { return K % 8 == 0 && 64 % (K / 8) == 0; }
+inline bool gain_vec_ok(int K) { return K % kCPT == 0 && 64 % (K / kCPT) == 0; }
 inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -951,7 +958,7 @@ int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, co
   const int bs = gain_block(K);
   if (gain_vec_ok(K) && aligned16(k) && aligned16(alpha) && aligned16(omega) && aligned16(kappa) &&
       aligned16(p_prev) && (prec_mode == 0 || aligned16(initial_precision))) {
-    const int NV = cdiv(T, kVecChunk), tiles = B * H * NV, tpb = 256 / (K / 8);
+    const int NV = cdiv(T, kVecChunk), tiles = B * H * NV, tpb = 256 / (K / kCPT);
     float* carry_v = maps + (int64_t)B * H * NV * K * 4;
     hipLaunchKernelGGL(diag_gain_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r, B, T,
                        H, K, NV, info_scale, maps);
@@ -990,7 +997,7 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
   if (gain_vec_ok(K) && aligned16(k) && aligned16(alpha) && aligned16(omega) && aligned16(dkappa) &&
       aligned16(p_prev) && aligned16(omega_raw) && aligned16(dk) && aligned16(dalpha) && aligned16(domega_raw) &&
       (prec_mode == 0 || (aligned16(initial_precision) && aligned16(dpart_out)))) {
-    const int NV = cdiv(T, kVecChunk), tiles = B * H * NV, tpb = 256 / (K / 8);
+    const int NV = cdiv(T, kVecChunk), tiles = B * H * NV, tpb = 256 / (K / kCPT);
     float* carry_v = ab + (int64_t)B * H * NV * K * 4;
     float* dpart_v = carry_v + (int64_t)B * H * NV * K;
     float* dpart_out_v = d_initial_precision ? (prec_mode == 1 ? d_initial_precision : dpart_v) : nullptr;
