@@ -156,6 +156,20 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
 int kdn_mem_step(const void* q, const void* k, const float* kappa_or_beta, int iso, const void* v, int qkv_bf16,
                  const float* g, int B, int H, int K, int V, float scale, float* state, void* o, int o_bf16,
                  hipStream_t stream);
+/* One token of the whole Kalman step with a carried state (decode): the single-token gain of
+ * _iso_kdn_gain_forward / _diag_kdn_gain_forward (iso_kdn_naive.py:200-251, diag_kdn_naive.py:
+ * 217-276) from the carried precision, then kdn_mem_step's memory update, in one launch.  No
+ * counterpart in the reference (it refuses caching for KDN layers, model.py:104,184).
+ * iso = 1: gain_a = a [B,H] (mean alpha^2), omega, r [B,H], precision [B,H], unit keys as on the
+ * production path: z = a/c + omega, beta = z / (r + z), c' = (r + s z) / (r z), s = info_scale / K.
+ * iso = 0: gain_a = alpha [B,H,K] (the gain's unclamped alpha), omega [B,H,K], r [B,H],
+ * k_gain [B,H,K] f32 (nullable: k), precision [B,H,K]: p_hat = alpha^2 / c + omega,
+ * kappa = p_hat k_gain / (r + sum p_hat k_gain^2), c' = (1 + s k_gain^2 p_hat / r) / p_hat,
+ * s = info_scale.  precision_out must not alias precision_in.  Other arguments as kdn_mem_step. */
+int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, const float* g, const float* gain_a,
+                    const float* omega, const float* r, const float* k_gain, const float* precision_in,
+                    float* precision_out, int iso, int B, int H, int K, int V, float scale, float info_scale,
+                    float* state, void* o, int o_bf16, hipStream_t stream);
 
 /* ---------------------------------------------------------------- layer frontends */
 /* Depthwise causal short convolution with SiLU, fixed length, width W = 4, no bias:

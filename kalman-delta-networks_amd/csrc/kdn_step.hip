@@ -115,6 +115,131 @@ __global__ __launch_bounds__(256) void mem_step_kernel(const TI* __restrict__ q,
   if (t < 8) st4(o + bh * V + col, f4_scale(scale, out));
 }
 
+// Sum of x over the 32 row groups (one value per row group, the same in its 8 column lanes);
+// valid in every thread.  `red` holds 4 floats.
+__device__ __forceinline__ float rows_sum_scalar(float x, float* red) {
+  x += __shfl_xor(x, 8, 64);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = x;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// One token of the full Kalman step: the gain from the carried precision, then the memory
+// update of mem_step_kernel.  grid (B * H * V / 32), block 256.
+//   iso:  p = 1 / c;  z = a p + w;  beta = z / (r + z);  p' = r z / (r + s z)  (unit keys; s = info_scale / K)
+//   diag: p = 1 / c;  p_hat = alpha^2 p + w;  kappa = p_hat k / (r + sum_i p_hat_i k_i^2);
+//         p' = p_hat / (1 + s k^2 p_hat / r)                                   (s = info_scale)
+// c' = 1 / p' goes to prec_out (written by the workgroup of the first column slice; every
+// workgroup of a (b, h) reads prec_in, so the two must not alias).
+template <int K, int V, typename TI, typename TO, bool ISO>
+__global__ __launch_bounds__(256) void kalman_step_kernel(
+    const TI* __restrict__ q, const TI* __restrict__ k, const TI* __restrict__ v, const float* __restrict__ g,
+    const float* __restrict__ ga, const float* __restrict__ gw, const float* __restrict__ gr,
+    const float* __restrict__ kg, const float* __restrict__ prec_in, float* __restrict__ prec_out, float scale,
+    float s, float* __restrict__ state, TO* __restrict__ o) {
+  constexpr int NS = V / 32, R = K / 32;
+  __shared__ float4 red[2][32];
+  __shared__ float redg[4];
+  const int64_t bh = blockIdx.x / NS;
+  const int slice = blockIdx.x % NS, t = threadIdx.x, lane = t & 63, c4 = t & 7, rg = t >> 3;
+  const TI* qp = q + bh * K;
+  const TI* kp = k + bh * K;
+  float qs = 1.f, ks = 1.f;
+  if (ISO) {
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int i = lane; i < K; i += 64) {
+      const float a = ld(qp, i), b = ld(kp, i);
+      sq = fmaf(a, a, sq);
+      sk = fmaf(b, b, sk);
+    }
+    qs = 1.f / sqrtf(wave_sum(sq) + kL2Eps);
+    ks = 1.f / sqrtf(wave_sum(sk) + kL2Eps);
+  }
+  const float rt = gr[bh], ir = 1.f / rt;
+  const int col = slice * 32 + 4 * c4;
+  float* sp = state + bh * K * V + col;
+  float4 S[R];
+  float kr[R], qr[R], kap[R];
+  float beta = 0.f;
+  if (ISO) {
+    const float p = 1.f / prec_in[bh];
+    const float z = ga[bh] * p + gw[bh];
+    beta = z / (rt + z);
+    if (slice == 0 && t == 0) prec_out[bh] = (rt + s * z) / (rt * z);
+  }
+  float ph[R], kgv[R], part = 0.f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int row = rg + 32 * j;
+    S[j] = *reinterpret_cast<const float4*>(sp + (int64_t)row * V);
+    kr[j] = ld(kp, row) * ks;
+    qr[j] = ld(qp, row) * qs;
+    if (!ISO) {
+      const int64_t e = bh * K + row;
+      const float al = ga[e];
+      kgv[j] = kg ? kg[e] : kr[j];
+      ph[j] = al * al / prec_in[e] + gw[e];
+      part = fmaf(ph[j] * kgv[j], kgv[j], part);
+    }
+    S[j] = f4_scale(exp2f(g[bh * K + row]), S[j]);
+  }
+  if (!ISO) {
+    const float iD = 1.f / (rt + rows_sum_scalar(part, redg));
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      kap[j] = ph[j] * kgv[j] * iD;
+      if (slice == 0 && c4 == 0) prec_out[bh * K + rg + 32 * j] = (1.f + s * kgv[j] * kgv[j] * ir * ph[j]) / ph[j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < R; ++j) kap[j] = beta * kr[j];
+  }
+  float4 acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < R; ++j) acc = f4_fma(kr[j], S[j], acc);
+  const float4 delta = f4_sub(ld4(v + bh * V + col), rows_sum(acc, red[0]));
+  acc = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    S[j] = f4_fma(kap[j], delta, S[j]);
+    *reinterpret_cast<float4*>(sp + (int64_t)(rg + 32 * j) * V) = S[j];
+    acc = f4_fma(qr[j], S[j], acc);
+  }
+  const float4 out = rows_sum(acc, red[1]);
+  if (t < 8) st4(o + bh * V + col, f4_scale(scale, out));
+}
+
+template <int K, int V, typename TI, typename TO>
+void launch_kalman(bool iso, const void* q, const void* k, const void* v, const float* g, const float* ga,
+                   const float* gw, const float* gr, const float* kg, const float* pin, float* pout, int BH,
+                   float scale, float s, float* state, void* o, hipStream_t stream) {
+  const dim3 grid(BH * (V / 32)), block(256);
+  if (iso)
+    hipLaunchKernelGGL((kalman_step_kernel<K, V, TI, TO, true>), grid, block, 0, stream, (const TI*)q, (const TI*)k,
+                       (const TI*)v, g, ga, gw, gr, kg, pin, pout, scale, s, state, (TO*)o);
+  else
+    hipLaunchKernelGGL((kalman_step_kernel<K, V, TI, TO, false>), grid, block, 0, stream, (const TI*)q, (const TI*)k,
+                       (const TI*)v, g, ga, gw, gr, kg, pin, pout, scale, s, state, (TO*)o);
+}
+
+template <int K, int V>
+void launch_kalman_kv(bool iso, const void* q, const void* k, const void* v, int qkv_bf16, const float* g,
+                      const float* ga, const float* gw, const float* gr, const float* kg, const float* pin, float* pout,
+                      int BH, float scale, float s, float* state, void* o, int o_bf16, hipStream_t stream) {
+  if (qkv_bf16 && o_bf16)
+    launch_kalman<K, V, bf16_t, bf16_t>(iso, q, k, v, g, ga, gw, gr, kg, pin, pout, BH, scale, s, state, o, stream);
+  else if (qkv_bf16)
+    launch_kalman<K, V, bf16_t, float>(iso, q, k, v, g, ga, gw, gr, kg, pin, pout, BH, scale, s, state, o, stream);
+  else if (o_bf16)
+    launch_kalman<K, V, float, bf16_t>(iso, q, k, v, g, ga, gw, gr, kg, pin, pout, BH, scale, s, state, o, stream);
+  else
+    launch_kalman<K, V, float, float>(iso, q, k, v, g, ga, gw, gr, kg, pin, pout, BH, scale, s, state, o, stream);
+}
+
 template <int K, int V, typename TI, typename TO>
 void launch_step(bool iso, const void* q, const void* k, const float* kb, const void* v, const float* g, int BH,
                  float scale, float* state, void* o, hipStream_t stream) {
@@ -156,6 +281,32 @@ int kdn_mem_step(const void* q, const void* k, const float* kappa_or_beta, int i
   else if (K == 64) launch_step_kv<64, 128>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
   else if (V == 64) launch_step_kv<128, 64>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
   else launch_step_kv<128, 128>(is_iso, q, k, qkv_bf16, kappa_or_beta, v, g, BH, scale, state, o, o_bf16, stream);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, const float* g, const float* gain_a,
+                    const float* omega, const float* r, const float* k_gain, const float* precision_in,
+                    float* precision_out, int iso, int B, int H, int K, int V, float scale, float info_scale,
+                    float* state, void* o, int o_bf16, hipStream_t stream) {
+  if (B < 0 || H <= 0 || (K != 64 && K != 128) || (V != 64 && V != 128) || !(info_scale > 0.f)) return KDN_ERR_ARG;
+  if (B == 0) return 0;
+  if (!q || !k || !v || !g || !gain_a || !omega || !r || !precision_in || !precision_out || !state || !o)
+    return KDN_ERR_ARG;
+  if (precision_in == precision_out) return KDN_ERR_ARG;  // every workgroup of a (b, h) reads precision_in
+  if (!aligned(state, 16) || !aligned(v, qkv_bf16 ? 8 : 16) || !aligned(o, o_bf16 ? 8 : 16)) return KDN_ERR_ARG;
+  const int BH = B * H;
+  const bool is_iso = iso != 0;
+  const float s = is_iso ? info_scale / (float)K : info_scale;
+  const float* kg = is_iso ? nullptr : k_gain;
+#define KDN_KS(KK, VV)                                                                                           \
+  launch_kalman_kv<KK, VV>(is_iso, q, k, v, qkv_bf16, g, gain_a, omega, r, kg, precision_in, precision_out, BH, \
+                           scale, s, state, o, o_bf16, stream)
+  if (K == 64 && V == 64) KDN_KS(64, 64);
+  else if (K == 64) KDN_KS(64, 128);
+  else if (V == 64) KDN_KS(128, 64);
+  else KDN_KS(128, 128);
+#undef KDN_KS
   KDN_CHECK_LAUNCH();
   return 0;
 }

@@ -3,13 +3,14 @@
 The reference has no decoding path for KDN models (``model.py:104,184`` refuse caching).  Every
 KDN layer's history is a fixed-size state (``KDNLayerState``), so a decode step costs the same at
 any context length: the chunked scan consumes the prompt (``prefill``), then each ``step`` runs
-one token through every block, the mixers through ``kdn_mem_step``.
+one token through every block, the mixers through ``kdn_kalman_step``.
 
 One decode step launches a few hundred small kernels (about 20 per block), so at small batch
 the step is bound by launch overhead, not by the GPU.  With ``use_graph=True`` the step is
 captured once as a HIP graph (``torch.cuda.CUDAGraph``) over fixed buffers -- the token ids, the
-logits and every layer's state -- and each later step is one graph replay; the captured step
-updates the state buffers in place.
+logits and every layer's state -- and each later step is one graph replay.  The decoder's layer
+states are in-place states (``KDNLayerState.inplace``): each layer advances its own buffers, the
+mixers through ``kdn_kalman_step`` (the single-token gain and memory update in one launch).
 """
 from __future__ import annotations
 
@@ -38,7 +39,7 @@ class KDNDecoder:
         logits, state = self.model(idx, return_state=True)
         if self.state is None:
             self.state = [KDNLayerState(tuple(c.clone() for c in s.conv), s.memory.clone(), s.precision.clone(),
-                                        s.seen_tokens) for s in state]
+                                        s.seen_tokens, inplace=True) for s in state]
             self.logits = torch.empty_like(logits[:, -1])
         else:
             self._assign(state)
@@ -54,27 +55,31 @@ class KDNDecoder:
                 c.copy_(nc)
 
     def _eager_step(self):
-        logits, new = self.model(self.tokens, state=self.state, return_state=True)
-        self._assign(new)
+        # the states are in-place states: the layers advance their buffers themselves
+        logits, _ = self.model(self.tokens, state=self.state, return_state=True)
         self.logits.copy_(logits[:, -1])
 
     def _capture(self):
         # warm up (library handles, allocator) on a side stream without advancing the state
-        saved = [(s.memory.clone(), s.precision.clone(), tuple(c.clone() for c in s.conv)) for s in self.state]
+        saved = [(s.memory.clone(), s.precision.clone(), tuple(c.clone() for c in s.conv), s.seen_tokens)
+                 for s in self.state]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(2):
                 self._eager_step()
         torch.cuda.current_stream().wait_stream(side)
-        for s, (m, p, cs) in zip(self.state, saved):
+        for s, (m, p, cs, n) in zip(self.state, saved):
             s.memory.copy_(m)
             s.precision.copy_(p)
             for c, sc in zip(s.conv, cs):
                 c.copy_(sc)
+            s.seen_tokens = n
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._eager_step()
+        for s, (_, _, _, n) in zip(self.state, saved):
+            s.seen_tokens = n  # capture records the step without running it
 
     @torch.no_grad()
     def step(self, tokens: torch.Tensor) -> torch.Tensor:
@@ -84,13 +89,13 @@ class KDNDecoder:
             raise RuntimeError("call prefill() before step()")
         self.tokens.copy_(tokens.view(self.B, 1))
         if not self.use_graph:
-            self._eager_step()
+            self._eager_step()  # advances seen_tokens itself
         else:
             if self.graph is None:
                 self._capture()
             self.graph.replay()
-        for s in self.state:
-            s.seen_tokens += 1
+            for s in self.state:
+                s.seen_tokens += 1
         return self.logits
 
 

@@ -23,8 +23,8 @@ from .kdn_ops.diag_kdn_chunk import (_chunk_kalman_as, _diag_kdn_frontend_precum
                                      _diag_kdn_normalize)
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.short_conv import causal_conv1d
-from .kdn_ops.step import kdn_memory_step
-from .kdn_state import CONV_TAIL, KDNLayerState, check_state, conv_input_with_tail
+from .kdn_ops.step import kdn_kalman_step
+from .kdn_state import CONV_TAIL, carry_state, check_state, conv_input_with_tail
 
 _OMEGA_MIN = 0.0
 _R_MIN = 0.01
@@ -161,21 +161,27 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
             # the f32 recurrence is stored at the value dtype, as the reference's .to(v.dtype) does
             output = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale, out_dtype=v.dtype)
         else:
-            kappa, precision = _diag_kdn_gain(k_gain, alpha, omega, r,
-                                              state.precision if state is not None else initial_precision,
-                                              omega_raw, r_raw, output_final_state=True)
-            if T == 1 and not torch.is_grad_enabled():
-                memory = (state.memory.clone() if state is not None else
-                          torch.zeros(B, H, K, V, device=q.device, dtype=torch.float32))
-                output = kdn_memory_step(q_memory, k_memory, v, g_cumsum, state=memory, kappa=kappa, scale=scale,
-                                         out_dtype=v.dtype)
+            prec0 = state.precision if state is not None else initial_precision
+            if T == 1 and not torch.is_grad_enabled():  # gain and memory of one token in one launch
+                inplace = state is not None and state.inplace
+                if state is None:
+                    memory = torch.zeros(B, H, K, V, device=q.device, dtype=torch.float32)
+                else:
+                    memory = state.memory if inplace else state.memory.clone()
+                pin = prec0.float().view(1, H, 1).expand(B, H, K) if prec0.ndim == 1 else prec0
+                output, precision = kdn_kalman_step(
+                    q_memory, k_memory, v, g_cumsum, state=memory, precision=pin.contiguous(), alpha=alpha,
+                    omega=omega, r=r, k_gain=k_gain, info_scale=float(K), scale=scale, out_dtype=v.dtype,
+                    precision_out=state.precision_scratch() if inplace else None)
             else:
+                kappa, precision = _diag_kdn_gain(k_gain, alpha, omega, r, prec0, omega_raw, r_raw,
+                                                  output_final_state=True)
                 output, memory = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale,
                                                   initial_state=state.memory if state is not None else None,
                                                   output_final_state=True, out_dtype=v.dtype)
-            if use_cache:
-                new_state = KDNLayerState(tuple(tails), memory, precision,
-                                          (state.seen_tokens if state is not None else 0) + T)
+            new_state = carry_state(state, tails, memory, precision, T)
+            if not use_cache:
+                new_state = None
         output = self.o_norm(output, self.g_proj(hidden_states).view(B, T, H, V))
         return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
 

@@ -22,8 +22,8 @@ from torch import nn
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
 from .kdn_ops.short_conv import qkv_causal_conv1d
-from .kdn_ops.step import kdn_memory_step
-from .kdn_state import CONV_TAIL, KDNLayerState, check_state, conv_input_with_tail
+from .kdn_ops.step import kdn_kalman_step
+from .kdn_state import CONV_TAIL, carry_state, check_state, conv_input_with_tail
 
 _SUPPORTED_HEAD_DIMS = (64, 128)
 _INITIAL_PRECISION = 1.0
@@ -204,20 +204,26 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
                                 info_scale=self.info_scale)
             output = _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain)
         else:
-            gain, precision = iso_kdn_gain(a, omega, r, state.precision if state is not None else initial_precision,
-                                           head_dim=K, out_dtype=torch.float32, info_scale=self.info_scale,
-                                           output_final_state=True)
-            if T == 1 and not torch.is_grad_enabled():
-                memory = (state.memory.clone() if state is not None else
-                          torch.zeros(B, H, K, self.head_v_dim, device=q.device, dtype=torch.float32))
-                output = kdn_memory_step(q, k, v, g_cumsum, state=memory, beta=gain)
+            prec0 = state.precision if state is not None else initial_precision
+            if T == 1 and not torch.is_grad_enabled():  # gain and memory of one token in one launch
+                inplace = state is not None and state.inplace
+                if state is None:
+                    memory = torch.zeros(B, H, K, self.head_v_dim, device=q.device, dtype=torch.float32)
+                else:
+                    memory = state.memory if inplace else state.memory.clone()
+                output, precision = kdn_kalman_step(
+                    q, k, v, g_cumsum, state=memory, precision=prec0.float().expand(B, H).contiguous(), a=a,
+                    omega=omega, r=r, info_scale=self.info_scale,
+                    precision_out=state.precision_scratch() if inplace else None)
             else:
+                gain, precision = iso_kdn_gain(a, omega, r, prec0, head_dim=K, out_dtype=torch.float32,
+                                               info_scale=self.info_scale, output_final_state=True)
                 output, memory = _chunk_kda_precumsum_paired(
                     q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain,
                     initial_state=state.memory if state is not None else None, output_final_state=True)
-            if use_cache:
-                new_state = KDNLayerState((conv_tail,), memory, precision,
-                                          (state.seen_tokens if state is not None else 0) + T)
+            new_state = carry_state(state, (conv_tail,), memory, precision, T)
+            if not use_cache:
+                new_state = None
         gate = self.g_proj(hidden_states).view(B, T, H, self.head_v_dim)
         output = self.o_norm(output, gate)
         return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state

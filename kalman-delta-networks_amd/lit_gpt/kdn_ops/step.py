@@ -12,6 +12,8 @@ final state continues here token by token, and a state written here continues a 
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -63,4 +65,69 @@ def kdn_memory_step(q, k, v, g_cumsum, *, state, beta=None, kappa=None, scale=No
     return o
 
 
-__all__ = ("kdn_memory_step",)
+def kdn_kalman_step(q, k, v, g_cumsum, *, state, precision, omega, r, info_scale, a=None, alpha=None, k_gain=None,
+                    scale=None, out_dtype=None, precision_out=None):
+    """One token of the whole Kalman step (gain from the carried precision + memory update) in one
+    launch (``kdn_kalman_step``).  Advances ``state`` [B,H,K,V] fp32 in place and returns
+    ``(o [B,1,H,V], new_precision)``; ``new_precision`` is written to ``precision_out`` when given
+    (it must not be ``precision``).
+
+    Isotropic form: ``a`` (mean alpha^2), ``omega``, ``r`` [B,1,H]; ``precision`` [B,H]; q, k are
+    L2-normalised inside and the production gain's unit-key form is used (as
+    :func:`iso_kdn_gain` does): z = a/c + omega, beta = z/(r+z), c' = (r + s z)/(r z),
+    s = info_scale / K.  Diagonal form: ``alpha`` (unclamped, the gain's input), ``omega``
+    [B,1,H,K], ``r`` [B,1,H], ``k_gain`` [B,1,H,K] fp32 (defaults to k), ``precision`` [B,H,K];
+    q, k already normalised.  ``g_cumsum`` [B,1,H,K] fp32 is the memory's base-2 log decay.
+    """
+    if (a is None) == (alpha is None):
+        raise ValueError("pass exactly one of a (isotropic) or alpha (diagonal)")
+    if q.ndim != 4 or q.shape[1] != 1 or k.shape != q.shape:
+        raise ValueError(f"q and k must share shape [B,1,H,K], got {tuple(q.shape)} and {tuple(k.shape)}")
+    B, _, H, K = q.shape
+    if v.ndim != 4 or v.shape[:3] != (B, 1, H):
+        raise ValueError(f"v must have shape [{B},1,{H},V], got {tuple(v.shape)}")
+    V = v.shape[-1]
+    if K not in (64, 128) or V not in (64, 128):
+        raise ValueError(f"the step kernel supports K, V in {{64, 128}}, got K={K}, V={V}")
+    if g_cumsum.shape != (B, 1, H, K) or g_cumsum.dtype != torch.float32:
+        raise ValueError(f"g_cumsum must be fp32 [{B},1,{H},{K}], got {g_cumsum.dtype} {tuple(g_cumsum.shape)}")
+    if state.shape != (B, H, K, V) or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError(f"state must be a contiguous fp32 tensor of shape {(B, H, K, V)}")
+    iso = a is not None
+    gain_a = a if iso else alpha
+    tok = (B, 1, H) if iso else (B, 1, H, K)
+    prec_shape = (B, H) if iso else (B, H, K)
+    for name, x, shp in (("a" if iso else "alpha", gain_a, tok), ("omega", omega, tok), ("r", r, (B, 1, H)),
+                         ("precision", precision, prec_shape)):
+        if tuple(x.shape) != shp:
+            raise ValueError(f"{name} must have shape {shp}, got {tuple(x.shape)}")
+    if not iso and k_gain is not None and tuple(k_gain.shape) != (B, 1, H, K):
+        raise ValueError(f"k_gain must have shape {(B, 1, H, K)}, got {tuple(k_gain.shape)}")
+    if not (float(info_scale) > 0 and math.isfinite(float(info_scale))):
+        raise ValueError(f"info_scale must be positive and finite, got {info_scale!r}")
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"q must be bf16 or fp32, got {q.dtype}")
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype must be bf16 or fp32, got {out_dtype}")
+    _lib.require_device(q, k, v, g_cumsum, state, precision, gain_a, omega, r, k_gain, precision_out)
+    dt = q.dtype
+    q, k, v = (x.to(dt).contiguous() for x in (q, k, v))
+    gain_a, omega, r, pin = (x.float().contiguous() for x in (gain_a, omega, r, precision))
+    kg = k_gain.float().contiguous() if (k_gain is not None and not iso) else None
+    if precision_out is None:
+        precision_out = torch.empty(prec_shape, device=q.device, dtype=torch.float32)
+    elif (precision_out.shape != prec_shape or precision_out.dtype != torch.float32
+          or not precision_out.is_contiguous() or precision_out.data_ptr() == pin.data_ptr()):
+        raise ValueError("precision_out must be a contiguous fp32 tensor of the precision's shape, distinct from it")
+    o = torch.empty((B, 1, H, V), device=q.device, dtype=out_dtype)
+    scale = K ** -0.5 if scale is None else float(scale)
+    with torch.cuda.device(q.device):
+        _lib.call("kdn_kalman_step", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.is_bf16(q), _lib.ptr(g_cumsum.contiguous()),
+                  _lib.ptr(gain_a), _lib.ptr(omega), _lib.ptr(r), _lib.ptr(kg), _lib.ptr(pin), _lib.ptr(precision_out),
+                  int(iso), B, H, K, V, scale, float(info_scale), _lib.ptr(state), _lib.ptr(o), _lib.is_bf16(o),
+                  _lib.stream_of(q), tag="kalman_step")
+    return o, precision_out
+
+
+__all__ = ("kdn_memory_step", "kdn_kalman_step")

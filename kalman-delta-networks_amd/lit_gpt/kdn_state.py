@@ -19,7 +19,8 @@ when the segments are differentiated together.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
+from typing import Optional
 
 import torch
 
@@ -28,15 +29,43 @@ CONV_TAIL = 3  # width-4 short convolution: 3 earlier inputs
 
 @dataclass
 class KDNLayerState:
+    """``inplace=True`` makes a layer advance this object's own buffers (inference only), so their
+    addresses stay fixed across calls, as a replayed HIP graph needs; otherwise every call
+    returns a new state and leaves this one unchanged."""
     conv: tuple
     memory: torch.Tensor
     precision: torch.Tensor
     seen_tokens: int = 0
+    inplace: bool = False
+    _scratch: Optional[torch.Tensor] = field(default=None, repr=False)
 
     def detach(self) -> "KDNLayerState":
         """The same state cut from the autograd graph (truncated back-propagation)."""
         return KDNLayerState(tuple(c.detach() for c in self.conv), self.memory.detach(), self.precision.detach(),
                              self.seen_tokens)
+
+    def precision_scratch(self) -> torch.Tensor:
+        """A second precision buffer for a kernel that must not read and write the same one."""
+        if self._scratch is None:
+            self._scratch = torch.empty_like(self.precision)
+        return self._scratch
+
+
+def carry_state(state, conv, memory, precision, T: int):
+    """The state after T more tokens: a new KDNLayerState, or ``state`` itself advanced in place
+    (its buffers overwritten) when it is an in-place state."""
+    if state is not None and state.inplace:
+        if torch.is_grad_enabled():
+            raise RuntimeError("in-place KDN layer states are for inference; run under torch.no_grad()")
+        for c, n in zip(state.conv, conv):
+            c.copy_(n)
+        if memory is not state.memory:
+            state.memory.copy_(memory)
+        if precision is not state.precision:
+            state.precision.copy_(precision)
+        state.seen_tokens += T
+        return state
+    return KDNLayerState(tuple(conv), memory, precision, (state.seen_tokens if state is not None else 0) + T)
 
 
 def conv_input_with_tail(x: torch.Tensor, tail):
@@ -68,4 +97,4 @@ def check_state(state, B: int, H: int, K: int, V: int, n_conv: int, precision_sh
             raise ValueError("the layer state must live on the hidden states' device")
 
 
-__all__ = ("KDNLayerState", "conv_input_with_tail", "check_state", "CONV_TAIL")
+__all__ = ("KDNLayerState", "carry_state", "conv_input_with_tail", "check_state", "CONV_TAIL")

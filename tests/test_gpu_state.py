@@ -7,6 +7,8 @@
 * ``kdn_mem_step``: several single-token steps from a random fp32 state against the oracle's
   tokenwise recurrence (``memory_tokenwise``, fed the same rounded inputs, with the FLA l2norm of
   q, k for the isotropic form): outputs and state at 1e-4 (fp32 outputs) / 1e-2 (bf16 outputs).
+  ``kdn_kalman_step`` (gain and memory in one launch) likewise, from a random precision too,
+  against the tokenwise gains feeding the same recurrence: outputs, state, precision at 1e-4.
 * Layers in eval mode (isotropic fp32; diagonal under bf16 autocast, its frontend taking bf16
   only): full sequence vs a chunked prefill, a second chunked segment and single-token steps,
   each against the oracle layer of the whole sequence (2e-2, or the autocast noise floor) and
@@ -121,6 +123,64 @@ def test_memory_step_matches_tokenwise(variant, K, V, dtype, out_dtype):
     assert o.dtype == out_dtype
     _check("o", o, o_ref, 1e-4 if out_dtype == torch.float32 else 1e-2)
     _check("state", state, S_ref, 1e-4)
+
+
+@pytest.mark.parametrize("variant,K,V,dtype", [("iso", 128, 128, torch.bfloat16), ("iso", 64, 128, torch.float32),
+                                               ("diag", 128, 128, torch.bfloat16), ("diag", 64, 64, torch.float32)])
+def test_kalman_step_matches_tokenwise(variant, K, V, dtype):
+    """``kdn_kalman_step`` (the single-token gain from the carried precision, then the memory
+    update, in one launch), six steps from a random state and precision, against the tokenwise
+    gain (iso: the production unit-key form; diag: ``diag_gain_tokenwise``) feeding
+    ``memory_tokenwise``: outputs, state and final precision at 1e-4."""
+    dev = gpu_or_skip()
+    log(f"case kalman step {variant} K={K} V={V} in={dtype}")
+    from lit_gpt.kdn_ops.step import kdn_kalman_step
+    B, H, steps = 2, 3, 6
+    g = torch.Generator().manual_seed(7 * K + V + (0 if variant == "iso" else 1))
+    q = 2.0 * torch.randn(B, steps, H, K, generator=g)
+    k = 2.0 * torch.randn(B, steps, H, K, generator=g)
+    if variant == "diag":
+        q, k = ko.diag_normalize(q), ko.diag_normalize(k)
+    k_gain = k.clone()  # the diagonal gain's fp32 key
+    q, k = q.to(dtype), k.to(dtype)
+    v = torch.randn(B, steps, H, V, generator=g).to(dtype)
+    g2 = ((-0.13 + 0.05 * torch.randn(B, steps, H, K, generator=g)).clamp(max=0.0) / LN2).float()
+    S0 = torch.randn(B, H, K, V, generator=g)
+    r = 0.01 + F.softplus(torch.randn(B, steps, H, generator=g))
+    qd, kd, vd = q.double(), k.double(), v.double()
+    if variant == "iso":
+        a = torch.sigmoid(2 + 0.5 * torch.randn(B, steps, H, generator=g)) ** 2
+        omega = F.softplus(torch.randn(B, steps, H, generator=g))
+        c0 = 0.5 + torch.rand(B, H, generator=g)
+        qd, kd = ko.l2norm_fla(qd), ko.l2norm_fla(kd)
+        beta_ref, c_ref = _iso_gain_ref(a.double(), omega.double(), r.double(), c0.double(), 1.0)
+        kap_ref = beta_ref[..., None] * kd
+        gain_kw = {"a": a}
+    else:
+        alpha = torch.sigmoid(2 + 0.5 * torch.randn(B, steps, H, K, generator=g))
+        omega = F.softplus(torch.randn(B, steps, H, K, generator=g))
+        c0 = 0.3 + torch.rand(B, H, K, generator=g)
+        kap_ref, c_ref = ko.diag_gain_tokenwise(k_gain.double(), alpha.double(), omega.double(), r.double(),
+                                                info_scale=float(K), initial_precision=c0.double(),
+                                                output_final_state=True)
+        gain_kw = {"alpha": alpha}
+    o_ref, S_ref = ko.memory_tokenwise(qd, kd, vd, (g2.double() * LN2).exp(), kap_ref, scale=K ** -0.5,
+                                       initial_state=S0.double())
+    state, prec = S0.to(dev).contiguous(), c0.to(dev)
+    outs = []
+    for t in range(steps):
+        sl = slice(t, t + 1)
+        kw = {n: x[:, sl].to(dev) for n, x in gain_kw.items()}
+        if variant == "diag":
+            kw["k_gain"] = k_gain[:, sl].to(dev)
+        o, prec = kdn_kalman_step(q[:, sl].to(dev), k[:, sl].to(dev), v[:, sl].to(dev), g2[:, sl].to(dev),
+                                  state=state, precision=prec, omega=omega[:, sl].to(dev), r=r[:, sl].to(dev),
+                                  info_scale=float(K), out_dtype=torch.float32, **kw)
+        outs.append(o)
+    torch.cuda.synchronize()
+    _check("o", torch.cat(outs, 1), o_ref, 1e-4)
+    _check("state", state, S_ref, 1e-4)
+    _check("final precision", prec, c_ref, 1e-4)
 
 
 def _oracle_layer(variant, p, x, head_dim, amp=False):
