@@ -1,0 +1,50 @@
+"""Inference-time caches for the decode path (no autograd).
+
+A decode step runs one token through every block, so every separate small GEMM and dtype cast
+is one more launch.  Projections that read the same input are packed into one weight, and the
+small gate parameters' fp32 copies are kept, both cached on the owning module and rebuilt when a
+source tensor's storage or version changes (``load_state_dict``, an optimiser step, ``.to()``).
+The caches are plain attributes, not buffers, so they never enter a state dict.
+"""
+from __future__ import annotations
+
+import torch
+
+# at most this many rows (B * T) take the packed projections: the launch-bound decode regime;
+# longer inputs keep the separate GEMMs, whose outputs are contiguous
+PACK_MAX_ROWS = 64
+
+
+def use_packed(x: torch.Tensor) -> bool:
+    return not torch.is_grad_enabled() and x.numel() // x.shape[-1] <= PACK_MAX_ROWS
+
+
+def _key(tensors):
+    return tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in tensors)
+
+
+def packed_weight(owner, name: str, tensors) -> torch.Tensor:
+    """torch.cat(tensors, 0), cached on ``owner`` under ``name``."""
+    cache = owner.__dict__.setdefault("_kdn_inference_cache", {})
+    key = _key(tensors)
+    hit = cache.get(name)
+    if hit is None or hit[0] != key:
+        hit = (key, torch.cat([t.detach() for t in tensors], 0))
+        cache[name] = hit
+    return hit[1]
+
+
+def as_f32(owner, name: str, t: torch.Tensor) -> torch.Tensor:
+    """``t.float()``; under no_grad the converted copy of a non-fp32 tensor is cached on ``owner``."""
+    if t.dtype == torch.float32 or torch.is_grad_enabled():
+        return t.float()
+    cache = owner.__dict__.setdefault("_kdn_inference_cache", {})
+    key = _key((t,))
+    hit = cache.get(name)
+    if hit is None or hit[0] != key:
+        hit = (key, t.detach().float())
+        cache[name] = hit
+    return hit[1]
+
+
+__all__ = ("PACK_MAX_ROWS", "use_packed", "packed_weight", "as_f32")

@@ -16,8 +16,10 @@ from __future__ import annotations
 import math
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
+from ._inference import as_f32, packed_weight, use_packed
 from .iso_kdn import _SUPPORTED_HEAD_DIMS, decay_parameters, initial_precision_inverse, validate_training_dtype
 from .kdn_ops.diag_kdn_chunk import (_chunk_kalman_as, _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain,
                                      _diag_kdn_normalize)
@@ -135,7 +137,24 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
         state = past_key_values
         if state is not None:
             check_state(state, B, H, K, V, 3, (B, H, K), hidden_states.device)
-        projections = (self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states))
+        gate = None
+        if use_packed(hidden_states):  # a few rows without autograd: the six biasless input GEMMs as one
+            D, d = self.key_dim, self.head_k_dim
+            w_in = packed_weight(self, "in_proj", (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                                                   self.f_proj[0].weight, self.omega_proj[0].weight,
+                                                   self.g_proj[0].weight))
+            yq, yk, yv, f_hidden, w_hidden, g_hidden = F.linear(hidden_states, w_in).split(
+                (D, D, self.value_dim, d, d, d), dim=-1)
+            projections = (yq, yk, yv)
+            retention_raw = self.f_proj[1](f_hidden).view(B, T, H, K)
+            omega_raw = self.omega_proj[1](w_hidden).view(B, T, H, K)
+            r_raw = self.r_proj(hidden_states)  # its bias rounds with the product, as in the layer's GEMM
+            gate = self.g_proj[1](g_hidden)
+        else:
+            projections = (self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states))
+            retention_raw = self.f_proj(hidden_states).view(B, T, H, K)
+            omega_raw = self.omega_proj(hidden_states).view(B, T, H, K)
+            r_raw = self.r_proj(hidden_states)
         convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d)
         if stateful:
             tails, outs = [], []
@@ -145,15 +164,12 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
                 tails.append(tail)
             q, k, v = outs
         else:
-            q, k, v = (conv(x) for x, conv in zip(projections, convs))
+            q, k, v = (conv(x.contiguous()) for x, conv in zip(projections, convs))
         q, k, v = q.reshape(B, T, H, K), k.reshape(B, T, H, K), v.reshape(B, T, H, V)
-        retention_raw = self.f_proj(hidden_states).view(B, T, H, K)
-        omega_raw = self.omega_proj(hidden_states).view(B, T, H, K)
-        r_raw = self.r_proj(hidden_states)
         q_memory, k_gain, k_memory = _diag_kdn_normalize(q, k)
         g_cumsum, alpha, omega, r, initial_precision = _diag_kdn_frontend_precumsum_paired(
-            retention_raw, omega_raw, r_raw, self.A_log.float(), self.dt_bias.float().view(H, K),
-            self.initial_precision_param.float())
+            retention_raw, omega_raw, r_raw, as_f32(self, "A_log", self.A_log),
+            as_f32(self, "dt_bias", self.dt_bias).view(H, K), as_f32(self, "mu_param", self.initial_precision_param))
         new_state = None
         scale = float(K ** -0.5)
         if not stateful:
@@ -182,7 +198,9 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
             new_state = carry_state(state, tails, memory, precision, T)
             if not use_cache:
                 new_state = None
-        output = self.o_norm(output, self.g_proj(hidden_states).view(B, T, H, V))
+        if gate is None:
+            gate = self.g_proj(hidden_states)
+        output = self.o_norm(output, gate.view(B, T, H, V))
         return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
 
 

@@ -19,6 +19,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from ._inference import as_f32, packed_weight, use_packed
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
 from .kdn_ops.short_conv import qkv_causal_conv1d
@@ -183,21 +184,30 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         state = past_key_values
         if state is not None:
             check_state(state, B, H, K, self.head_v_dim, 1, (B, H), hidden_states.device)
+        gate = None
+        if use_packed(hidden_states):  # a few rows without autograd: the three input GEMMs as one
+            w_in = packed_weight(self, "in_proj", (self.qkv_pack.projection_weight, self.f_omega_r_proj.weight,
+                                                   self.g_proj[0].weight))
+            x_lin, packed, g_hidden = F.linear(hidden_states, w_in).split(
+                (self.qkv_pack.out_features, self.head_v_dim + 2 * H, self.head_v_dim), dim=-1)
+            gate = self.g_proj[1](g_hidden)
+        else:
+            x_lin = F.linear(hidden_states, self.qkv_pack.projection_weight)
+            packed = self.f_omega_r_proj.forward_packed(hidden_states)
         if stateful:
-            x_proj, conv_tail = conv_input_with_tail(F.linear(hidden_states, self.qkv_pack.projection_weight),
-                                                     state.conv[0] if state is not None else None)
+            x_proj, conv_tail = conv_input_with_tail(x_lin, state.conv[0] if state is not None else None)
             q, k, v = (t[:, CONV_TAIL:] for t in qkv_causal_conv1d(x_proj, self.qkv_pack.convolution_weight))
         else:
-            q, k, v = self.qkv_pack(hidden_states)
-        packed = self.f_omega_r_proj.forward_packed(hidden_states)
+            q, k, v = qkv_causal_conv1d(x_lin.contiguous(), self.qkv_pack.convolution_weight)
         f_hidden, omega_r_raw = packed.split((self.head_v_dim, 2 * H), dim=-1)
         g_raw = self.f_proj[1](f_hidden)
         q, k = q.reshape(B, T, H, K), k.reshape(B, T, H, K)
         v = v.reshape(B, T, H, self.head_v_dim)
         g_raw = g_raw.view(B, T, H, K)
         g_cumsum, a, omega, r, initial_precision = _iso_kdn_gate_precumsum_paired(
-            g_raw, omega_r_raw, self.omega_proj.bias.float(), self.r_proj.bias.float(), self.A_log.float(),
-            self.dt_bias.float(), self.initial_precision_param.float(), self.omega_min, self.r_min)
+            g_raw, omega_r_raw, as_f32(self, "omega_bias", self.omega_proj.bias), as_f32(self, "r_bias", self.r_proj.bias),
+            as_f32(self, "A_log", self.A_log), as_f32(self, "dt_bias", self.dt_bias),
+            as_f32(self, "mu_param", self.initial_precision_param), self.omega_min, self.r_min)
         new_state = None
         if not stateful:
             gain = iso_kdn_gain(a, omega, r, initial_precision, head_dim=K, out_dtype=torch.float32,
@@ -224,8 +234,9 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
             new_state = carry_state(state, (conv_tail,), memory, precision, T)
             if not use_cache:
                 new_state = None
-        gate = self.g_proj(hidden_states).view(B, T, H, self.head_v_dim)
-        output = self.o_norm(output, gate)
+        if gate is None:
+            gate = self.g_proj(hidden_states)
+        output = self.o_norm(output, gate.view(B, T, H, self.head_v_dim))
         return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
 
 

@@ -25,6 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from ._inference import packed_weight, use_packed
 from .config import Config
 
 
@@ -174,6 +175,9 @@ class SwiGLU(nn.Module):
         self.w3 = nn.Linear(hidden_features, in_features, bias=bias)
 
     def forward(self, x):
+        if self.w1.bias is None and self.w2.bias is None and use_packed(x):  # decode: w1 | w2 as one GEMM
+            h1, h2 = F.linear(x, packed_weight(self, "w12", (self.w1.weight, self.w2.weight))).chunk(2, dim=-1)
+            return self.w3(F.silu(h1) * h2)
         return self.w3(F.silu(self.w1(x)) * self.w2(x))
 
 

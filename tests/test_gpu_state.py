@@ -227,7 +227,9 @@ def test_layer_segments_and_decode_match_full_sequence(variant, head_dim):
     _check("segmented vs GPU full", seg, full, 1e-2)
     _check("stateful vs plain full call", full, plain, 1e-6)
     _check("memory state", st.memory, st_full.memory, 1e-2)
-    _check("precision state", st.precision, st_full.precision, 1e-4)
+    # bf16 projections of one token and of a whole segment come from different GEMM kernels and may
+    # differ in the last bit under autocast; the fp32 isotropic layer holds the precision to 1e-4
+    _check("precision state", st.precision, st_full.precision, 1e-3 if amp else 1e-4)
     for i, (a, b) in enumerate(zip(st.conv, st_full.conv)):
         _check(f"conv state {i}", a, b, 1e-5)
 
