@@ -306,13 +306,15 @@ def run_decode(name: str, steps: int, warmup: int, prompt: int = 1024):
     """Token-by-token decoding of the random-init config-4 model (bf16 weights, eval) after a
     ``prompt``-token prefill, eager and as a replayed HIP graph (``KDNDecoder``), at batch 1 and 32:
     ms per decode step (one token for each of B sequences) and tokens/s = B / step time.  Beside it,
-    the single-token memory kernel ``kdn_mem_step`` alone at the model's H18 d128 and B in {1, 64}:
-    HBM-bound, algorithmic bytes = B H (2 K V 4 state read + write, q, k, v, o bf16, g f32, beta)."""
+    the single-token kernels alone at the model's H18 d128 and B in {1, 64}: ``kdn_mem_step``
+    (memory only) and ``kdn_kalman_step`` (the iso gain from the carried precision + memory, the
+    kernel the model's decode runs); HBM-bound, algorithmic bytes = B H (2 K V 4 state read +
+    write, q, k, v, o bf16, g f32, and beta or a, omega, r, precision in and out)."""
     import torch
 
     from lit_gpt.decode import KDNDecoder
     from lit_gpt.kdn_ops import _lib
-    from lit_gpt.kdn_ops.step import kdn_memory_step
+    from lit_gpt.kdn_ops.step import kdn_kalman_step, kdn_memory_step
     from lit_gpt.model import GPT
 
     dev = torch.device("cuda:0")
@@ -351,7 +353,7 @@ def run_decode(name: str, steps: int, warmup: int, prompt: int = 1024):
         out["model"][f"B{B}"] = row
     del model
     torch.cuda.empty_cache()
-    kern = {}
+    kern, kal = {}, {}
     for B in (1, 64):
         g = torch.Generator(device=dev).manual_seed(B)
         q = torch.randn(B, 1, H, K, device=dev, generator=g).bfloat16()
@@ -359,18 +361,26 @@ def run_decode(name: str, steps: int, warmup: int, prompt: int = 1024):
         v = torch.randn(B, 1, H, K, device=dev, generator=g).bfloat16()
         gc = (-0.1 * torch.rand(B, 1, H, K, device=dev, generator=g)).float()
         beta = torch.rand(B, 1, H, device=dev, generator=g)
+        a, w, r = (0.5 + torch.rand(B, 1, H, device=dev, generator=g) for _ in range(3))
+        prec = [torch.ones(B, H, device=dev), torch.empty(B, H, device=dev)]
         S = torch.zeros(B, H, K, K, device=dev)
         for _ in range(warmup):
             kdn_memory_step(q, k, v, gc, state=S, beta=beta)
+            kdn_kalman_step(q, k, v, gc, state=S, precision=prec[0], precision_out=prec[1], a=a, omega=w, r=r,
+                            info_scale=float(K))
         with _lib.KernelTimer() as kt:
-            for _ in range(steps):
+            for i in range(steps):
                 kdn_memory_step(q, k, v, gc, state=S, beta=beta)
-        ms = kt.mean_ms("mem_step")
-        alg = B * H * (2 * K * K * 4 + 3 * K * 2 + K * 4 + 4 + K * 2)
-        gbs = alg / (ms * 1e-3) / 1e9
-        kern[f"B{B}"] = {"us": round(ms * 1e3, 2), "alg_bytes": alg, "achieved_GBps": round(gbs, 1),
-                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                kdn_kalman_step(q, k, v, gc, state=S, precision=prec[i % 2], precision_out=prec[1 - i % 2], a=a,
+                                omega=w, r=r, info_scale=float(K))
+        for tag, extra, dst in (("mem_step", 4, kern), ("kalman_step", 5 * 4, kal)):
+            ms = kt.mean_ms(tag)
+            alg = B * H * (2 * K * K * 4 + 3 * K * 2 + K * 4 + extra + K * 2)
+            gbs = alg / (ms * 1e-3) / 1e9
+            dst[f"B{B}"] = {"us": round(ms * 1e3, 2), "alg_bytes": alg, "achieved_GBps": round(gbs, 1),
+                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     out["mem_step_kernel"] = kern
+    out["kalman_step_kernel"] = kal
     return out
 
 
