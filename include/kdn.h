@@ -90,7 +90,9 @@ int kdn_diag_frontend_fwd(const uint16_t* retention_raw, const uint16_t* omega_r
                           int chunk, float* g_cumsum, float* alpha, float* omega, float* r, float* mu,
                           hipStream_t stream);
 size_t kdn_diag_frontend_bwd_workspace_size(int B, int T, int H, int K, int chunk);
-/* _diag_kdn_frontend_backward (diag_kdn_chunk.py:2265-2423, kernels :1907-2016). */
+/* _diag_kdn_frontend_backward (diag_kdn_chunk.py:2265-2423, kernels :1907-2016).  alpha is the
+ * forward's output; the vectorised path (K % 8 == 0, 16-byte aligned) recomputes it bit-identically
+ * from retention_raw instead of reading it. */
 int kdn_diag_frontend_bwd(const uint16_t* retention_raw, const uint16_t* omega_raw, const uint16_t* r_raw,
                           const float* A_log, const float* dt_bias, const float* mu_param, const float* alpha,
                           const float* d_g_cumsum, const float* d_alpha, const float* d_omega, const float* d_r,

@@ -64,6 +64,15 @@ __device__ __forceinline__ float softplusf(float x) {
   return y < 1e-3f ? y * (1.f - 0.5f * y) : __logf(1.f + y);
 }
 __device__ __forceinline__ float sigmoidf(float x) { return __frcp_rn(1.f + __expf(-x)); }
+// softplus(x) and sigmoid(x) from one exponential y = e^min(x, 20): softplus = x above 20 (torch's
+// threshold), else log(1 + y) (y (1 - y/2) below y = 1e-3); sigmoid = y / (1 + y) with the hardware
+// reciprocal (~1 ulp; it rounds to 1 above 20, as 1 / (1 + e^-x) does in fp32).
+__device__ __forceinline__ void softplus_sigmoid(float x, float& sp, float& sg) {
+  const float y = __expf(fminf(x, 20.f));
+  const float d = 1.f + y;
+  sg = y * __builtin_amdgcn_rcpf(d);
+  sp = x > 20.f ? x : (y < 1e-3f ? y * (1.f - 0.5f * y) : __logf(d));
+}
 
 // ---- wave64 reductions -----------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

@@ -292,10 +292,12 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float xb = xr[u][j] + bias[j];
-        const float g = -rate * softplusf(xb);
+        float sp, sg;
+        softplus_sigmoid(xb, sp, sg);
+        const float g = -rate * sp;
         float dgl = dg_pre ? off[j] + dgp[u][j] : 0.f;
         if (da) dgl += dau * __expf(2.f * g);
-        dgr[j] = dgl * (-rate) * sigmoidf(xb);
+        dgr[j] = dgl * (-rate) * sg;
         dA_term += dgl * g;
         ddt[j] += dgr[j];
       }
@@ -728,14 +730,14 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
   const float rate = __expf(A_log[h]);
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
-  // the loads of all this thread's tokens go out first (rows clamped to the chunk)
-  float dGr[4][8], xr[4][8], alr[4][8], dar[4][8];
+  // the loads of all this thread's tokens go out first (rows clamped to the chunk); alpha is
+  // recomputed from f_raw with the forward's own operations (bit-identical), not read back
+  float dGr[4][8], xr[4][8], dar[4][8];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int64_t off = (((int64_t)b * T + t0 + min(tg * TPG + u, L - 1)) * H + h) * K + i0;
     if (dG) load8<float>(dG + off, dGr[u]);
     load8<bf16_t>(f_raw + off, xr[u]);
-    load8<float>(alpha + off, alr[u]);
     if (dalpha) load8<float>(dalpha + off, dar[u]);
   }
   // local suffix sums of dG over this thread's tokens
@@ -769,15 +771,17 @@ __global__ __launch_bounds__(256) void diag_frontend_bwd_vec_kernel(
       const int64_t off = (((int64_t)b * T + t0 + t) * H + h) * K + i0;
       float df[8];
       const float* x = xr[u];
-      const float* al = alr[u];
       const float* da = dar[u];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float xb = x[j] + bias[j];
-        const float ell = -rate * softplusf(xb);
-        float dell = (dG && al[j] >= 1e-6f) ? offs[j] + dgs[u][j] : 0.f;
-        if (dalpha) dell += da[j] * al[j];
-        df[j] = dell * (-rate) * sigmoidf(xb);
+        float sp, sg;
+        softplus_sigmoid(xb, sp, sg);
+        const float ell = -rate * sp;
+        const float al = __expf(ell);
+        float dell = (dG && al >= 1e-6f) ? offs[j] + dgs[u][j] : 0.f;
+        if (dalpha) dell += da[j] * al;
+        df[j] = dell * (-rate) * sg;
         dA_term += dell * ell;
         ddt[j] += df[j];
       }
