@@ -164,6 +164,9 @@ def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K
         per_kernel[tag] = dict(ms=round(t * 1e3, 4), bound=bound, achieved=round(achieved, 2), peak=peak,
                                unit=unit, frac=round(achieved / peak, 4), mfma=MFMA_PATH.get(tag, "f32"),
                                alg_bytes=int(nbytes), alg_flops=int(flops))
+        if tag in MFMA_PATH:  # the MFMA view beside the binding one: algorithmic FLOP/s against the path peak
+            per_kernel[tag]["mfma_tflops"] = round(flops / t / 1e12, 2)
+            per_kernel[tag]["mfma_frac"] = round(flops / t / 1e12 / mfma_peak(tag), 4)
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
     return dict(ms_per_step=ms, tokens_per_s=B * T / (ms * 1e-3), kernels=per_kernel, dominant=dominant)
 
