@@ -244,7 +244,6 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
   float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
-  __shared__ float sSpan[4];
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
@@ -265,19 +264,42 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
   float* An = Ag + ((int64_t)bh * NT + n) * C * C;
 
+  // ---- 0. the chunk's decay span max_i (G_0 - G_{L-1})_i, from rows 0 and L-1 alone, before any
+  // other load or store: a chunk past the single anchor's range goes to the block-anchor kernel
+  // without paying for the rest.  Lane groups g4 cover all K channels, so every wave computes the
+  // same span and the early return is uniform across the workgroup (no barrier needed).
+  float g0s[KB][8], gls[KB][8];  // rows 0 and L-1, kept for stage 1
+  {
+    float span = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int i0 = 32 * kb + 8 * g4;
+      ld8(rG, i0 * 4, g0s[kb]);
+      ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gls[kb]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) span = fmaxf(span, g0s[kb][j] - gls[kb][j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
+    if (!(span <= kAnchorSpanMax)) {  // the block-anchor kernel (or, past it, the exact one) takes this chunk
+      if (tid == 0) flags[(int64_t)bh * NT + n] = 1;
+      return;
+    }
+  }
+  if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
+
   // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels
   const int c = 16 * w + r16;
   const uint32_t crow = (uint32_t)(c * H);
   uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
-  float span = 0.f;
   const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int i0 = 32 * kb + 8 * g4;
-    float gcv[8], g0[8], gl[8], kv[8], qv[8], av[8];
+    float gcv[8], kv[8], qv[8], av[8];
+    const float* g0 = g0s[kb];
+    const float* gl = gls[kb];
     ld8(rG, (crow * K + i0) * 4, gcv);
-    ld8(rG, i0 * 4, g0);
-    ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
     unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
     unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
     if (ISO) {
@@ -295,7 +317,6 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
       rr[j] = av[j] * exp2f(g0[j] - gcv[j]);
       kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
       qg[j] = scale * qv[j] * exp2f(gcv[j]);
-      span = fmaxf(span, g0[j] - gl[j]);
     }
     split8(lk, lkh[kb], lkl[kb]);
     split8(lq, lqh[kb], lql[kb]);
@@ -306,16 +327,7 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
     st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) span = fmaxf(span, __shfl_xor(span, o, 64));
-  if (lane == 0) sSpan[w] = span;
-  __syncthreads();
-  const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
-  if (!(cspan <= kAnchorSpanMax)) {  // the block-anchor kernel (or, past it, the exact one) takes this chunk
-    if (tid == 0) flags[(int64_t)bh * NT + n] = 1;
-    return;
-  }
-  if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
+  __syncthreads();  // R fragments of every row block
 
   // ---- 2. N and M tiles of row block I = w
   const bufrsrc rM = make_buf(Mn, C * C * 4);
