@@ -172,6 +172,14 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
                     const float* omega, const float* r, const float* k_gain, const float* precision_in,
                     float* precision_out, int iso, int B, int H, int K, int V, float scale, float info_scale,
                     float* state, void* o, int o_bf16, hipStream_t stream);
+/* Decode projections: y[m, :] = W x[m, :] (+ bias) for M <= 8 rows, the one-token-per-sequence
+ * form of the layers' nn.Linear products (the reference runs every projection as a torch GEMM,
+ * e.g. iso_kdn.py:277-312, model.py:415-464; this is no port of one).  W [N,K] bf16 row-major,
+ * bias [N] bf16 (nullable), fp32 accumulation; x [M,K] bf16 (x_bf16) or f32 with row stride
+ * x_row_stride elements, y [M,N] in x's dtype with row stride y_row_stride.  K % 128 == 0; W and
+ * the rows of x 16-byte aligned. */
+int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias, int M, int N,
+             int K, void* y, int64_t y_row_stride, hipStream_t stream);
 
 /* ---------------------------------------------------------------- layer frontends */
 /* Depthwise causal short convolution with SiLU, fixed length, width W = 4, no bias:

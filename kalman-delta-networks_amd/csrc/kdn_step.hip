@@ -312,3 +312,109 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------------------------
+// Decode projections: y[m, n] = sum_k x[m, k] W[n, k] (+ bias[n]) for a few rows m (M <= 8) and a
+// bf16 weight W [N, K] (an nn.Linear weight), fp32 accumulation.  With one token per sequence the
+// product reads every weight element once, so it is bound by the weight stream.  block 256 = 16
+// output rows (4 per wave, 16 lanes per row); a lane reads 16 bytes of its row per 128-column step
+// with 8 steps in flight (the 16 lanes of a row cover 256 contiguous bytes), x through the cache,
+// and the row's partial sums meet in 4 xor shuffles.  K % 128 == 0.
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+constexpr int kGemvLanes = 16;                 // lanes per output row
+constexpr int kGemvRows = 256 / kGemvLanes;    // output rows per workgroup
+constexpr int kGemvStep = 8 * kGemvLanes;      // columns per step
+constexpr int kGemvInFlight = 8;               // steps whose weight loads are issued together
+
+// MM = the instantiated row capacity; rows m >= M (runtime) are neither read nor written.
+template <int MM, typename TX, typename TY>
+__global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int64_t xs, const bf16_t* __restrict__ W,
+                                                   const bf16_t* __restrict__ bias, int M, int N, int K,
+                                                   TY* __restrict__ y, int64_t ys) {
+  const int t = threadIdx.x, j = t % kGemvLanes;
+  const int n = blockIdx.x * kGemvRows + t / kGemvLanes;
+  const bool live = n < N;
+  const bf16_t* wr = W + (int64_t)(live ? n : 0) * K + 8 * j;
+  float acc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) acc[m] = 0.f;
+  constexpr int U = kGemvInFlight;
+  for (int k0 = 0; k0 < K; k0 += kGemvStep * U) {
+    uint4 wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      wv[u] = k0 + kGemvStep * u < K ? *reinterpret_cast<const uint4*>(wr + k0 + kGemvStep * u) : uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k0 + kGemvStep * u + 8 * j;
+      if (k0 + kGemvStep * u >= K) break;
+      const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      float wf[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        wf[2 * q] = __uint_as_float(ww[q] << 16);
+        wf[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        if (m >= M) break;
+        float xf[8];
+        if constexpr (sizeof(TX) == 2) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(x + m * xs + kk);
+          const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            xf[2 * q] = __uint_as_float(xx[q] << 16);
+            xf[2 * q + 1] = __uint_as_float(xx[q] & 0xffff0000u);
+          }
+        } else {
+          const float4 a = *reinterpret_cast<const float4*>(x + m * xs + kk);
+          const float4 b = *reinterpret_cast<const float4*>(x + m * xs + kk + 4);
+          xf[0] = a.x, xf[1] = a.y, xf[2] = a.z, xf[3] = a.w, xf[4] = b.x, xf[5] = b.y, xf[6] = b.z, xf[7] = b.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m] = fmaf(wf[e], xf[e], acc[m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int o = 1; o < kGemvLanes; o <<= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+  if (live && j == 0) {
+    const float bb = bias ? bf2f(bias[n]) : 0.f;
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      if (m < M) st(y, m * ys + n, acc[m] + bb);
+  }
+}
+
+template <int MM>
+void launch_gemv(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
+                 void* y, int64_t ys, hipStream_t stream) {
+  const dim3 grid((N + kGemvRows - 1) / kGemvRows), block(256);
+  if (x_bf16)
+    hipLaunchKernelGGL((gemv_kernel<MM, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias, M, N,
+                       K, (bf16_t*)y, ys);
+  else
+    hipLaunchKernelGGL((gemv_kernel<MM, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M, N, K,
+                       (float*)y, ys);
+}
+
+}  // namespace
+
+extern "C" int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias,
+                        int M, int N, int K, void* y, int64_t y_row_stride, hipStream_t stream) {
+  if (M < 0 || M > 8 || N < 0 || K <= 0 || K % kGemvStep || !W || !x || !y) return KDN_ERR_ARG;
+  if (M == 0 || N == 0) return 0;
+  // 16-byte rows: W rows are K * 2 bytes (K % 128 == 0); x rows 16-byte aligned
+  if (!aligned(W, 16) || !aligned(x, 16) || (x_row_stride * (x_bf16 ? 2 : 4)) % 16) return KDN_ERR_ARG;
+  if (M == 1) launch_gemv<1>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
+  else if (M == 2) launch_gemv<2>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
+  else if (M <= 4) launch_gemv<4>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
+  else launch_gemv<8>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}

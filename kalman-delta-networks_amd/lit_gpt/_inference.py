@@ -9,10 +9,13 @@ The caches are plain attributes, not buffers, so they never enter a state dict.
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 # at most this many rows (B * T) take the packed projections: the launch-bound decode regime;
 # longer inputs keep the separate GEMMs, whose outputs are contiguous
 PACK_MAX_ROWS = 64
+# at most this many rows with bf16 activations and weights go through the weight-streaming GEMV
+GEMV_MAX_ROWS = 8
 
 
 def use_packed(x: torch.Tensor) -> bool:
@@ -47,4 +50,17 @@ def as_f32(owner, name: str, t: torch.Tensor) -> torch.Tensor:
     return hit[1]
 
 
-__all__ = ("PACK_MAX_ROWS", "use_packed", "packed_weight", "as_f32")
+def linear(x: torch.Tensor, weight: torch.Tensor, bias=None) -> torch.Tensor:
+    """``F.linear``; a no-grad call of at most ``GEMV_MAX_ROWS`` rows with bf16 activations, weight
+    and bias (the one-token decode step of a bf16 model) reads the weight through ``kdn_gemv``
+    instead of a small-M GEMM."""
+    if (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and (bias is None or bias.dtype == torch.bfloat16) and x.shape[-1] % 128 == 0 and weight.is_contiguous()
+            and x.numel() // max(x.shape[-1], 1) <= GEMV_MAX_ROWS
+            and not torch.is_autocast_enabled("cuda")):
+        from .kdn_ops.step import kdn_gemv
+        return kdn_gemv(x, weight, bias)
+    return F.linear(x, weight, bias)
+
+
+__all__ = ("PACK_MAX_ROWS", "GEMV_MAX_ROWS", "use_packed", "packed_weight", "as_f32", "linear")

@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ._inference import as_f32, packed_weight, use_packed
+from ._inference import as_f32, linear, packed_weight, use_packed
 from .iso_kdn import _SUPPORTED_HEAD_DIMS, decay_parameters, initial_precision_inverse, validate_training_dtype
 from .kdn_ops.diag_kdn_chunk import (_chunk_kalman_as, _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain,
                                      _diag_kdn_normalize)
@@ -143,13 +143,13 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
             w_in = packed_weight(self, "in_proj", (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
                                                    self.f_proj[0].weight, self.omega_proj[0].weight,
                                                    self.g_proj[0].weight))
-            yq, yk, yv, f_hidden, w_hidden, g_hidden = F.linear(hidden_states, w_in).split(
+            yq, yk, yv, f_hidden, w_hidden, g_hidden = linear(hidden_states, w_in).split(
                 (D, D, self.value_dim, d, d, d), dim=-1)
             projections = (yq, yk, yv)
-            retention_raw = self.f_proj[1](f_hidden).view(B, T, H, K)
-            omega_raw = self.omega_proj[1](w_hidden).view(B, T, H, K)
-            r_raw = self.r_proj(hidden_states)  # its bias rounds with the product, as in the layer's GEMM
-            gate = self.g_proj[1](g_hidden)
+            retention_raw = linear(f_hidden, self.f_proj[1].weight).view(B, T, H, K)
+            omega_raw = linear(w_hidden, self.omega_proj[1].weight, self.omega_proj[1].bias).view(B, T, H, K)
+            r_raw = linear(hidden_states, self.r_proj.weight, self.r_proj.bias)  # not packed: its bias rounds with the product
+            gate = linear(g_hidden, self.g_proj[1].weight, self.g_proj[1].bias)
         else:
             projections = (self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states))
             retention_raw = self.f_proj(hidden_states).view(B, T, H, K)
@@ -201,7 +201,7 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
         if gate is None:
             gate = self.g_proj(hidden_states)
         output = self.o_norm(output, gate.view(B, T, H, V))
-        return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
+        return linear(output.reshape(B, T, self.value_dim), self.o_proj.weight), None, new_state
 
 
 __all__ = ("DiagonalKalmanDeltaNetwork", "ShortConvolution")

@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ._inference import as_f32, packed_weight, use_packed
+from ._inference import as_f32, linear, packed_weight, use_packed
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
 from .kdn_ops.short_conv import qkv_causal_conv1d
@@ -188,9 +188,9 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         if use_packed(hidden_states):  # a few rows without autograd: the three input GEMMs as one
             w_in = packed_weight(self, "in_proj", (self.qkv_pack.projection_weight, self.f_omega_r_proj.weight,
                                                    self.g_proj[0].weight))
-            x_lin, packed, g_hidden = F.linear(hidden_states, w_in).split(
+            x_lin, packed, g_hidden = linear(hidden_states, w_in).split(
                 (self.qkv_pack.out_features, self.head_v_dim + 2 * H, self.head_v_dim), dim=-1)
-            gate = self.g_proj[1](g_hidden)
+            gate = linear(g_hidden, self.g_proj[1].weight, self.g_proj[1].bias)
         else:
             x_lin = F.linear(hidden_states, self.qkv_pack.projection_weight)
             packed = self.f_omega_r_proj.forward_packed(hidden_states)
@@ -200,7 +200,7 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         else:
             q, k, v = qkv_causal_conv1d(x_lin.contiguous(), self.qkv_pack.convolution_weight)
         f_hidden, omega_r_raw = packed.split((self.head_v_dim, 2 * H), dim=-1)
-        g_raw = self.f_proj[1](f_hidden)
+        g_raw = linear(f_hidden, self.f_proj[1].weight)
         q, k = q.reshape(B, T, H, K), k.reshape(B, T, H, K)
         v = v.reshape(B, T, H, self.head_v_dim)
         g_raw = g_raw.view(B, T, H, K)
@@ -237,7 +237,7 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         if gate is None:
             gate = self.g_proj(hidden_states)
         output = self.o_norm(output, gate.view(B, T, H, self.head_v_dim))
-        return self.o_proj(output.reshape(B, T, self.value_dim)), None, new_state
+        return linear(output.reshape(B, T, self.value_dim), self.o_proj.weight), None, new_state
 
 
 __all__ = ("IsotropicKalmanDeltaNetwork", "PackedQKV", "PackedLinear")

@@ -39,6 +39,7 @@ _SIGS = {
     "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppis",
     "kdn_mem_step": "pppipipiiiifppis",
     "kdn_kalman_step": "pppipppppppiiiiiffppis",
+    "kdn_gemv": "pilppiiipls",
     "kdn_short_conv_fwd": "pillpiiiiiplls",
     "kdn_short_conv_bwd_workspace_size": "iii",
     "kdn_short_conv_bwd": "pillpiplliiiiipllppzs",

@@ -130,4 +130,34 @@ def kdn_kalman_step(q, k, v, g_cumsum, *, state, precision, omega, r, info_scale
     return o, precision_out
 
 
-__all__ = ("kdn_memory_step", "kdn_kalman_step")
+def kdn_gemv(x, weight, bias=None):
+    """``F.linear(x, weight, bias)`` for at most 8 rows through the weight-streaming ``kdn_gemv``:
+    bf16 ``weight`` [N,K] (K % 128 == 0), bf16 ``bias`` or None, ``x`` [..., K] bf16 or fp32;
+    fp32 accumulation, output in x's dtype."""
+    *lead, K = x.shape
+    N = weight.shape[0]
+    if weight.dtype != torch.bfloat16 or weight.shape != (N, K) or not weight.is_contiguous() or K % 128:
+        raise ValueError("kdn_gemv needs a contiguous bf16 weight [N, K] with K % 128 == 0")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (N,) or not bias.is_contiguous()):
+        raise ValueError("kdn_gemv takes a contiguous bf16 bias [N] or None")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be bf16 or fp32, got {x.dtype}")
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    if M > 8:
+        raise ValueError(f"kdn_gemv takes at most 8 rows, got {M}")
+    # 16-byte aligned rows; a view of one row keeps its parent's stride and offset (contiguous()
+    # returns such a view unchanged), so misaligned inputs are cloned
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (M > 1 and (x2.stride(0) * x2.element_size()) % 16):
+        x2 = x2.clone(memory_format=torch.contiguous_format)
+    row_stride = x2.stride(0) if M > 1 else K
+    _lib.require_device(x2, weight, bias)
+    y = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    if M and N:
+        with torch.cuda.device(x.device):
+            _lib.call("kdn_gemv", _lib.ptr(x2), _lib.is_bf16(x2), row_stride, _lib.ptr(weight), _lib.ptr(bias), M, N, K,
+                      _lib.ptr(y), y.stride(0), _lib.stream_of(x2))
+    return y.view(*lead, N)
+
+
+__all__ = ("kdn_memory_step", "kdn_kalman_step", "kdn_gemv")

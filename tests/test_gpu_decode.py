@@ -1,5 +1,7 @@
 """GPU tests of ``KDNDecoder``: prefill with the chunked scan, then one token per step, eagerly and
-as a replayed HIP graph.
+as a replayed HIP graph; and of ``kdn_gemv``, the decode step's weight-streaming projection
+(against an fp64 product of the same bf16 weight: 1e-5 for fp32 activations, 1e-2 for bf16
+outputs, over 1-8 rows, odd N, K from 128 to 6144, with and without bias, strided rows).
 
 Each graph replay is checked against the eager decoder's step on the same token (the same
 kernels on the same inputs: 1e-5), with the eager decoder's own work and a device
@@ -66,3 +68,28 @@ def test_graph_decoder_matches_eager_and_full_sequence(mixer_type):
         # deeper layers' gate inputs carry the upstream layers' output differences
         _check(f"layer {i} precision state vs prefill of the whole sequence", s.precision, f.precision,
                tol_prec if i == 0 else tol_full)
+
+
+@pytest.mark.parametrize("M,N,K,dtype,has_bias,strided", [
+    (1, 7204, 2304, torch.bfloat16, False, False), (2, 33, 128, torch.float32, True, False),
+    (3, 2304, 6144, torch.bfloat16, True, True), (5, 1, 2304, torch.float32, False, True),
+    (8, 12288, 2304, torch.bfloat16, False, False), (8, 300, 128, torch.float32, True, False),
+    (1, 2304, 128, torch.bfloat16, True, "offset")])
+def test_gemv_matches_fp64(M, N, K, dtype, has_bias, strided):
+    dev = gpu_or_skip()
+    log(f"case gemv M={M} N={N} K={K} {dtype} bias={has_bias} strided={strided}")
+    from lit_gpt.kdn_ops.step import kdn_gemv
+    g = torch.Generator().manual_seed(M * 1000 + N)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).bfloat16()
+    bias = torch.randn(N, generator=g).bfloat16() if has_bias else None
+    x = torch.randn(M, 2 * K if strided else K, generator=g).to(dtype)
+    if strided == "offset":
+        x = x[:, 4:K + 4]  # one row at an 8-byte offset, as a packed projection's split leaves it
+    elif strided:
+        x = x[:, :K]  # rows 2K elements apart
+    ref = x.double() @ W.double().T + (bias.double() if has_bias else 0.0)
+    y = kdn_gemv(x.to(dev), W.to(dev), bias.to(dev) if has_bias else None)
+    torch.cuda.synchronize()
+    assert y.shape == (M, N) and y.dtype == dtype
+    _check("y", y, ref, 1e-5 if dtype == torch.float32 else 1e-2)
+
