@@ -224,11 +224,17 @@ def run_config4(name: str, steps: int, warmup: int, B: int, T: int):
       padded vocabulary.  The KDN-mixer share is one mixer layer's forward at the same shape,
       timed alone, times the layer count, over the model's forward time.
     * training step (reported beside it): fp32 master weights, forward under CUDA bf16 autocast,
-      cross-entropy, backward, fused AdamW; mixer share from one mixer layer's fwd+bwd alone.
+      the fused cross-entropy on the bf16 logits (``FusedCrossEntropyLoss``, as the reference's
+      pretrain.py:1165,1258 applies it), backward, fused AdamW; mixer share from one mixer
+      layer's fwd+bwd alone.
+    * the cross-entropy kernels alone on [B*T, vocab] bf16 logits, each in its own loop, timed
+      with HIP events, with their HBM fraction (forward reads the logits once; backward reads
+      them and writes the gradient).
     """
     import torch
-    import torch.nn.functional as F
 
+    from lit_gpt.fused_cross_entropy import FusedCrossEntropyLoss
+    from lit_gpt.kdn_ops import _lib
     from lit_gpt.model import GPT
 
     dev = torch.device("cuda:0")
@@ -258,11 +264,12 @@ def run_config4(name: str, steps: int, warmup: int, B: int, T: int):
     # training step
     model.train()
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.1, fused=True)
+    loss_fn = FusedCrossEntropyLoss()
 
     def train_step():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             logits = model(idx[:, :-1])
-        loss = F.cross_entropy(logits.float().view(-1, V), idx[:, 1:].reshape(-1))
+        loss = loss_fn(logits, idx[:, 1:])
         loss.backward()
         opt.step()
         opt.zero_grad(set_to_none=True)
@@ -293,13 +300,42 @@ def run_config4(name: str, steps: int, warmup: int, B: int, T: int):
     mixer_fwd_ms = timed(mixer_fwd, steps, warmup)
     del model
     torch.cuda.empty_cache()
+
+    # cross-entropy kernels alone, each in a steady-state loop of its own (forward repeatedly,
+    # then backward into one gradient buffer), so neither pays for another kernel's write-back
+    from lit_gpt.fused_cross_entropy import xent_backward, xent_forward
+    n = B * T
+    logits = torch.randn(n, V, device=dev, dtype=torch.bfloat16).mul_(4)
+    labels = idx[:, 1:].reshape(-1)
+    dlogits = torch.empty_like(logits)
+    dloss = torch.full((n,), 1.0 / n, device=dev)
+    _, lse, _ = xent_forward(logits, labels)
+    reps = max(steps, 10)
+    xent_us = {}
+    for tag, fn in (("xent_fwd", lambda: xent_forward(logits, labels)),
+                    ("xent_bwd", lambda: xent_backward(dloss, logits, lse, labels, dlogits=dlogits))):
+        timed(fn, 2, 2)
+        with _lib.KernelTimer() as kt:
+            for _ in range(reps):
+                fn()
+            xent_us[tag] = kt.mean_ms(tag) * 1e3
+    del logits, dlogits
+    torch.cuda.empty_cache()
+    xent_bytes = {"xent_fwd": n * V * 2 + n * 8 + 3 * n * 4, "xent_bwd": 2 * n * V * 2 + n * 8 + 2 * n * 4}
+    xent_rep = {}
+    for tag, us in xent_us.items():
+        gbs = xent_bytes[tag] / (us * 1e-6) / 1e9
+        xent_rep[tag] = {"us": round(us, 2), "alg_bytes": int(xent_bytes[tag]), "achieved_GBps": round(gbs, 1),
+                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     L = cfg.n_layer
     return {"workload": f"{name} forward, random init (mamba), bf16 weights, synthetic token ids, logits over "
                         f"{V}; training step beside it",
             "B": B, "T": T, "n_layer": L, "value": round(B * T / (fwd_ms * 1e-3), 1), "unit": "tokens/s",
             "ms_per_forward": round(fwd_ms, 3), "mixer_layer_fwd_ms": round(mixer_fwd_ms, 3),
             "mixer_share": round(L * mixer_fwd_ms / fwd_ms, 4),
-            "train_step": {"what": "fwd (bf16 autocast, fp32 master weights) + cross-entropy + bwd + fused AdamW",
+            "cross_entropy_kernels": {"shape": [n, V], "dtype": "bf16", **xent_rep},
+            "train_step": {"what": "fwd (bf16 autocast, fp32 master weights) + fused cross-entropy on the bf16 "
+                                   "logits + bwd + fused AdamW",
                            "value": round(B * T / (train_ms * 1e-3), 1), "unit": "tokens/s",
                            "ms_per_step": round(train_ms, 3), "mixer_layer_fwd_bwd_ms": round(mixer_train_ms, 3),
                            "mixer_share": round(L * mixer_train_ms / train_ms, 4)}}
@@ -318,6 +354,8 @@ def run_decode(name: str, steps: int, warmup: int, prompt: int = 1024):
     from lit_gpt.decode import KDNDecoder
     from lit_gpt.kdn_ops import _lib
     from lit_gpt.kdn_ops.step import kdn_kalman_step, kdn_memory_step
+    from lit_gpt.fused_cross_entropy import FusedCrossEntropyLoss
+    from lit_gpt.kdn_ops import _lib
     from lit_gpt.model import GPT
 
     dev = torch.device("cuda:0")

@@ -181,6 +181,32 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
 int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias, int M, int N,
              int K, void* y, int64_t y_row_stride, hipStream_t stream);
 
+/* ---------------------------------------------------------------- language-model loss */
+/* Fused cross-entropy forward, one row of logits per token.  Replaces cross_entropy_fwd_kernel
+ * (lit_gpt/fused_cross_entropy.py:29-100) as launched by CrossEntropyLoss.forward (:156-260).
+ * logits [n_rows, n_cols] with row stride logits_row_stride elements, logits_dtype 0 f32, 1 bf16,
+ * 2 f16; labels [n_rows] int64 (labels_i64) or int32.  Per row: lse = log sum exp(logit_scale x)
+ * (read from lse when precomputed_lse, which needs smoothing 0 and logit_scale 1); loss = lse -
+ * (1 - smoothing) x_label - smoothing sum(x) / total_classes + lse_square_scale lse^2 (z_loss, the
+ * last term); 0 on rows whose label is ignore_index; a label outside this slice's classes
+ * [class_start_idx, class_start_idx + n_cols) keeps only the smoothing term.  split != 0 is the
+ * vocabulary-split mode: lse is this slice's, the loss leaves out lse and the z-loss, and z_losses
+ * is not written (nullable).  losses, lse, z_losses [n_rows] f32. */
+int kdn_xent_fwd(const void* logits, int logits_dtype, int64_t logits_row_stride, const void* labels, int labels_i64,
+                 int n_rows, int n_cols, float smoothing, float logit_scale, float lse_square_scale,
+                 int64_t ignore_index, int64_t total_classes, int64_t class_start_idx, int split,
+                 int precomputed_lse, float* losses, float* lse, float* z_losses, hipStream_t stream);
+/* Fused cross-entropy backward.  Replaces cross_entropy_bwd_kernel (fused_cross_entropy.py:103-150)
+ * as launched by CrossEntropyLoss.backward (:262-294): dlogits[r, c] = dlosses[r] logit_scale
+ * (p (1 + 2 lse_square_scale lse) - [c == label](1 - smoothing) - smoothing / total_classes),
+ * p = exp(logit_scale x - lse[r]); 0 on ignored rows.  dlogits has logits' dtype and may be logits
+ * itself (in-place backward, same row stride); dlosses [n_rows] f32 with stride dlosses_stride. */
+int kdn_xent_bwd(void* dlogits, int64_t dlogits_row_stride, const float* dlosses, int64_t dlosses_stride,
+                 const void* logits, int logits_dtype, int64_t logits_row_stride, const float* lse,
+                 const void* labels, int labels_i64, int n_rows, int n_cols, float smoothing, float logit_scale,
+                 float lse_square_scale, int64_t ignore_index, int64_t total_classes, int64_t class_start_idx,
+                 hipStream_t stream);
+
 /* ---------------------------------------------------------------- layer frontends */
 /* Depthwise causal short convolution with SiLU, fixed length, width W = 4, no bias:
  * y[b,t,d] = silu(sum_j w[d,j] x[b,t-3+j,d]), x before t = 0 is 0, computed in f32 and rounded to

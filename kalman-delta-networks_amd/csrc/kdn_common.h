@@ -11,12 +11,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---- bf16 <-> fp32 ----------------------------------------------------------
 __device__ __forceinline__ float bf2f(bf16_t u) { return __uint_as_float(((uint32_t)u) << 16); }
-__device__ __forceinline__ bf16_t f2bf(float x) {  // round to nearest even, NaN kept quiet
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
-}
+// round to nearest even (NaN stays NaN): gfx950's v_cvt_pk_bf16_f32, one instruction for two values
+__device__ __forceinline__ bf16_t f2bf(float x) { return __builtin_bit_cast(bf16_t, (__bf16)x); }
 
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i);
 template <> __device__ __forceinline__ float ld<float>(const float* p, int64_t i) { return p[i]; }

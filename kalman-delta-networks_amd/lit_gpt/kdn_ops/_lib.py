@@ -40,6 +40,8 @@ _SIGS = {
     "kdn_mem_step": "pppipipiiiifppis",
     "kdn_kalman_step": "pppipppppppiiiiiffppis",
     "kdn_gemv": "pilppiiipls",
+    "kdn_xent_fwd": "pilpiiifffllliippps",
+    "kdn_xent_bwd": "plplpilppiiifffllls",
     "kdn_short_conv_fwd": "pillpiiiiiplls",
     "kdn_short_conv_bwd_workspace_size": "iii",
     "kdn_short_conv_bwd": "pillpiplliiiiipllppzs",
