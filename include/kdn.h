@@ -176,7 +176,7 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
  * form of the layers' nn.Linear products (the reference runs every projection as a torch GEMM,
  * e.g. iso_kdn.py:277-312, model.py:415-464; this is no port of one).  W [N,K] bf16 row-major,
  * bias [N] bf16 (nullable), fp32 accumulation; x [M,K] bf16 (x_bf16) or f32 with row stride
- * x_row_stride elements, y [M,N] in x's dtype with row stride y_row_stride.  K % 128 == 0; W and
+ * x_row_stride elements, y [M,N] in x's dtype with row stride y_row_stride.  K % 8 == 0; W and
  * the rows of x 16-byte aligned. */
 int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias, int M, int N,
              int K, void* y, int64_t y_row_stride, hipStream_t stream);

@@ -317,24 +317,27 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
 // Decode projections: y[m, n] = sum_k x[m, k] W[n, k] (+ bias[n]) for a few rows m (M <= 8) and a
 // bf16 weight W [N, K] (an nn.Linear weight), fp32 accumulation.  With one token per sequence the
 // product reads every weight element once, so it is bound by the weight stream.  block 256 = 16
-// output rows (4 per wave, 16 lanes per row); a lane reads 16 bytes of its row per 128-column step
-// with 8 steps in flight (the 16 lanes of a row cover 256 contiguous bytes), x through the cache,
-// and the row's partial sums meet in 4 xor shuffles.  K % 128 == 0.
+// output rows (4 per wave, 16 lanes per row), or 8 rows of 32 lanes for outputs narrower than 4096;
+// a lane reads 16 bytes of its row per step with 8 steps in flight (the lanes of a row cover 256 or
+// 512 contiguous bytes), x through the cache, and the row's partial sums meet in xor shuffles.  K % 8 == 0: a lane's 8-column segment past K
+// (the last step of a K that is not a multiple of 128) loads the row's last segment instead and
+// its weights are zeroed, so no load sits under a branch and a lane's loads all issue together.
 // ---------------------------------------------------------------------------------------------
 namespace {
 
-constexpr int kGemvLanes = 16;                 // lanes per output row
-constexpr int kGemvRows = 256 / kGemvLanes;    // output rows per workgroup
-constexpr int kGemvStep = 8 * kGemvLanes;      // columns per step
-constexpr int kGemvInFlight = 8;               // steps whose weight loads are issued together
+constexpr int kGemvInFlight = 8;  // steps whose weight loads are issued together
+// lanes per output row: 16 (16 rows a workgroup), or 32 for narrow outputs (N below
+// kGemvNarrowN), whose 8 rows a workgroup give twice the workgroups for the same N
+constexpr int kGemvNarrowN = 4096;
 
 // MM = the instantiated row capacity; rows m >= M (runtime) are neither read nor written.
-template <int MM, typename TX, typename TY>
+template <int MM, int LANES, typename TX, typename TY>
 __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int64_t xs, const bf16_t* __restrict__ W,
                                                    const bf16_t* __restrict__ bias, int M, int N, int K,
                                                    TY* __restrict__ y, int64_t ys) {
-  const int t = threadIdx.x, j = t % kGemvLanes;
-  const int n = blockIdx.x * kGemvRows + t / kGemvLanes;
+  constexpr int kGemvRows = 256 / LANES, kGemvStep = 8 * LANES;
+  const int t = threadIdx.x, j = t % LANES;
+  const int n = blockIdx.x * kGemvRows + t / LANES;
   const bool live = n < N;
   const bf16_t* wr = W + (int64_t)(live ? n : 0) * K + 8 * j;
   float acc[MM];
@@ -344,18 +347,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
   for (int k0 = 0; k0 < K; k0 += kGemvStep * U) {
     uint4 wv[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      wv[u] = k0 + kGemvStep * u < K ? *reinterpret_cast<const uint4*>(wr + k0 + kGemvStep * u) : uint4{0u, 0u, 0u, 0u};
+    for (int u = 0; u < U; ++u) {
+      const int kk = min(k0 + kGemvStep * u + 8 * j, K - 8);  // clamped into the row
+      wv[u] = *reinterpret_cast<const uint4*>(wr - 8 * j + kk);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kk = k0 + kGemvStep * u + 8 * j;
-      if (k0 + kGemvStep * u >= K) break;
+      if (k0 + kGemvStep * u >= K) break;  // uniform: no lane has columns left
+      const int kk_raw = k0 + kGemvStep * u + 8 * j;
+      const bool in = kk_raw < K;  // K % 8 == 0: the whole segment is inside the row
+      const int kk = in ? kk_raw : K - 8;
       const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
       float wf[8];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        wf[2 * q] = __uint_as_float(ww[q] << 16);
-        wf[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
+        wf[2 * q] = in ? __uint_as_float(ww[q] << 16) : 0.f;
+        wf[2 * q + 1] = in ? __uint_as_float(ww[q] & 0xffff0000u) : 0.f;
       }
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
@@ -382,7 +389,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int o = 1; o < kGemvLanes; o <<= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+    for (int o = 1; o < LANES; o <<= 1) acc[m] += __shfl_xor(acc[m], o, 64);
   if (live && j == 0) {
     const float bb = bias ? bf2f(bias[n]) : 0.f;
 #pragma unroll
@@ -391,25 +398,35 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
   }
 }
 
+template <int MM, int LANES>
+void launch_gemv_l(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
+                   void* y, int64_t ys, hipStream_t stream) {
+  constexpr int rows = 256 / LANES;
+  const dim3 grid((N + rows - 1) / rows), block(256);
+  if (x_bf16)
+    hipLaunchKernelGGL((gemv_kernel<MM, LANES, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias,
+                       M, N, K, (bf16_t*)y, ys);
+  else
+    hipLaunchKernelGGL((gemv_kernel<MM, LANES, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M,
+                       N, K, (float*)y, ys);
+}
+
 template <int MM>
 void launch_gemv(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
                  void* y, int64_t ys, hipStream_t stream) {
-  const dim3 grid((N + kGemvRows - 1) / kGemvRows), block(256);
-  if (x_bf16)
-    hipLaunchKernelGGL((gemv_kernel<MM, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias, M, N,
-                       K, (bf16_t*)y, ys);
+  if (N < kGemvNarrowN)
+    launch_gemv_l<MM, 32>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
   else
-    hipLaunchKernelGGL((gemv_kernel<MM, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M, N, K,
-                       (float*)y, ys);
+    launch_gemv_l<MM, 16>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
 }
 
 }  // namespace
 
 extern "C" int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias,
                         int M, int N, int K, void* y, int64_t y_row_stride, hipStream_t stream) {
-  if (M < 0 || M > 8 || N < 0 || K <= 0 || K % kGemvStep || !W || !x || !y) return KDN_ERR_ARG;
+  if (M < 0 || M > 8 || N < 0 || K <= 0 || K % 8 || !W || !x || !y) return KDN_ERR_ARG;
   if (M == 0 || N == 0) return 0;
-  // 16-byte rows: W rows are K * 2 bytes (K % 128 == 0); x rows 16-byte aligned
+  // 16-byte rows: W rows are K * 2 bytes (K % 8 == 0); x rows 16-byte aligned
   if (!aligned(W, 16) || !aligned(x, 16) || (x_row_stride * (x_bf16 ? 2 : 4)) % 16) return KDN_ERR_ARG;
   if (M == 1) launch_gemv<1>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
   else if (M == 2) launch_gemv<2>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);

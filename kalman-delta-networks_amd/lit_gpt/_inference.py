@@ -55,7 +55,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias=None) -> torch.Tensor:
     and bias (the one-token decode step of a bf16 model) reads the weight through ``kdn_gemv``
     instead of a small-M GEMM."""
     if (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
-            and (bias is None or bias.dtype == torch.bfloat16) and x.shape[-1] % 128 == 0 and weight.is_contiguous()
+            and (bias is None or bias.dtype == torch.bfloat16) and x.shape[-1] % 8 == 0 and weight.is_contiguous()
             and x.numel() // max(x.shape[-1], 1) <= GEMV_MAX_ROWS
             and not torch.is_autocast_enabled("cuda")):
         from .kdn_ops.step import kdn_gemv

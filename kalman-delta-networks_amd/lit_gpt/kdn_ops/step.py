@@ -132,12 +132,12 @@ def kdn_kalman_step(q, k, v, g_cumsum, *, state, precision, omega, r, info_scale
 
 def kdn_gemv(x, weight, bias=None):
     """``F.linear(x, weight, bias)`` for at most 8 rows through the weight-streaming ``kdn_gemv``:
-    bf16 ``weight`` [N,K] (K % 128 == 0), bf16 ``bias`` or None, ``x`` [..., K] bf16 or fp32;
+    bf16 ``weight`` [N,K] (K % 8 == 0), bf16 ``bias`` or None, ``x`` [..., K] bf16 or fp32;
     fp32 accumulation, output in x's dtype."""
     *lead, K = x.shape
     N = weight.shape[0]
-    if weight.dtype != torch.bfloat16 or weight.shape != (N, K) or not weight.is_contiguous() or K % 128:
-        raise ValueError("kdn_gemv needs a contiguous bf16 weight [N, K] with K % 128 == 0")
+    if weight.dtype != torch.bfloat16 or weight.shape != (N, K) or not weight.is_contiguous() or K % 8:
+        raise ValueError("kdn_gemv needs a contiguous bf16 weight [N, K] with K % 8 == 0")
     if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (N,) or not bias.is_contiguous()):
         raise ValueError("kdn_gemv takes a contiguous bf16 bias [N] or None")
     if x.dtype not in (torch.bfloat16, torch.float32):

@@ -74,7 +74,9 @@ def test_graph_decoder_matches_eager_and_full_sequence(mixer_type):
     (1, 7204, 2304, torch.bfloat16, False, False), (2, 33, 128, torch.float32, True, False),
     (3, 2304, 6144, torch.bfloat16, True, True), (5, 1, 2304, torch.float32, False, True),
     (8, 12288, 2304, torch.bfloat16, False, False), (8, 300, 128, torch.float32, True, False),
-    (1, 2304, 128, torch.bfloat16, True, "offset")])
+    (1, 2304, 128, torch.bfloat16, True, "offset"), (1, 2304, 7208, torch.bfloat16, False, False),
+    (4, 2304, 40, torch.bfloat16, True, False), (2, 17, 8, torch.float32, False, True),
+    (7, 513, 1160, torch.float32, True, False)])
 def test_gemv_matches_fp64(M, N, K, dtype, has_bias, strided):
     dev = gpu_or_skip()
     log(f"case gemv M={M} N={N} K={K} {dtype} bias={has_bias} strided={strided}")
