@@ -414,12 +414,10 @@ void launch_gemv_l(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const
 template <int MM>
 void launch_gemv(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
                  void* y, int64_t ys, hipStream_t stream) {
-  if (N < kGemvNarrowN)
+  if (N < 20000)
     launch_gemv_l<MM, 64>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
-  else if (N < 20000)
-    launch_gemv_l<MM, 32>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
   else
-    launch_gemv_l<MM, 16>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
+    launch_gemv_l<MM, 32>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
 }
 
 }  // namespace
