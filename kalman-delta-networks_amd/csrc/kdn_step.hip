@@ -316,28 +316,28 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
 // ---------------------------------------------------------------------------------------------
 // Decode projections: y[m, n] = sum_k x[m, k] W[n, k] (+ bias[n]) for a few rows m (M <= 8) and a
 // bf16 weight W [N, K] (an nn.Linear weight), fp32 accumulation.  With one token per sequence the
-// product reads every weight element once, so it is bound by the weight stream.  block 256 = 16
-// output rows (4 per wave, 16 lanes per row), or 8 rows of 32 lanes for outputs narrower than 4096;
-// a lane reads 16 bytes of its row per step with 8 steps in flight (the lanes of a row cover 256 or
-// 512 contiguous bytes), x through the cache, and the row's partial sums meet in xor shuffles.  K % 8 == 0: a lane's 8-column segment past K
-// (the last step of a K that is not a multiple of 128) loads the row's last segment instead and
-// its weights are zeroed, so no load sits under a branch and a lane's loads all issue together.
+// product reads every weight element once, so it is bound by the weight stream.  One wave per
+// output row, 4 rows a workgroup (N / 4 workgroups: 576 at N = 2304, so even the narrow
+// projections fill the chip; 16 lanes per row gave a quarter of that and 20% slower decode steps).
+// A lane reads 16 bytes of its row per 512-column step with 8 steps in flight (a wave covers 1 KiB
+// contiguous per step), x through the cache, and the row's sum meets in 6 xor shuffles.
+// K % 8 == 0: a lane's 8-column segment past K (the last step of a K that is not a multiple of
+// 512) loads the row's last segment instead and its weights are zeroed, so no load sits under a
+// branch and a lane's loads all issue together.
 // ---------------------------------------------------------------------------------------------
 namespace {
 
 constexpr int kGemvInFlight = 8;  // steps whose weight loads are issued together
-// lanes per output row: 16 (16 rows a workgroup), or 32 for narrow outputs (N below
-// kGemvNarrowN), whose 8 rows a workgroup give twice the workgroups for the same N
-constexpr int kGemvNarrowN = 4096;
+constexpr int kGemvLanes = 64;    // lanes per output row
 
 // MM = the instantiated row capacity; rows m >= M (runtime) are neither read nor written.
-template <int MM, int LANES, typename TX, typename TY>
+template <int MM, typename TX, typename TY>
 __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int64_t xs, const bf16_t* __restrict__ W,
                                                    const bf16_t* __restrict__ bias, int M, int N, int K,
                                                    TY* __restrict__ y, int64_t ys) {
-  constexpr int kGemvRows = 256 / LANES, kGemvStep = 8 * LANES;
-  const int t = threadIdx.x, j = t % LANES;
-  const int n = blockIdx.x * kGemvRows + t / LANES;
+  constexpr int kGemvRows = 256 / kGemvLanes, kGemvStep = 8 * kGemvLanes;
+  const int t = threadIdx.x, j = t % kGemvLanes;
+  const int n = blockIdx.x * kGemvRows + t / kGemvLanes;
   const bool live = n < N;
   const bf16_t* wr = W + (int64_t)(live ? n : 0) * K + 8 * j;
   float acc[MM];
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int o = 1; o < LANES; o <<= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+    for (int o = 1; o < kGemvLanes; o <<= 1) acc[m] += __shfl_xor(acc[m], o, 64);
   if (live && j == 0) {
     const float bb = bias ? bf2f(bias[n]) : 0.f;
 #pragma unroll
@@ -398,26 +398,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
   }
 }
 
-template <int MM, int LANES>
-void launch_gemv_l(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
-                   void* y, int64_t ys, hipStream_t stream) {
-  constexpr int rows = 256 / LANES;
-  const dim3 grid((N + rows - 1) / rows), block(256);
-  if (x_bf16)
-    hipLaunchKernelGGL((gemv_kernel<MM, LANES, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias,
-                       M, N, K, (bf16_t*)y, ys);
-  else
-    hipLaunchKernelGGL((gemv_kernel<MM, LANES, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M,
-                       N, K, (float*)y, ys);
-}
-
 template <int MM>
 void launch_gemv(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
                  void* y, int64_t ys, hipStream_t stream) {
-  if (N < 20000)
-    launch_gemv_l<MM, 64>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
+  constexpr int rows = 256 / kGemvLanes;
+  const dim3 grid((N + rows - 1) / rows), block(256);
+  if (x_bf16)
+    hipLaunchKernelGGL((gemv_kernel<MM, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias, M, N,
+                       K, (bf16_t*)y, ys);
   else
-    launch_gemv_l<MM, 32>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
+    hipLaunchKernelGGL((gemv_kernel<MM, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M, N, K,
+                       (float*)y, ys);
 }
 
 }  // namespace
