@@ -177,9 +177,10 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
  * e.g. iso_kdn.py:277-312, model.py:415-464; this is no port of one).  W [N,K] bf16 row-major,
  * bias [N] bf16 (nullable), fp32 accumulation; x [M,K] bf16 (x_bf16) or f32 with row stride
  * x_row_stride elements, y [M,N] in x's dtype with row stride y_row_stride.  K % 8 == 0; W and
- * the rows of x 16-byte aligned. */
+ * the rows of x 16-byte aligned.  gated != 0 fuses the SwiGLU gate of model.py:467-470 (the packed
+ * decode form): W [2N,K] = [w1; w2], bias [2N], y[m, n] = silu(w1 x + b1)[n] * (w2 x + b2)[n]. */
 int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias, int M, int N,
-             int K, void* y, int64_t y_row_stride, hipStream_t stream);
+             int K, int gated, void* y, int64_t y_row_stride, hipStream_t stream);
 
 /* ---------------------------------------------------------------- language-model loss */
 /* Fused cross-entropy forward, one row of logits per token.  Replaces cross_entropy_fwd_kernel

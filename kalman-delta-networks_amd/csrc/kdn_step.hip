@@ -323,7 +323,8 @@ int kdn_kalman_step(const void* q, const void* k, const void* v, int qkv_bf16, c
 // contiguous per step), x through the cache, and the row's sum meets in 6 xor shuffles.
 // K % 8 == 0: a lane's 8-column segment past K (the last step of a K that is not a multiple of
 // 512) loads the row's last segment instead and its weights are zeroed, so no load sits under a
-// branch and a lane's loads all issue together.
+// branch and a lane's loads all issue together.  gated != 0 is the fused SwiGLU gate over a
+// packed [w1; w2] weight (below).
 // ---------------------------------------------------------------------------------------------
 namespace {
 
@@ -331,7 +332,9 @@ constexpr int kGemvInFlight = 8;  // steps whose weight loads are issued togethe
 constexpr int kGemvLanes = 64;    // lanes per output row
 
 // MM = the instantiated row capacity; rows m >= M (runtime) are neither read nor written.
-template <int MM, typename TX, typename TY>
+// GATED: W holds 2N rows [W1; W2] (and bias 2N entries); the wave of output n also reads row N + n
+// and writes silu(W1 x + b1) * (W2 x + b2), the SwiGLU gate, in fp32 before the one rounding.
+template <int MM, bool GATED, typename TX, typename TY>
 __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int64_t xs, const bf16_t* __restrict__ W,
                                                    const bf16_t* __restrict__ bias, int M, int N, int K,
                                                    TY* __restrict__ y, int64_t ys) {
@@ -340,16 +343,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
   const int n = blockIdx.x * kGemvRows + t / kGemvLanes;
   const bool live = n < N;
   const bf16_t* wr = W + (int64_t)(live ? n : 0) * K + 8 * j;
-  float acc[MM];
+  const bf16_t* wr2 = wr + (int64_t)N * K;  // GATED: row N + n
+  float acc[MM], acc2[MM];
 #pragma unroll
-  for (int m = 0; m < MM; ++m) acc[m] = 0.f;
+  for (int m = 0; m < MM; ++m) acc[m] = 0.f, acc2[m] = 0.f;
   constexpr int U = kGemvInFlight;
   for (int k0 = 0; k0 < K; k0 += kGemvStep * U) {
-    uint4 wv[U];
+    uint4 wv[U], wv2[GATED ? U : 1];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = min(k0 + kGemvStep * u + 8 * j, K - 8);  // clamped into the row
       wv[u] = *reinterpret_cast<const uint4*>(wr - 8 * j + kk);
+      if constexpr (GATED) wv2[u] = *reinterpret_cast<const uint4*>(wr2 - 8 * j + kk);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -358,11 +363,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
       const bool in = kk_raw < K;  // K % 8 == 0: the whole segment is inside the row
       const int kk = in ? kk_raw : K - 8;
       const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-      float wf[8];
+      float wf[8], wf2[8];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         wf[2 * q] = in ? __uint_as_float(ww[q] << 16) : 0.f;
         wf[2 * q + 1] = in ? __uint_as_float(ww[q] & 0xffff0000u) : 0.f;
+      }
+      if constexpr (GATED) {
+        const uint32_t w2[4] = {wv2[u].x, wv2[u].y, wv2[u].z, wv2[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          wf2[2 * q] = in ? __uint_as_float(w2[q] << 16) : 0.f;
+          wf2[2 * q + 1] = in ? __uint_as_float(w2[q] & 0xffff0000u) : 0.f;
+        }
       }
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
@@ -382,47 +395,65 @@ __global__ __launch_bounds__(256) void gemv_kernel(const TX* __restrict__ x, int
           xf[0] = a.x, xf[1] = a.y, xf[2] = a.z, xf[3] = a.w, xf[4] = b.x, xf[5] = b.y, xf[6] = b.z, xf[7] = b.w;
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[m] = fmaf(wf[e], xf[e], acc[m]);
+        for (int e = 0; e < 8; ++e) {
+          acc[m] = fmaf(wf[e], xf[e], acc[m]);
+          if constexpr (GATED) acc2[m] = fmaf(wf2[e], xf[e], acc2[m]);
+        }
       }
     }
   }
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
-    for (int o = 1; o < kGemvLanes; o <<= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+    for (int o = 1; o < kGemvLanes; o <<= 1) {
+      acc[m] += __shfl_xor(acc[m], o, 64);
+      if constexpr (GATED) acc2[m] += __shfl_xor(acc2[m], o, 64);
+    }
   if (live && j == 0) {
     const float bb = bias ? bf2f(bias[n]) : 0.f;
+    const float bb2 = (GATED && bias) ? bf2f(bias[N + n]) : 0.f;
 #pragma unroll
     for (int m = 0; m < MM; ++m)
-      if (m < M) st(y, m * ys + n, acc[m] + bb);
+      if (m < M) {
+        const float v = acc[m] + bb;
+        // silu(v) = v / (1 + e^-v); e^-v = inf for very negative v gives -0
+        st(y, m * ys + n, GATED ? v / (1.f + __expf(-v)) * (acc2[m] + bb2) : v);
+      }
   }
+}
+
+template <int MM, bool GATED>
+void launch_gemv_g(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
+                   void* y, int64_t ys, hipStream_t stream) {
+  constexpr int rows = 256 / kGemvLanes;
+  const dim3 grid((N + rows - 1) / rows), block(256);
+  if (x_bf16)
+    hipLaunchKernelGGL((gemv_kernel<MM, GATED, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias,
+                       M, N, K, (bf16_t*)y, ys);
+  else
+    hipLaunchKernelGGL((gemv_kernel<MM, GATED, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M,
+                       N, K, (float*)y, ys);
 }
 
 template <int MM>
 void launch_gemv(const void* x, int x_bf16, int64_t xs, const bf16_t* W, const bf16_t* bias, int M, int N, int K,
-                 void* y, int64_t ys, hipStream_t stream) {
-  constexpr int rows = 256 / kGemvLanes;
-  const dim3 grid((N + rows - 1) / rows), block(256);
-  if (x_bf16)
-    hipLaunchKernelGGL((gemv_kernel<MM, bf16_t, bf16_t>), grid, block, 0, stream, (const bf16_t*)x, xs, W, bias, M, N,
-                       K, (bf16_t*)y, ys);
-  else
-    hipLaunchKernelGGL((gemv_kernel<MM, float, float>), grid, block, 0, stream, (const float*)x, xs, W, bias, M, N, K,
-                       (float*)y, ys);
+                 int gated, void* y, int64_t ys, hipStream_t stream) {
+  if (gated) launch_gemv_g<MM, true>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
+  else launch_gemv_g<MM, false>(x, x_bf16, xs, W, bias, M, N, K, y, ys, stream);
 }
 
 }  // namespace
 
 extern "C" int kdn_gemv(const void* x, int x_bf16, int64_t x_row_stride, const uint16_t* W, const uint16_t* bias,
-                        int M, int N, int K, void* y, int64_t y_row_stride, hipStream_t stream) {
+                        int M, int N, int K, int gated, void* y, int64_t y_row_stride, hipStream_t stream) {
   if (M < 0 || M > 8 || N < 0 || K <= 0 || K % 8 || !W || !x || !y) return KDN_ERR_ARG;
   if (M == 0 || N == 0) return 0;
   // 16-byte rows: W rows are K * 2 bytes (K % 8 == 0); x rows 16-byte aligned
   if (!aligned(W, 16) || !aligned(x, 16) || (x_row_stride * (x_bf16 ? 2 : 4)) % 16) return KDN_ERR_ARG;
-  if (M == 1) launch_gemv<1>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
-  else if (M == 2) launch_gemv<2>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
-  else if (M <= 4) launch_gemv<4>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
-  else launch_gemv<8>(x, x_bf16, x_row_stride, W, bias, M, N, K, y, y_row_stride, stream);
+  if (M == 1) launch_gemv<1>(x, x_bf16, x_row_stride, W, bias, M, N, K, gated, y, y_row_stride, stream);
+  else if (M == 2) launch_gemv<2>(x, x_bf16, x_row_stride, W, bias, M, N, K, gated, y, y_row_stride, stream);
+  else if (M <= 4) launch_gemv<4>(x, x_bf16, x_row_stride, W, bias, M, N, K, gated, y, y_row_stride, stream);
+  else launch_gemv<8>(x, x_bf16, x_row_stride, W, bias, M, N, K, gated, y, y_row_stride, stream);
   KDN_CHECK_LAUNCH();
   return 0;
 }

@@ -50,17 +50,31 @@ def as_f32(owner, name: str, t: torch.Tensor) -> torch.Tensor:
     return hit[1]
 
 
+def _gemv_ok(x, weight, bias) -> bool:
+    return (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
+            and (bias is None or bias.dtype == torch.bfloat16) and x.shape[-1] % 8 == 0 and weight.is_contiguous()
+            and x.numel() // max(x.shape[-1], 1) <= GEMV_MAX_ROWS
+            and not torch.is_autocast_enabled("cuda"))
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias=None) -> torch.Tensor:
     """``F.linear``; a no-grad call of at most ``GEMV_MAX_ROWS`` rows with bf16 activations, weight
     and bias (the one-token decode step of a bf16 model) reads the weight through ``kdn_gemv``
     instead of a small-M GEMM."""
-    if (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16
-            and (bias is None or bias.dtype == torch.bfloat16) and x.shape[-1] % 8 == 0 and weight.is_contiguous()
-            and x.numel() // max(x.shape[-1], 1) <= GEMV_MAX_ROWS
-            and not torch.is_autocast_enabled("cuda")):
+    if _gemv_ok(x, weight, bias):
         from .kdn_ops.step import kdn_gemv
         return kdn_gemv(x, weight, bias)
     return F.linear(x, weight, bias)
 
 
-__all__ = ("PACK_MAX_ROWS", "GEMV_MAX_ROWS", "use_packed", "packed_weight", "as_f32", "linear")
+def swiglu_gate(x: torch.Tensor, w12: torch.Tensor) -> torch.Tensor:
+    """silu(x w1^T) * (x w2^T) for a packed ``w12`` = [w1; w2]; in the decode regime of ``linear``
+    one ``kdn_gemv`` launch computes both products and the gate."""
+    if _gemv_ok(x, w12, None) and w12.shape[0] % 2 == 0:
+        from .kdn_ops.step import kdn_gemv
+        return kdn_gemv(x, w12, None, gated=True)
+    h1, h2 = linear(x, w12).chunk(2, dim=-1)
+    return F.silu(h1) * h2
+
+
+__all__ = ("PACK_MAX_ROWS", "GEMV_MAX_ROWS", "use_packed", "packed_weight", "as_f32", "linear", "swiglu_gate")

@@ -39,7 +39,7 @@ _SIGS = {
     "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppis",
     "kdn_mem_step": "pppipipiiiifppis",
     "kdn_kalman_step": "pppipppppppiiiiiffppis",
-    "kdn_gemv": "pilppiiipls",
+    "kdn_gemv": "pilppiiiipls",
     "kdn_xent_fwd": "pilpiiifffllliippps",
     "kdn_xent_bwd": "plplpilppiiifffllls",
     "kdn_short_conv_fwd": "pillpiiiiiplls",

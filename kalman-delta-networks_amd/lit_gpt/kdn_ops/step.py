@@ -130,16 +130,20 @@ def kdn_kalman_step(q, k, v, g_cumsum, *, state, precision, omega, r, info_scale
     return o, precision_out
 
 
-def kdn_gemv(x, weight, bias=None):
+def kdn_gemv(x, weight, bias=None, *, gated=False):
     """``F.linear(x, weight, bias)`` for at most 8 rows through the weight-streaming ``kdn_gemv``:
     bf16 ``weight`` [N,K] (K % 8 == 0), bf16 ``bias`` or None, ``x`` [..., K] bf16 or fp32;
-    fp32 accumulation, output in x's dtype."""
+    fp32 accumulation, output in x's dtype.  ``gated=True`` takes a packed ``weight`` [2N,K] =
+    [w1; w2] (bias [2N]) and returns the SwiGLU gate silu(x w1^T + b1) * (x w2^T + b2), [..., N]."""
     *lead, K = x.shape
-    N = weight.shape[0]
-    if weight.dtype != torch.bfloat16 or weight.shape != (N, K) or not weight.is_contiguous() or K % 8:
+    R = weight.shape[0]
+    if weight.dtype != torch.bfloat16 or weight.shape != (R, K) or not weight.is_contiguous() or K % 8:
         raise ValueError("kdn_gemv needs a contiguous bf16 weight [N, K] with K % 8 == 0")
-    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (N,) or not bias.is_contiguous()):
-        raise ValueError("kdn_gemv takes a contiguous bf16 bias [N] or None")
+    if gated and R % 2:
+        raise ValueError(f"a gated kdn_gemv takes a packed [2N, K] weight, got {R} rows")
+    N = R // 2 if gated else R
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.shape != (R,) or not bias.is_contiguous()):
+        raise ValueError(f"kdn_gemv takes a contiguous bf16 bias [{R}] or None")
     if x.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"x must be bf16 or fp32, got {x.dtype}")
     x2 = x.reshape(-1, K)
@@ -156,7 +160,7 @@ def kdn_gemv(x, weight, bias=None):
     if M and N:
         with torch.cuda.device(x.device):
             _lib.call("kdn_gemv", _lib.ptr(x2), _lib.is_bf16(x2), row_stride, _lib.ptr(weight), _lib.ptr(bias), M, N, K,
-                      _lib.ptr(y), y.stride(0), _lib.stream_of(x2))
+                      int(bool(gated)), _lib.ptr(y), y.stride(0), _lib.stream_of(x2))
     return y.view(*lead, N)
 
 

@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ._inference import linear, packed_weight, use_packed
+from ._inference import linear, packed_weight, swiglu_gate, use_packed
 from .config import Config
 
 
@@ -176,8 +176,8 @@ class SwiGLU(nn.Module):
 
     def forward(self, x):
         if self.w1.bias is None and self.w2.bias is None and use_packed(x):  # decode: w1 | w2 as one GEMM
-            h1, h2 = linear(x, packed_weight(self, "w12", (self.w1.weight, self.w2.weight))).chunk(2, dim=-1)
-            return linear(F.silu(h1) * h2, self.w3.weight, self.w3.bias)
+            h = swiglu_gate(x, packed_weight(self, "w12", (self.w1.weight, self.w2.weight)))
+            return linear(h, self.w3.weight, self.w3.bias)
         return self.w3(F.silu(self.w1(x)) * self.w2(x))
 
 

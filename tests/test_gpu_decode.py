@@ -95,3 +95,23 @@ def test_gemv_matches_fp64(M, N, K, dtype, has_bias, strided):
     assert y.shape == (M, N) and y.dtype == dtype
     _check("y", y, ref, 1e-5 if dtype == torch.float32 else 1e-2)
 
+
+
+@pytest.mark.parametrize("M,N,K,dtype,has_bias", [
+    (1, 7208, 2304, torch.bfloat16, False), (3, 100, 200, torch.bfloat16, True), (8, 513, 1160, torch.float32, True),
+    (2, 2304, 128, torch.float32, False)])
+def test_gated_gemv_is_swiglu_gate(M, N, K, dtype, has_bias):
+    # the fused SwiGLU gate over a packed [w1; w2] weight against fp64 silu(x w1^T + b1) * (x w2^T + b2)
+    dev = gpu_or_skip()
+    log(f"case gated gemv M={M} N={N} K={K} {dtype} bias={has_bias}")
+    from lit_gpt.kdn_ops.step import kdn_gemv
+    g = torch.Generator().manual_seed(M * 7 + N)
+    W = (torch.randn(2 * N, K, generator=g) / K ** 0.5).bfloat16()
+    bias = torch.randn(2 * N, generator=g).bfloat16() if has_bias else None
+    x = torch.randn(M, K, generator=g).to(dtype)
+    h = x.double() @ W.double().T + (bias.double() if has_bias else 0.0)
+    ref = torch.nn.functional.silu(h[:, :N]) * h[:, N:]
+    y = kdn_gemv(x.to(dev), W.to(dev), bias.to(dev) if has_bias else None, gated=True)
+    torch.cuda.synchronize()
+    assert y.shape == (M, N) and y.dtype == dtype
+    _check("y", y, ref, 1e-5 if dtype == torch.float32 else 1e-2)
