@@ -219,6 +219,14 @@ int kdn_xent_bwd(void* dlogits, int64_t dlogits_row_stride, const float* dlosses
 int kdn_short_conv_fwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_stride_t, const void* weight,
                        int w_bf16, int B, int T, int D, int W, void* y, int64_t y_stride_b, int64_t y_stride_t,
                        hipStream_t stream);
+/* One token of the short convolution from carried inputs (decoding; no reference counterpart: the
+ * reference refuses caching, model.py:104,184).  x [B,1,D] with batch stride x_stride_b, tail [B,3,D]
+ * (the 3 earlier inputs, x's dtype, row stride D, batch stride tail_stride_b), y [B,1,D]:
+ * y = silu(sum_j w[d,j] [tail_0, tail_1, tail_2, x]_j), equal to kdn_short_conv_fwd over the 4 rows;
+ * then the tail is advanced in place to [tail_1, tail_2, x].  x, tail, y, weight 16-byte aligned. */
+int kdn_short_conv_step(const void* x, int x_bf16, int64_t x_stride_b, void* tail, int64_t tail_stride_b,
+                        const void* weight, int w_bf16, int B, int D, void* y, int64_t y_stride_b,
+                        hipStream_t stream);
 /* Workspace of kdn_short_conv_bwd when dweight is requested: f32 partials per (b, 64-token block). */
 size_t kdn_short_conv_bwd_workspace_size(int B, int T, int D);
 /* Backward (iso_kdn_chunk.py:127-254, 379-437): g = dy * silu'(y) with the preactivation y recomputed

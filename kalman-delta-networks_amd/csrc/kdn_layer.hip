@@ -133,6 +133,42 @@ __global__ __launch_bounds__(256) void short_conv_fwd_kernel(const TX* __restric
 }
 
 // ---------------------------------------------------------------------------
+// One token of the short convolution with its carried inputs (decoding): thread = (b, 8 channels).
+// y = silu(w_0 s_0 + w_1 s_1 + w_2 s_2 + w_3 x) with s the 3 earlier inputs (tail [B,3,D], x's
+// dtype), summed in the order of short_conv_fwd_kernel, so it equals that kernel run over
+// [s, x]; then the tail shifts in place to [s_1, s_2, x].  Each thread reads its own channels'
+// tail before writing them.
+// ---------------------------------------------------------------------------
+template <typename TX, typename TW>
+__global__ __launch_bounds__(256) void short_conv_step_kernel(const TX* __restrict__ x, int64_t xsb,
+                                                              TX* __restrict__ tail, int64_t tsb,
+                                                              const TW* __restrict__ w, int B, int D,
+                                                              TX* __restrict__ y, int64_t ysb) {
+  const int CG = D / 8;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (int64_t)B * CG) return;
+  const int cg = (int)(gid % CG), b = (int)(gid / CG), d0 = 8 * cg;
+  float wt[8][kConvW];
+  ld_taps(w + (int64_t)d0 * kConvW, wt);
+  float xr[kConvW][8];
+  TX* tb = tail + (int64_t)b * tsb + d0;
+#pragma unroll
+  for (int r = 0; r < kConvW - 1; ++r) ld8v(tb + (int64_t)r * D, xr[r]);
+  ld8v(x + (int64_t)b * xsb + d0, xr[kConvW - 1]);
+  float o[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < kConvW; ++j) a += wt[c][j] * xr[j][c];
+    o[c] = a * sigmoidf(a);
+  }
+  st8v(y + (int64_t)b * ysb + d0, o);
+#pragma unroll
+  for (int r = 0; r < kConvW - 1; ++r) st8v(tb + (int64_t)r * D, xr[r + 1]);  // exact: values of TX
+}
+
+// ---------------------------------------------------------------------------
 // Short convolution backward.  Block = 32 channel groups x 8 runs of 8 tokens (one 64-token
 // block of 256 channels); thread = (run, channel group), all its loads issued at once.
 // g_t = dy_t silu'(y_t) with y the recomputed preactivation (rounded to x's dtype when round_y,
@@ -464,6 +500,28 @@ int kdn_short_conv_fwd(const void* x, int x_bf16, int64_t x_stride_b, int64_t x_
   else if (w_bf16) KDN_CONV_FWD(float, bf16_t);
   else KDN_CONV_FWD(float, float);
 #undef KDN_CONV_FWD
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_short_conv_step(const void* x, int x_bf16, int64_t x_stride_b, void* tail, int64_t tail_stride_b,
+                        const void* weight, int w_bf16, int B, int D, void* y, int64_t y_stride_b,
+                        hipStream_t stream) {
+  if (B < 0 || D <= 0 || D % 8 != 0 || !x || !tail || !weight || !y) return KDN_ERR_ARG;
+  if (!al16(x) || !al16(y) || !al16(tail) || !al16(weight) || x_stride_b % 8 != 0 || y_stride_b % 8 != 0 ||
+      tail_stride_b % 8 != 0 || tail_stride_b < (int64_t)(kConvW - 1) * D)
+    return KDN_ERR_ARG;
+  if (B == 0) return 0;
+  const int64_t threads = (int64_t)B * (D / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+#define KDN_CONV_STEP(TX, TW)                                                                                        \
+  hipLaunchKernelGGL((short_conv_step_kernel<TX, TW>), grid, dim3(256), 0, stream, (const TX*)x, x_stride_b,        \
+                     (TX*)tail, tail_stride_b, (const TW*)weight, B, D, (TX*)y, y_stride_b)
+  if (x_bf16 && w_bf16) KDN_CONV_STEP(bf16_t, bf16_t);
+  else if (x_bf16) KDN_CONV_STEP(bf16_t, float);
+  else if (w_bf16) KDN_CONV_STEP(float, bf16_t);
+  else KDN_CONV_STEP(float, float);
+#undef KDN_CONV_STEP
   KDN_CHECK_LAUNCH();
   return 0;
 }

@@ -22,7 +22,7 @@ from torch import nn
 from ._inference import as_f32, linear, packed_weight, use_packed
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
-from .kdn_ops.short_conv import qkv_causal_conv1d
+from .kdn_ops.short_conv import qkv_causal_conv1d, short_conv_step
 from .kdn_ops.step import kdn_kalman_step
 from .kdn_state import CONV_TAIL, carry_state, check_state, conv_input_with_tail
 
@@ -194,9 +194,18 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         else:
             x_lin = F.linear(hidden_states, self.qkv_pack.projection_weight)
             packed = self.f_omega_r_proj.forward_packed(hidden_states)
-        if stateful:
+        cw = self.qkv_pack.convolution_weight
+        if (stateful and T == 1 and state is not None and state.inplace and not torch.is_grad_enabled()
+                and state.conv[0].dtype == x_lin.dtype and x_lin.data_ptr() % 16 == 0 and x_lin.stride(0) % 8 == 0
+                and x_lin.stride(-1) == 1 and cw.is_contiguous()):
+            # decode step: one launch convolves the token with the carried inputs and advances them
+            y = short_conv_step(x_lin, state.conv[0], cw)
+            d = y.shape[-1] // 3
+            q, k, v = y[..., :d], y[..., d:2 * d], y[..., 2 * d:]
+            conv_tail = state.conv[0]
+        elif stateful:
             x_proj, conv_tail = conv_input_with_tail(x_lin, state.conv[0] if state is not None else None)
-            q, k, v = (t[:, CONV_TAIL:] for t in qkv_causal_conv1d(x_proj, self.qkv_pack.convolution_weight))
+            q, k, v = (t[:, CONV_TAIL:] for t in qkv_causal_conv1d(x_proj, cw))
         else:
             q, k, v = qkv_causal_conv1d(x_lin.contiguous(), self.qkv_pack.convolution_weight)
         f_hidden, omega_r_raw = packed.split((self.head_v_dim, 2 * H), dim=-1)

@@ -43,6 +43,7 @@ _SIGS = {
     "kdn_xent_fwd": "pilpiiifffllliippps",
     "kdn_xent_bwd": "plplpilppiiifffllls",
     "kdn_short_conv_fwd": "pillpiiiiiplls",
+    "kdn_short_conv_step": "pilplpiiipls",
     "kdn_short_conv_bwd_workspace_size": "iii",
     "kdn_short_conv_bwd": "pillpiplliiiiipllppzs",
     "kdn_rms_norm_fwd": "pipilifpps",

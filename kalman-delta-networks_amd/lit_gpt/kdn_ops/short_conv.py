@@ -195,4 +195,24 @@ def qkv_causal_conv1d(x: torch.Tensor, weight: torch.Tensor):
     return _QKVCausalConv1d.apply(x, weight)
 
 
-__all__ = ("causal_conv1d", "qkv_causal_conv1d", "GROUPS", "KERNEL_WIDTH")
+def short_conv_step(x: torch.Tensor, tail: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """One token of the SiLU short convolution from its 3 carried inputs (decoding, no autograd):
+    x [B,1,D] (unit channel stride, batch stride a multiple of 8), ``tail`` [B,3,D] contiguous in x's
+    dtype, ``weight`` [D,4] contiguous.  Returns y [B,1,D], equal to the convolution of [tail, x]
+    at its last token, and advances ``tail`` in place to its last 2 rows and x (``kdn_short_conv_step``)."""
+    if x.ndim != 3 or x.shape[1] != 1 or x.stride(-1) != 1:
+        raise ValueError(f"x must be [B,1,D] with unit channel stride, got {tuple(x.shape)}")
+    B, _, D = x.shape
+    if tail.shape != (B, KERNEL_WIDTH - 1, D) or tail.dtype != x.dtype or not tail.is_contiguous():
+        raise ValueError(f"tail must be a contiguous {x.dtype} tensor of shape {(B, KERNEL_WIDTH - 1, D)}")
+    if weight.shape != (D, KERNEL_WIDTH) or not weight.is_contiguous():
+        raise ValueError(f"weight must be a contiguous [{D},{KERNEL_WIDTH}] tensor")
+    _lib.require_device(x, tail, weight)
+    y = torch.empty((B, 1, D), device=x.device, dtype=x.dtype)
+    with torch.cuda.device(x.device):
+        _lib.call("kdn_short_conv_step", _lib.ptr(x), _lib.is_bf16(x), x.stride(0), _lib.ptr(tail), tail.stride(0),
+                  _lib.ptr(weight), _lib.is_bf16(weight), B, D, _lib.ptr(y), y.stride(0), _lib.stream_of(x))
+    return y
+
+
+__all__ = ("causal_conv1d", "qkv_causal_conv1d", "short_conv_step", "GROUPS", "KERNEL_WIDTH")

@@ -58,7 +58,8 @@ def carry_state(state, conv, memory, precision, T: int):
         if torch.is_grad_enabled():
             raise RuntimeError("in-place KDN layer states are for inference; run under torch.no_grad()")
         for c, n in zip(state.conv, conv):
-            c.copy_(n)
+            if n is not c:  # a single-token step may already have advanced the buffer itself
+                c.copy_(n)
         if memory is not state.memory:
             state.memory.copy_(memory)
         if precision is not state.precision:

@@ -115,3 +115,24 @@ def test_gated_gemv_is_swiglu_gate(M, N, K, dtype, has_bias):
     torch.cuda.synchronize()
     assert y.shape == (M, N) and y.dtype == dtype
     _check("y", y, ref, 1e-5 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("B,D,dtype,wdtype", [(1, 6912, torch.bfloat16, torch.bfloat16), (3, 24, torch.float32, torch.float32),
+                                             (2, 136, torch.bfloat16, torch.float32)])
+def test_short_conv_step_matches_conv_of_tail_and_token(B, D, dtype, wdtype):
+    # the single-token step equals the fixed-length convolution of [tail, x] at its last token
+    # (same summation order: bit-identical), and the tail advances to [tail_1, tail_2, x]
+    dev = gpu_or_skip()
+    log(f"case short_conv_step B={B} D={D} {dtype} w={wdtype}")
+    from lit_gpt.kdn_ops.short_conv import _conv_fwd, short_conv_step
+    g = torch.Generator().manual_seed(B * 100 + D)
+    tail = torch.randn(B, 3, D, generator=g).to(dtype).to(dev)
+    xp = torch.randn(B, 1, D + 8, generator=g).to(dtype).to(dev)
+    x = xp[..., :D]  # batch stride D + 8, as a packed projection's split leaves it
+    w = torch.randn(D, 4, generator=g).to(wdtype).to(dev)
+    want = _conv_fwd(torch.cat([tail, x], 1).contiguous(), w)[:, 3:]
+    new_tail = torch.cat([tail[:, 1:], x], 1)
+    y = short_conv_step(x, tail, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y, want)
+    assert torch.equal(tail, new_tail)
