@@ -31,6 +31,11 @@ HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3   # dense fp32 MFMA (v_mfma_f32_16x16x4_f32)
 BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 C = 64
+# minimum I/O of the whole mixer scan op per token-head (inputs read once, outputs written once):
+# iso fwd 1,544 + bwd 2,832; diag fwd 2,052 + bwd 3,848 (d = 128)
+OP_BYTES = {"iso": lambda d: (6 * d + 4 * d + 8 + 2 * d) + (22 * d + 16),
+            "diag": lambda d: (6 * d + 4 * d + 4 * d + 4 + 2 * d) + (30 * d + 8)}
+OP_FWD_BYTES = {"diag": lambda d: 6 * d + 4 * d + 4 * d + 4 + 2 * d}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
 
 # MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
@@ -113,6 +118,16 @@ def frontend_counts(variant: str, B: int, T: int, H: int, K: int):
             "diag_gain_bwd": 32 * E + 12 * N,
         }
     return {k: (b, 0) for k, b in per.items()}
+
+
+def op_roofline(variant: str, ms: float, B: int, T: int, H: int, K: int):
+    """The whole op against its HBM floor: the minimum I/O bytes of the mixer scan fwd+bwd (OP_BYTES per
+    token-head times B*T*H) over the measured step time."""
+    nbytes = OP_BYTES[variant](K) * B * T * H
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "bytes_per_token_head": OP_BYTES[variant](K), "alg_bytes": int(nbytes),
+            "ceiling_ms": round(nbytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4), "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K: int):
@@ -450,6 +465,92 @@ def cpu_baseline(variant: str, slices: int, T: int, K: int, B: int, H: int):
                        f"(autograd), {per_slice:.2f} s/slice, extrapolated to the {B}x{H} job")
 
 
+def run_config3(steps: int, warmup: int, B: int = 1, T: int = 32768, H: int = 18, K: int = 128):
+    """the diag mixer scan forward at B1 H18 T32768 d128 (bf16 inputs) from a carried
+    state: S0 ~ N(0, 0.02^2) fp32 [B,H,K,V] and a per-channel initial precision softplus(N(0,1))
+    [B,H,K] (the oracle's initial_precision, diag_kdn_naive.py:503-516), returning the final memory and
+    precision.  Forward only, no autograd.  The op's minimum HBM bytes are 2,052 per token-head plus
+    the state and precision read and written; the per-kernel fractions use the kernels' own
+    algorithmic bytes at this shape."""
+    import torch
+
+    from lit_gpt.kdn_ops import _lib
+    from lit_gpt.kdn_ops.scan import diag_kdn_scan
+    from lit_gpt.kdn_ops.synthetic import make_inputs
+
+    dev = torch.device("cuda:0")
+    inputs, _ = make_inputs("diag", B, T, H, K, seed=0, device=dev)
+    g = torch.Generator().manual_seed(3)
+    S0 = (0.02 * torch.randn(B, H, K, K, generator=g)).to(dev)
+    P0 = torch.nn.functional.softplus(torch.randn(B, H, K, generator=g)).to(dev)
+
+    @torch.no_grad()
+    def step():
+        return diag_kdn_scan(**inputs, initial_state=S0, initial_precision=P0, output_final_state=True)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    with _lib.KernelTimer() as timer:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    fwd_tags = ("diag_norm_fwd", "diag_frontend_fwd", "diag_gain_fwd", "mem_intra_fwd", "mem_state_fwd",
+                "mem_readout_fwd")
+    counts = kernel_counts("diag", B, T, H, K, K)
+    counts.update(frontend_counts("diag", B, T, H, K))
+    kernels = {}
+    for tag in fwd_tags:
+        nbytes, _fl = counts[tag]
+        if tag == "mem_readout_fwd":  # the long-context output is bf16 (v's dtype), not the fp32 of kernel_counts
+            nbytes -= 2 * K * B * T * H
+        t = timer.mean_ms(tag) * 1e-3
+        gbs = nbytes / t / 1e9
+        kernels[tag] = {"ms": round(t * 1e3, 4), "bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": int(nbytes)}
+    N = B * T * H
+    op_bytes = OP_FWD_BYTES["diag"](K) * N + 2 * (B * H * K * K * 4 + B * H * K * 4)
+    dominant = max(kernels, key=lambda k: kernels[k]["ms"])
+    return {"workload": "diag_kdn mixer scan forward from a carried state (S0 ~ N(0, 0.02^2), per-channel "
+                        "precision softplus(N(0,1))), returning the final memory and precision",
+            "B": B, "T": T, "H": H, "d": K, "inputs": "bf16", "state": "fp32",
+            "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_forward": round(ms, 4),
+            "op_roofline": {"bound": "hbm", "alg_bytes": int(op_bytes), "ceiling_ms": round(op_bytes / 8e12 * 1e3, 4),
+                            "achieved": round(op_bytes / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(op_bytes / (ms * 1e-3) / 8e12, 4)},
+            "dominant": dominant, "kernels": kernels}
+
+
+def cpu_baseline_config3(T: int, K: int, B: int, H: int):
+    """The oracle's diag mixer forward (fp32: tokenwise gain, WY-chunked memory) from a carried state on
+    one (b, h) slice of the config-3 workload, extrapolated to the B x H job."""
+    import torch
+
+    from lit_gpt.kdn_ops.synthetic import make_inputs
+    from oracle import kdn_oracle as ko
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    inputs, _ = make_inputs("diag", 1, T, 1, K, seed=100, device="cpu", dtype=torch.float32)
+    g = torch.Generator().manual_seed(3)
+    S0 = 0.02 * torch.randn(1, 1, K, K, generator=g)
+    P0 = torch.nn.functional.softplus(torch.randn(1, 1, K, generator=g))
+    names = {"q": "q_raw", "k": "k_raw", "initial_precision_param": "mu_param"}
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        ko.diag_mixer(**{names.get(k, k): x for k, x in inputs.items()}, chunked=True, gain_chunked=False,
+                      initial_state=S0, initial_precision=P0, output_final_state=True)
+    per_slice = time.perf_counter() - t0
+    return dict(value=round(B * T / (per_slice * B * H), 2), unit="tokens/s", cores=torch.get_num_threads(),
+                kind="port", sample=f"1 of {B * H} (b,h) slices at T={T}, d={K}: oracle diag mixer forward "
+                                    f"(fp32, WY-chunked memory) from a carried state, {per_slice:.2f} s/slice, "
+                                    f"extrapolated to the {B}x{H} job")
+
+
 def measured_traffic(kernel: str, config: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
@@ -486,6 +587,9 @@ def main():
     ap.add_argument("--no-config4", action="store_true", help="skip the whole-model (config 4) measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode (state-carry) measurement")
     ap.add_argument("--decode-only", action="store_true", help="measure only decoding and print its line")
+    ap.add_argument("--no-config3", action="store_true", help="skip the long-context (config 3) measurement")
+    ap.add_argument("--config3-only", action="store_true",
+                    help="measure only the long-context diag forward (config 3) and print its line")
     ap.add_argument("--config4-only", action="store_true",
                     help="measure only the whole model (config 4) and print its line (for profiling)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
@@ -511,6 +615,10 @@ def main():
         line = run_decode(f"{main_v}_kdn_1.3B", max(args.steps, 20), args.warmup)
         print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B decode tokens/s")), flush=True)
         return
+    if args.config3_only:
+        line = run_config3(args.steps, args.warmup)
+        print(json.dumps(dict(line, metric="diag_kdn long-context forward tokens/s (config 3)")), flush=True)
+        return
     if args.config4_only:
         line = run_config4(f"{main_v}_kdn_1.3B", args.steps, args.warmup, 1, T)
         print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B forward tokens/s (config 4)")), flush=True)
@@ -532,7 +640,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "bf16 inputs / fp32 state",
         "data": "synthetic",
         "config": {"workload": f"{main_v}_kdn mixer scan fwd+bwd (frontend+gain+chunked memory, all input grads)",
                    "B": B, "T": T, "H": H, "d_k": K, "d_v": K, "chunk": C, "inputs": "bf16",
@@ -540,15 +648,19 @@ def main():
         "roofline": {"kernel": res["dominant"], "bound": dom["bound"], "achieved": dom["achieved"],
                      "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,
                      "traffic_source": (os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None)},
+        "op_roofline": op_roofline(main_v, res["ms_per_step"], B, T, H, K),
         "kernels": res["kernels"],
         "also": {f"{other}_kdn": {"value": round(res_other["tokens_per_s"], 1), "unit": "tokens/s",
                                   "ms_per_step": round(res_other["ms_per_step"], 4),
+                                  "op_roofline": op_roofline(other, res_other["ms_per_step"], B, T, H, K),
                                   "dominant": res_other["dominant"],
                                   "kernels": res_other["kernels"]},
                  "layer_frontends": {"workload": "packed q|k|v short conv + SiLU and sigmoid-gated RMS norm, "
                                                  "fwd+bwd, bf16, same B/T/H/d",
                                      "kernels": run_layer_frontends(args.steps, args.warmup, B, T, H, K)}},
     }
+    if not args.no_config3:
+        line["also"]["config3"] = run_config3(min(args.steps, 10), args.warmup)
     if not args.no_config4:
         line["also"]["config4"] = run_config4(f"{main_v}_kdn_1.3B", min(args.steps, 10), args.warmup, 1, T)
     if not args.no_decode:
@@ -557,6 +669,9 @@ def main():
         calib_copy(args.calib_copy)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(main_v, args.cpu_slices, T, K, B, H)
+        line["also"][f"{other}_kdn"]["cpu_baseline"] = cpu_baseline(other, args.cpu_slices, T, K, B, H)
+        if not args.no_config3:
+            line["also"]["config3"]["cpu_baseline"] = cpu_baseline_config3(32768, K, 1, H)
     print(json.dumps(line), flush=True)
 
 

@@ -27,7 +27,9 @@
 extern "C" {
 #endif
 
-#define KDN_ERR_ARG_VALUE (-1)
+/* Returned for a rejected argument (shape, dtype flag, size, alignment or workspace too small). */
+#define KDN_ERR_ARG (-1)
+#define KDN_ERR_ARG_VALUE KDN_ERR_ARG /* earlier name, kept as an alias */
 
 /* ---------------------------------------------------------------- iso frontend */
 /* _iso_kdn_gate_precumsum_fwd (iso_kdn_chunk.py:1059-1113, kernel :739-813).

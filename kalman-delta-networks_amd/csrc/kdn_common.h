@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "kdn.h"
 
 #define KDN_LN2 0.6931471805599453f
 #define KDN_LOG2E 1.4426950408889634f
@@ -89,8 +90,7 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
   return t;
 }
 
-// Error codes returned by the C ABI besides hipError_t values.
-#define KDN_ERR_ARG (-1)
+// Error codes returned by the C ABI besides hipError_t values (KDN_ERR_ARG) come from the public header.
 #define KDN_CHECK_LAUNCH()                       \
   do {                                           \
     hipError_t e_ = hipGetLastError();           \

@@ -508,9 +508,10 @@ int kdn_short_conv_step(const void* x, int x_bf16, int64_t x_stride_b, void* tai
                         const void* weight, int w_bf16, int B, int D, void* y, int64_t y_stride_b,
                         hipStream_t stream) {
   if (B < 0 || D <= 0 || D % 8 != 0 || !x || !tail || !weight || !y) return KDN_ERR_ARG;
-  if (!al16(x) || !al16(y) || !al16(tail) || !al16(weight) || x_stride_b % 8 != 0 || y_stride_b % 8 != 0 ||
-      tail_stride_b % 8 != 0 || tail_stride_b < (int64_t)(kConvW - 1) * D)
+  // batch strides are used only for B > 1; they keep every row 16-byte aligned
+  if (!al16(x) || !al16(y) || !al16(tail) || !al16(weight) || tail_stride_b < (int64_t)(kConvW - 1) * D)
     return KDN_ERR_ARG;
+  if (B > 1 && (x_stride_b % 8 != 0 || y_stride_b % 8 != 0 || tail_stride_b % 8 != 0)) return KDN_ERR_ARG;
   if (B == 0) return 0;
   const int64_t threads = (int64_t)B * (D / 8);
   const dim3 grid((unsigned)((threads + 255) / 256));

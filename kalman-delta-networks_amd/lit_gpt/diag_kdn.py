@@ -138,7 +138,7 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
         if state is not None:
             check_state(state, B, H, K, V, 3, (B, H, K), hidden_states.device)
         gate = None
-        if use_packed(hidden_states):  # a few rows without autograd: the six biasless input GEMMs as one
+        if use_packed(hidden_states, self):  # a few rows without autograd: the six biasless input GEMMs as one
             D, d = self.key_dim, self.head_k_dim
             w_in = packed_weight(self, "in_proj", (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
                                                    self.f_proj[0].weight, self.omega_proj[0].weight,

@@ -185,18 +185,22 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         if state is not None:
             check_state(state, B, H, K, self.head_v_dim, 1, (B, H), hidden_states.device)
         gate = None
-        if use_packed(hidden_states):  # a few rows without autograd: the three input GEMMs as one
+        if use_packed(hidden_states, self):  # a few rows without autograd: the three input GEMMs as one
+            # rows padded to a multiple of 8, so each token's q|k|v slice starts 16-byte aligned (the
+            # single-token convolution kernel's vector loads)
             w_in = packed_weight(self, "in_proj", (self.qkv_pack.projection_weight, self.f_omega_r_proj.weight,
-                                                   self.g_proj[0].weight))
-            x_lin, packed, g_hidden = linear(hidden_states, w_in).split(
-                (self.qkv_pack.out_features, self.head_v_dim + 2 * H, self.head_v_dim), dim=-1)
+                                                   self.g_proj[0].weight), row_multiple=8)
+            sizes = (self.qkv_pack.out_features, self.head_v_dim + 2 * H, self.head_v_dim)
+            x_lin, packed, g_hidden = linear(hidden_states, w_in).split(sizes + (w_in.shape[0] - sum(sizes),),
+                                                                         dim=-1)[:3]
             gate = linear(g_hidden, self.g_proj[1].weight, self.g_proj[1].bias)
         else:
             x_lin = F.linear(hidden_states, self.qkv_pack.projection_weight)
             packed = self.f_omega_r_proj.forward_packed(hidden_states)
         cw = self.qkv_pack.convolution_weight
         if (stateful and T == 1 and state is not None and state.inplace and not torch.is_grad_enabled()
-                and state.conv[0].dtype == x_lin.dtype and x_lin.data_ptr() % 16 == 0 and x_lin.stride(0) % 8 == 0
+                and state.conv[0].dtype == x_lin.dtype and x_lin.data_ptr() % 16 == 0
+                and (B == 1 or x_lin.stride(0) % 8 == 0)
                 and x_lin.stride(-1) == 1 and cw.is_contiguous()):
             # decode step: one launch convolves the token with the carried inputs and advances them
             y = short_conv_step(x_lin, state.conv[0], cw)

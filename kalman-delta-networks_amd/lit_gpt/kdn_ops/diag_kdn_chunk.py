@@ -305,6 +305,12 @@ def _diag_kdn_gain(k_gain, alpha, omega, r, initial_precision, omega_raw, r_raw,
             raise TypeError(f"{name} must be torch.float32")
     if omega_raw.dtype != _DIAG_KDN_VECTOR_DTYPE or r_raw.dtype != _DIAG_KDN_VECTOR_DTYPE:
         raise TypeError("omega_raw and r_raw must be torch.bfloat16")
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (k_gain, alpha, initial_precision, omega_raw,
+                                                                       r_raw))):
+        # forward only: the backward's per-token state (p_prev, D) is not written
+        kappa, _, _, fprec = _diag_kdn_gain_forward(k_gain, alpha, omega, r, initial_precision, save_state=False,
+                                                    output_final_state=output_final_state)
+        return (kappa, fprec) if output_final_state else kappa
     return _DiagKdnGainFunction.apply(k_gain, alpha, omega.detach(), r.detach(), initial_precision, omega_raw, r_raw,
                                       bool(output_final_state))
 

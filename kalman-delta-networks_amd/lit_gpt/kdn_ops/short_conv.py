@@ -197,7 +197,7 @@ def qkv_causal_conv1d(x: torch.Tensor, weight: torch.Tensor):
 
 def short_conv_step(x: torch.Tensor, tail: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """One token of the SiLU short convolution from its 3 carried inputs (decoding, no autograd):
-    x [B,1,D] (unit channel stride, batch stride a multiple of 8), ``tail`` [B,3,D] contiguous in x's
+    x [B,1,D] (unit channel stride; for B > 1 a batch stride that is a multiple of 8), ``tail`` [B,3,D] contiguous in x's
     dtype, ``weight`` [D,4] contiguous.  Returns y [B,1,D], equal to the convolution of [tail, x]
     at its last token, and advances ``tail`` in place to its last 2 rows and x (``kdn_short_conv_step``)."""
     if x.ndim != 3 or x.shape[1] != 1 or x.stride(-1) != 1:

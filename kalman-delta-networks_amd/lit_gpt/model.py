@@ -175,7 +175,7 @@ class SwiGLU(nn.Module):
         self.w3 = nn.Linear(hidden_features, in_features, bias=bias)
 
     def forward(self, x):
-        if self.w1.bias is None and self.w2.bias is None and use_packed(x):  # decode: w1 | w2 as one GEMM
+        if self.w1.bias is None and self.w2.bias is None and use_packed(x, self):  # decode: w1 | w2 as one GEMM
             h = swiglu_gate(x, packed_weight(self, "w12", (self.w1.weight, self.w2.weight)))
             return linear(h, self.w3.weight, self.w3.bias)
         return self.w3(F.silu(self.w1(x)) * self.w2(x))

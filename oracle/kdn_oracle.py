@@ -21,10 +21,16 @@ What each function restates (reference = ngocbh/kalman-delta-networks):
   diag_kdn_naive.py:570-655 (second, independent form)
 * ``iso_gate_frontend``      -- iso_kdn_chunk.py:787-813 (gate/a/omega/r/mu maps)
 * ``diag_frontend``          -- diag_kdn_chunk.py:1885-1905 (alpha clamp, omega, r, mu)
-* ``diag_normalize``         -- diag_kdn_chunk.py:194-232 (x / max(||x||, 1e-12))
+* ``iso_gain_unit_key``      -- the production unit-key iso gain (iso_kdn_chunk.py:1496-1518,
+  1586-1594), evaluated through ``iso_gain_tokenwise`` itself on a one-channel problem, so it is
+  pinned by the golden vectors of the tokenwise gain; a CPU test also checks it against the
+  closed form z/(r+z), p' = r z/(r + s z) and against the tokenwise gain on random unit keys.
+* ``diag_normalize``         -- diag_kdn_chunk.py:194-232 (x / max(||x||, 1e-12)); pinned
+  against torch.nn.functional.normalize (a library routine with the same definition).
 * ``l2norm_fla``             -- FLA l2norm_fwd used at iso_kdn_chunk.py:2203-2204
-  (flash-linear-attention @ 4b02d15d; x * rsqrt(sum x^2 + 1e-6)).  FLA is not
-  vendored in the reference, so this convention is PARITY UNPINNED.
+  (flash-linear-attention @ 4b02d15d; x * rsqrt(sum x^2 + 1e-6)).  FLA is not vendored in
+  the reference, so no golden vector covers it; it is pinned by its properties (unit norm,
+  zero row, scale invariance, and the eps inside the square root at |x|^2 = eps).
 * ``iso_mixer`` / ``diag_mixer`` -- the composition order of iso_kdn.py:277-304 and
   diag_kdn.py:315-345 (frontend -> gain -> memory scan).
 * ``short_conv_silu``        -- fixed-length causal depthwise convolution (width 4, no bias)
@@ -156,6 +162,20 @@ def diag_gain_tokenwise(k, alpha, omega, r, *, info_scale=None, initial_precisio
         p = ph / (1.0 + s * kt.square() / r[:, t, :, None] * ph)
     kappa = torch.stack(gains, 1) if T else k * 0
     return kappa, ((1.0 / p) if output_final_state else None)
+
+
+def iso_gain_unit_key(a, omega, r, initial_precision, *, posterior_scale=1.0, output_final_state=False):
+    """The production iso gain (iso_kdn_chunk.py:1496-1518,1586-1594): the scalars a = mean_i alpha_i^2,
+    omega, r [B,T,H] with |k| = 1, s = info_scale / head_dim = ``posterior_scale``.
+
+    Evaluated as ``iso_gain_tokenwise`` itself (golden-pinned) on a one-channel problem with the
+    same a, omega, r: k = 1 and alpha = sqrt(a) give mean alpha^2 = a and |k|^2 = 1, and
+    info_scale = s (the one-channel s / K).  So z = a / c + omega, beta = z / (r + z),
+    c' = 1 / z + s / r -- the unit-key form the kernels implement.  Returns (beta, c_T or None)."""
+    one = torch.ones_like(a)[..., None]
+    beta, c = iso_gain_tokenwise(one, a.sqrt()[..., None], omega, r, info_scale=posterior_scale,
+                                 initial_precision=initial_precision, output_final_state=output_final_state)
+    return beta, c
 
 
 # ----------------------------------------------------------------------------
@@ -334,7 +354,10 @@ def _w(x):
 
 
 def l2norm_fla(x, eps: float = 1e-6):
-    """x * rsqrt(sum x^2 + eps) over the last dim (FLA l2norm_fwd; parity unpinned)."""
+    """x * rsqrt(sum x^2 + eps) over the last dim (FLA l2norm_fwd, flash-linear-attention @ 4b02d15d,
+    as called at iso_kdn_chunk.py:2203-2204).  Pinned by its properties: unit norm when
+    sum x^2 >> eps, a zero row maps to zero, invariance to positive scaling of large rows, and the
+    eps inside the square root (x = c e_1 with c^2 = eps maps to 1/sqrt(2) e_1)."""
     return x * torch.rsqrt(x.square().sum(-1, keepdim=True) + eps)
 
 
@@ -397,29 +420,24 @@ def diag_frontend(retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, chu
 # ----------------------------------------------------------------------------
 
 def iso_mixer(q_raw, k_raw, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu_param,
-              *, omega_min=0.0, r_min=0.01, info_scale=None, scale=None, chunked=False):
+              *, omega_min=0.0, r_min=0.01, info_scale=None, scale=None, chunked=False, round_qk=False):
     """iso_kdn.py:277-304: gate frontend, scalar gain on unit keys, KDA memory scan.
 
     The production gain consumes (a, omega, r, mu) only and assumes |k| = 1
     (iso_kdn_chunk.py:1586-1594); the memory scan L2-normalises q and k inside
-    (iso_kdn_chunk.py:2203-2204) and uses alpha = exp(g) per channel.
+    (iso_kdn_chunk.py:2203-2204) and uses alpha = exp(g) per channel.  ``round_qk`` models
+    bf16 inputs: FLA's l2norm_fwd writes its output in the input's dtype, so the production scan
+    consumes the normalised q, k rounded to bf16 (and their cotangents come back in bf16).
     """
     K = q_raw.shape[-1]
     g, _gc, a, omega, r, mu = iso_gate_frontend(g_raw, omega_r_raw, omega_bias, r_bias, A_log,
                                                 dt_bias, mu_param, omega_min, r_min)
-    qn = l2norm_fla(_w(q_raw))
-    kn = l2norm_fla(_w(k_raw))
+    qn = amp_round(l2norm_fla(_w(q_raw)), round_qk)
+    kn = amp_round(l2norm_fla(_w(k_raw)), round_qk)
     alpha = g.exp()
-    # Gain on the production scalars: beta = z / (r + z) with unit-norm keys.
-    B, T, H, _ = q_raw.shape
+    # Gain on the production scalars (unit-norm keys): beta = z / (r + z)
     s = (float(K) if info_scale is None else float(info_scale)) / K
-    p = (1.0 / mu).view(1, H).expand(B, H)
-    betas = []
-    for t in range(T):
-        z = a[:, t] * p + omega[:, t]
-        betas.append(z / (r[:, t] + z))
-        p = r[:, t] * z / (r[:, t] + s * z)
-    beta = torch.stack(betas, 1)
+    beta, _ = iso_gain_unit_key(a, omega, r, mu, posterior_scale=s)
     sc = K ** -0.5 if scale is None else scale
     mem = memory_chunked_wy if chunked else memory_tokenwise
     o, _ = mem(qn, kn, _w(v), alpha, beta[..., None] * kn, scale=sc)
@@ -428,23 +446,28 @@ def iso_mixer(q_raw, k_raw, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt
 
 def diag_mixer(q_raw, k_raw, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param,
                *, scale=None, chunked=False, initial_state=None, initial_precision=None,
-               output_final_state=False):
+               output_final_state=False, gain_chunked=None, round_qk=True):
     """diag_kdn.py:315-345: normalise, frontend, vector gain, memory scan (fp32 output).
 
     The memory path consumes alpha clamped at 1e-6 (through g_cumsum) while the
-    gain consumes the unclamped alpha (diag_kdn_chunk.py:1887-1898).
+    gain consumes the unclamped alpha (diag_kdn_chunk.py:1887-1898).  ``chunked`` selects the WY
+    chunk form of the memory and (unless ``gain_chunked`` says otherwise) the Mobius form of the
+    gain; the forms agree to rounding (tokenwise == chunked is pinned on the CPU).  ``round_qk``
+    (default on, as in production) models the normalisation's bf16 memory operands: q_memory and
+    k_memory are bf16 while the gain's k is fp32 (diag_kdn_chunk.py:2045-2076), cotangents included.
     """
     K = q_raw.shape[-1]
     qn = diag_normalize(_w(q_raw))
     kn = diag_normalize(_w(k_raw))
     l_mem, _gc, alpha, omega, r, mu = diag_frontend(retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param)
     prec = mu if initial_precision is None else initial_precision
-    gain = diag_gain_mobius if chunked else diag_gain_tokenwise
+    gain = diag_gain_mobius if (chunked if gain_chunked is None else gain_chunked) else diag_gain_tokenwise
     kappa, fprec = gain(kn, alpha, omega, r, info_scale=float(K), initial_precision=prec,
                         output_final_state=True)
     sc = K ** -0.5 if scale is None else scale
     mem = memory_chunked_wy if chunked else memory_tokenwise
-    o, S = mem(qn, kn, _w(v), l_mem.exp(), kappa, scale=sc, initial_state=initial_state)
+    o, S = mem(amp_round(qn, round_qk), amp_round(kn, round_qk), _w(v), l_mem.exp(), kappa, scale=sc,
+               initial_state=initial_state)
     if output_final_state:
         return o, (S, fprec)
     return o
@@ -512,9 +535,23 @@ def rms_norm(x, weight, eps: float = 1e-5):
     return xw * torch.rsqrt(xw.square().mean(-1, keepdim=True) + eps) * _w(weight)
 
 
+class _Bf16Round(torch.autograd.Function):
+    """Rounds to bf16 in the forward and rounds the cotangent to bf16 in the backward: a tensor that
+    autocast stores in bf16 also receives its gradient in bf16."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.to(torch.bfloat16).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
 def amp_round(x, amp: bool):
-    """Round to bf16 where CUDA bf16 autocast stores a bf16 tensor (identity otherwise)."""
-    return x.to(torch.bfloat16).to(x.dtype) if amp else x
+    """Round to bf16 where CUDA bf16 autocast stores a bf16 tensor (identity otherwise); the
+    backward rounds that tensor's cotangent to bf16 as well, as autograd does for a bf16 tensor."""
+    return _Bf16Round.apply(x) if amp else x
 
 
 def linear(x, weight, bias=None, amp: bool = False):
@@ -550,7 +587,8 @@ def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp
     g_raw = linear(f_hidden, p["f_proj.1.weight"], amp=amp)
     o = iso_mixer(q.view(B, T, H, K), k.view(B, T, H, K), v.view(B, T, H, K), g_raw.view(B, T, H, K),
                   omega_r_raw, p["omega_proj.bias"], p["r_proj.bias"], p["A_log"], p["dt_bias"],
-                  p["initial_precision_param"], omega_min=omega_min, r_min=r_min, info_scale=info_scale)
+                  p["initial_precision_param"], omega_min=omega_min, r_min=r_min, info_scale=info_scale,
+                  round_qk=amp)
     o = amp_round(o, amp)
     gate = linear(linear(x, p["g_proj.0.weight"], amp=amp), p["g_proj.1.weight"], p["g_proj.1.bias"], amp=amp)
     y = amp_round(rms_norm_gated(o, gate.view(B, T, H, K), p["o_norm.weight"], eps, "sigmoid"), amp)

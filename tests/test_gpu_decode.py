@@ -136,3 +136,42 @@ def test_short_conv_step_matches_conv_of_tail_and_token(B, D, dtype, wdtype):
     torch.cuda.synchronize()
     assert torch.equal(y, want)
     assert torch.equal(tail, new_tail)
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_iso_layer_decode_step_uses_single_token_convolution(B, monkeypatch):
+    """At the iso_kdn_1.3B layer width (2304, 18 x 128 heads, bf16, eval, no_grad) a one-token call on
+    an in-place state convolves through ``short_conv_step`` (the packed projection's rows are padded to
+    a multiple of 8, so its q|k|v slice is aligned for every batch row), and the decoded outputs match
+    the whole sequence run at once (2e-2, bf16)."""
+    dev = gpu_or_skip()
+    log(f"case iso layer decode at width 2304, B={B}: single-token convolution kernel taken")
+    from lit_gpt import iso_kdn
+    from lit_gpt.kdn_state import KDNLayerState
+    torch.manual_seed(7)
+    layer = iso_kdn.IsotropicKalmanDeltaNetwork(hidden_size=2304, head_dim=128, num_heads=18)
+    layer = layer.to(dev).to(torch.bfloat16).eval()
+    calls = []
+    real = iso_kdn.short_conv_step
+
+    def counted(*args, **kwargs):
+        calls.append(args[0].shape)
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(iso_kdn, "short_conv_step", counted)
+    g = torch.Generator().manual_seed(8)
+    T, pre = 12, 8
+    x = torch.randn(B, T, 2304, generator=g).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        full, _, _ = layer(x, use_cache=True)
+        _, _, st = layer(x[:, :pre], use_cache=True)
+        st = KDNLayerState(tuple(c.clone() for c in st.conv), st.memory.clone(), st.precision.clone(),
+                           st.seen_tokens, inplace=True)
+        outs = []
+        for t in range(pre, T):
+            o, _, st2 = layer(x[:, t:t + 1], past_key_values=st, use_cache=True)
+            assert st2 is st
+            outs.append(o)
+    torch.cuda.synchronize()
+    assert len(calls) == T - pre, f"short_conv_step ran {len(calls)} times for {T - pre} decode steps"
+    _check("decoded steps vs whole sequence", torch.cat(outs, 1), full[:, pre:], 2e-2)

@@ -19,15 +19,8 @@ def _check(name, got, ref, tol):
 
 
 def _iso_gain_oracle(a, omega, r, mu, s):
-    """Production iso gain on unit keys: z = a p + w, beta = z/(r+z), p' = r z/(r+s z)."""
-    B, T, H = a.shape
-    p = (1.0 / mu).view(1, H).expand(B, H)
-    out = []
-    for t in range(T):
-        z = a[:, t] * p + omega[:, t]
-        out.append(z / (r[:, t] + z))
-        p = r[:, t] * z / (r[:, t] + s * z)
-    return torch.stack(out, 1)
+    """Production iso gain on unit keys (the oracle's golden-pinned tokenwise gain)."""
+    return ko.iso_gain_unit_key(a, omega, r, mu, posterior_scale=s)[0]
 
 
 @pytest.mark.parametrize("T", [1, 63, 300, 4100])

@@ -188,10 +188,9 @@ def test_gpt_fp32_eval_matches_oracle():
 @pytest.mark.parametrize("mixer_type", ["iso_kdn", "diag_kdn"])
 def test_gpt_bf16_autocast_matches_oracle(mixer_type):
     """Two-layer GPT under CUDA bf16 autocast (training mode) against the oracle GPT with autocast's
-    rounding points.  Through two blocks of bf16 GEMMs the order of bf16 roundings cannot be matched
-    exactly, so each quantity's tolerance is max(2e-2, 1.5 x the oracle's own autocast effect
-    |oracle_amp - oracle_fp64| / max|oracle_fp64|): the kernels may differ from the autocast oracle by
-    no more than autocast itself moves the exact result."""
+    rounding points, forward and backward (the oracle rounds a bf16 tensor's cotangent to bf16, as
+    autograd does): logits and gradients at 2e-2.  The oracle's own autocast effect
+    |oracle_amp - oracle_fp64| / max|oracle_fp64| is printed beside each measurement."""
     dev = gpu_or_skip()
     B, T = 1, 100
     log(f"case GPT {mixer_type} 2 layers autocast B={B} T={T}")
@@ -213,5 +212,5 @@ def test_gpt_bf16_autocast_matches_oracle(mixer_type):
     grads = torch.autograd.grad(logits, [params[n] for n in names], dl.to(dev).to(logits.dtype))
     torch.cuda.synchronize()
     for n, got, exact, amp_ref in zip(["logits"] + names, [logits] + list(grads), refs[False], refs[True]):
-        tol = max(TOL_LAYER, 1.5 * rel(amp_ref, exact))
-        _check(n if n == "logits" else f"d {n}", got, amp_ref, tol)
+        log(f"  ({n}: oracle autocast effect {rel(amp_ref, exact):.3e})")
+        _check(n if n == "logits" else f"d {n}", got, amp_ref, TOL_LAYER)

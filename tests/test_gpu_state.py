@@ -40,15 +40,9 @@ def _check(name, got, ref, tol):
 
 
 def _iso_gain_ref(a, omega, r, mu, s):
-    """Production iso gain on unit keys from p_0 = 1/mu (mu [H] or [B,H]); returns (beta, 1/p_T)."""
-    B, T, H = a.shape
-    p = 1.0 / (mu.view(1, H).expand(B, H) if mu.ndim == 1 else mu)
-    out = []
-    for t in range(T):
-        z = a[:, t] * p + omega[:, t]
-        out.append(z / (r[:, t] + z))
-        p = r[:, t] * z / (r[:, t] + s * z)
-    return torch.stack(out, 1), 1.0 / p
+    """Production iso gain on unit keys from p_0 = 1/mu (mu [H] or [B,H]); returns (beta, 1/p_T).
+    The oracle's golden-pinned tokenwise gain."""
+    return ko.iso_gain_unit_key(a, omega, r, mu, posterior_scale=s, output_final_state=True)
 
 
 @pytest.mark.parametrize("T1,T2,info_scale", [(70, 80, None), (64, 1, 64.0), (1, 130, None)])
@@ -190,9 +184,10 @@ def _oracle_layer(variant, p, x, head_dim, amp=False):
 
 
 def _amp_tol(amp_ref, exact):
-    """Autocast noise floor: a bf16 run may differ from the autocast oracle by no more than
-    autocast itself moves the exact result (and by 2e-2 in any case)."""
-    return max(2e-2, 1.5 * rel(amp_ref, exact))
+    """Oracle-side bar under autocast: 2e-2, as without it.  The oracle rounds to bf16 at autocast's
+    rounding points; its own autocast effect (amp vs exact) is printed beside the measurement."""
+    log(f"  (oracle autocast effect {rel(amp_ref, exact):.3e})")
+    return 2e-2
 
 
 @pytest.mark.parametrize("variant,head_dim", [("iso", 64), ("diag", 64), ("iso", 128), ("diag", 128)])
@@ -239,10 +234,8 @@ def test_layer_state_carry_gradients_under_autocast(variant):
     """Two differentiable segments with the state carried between them: output and every gradient
     against the same layer run on the whole sequence at once (1e-2: the runs differ only in chunk
     boundaries; this is the carry's contract), and against the autocast oracle of the whole
-    sequence at max(3e-2, 1.5 x the oracle's own autocast effect).  The oracle emulates autocast's
-    forward roundings only, not the bf16 cotangents of the backward, and the omega / r bias
-    gradients are sums over B T tokens with cancellation: across seeds the plain layer's bias
-    gradients differ from the autocast oracle by 0.3-2.4% of their largest entry."""
+    sequence at 2e-2.  The oracle rounds to bf16 where autocast stores bf16 tensors, in the forward
+    and in the backward (a bf16 tensor's cotangent is bf16)."""
     dev = gpu_or_skip()
     B, T, cut, head_dim = 2, 130, 70, 64
     log(f"case {variant} layer autocast training, two segments carried 0:{cut}:{T}")
@@ -273,8 +266,7 @@ def test_layer_state_carry_gradients_under_autocast(variant):
     torch.cuda.synchronize()
     for i, n in enumerate(["output", "d hidden"] + [f"d {n}" for n in names]):
         _check(f"{n} segments vs full", runs["segments"][i], runs["full"][i], 1e-2)
-        _check(f"{n} segments vs oracle", runs["segments"][i], refs[True][i],
-               max(3e-2, _amp_tol(refs[True][i], refs[False][i])))
+        _check(f"{n} segments vs oracle", runs["segments"][i], refs[True][i], 2e-2)
 
 
 @pytest.mark.parametrize("mixer_type", ["iso_kdn", "diag_kdn"])
