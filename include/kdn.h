@@ -60,6 +60,19 @@ size_t kdn_iso_gain_workspace_size(int B, int T, int H);
 int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const float* initial_precision,
                      int prec_mode, int B, int T, int H, float posterior_scale, float* beta, float* p_prev,
                      float* final_precision, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* Allocation-free variant of kdn_iso_gain_fwd (same arguments and results, bit-identical), with no
+ * counterpart in the reference.  For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the map / carry workspace is a fixed
+ * device array inside the library, KDN_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, so
+ * B * H * ceil(T / 64) * 20 bytes must not exceed it (else KDN_ERR_ARG; 4 MiB covers B*H*ceil(T/64) up
+ * to 209,715, e.g. B = 182 at H = 18, T = 4096).  It calls no hipMalloc / hipFree.  The array belongs to
+ * the current device, and `stream` must run on that device (else KDN_ERR_ARG).  Every call on one GPU
+ * shares the array (each call writes all of the part it reads, so no clearing is needed): calls that
+ * overlap in time on one GPU, e.g. on two streams, race and must be serialised by the caller. */
+#define KDN_NOALLOC_SCRATCH_BYTES (4u << 20)
+int kdn_iso_gain_fwd_noalloc(const float* a, const float* omega, const float* r, const float* initial_precision,
+                             int prec_mode, int B, int T, int H, float posterior_scale, float* beta, float* p_prev,
+                             float* final_precision, hipStream_t stream);
 /* _iso_kdn_gain_backward (iso_kdn_chunk.py:1817-1893); d_initial_precision is [H] summed over B
  * in a fixed order (deterministic) for prec_mode 0, [B,H] for prec_mode 1.  d_final_precision
  * (nullable; needs final_precision from the forward) is the cotangent of final_precision. */

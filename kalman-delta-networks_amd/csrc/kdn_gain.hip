@@ -14,6 +14,8 @@
 //   map / carry / emit passes over 64-token chunks, one workgroup per (chunk, b, h),
 //   thread = key channel; the per-token cross-channel sums are wave reductions whose
 //   partials are deferred to LDS so no barrier sits inside the token loop.
+#include <mutex>
+
 #include "kdn_common.h"
 #include "../../include/kdn.h"
 
@@ -877,6 +879,33 @@ __global__ void sum_over_batch_kernel(const float* __restrict__ part, int B, int
 }
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+// Fixed device workspace of kdn_iso_gain_fwd_noalloc (the per-chunk maps and carries of the iso gain),
+// for callers that cannot allocate.  Each GPU the library runs on holds its own copy until the process
+// ends.  In host code `scratch` names a host-side stand-in; the device address comes from
+// hipGetSymbolAddress, taken once per device with that device current and kept in g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[KDN_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch` (looked up on the first call per device).
+int current_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return KDN_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 inline int gain_block(int K) { return ((K + 63) / 64) * 64; }
 inline bool gain_vec_ok(int K) { return K % kCPT == 0 && 64 % (K / kCPT) == 0; }
 inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -911,6 +940,29 @@ int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const f
                      posterior_scale, unit, carry, beta, p_prev);
   KDN_CHECK_LAUNCH();
   return 0;
+}
+
+int kdn_iso_gain_fwd_noalloc(const float* a, const float* omega, const float* r, const float* initial_precision,
+                             int prec_mode, int B, int T, int H, float posterior_scale, float* beta, float* p_prev,
+                             float* final_precision, hipStream_t stream) {
+  if (B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f) || (prec_mode != 0 && prec_mode != 1))
+    return KDN_ERR_ARG;
+  if (B == 0 || T == 0) return 0;
+  const size_t need = kdn_iso_gain_workspace_size(B, T, H);
+  if (need > (size_t)KDN_NOALLOC_SCRATCH_BYTES) return KDN_ERR_ARG;
+  if (stream != nullptr) {  // the fixed workspace used is the current device's: the stream must run there
+    int sdev = -1, dev = -1;
+    hipError_t e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return (int)e;
+    e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (sdev != dev) return KDN_ERR_ARG;
+  }
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc != 0) return rc;
+  return kdn_iso_gain_fwd(a, omega, r, initial_precision, prec_mode, B, T, H, posterior_scale, beta, p_prev,
+                          final_precision, ws, need, stream);
 }
 
 int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const float* initial_precision,

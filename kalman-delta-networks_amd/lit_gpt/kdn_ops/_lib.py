@@ -21,6 +21,7 @@ _SIGS = {
     "kdn_iso_gate_bwd": "pipillppppppppppiiiiippppppppzs",
     "kdn_iso_gain_workspace_size": "iii",
     "kdn_iso_gain_fwd": "ppppiiiifppppzs",
+    "kdn_iso_gain_fwd_noalloc": "ppppiiiifppps",
     "kdn_iso_gain_bwd": "ppppippppiiifpppppzs",
     "kdn_l2norm_fwd": "pilifpips",
     "kdn_l2norm_bwd": "pippilips",
