@@ -136,6 +136,12 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
 
 /* ---------------------------------------------------------------- memory scan */
 int kdn_mem_chunk_size(void);
+/* Chunk groups the serial state passes of kdn_mem_fwd / kdn_mem_bwd use at this shape (1: a single
+ * serial pass; more: the two-level scan that fills the CUs when B*H is small), or KDN_ERR_ARG.  An
+ * implementation detail of this library (the reference's state kernel is one serial pass,
+ * diag_kdn_chunk.py:720-1229); callers need it only to size nothing -- the *_size() queries already
+ * include the group buffers. */
+int kdn_mem_state_groups(int B, int T, int H, int K, int V);
 size_t kdn_mem_saved_size(int B, int T, int H, int K, int V);
 size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
 /* Forward of the chunked memory scan: replaces _chunk_kda_fwd_precum (iso_kdn_chunk.py:2037-2086,

@@ -733,11 +733,47 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+// Chunk groups of the serial state passes (kdn_state.h, GroupPlan).  One state workgroup runs per
+// CU (the passes use 1 wave per SIMD), so with B*H*V/64 workgroups below the 256 CUs a two-level
+// scan fills the chip.  Cost model in chunk steps, per pass: a launch of n workgroups takes
+// ceil(n / 256) rounds of its groups' m steps; pass A runs the first group (V/64 slices per head)
+// and the NG - 2 middle groups' maps ((V + K)/64 slices), pass C the NG - 1 later groups, pass B
+// NG - 2 combine steps.  NG = 1 is the single serial pass.
+constexpr int kStateSlots = 256;
+struct GroupCount {
+  int NG, m;
+};
+inline GroupCount plan_groups(int BH, int NT, int K, int V) {
+  const int NV = V / kdn_state::state_cols(V), NPHI = K / kdn_state::state_cols(V);
+  auto rounds = [](int64_t n) { return (n + kStateSlots - 1) / kStateSlots; };
+  GroupCount best{1, NT};
+  int64_t best_cost = rounds((int64_t)BH * NV) * NT;
+  for (int NG = 2; NG <= 64 && 2 * NG <= NT; ++NG) {
+    const int m = cdiv(NT, NG);
+    if ((int64_t)(NG - 1) * m >= NT) continue;  // the last group would be empty
+    const int64_t a = (int64_t)BH * NV + (int64_t)BH * (NG - 2) * (NV + NPHI);
+    const int64_t c = (int64_t)BH * (NG - 1) * NV;
+    const int64_t cost = (rounds(a) + rounds(c)) * m + (NG - 2);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = GroupCount{NG, m};
+    }
+  }
+  return best;
+}
+// floats of a grouped pass's buffers: Sg [BH][NG][K][V] and Mg [BH][NG][K][V + K]
+inline int64_t group_floats(int64_t BH, GroupCount gc, int K, int V) {
+  return gc.NG > 1 ? BH * gc.NG * K * (2 * (int64_t)V + K) : 0;
+}
+inline int64_t round64(int64_t x) { return (x + 63) / 64 * 64; }
+
 // saved-buffer layout (floats), TT = B*H*T, NB = B*H*NT
 struct MemLayout {
-  int64_t U, W, Kf, Qg, M, A, h, D, flags, total;
+  int64_t U, W, Kf, Qg, M, A, h, D, flags, grp, total;
+  GroupCount gc;
   MemLayout(int B, int T, int H, int K, int V) {
     const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
+    gc = plan_groups(B * H, cdiv(T, C), K, V);
     U = 0;
     W = U + TT * V;
     Kf = W + TT * K;
@@ -747,13 +783,16 @@ struct MemLayout {
     h = A + NB * C * C;
     D = h + NB * K * V;
     flags = D + TT * V;  // NB ints: chunk taken by the exact intra-chunk path
-    total = flags + NB;
+    grp = round64(flags + NB);  // the forward state pass's group buffers (dead after the forward)
+    total = grp + group_floats((int64_t)B * H, gc, K, V);
   }
 };
 struct BwdLayout {
-  int64_t dh, dD, dQg, dW, dKf, dM, dgl, dKg, dN, total;
+  int64_t dh, dD, dQg, dW, dKf, dM, dgl, dKg, dN, grp, total;
+  GroupCount gc;
   BwdLayout(int B, int T, int H, int K, int V) {
     const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
+    gc = plan_groups(B * H, cdiv(T, C), K, V);
     dh = 0;
     dD = dh + NB * K * V;
     dQg = dD + TT * V;
@@ -763,9 +802,38 @@ struct BwdLayout {
     dgl = dM + NB * C * C;
     dKg = dgl + NB * K;
     dN = dKg + TT * K;
-    total = dN + NB * C * C;
+    grp = round64(dN + NB * C * C);  // the reverse state pass's group buffers
+    total = grp + group_floats((int64_t)B * H, gc, K, V);
   }
 };
+
+// Launch pass A / B / C of a state pass (or the single serial pass).  launch(grid, plan) issues the
+// state kernel of one pass.
+template <int K, int V, typename Launch>
+int run_state_pass(int BH, GroupCount gc, float* grp, bool reverse, hipStream_t stream, Launch launch) {
+  constexpr int NV = V / kdn_state::state_cols(V), NS = NV + K / kdn_state::state_cols(V);
+  kdn_state::GroupPlan P{gc.NG, gc.m, 0, grp, grp + (gc.NG > 1 ? (int64_t)BH * gc.NG * K * V : 0)};
+  if (gc.NG == 1) {
+    launch(dim3(BH * NV), P);
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
+  launch(dim3(BH * (gc.NG - 1) * NS), P);  // pass A
+  KDN_CHECK_LAUNCH();
+  if (gc.NG > 2) {  // pass B
+    if (reverse)
+      hipLaunchKernelGGL((kdn_state::state_combine_kernel<K, V>), dim3(BH * NV), dim3(kdn_state::state_threads(V)), 0,
+                         stream, P, BH, gc.NG - 2, gc.NG - 2, -1);
+    else
+      hipLaunchKernelGGL((kdn_state::state_combine_kernel<K, V>), dim3(BH * NV), dim3(kdn_state::state_threads(V)), 0,
+                         stream, P, BH, 1, gc.NG - 2, 1);
+    KDN_CHECK_LAUNCH();
+  }
+  P.pass = 1;
+  launch(dim3(BH * (gc.NG - 1) * NV), P);  // pass C
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
 
 
 template <int K, int V>
@@ -797,11 +865,14 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     }
     KDN_CHECK_LAUNCH();
   }
-  if (stages & 2) {  // serial state pass: h per chunk, delta, final state
-    const dim3 gs(B * H * (V / kdn_state::state_cols(V))), bs(kdn_state::state_threads(V));
-    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), gs, bs, 0, stream, U, W, Kf, gc, h0, T, H, NT, B * H, hb,
-                       D, ht);
-    KDN_CHECK_LAUNCH();
+  if (stages & 2) {  // serial state pass (one- or two-level): h per chunk, delta, final state
+    const dim3 bs(kdn_state::state_threads(V));
+    const int rc = run_state_pass<K, V>(B * H, lay.gc, saved + lay.grp, false, stream,
+                                        [&](dim3 grid, const kdn_state::GroupPlan& P) {
+                                          hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), grid, bs, 0, stream, U,
+                                                             W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht, P);
+                                        });
+    if (rc) return rc;
   }
   if (stages & 4) {  // chunk-parallel readout O = Qg h + M delta
     const int NCH = NT * B * H;  // chunk-heads; with two V halves the grid is padded to pairs of 8
@@ -831,11 +902,15 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   float *dh = work + bl.dh, *dD = work + bl.dD, *dQg = work + bl.dQg, *dW = work + bl.dW, *dKf = work + bl.dKf,
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
-  if (stages & 1) {
-    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO>), dim3(B * H * (V / kdn_state::state_cols(V))),
-                       dim3(kdn_state::state_threads(V)), 0, stream,
-                       M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H, dh, dD, dh0);
-    KDN_CHECK_LAUNCH();
+  if (stages & 1) {  // reverse state pass (one- or two-level): dh per chunk, d delta, d h0
+    const dim3 bs(kdn_state::state_threads(V));
+    const int rc = run_state_pass<K, V>(B * H, bl.gc, work + bl.grp, true, stream,
+                                        [&](dim3 grid, const kdn_state::GroupPlan& P) {
+                                          hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO>), grid, bs, 0,
+                                                             stream, M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H, dh,
+                                                             dD, dh0, P);
+                                        });
+    if (rc) return rc;
   }
   if (stages & 2) {
     hipLaunchKernelGGL((kdn_bwd::hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H,
@@ -877,6 +952,12 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
 extern "C" {
 
 int kdn_mem_chunk_size(void) { return C; }
+
+int kdn_mem_state_groups(int B, int T, int H, int K, int V) {
+  if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
+  if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
+  return plan_groups(B * H, cdiv(T, C), K, V).NG;
+}
 
 size_t kdn_mem_saved_size(int B, int T, int H, int K, int V) {
   return (size_t)MemLayout(B, T, H, K, V).total * sizeof(float);

@@ -180,7 +180,65 @@ __device__ __forceinline__ int64_t row_bthk(int b, int t, int h, int T, int H, i
 }
 
 // ===========================================================================
-// Forward state pass.  grid (B*H*V/COLS), block 4 COLS.  LDS 64.5 KB.
+// Chunk groups (two-level scan).  With NG > 1 groups of m chunks, each state pass runs as
+//   pass A  the first group in order (the true state), plus every middle group's affine map
+//           S_out = Phi S_in + Psi, taken by running the group from [0 | I] on V + K columns
+//           (the Psi columns see U / dO, the Phi columns start at the identity and see none);
+//   pass B  state_combine_kernel: the group-start states, serially, S_{g+1} = Phi_g S_g + Psi_g;
+//   pass C  every later group from its true incoming state (h / delta stores, final state).
+// Pass A's middle groups and pass C's groups all run in parallel, so the serial depth is about
+// 2 m + NG chunk steps instead of NT.  The map columns cost K more columns per middle group, so
+// the host takes NG > 1 only where B * H leaves CUs idle (kdn_memory.hip, plan_groups).
+//   forward:  Sg[g]  = state entering group g (g >= 1);   Mg[g] = [Psi_g | Phi_g] (1 <= g <= NG-2)
+//   backward: Sg[g]  = cotangent leaving group g (g <= NG-2), Mg[g] likewise for the reverse map.
+// Sg is [BH][NG][K][V], Mg is [BH][NG][K][V + K].
+// ===========================================================================
+struct GroupPlan {
+  int NG;     // number of chunk groups (1: a single serial pass over every chunk)
+  int m;      // chunks per group (the last group may be shorter)
+  int pass;   // 0: pass A, 1: pass C (unused when NG == 1)
+  float* Sg;
+  float* Mg;
+};
+
+// Workgroup -> (bh, column slice, group, role) of a state pass.  `real`: the group is run on the
+// true state (stores per-chunk results); otherwise it is a map group.  `phi`: the slice's columns
+// are Phi columns (col - V indexes the identity's column).  Returns false for a padding workgroup.
+template <int V, int K, bool REVERSE>
+__device__ __forceinline__ bool group_task(const GroupPlan& P, int BH, int& bh, int& vs, int& g, bool& real,
+                                           bool& phi) {
+  constexpr int NV = V / state_cols(V), NS = NV + K / state_cols(V);
+  phi = false;
+  real = true;
+  if (P.NG == 1) {
+    xcd_map(blockIdx.x, NV, BH, bh, vs);
+    g = 0;
+    return true;
+  }
+  const int G1 = P.NG - 1;
+  int u;
+  if (P.pass == 0) {
+    xcd_map(blockIdx.x, NS, BH * G1, u, vs);
+    bh = u / G1;
+    const int gi = u % G1;
+    if (gi == 0) {  // the group that starts from the true state: first (forward) or last (reverse)
+      g = REVERSE ? P.NG - 1 : 0;
+      return vs < NV;
+    }
+    g = gi;
+    real = false;
+    phi = vs >= NV;
+    return true;
+  }
+  xcd_map(blockIdx.x, NV, BH * G1, u, vs);
+  bh = u / G1;
+  g = REVERSE ? u % G1 : u % G1 + 1;
+  return true;
+}
+
+// ===========================================================================
+// Forward state pass.  grid: (B*H*V/COLS) for one group, or the pass's task count (GroupPlan);
+// block 4 COLS.  LDS 64.5 KB.
 // The readout O = Qg h + M delta is left to readout_kernel: it is off the serial chain, and its
 // operands (Qg, M) would double the chunk operands staged on the chain's critical path.
 // ===========================================================================
@@ -189,8 +247,8 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
                                                         const float* __restrict__ Kf, const float* __restrict__ gc,
                                                         const float* __restrict__ h0, int T, int H, int NT, int BH,
                                                         float* __restrict__ hbuf, float* __restrict__ Dl,
-                                                        float* __restrict__ ht) {
-  constexpr int COLS = state_cols(V), NTHR = state_threads(V), NV = V / COLS;
+                                                        float* __restrict__ ht, GroupPlan P) {
+  constexpr int COLS = state_cols(V), NTHR = state_threads(V);
   constexpr int KB = K / 32;           // k-blocks of a contraction over K
   constexpr int ST = K / 16;           // state row tiles per wave
   static_assert((C * K / 4) % NTHR == 0, "staging units per thread");
@@ -198,11 +256,13 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
   __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
   __shared__ __attribute__((aligned(16))) float sE[K];
-  int bh, vs;
-  xcd_map(blockIdx.x, NV, BH, bh, vs);
+  int bh, vs, g;
+  bool real, phi;
+  if (!group_task<V, K, false>(P, BH, bh, vs, g, real, phi)) return;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
-  const int col = vs * COLS + 16 * w + (lane & 15);  // this lane's state column
+  const int col = vs * COLS + 16 * w + (lane & 15);  // this lane's state column (>= V: a Phi column)
+  const int n0 = g * P.m, n1 = P.NG == 1 ? NT : min(NT, n0 + P.m);
 
   float4 rW[UN];
   float rK[UN][4], rU[4][4], rE = 0.f;
@@ -218,7 +278,7 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
   auto load_K = [&](int n) {  // Kf^T (rows i, k = c), U rows of this lane, e^{g_last}
     const int t0 = n * C, L = min(C, T - t0);
     const bufrsrc rk = make_buf(Kf + row_bht(bh, t0, T, K), L * K * 4);
-    const bufrsrc ru = make_buf(U + row_bht(bh, t0, T, V), L * V * 4);
+    const bufrsrc ru = make_buf(U + row_bht(bh, t0, T, V), phi ? 0u : L * V * 4);  // Phi columns: U = 0
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const Unit x = unit<C>(tid + NTHR * u);
@@ -244,19 +304,29 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
     if (tid < K) sE[tid] = exp2f(rE);
   };
 
+  // the state entering the group: h0 (or 0) for the first group, the combined group-start state for
+  // a later group, [0 | I] for a map group
   f32x4 S[ST];
+  {
+    const float* src = !real ? nullptr
+                       : g == 0 ? (h0 ? h0 + (int64_t)bh * K * V : nullptr)
+                                : P.Sg + ((int64_t)bh * P.NG + g) * K * V;
 #pragma unroll
-  for (int ib = 0; ib < ST; ++ib)
+    for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) S[ib][j] = h0 ? h0[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] : 0.f;
+      for (int j = 0; j < 4; ++j) {
+        const int row = 16 * ib + 4 * g4 + j;
+        S[ib][j] = src ? src[(int64_t)row * V + col] : (phi && row == col - V ? 1.f : 0.f);
+      }
+  }
 
-  load_W(0);
+  load_W(n0);
   stage_W();
-  load_K(0);
+  load_K(n0);
   __syncthreads();
-  for (int n = 0; n < NT; ++n) {
+  for (int n = n0; n < n1; ++n) {
     const int t0 = n * C, L = min(C, T - t0);
-    {
+    if (real) {
       const float* hb = hbuf + ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
       for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, S[ib]);
@@ -269,7 +339,7 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) cU[cb][j] = rU[cb][j];
-    if (n + 1 < NT) load_W(n + 1);
+    if (n + 1 < n1) load_W(n + 1);
     f32x4 D[4];
     {
       uint4 bh_[KB], bl_[KB];
@@ -282,18 +352,21 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
                            [&](int st, const uint4& ah, const uint4& al) {
                              D[st & 3] = mma3(ah, al, bh_[st >> 2], bl_[st >> 2], D[st & 3]);
                            });
-      const float* dl = Dl + row_bht(bh, t0, T, V);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
+      for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) D[cb][j] = cU[cb][j] - D[cb][j];
-        st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, D[cb]);  // rows past L dropped
+      if (real) {
+        const float* dl = Dl + row_bht(bh, t0, T, V);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, D[cb]);  // rows past L dropped
       }
     }
     __syncthreads();
 
     // ---- phase 2: S = e S + Kf^T delta   (reads sK; fills sW with chunk n+1; loads Kf, U, e of n+1)
-    if (n + 1 < NT) {
+    if (n + 1 < n1) {
       stage_W();
       load_K(n + 1);
     }
@@ -314,11 +387,23 @@ __global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float
     }
     __syncthreads();
   }
-  if (ht) {
+  // the state leaving the group: the final state (last group), the next group's start (first group
+  // of a grouped pass), or the group map [Psi | Phi]
+  float* dst = nullptr;
+  int64_t ld = V;
+  if (!real) {
+    dst = P.Mg + ((int64_t)bh * P.NG + g) * K * (V + K);
+    ld = V + K;
+  } else if (g == P.NG - 1) {
+    dst = ht ? ht + (int64_t)bh * K * V : nullptr;
+  } else if (g == 0) {
+    dst = P.Sg + ((int64_t)bh * P.NG + 1) * K * V;
+  }
+  if (dst) {
 #pragma unroll
     for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ht[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] = S[ib][j];
+      for (int j = 0; j < 4; ++j) dst[(int64_t)(16 * ib + 4 * g4 + j) * ld + col] = S[ib][j];
   }
 }
 
@@ -443,7 +528,8 @@ __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict
 }
 
 // ===========================================================================
-// Reverse state pass.  grid (B*H*V/COLS), block 4 COLS.  LDS 112.5 KB.
+// Reverse state pass.  grid: (B*H*V/COLS) for one group, or the pass's task count (GroupPlan);
+// block 4 COLS.  LDS 112.5 KB.
 // ===========================================================================
 template <int K, int V, typename TDO>
 __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float* __restrict__ Mg, const float* __restrict__ Kf,
@@ -451,8 +537,8 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
                                                         const float* __restrict__ gc, const TDO* __restrict__ dO,
                                                         const float* __restrict__ dht, int T, int H, int NT, int BH,
                                                         float* __restrict__ dhbuf, float* __restrict__ dDl,
-                                                        float* __restrict__ dh0) {
-  constexpr int COLS = state_cols(V), NTHR = state_threads(V), NV = V / COLS;
+                                                        float* __restrict__ dh0, GroupPlan P) {
+  constexpr int COLS = state_cols(V), NTHR = state_threads(V);
   constexpr int KB = K / 32;
   constexpr int ST = K / 16;
   static_assert((C * K / 4) % NTHR == 0 && (C * C / 4) % NTHR == 0, "staging units per thread");
@@ -465,11 +551,13 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
   __shared__ __attribute__((aligned(16))) bf16_t sQ[(K / 16) * (C / 32) * TILE];
   __shared__ __attribute__((aligned(16))) bf16_t sWt[(K / 16) * (C / 32) * TILE];
   __shared__ __attribute__((aligned(16))) float sE[K];
-  int bh, vs;
-  xcd_map(blockIdx.x, NV, BH, bh, vs);
+  int bh, vs, g;
+  bool real, phi;
+  if (!group_task<V, K, true>(P, BH, bh, vs, g, real, phi)) return;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
-  const int col = vs * COLS + 16 * w + (lane & 15);
+  const int col = vs * COLS + 16 * w + (lane & 15);  // >= V: a Phi column (its dO is zero)
+  const int n0 = g * P.m, n1 = P.NG == 1 ? NT : min(NT, n0 + P.m);
 
   float rM[UM][4], rQ[UN][4], rWt[UN][4], rE = 0.f;
   // dO as loaded (raw bf16 bits or fp32), widened only where the fragments are built, so the
@@ -517,7 +605,7 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
       // dO rows 16 cb .. are H*V apart; the descriptor ends right after row L-1's head h
       const int r0 = 16 * cb;
       const bufrsrc ro = make_buf(dO + row_bthk(b, t0 + r0, h, T, H, V),
-                                  L > r0 ? ((L - 1 - r0) * H + 1) * V * (uint32_t)sizeof(TDO) : 0u);
+                                  (!phi && L > r0) ? ((L - 1 - r0) * H + 1) * V * (uint32_t)sizeof(TDO) : 0u);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t e = (uint32_t)((4 * g4 + j) * H * V + col);
@@ -547,19 +635,29 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
     if (tid < K) sE[tid] = exp2f(rE);
   };
 
+  // the cotangent leaving the group: dht (or 0) for the last group, the combined one for an earlier
+  // group, [0 | I] for a map group
   f32x4 dS[ST];
+  {
+    const float* src = !real ? nullptr
+                       : g == P.NG - 1 ? (dht ? dht + (int64_t)bh * K * V : nullptr)
+                                       : P.Sg + ((int64_t)bh * P.NG + g) * K * V;
 #pragma unroll
-  for (int ib = 0; ib < ST; ++ib)
+    for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dS[ib][j] = dht ? dht[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] : 0.f;
+      for (int j = 0; j < 4; ++j) {
+        const int row = 16 * ib + 4 * g4 + j;
+        dS[ib][j] = src ? src[(int64_t)row * V + col] : (phi && row == col - V ? 1.f : 0.f);
+      }
+  }
 
-  load_p1(NT - 1);
+  load_p1(n1 - 1);
   stage_p1();
-  load_p2(NT - 1);
+  load_p2(n1 - 1);
   __syncthreads();
-  for (int n = NT - 1; n >= 0; --n) {
+  for (int n = n1 - 1; n >= n0; --n) {
     const int t0 = n * C, L = min(C, T - t0);
-    {
+    if (real) {
       const float* hb = dhbuf + ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
       for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, dS[ib]);
@@ -576,7 +674,7 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
 
     // ---- phase 1: d delta = M^T dO + Kf dS   (reads sM, sKn; fills sQ, sWt with chunk n)
     stage_p2();
-    if (n > 0) load_p1(n - 1);
+    if (n > n0) load_p1(n - 1);
     f32x4 dD[4];
     {
       uint4 bh_[KB], bl_[KB];
@@ -605,15 +703,17 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
               dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
             }
           });
-      const float* dl = dDl + row_bht(bh, t0, T, V);
+      if (real) {
+        const float* dl = dDl + row_bht(bh, t0, T, V);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-        st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, dD[cb]);  // rows past L dropped
+        for (int cb = 0; cb < 4; ++cb)
+          st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, dD[cb]);  // rows past L dropped
+      }
     }
     __syncthreads();
 
     // ---- phase 2: dS <- e dS + Qg^T dO - W^T d delta   (reads sQ, sWt; fills sM, sKn with n-1)
-    if (n > 0) {
+    if (n > n0) {
       stage_p1();
       load_p2(n - 1);
     }
@@ -639,11 +739,96 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
     }
     __syncthreads();
   }
-  if (dh0) {
+  // the cotangent entering the group: d h0 (first group), the cotangent leaving group NG-2 (the last
+  // group of a grouped pass), or the group's reverse map [Psi | Phi]
+  float* dst = nullptr;
+  int64_t ld = V;
+  if (!real) {
+    dst = P.Mg + ((int64_t)bh * P.NG + g) * K * (V + K);
+    ld = V + K;
+  } else if (g == 0) {
+    dst = dh0 ? dh0 + (int64_t)bh * K * V : nullptr;
+  } else if (g == P.NG - 1) {
+    dst = P.Sg + ((int64_t)bh * P.NG + P.NG - 2) * K * V;
+  }
+  if (dst) {
 #pragma unroll
     for (int ib = 0; ib < ST; ++ib)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dh0[((int64_t)bh * K + 16 * ib + 4 * g4 + j) * V + col] = dS[ib][j];
+      for (int j = 0; j < 4; ++j) dst[(int64_t)(16 * ib + 4 * g4 + j) * ld + col] = dS[ib][j];
+  }
+}
+
+// ===========================================================================
+// Pass B of a grouped state pass: `count` serial steps g = g0, g0 + dir, ... of
+//   Sg[g + dir] = Phi_g Sg[g] + Psi_g        ([Psi_g | Phi_g] = Mg[g], K x (V + K))
+// forward dir = +1 (group-start states), reverse dir = -1 (cotangents leaving each group).
+// grid (B*H*V/COLS), block 4 COLS: a wave keeps its 16 columns of S in accumulators, as the state
+// passes do; Phi_g (the A operand, rows i, k = j) is split into bf16 hi/lo fragments in LDS.  The
+// next step's Phi and Psi are loaded while this step multiplies.  LDS 64 KB.
+// ===========================================================================
+template <int K, int V>
+__global__ __launch_bounds__(state_threads(V)) void state_combine_kernel(GroupPlan P, int BH, int g0, int count,
+                                                                            int dir) {
+  constexpr int COLS = state_cols(V), NTHR = state_threads(V), NV = V / COLS;
+  constexpr int KB = K / 32, ST = K / 16, LD = V + K;
+  static_assert((K * K / 4) % NTHR == 0, "staging units per thread");
+  constexpr int UP = K * K / 4 / NTHR;  // staging units per thread of Phi
+  __shared__ __attribute__((aligned(16))) bf16_t sP[(K / 16) * KB * TILE];
+  int bh, vs;
+  xcd_map(blockIdx.x, NV, BH, bh, vs);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
+  const int col = vs * COLS + 16 * w + (lane & 15);
+  float4 rP[UP];
+  float rPsi[ST][4];
+  auto load = [&](int g) {
+    const float* m = P.Mg + ((int64_t)bh * P.NG + g) * K * LD;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) {
+      const Unit x = unit<K>(tid + NTHR * u);
+      rP[u] = *reinterpret_cast<const float4*>(m + x.row * LD + V + x.k0);
+    }
+#pragma unroll
+    for (int ib = 0; ib < ST; ++ib)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rPsi[ib][j] = m[(16 * ib + 4 * g4 + j) * LD + col];
+  };
+  f32x4 S[ST];
+  {
+    const float* s0 = P.Sg + ((int64_t)bh * P.NG + g0) * K * V;
+#pragma unroll
+    for (int ib = 0; ib < ST; ++ib)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[ib][j] = s0[(16 * ib + 4 * g4 + j) * V + col];
+  }
+  load(g0);
+  for (int i = 0; i < count; ++i) {
+    const int g = g0 + i * dir;
+#pragma unroll
+    for (int u = 0; u < UP; ++u) put_unit(sP, unit<K>(tid + NTHR * u).off, rP[u].x, rP[u].y, rP[u].z, rP[u].w);
+    f32x4 acc[ST];
+#pragma unroll
+    for (int ib = 0; ib < ST; ++ib) acc[ib] = f32x4{rPsi[ib][0], rPsi[ib][1], rPsi[ib][2], rPsi[ib][3]};
+    __syncthreads();
+    if (i + 1 < count) load(g + dir);
+    {
+      uint4 bh_[KB], bl_[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) bfrag(S[2 * kb], S[2 * kb + 1], bh_[kb], bl_[kb]);
+      // step s: ib = s / KB, kb = s % KB
+      mfma_pipe<ST * KB, 2>([&](int st, uint4& ah, uint4& al) { afrag(sP, st, lane, ah, al); },
+                            [&](int st, const uint4& ah, const uint4& al) {
+                              acc[st / KB] = mma3(ah, al, bh_[st % KB], bl_[st % KB], acc[st / KB]);
+                            });
+    }
+    float* dst = P.Sg + ((int64_t)bh * P.NG + g + dir) * K * V;
+#pragma unroll
+    for (int ib = 0; ib < ST; ++ib) {
+      S[ib] = acc[ib];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[(16 * ib + 4 * g4 + j) * V + col] = acc[ib][j];
+    }
+    __syncthreads();
   }
 }
 

@@ -34,6 +34,7 @@ _SIGS = {
     "kdn_diag_gain_fwd": "pppppiiiiifpppppzs",
     "kdn_diag_gain_bwd": "pppppipppppppiiiifpppppppzs",
     "kdn_mem_chunk_size": "",
+    "kdn_mem_state_groups": "iiiii",
     "kdn_mem_saved_size": "iiiii",
     "kdn_mem_bwd_workspace_size": "iiiii",
     "kdn_mem_fwd": "pppippiiiiifppzppiis",

@@ -218,3 +218,37 @@ def test_diag_bf16_output_equals_fp32_output_cast():
         outs.append([o] + list(grads))
     for name, a, b in zip(("o", "dq", "dk", "dkappa", "dv", "dg"), outs[0], outs[1]):
         assert a.dtype == b.dtype and torch.equal(a, b), f"{name} differs"
+
+
+def _state_groups(B, T, H, K, V):
+    from lit_gpt.kdn_ops import _lib
+    return int(_lib.load().kdn_mem_state_groups(B, T, H, K, V))
+
+
+@pytest.mark.parametrize("variant,B,T,H,K,V", [("iso", 1, 1000, 2, 128, 128), ("diag", 1, 1000, 2, 128, 128),
+                                               ("iso", 1, 777, 1, 64, 128), ("diag", 2, 1500, 1, 64, 64)])
+def test_memory_scan_grouped_state_passes(variant, B, T, H, K, V):
+    """Shapes whose few (b, h) streams make the state passes two-level (chunk groups: the first group
+    in order and the middle groups' affine maps, a serial combine, then the later groups from their
+    true incoming states), forward and reverse, with a carried initial state and a final-state
+    cotangent, against the fp64 tokenwise recurrence.  Ragged T leaves a short last group."""
+    dev = gpu_or_skip()
+    NG = _state_groups(B, T, H, K, V)
+    log(f"case memory grouped {variant} B={B} T={T} H={H} K={K} V={V}: {NG} chunk groups")
+    assert NG > 1
+    iso = variant == "iso"
+    q, k, v, ell, kap, do = memory_inputs(3 + T, B, T, H, K, V, diag=not iso)
+    g = torch.Generator().manual_seed(T)
+    h0 = 0.3 * torch.randn(B, H, K, V, generator=g)
+    dS = torch.randn(B, H, K, V, generator=g)
+    scale = K ** -0.5
+    o_ref, S_ref, g_ref = _oracle(q, k, v, ell, kap, do, iso=iso, scale=scale, h0=h0, dS=dS)
+    o, ht, dq, dkk, dv, dell, dkap, dh0 = _gpu(q, k, v, ell, kap, do, iso=iso, scale=scale, dev=dev, h0=h0, dS=dS)
+    _check("o", o, o_ref, TOL_F32)
+    _check("final state", ht, S_ref, TOL_F32)
+    _check("dq", dq, g_ref[0], TOL_BF16)
+    _check("dk", dkk, g_ref[1], TOL_BF16)
+    _check("dv", dv, g_ref[2], TOL_BF16)
+    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
+    _check("dbeta" if iso else "dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("d initial state", dh0, g_ref[5], TOL_F32)
