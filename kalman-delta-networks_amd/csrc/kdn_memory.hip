@@ -733,27 +733,31 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
-// Chunk groups of the serial state passes (kdn_state.h, GroupPlan).  One state workgroup runs per
-// CU (the passes use 1 wave per SIMD), so with B*H*V/64 workgroups below the 256 CUs a two-level
-// scan fills the chip.  Cost model in chunk steps, per pass: a launch of n workgroups takes
-// ceil(n / 256) rounds of its groups' m steps; pass A runs the first group (V/64 slices per head)
-// and the NG - 2 middle groups' maps ((V + K)/64 slices), pass C the NG - 1 later groups, pass B
-// NG - 2 combine steps.  NG = 1 is the single serial pass.
+// Chunk groups of the serial state passes (kdn_state.h, GroupPlan).  With few B*H*V/64 workgroups a
+// two-level scan fills the chip.  Cost model in chunk steps, fitted to measured passes (both the
+// forward pass, two workgroups per CU, and the reverse pass, one): a launch of n workgroups costs
+// max(1, n / 256) times its groups' m steps; pass A runs the first group (V/64 slices per head) and
+// the NG - 2 middle groups' maps ((V + K)/64 slices), pass C the NG - 1 later groups, pass B NG - 2
+// combine steps.  Once the single pass occupies half the CUs, per-step contention makes the extra
+// map work a loss (B4 H18: one pass 334 us, three groups 441 us), so NG = 1 there.
+// Measured optima: B1 H18 T4096 -> 8 groups (forward 272 -> 144 us, reverse 418 -> 225 us),
+// B2 -> 4, B1 T32768 -> 8 (forward 2163 -> 879 us).
 constexpr int kStateSlots = 256;
 struct GroupCount {
   int NG, m;
 };
 inline GroupCount plan_groups(int BH, int NT, int K, int V) {
   const int NV = V / kdn_state::state_cols(V), NPHI = K / kdn_state::state_cols(V);
-  auto rounds = [](int64_t n) { return (n + kStateSlots - 1) / kStateSlots; };
   GroupCount best{1, NT};
-  int64_t best_cost = rounds((int64_t)BH * NV) * NT;
+  if ((int64_t)BH * NV > kStateSlots / 2) return best;
+  auto load = [](int64_t n) { return n > kStateSlots ? (double)n / kStateSlots : 1.0; };
+  double best_cost = NT;
   for (int NG = 2; NG <= 64 && 2 * NG <= NT; ++NG) {
     const int m = cdiv(NT, NG);
     if ((int64_t)(NG - 1) * m >= NT) continue;  // the last group would be empty
     const int64_t a = (int64_t)BH * NV + (int64_t)BH * (NG - 2) * (NV + NPHI);
     const int64_t c = (int64_t)BH * (NG - 1) * NV;
-    const int64_t cost = (rounds(a) + rounds(c)) * m + (NG - 2);
+    const double cost = (load(a) + load(c)) * m + (NG - 2);
     if (cost < best_cost) {
       best_cost = cost;
       best = GroupCount{NG, m};

@@ -243,7 +243,7 @@ __device__ __forceinline__ bool group_task(const GroupPlan& P, int BH, int& bh, 
 // operands (Qg, M) would double the chunk operands staged on the chain's critical path.
 // ===========================================================================
 template <int K, int V>
-__global__ __launch_bounds__(state_threads(V)) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
+__global__ __launch_bounds__(state_threads(V), 2) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
                                                         const float* __restrict__ Kf, const float* __restrict__ gc,
                                                         const float* __restrict__ h0, int T, int H, int NT, int BH,
                                                         float* __restrict__ hbuf, float* __restrict__ Dl,
