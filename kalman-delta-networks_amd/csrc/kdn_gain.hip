@@ -788,6 +788,78 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_carry_v_kernel(const float2
   }
 }
 
+// Two-level carries for long streams.  A (b, h) stream of NT chunk maps per channel is cut into
+// groups of kCarryGroup chunks: the groups' composite maps are formed in parallel (group_map), the
+// serial carry kernel runs over the NG composites only, and every group then replays its own chunk
+// maps from its start value (group_fill).  The serial depth drops from NT to NG + 2 kCarryGroup steps.
+// Forward maps are 2x2 Mobius maps on p (composed with max-abs renormalisation); backward maps are
+// affine, lambda <- A lambda + B, applied from the last chunk down.
+constexpr int kCarryGroup = 32;
+
+// grid (B*H, NG), block K: composite of chunks [g G, min(NT, (g+1) G)) per channel
+__global__ __launch_bounds__(256) void diag_gain_group_map_kernel(const float4* __restrict__ maps, int K, int NT,
+                                                                  int NG, float4* __restrict__ gmaps) {
+  const int bh = blockIdx.x, gi = blockIdx.y, i = threadIdx.x;
+  if (i >= K) return;
+  const int64_t cb = (int64_t)bh * NT;
+  const int n0 = gi * kCarryGroup, n1 = min(NT, n0 + kCarryGroup);
+  Map2 M{1.f, 0.f, 0.f, 1.f};
+#pragma unroll 8
+  for (int n = n0; n < n1; ++n) {
+    const float4 m = maps[(cb + n) * K + i];
+    M = map_mul(Map2{m.x, m.y, m.z, m.w}, M);
+  }
+  gmaps[((int64_t)bh * NG + gi) * K + i] = float4{M.m0, M.m1, M.m2, M.m3};
+}
+// grid (B*H, NG), block K: per-chunk carries (p entering each chunk) of group g from its start value
+__global__ __launch_bounds__(256) void diag_gain_group_fill_kernel(const float4* __restrict__ maps,
+                                                                   const float* __restrict__ gstart, int K, int NT,
+                                                                   int NG, float* __restrict__ carry) {
+  const int bh = blockIdx.x, gi = blockIdx.y, i = threadIdx.x;
+  if (i >= K) return;
+  const int64_t cb = (int64_t)bh * NT;
+  const int n0 = gi * kCarryGroup, n1 = min(NT, n0 + kCarryGroup);
+  float p = gstart[((int64_t)bh * NG + gi) * K + i];
+#pragma unroll 8
+  for (int n = n0; n < n1; ++n) {
+    const float4 m = maps[(cb + n) * K + i];
+    carry[(cb + n) * K + i] = p;
+    p = (m.x * p + m.y) / (m.z * p + m.w);
+  }
+}
+// grid (B*H, NG), block K: composite (A, B) of group g's reverse affine maps, last chunk first
+__global__ __launch_bounds__(256) void diag_gain_bwd_group_map_kernel(const float2* __restrict__ ab, int K, int NT,
+                                                                      int NG, float2* __restrict__ gab) {
+  const int bh = blockIdx.x, gi = blockIdx.y, i = threadIdx.x;
+  if (i >= K) return;
+  const int64_t cb = (int64_t)bh * NT;
+  const int n0 = gi * kCarryGroup, n1 = min(NT, n0 + kCarryGroup);
+  float A = 1.f, Bc = 0.f;
+#pragma unroll 8
+  for (int n = n1 - 1; n >= n0; --n) {
+    const float2 m = ab[(cb + n) * K + i];
+    Bc = m.x * Bc + m.y;
+    A = m.x * A;
+  }
+  gab[((int64_t)bh * NG + gi) * K + i] = float2{A, Bc};
+}
+// grid (B*H, NG), block K: per-chunk adjoint carries of group g from lambda leaving the group
+__global__ __launch_bounds__(256) void diag_gain_bwd_group_fill_kernel(const float2* __restrict__ ab,
+                                                                       const float* __restrict__ gend, int K, int NT,
+                                                                       int NG, float* __restrict__ carry) {
+  const int bh = blockIdx.x, gi = blockIdx.y, i = threadIdx.x;
+  if (i >= K) return;
+  const int64_t cb = (int64_t)bh * NT;
+  const int n0 = gi * kCarryGroup, n1 = min(NT, n0 + kCarryGroup);
+  float lam = gend[((int64_t)bh * NG + gi) * K + i];
+#pragma unroll 8
+  for (int n = n1 - 1; n >= n0; --n) {
+    const float2 m = ab[(cb + n) * K + i];
+    carry[(cb + n) * K + i] = lam;
+    lam = m.x * lam + m.y;
+  }
+}
+
 __global__ __launch_bounds__(256) void diag_gain_bwd_emit_v_kernel(
     const float* __restrict__ k, const float* __restrict__ alpha, const float* __restrict__ omega,
     const float* __restrict__ r, const float* __restrict__ dkappa, const float* __restrict__ p_prev,
@@ -994,8 +1066,10 @@ int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const f
 
 size_t kdn_diag_gain_workspace_size(int B, int T, int H, int K) {
   const int64_t NT = cdiv(T, kVecChunk);  // covers both chunkings (kVecChunk <= kGainChunk)
-  // maps (4) + carry (1) per (b, h, chunk, channel), plus [B,H,K] precision partials
-  return (size_t)((int64_t)B * H * NT * K * 5 + (int64_t)B * H * K) * sizeof(float);
+  // maps (4) + carry (1) per (b, h, chunk, channel), [B,H,K] precision partials, then the two-level
+  // carry's group composites (4) and group start values (1)
+  return (size_t)((int64_t)B * H * NT * K * 5 + (int64_t)B * H * K +
+                  (int64_t)B * H * cdiv(NT, kCarryGroup) * K * 5) * sizeof(float);
 }
 
 int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, const float* r,
@@ -1014,8 +1088,21 @@ int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, co
     float* carry_v = maps + (int64_t)B * H * NV * K * 4;
     hipLaunchKernelGGL(diag_gain_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r, B, T,
                        H, K, NV, info_scale, maps);
-    hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)maps,
-                       initial_precision, prec_mode, H, K, NV, carry_v, final_precision);
+    if (NV > 2 * kCarryGroup) {  // two-level carry
+      const int NG = cdiv(NV, kCarryGroup);
+      float* grp = maps + (int64_t)B * H * NV * K * 5 + (int64_t)B * H * K;
+      float4* gmaps = reinterpret_cast<float4*>(grp);
+      float* gstart = grp + (int64_t)B * H * NG * K * 4;
+      hipLaunchKernelGGL(diag_gain_group_map_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float4*)maps, K, NV,
+                         NG, gmaps);
+      hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)gmaps,
+                         initial_precision, prec_mode, H, K, NG, gstart, final_precision);
+      hipLaunchKernelGGL(diag_gain_group_fill_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float4*)maps,
+                         gstart, K, NV, NG, carry_v);
+    } else {
+      hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)maps,
+                         initial_precision, prec_mode, H, K, NV, carry_v, final_precision);
+    }
     hipLaunchKernelGGL(diag_gain_emit_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
                        carry_v, B, T, H, K, NV, info_scale, kappa, p_prev, D);
     KDN_CHECK_LAUNCH();
@@ -1056,8 +1143,21 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
     dpart = dpart_v;
     hipLaunchKernelGGL(diag_gain_bwd_map_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
                        dkappa, p_prev, D, B, T, H, K, NV, info_scale, ab, G_scratch);
-    hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)ab,
-                       d_final_precision, final_precision, H, K, NV, carry_v);
+    if (NV > 2 * kCarryGroup) {  // two-level carry
+      const int NG = cdiv(NV, kCarryGroup);
+      float* grp = ab + (int64_t)B * H * NV * K * 5 + (int64_t)B * H * K;
+      float2* gab = reinterpret_cast<float2*>(grp);
+      float* gend = grp + (int64_t)B * H * NG * K * 4;
+      hipLaunchKernelGGL(diag_gain_bwd_group_map_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float2*)ab, K,
+                         NV, NG, gab);
+      hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)gab,
+                         d_final_precision, final_precision, H, K, NG, gend);
+      hipLaunchKernelGGL(diag_gain_bwd_group_fill_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float2*)ab,
+                         gend, K, NV, NG, carry_v);
+    } else {
+      hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)ab,
+                         d_final_precision, final_precision, H, K, NV, carry_v);
+    }
     hipLaunchKernelGGL(diag_gain_bwd_emit_v_kernel, dim3(cdiv(tiles, tpb)), dim3(256), 0, stream, k, alpha, omega, r,
                        dkappa, p_prev, D, G_scratch, carry_v, omega_raw, r_raw, initial_precision, prec_mode, B, T, H,
                        K, NV, info_scale, dk, dalpha, domega_raw, dr_raw, dpart_out_v);
