@@ -640,4 +640,380 @@ __global__ __launch_bounds__(256, 2) void contrib_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// solve + contrib in one kernel: the transposed solves of solve_kernel, then the gradients of
+// contrib_kernel, with dKg and dN kept on chip instead of a round trip through HBM.
+//  * Solve phase.  The V blocks of d delta go to the waves round-robin as in solve_kernel (dv is
+//    stored).  The K columns are taken per wave as contrib's channel tiles it = w + 4 u: the D tiles
+//    of dKg^T then give each lane 4 consecutive channels of one chunk row -- the elementwise
+//    operand layout of the contrib phase -- so they stay in registers (kg[u][tl]).
+//  * The per-wave dN^T partials are summed in the order of solve_kernel straight into the dN
+//    staging units of the contrib phase (dN = minus their sum, strictly lower).
+//  * LDS: the solve phase's A^T and partials (57 KB) and the contrib phase's fragments (64 KB)
+//    share one buffer: the partials are read into registers before the fragments are written.
+// grid (NT, B*H), block 256.  Chunks flagged by the forward are left to the exact kernels.
+// ---------------------------------------------------------------------------------------------
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256, 2) void solve_contrib_kernel(
+    const float* __restrict__ At, const float* __restrict__ dDl, const float* __restrict__ dWg,
+    const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, const float* __restrict__ dMg, const float* __restrict__ dQg,
+    const float* __restrict__ dKf, const float* __restrict__ dgl, int T, int H, int NT, float scale,
+    bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap,
+    float* __restrict__ dbeta, float* __restrict__ dg) {
+  constexpr int NIT = K / 16;
+  constexpr int ITW = (NIT + 3) / 4;  // channel tiles per wave (1 or 2)
+  constexpr int FR = 8 * TILE;        // one 64 x 64 operand as (4 row tiles x 2 k-blocks) fragments
+  constexpr int AP4 = C + 4;          // LDS row stride of A^T
+  constexpr int SOLVE_FLOATS = C * AP4 + 4 * 10 * 256;
+  constexpr int LDS_BYTES = SOLVE_FLOATS * 4 > 4 * FR * 2 ? SOLVE_FLOATS * 4 : 4 * FR * 2;
+  static_assert(ITW == 1 || ITW == 2, "K in {64, 128}");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+  __shared__ float sBeta[4 * C];
+  float* sAt = reinterpret_cast<float*>(smem);
+  float* sP = sAt + C * AP4;                        // per-wave partial dN^T tiles
+  bf16_t* sF = reinterpret_cast<bf16_t*>(smem);    // contrib phase: dN, dM, dN^T, dM^T fragments
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int64_t chunk = (int64_t)bh * NT + n;
+  if (flags[chunk]) return;
+
+  // ================================ solve phase ================================
+  {
+    const bufrsrc rA = make_buf(At + chunk * C * C, C * C * 4);
+#pragma unroll
+    for (int u = 0; u < C * C / 4 / 256; ++u) {
+      const int e4 = tid + 256 * u, sr = e4 / (C / 4), c4 = e4 % (C / 4);
+      *reinterpret_cast<float4*>(sAt + sr * AP4 + 4 * c4) = buf_ld4(rA, (sr * C + 4 * c4) * 4);
+    }
+  }
+  __syncthreads();
+
+  const bufrsrc rdv = make_buf(dv + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * 2);
+  f32x4 part[10];
+#pragma unroll
+  for (int t = 0; t < 10; ++t) part[t] = zero4();
+  f32x4 kg[ITW][4];  // dKg^T tiles of this wave's channel tiles: lane -> row 16 J + r16, 4 channels
+
+  // One column block: two 16-column tiles at columns cA, cB (cB < 0: absent) of X ([T][D] d delta or
+  // dW) and Y ([T][D] U or W).  Y^T tiles Yt = X^T A for the four time blocks, then this block's
+  // share of dN^T = (U|W) Y.
+  auto solve_block = [&](const float* Xg, const float* Yg, int D, int cA, int cB, f32x4 (&Yt)[2][4]) {
+    const bufrsrc rX = make_buf(Xg + ((int64_t)bh * T + t0) * D, L * D * 4);
+    const bufrsrc rY = make_buf(Yg + ((int64_t)bh * T + t0) * D, L * D * 4);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int J = 0; J < 4; ++J) Yt[ct][J] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      uint4 xh[2], xl[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int col = ct == 0 ? cA : cB;
+        float xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          xv[j] = col >= 0 ? buf_ld(rX, ((32 * kb + 8 * g4 + j) * D + col + r16) * 4) : 0.f;
+        split8(xv, xh[ct], xl[ct]);
+      }
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        if (J > 2 * kb + 1) continue;  // A[c][s] = 0 for c < s
+        const float* row = sAt + (16 * J + r16) * AP4 + 32 * kb + 8 * g4;
+        const float4 a0 = *reinterpret_cast<const float4*>(row), a1 = *reinterpret_cast<const float4*>(row + 4);
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        uint4 ah, al;
+        split8(av, ah, al);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) Yt[ct][J] = mma3(xh[ct], xl[ct], ah, al, Yt[ct][J]);
+      }
+    }
+    uint4 uh[4], ul[4], yh[4], yl[4];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      const uint32_t sr = (uint32_t)(16 * J + r16);
+      const float4 a0 = buf_ld4(rY, (sr * D + cA + 4 * g4) * 4);
+      const float4 a1 = cB >= 0 ? buf_ld4(rY, (sr * D + cB + 4 * g4) * 4) : float4{0.f, 0.f, 0.f, 0.f};
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      split8(av, uh[J], ul[J]);
+      kdn_state::bfrag(Yt[0][J], Yt[1][J], yh[J], yl[J]);
+    }
+#pragma unroll
+    for (int t = 0; t < 10; ++t) {
+      int I, J;
+      lower_tile(t, I, J);
+      part[t] = mma3(uh[J], ul[J], yh[I], yl[I], part[t]);
+    }
+  };
+  // V blocks of d delta: dv^T tiles stored (bf16 [B,T,H,V])
+#pragma unroll 1
+  for (int vb = w; vb < V / 32; vb += 4) {
+    f32x4 Yt[2][4];
+    solve_block(dDl, U, V, 32 * vb, 32 * vb + 16, Yt);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int J = 0; J < 4; ++J) {
+        const uint32_t tr = (uint32_t)(16 * J + r16), x0 = (uint32_t)(32 * vb + 16 * ct + 4 * g4);
+        const f32x4 y = Yt[ct][J];
+        const uint32_t lo = (uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16);
+        const uint32_t hi = (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rdv, ((tr * H) * V + x0) * 2, 0, 0);
+      }
+  }
+  // K columns of dW: this wave's channel tiles w, w + 4 (ITW = 2) or w (ITW = 1); dKg^T kept
+  {
+    f32x4 Yt[2][4];
+    solve_block(dWg, W, K, 16 * w, ITW == 2 ? 16 * (w + 4) : -1, Yt);
+#pragma unroll
+    for (int u = 0; u < ITW; ++u)
+#pragma unroll
+      for (int J = 0; J < 4; ++J) kg[u][J] = Yt[u][J];
+  }
+#pragma unroll
+  for (int t = 0; t < 10; ++t) *reinterpret_cast<f32x4*>(sP + ((w * 10 + t) * 64 + lane) * 4) = part[t];
+  __syncthreads();
+
+  // ======================= dN, dM staging (contrib's fragments) =======================
+  // unit (row c, kb, hh, gg) -> 4 consecutive s = k0 .. k0+3 of one lane's fragment slots
+  float4 dNu[4], dMu[4];
+  {
+    const bufrsrc rM = make_buf(dMg + chunk * C * C, C * C * 4);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
+      const int k0 = 32 * kb + 16 * hh + 4 * gg;
+      dMu[u] = buf_ld4(rM, (row * C + k0) * 4);
+      // dN[c][s] = -sum over the waves' dN^T partials, strictly lower (s < c); D layout of tile
+      // (c-block I, s-block J): lane (c % 16) + 16 ((s % 16) / 4), slot s % 4
+      float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+      if ((k0 >> 4) <= (row >> 4)) {
+        const int t = lower_tile_index(row >> 4, k0 >> 4), ln = (row & 15) + 16 * ((k0 & 15) >> 2);
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+          const float4 v = *reinterpret_cast<const float4*>(sP + ((ww * 10 + t) * 64 + ln) * 4);
+          acc.x -= v.x, acc.y -= v.y, acc.z -= v.z, acc.w -= v.w;
+        }
+        if (k0 + 0 >= row) acc.x = 0.f;
+        if (k0 + 1 >= row) acc.y = 0.f;
+        if (k0 + 2 >= row) acc.z = 0.f;
+        if (k0 + 3 >= row) acc.w = 0.f;
+      }
+      dNu[u] = acc;
+    }
+  }
+  __syncthreads();  // every partial read before the fragments overwrite them
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
+    const int k0 = 32 * kb + 16 * hh + 4 * gg;
+    const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
+    const float4 a = dNu[u], bq = dMu[u];
+    kdn_state::put_unit(sF, off, a.x, a.y, a.z, a.w);
+    kdn_state::put_unit(sF + FR, off, bq.x, bq.y, bq.z, bq.w);
+    const int rk = row & 31, tg = (rk & 15) >> 2, ts = (rk & 3) + 4 * (rk >> 4);
+    const float xv[4] = {a.x, a.y, a.z, a.w}, yv[4] = {bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sr = k0 + j;
+      const int toff = ((sr >> 4) * 2 + (row >> 5)) * TILE + ((sr & 15) + 16 * tg) * 8 + ts;
+      const bf16_t xhi = f2bf(xv[j]), yhi = f2bf(yv[j]);
+      sF[2 * FR + toff] = xhi;
+      sF[2 * FR + toff + 512] = f2bf(xv[j] - bf2f(xhi));
+      sF[3 * FR + toff] = yhi;
+      sF[3 * FR + toff + 512] = f2bf(yv[j] - bf2f(yhi));
+    }
+  }
+  __syncthreads();
+
+  // ================================ contrib phase ================================
+  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
+  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
+  const bufrsrc rdkap = ISO ? make_buf(dkap, 0) : make_buf(dkap + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rdg = make_buf(dg + in_row0 * K, rows_in * K * 4);
+  const bufrsrc rdQg = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
+  const bufrsrc rdKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
+  float bpart[4];  // iso: dbeta partials of rows 16 tl + r16
+#pragma unroll
+  for (int p = 0; p < 4; ++p) bpart[p] = 0.f;
+
+#pragma unroll 1
+  for (int u = 0; u < ITW; ++u) {
+    const int it = w + 4 * u;
+    const int i = 16 * it + r16;
+    f32x4 kgu[4];  // this tile's dKg (a select, not a runtime index, keeps kg in registers)
+#pragma unroll
+    for (int J = 0; J < 4; ++J) kgu[J] = (ITW == 1 || u == 0) ? kg[0][J] : kg[ITW - 1][J];
+    int lg4 = g4, lr16 = r16;
+    asm volatile("" : "+v"(lg4), "+v"(lr16));
+    float av[16], Gv[16];
+    uint16_t kraw[16], qraw[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const int c = 16 * (p >> 2) + 4 * lg4 + (p & 3);
+      const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
+      kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
+      qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
+      av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);
+      Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float mA[4];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) mA[J] = 0.5f * (__shfl(Gv[4 * J], r16, 64) + __shfl(Gv[4 * J + 3], 48 + r16, 64));
+    float Rown[16], Kown[16], Qown[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const float kvp = bf2f(kraw[p]), e = exp2f(Gv[p] - mA[p >> 2]);
+      Kown[p] = kvp * e;
+      Qown[p] = scale * bf2f(qraw[p]) * e;
+      Rown[p] = (ISO ? av[p] * kvp : av[p]) * __frcp_rn(e);
+    }
+    const int i0 = 16 * it + 4 * g4;
+    const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
+    u32x2 kq4[4], qq4[4];
+    float4 kap4[4], G4[4], dqg4[4], dkf4[4];
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      const uint32_t c = (uint32_t)(16 * tl + lr16), o = c * H * K + i0, ol = c * K + i0;
+      kq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rk, o * 2, 0, 0);
+      qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
+      if (ISO) {
+        const float be = buf_ld(rkap, c * H * 4);
+        kap4[tl] = float4{be, be, be, be};
+      } else {
+        kap4[tl] = buf_ld4(rkap, o * 4);
+      }
+      G4[tl] = buf_ld4(rG, ((uint32_t)(min(16 * tl + lr16, L - 1) * H) * K + i0) * 4);
+      dqg4[tl] = buf_ld4(rdQg, ol * 4);
+      dkf4[tl] = buf_ld4(rdKf, ol * 4);
+    }
+    float colpart[4] = {0.f, 0.f, 0.f, 0.f};
+    float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
+    bool has_last = false;
+    const float gla[4] = {glv.x, glv.y, glv.z, glv.w};
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      f32x4 dLk = zero4(), dLq = zero4(), dR = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        uint4 ah, al;
+        if (kb <= tl / 2) {
+          const float s0 = 2 * kb <= tl ? exp2f(mA[tl] - mA[2 * kb]) : 0.f;
+          const float s1 = 2 * kb + 1 <= tl ? exp2f(mA[tl] - mA[2 * kb + 1]) : 0.f;
+          float rv[8];
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) rv[sl] = Rown[8 * kb + sl] * (sl < 4 ? s0 : s1);
+          uint4 Rh, Rl;
+          split8(rv, Rh, Rl);
+          afrag(sF, tl * 2 + kb, lane, ah, al);
+          dLk = mma3(Rh, Rl, ah, al, dLk);
+          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
+          dLq = mma3(Rh, Rl, ah, al, dLq);
+        }
+        if (2 * kb + 1 >= tl) {
+          const float s0 = 2 * kb >= tl ? exp2f(mA[2 * kb] - mA[tl]) : 0.f;
+          const float s1 = 2 * kb + 1 >= tl ? exp2f(mA[2 * kb + 1] - mA[tl]) : 0.f;
+          float lk[8], lq[8];
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) {
+            const float sc = sl < 4 ? s0 : s1;
+            lk[sl] = Kown[8 * kb + sl] * sc;
+            lq[sl] = Qown[8 * kb + sl] * sc;
+          }
+          uint4 Kh, Kl, Qh, Ql;
+          split8(lk, Kh, Kl);
+          split8(lq, Qh, Ql);
+          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
+          dR = mma3(Kh, Kl, ah, al, dR);
+          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
+          dR = mma3(Qh, Ql, ah, al, dR);
+        }
+      }
+      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
+      const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
+                            __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
+      const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
+                            __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
+      const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
+      const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
+      const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
+                           __shfl(mA[tl], 4 * g4 + 3, 64)};
+      const f32x4 kgt = kgu[tl];
+      const float dkgv[4] = {kgt[0], kgt[1], kgt[2], kgt[3]};
+      const float dqgv[4] = {dqg4[tl].x, dqg4[tl].y, dqg4[tl].z, dqg4[tl].w};
+      const float dkfv[4] = {dkf4[tl].x, dkf4[tl].y, dkf4[tl].z, dkf4[tl].w};
+      float dkv[4], dqv[4], dav[4], dgv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float beta = ISO ? a4[j] : 0.f;
+        const float kap_p = ISO ? beta * kv4[j] : a4[j];
+        const float e = exp2f(gv[j] - mz[j]), er = __frcp_rn(e);
+        const float eg = exp2f(gv[j]), f = exp2f(gla[j] - gv[j]);
+        const float a_lk = dLk[j], a_lq = dLq[j] * scale, a_r = dR[j];
+        dkv[j] = a_lk * e + dkgv[j] * eg;
+        dqv[j] = a_lq * e + scale * dqgv[j] * eg;
+        dav[j] = a_r * er + dkfv[j] * f;
+        dgv[j] = kv4[j] * e * a_lk + qv4[j] * e * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv[j] +
+                 scale * qv4[j] * eg * dqgv[j] - kap_p * f * dkfv[j];
+        if ((int)c < L) colpart[j] += kap_p * f * dkfv[j];
+        if (ISO) {
+          dkv[j] += beta * dav[j];
+          bpart[tl] += dav[j] * kv4[j];
+        }
+      }
+      if (!ISO)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(dav[0]), __float_as_uint(dav[1]), __float_as_uint(dav[2]), __float_as_uint(dav[3])},
+            rdkap, o * 4, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16), (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
+          rdq, o * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16), (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
+          rdk, o * 2, 0, 0);
+      if ((int)c == L - 1) {
+        dg_last = float4{dgv[0], dgv[1], dgv[2], dgv[3]};
+        has_last = true;
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(dgv[0]), __float_as_uint(dgv[1]), __float_as_uint(dgv[2]), __float_as_uint(dgv[3])},
+            rdg, o * 4, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) colpart[j] += __shfl_xor(colpart[j], m, 64);
+    if (has_last) {
+      const float4 gl4 = *reinterpret_cast<const float4*>(dgl + chunk * K + i0);
+      const float4 v = float4{dg_last.x + colpart[0] + gl4.x, dg_last.y + colpart[1] + gl4.y,
+                              dg_last.z + colpart[2] + gl4.z, dg_last.w + colpart[3] + gl4.w};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rdg,
+                                             ((uint32_t)((L - 1) * H) * K + i0) * 4, 0, 0);
+    }
+  }
+  if (ISO) {
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      float v = bpart[tl];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (g4 == 0) sBeta[w * C + 16 * tl + r16] = v;
+    }
+    __syncthreads();
+    if (tid < L) dbeta[((int64_t)b * T + t0 + tid) * H + h] = sBeta[tid] + sBeta[C + tid] + sBeta[2 * C + tid] +
+                                                               sBeta[3 * C + tid];
+  }
+}
+
 }  // namespace kdn_bwd

@@ -921,10 +921,8 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
                        NT, dQg, dW, dKf, dM, dgl);
     KDN_CHECK_LAUNCH();
   }
-  if (stages & 4) {
+  if (stages & 4) {  // the chunks left to the exact path: transposed solves into dv, dKg, dN
     const int NB = B * H * NT, gx = min(NB, 512);
-    hipLaunchKernelGGL((kdn_bwd::solve_kernel<K, V>), gchunk, dim3(256), 0, stream, A, dD, dW, U, W, flags, T, H, NT, dv,
-                       dKg, dN);
     if (iso)
       hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD, dW,
                          U, W, T, H, NT, NB, flags, dv, dKg, dN);
@@ -935,14 +933,14 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   }
   if (stages & 8) {
     const int NB = B * H * NT, gx = min(NB, 512);
-    if (iso) {
-      hipLaunchKernelGGL((kdn_bwd::contrib_kernel<K, true>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM, dQg,
-                         dKg, dKf, dgl, flags, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+    if (iso) {  // solves and gradients of every other chunk in one kernel; then the exact path's gradients
+      hipLaunchKernelGGL((kdn_bwd::solve_contrib_kernel<K, V, true>), gchunk, dim3(256), 0, stream, A, dD, dW, U, W,
+                         flags, q, k, kap, gc, dM, dQg, dKf, dgl, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg);
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc, dN,
                          dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
     } else {
-      hipLaunchKernelGGL((kdn_bwd::contrib_kernel<K, false>), gchunk, dim3(256), 0, stream, q, k, kap, gc, dN, dM, dQg,
-                         dKg, dKf, dgl, flags, T, H, NT, scale, dq, dk, dkap, dbeta, dg);
+      hipLaunchKernelGGL((kdn_bwd::solve_contrib_kernel<K, V, false>), gchunk, dim3(256), 0, stream, A, dD, dW, U, W,
+                         flags, q, k, kap, gc, dM, dQg, dKf, dgl, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg);
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc,
                          dN, dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
     }

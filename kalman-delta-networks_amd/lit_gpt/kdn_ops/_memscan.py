@@ -10,7 +10,9 @@ import torch
 from . import _lib
 
 FWD_STAGES = ((1, "mem_intra_fwd"), (2, "mem_state_fwd"), (4, "mem_readout_fwd"))
-BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_hgrad"), (4, "mem_bwd_solve"), (8, "mem_bwd_contrib"))
+# bit 4: the transposed solves of the chunks left to the exact path; bit 8: solves + gradients of
+# every other chunk in one kernel, then the exact path's gradients
+BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_hgrad"), (4, "mem_bwd_exact_solve"), (8, "mem_bwd_solve_contrib"))
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
