@@ -589,6 +589,8 @@ def main():
                     help="measure only the long-context diag forward (config 3) and print its line")
     ap.add_argument("--config4-only", action="store_true",
                     help="measure only the whole model (config 4) and print its line (for profiling)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the main variant's step and print its line (for profiling)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain copy of MIB MiB (PMC byte-counter calibration)")
     ap.add_argument("--B", type=int, default=4)
@@ -622,6 +624,14 @@ def main():
         return
     other = "diag" if main_v == "iso" else "iso"
     res = run_variant(main_v, args.steps, args.warmup, B, T, H, K)
+    if args.headline_only:
+        if args.calib_copy:
+            calib_copy(args.calib_copy)
+        print(json.dumps({"metric": METRIC, "value": round(res["tokens_per_s"], 1), "unit": "tokens/s",
+                          "ms_per_step": round(res["ms_per_step"], 4), "steps": args.steps, "warmup": args.warmup,
+                          "op_roofline": op_roofline(main_v, res["ms_per_step"], B, T, H, K),
+                          "kernels": res["kernels"]}), flush=True)
+        return
     res_other = run_variant(other, args.steps, args.warmup, B, T, H, K)
     dom = res["kernels"][res["dominant"]]
     cfg_key = f"{main_v} B{B} T{T} H{H} d{K}"
