@@ -100,19 +100,18 @@ def frontend_counts(variant: str, B: int, T: int, H: int, K: int):
             "l2norm_bwd": 6 * E + 4 * N,
         }
     else:
+        # the scan's front half runs fused (normalisation -> frontend -> gain, lit_gpt/kdn_ops/diag_kdn_chunk.py
+        # diag_kdn_front): alpha, omega, r and the fp32 gain key never reach HBM
         per = {
-            # q, k bf16 -> q_memory bf16, k_gain f32, k_memory bf16, two norms
-            "diag_norm_fwd": 12 * E + 8 * N,
-            # q, k, norms, d q_memory bf16, d k_gain f32, d k_memory bf16 -> dq, dk bf16
-            "diag_norm_bwd": 16 * E + 8 * N,
-            # retention, omega raw bf16, r raw bf16 -> g_cumsum, alpha, omega f32, r
-            "diag_frontend_fwd": 16 * E + 6 * N,
-            # retention raw, alpha, d g_cumsum, d alpha -> d retention raw bf16
-            "diag_frontend_bwd": 16 * E,
-            # k, alpha, omega f32, r -> kappa, p_prev f32, D
-            "diag_gain_fwd": 20 * E + 8 * N,
-            # k, alpha, omega, r, dkappa, p_prev, D, omega raw, r raw -> dk, dalpha f32, d omega raw, d r raw
-            "diag_gain_bwd": 32 * E + 12 * N,
+            # q, k bf16 -> q_memory, k_memory bf16, two norms
+            "diag_front_norm_fwd": 8 * E + 8 * N,
+            # k bf16, k norm, retention, omega raw bf16, r raw bf16 -> g_cumsum, kappa f32
+            "diag_front_fwd": 14 * E + 6 * N,
+            # k, k norm, retention, omega raw, r raw, d g_cumsum, d kappa f32, d k_memory bf16
+            #   -> dk, d retention raw, d omega raw bf16, d r raw
+            "diag_front_bwd": 22 * E + 8 * N,
+            # q bf16, q norm, d q_memory bf16 -> dq bf16
+            "diag_front_norm_bwd": 6 * E + 4 * N,
         }
     return {k: (b, 0) for k, b in per.items()}
 
@@ -497,8 +496,7 @@ def run_config3(steps: int, warmup: int, B: int = 1, T: int = 32768, H: int = 18
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
-    fwd_tags = ("diag_norm_fwd", "diag_frontend_fwd", "diag_gain_fwd", "mem_intra_fwd", "mem_state_fwd",
-                "mem_readout_fwd")
+    fwd_tags = ("diag_front_norm_fwd", "diag_front_fwd", "mem_intra_fwd", "mem_state_fwd", "mem_readout_fwd")
     counts = kernel_counts("diag", B, T, H, K, K)
     counts.update(frontend_counts("diag", B, T, H, K))
     kernels = {}

@@ -134,6 +134,39 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
                       float* dk, float* dalpha, uint16_t* domega_raw, uint16_t* dr_raw, float* d_initial_precision,
                       float* G_scratch, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------- fused diag frontend + gain */
+/* The front half of the layer composition (reference lit_gpt/diag_kdn.py:315-345): the gain key
+ * k / max(||k||, 1e-12) of _diag_kdn_normalize (diag_kdn_chunk.py:2162-2168), the frontend
+ * _diag_kdn_frontend_precumsum_paired (:2471-2495) and the gain _diag_kdn_gain (:2737-2791) in
+ * one op whose passes recompute alpha, omega, r and the fp32 key per token instead of passing them
+ * through memory.  k_raw [B,T,H,K] (bf16 or f32) with its row norms k_norm [B,T,H] (kdn_diag_norm_fwd
+ * writes them; its k_gain output may then be null).  The prior precision is mu = 0.1 +
+ * softplus(mu_param) [H] (mu_param non-null, initial_precision null, prec_mode 0) or an explicit
+ * initial_precision [H] (prec_mode 0) or [B,H,K] (prec_mode 1).  Outputs g_cumsum and kappa
+ * [B,T,H,K] f32; final_precision [B,H,K] nullable; saved (kdn_diag_front_saved_size bytes,
+ * nullable for a forward-only call) keeps the per-16-token-tile entry precision the backward
+ * replays.  K in {64, 128}, chunk a multiple of 16, 16-byte aligned arrays. */
+size_t kdn_diag_front_saved_size(int B, int T, int H, int K);
+size_t kdn_diag_front_workspace_size(int B, int T, int H, int K);
+int kdn_diag_front_fwd(const void* k_raw, int k_bf16, const float* k_norm, const uint16_t* retention_raw,
+                       const uint16_t* omega_raw, const uint16_t* r_raw, const float* A_log, const float* dt_bias,
+                       const float* mu_param, const float* initial_precision, int prec_mode, int B, int T, int H,
+                       int K, int chunk, float info_scale, float* g_cumsum, float* kappa, float* final_precision,
+                       float* saved, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* Backward of kdn_diag_front_fwd: _diag_kdn_gain_backward (diag_kdn_chunk.py:2569-2683), the
+ * frontend backward (:2265-2423) and the k part of _diag_kdn_norm_backward (:2079-2159), which
+ * takes d_k_memory (bf16, nullable) so dk_raw (nullable) is the VJP of dk_gain + dk_memory.
+ * d_retention_raw, d_omega_raw, d_r_raw are bf16 and required; dA_log, ddt_bias, d_mu_param
+ * (with mu_param) and d_initial_precision (without) are nullable. */
+int kdn_diag_front_bwd(const void* k_raw, int k_bf16, const float* k_norm, const uint16_t* retention_raw,
+                       const uint16_t* omega_raw, const uint16_t* r_raw, const float* A_log, const float* dt_bias,
+                       const float* mu_param, const float* initial_precision, int prec_mode, const float* saved,
+                       const float* final_precision, const float* d_g_cumsum, const float* d_kappa,
+                       const uint16_t* d_k_memory, const float* d_final_precision, int B, int T, int H, int K,
+                       int chunk, float info_scale, void* dk_raw, uint16_t* d_retention_raw, uint16_t* d_omega_raw,
+                       uint16_t* d_r_raw, float* dA_log, float* ddt_bias, float* d_mu_param,
+                       float* d_initial_precision, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---------------------------------------------------------------- memory scan */
 int kdn_mem_chunk_size(void);
 /* Chunk groups the serial state passes of kdn_mem_fwd / kdn_mem_bwd use at this shape (1: a single

@@ -336,26 +336,6 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
   }
 }
 
-// out[j] = sum_p part[p * stride + j] for j < n, deterministic order: block = 64 outputs x 4
-// partial stripes (each 8-way unrolled over p), stripes combined in order.  grid ceil(n/64).
-__global__ __launch_bounds__(256) void reduce_partials_vec_kernel(const float* __restrict__ part, int NP,
-                                                                  int64_t stride, int n, float* __restrict__ out) {
-  __shared__ float s[4][64];
-  const int jj = threadIdx.x & 63, st4 = threadIdx.x >> 6, j = blockIdx.x * 64 + jj;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (j < n) {
-    int pp = st4;
-    for (; pp + 28 < NP; pp += 32) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) acc[q] += part[(int64_t)(pp + 4 * q) * stride + j];
-    }
-    for (; pp < NP; pp += 4) acc[0] += part[(int64_t)pp * stride + j];
-  }
-  s[st4][jj] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-  __syncthreads();
-  if (st4 == 0 && j < n) out[j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
-}
-
 // out[j] = sum_p part[p * stride + j] for j < n, deterministic order.  grid ceil(n/256).
 __global__ void reduce_partials_kernel(const float* __restrict__ part, int NP, int64_t stride, int n,
                                        float* __restrict__ out) {
@@ -512,7 +492,7 @@ __global__ __launch_bounds__(256) void diag_norm_fwd_kernel(const TX* __restrict
     if (c < K) {
       q_mem[row * K + c] = f2bf(qv[j] / dq);
       const float kn = kv[j] / dk;
-      k_gain[row * K + c] = kn;
+      if (k_gain) k_gain[row * K + c] = kn;
       k_mem[row * K + c] = f2bf(kn);
     }
   }
@@ -833,7 +813,7 @@ __global__ __launch_bounds__(256) void diag_norm_fwd_vec_kernel(const TX* __rest
     kv[j] *= ik;
   }
   store8<bf16_t>(q_mem + row * K + 8 * sub, qv);
-  store8<float>(k_gain + row * K + 8 * sub, kv);
+  if (k_gain) store8<float>(k_gain + row * K + 8 * sub, kv);  // null: the fused gain recomputes it
   store8<bf16_t>(k_mem + row * K + 8 * sub, kv);
   if (sub == 0) {
     q_norm[row] = nq;

@@ -14,6 +14,7 @@
 //   map / carry / emit passes over 64-token chunks, one workgroup per (chunk, b, h),
 //   thread = key channel; the per-token cross-channel sums are wave reductions whose
 //   partials are deferred to LDS so no barrier sits inside the token loop.
+#include <algorithm>
 #include <mutex>
 
 #include "kdn_common.h"
@@ -950,6 +951,465 @@ __global__ void sum_over_batch_kernel(const float* __restrict__ part, int B, int
   out[h] = s;
 }
 
+// ----------------------------------------------------------------------------
+// Fused diag frontend + gain ("front").  The layer composition (reference lit_gpt/diag_kdn.py:315-345)
+// runs the q/k normalisation, the retention frontend and the vector gain back to back, and the
+// frontend's alpha, omega, r and the normalised fp32 key feed only the gain.  Here the gain's map and
+// emit passes recompute them per token from the raw bf16 logits and the raw key with its row norm,
+// using the standalone kernels' own operations, and the emit pass also writes the chunk-local base-2
+// log-decay prefix g_cumsum.  So alpha, omega and the fp32 key are never written or read back.
+// The backward replays each 16-token tile's precision from the tile's saved entry value (the
+// forward's carry, B*H*NV*K floats) instead of reading a stored p_prev [B,T,H,K], and finishes
+// with the raw-logit, decay-parameter and key-normalisation VJPs in the same pass.
+// Tiles are the vectorised gain's: (b, h, 16 tokens) x K channels, kCPT channels per thread.
+// ----------------------------------------------------------------------------
+// Addresses in the fused kernels are 32-bit element offsets from a kernel-argument base (the
+// scalar-base + vector-offset form, one offset register per access instead of a 64-bit address
+// pair); the host splits a launch over the batch so every array stays below 2^30 elements.
+template <typename T> __device__ __forceinline__ T* off32(T* base, uint32_t elem) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(base) + elem * (uint32_t)sizeof(T));
+}
+template <typename T> __device__ __forceinline__ const T* off32(const T* base, uint32_t elem) {
+  return reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + elem * (uint32_t)sizeof(T));
+}
+__device__ __forceinline__ uint32_t front_row(const GainTile& g, int T, int H, int t) {
+  return ((uint32_t)g.b * (uint32_t)T + (uint32_t)t) * (uint32_t)H + (uint32_t)g.h;
+}
+constexpr float kFloorLog = -13.815510557964274f;  // log(1e-6): the memory path's alpha floor
+
+template <typename TX> __device__ __forceinline__ void ldk4(const TX* p, float* f);
+template <> __device__ __forceinline__ void ldk4<float>(const float* p, float* f) { ldcf(p, f); }
+template <> __device__ __forceinline__ void ldk4<bf16_t>(const bf16_t* p, float* f) { ldc_bf16(p, f); }
+template <typename TX> __device__ __forceinline__ void stk4(TX* p, const float* f);
+template <> __device__ __forceinline__ void stk4<float>(float* p, const float* f) { stcf(p, f); }
+template <> __device__ __forceinline__ void stk4<bf16_t>(bf16_t* p, const float* f) { stc_bf16(p, f); }
+
+template <typename TX>
+struct FrontArgs {
+  const TX* k;           // key before normalisation [B,T,H,K]
+  const float* knorm;    // its row norms ||k|| [B,T,H]
+  const bf16_t* f;       // retention logits [B,T,H,K]
+  const bf16_t* z;       // omega logits [B,T,H,K]
+  const bf16_t* y;       // r logits [B,T,H]
+  const float* A_log;    // [H]
+  const float* dt_bias;  // [H,K]
+  int B, T, H, K, NV;    // NV 16-token tiles per (b, h) stream
+  int tpc;               // tiles per decay chunk (chunk / 16)
+  float s;               // info scale
+};
+
+// Raw inputs of one token for one thread's kCPT channels.  bf16 values stay packed until use, which
+// keeps the loads of two tokens in flight within the register budget.
+struct Bf4 {
+  uint2 v;
+};
+__device__ __forceinline__ Bf4 ldbf4(const bf16_t* p) { return Bf4{*reinterpret_cast<const uint2*>(p)}; }
+__device__ __forceinline__ float bfj(const Bf4& b, int j) {
+  const uint32_t w = j < 2 ? b.v.x : b.v.y;
+  return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+template <typename TX> struct K4;
+template <> struct K4<bf16_t> {
+  Bf4 b;
+  __device__ __forceinline__ void load(const bf16_t* p) { b = ldbf4(p); }
+  __device__ __forceinline__ float operator[](int j) const { return bfj(b, j); }
+};
+template <> struct K4<float> {
+  float4 v;
+  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ float operator[](int j) const { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
+};
+template <typename TX>
+struct FrontRaw {
+  K4<TX> k;
+  Bf4 f, z;
+  float kn, y;
+};
+template <typename TX>
+__device__ __forceinline__ void front_load(const FrontArgs<TX>& a, uint32_t row, int i0, FrontRaw<TX>& r) {
+  const uint32_t e = row * (uint32_t)a.K + (uint32_t)i0;
+  r.k.load(off32(a.k, e));
+  r.f = ldbf4(off32(a.f, e));
+  r.z = ldbf4(off32(a.z, e));
+  r.kn = *off32(a.knorm, row);
+  r.y = bf2f(*off32(a.y, row));
+}
+// The gain's per-token inputs, as the standalone kernels form them: kt = k / max(||k||, 1e-12),
+// ell = -e^A softplus(f + dt_bias), alpha = e^ell, omega = softplus(z); returns r = 0.01 + softplus(y).
+template <typename TX>
+__device__ __forceinline__ float front_inputs(const FrontRaw<TX>& r, float rate, const float* bias, float* kt,
+                                              float* ell, float* al, float* wt) {
+  const float ik = 1.f / fmaxf(r.kn, 1e-12f);
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) {
+    kt[j] = r.k[j] * ik;
+    ell[j] = -rate * softplusf(bfj(r.f, j) + bias[j]);
+    al[j] = __expf(ell[j]);
+    wt[j] = softplusf(bfj(r.z, j));
+  }
+  return 0.01f + softplusf(r.y);
+}
+// the memory path's clamped log-decay (NaN propagates)
+__device__ __forceinline__ float ell_mem(float ell, float al) { return (al >= 1e-6f || al != al) ? ell : kFloorLog; }
+
+// Forward map: per channel the tile's composite Mobius map, and the tile's sum of clamped log-decays.
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_front_map_kernel(FrontArgs<TX> a, float* __restrict__ maps,
+                                                             float* __restrict__ tsum) {
+  constexpr int NB = 4;
+  const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
+  if (!g.ok) return;
+  const float rate = __expf(a.A_log[g.h]);
+  float bias[kCPT], es[kCPT];
+  ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
+  Map2 M[kCPT];
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) M[j] = Map2{1.f, 0.f, 0.f, 1.f}, es[j] = 0.f;
+  for (int t = g.t0; t < g.t1; t += NB) {
+    FrontRaw<TX> raw[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) front_load(a, front_row(g, a.T, a.H, min(t + u, g.t1 - 1)), g.i0, raw[u]);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (t + u >= g.t1) break;
+      float kt[kCPT], ell[kCPT], al[kCPT], wt[kCPT];
+      const float rt = front_inputs(raw[u], rate, bias, kt, ell, al, wt);
+      const float iru = 1.f / rt;
+#pragma unroll
+      for (int j = 0; j < kCPT; ++j) {
+        es[j] += ell_mem(ell[j], al[j]);
+        const float a2 = al[j] * al[j], uu = a.s * kt[j] * kt[j] * iru;
+        M[j] = map_mul(Map2{a2, wt[j], uu * a2, 1.f + uu * wt[j]}, M[j]);
+      }
+    }
+  }
+  const uint32_t tb = (((uint32_t)g.b * a.H + g.h) * a.NV + g.nt) * (uint32_t)a.K + g.i0;
+  float4* dst = reinterpret_cast<float4*>(off32(maps, tb * 4u));
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) dst[j] = float4{M[j].m0, M[j].m1, M[j].m2, M[j].m3};
+  stcf(off32(tsum, tb), es);
+}
+
+// Forward emit: kappa and g_cumsum per token from the tile's entry precision.  The decay prefix
+// starts from the sum of the earlier tiles of the same decay chunk.
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, const float* __restrict__ carry,
+                                                              const float* __restrict__ tsum,
+                                                              float* __restrict__ g_cumsum,
+                                                              float* __restrict__ kappa) {
+  constexpr int NB = 4;
+  const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
+  if (!g.ok) return;
+  const int tpt = a.K / kCPT;
+  const float rate = __expf(a.A_log[g.h]);
+  float bias[kCPT], p[kCPT], acc[kCPT];
+  ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
+  const uint32_t sb = ((uint32_t)g.b * a.H + g.h) * a.NV;
+  ldcf(off32(carry, (sb + g.nt) * (uint32_t)a.K + g.i0), p);
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) acc[j] = 0.f;
+  for (int n = g.nt - g.nt % a.tpc; n < g.nt; ++n) {
+    float e[kCPT];
+    ldcf(off32(tsum, (sb + n) * (uint32_t)a.K + g.i0), e);
+#pragma unroll
+    for (int j = 0; j < kCPT; ++j) acc[j] += e[j];
+  }
+  for (int t = g.t0; t < g.t1; t += NB) {
+    FrontRaw<TX> raw[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) front_load(a, front_row(g, a.T, a.H, min(t + u, g.t1 - 1)), g.i0, raw[u]);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (t + u >= g.t1) break;
+      const uint32_t row = front_row(g, a.T, a.H, t + u);
+      float kt[kCPT], ell[kCPT], al[kCPT], wt[kCPT], num[kCPT], gc[kCPT], sq = 0.f;
+      const float rt = front_inputs(raw[u], rate, bias, kt, ell, al, wt);
+      const float ir = 1.f / rt;
+#pragma unroll
+      for (int j = 0; j < kCPT; ++j) {
+        acc[j] += ell_mem(ell[j], al[j]);
+        gc[j] = acc[j] * KDN_LOG2E;
+        const float ph = al[j] * al[j] * p[j] + wt[j];
+        num[j] = ph * kt[j];
+        sq += num[j] * kt[j];
+        p[j] = ph / (1.f + a.s * kt[j] * kt[j] * ir * ph);
+      }
+      const float D = rt + tile_sum(sq, tpt), iD = 1.f / D;
+#pragma unroll
+      for (int j = 0; j < kCPT; ++j) num[j] *= iD;
+      stcf(off32(kappa, row * (uint32_t)a.K + (uint32_t)g.i0), num);
+      stcf(off32(g_cumsum, row * (uint32_t)a.K + (uint32_t)g.i0), gc);
+    }
+  }
+}
+
+// The backward passes need p_{t-1}, the precision entering each token, in reverse token order.  A
+// tile first replays its forward recurrence from its saved entry value and keeps the precision
+// entering every even token in LDS (kVecChunk / 2 float4 per thread, 8 KB per wave); the reverse
+// pass then takes the tokens in pairs (2q + 1, 2q) and re-derives the odd token's entry value with
+// one forward step of token 2q, whose inputs it has loaded anyway.
+constexpr int kPairs = kVecChunk / 2;
+__device__ __forceinline__ float4 f4(const float* x) { return float4{x[0], x[1], x[2], x[3]}; }
+__device__ __forceinline__ void unf4(float4 v, float* x) { x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w; }
+
+template <typename TX>
+__device__ __forceinline__ void front_replay(const FrontArgs<TX>& a, const GainTile& g, float rate, const float* bias,
+                                             const float* carry, float4 (*lp)[256]) {
+  constexpr int NB = 4;
+  const int L = g.t1 - g.t0;
+  float p[kCPT];
+  ldcf(off32(carry, (((uint32_t)g.b * a.H + g.h) * a.NV + g.nt) * (uint32_t)a.K + g.i0), p);
+  for (int t = 0; t < L; t += NB) {
+    FrontRaw<TX> raw[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) front_load(a, front_row(g, a.T, a.H, g.t0 + min(t + u, L - 1)), g.i0, raw[u]);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (t + u >= L) break;
+      if (((t + u) & 1) == 0) lp[(t + u) >> 1][threadIdx.x] = f4(p);
+      float kt[kCPT], ell[kCPT], al[kCPT], wt[kCPT];
+      const float ir = 1.f / front_inputs(raw[u], rate, bias, kt, ell, al, wt);
+#pragma unroll
+      for (int j = 0; j < kCPT; ++j) {
+        const float ph = al[j] * al[j] * p[j] + wt[j];
+        p[j] = ph / (1.f + a.s * kt[j] * kt[j] * ir * ph);
+      }
+    }
+  }
+}
+// One forward precision step of a token: p entering the next token.
+__device__ __forceinline__ void front_step(const float* pin, const float* kt, const float* al, const float* wt,
+                                           float ir, float s, float* pout) {
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) {
+    const float ph = al[j] * al[j] * pin[j] + wt[j];
+    pout[j] = ph / (1.f + s * kt[j] * kt[j] * ir * ph);
+  }
+}
+
+// Backward map (reverse over the tile): the affine adjoint map (A, B) per channel, the per-token
+// gain denominator D_t and G_t = sum_i dkappa_i p_hat_i k_i / D_t (saved for the emit pass), and the
+// tile's sum of the g_cumsum cotangent (for the emit pass's chunk-suffix sums).
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a, const float* __restrict__ carry,
+                                                                 const float* __restrict__ dkappa,
+                                                                 const float* __restrict__ dG, float* __restrict__ ab,
+                                                                 float* __restrict__ tdg, float* __restrict__ Gsave,
+                                                                 float* __restrict__ Dsave) {
+  __shared__ float4 lp[kPairs][256];
+  const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
+  if (!g.ok) return;
+  const int tpt = a.K / kCPT, L = g.t1 - g.t0;
+  const float rate = __expf(a.A_log[g.h]);
+  float bias[kCPT];
+  ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
+  front_replay(a, g, rate, bias, carry, lp);
+  float Aacc[kCPT], Bacc[kCPT], sg[kCPT];
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f, sg[j] = 0.f;
+#pragma unroll 1
+  for (int q = (L - 1) >> 1; q >= 0; --q) {
+    FrontRaw<TX> raw[2];
+    float dk_[2][kCPT], dg_[2][kCPT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {  // u = 0: token 2q + 1, u = 1: token 2q
+      const uint32_t row = front_row(g, a.T, a.H, g.t0 + min(2 * q + 1 - u, L - 1));
+      front_load(a, row, g.i0, raw[u]);
+      ldcf(off32(dkappa, row * (uint32_t)a.K + (uint32_t)g.i0), dk_[u]);
+      ldcf(off32(dG, row * (uint32_t)a.K + (uint32_t)g.i0), dg_[u]);
+    }
+    float kt[2][kCPT], ell[2][kCPT], al[2][kCPT], wt[2][kCPT], ir[2], rt[2], pp[2][kCPT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      rt[u] = front_inputs(raw[u], rate, bias, kt[u], ell[u], al[u], wt[u]);
+      ir[u] = 1.f / rt[u];
+    }
+    unf4(lp[q][threadIdx.x], pp[1]);
+    front_step(pp[1], kt[1], al[1], wt[1], ir[1], a.s, pp[0]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tt = 2 * q + 1 - u;
+      if (tt < L) {
+        float ph[kCPT], sq = 0.f, gp = 0.f;
+#pragma unroll
+        for (int j = 0; j < kCPT; ++j) {
+          ph[j] = al[u][j] * al[u][j] * pp[u][j] + wt[u][j];
+          const float num = ph[j] * kt[u][j];
+          sq += num * kt[u][j];
+          gp += dk_[u][j] * ph[j] * kt[u][j];
+        }
+        const float D = rt[u] + tile_sum(sq, tpt), iD = 1.f / D;
+        const float G = tile_sum(gp, tpt) * iD;
+#pragma unroll
+        for (int j = 0; j < kCPT; ++j) {
+          const float a2 = al[u][j] * al[u][j];
+          const float hh = 1.f + a.s * kt[u][j] * kt[u][j] * ir[u] * ph[j];
+          const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD;
+          const float At = a2 / (hh * hh);
+          Bacc[j] = At * Bacc[j] + a2 * pbar;
+          Aacc[j] = At * Aacc[j];
+          sg[j] += dg_[u][j];
+        }
+        if (g.sub == 0) {
+          const uint32_t row = front_row(g, a.T, a.H, g.t0 + tt);
+          *off32(Gsave, row) = G;
+          *off32(Dsave, row) = D;
+        }
+      }
+    }
+  }
+  const uint32_t tb = (((uint32_t)g.b * a.H + g.h) * a.NV + g.nt) * (uint32_t)a.K + g.i0;
+  float4* dst = reinterpret_cast<float4*>(off32(ab, tb * 2u));
+#pragma unroll
+  for (int q = 0; q < kCPT / 2; ++q) dst[q] = float4{Aacc[2 * q], Bacc[2 * q], Aacc[2 * q + 1], Bacc[2 * q + 1]};
+  stcf(off32(tdg, tb), sg);
+}
+
+// Backward emit (reverse over the tile): the gain adjoint from the carried lambda, then per token
+//   d omega_raw = p_bar sigmoid(z), d r_raw (tile sum), d retention_raw from
+//   d ell = [alpha >= 1e-6] (suffix sum of dG in the decay chunk) + d alpha * alpha,
+// per-tile partials of dA_log (sum d ell * ell) and d dt_bias (sum d f), and the key VJP of
+// k / max(||k||, 1e-12) applied to dk_gain + dk_memory (dk_memory nullable; dk nullable).
+template <typename TX>
+__global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
+    FrontArgs<TX> a, const float* __restrict__ carry, const float* __restrict__ lcarry,
+    const float* __restrict__ dkappa, const float* __restrict__ dG, const float* __restrict__ tdg,
+    const float* __restrict__ Gsave, const float* __restrict__ Dsave, const bf16_t* __restrict__ dk_mem,
+    const float* __restrict__ prec0, int prec_mode, TX* __restrict__ dk, bf16_t* __restrict__ df,
+    bf16_t* __restrict__ dz, bf16_t* __restrict__ dy, float* __restrict__ part_A, float* __restrict__ part_dt,
+    float* __restrict__ dprec_part) {
+  __shared__ float4 lp[kPairs][256];
+  const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
+  if (!g.ok) return;
+  const int tpt = a.K / kCPT, L = g.t1 - g.t0;
+  const float rate = __expf(a.A_log[g.h]);
+  float bias[kCPT];
+  ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
+  front_replay(a, g, rate, bias, carry, lp);
+  const uint32_t sb = ((uint32_t)g.b * a.H + g.h) * a.NV;
+  float lam[kCPT], accg[kCPT], ddt[kCPT], dA = 0.f;
+  ldcf(off32(lcarry, (sb + g.nt) * (uint32_t)a.K + g.i0), lam);
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) accg[j] = 0.f, ddt[j] = 0.f;
+  const int n_end = min(a.NV, g.nt - g.nt % a.tpc + a.tpc);
+  for (int n = g.nt + 1; n < n_end; ++n) {
+    float e[kCPT];
+    ldcf(off32(tdg, (sb + n) * (uint32_t)a.K + g.i0), e);
+#pragma unroll
+    for (int j = 0; j < kCPT; ++j) accg[j] += e[j];
+  }
+#pragma unroll 1
+  for (int q = (L - 1) >> 1; q >= 0; --q) {
+    FrontRaw<TX> raw[2];
+    float dk_[2][kCPT], dg_[2][kCPT], Gv[2], Dv[2];
+    Bf4 dkm[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {  // u = 0: token 2q + 1, u = 1: token 2q
+      const uint32_t row = front_row(g, a.T, a.H, g.t0 + min(2 * q + 1 - u, L - 1));
+      front_load(a, row, g.i0, raw[u]);
+      ldcf(off32(dkappa, row * (uint32_t)a.K + (uint32_t)g.i0), dk_[u]);
+      ldcf(off32(dG, row * (uint32_t)a.K + (uint32_t)g.i0), dg_[u]);
+      dkm[u] = dk_mem ? ldbf4(off32(dk_mem, row * (uint32_t)a.K + (uint32_t)g.i0)) : Bf4{uint2{0u, 0u}};
+      Gv[u] = *off32(Gsave, row);
+      Dv[u] = *off32(Dsave, row);
+    }
+    float kt[2][kCPT], ell[2][kCPT], al[2][kCPT], wt[2][kCPT], ir[2], pp[2][kCPT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) ir[u] = 1.f / front_inputs(raw[u], rate, bias, kt[u], ell[u], al[u], wt[u]);
+    unf4(lp[q][threadIdx.x], pp[1]);
+    front_step(pp[1], kt[1], al[1], wt[1], ir[1], a.s, pp[0]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tt = 2 * q + 1 - u;
+      if (tt < L) {
+        const uint32_t row = front_row(g, a.T, a.H, g.t0 + tt);
+        float dko[kCPT], dfo[kCPT], dwo[kCPT];
+        const float G = Gv[u], iD = 1.f / Dv[u];
+        float urr = 0.f;
+#pragma unroll
+        for (int j = 0; j < kCPT; ++j) {
+          const float a2 = al[u][j] * al[u][j];
+          const float ph = a2 * pp[u][j] + wt[u][j];
+          const float uu = a.s * kt[u][j] * kt[u][j] * ir[u];
+          const float hh = 1.f + uu * ph, ihh = 1.f / hh;
+          const float pnext = ph * ihh;
+          const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD + lam[j] * ihh * ihh;
+          const float ubar = -lam[j] * pnext * pnext;
+          dko[j] = dk_[u][j] * ph * iD - 2.f * ph * kt[u][j] * G * iD + ubar * (2.f * a.s * kt[u][j] * ir[u]);
+          const float dao = 2.f * al[u][j] * pp[u][j] * pbar;
+          dwo[j] = pbar * sigmoidf(bfj(raw[u].z, j));
+          urr += ubar * (-a.s * kt[u][j] * kt[u][j] * ir[u] * ir[u]);
+          lam[j] = a2 * pbar;
+          // retention frontend: alpha = exp(ell), ell = -e^A softplus(f + dt_bias)
+          float sp, sgm;
+          softplus_sigmoid(bfj(raw[u].f, j) + bias[j], sp, sgm);
+          accg[j] += dg_[u][j];
+          float dell = al[u][j] >= 1e-6f ? accg[j] : 0.f;
+          dell += dao * al[u][j];
+          dfo[j] = dell * (-rate) * sgm;
+          dA += dell * ell[u][j];
+          ddt[j] += dfo[j];
+        }
+        stc_bf16(off32(df, row * (uint32_t)a.K + (uint32_t)g.i0), dfo);
+        stc_bf16(off32(dz, row * (uint32_t)a.K + (uint32_t)g.i0), dwo);
+        const float utot = tile_sum(urr, tpt);
+        if (g.sub == 0) *off32(dy, row) = f2bf((-G * iD + utot) * sigmoidf(raw[u].y));
+        if (dk) {  // VJP of kt = k / max(||k||, 1e-12) applied to dk_gain + dk_memory
+          float gk[kCPT], dot = 0.f;
+#pragma unroll
+          for (int j = 0; j < kCPT; ++j) {
+            gk[j] = dko[j];
+            gk[j] += bfj(dkm[u], j);
+            dot += kt[u][j] * gk[j];
+          }
+          dot = tile_sum(dot, tpt);
+          const float id = 1.f / fmaxf(raw[u].kn, 1e-12f);
+          const bool clamped = !(raw[u].kn > 1e-12f);
+#pragma unroll
+          for (int j = 0; j < kCPT; ++j) gk[j] = clamped ? gk[j] * id : (gk[j] - kt[u][j] * dot) * id;
+          stk4<TX>(off32(dk, row * (uint32_t)a.K + (uint32_t)g.i0), gk);
+        }
+      }
+    }
+  }
+  const uint32_t P = (uint32_t)g.b * a.NV + g.nt;
+  if (part_dt) stcf(off32(part_dt, (P * a.H + g.h) * (uint32_t)a.K + g.i0), ddt);
+  dA = tile_sum(dA, tpt);
+  if (part_A && g.sub == 0) *off32(part_A, P * a.H + g.h) = dA;
+  if (g.nt == 0 && dprec_part) {  // lam holds dL/dp_{-1}; p_{-1} = 1/c  ->  dL/dc = -lam p^2
+    float cN[kCPT], part = 0.f;
+    if (prec_mode == 1) ldcf(prec0 + ((int64_t)g.b * a.H + g.h) * a.K + g.i0, cN);
+#pragma unroll
+    for (int j = 0; j < kCPT; ++j) {
+      const float c = prec_mode == 0 ? prec0[g.h] : cN[j];
+      const float p0 = 1.f / c;
+      cN[j] = -lam[j] * p0 * p0;
+      part += cN[j];
+    }
+    if (prec_mode == 1) {
+      stcf(dprec_part + ((int64_t)g.b * a.H + g.h) * a.K + g.i0, cN);
+    } else {
+      part = tile_sum(part, tpt);
+      if (g.sub == 0) dprec_part[(int64_t)g.b * a.H + g.h] = part;
+    }
+  }
+}
+
+// mu = 0.1 + softplus(mu_param) (the frontend's per-head prior precision)
+__global__ void front_mu_kernel(const float* __restrict__ mu_param, int H, float* __restrict__ mu) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h < H) mu[h] = 0.1f + softplusf(mu_param[h]);
+}
+// d mu_param = sigmoid(mu_param) * sum_b part[b, h]   (or d prior [H] = sum_b part[b, h] when mu_param is null)
+__global__ void front_dmu_kernel(const float* __restrict__ part, const float* __restrict__ mu_param, int B, int H,
+                                 float* __restrict__ out) {
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  float s = 0.f;
+  for (int b = 0; b < B; ++b) s += part[(int64_t)b * H + h];
+  out[h] = mu_param ? s * sigmoidf(mu_param[h]) : s;
+}
+
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // Fixed device workspace of kdn_iso_gain_fwd_noalloc (the per-chunk maps and carries of the iso gain),
 // for callers that cannot allocate.  Each GPU the library runs on holds its own copy until the process
@@ -1175,6 +1635,244 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
                        d_initial_precision);
   KDN_CHECK_LAUNCH();
   return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- fused diag frontend + gain
+namespace {
+struct FrontLayout {  // float offsets into the workspace (each 64-float aligned)
+  int64_t maps, tsum, carry, mu, grp, ab, lcarry, tdg, G, D, partA, partdt, dpart, total;
+};
+inline int64_t al64(int64_t x) { return (x + 63) / 64 * 64; }
+constexpr int64_t kFrontMaxElems = int64_t(1) << 30;  // per launch, so 32-bit byte offsets of f32 arrays hold
+// Batch rows per launch of the tile kernels.
+inline int front_batch_chunk(int B, int T, int H, int K) {
+  const int64_t per_b = (int64_t)T * H * K;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(B, kFrontMaxElems / per_b));
+}
+// The args of batch rows [b0, b0 + Bc).
+template <typename TX>
+FrontArgs<TX> front_shift(const FrontArgs<TX>& a, int b0, int Bc) {
+  FrontArgs<TX> c = a;
+  const int64_t e = (int64_t)b0 * a.T * a.H * a.K, r = (int64_t)b0 * a.T * a.H;
+  c.k = a.k + e, c.f = a.f + e, c.z = a.z + e, c.knorm = a.knorm + r, c.y = a.y + r, c.B = Bc;
+  return c;
+}
+FrontLayout front_layout(int B, int T, int H, int K) {
+  const int64_t NV = cdiv(T, kVecChunk), NG = cdiv(NV, kCarryGroup), BHK = (int64_t)B * H * K;
+  FrontLayout L{};
+  int64_t o = 0;
+  L.maps = o; o += al64(BHK * NV * 4);   // forward tile maps; the backward's (A, B) maps reuse it
+  L.ab = L.maps;
+  L.tsum = o; o += al64(BHK * NV);       // forward tile log-decay sums; backward tile dG sums reuse it
+  L.tdg = L.tsum;
+  L.carry = o; o += al64(BHK * NV);      // forward tile carries (when not saved); backward lambda carries
+  L.lcarry = L.carry;
+  L.mu = o; o += al64(H);
+  L.grp = o; o += al64(BHK * NG * 5);    // two-level carry composites and start values
+  L.G = o; o += al64((int64_t)B * T * H);
+  L.D = o; o += al64((int64_t)B * T * H);
+  L.partA = o; o += al64((int64_t)B * NV * H);
+  L.partdt = o; o += al64(BHK * NV);
+  L.dpart = o; o += al64((int64_t)B * H);
+  L.total = o;
+  return L;
+}
+bool front_args_ok(const void* k_raw, const float* k_norm, const uint16_t* f, const uint16_t* z, const uint16_t* y,
+                   const float* A_log, const float* dt_bias, const float* mu_param, const float* prec0,
+                   int prec_mode, int B, int T, int H, int K, int chunk) {
+  if (B <= 0 || T <= 0 || H <= 0 || (K != 64 && K != 128) || chunk <= 0 || chunk % kVecChunk != 0) return false;
+  if (!k_raw || !k_norm || !f || !z || !y || !A_log || !dt_bias) return false;
+  if ((int64_t)T * H * K > kFrontMaxElems) return false;  // one batch row must fit the 32-bit offsets
+  if (prec_mode != 0 && prec_mode != 1) return false;
+  if (mu_param ? (prec0 != nullptr || prec_mode != 0) : prec0 == nullptr) return false;
+  return aligned16(k_raw) && aligned16(f) && aligned16(z) && aligned16(dt_bias) &&
+         (prec_mode == 0 || aligned16(prec0));
+}
+template <typename TX>
+FrontArgs<TX> front_args(const void* k_raw, const float* k_norm, const uint16_t* f, const uint16_t* z,
+                         const uint16_t* y, const float* A_log, const float* dt_bias, int B, int T, int H, int K,
+                         int chunk, float info_scale) {
+  return FrontArgs<TX>{(const TX*)k_raw, k_norm, f, z, y, A_log, dt_bias, B, T, H, K, cdiv(T, kVecChunk),
+                       chunk / kVecChunk, info_scale};
+}
+
+template <typename TX>
+int front_fwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0, int prec_mode, float* g_cumsum,
+              float* kappa, float* final_precision, float* saved, float* ws, hipStream_t stream) {
+  const FrontLayout L = front_layout(a.B, a.T, a.H, a.K);
+  const int NV = a.NV, tpb = 256 / (a.K / kCPT), bs = gain_block(a.K);
+  float* maps = ws + L.maps;
+  float* tsum = ws + L.tsum;
+  float* carry = saved ? saved : ws + L.carry;
+  if (mu_param) {
+    hipLaunchKernelGGL(front_mu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, mu_param, a.H, ws + L.mu);
+    prec0 = ws + L.mu;
+  }
+  const int Bc = front_batch_chunk(a.B, a.T, a.H, a.K);
+  const int64_t ev = (int64_t)a.H * NV * a.K, ee = (int64_t)a.T * a.H * a.K;  // per batch row
+  for (int b0 = 0; b0 < a.B; b0 += Bc) {
+    const int nb = std::min(Bc, a.B - b0);
+    hipLaunchKernelGGL((diag_front_map_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
+                       front_shift(a, b0, nb), maps + b0 * ev * 4, tsum + b0 * ev);
+  }
+  if (NV > 2 * kCarryGroup) {  // two-level carry
+    const int NG = cdiv(NV, kCarryGroup);
+    float4* gmaps = reinterpret_cast<float4*>(ws + L.grp);
+    float* gstart = ws + L.grp + (int64_t)a.B * a.H * NG * a.K * 4;
+    hipLaunchKernelGGL(diag_gain_group_map_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float4*)maps, a.K,
+                       NV, NG, gmaps);
+    hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float4*)gmaps, prec0,
+                       prec_mode, a.H, a.K, NG, gstart, final_precision);
+    hipLaunchKernelGGL(diag_gain_group_fill_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float4*)maps,
+                       gstart, a.K, NV, NG, carry);
+  } else {
+    hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float4*)maps, prec0,
+                       prec_mode, a.H, a.K, NV, carry, final_precision);
+  }
+  for (int b0 = 0; b0 < a.B; b0 += Bc) {
+    const int nb = std::min(Bc, a.B - b0);
+    hipLaunchKernelGGL((diag_front_emit_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
+                       front_shift(a, b0, nb), carry + b0 * ev, tsum + b0 * ev, g_cumsum + b0 * ee, kappa + b0 * ee);
+  }
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+template <typename TX>
+int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0, int prec_mode, const float* saved,
+              const float* final_precision, const float* d_g_cumsum, const float* d_kappa, const uint16_t* d_k_memory,
+              const float* d_final_precision, void* dk_raw, uint16_t* d_ret, uint16_t* d_omega, uint16_t* d_r,
+              float* dA_log, float* ddt_bias, float* d_mu_param, float* d_prec, float* ws, hipStream_t stream) {
+  const FrontLayout L = front_layout(a.B, a.T, a.H, a.K);
+  const int NV = a.NV, tpb = 256 / (a.K / kCPT), bs = gain_block(a.K);
+  float* ab = ws + L.ab;
+  float* lcarry = ws + L.lcarry;
+  float* tdg = ws + L.tdg;
+  float* G = ws + L.G;
+  float* D = ws + L.D;
+  if (mu_param) {
+    hipLaunchKernelGGL(front_mu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, mu_param, a.H, ws + L.mu);
+    prec0 = ws + L.mu;
+  }
+  const int Bc = front_batch_chunk(a.B, a.T, a.H, a.K);
+  const int64_t ev = (int64_t)a.H * NV * a.K, ee = (int64_t)a.T * a.H * a.K, er = (int64_t)a.T * a.H;
+  for (int b0 = 0; b0 < a.B; b0 += Bc) {
+    const int nb = std::min(Bc, a.B - b0);
+    hipLaunchKernelGGL((diag_front_bwd_map_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
+                       front_shift(a, b0, nb), saved + b0 * ev, d_kappa + b0 * ee, d_g_cumsum + b0 * ee,
+                       ab + b0 * ev * 2, tdg + b0 * ev, G + b0 * er, D + b0 * er);
+  }
+  if (NV > 2 * kCarryGroup) {  // two-level carry
+    const int NG = cdiv(NV, kCarryGroup);
+    float2* gab = reinterpret_cast<float2*>(ws + L.grp);
+    float* gend = ws + L.grp + (int64_t)a.B * a.H * NG * a.K * 2;
+    hipLaunchKernelGGL(diag_gain_bwd_group_map_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float2*)ab,
+                       a.K, NV, NG, gab);
+    hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float2*)gab,
+                       d_final_precision, final_precision, a.H, a.K, NG, gend);
+    hipLaunchKernelGGL(diag_gain_bwd_group_fill_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float2*)ab,
+                       gend, a.K, NV, NG, lcarry);
+  } else {
+    hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float2*)ab,
+                       d_final_precision, final_precision, a.H, a.K, NV, lcarry);
+  }
+  const bool want_prec = d_mu_param || d_prec;
+  float* dprec_out = want_prec ? (prec_mode == 1 ? d_prec : ws + L.dpart) : nullptr;
+  for (int b0 = 0; b0 < a.B; b0 += Bc) {
+    const int nb = std::min(Bc, a.B - b0);
+    const int64_t ep = prec_mode == 1 ? (int64_t)a.H * a.K : a.H;  // per batch row of [B,H,K] / [B,H]
+    hipLaunchKernelGGL((diag_front_bwd_emit_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
+                       front_shift(a, b0, nb), saved + b0 * ev, lcarry + b0 * ev, d_kappa + b0 * ee,
+                       d_g_cumsum + b0 * ee, tdg + b0 * ev, G + b0 * er, D + b0 * er,
+                       d_k_memory ? (const bf16_t*)d_k_memory + b0 * ee : nullptr,
+                       prec_mode == 1 ? prec0 + b0 * ep : prec0, prec_mode,
+                       dk_raw ? (TX*)dk_raw + b0 * ee : nullptr, (bf16_t*)d_ret + b0 * ee, (bf16_t*)d_omega + b0 * ee,
+                       (bf16_t*)d_r + b0 * er, dA_log ? ws + L.partA + (int64_t)b0 * NV * a.H : nullptr,
+                       ddt_bias ? ws + L.partdt + b0 * ev : nullptr, dprec_out ? dprec_out + b0 * ep : nullptr);
+  }
+  const int NP = a.B * NV;
+  if (dA_log)
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(a.H, 64)), dim3(256), 0, stream, ws + L.partA, NP,
+                       (int64_t)a.H, a.H, dA_log);
+  if (ddt_bias)
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv((int64_t)a.H * a.K, 64)), dim3(256), 0, stream,
+                       ws + L.partdt, NP, (int64_t)a.H * a.K, a.H * a.K, ddt_bias);
+  if (want_prec && prec_mode == 0)
+    hipLaunchKernelGGL(front_dmu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, ws + L.dpart,
+                       d_mu_param ? mu_param : nullptr, a.B, a.H, d_mu_param ? d_mu_param : d_prec);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+size_t kdn_diag_front_saved_size(int B, int T, int H, int K) {
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return 0;
+  return (size_t)((int64_t)B * H * cdiv(T, kVecChunk) * K) * sizeof(float);
+}
+
+size_t kdn_diag_front_workspace_size(int B, int T, int H, int K) {
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return 0;
+  return (size_t)front_layout(B, T, H, K).total * sizeof(float);
+}
+
+int kdn_diag_front_fwd(const void* k_raw, int k_bf16, const float* k_norm, const uint16_t* retention_raw,
+                       const uint16_t* omega_raw, const uint16_t* r_raw, const float* A_log, const float* dt_bias,
+                       const float* mu_param, const float* initial_precision, int prec_mode, int B, int T, int H,
+                       int K, int chunk, float info_scale, float* g_cumsum, float* kappa, float* final_precision,
+                       float* saved, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!front_args_ok(k_raw, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, initial_precision,
+                     prec_mode, B, T, H, K, chunk))
+    return KDN_ERR_ARG;
+  if (!g_cumsum || !kappa || !aligned16(g_cumsum) || !aligned16(kappa) || !aligned16(saved) ||
+      !aligned16(workspace) || !(info_scale > 0.f))
+    return KDN_ERR_ARG;
+  if (workspace_bytes < kdn_diag_front_workspace_size(B, T, H, K)) return KDN_ERR_ARG;
+  float* ws = (float*)workspace;
+  if (k_bf16)
+    return front_fwd(front_args<bf16_t>(k_raw, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, B, T, H, K,
+                                        chunk, info_scale),
+                     mu_param, initial_precision, prec_mode, g_cumsum, kappa, final_precision, saved, ws, stream);
+  return front_fwd(front_args<float>(k_raw, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, B, T, H, K, chunk,
+                                     info_scale),
+                   mu_param, initial_precision, prec_mode, g_cumsum, kappa, final_precision, saved, ws, stream);
+}
+
+int kdn_diag_front_bwd(const void* k_raw, int k_bf16, const float* k_norm, const uint16_t* retention_raw,
+                       const uint16_t* omega_raw, const uint16_t* r_raw, const float* A_log, const float* dt_bias,
+                       const float* mu_param, const float* initial_precision, int prec_mode, const float* saved,
+                       const float* final_precision, const float* d_g_cumsum, const float* d_kappa,
+                       const uint16_t* d_k_memory, const float* d_final_precision, int B, int T, int H, int K,
+                       int chunk, float info_scale, void* dk_raw, uint16_t* d_retention_raw, uint16_t* d_omega_raw,
+                       uint16_t* d_r_raw, float* dA_log, float* ddt_bias, float* d_mu_param,
+                       float* d_initial_precision, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!front_args_ok(k_raw, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, initial_precision,
+                     prec_mode, B, T, H, K, chunk))
+    return KDN_ERR_ARG;
+  if (!saved || !d_g_cumsum || !d_kappa || !d_retention_raw || !d_omega_raw || !d_r_raw) return KDN_ERR_ARG;
+  if (d_final_precision && !final_precision) return KDN_ERR_ARG;
+  if (d_mu_param && !mu_param) return KDN_ERR_ARG;
+  if (d_initial_precision && mu_param) return KDN_ERR_ARG;
+  if (!aligned16(saved) || !aligned16(d_g_cumsum) || !aligned16(d_kappa) || !aligned16(d_k_memory) ||
+      !aligned16(dk_raw) || !aligned16(d_retention_raw) || !aligned16(d_omega_raw) || !aligned16(ddt_bias) ||
+      !aligned16(workspace) || (prec_mode == 1 && !aligned16(d_initial_precision)) || !(info_scale > 0.f))
+    return KDN_ERR_ARG;
+  if (workspace_bytes < kdn_diag_front_workspace_size(B, T, H, K)) return KDN_ERR_ARG;
+  float* ws = (float*)workspace;
+  if (k_bf16)
+    return front_bwd(front_args<bf16_t>(k_raw, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, B, T, H, K,
+                                        chunk, info_scale),
+                     mu_param, initial_precision, prec_mode, saved, final_precision, d_g_cumsum, d_kappa, d_k_memory,
+                     d_final_precision, dk_raw, d_retention_raw, d_omega_raw, d_r_raw, dA_log, ddt_bias, d_mu_param,
+                     d_initial_precision, ws, stream);
+  return front_bwd(front_args<float>(k_raw, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, B, T, H, K, chunk,
+                                     info_scale),
+                   mu_param, initial_precision, prec_mode, saved, final_precision, d_g_cumsum, d_kappa, d_k_memory,
+                   d_final_precision, dk_raw, d_retention_raw, d_omega_raw, d_r_raw, dA_log, ddt_bias, d_mu_param,
+                   d_initial_precision, ws, stream);
 }
 
 }  // extern "C"

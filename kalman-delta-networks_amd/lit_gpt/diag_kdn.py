@@ -21,8 +21,8 @@ from torch import nn
 
 from ._inference import as_f32, linear, packed_weight, use_packed
 from .iso_kdn import _SUPPORTED_HEAD_DIMS, decay_parameters, initial_precision_inverse, validate_training_dtype
-from .kdn_ops.diag_kdn_chunk import (_chunk_kalman_as, _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain,
-                                     _diag_kdn_normalize)
+from .kdn_ops.diag_kdn_chunk import (_chunk_kalman_as, _diag_kdn_frontend_precumsum_paired, _diag_kdn_normalize,
+                                     diag_kdn_front)
 from .kdn_ops.gated_norm import FusedRMSNormGated
 from .kdn_ops.short_conv import causal_conv1d
 from .kdn_ops.step import kdn_kalman_step
@@ -166,19 +166,23 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
         else:
             q, k, v = (conv(x.contiguous()) for x, conv in zip(projections, convs))
         q, k, v = q.reshape(B, T, H, K), k.reshape(B, T, H, K), v.reshape(B, T, H, V)
-        q_memory, k_gain, k_memory = _diag_kdn_normalize(q, k)
-        g_cumsum, alpha, omega, r, initial_precision = _diag_kdn_frontend_precumsum_paired(
-            retention_raw, omega_raw, r_raw, as_f32(self, "A_log", self.A_log),
-            as_f32(self, "dt_bias", self.dt_bias).view(H, K), as_f32(self, "mu_param", self.initial_precision_param))
+        A_log = as_f32(self, "A_log", self.A_log)
+        dt_bias = as_f32(self, "dt_bias", self.dt_bias).view(H, K)
+        mu_param = as_f32(self, "mu_param", self.initial_precision_param)
         new_state = None
         scale = float(K ** -0.5)
         if not stateful:
-            kappa = _diag_kdn_gain(k_gain, alpha, omega, r, initial_precision, omega_raw, r_raw)
+            # normalisation -> frontend -> gain fused (the reference's three ops, same results)
+            q_memory, k_memory, g_cumsum, kappa = diag_kdn_front(q, k, retention_raw, omega_raw, r_raw, A_log,
+                                                                 dt_bias, mu_param)
             # the f32 recurrence is stored at the value dtype, as the reference's .to(v.dtype) does
             output = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale, out_dtype=v.dtype)
         else:
-            prec0 = state.precision if state is not None else initial_precision
             if T == 1 and not torch.is_grad_enabled():  # gain and memory of one token in one launch
+                q_memory, k_gain, k_memory = _diag_kdn_normalize(q, k)
+                g_cumsum, alpha, omega, r, initial_precision = _diag_kdn_frontend_precumsum_paired(
+                    retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param)
+                prec0 = state.precision if state is not None else initial_precision
                 inplace = state is not None and state.inplace
                 if state is None:
                     memory = torch.zeros(B, H, K, V, device=q.device, dtype=torch.float32)
@@ -190,8 +194,9 @@ class DiagonalKalmanDeltaNetwork(nn.Module):
                     omega=omega, r=r, k_gain=k_gain, info_scale=float(K), scale=scale, out_dtype=v.dtype,
                     precision_out=state.precision_scratch() if inplace else None)
             else:
-                kappa, precision = _diag_kdn_gain(k_gain, alpha, omega, r, prec0, omega_raw, r_raw,
-                                                  output_final_state=True)
+                q_memory, k_memory, g_cumsum, kappa, precision = diag_kdn_front(
+                    q, k, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param,
+                    initial_precision=state.precision if state is not None else None, output_final_state=True)
                 output, memory = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale,
                                                   initial_state=state.memory if state is not None else None,
                                                   output_final_state=True, out_dtype=v.dtype)

@@ -33,6 +33,10 @@ _SIGS = {
     "kdn_diag_gain_workspace_size": "iiii",
     "kdn_diag_gain_fwd": "pppppiiiiifpppppzs",
     "kdn_diag_gain_bwd": "pppppipppppppiiiifpppppppzs",
+    "kdn_diag_front_saved_size": "iiii",
+    "kdn_diag_front_workspace_size": "iiii",
+    "kdn_diag_front_fwd": "pipppppppp" "iiiiii" "f" "pppppzs",
+    "kdn_diag_front_bwd": "pipppppppp" "i" "pppppp" "iiiii" "f" "ppppppppp" "zs",
     "kdn_mem_chunk_size": "",
     "kdn_mem_state_groups": "iiiii",
     "kdn_mem_saved_size": "iiiii",
@@ -56,7 +60,8 @@ _SIGS = {
     "kdn_rms_norm_gated_bwd": "pipipippliippppzs",
 }
 _SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_iso_gain_workspace_size", "kdn_diag_frontend_bwd_workspace_size",
-             "kdn_diag_gain_workspace_size", "kdn_mem_saved_size", "kdn_mem_bwd_workspace_size",
+             "kdn_diag_gain_workspace_size", "kdn_diag_front_saved_size",
+             "kdn_diag_front_workspace_size", "kdn_mem_saved_size", "kdn_mem_bwd_workspace_size",
              "kdn_short_conv_bwd_workspace_size", "kdn_rms_norm_gated_bwd_workspace_size",
              "kdn_rms_norm_bwd_workspace_size"}
 _CT = {"p": ctypes.c_void_p, "i": ctypes.c_int, "l": ctypes.c_int64, "f": ctypes.c_float,

@@ -316,6 +316,140 @@ def _diag_kdn_gain(k_gain, alpha, omega, r, initial_precision, omega_raw, r_raw,
 
 
 # ---------------------------------------------------------------------------
+# Fused front half of the layer composition
+# ---------------------------------------------------------------------------
+
+_FRONT_MAX_ELEMS = 1 << 30  # one batch row of [T,H,K] per launch (the kernels' 32-bit offsets)
+
+
+class _DiagKdnFrontFunction(torch.autograd.Function):
+    """The layer's normalisation -> frontend -> gain chain (reference lit_gpt/diag_kdn.py:315-345 over
+    diag_kdn_chunk.py:2162-2168, 2471-2495, 2737-2791) as one op.  Returns (q_memory, k_memory,
+    g_cumsum, kappa, final_precision); alpha, omega, r and the fp32 gain key exist only inside the
+    kernels, and the backward replays the precision per 16-token tile instead of reading p_prev."""
+
+    @staticmethod
+    def forward(ctx, q_raw, k_raw, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, initial_precision,
+                save):
+        B, T, H, K = q_raw.shape
+        dev = q_raw.device
+        rows = B * T * H
+        q_memory = torch.empty((B, T, H, K), device=dev, dtype=torch.bfloat16)
+        k_memory = torch.empty_like(q_memory)
+        q_norm = torch.empty((B, T, H), device=dev, dtype=torch.float32)
+        k_norm = torch.empty_like(q_norm)
+        g_cumsum = torch.empty((B, T, H, K), device=dev, dtype=torch.float32)
+        kappa = torch.empty_like(g_cumsum)
+        fprec = torch.empty((B, H, K), device=dev, dtype=torch.float32)
+        saved = (torch.empty((_lib.size("kdn_diag_front_saved_size", B, T, H, K) // 4,), device=dev,
+                             dtype=torch.float32) if save else None)
+        ws_bytes = _lib.size("kdn_diag_front_workspace_size", B, T, H, K)
+        ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+        prec_mode = 0 if initial_precision is None or initial_precision.ndim == 1 else 1
+        with torch.cuda.device(dev):
+            stream = _lib.stream_of(q_raw)
+            _lib.call("kdn_diag_norm_fwd", _lib.ptr(q_raw), _lib.ptr(k_raw), _lib.is_bf16(q_raw), rows, K,
+                      _lib.ptr(q_memory), None, _lib.ptr(k_memory), _lib.ptr(q_norm), _lib.ptr(k_norm), stream,
+                      tag="diag_front_norm_fwd")
+            _lib.call("kdn_diag_front_fwd", _lib.ptr(k_raw), _lib.is_bf16(k_raw), _lib.ptr(k_norm),
+                      _lib.ptr(retention_raw), _lib.ptr(omega_raw), _lib.ptr(r_raw), _lib.ptr(A_log),
+                      _lib.ptr(dt_bias), _lib.ptr(mu_param) if initial_precision is None else None,
+                      _lib.ptr(initial_precision), prec_mode, B, T, H, K, _DIAG_KDN_MEMORY_CHUNK_SIZE, float(K),
+                      _lib.ptr(g_cumsum), _lib.ptr(kappa), _lib.ptr(fprec), _lib.ptr(saved), _lib.ptr(ws), ws_bytes,
+                      stream)
+        if save:
+            ctx.save_for_backward(q_raw, k_raw, q_norm, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias,
+                                  mu_param, initial_precision, saved, fprec)
+        ctx.set_materialize_grads(False)
+        return q_memory, k_memory, g_cumsum, kappa, fprec
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, d_q_memory, d_k_memory, d_g_cumsum, d_kappa, d_final_precision):
+        (q_raw, k_raw, q_norm, k_norm, retention_raw, omega_raw, r_raw, A_log, dt_bias, mu_param, initial_precision,
+         saved, fprec) = ctx.saved_tensors
+        B, T, H, K = q_raw.shape
+        dev = q_raw.device
+        needs = ctx.needs_input_grad
+        prec_mode = 0 if initial_precision is None or initial_precision.ndim == 1 else 1
+        d_g_cumsum = (torch.zeros((B, T, H, K), device=dev, dtype=torch.float32) if d_g_cumsum is None
+                      else d_g_cumsum.float().contiguous())
+        d_kappa = (torch.zeros((B, T, H, K), device=dev, dtype=torch.float32) if d_kappa is None
+                   else d_kappa.float().contiguous())
+        d_k_memory = d_k_memory.to(torch.bfloat16).contiguous() if d_k_memory is not None else None
+        dfp = d_final_precision.float().contiguous() if d_final_precision is not None else None
+        dk = torch.empty_like(k_raw) if needs[1] else None
+        dret = torch.empty_like(retention_raw)
+        domega = torch.empty_like(omega_raw)
+        dr = torch.empty_like(r_raw)
+        dA = torch.empty_like(A_log) if needs[5] else None
+        ddt = torch.empty_like(dt_bias) if needs[6] else None
+        dmu = torch.empty_like(mu_param) if (needs[7] and initial_precision is None) else None
+        dinit = torch.empty_like(initial_precision) if (initial_precision is not None and needs[8]) else None
+        ws_bytes = _lib.size("kdn_diag_front_workspace_size", B, T, H, K)
+        ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+        dq = None
+        with torch.cuda.device(dev):
+            stream = _lib.stream_of(q_raw)
+            _lib.call("kdn_diag_front_bwd", _lib.ptr(k_raw), _lib.is_bf16(k_raw), _lib.ptr(k_norm),
+                      _lib.ptr(retention_raw), _lib.ptr(omega_raw), _lib.ptr(r_raw), _lib.ptr(A_log),
+                      _lib.ptr(dt_bias), _lib.ptr(mu_param) if initial_precision is None else None,
+                      _lib.ptr(initial_precision), prec_mode, _lib.ptr(saved), _lib.ptr(fprec), _lib.ptr(d_g_cumsum),
+                      _lib.ptr(d_kappa), _lib.ptr(d_k_memory), _lib.ptr(dfp), B, T, H, K,
+                      _DIAG_KDN_MEMORY_CHUNK_SIZE, float(K), _lib.ptr(dk), _lib.ptr(dret), _lib.ptr(domega),
+                      _lib.ptr(dr), _lib.ptr(dA), _lib.ptr(ddt), _lib.ptr(dmu), _lib.ptr(dinit), _lib.ptr(ws),
+                      ws_bytes, stream)
+            if needs[0] and d_q_memory is not None:
+                dq = torch.empty_like(q_raw)
+                d_q_memory = d_q_memory.to(torch.bfloat16).contiguous()
+                _lib.call("kdn_diag_norm_bwd", _lib.ptr(q_raw), _lib.ptr(k_raw), _lib.is_bf16(q_raw),
+                          _lib.ptr(q_norm), _lib.ptr(k_norm), _lib.ptr(d_q_memory), None, None, B * T * H, K,
+                          _lib.ptr(dq), None, stream, tag="diag_front_norm_bwd")
+        return (dq, dk, dret if needs[2] else None, domega if needs[3] else None, dr if needs[4] else None, dA, ddt,
+                dmu, dinit, None)
+
+
+def diag_kdn_front(q_raw, k_raw, retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param, *,
+                   initial_precision=None, output_final_state=False):
+    """``_diag_kdn_normalize`` -> ``_diag_kdn_frontend_precumsum_paired`` -> ``_diag_kdn_gain`` as the
+    layer composes them (reference lit_gpt/diag_kdn.py:315-345), fused: returns
+    ``(q_memory, k_memory, g_cumsum, kappa)`` (plus ``final_precision`` [B,H,K] with
+    ``output_final_state``), equal to the three ops' outputs.  The prior precision is the frontend's
+    ``0.1 + softplus(initial_precision_param)`` unless ``initial_precision`` ([H] or [B,H,K]) is given.
+    Same argument checks and errors as the three ops."""
+    _validate_diag_kdn_norm_inputs(q_raw, k_raw)
+    B, T, H, K = _validate_diag_kdn_frontend_inputs(retention_raw, omega_raw, r_raw, A_log, dt_bias,
+                                                    initial_precision_param)
+    if tuple(q_raw.shape) != (B, T, H, K) or q_raw.device != retention_raw.device:
+        raise ValueError("q_raw and k_raw must match retention_raw's shape and device")
+    if initial_precision is not None:
+        if not isinstance(initial_precision, torch.Tensor):
+            raise TypeError("initial_precision must be a torch.Tensor")
+        if initial_precision.shape not in ((H,), (B, H, K)):
+            raise ValueError(f"initial_precision must have shape [{H}] or [{B},{H},{K}]")
+        if initial_precision.dtype != torch.float32:
+            raise TypeError("initial_precision must be torch.float32")
+        if not initial_precision.is_contiguous() or initial_precision.device != retention_raw.device:
+            raise ValueError("initial_precision must be a contiguous tensor on the inputs' device")
+    if T * H * K > _FRONT_MAX_ELEMS:  # longer than the fused kernels address: the three ops, still all HIP
+        q_memory, k_gain, k_memory = _diag_kdn_normalize(q_raw, k_raw)
+        g_cumsum, alpha, omega, r, mu = _diag_kdn_frontend_precumsum_paired(
+            retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param)
+        prec = mu if initial_precision is None else initial_precision
+        out = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw, output_final_state=output_final_state)
+        if output_final_state:
+            return q_memory, k_memory, g_cumsum, out[0], out[1]
+        return q_memory, k_memory, g_cumsum, out
+    inputs = (q_raw, k_raw, retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param,
+              initial_precision)
+    save = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in inputs)
+    q_memory, k_memory, g_cumsum, kappa, fprec = _DiagKdnFrontFunction.apply(*inputs, save)
+    if output_final_state:
+        return q_memory, k_memory, g_cumsum, kappa, fprec
+    return q_memory, k_memory, g_cumsum, kappa
+
+
+# ---------------------------------------------------------------------------
 # Chunked memory scan
 # ---------------------------------------------------------------------------
 

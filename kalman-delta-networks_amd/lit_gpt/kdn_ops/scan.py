@@ -3,14 +3,14 @@
 ``iso_kdn_scan`` follows lit_gpt/iso_kdn.py:277-304 (gate frontend -> scalar gain ->
 chunked memory scan with in-op q/k normalisation); ``diag_kdn_scan`` follows
 lit_gpt/diag_kdn.py:315-345 (q/k normalisation -> frontend -> vector gain -> memory scan,
-output materialised at v's dtype).  Projections, short convolutions and the gated output
+output materialised at v's dtype), with the first three as one fused op (``diag_kdn_front``).  Projections, short convolutions and the gated output
 norm of the layers are not part of the scan.
 """
 from __future__ import annotations
 
 import torch
 
-from .diag_kdn_chunk import _chunk_kalman_as, _diag_kdn_frontend_precumsum_paired, _diag_kdn_gain, _diag_kdn_normalize
+from .diag_kdn_chunk import _chunk_kalman_as, diag_kdn_front
 from .iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
 
 
@@ -35,18 +35,15 @@ def diag_kdn_scan(q, k, v, retention_raw, omega_raw, r_raw, A_log, dt_bias, init
     ``initial_precision`` [B,H,K] fp32 replaces the learned [H] prior, and with
     ``output_final_state`` the call returns ``(o, (final_state, final_precision))``."""
     K = q.shape[-1]
-    q_memory, k_gain, k_memory = _diag_kdn_normalize(q, k)
-    g_cumsum, alpha, omega, r, mu = _diag_kdn_frontend_precumsum_paired(
-        retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param)
-    prec = mu if initial_precision is None else initial_precision
+    # normalisation -> frontend -> gain as one fused op (same results as the three reference ops)
+    front = diag_kdn_front(q, k, retention_raw, omega_raw, r_raw, A_log, dt_bias, initial_precision_param,
+                           initial_precision=initial_precision, output_final_state=output_final_state)
+    q_memory, k_memory, g_cumsum, kappa = front[:4]
     scale = float(K ** -0.5)
     if output_final_state:
-        kappa, final_precision = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw,
-                                                output_final_state=True)
         out, final_state = _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale,
                                             initial_state=initial_state, output_final_state=True, out_dtype=v.dtype)
-        return out, (final_state, final_precision)
-    kappa = _diag_kdn_gain(k_gain, alpha, omega, r, prec, omega_raw, r_raw)
+        return out, (final_state, front[4])
     # chunk_kalman(...).to(v.dtype) with the cast at the kernel's store
     return _chunk_kalman_as(q_memory, k_memory, kappa, v, g_cumsum, scale, initial_state=initial_state,
                             out_dtype=v.dtype)
