@@ -92,23 +92,26 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
 
 namespace {
 // out[j] = sum_p part[p * stride + j] for j < n, deterministic order: block = 64 outputs x 4
-// partial stripes (each 8-way unrolled over p), stripes combined in order.  grid ceil(n/64).
+// partial stripes (each 8-way unrolled over p), stripes combined in order.  grid (ceil(n/64), S): with
+// S > 1 segment y sums rows [NP y / S, NP (y + 1) / S) into out[y * n + j] (a second call with NP = S
+// finishes), so a tall partial array is reduced by S times more workgroups.
 __global__ __launch_bounds__(256) void reduce_partials_vec_kernel(const float* __restrict__ part, int NP,
                                                                   int64_t stride, int n, float* __restrict__ out) {
   __shared__ float s[4][64];
   const int jj = threadIdx.x & 63, st4 = threadIdx.x >> 6, j = blockIdx.x * 64 + jj;
+  const int p0 = (int)((int64_t)NP * blockIdx.y / gridDim.y), p1 = (int)((int64_t)NP * (blockIdx.y + 1) / gridDim.y);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (j < n) {
-    int pp = st4;
-    for (; pp + 28 < NP; pp += 32) {
+    int pp = p0 + st4;
+    for (; pp + 28 < p1; pp += 32) {
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] += part[(int64_t)(pp + 4 * q) * stride + j];
     }
-    for (; pp < NP; pp += 4) acc[0] += part[(int64_t)pp * stride + j];
+    for (; pp < p1; pp += 4) acc[0] += part[(int64_t)pp * stride + j];
   }
   s[st4][jj] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (st4 == 0 && j < n) out[j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
+  if (st4 == 0 && j < n) out[(int64_t)blockIdx.y * n + j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
 }
 }  // namespace
 

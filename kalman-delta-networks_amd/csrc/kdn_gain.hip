@@ -634,6 +634,14 @@ __global__ __launch_bounds__(256) void diag_gain_map_v_kernel(const float* __res
   for (int j = 0; j < kCPT; ++j) dst[j] = float4{M[j].m0, M[j].m1, M[j].m2, M[j].m3};
 }
 
+// The prior precision c of channel i of stream (b, h): prec_mode 0 -> prec0[h] ([H] values), 1 -> [B,H,K]
+// values, 2 -> prec0 holds the frontend's mu_param [H] and c = mu = 0.1 + softplus(mu_param).
+__device__ __forceinline__ float prior_precision(const float* prec0, int prec_mode, int b, int h, int H, int K,
+                                                int i) {
+  if (prec_mode == 1) return prec0[((int64_t)b * H + h) * K + i];
+  return prec_mode == 2 ? 0.1f + softplusf(prec0[h]) : prec0[h];
+}
+
 // grid (B*H), block K: per channel, the chunk maps in groups of 8 with the next group's loads in
 // flight while the current group is applied.
 __global__ __launch_bounds__(256) void diag_gain_carry_v_kernel(const float4* __restrict__ maps,
@@ -642,7 +650,7 @@ __global__ __launch_bounds__(256) void diag_gain_carry_v_kernel(const float4* __
                                                                 float* __restrict__ final_prec) {
   const int bh = blockIdx.x, b = bh / H, h = bh % H, i = threadIdx.x;
   if (i >= K) return;
-  float p = 1.f / (prec_mode == 0 ? prec0[h] : prec0[((int64_t)b * H + h) * K + i]);
+  float p = 1.f / prior_precision(prec0, prec_mode, b, h, H, K, i);
   const int64_t cb = (int64_t)bh * NT;
   float4 cur[8], nxt[8];
 #pragma unroll
@@ -1034,23 +1042,93 @@ __device__ __forceinline__ void front_load(const FrontArgs<TX>& a, uint32_t row,
   r.kn = *off32(a.knorm, row);
   r.y = bf2f(*off32(a.y, row));
 }
-// The gain's per-token inputs, as the standalone kernels form them: kt = k / max(||k||, 1e-12),
-// ell = -e^A softplus(f + dt_bias), alpha = e^ell, omega = softplus(z); returns r = 0.01 + softplus(y).
-template <typename TX>
-__device__ __forceinline__ float front_inputs(const FrontRaw<TX>& r, float rate, const float* bias, float* kt,
-                                              float* ell, float* al, float* wt) {
-  const float ik = 1.f / fmaxf(r.kn, 1e-12f);
+// The gain's per-token inputs for one thread's kCPT channels: kt = k / max(||k||, 1e-12),
+// ell = -e^A softplus(f + dt_bias), alpha = e^ell, omega = softplus(z), 1/r with r = 0.01 + softplus(y).
+// With BWD also the sigmoids the backward needs (sigma(f + dt_bias), sigma(z), sigma(y)), each from
+// the exponential its softplus already took.  Reciprocals are the hardware v_rcp_f32 (1 ulp): these
+// passes are bound by vector-ALU issue, and an IEEE division costs ten instructions.
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// exp and softplus on the hardware exp2 / log2 (one v_exp_f32 / v_log_f32 each, ~1 ulp), without
+// branches: both sides of torch's threshold (x > 20 -> x) and of the small-value series are formed
+// and selected, so no exec-mask branching sits in the token loops.  NaN propagates.
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * KDN_LOG2E); }
+__device__ __forceinline__ float fsoftplus_y(float x, float y, float d) {  // y = e^min(x, 20), d = 1 + y
+  // every operand is computed first, so both conditionals are selects (a conditional over an
+  // expression is emitted as a branch, and the logarithm would be sunk into it)
+  const float l = __builtin_amdgcn_logf(d) * KDN_LN2;
+  const float small = y * (1.f - 0.5f * y);
+  const float t = y < 1e-3f ? small : l;
+  return x > 20.f ? x : t;
+}
+__device__ __forceinline__ float fsoftplus(float x) {
+  const float y = fexp(x > 20.f ? 20.f : x);
+  return fsoftplus_y(x, y, 1.f + y);
+}
+__device__ __forceinline__ void fsoftplus_sigmoid(float x, float& sp, float& sg) {
+  const float y = fexp(x > 20.f ? 20.f : x);
+  const float d = 1.f + y;
+  sg = y * frcp(d);
+  sp = fsoftplus_y(x, y, d);
+}
+struct FrontTok {
+  float kt[kCPT], al[kCPT], wt[kCPT], ell[kCPT];
+  float r, ir;
+};
+struct FrontSig {
+  float f[kCPT], z[kCPT];
+  float y;
+};
+template <bool BWD, typename TX>
+__device__ __forceinline__ void front_tok(const FrontRaw<TX>& r, float rate, const float* bias, FrontTok& o,
+                                          FrontSig& sg) {
+  const float ik = frcp(fmaxf(r.kn, 1e-12f));
 #pragma unroll
   for (int j = 0; j < kCPT; ++j) {
-    kt[j] = r.k[j] * ik;
-    ell[j] = -rate * softplusf(bfj(r.f, j) + bias[j]);
-    al[j] = __expf(ell[j]);
-    wt[j] = softplusf(bfj(r.z, j));
+    o.kt[j] = r.k[j] * ik;
+    float spf;
+    if (BWD) {
+      fsoftplus_sigmoid(bfj(r.f, j) + bias[j], spf, sg.f[j]);
+      fsoftplus_sigmoid(bfj(r.z, j), o.wt[j], sg.z[j]);
+    } else {
+      spf = fsoftplus(bfj(r.f, j) + bias[j]);
+      o.wt[j] = fsoftplus(bfj(r.z, j));
+    }
+    o.ell[j] = -rate * spf;
+    o.al[j] = fexp(o.ell[j]);
   }
-  return 0.01f + softplusf(r.y);
+  float spy;
+  if (BWD) {
+    fsoftplus_sigmoid(r.y, spy, sg.y);
+  } else {
+    spy = fsoftplus(r.y);
+  }
+  o.r = 0.01f + spy;
+  o.ir = frcp(o.r);
 }
 // the memory path's clamped log-decay (NaN propagates)
-__device__ __forceinline__ float ell_mem(float ell, float al) { return (al >= 1e-6f || al != al) ? ell : kFloorLog; }
+__device__ __forceinline__ float ell_mem(float ell, float al) {
+  const bool floor = al < 1e-6f;  // false for NaN, which propagates
+  return floor ? kFloorLog : ell;
+}
+// p entering the next token: p' = p_hat / (1 + s k^2 / r p_hat), p_hat = alpha^2 p + omega
+__device__ __forceinline__ void front_step(const float* pin, const FrontTok& t, float s, float* pout) {
+#pragma unroll
+  for (int j = 0; j < kCPT; ++j) {
+    const float ph = t.al[j] * t.al[j] * pin[j] + t.wt[j];
+    pout[j] = ph * frcp(1.f + s * t.kt[j] * t.kt[j] * t.ir * ph);
+  }
+}
+// 2x2 product without renormalisation (entries are non-negative and the (2,2) entry of a product of
+// token maps is >= 1, so four tokens stay far inside fp32 range before the renormalisation)
+__device__ __forceinline__ Map2 map_mul_raw(const Map2& a, const Map2& b) {
+  return Map2{a.m0 * b.m0 + a.m1 * b.m2, a.m0 * b.m1 + a.m1 * b.m3, a.m2 * b.m0 + a.m3 * b.m2,
+              a.m2 * b.m1 + a.m3 * b.m3};
+}
+__device__ __forceinline__ void map_renorm(Map2& c) {
+  const float s = fmaxf(fmaxf(fabsf(c.m0), fabsf(c.m1)), fmaxf(fabsf(c.m2), fabsf(c.m3)));
+  const float inv = frcp(fmaxf(s, 1e-30f));
+  c.m0 *= inv, c.m1 *= inv, c.m2 *= inv, c.m3 *= inv;
+}
 
 // Forward map: per channel the tile's composite Mobius map, and the tile's sum of clamped log-decays.
 template <typename TX>
@@ -1072,16 +1150,18 @@ __global__ __launch_bounds__(256) void diag_front_map_kernel(FrontArgs<TX> a, fl
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       if (t + u >= g.t1) break;
-      float kt[kCPT], ell[kCPT], al[kCPT], wt[kCPT];
-      const float rt = front_inputs(raw[u], rate, bias, kt, ell, al, wt);
-      const float iru = 1.f / rt;
+      FrontTok tk;
+      FrontSig unused;
+      front_tok<false>(raw[u], rate, bias, tk, unused);
 #pragma unroll
       for (int j = 0; j < kCPT; ++j) {
-        es[j] += ell_mem(ell[j], al[j]);
-        const float a2 = al[j] * al[j], uu = a.s * kt[j] * kt[j] * iru;
-        M[j] = map_mul(Map2{a2, wt[j], uu * a2, 1.f + uu * wt[j]}, M[j]);
+        es[j] += ell_mem(tk.ell[j], tk.al[j]);
+        const float a2 = tk.al[j] * tk.al[j], uu = a.s * tk.kt[j] * tk.kt[j] * tk.ir;
+        M[j] = map_mul_raw(Map2{a2, tk.wt[j], uu * a2, 1.f + uu * tk.wt[j]}, M[j]);
       }
     }
+#pragma unroll
+    for (int j = 0; j < kCPT; ++j) map_renorm(M[j]);
   }
   const uint32_t tb = (((uint32_t)g.b * a.H + g.h) * a.NV + g.nt) * (uint32_t)a.K + g.i0;
   float4* dst = reinterpret_cast<float4*>(off32(maps, tb * 4u));
@@ -1122,19 +1202,20 @@ __global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, c
     for (int u = 0; u < NB; ++u) {
       if (t + u >= g.t1) break;
       const uint32_t row = front_row(g, a.T, a.H, t + u);
-      float kt[kCPT], ell[kCPT], al[kCPT], wt[kCPT], num[kCPT], gc[kCPT], sq = 0.f;
-      const float rt = front_inputs(raw[u], rate, bias, kt, ell, al, wt);
-      const float ir = 1.f / rt;
+      FrontTok tk;
+      FrontSig unused;
+      front_tok<false>(raw[u], rate, bias, tk, unused);
+      float num[kCPT], gc[kCPT], sq = 0.f;
 #pragma unroll
       for (int j = 0; j < kCPT; ++j) {
-        acc[j] += ell_mem(ell[j], al[j]);
+        acc[j] += ell_mem(tk.ell[j], tk.al[j]);
         gc[j] = acc[j] * KDN_LOG2E;
-        const float ph = al[j] * al[j] * p[j] + wt[j];
-        num[j] = ph * kt[j];
-        sq += num[j] * kt[j];
-        p[j] = ph / (1.f + a.s * kt[j] * kt[j] * ir * ph);
+        const float ph = tk.al[j] * tk.al[j] * p[j] + tk.wt[j];
+        num[j] = ph * tk.kt[j];
+        sq += num[j] * tk.kt[j];
+        p[j] = ph * frcp(1.f + a.s * tk.kt[j] * tk.kt[j] * tk.ir * ph);
       }
-      const float D = rt + tile_sum(sq, tpt), iD = 1.f / D;
+      const float iD = frcp(tk.r + tile_sum(sq, tpt));
 #pragma unroll
       for (int j = 0; j < kCPT; ++j) num[j] *= iD;
       stcf(off32(kappa, row * (uint32_t)a.K + (uint32_t)g.i0), num);
@@ -1147,7 +1228,7 @@ __global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, c
 // tile first replays its forward recurrence from its saved entry value and keeps the precision
 // entering every even token in LDS (kVecChunk / 2 float4 per thread, 8 KB per wave); the reverse
 // pass then takes the tokens in pairs (2q + 1, 2q) and re-derives the odd token's entry value with
-// one forward step of token 2q, whose inputs it has loaded anyway.
+// one forward step of token 2q, whose inputs it computes anyway.
 constexpr int kPairs = kVecChunk / 2;
 __device__ __forceinline__ float4 f4(const float* x) { return float4{x[0], x[1], x[2], x[3]}; }
 __device__ __forceinline__ void unf4(float4 v, float* x) { x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w; }
@@ -1166,24 +1247,12 @@ __device__ __forceinline__ void front_replay(const FrontArgs<TX>& a, const GainT
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       if (t + u >= L) break;
-      if (((t + u) & 1) == 0) lp[(t + u) >> 1][threadIdx.x] = f4(p);
-      float kt[kCPT], ell[kCPT], al[kCPT], wt[kCPT];
-      const float ir = 1.f / front_inputs(raw[u], rate, bias, kt, ell, al, wt);
-#pragma unroll
-      for (int j = 0; j < kCPT; ++j) {
-        const float ph = al[j] * al[j] * p[j] + wt[j];
-        p[j] = ph / (1.f + a.s * kt[j] * kt[j] * ir * ph);
-      }
+      if ((u & 1) == 0) lp[(t + u) >> 1][threadIdx.x] = f4(p);  // t is a multiple of NB (even)
+      FrontTok tk;
+      FrontSig unused;
+      front_tok<false>(raw[u], rate, bias, tk, unused);
+      front_step(p, tk, a.s, p);
     }
-  }
-}
-// One forward precision step of a token: p entering the next token.
-__device__ __forceinline__ void front_step(const float* pin, const float* kt, const float* al, const float* wt,
-                                           float ir, float s, float* pout) {
-#pragma unroll
-  for (int j = 0; j < kCPT; ++j) {
-    const float ph = al[j] * al[j] * pin[j] + wt[j];
-    pout[j] = ph / (1.f + s * kt[j] * kt[j] * ir * ph);
   }
 }
 
@@ -1218,14 +1287,13 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
       ldcf(off32(dkappa, row * (uint32_t)a.K + (uint32_t)g.i0), dk_[u]);
       ldcf(off32(dG, row * (uint32_t)a.K + (uint32_t)g.i0), dg_[u]);
     }
-    float kt[2][kCPT], ell[2][kCPT], al[2][kCPT], wt[2][kCPT], ir[2], rt[2], pp[2][kCPT];
+    FrontTok tk[2];
+    FrontSig unused;
+    float pp[2][kCPT];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      rt[u] = front_inputs(raw[u], rate, bias, kt[u], ell[u], al[u], wt[u]);
-      ir[u] = 1.f / rt[u];
-    }
+    for (int u = 0; u < 2; ++u) front_tok<false>(raw[u], rate, bias, tk[u], unused);
     unf4(lp[q][threadIdx.x], pp[1]);
-    front_step(pp[1], kt[1], al[1], wt[1], ir[1], a.s, pp[0]);
+    front_step(pp[1], tk[1], a.s, pp[0]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tt = 2 * q + 1 - u;
@@ -1233,19 +1301,19 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
         float ph[kCPT], sq = 0.f, gp = 0.f;
 #pragma unroll
         for (int j = 0; j < kCPT; ++j) {
-          ph[j] = al[u][j] * al[u][j] * pp[u][j] + wt[u][j];
-          const float num = ph[j] * kt[u][j];
-          sq += num * kt[u][j];
-          gp += dk_[u][j] * ph[j] * kt[u][j];
+          ph[j] = tk[u].al[j] * tk[u].al[j] * pp[u][j] + tk[u].wt[j];
+          const float num = ph[j] * tk[u].kt[j];
+          sq += num * tk[u].kt[j];
+          gp += dk_[u][j] * num;
         }
-        const float D = rt[u] + tile_sum(sq, tpt), iD = 1.f / D;
+        const float D = tk[u].r + tile_sum(sq, tpt), iD = frcp(D);
         const float G = tile_sum(gp, tpt) * iD;
 #pragma unroll
         for (int j = 0; j < kCPT; ++j) {
-          const float a2 = al[u][j] * al[u][j];
-          const float hh = 1.f + a.s * kt[u][j] * kt[u][j] * ir[u] * ph[j];
-          const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD;
-          const float At = a2 / (hh * hh);
+          const float a2 = tk[u].al[j] * tk[u].al[j], k2 = tk[u].kt[j] * tk[u].kt[j];
+          const float ihh = frcp(1.f + a.s * k2 * tk[u].ir * ph[j]);
+          const float pbar = (dk_[u][j] * tk[u].kt[j] - k2 * G) * iD;
+          const float At = a2 * ihh * ihh;
           Bacc[j] = At * Bacc[j] + a2 * pbar;
           Aacc[j] = At * Aacc[j];
           sg[j] += dg_[u][j];
@@ -1313,60 +1381,60 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
       Gv[u] = *off32(Gsave, row);
       Dv[u] = *off32(Dsave, row);
     }
-    float kt[2][kCPT], ell[2][kCPT], al[2][kCPT], wt[2][kCPT], ir[2], pp[2][kCPT];
+    FrontTok tk[2];
+    FrontSig sgm[2];
+    float pp[2][kCPT];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) ir[u] = 1.f / front_inputs(raw[u], rate, bias, kt[u], ell[u], al[u], wt[u]);
+    for (int u = 0; u < 2; ++u) front_tok<true>(raw[u], rate, bias, tk[u], sgm[u]);
     unf4(lp[q][threadIdx.x], pp[1]);
-    front_step(pp[1], kt[1], al[1], wt[1], ir[1], a.s, pp[0]);
+    front_step(pp[1], tk[1], a.s, pp[0]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tt = 2 * q + 1 - u;
       if (tt < L) {
         const uint32_t row = front_row(g, a.T, a.H, g.t0 + tt);
+        const FrontTok& t = tk[u];
         float dko[kCPT], dfo[kCPT], dwo[kCPT];
-        const float G = Gv[u], iD = 1.f / Dv[u];
+        const float G = Gv[u], iD = frcp(Dv[u]);
         float urr = 0.f;
 #pragma unroll
         for (int j = 0; j < kCPT; ++j) {
-          const float a2 = al[u][j] * al[u][j];
-          const float ph = a2 * pp[u][j] + wt[u][j];
-          const float uu = a.s * kt[u][j] * kt[u][j] * ir[u];
-          const float hh = 1.f + uu * ph, ihh = 1.f / hh;
+          const float a2 = t.al[j] * t.al[j], k2 = t.kt[j] * t.kt[j];
+          const float ph = a2 * pp[u][j] + t.wt[j];
+          const float uu = a.s * k2 * t.ir;
+          const float ihh = frcp(1.f + uu * ph);
           const float pnext = ph * ihh;
-          const float pbar = dk_[u][j] * kt[u][j] * iD - kt[u][j] * kt[u][j] * G * iD + lam[j] * ihh * ihh;
+          const float pbar = (dk_[u][j] * t.kt[j] - k2 * G) * iD + lam[j] * ihh * ihh;
           const float ubar = -lam[j] * pnext * pnext;
-          dko[j] = dk_[u][j] * ph * iD - 2.f * ph * kt[u][j] * G * iD + ubar * (2.f * a.s * kt[u][j] * ir[u]);
-          const float dao = 2.f * al[u][j] * pp[u][j] * pbar;
-          dwo[j] = pbar * sigmoidf(bfj(raw[u].z, j));
-          urr += ubar * (-a.s * kt[u][j] * kt[u][j] * ir[u] * ir[u]);
+          dko[j] = (dk_[u][j] - 2.f * t.kt[j] * G) * ph * iD + ubar * (2.f * a.s * t.kt[j] * t.ir);
+          const float dao = 2.f * t.al[j] * pp[u][j] * pbar;
+          dwo[j] = pbar * sgm[u].z[j];
+          urr -= ubar * uu * t.ir;
           lam[j] = a2 * pbar;
           // retention frontend: alpha = exp(ell), ell = -e^A softplus(f + dt_bias)
-          float sp, sgm;
-          softplus_sigmoid(bfj(raw[u].f, j) + bias[j], sp, sgm);
           accg[j] += dg_[u][j];
-          float dell = al[u][j] >= 1e-6f ? accg[j] : 0.f;
-          dell += dao * al[u][j];
-          dfo[j] = dell * (-rate) * sgm;
-          dA += dell * ell[u][j];
+          float dell = t.al[j] >= 1e-6f ? accg[j] : 0.f;
+          dell += dao * t.al[j];
+          dfo[j] = dell * (-rate) * sgm[u].f[j];
+          dA += dell * t.ell[j];
           ddt[j] += dfo[j];
         }
         stc_bf16(off32(df, row * (uint32_t)a.K + (uint32_t)g.i0), dfo);
         stc_bf16(off32(dz, row * (uint32_t)a.K + (uint32_t)g.i0), dwo);
         const float utot = tile_sum(urr, tpt);
-        if (g.sub == 0) *off32(dy, row) = f2bf((-G * iD + utot) * sigmoidf(raw[u].y));
+        if (g.sub == 0) *off32(dy, row) = f2bf((-G * iD + utot) * sgm[u].y);
         if (dk) {  // VJP of kt = k / max(||k||, 1e-12) applied to dk_gain + dk_memory
           float gk[kCPT], dot = 0.f;
 #pragma unroll
           for (int j = 0; j < kCPT; ++j) {
-            gk[j] = dko[j];
-            gk[j] += bfj(dkm[u], j);
-            dot += kt[u][j] * gk[j];
+            gk[j] = dko[j] + bfj(dkm[u], j);
+            dot += t.kt[j] * gk[j];
           }
           dot = tile_sum(dot, tpt);
-          const float id = 1.f / fmaxf(raw[u].kn, 1e-12f);
+          const float id = frcp(fmaxf(raw[u].kn, 1e-12f));
           const bool clamped = !(raw[u].kn > 1e-12f);
 #pragma unroll
-          for (int j = 0; j < kCPT; ++j) gk[j] = clamped ? gk[j] * id : (gk[j] - kt[u][j] * dot) * id;
+          for (int j = 0; j < kCPT; ++j) gk[j] = clamped ? gk[j] * id : (gk[j] - t.kt[j] * dot) * id;
           stk4<TX>(off32(dk, row * (uint32_t)a.K + (uint32_t)g.i0), gk);
         }
       }
@@ -1379,9 +1447,10 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
   if (g.nt == 0 && dprec_part) {  // lam holds dL/dp_{-1}; p_{-1} = 1/c  ->  dL/dc = -lam p^2
     float cN[kCPT], part = 0.f;
     if (prec_mode == 1) ldcf(prec0 + ((int64_t)g.b * a.H + g.h) * a.K + g.i0, cN);
+    const float c_head = prec_mode == 1 ? 0.f : prior_precision(prec0, prec_mode, g.b, g.h, a.H, a.K, 0);
 #pragma unroll
     for (int j = 0; j < kCPT; ++j) {
-      const float c = prec_mode == 0 ? prec0[g.h] : cN[j];
+      const float c = prec_mode == 1 ? cN[j] : c_head;
       const float p0 = 1.f / c;
       cN[j] = -lam[j] * p0 * p0;
       part += cN[j];
@@ -1395,11 +1464,6 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
   }
 }
 
-// mu = 0.1 + softplus(mu_param) (the frontend's per-head prior precision)
-__global__ void front_mu_kernel(const float* __restrict__ mu_param, int H, float* __restrict__ mu) {
-  const int h = blockIdx.x * blockDim.x + threadIdx.x;
-  if (h < H) mu[h] = 0.1f + softplusf(mu_param[h]);
-}
 // d mu_param = sigmoid(mu_param) * sum_b part[b, h]   (or d prior [H] = sum_b part[b, h] when mu_param is null)
 __global__ void front_dmu_kernel(const float* __restrict__ part, const float* __restrict__ mu_param, int B, int H,
                                  float* __restrict__ out) {
@@ -1642,9 +1706,10 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
 // ---------------------------------------------------------------- fused diag frontend + gain
 namespace {
 struct FrontLayout {  // float offsets into the workspace (each 64-float aligned)
-  int64_t maps, tsum, carry, mu, grp, ab, lcarry, tdg, G, D, partA, partdt, dpart, total;
+  int64_t maps, tsum, carry, grp, ab, lcarry, tdg, G, D, partA, partdt, dpart, seg, total;
 };
 inline int64_t al64(int64_t x) { return (x + 63) / 64 * 64; }
+constexpr int kFrontReduceSegments = 32;
 constexpr int64_t kFrontMaxElems = int64_t(1) << 30;  // per launch, so 32-bit byte offsets of f32 arrays hold
 // Batch rows per launch of the tile kernels.
 inline int front_batch_chunk(int B, int T, int H, int K) {
@@ -1669,13 +1734,13 @@ FrontLayout front_layout(int B, int T, int H, int K) {
   L.tdg = L.tsum;
   L.carry = o; o += al64(BHK * NV);      // forward tile carries (when not saved); backward lambda carries
   L.lcarry = L.carry;
-  L.mu = o; o += al64(H);
   L.grp = o; o += al64(BHK * NG * 5);    // two-level carry composites and start values
   L.G = o; o += al64((int64_t)B * T * H);
   L.D = o; o += al64((int64_t)B * T * H);
   L.partA = o; o += al64((int64_t)B * NV * H);
   L.partdt = o; o += al64(BHK * NV);
   L.dpart = o; o += al64((int64_t)B * H);
+  L.seg = o; o += al64((int64_t)kFrontReduceSegments * H * K);
   L.total = o;
   return L;
 }
@@ -1706,10 +1771,7 @@ int front_fwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   float* maps = ws + L.maps;
   float* tsum = ws + L.tsum;
   float* carry = saved ? saved : ws + L.carry;
-  if (mu_param) {
-    hipLaunchKernelGGL(front_mu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, mu_param, a.H, ws + L.mu);
-    prec0 = ws + L.mu;
-  }
+  if (mu_param) prec0 = mu_param, prec_mode = 2;  // the kernels form mu = 0.1 + softplus(mu_param)
   const int Bc = front_batch_chunk(a.B, a.T, a.H, a.K);
   const int64_t ev = (int64_t)a.H * NV * a.K, ee = (int64_t)a.T * a.H * a.K;  // per batch row
   for (int b0 = 0; b0 < a.B; b0 += Bc) {
@@ -1752,10 +1814,7 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   float* tdg = ws + L.tdg;
   float* G = ws + L.G;
   float* D = ws + L.D;
-  if (mu_param) {
-    hipLaunchKernelGGL(front_mu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, mu_param, a.H, ws + L.mu);
-    prec0 = ws + L.mu;
-  }
+  if (mu_param) prec0 = mu_param, prec_mode = 2;  // the kernels form mu = 0.1 + softplus(mu_param)
   const int Bc = front_batch_chunk(a.B, a.T, a.H, a.K);
   const int64_t ev = (int64_t)a.H * NV * a.K, ee = (int64_t)a.T * a.H * a.K, er = (int64_t)a.T * a.H;
   for (int b0 = 0; b0 < a.B; b0 += Bc) {
@@ -1779,7 +1838,7 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
                        d_final_precision, final_precision, a.H, a.K, NV, lcarry);
   }
   const bool want_prec = d_mu_param || d_prec;
-  float* dprec_out = want_prec ? (prec_mode == 1 ? d_prec : ws + L.dpart) : nullptr;
+  float* dprec_out = want_prec ? (prec_mode == 1 ? d_prec : ws + L.dpart) : nullptr;  // [B,H,K] or [B,H]
   for (int b0 = 0; b0 < a.B; b0 += Bc) {
     const int nb = std::min(Bc, a.B - b0);
     const int64_t ep = prec_mode == 1 ? (int64_t)a.H * a.K : a.H;  // per batch row of [B,H,K] / [B,H]
@@ -1796,10 +1855,16 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   if (dA_log)
     hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(a.H, 64)), dim3(256), 0, stream, ws + L.partA, NP,
                        (int64_t)a.H, a.H, dA_log);
-  if (ddt_bias)
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv((int64_t)a.H * a.K, 64)), dim3(256), 0, stream,
-                       ws + L.partdt, NP, (int64_t)a.H * a.K, a.H * a.K, ddt_bias);
-  if (want_prec && prec_mode == 0)
+  if (ddt_bias) {  // B*NV partial rows of H*K: segments first, then the segment sums
+    const int S = std::max(1, std::min(kFrontReduceSegments, NP / 64));
+    float* seg = ws + L.seg;
+    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv((int64_t)a.H * a.K, 64), S), dim3(256), 0, stream,
+                       ws + L.partdt, NP, (int64_t)a.H * a.K, a.H * a.K, S > 1 ? seg : ddt_bias);
+    if (S > 1)
+      hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv((int64_t)a.H * a.K, 64)), dim3(256), 0, stream, seg,
+                         S, (int64_t)a.H * a.K, a.H * a.K, ddt_bias);
+  }
+  if (want_prec && prec_mode != 1)
     hipLaunchKernelGGL(front_dmu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, ws + L.dpart,
                        d_mu_param ? mu_param : nullptr, a.B, a.H, d_mu_param ? d_mu_param : d_prec);
   KDN_CHECK_LAUNCH();

@@ -3,11 +3,12 @@ frontend -> vector gain in one op, reference lit_gpt/diag_kdn.py:315-345) agains
 ops it replaces (``_diag_kdn_normalize``, ``_diag_kdn_frontend_precumsum_paired``, ``_diag_kdn_gain``),
 which the other GPU tests pin to the CPU oracle.
 
-The fused kernels recompute alpha, omega, r and the fp32 gain key with the standalone kernels' own
-operations, so kappa, the final precision and the normalised q/k agree to the last few ulp; the
-log-decay prefix and the parameter gradients are sums taken in a different order (per 16-token tile
-instead of per 4-token group), so they agree to fp32 rounding.  Tolerances: 1e-6 for forward values,
-2e-5 (max-relative) for fp32 gradients; a bf16 gradient (the raw logits', and the key's for bf16 keys)
+The normalised q/k come from the same kernel (bit-identical).  The fused kernels recompute alpha,
+omega and r on the hardware exp2 / log2 / reciprocal (~1 ulp each, branch-free) where the standalone
+kernels use the library exp / log and IEEE division, and sum the log-decay prefix and the parameter
+gradients in another order (per 16-token tile instead of per 4-token group); alpha = exp(-e^A
+softplus(.)) carries a relative error of about e^A softplus(.) ulp.  Tolerances: 2e-5 (max-relative)
+for forward values and fp32 gradients; a bf16 gradient (the raw logits', and the key's for bf16 keys)
 may differ by one bf16 rounding step where the fp32 values straddle a rounding boundary, so each of its
 elements must agree within 2^-7 relative (one bf16 ulp is 2^-8 to 2^-7 of the value) plus 1e-6 of the
 tensor's largest element."""
@@ -18,7 +19,7 @@ from gpu_util import gpu_or_skip, log, rel
 
 pytestmark = pytest.mark.gpu
 
-TOL_FWD = 1e-6
+TOL_FWD = 2e-5
 TOL_GRAD = 2e-5
 
 
