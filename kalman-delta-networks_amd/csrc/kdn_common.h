@@ -71,6 +71,35 @@ __device__ __forceinline__ void softplus_sigmoid(float x, float& sp, float& sg) 
   sp = x > 20.f ? x : (y < 1e-3f ? y * (1.f - 0.5f * y) : __logf(d));
 }
 
+// Fast forms for kernels bound by vector-ALU issue: the hardware reciprocal (v_rcp_f32, 1 ulp; an IEEE
+// division is about ten instructions), exp and log on v_exp_f32 / v_log_f32 (~1 ulp), and
+// branch-free softplus / sigmoid.
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// exp and softplus on the hardware exp2 / log2 (one v_exp_f32 / v_log_f32 each, ~1 ulp), without
+// branches: both sides of torch's threshold (x > 20 -> x) and of the small-value series are formed
+// and selected, so no exec-mask branching sits in the token loops.  NaN propagates.
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * KDN_LOG2E); }
+__device__ __forceinline__ float fsoftplus_y(float x, float y, float d) {  // y = e^min(x, 20), d = 1 + y
+  // every operand is computed first, so both conditionals are selects (a conditional over an
+  // expression is emitted as a branch, and the logarithm would be sunk into it)
+  const float l = __builtin_amdgcn_logf(d) * KDN_LN2;
+  const float small = y * (1.f - 0.5f * y);
+  const float t = y < 1e-3f ? small : l;
+  return x > 20.f ? x : t;
+}
+__device__ __forceinline__ float fsoftplus(float x) {
+  const float y = fexp(x > 20.f ? 20.f : x);
+  return fsoftplus_y(x, y, 1.f + y);
+}
+__device__ __forceinline__ void fsoftplus_sigmoid(float x, float& sp, float& sg) {
+  const float y = fexp(x > 20.f ? 20.f : x);
+  const float d = 1.f + y;
+  sg = y * frcp(d);
+  sp = fsoftplus_y(x, y, d);
+}
+// sigmoid(x) = 1 / (1 + e^-x) on the hardware exp and reciprocal
+__device__ __forceinline__ float fsigmoid(float x) { return frcp(1.f + fexp(-x)); }
+
 // ---- wave64 reductions -----------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

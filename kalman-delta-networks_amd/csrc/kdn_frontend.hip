@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
   const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
-  const float rate = __expf(A_log[h]);
+  const float rate = __expf(A_log[h]);  // once per thread
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
   // per-token omega / r: thread tid owns token tid (chunk <= 256; loads clamped to the chunk)
@@ -171,8 +171,8 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
   }
   if (tid < L) {
     const int64_t o = ((int64_t)b * T + t0 + tid) * H + h;
-    omega_out[o] = omega_min + softplusf(or_t + omega_bias[h]);
-    r_out[o] = r_min + softplusf(rr_t + r_bias[h]);
+    omega_out[o] = omega_min + fsoftplus(or_t + omega_bias[h]);
+    r_out[o] = r_min + fsoftplus(rr_t + r_bias[h]);
   }
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float pre[4][8];  // local inclusive prefix per token (TPG <= 4 when K >= 64 and chunk <= 64)
@@ -184,10 +184,10 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     if (u < TPG && t < L) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float g = -rate * softplusf(xr[u][j] + bias[j]);
+        const float g = -rate * fsoftplus(xr[u][j] + bias[j]);
         acc[j] += g;
         pre[u][j] = acc[j];
-        e2[u] += __expf(2.f * g);
+        e2[u] += fexp(2.f * g);
       }
     }
   }
@@ -212,9 +212,9 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     // a = mean over channels of e^{2g}: reduce over the CG consecutive lanes of this token group
     float s = e2[u];
     for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
-    if (cg == 0 && u < TPG && t < L) a_out[((int64_t)b * T + t0 + t) * H + h] = s / (float)K;
+    if (cg == 0 && u < TPG && t < L) a_out[((int64_t)b * T + t0 + t) * H + h] = s * (1.f / (float)K);  // K is a power of two: exact
   }
-  if (blockIdx.x < H && tid == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
+  if (blockIdx.x < H && tid == 0) mu_out[h] = 0.1f + fsoftplus(mu_param[h]);
 }
 
 // grid (H * B * NT) with the head fastest, block 256.  Per-block partials as in iso_gate_bwd_kernel.
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
   const int t0 = nt * chunk, L = min(chunk, T - t0);
   const int p = blockIdx.x / H;
-  const float rate = __expf(A_log[h]);
+  const float rate = __expf(A_log[h]);  // once per thread
   float bias[8];
   load8<float>(dt_bias + h * K + i0, bias);
   // per-token scalars: thread tid owns token tid (chunk <= 256; loads clamped to the chunk, only
@@ -293,10 +293,10 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
       for (int j = 0; j < 8; ++j) {
         const float xb = xr[u][j] + bias[j];
         float sp, sg;
-        softplus_sigmoid(xb, sp, sg);
+        fsoftplus_sigmoid(xb, sp, sg);
         const float g = -rate * sp;
         float dgl = dg_pre ? off[j] + dgp[u][j] : 0.f;
-        if (da) dgl += dau * __expf(2.f * g);
+        if (da) dgl += dau * fexp(2.f * g);
         dgr[j] = dgl * (-rate) * sg;
         dA_term += dgl * g;
         ddt[j] += dgr[j];
@@ -305,8 +305,8 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     }
   }
   if (tid < L) {  // the per-token omega / r terms of token tid
-    const float ob = domega ? do_t * sigmoidf(or_t + omega_bias[h]) : 0.f;
-    const float rb = dr ? dr_t * sigmoidf(rr_t + r_bias[h]) : 0.f;
+    const float ob = domega ? do_t * fsigmoid(or_t + omega_bias[h]) : 0.f;
+    const float rb = dr ? dr_t * fsigmoid(rr_t + r_bias[h]) : 0.f;
     dob = ob;
     drb = rb;
     if (dorr) {

@@ -239,7 +239,9 @@ def _iso_kdn_gain_backward(a, omega, r, initial_precision, dgain, p_prev, *, pos
     da = torch.empty_like(a)
     domega = torch.empty_like(omega)
     dr = torch.empty_like(r)
-    dmu = torch.zeros(initial_precision.shape, dtype=torch.float32, device=device)
+    # the backward carry kernel writes every entry of dmu; only the token-free case needs zeros
+    dmu = (torch.empty if (T > 0 and B > 0) else torch.zeros)(initial_precision.shape, dtype=torch.float32,
+                                                              device=device)
     if T > 0 and B > 0:
         ws_bytes = _lib.size("kdn_iso_gain_workspace_size", B, T, H)
         ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=device)
