@@ -41,6 +41,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
 # MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
 # MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
 MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_fwd": "bf16x3", "mem_readout_fwd": "bf16x3",
+             "mem_state_readout_fwd": "bf16x3",
              "mem_state_bwd": "bf16x3", "mem_bwd_hgrad": "bf16x3", "mem_bwd_solve_contrib": "bf16x3"}
 
 
@@ -66,6 +67,10 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
         # Qg, M, h, delta -> o  (chunk-parallel readout)
         "mem_readout_fwd": (4 * K + mm + h_b + 4 * V + (2 if variant == "iso" else 4) * V,
                             2 * (K * V + C * V / 2)),
+        # U, W, Kf, g_last, Qg, M -> h, delta, o  (one chunk group: the state pass does the readout)
+        "mem_state_readout_fwd": (4 * V + 8 * K + 4 * K / C + h_b + 4 * V + 4 * K + mm
+                                  + (2 if variant == "iso" else 4) * V,
+                                  2 * 2 * K * V + 2 * (K * V + C * V / 2)),
         # M, Kf, Qg, W, dO -> dh, d delta
         "mem_state_bwd": (mm + 12 * K + do_b + h_b + 4 * V, 2 * (C * V / 2 + 3 * K * V)),
         # h, dh, delta, d delta, dO -> dQg, dW, dKf, dM
@@ -164,7 +169,9 @@ def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K
     counts.update(frontend_counts(variant, B, T, H, K))
     per_kernel = {}
     for tag, (nbytes, flops) in counts.items():
-        t = kernel_ms.get(tag, float("nan")) * 1e-3
+        if tag not in kernel_ms:  # an entry point this shape does not call (e.g. the separate readout when fused)
+            continue
+        t = kernel_ms[tag] * 1e-3
         t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
         t_mfma = flops / (mfma_peak(tag) * 1e12)
         bound = "hbm" if t_hbm >= t_mfma else "mfma"

@@ -44,7 +44,7 @@ using kdn_state::zero4;
 constexpr float kAnchorSpanMax = 100.f;  // base 2, one anchor per chunk: R <= 2^100 stays far inside fp32
 constexpr float kBlockSpanMax = 120.f;   // base 2, per 16-token block: every product stays below 2^120
 constexpr int AP = C + 1;                // LDS row stride of the fp32 N and A tiles
-constexpr int XS = C + 4;                // LDS row stride of the staged [column][s] operands
+constexpr int XR = 128 + 4;              // LDS row stride of the staged [s][column] operands (<= 128 columns)
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -164,8 +164,8 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
       const float x[8] = {row[0], row[1], row[2], row[3], row[16], row[17], row[18], row[19]};
       split8(x, ah[I][kb], al[I][kb]);
     }
-  // U = A V and W = A Kg (Kg = k 2^G) in transposed form: the operand (staged in LDS as columns
-  // [col][s], loaded coalesced as rows) is the A fragment and A's rows the B fragment, so the D
+  // U = A V and W = A Kg (Kg = k 2^G) in transposed form: the operand (loaded coalesced as rows and
+  // staged in LDS row-major [s][col], read back by columns) is the A fragment and A's rows the B fragment, so the D
   // tile gives each lane 4 consecutive output columns of one chunk row (16-byte stores).
   __syncthreads();  // every wave has its A fragments; the buffer is free
   auto stage = [&](auto is_u) {
@@ -185,8 +185,10 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] *= exp2f(g[j]);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sX[(c8 + j) * XS + sr] = x[j];
+      // row-major [s][col]: the 16 lanes of a row write consecutive 16-byte pieces (a column-major
+      // store here put 16 lanes on one bank)
+      *reinterpret_cast<float4*>(sX + sr * XR + c8) = float4{x[0], x[1], x[2], x[3]};
+      *reinterpret_cast<float4*>(sX + sr * XR + c8 + 4) = float4{x[4], x[5], x[6], x[7]};
     }
   };
   auto tile = [&](auto is_u, int t) {
@@ -195,9 +197,15 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
     uint4 xh[2], xl[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const float* colp = sX + (16 * t + r16) * XS + 32 * kb + 4 * g4;
-      const float4 a0 = *reinterpret_cast<const float4*>(colp), a1 = *reinterpret_cast<const float4*>(colp + 16);
-      const float x[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      // column 16 t + r16, rows 32 kb + 4 g4 + (0..3) and + 16: with the row pitch XR = 4 (mod 64)
+      // the 64 lanes of each read fall on 64 different banks
+      const float* colp = sX + (32 * kb + 4 * g4) * XR + 16 * t + r16;
+      float x[8];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        x[jj] = colp[jj * XR];
+        x[4 + jj] = colp[(16 + jj) * XR];
+      }
       split8(x, xh[kb], xl[kb]);  // exact for V (lo = 0)
     }
     const bufrsrc rO = isU ? rU : rW;
@@ -237,13 +245,13 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
   constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
   // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
-  constexpr int SBYTES = RABYTES + C * AP * 4 > 128 * XS * 4 ? RABYTES + C * AP * 4 : 128 * XS * 4;
+  constexpr int SBYTES = RABYTES + C * AP * 4 > C * XR * 4 ? RABYTES + C * AP * 4 : C * XR * 4;
   static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
   __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
   bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
-  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
+  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand rows [s][col], pitch XR
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
@@ -371,13 +379,13 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
   constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
   // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
-  constexpr int SBYTES = RABYTES + C * AP * 4 > 128 * XS * 4 ? RABYTES + C * AP * 4 : 128 * XS * 4;
+  constexpr int SBYTES = RABYTES + C * AP * 4 > C * XR * 4 ? RABYTES + C * AP * 4 : C * XR * 4;
   static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
   __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
   bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
-  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand columns [col][s], pitch XS
+  float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand rows [s][col], pitch XR
   __shared__ float sSpan[4];
   __shared__ __attribute__((aligned(16))) float sMid[4 * K];  // block anchors m_J per channel
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;

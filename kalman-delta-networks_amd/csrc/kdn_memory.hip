@@ -869,6 +869,21 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     }
     KDN_CHECK_LAUNCH();
   }
+  // One chunk group and both stages asked for: the state pass does the readout itself (helper waves
+  // stage Qg and M; see state_fwd_kernel), so the chunk-parallel readout is not launched.
+  const bool fused_readout = (stages & 6) == 6 && lay.gc.NG == 1;
+  if (fused_readout) {
+    const dim3 grid(B * H * (V / kdn_state::state_cols(V))), bs(2 * kdn_state::state_threads(V));
+    const kdn_state::GroupPlan P{1, NT, 0, nullptr, nullptr};
+    if (o_bf16)
+      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t, true>), grid, bs, 0, stream, U, W, Kf, gc, h0, T,
+                         H, NT, B * H, hb, D, ht, P, Qg, M, (bf16_t*)o);
+    else
+      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, true>), grid, bs, 0, stream, U, W, Kf, gc, h0, T,
+                         H, NT, B * H, hb, D, ht, P, Qg, M, (float*)o);
+    KDN_CHECK_LAUNCH();
+    return 0;
+  }
   if (stages & 2) {  // serial state pass (one- or two-level): h per chunk, delta, final state
     const dim3 bs(kdn_state::state_threads(V));
     const int rc = run_state_pass<K, V>(B * H, lay.gc, saved + lay.grp, false, stream,

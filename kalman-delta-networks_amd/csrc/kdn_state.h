@@ -139,6 +139,8 @@ __device__ __forceinline__ void afrag(const bf16_t* buf, int tile, int lane, uin
 // Stores of one lane's 4 D-layout values (rows r0 + j of a column) with one voffset: the row
 // block goes into the descriptor base (rows past the end stay range-checked) and the row j
 // into the instruction's immediate offset, so no per-element address registers are kept.
+// (Quad-transposing the tile for 16-byte stores measured slower on the serial chain: the DPP
+// transposes cost more issue than the store instructions they save.)
 __device__ __forceinline__ void st_rows4(bufrsrc r, uint32_t vbase, uint32_t row_bytes, const f32x4& x) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x[j]), r, vbase + j * row_bytes, 0, 0);
@@ -242,20 +244,31 @@ __device__ __forceinline__ bool group_task(const GroupPlan& P, int BH, int& bh, 
 // The readout O = Qg h + M delta is left to readout_kernel: it is off the serial chain, and its
 // operands (Qg, M) would double the chunk operands staged on the chain's critical path.
 // ===========================================================================
-template <int K, int V>
-__global__ __launch_bounds__(state_threads(V), 2) void state_fwd_kernel(const float* __restrict__ U, const float* __restrict__ W,
-                                                        const float* __restrict__ Kf, const float* __restrict__ gc,
-                                                        const float* __restrict__ h0, int T, int H, int NT, int BH,
-                                                        float* __restrict__ hbuf, float* __restrict__ Dl,
-                                                        float* __restrict__ ht, GroupPlan P) {
+// With RO (one chunk group only) the pass also does the readout O = Qg h + M delta of every chunk.
+// The block gets four readout waves.  In phase 1 of chunk n each state wave publishes the split B
+// fragments of h_n (its state, as it multiplies W with it) and of delta_n to LDS; in phase 2 the
+// readout waves multiply them with the A fragments of their 16 chunk rows of Qg and M (loaded from
+// HBM one chunk ahead, straight into registers) and store o.  That drops readout_kernel and its
+// re-reads of h and delta, and keeps the readout's MFMAs and stores off the serial chain, which only
+// pays for the fragment stores.  Both wave groups run the same barrier sequence.
+template <int K, int V, typename TO = float, bool RO = false>
+__global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 1 : 2) void state_fwd_kernel(
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ Kf,
+    const float* __restrict__ gc, const float* __restrict__ h0, int T, int H, int NT, int BH,
+    float* __restrict__ hbuf, float* __restrict__ Dl, float* __restrict__ ht, GroupPlan P,
+    const float* __restrict__ Qg = nullptr, const float* __restrict__ Mg = nullptr, TO* __restrict__ out = nullptr) {
   constexpr int COLS = state_cols(V), NTHR = state_threads(V);
   constexpr int KB = K / 32;           // k-blocks of a contraction over K
   constexpr int ST = K / 16;           // state row tiles per wave
   static_assert((C * K / 4) % NTHR == 0, "staging units per thread");
   constexpr int UN = C * K / 4 / NTHR;  // staging units per thread of a C x K operand
+  constexpr int UM = C * C / 4 / NTHR;  // ... of the C x C readout matrix M
   __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
   __shared__ __attribute__((aligned(16))) float sE[K];
+  // RO: B fragments of h_n ([wave][kb][hi, lo][lane], K / 32 k-blocks) then of delta_n (2 k-blocks)
+  constexpr int NHF = 4 * KB * 2 * 64, NDF = 4 * 2 * 2 * 64;
+  __shared__ __attribute__((aligned(16))) uint4 sHD[RO ? NHF + NDF : 1];
   int bh, vs, g;
   bool real, phi;
   if (!group_task<V, K, false>(P, BH, bh, vs, g, real, phi)) return;
@@ -263,6 +276,77 @@ __global__ __launch_bounds__(state_threads(V), 2) void state_fwd_kernel(const fl
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
   const int col = vs * COLS + 16 * w + (lane & 15);  // this lane's state column (>= V: a Phi column)
   const int n0 = g * P.m, n1 = P.NG == 1 ? NT : min(NT, n0 + P.m);
+
+  if constexpr (RO) {
+    if (tid >= NTHR) {  // readout waves: wave rw owns chunk rows 16 rw .. 16 rw + 15 of all COLS columns
+      const int rw = w - 4, r16 = lane & 15;
+      const uint32_t c = (uint32_t)(16 * rw + r16);
+      float4 rq[KB][2], rm[2][2];
+      auto load_QM = [&](int n) {  // this lane's A fragment slots of Qg and M rows (permuted k order)
+        const int t0 = n * C, L = min(C, T - t0);
+        const bufrsrc rq_ = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);  // rows past L read 0
+        const bufrsrc rm_ = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) rq[kb][hf] = buf_ld4(rq_, (c * K + 32 * kb + 16 * hf + 4 * g4) * 4);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) rm[kb][hf] = buf_ld4(rm_, (c * C + 32 * kb + 16 * hf + 4 * g4) * 4);
+      };
+      load_QM(n0);
+      __syncthreads();  // the state waves' prologue barrier
+      for (int n = n0; n < n1; ++n) {
+        const int t0 = n * C, L = min(C, T - t0);
+        uint4 qh[KB], ql[KB], mh[2], ml[2];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const float x[8] = {rq[kb][0].x, rq[kb][0].y, rq[kb][0].z, rq[kb][0].w,
+                              rq[kb][1].x, rq[kb][1].y, rq[kb][1].z, rq[kb][1].w};
+          split8v(x, qh[kb], ql[kb]);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const float x[8] = {rm[kb][0].x, rm[kb][0].y, rm[kb][0].z, rm[kb][0].w,
+                              rm[kb][1].x, rm[kb][1].y, rm[kb][1].z, rm[kb][1].w};
+          split8v(x, mh[kb], ml[kb]);
+        }
+        if (n + 1 < n1) load_QM(n + 1);
+        __syncthreads();  // end of phase 1: h_n and delta_n fragments published
+        const bufrsrc ro = make_buf(out + row_bthk(b, t0, h, T, H, V), (uint32_t)((L - 1) * H + 1) * V * sizeof(TO));
+        const int qr = lane & 3;
+#pragma unroll
+        for (int sw = 0; sw < 4; ++sw) {  // the 16 columns of state wave sw (four independent chains)
+          f32x4 O = zero4();
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            const uint4 bh2 = sHD[((sw * KB + kb) * 2) * 64 + lane], bl2 = sHD[((sw * KB + kb) * 2 + 1) * 64 + lane];
+            O = mma3(qh[kb], ql[kb], bh2, bl2, O);
+          }
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            if (kb == 1 && rw < 2) continue;  // M[c][s] = 0 for s > c
+            const uint4 dh2 = sHD[NHF + ((sw * 2 + kb) * 2) * 64 + lane], dl2 = sHD[NHF + ((sw * 2 + kb) * 2 + 1) * 64 + lane];
+            O = mma3(mh[kb], ml[kb], dh2, dl2, O);
+          }
+          // lane (column 4 q + r, rows 4 g4 ..) -> quad transpose -> row 4 g4 + r, columns 4 q .. 4 q + 3
+          const float4 y = quad_transpose(float4{O[0], O[1], O[2], O[3]}, qr);
+          const uint32_t e = (uint32_t)((16 * rw + 4 * g4 + qr) * H) * V +
+                             (uint32_t)(vs * COLS + 16 * sw + 4 * ((lane & 15) >> 2));  // rows past L dropped
+          if constexpr (sizeof(TO) == 2) {
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{(uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16), (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16)},
+                ro, e * 2, 0, 0);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, e * 4, 0, 0);
+          }
+        }
+        __syncthreads();  // end of phase 2: the fragments may be overwritten
+      }
+      return;
+    }
+  }
 
   float4 rW[UN];
   float rK[UN][4], rU[4][4], rE = 0.f;
@@ -361,6 +445,20 @@ __global__ __launch_bounds__(state_threads(V), 2) void state_fwd_kernel(const fl
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
           st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, D[cb]);  // rows past L dropped
+      }
+      if constexpr (RO) {  // publish the B fragments of h_n (multiplied with W above) and delta_n
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          sHD[((w * KB + kb) * 2) * 64 + lane] = bh_[kb];
+          sHD[((w * KB + kb) * 2 + 1) * 64 + lane] = bl_[kb];
+        }
+        uint4 dh2, dl2;
+        bfrag(D[0], D[1], dh2, dl2);
+        sHD[NHF + ((w * 2) * 2) * 64 + lane] = dh2;
+        sHD[NHF + ((w * 2) * 2 + 1) * 64 + lane] = dl2;
+        bfrag(D[2], D[3], dh2, dl2);
+        sHD[NHF + ((w * 2 + 1) * 2) * 64 + lane] = dh2;
+        sHD[NHF + ((w * 2 + 1) * 2 + 1) * 64 + lane] = dl2;
       }
     }
     __syncthreads();

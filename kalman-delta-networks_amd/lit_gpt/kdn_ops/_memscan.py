@@ -10,6 +10,13 @@ import torch
 from . import _lib
 
 FWD_STAGES = ((1, "mem_intra_fwd"), (2, "mem_state_fwd"), (4, "mem_readout_fwd"))
+# with one chunk group the state pass also does the readout (one launch for bits 2 and 4)
+FWD_STAGES_FUSED = ((1, "mem_intra_fwd"), (6, "mem_state_readout_fwd"))
+
+
+def state_groups(B: int, T: int, H: int, K: int, V: int) -> int:
+    """Chunk groups of the serial state passes at this shape (1: one pass, readout fused)."""
+    return int(_lib.load().kdn_mem_state_groups(B, T, H, K, V))
 # bit 4: the transposed solves of the chunks left to the exact path; bit 8: solves + gradients of
 # every other chunk in one kernel, then the exact path's gradients
 BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_hgrad"), (4, "mem_bwd_exact_solve"), (8, "mem_bwd_solve_contrib"))
@@ -27,7 +34,7 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
     ht = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if output_final_state else None
     h0 = initial_state.float().contiguous() if initial_state is not None else None
     stream = _lib.stream_of(q)
-    for bit, tag in FWD_STAGES:
+    for bit, tag in (FWD_STAGES_FUSED if state_groups(B, T, H, K, V) == 1 else FWD_STAGES):
         _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(v),
                   _lib.ptr(g_cumsum), B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(),
                   _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), bit, stream, tag=tag)
