@@ -922,12 +922,13 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
   dim3 gchunk(NT, B * H);
   if (stages & 1) {  // reverse state pass (one- or two-level): dh per chunk, d delta, d h0
-    const dim3 bs(kdn_state::state_threads(V));
+    // helper waves take M^T dO and Qg^T dO off the serial chain (see state_bwd_kernel)
+    const dim3 bs(2 * kdn_state::state_threads(V));
     const int rc = run_state_pass<K, V>(B * H, bl.gc, work + bl.grp, true, stream,
                                         [&](dim3 grid, const kdn_state::GroupPlan& P) {
-                                          hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO>), grid, bs, 0,
-                                                             stream, M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H, dh,
-                                                             dD, dh0, P);
+                                          hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO, true>), grid, bs,
+                                                             0, stream, M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H,
+                                                             dh, dD, dh0, P);
                                         });
     if (rc) return rc;
   }

@@ -628,76 +628,58 @@ __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict
 // ===========================================================================
 // Reverse state pass.  grid: (B*H*V/COLS) for one group, or the pass's task count (GroupPlan);
 // block 4 COLS.  LDS 112.5 KB.
+// With HW the block gets four helper waves (block 8 COLS, LDS 128.5 KB).  The products M^T dO and
+// Qg^T dO do not depend on the recurrence, so the helpers compute them one phase ahead of the state
+// waves and hand them over through LDS in the state waves' D layout: Qg^T dO of chunk n during
+// phase 1 of chunk n (added to dS in phase 2), M^T dO of chunk n - 1 during phase 2 of chunk n
+// (added to d delta in phase 1 of chunk n - 1).  Helper wave hw owns the row tiles of those
+// products (Qg^T row tiles hw ST/4 .., M^T row tile hw) for all four column groups: their A
+// fragments (columns of Qg and M) are loaded straight into registers, one chunk ahead; each helper
+// loads dO of one column group and publishes its B fragments to the others through LDS.  The state
+// waves then stage only Kf and W^T and issue 32 split products per chunk instead of 56.  Both wave
+// groups run the same barrier sequence: two in the prologue, two per chunk.
 // ===========================================================================
-template <int K, int V, typename TDO>
-__global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float* __restrict__ Mg, const float* __restrict__ Kf,
-                                                        const float* __restrict__ Qg, const float* __restrict__ W,
-                                                        const float* __restrict__ gc, const TDO* __restrict__ dO,
-                                                        const float* __restrict__ dht, int T, int H, int NT, int BH,
-                                                        float* __restrict__ dhbuf, float* __restrict__ dDl,
-                                                        float* __restrict__ dh0, GroupPlan P) {
+template <int K, int V, typename TDO, bool HW = false>
+__global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void state_bwd_kernel(
+    const float* __restrict__ Mg, const float* __restrict__ Kf, const float* __restrict__ Qg,
+    const float* __restrict__ W, const float* __restrict__ gc, const TDO* __restrict__ dO,
+    const float* __restrict__ dht, int T, int H, int NT, int BH, float* __restrict__ dhbuf,
+    float* __restrict__ dDl, float* __restrict__ dh0, GroupPlan P) {
   constexpr int COLS = state_cols(V), NTHR = state_threads(V);
   constexpr int KB = K / 32;
   constexpr int ST = K / 16;
   static_assert((C * K / 4) % NTHR == 0 && (C * C / 4) % NTHR == 0, "staging units per thread");
+  static_assert(!HW || (COLS == 64 && ST % 4 == 0), "helper waves: four state waves, K a multiple of 64");
   constexpr int UN = C * K / 4 / NTHR;  // staging units per thread of a C x K operand
   constexpr int UM = C * C / 4 / NTHR;  // ... of M^T
   constexpr bool DO_BF16 = sizeof(TDO) == 2;
-  // phase 1: M^T (rows c', k = c) and Kf (rows c, k = i);  phase 2: Qg^T, W^T (rows i, k = c)
-  __shared__ __attribute__((aligned(16))) bf16_t sM[(C / 16) * (C / 32) * TILE];
+  // phase 1: M^T (rows c', k = c) and Kf (rows c, k = i);  phase 2: Qg^T, W^T (rows i, k = c).
+  // HW: M^T and Qg^T are not staged; the helpers' products and dO fragments take their place.
+  __shared__ __attribute__((aligned(16))) bf16_t sM[HW ? 8 : (C / 16) * (C / 32) * TILE];
   __shared__ __attribute__((aligned(16))) bf16_t sKn[(C / 16) * KB * TILE];
-  __shared__ __attribute__((aligned(16))) bf16_t sQ[(K / 16) * (C / 32) * TILE];
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[HW ? 8 : (K / 16) * (C / 32) * TILE];
   __shared__ __attribute__((aligned(16))) bf16_t sWt[(K / 16) * (C / 32) * TILE];
   __shared__ __attribute__((aligned(16))) float sE[K];
+  __shared__ f32x4 sPA[HW ? 4 * 4 * 64 : 1];   // M^T dO: [state wave][row tile cb][lane]
+  __shared__ f32x4 sPB[HW ? 4 * ST * 64 : 1];  // Qg^T dO: [state wave][row tile ib][lane]
+  __shared__ uint4 sO[HW ? 4 * 2 * 2 * 64 : 1];  // dO B fragments: [column group][kb][hi, lo][lane]
   int bh, vs, g;
   bool real, phi;
   if (!group_task<V, K, true>(P, BH, bh, vs, g, real, phi)) return;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
-  const int col = vs * COLS + 16 * w + (lane & 15);  // >= V: a Phi column (its dO is zero)
   const int n0 = g * P.m, n1 = P.NG == 1 ? NT : min(NT, n0 + P.m);
 
-  float rM[UM][4], rQ[UN][4], rWt[UN][4], rE = 0.f;
   // dO as loaded (raw bf16 bits or fp32), widened only where the fragments are built, so the
   // loads of a chunk are all issued before any of them is waited for
   using RawO = std::conditional_t<DO_BF16, uint16_t, float>;
-  RawO rO[4][4];
   auto widen = [](RawO x) -> float {
     if constexpr (DO_BF16) return bf2f(x);
     else return x;
   };
-  float4 rKn[UN];
-  auto load_p1 = [&](int n) {  // M^T and Kf of chunk n
+  // dO rows 4 g4 + j (+ 16 cb) of column `col` of chunk n (rows past L and Phi columns read 0)
+  auto load_dO = [&](int n, int col, RawO (&rO)[4][4]) {
     const int t0 = n * C, L = min(C, T - t0);
-    const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][c'] row-major
-    const bufrsrc rk = make_buf(Kf + row_bht(bh, t0, T, K), L * K * 4);
-#pragma unroll
-    for (int u = 0; u < UM; ++u) {
-      const Unit x = unit<C>(tid + NTHR * u);  // row = c' (the d delta index), k = c
-#pragma unroll
-      for (int j = 0; j < 4; ++j) rM[u][j] = buf_ld(rm, ((x.k0 + j) * C + x.row) * 4);
-    }
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const Unit x = unit<K>(tid + NTHR * u);
-      rKn[u] = buf_ld4(rk, (x.row * K + x.k0) * 4);
-    }
-  };
-  auto load_p2 = [&](int n) {  // Qg^T, W^T, dO rows of this lane, e^{g_last} of chunk n
-    const int t0 = n * C, L = min(C, T - t0);
-    const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
-    const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);
-
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const Unit x = unit<C>(tid + NTHR * u);  // row = i, k = c
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t o = ((x.k0 + j) * K + x.row) * 4;
-        rQ[u][j] = buf_ld(rq, o);
-        rWt[u][j] = buf_ld(rw, o);
-      }
-    }
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       // dO rows 16 cb .. are H*V apart; the descriptor ends right after row L-1's head h
@@ -711,14 +693,182 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
         else rO[cb][j] = buf_ld(ro, e * 4);
       }
     }
+  };
+  // the B fragments (k = c) of those rows; a bf16 dO has ol = 0
+  auto dO_frags = [&](const RawO (&rO)[4][4], uint4 (&oh)[2], uint4 (&ol)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      bfrag(f32x4{widen(rO[2 * kb][0]), widen(rO[2 * kb][1]), widen(rO[2 * kb][2]), widen(rO[2 * kb][3])},
+            f32x4{widen(rO[2 * kb + 1][0]), widen(rO[2 * kb + 1][1]), widen(rO[2 * kb + 1][2]),
+                  widen(rO[2 * kb + 1][3])},
+            oh[kb], ol[kb]);
+  };
+
+  if constexpr (HW) {
+    if (tid >= NTHR) {
+      constexpr int RT = ST / 4;  // Qg^T row tiles per helper wave
+      const int hw = w - 4, r16 = lane & 15;
+      // A fragment slot s of lane group g4 in k-block kb: chunk row c = 32 kb + 4 g4 + s (s < 4) or
+      // 32 kb + 16 + 4 g4 + s - 4
+      auto crow = [&](int kb, int s) { return (uint32_t)(32 * kb + 16 * (s >> 2) + 4 * g4 + (s & 3)); };
+      float rq[RT][2][8], rm[2][8];
+      RawO rO[4][4];
+      auto load_Q = [&](int n) {  // Qg^T rows i = 16 (hw RT + t) + r16: Qg[c][i]
+        const int t0 = n * C, L = min(C, T - t0);
+        const bufrsrc r = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);  // rows past L read 0
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+              rq[t][kb][s] = buf_ld(r, (crow(kb, s) * K + (uint32_t)(16 * (hw * RT + t) + r16)) * 4);
+      };
+      auto load_M = [&](int n) {  // M^T rows c' = 16 hw + r16: M[c][c'] (k-block 0 is zero for hw >= 2)
+        const bufrsrc r = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int s = 0; s < 8; ++s)
+            rm[kb][s] = (kb == 0 && hw >= 2) ? 0.f : buf_ld(r, (crow(kb, s) * C + (uint32_t)(16 * hw + r16)) * 4);
+      };
+      const int ocol = vs * COLS + 16 * hw + r16;  // the column group whose dO this wave loads
+      auto publish_O = [&]() {
+        uint4 oh[2], ol[2];
+        dO_frags(rO, oh, ol);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          sO[((hw * 2 + kb) * 2) * 64 + lane] = oh[kb];
+          if constexpr (!DO_BF16) sO[((hw * 2 + kb) * 2 + 1) * 64 + lane] = ol[kb];
+        }
+      };
+      uint4 foh[4][2], fol[4][2];  // dO fragments of all four column groups
+      auto read_O = [&]() {
+#pragma unroll
+        for (int sw = 0; sw < 4; ++sw)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            foh[sw][kb] = sO[((sw * 2 + kb) * 2) * 64 + lane];
+            if constexpr (!DO_BF16) fol[sw][kb] = sO[((sw * 2 + kb) * 2 + 1) * 64 + lane];
+          }
+      };
+      auto prod = [&](const uint4& ah, const uint4& al, int sw, int kb, f32x4 acc) {
+        if constexpr (DO_BF16) return mma2(ah, al, foh[sw][kb], acc);
+        else return mma3(ah, al, foh[sw][kb], fol[sw][kb], acc);
+      };
+      auto product_A = [&]() {  // M^T dO (row tile hw) -> sPA
+        uint4 mh[2], ml[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) split8v(rm[kb], mh[kb], ml[kb]);
+#pragma unroll
+        for (int sw = 0; sw < 4; ++sw) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+            if (kb == 0 && hw >= 2) continue;  // M^T[c'][c] = 0 for c < c'
+            acc = prod(mh[kb], ml[kb], sw, kb, acc);
+          }
+          sPA[(sw * 4 + hw) * 64 + lane] = acc;
+        }
+      };
+      auto product_B = [&]() {  // Qg^T dO (row tiles hw RT ..) -> sPB
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          uint4 qh[2], ql[2];
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) split8v(rq[t][kb], qh[kb], ql[kb]);
+#pragma unroll
+          for (int sw = 0; sw < 4; ++sw) {
+            f32x4 acc = zero4();
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) acc = prod(qh[kb], ql[kb], sw, kb, acc);
+            sPB[(sw * ST + hw * RT + t) * 64 + lane] = acc;
+          }
+        }
+      };
+      const int nl = n1 - 1;
+      load_dO(nl, ocol, rO);
+      load_M(nl);
+      load_Q(nl);
+      publish_O();
+      __syncthreads();  // prologue 1: dO fragments of chunk nl
+      read_O();
+      product_A();
+      if (nl > n0) {
+        load_dO(nl - 1, ocol, rO);
+        load_M(nl - 1);
+      }
+      __syncthreads();  // prologue 2: M^T dO of chunk nl
+      for (int n = nl; n >= n0; --n) {
+        // phase 1: Qg^T dO of chunk n; dO fragments of chunk n - 1
+        product_B();
+        if (n > n0) {
+          load_Q(n - 1);
+          publish_O();
+        }
+        __syncthreads();
+        // phase 2: M^T dO of chunk n - 1
+        if (n > n0) {
+          read_O();
+          product_A();
+          if (n - 1 > n0) {
+            load_dO(n - 2, ocol, rO);
+            load_M(n - 2);
+          }
+        }
+        __syncthreads();
+      }
+      return;
+    }
+  }
+
+  const int col = vs * COLS + 16 * w + (lane & 15);  // >= V: a Phi column (its dO is zero)
+  float rM[HW ? 1 : UM][4], rQ[HW ? 1 : UN][4], rWt[UN][4], rE = 0.f;
+  RawO rO[4][4];
+  float4 rKn[UN];
+  auto load_p1 = [&](int n) {  // M^T and Kf of chunk n
+    const int t0 = n * C, L = min(C, T - t0);
+    if constexpr (!HW) {
+      const bufrsrc rm = make_buf(Mg + ((int64_t)bh * NT + n) * C * C, C * C * 4);  // M[c][c'] row-major
+#pragma unroll
+      for (int u = 0; u < UM; ++u) {
+        const Unit x = unit<C>(tid + NTHR * u);  // row = c' (the d delta index), k = c
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rM[u][j] = buf_ld(rm, ((x.k0 + j) * C + x.row) * 4);
+      }
+    }
+    const bufrsrc rk = make_buf(Kf + row_bht(bh, t0, T, K), L * K * 4);
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const Unit x = unit<K>(tid + NTHR * u);
+      rKn[u] = buf_ld4(rk, (x.row * K + x.k0) * 4);
+    }
+  };
+  auto load_p2 = [&](int n) {  // Qg^T, W^T, dO rows of this lane, e^{g_last} of chunk n
+    const int t0 = n * C, L = min(C, T - t0);
+    const bufrsrc rq = make_buf(Qg + row_bht(bh, t0, T, K), L * K * 4);
+    const bufrsrc rw = make_buf(W + row_bht(bh, t0, T, K), L * K * 4);
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const Unit x = unit<C>(tid + NTHR * u);  // row = i, k = c
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t o = ((x.k0 + j) * K + x.row) * 4;
+        if constexpr (!HW) rQ[u][j] = buf_ld(rq, o);
+        rWt[u][j] = buf_ld(rw, o);
+      }
+    }
+    if constexpr (!HW) load_dO(n, col, rO);
     {  // raw g_last of the chunk; the exponential is taken when staging, so no wait sits here
       const bufrsrc rg = make_buf(gc + row_bthk(b, t0 + L - 1, h, T, H, K), K * 4);  // lanes >= K read 0
       rE = buf_ld(rg, tid * 4);
     }
   };
   auto stage_p1 = [&]() {
+    if constexpr (!HW) {
 #pragma unroll
-    for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + NTHR * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
+      for (int u = 0; u < UM; ++u) put_unit(sM, unit<C>(tid + NTHR * u).off, rM[u][0], rM[u][1], rM[u][2], rM[u][3]);
+    }
 #pragma unroll
     for (int u = 0; u < UN; ++u)
       put_unit(sKn, unit<K>(tid + NTHR * u).off, rKn[u].x, rKn[u].y, rKn[u].z, rKn[u].w);
@@ -727,7 +877,7 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
       const int off = unit<C>(tid + NTHR * u).off;
-      put_unit(sQ, off, rQ[u][0], rQ[u][1], rQ[u][2], rQ[u][3]);
+      if constexpr (!HW) put_unit(sQ, off, rQ[u][0], rQ[u][1], rQ[u][2], rQ[u][3]);
       put_unit(sWt, off, rWt[u][0], rWt[u][1], rWt[u][2], rWt[u][3]);
     }
     if (tid < K) sE[tid] = exp2f(rE);
@@ -752,6 +902,7 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
   load_p1(n1 - 1);
   stage_p1();
   load_p2(n1 - 1);
+  if constexpr (HW) __syncthreads();  // the helpers' first barrier
   __syncthreads();
   for (int n = n1 - 1; n >= n0; --n) {
     const int t0 = n * C, L = min(C, T - t0);
@@ -761,14 +912,9 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
       for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, dS[ib]);
     }
 
-    // dO of this chunk as B fragments (k = c), kept for both phases; a bf16 dO has ol = 0
+    // dO of this chunk as B fragments (k = c), kept for both phases
     uint4 oh[2], ol[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      bfrag(f32x4{widen(rO[2 * kb][0]), widen(rO[2 * kb][1]), widen(rO[2 * kb][2]), widen(rO[2 * kb][3])},
-            f32x4{widen(rO[2 * kb + 1][0]), widen(rO[2 * kb + 1][1]), widen(rO[2 * kb + 1][2]),
-                  widen(rO[2 * kb + 1][3])},
-            oh[kb], ol[kb]);
+    if constexpr (!HW) dO_frags(rO, oh, ol);
 
     // ---- phase 1: d delta = M^T dO + Kf dS   (reads sM, sKn; fills sQ, sWt with chunk n)
     stage_p2();
@@ -778,29 +924,39 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
       uint4 bh_[KB], bl_[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) bfrag(dS[2 * kb], dS[2 * kb + 1], bh_[kb], bl_[kb]);
+      if constexpr (HW) {
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) dD[cb] = zero4();
-      // steps 0..5: M^T dO over the nonzero tiles (cb, kb): (0,0) (1,0) (0,1) (1,1) (2,1) (3,1)
-      // (M^T[c'][c] = M[c][c'] = 0 for c < c'); then Kf dS (kb = m / 4, cb = m % 4)
-      mfma_pipe<6 + 4 * KB, 2>(
-          [&](int st, uint4& ah, uint4& al) {
-            if (st < 6) {
-              const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
-              afrag(sM, cb * 2 + kb, lane, ah, al);
-            } else {
-              const int m = st - 6;
-              afrag(sKn, (m & 3) * KB + (m >> 2), lane, ah, al);
-            }
-          },
-          [&](int st, const uint4& ah, const uint4& al) {
-            if (st < 6) {
-              const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
-              dD[cb] = DO_BF16 ? mma2(ah, al, oh[kb], dD[cb]) : mma3(ah, al, oh[kb], ol[kb], dD[cb]);
-            } else {
-              const int m = st - 6, cb = m & 3, kb = m >> 2;
-              dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
-            }
-          });
+        for (int cb = 0; cb < 4; ++cb) dD[cb] = sPA[(w * 4 + cb) * 64 + lane];
+        // step m: Kf dS (kb = m / 4, cb = m % 4)
+        mfma_pipe<4 * KB, 2>([&](int st, uint4& ah, uint4& al) { afrag(sKn, (st & 3) * KB + (st >> 2), lane, ah, al); },
+                             [&](int st, const uint4& ah, const uint4& al) {
+                               dD[st & 3] = mma3(ah, al, bh_[st >> 2], bl_[st >> 2], dD[st & 3]);
+                             });
+      } else {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) dD[cb] = zero4();
+        // steps 0..5: M^T dO over the nonzero tiles (cb, kb): (0,0) (1,0) (0,1) (1,1) (2,1) (3,1)
+        // (M^T[c'][c] = M[c][c'] = 0 for c < c'); then Kf dS (kb = m / 4, cb = m % 4)
+        mfma_pipe<6 + 4 * KB, 2>(
+            [&](int st, uint4& ah, uint4& al) {
+              if (st < 6) {
+                const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
+                afrag(sM, cb * 2 + kb, lane, ah, al);
+              } else {
+                const int m = st - 6;
+                afrag(sKn, (m & 3) * KB + (m >> 2), lane, ah, al);
+              }
+            },
+            [&](int st, const uint4& ah, const uint4& al) {
+              if (st < 6) {
+                const int cb = st < 2 ? st : st - 2, kb = st < 2 ? 0 : 1;
+                dD[cb] = DO_BF16 ? mma2(ah, al, oh[kb], dD[cb]) : mma3(ah, al, oh[kb], ol[kb], dD[cb]);
+              } else {
+                const int m = st - 6, cb = m & 3, kb = m >> 2;
+                dD[cb] = mma3(ah, al, bh_[kb], bl_[kb], dD[cb]);
+              }
+            });
+      }
       if (real) {
         const float* dl = dDl + row_bht(bh, t0, T, V);
 #pragma unroll
@@ -823,17 +979,26 @@ __global__ __launch_bounds__(state_threads(V)) void state_bwd_kernel(const float
       for (int ib = 0; ib < ST; ++ib) {
         const float4 e = *reinterpret_cast<const float4*>(sE + 16 * ib + 4 * g4);
         dS[ib] = f32x4{e.x * dS[ib][0], e.y * dS[ib][1], e.z * dS[ib][2], e.w * dS[ib][3]};
+        if constexpr (HW) dS[ib] += sPB[(w * ST + ib) * 64 + lane];
       }
-      // step s: kb = s / (2 ST), ib = (s / 2) % ST, operand Qg^T (even s, B = dO) or W^T (odd s)
-      mfma_pipe<4 * ST, 2>(
-          [&](int st, uint4& ah, uint4& al) {
-            afrag((st & 1) ? sWt : sQ, ((st >> 1) % ST) * 2 + st / (2 * ST), lane, ah, al);
-          },
-          [&](int st, const uint4& ah, const uint4& al) {
-            const int kb = st / (2 * ST), ib = (st >> 1) % ST;
-            if (st & 1) dS[ib] = mma3(ah, al, dh_[kb], dl_[kb], dS[ib]);
-            else dS[ib] = DO_BF16 ? mma2(ah, al, oh[kb], dS[ib]) : mma3(ah, al, oh[kb], ol[kb], dS[ib]);
-          });
+      if constexpr (HW) {
+        // step s: dS[ib] -= W^T d delta (kb = s / ST, ib = s % ST)
+        mfma_pipe<2 * ST, 2>([&](int st, uint4& ah, uint4& al) { afrag(sWt, (st % ST) * 2 + st / ST, lane, ah, al); },
+                             [&](int st, const uint4& ah, const uint4& al) {
+                               dS[st % ST] = mma3(ah, al, dh_[st / ST], dl_[st / ST], dS[st % ST]);
+                             });
+      } else {
+        // step s: kb = s / (2 ST), ib = (s / 2) % ST, operand Qg^T (even s, B = dO) or W^T (odd s)
+        mfma_pipe<4 * ST, 2>(
+            [&](int st, uint4& ah, uint4& al) {
+              afrag((st & 1) ? sWt : sQ, ((st >> 1) % ST) * 2 + st / (2 * ST), lane, ah, al);
+            },
+            [&](int st, const uint4& ah, const uint4& al) {
+              const int kb = st / (2 * ST), ib = (st >> 1) % ST;
+              if (st & 1) dS[ib] = mma3(ah, al, dh_[kb], dl_[kb], dS[ib]);
+              else dS[ib] = DO_BF16 ? mma2(ah, al, oh[kb], dS[ib]) : mma3(ah, al, oh[kb], ol[kb], dS[ib]);
+            });
+      }
     }
     __syncthreads();
   }
