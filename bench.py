@@ -42,7 +42,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
 # MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
 MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_fwd": "bf16x3", "mem_readout_fwd": "bf16x3",
              "mem_state_readout_fwd": "bf16x3",
-             "mem_state_bwd": "bf16x3", "mem_bwd_hgrad": "bf16x3", "mem_bwd_solve_contrib": "bf16x3"}
+             "mem_state_bwd": "bf16x3", "mem_bwd_chunk": "bf16x3"}
 
 
 def mfma_peak(tag: str) -> float:
@@ -73,12 +73,12 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
                                   2 * 2 * K * V + 2 * (K * V + C * V / 2)),
         # M, Kf, Qg, W, dO -> dh, d delta
         "mem_state_bwd": (mm + 12 * K + do_b + h_b + 4 * V, 2 * (C * V / 2 + 3 * K * V)),
-        # h, dh, delta, d delta, dO -> dQg, dW, dKf, dM
-        "mem_bwd_hgrad": (2 * h_b + 8 * V + do_b + 12 * K + mm, 2 * (3 * K * V + C * V / 2)),
-        # A^T, d delta, dW, U, W, q, k, kappa, g, dM, dQg, dKf -> dv, dq, dk, dkappa, dg (dKg, dN stay on chip)
-        "mem_bwd_solve_contrib": (mm + 4 * V + 4 * K + 4 * V + 4 * K + 4 * K + kap_in + 4 * K + mm + 8 * K
-                                  + 2 * V + 4 * K + dkap_out + 4 * K,
-                                  2 * (C * (V + K) / 2 + C * (V + K) / 2) + 2 * 2 * (C * K)),
+        # h, dh, delta, d delta, dO, A^T, U, W, q, k, kappa, g -> dv, dq, dk, dkappa, dg (dQg, dW, dKf, dM,
+        # dKg and dN stay on chip); FLOPs: the state-gradient products, the solves and dN, the gradient
+        # contractions
+        "mem_bwd_chunk": (2 * h_b + 8 * V + do_b + mm + 4 * V + 4 * K + 2 * 2 * K + kap_in + 4 * K
+                          + 2 * V + 2 * 2 * K + dkap_out + 4 * K,
+                          2 * (3 * K * V + C * V / 2) + 2 * (C * (V + K) / 2 + C * (V + K) / 2) + 2 * 2 * (C * K)),
     }
     return {k: (b * N, f * N) for k, (b, f) in per.items()}
 

@@ -1016,4 +1016,577 @@ __global__ __launch_bounds__(256, 2) void solve_contrib_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The whole chunk-parallel backward of one chunk in one kernel: the state-gradient products of
+// hgrad_kernel, the transposed solves and the gradients of solve_contrib_kernel.  dQg, dW, dKf, dM
+// and the g_last dots never go to HBM: each is produced in the register layout its consumer takes.
+// grid (NT, B*H), block 512 (8 waves), one workgroup per CU (LDS ~99 KB).
+//  * Staging.  The chunk rows of dO, delta and d delta are split into LDS fragments (rows c,
+//    k = v, natural order), all 64 rows at once.
+//  * Wave w owns channel tile it = w (16 channels of K) and V tile w (16 columns of V).  It loads
+//    its 16 rows of h and of dh straight into split fragments (one layout serves as the A operand
+//    h (rows i, k = v) and as the B operand h^T (k = v, cols i)) and forms
+//      dQg^T = h dO^T,  dKf^T = dh delta^T    (D tile: lane -> chunk row, 4 consecutive channels:
+//                                              the layout of the gradient phase's elementwise terms)
+//      -dW   = d delta h^T                    (D tile: lane -> channel, 4 chunk rows: two stacked
+//                                              tiles are the solve's A operand in permuted k order)
+//      dgl_i = 2^{G_last,i} sum_v h_iv dh_iv,  and dM = lower(dO delta^T) for lower tiles w, w + 8.
+//  * Solve.  Per wave one 32-column block: its V tile of d delta (dv stored) and its K tile of dW
+//    (dKg kept in registers), with A^T read in the same permuted k order; the block's dN^T share
+//    over the 8 waves is summed through LDS in two steps (waves 4..7 into 0..3, then the four).
+//  * Gradients: as in solve_contrib_kernel, one channel tile per wave.
+// Chunks flagged by the forward store the products (dQg, dW, dKf, dM, dgl) for the exact kernels
+// and stop after them.
+// ---------------------------------------------------------------------------------------------
+template <int K, int V, bool ISO, typename TDO>
+__global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
+    const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
+    const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
+    const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, int T, int H, int NT, float scale, bf16_t* __restrict__ dv,
+    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
+    float* __restrict__ dg, float* __restrict__ xQg, float* __restrict__ xW, float* __restrict__ xKf,
+    float* __restrict__ xM, float* __restrict__ xgl) {
+  constexpr bool DO_BF16 = sizeof(TDO) == 2;
+  constexpr int NW = 8;
+  constexpr int VB = V / 32;        // k-blocks of the V contraction
+  constexpr int NIT = K / 16;       // channel tiles (waves 0 .. NIT-1 own one each)
+  constexpr int NVT = V / 16;       // V tiles (waves 0 .. NVT-1)
+  constexpr int RB = VB * TILE;     // one 16-row block of a [rows][V] operand as fragments
+  constexpr int FR = 8 * TILE;      // one 64 x 64 operand as (4 row tiles x 2 k-blocks) fragments
+  constexpr int AP4 = C + 4;        // LDS row stride of A^T (and of dM while it is passed on)
+  constexpr int STAGE_BYTES = 3 * 4 * RB * 2;
+  constexpr int SOLVE_BYTES = (C * AP4 + 4 * 10 * 256) * 4;
+  constexpr int CONTRIB_BYTES = 4 * FR * 2;
+  constexpr int LDS_A = STAGE_BYTES > SOLVE_BYTES ? STAGE_BYTES : SOLVE_BYTES;
+  constexpr int LDS_BYTES = LDS_A > CONTRIB_BYTES ? LDS_A : CONTRIB_BYTES;
+  constexpr int SU = C * V / 8 / 512;  // staging units (8 consecutive v of one row) per thread per operand
+  static_assert(SU >= 1 && (C * V / 8) % 512 == 0, "staging units per thread");
+  static_assert(NIT <= NW && NVT <= NW, "K, V <= 128");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+  __shared__ float sDgl[K];
+  __shared__ float sBeta[NW * C];
+  bf16_t* sO = reinterpret_cast<bf16_t*>(smem);  // phase 1: dO, delta, d delta row fragments
+  bf16_t* sD = sO + 4 * RB;
+  bf16_t* sdD = sD + 4 * RB;
+  float* sAt = reinterpret_cast<float*>(smem);   // solve: A^T [C][AP4]; then dM [C][AP4]
+  float* sP = sAt + C * AP4;                      // per-wave partial dN^T tiles (4 slots)
+  bf16_t* sF = reinterpret_cast<bf16_t*>(smem);  // gradients: dN, dM, dN^T, dM^T fragments
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int t0 = n * C, L = min(C, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+  const int64_t chunk = (int64_t)bh * NT + n;
+  const bool flagged = flags[chunk] != 0;
+  const bool own_k = w < NIT, own_v = w < NVT;
+  const int it = w;  // this wave's channel tile (when own_k)
+  const int i0 = 16 * it + 4 * g4;
+
+  // ================================ loads ================================
+  const bufrsrc rD = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);  // rows past L read 0
+  const bufrsrc rdD = make_buf(dDl + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const bufrsrc rO = make_buf(dO + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * sizeof(TDO));
+  float4 sr_D[SU][2], sr_dD[SU][2];
+  u32x4 sr_O[SU][DO_BF16 ? 1 : 2];
+#pragma unroll
+  for (int u = 0; u < SU; ++u) {  // unit e: 16-row block, k-block, fragment lane
+    const int e = tid + 512 * u, blk = e / (VB * 64), kb = (e / 64) % VB, sl = e & 63;
+    const uint32_t c = (uint32_t)(16 * blk + (sl & 15)), v0 = (uint32_t)(32 * kb + 8 * (sl >> 4));
+    sr_D[u][0] = buf_ld4(rD, (c * V + v0) * 4);
+    sr_D[u][1] = buf_ld4(rD, (c * V + v0) * 4 + 16);
+    sr_dD[u][0] = buf_ld4(rdD, (c * V + v0) * 4);
+    sr_dD[u][1] = buf_ld4(rdD, (c * V + v0) * 4 + 16);
+    if constexpr (DO_BF16) {
+      sr_O[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + v0) * 2, 0, 0);
+    } else {
+      sr_O[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + v0) * 4, 0, 0);
+      sr_O[u][1] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + v0) * 4 + 16, 0, 0);
+    }
+  }
+  // this wave's rows of h and dh (row i = 16 it + r16, v = 32 kb + 8 g4 .. + 7) and the g_last factor
+  const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
+  const bufrsrc rdh = make_buf(dhbuf + chunk * K * V, K * V * 4);
+  float hv[VB][8], dhv[VB][8];
+  float gl_i = 0.f;
+  if (own_k) {
+    const int i = 16 * it + r16;
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) {
+      const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
+      kdn_intra::ld8(rh, e * 4, hv[kb]);
+      kdn_intra::ld8(rdh, e * 4, dhv[kb]);
+    }
+    gl_i = buf_ld(make_buf(gc + (((int64_t)b * T + t0 + L - 1) * H + h) * K, K * 4), i * 4);
+  }
+  // A^T of the chunk (staged for the solve once the phase-1 fragments are dead)
+  constexpr int AU = C * C / 4 / 512;
+  float4 at_r[AU];
+  if (!flagged) {
+    const bufrsrc rA = make_buf(At + chunk * C * C, C * C * 4);
+#pragma unroll
+    for (int u = 0; u < AU; ++u) at_r[u] = buf_ld4(rA, (tid + 512 * u) * 16);
+  }
+
+  // ---- phase-1 fragments into LDS
+#pragma unroll
+  for (int u = 0; u < SU; ++u) {
+    const int e = tid + 512 * u, blk = e / (VB * 64), kb = (e / 64) % VB, sl = e & 63;
+    const int off = blk * RB + kb * TILE + sl * 8;
+    auto put8 = [&](bf16_t* dst, const float4& x0, const float4& x1) {
+      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      uint4 hi, lo;
+      split8(x, hi, lo);
+      *reinterpret_cast<uint4*>(dst + off) = hi;
+      *reinterpret_cast<uint4*>(dst + off + 512) = lo;
+    };
+    put8(sD, sr_D[u][0], sr_D[u][1]);
+    put8(sdD, sr_dD[u][0], sr_dD[u][1]);
+    if constexpr (DO_BF16)
+      *reinterpret_cast<uint4*>(sO + off) = uint4{sr_O[u][0].x, sr_O[u][0].y, sr_O[u][0].z, sr_O[u][0].w};
+    else
+      put8(sO, __builtin_bit_cast(float4, sr_O[u][0]), __builtin_bit_cast(float4, sr_O[u][1]));
+  }
+  __syncthreads();
+
+  // ================================ phase 1: products with h, dh ================================
+  f32x4 aQ[4], aW[4], aK[4];  // dQg^T (rows i, cols c), d delta h^T (rows c, cols i), dKf^T
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl) aQ[tl] = aW[tl] = aK[tl] = zero4();
+  if (own_k) {
+    uint4 fh[VB], fl[VB];
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) split8(hv[kb], fh[kb], fl[kb]);
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb)
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) {
+        if constexpr (DO_BF16) {
+          const uint4 ob = *reinterpret_cast<const uint4*>(sO + tl * RB + kb * TILE + lane * 8);
+          aQ[tl] = kdn_state::mma2(fh[kb], fl[kb], ob, aQ[tl]);
+        } else {
+          uint4 oh, ol;
+          afrag(sO + tl * RB, kb, lane, oh, ol);
+          aQ[tl] = mma3(fh[kb], fl[kb], oh, ol, aQ[tl]);
+        }
+        uint4 xh, xl;
+        afrag(sdD + tl * RB, kb, lane, xh, xl);
+        aW[tl] = mma3(xh, xl, fh[kb], fl[kb], aW[tl]);
+      }
+    float dot = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dot += hv[kb][j] * dhv[kb][j];
+      split8(dhv[kb], fh[kb], fl[kb]);
+    }
+    dot += __shfl_xor(dot, 16, 64);
+    dot += __shfl_xor(dot, 32, 64);
+    if (g4 == 0) sDgl[16 * it + r16] = dot * exp2f(gl_i);
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb)
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) {
+        uint4 xh, xl;
+        afrag(sD + tl * RB, kb, lane, xh, xl);
+        aK[tl] = mma3(fh[kb], fl[kb], xh, xl, aK[tl]);
+      }
+  }
+  // dM tiles (c-block I, s-block J) = lower(dO delta^T) for lower tiles w and w + 8: lane -> column
+  // s = 16 J + r16, rows c = 16 I + 4 g4 + j
+  f32x4 mt[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    mt[x] = zero4();
+    const int t = w + NW * x;
+    if (t >= 10) continue;
+    int I, J;
+    lower_tile(t, I, J);
+#pragma unroll
+    for (int kb = 0; kb < VB; ++kb) {
+      uint4 xh, xl;
+      afrag(sD + J * RB, kb, lane, xh, xl);
+      if constexpr (DO_BF16) {
+        const uint4 ob = *reinterpret_cast<const uint4*>(sO + I * RB + kb * TILE + lane * 8);
+        mt[x] = mma2b(ob, xh, xl, mt[x]);
+      } else {
+        uint4 oh, ol;
+        afrag(sO + I * RB, kb, lane, oh, ol);
+        mt[x] = mma3(oh, ol, xh, xl, mt[x]);
+      }
+    }
+    if (I == J) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (r16 > 4 * g4 + j) mt[x][j] = 0.f;
+    }
+  }
+
+  if (flagged) {  // the exact kernels take it from here: store the products in their layouts
+    __syncthreads();  // sDgl
+    if (own_k) {
+      const bufrsrc rQ = make_buf(xQg + ((int64_t)bh * T + t0) * K, L * K * 4);
+      const bufrsrc rW = make_buf(xW + ((int64_t)bh * T + t0) * K, L * K * 4);
+      const bufrsrc rKf = make_buf(xKf + ((int64_t)bh * T + t0) * K, L * K * 4);
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) {
+        const uint32_t c = (uint32_t)(16 * tl + r16);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, aQ[tl]), rQ, (c * K + i0) * 4, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, aK[tl]), rKf, (c * K + i0) * 4, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          buf_st(rW, ((uint32_t)(16 * tl + 4 * g4 + j) * K + 16 * it + r16) * 4, -aW[tl][j]);
+      }
+      if (g4 == 0) xgl[chunk * K + 16 * it + r16] = sDgl[16 * it + r16];
+    }
+    float* Mn = xM + chunk * C * C;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int t = w + NW * x;
+      if (t >= 10) continue;
+      int I, J;
+      lower_tile(t, I, J);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Mn[(16 * I + 4 * g4 + j) * C + 16 * J + r16] = mt[x][j];
+    }
+    if (w < 6) {  // upper tiles are zero
+      int I, J;
+      upper_tile(w, I, J);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Mn[(16 * I + 4 * g4 + j) * C + 16 * J + r16] = 0.f;
+    }
+    return;
+  }
+  __syncthreads();  // phase-1 fragments dead: A^T may overwrite them
+#pragma unroll
+  for (int u = 0; u < AU; ++u) {
+    const int e4 = tid + 512 * u, sr = e4 / (C / 4), c4 = e4 % (C / 4);
+    *reinterpret_cast<float4*>(sAt + sr * AP4 + 4 * c4) = at_r[u];
+  }
+  __syncthreads();
+
+  // ================================ solve ================================
+  // Yt[0] = d delta^T A (V tile w), Yt[1] = dW^T A (K tile w); k = chunk row c in permuted order:
+  // slot j of lane group g4 <-> c = 32 kb + 4 g4 + j (j < 4) or 32 kb + 16 + 4 g4 + (j - 4)
+  const bufrsrc rdv = make_buf(dv + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * 2);
+  f32x4 Yt[2][4];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int J = 0; J < 4; ++J) Yt[ct][J] = zero4();
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    uint4 xh0, xl0, xh1, xl1;
+    {
+      float xv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = 32 * kb + (j < 4 ? 4 * g4 + j : 16 + 4 * g4 + j - 4);
+        xv[j] = own_v ? buf_ld(rdD, ((uint32_t)c * V + 16 * w + r16) * 4) : 0.f;
+      }
+      split8(xv, xh0, xl0);
+    }
+    {
+      const f32x4 t0_ = -aW[2 * kb], t1_ = -aW[2 * kb + 1];  // zero for waves without a channel tile
+      kdn_state::bfrag(t0_, t1_, xh1, xl1);
+    }
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      if (J > 2 * kb + 1) continue;  // A[c][s] = 0 for c < s
+      const float* row = sAt + (16 * J + r16) * AP4 + 32 * kb + 4 * g4;
+      const float4 a0 = *reinterpret_cast<const float4*>(row), a1 = *reinterpret_cast<const float4*>(row + 16);
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      uint4 ah, al;
+      split8(av, ah, al);
+      Yt[0][J] = mma3(xh0, xl0, ah, al, Yt[0][J]);
+      Yt[1][J] = mma3(xh1, xl1, ah, al, Yt[1][J]);
+    }
+  }
+  if (own_v) {  // dv rows s = 16 J + r16, columns 16 w + 4 g4 .. + 3
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      const uint32_t tr = (uint32_t)(16 * J + r16), x0 = (uint32_t)(16 * w + 4 * g4);
+      const f32x4 y = Yt[0][J];
+      const uint32_t lo = (uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16);
+      const uint32_t hi = (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16);
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rdv, ((tr * H) * V + x0) * 2, 0, 0);
+    }
+  }
+  // this block's share of dN^T[s][c] = sum_x (U|W)[s][x] Y[x][c]
+  f32x4 part[10];
+  {
+    const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
+    const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
+    uint4 uh[4], ul[4], yh[4], yl[4];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      const uint32_t sr = (uint32_t)(16 * J + r16);
+      const float4 a0 = own_v ? buf_ld4(rU, (sr * V + 16 * w + 4 * g4) * 4) : float4{0.f, 0.f, 0.f, 0.f};
+      const float4 a1 = own_k ? buf_ld4(rW, (sr * K + i0) * 4) : float4{0.f, 0.f, 0.f, 0.f};
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      split8(av, uh[J], ul[J]);
+      kdn_state::bfrag(Yt[0][J], Yt[1][J], yh[J], yl[J]);
+    }
+#pragma unroll
+    for (int t = 0; t < 10; ++t) {
+      int I, J;
+      lower_tile(t, I, J);
+      part[t] = mma3(uh[J], ul[J], yh[I], yl[I], zero4());
+    }
+  }
+  f32x4 kg[4];  // dKg^T tiles: lane -> chunk row 16 J + r16, channels i0 .. i0 + 3
+#pragma unroll
+  for (int J = 0; J < 4; ++J) kg[J] = Yt[1][J];
+  __syncthreads();  // every A^T read done: sAt now carries dM, sP the partials
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {  // dM rows c, columns s (lower tiles computed, upper zero)
+    const int t = w + NW * x;
+    if (t >= 16) continue;
+    int I, J;
+    f32x4 v = zero4();
+    if (t < 10) {
+      lower_tile(t, I, J);
+      v = mt[x];
+    } else {
+      upper_tile(t - 10, I, J);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sAt[(16 * I + 4 * g4 + j) * AP4 + 16 * J + r16] = v[j];
+  }
+  if (w >= 4) {
+#pragma unroll
+    for (int t = 0; t < 10; ++t) *reinterpret_cast<f32x4*>(sP + (((w - 4) * 10 + t) * 64 + lane) * 4) = part[t];
+  }
+  __syncthreads();
+  if (w < 4) {
+#pragma unroll
+    for (int t = 0; t < 10; ++t) {
+      f32x4* slot = reinterpret_cast<f32x4*>(sP + ((w * 10 + t) * 64 + lane) * 4);
+      *slot = *slot + part[t];
+    }
+  }
+  __syncthreads();
+
+  // ======================= dN, dM staging (the gradient phase's fragments) =======================
+  float4 dNu[2], dMu[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {  // unit (row c, kb, hh, gg) -> 4 consecutive s of one lane's slots
+    const int e = tid + 512 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
+    const int k0 = 32 * kb + 16 * hh + 4 * gg;
+    dMu[u] = *reinterpret_cast<const float4*>(sAt + row * AP4 + k0);
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    if ((k0 >> 4) <= (row >> 4)) {
+      const int t = lower_tile_index(row >> 4, k0 >> 4), ln = (row & 15) + 16 * ((k0 & 15) >> 2);
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float4 v = *reinterpret_cast<const float4*>(sP + ((ww * 10 + t) * 64 + ln) * 4);
+        acc.x -= v.x, acc.y -= v.y, acc.z -= v.z, acc.w -= v.w;
+      }
+      if (k0 + 0 >= row) acc.x = 0.f;
+      if (k0 + 1 >= row) acc.y = 0.f;
+      if (k0 + 2 >= row) acc.z = 0.f;
+      if (k0 + 3 >= row) acc.w = 0.f;
+    }
+    dNu[u] = acc;
+  }
+  __syncthreads();  // every partial and dM read before the fragments overwrite them
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = tid + 512 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
+    const int k0 = 32 * kb + 16 * hh + 4 * gg;
+    const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
+    const float4 a = dNu[u], bq = dMu[u];
+    kdn_state::put_unit(sF, off, a.x, a.y, a.z, a.w);
+    kdn_state::put_unit(sF + FR, off, bq.x, bq.y, bq.z, bq.w);
+    const int rk = row & 31, tg = (rk & 15) >> 2, ts = (rk & 3) + 4 * (rk >> 4);
+    const float xv[4] = {a.x, a.y, a.z, a.w}, yv[4] = {bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sr = k0 + j;
+      const int toff = ((sr >> 4) * 2 + (row >> 5)) * TILE + ((sr & 15) + 16 * tg) * 8 + ts;
+      const bf16_t xhi = f2bf(xv[j]), yhi = f2bf(yv[j]);
+      sF[2 * FR + toff] = xhi;
+      sF[2 * FR + toff + 512] = f2bf(xv[j] - bf2f(xhi));
+      sF[3 * FR + toff] = yhi;
+      sF[3 * FR + toff + 512] = f2bf(yv[j] - bf2f(yhi));
+    }
+  }
+  __syncthreads();
+
+  // ================================ gradient phase ================================
+  float bpart[4] = {0.f, 0.f, 0.f, 0.f};  // iso: dbeta partials of rows 16 tl + r16
+  if (own_k) {
+    const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+    const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
+    const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
+    const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
+    const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
+    const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
+    const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
+    const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
+    const bufrsrc rdkap = ISO ? make_buf(dkap, 0) : make_buf(dkap + in_row0 * K, rows_in * K * 4);
+    const bufrsrc rdg = make_buf(dg + in_row0 * K, rows_in * K * 4);
+    const int i = 16 * it + r16;
+    // ---- factor loads, one channel per lane: rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j; the gate
+    // of rows past L repeats row L-1 (their k, q, kappa read zero)
+    float av[16], Gv[16];
+    uint16_t kraw[16], qraw[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const int c = 16 * (p >> 2) + 4 * g4 + (p & 3);
+      const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
+      kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
+      qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
+      av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);
+      Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float mA[4];  // block anchors m_J = (G_{16J} + G_{16J+15}) / 2 of this lane's channel
+#pragma unroll
+    for (int J = 0; J < 4; ++J) mA[J] = 0.5f * (__shfl(Gv[4 * J], r16, 64) + __shfl(Gv[4 * J + 3], 48 + r16, 64));
+    float Rown[16], Kown[16], Qown[16];
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const float kvp = bf2f(kraw[p]), e = exp2f(Gv[p] - mA[p >> 2]);
+      Kown[p] = kvp * e;
+      Qown[p] = scale * bf2f(qraw[p]) * e;
+      Rown[p] = (ISO ? av[p] * kvp : av[p]) * __frcp_rn(e);
+    }
+    const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
+    u32x2 kq4[4], qq4[4];
+    float4 kap4[4], G4[4];
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
+      kq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rk, o * 2, 0, 0);
+      qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
+      if (ISO) {
+        const float be = buf_ld(rkap, c * H * 4);
+        kap4[tl] = float4{be, be, be, be};
+      } else {
+        kap4[tl] = buf_ld4(rkap, o * 4);
+      }
+      G4[tl] = buf_ld4(rG, ((uint32_t)(min(16 * tl + r16, L - 1) * H) * K + i0) * 4);
+    }
+    float colpart[4] = {0.f, 0.f, 0.f, 0.f};
+    float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
+    bool has_last = false;
+    const float gla[4] = {glv.x, glv.y, glv.z, glv.w};
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      f32x4 dLk = zero4(), dLq = zero4(), dR = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        uint4 ah, al;
+        if (kb <= tl / 2) {
+          const float s0 = 2 * kb <= tl ? exp2f(mA[tl] - mA[2 * kb]) : 0.f;
+          const float s1 = 2 * kb + 1 <= tl ? exp2f(mA[tl] - mA[2 * kb + 1]) : 0.f;
+          float rv[8];
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) rv[sl] = Rown[8 * kb + sl] * (sl < 4 ? s0 : s1);
+          uint4 Rh, Rl;
+          split8(rv, Rh, Rl);
+          afrag(sF, tl * 2 + kb, lane, ah, al);
+          dLk = mma3(Rh, Rl, ah, al, dLk);
+          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
+          dLq = mma3(Rh, Rl, ah, al, dLq);
+        }
+        if (2 * kb + 1 >= tl) {
+          const float s0 = 2 * kb >= tl ? exp2f(mA[2 * kb] - mA[tl]) : 0.f;
+          const float s1 = 2 * kb + 1 >= tl ? exp2f(mA[2 * kb + 1] - mA[tl]) : 0.f;
+          float lk[8], lq[8];
+#pragma unroll
+          for (int sl = 0; sl < 8; ++sl) {
+            const float sc = sl < 4 ? s0 : s1;
+            lk[sl] = Kown[8 * kb + sl] * sc;
+            lq[sl] = Qown[8 * kb + sl] * sc;
+          }
+          uint4 Kh, Kl, Qh, Ql;
+          split8(lk, Kh, Kl);
+          split8(lq, Qh, Ql);
+          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
+          dR = mma3(Kh, Kl, ah, al, dR);
+          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
+          dR = mma3(Qh, Ql, ah, al, dR);
+        }
+      }
+      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
+      const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
+                            __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
+      const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
+                            __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
+      const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
+      const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
+      const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
+                           __shfl(mA[tl], 4 * g4 + 3, 64)};
+      float dkv[4], dqv[4], dav[4], dgv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float beta = ISO ? a4[j] : 0.f;
+        const float kap_p = ISO ? beta * kv4[j] : a4[j];
+        const float e = exp2f(gv[j] - mz[j]), er = __frcp_rn(e);
+        const float eg = exp2f(gv[j]), f = exp2f(gla[j] - gv[j]);
+        const float a_lk = dLk[j], a_lq = dLq[j] * scale, a_r = dR[j];
+        const float dkgv = kg[tl][j], dqgv = aQ[tl][j], dkfv = aK[tl][j];
+        dkv[j] = a_lk * e + dkgv * eg;
+        dqv[j] = a_lq * e + scale * dqgv * eg;
+        dav[j] = a_r * er + dkfv * f;
+        dgv[j] = kv4[j] * e * a_lk + qv4[j] * e * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv +
+                 scale * qv4[j] * eg * dqgv - kap_p * f * dkfv;
+        if ((int)c < L) colpart[j] += kap_p * f * dkfv;
+        if (ISO) {
+          dkv[j] += beta * dav[j];
+          bpart[tl] += dav[j] * kv4[j];
+        }
+      }
+      if (!ISO)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(dav[0]), __float_as_uint(dav[1]), __float_as_uint(dav[2]), __float_as_uint(dav[3])},
+            rdkap, o * 4, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16), (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
+          rdq, o * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(
+          u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16), (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
+          rdk, o * 2, 0, 0);
+      if ((int)c == L - 1) {
+        dg_last = float4{dgv[0], dgv[1], dgv[2], dgv[3]};
+        has_last = true;
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(dgv[0]), __float_as_uint(dgv[1]), __float_as_uint(dgv[2]), __float_as_uint(dgv[3])},
+            rdg, o * 4, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) colpart[j] += __shfl_xor(colpart[j], m, 64);
+    if (has_last) {
+      const float4 gl4 = *reinterpret_cast<const float4*>(sDgl + i0);
+      const float4 v = float4{dg_last.x + colpart[0] + gl4.x, dg_last.y + colpart[1] + gl4.y,
+                              dg_last.z + colpart[2] + gl4.z, dg_last.w + colpart[3] + gl4.w};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rdg,
+                                             ((uint32_t)((L - 1) * H) * K + i0) * 4, 0, 0);
+    }
+  }
+  if (ISO) {
+    if (own_k) {
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) {
+        float v = bpart[tl];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (g4 == 0) sBeta[w * C + 16 * tl + r16] = v;
+      }
+    }
+    __syncthreads();
+    if (tid < L) {
+      float s = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NIT; ++ww) s += sBeta[ww * C + tid];
+      dbeta[((int64_t)b * T + t0 + tid) * H + h] = s;
+    }
+  }
+}
+
 }  // namespace kdn_bwd

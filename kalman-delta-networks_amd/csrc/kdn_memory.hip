@@ -932,9 +932,15 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
                                         });
     if (rc) return rc;
   }
-  if (stages & 2) {
-    hipLaunchKernelGGL((kdn_bwd::hgrad_kernel<K, V, TDO>), gchunk, dim3(256), 0, stream, hb, dh, D, dD, dO, gc, T, H,
-                       NT, dQg, dW, dKf, dM, dgl);
+  if (stages & 2) {  // every chunk's products with h / dh; the solves and gradients of the unflagged ones
+    if (iso)
+      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, true, TDO>), gchunk, dim3(512), 0, stream, hb, dh, D, dD, dO,
+                         A, U, W, flags, q, k, kap, gc, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf,
+                         dM, dgl);
+    else
+      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, false, TDO>), gchunk, dim3(512), 0, stream, hb, dh, D, dD,
+                         dO, A, U, W, flags, q, k, kap, gc, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf,
+                         dM, dgl);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 4) {  // the chunks left to the exact path: transposed solves into dv, dKg, dN
@@ -947,19 +953,14 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
                          dW, U, W, T, H, NT, NB, flags, dv, dKg, dN);
     KDN_CHECK_LAUNCH();
   }
-  if (stages & 8) {
+  if (stages & 8) {  // the exact path's gradients
     const int NB = B * H * NT, gx = min(NB, 512);
-    if (iso) {  // solves and gradients of every other chunk in one kernel; then the exact path's gradients
-      hipLaunchKernelGGL((kdn_bwd::solve_contrib_kernel<K, V, true>), gchunk, dim3(256), 0, stream, A, dD, dW, U, W,
-                         flags, q, k, kap, gc, dM, dQg, dKf, dgl, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg);
+    if (iso)
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc, dN,
                          dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
-    } else {
-      hipLaunchKernelGGL((kdn_bwd::solve_contrib_kernel<K, V, false>), gchunk, dim3(256), 0, stream, A, dD, dW, U, W,
-                         flags, q, k, kap, gc, dM, dQg, dKf, dgl, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg);
+    else
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc,
                          dN, dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
-    }
     KDN_CHECK_LAUNCH();
   }
   return 0;

@@ -17,9 +17,9 @@ FWD_STAGES_FUSED = ((1, "mem_intra_fwd"), (6, "mem_state_readout_fwd"))
 def state_groups(B: int, T: int, H: int, K: int, V: int) -> int:
     """Chunk groups of the serial state passes at this shape (1: one pass, readout fused)."""
     return int(_lib.load().kdn_mem_state_groups(B, T, H, K, V))
-# bit 4: the transposed solves of the chunks left to the exact path; bit 8: solves + gradients of
-# every other chunk in one kernel, then the exact path's gradients
-BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_hgrad"), (4, "mem_bwd_exact_solve"), (8, "mem_bwd_solve_contrib"))
+# bit 2: the chunk-parallel backward of every chunk (products with h and dh; solves and gradients of
+# the chunks the forward factored); bits 4 | 8: the exact path's solves and gradients (flagged chunks)
+BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_chunk"), (12, "mem_bwd_exact"))
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
