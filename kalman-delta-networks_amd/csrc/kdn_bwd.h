@@ -1,11 +1,21 @@
-// Chunk-parallel backward kernels of the KDN memory scan on bf16x3 MFMA.
+// Chunk-parallel backward of the KDN memory scan on bf16x3 MFMA (one kernel per chunk).
 //
-// State-gradient products (per chunk, h = state entering the chunk, dh = gradient of the
-// state leaving it, delta / d delta = the chunk's delta and its gradient):
-//   dQg = dO h^T,  dW = -d delta h^T,  dKf = delta dh^T,  dM = lower(dO delta^T),
-//   dgl_i = 2^{G_last,i} sum_v h_iv dh_iv
-// Every product contracts over V, the contiguous index of all five operands, so MFMA fragments
-// are 8 consecutive v of one row.
+// Per chunk of C = 64 tokens (h = state entering the chunk, dh = gradient of the state leaving
+// it, delta / d delta = the chunk's delta and its gradient, A = (I + N)^{-1} saved by the forward):
+//   state-gradient products  dQg = dO h^T,  dW = -d delta h^T,  dKf = delta dh^T,
+//                            dM = lower(dO delta^T),  dgl_i = 2^{G_last,i} sum_v h_iv dh_iv
+//   transposed solves        dV = A^T d delta,  dKg = A^T dW,  dN = -strict_lower(dV U^T + dKg W^T)
+//   gradients                with block anchors m (below): e = 2^{G_c - m}, Lk = k e, Lq = q e,
+//                            R = kappa / e, eg = 2^{G_c}, f = 2^{G_last - G_c}
+//                            dLk = dN R,  dLq = scale dM R,  dR = dN^T Lk + scale dM^T Lq
+//                            dk = dLk e + dKg eg,  dq = dLq e + scale dQg eg,  dkappa = dR / e + dKf f
+//                            dg = Lk dLk + Lq dLq - R dR + k eg dKg + scale q eg dQg - kappa f dKf
+//                            dg[last row] += sum_c kappa f dKf + dgl;  iso: dbeta = sum_i dkappa k,
+//                            dk += beta dkappa
+// dg is in natural-log coordinates.  Each output row block tl uses the forward's anchor of that block,
+// m = (G_{16tl} + G_{16tl+15}) / 2 per channel (rows clamped to the chunk), for every factor it
+// contracts with, so each factor is <= 2^{span/2} on the diagonal block and <= 1 off it; the anchor
+// terms cancel exactly (N and M do not depend on the anchors) and are omitted.
 #pragma once
 #include "kdn_common.h"
 #include "kdn_intra.h"
@@ -41,985 +51,16 @@ __device__ __forceinline__ void upper_tile(int t, int& I, int& J) {
   J = (0xfb9u >> (2 * t)) & 3;
 }
 
-// A fragment (row r, 8 consecutive v from v0) of a [rows][V] operand; bf16 input is exact (lo = 0).
-template <typename T>
-__device__ __forceinline__ void row_frag(bufrsrc r, uint32_t elem, uint4& hi, uint4& lo);
-template <>
-__device__ __forceinline__ void row_frag<float>(bufrsrc r, uint32_t elem, uint4& hi, uint4& lo) {
-  float x[8];
-  ld8(r, elem * 4, x);
-  split8(x, hi, lo);
-}
-template <>
-__device__ __forceinline__ void row_frag<bf16_t>(bufrsrc r, uint32_t elem, uint4& hi, uint4& lo) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, elem * 2, 0, 0);
-  hi = uint4{v.x, v.y, v.z, v.w};
-  lo = uint4{0u, 0u, 0u, 0u};
-}
-
-// grid (NT, B*H), block 256, two workgroups per CU (LDS 64 KB).
-//
-// The chunk rows of dO, d delta and delta are staged once per workgroup, 16 rows at a time, as
-// split fragments in LDS (double-buffered; delta's blocks are kept for the dM tiles), so each
-// row is loaded and split once instead of once per wave.  Each wave keeps its K-row tiles of h
-// and dh as split A fragments and computes the transposed products
-//   dQg^T = h dO^T,  dW^T = -h d delta^T,  dKf^T = dh delta^T,  dM^T = delta dO^T (lower part)
-// whose D tiles give each lane 4 consecutive K (or s) entries of one chunk row: 16-byte stores.
-template <int K, int V, typename TDO>
-__global__ __launch_bounds__(256, 2) void hgrad_kernel(const float* __restrict__ hbuf, const float* __restrict__ dhbuf,
-                                                       const float* __restrict__ Dl, const float* __restrict__ dDl,
-                                                       const TDO* __restrict__ dO, const float* __restrict__ gc,
-                                                       int T, int H, int NT, float* __restrict__ dQg,
-                                                       float* __restrict__ dW, float* __restrict__ dKf,
-                                                       float* __restrict__ dMg, float* __restrict__ dgl) {
-  constexpr bool DO_BF16 = sizeof(TDO) == 2;
-  constexpr int VB = V / 32;          // k-blocks of the V contraction
-  constexpr int NIT = K / 16;         // K-row tiles of h / dh
-  constexpr int ITW = (NIT + 3) / 4;  // per wave
-  constexpr int RB = VB * TILE;       // one 16-row block of a [rows][V] operand as fragments
-  constexpr int NST = 2 * V;          // staging threads: 8 consecutive v of one row each
-  static_assert(NST <= 256, "one staging slice per thread");
-  __shared__ __attribute__((aligned(16))) bf16_t sO[2][RB];       // dO rows of the current / next block
-  __shared__ __attribute__((aligned(16))) bf16_t sdD[2][RB];      // d delta rows
-  __shared__ __attribute__((aligned(16))) bf16_t sD[C / 16][RB];  // delta rows, all blocks
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-
-  const int64_t chunk = (int64_t)bh * NT + n;
-  const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
-  const bufrsrc rdh = make_buf(dhbuf + chunk * K * V, K * V * 4);
-  const bufrsrc rD = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);
-  const bufrsrc rdD = make_buf(dDl + ((int64_t)bh * T + t0) * V, L * V * 4);
-  const bufrsrc rO = make_buf(dO + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * sizeof(TDO));
-  const bufrsrc rQ = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rW = make_buf(dW + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rM = make_buf(dMg + chunk * C * C, C * C * 4);
-
-  // ---- staging slice: row sr of a 16-row block, v = sv0 .. sv0 + 7, fragment slot so
-  const int skb = tid >> 6, sl = tid & 63, sr = sl & 15, sv0 = 32 * skb + 8 * (sl >> 4), so = skb * TILE + sl * 8;
-  const bool stager = tid < NST;
-  u32x4 oraw[DO_BF16 ? 1 : 2];
-  float4 ddraw[2], draw[2];
-  auto load_block = [&](int blk) {
-    const uint32_t c = (uint32_t)(16 * blk + sr);
-    if constexpr (DO_BF16) {
-      oraw[0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + sv0) * 2, 0, 0);
-    } else {
-      oraw[0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + sv0) * 4, 0, 0);
-      oraw[1] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + sv0) * 4 + 16, 0, 0);
-    }
-    ddraw[0] = buf_ld4(rdD, (c * V + sv0) * 4);
-    ddraw[1] = buf_ld4(rdD, (c * V + sv0) * 4 + 16);
-    draw[0] = buf_ld4(rD, (c * V + sv0) * 4);
-    draw[1] = buf_ld4(rD, (c * V + sv0) * 4 + 16);
-  };
-  auto put8 = [&](bf16_t* dst, const float4& x0, const float4& x1) {
-    const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    uint4 hi, lo;
-    split8(x, hi, lo);
-    *reinterpret_cast<uint4*>(dst + so) = hi;
-    *reinterpret_cast<uint4*>(dst + so + 512) = lo;
-  };
-  auto stage_block = [&](int blk) {
-    const int p = blk & 1;
-    if constexpr (DO_BF16) {
-      *reinterpret_cast<uint4*>(sO[p] + so) = uint4{oraw[0].x, oraw[0].y, oraw[0].z, oraw[0].w};  // exact, lo = 0
-    } else {
-      put8(sO[p], __builtin_bit_cast(float4, oraw[0]), __builtin_bit_cast(float4, oraw[1]));
-    }
-    put8(sdD[p], ddraw[0], ddraw[1]);
-    put8(sD[blk], draw[0], draw[1]);
-  };
-
-  if (stager) load_block(0);
-
-  // ---- h and dh rows of this wave's tiles as split A fragments (row i, k = v), and the g_last dot
-  uint4 hh[ITW][VB], hl[ITW][VB], dhh[ITW][VB], dhl[ITW][VB];
-  {
-    const bufrsrc rg = make_buf(gc + (((int64_t)b * T + t0 + L - 1) * H + h) * K, K * 4);
-#pragma unroll
-    for (int u = 0; u < ITW; ++u) {
-      const int it = w + 4 * u;
-      if (it >= NIT) break;
-      const int i = 16 * it + r16;
-      const float gl = buf_ld(rg, i * 4);
-      float dot = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < VB; ++kb) {
-        const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
-        float x[8], y[8];
-        ld8(rh, e * 4, x);
-        ld8(rdh, e * 4, y);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dot += x[j] * y[j];
-        split8(x, hh[u][kb], hl[u][kb]);
-        split8(y, dhh[u][kb], dhl[u][kb]);
-      }
-      dot += __shfl_xor(dot, 16, 64);
-      dot += __shfl_xor(dot, 32, 64);
-      if (g4 == 0) dgl[chunk * K + i] = dot * exp2f(gl);
-    }
-  }
-  if (stager) {
-    stage_block(0);
-    load_block(1);
-  }
-  __syncthreads();
-
-#pragma unroll 1
-  for (int cb = 0; cb < C / 16; ++cb) {
-    const int p = cb & 1;
-    // ---- dQg^T, dW^T, dKf^T for this block's 16 chunk rows x this wave's K tiles
-    f32x4 aQ[ITW], aW[ITW], aK[ITW];
-#pragma unroll
-    for (int u = 0; u < ITW; ++u) aQ[u] = aW[u] = aK[u] = zero4();
-#pragma unroll
-    for (int kb = 0; kb < VB; ++kb) {
-      uint4 oh, ol, ddh, ddl, dh_, dl_;
-      oh = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + lane * 8);
-      if constexpr (!DO_BF16) ol = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + 512 + lane * 8);
-      afrag(sdD[p], kb, lane, ddh, ddl);
-      afrag(sD[cb], kb, lane, dh_, dl_);
-#pragma unroll
-      for (int u = 0; u < ITW; ++u) {
-        if (w + 4 * u >= NIT) break;
-        if constexpr (DO_BF16) aQ[u] = kdn_state::mma2(hh[u][kb], hl[u][kb], oh, aQ[u]);
-        else aQ[u] = mma3(hh[u][kb], hl[u][kb], oh, ol, aQ[u]);
-        aW[u] = mma3(hh[u][kb], hl[u][kb], ddh, ddl, aW[u]);
-        aK[u] = mma3(dhh[u][kb], dhl[u][kb], dh_, dl_, aK[u]);
-      }
-    }
-    {
-      const uint32_t c = (uint32_t)(16 * cb + r16);  // rows past L are dropped by the descriptors
-#pragma unroll
-      for (int u = 0; u < ITW; ++u) {
-        const int it = w + 4 * u;
-        if (it >= NIT) break;
-        const uint32_t o = (c * K + 16 * it + 4 * g4) * 4;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, aQ[u]), rQ, o, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, -aW[u]), rW, o, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, aK[u]), rKf, o, 0, 0);
-      }
-    }
-    // ---- dM rows of this block: tile (cb, J) = lower(dO delta^T), zero above the diagonal;
-    // tile J goes to wave (J + cb) % 4
-#pragma unroll
-    for (int J = 0; J < C / 16; ++J) {
-      if (((J + cb) & 3) != w) continue;
-      const uint32_t c = (uint32_t)(16 * cb + r16), s0 = (uint32_t)(16 * J + 4 * g4);
-      f32x4 acc = zero4();
-      if (J <= cb) {
-#pragma unroll
-        for (int kb = 0; kb < VB; ++kb) {
-          uint4 oh, ol, xh, xl;
-          oh = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + lane * 8);
-          afrag(sD[J], kb, lane, xh, xl);
-          if constexpr (DO_BF16) {
-            acc = kdn_state::mma2(xh, xl, oh, acc);
-          } else {
-            ol = *reinterpret_cast<const uint4*>(sO[p] + kb * TILE + 512 + lane * 8);
-            acc = mma3(xh, xl, oh, ol, acc);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (s0 + j > c) acc[j] = 0.f;
-      }
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), rM, (c * C + s0) * 4, 0, 0);
-    }
-    // ---- next block into the other buffer, and the loads of the one after
-    if (cb + 1 < C / 16 && stager) {
-      stage_block(cb + 1);
-      if (cb + 2 < C / 16) load_block(cb + 2);
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Transposed solves with the saved inverse (At[s][c] = A[c][s], A = (I + N)^{-1}) and dN:
-//   dV^T = d delta^T A,  dKg^T = dW^T A          (contraction over chunk rows c >= s)
-//   dN = -strict_lower(dV U^T + dKg W^T)
-// Column blocks of 32 (V/32 of d delta, then K/32 of dW) go to the waves round-robin.  A block's
-// dV^T (dKg^T) tiles stay in the accumulator layout, which is the B operand (k = column, permuted
-// order) of the block's share of dN^T; the four per-wave shares are summed through LDS.
-// Chunks flagged by the forward (outside the single-anchor range) are left to the exact kernel.
-// grid (NT, B*H), block 256.
-// ---------------------------------------------------------------------------------------------
+// index of lower tile (I, J) in the order of lower_tile
 __device__ __forceinline__ int lower_tile_index(int I, int J) {
   const int d = I - J;
   return d == 0 ? I : d == 1 ? 4 + J : d == 2 ? 7 + J : 9;
 }
 
-template <int K, int V>
-__global__ __launch_bounds__(256, 2) void solve_kernel(const float* __restrict__ At, const float* __restrict__ dDl,
-                                                       const float* __restrict__ dWg, const float* __restrict__ U,
-                                                       const float* __restrict__ W, const int* __restrict__ flags,
-                                                       int T, int H, int NT, bf16_t* __restrict__ dv,
-                                                       float* __restrict__ dKg, float* __restrict__ dNg) {
-  constexpr int NBLK = (V + K) / 32;
-  constexpr int AP4 = C + 4;  // LDS row stride of A^T (16-byte rows)
-  __shared__ __attribute__((aligned(16))) float sAt[C * AP4];
-  __shared__ __attribute__((aligned(16))) float sP[4 * 10 * 256];  // per-wave partial dN^T tiles
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  const int64_t chunk = (int64_t)bh * NT + n;
-  if (flags[chunk]) return;
-
-  {
-    const bufrsrc rA = make_buf(At + chunk * C * C, C * C * 4);
-#pragma unroll
-    for (int u = 0; u < C * C / 4 / 256; ++u) {
-      const int e4 = tid + 256 * u, sr = e4 / (C / 4), c4 = e4 % (C / 4);
-      *reinterpret_cast<float4*>(sAt + sr * AP4 + 4 * c4) = buf_ld4(rA, (sr * C + 4 * c4) * 4);
-    }
-  }
-  __syncthreads();
-
-  const bufrsrc rdv = make_buf(dv + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * 2);
-  const bufrsrc rdKg = make_buf(dKg + ((int64_t)bh * T + t0) * K, L * K * 4);
-  f32x4 part[10];
-#pragma unroll
-  for (int t = 0; t < 10; ++t) part[t] = zero4();
-
-#pragma unroll 1
-  for (int blk = w; blk < NBLK; blk += 4) {
-    const bool isV = blk < V / 32;
-    const int col0 = 32 * (isV ? blk : blk - V / 32), D = isV ? V : K;
-    const bufrsrc rX = make_buf((isV ? dDl : dWg) + ((int64_t)bh * T + t0) * D, L * D * 4);
-    const bufrsrc rY = make_buf((isV ? U : W) + ((int64_t)bh * T + t0) * D, L * D * 4);
-    // ---- Y = X^T A for the block's two column tiles and the four time blocks
-    f32x4 Y[2][4];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int J = 0; J < 4; ++J) Y[ct][J] = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      uint4 xh[2], xl[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        float xv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) xv[j] = buf_ld(rX, ((32 * kb + 8 * g4 + j) * D + col0 + 16 * ct + r16) * 4);
-        split8(xv, xh[ct], xl[ct]);
-      }
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        if (J > 2 * kb + 1) continue;  // A[c][s] = 0 for c < s
-        const float* row = sAt + (16 * J + r16) * AP4 + 32 * kb + 8 * g4;
-        const float4 a0 = *reinterpret_cast<const float4*>(row), a1 = *reinterpret_cast<const float4*>(row + 4);
-        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        uint4 ah, al;
-        split8(av, ah, al);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Y[ct][J] = mma3(xh[ct], xl[ct], ah, al, Y[ct][J]);
-      }
-    }
-    // ---- outputs: dv (bf16 [B,T,H,V]) or dKg (fp32 [B*H,T,K]); Y rows = columns, Y cols = time
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        const uint32_t tr = (uint32_t)(16 * J + r16), x0 = (uint32_t)(col0 + 16 * ct + 4 * g4);
-        const f32x4 y = Y[ct][J];
-        if (isV) {
-          const uint32_t lo = (uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16);
-          const uint32_t hi = (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16);
-          __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rdv, ((tr * H) * V + x0) * 2, 0, 0);
-        } else {
-          __builtin_amdgcn_raw_buffer_store_b128(
-              u32x4{__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]), __float_as_uint(y[3])}, rdKg,
-              (tr * K + x0) * 4, 0, 0);
-        }
-      }
-    // ---- this block's share of dN^T[s][c] = sum_x (U|W)[s][x] Y[x][c]: A = U|W rows (k = x, permuted), B = Y
-    uint4 uh[4], ul[4], yh[4], yl[4];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      const uint32_t sr = (uint32_t)(16 * J + r16);
-      const float4 a0 = buf_ld4(rY, (sr * D + col0 + 4 * g4) * 4), a1 = buf_ld4(rY, (sr * D + col0 + 16 + 4 * g4) * 4);
-      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      split8(av, uh[J], ul[J]);
-      kdn_state::bfrag(Y[0][J], Y[1][J], yh[J], yl[J]);
-    }
-#pragma unroll
-    for (int t = 0; t < 10; ++t) {
-      int I, J;
-      lower_tile(t, I, J);  // dN tile (c-block I, s-block J) = dN^T tile (rows s-block J, cols c-block I)
-      part[t] = mma3(uh[J], ul[J], yh[I], yl[I], part[t]);
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < 10; ++t)
-    *reinterpret_cast<f32x4*>(sP + ((w * 10 + t) * 64 + lane) * 4) = part[t];
-  __syncthreads();
-  // dN[c][s] = -sum over waves, strictly lower; zeros elsewhere
-  const bufrsrc rN = make_buf(dNg + chunk * C * C, C * C * 4);
-#pragma unroll 4
-  for (int u = 0; u < C * C / 256; ++u) {
-    const int e = tid + 256 * u, c = e / C, sc = e % C;
-    float val = 0.f;
-    if (sc < c) {
-      const int t = lower_tile_index(c >> 4, sc >> 4), ln = (c & 15) + 16 * ((sc & 15) >> 2), j = sc & 3;
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww) val -= sP[((ww * 10 + t) * 64 + ln) * 4 + j];
-    }
-    buf_st(rN, e * 4, val);
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
-// Gradients of q, k, kappa (iso: beta) and the gate, from dN, dM and the elementwise factors.
-// Each output row block tl uses the forward's anchor of that block, m = (G_{16tl} + G_{16tl+15})/2
-// per channel (rows clamped to the chunk), for every factor it contracts with, so each factor is
-// <= 2^{span/2} on the diagonal block and <= 1 off it.  Per element (c, i) of block tl:
-//   e = 2^{G_c - m}, Lk = k e, Lq = q e, R = kappa / e, eg = 2^{G_c}, f = 2^{G_last - G_c}
-//   dLk = dN R,  dLq = scale dM R,  dR = dN^T Lk + scale dM^T Lq          (bf16x3 MFMA)
-//   dk = dLk e + dKg eg,  dq = dLq e + scale dQg eg,  dkappa = dR / e + dKf f
-//   dg = Lk dLk + Lq dLq - R dR + k eg dKg + scale q eg dQg - kappa f dKf  (natural-log coordinates)
-//   dg[last row] += sum_c kappa f dKf + dgl;   iso: dbeta = sum_i dkappa k, dk += beta dkappa
-// The anchor terms cancel exactly (N and M do not depend on the anchors) and are omitted.
-// Wave w owns the channel tiles w, w+4.  The factors R, Lk, Lq are built per lane for one
-// channel and 16 chunk rows (the permuted-k fragment order), rows outside the contraction's
-// nonzero range zeroed, and enter the time contractions as the A operand, with dN, dM, dN^T,
-// dM^T (split once per workgroup into LDS fragments) as B: the transposed D tiles give each lane
-// 4 consecutive channels of one chunk row, so the elementwise inputs and outputs move as 16-byte
-// (fp32) and 8-byte (bf16) vectors.
-// grid (NT, B*H), block 256.  Chunks flagged by the forward go to the exact kernel.
-// ---------------------------------------------------------------------------------------------
-template <int K, bool ISO>
-__global__ __launch_bounds__(256, 2) void contrib_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
-    const float* __restrict__ gc, const float* __restrict__ dNg, const float* __restrict__ dMg,
-    const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
-    const float* __restrict__ dgl, const int* __restrict__ flags, int T, int H, int NT, float scale,
-    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
-    float* __restrict__ dg) {
-  constexpr int NIT = K / 16;
-  constexpr int ITW = (NIT + 3) / 4;
-  constexpr int FR = 8 * TILE;  // one 64 x 64 operand as (4 row tiles x 2 k-blocks) fragments
-  __shared__ __attribute__((aligned(16))) bf16_t sF[4 * FR];  // dN rows, dM rows, dN^T rows, dM^T rows
-  __shared__ float sBeta[4 * C];
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  const int64_t chunk = (int64_t)bh * NT + n;
-  if (flags[chunk]) return;
-
-  // ---- stage dN, dM (rows c, k = s) and their transposes (rows s, k = c) as split fragments in
-  // the permuted k order: slot 4h + j of lane group g <-> k = 32 kb + 16 h + 4 g + j
-  {
-    const bufrsrc rN = make_buf(dNg + chunk * C * C, C * C * 4), rM = make_buf(dMg + chunk * C * C, C * C * 4);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {  // unit: (row, kb, h, g) -> 4 consecutive slots of one lane
-      const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
-      const int k0 = 32 * kb + 16 * hh + 4 * gg;
-      const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
-      const float4 a = buf_ld4(rN, (row * C + k0) * 4), bq = buf_ld4(rM, (row * C + k0) * 4);
-      kdn_state::put_unit(sF, off, a.x, a.y, a.z, a.w);
-      kdn_state::put_unit(sF + FR, off, bq.x, bq.y, bq.z, bq.w);
-      // the same values as the transposed operands: element (row s = k0 + j, k = row) of dN^T, dM^T,
-      // one bf16 hi and lo each (tile (s/16, row/32), lane s%16 + 16 g', slot from row%32)
-      const int rk = row & 31, tg = (rk & 15) >> 2, ts = (rk & 3) + 4 * (rk >> 4);
-      const float xv[4] = {a.x, a.y, a.z, a.w}, yv[4] = {bq.x, bq.y, bq.z, bq.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int sr = k0 + j;
-        const int toff = ((sr >> 4) * 2 + (row >> 5)) * TILE + ((sr & 15) + 16 * tg) * 8 + ts;
-        const bf16_t xhi = f2bf(xv[j]), yhi = f2bf(yv[j]);
-        sF[2 * FR + toff] = xhi;
-        sF[2 * FR + toff + 512] = f2bf(xv[j] - bf2f(xhi));
-        sF[3 * FR + toff] = yhi;
-        sF[3 * FR + toff + 512] = f2bf(yv[j] - bf2f(yhi));
-      }
-    }
-  }
-  __syncthreads();
-
-  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
-  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
-  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rdkap = ISO ? make_buf(dkap, 0) : make_buf(dkap + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rdg = make_buf(dg + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rdQg = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rdKg = make_buf(dKg + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rdKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
-  float bpart[4];  // iso: dbeta partials of rows 16 tl + r16
-#pragma unroll
-  for (int p = 0; p < 4; ++p) bpart[p] = 0.f;
-
-#pragma unroll 1
-  for (int u = 0; u < ITW; ++u) {
-    const int it = w + 4 * u;
-    if (it >= NIT) break;
-    const int i = 16 * it + r16;
-    // the row offsets below are recomputed per iteration rather than held across the loop
-    int lg4 = g4, lr16 = r16;
-    asm volatile("" : "+v"(lg4), "+v"(lr16));
-    // ---- factor loads, one channel per lane: rows c = 16 tl + 4 g4 + j, slot p = 4 tl + j; the gate
-    // of rows past L repeats row L-1 (their k, q, kappa read zero)
-    float av[16], Gv[16];
-    uint16_t kraw[16], qraw[16];
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const int c = 16 * (p >> 2) + 4 * lg4 + (p & 3);
-      const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
-      kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
-      qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
-      av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);  // iso: beta of the row
-      Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep the batch together (raw bf16 held until every load is out)
-    // block anchors of channel i: rows 16J and 16J + 15 (clamped) are slot 4J of lane group 0 and
-    // slot 4J + 3 of lane group 3
-    float mA[4];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) mA[J] = 0.5f * (__shfl(Gv[4 * J], r16, 64) + __shfl(Gv[4 * J + 3], 48 + r16, 64));
-    // factors of each slot anchored at its own block J = p / 4 (<= 2^{span_J / 2}); another block's
-    // anchor is one per-lane scale 2^{m_tl - m_J} (R side, J <= tl) or 2^{m_J - m_tl} (k side, J >= tl)
-    float Rown[16], Kown[16], Qown[16];
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const float kvp = bf2f(kraw[p]), e = exp2f(Gv[p] - mA[p >> 2]);
-      Kown[p] = kvp * e;
-      Qown[p] = scale * bf2f(qraw[p]) * e;
-      Rown[p] = (ISO ? av[p] * kvp : av[p]) * __frcp_rn(e);
-    }
-    // ---- elementwise inputs at the transposed tile positions: row c = 16 tl + r16, channels
-    // i0 .. i0+3 (16-byte / 8-byte loads), issued before the contractions
-    const int i0 = 16 * it + 4 * g4;
-    const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
-    u32x2 kq4[4], qq4[4];
-    float4 kap4[4], G4[4], dkg4[4], dqg4[4], dkf4[4];
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      const uint32_t c = (uint32_t)(16 * tl + lr16), o = c * H * K + i0, ol = c * K + i0;
-      kq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rk, o * 2, 0, 0);
-      qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
-      if (ISO) {
-        const float be = buf_ld(rkap, c * H * 4);
-        kap4[tl] = float4{be, be, be, be};
-      } else {
-        kap4[tl] = buf_ld4(rkap, o * 4);
-      }
-      G4[tl] = buf_ld4(rG, ((uint32_t)(min(16 * tl + lr16, L - 1) * H) * K + i0) * 4);
-      dkg4[tl] = buf_ld4(rdKg, ol * 4);
-      dqg4[tl] = buf_ld4(rdQg, ol * 4);
-      dkf4[tl] = buf_ld4(rdKf, ol * 4);
-    }
-    float colpart[4] = {0.f, 0.f, 0.f, 0.f};
-    float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
-    bool has_last = false;
-    const float gla[4] = {glv.x, glv.y, glv.z, glv.w};
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      // ---- time contractions of row block tl, transposed (factor fragments anchored at block tl as
-      // A, dN/dM fragments as B): the D tile gives lane (row 16 tl + r16) the channels i0 .. i0+3
-      f32x4 dLk = zero4(), dLq = zero4(), dR = zero4();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        uint4 ah, al;
-        if (kb <= tl / 2) {  // dN, dM rows c: nonzero for s <= c; R of rows in blocks <= tl
-          const float s0 = 2 * kb <= tl ? exp2f(mA[tl] - mA[2 * kb]) : 0.f;
-          const float s1 = 2 * kb + 1 <= tl ? exp2f(mA[tl] - mA[2 * kb + 1]) : 0.f;
-          float rv[8];
-#pragma unroll
-          for (int sl = 0; sl < 8; ++sl) rv[sl] = Rown[8 * kb + sl] * (sl < 4 ? s0 : s1);
-          uint4 Rh, Rl;
-          split8(rv, Rh, Rl);
-          afrag(sF, tl * 2 + kb, lane, ah, al);
-          dLk = mma3(Rh, Rl, ah, al, dLk);
-          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
-          dLq = mma3(Rh, Rl, ah, al, dLq);
-        }
-        if (2 * kb + 1 >= tl) {  // dN^T, dM^T rows s: nonzero for c >= s; Lk, Lq of rows in blocks >= tl
-          const float t0 = 2 * kb >= tl ? exp2f(mA[2 * kb] - mA[tl]) : 0.f;
-          const float t1 = 2 * kb + 1 >= tl ? exp2f(mA[2 * kb + 1] - mA[tl]) : 0.f;
-          float lk[8], lq[8];
-#pragma unroll
-          for (int sl = 0; sl < 8; ++sl) {
-            const float t = sl < 4 ? t0 : t1;
-            lk[sl] = Kown[8 * kb + sl] * t;
-            lq[sl] = Qown[8 * kb + sl] * t;
-          }
-          uint4 Kh, Kl, Qh, Ql;
-          split8(lk, Kh, Kl);
-          split8(lq, Qh, Ql);
-          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
-          dR = mma3(Kh, Kl, ah, al, dR);
-          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
-          dR = mma3(Qh, Ql, ah, al, dR);
-        }
-      }
-      // ---- assemble row block tl
-      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
-      const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
-                            __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
-      const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
-                            __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
-      const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
-      const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
-      // anchors of channels i0 .. i0+3 = 16 it + 4 g4 + j, held by lanes 4 g4 + j
-      const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
-                           __shfl(mA[tl], 4 * g4 + 3, 64)};
-      const float dkgv[4] = {dkg4[tl].x, dkg4[tl].y, dkg4[tl].z, dkg4[tl].w};
-      const float dqgv[4] = {dqg4[tl].x, dqg4[tl].y, dqg4[tl].z, dqg4[tl].w};
-      const float dkfv[4] = {dkf4[tl].x, dkf4[tl].y, dkf4[tl].z, dkf4[tl].w};
-      float dkv[4], dqv[4], dav[4], dgv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float beta = ISO ? a4[j] : 0.f;
-        const float kap_p = ISO ? beta * kv4[j] : a4[j];
-        const float e = exp2f(gv[j] - mz[j]), er = __frcp_rn(e);
-        const float eg = exp2f(gv[j]), f = exp2f(gla[j] - gv[j]);
-        const float a_lk = dLk[j], a_lq = dLq[j] * scale, a_r = dR[j];
-        dkv[j] = a_lk * e + dkgv[j] * eg;
-        dqv[j] = a_lq * e + scale * dqgv[j] * eg;
-        dav[j] = a_r * er + dkfv[j] * f;
-        // Lk = k e, Lq (unscaled) = q e, R = kappa er
-        dgv[j] = kv4[j] * e * a_lk + qv4[j] * e * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv[j] +
-                 scale * qv4[j] * eg * dqgv[j] - kap_p * f * dkfv[j];
-        if ((int)c < L) colpart[j] += kap_p * f * dkfv[j];
-        if (ISO) {
-          dkv[j] += beta * dav[j];
-          bpart[tl] += dav[j] * kv4[j];
-        }
-      }
-      if (!ISO)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            u32x4{__float_as_uint(dav[0]), __float_as_uint(dav[1]), __float_as_uint(dav[2]), __float_as_uint(dav[3])},
-            rdkap, o * 4, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16), (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
-          rdq, o * 2, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16), (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
-          rdk, o * 2, 0, 0);
-      if ((int)c == L - 1) {
-        dg_last = float4{dgv[0], dgv[1], dgv[2], dgv[3]};
-        has_last = true;
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b128(
-            u32x4{__float_as_uint(dgv[0]), __float_as_uint(dgv[1]), __float_as_uint(dgv[2]), __float_as_uint(dgv[3])},
-            rdg, o * 4, 0, 0);
-      }
-    }
-    // column sums over the chunk rows: the 16 lanes of a channel group hold rows r16 of each block
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) colpart[j] += __shfl_xor(colpart[j], m, 64);
-    if (has_last) {
-      const float4 gl4 = *reinterpret_cast<const float4*>(dgl + chunk * K + i0);
-      const float4 v = float4{dg_last.x + colpart[0] + gl4.x, dg_last.y + colpart[1] + gl4.y,
-                              dg_last.z + colpart[2] + gl4.z, dg_last.w + colpart[3] + gl4.w};
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rdg,
-                                             ((uint32_t)((L - 1) * H) * K + i0) * 4, 0, 0);
-    }
-  }
-  if (ISO) {  // dbeta[c] = sum_i dkappa k: over the 4 lane groups (channels), then the waves
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      float v = bpart[tl];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (g4 == 0) sBeta[w * C + 16 * tl + r16] = v;
-    }
-    __syncthreads();
-    if (tid < L) dbeta[((int64_t)b * T + t0 + tid) * H + h] = sBeta[tid] + sBeta[C + tid] + sBeta[2 * C + tid] +
-                                                               sBeta[3 * C + tid];
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// solve + contrib in one kernel: the transposed solves of solve_kernel, then the gradients of
-// contrib_kernel, with dKg and dN kept on chip instead of a round trip through HBM.
-//  * Solve phase.  The V blocks of d delta go to the waves round-robin as in solve_kernel (dv is
-//    stored).  The K columns are taken per wave as contrib's channel tiles it = w + 4 u: the D tiles
-//    of dKg^T then give each lane 4 consecutive channels of one chunk row -- the elementwise
-//    operand layout of the contrib phase -- so they stay in registers (kg[u][tl]).
-//  * The per-wave dN^T partials are summed in the order of solve_kernel straight into the dN
-//    staging units of the contrib phase (dN = minus their sum, strictly lower).
-//  * LDS: the solve phase's A^T and partials (57 KB) and the contrib phase's fragments (64 KB)
-//    share one buffer: the partials are read into registers before the fragments are written.
-// grid (NT, B*H), block 256.  Chunks flagged by the forward are left to the exact kernels.
-// ---------------------------------------------------------------------------------------------
-template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256, 2) void solve_contrib_kernel(
-    const float* __restrict__ At, const float* __restrict__ dDl, const float* __restrict__ dWg,
-    const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
-    const float* __restrict__ gc, const float* __restrict__ dMg, const float* __restrict__ dQg,
-    const float* __restrict__ dKf, const float* __restrict__ dgl, int T, int H, int NT, float scale,
-    bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap,
-    float* __restrict__ dbeta, float* __restrict__ dg) {
-  constexpr int NIT = K / 16;
-  constexpr int ITW = (NIT + 3) / 4;  // channel tiles per wave (1 or 2)
-  constexpr int FR = 8 * TILE;        // one 64 x 64 operand as (4 row tiles x 2 k-blocks) fragments
-  constexpr int AP4 = C + 4;          // LDS row stride of A^T
-  constexpr int SOLVE_FLOATS = C * AP4 + 4 * 10 * 256;
-  constexpr int LDS_BYTES = SOLVE_FLOATS * 4 > 4 * FR * 2 ? SOLVE_FLOATS * 4 : 4 * FR * 2;
-  static_assert(ITW == 1 || ITW == 2, "K in {64, 128}");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
-  __shared__ float sBeta[4 * C];
-  float* sAt = reinterpret_cast<float*>(smem);
-  float* sP = sAt + C * AP4;                        // per-wave partial dN^T tiles
-  bf16_t* sF = reinterpret_cast<bf16_t*>(smem);    // contrib phase: dN, dM, dN^T, dM^T fragments
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  const int64_t chunk = (int64_t)bh * NT + n;
-  if (flags[chunk]) return;
-
-  // ================================ solve phase ================================
-  {
-    const bufrsrc rA = make_buf(At + chunk * C * C, C * C * 4);
-#pragma unroll
-    for (int u = 0; u < C * C / 4 / 256; ++u) {
-      const int e4 = tid + 256 * u, sr = e4 / (C / 4), c4 = e4 % (C / 4);
-      *reinterpret_cast<float4*>(sAt + sr * AP4 + 4 * c4) = buf_ld4(rA, (sr * C + 4 * c4) * 4);
-    }
-  }
-  __syncthreads();
-
-  const bufrsrc rdv = make_buf(dv + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * 2);
-  f32x4 part[10];
-#pragma unroll
-  for (int t = 0; t < 10; ++t) part[t] = zero4();
-  f32x4 kg[ITW][4];  // dKg^T tiles of this wave's channel tiles: lane -> row 16 J + r16, 4 channels
-
-  // One column block: two 16-column tiles at columns cA, cB (cB < 0: absent) of X ([T][D] d delta or
-  // dW) and Y ([T][D] U or W).  Y^T tiles Yt = X^T A for the four time blocks, then this block's
-  // share of dN^T = (U|W) Y.
-  auto solve_block = [&](const float* Xg, const float* Yg, int D, int cA, int cB, f32x4 (&Yt)[2][4]) {
-    const bufrsrc rX = make_buf(Xg + ((int64_t)bh * T + t0) * D, L * D * 4);
-    const bufrsrc rY = make_buf(Yg + ((int64_t)bh * T + t0) * D, L * D * 4);
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int J = 0; J < 4; ++J) Yt[ct][J] = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      uint4 xh[2], xl[2];
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int col = ct == 0 ? cA : cB;
-        float xv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          xv[j] = col >= 0 ? buf_ld(rX, ((32 * kb + 8 * g4 + j) * D + col + r16) * 4) : 0.f;
-        split8(xv, xh[ct], xl[ct]);
-      }
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        if (J > 2 * kb + 1) continue;  // A[c][s] = 0 for c < s
-        const float* row = sAt + (16 * J + r16) * AP4 + 32 * kb + 8 * g4;
-        const float4 a0 = *reinterpret_cast<const float4*>(row), a1 = *reinterpret_cast<const float4*>(row + 4);
-        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        uint4 ah, al;
-        split8(av, ah, al);
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) Yt[ct][J] = mma3(xh[ct], xl[ct], ah, al, Yt[ct][J]);
-      }
-    }
-    uint4 uh[4], ul[4], yh[4], yl[4];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      const uint32_t sr = (uint32_t)(16 * J + r16);
-      const float4 a0 = buf_ld4(rY, (sr * D + cA + 4 * g4) * 4);
-      const float4 a1 = cB >= 0 ? buf_ld4(rY, (sr * D + cB + 4 * g4) * 4) : float4{0.f, 0.f, 0.f, 0.f};
-      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      split8(av, uh[J], ul[J]);
-      kdn_state::bfrag(Yt[0][J], Yt[1][J], yh[J], yl[J]);
-    }
-#pragma unroll
-    for (int t = 0; t < 10; ++t) {
-      int I, J;
-      lower_tile(t, I, J);
-      part[t] = mma3(uh[J], ul[J], yh[I], yl[I], part[t]);
-    }
-  };
-  // V blocks of d delta: dv^T tiles stored (bf16 [B,T,H,V])
-#pragma unroll 1
-  for (int vb = w; vb < V / 32; vb += 4) {
-    f32x4 Yt[2][4];
-    solve_block(dDl, U, V, 32 * vb, 32 * vb + 16, Yt);
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        const uint32_t tr = (uint32_t)(16 * J + r16), x0 = (uint32_t)(32 * vb + 16 * ct + 4 * g4);
-        const f32x4 y = Yt[ct][J];
-        const uint32_t lo = (uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16);
-        const uint32_t hi = (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16);
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rdv, ((tr * H) * V + x0) * 2, 0, 0);
-      }
-  }
-  // K columns of dW: this wave's channel tiles w, w + 4 (ITW = 2) or w (ITW = 1); dKg^T kept
-  {
-    f32x4 Yt[2][4];
-    solve_block(dWg, W, K, 16 * w, ITW == 2 ? 16 * (w + 4) : -1, Yt);
-#pragma unroll
-    for (int u = 0; u < ITW; ++u)
-#pragma unroll
-      for (int J = 0; J < 4; ++J) kg[u][J] = Yt[u][J];
-  }
-#pragma unroll
-  for (int t = 0; t < 10; ++t) *reinterpret_cast<f32x4*>(sP + ((w * 10 + t) * 64 + lane) * 4) = part[t];
-  __syncthreads();
-
-  // ======================= dN, dM staging (contrib's fragments) =======================
-  // unit (row c, kb, hh, gg) -> 4 consecutive s = k0 .. k0+3 of one lane's fragment slots
-  float4 dNu[4], dMu[4];
-  {
-    const bufrsrc rM = make_buf(dMg + chunk * C * C, C * C * 4);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
-      const int k0 = 32 * kb + 16 * hh + 4 * gg;
-      dMu[u] = buf_ld4(rM, (row * C + k0) * 4);
-      // dN[c][s] = -sum over the waves' dN^T partials, strictly lower (s < c); D layout of tile
-      // (c-block I, s-block J): lane (c % 16) + 16 ((s % 16) / 4), slot s % 4
-      float4 acc = float4{0.f, 0.f, 0.f, 0.f};
-      if ((k0 >> 4) <= (row >> 4)) {
-        const int t = lower_tile_index(row >> 4, k0 >> 4), ln = (row & 15) + 16 * ((k0 & 15) >> 2);
-#pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
-          const float4 v = *reinterpret_cast<const float4*>(sP + ((ww * 10 + t) * 64 + ln) * 4);
-          acc.x -= v.x, acc.y -= v.y, acc.z -= v.z, acc.w -= v.w;
-        }
-        if (k0 + 0 >= row) acc.x = 0.f;
-        if (k0 + 1 >= row) acc.y = 0.f;
-        if (k0 + 2 >= row) acc.z = 0.f;
-        if (k0 + 3 >= row) acc.w = 0.f;
-      }
-      dNu[u] = acc;
-    }
-  }
-  __syncthreads();  // every partial read before the fragments overwrite them
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int e = tid + 256 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
-    const int k0 = 32 * kb + 16 * hh + 4 * gg;
-    const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
-    const float4 a = dNu[u], bq = dMu[u];
-    kdn_state::put_unit(sF, off, a.x, a.y, a.z, a.w);
-    kdn_state::put_unit(sF + FR, off, bq.x, bq.y, bq.z, bq.w);
-    const int rk = row & 31, tg = (rk & 15) >> 2, ts = (rk & 3) + 4 * (rk >> 4);
-    const float xv[4] = {a.x, a.y, a.z, a.w}, yv[4] = {bq.x, bq.y, bq.z, bq.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int sr = k0 + j;
-      const int toff = ((sr >> 4) * 2 + (row >> 5)) * TILE + ((sr & 15) + 16 * tg) * 8 + ts;
-      const bf16_t xhi = f2bf(xv[j]), yhi = f2bf(yv[j]);
-      sF[2 * FR + toff] = xhi;
-      sF[2 * FR + toff + 512] = f2bf(xv[j] - bf2f(xhi));
-      sF[3 * FR + toff] = yhi;
-      sF[3 * FR + toff + 512] = f2bf(yv[j] - bf2f(yhi));
-    }
-  }
-  __syncthreads();
-
-  // ================================ contrib phase ================================
-  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
-  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
-  const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rkap = ISO ? make_buf(kap + in_row0, rows_in * 4) : make_buf(kap + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
-  const bufrsrc rdkap = ISO ? make_buf(dkap, 0) : make_buf(dkap + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rdg = make_buf(dg + in_row0 * K, rows_in * K * 4);
-  const bufrsrc rdQg = make_buf(dQg + ((int64_t)bh * T + t0) * K, L * K * 4);
-  const bufrsrc rdKf = make_buf(dKf + ((int64_t)bh * T + t0) * K, L * K * 4);
-  float bpart[4];  // iso: dbeta partials of rows 16 tl + r16
-#pragma unroll
-  for (int p = 0; p < 4; ++p) bpart[p] = 0.f;
-
-#pragma unroll 1
-  for (int u = 0; u < ITW; ++u) {
-    const int it = w + 4 * u;
-    const int i = 16 * it + r16;
-    f32x4 kgu[4];  // this tile's dKg (a select, not a runtime index, keeps kg in registers)
-#pragma unroll
-    for (int J = 0; J < 4; ++J) kgu[J] = (ITW == 1 || u == 0) ? kg[0][J] : kg[ITW - 1][J];
-    int lg4 = g4, lr16 = r16;
-    asm volatile("" : "+v"(lg4), "+v"(lr16));
-    float av[16], Gv[16];
-    uint16_t kraw[16], qraw[16];
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const int c = 16 * (p >> 2) + 4 * lg4 + (p & 3);
-      const uint32_t crow = (uint32_t)(c * H), o = crow * K + i;
-      kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
-      qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
-      av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);
-      Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    float mA[4];
-#pragma unroll
-    for (int J = 0; J < 4; ++J) mA[J] = 0.5f * (__shfl(Gv[4 * J], r16, 64) + __shfl(Gv[4 * J + 3], 48 + r16, 64));
-    float Rown[16], Kown[16], Qown[16];
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const float kvp = bf2f(kraw[p]), e = exp2f(Gv[p] - mA[p >> 2]);
-      Kown[p] = kvp * e;
-      Qown[p] = scale * bf2f(qraw[p]) * e;
-      Rown[p] = (ISO ? av[p] * kvp : av[p]) * __frcp_rn(e);
-    }
-    const int i0 = 16 * it + 4 * g4;
-    const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
-    u32x2 kq4[4], qq4[4];
-    float4 kap4[4], G4[4], dqg4[4], dkf4[4];
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      const uint32_t c = (uint32_t)(16 * tl + lr16), o = c * H * K + i0, ol = c * K + i0;
-      kq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rk, o * 2, 0, 0);
-      qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
-      if (ISO) {
-        const float be = buf_ld(rkap, c * H * 4);
-        kap4[tl] = float4{be, be, be, be};
-      } else {
-        kap4[tl] = buf_ld4(rkap, o * 4);
-      }
-      G4[tl] = buf_ld4(rG, ((uint32_t)(min(16 * tl + lr16, L - 1) * H) * K + i0) * 4);
-      dqg4[tl] = buf_ld4(rdQg, ol * 4);
-      dkf4[tl] = buf_ld4(rdKf, ol * 4);
-    }
-    float colpart[4] = {0.f, 0.f, 0.f, 0.f};
-    float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
-    bool has_last = false;
-    const float gla[4] = {glv.x, glv.y, glv.z, glv.w};
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      f32x4 dLk = zero4(), dLq = zero4(), dR = zero4();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        uint4 ah, al;
-        if (kb <= tl / 2) {
-          const float s0 = 2 * kb <= tl ? exp2f(mA[tl] - mA[2 * kb]) : 0.f;
-          const float s1 = 2 * kb + 1 <= tl ? exp2f(mA[tl] - mA[2 * kb + 1]) : 0.f;
-          float rv[8];
-#pragma unroll
-          for (int sl = 0; sl < 8; ++sl) rv[sl] = Rown[8 * kb + sl] * (sl < 4 ? s0 : s1);
-          uint4 Rh, Rl;
-          split8(rv, Rh, Rl);
-          afrag(sF, tl * 2 + kb, lane, ah, al);
-          dLk = mma3(Rh, Rl, ah, al, dLk);
-          afrag(sF + FR, tl * 2 + kb, lane, ah, al);
-          dLq = mma3(Rh, Rl, ah, al, dLq);
-        }
-        if (2 * kb + 1 >= tl) {
-          const float s0 = 2 * kb >= tl ? exp2f(mA[2 * kb] - mA[tl]) : 0.f;
-          const float s1 = 2 * kb + 1 >= tl ? exp2f(mA[2 * kb + 1] - mA[tl]) : 0.f;
-          float lk[8], lq[8];
-#pragma unroll
-          for (int sl = 0; sl < 8; ++sl) {
-            const float sc = sl < 4 ? s0 : s1;
-            lk[sl] = Kown[8 * kb + sl] * sc;
-            lq[sl] = Qown[8 * kb + sl] * sc;
-          }
-          uint4 Kh, Kl, Qh, Ql;
-          split8(lk, Kh, Kl);
-          split8(lq, Qh, Ql);
-          afrag(sF + 2 * FR, tl * 2 + kb, lane, ah, al);
-          dR = mma3(Kh, Kl, ah, al, dR);
-          afrag(sF + 3 * FR, tl * 2 + kb, lane, ah, al);
-          dR = mma3(Qh, Ql, ah, al, dR);
-        }
-      }
-      const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
-      const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
-                            __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
-      const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
-                            __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
-      const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
-      const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
-      const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
-                           __shfl(mA[tl], 4 * g4 + 3, 64)};
-      const f32x4 kgt = kgu[tl];
-      const float dkgv[4] = {kgt[0], kgt[1], kgt[2], kgt[3]};
-      const float dqgv[4] = {dqg4[tl].x, dqg4[tl].y, dqg4[tl].z, dqg4[tl].w};
-      const float dkfv[4] = {dkf4[tl].x, dkf4[tl].y, dkf4[tl].z, dkf4[tl].w};
-      float dkv[4], dqv[4], dav[4], dgv[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float beta = ISO ? a4[j] : 0.f;
-        const float kap_p = ISO ? beta * kv4[j] : a4[j];
-        const float e = exp2f(gv[j] - mz[j]), er = __frcp_rn(e);
-        const float eg = exp2f(gv[j]), f = exp2f(gla[j] - gv[j]);
-        const float a_lk = dLk[j], a_lq = dLq[j] * scale, a_r = dR[j];
-        dkv[j] = a_lk * e + dkgv[j] * eg;
-        dqv[j] = a_lq * e + scale * dqgv[j] * eg;
-        dav[j] = a_r * er + dkfv[j] * f;
-        dgv[j] = kv4[j] * e * a_lk + qv4[j] * e * a_lq - kap_p * er * a_r + kv4[j] * eg * dkgv[j] +
-                 scale * qv4[j] * eg * dqgv[j] - kap_p * f * dkfv[j];
-        if ((int)c < L) colpart[j] += kap_p * f * dkfv[j];
-        if (ISO) {
-          dkv[j] += beta * dav[j];
-          bpart[tl] += dav[j] * kv4[j];
-        }
-      }
-      if (!ISO)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            u32x4{__float_as_uint(dav[0]), __float_as_uint(dav[1]), __float_as_uint(dav[2]), __float_as_uint(dav[3])},
-            rdkap, o * 4, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16), (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
-          rdq, o * 2, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16), (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
-          rdk, o * 2, 0, 0);
-      if ((int)c == L - 1) {
-        dg_last = float4{dgv[0], dgv[1], dgv[2], dgv[3]};
-        has_last = true;
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b128(
-            u32x4{__float_as_uint(dgv[0]), __float_as_uint(dgv[1]), __float_as_uint(dgv[2]), __float_as_uint(dgv[3])},
-            rdg, o * 4, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) colpart[j] += __shfl_xor(colpart[j], m, 64);
-    if (has_last) {
-      const float4 gl4 = *reinterpret_cast<const float4*>(dgl + chunk * K + i0);
-      const float4 v = float4{dg_last.x + colpart[0] + gl4.x, dg_last.y + colpart[1] + gl4.y,
-                              dg_last.z + colpart[2] + gl4.z, dg_last.w + colpart[3] + gl4.w};
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rdg,
-                                             ((uint32_t)((L - 1) * H) * K + i0) * 4, 0, 0);
-    }
-  }
-  if (ISO) {
-#pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      float v = bpart[tl];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (g4 == 0) sBeta[w * C + 16 * tl + r16] = v;
-    }
-    __syncthreads();
-    if (tid < L) dbeta[((int64_t)b * T + t0 + tid) * H + h] = sBeta[tid] + sBeta[C + tid] + sBeta[2 * C + tid] +
-                                                               sBeta[3 * C + tid];
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// The whole chunk-parallel backward of one chunk in one kernel: the state-gradient products of
-// hgrad_kernel, the transposed solves and the gradients of solve_contrib_kernel.  dQg, dW, dKf, dM
-// and the g_last dots never go to HBM: each is produced in the register layout its consumer takes.
+// The whole chunk-parallel backward of one chunk in one kernel: the state-gradient products, the
+// transposed solves and the gradients.  dQg, dW, dKf, dM, dKg, dN and the g_last dots never go to
+// HBM: each is produced in the register or LDS layout its consumer takes.
 // grid (NT, B*H), block 512 (8 waves), one workgroup per CU (LDS ~99 KB).
 //  * Staging.  The chunk rows of dO, delta and d delta are split into LDS fragments (rows c,
 //    k = v, natural order), all 64 rows at once.
@@ -1034,7 +75,13 @@ __global__ __launch_bounds__(256, 2) void solve_contrib_kernel(
 //  * Solve.  Per wave one 32-column block: its V tile of d delta (dv stored) and its K tile of dW
 //    (dKg kept in registers), with A^T read in the same permuted k order; the block's dN^T share
 //    over the 8 waves is summed through LDS in two steps (waves 4..7 into 0..3, then the four).
-//  * Gradients: as in solve_contrib_kernel, one channel tile per wave.
+//  * Gradients.  dN, dM and their transposes are split once into LDS fragments (permuted k order:
+//    slot 4h + j of lane group g <-> k = 32 kb + 16 h + 4 g + j).  Per channel tile the factors R,
+//    Lk, Lq are built per lane for one channel and 16 chunk rows (rows outside the contraction's
+//    nonzero range zeroed) and enter the time contractions as the A operand, with the dN / dM
+//    fragments as B: the D tiles give each lane 4 consecutive channels of one chunk row, the layout
+//    of dQg, dKf and dKg, so the elementwise inputs and outputs move as 16-byte (fp32) and 8-byte
+//    (bf16) vectors.
 // Chunks flagged by the forward store the products (dQg, dW, dKf, dM, dgl) for the exact kernels
 // and stop after them.
 // ---------------------------------------------------------------------------------------------
@@ -1181,7 +228,7 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
     }
     dot += __shfl_xor(dot, 16, 64);
     dot += __shfl_xor(dot, 32, 64);
-    if (g4 == 0) sDgl[16 * it + r16] = dot * exp2f(gl_i);
+    if (g4 == 0) sDgl[16 * it + r16] = dot * fexp2(gl_i);
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb)
 #pragma unroll
@@ -1446,10 +493,10 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
     float Rown[16], Kown[16], Qown[16];
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
-      const float kvp = bf2f(kraw[p]), e = exp2f(Gv[p] - mA[p >> 2]);
+      const float kvp = bf2f(kraw[p]), e = fexp2(Gv[p] - mA[p >> 2]);
       Kown[p] = kvp * e;
       Qown[p] = scale * bf2f(qraw[p]) * e;
-      Rown[p] = (ISO ? av[p] * kvp : av[p]) * __frcp_rn(e);
+      Rown[p] = (ISO ? av[p] * kvp : av[p]) * frcp(e);
     }
     const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
     u32x2 kq4[4], qq4[4];
@@ -1478,8 +525,8 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
       for (int kb = 0; kb < 2; ++kb) {
         uint4 ah, al;
         if (kb <= tl / 2) {
-          const float s0 = 2 * kb <= tl ? exp2f(mA[tl] - mA[2 * kb]) : 0.f;
-          const float s1 = 2 * kb + 1 <= tl ? exp2f(mA[tl] - mA[2 * kb + 1]) : 0.f;
+          const float s0 = 2 * kb <= tl ? fexp2(mA[tl] - mA[2 * kb]) : 0.f;
+          const float s1 = 2 * kb + 1 <= tl ? fexp2(mA[tl] - mA[2 * kb + 1]) : 0.f;
           float rv[8];
 #pragma unroll
           for (int sl = 0; sl < 8; ++sl) rv[sl] = Rown[8 * kb + sl] * (sl < 4 ? s0 : s1);
@@ -1491,8 +538,8 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
           dLq = mma3(Rh, Rl, ah, al, dLq);
         }
         if (2 * kb + 1 >= tl) {
-          const float s0 = 2 * kb >= tl ? exp2f(mA[2 * kb] - mA[tl]) : 0.f;
-          const float s1 = 2 * kb + 1 >= tl ? exp2f(mA[2 * kb + 1] - mA[tl]) : 0.f;
+          const float s0 = 2 * kb >= tl ? fexp2(mA[2 * kb] - mA[tl]) : 0.f;
+          const float s1 = 2 * kb + 1 >= tl ? fexp2(mA[2 * kb + 1] - mA[tl]) : 0.f;
           float lk[8], lq[8];
 #pragma unroll
           for (int sl = 0; sl < 8; ++sl) {
@@ -1523,8 +570,8 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
       for (int j = 0; j < 4; ++j) {
         const float beta = ISO ? a4[j] : 0.f;
         const float kap_p = ISO ? beta * kv4[j] : a4[j];
-        const float e = exp2f(gv[j] - mz[j]), er = __frcp_rn(e);
-        const float eg = exp2f(gv[j]), f = exp2f(gla[j] - gv[j]);
+        const float e = fexp2(gv[j] - mz[j]), er = frcp(e);
+        const float eg = fexp2(gv[j]), f = fexp2(gla[j] - gv[j]);
         const float a_lk = dLk[j], a_lq = dLq[j] * scale, a_r = dR[j];
         const float dkgv = kg[tl][j], dqgv = aQ[tl][j], dkfv = aK[tl][j];
         dkv[j] = a_lk * e + dkgv * eg;

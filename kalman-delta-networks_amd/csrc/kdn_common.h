@@ -79,6 +79,9 @@ __device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x)
 // branches: both sides of torch's threshold (x > 20 -> x) and of the small-value series are formed
 // and selected, so no exec-mask branching sits in the token loops.  NaN propagates.
 __device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * KDN_LOG2E); }
+// 2^x on the hardware exp2 (one v_exp_f32): results below 2^-126 flush towards zero, where exp2f
+// would produce denormals; every use multiplies it with O(1) terms, so the difference is below 1e-38.
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fsoftplus_y(float x, float y, float d) {  // y = e^min(x, 20), d = 1 + y
   // every operand is computed first, so both conditionals are selects (a conditional over an
   // expression is emitted as a branch, and the logarithm would be sunk into it)

@@ -183,7 +183,7 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
         unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, o * 2, 0, 0), x);
         ld8(rG, o * 4, g);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] *= exp2f(g[j]);
+        for (int j = 0; j < 8; ++j) x[j] *= fexp2(g[j]);
       }
       // row-major [s][col]: the 16 lanes of a row write consecutive 16-byte pieces (a column-major
       // store here put 16 lanes on one bank)
@@ -319,12 +319,12 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     float lk[8], lq[8], rr[8], kf[8], qg[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float e = exp2f(gcv[j] - g0[j]);
+      const float e = fexp2(gcv[j] - g0[j]);
       lk[j] = kv[j] * e;
       lq[j] = scale * qv[j] * e;
-      rr[j] = av[j] * exp2f(g0[j] - gcv[j]);
-      kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
-      qg[j] = scale * qv[j] * exp2f(gcv[j]);
+      rr[j] = av[j] * fexp2(g0[j] - gcv[j]);
+      kf[j] = av[j] * fexp2(gl[j] - gcv[j]);
+      qg[j] = scale * qv[j] * fexp2(gcv[j]);
     }
     split8(lk, lkh[kb], lkl[kb]);
     split8(lq, lqh[kb], lql[kb]);
@@ -456,12 +456,12 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
     float lk[8], lq[8], rr[8], kf[8], qg[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float e = exp2f(gcv[j] - mid[j]);
+      const float e = fexp2(gcv[j] - mid[j]);
       lk[j] = kv[j] * e;
       lq[j] = scale * qv[j] * e;
-      rr[j] = av[j] * exp2f(mid[j] - gcv[j]);
-      kf[j] = av[j] * exp2f(gl[j] - gcv[j]);
-      qg[j] = scale * qv[j] * exp2f(gcv[j]);
+      rr[j] = av[j] * fexp2(mid[j] - gcv[j]);
+      kf[j] = av[j] * fexp2(gl[j] - gcv[j]);
+      qg[j] = scale * qv[j] * fexp2(gcv[j]);
     }
     split8(lk, lkh[kb], lkl[kb]);
     split8(lq, lqh[kb], lql[kb]);
@@ -500,8 +500,8 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
         const float4 m1 = *reinterpret_cast<const float4*>(sMid + w * K + i0 + 4);
         const float4 p0 = *reinterpret_cast<const float4*>(sMid + J * K + i0);
         const float4 p1 = *reinterpret_cast<const float4*>(sMid + J * K + i0 + 4);
-        const float f[8] = {exp2f(m0.x - p0.x), exp2f(m0.y - p0.y), exp2f(m0.z - p0.z), exp2f(m0.w - p0.w),
-                            exp2f(m1.x - p1.x), exp2f(m1.y - p1.y), exp2f(m1.z - p1.z), exp2f(m1.w - p1.w)};
+        const float f[8] = {fexp2(m0.x - p0.x), fexp2(m0.y - p0.y), fexp2(m0.z - p0.z), fexp2(m0.w - p0.w),
+                            fexp2(m1.x - p1.x), fexp2(m1.y - p1.y), fexp2(m1.z - p1.z), fexp2(m1.w - p1.w)};
         uint4 xh, xl, rh, rl;
         afrag(sR, J * KB + kb, lane, rh, rl);
         rescale8(lkh[kb], lkl[kb], f, xh, xl);

@@ -18,9 +18,12 @@
 //   state_fwd    serial over chunks, one workgroup per (V-slice, b, h): h per chunk, delta
 //   readout      chunk-parallel O = Qg h + M delta (kdn_state.h)
 //   state_bwd    serial reverse (kdn_state.h): d delta = M^T dO + Kf dS;  dS <- e dS + Qg^T dO - W^T d delta
-//   bwd_hgrad    dQg = dO h^T, dW = -d delta h^T, dKf = delta dh^T, dM = dO delta^T, g_last terms
-//   bwd_solve    dV = (I+N)^-T d delta, dKg = (I+N)^-T dW, dN = -(dV U^T + dKg W^T)
-//   bwd_contrib  dq, dk, dkappa (or dbeta), dg from dN, dM and the elementwise factors
+//   chunk_bwd    (kdn_bwd.h, 512 threads) per chunk: dQg = dO h^T, dW = -d delta h^T, dKf = delta dh^T,
+//                dM = dO delta^T, g_last terms; dV = (I+N)^-T d delta, dKg = (I+N)^-T dW,
+//                dN = -(dV U^T + dKg W^T); dq, dk, dkappa (or dbeta), dg from dN, dM and the
+//                elementwise factors
+//   *_exact      the chunks the forward flagged: the same backward by per-block anchors and scalar
+//                substitution (the products above come from chunk_bwd through HBM)
 //
 // g is kept in the base-2 units of g_cumsum, so e^{g_c - g_s} = exp2(G_c - G_s).
 // Decay factors (c >= s) are split at the start a of the row block (16 tokens):
@@ -333,100 +336,6 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
     if (flags[lin] == 0) continue;
     __syncthreads();  // LDS of the previous chunk is dead
     intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, lin % NT, lin / NT);
-  }
-}
-
-// ===========================================================================
-// Backward: products with the chunk's entry state h and exit-state gradient dh.
-// ===========================================================================
-template <int K, int V, typename TDO>
-__global__ __launch_bounds__(256) void mem_bwd_hgrad_kernel(
-    const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
-    const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ gc, int T, int H, int NT,
-    float* __restrict__ dQg, float* __restrict__ dW, float* __restrict__ dKf, float* __restrict__ dMg,
-    float* __restrict__ dgl) {
-  constexpr int VP = V + 4;
-  __shared__ __attribute__((aligned(16))) float sH[K * VP], sX[C * VP], sY[C * VP];
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
-  const int t0 = n * C, L = min(C, T - t0);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const float* hn = hbuf + ((int64_t)bh * NT + n) * K * V;
-  const float* dhn = dhbuf + ((int64_t)bh * NT + n) * K * V;
-  // phase 1: sH = h, sX = dO, sY = d delta
-  stage_f32<K, V, VP>(hn, V, K, sH);
-  if constexpr (sizeof(TDO) == 2)
-    stage_bf16<C, V, VP>(reinterpret_cast<const bf16_t*>(dO) + bthk(b, t0, h, 0, T, H, V), (int64_t)H * V, L, sX);
-  else
-    stage_f32<C, V, VP>(reinterpret_cast<const float*>(dO) + bthk(b, t0, h, 0, T, H, V), (int64_t)H * V, L, sX);
-  stage_f32<C, V, VP>(dDl + bht(bh, t0, T, V), V, L, sY);
-  __syncthreads();
-  constexpr int NTL = (C / 16) * (K / 16);
-  for (int tile = w; tile < 2 * NTL; tile += 4) {
-    const bool second = tile >= NTL;
-    const int tt = second ? tile - NTL : tile;
-    const int cb = tt / (K / 16), ib = tt % (K / 16);
-    const float* sA_ = second ? sY : sX;
-    f32x4 acc = zero4();
-    const int cA = 16 * cb + (lane & 15), iB = 16 * ib + (lane & 15);
-#pragma unroll 8
-    for (int st = 0; st < V / 4; ++st) {
-      const int vv = 4 * st + (lane >> 4);
-      acc = mfma4(sA_[cA * VP + vv], sH[iB * VP + vv], acc);
-    }
-    float* dst = second ? dW : dQg;
-    const float sg = second ? -1.f : 1.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = 16 * cb + 4 * (lane >> 4) + j;
-      if (c < L) dst[bht(bh, t0 + c, T, K) + iB] = sg * acc[j];
-    }
-  }
-  __syncthreads();
-  // phase 2: sH = dh, sY = delta (sX keeps dO)
-  stage_f32<K, V, VP>(dhn, V, K, sH);
-  stage_f32<C, V, VP>(Dl + bht(bh, t0, T, V), V, L, sY);
-  __syncthreads();
-  // dKf = delta dh^T  (C x K)
-  for (int tile = w; tile < NTL; tile += 4) {
-    const int cb = tile / (K / 16), ib = tile % (K / 16);
-    f32x4 acc = zero4();
-    const int cA = 16 * cb + (lane & 15), iB = 16 * ib + (lane & 15);
-#pragma unroll 8
-    for (int st = 0; st < V / 4; ++st) {
-      const int vv = 4 * st + (lane >> 4);
-      acc = mfma4(sY[cA * VP + vv], sH[iB * VP + vv], acc);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = 16 * cb + 4 * (lane >> 4) + j;
-      if (c < L) dKf[bht(bh, t0 + c, T, K) + iB] = acc[j];
-    }
-  }
-  // dM = dO delta^T (lower incl. diagonal), zeros above
-  float* dMn = dMg + ((int64_t)bh * NT + n) * C * C;
-  for (int tile = w; tile < 16; tile += 4) {
-    const int I = tile >> 2, J = tile & 3;
-    f32x4 acc = zero4();
-    if (J <= I) {
-      const int cA = 16 * I + (lane & 15), sB = 16 * J + (lane & 15);
-#pragma unroll 8
-      for (int st = 0; st < V / 4; ++st) {
-        const int vv = 4 * st + (lane >> 4);
-        acc = mfma4(sX[cA * VP + vv], sY[sB * VP + vv], acc);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = 16 * I + 4 * (lane >> 4) + j, s = 16 * J + (lane & 15);
-      dMn[c * C + s] = (s <= c) ? acc[j] : 0.f;
-    }
-  }
-  // g_last term: e^{g_last,i} sum_v h[i][v] dh[i][v]
-  if (tid < K) {
-    const int i = tid;
-    float sacc = 0.f;
-    for (int vv = 0; vv < V; ++vv) sacc += hn[(int64_t)i * V + vv] * sH[i * VP + vv];
-    dgl[((int64_t)bh * NT + n) * K + i] = sacc * exp2f(gc[bthk(b, t0 + L - 1, h, i, T, H, K)]);
   }
 }
 

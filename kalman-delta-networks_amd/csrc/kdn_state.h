@@ -385,7 +385,7 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
   auto stage_K = [&]() {
 #pragma unroll
     for (int u = 0; u < UN; ++u) put_unit(sK, unit<C>(tid + NTHR * u).off, rK[u][0], rK[u][1], rK[u][2], rK[u][3]);
-    if (tid < K) sE[tid] = exp2f(rE);
+    if (tid < K) sE[tid] = fexp2(rE);
   };
 
   // the state entering the group: h0 (or 0) for the first group, the combined group-start state for
@@ -880,7 +880,7 @@ __global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void 
       if constexpr (!HW) put_unit(sQ, off, rQ[u][0], rQ[u][1], rQ[u][2], rQ[u][3]);
       put_unit(sWt, off, rWt[u][0], rWt[u][1], rWt[u][2], rWt[u][3]);
     }
-    if (tid < K) sE[tid] = exp2f(rE);
+    if (tid < K) sE[tid] = fexp2(rE);
   };
 
   // the cotangent leaving the group: dht (or 0) for the last group, the combined one for an earlier
