@@ -192,14 +192,20 @@ int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
 /* Backward: replaces _chunk_kda_bwd_precum (iso_kdn_chunk.py:2089-2187) and
  * _DiagKdnMemoryFunction.backward (diag_kdn_chunk.py:3258-3312).  dq, dk, dv bf16; dkappa
  * [B,T,H,K] f32 (diag) or dbeta [B,T,H] f32 (iso); dg [B,T,H,K] f32 in natural-log coordinates,
- * not reverse-summed.  d_final_state / d_initial_state nullable.  `stages`: bit 0 reverse state
- * pass, bit 1 state-gradient products, bit 2 transposed solves, bit 3 q/k/kappa/gate gradients
- * (-1 = all, in this order). */
+ * not reverse-summed.  d_final_state / d_initial_state nullable.
+ * q_rstd / k_rstd [B,T,H] f32 (both or neither): the in-op L2 norm of _chunk_kda_precumsum_paired
+ * (iso_kdn_chunk.py:2203-2204, 2229-2230).  Given, q and k are still the normalised bf16 operands
+ * y = x rstd (kdn_l2norm_fwd's outputs, whose rstd these are), and dq, dk are returned for the raw
+ * inputs x: the norm's backward dx = rstd (dy - y (y . dy)) is applied to the fp32 dy in the kernel
+ * (kdn_l2norm_bwd recomputes y from x instead; the two agree to bf16 rounding).
+ * `stages`: bit 0 reverse state pass, bit 1 the chunk-parallel backward, bits 2 and 3 the exact
+ * path's solves and gradients for the chunks outside the factored range (-1 = all, in this order). */
 int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const float* g_cumsum,
                 int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
-                float* dg, float* d_initial_state, int stages, hipStream_t stream);
+                float* dg, float* d_initial_state, const float* q_rstd, const float* k_rstd, int stages,
+                hipStream_t stream);
 /* One token of the memory recurrence with a carried state (decode).  The reference has no step
  * kernel (it refuses caching for KDN layers, model.py:104,184); this is the tokenwise recurrence
  * of iso_kdn_naive.py:308-332 / diag_kdn_naive.py:479-500 on the scan's state layout:

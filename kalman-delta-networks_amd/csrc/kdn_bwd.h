@@ -91,10 +91,10 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
     const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
     const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
-    const float* __restrict__ gc, int T, int H, int NT, float scale, bf16_t* __restrict__ dv,
-    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
-    float* __restrict__ dg, float* __restrict__ xQg, float* __restrict__ xW, float* __restrict__ xKf,
-    float* __restrict__ xM, float* __restrict__ xgl) {
+    const float* __restrict__ gc, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, int T, int H,
+    int NT, float scale, bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk,
+    float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, float* __restrict__ xQg,
+    float* __restrict__ xW, float* __restrict__ xKf, float* __restrict__ xM, float* __restrict__ xgl) {
   constexpr bool DO_BF16 = sizeof(TDO) == 2;
   constexpr int NW = 8;
   constexpr int VB = V / 32;        // k-blocks of the V contraction
@@ -114,6 +114,7 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
   __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
   __shared__ float sDgl[K];
   __shared__ float sBeta[NW * C];
+  __shared__ float sDot[2][NW][C];  // in-op L2 norm: per-wave partial row dots y . dy of q and k
   bf16_t* sO = reinterpret_cast<bf16_t*>(smem);  // phase 1: dO, delta, d delta row fragments
   bf16_t* sD = sO + 4 * RB;
   bf16_t* sdD = sD + 4 * RB;
@@ -460,10 +461,16 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
   __syncthreads();
 
   // ================================ gradient phase ================================
+  // With the in-op L2 norm (q_rstd, k_rstd [B,T,H] given), dq and dk are returned for the raw inputs
+  // x = y / rstd of the normalised q, k (= y) this kernel takes: dx = rstd (dy - y (y . dy)), the row
+  // dot summed over the waves.  y is the bf16 normalised operand the forward used.
+  const bool qk_norm = q_rstd != nullptr;
   float bpart[4] = {0.f, 0.f, 0.f, 0.f};  // iso: dbeta partials of rows 16 tl + r16
+  float dqs[4][4], dks[4][4];             // in-op norm: dy of q, k (rows 16 tl + r16, channels i0 ..)
+  u32x2 yq2[4], yk2[4];                   // ... and y (bf16 pairs)
+  const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
+  const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
   if (own_k) {
-    const int64_t in_row0 = ((int64_t)b * T + t0) * H + h;
-    const uint32_t rows_in = (uint32_t)((L - 1) * H + 1);
     const bufrsrc rG = make_buf(gc + in_row0 * K, rows_in * K * 4);
     const bufrsrc rk = make_buf(k + in_row0 * K, rows_in * K * 2);
     const bufrsrc rq = make_buf(q + in_row0 * K, rows_in * K * 2);
@@ -561,6 +568,8 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
                             __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
       const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
                             __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
+      yk2[tl] = kq4[tl];
+      yq2[tl] = qq4[tl];
       const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
       const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
       const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
@@ -589,12 +598,20 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
         __builtin_amdgcn_raw_buffer_store_b128(
             u32x4{__float_as_uint(dav[0]), __float_as_uint(dav[1]), __float_as_uint(dav[2]), __float_as_uint(dav[3])},
             rdkap, o * 4, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16), (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
-          rdq, o * 2, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b64(
-          u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16), (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
-          rdk, o * 2, 0, 0);
+      if (qk_norm) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dqs[tl][j] = dqv[j];
+          dks[tl][j] = dkv[j];
+        }
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)f2bf(dqv[0]) | ((uint32_t)f2bf(dqv[1]) << 16),
+                                                    (uint32_t)f2bf(dqv[2]) | ((uint32_t)f2bf(dqv[3]) << 16)},
+                                              rdq, o * 2, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)f2bf(dkv[0]) | ((uint32_t)f2bf(dkv[1]) << 16),
+                                                    (uint32_t)f2bf(dkv[2]) | ((uint32_t)f2bf(dkv[3]) << 16)},
+                                              rdk, o * 2, 0, 0);
+      }
       if ((int)c == L - 1) {
         dg_last = float4{dgv[0], dgv[1], dgv[2], dgv[3]};
         has_last = true;
@@ -616,22 +633,79 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
                                              ((uint32_t)((L - 1) * H) * K + i0) * 4, 0, 0);
     }
   }
-  if (ISO) {
-    if (own_k) {
+  if (!ISO && !qk_norm) return;
+  auto unpack4 = [](u32x2 v, float* f) {
+    f[0] = __uint_as_float(v.x << 16), f[1] = __uint_as_float(v.x & 0xffff0000u);
+    f[2] = __uint_as_float(v.y << 16), f[3] = __uint_as_float(v.y & 0xffff0000u);
+  };
+  if (own_k) {  // per-wave partials over this wave's 16 channels of rows 16 tl + r16
 #pragma unroll
-      for (int tl = 0; tl < 4; ++tl) {
-        float v = bpart[tl];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (g4 == 0) sBeta[w * C + 16 * tl + r16] = v;
+    for (int tl = 0; tl < 4; ++tl) {
+      float v = bpart[tl], pq = 0.f, pk = 0.f;
+      if (qk_norm) {
+        float yq[4], yk[4];
+        unpack4(yq2[tl], yq);
+        unpack4(yk2[tl], yk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pq += yq[j] * dqs[tl][j];
+          pk += yk[j] * dks[tl][j];
+        }
+      }
+#pragma unroll
+      for (int m = 16; m < 64; m <<= 1) {
+        v += __shfl_xor(v, m, 64);
+        pq += __shfl_xor(pq, m, 64);
+        pk += __shfl_xor(pk, m, 64);
+      }
+      if (g4 == 0) {
+        sBeta[w * C + 16 * tl + r16] = v;
+        sDot[0][w][16 * tl + r16] = pq;
+        sDot[1][w][16 * tl + r16] = pk;
       }
     }
-    __syncthreads();
-    if (tid < L) {
-      float s = 0.f;
+  }
+  __syncthreads();
+  if (ISO && tid < L) {
+    float s = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < NIT; ++ww) s += sBeta[ww * C + tid];
-      dbeta[((int64_t)b * T + t0 + tid) * H + h] = s;
+    for (int ww = 0; ww < NIT; ++ww) s += sBeta[ww * C + tid];
+    dbeta[((int64_t)b * T + t0 + tid) * H + h] = s;
+  }
+  if (!qk_norm) return;
+  if (tid < 2 * C) {  // the row dots: sum of the waves' partials, into slot 0
+    const int tq = tid >> 6, c = tid & 63;
+    float dsum = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NIT; ++ww) dsum += sDot[tq][ww][c];
+    sDot[tq][NW - 1][c] = dsum;  // each (tensor, row) is read and overwritten by this one thread
+  }
+  __syncthreads();
+  if (own_k) {  // dx = rstd (dy - y (y . dy)) for the raw q, k
+    const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
+    const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
+    const bufrsrc rrq = make_buf(q_rstd + in_row0, rows_in * 4);
+    const bufrsrc rrk = make_buf(k_rstd + in_row0, rows_in * 4);
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      const int c = 16 * tl + r16;
+      const float dotq = sDot[0][NW - 1][c], dotk = sDot[1][NW - 1][c];
+      const float rq_ = buf_ld(rrq, (uint32_t)(c * H) * 4), rk_ = buf_ld(rrk, (uint32_t)(c * H) * 4);
+      float yq[4], yk[4], xq[4], xk[4];
+      unpack4(yq2[tl], yq);
+      unpack4(yk2[tl], yk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xq[j] = rq_ * (dqs[tl][j] - yq[j] * dotq);
+        xk[j] = rk_ * (dks[tl][j] - yk[j] * dotk);
+      }
+      const uint32_t o = (uint32_t)(c * H) * K + i0;
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)f2bf(xq[0]) | ((uint32_t)f2bf(xq[1]) << 16),
+                                                  (uint32_t)f2bf(xq[2]) | ((uint32_t)f2bf(xq[3]) << 16)},
+                                            rdq, o * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{(uint32_t)f2bf(xk[0]) | ((uint32_t)f2bf(xk[1]) << 16),
+                                                  (uint32_t)f2bf(xk[2]) | ((uint32_t)f2bf(xk[3]) << 16)},
+                                            rdk, o * 2, 0, 0);
     }
   }
 }

@@ -640,6 +640,42 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
   }
 }
 
+// The in-op L2 norm's backward for the rows of the flagged chunks (whose dq, dk the exact kernel
+// above wrote for the normalised operands y = q, k): dx = rstd (dy - y (y . dy)), in place.
+// One wave per row (K / 64 elements per lane); a row is read whole before it is written.
+template <int K>
+__global__ __launch_bounds__(256) void l2norm_bwd_flagged_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ q_rstd,
+    const float* __restrict__ k_rstd, int T, int H, int NT, int NB, const int* __restrict__ flags,
+    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk) {
+  constexpr int PL = K / 64;
+  if (!any_flagged(flags, NB)) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
+    if (flags[lin] == 0) continue;
+    const int n = lin % NT, bh = lin / NT, b = bh / H, h = bh % H;
+    const int t0 = n * C, L = min(C, T - t0);
+    for (int r = w; r < 2 * L; r += 4) {
+      const bool isq = r < L;
+      const int c = isq ? r : r - L;
+      const int64_t row = ((int64_t)b * T + t0 + c) * H + h;
+      const bf16_t* x = isq ? q : k;
+      bf16_t* d = isq ? dq : dk;
+      const float rs = (isq ? q_rstd : k_rstd)[row];
+      float y[PL], g[PL], dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < PL; ++j) {
+        y[j] = bf2f(x[row * K + lane + 64 * j]);
+        g[j] = bf2f(d[row * K + lane + 64 * j]);
+        dot += y[j] * g[j];
+      }
+      dot = wave_sum(dot);
+#pragma unroll
+      for (int j = 0; j < PL; ++j) d[row * K + lane + 64 * j] = f2bf(rs * (g[j] - y[j] * dot));
+    }
+  }
+}
+
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 // Chunk groups of the serial state passes (kdn_state.h, GroupPlan).  With few B*H*V/64 workgroups a
@@ -819,8 +855,8 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
 template <int K, int V, typename TDO>
 int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const float* gc, int B, int T, int H,
                  float scale, const TDO* dO, const float* dht, const float* saved, float* work, bf16_t* dq,
-                 bf16_t* dk, float* dkap, float* dbeta, bf16_t* dv, float* dg, float* dh0, int stages,
-                 hipStream_t stream) {
+                 bf16_t* dk, float* dkap, float* dbeta, bf16_t* dv, float* dg, float* dh0, const float* q_rstd,
+                 const float* k_rstd, int stages, hipStream_t stream) {
   const int NT = cdiv(T, C);
   MemLayout lay(B, T, H, K, V);
   BwdLayout bl(B, T, H, K, V);
@@ -844,12 +880,12 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   if (stages & 2) {  // every chunk's products with h / dh; the solves and gradients of the unflagged ones
     if (iso)
       hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, true, TDO>), gchunk, dim3(512), 0, stream, hb, dh, D, dD, dO,
-                         A, U, W, flags, q, k, kap, gc, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf,
-                         dM, dgl);
+                         A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg,
+                         dQg, dW, dKf, dM, dgl);
     else
       hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, false, TDO>), gchunk, dim3(512), 0, stream, hb, dh, D, dD,
-                         dO, A, U, W, flags, q, k, kap, gc, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf,
-                         dM, dgl);
+                         dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, scale, dv, dq, dk, dkap, dbeta,
+                         dg, dQg, dW, dKf, dM, dgl);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 4) {  // the chunks left to the exact path: transposed solves into dv, dKg, dN
@@ -871,6 +907,11 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc,
                          dN, dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
     KDN_CHECK_LAUNCH();
+    if (q_rstd) {  // the in-op norm's backward for the flagged chunks' rows
+      hipLaunchKernelGGL((l2norm_bwd_flagged_kernel<K>), dim3(gx), dim3(256), 0, stream, q, k, q_rstd, k_rstd, T, H,
+                         NT, NB, flags, dq, dk);
+      KDN_CHECK_LAUNCH();
+    }
   }
   return 0;
 }
@@ -917,12 +958,14 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
                 int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, uint16_t* dq, uint16_t* dk, float* dkappa, float* dbeta, uint16_t* dv,
-                float* dg, float* d_initial_state, int stages, hipStream_t stream) {
+                float* dg, float* d_initial_state, const float* q_rstd, const float* k_rstd, int stages,
+                hipStream_t stream) {
   if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
   if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
   if (saved_bytes < kdn_mem_saved_size(B, T, H, K, V)) return KDN_ERR_ARG;
   if (workspace_bytes < kdn_mem_bwd_workspace_size(B, T, H, K, V)) return KDN_ERR_ARG;
   if (iso ? dbeta == nullptr : dkappa == nullptr) return KDN_ERR_ARG;
+  if ((q_rstd == nullptr) != (k_rstd == nullptr)) return KDN_ERR_ARG;
   const float* sv = (const float*)saved;
   float* wk = (float*)workspace;
 #define KDN_MEM_BWD(KK, VV)                                                                                          \
@@ -930,10 +973,10 @@ int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
     if (do_bf16)                                                                                                     \
       return mem_bwd_impl<KK, VV, bf16_t>(q, k, kappa_or_beta, iso, g_cumsum, B, T, H, scale, (const bf16_t*)d_o,   \
                                           d_final_state, sv, wk, dq, dk, dkappa, dbeta, dv, dg, d_initial_state,     \
-                                          stages, stream);                                                                   \
+                                          q_rstd, k_rstd, stages, stream);                                           \
     return mem_bwd_impl<KK, VV, float>(q, k, kappa_or_beta, iso, g_cumsum, B, T, H, scale, (const float*)d_o,       \
                                        d_final_state, sv, wk, dq, dk, dkappa, dbeta, dv, dg, d_initial_state,        \
-                                       stages, stream);                                                                      \
+                                       q_rstd, k_rstd, stages, stream);                                              \
   } while (0)
   if (K == 128 && V == 128) KDN_MEM_BWD(128, 128);
   if (K == 64 && V == 64) KDN_MEM_BWD(64, 64);

@@ -42,7 +42,7 @@ _SIGS = {
     "kdn_mem_saved_size": "iiiii",
     "kdn_mem_bwd_workspace_size": "iiiii",
     "kdn_mem_fwd": "pppippiiiiifppzppiis",
-    "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppis",
+    "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppppis",
     "kdn_mem_step": "pppipipiiiifppis",
     "kdn_kalman_step": "pppipppppppiiiiiffppis",
     "kdn_gemv": "pilppiiiipls",

@@ -42,9 +42,12 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
 
 
 def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do, *, d_final_state=None,
-            need_initial_state_grad=False):
+            need_initial_state_grad=False, q_rstd=None, k_rstd=None):
     """Returns (dq bf16, dk bf16, dv bf16, dkappa f32 [B,T,H,K] or dbeta f32 [B,T,H],
-    dg f32 natural-log not reverse-summed, d_initial_state or None)."""
+    dg f32 natural-log not reverse-summed, d_initial_state or None).
+
+    With ``q_rstd`` / ``k_rstd`` [B,T,H] (the in-op L2 norm) q and k are the raw bf16 inputs whose
+    normalised values the forward took, and dq, dk are the gradients of the raw inputs."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device
@@ -65,5 +68,5 @@ def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do
                   B, T, H, K, V, float(scale), _lib.ptr(do), _lib.is_bf16(do), _lib.ptr(dht), _lib.ptr(saved),
                   saved.numel(), _lib.ptr(ws), ws.numel(), _lib.ptr(dq), _lib.ptr(dk),
                   None if iso else _lib.ptr(dkap), _lib.ptr(dkap) if iso else None, _lib.ptr(dv), _lib.ptr(dg),
-                  _lib.ptr(dh0), bit, stream, tag=tag)
+                  _lib.ptr(dh0), _lib.ptr(q_rstd), _lib.ptr(k_rstd), bit, stream, tag=tag)
     return dq, dk, dv, dkap, dg, dh0

@@ -366,15 +366,20 @@ def _chunk_kda_fwd_precum(q, k, v, g_cumsum, beta, scale, *, initial_state=None,
 
 
 def _chunk_kda_bwd_precum(q, k, v, g_cumsum, beta, saved, scale, do, *, d_final_state=None,
-                          need_initial_state_grad=False):
-    """Memory scan backward (reference :2089-2187): natural-log dg, no reverse cumsum."""
+                          need_initial_state_grad=False, q_rstd=None, k_rstd=None):
+    """Memory scan backward (reference :2089-2187): natural-log dg, no reverse cumsum.  With q_rstd /
+    k_rstd (the in-op L2 norm's, q and k still the normalised operands) dq, dk are returned for the
+    raw inputs, the norm's backward included."""
     return _memscan.mem_bwd(q, k, beta, True, v, g_cumsum, saved, scale, do, d_final_state=d_final_state,
-                            need_initial_state_grad=need_initial_state_grad)
+                            need_initial_state_grad=need_initial_state_grad, q_rstd=q_rstd, k_rstd=k_rstd)
 
 
 class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
     """Reference iso_kdn_chunk.py:2190-2238: L2-normalise q, k inside; memory scan; VJPs.  With an
-    initial state h0 [B,H,K,V] and / or the final state requested, their gradients flow too."""
+    initial state h0 [B,H,K,V] and / or the final state requested, their gradients flow too.
+
+    For bf16 q, k the norm's backward runs inside the scan's backward kernel (kdn_mem_bwd with the
+    forward's rstd, y = the normalised bf16 operands); fp32 q, k keep the separate kdn_l2norm_bwd."""
 
     @staticmethod
     def forward(ctx, q, k, v, g_cumsum, beta, scale, initial_state=None, output_final_state=False):
@@ -386,7 +391,11 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
             o, saved, ht = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
                                                  initial_state=initial_state, output_final_state=output_final_state,
                                                  out_dtype=q.dtype if q.dtype == torch.float32 else torch.bfloat16)
-        ctx.save_for_backward(q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved)
+        ctx.fused_norm = q.dtype == torch.bfloat16
+        if ctx.fused_norm:
+            ctx.save_for_backward(qn, q_rstd, kn, k_rstd, vb, g_cumsum, beta, saved)
+        else:
+            ctx.save_for_backward(q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved)
         ctx.scale = scale
         ctx.h0_dtype = initial_state.dtype if initial_state is not None else None
         o = o if o.dtype == q.dtype else o.to(q.dtype)
@@ -394,13 +403,19 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dht=None):
-        q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved = ctx.saved_tensors
         need_h0 = ctx.h0_dtype is not None and ctx.needs_input_grad[6]
-        with torch.cuda.device(q.device):
-            dqn, dkn, dv, db, dg, dh0 = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do,
-                                                              d_final_state=dht, need_initial_state_grad=need_h0)
-            dq = _l2norm_bwd(q, q_rstd, dqn)
-            dk = _l2norm_bwd(k, k_rstd, dkn)
+        with torch.cuda.device(do.device):
+            if ctx.fused_norm:
+                qn, q_rstd, kn, k_rstd, vb, g_cumsum, beta, saved = ctx.saved_tensors
+                dq, dk, dv, db, dg, dh0 = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do,
+                                                                d_final_state=dht, need_initial_state_grad=need_h0,
+                                                                q_rstd=q_rstd, k_rstd=k_rstd)
+            else:
+                q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved = ctx.saved_tensors
+                dqn, dkn, dv, db, dg, dh0 = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do,
+                                                                  d_final_state=dht, need_initial_state_grad=need_h0)
+                dq = _l2norm_bwd(q, q_rstd, dqn)
+                dk = _l2norm_bwd(k, k_rstd, dkn)
         dh0 = dh0.to(ctx.h0_dtype) if dh0 is not None else None
         return dq, dk, dv, dg, db, None, dh0, None
 
