@@ -49,9 +49,11 @@ def mfma_peak(tag: str) -> float:
     return FP32_PEAK_TFLOPS if MFMA_PATH.get(tag, "f32") == "f32" else BF16_PEAK_TFLOPS / 3.0
 
 
-def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
+def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int, infer: bool = False):
     """Algorithmic HBM bytes and FLOPs per launch of each kernel (inputs read once, outputs
-    written once, no recompute).  N = B*T*H token-heads; per-token-head figures times N."""
+    written once, no recompute).  N = B*T*H token-heads; per-token-head figures times N.  With
+    ``infer`` (no backward follows) the forward kernels skip what only the backward reads: A^T, and
+    h and delta of the fused state pass."""
     N = B * T * H
     kap_in = 4 * K if variant == "diag" else 4           # kappa fp32 [K] or beta fp32
     dkap_out = 4 * K if variant == "diag" else 4
@@ -80,6 +82,11 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int):
                           + 2 * V + 2 * 2 * K + dkap_out + 4 * K,
                           2 * (3 * K * V + C * V / 2) + 2 * (C * (V + K) / 2 + C * (V + K) / 2) + 2 * 2 * (C * K)),
     }
+    if infer:
+        b, f = per["mem_intra_fwd"]
+        per["mem_intra_fwd"] = (b - mm, f)
+        b, f = per["mem_state_readout_fwd"]
+        per["mem_state_readout_fwd"] = (b - h_b - 4 * V, f)
     return {k: (b * N, f * N) for k, (b, f) in per.items()}
 
 
@@ -503,13 +510,13 @@ def run_config3(steps: int, warmup: int, B: int = 1, T: int = 32768, H: int = 18
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
-    fwd_tags = ("diag_front_norm_fwd", "diag_front_fwd", "mem_intra_fwd", "mem_state_fwd", "mem_readout_fwd")
-    counts = kernel_counts("diag", B, T, H, K, K)
+    fwd_tags = ("diag_front_norm_fwd", "diag_front_fwd", "mem_intra_fwd", "mem_state_readout_fwd")
+    counts = kernel_counts("diag", B, T, H, K, K, infer=True)
     counts.update(frontend_counts("diag", B, T, H, K))
     kernels = {}
     for tag in fwd_tags:
         nbytes, _fl = counts[tag]
-        if tag == "mem_readout_fwd":  # the long-context output is bf16 (v's dtype), not the fp32 of kernel_counts
+        if tag == "mem_state_readout_fwd":  # the long-context output is bf16 (v's dtype), not the fp32 of kernel_counts
             nbytes -= 2 * K * B * T * H
         t = timer.mean_ms(tag) * 1e-3
         gbs = nbytes / t / 1e9

@@ -184,7 +184,10 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
  * initial_memory / output_final_state, iso_kdn_naive.py:376-440).  `saved` receives the
  * intermediates the backward consumes (kdn_mem_saved_size bytes).  `stages` selects kernels
  * (bit 0 intra-chunk WY build, bit 1 serial state pass, bit 2 readout o; -1 = all) so that a
- * caller can launch and time them one at a time; the stages must run in this order. */
+ * caller can launch and time them one at a time; the stages must run in this order.  Bits 1 and 2
+ * in one call run the state pass with the readout fused.  Bit 3 (with stages >= 0) declares that
+ * no backward follows (inference, as under torch.no_grad): the intermediates only the backward
+ * reads are then not written, and `saved` is scratch for this call alone. */
 int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
                 const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
                 void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, int stages,

@@ -142,7 +142,7 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
 
   // ---- 5. save A^T ([s][c], the orientation the backward contracts over) for the backward
   {
-    const bufrsrc rA = make_buf(An, C * C * 4);
+    const bufrsrc rA = make_buf(An, An ? C * C * 4 : 0u);  // no backward follows: nothing to save
 #pragma unroll
     for (int u = 0; u < C * C / 4 / 256; ++u) {
       const int e = 4 * (tid + 256 * u), sr = e / C, c0 = e % C;  // A^T[sr][c0 .. c0+3] = A[c0 + j][sr]
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
   const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
   float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
-  float* An = Ag + ((int64_t)bh * NT + n) * C * C;
+  float* An = Ag ? Ag + ((int64_t)bh * NT + n) * C * C : nullptr;
 
   // ---- 0. the chunk's decay span max_i (G_0 - G_{L-1})_i, from rows 0 and L-1 alone, before any
   // other load or store: a chunk past the single anchor's range goes to the block-anchor kernel
@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
   const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
   float* Mn = Mg + ((int64_t)bh * NT + n) * C * C;
-  float* An = Ag + ((int64_t)bh * NT + n) * C * C;
+  float* An = Ag ? Ag + ((int64_t)bh * NT + n) * C * C : nullptr;
 
   // ---- 0. block anchors m_J = (G_{16J} + G_{16J+15}) / 2 per channel (rows clamped to the chunk)
   // and the block spans; a chunk with a span past kBlockSpanMax stays for the exact kernel

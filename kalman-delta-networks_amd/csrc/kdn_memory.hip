@@ -794,38 +794,74 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg, *M = saved + lay.M,
         *A = saved + lay.A, *hb = saved + lay.h, *D = saved + lay.D;
   int* flags = reinterpret_cast<int*>(saved + lay.flags);
+  // bit 3 (stages >= 0): no backward follows, so A^T and, where the readout is fused, h and delta
+  // are not written
+  const bool infer = stages >= 0 && (stages & 8) != 0;
+  float* Asave = infer ? nullptr : A;
   dim3 gchunk(NT, B * H);
   if (stages & 1) {
     const int NB = B * H * NT, gx = min(NB, 512);
     if (iso) {
       hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T,
-                         H, NT, scale, U, W, Kf, Qg, M, A, flags);
+                         H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
       hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap,
-                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
+                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
       hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
-                         T, H, NT, NB, scale, U, W, Kf, Qg, M, A, flags);
+                         T, H, NT, NB, scale, U, W, Kf, Qg, M, Asave, flags);
     } else {
       hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc,
-                         T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
+                         T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
       hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap,
-                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, A, flags);
+                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
       hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
-                         T, H, NT, NB, scale, U, W, Kf, Qg, M, A, flags);
+                         T, H, NT, NB, scale, U, W, Kf, Qg, M, Asave, flags);
     }
     KDN_CHECK_LAUNCH();
   }
-  // One chunk group and both stages asked for: the state pass does the readout itself (helper waves
-  // stage Qg and M; see state_fwd_kernel), so the chunk-parallel readout is not launched.
-  const bool fused_readout = (stages & 6) == 6 && lay.gc.NG == 1;
-  if (fused_readout) {
-    const dim3 grid(B * H * (V / kdn_state::state_cols(V))), bs(2 * kdn_state::state_threads(V));
-    const kdn_state::GroupPlan P{1, NT, 0, nullptr, nullptr};
+  auto launch_ro = [&](dim3 grid, const kdn_state::GroupPlan& P, float* hstore, float* dstore) {
+    const dim3 bs(2 * kdn_state::state_threads(V));
     if (o_bf16)
       hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t, true>), grid, bs, 0, stream, U, W, Kf, gc, h0, T,
-                         H, NT, B * H, hb, D, ht, P, Qg, M, (bf16_t*)o);
+                         H, NT, B * H, hstore, dstore, ht, P, Qg, M, (bf16_t*)o);
     else
       hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, true>), grid, bs, 0, stream, U, W, Kf, gc, h0, T,
-                         H, NT, B * H, hb, D, ht, P, Qg, M, (float*)o);
+                         H, NT, B * H, hstore, dstore, ht, P, Qg, M, (float*)o);
+  };
+  auto launch_readout = [&](int NR) {  // chunk-parallel readout O = Qg h + M delta of the first NR chunks
+    const int NCH = NR * B * H;        // chunk-heads; with two V halves the grid is padded to pairs of 8
+    const dim3 gr(V / 64 == 2 ? 16 * cdiv(NCH, 8) : NCH);
+    if (o_bf16)
+      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, bf16_t>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
+                         NR, B * H, (bf16_t*)o);
+    else
+      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, float>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
+                         NR, B * H, (float*)o);
+  };
+  if ((stages & 6) == 6) {  // state pass with the readout fused
+    const GroupCount gcnt = lay.gc;
+    if (gcnt.NG == 1) {
+      launch_ro(dim3(B * H * (V / kdn_state::state_cols(V))), kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr},
+                infer ? nullptr : hb, infer ? nullptr : D);
+      KDN_CHECK_LAUNCH();
+      return 0;
+    }
+    // two-level: pass A (first group, which stores its h and delta, and the middle groups' maps),
+    // the combine, pass C with the readout fused, then the first group's readout
+    constexpr int NV = V / kdn_state::state_cols(V), NS = NV + K / kdn_state::state_cols(V);
+    float* grp = saved + lay.grp;
+    kdn_state::GroupPlan P{gcnt.NG, gcnt.m, 0, grp, grp + (int64_t)B * H * gcnt.NG * K * V};
+    hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), dim3(B * H * (gcnt.NG - 1) * NS),
+                       dim3(kdn_state::state_threads(V)), 0, stream, U, W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht, P);
+    KDN_CHECK_LAUNCH();
+    if (gcnt.NG > 2) {
+      hipLaunchKernelGGL((kdn_state::state_combine_kernel<K, V>), dim3(B * H * NV), dim3(kdn_state::state_threads(V)),
+                         0, stream, P, B * H, 1, gcnt.NG - 2, 1);
+      KDN_CHECK_LAUNCH();
+    }
+    P.pass = 1;
+    launch_ro(dim3(B * H * (gcnt.NG - 1) * NV), P, infer ? nullptr : hb, infer ? nullptr : D);
+    KDN_CHECK_LAUNCH();
+    launch_readout(gcnt.m);
     KDN_CHECK_LAUNCH();
     return 0;
   }
@@ -838,15 +874,8 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
                                         });
     if (rc) return rc;
   }
-  if (stages & 4) {  // chunk-parallel readout O = Qg h + M delta
-    const int NCH = NT * B * H;  // chunk-heads; with two V halves the grid is padded to pairs of 8
-    const dim3 gr(V / 64 == 2 ? 16 * cdiv(NCH, 8) : NCH);
-    if (o_bf16)
-      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, bf16_t>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
-                         B * H, (bf16_t*)o);
-    else
-      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, float>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
-                         B * H, (float*)o);
+  if (stages & 4) {  // chunk-parallel readout O = Qg h + M delta of every chunk
+    launch_readout(NT);
     KDN_CHECK_LAUNCH();
   }
   return 0;

@@ -244,7 +244,8 @@ __device__ __forceinline__ bool group_task(const GroupPlan& P, int BH, int& bh, 
 // The readout O = Qg h + M delta is left to readout_kernel: it is off the serial chain, and its
 // operands (Qg, M) would double the chunk operands staged on the chain's critical path.
 // ===========================================================================
-// With RO (one chunk group only) the pass also does the readout O = Qg h + M delta of every chunk.
+// With RO (one chunk group, or pass C of a grouped pass: every workgroup runs a group from its true
+// state) the pass also does the readout O = Qg h + M delta of every chunk it runs.
 // The block gets four readout waves.  In phase 1 of chunk n each state wave publishes the split B
 // fragments of h_n (its state, as it multiplies W with it) and of delta_n to LDS; in phase 2 the
 // readout waves multiply them with the A fragments of their 16 chunk rows of Qg and M (loaded from
@@ -410,7 +411,7 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
   __syncthreads();
   for (int n = n0; n < n1; ++n) {
     const int t0 = n * C, L = min(C, T - t0);
-    if (real) {
+    if (real && hbuf) {  // (no h, delta stores when the readout is fused and no backward follows)
       const float* hb = hbuf + ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
       for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, S[ib]);
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
       for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) D[cb][j] = cU[cb][j] - D[cb][j];
-      if (real) {
+      if (real && Dl) {
         const float* dl = Dl + row_bht(bh, t0, T, V);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
@@ -507,8 +508,9 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
 
 // ===========================================================================
 // Forward readout, chunk-parallel:  O = Qg h + M delta  per chunk, from the state pass's h (the
-// state entering the chunk) and delta.  grid: one workgroup per (chunk, head, 64 columns of V), see
-// below; block 256, LDS 48 KB.
+// state entering the chunk) and delta, for the first NR chunks of every head (NR = NT: all of them;
+// a grouped pass whose later groups read out in pass C: the first group's).  grid: one workgroup per
+// (chunk, head, 64 columns of V), see below; block 256, LDS 48 KB.
 // Computed transposed, O^T = h^T Qg^T + delta^T M^T, so each lane's D tile holds 4 consecutive
 // columns of one chunk row (8- or 16-byte stores).  h^T and delta^T (A operands, contraction over
 // the state row i / the chunk row s) are staged once per workgroup as split fragments in LDS; the
@@ -518,7 +520,7 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
 template <int K, int V, typename TO>
 __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict__ Qg, const float* __restrict__ Mg,
                                                          const float* __restrict__ hbuf, const float* __restrict__ Dl,
-                                                         int T, int H, int NT, int BH, TO* __restrict__ out) {
+                                                         int T, int H, int NT, int NR, int BH, TO* __restrict__ out) {
   constexpr int VC = 64;                 // columns of V per workgroup
   constexpr int KB = K / 32, VT = VC / 16;
   static_assert(V % VC == 0, "V is a multiple of 64");
@@ -529,8 +531,8 @@ __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict
   static_assert(V / VC == 2 || V / VC == 1, "one or two column halves");
   const int lin = blockIdx.x, NH = V / VC;
   const int ch = NH == 2 ? 8 * (lin >> 4) + (lin & 7) : lin, half = NH == 2 ? (lin >> 3) & 1 : 0;
-  if (ch >= NT * BH) return;
-  const int n = ch % NT, bh = ch / NT, v0 = VC * half, b = bh / H, h = bh % H;
+  if (ch >= NR * BH) return;  // the first NR chunks of each head (NR = NT: all)
+  const int n = ch % NR, bh = ch / NR, v0 = VC * half, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   const int64_t chunk = (int64_t)bh * NT + n;

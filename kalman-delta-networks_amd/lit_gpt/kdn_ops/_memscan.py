@@ -9,9 +9,10 @@ import torch
 
 from . import _lib
 
-FWD_STAGES = ((1, "mem_intra_fwd"), (2, "mem_state_fwd"), (4, "mem_readout_fwd"))
-# with one chunk group the state pass also does the readout (one launch for bits 2 and 4)
-FWD_STAGES_FUSED = ((1, "mem_intra_fwd"), (6, "mem_state_readout_fwd"))
+# bits 1 | 2 in one call: the state pass with the readout fused (with chunk groups, fused into the
+# groups that start from their true state; the first group's readout follows in the same call)
+FWD_STAGES = ((1, "mem_intra_fwd"), (6, "mem_state_readout_fwd"))
+NO_BACKWARD = 8  # stage bit: no backward follows, intermediates only the backward reads are not written
 
 
 def state_groups(B: int, T: int, H: int, K: int, V: int) -> int:
@@ -23,9 +24,10 @@ BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_chunk"), (12, "mem_bwd_exact"))
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
-            output_final_state=False, out_dtype=torch.float32):
+            output_final_state=False, out_dtype=torch.float32, need_backward=True):
     """q, k, v bf16 [B,T,H,*]; kappa [B,T,H,K] f32 (diag) or beta [B,T,H] f32 (iso).
-    Returns (o, saved, final_state or None)."""
+    Returns (o, saved, final_state or None); with ``need_backward=False`` saved is not usable by
+    mem_bwd (the intermediates only the backward reads are skipped)."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device
@@ -34,10 +36,11 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
     ht = torch.empty((B, H, K, V), device=dev, dtype=torch.float32) if output_final_state else None
     h0 = initial_state.float().contiguous() if initial_state is not None else None
     stream = _lib.stream_of(q)
-    for bit, tag in (FWD_STAGES_FUSED if state_groups(B, T, H, K, V) == 1 else FWD_STAGES):
+    extra = 0 if need_backward else NO_BACKWARD
+    for bit, tag in FWD_STAGES:
         _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(v),
                   _lib.ptr(g_cumsum), B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(),
-                  _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), bit, stream, tag=tag)
+                  _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), bit | extra, stream, tag=tag)
     return o, saved, ht
 
 

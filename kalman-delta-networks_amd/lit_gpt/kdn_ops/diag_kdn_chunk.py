@@ -493,10 +493,14 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, kappa, v, g_cumsum, scale, initial_state, output_final_state, out_dtype=torch.float32):
+        # no input needs a gradient (inference): the intermediates only the backward reads are skipped
+        need_backward = any(ctx.needs_input_grad)
         with torch.cuda.device(q.device):
             o, saved, ht = _memscan.mem_fwd(q, k, kappa, False, v, g_cumsum, scale, initial_state=initial_state,
-                                            output_final_state=output_final_state, out_dtype=out_dtype)
-        ctx.save_for_backward(q, k, kappa, v, g_cumsum, saved)
+                                            output_final_state=output_final_state, out_dtype=out_dtype,
+                                            need_backward=need_backward)
+        if need_backward:
+            ctx.save_for_backward(q, k, kappa, v, g_cumsum, saved)
         ctx.scale = scale
         ctx.has_h0 = initial_state is not None
         ctx.set_materialize_grads(False)

@@ -359,10 +359,12 @@ def _l2norm_bwd(x, rstd, dy):
 
 
 def _chunk_kda_fwd_precum(q, k, v, g_cumsum, beta, scale, *, initial_state=None, output_final_state=False,
-                          out_dtype=torch.bfloat16):
-    """Memory scan forward on normalised bf16 q, k (reference :2037-2086); kappa = beta k."""
+                          out_dtype=torch.bfloat16, need_backward=True):
+    """Memory scan forward on normalised bf16 q, k (reference :2037-2086); kappa = beta k.  With
+    need_backward=False the returned saved buffer cannot feed _chunk_kda_bwd_precum."""
     return _memscan.mem_fwd(q, k, beta, True, v, g_cumsum, scale, initial_state=initial_state,
-                            output_final_state=output_final_state, out_dtype=out_dtype)
+                            output_final_state=output_final_state, out_dtype=out_dtype,
+                            need_backward=need_backward)
 
 
 def _chunk_kda_bwd_precum(q, k, v, g_cumsum, beta, saved, scale, do, *, d_final_state=None,
@@ -390,7 +392,8 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
             vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
             o, saved, ht = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
                                                  initial_state=initial_state, output_final_state=output_final_state,
-                                                 out_dtype=q.dtype if q.dtype == torch.float32 else torch.bfloat16)
+                                                 out_dtype=q.dtype if q.dtype == torch.float32 else torch.bfloat16,
+                                                 need_backward=any(ctx.needs_input_grad))
         ctx.fused_norm = q.dtype == torch.bfloat16
         if ctx.fused_norm:
             ctx.save_for_backward(qn, q_rstd, kn, k_rstd, vb, g_cumsum, beta, saved)
