@@ -104,7 +104,7 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
   constexpr int FR = 8 * TILE;      // one 64 x 64 operand as (4 row tiles x 2 k-blocks) fragments
   constexpr int AP4 = C + 4;        // LDS row stride of A^T (and of dM while it is passed on)
   constexpr int STAGE_BYTES = 3 * 4 * RB * 2;
-  constexpr int SOLVE_BYTES = (C * AP4 + 4 * 10 * 256) * 4;
+  constexpr int SOLVE_BYTES = (C * AP4 + 2 * 4 * 10 * 256) * 4;
   constexpr int CONTRIB_BYTES = 4 * FR * 2;
   constexpr int LDS_A = STAGE_BYTES > SOLVE_BYTES ? STAGE_BYTES : SOLVE_BYTES;
   constexpr int LDS_BYTES = LDS_A > CONTRIB_BYTES ? LDS_A : CONTRIB_BYTES;
@@ -118,8 +118,9 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
   bf16_t* sO = reinterpret_cast<bf16_t*>(smem);  // phase 1: dO, delta, d delta row fragments
   bf16_t* sD = sO + 4 * RB;
   bf16_t* sdD = sD + 4 * RB;
-  float* sAt = reinterpret_cast<float*>(smem);   // solve: A^T [C][AP4]; then dM [C][AP4]
+  float* sAt = reinterpret_cast<float*>(smem);   // solve: A^T [C][AP4]
   float* sP = sAt + C * AP4;                      // per-wave partial dN^T tiles (4 slots)
+  float* sP2 = sP + 4 * 10 * 256;                 // ... and the same partials transposed (dN tiles)
   bf16_t* sF = reinterpret_cast<bf16_t*>(smem);  // gradients: dN, dM, dN^T, dM^T fragments
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
@@ -197,6 +198,20 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
   __syncthreads();
 
   // ================================ phase 1: products with h, dh ================================
+  // the solve's rows of U (V tile w) and W (K tile w), issued once phase 1's operands have arrived so
+  // they load during its products (issued with those operands they delay them; after the solve's
+  // products their latency is exposed).  Zero-size descriptors read 0 for a wave without the tile.
+  float4 uw[4][2];
+  {
+    const bufrsrc rUv = make_buf(U + ((int64_t)bh * T + t0) * V, own_v ? L * V * 4 : 0u);
+    const bufrsrc rWk = make_buf(W + ((int64_t)bh * T + t0) * K, own_k ? L * K * 4 : 0u);
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      const uint32_t sr = (uint32_t)(16 * J + r16);
+      uw[J][0] = buf_ld4(rUv, (sr * V + 16 * w + 4 * g4) * 4);
+      uw[J][1] = buf_ld4(rWk, (sr * K + i0) * 4);
+    }
+  }
   f32x4 aQ[4], aW[4], aK[4];  // dQg^T (rows i, cols c), d delta h^T (rows c, cols i), dKf^T
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl) aQ[tl] = aW[tl] = aK[tl] = zero4();
@@ -239,12 +254,13 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
         aK[tl] = mma3(fh[kb], fl[kb], xh, xl, aK[tl]);
       }
   }
-  // dM tiles (c-block I, s-block J) = lower(dO delta^T) for lower tiles w and w + 8: lane -> column
-  // s = 16 J + r16, rows c = 16 I + 4 g4 + j
-  f32x4 mt[2];
+  // dM tiles (c-block I, s-block J) = lower(dO delta^T) for lower tiles w and w + 8: mt lane -> column
+  // s = 16 J + r16, rows c = 16 I + 4 g4 + j; mtT the same tile transposed, lane -> row c = 16 I + r16,
+  // columns s = 16 J + 4 g4 + j.  Each gives one of the gradient phase's fragment forms directly.
+  f32x4 mt[2], mtT[2];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    mt[x] = zero4();
+    mt[x] = mtT[x] = zero4();
     const int t = w + NW * x;
     if (t >= 10) continue;
     int I, J;
@@ -256,16 +272,20 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
       if constexpr (DO_BF16) {
         const uint4 ob = *reinterpret_cast<const uint4*>(sO + I * RB + kb * TILE + lane * 8);
         mt[x] = mma2b(ob, xh, xl, mt[x]);
+        mtT[x] = kdn_state::mma2(xh, xl, ob, mtT[x]);
       } else {
         uint4 oh, ol;
         afrag(sO + I * RB, kb, lane, oh, ol);
         mt[x] = mma3(oh, ol, xh, xl, mt[x]);
+        mtT[x] = mma3(xh, xl, oh, ol, mtT[x]);
       }
     }
     if (I == J) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j) {
         if (r16 > 4 * g4 + j) mt[x][j] = 0.f;
+        if (4 * g4 + j > r16) mtT[x][j] = 0.f;
+      }
     }
   }
 
@@ -359,17 +379,14 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
       __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rdv, ((tr * H) * V + x0) * 2, 0, 0);
     }
   }
-  // this block's share of dN^T[s][c] = sum_x (U|W)[s][x] Y[x][c]
-  f32x4 part[10];
+  // this block's share of dN^T[s][c] = sum_x (U|W)[s][x] Y[x][c] (part: D tiles rows s, cols c) and the
+  // same products transposed (part2: rows c, cols s), for the two orientations of the dN fragments
+  f32x4 part[10], part2[10];
   {
-    const bufrsrc rU = make_buf(U + ((int64_t)bh * T + t0) * V, L * V * 4);
-    const bufrsrc rW = make_buf(W + ((int64_t)bh * T + t0) * K, L * K * 4);
     uint4 uh[4], ul[4], yh[4], yl[4];
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
-      const uint32_t sr = (uint32_t)(16 * J + r16);
-      const float4 a0 = own_v ? buf_ld4(rU, (sr * V + 16 * w + 4 * g4) * 4) : float4{0.f, 0.f, 0.f, 0.f};
-      const float4 a1 = own_k ? buf_ld4(rW, (sr * K + i0) * 4) : float4{0.f, 0.f, 0.f, 0.f};
+      const float4 a0 = uw[J][0], a1 = uw[J][1];
       const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
       split8(av, uh[J], ul[J]);
       kdn_state::bfrag(Yt[0][J], Yt[1][J], yh[J], yl[J]);
@@ -379,30 +396,19 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
       int I, J;
       lower_tile(t, I, J);
       part[t] = mma3(uh[J], ul[J], yh[I], yl[I], zero4());
+      part2[t] = mma3(yh[I], yl[I], uh[J], ul[J], zero4());
     }
   }
   f32x4 kg[4];  // dKg^T tiles: lane -> chunk row 16 J + r16, channels i0 .. i0 + 3
 #pragma unroll
   for (int J = 0; J < 4; ++J) kg[J] = Yt[1][J];
-  __syncthreads();  // every A^T read done: sAt now carries dM, sP the partials
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {  // dM rows c, columns s (lower tiles computed, upper zero)
-    const int t = w + NW * x;
-    if (t >= 16) continue;
-    int I, J;
-    f32x4 v = zero4();
-    if (t < 10) {
-      lower_tile(t, I, J);
-      v = mt[x];
-    } else {
-      upper_tile(t - 10, I, J);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sAt[(16 * I + 4 * g4 + j) * AP4 + 16 * J + r16] = v[j];
-  }
+  __syncthreads();  // every A^T read done: the partials may overwrite it
   if (w >= 4) {
 #pragma unroll
-    for (int t = 0; t < 10; ++t) *reinterpret_cast<f32x4*>(sP + (((w - 4) * 10 + t) * 64 + lane) * 4) = part[t];
+    for (int t = 0; t < 10; ++t) {
+      *reinterpret_cast<f32x4*>(sP + (((w - 4) * 10 + t) * 64 + lane) * 4) = part[t];
+      *reinterpret_cast<f32x4*>(sP2 + (((w - 4) * 10 + t) * 64 + lane) * 4) = part2[t];
+    }
   }
   __syncthreads();
   if (w < 4) {
@@ -410,19 +416,27 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
     for (int t = 0; t < 10; ++t) {
       f32x4* slot = reinterpret_cast<f32x4*>(sP + ((w * 10 + t) * 64 + lane) * 4);
       *slot = *slot + part[t];
+      f32x4* slot2 = reinterpret_cast<f32x4*>(sP2 + ((w * 10 + t) * 64 + lane) * 4);
+      *slot2 = *slot2 + part2[t];
     }
   }
   __syncthreads();
 
   // ======================= dN, dM staging (the gradient phase's fragments) =======================
-  float4 dNu[2], dMu[2];
+  // fragment offset of 4 consecutive k = k0 .. k0 + 3 (k0 % 4 == 0) of one row: permuted k order, slot
+  // 4 hh + j of lane group gg <-> k = 32 kb + 16 hh + 4 gg + j
+  auto foff = [](int row, int k0) {
+    return ((row >> 4) * 2 + (k0 >> 5)) * TILE + ((row & 15) + 16 * ((k0 & 15) >> 2)) * 8 + 4 * ((k0 >> 4) & 1);
+  };
+  // dN[c][s] = -(sum of the waves' partials), strictly lower: units (row, k0) of the rows form (row c,
+  // k = s, from the part D tiles) and of the transposed form (row s, k = c, from the part2 D tiles)
+  float4 dNu[2], dNtu[2];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {  // unit (row c, kb, hh, gg) -> 4 consecutive s of one lane's slots
+  for (int u = 0; u < 2; ++u) {
     const int e = tid + 512 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
     const int k0 = 32 * kb + 16 * hh + 4 * gg;
-    dMu[u] = *reinterpret_cast<const float4*>(sAt + row * AP4 + k0);
-    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
-    if ((k0 >> 4) <= (row >> 4)) {
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f}, acct = float4{0.f, 0.f, 0.f, 0.f};
+    if ((k0 >> 4) <= (row >> 4)) {  // rows form: tile (c-block row / 16, s-block k0 / 16)
       const int t = lower_tile_index(row >> 4, k0 >> 4), ln = (row & 15) + 16 * ((k0 & 15) >> 2);
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
@@ -434,29 +448,44 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
       if (k0 + 2 >= row) acc.z = 0.f;
       if (k0 + 3 >= row) acc.w = 0.f;
     }
+    if ((k0 >> 4) >= (row >> 4)) {  // transposed form: tile (c-block k0 / 16, s-block row / 16)
+      const int t = lower_tile_index(k0 >> 4, row >> 4), ln = (row & 15) + 16 * ((k0 & 15) >> 2);
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float4 v = *reinterpret_cast<const float4*>(sP2 + ((ww * 10 + t) * 64 + ln) * 4);
+        acct.x -= v.x, acct.y -= v.y, acct.z -= v.z, acct.w -= v.w;
+      }
+      if (k0 + 0 <= row) acct.x = 0.f;
+      if (k0 + 1 <= row) acct.y = 0.f;
+      if (k0 + 2 <= row) acct.z = 0.f;
+      if (k0 + 3 <= row) acct.w = 0.f;
+    }
     dNu[u] = acc;
+    dNtu[u] = acct;
   }
-  __syncthreads();  // every partial and dM read before the fragments overwrite them
+  __syncthreads();  // every partial read before the fragments overwrite them
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int e = tid + 512 * u, row = e >> 4, kb = (e >> 3) & 1, hh = (e >> 2) & 1, gg = e & 3;
-    const int k0 = 32 * kb + 16 * hh + 4 * gg;
-    const int off = ((row >> 4) * 2 + kb) * TILE + ((row & 15) + 16 * gg) * 8 + 4 * hh;
-    const float4 a = dNu[u], bq = dMu[u];
-    kdn_state::put_unit(sF, off, a.x, a.y, a.z, a.w);
-    kdn_state::put_unit(sF + FR, off, bq.x, bq.y, bq.z, bq.w);
-    const int rk = row & 31, tg = (rk & 15) >> 2, ts = (rk & 3) + 4 * (rk >> 4);
-    const float xv[4] = {a.x, a.y, a.z, a.w}, yv[4] = {bq.x, bq.y, bq.z, bq.w};
+    const int off = foff(row, 32 * kb + 16 * hh + 4 * gg);
+    kdn_state::put_unit(sF, off, dNu[u].x, dNu[u].y, dNu[u].z, dNu[u].w);
+    kdn_state::put_unit(sF + 2 * FR, off, dNtu[u].x, dNtu[u].y, dNtu[u].z, dNtu[u].w);
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int sr = k0 + j;
-      const int toff = ((sr >> 4) * 2 + (row >> 5)) * TILE + ((sr & 15) + 16 * tg) * 8 + ts;
-      const bf16_t xhi = f2bf(xv[j]), yhi = f2bf(yv[j]);
-      sF[2 * FR + toff] = xhi;
-      sF[2 * FR + toff + 512] = f2bf(xv[j] - bf2f(xhi));
-      sF[3 * FR + toff] = yhi;
-      sF[3 * FR + toff + 512] = f2bf(yv[j] - bf2f(yhi));
+  for (int x = 0; x < 2; ++x) {  // dM rows (row c, k = s) from mtT, dM^T rows (row s, k = c) from mt
+    const int t = w + NW * x;
+    if (t >= 16) continue;
+    int I, J;
+    f32x4 a = zero4(), at = zero4();
+    if (t < 10) {
+      lower_tile(t, I, J);
+      a = mtT[x];
+      at = mt[x];
+    } else {
+      upper_tile(t - 10, I, J);  // I < J: zero tiles of both forms
     }
+    kdn_state::put_unit(sF + FR, foff(16 * I + r16, 16 * J + 4 * g4), a[0], a[1], a[2], a[3]);
+    kdn_state::put_unit(sF + 3 * FR, foff(16 * J + r16, 16 * I + 4 * g4), at[0], at[1], at[2], at[3]);
   }
   __syncthreads();
 
