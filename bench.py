@@ -40,8 +40,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
 
 # MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
 # MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
-MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_fwd": "bf16x3", "mem_readout_fwd": "bf16x3",
-             "mem_state_readout_fwd": "bf16x3",
+MFMA_PATH = {"mem_intra_fwd": "bf16x3", "mem_state_readout_fwd": "bf16x3",
              "mem_state_bwd": "bf16x3", "mem_bwd_chunk": "bf16x3"}
 
 
@@ -64,22 +63,17 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int, infer: b
         # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M, A^T (the inverse, saved)
         "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + 2 * mm,
                           2 * (C * K + C * (V + K) / 2)),
-        # U, W, Kf, g_last -> h, delta  (serial chain)
-        "mem_state_fwd": (4 * V + 8 * K + 4 * K / C + h_b + 4 * V, 2 * 2 * K * V),
-        # Qg, M, h, delta -> o  (chunk-parallel readout)
-        "mem_readout_fwd": (4 * K + mm + h_b + 4 * V + (2 if variant == "iso" else 4) * V,
-                            2 * (K * V + C * V / 2)),
         # U, W, Kf, g_last, Qg, M -> h, delta, o  (one chunk group: the state pass does the readout)
         "mem_state_readout_fwd": (4 * V + 8 * K + 4 * K / C + h_b + 4 * V + 4 * K + mm
                                   + (2 if variant == "iso" else 4) * V,
                                   2 * 2 * K * V + 2 * (K * V + C * V / 2)),
         # M, Kf, Qg, W, dO -> dh, d delta
         "mem_state_bwd": (mm + 12 * K + do_b + h_b + 4 * V, 2 * (C * V / 2 + 3 * K * V)),
-        # h, dh, delta, d delta, dO, A^T, U, W, q, k, kappa, g -> dv, dq, dk, dkappa, dg (dQg, dW, dKf, dM,
-        # dKg and dN stay on chip); FLOPs: the state-gradient products, the solves and dN, the gradient
-        # contractions
+        # h, dh, delta, d delta, dO, A^T, U, W, q, k, kappa, g (iso: and the q / k rstd of the in-op norm,
+        # whose backward it applies) -> dv, dq, dk, dkappa, dg (dQg, dW, dKf, dM, dKg and dN stay on chip);
+        # FLOPs: the state-gradient products, the solves and dN, the gradient contractions
         "mem_bwd_chunk": (2 * h_b + 8 * V + do_b + mm + 4 * V + 4 * K + 2 * 2 * K + kap_in + 4 * K
-                          + 2 * V + 2 * 2 * K + dkap_out + 4 * K,
+                          + 2 * V + 2 * 2 * K + dkap_out + 4 * K + (8 if variant == "iso" else 0),
                           2 * (3 * K * V + C * V / 2) + 2 * (C * (V + K) / 2 + C * (V + K) / 2) + 2 * 2 * (C * K)),
     }
     if infer:
