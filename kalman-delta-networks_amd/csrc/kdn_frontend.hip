@@ -963,19 +963,19 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   else KDN_GATE_BWD(float, float);
 #undef KDN_GATE_BWD
   KDN_CHECK_LAUNCH();
-  if (dA_log)
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_A, NP, (int64_t)H, H, dA_log);
-  if (ddt_bias)
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H * K, 64)), dim3(256), 0, stream, part_dt, NP,
-                       (int64_t)H * K, H * K, ddt_bias);
+  // the parameter gradients' partial sums and the prior-precision VJP, one launch
+  PartSegs P{};
+  if (dA_log) P.seg[P.nseg++] = PartSeg{part_A, (int64_t)H, H, dA_log};
+  if (ddt_bias) P.seg[P.nseg++] = PartSeg{part_dt, (int64_t)H * K, H * K, ddt_bias};
   // part_bias rows are [omega(H) | r(H)]
-  if (domega_bias)
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_bias, NP,
-                       (int64_t)2 * H, H, domega_bias);
-  if (dr_bias)
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(H, 64)), dim3(256), 0, stream, part_bias + H, NP,
-                       (int64_t)2 * H, H, dr_bias);
-  if (dmu_param) hipLaunchKernelGGL(mu_vjp_kernel, dim3(cdiv(H, 256)), dim3(256), 0, stream, mu_param, dmu, H, dmu_param);
+  if (domega_bias) P.seg[P.nseg++] = PartSeg{part_bias, (int64_t)2 * H, H, domega_bias};
+  if (dr_bias) P.seg[P.nseg++] = PartSeg{part_bias + H, (int64_t)2 * H, H, dr_bias};
+  P.mu_param = mu_param;
+  P.dmu = dmu;
+  P.H = H;
+  P.dmu_param = dmu_param;
+  const int nblk = part_segs_blocks(P);
+  if (nblk > 0) hipLaunchKernelGGL(reduce_partials_multi_kernel, dim3(nblk), dim3(256), 0, stream, P, NP);
   KDN_CHECK_LAUNCH();
   return 0;
 }
