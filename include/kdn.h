@@ -202,7 +202,12 @@ int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
  * inputs x: the norm's backward dx = rstd (dy - y (y . dy)) is applied to the fp32 dy in the kernel
  * (kdn_l2norm_bwd recomputes y from x instead; the two agree to bf16 rounding).
  * `stages`: bit 0 reverse state pass, bit 1 the chunk-parallel backward, bits 2 and 3 the exact
- * path's solves and gradients for the chunks outside the factored range (-1 = all, in this order). */
+ * path's solves and gradients for the chunks outside the factored range (-1 = all, in this order).
+ * Bits 0 and 1 in one call, with one chunk group (kdn_mem_state_groups == 1), at least 16 chunks
+ * and CUs the pass leaves idle: the reverse pass runs in two segments, and chunk-backward work of
+ * the first segment's chunks runs beside the second on a stream of the library's own (one per
+ * device, created on first use); the call returns with `stream` ordered after both, and the results
+ * are identical to separate calls.  Calls on one device serialise their enqueue on a mutex. */
 int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const float* g_cumsum,
                 int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,

@@ -61,7 +61,8 @@ __device__ __forceinline__ int lower_tile_index(int I, int J) {
 // The whole chunk-parallel backward of one chunk in one kernel: the state-gradient products, the
 // transposed solves and the gradients.  dQg, dW, dKf, dM, dKg, dN and the g_last dots never go to
 // HBM: each is produced in the register or LDS layout its consumer takes.
-// grid (NT, B*H), block 512 (8 waves), one workgroup per CU (LDS ~99 KB).
+// One chunk-head task of the order task = (NT - 1 - n) * B*H + bh (last chunks first, the order in
+// which the reverse state pass finishes them); block 512 (8 waves), one workgroup per CU (LDS ~106 KB).
 //  * Staging.  The chunk rows of dO, delta and d delta are split into LDS fragments (rows c,
 //    k = v, natural order), all 64 rows at once.
 //  * Wave w owns channel tile it = w (16 channels of K) and V tile w (16 columns of V).  It loads
@@ -86,13 +87,13 @@ __device__ __forceinline__ int lower_tile_index(int I, int J) {
 // and stop after them.
 // ---------------------------------------------------------------------------------------------
 template <int K, int V, bool ISO, typename TDO>
-__global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
-    const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
+__device__ __forceinline__ void chunk_bwd_task(
+    int task, const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
     const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
     const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const float* __restrict__ gc, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, int T, int H,
-    int NT, float scale, bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk,
+    int NT, int BH, float scale, bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk,
     float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, float* __restrict__ xQg,
     float* __restrict__ xW, float* __restrict__ xKf, float* __restrict__ xM, float* __restrict__ xgl) {
   constexpr bool DO_BF16 = sizeof(TDO) == 2;
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
   float* sP = sAt + C * AP4;                      // per-wave partial dN^T tiles (4 slots)
   float* sP2 = sP + 4 * 10 * 256;                 // ... and the same partials transposed (dN tiles)
   bf16_t* sF = reinterpret_cast<bf16_t*>(smem);  // gradients: dN, dM, dN^T, dM^T fragments
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int n = NT - 1 - task / BH, bh = task % BH, b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   const int64_t chunk = (int64_t)bh * NT + n;
@@ -737,6 +738,22 @@ __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
                                             rdk, o * 2, 0, 0);
     }
   }
+}
+
+// One workgroup per task: tasks task0 .. task0 + gridDim.x - 1.
+template <int K, int V, bool ISO, typename TDO>
+__global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
+    const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
+    const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
+    const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, int T, int H,
+    int NT, int BH, int task0, float scale, bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk,
+    float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, float* __restrict__ xQg,
+    float* __restrict__ xW, float* __restrict__ xKf, float* __restrict__ xM, float* __restrict__ xgl) {
+  chunk_bwd_task<K, V, ISO, TDO>(task0 + (int)blockIdx.x, hbuf, dhbuf, Dl, dDl, dO, At, U, W, flags, q, k, kap, gc,
+                                 q_rstd, k_rstd, T, H, NT, BH, scale, dv, dq, dk, dkap, dbeta, dg, xQg, xW, xKf, xM,
+                                 xgl);
 }
 
 }  // namespace kdn_bwd

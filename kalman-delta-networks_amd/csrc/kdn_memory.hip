@@ -31,6 +31,8 @@
 // non-increasing G.  Diagonal blocks use the split only when the block's decay span
 // is <= 86 (base 2, no overflow); otherwise an exact per-element path runs.
 // Products use fp32 MFMA (v_mfma_f32_16x16x4_f32), fp32 accumulate.
+#include <mutex>
+
 #include "kdn_common.h"
 #include "kdn_state.h"
 #include "kdn_intra.h"
@@ -737,7 +739,7 @@ struct MemLayout {
   }
 };
 struct BwdLayout {
-  int64_t dh, dD, dQg, dW, dKf, dM, dgl, dKg, dN, grp, total;
+  int64_t dh, dD, dQg, dW, dKf, dM, dgl, dKg, dN, carry, grp, total;
   GroupCount gc;
   BwdLayout(int B, int T, int H, int K, int V) {
     const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
@@ -751,10 +753,79 @@ struct BwdLayout {
     dgl = dM + NB * C * C;
     dKg = dgl + NB * K;
     dN = dKg + TT * K;
-    grp = round64(dN + NB * C * C);  // the reverse state pass's group buffers
+    carry = round64(dN + NB * C * C);  // two cotangents carried between segments of the reverse pass
+    grp = carry + 2 * (int64_t)B * H * K * V;  // the reverse state pass's group buffers
     total = grp + group_floats((int64_t)B * H, gc, K, V);
   }
 };
+
+// Overlapped schedule of the reverse state pass and the chunk backward (one call with both).  With
+// one chunk group the pass occupies B*H*V/64 workgroups, one per CU (144 at B4 H18), and leaves
+// `idle` CUs.  It runs in two segments: the last m1 chunks, then the rest (the state gradient
+// crosses the boundary in fp32, so results are bit-identical to one pass).  Once the first segment
+// is done, a second stream runs the chunk-backward tasks of its chunks: the second segment's
+// workgroups take the CUs the first one frees (the side launch starts a few microseconds later), and
+// the side launch's workgroups fill the idle CUs and backfill them as they finish.  The remaining
+// tasks run at full width after the pass.  A chunk-backward task lasts about kStepsPerTask chunk
+// steps of the pass running beside it (~36 us against ~5.7 us), which sizes the first segment so
+// that its tasks keep the idle CUs busy until the pass ends.
+constexpr float kStepsPerTask = 6.4f;
+constexpr unsigned kSideDelayTicks = 300;  // of the 100 MHz wall clock: 3 us
+struct BwdOverlap {
+  int m1 = 0, side_tasks = 0;
+};
+inline BwdOverlap plan_bwd_overlap(int BH, int NT, int NV, GroupCount gc, int cus) {
+  BwdOverlap o;
+  const int idle = cus - BH * NV;
+  if (gc.NG != 1 || idle < 32 || NT < 16) return o;
+  const int m1 = max(1, min(NT / 2, (int)ceilf((float)NT * idle / (kStepsPerTask * BH + idle))));
+  const int iters = (int)lrintf((NT - m1) / kStepsPerTask);
+  o.m1 = m1;
+  o.side_tasks = min(m1 * BH, iters * idle);
+  return o;
+}
+// One wave that returns after `ticks` of the constant 100 MHz clock (bounded wait, no memory access).
+__global__ void side_delay_kernel(unsigned ticks) {
+  const uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
+// The second stream of a device and the events that order it against the caller's stream: made
+// on first use (default priority, non-blocking), kept until the process ends.  Every call on a
+// device shares them, so one schedule's enqueue holds the mutex.
+struct SideQueue {
+  hipStream_t s = nullptr;
+  hipEvent_t ev[2] = {};
+  int cus = 0;  // compute units of the device
+};
+std::mutex g_side_mu;
+constexpr int kMaxDevices = 64;
+SideQueue g_side[kMaxDevices];
+// Call with g_side_mu held.
+int side_queue(SideQueue** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return KDN_ERR_ARG;
+  SideQueue& q = g_side[dev];
+  if (!q.s) {
+    if ((e = hipDeviceGetAttribute(&q.cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return (int)e;
+    for (auto& ev : q.ev)
+      if (!ev && (e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return (int)e;
+    if ((e = hipStreamCreateWithFlags(&q.s, hipStreamNonBlocking)) != hipSuccess) {
+      q.s = nullptr;
+      return (int)e;
+    }
+  }
+  *out = &q;
+  return 0;
+}
+// `to` waits for the work enqueued on `from` so far
+inline int stream_wait(hipStream_t to, hipStream_t from, hipEvent_t ev) {
+  hipError_t e = hipEventRecord(ev, from);
+  if (e == hipSuccess) e = hipStreamWaitEvent(to, ev, 0);
+  return (int)e;
+}
 
 // Launch pass A / B / C of a state pass (or the single serial pass).  launch(grid, plan) issues the
 // state kernel of one pass.
@@ -894,27 +965,62 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   const int* flags = reinterpret_cast<const int*>(saved + lay.flags);
   float *dh = work + bl.dh, *dD = work + bl.dD, *dQg = work + bl.dQg, *dW = work + bl.dW, *dKf = work + bl.dKf,
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
-  dim3 gchunk(NT, B * H);
-  if (stages & 1) {  // reverse state pass (one- or two-level): dh per chunk, d delta, d h0
-    // helper waves take M^T dO and Qg^T dO off the serial chain (see state_bwd_kernel)
-    const dim3 bs(2 * kdn_state::state_threads(V));
+  constexpr int NV = V / kdn_state::state_cols(V);
+  const dim3 bs(2 * kdn_state::state_threads(V));  // helper waves take M^T dO and Qg^T dO off the chain
+  auto launch_state = [&](dim3 grid, const kdn_state::GroupPlan& P, const float* dS_in, float* dS_out,
+                          hipStream_t st) {
+    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO, true>), grid, bs, 0, st, M, Kf, Qg, W, gc, dO, dS_in,
+                       T, H, NT, B * H, dh, dD, dS_out, P);
+  };
+  // every chunk's products with h / dh; the solves and gradients of the unflagged ones: the
+  // chunk-head tasks task0 .. task_end - 1 (order of chunk_bwd_task: last chunks first)
+  auto launch_chunk = [&](int task0, int task_end, hipStream_t st) {
+    if (iso)
+      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, true, TDO>), dim3(task_end - task0), dim3(512), 0, st, hb,
+                         dh, D, dD, dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, B * H, task0, scale,
+                         dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf, dM, dgl);
+    else
+      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, false, TDO>), dim3(task_end - task0), dim3(512), 0, st, hb,
+                         dh, D, dD, dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, B * H, task0, scale,
+                         dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf, dM, dgl);
+  };
+  const int tasks = NT * B * H;
+  bool overlapped = false;
+  if ((stages & 3) == 3 && bl.gc.NG == 1) {
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    SideQueue* sq = nullptr;
+    int rc = side_queue(&sq);
+    if (rc) return rc;
+    const BwdOverlap ov = plan_bwd_overlap(B * H, NT, NV, bl.gc, sq->cus);
+    if (ov.side_tasks > 0) {
+      const int c1 = NT - ov.m1;
+      float* carry = work + bl.carry;
+      launch_state(dim3(B * H * NV), kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr, c1, NT}, dht, carry, stream);
+      KDN_CHECK_LAUNCH();
+      if ((rc = stream_wait(sq->s, stream, sq->ev[0]))) return rc;
+      // a few microseconds on the side stream first, so that the second segment's workgroups are
+      // dispatched onto the CUs the first one frees before the side launch competes for them
+      hipLaunchKernelGGL(side_delay_kernel, dim3(1), dim3(64), 0, sq->s, kSideDelayTicks);
+      KDN_CHECK_LAUNCH();
+      launch_chunk(0, ov.side_tasks, sq->s);
+      KDN_CHECK_LAUNCH();
+      launch_state(dim3(B * H * NV), kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr, 0, c1}, carry, dh0, stream);
+      KDN_CHECK_LAUNCH();
+      launch_chunk(ov.side_tasks, tasks, stream);
+      KDN_CHECK_LAUNCH();
+      if ((rc = stream_wait(stream, sq->s, sq->ev[1]))) return rc;
+      overlapped = true;
+    }
+  }
+  if (!overlapped && (stages & 1)) {  // reverse state pass (one- or two-level): dh per chunk, d delta, d h0
     const int rc = run_state_pass<K, V>(B * H, bl.gc, work + bl.grp, true, stream,
                                         [&](dim3 grid, const kdn_state::GroupPlan& P) {
-                                          hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO, true>), grid, bs,
-                                                             0, stream, M, Kf, Qg, W, gc, dO, dht, T, H, NT, B * H,
-                                                             dh, dD, dh0, P);
+                                          launch_state(grid, P, dht, dh0, stream);
                                         });
     if (rc) return rc;
   }
-  if (stages & 2) {  // every chunk's products with h / dh; the solves and gradients of the unflagged ones
-    if (iso)
-      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, true, TDO>), gchunk, dim3(512), 0, stream, hb, dh, D, dD, dO,
-                         A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, scale, dv, dq, dk, dkap, dbeta, dg,
-                         dQg, dW, dKf, dM, dgl);
-    else
-      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, false, TDO>), gchunk, dim3(512), 0, stream, hb, dh, D, dD,
-                         dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, scale, dv, dq, dk, dkap, dbeta,
-                         dg, dQg, dW, dKf, dM, dgl);
+  if (!overlapped && (stages & 2)) {
+    launch_chunk(0, tasks, stream);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 4) {  // the chunks left to the exact path: transposed solves into dv, dKg, dN

@@ -196,12 +196,24 @@ __device__ __forceinline__ int64_t row_bthk(int b, int t, int h, int T, int H, i
 // Sg is [BH][NG][K][V], Mg is [BH][NG][K][V + K].
 // ===========================================================================
 struct GroupPlan {
-  int NG;     // number of chunk groups (1: a single serial pass over every chunk)
+  int NG;     // number of chunk groups (1: a single serial pass)
   int m;      // chunks per group (the last group may be shorter)
   int pass;   // 0: pass A, 1: pass C (unused when NG == 1)
   float* Sg;
   float* Mg;
+  // NG == 1: the pass runs chunks c0 .. c1 - 1 (c1 <= 0: every chunk from c0), entering from h0 (dht)
+  // and leaving into ht (dh0); a sequence split into segments runs as consecutive such passes
+  int c0 = 0, c1 = 0;
 };
+__device__ __forceinline__ void plan_range(const GroupPlan& P, int g, int NT, int& n0, int& n1) {
+  if (P.NG == 1) {
+    n0 = P.c0;
+    n1 = P.c1 > 0 ? min(P.c1, NT) : NT;
+  } else {
+    n0 = g * P.m;
+    n1 = min(NT, n0 + P.m);
+  }
+}
 
 // Workgroup -> (bh, column slice, group, role) of a state pass.  `real`: the group is run on the
 // true state (stores per-chunk results); otherwise it is a map group.  `phi`: the slice's columns
@@ -276,7 +288,8 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
   const int col = vs * COLS + 16 * w + (lane & 15);  // this lane's state column (>= V: a Phi column)
-  const int n0 = g * P.m, n1 = P.NG == 1 ? NT : min(NT, n0 + P.m);
+  int n0, n1;
+  plan_range(P, g, NT, n0, n1);
 
   if constexpr (RO) {
     if (tid >= NTHR) {  // readout waves: wave rw owns chunk rows 16 rw .. 16 rw + 15 of all COLS columns
@@ -670,7 +683,8 @@ __global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void 
   if (!group_task<V, K, true>(P, BH, bh, vs, g, real, phi)) return;
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g4 = lane >> 4;
-  const int n0 = g * P.m, n1 = P.NG == 1 ? NT : min(NT, n0 + P.m);
+  int n0, n1;
+  plan_range(P, g, NT, n0, n1);
 
   // dO as loaded (raw bf16 bits or fp32), widened only where the fragments are built, so the
   // loads of a chunk are all issued before any of them is waited for

@@ -138,6 +138,11 @@ class KernelTimer:
 _timer: KernelTimer | None = None
 
 
+def timing() -> bool:
+    """True while a KernelTimer is active (callers then launch one kernel per call)."""
+    return _timer is not None
+
+
 def call(name: str, *args, tag: str | None = None):
     """Call entry point ``name``; under a KernelTimer the call is timed as ``tag`` (default: the
     entry name without its ``kdn_`` prefix)."""

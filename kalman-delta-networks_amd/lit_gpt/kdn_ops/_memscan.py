@@ -21,6 +21,9 @@ def state_groups(B: int, T: int, H: int, K: int, V: int) -> int:
 # bit 2: the chunk-parallel backward of every chunk (products with h and dh; solves and gradients of
 # the chunks the forward factored); bits 4 | 8: the exact path's solves and gradients (flagged chunks)
 BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_chunk"), (12, "mem_bwd_exact"))
+# bits 1 | 2 in one call: with one chunk group the reverse pass runs in segments and each finished
+# segment's chunk backward overlaps the next segment's pass on a second stream (same results)
+BWD_STAGES_OVERLAP = ((3, "mem_state_chunk_bwd"), (12, "mem_bwd_exact"))
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
@@ -45,9 +48,12 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
 
 
 def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do, *, d_final_state=None,
-            need_initial_state_grad=False, q_rstd=None, k_rstd=None):
+            need_initial_state_grad=False, q_rstd=None, k_rstd=None, overlap=None):
     """Returns (dq bf16, dk bf16, dv bf16, dkappa f32 [B,T,H,K] or dbeta f32 [B,T,H],
     dg f32 natural-log not reverse-summed, d_initial_state or None).
+
+    ``overlap`` (default: unless a KernelTimer is timing each kernel) launches the reverse pass and
+    the chunk backward in one call, which overlaps them where the shape allows.
 
     With ``q_rstd`` / ``k_rstd`` [B,T,H] (the in-op L2 norm) q and k are the raw bf16 inputs whose
     normalised values the forward took, and dq, dk are the gradients of the raw inputs."""
@@ -66,7 +72,9 @@ def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do
         do = do.float()
     do = do.contiguous()
     stream = _lib.stream_of(q)
-    for bit, tag in BWD_STAGES:
+    if overlap is None:
+        overlap = not _lib.timing()
+    for bit, tag in (BWD_STAGES_OVERLAP if overlap else BWD_STAGES):
         _lib.call("kdn_mem_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(g_cumsum),
                   B, T, H, K, V, float(scale), _lib.ptr(do), _lib.is_bf16(do), _lib.ptr(dht), _lib.ptr(saved),
                   saved.numel(), _lib.ptr(ws), ws.numel(), _lib.ptr(dq), _lib.ptr(dk),

@@ -1,0 +1,69 @@
+"""The overlapped schedule of the memory-scan backward (kdn_mem_bwd with stage bits 0 and 1 in one
+call): with one chunk group the reverse state pass runs in two segments, and chunk-backward tasks of
+the first segment's chunks run on a second stream, in launches no wider than the CUs the pass leaves
+idle, while the pass continues; the remaining tasks run after the pass.
+
+The state gradient crosses the segment boundary in fp32 and every kernel computes what it computes
+in the serial schedule, so every output must be bit-identical to separate calls (reverse pass, then
+chunk backward), which the other memory-scan tests pin to the fp64 oracle.  Shapes have B*H large
+enough for one chunk group (checked): 33 chunks (8 in the first segment, 400 side tasks in 4
+launches) and the benchmark's 64 chunks (16; 768 side tasks in 7 launches), with a ragged last chunk,
+a chunk taken by the exact path, a final-state cotangent and the initial-state gradient; iso (beta,
+bf16 dO) and diag (kappa, fp32 dO).
+"""
+import pytest
+import torch
+
+from gpu_util import gpu_or_skip, log
+
+pytestmark = pytest.mark.gpu
+CHUNK = 64
+
+
+def _inputs(dev, seed, B, T, H, K, V, diag, extreme):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, device=dev)  # noqa: E731
+    q = torch.nn.functional.normalize(rn(B, T, H, K), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(rn(B, T, H, K), dim=-1).bfloat16()
+    v = rn(B, T, H, V).bfloat16()
+    ell = (-0.13 + 0.05 * rn(B, T, H, K)).clamp(max=0.0)
+    if extreme:  # one chunk of one head beyond the factored range
+        ell[0, 64:128, 0] = (-8.0 + 2.0 * rn(64, K)).clamp(max=0.0)
+    G = torch.cat([ell[:, c:c + CHUNK].cumsum(1) for c in range(0, T, CHUNK)], 1) / 0.6931471805599453
+    if diag:
+        kap = 0.5 * torch.rand(B, T, H, K, generator=g, device=dev) * k.float()
+        do = rn(B, T, H, V)
+    else:
+        kap = 0.2 + 0.8 * torch.rand(B, T, H, generator=g, device=dev)
+        do = rn(B, T, H, V).bfloat16()
+    dht = 0.1 * rn(B, H, K, V)
+    return q, k, v, G.contiguous(), kap.contiguous(), do, dht
+
+
+@pytest.mark.parametrize("B,T,H,variant,extreme", [
+    (2, 2048 + 37, 36, "iso", True),   # 33 chunks
+    (4, 4096, 18, "iso", False),       # 64 chunks (the benchmark shape)
+    (4, 4096, 18, "diag", True),
+])
+def test_overlapped_backward_is_bit_identical(B, T, H, variant, extreme):
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import _memscan
+    K = V = 128
+    diag = variant == "diag"
+    assert _memscan.state_groups(B, T, H, K, V) == 1, "shape must run one chunk group"
+    log(f"case overlapped-bwd {variant} B={B} T={T} H={H} extreme={extreme}")
+    q, k, v, G, kap, do, dht = _inputs(dev, 11 + T + H, B, T, H, K, V, diag, extreme)
+    scale = K ** -0.5
+    out_dtype = torch.float32 if diag else torch.bfloat16
+    _, saved, _ = _memscan.mem_fwd(q, k, kap, not diag, v, G, scale, out_dtype=out_dtype)
+    runs = []
+    for overlap in (False, True, True):  # twice overlapped: the side stream's events are reused
+        runs.append(_memscan.mem_bwd(q, k, kap, not diag, v, G, saved, scale, do, d_final_state=dht,
+                                     need_initial_state_grad=True, overlap=overlap))
+    torch.cuda.synchronize()
+    names = ("dq", "dk", "dv", "dkappa" if diag else "dbeta", "dg", "d initial state")
+    for run in runs[1:]:
+        for name, a, b in zip(names, runs[0], run):
+            assert torch.isfinite(a).all(), name
+            assert torch.equal(a, b), f"{name}: overlapped schedule differs from the serial one"
+    log("  bit-identical")
