@@ -61,7 +61,9 @@ def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int, infer: b
     mm = C * C / C * 4                                    # one fp32 C x C matrix per chunk
     per = {
         # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M, A^T (the inverse, saved)
-        "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + 2 * mm,
+        # (iso: q, k raw, normalised in the kernel, and their rows' rstd written)
+        "mem_intra_fwd": (2 * 2 * K + 2 * V + kap_in + 4 * K + 4 * (V + 3 * K) + 2 * mm
+                          + (8 if variant == "iso" else 0),
                           2 * (C * K + C * (V + K) / 2)),
         # U, W, Kf, g_last, Qg, M -> h, delta, o  (one chunk group: the state pass does the readout)
         "mem_state_readout_fwd": (4 * V + 8 * K + 4 * K / C + h_b + 4 * V + 4 * K + mm

@@ -187,20 +187,24 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
  * caller can launch and time them one at a time; the stages must run in this order.  Bits 1 and 2
  * in one call run the state pass with the readout fused.  Bit 3 (with stages >= 0) declares that
  * no backward follows (inference, as under torch.no_grad): the intermediates only the backward
- * reads are then not written, and `saved` is scratch for this call alone. */
+ * reads are then not written, and `saved` is scratch for this call alone.
+ * q_rstd / k_rstd [B,T,H] f32 (both or neither, outputs): the in-op L2 norm of
+ * _chunk_kda_precumsum_paired (iso_kdn_chunk.py:2203-2204).  Given, q and k are the raw bf16 inputs;
+ * the scan consumes y = bf16(x / sqrt(sum x^2 + 1e-6)) per row, exactly what kdn_l2norm_fwd (eps 1e-6)
+ * writes, and the rows' rstd are written here for kdn_mem_bwd. */
 int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
                 const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
-                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, int stages,
-                hipStream_t stream);
+                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, float* q_rstd,
+                float* k_rstd, int stages, hipStream_t stream);
 /* Backward: replaces _chunk_kda_bwd_precum (iso_kdn_chunk.py:2089-2187) and
  * _DiagKdnMemoryFunction.backward (diag_kdn_chunk.py:3258-3312).  dq, dk, dv bf16; dkappa
  * [B,T,H,K] f32 (diag) or dbeta [B,T,H] f32 (iso); dg [B,T,H,K] f32 in natural-log coordinates,
  * not reverse-summed.  d_final_state / d_initial_state nullable.
  * q_rstd / k_rstd [B,T,H] f32 (both or neither): the in-op L2 norm of _chunk_kda_precumsum_paired
- * (iso_kdn_chunk.py:2203-2204, 2229-2230).  Given, q and k are still the normalised bf16 operands
- * y = x rstd (kdn_l2norm_fwd's outputs, whose rstd these are), and dq, dk are returned for the raw
- * inputs x: the norm's backward dx = rstd (dy - y (y . dy)) is applied to the fp32 dy in the kernel
- * (kdn_l2norm_bwd recomputes y from x instead; the two agree to bf16 rounding).
+ * (iso_kdn_chunk.py:2203-2204, 2229-2230), as kdn_mem_fwd wrote them.  Given, q and k are the raw bf16
+ * inputs x the forward took, the kernels form the operand y = bf16(x rstd) again, and dq, dk are
+ * returned for x: the norm's backward dx = rstd (dy - y (y . dy)) is applied to the fp32 dy in the
+ * kernel (kdn_l2norm_bwd takes the bf16-rounded dy instead; the two agree to bf16 rounding).
  * `stages`: bit 0 reverse state pass, bit 1 the chunk-parallel backward, bits 2 and 3 the exact
  * path's solves and gradients for the chunks outside the factored range (-1 = all, in this order).
  * Bits 0 and 1 in one call, with one chunk group (kdn_mem_state_groups == 1), at least 16 chunks

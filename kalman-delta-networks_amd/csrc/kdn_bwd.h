@@ -116,6 +116,7 @@ __device__ __forceinline__ void chunk_bwd_task(
   __shared__ float sDgl[K];
   __shared__ float sBeta[NW * C];
   __shared__ float sDot[2][NW][C];  // in-op L2 norm: per-wave partial row dots y . dy of q and k
+  __shared__ float sRs[2][C];       // ... and the rows' rstd of q and k (their raw values in memory)
   bf16_t* sO = reinterpret_cast<bf16_t*>(smem);  // phase 1: dO, delta, d delta row fragments
   bf16_t* sD = sO + 4 * RB;
   bf16_t* sdD = sD + 4 * RB;
@@ -131,6 +132,10 @@ __device__ __forceinline__ void chunk_bwd_task(
   const bool own_k = w < NIT, own_v = w < NVT;
   const int it = w;  // this wave's channel tile (when own_k)
   const int i0 = 16 * it + 4 * g4;
+  if (q_rstd && tid < 2 * C) {  // read in the gradient phase, after phase 1's barriers
+    const int c = tid & 63;
+    sRs[tid >> 6][c] = c < L ? ((tid >> 6) ? k_rstd : q_rstd)[((int64_t)b * T + t0 + c) * H + h] : 0.f;
+  }
 
   // ================================ loads ================================
   const bufrsrc rD = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);  // rows past L read 0
@@ -491,9 +496,9 @@ __device__ __forceinline__ void chunk_bwd_task(
   __syncthreads();
 
   // ================================ gradient phase ================================
-  // With the in-op L2 norm (q_rstd, k_rstd [B,T,H] given), dq and dk are returned for the raw inputs
-  // x = y / rstd of the normalised q, k (= y) this kernel takes: dx = rstd (dy - y (y . dy)), the row
-  // dot summed over the waves.  y is the bf16 normalised operand the forward used.
+  // With the in-op L2 norm (q_rstd, k_rstd [B,T,H] given) q and k are the raw inputs x, the operand is
+  // y = bf16(x rstd) (the forward's), and dq, dk are returned for x: dx = rstd (dy - y (y . dy)), the
+  // row dot summed over the waves.
   const bool qk_norm = q_rstd != nullptr;
   float bpart[4] = {0.f, 0.f, 0.f, 0.f};  // iso: dbeta partials of rows 16 tl + r16
   float dqs[4][4], dks[4][4];             // in-op norm: dy of q, k (rows 16 tl + r16, channels i0 ..)
@@ -530,9 +535,15 @@ __device__ __forceinline__ void chunk_bwd_task(
     float Rown[16], Kown[16], Qown[16];
 #pragma unroll
     for (int p = 0; p < 16; ++p) {
-      const float kvp = bf2f(kraw[p]), e = fexp2(Gv[p] - mA[p >> 2]);
+      const int c = 16 * (p >> 2) + 4 * g4 + (p & 3);
+      float kvp = bf2f(kraw[p]), qvp = bf2f(qraw[p]);
+      if (qk_norm) {
+        kvp = l2n(kvp, sRs[1][c]);
+        qvp = l2n(qvp, sRs[0][c]);
+      }
+      const float e = fexp2(Gv[p] - mA[p >> 2]);
       Kown[p] = kvp * e;
-      Qown[p] = scale * bf2f(qraw[p]) * e;
+      Qown[p] = scale * qvp * e;
       Rown[p] = (ISO ? av[p] * kvp : av[p]) * frcp(e);
     }
     const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
@@ -594,12 +605,22 @@ __device__ __forceinline__ void chunk_bwd_task(
         }
       }
       const uint32_t c = (uint32_t)(16 * tl + r16), o = c * H * K + i0;
-      const float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
-                            __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
-      const float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
-                            __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
-      yk2[tl] = kq4[tl];
-      yq2[tl] = qq4[tl];
+      float kv4[4] = {__uint_as_float(kq4[tl].x << 16), __uint_as_float(kq4[tl].x & 0xffff0000u),
+                      __uint_as_float(kq4[tl].y << 16), __uint_as_float(kq4[tl].y & 0xffff0000u)};
+      float qv4[4] = {__uint_as_float(qq4[tl].x << 16), __uint_as_float(qq4[tl].x & 0xffff0000u),
+                      __uint_as_float(qq4[tl].y << 16), __uint_as_float(qq4[tl].y & 0xffff0000u)};
+      if (qk_norm) {
+        const float rk_ = sRs[1][c], rq_ = sRs[0][c];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          kv4[j] = l2n(kv4[j], rk_);
+          qv4[j] = l2n(qv4[j], rq_);
+        }
+        yk2[tl] = u32x2{(uint32_t)f2bf(kv4[0]) | ((uint32_t)f2bf(kv4[1]) << 16),
+                        (uint32_t)f2bf(kv4[2]) | ((uint32_t)f2bf(kv4[3]) << 16)};  // exact: already bf16
+        yq2[tl] = u32x2{(uint32_t)f2bf(qv4[0]) | ((uint32_t)f2bf(qv4[1]) << 16),
+                        (uint32_t)f2bf(qv4[2]) | ((uint32_t)f2bf(qv4[3]) << 16)};
+      }
       const float a4[4] = {kap4[tl].x, kap4[tl].y, kap4[tl].z, kap4[tl].w};
       const float gv[4] = {G4[tl].x, G4[tl].y, G4[tl].z, G4[tl].w};
       const float mz[4] = {__shfl(mA[tl], 4 * g4, 64), __shfl(mA[tl], 4 * g4 + 1, 64), __shfl(mA[tl], 4 * g4 + 2, 64),
@@ -714,13 +735,11 @@ __device__ __forceinline__ void chunk_bwd_task(
   if (own_k) {  // dx = rstd (dy - y (y . dy)) for the raw q, k
     const bufrsrc rdq = make_buf(dq + in_row0 * K, rows_in * K * 2);
     const bufrsrc rdk = make_buf(dk + in_row0 * K, rows_in * K * 2);
-    const bufrsrc rrq = make_buf(q_rstd + in_row0, rows_in * 4);
-    const bufrsrc rrk = make_buf(k_rstd + in_row0, rows_in * 4);
 #pragma unroll
     for (int tl = 0; tl < 4; ++tl) {
       const int c = 16 * tl + r16;
       const float dotq = sDot[0][NW - 1][c], dotk = sDot[1][NW - 1][c];
-      const float rq_ = buf_ld(rrq, (uint32_t)(c * H) * 4), rk_ = buf_ld(rrk, (uint32_t)(c * H) * 4);
+      const float rq_ = sRs[0][c], rk_ = sRs[1][c];
       float yq[4], yk[4], xq[4], xk[4];
       unpack4(yq2[tl], yq);
       unpack4(yk2[tl], yk);

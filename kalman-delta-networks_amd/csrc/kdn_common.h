@@ -78,6 +78,30 @@ __device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x)
 // exp and softplus on the hardware exp2 / log2 (one v_exp_f32 / v_log_f32 each, ~1 ulp), without
 // branches: both sides of torch's threshold (x > 20 -> x) and of the small-value series are formed
 // and selected, so no exec-mask branching sits in the token loops.  NaN propagates.
+// The in-op L2 norm of the isotropic scan (FLA l2norm_fwd, iso_kdn_chunk.py:2203-2204): the scan
+// consumes y = bf16(x rstd), rstd = 1 / sqrt(sum x^2 + 1e-6), per 128- or 64-channel row.  Kernels
+// that take the raw bf16 q, k with their rows' rstd form y at the load with l2n; kdn_l2norm_fwd forms
+// the same y (same expression, same rounding).
+constexpr float kL2NormEps = 1e-6f;
+__device__ __forceinline__ float l2n_rstd(float ss) { return 1.f / sqrtf(ss + kL2NormEps); }
+__device__ __forceinline__ float l2n(float x, float rs) { return bf2f(f2bf(x * rs)); }
+// The sum of squares of a row of 8 * NS channels given as NS runs of 8, in the order of
+// l2norm_fwd_vec_kernel: each run summed in order, then the runs pairwise (run s with s ^ 1, then
+// pairs of pairs, ...), the xor tree of its 8-channel lanes.  S[s] = sum of run s.
+template <int NS>
+__device__ __forceinline__ float l2n_tree(float* S) {
+#pragma unroll
+  for (int d = 1; d < NS; d <<= 1)
+#pragma unroll
+    for (int s = 0; s < NS; s += 2 * d) S[s] = S[s] + S[s + d];
+  return S[0];
+}
+__device__ __forceinline__ float l2n_run(const float* x) {  // one run of 8, summed in order
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+  return ss;
+}
 __device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * KDN_LOG2E); }
 // 2^x on the hardware exp2 (one v_exp_f32): results below 2^-126 flush towards zero, where exp2f
 // would produce denormals; every use multiplies it with O(1) terms, so the difference is below 1e-38.

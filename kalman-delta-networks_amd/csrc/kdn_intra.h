@@ -91,9 +91,11 @@ __device__ __forceinline__ void st8(bufrsrc r, uint32_t off, const float* f) {
 // Stages after the N / M build, shared by both kernels: the inverse A = (I + N)^{-1} from sN, A^T
 // saved to An, then U = A V and W = A (k 2^G) (rows past L dropped by the output descriptors).
 // The whole LDS buffer (sA / sN / sX) is free for this function's staging after the first barrier.
-template <int K, int V>
+// NORM (in-op L2 norm): k is raw in memory, sRk holds the rows' rstd.
+template <int K, int V, bool NORM>
 __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX, float* An, bufrsrc rv, bufrsrc rk,
-                                                 bufrsrc rG, bufrsrc rU, bufrsrc rW, int H, int tid) {
+                                                 bufrsrc rG, bufrsrc rU, bufrsrc rW, int H, int tid,
+                                                 const float* sRk) {
   const int lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
   // ---- 3. diagonal blocks of A: X_I = (I + N_II)^{-1}, lane j < 16 of wave I owns column j
   if (lane < 16) {
@@ -182,6 +184,11 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
         float g[8];
         unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, o * 2, 0, 0), x);
         ld8(rG, o * 4, g);
+        if constexpr (NORM) {
+          const float rs = sRk[sr];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) x[j] = l2n(x[j], rs);
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] *= fexp2(g[j]);
       }
@@ -233,13 +240,34 @@ __device__ __forceinline__ void intra_solve_emit(float* sA, float* sN, float* sX
   for (int t = w; t < K / 16; t += 4) tile(std::false_type{}, t);
 }
 
+// In-op L2 norm of a chunk row held by the four lane groups of a wave (lane group g4 = lane >> 4
+// holds channels 32 kb + 8 g4 .. + 7 as raw bf16): the row's rstd, its sum of squares taken in the
+// order of l2norm_fwd_vec_kernel (runs of 8 channels, then the xor tree: g4 ^ 1, g4 ^ 2 across lanes,
+// kb pairs in the lane), so it is bit-identical to that kernel's.
+template <int KB>
+__device__ __forceinline__ float row_rstd(const u32x4 (&raw)[KB]) {
+  float t[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    float x[8];
+    unpack8(raw[kb], x);
+    t[kb] = l2n_run(x);
+  }
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) t[kb] = t[kb] + __shfl_xor(t[kb], 16, 64);
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) t[kb] = t[kb] + __shfl_xor(t[kb], 32, 64);
+  return l2n_rstd(l2n_tree<KB>(t));
+}
+
 // grid (NT, B*H), block 256.
-template <int K, int V, bool ISO>
+template <int K, int V, bool ISO, bool NORM = false>
 __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags) {
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd = nullptr,
+    float* __restrict__ k_rstd = nullptr) {
   constexpr int KB = K / 32;
   // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
@@ -248,6 +276,7 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   constexpr int SBYTES = RABYTES + C * AP * 4 > C * XR * 4 ? RABYTES + C * AP * 4 : C * XR * 4;
   static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
   __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
+  __shared__ float sRk[C];  // in-op L2 norm: the rows' k rstd for the W stage
   bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
@@ -301,15 +330,49 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   const uint32_t crow = (uint32_t)(c * H);
   uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
   const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+  // with the in-op L2 norm (NORM) q, k are raw: this workgroup normalises its rows
+  float rsq = 1.f, rsk = 1.f;
+  u32x4 kraw[KB], qraw[KB];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      kraw[kb] = __builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + 32 * kb + 8 * g4) * 2, 0, 0);
+      qraw[kb] = __builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + 32 * kb + 8 * g4) * 2, 0, 0);
+    }
+    rsq = row_rstd<KB>(qraw);
+    rsk = row_rstd<KB>(kraw);
+    if (g4 == 0) {
+      buf_st(make_buf(q_rstd + in_row0, rows_in * 4), crow * 4, rsq);  // rows past L are dropped
+      buf_st(make_buf(k_rstd + in_row0, rows_in * 4), crow * 4, rsk);
+      sRk[c] = rsk;
+    }
+  }
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int i0 = 32 * kb + 8 * g4;
     float gcv[8], kv[8], qv[8], av[8];
-    const float* g0 = g0s[kb];
-    const float* gl = gls[kb];
+    float g0x[8], glx[8];
+    if constexpr (NORM) {  // rows 0 and L-1 again (cached): the raw q, k rows take their registers
+      ld8(rG, i0 * 4, g0x);
+      ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, glx);
+    }
+    const float* g0 = NORM ? g0x : g0s[kb];
+    const float* gl = NORM ? glx : gls[kb];
     ld8(rG, (crow * K + i0) * 4, gcv);
-    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
-    unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
+    if constexpr (NORM) {
+      unpack8(kraw[kb], kv);
+      unpack8(qraw[kb], qv);
+    } else {
+      unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
+      unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
+    }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kv[j] = l2n(kv[j], rsk);
+        qv[j] = l2n(qv[j], rsq);
+      }
+    }
     if (ISO) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) av[j] = beta * kv[j];
@@ -364,16 +427,17 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   }
   __syncthreads();
 
-  intra_solve_emit<K, V>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid);
+  intra_solve_emit<K, V, NORM>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid, sRk);
 }
 
 // grid (NT, B*H), block 256; a workgroup whose chunk intra_fwd_kernel did not flag exits at once.
-template <int K, int V, bool ISO>
+template <int K, int V, bool ISO, bool NORM = false>
 __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags) {
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd = nullptr,
+    float* __restrict__ k_rstd = nullptr) {
   constexpr int KB = K / 32;
   // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
@@ -382,6 +446,7 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   constexpr int SBYTES = RABYTES + C * AP * 4 > C * XR * 4 ? RABYTES + C * AP * 4 : C * XR * 4;
   static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
   __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
+  __shared__ float sRk[C];  // in-op L2 norm: the rows' k rstd for the W stage
   bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
@@ -436,6 +501,22 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   const uint32_t crow = (uint32_t)(c * H), grow = (uint32_t)(min(c, L - 1) * H);
   uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];  // k 2^{G - m_I}, scale q 2^{G - m_I} as split fragments
   const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+  float rsq = 1.f, rsk = 1.f;  // in-op L2 norm: this workgroup normalises its rows (as intra_fwd_kernel)
+  if constexpr (NORM) {
+    u32x4 kraw[KB], qraw[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      kraw[kb] = __builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + 32 * kb + 8 * g4) * 2, 0, 0);
+      qraw[kb] = __builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + 32 * kb + 8 * g4) * 2, 0, 0);
+    }
+    rsq = row_rstd<KB>(qraw);
+    rsk = row_rstd<KB>(kraw);
+    if (g4 == 0) {
+      buf_st(make_buf(q_rstd + in_row0, rows_in * 4), crow * 4, rsq);  // rows past L are dropped
+      buf_st(make_buf(k_rstd + in_row0, rows_in * 4), crow * 4, rsk);
+      sRk[c] = rsk;
+    }
+  }
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int i0 = 32 * kb + 8 * g4;
@@ -444,6 +525,13 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
     ld8(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4, gl);
     unpack8(__builtin_amdgcn_raw_buffer_load_b128(rk, (crow * K + i0) * 2, 0, 0), kv);
     unpack8(__builtin_amdgcn_raw_buffer_load_b128(rq, (crow * K + i0) * 2, 0, 0), qv);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kv[j] = l2n(kv[j], rsk);
+        qv[j] = l2n(qv[j], rsq);
+      }
+    }
     if (ISO) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) av[j] = beta * kv[j];
@@ -520,7 +608,7 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   }
   __syncthreads();
 
-  intra_solve_emit<K, V>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid);
+  intra_solve_emit<K, V, NORM>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid, sRk);
   if (tid == 0) flags[lin] = 0;
 }
 

@@ -125,10 +125,51 @@ struct QKStride {
   static constexpr int value = sizeof(TQK) == 2 ? K + 8 : K + 4;
 };
 
+// In-op L2 norm of a staged chunk of raw q or k rows (L rows, LDS stride KQ): with rs_out each row's
+// rstd is computed (sum of squares in the order of l2norm_fwd_vec_kernel) and written to rs_out,
+// else it is read from rs_in ([B,T,H], row c of the chunk at row0 + c H).  The staged values become
+// the scan's operand y = bf16(x rstd).  Ends with a barrier.
+template <int K, typename TQK>
+__device__ void l2n_staged(TQK* sX, int L, int64_t row0, int H, const float* __restrict__ rs_in,
+                           float* __restrict__ rs_out, float* sRs) {
+  constexpr int KQ = QKStride<K, TQK>::value;
+  const int tid = threadIdx.x;
+  if (tid < L) {
+    float rs;
+    if (rs_out) {
+      float S[K / 8];
+#pragma unroll
+      for (int r = 0; r < K / 8; ++r) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = lds_f(sX, tid * KQ + 8 * r + j);
+        S[r] = l2n_run(x);
+      }
+      rs = l2n_rstd(l2n_tree<K / 8>(S));
+      rs_out[row0 + (int64_t)tid * H] = rs;
+    } else {
+      rs = rs_in[row0 + (int64_t)tid * H];
+    }
+    sRs[tid] = rs;
+  }
+  __syncthreads();
+  for (int e = tid; e < L * K; e += 256) {
+    const int c = e / K, i = e - c * K;
+    const float y = l2n(lds_f(sX, c * KQ + i), sRs[c]);
+    if constexpr (sizeof(TQK) == 2) sX[c * KQ + i] = f2bf(y);
+    else sX[c * KQ + i] = y;
+  }
+  __syncthreads();
+}
+
+// Stage a chunk's g, kappa, k and (sQ non-null) q rows.  With the in-op L2 norm (iso scan) q and k
+// are raw: the forward (rs_out) normalises them and writes their rows' rstd, the backward (rs_in)
+// normalises them with the forward's.
 template <int K, bool ISO, typename TQK>
 __device__ void stage_chunk(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
                             const float* __restrict__ gc, int b, int h, int T, int H, int t0, int L, TQK* sQ,
-                            TQK* sK, float* sA, float* sG, float* sSpan) {
+                            TQK* sK, float* sA, float* sG, float* sSpan, const float* q_rs_in = nullptr,
+                            const float* k_rs_in = nullptr, float* q_rs_out = nullptr, float* k_rs_out = nullptr) {
   constexpr int KP = K + 4;
   constexpr int KQ = QKStride<K, TQK>::value;
   const int tid = threadIdx.x;
@@ -138,6 +179,12 @@ __device__ void stage_chunk(const bf16_t* __restrict__ q, const bf16_t* __restri
   stage_bf16<C, K, KQ>(k + base, stride, L, sK);
   if (sQ) stage_bf16<C, K, KQ>(q + base, stride, L, sQ);
   __syncthreads();
+  if (k_rs_in || k_rs_out) {
+    __shared__ float sRs[C];
+    const int64_t row0 = ((int64_t)b * T + t0) * H + h;
+    l2n_staged<K, TQK>(sK, L, row0, H, k_rs_in, k_rs_out, sRs);
+    if (sQ) l2n_staged<K, TQK>(sQ, L, row0, H, q_rs_in, q_rs_out, sRs);
+  }
   if (ISO) {  // kappa = beta k
     for (int e = tid; e < C * K; e += 256) {
       const int c = e / K, i = e - c * K;
@@ -242,7 +289,8 @@ __device__ void intra_fwd_exact_chunk(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, int n, int bh) {
+    float* __restrict__ Mg, float* __restrict__ Ag, int n, int bh, float* __restrict__ q_rstd,
+    float* __restrict__ k_rstd) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // sQ | sA are dead after Kf / Qg are written and are then reused for the solve's sX [C][XP]
@@ -258,7 +306,8 @@ __device__ void intra_fwd_exact_chunk(
   const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x;
-  stage_chunk<K, ISO, float>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
+  stage_chunk<K, ISO, float>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan, nullptr, nullptr, q_rstd,
+                             k_rstd);
   build_NM<K, true, true>(sQ, sK, sA, sG, sSpan, scale, sN, Mg + ((int64_t)bh * NT + n) * C * C);
   // Kf = kappa e^{g_last - g};  Qg = scale q e^g
   if (tid < 2 * K) {
@@ -332,12 +381,14 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, int NB, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, const int* __restrict__ flags) {
+    float* __restrict__ Mg, float* __restrict__ Ag, const int* __restrict__ flags, float* __restrict__ q_rstd,
+    float* __restrict__ k_rstd) {
   if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();  // LDS of the previous chunk is dead
-    intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, lin % NT, lin / NT);
+    intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, lin % NT, lin / NT,
+                                     q_rstd, k_rstd);
   }
 }
 
@@ -351,7 +402,7 @@ __device__ void bwd_solve_exact_chunk(
     const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, bf16_t* __restrict__ dv, float* __restrict__ dKg,
-    float* __restrict__ dNg, int n, int bh) {
+    float* __restrict__ dNg, int n, int bh, const float* __restrict__ k_rstd) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // phase 1: sK | sA | sG (3 x C x KP); phase 2 (after the solve) reuses it as sX | sUW (2 x C x XP)
@@ -366,7 +417,8 @@ __device__ void bwd_solve_exact_chunk(
   const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  stage_chunk<K, ISO, float>(nullptr, k, kap, gc, b, h, T, H, t0, L, (float*)nullptr, sK, sA, sG, sSpan);
+  stage_chunk<K, ISO, float>(nullptr, k, kap, gc, b, h, T, H, t0, L, (float*)nullptr, sK, sA, sG, sSpan, nullptr,
+                             k_rstd);
   build_NM<K, false, false>(nullptr, sK, sA, sG, sSpan, 0.f, sN, nullptr);
   __syncthreads();  // sK / sA / sG are dead from here on; sX reuses their space
   float* sX = sBuf;
@@ -445,12 +497,12 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_exact_kernel(
     const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, int NB, const int* __restrict__ flags, bf16_t* __restrict__ dv,
-    float* __restrict__ dKg, float* __restrict__ dNg) {
+    float* __restrict__ dKg, float* __restrict__ dNg, const float* __restrict__ k_rstd) {
   if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
-    bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, lin % NT, lin / NT);
+    bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, lin % NT, lin / NT, k_rstd);
   }
 }
 
@@ -467,7 +519,7 @@ __device__ void bwd_contrib_exact_chunk(
     const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
     const float* __restrict__ dgl, int T, int H, int NT, float scale, bf16_t* __restrict__ dq,
     bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, int n,
-    int bh) {
+    int bh, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd) {
   constexpr int KP = K + 4;
   constexpr int NCT = K / 16;  // channel tiles
   constexpr int KQ = QKStride<K, bf16_t>::value;
@@ -481,7 +533,7 @@ __device__ void bwd_contrib_exact_chunk(
   const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  stage_chunk<K, ISO, bf16_t>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan);
+  stage_chunk<K, ISO, bf16_t>(q, k, kap, gc, b, h, T, H, t0, L, sQ, sK, sA, sG, sSpan, q_rstd, k_rstd);
   stage_f32<C, C, NS>(dNg + ((int64_t)bh * NT + n) * C * C, C, C, sDN);
   stage_f32<C, C, NS>(dMg + ((int64_t)bh * NT + n) * C * C, C, C, sDM);
   for (int e = tid; e < 4 * K; e += 256) sColPart[e] = 0.f;
@@ -632,18 +684,19 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
     const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
     const float* __restrict__ dgl, int T, int H, int NT, int NB, const int* __restrict__ flags, float scale,
     bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
-    float* __restrict__ dg) {
+    float* __restrict__ dg, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd) {
   if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
     bwd_contrib_exact_chunk<K, V, ISO>(q, k, kap, gc, dNg, dMg, dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap,
-                                       dbeta, dg, lin % NT, lin / NT);
+                                       dbeta, dg, lin % NT, lin / NT, q_rstd, k_rstd);
   }
 }
 
 // The in-op L2 norm's backward for the rows of the flagged chunks (whose dq, dk the exact kernel
-// above wrote for the normalised operands y = q, k): dx = rstd (dy - y (y . dy)), in place.
+// above wrote for the normalised operands y = bf16(x rstd) of the raw q, k): dx = rstd (dy - y (y . dy)),
+// in place.
 // One wave per row (K / 64 elements per lane); a row is read whole before it is written.
 template <int K>
 __global__ __launch_bounds__(256) void l2norm_bwd_flagged_kernel(
@@ -667,7 +720,7 @@ __global__ __launch_bounds__(256) void l2norm_bwd_flagged_kernel(
       float y[PL], g[PL], dot = 0.f;
 #pragma unroll
       for (int j = 0; j < PL; ++j) {
-        y[j] = bf2f(x[row * K + lane + 64 * j]);
+        y[j] = l2n(bf2f(x[row * K + lane + 64 * j]), rs);
         g[j] = bf2f(d[row * K + lane + 64 * j]);
         dot += y[j] * g[j];
       }
@@ -859,7 +912,7 @@ int run_state_pass(int BH, GroupCount gc, float* grp, bool reverse, hipStream_t 
 template <int K, int V>
 int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, const bf16_t* v, const float* gc, int B,
                  int T, int H, float scale, const float* h0, float* saved, float* ht, void* o, int o_bf16,
-                 int stages, hipStream_t stream) {
+                 float* q_rstd, float* k_rstd, int stages, hipStream_t stream) {
   const int NT = cdiv(T, C);
   MemLayout lay(B, T, H, K, V);
   float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg, *M = saved + lay.M,
@@ -872,21 +925,22 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   dim3 gchunk(NT, B * H);
   if (stages & 1) {
     const int NB = B * H * NT, gx = min(NB, 512);
-    if (iso) {
-      hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc, T,
-                         H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
-      hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, true>), gchunk, dim3(256), 0, stream, q, k, kap,
-                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
-      hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
-                         T, H, NT, NB, scale, U, W, Kf, Qg, M, Asave, flags);
-    } else {
-      hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap, v, gc,
-                         T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
-      hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, false>), gchunk, dim3(256), 0, stream, q, k, kap,
-                         v, gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags);
-      hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc,
-                         T, H, NT, NB, scale, U, W, Kf, Qg, M, Asave, flags);
-    }
+    // the in-op L2 norm (q_rstd given) is a template variant: its row loads would otherwise cost the
+    // plain kernels registers
+#define KDN_INTRA(ISO_, NORM_)                                                                                       \
+  do {                                                                                                               \
+    hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, stream, q, k, kap, v, \
+                       gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                          \
+    hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, stream, q, k,   \
+                       kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                  \
+    hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, ISO_>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc, T, \
+                       H, NT, NB, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                             \
+  } while (0)
+    if (iso && q_rstd) KDN_INTRA(true, true);
+    else if (iso) KDN_INTRA(true, false);
+    else if (q_rstd) KDN_INTRA(false, true);
+    else KDN_INTRA(false, false);
+#undef KDN_INTRA
     KDN_CHECK_LAUNCH();
   }
   auto launch_ro = [&](dim3 grid, const kdn_state::GroupPlan& P, float* hstore, float* dstore) {
@@ -1027,20 +1081,20 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     const int NB = B * H * NT, gx = min(NB, 512);
     if (iso)
       hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD, dW,
-                         U, W, T, H, NT, NB, flags, dv, dKg, dN);
+                         U, W, T, H, NT, NB, flags, dv, dKg, dN, k_rstd);
     else
       hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD,
-                         dW, U, W, T, H, NT, NB, flags, dv, dKg, dN);
+                         dW, U, W, T, H, NT, NB, flags, dv, dKg, dN, k_rstd);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 8) {  // the exact path's gradients
     const int NB = B * H * NT, gx = min(NB, 512);
     if (iso)
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc, dN,
-                         dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
+                         dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg, q_rstd, k_rstd);
     else
       hipLaunchKernelGGL((mem_bwd_contrib_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc,
-                         dN, dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg);
+                         dN, dM, dQg, dKg, dKf, dgl, T, H, NT, NB, flags, scale, dq, dk, dkap, dbeta, dg, q_rstd, k_rstd);
     KDN_CHECK_LAUNCH();
     if (q_rstd) {  // the in-op norm's backward for the flagged chunks' rows
       hipLaunchKernelGGL((l2norm_bwd_flagged_kernel<K>), dim3(gx), dim3(256), 0, stream, q, k, q_rstd, k_rstd, T, H,
@@ -1073,15 +1127,16 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V) {
 
 int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const uint16_t* v,
                 const float* g_cumsum, int B, int T, int H, int K, int V, float scale, const float* initial_state,
-                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, int stages,
-                hipStream_t stream) {
+                void* saved, size_t saved_bytes, float* final_state, void* o, int o_bf16, float* q_rstd,
+                float* k_rstd, int stages, hipStream_t stream) {
   if (B <= 0 || T <= 0 || H <= 0) return KDN_ERR_ARG;
   if (!((K == 64 || K == 128) && (V == 64 || V == 128))) return KDN_ERR_ARG;
   if (saved_bytes < kdn_mem_saved_size(B, T, H, K, V)) return KDN_ERR_ARG;
+  if ((q_rstd == nullptr) != (k_rstd == nullptr)) return KDN_ERR_ARG;
   float* sv = (float*)saved;
 #define KDN_MEM_FWD(KK, VV) \
   return mem_fwd_impl<KK, VV>(q, k, kappa_or_beta, iso, v, g_cumsum, B, T, H, scale, initial_state, sv, final_state, o, \
-                              o_bf16, stages, stream)
+                              o_bf16, q_rstd, k_rstd, stages, stream)
   if (K == 128 && V == 128) KDN_MEM_FWD(128, 128);
   if (K == 64 && V == 64) KDN_MEM_FWD(64, 64);
   if (K == 128 && V == 64) KDN_MEM_FWD(128, 64);

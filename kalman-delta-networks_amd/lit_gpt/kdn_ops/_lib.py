@@ -41,7 +41,7 @@ _SIGS = {
     "kdn_mem_state_groups": "iiiii",
     "kdn_mem_saved_size": "iiiii",
     "kdn_mem_bwd_workspace_size": "iiiii",
-    "kdn_mem_fwd": "pppippiiiiifppzppiis",
+    "kdn_mem_fwd": "pppippiiiiifppzppippis",
     "kdn_mem_bwd": "pppipiiiiifpippzpzpppppppppis",
     "kdn_mem_step": "pppipipiiiifppis",
     "kdn_kalman_step": "pppipppppppiiiiiffppis",

@@ -27,10 +27,13 @@ BWD_STAGES_OVERLAP = ((3, "mem_state_chunk_bwd"), (12, "mem_bwd_exact"))
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
-            output_final_state=False, out_dtype=torch.float32, need_backward=True):
+            output_final_state=False, out_dtype=torch.float32, need_backward=True, q_rstd=None, k_rstd=None):
     """q, k, v bf16 [B,T,H,*]; kappa [B,T,H,K] f32 (diag) or beta [B,T,H] f32 (iso).
     Returns (o, saved, final_state or None); with ``need_backward=False`` saved is not usable by
-    mem_bwd (the intermediates only the backward reads are skipped)."""
+    mem_bwd (the intermediates only the backward reads are skipped).
+
+    With ``q_rstd`` / ``k_rstd`` (f32 [B,T,H] outputs, the in-op L2 norm) q and k are the raw inputs:
+    the scan normalises their rows as kdn_l2norm_fwd would and writes the rows' rstd for mem_bwd."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device
@@ -43,7 +46,8 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
     for bit, tag in FWD_STAGES:
         _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(v),
                   _lib.ptr(g_cumsum), B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(),
-                  _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), bit | extra, stream, tag=tag)
+                  _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), _lib.ptr(q_rstd), _lib.ptr(k_rstd), bit | extra,
+                  stream, tag=tag)
     return o, saved, ht
 
 
@@ -55,8 +59,8 @@ def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do
     ``overlap`` (default: unless a KernelTimer is timing each kernel) launches the reverse pass and
     the chunk backward in one call, which overlaps them where the shape allows.
 
-    With ``q_rstd`` / ``k_rstd`` [B,T,H] (the in-op L2 norm) q and k are the raw bf16 inputs whose
-    normalised values the forward took, and dq, dk are the gradients of the raw inputs."""
+    With ``q_rstd`` / ``k_rstd`` [B,T,H] (the in-op L2 norm, as mem_fwd wrote them) q and k are the
+    raw bf16 inputs the forward normalised, and dq, dk are the gradients of the raw inputs."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device

@@ -359,18 +359,19 @@ def _l2norm_bwd(x, rstd, dy):
 
 
 def _chunk_kda_fwd_precum(q, k, v, g_cumsum, beta, scale, *, initial_state=None, output_final_state=False,
-                          out_dtype=torch.bfloat16, need_backward=True):
+                          out_dtype=torch.bfloat16, need_backward=True, q_rstd=None, k_rstd=None):
     """Memory scan forward on normalised bf16 q, k (reference :2037-2086); kappa = beta k.  With
-    need_backward=False the returned saved buffer cannot feed _chunk_kda_bwd_precum."""
+    need_backward=False the returned saved buffer cannot feed _chunk_kda_bwd_precum.  With q_rstd /
+    k_rstd (f32 [B,T,H], filled here) q, k are raw and the scan applies the in-op L2 norm itself."""
     return _memscan.mem_fwd(q, k, beta, True, v, g_cumsum, scale, initial_state=initial_state,
                             output_final_state=output_final_state, out_dtype=out_dtype,
-                            need_backward=need_backward)
+                            need_backward=need_backward, q_rstd=q_rstd, k_rstd=k_rstd)
 
 
 def _chunk_kda_bwd_precum(q, k, v, g_cumsum, beta, saved, scale, do, *, d_final_state=None,
                           need_initial_state_grad=False, q_rstd=None, k_rstd=None):
     """Memory scan backward (reference :2089-2187): natural-log dg, no reverse cumsum.  With q_rstd /
-    k_rstd (the in-op L2 norm's, q and k still the normalised operands) dq, dk are returned for the
+    k_rstd (the in-op L2 norm's, from the forward; q and k the raw inputs) dq, dk are returned for the
     raw inputs, the norm's backward included."""
     return _memscan.mem_bwd(q, k, beta, True, v, g_cumsum, saved, scale, do, d_final_state=d_final_state,
                             need_initial_state_grad=need_initial_state_grad, q_rstd=q_rstd, k_rstd=k_rstd)
@@ -380,23 +381,36 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
     """Reference iso_kdn_chunk.py:2190-2238: L2-normalise q, k inside; memory scan; VJPs.  With an
     initial state h0 [B,H,K,V] and / or the final state requested, their gradients flow too.
 
-    For bf16 q, k the norm's backward runs inside the scan's backward kernel (kdn_mem_bwd with the
-    forward's rstd, y = the normalised bf16 operands); fp32 q, k keep the separate kdn_l2norm_bwd."""
+    For bf16 q, k the norm runs inside the scan: the forward normalises the rows of the raw q, k as
+    it loads them and writes their rstd, and the backward forms the normalised operands again and
+    applies the norm's backward in its kernel.  fp32 q, k keep kdn_l2norm_fwd / kdn_l2norm_bwd."""
 
     @staticmethod
     def forward(ctx, q, k, v, g_cumsum, beta, scale, initial_state=None, output_final_state=False):
         dev = q.device
+        ctx.fused_norm = q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
         with torch.cuda.device(dev):
-            qn, q_rstd = _l2norm_fwd(q)
-            kn, k_rstd = _l2norm_fwd(k)
             vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
-            o, saved, ht = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
-                                                 initial_state=initial_state, output_final_state=output_final_state,
-                                                 out_dtype=q.dtype if q.dtype == torch.float32 else torch.bfloat16,
-                                                 need_backward=any(ctx.needs_input_grad))
-        ctx.fused_norm = q.dtype == torch.bfloat16
+            out_dtype = q.dtype if q.dtype == torch.float32 else torch.bfloat16
+            if ctx.fused_norm:
+                q = q.contiguous()
+                k = k.contiguous()
+                q_rstd = torch.empty(q.shape[:-1], device=dev, dtype=torch.float32)
+                k_rstd = torch.empty(k.shape[:-1], device=dev, dtype=torch.float32)
+                o, saved, ht = _chunk_kda_fwd_precum(q, k, vb.contiguous(), g_cumsum, beta, scale,
+                                                     initial_state=initial_state,
+                                                     output_final_state=output_final_state, out_dtype=out_dtype,
+                                                     need_backward=any(ctx.needs_input_grad), q_rstd=q_rstd,
+                                                     k_rstd=k_rstd)
+            else:
+                qn, q_rstd = _l2norm_fwd(q)
+                kn, k_rstd = _l2norm_fwd(k)
+                o, saved, ht = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
+                                                     initial_state=initial_state,
+                                                     output_final_state=output_final_state, out_dtype=out_dtype,
+                                                     need_backward=any(ctx.needs_input_grad))
         if ctx.fused_norm:
-            ctx.save_for_backward(qn, q_rstd, kn, k_rstd, vb, g_cumsum, beta, saved)
+            ctx.save_for_backward(q, q_rstd, k, k_rstd, vb, g_cumsum, beta, saved)
         else:
             ctx.save_for_backward(q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved)
         ctx.scale = scale
@@ -409,8 +423,8 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
         need_h0 = ctx.h0_dtype is not None and ctx.needs_input_grad[6]
         with torch.cuda.device(do.device):
             if ctx.fused_norm:
-                qn, q_rstd, kn, k_rstd, vb, g_cumsum, beta, saved = ctx.saved_tensors
-                dq, dk, dv, db, dg, dh0 = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do,
+                q, q_rstd, k, k_rstd, vb, g_cumsum, beta, saved = ctx.saved_tensors
+                dq, dk, dv, db, dg, dh0 = _chunk_kda_bwd_precum(q, k, vb, g_cumsum, beta, saved, ctx.scale, do,
                                                                 d_final_state=dht, need_initial_state_grad=need_h0,
                                                                 q_rstd=q_rstd, k_rstd=k_rstd)
             else:

@@ -1,6 +1,10 @@
-"""The isotropic scan's in-op L2 norm with its backward folded into the memory-scan backward
-(kdn_mem_bwd with q_rstd / k_rstd; reference iso_kdn_chunk.py:2190-2238, which normalises q and k
-inside the op and applies FLA's l2norm_bwd to dq, dk).
+"""The isotropic scan's in-op L2 norm folded into the memory scan: the forward normalises the raw
+q, k rows as it loads them and writes their rstd (kdn_mem_fwd with q_rstd / k_rstd), the backward
+forms the normalised operands again and applies the norm's backward in its kernel (kdn_mem_bwd with
+q_rstd / k_rstd); reference iso_kdn_chunk.py:2190-2238, which normalises q and k inside the op
+(FLA l2norm_fwd) and applies FLA's l2norm_bwd to dq, dk.
+
+* The forward's rstd and o are bit-identical to kdn_l2norm_fwd followed by the scan on its output.
 
 * Against the unfused composition on the same inputs -- kdn_l2norm_fwd, the scan backward on the
   normalised q, k, kdn_l2norm_bwd -- which the other memory-scan tests pin to the fp64 oracle: dv,
@@ -60,7 +64,13 @@ def test_fused_norm_backward_matches_composition_and_oracle(B, T, H, K, V, extre
                                                          need_initial_state_grad=True)
     dq = ik._l2norm_bwd(qg, q_rstd, dqn)
     dk = ik._l2norm_bwd(kg, k_rstd, dkn)
+    # the norm inside the scan forward writes the same rstd as kdn_l2norm_fwd (same sum order)
+    q_rs2 = torch.empty_like(q_rstd)
+    k_rs2 = torch.empty_like(k_rstd)
+    o3, _, _ = ik._chunk_kda_fwd_precum(qg, kg, vg, Gg, bg, scale, initial_state=h0g, q_rstd=q_rs2, k_rstd=k_rs2)
     torch.cuda.synchronize()
+    assert torch.equal(q_rs2, q_rstd) and torch.equal(k_rs2, k_rstd), "rstd differs from kdn_l2norm_fwd's"
+    assert torch.equal(o3, o2)
     assert torch.equal(o, o2)
     for name, a, b_ in (("dv", fused[2], dv), ("dbeta", fused[4], db), ("d initial state", fused[5], dh0)):
         assert torch.equal(a, b_), f"{name} differs from the unfused composition"
