@@ -601,6 +601,9 @@ def main():
                     help="time only the main variant's step and print its line (for profiling)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain copy of MIB MiB (PMC byte-counter calibration)")
+    ap.add_argument("--serial-schedule", action="store_true",
+                    help="launch every memory-scan kernel in its own call, no overlapped segments (for a "
+                         "profiler that averages per-kernel durations, as the bench's event-timed pass does)")
     ap.add_argument("--B", type=int, default=4)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--H", type=int, default=18)
@@ -618,6 +621,9 @@ def main():
         sys.exit(1)
     B, T, H, K = args.B, args.T, args.H, args.d
     main_v = args.variant
+    if args.serial_schedule:
+        from lit_gpt.kdn_ops import _memscan
+        _memscan.DEFAULT_OVERLAP = False
     if args.decode_only:
         line = run_decode(f"{main_v}_kdn_1.3B", max(args.steps, 20), args.warmup)
         print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B decode tokens/s")), flush=True)

@@ -24,6 +24,9 @@ BWD_STAGES = ((1, "mem_state_bwd"), (2, "mem_bwd_chunk"), (12, "mem_bwd_exact"))
 # bits 1 | 2 in one call: with one chunk group the reverse pass runs in segments and each finished
 # segment's chunk backward overlaps the next segment's pass on a second stream (same results)
 BWD_STAGES_OVERLAP = ((3, "mem_state_chunk_bwd"), (12, "mem_bwd_exact"))
+# the default of mem_bwd's ``overlap`` outside a KernelTimer (a profiler that averages per-kernel
+# durations wants every kernel in its own call)
+DEFAULT_OVERLAP = True
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
@@ -77,7 +80,7 @@ def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do
     do = do.contiguous()
     stream = _lib.stream_of(q)
     if overlap is None:
-        overlap = not _lib.timing()
+        overlap = DEFAULT_OVERLAP and not _lib.timing()
     for bit, tag in (BWD_STAGES_OVERLAP if overlap else BWD_STAGES):
         _lib.call("kdn_mem_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(g_cumsum),
                   B, T, H, K, V, float(scale), _lib.ptr(do), _lib.is_bf16(do), _lib.ptr(dht), _lib.ptr(saved),
