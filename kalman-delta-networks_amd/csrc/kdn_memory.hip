@@ -873,6 +873,13 @@ int side_queue(SideQueue** out) {
   *out = &q;
   return 0;
 }
+// true once this device's side queue exists
+inline bool side_ready() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  return g_side[dev].s != nullptr;
+}
 // `to` waits for the work enqueued on `from` so far
 inline int stream_wait(hipStream_t to, hipStream_t from, hipEvent_t ev) {
   hipError_t e = hipEventRecord(ev, from);
@@ -1040,7 +1047,11 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   };
   const int tasks = NT * B * H;
   bool overlapped = false;
-  if ((stages & 3) == 3 && bl.gc.NG == 1) {
+  // a stream under graph capture takes the overlapped schedule only once the side queue exists (it
+  // is made outside capture: stream and event creation are not capturable)
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return KDN_ERR_ARG;
+  if ((stages & 3) == 3 && bl.gc.NG == 1 && (cap == hipStreamCaptureStatusNone || side_ready())) {
     std::lock_guard<std::mutex> lock(g_side_mu);
     SideQueue* sq = nullptr;
     int rc = side_queue(&sq);

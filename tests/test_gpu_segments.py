@@ -67,3 +67,41 @@ def test_overlapped_backward_is_bit_identical(B, T, H, variant, extreme):
             assert torch.isfinite(a).all(), name
             assert torch.equal(a, b), f"{name}: overlapped schedule differs from the serial one"
     log("  bit-identical")
+
+
+def test_overlapped_backward_under_graph_capture():
+    """The overlapped backward captured into a HIP graph (the second stream forks from and joins the
+    capturing stream): every replay, with eager work and synchronisations between them, equals the
+    eager call bit for bit.  The side queue is made by the eager calls first; a first call inside
+    a capture takes the serial schedule instead (stream and event creation are not capturable)."""
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import _memscan
+    B, T, H, K = 4, 4096, 18, 128
+    assert _memscan.state_groups(B, T, H, K, K) == 1
+    log(f"case overlapped-bwd graph capture iso B={B} T={T} H={H}")
+    q, k, v, G, kap, do, dht = _inputs(dev, 3, B, T, H, K, K, False, False)
+    scale = K ** -0.5
+    _, saved, _ = _memscan.mem_fwd(q, k, kap, True, v, G, scale, out_dtype=torch.bfloat16)
+    call = lambda: _memscan.mem_bwd(q, k, kap, True, v, G, saved, scale, do, d_final_state=dht,  # noqa: E731
+                                    need_initial_state_grad=True, overlap=True)
+    eager = call()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call()
+    names = ("dq", "dk", "dv", "dbeta", "dg", "d initial state")
+    for rep in range(3):
+        noise = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+        again = call()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        for name, a, b, c in zip(names, eager, out, again):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager call"
+            assert torch.equal(a, c), f"{name}: eager call {rep} differs"
+    log("  replays bit-identical")
