@@ -114,10 +114,10 @@ def frontend_counts(variant: str, B: int, T: int, H: int, K: int):
             # q, k bf16 -> q_memory, k_memory bf16, two norms
             "diag_front_norm_fwd": 8 * E + 8 * N,
             # k bf16, k norm, retention, omega raw bf16, r raw bf16 -> g_cumsum, kappa f32
-            "diag_front_fwd": 14 * E + 6 * N,
+            "diag_front_fwd": 16 * E + 6 * N,  # with the even tokens' precisions saved for the backward
             # k, k norm, retention, omega raw, r raw, d g_cumsum, d kappa f32, d k_memory bf16
             #   -> dk, d retention raw, d omega raw bf16, d r raw
-            "diag_front_bwd": 22 * E + 8 * N,
+            "diag_front_bwd": 24 * E + 8 * N,  # ... which it reads
             # q bf16, q norm, d q_memory bf16 -> dq bf16
             "diag_front_norm_bwd": 6 * E + 4 * N,
         }

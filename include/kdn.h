@@ -144,8 +144,8 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
  * softplus(mu_param) [H] (mu_param non-null, initial_precision null, prec_mode 0) or an explicit
  * initial_precision [H] (prec_mode 0) or [B,H,K] (prec_mode 1).  Outputs g_cumsum and kappa
  * [B,T,H,K] f32; final_precision [B,H,K] nullable; saved (kdn_diag_front_saved_size bytes,
- * nullable for a forward-only call) keeps the per-16-token-tile entry precision the backward
- * replays.  K in {64, 128}, chunk a multiple of 16, 16-byte aligned arrays. */
+ * nullable for a forward-only call) keeps the precision entering every even token (per 16-token
+ * tile, fp32, half of a [B,T,H,K] tensor), from which the backward re-derives the odd tokens'.  K in {64, 128}, chunk a multiple of 16, 16-byte aligned arrays. */
 size_t kdn_diag_front_saved_size(int B, int T, int H, int K);
 size_t kdn_diag_front_workspace_size(int B, int T, int H, int K);
 int kdn_diag_front_fwd(const void* k_raw, int k_bf16, const float* k_norm, const uint16_t* retention_raw,

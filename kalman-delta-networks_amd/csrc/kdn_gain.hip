@@ -984,6 +984,8 @@ __device__ __forceinline__ uint32_t front_row(const GainTile& g, int T, int H, i
   return ((uint32_t)g.b * (uint32_t)T + (uint32_t)t) * (uint32_t)H + (uint32_t)g.h;
 }
 constexpr float kFloorLog = -13.815510557964274f;  // log(1e-6): the memory path's alpha floor
+constexpr int kPairs = kVecChunk / 2;  // token pairs of a tile (the saved precisions: one per even token)
+static_assert(kCPT == 4, "a thread's saved precisions are one float4");
 
 template <typename TX> __device__ __forceinline__ void ldk4(const TX* p, float* f);
 template <> __device__ __forceinline__ void ldk4<float>(const float* p, float* f) { ldcf(p, f); }
@@ -1153,7 +1155,7 @@ template <typename TX>
 __global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, const float* __restrict__ carry,
                                                               const float* __restrict__ tsum,
                                                               float* __restrict__ g_cumsum,
-                                                              float* __restrict__ kappa) {
+                                                              float* __restrict__ kappa, float* __restrict__ pe) {
   constexpr int NB = 4;
   const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
   if (!g.ok) return;
@@ -1179,6 +1181,9 @@ __global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, c
     for (int u = 0; u < NB; ++u) {
       if (t + u >= g.t1) break;
       const uint32_t row = front_row(g, a.T, a.H, t + u);
+      if (pe && ((t + u - g.t0) & 1) == 0)  // the precision entering an even token, for the backward
+        *reinterpret_cast<float4*>(off32(pe, ((sb + g.nt) * kPairs + ((t + u - g.t0) >> 1)) * (uint32_t)a.K + g.i0)) =
+            float4{p[0], p[1], p[2], p[3]};
       FrontTok tk;
       FrontSig unused;
       front_tok<false>(raw[u], rate, bias, tk, unused);
@@ -1201,43 +1206,29 @@ __global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, c
   }
 }
 
-// The backward passes need p_{t-1}, the precision entering each token, in reverse token order.  A
-// tile first replays its forward recurrence from its saved entry value and keeps the precision
-// entering every even token in LDS (kVecChunk / 2 float4 per thread, 8 KB per wave); the reverse
-// pass then takes the tokens in pairs (2q + 1, 2q) and re-derives the odd token's entry value with
-// one forward step of token 2q, whose inputs it computes anyway.
-constexpr int kPairs = kVecChunk / 2;
+// The backward passes need p_{t-1}, the precision entering each token, in reverse token order.  The
+// forward's emit pass saved the precision entering every even token of each tile (pe); a tile loads
+// its kVecChunk / 2 values into LDS (float4 per thread, 8 KB per wave), and the reverse pass takes
+// the tokens in pairs (2q + 1, 2q) and re-derives the odd token's entry value with one forward step
+// of token 2q, whose inputs it computes anyway.
 __device__ __forceinline__ float4 f4(const float* x) { return float4{x[0], x[1], x[2], x[3]}; }
 __device__ __forceinline__ void unf4(float4 v, float* x) { x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w; }
 
-template <typename TX>
-__device__ __forceinline__ void front_replay(const FrontArgs<TX>& a, const GainTile& g, float rate, const float* bias,
-                                             const float* carry, float4 (*lp)[256]) {
-  constexpr int NB = 4;
-  const int L = g.t1 - g.t0;
-  float p[kCPT];
-  ldcf(off32(carry, (((uint32_t)g.b * a.H + g.h) * a.NV + g.nt) * (uint32_t)a.K + g.i0), p);
-  for (int t = 0; t < L; t += NB) {
-    FrontRaw<TX> raw[NB];
+__device__ __forceinline__ void front_pe_load(const float* __restrict__ pe, const GainTile& g, int H, int NV, int K,
+                                              float4 (*lp)[256]) {
+  const int np = (g.t1 - g.t0 + 1) >> 1;
+  const uint32_t tile = ((uint32_t)g.b * H + g.h) * NV + g.nt;
 #pragma unroll
-    for (int u = 0; u < NB; ++u) front_load(a, front_row(g, a.T, a.H, g.t0 + min(t + u, L - 1)), g.i0, raw[u]);
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      if (t + u >= L) break;
-      if ((u & 1) == 0) lp[(t + u) >> 1][threadIdx.x] = f4(p);  // t is a multiple of NB (even)
-      FrontTok tk;
-      FrontSig unused;
-      front_tok<false>(raw[u], rate, bias, tk, unused);
-      front_step(p, tk, a.s, p);
-    }
-  }
+  for (int q = 0; q < kPairs; ++q)
+    if (q < np)
+      lp[q][threadIdx.x] = *reinterpret_cast<const float4*>(off32(pe, (tile * kPairs + q) * (uint32_t)K + g.i0));
 }
 
 // Backward map (reverse over the tile): the affine adjoint map (A, B) per channel, the per-token
 // gain denominator D_t and G_t = sum_i dkappa_i p_hat_i k_i / D_t (saved for the emit pass), and the
 // tile's sum of the g_cumsum cotangent (for the emit pass's chunk-suffix sums).
 template <typename TX>
-__global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a, const float* __restrict__ carry,
+__global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a, const float* __restrict__ pe,
                                                                  const float* __restrict__ dkappa,
                                                                  const float* __restrict__ dG, float* __restrict__ ab,
                                                                  float* __restrict__ tdg, float* __restrict__ Gsave,
@@ -1249,7 +1240,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
   const float rate = __expf(a.A_log[g.h]);
   float bias[kCPT];
   ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
-  front_replay(a, g, rate, bias, carry, lp);
+  front_pe_load(pe, g, a.H, a.NV, a.K, lp);
   float Aacc[kCPT], Bacc[kCPT], sg[kCPT];
 #pragma unroll
   for (int j = 0; j < kCPT; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f, sg[j] = 0.f;
@@ -1317,7 +1308,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
 // k / max(||k||, 1e-12) applied to dk_gain + dk_memory (dk_memory nullable; dk nullable).
 template <typename TX>
 __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
-    FrontArgs<TX> a, const float* __restrict__ carry, const float* __restrict__ lcarry,
+    FrontArgs<TX> a, const float* __restrict__ pe, const float* __restrict__ lcarry,
     const float* __restrict__ dkappa, const float* __restrict__ dG, const float* __restrict__ tdg,
     const float* __restrict__ Gsave, const float* __restrict__ Dsave, const bf16_t* __restrict__ dk_mem,
     const float* __restrict__ prec0, int prec_mode, TX* __restrict__ dk, bf16_t* __restrict__ df,
@@ -1330,7 +1321,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
   const float rate = __expf(a.A_log[g.h]);
   float bias[kCPT];
   ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
-  front_replay(a, g, rate, bias, carry, lp);
+  front_pe_load(pe, g, a.H, a.NV, a.K, lp);
   const uint32_t sb = ((uint32_t)g.b * a.H + g.h) * a.NV;
   float lam[kCPT], accg[kCPT], ddt[kCPT], dA = 0.f;
   ldcf(off32(lcarry, (sb + g.nt) * (uint32_t)a.K + g.i0), lam);
@@ -1709,7 +1700,7 @@ FrontLayout front_layout(int B, int T, int H, int K) {
   L.ab = L.maps;
   L.tsum = o; o += al64(BHK * NV);       // forward tile log-decay sums; backward tile dG sums reuse it
   L.tdg = L.tsum;
-  L.carry = o; o += al64(BHK * NV);      // forward tile carries (when not saved); backward lambda carries
+  L.carry = o; o += al64(BHK * NV);      // forward tile carries; backward lambda carries
   L.lcarry = L.carry;
   L.grp = o; o += al64(BHK * NG * 5);    // two-level carry composites and start values
   L.G = o; o += al64((int64_t)B * T * H);
@@ -1747,7 +1738,7 @@ int front_fwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   const int NV = a.NV, tpb = 256 / (a.K / kCPT), bs = gain_block(a.K);
   float* maps = ws + L.maps;
   float* tsum = ws + L.tsum;
-  float* carry = saved ? saved : ws + L.carry;
+  float* carry = ws + L.carry;  // the tiles' entry precisions (saved: every even token's, for the backward)
   if (mu_param) prec0 = mu_param, prec_mode = 2;  // the kernels form mu = 0.1 + softplus(mu_param)
   const int Bc = front_batch_chunk(a.B, a.T, a.H, a.K);
   const int64_t ev = (int64_t)a.H * NV * a.K, ee = (int64_t)a.T * a.H * a.K;  // per batch row
@@ -1773,7 +1764,8 @@ int front_fwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   for (int b0 = 0; b0 < a.B; b0 += Bc) {
     const int nb = std::min(Bc, a.B - b0);
     hipLaunchKernelGGL((diag_front_emit_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
-                       front_shift(a, b0, nb), carry + b0 * ev, tsum + b0 * ev, g_cumsum + b0 * ee, kappa + b0 * ee);
+                       front_shift(a, b0, nb), carry + b0 * ev, tsum + b0 * ev, g_cumsum + b0 * ee, kappa + b0 * ee,
+                       saved ? saved + b0 * ev * kPairs : nullptr);
   }
   KDN_CHECK_LAUNCH();
   return 0;
@@ -1797,7 +1789,7 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   for (int b0 = 0; b0 < a.B; b0 += Bc) {
     const int nb = std::min(Bc, a.B - b0);
     hipLaunchKernelGGL((diag_front_bwd_map_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
-                       front_shift(a, b0, nb), saved + b0 * ev, d_kappa + b0 * ee, d_g_cumsum + b0 * ee,
+                       front_shift(a, b0, nb), saved + b0 * ev * kPairs, d_kappa + b0 * ee, d_g_cumsum + b0 * ee,
                        ab + b0 * ev * 2, tdg + b0 * ev, G + b0 * er, D + b0 * er);
   }
   if (NV > 2 * kCarryGroup) {  // two-level carry
@@ -1820,7 +1812,7 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
     const int nb = std::min(Bc, a.B - b0);
     const int64_t ep = prec_mode == 1 ? (int64_t)a.H * a.K : a.H;  // per batch row of [B,H,K] / [B,H]
     hipLaunchKernelGGL((diag_front_bwd_emit_kernel<TX>), dim3(cdiv((int64_t)nb * a.H * NV, tpb)), dim3(256), 0, stream,
-                       front_shift(a, b0, nb), saved + b0 * ev, lcarry + b0 * ev, d_kappa + b0 * ee,
+                       front_shift(a, b0, nb), saved + b0 * ev * kPairs, lcarry + b0 * ev, d_kappa + b0 * ee,
                        d_g_cumsum + b0 * ee, tdg + b0 * ev, G + b0 * er, D + b0 * er,
                        d_k_memory ? (const bf16_t*)d_k_memory + b0 * ee : nullptr,
                        prec_mode == 1 ? prec0 + b0 * ep : prec0, prec_mode,
@@ -1853,7 +1845,7 @@ extern "C" {
 
 size_t kdn_diag_front_saved_size(int B, int T, int H, int K) {
   if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return 0;
-  return (size_t)((int64_t)B * H * cdiv(T, kVecChunk) * K) * sizeof(float);
+  return (size_t)((int64_t)B * H * cdiv(T, kVecChunk) * kPairs * K) * sizeof(float);
 }
 
 size_t kdn_diag_front_workspace_size(int B, int T, int H, int K) {
