@@ -581,6 +581,11 @@ def calib_copy(mib: int):
     torch.cuda.synchronize()
 
 
+def _lib_size(name: str, *dims) -> int:
+    from lit_gpt.kdn_ops import _lib
+    return int(_lib.size(name, *dims))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -604,6 +609,9 @@ def main():
     ap.add_argument("--serial-schedule", action="store_true",
                     help="launch every memory-scan kernel in its own call, no overlapped segments (for a "
                          "profiler that averages per-kernel durations, as the bench's event-timed pass does)")
+    ap.add_argument("--backward-mode", choices=("save", "recompute"), default="save",
+                    help="what the memory scan's forward keeps for the backward (the headline uses 'save'; "
+                         "the full run reports 'recompute' beside it under also.recompute_backward)")
     ap.add_argument("--B", type=int, default=4)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--H", type=int, default=18)
@@ -621,9 +629,10 @@ def main():
         sys.exit(1)
     B, T, H, K = args.B, args.T, args.H, args.d
     main_v = args.variant
+    from lit_gpt.kdn_ops import _memscan
     if args.serial_schedule:
-        from lit_gpt.kdn_ops import _memscan
         _memscan.DEFAULT_OVERLAP = False
+    _memscan.set_backward_mode(args.backward_mode)
     if args.decode_only:
         line = run_decode(f"{main_v}_kdn_1.3B", max(args.steps, 20), args.warmup)
         print(json.dumps(dict(line, metric=f"{main_v}_kdn_1.3B decode tokens/s")), flush=True)
@@ -680,6 +689,17 @@ def main():
                                                  "fwd+bwd, bf16, same B/T/H/d",
                                      "kernels": run_layer_frontends(args.steps, args.warmup, B, T, H, K)}},
     }
+    if args.backward_mode == "save":
+        # the same steps with the reference's memory policy: the forward keeps only the op's inputs and
+        # the backward rebuilds the intra-chunk factors and per-chunk states first
+        _memscan.set_backward_mode("recompute")
+        rec = {v: run_variant(v, min(args.steps, 10), args.warmup, B, T, H, K)["ms_per_step"] for v in ("iso", "diag")}
+        _memscan.set_backward_mode("save")
+        line["also"]["recompute_backward"] = {
+            "ms_per_step": {v: round(x, 4) for v, x in rec.items()},
+            "tokens_per_s": {v: round(B * T / (x * 1e-3), 1) for v, x in rec.items()},
+            "saved_bytes_save_mode": _lib_size("kdn_mem_saved_size", B, T, H, K, K),
+            "note": "forward keeps the op's inputs only (no WY factors, A^T or per-chunk states); identical gradients"}
     if not args.no_config3:
         line["also"]["config3"] = run_config3(min(args.steps, 10), args.warmup)
     if not args.no_config4:

@@ -187,7 +187,11 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
  * caller can launch and time them one at a time; the stages must run in this order.  Bits 1 and 2
  * in one call run the state pass with the readout fused.  Bit 3 (with stages >= 0) declares that
  * no backward follows (inference, as under torch.no_grad): the intermediates only the backward
- * reads are then not written, and `saved` is scratch for this call alone.
+ * reads are then not written, and `saved` is scratch for this call alone.  A caller that keeps no
+ * `saved` from a training forward (the reference's policy: it re-runs recompute_w_u_fwd and the state
+ * forward in its backward, iso_kdn_chunk.py:2101-2140, diag_kdn_chunk.py:3271-3277) rebuilds it for
+ * kdn_mem_bwd with bit 0, then bit 1 alone (the state pass without the readout; o and final_state
+ * may be null): the same kernels on the same inputs write the same intermediates.
  * q_rstd / k_rstd [B,T,H] f32 (both or neither, outputs): the in-op L2 norm of
  * _chunk_kda_precumsum_paired (iso_kdn_chunk.py:2203-2204).  Given, q and k are the raw bf16 inputs;
  * the scan consumes y = bf16(x / sqrt(sum x^2 + 1e-6)) per row, exactly what kdn_l2norm_fwd (eps 1e-6)

@@ -5,6 +5,8 @@ kernels.  Shared by the iso (kappa = beta k) and diag (explicit kappa) operators
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -27,6 +29,35 @@ BWD_STAGES_OVERLAP = ((3, "mem_state_chunk_bwd"), (12, "mem_bwd_exact"))
 # the default of mem_bwd's ``overlap`` outside a KernelTimer (a profiler that averages per-kernel
 # durations wants every kernel in its own call)
 DEFAULT_OVERLAP = True
+
+
+# What a training forward keeps for its backward; both give bit-identical gradients.
+#  "save"       the intra-chunk WY factors, A^T and the per-chunk states h, delta (kdn_mem_saved_size
+#               bytes, ~4.1 KB per token-head at K = V = 128: 1.21 GB at B4 T4096 H18), so the backward
+#               starts at its own passes;
+#  "recompute"  only the op's inputs (and the in-op norm's rstd), as the reference's autograd functions
+#               keep them (iso_kdn_chunk.py:2206, diag_kdn_chunk.py:3253); the backward first rebuilds
+#               the intermediates per chunk (the intra-chunk build, then the forward state pass without
+#               its readout) before its own passes, as the reference re-runs recompute_w_u_fwd and the
+#               state forward (iso_kdn_chunk.py:2101-2140, diag_kdn_chunk.py:3271-3277).
+# The environment variable KDN_MEMORY_BACKWARD sets the mode a process starts with.
+BACKWARD_MODES = ("save", "recompute")
+_backward_mode = os.environ.get("KDN_MEMORY_BACKWARD", "save")
+if _backward_mode not in BACKWARD_MODES:
+    raise ValueError(f"KDN_MEMORY_BACKWARD must be one of {BACKWARD_MODES}, got {_backward_mode!r}")
+
+
+def set_backward_mode(mode: str) -> str:
+    """Select what the memory scan's forward keeps for the backward; returns the previous mode."""
+    global _backward_mode
+    if mode not in BACKWARD_MODES:
+        raise ValueError(f"backward mode must be one of {BACKWARD_MODES}, got {mode!r}")
+    prev, _backward_mode = _backward_mode, mode
+    return prev
+
+
+def backward_mode() -> str:
+    return _backward_mode
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
@@ -52,6 +83,28 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
                   _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), _lib.ptr(q_rstd), _lib.ptr(k_rstd), bit | extra,
                   stream, tag=tag)
     return o, saved, ht
+
+
+def rebuild_saved(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
+                  fused_norm=False):
+    """The buffer mem_fwd(need_backward=True) returns as ``saved``, rebuilt from the op's inputs for
+    mem_bwd (the "recompute" backward mode): the intra-chunk build (stage bit 0) and the serial state
+    pass without the readout (bit 1), on the same kernels as the forward, so every intermediate is
+    bit-identical to the forward's.  With ``fused_norm`` q and k are the raw inputs of the in-op L2
+    norm; the rows' rstd it writes again go to scratch (the forward's are the ones mem_bwd takes)."""
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    dev = q.device
+    saved = torch.empty((_lib.size("kdn_mem_saved_size", B, T, H, K, V),), device=dev, dtype=torch.uint8)
+    h0 = initial_state.float().contiguous() if initial_state is not None else None
+    rs = torch.empty((2, B, T, H), device=dev, dtype=torch.float32) if fused_norm else None
+    stream = _lib.stream_of(q)
+    for bit, tag in ((1, "mem_intra_fwd"), (2, "mem_state_fwd")):
+        _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(v),
+                  _lib.ptr(g_cumsum), B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(),
+                  None, None, 0, _lib.ptr(rs[0]) if fused_norm else None,
+                  _lib.ptr(rs[1]) if fused_norm else None, bit, stream, tag=tag)
+    return saved
 
 
 def mem_bwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, saved, scale: float, do, *, d_final_state=None,

@@ -493,14 +493,17 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, kappa, v, g_cumsum, scale, initial_state, output_final_state, out_dtype=torch.float32):
-        # no input needs a gradient (inference): the intermediates only the backward reads are skipped
+        # no input needs a gradient (inference), or the "recompute" backward mode: the intermediates
+        # only the backward reads are skipped (in that mode the backward rebuilds them from the inputs)
         need_backward = any(ctx.needs_input_grad)
+        ctx.recompute = need_backward and _memscan.backward_mode() == "recompute"
         with torch.cuda.device(q.device):
             o, saved, ht = _memscan.mem_fwd(q, k, kappa, False, v, g_cumsum, scale, initial_state=initial_state,
                                             output_final_state=output_final_state, out_dtype=out_dtype,
-                                            need_backward=need_backward)
+                                            need_backward=need_backward and not ctx.recompute)
         if need_backward:
-            ctx.save_for_backward(q, k, kappa, v, g_cumsum, saved)
+            ctx.save_for_backward(q, k, kappa, v, g_cumsum, None if ctx.recompute else saved,
+                                  initial_state if ctx.recompute else None)
         ctx.scale = scale
         ctx.has_h0 = initial_state is not None
         ctx.set_materialize_grads(False)
@@ -511,7 +514,7 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, do, d_final_state=None):
-        q, k, kappa, v, g_cumsum, saved = ctx.saved_tensors
+        q, k, kappa, v, g_cumsum, saved, h0 = ctx.saved_tensors
         if do is None and d_final_state is None:
             return None, None, None, None, None, None, None, None, None
         B, T, H, K = q.shape
@@ -525,6 +528,8 @@ class _DiagKdnMemoryFunction(torch.autograd.Function):
             do = do.contiguous()
         need_h0 = ctx.has_h0 and ctx.needs_input_grad[6]
         with torch.cuda.device(dev):
+            if ctx.recompute:
+                saved = _memscan.rebuild_saved(q, k, kappa, False, v, g_cumsum, ctx.scale, initial_state=h0)
             dq, dk, dv, dkappa, dg, dh0 = _memscan.mem_bwd(q, k, kappa, False, v, g_cumsum, saved, ctx.scale, do,
                                                           d_final_state=d_final_state,
                                                           need_initial_state_grad=need_h0)

@@ -383,12 +383,18 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
 
     For bf16 q, k the norm runs inside the scan: the forward normalises the rows of the raw q, k as
     it loads them and writes their rstd, and the backward forms the normalised operands again and
-    applies the norm's backward in its kernel.  fp32 q, k keep kdn_l2norm_fwd / kdn_l2norm_bwd."""
+    applies the norm's backward in its kernel.  fp32 q, k keep kdn_l2norm_fwd / kdn_l2norm_bwd.
+
+    In the "recompute" backward mode (_memscan.set_backward_mode) the forward keeps only its inputs
+    and the rows' rstd, and the backward rebuilds the scan's intermediates first (same gradients)."""
 
     @staticmethod
     def forward(ctx, q, k, v, g_cumsum, beta, scale, initial_state=None, output_final_state=False):
         dev = q.device
         ctx.fused_norm = q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
+        need_backward = any(ctx.needs_input_grad)
+        ctx.recompute = need_backward and _memscan.backward_mode() == "recompute"
+        keep = need_backward and not ctx.recompute  # the forward's intermediates feed the backward
         with torch.cuda.device(dev):
             vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
             out_dtype = q.dtype if q.dtype == torch.float32 else torch.bfloat16
@@ -400,19 +406,20 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
                 o, saved, ht = _chunk_kda_fwd_precum(q, k, vb.contiguous(), g_cumsum, beta, scale,
                                                      initial_state=initial_state,
                                                      output_final_state=output_final_state, out_dtype=out_dtype,
-                                                     need_backward=any(ctx.needs_input_grad), q_rstd=q_rstd,
-                                                     k_rstd=k_rstd)
+                                                     need_backward=keep, q_rstd=q_rstd, k_rstd=k_rstd)
             else:
                 qn, q_rstd = _l2norm_fwd(q)
                 kn, k_rstd = _l2norm_fwd(k)
                 o, saved, ht = _chunk_kda_fwd_precum(qn, kn, vb.contiguous(), g_cumsum, beta, scale,
                                                      initial_state=initial_state,
                                                      output_final_state=output_final_state, out_dtype=out_dtype,
-                                                     need_backward=any(ctx.needs_input_grad))
+                                                     need_backward=keep)
+        saved = saved if keep else None
+        h0 = initial_state if ctx.recompute else None  # the state pass starts from it again
         if ctx.fused_norm:
-            ctx.save_for_backward(q, q_rstd, k, k_rstd, vb, g_cumsum, beta, saved)
+            ctx.save_for_backward(q, q_rstd, k, k_rstd, vb, g_cumsum, beta, saved, h0)
         else:
-            ctx.save_for_backward(q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved)
+            ctx.save_for_backward(q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved, h0)
         ctx.scale = scale
         ctx.h0_dtype = initial_state.dtype if initial_state is not None else None
         o = o if o.dtype == q.dtype else o.to(q.dtype)
@@ -423,12 +430,17 @@ class _ChunkKDAPrecumsumFunction(torch.autograd.Function):
         need_h0 = ctx.h0_dtype is not None and ctx.needs_input_grad[6]
         with torch.cuda.device(do.device):
             if ctx.fused_norm:
-                q, q_rstd, k, k_rstd, vb, g_cumsum, beta, saved = ctx.saved_tensors
+                q, q_rstd, k, k_rstd, vb, g_cumsum, beta, saved, h0 = ctx.saved_tensors
+                if ctx.recompute:
+                    saved = _memscan.rebuild_saved(q, k, beta, True, vb, g_cumsum, ctx.scale, initial_state=h0,
+                                                   fused_norm=True)
                 dq, dk, dv, db, dg, dh0 = _chunk_kda_bwd_precum(q, k, vb, g_cumsum, beta, saved, ctx.scale, do,
                                                                 d_final_state=dht, need_initial_state_grad=need_h0,
                                                                 q_rstd=q_rstd, k_rstd=k_rstd)
             else:
-                q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved = ctx.saved_tensors
+                q, q_rstd, qn, k, k_rstd, kn, vb, g_cumsum, beta, saved, h0 = ctx.saved_tensors
+                if ctx.recompute:
+                    saved = _memscan.rebuild_saved(qn, kn, beta, True, vb, g_cumsum, ctx.scale, initial_state=h0)
                 dqn, dkn, dv, db, dg, dh0 = _chunk_kda_bwd_precum(qn, kn, vb, g_cumsum, beta, saved, ctx.scale, do,
                                                                   d_final_state=dht, need_initial_state_grad=need_h0)
                 dq = _l2norm_bwd(q, q_rstd, dqn)
