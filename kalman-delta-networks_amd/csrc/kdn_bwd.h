@@ -673,9 +673,7 @@ __device__ __forceinline__ void chunk_bwd_task(
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) colpart[j] += __shfl_xor(colpart[j], m, 64);
+    for (int j = 0; j < 4; ++j) colpart[j] = row16_sum(colpart[j]);
     if (has_last) {
       const float4 gl4 = *reinterpret_cast<const float4*>(sDgl + i0);
       const float4 v = float4{dg_last.x + colpart[0] + gl4.x, dg_last.y + colpart[1] + gl4.y,
@@ -703,12 +701,12 @@ __device__ __forceinline__ void chunk_bwd_task(
           pk += yk[j] * dks[tl][j];
         }
       }
-#pragma unroll
-      for (int m = 16; m < 64; m <<= 1) {
-        v += __shfl_xor(v, m, 64);
-        pq += __shfl_xor(pq, m, 64);
-        pk += __shfl_xor(pk, m, 64);
-      }
+      v = swz16_add(v);
+      pq = swz16_add(pq);
+      pk = swz16_add(pk);
+      v += __shfl_xor(v, 32, 64);
+      pq += __shfl_xor(pq, 32, 64);
+      pk += __shfl_xor(pk, 32, 64);
       if (g4 == 0) {
         sBeta[w * C + 16 * tl + r16] = v;
         sDot[0][w][16 * tl + r16] = pq;

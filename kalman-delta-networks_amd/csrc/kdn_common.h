@@ -128,6 +128,28 @@ __device__ __forceinline__ void fsoftplus_sigmoid(float x, float& sp, float& sg)
 __device__ __forceinline__ float fsigmoid(float x) { return frcp(1.f + fexp(-x)); }
 
 // ---- wave64 reductions -----------------------------------------------------------
+// x + (x of lane ^ 1 or ^ 2) by a DPP quad permutation, or + (x of lane 7 - i in its 8-lane group /
+// 15 - i in its 16-lane row) by a DPP mirror, or + (x of lane ^ 16) by a swizzle: one instruction each,
+// no lane-index arithmetic and no LDS-crossbar round trip.  Every lane of the group must be active.
+// Used as the steps of an xor butterfly (x += x[lane ^ o], o = 1, 2, 4, 8, 16) they add the same values:
+// after the two quad steps all lanes of a quad hold the same sum, so the half-row mirror adds the same
+// partner as lane ^ 4 would, and after it the row mirror the same as lane ^ 8; the result is
+// bit-identical to the butterfly's.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swz16_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));  // and 31, xor 16
+}
+// the xor butterfly over the 16 lanes of a row (o = 1, 2, 4, 8), bit-identical to it
+__device__ __forceinline__ float row16_sum(float x) {
+  return dpp_add<kDppMirror>(dpp_add<kDppHalfMirror>(dpp_add<kDppXor2>(dpp_add<kDppXor1>(x))));
+}
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

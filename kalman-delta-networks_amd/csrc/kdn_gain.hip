@@ -566,25 +566,15 @@ __device__ __forceinline__ void stc_bf16(bf16_t* p, const float* f) {
   *reinterpret_cast<uint2*>(p) = uint2{(uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16),
                                        (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16)};
 }
-// x + (x of lane ^ 1 or ^ 2) by a DPP quad permutation, or + (x of lane 7 - i in its 8-lane group /
-// 15 - i in its 16-lane row) by a DPP mirror, or + (x of lane ^ 16) by a swizzle: one instruction each,
-// no lane-index arithmetic.  Every lane of the group must be active.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float x) {
-  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float swz16_add(float x) {
-  return x + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));  // and 31, xor 16
-}
 // Sum over the tpt (a power of two <= 64) consecutive lanes of a tile, all of them active, every lane
 // getting the total.  The same additions as the xor butterfly x += x[lane ^ o], o = 1, 2, 4, ...: after
 // the quad steps all lanes of a quad hold the same value, so the mirrors add the same partner sums as
 // lane ^ 4 and lane ^ 8 would, and the result is bit-identical to the butterfly's.
 __device__ __forceinline__ float tile_sum(float x, int tpt) {
-  if (tpt >= 2) x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
-  if (tpt >= 4) x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
-  if (tpt >= 8) x = dpp_add<0x141>(x);  // row_half_mirror
-  if (tpt >= 16) x = dpp_add<0x140>(x); // row_mirror
+  if (tpt >= 2) x = dpp_add<kDppXor1>(x);
+  if (tpt >= 4) x = dpp_add<kDppXor2>(x);
+  if (tpt >= 8) x = dpp_add<kDppHalfMirror>(x);
+  if (tpt >= 16) x = dpp_add<kDppMirror>(x);
   if (tpt >= 32) x = swz16_add(x);
   if (tpt >= 64) x += __shfl_xor(x, 32, 64);
   return x;
