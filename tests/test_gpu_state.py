@@ -16,7 +16,7 @@
 * Layers in training mode under bf16 autocast: two differentiable segments with the state carried
   between them, output and every gradient (crossing the carried memory, precision and convolution
   inputs) against the GPU run of the whole sequence at 1e-2 and against the autocast oracle at
-  max(2e-2, 1.5 x the oracle's own autocast effect).
+  2e-2 (the oracle rounds bf16 cotangents as autograd does).
 * GPT: prefill then decode under no_grad against the oracle GPT of the whole sequence.
 """
 import math
