@@ -275,7 +275,6 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
   constexpr int ST = K / 16;           // state row tiles per wave
   static_assert((C * K / 4) % NTHR == 0, "staging units per thread");
   constexpr int UN = C * K / 4 / NTHR;  // staging units per thread of a C x K operand
-  constexpr int UM = C * C / 4 / NTHR;  // ... of the C x C readout matrix M
   __shared__ __attribute__((aligned(16))) bf16_t sW[(C / 16) * KB * TILE];        // W: rows c, k = i
   __shared__ __attribute__((aligned(16))) bf16_t sK[(K / 16) * (C / 32) * TILE];  // Kf^T: rows i, k = c
   __shared__ __attribute__((aligned(16))) float sE[K];
