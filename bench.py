@@ -124,6 +124,37 @@ def frontend_counts(variant: str, B: int, T: int, H: int, K: int):
     return {k: (b, 0) for k, b in per.items()}
 
 
+# The scope's own per-unit figures for the kernels it prices (per token-head, d = K = V, C = 64):
+# the chunk backward carries the whole backward's minimum I/O (iso 22d+16, diag 30d+8), the state pass
+# reads w, u, kg and writes v_new plus one state per chunk (16d + 4d^2/C).  A kernel the scope gives
+# no byte figure for falls back to its decomposition bytes.
+S8D_BYTES = {"mem_bwd_chunk": {"iso": lambda d: 22 * d + 16, "diag": lambda d: 30 * d + 8},
+             "mem_state_readout_fwd": {"iso": lambda d: 16 * d + 4 * d * d / C,
+                                       "diag": lambda d: 16 * d + 4 * d * d / C}}
+
+
+def headline_roofline(variant: str, tag: str, kern: dict, B: int, T: int, H: int, K: int, traffic):
+    """The dominant kernel against MI355X's HBM peak, priced on the scope's algorithmic bytes for it
+    (S8D_BYTES per token-head times B*T*H) over its mean event-timed duration; the figure on this
+    decomposition's own bytes (kernel_counts) is kept beside it."""
+    t = kern["ms"] * 1e-3
+    per = S8D_BYTES.get(tag, {}).get(variant)
+    out = {"kernel": tag, "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "traffic": traffic,
+           "traffic_source": (os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None),
+           "kernel_ms": kern["ms"]}
+    if per is not None:
+        nbytes = per(K) * B * T * H
+        out.update(achieved=round(nbytes / t / 1e9, 2), frac=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                   alg_bytes=int(nbytes), bytes_per_token_head=per(K),
+                   basis="scope minimum bytes (backward minimum for the chunk backward)")
+    else:
+        out.update(achieved=kern["achieved"], frac=kern["frac"], alg_bytes=kern["alg_bytes"],
+                   basis="decomposition bytes")
+    out["decomposition"] = {"alg_bytes": kern["alg_bytes"], "achieved": kern["achieved"], "frac": kern["frac"],
+                            "note": "this build's own reads and writes for the kernel (inputs once, outputs once)"}
+    return out
+
+
 def op_roofline(variant: str, ms: float, B: int, T: int, H: int, K: int):
     """The whole op against its HBM floor: the minimum I/O bytes of the mixer scan fwd+bwd (OP_BYTES per
     token-head times B*T*H) over the measured step time."""
@@ -652,6 +683,8 @@ def main():
             calib_copy(args.calib_copy)
         print(json.dumps({"metric": METRIC, "value": round(res["tokens_per_s"], 1), "unit": "tokens/s",
                           "ms_per_step": round(res["ms_per_step"], 4), "steps": args.steps, "warmup": args.warmup,
+                          "roofline": headline_roofline(main_v, res["dominant"], res["kernels"][res["dominant"]],
+                                                        B, T, H, K, None),
                           "op_roofline": op_roofline(main_v, res["ms_per_step"], B, T, H, K),
                           "kernels": res["kernels"]}), flush=True)
         return
@@ -675,14 +708,15 @@ def main():
         "config": {"workload": f"{main_v}_kdn mixer scan fwd+bwd (frontend+gain+chunked memory, all input grads)",
                    "B": B, "T": T, "H": H, "d_k": K, "d_v": K, "chunk": C, "inputs": "bf16",
                    "state": "fp32", "parallelism": "single GPU"},
-        "roofline": {"kernel": res["dominant"], "bound": dom["bound"], "achieved": dom["achieved"],
-                     "peak": dom["peak"], "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,
-                     "traffic_source": (os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None)},
+        "roofline": headline_roofline(main_v, res["dominant"], dom, B, T, H, K, traffic),
         "op_roofline": op_roofline(main_v, res["ms_per_step"], B, T, H, K),
         "kernels": res["kernels"],
         "also": {f"{other}_kdn": {"value": round(res_other["tokens_per_s"], 1), "unit": "tokens/s",
                                   "ms_per_step": round(res_other["ms_per_step"], 4),
                                   "op_roofline": op_roofline(other, res_other["ms_per_step"], B, T, H, K),
+                                  "roofline": headline_roofline(other, res_other["dominant"],
+                                                                res_other["kernels"][res_other["dominant"]],
+                                                                B, T, H, K, None),
                                   "dominant": res_other["dominant"],
                                   "kernels": res_other["kernels"]},
                  "layer_frontends": {"workload": "packed q|k|v short conv + SiLU and sigmoid-gated RMS norm, "

@@ -2,9 +2,15 @@
  * kdn.h -- C ABI of the MI355X (gfx950) Kalman Delta Network scan library (libkdn_hip.so).
  *
  * Every entry point takes raw device pointers, plain sizes, and the hipStream_t to launch
- * on; it allocates nothing (the caller passes outputs and workspaces, sized by the
+ * on; it allocates no device memory (the caller passes outputs and workspaces, sized by the
  * *_size() queries) and returns 0 on success, KDN_ERR_ARG (-1) on a rejected argument,
- * or a positive hipError_t value from the launch.  Tensors are dense row-major:
+ * or a positive hipError_t value from the launch.  Every entry point launches only on
+ * `stream` and keeps no state between calls, with one exception: kdn_mem_bwd called with its
+ * stage bits 0 and 1 together may use its overlapped schedule, which also launches on a stream
+ * of the library's own and keeps that stream, two events and a mutex per device for the
+ * life of the process (its declaration below says when and how; calling the two stages
+ * separately keeps to `stream` alone).  kdn_iso_gain_fwd_noalloc keeps a fixed device
+ * array per GPU.  Tensors are dense row-major:
  *   [B,T,H,D]  token-major with heads interleaved (the reference layout),
  *   bf16 arguments are raw uint16_t bit patterns.
  * Dtype flags (*_bf16) select bf16 (1) or fp32 (0) for arguments typed void*.
@@ -68,7 +74,10 @@ int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const f
  * to 209,715, e.g. B = 182 at H = 18, T = 4096).  It calls no hipMalloc / hipFree.  The array belongs to
  * the current device, and `stream` must run on that device (else KDN_ERR_ARG).  Every call on one GPU
  * shares the array (each call writes all of the part it reads, so no clearing is needed): calls that
- * overlap in time on one GPU, e.g. on two streams, race and must be serialised by the caller. */
+ * overlap in time on one GPU, e.g. on two streams, race and must be serialised by the caller.  The
+ * first call on each device looks the array's address up (hipGetSymbolAddress) and must be made
+ * outside HIP graph capture; later calls may be captured, and every replay of such a graph uses the
+ * same array, so it too must not overlap another call on that GPU. */
 #define KDN_NOALLOC_SCRATCH_BYTES (4u << 20)
 int kdn_iso_gain_fwd_noalloc(const float* a, const float* omega, const float* r, const float* initial_precision,
                              int prec_mode, int B, int T, int H, float posterior_scale, float* beta, float* p_prev,
@@ -212,10 +221,18 @@ int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
  * `stages`: bit 0 reverse state pass, bit 1 the chunk-parallel backward, bits 2 and 3 the exact
  * path's solves and gradients for the chunks outside the factored range (-1 = all, in this order).
  * Bits 0 and 1 in one call, with one chunk group (kdn_mem_state_groups == 1), at least 16 chunks
- * and CUs the pass leaves idle: the reverse pass runs in two segments, and chunk-backward work of
- * the first segment's chunks runs beside the second on a stream of the library's own (one per
- * device, created on first use); the call returns with `stream` ordered after both, and the results
- * are identical to separate calls.  Calls on one device serialise their enqueue on a mutex. */
+ * and at least 32 CUs the pass leaves idle (the overlapped schedule): the reverse pass runs in two
+ * segments, and chunk-backward work of the first segment's chunks runs beside the second on a
+ * stream of the library's own.  That stream (non-blocking, default priority) and two events that
+ * order it against `stream` are created per device on the first such call made outside HIP graph
+ * capture, and kept until the process ends; a first call inside a capture takes the serial
+ * schedule.  The side stream's launch starts with a one-wave kernel that waits 3 us on the
+ * device's constant wall clock (a bounded wait, no memory access), so that the pass's second
+ * segment is dispatched onto the CUs the first segment frees before the side work takes them.
+ * Under capture the side stream forks from and joins the capturing stream.  The call returns with
+ * `stream` ordered after both streams' work, and the results are bit-identical to separate calls
+ * (bit 0, then bit 1), which launch on `stream` alone.  Calls on one device serialise their
+ * enqueue on a library mutex. */
 int kdn_mem_bwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta, int iso, const float* g_cumsum,
                 int B, int T, int H, int K, int V, float scale, const void* d_o, int do_bf16,
                 const float* d_final_state, const void* saved, size_t saved_bytes, void* workspace,

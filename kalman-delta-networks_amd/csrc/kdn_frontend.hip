@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_kernel(
   if (blockIdx.x < H && i == 0) mu_out[h] = 0.1f + softplusf(mu_param[h]);
 }
 
-// iso gate backward.  Writes per-tile partial sums; reduce_partials_kernel finishes them.
+// iso gate backward.  Writes per-tile partial sums; reduce_partials_multi_kernel finishes them.
 template <typename TG, typename TO>
 __global__ __launch_bounds__(256) void iso_gate_bwd_kernel(
     const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
@@ -334,16 +334,6 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     part_bias[(int64_t)p * 2 * H + h] = sO;
     part_bias[(int64_t)p * 2 * H + H + h] = sR;
   }
-}
-
-// out[j] = sum_p part[p * stride + j] for j < n, deterministic order.  grid ceil(n/256).
-__global__ void reduce_partials_kernel(const float* __restrict__ part, int NP, int64_t stride, int n,
-                                       float* __restrict__ out) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  float s = 0.f;
-  for (int p = 0; p < NP; ++p) s += part[(int64_t)p * stride + j];
-  out[j] = s;
 }
 
 __global__ void mu_fwd_kernel(const float* __restrict__ mu_param, int H, float* __restrict__ mu) {

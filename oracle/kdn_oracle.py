@@ -569,11 +569,12 @@ def swiglu(x, w1, w2, w3, amp: bool = False):
     return linear(amp_round(amp_round(F.silu(a), amp) * b, amp), w3, amp=amp)
 
 
-def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp=False):
+def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp=False, chunked=False):
     """IsotropicKalmanDeltaNetwork.forward (iso_kdn.py:262-314) on a state dict ``p`` of the
     layer (reference parameter names): packed q|k|v projection + per-group SiLU short
     convolution; [f0 | omega | r] packed projection, f_proj[1] on the f0 slice; iso_mixer;
-    sigmoid-gated RMS norm against g_proj(x); o_proj."""
+    sigmoid-gated RMS norm against g_proj(x); o_proj.  ``chunked`` runs the mixer's memory in the
+    WY chunk form (equal to the tokenwise form to rounding; faster at long T)."""
     H = p["A_log"].shape[0]
     Dm = p["qkv_pack.projection_weight"].shape[0] // 3
     K = Dm // H
@@ -588,7 +589,7 @@ def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp
     o = iso_mixer(q.view(B, T, H, K), k.view(B, T, H, K), v.view(B, T, H, K), g_raw.view(B, T, H, K),
                   omega_r_raw, p["omega_proj.bias"], p["r_proj.bias"], p["A_log"], p["dt_bias"],
                   p["initial_precision_param"], omega_min=omega_min, r_min=r_min, info_scale=info_scale,
-                  round_qk=amp)
+                  round_qk=amp, chunked=chunked)
     o = amp_round(o, amp)
     gate = linear(linear(x, p["g_proj.0.weight"], amp=amp), p["g_proj.1.weight"], p["g_proj.1.bias"], amp=amp)
     y = amp_round(rms_norm_gated(o, gate.view(B, T, H, K), p["o_norm.weight"], eps, "sigmoid"), amp)

@@ -15,7 +15,11 @@
 * The same workload split at T/2 with the memory and precision carried: equals the one-pass run
   (bf16 tensors at 1e-2, fp32 at 1e-3), every gradient finite, over all 72 heads.
 * Config 4 at full width (iso_kdn_1.3B: width 2304, 18 x 128 heads, vocab 32000) cut to two layers,
-  T = 256, fp32 eval mode, against the fp64 oracle GPT: logits and gradients at 2e-2.
+  fp32 eval mode, against the oracle GPT: logits and gradients at 2e-2, at T = 256 (fp64 oracle,
+  tokenwise memory) and at the config's T = 4096 (64 chunks per head inside the model; fp32 oracle
+  with the WY-chunked memory, which equals the tokenwise form to rounding on the CPU).
+* Config 4's workload itself: the whole 18-layer iso_kdn_1.3B in bf16 (eval) at B1 T4096.  Its logits
+  are finite, and one pass equals a 2048-token prefill continued from the 18 layer states (1e-2).
 """
 import math
 import pathlib
@@ -192,14 +196,20 @@ def test_full_shape_split_at_half_equals_one_pass(variant):
 
 # ---------------------------------------------------------------------------- config 4, full width
 
-def test_config4_full_width_two_layers_match_oracle():
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("T", [256, 4096])
+def test_config4_full_width_two_layers_match_oracle(T):
     dev = gpu_or_skip()
     from lit_gpt.config import Config
     from lit_gpt.model import GPT
-    B, T = 1, 256
+    B = 1
+    # at T = 4096 the oracle runs in fp32 with the WY-chunked memory (tens of seconds on the host
+    # instead of many minutes for the fp64 tokenwise loop)
+    long = T > 256
+    odt = torch.float32 if long else torch.float64
     cfg = Config.from_name("iso_kdn_1.3B", n_layer=2)
     log(f"case config-4 width {cfg.n_embd}, {cfg.n_head}x{cfg.head_size} heads, vocab {cfg.padded_vocab_size}, "
-        f"2 layers, B={B} T={T}, fp32 eval vs fp64 oracle")
+        f"2 layers, B={B} T={T}, fp32 eval vs {odt} oracle")
     torch.manual_seed(5)
     model = GPT(cfg)
     model.init_weights()
@@ -215,12 +225,46 @@ def test_config4_full_width_two_layers_match_oracle():
     grads = torch.autograd.grad(logits, [params[n] for n in names], dl.to(dev))
     torch.cuda.synchronize()
     logits, grads = logits.detach().cpu(), [x.cpu() for x in grads]
-    p_ref = {k: v.detach().cpu().double().requires_grad_(True) for k, v in model.state_dict().items()}
+    p_ref = {k: v.detach().cpu().to(odt).requires_grad_(True) for k, v in model.state_dict().items()}
     del model, params
     torch.cuda.empty_cache()
     torch.set_num_threads(max(1, min(16, torch.get_num_threads())))
-    logits_ref = ko.gpt_forward(p_ref, idx, n_layer=2, mixer_type="iso_kdn", info_scale=cfg.kdn_info_scale)
+    log("  GPU done; oracle forward on the host")
+    logits_ref = ko.gpt_forward(p_ref, idx, n_layer=2, mixer_type="iso_kdn", info_scale=cfg.kdn_info_scale,
+                                chunked=long)
     _check("logits", logits, logits_ref, TOL)
-    grads_ref = torch.autograd.grad((logits_ref * dl.double()).sum(), [p_ref[n] for n in names])
+    log("  oracle backward on the host")
+    grads_ref = torch.autograd.grad((logits_ref * dl.to(odt)).sum(), [p_ref[n] for n in names])
     for n, gg, gr in zip(names, grads, grads_ref):
         _check(f"d {n}", gg, gr, TOL)
+
+
+def test_config4_full_model_prefill_continuation():
+    """The config-4 workload (model.py:95-161, config.py:137-160): all 18 layers of the random-init
+    iso_kdn_1.3B in bf16, eval, B1 T4096.  The logits are finite, and the one-pass forward equals a
+    2048-token prefill whose 18 layer states (short-convolution tails, memory, precision) carry into
+    the second 2048 tokens."""
+    dev = gpu_or_skip()
+    from lit_gpt.model import GPT
+    B, T, T1 = 1, 4096, 2048
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = GPT.from_name("iso_kdn_1.3B")
+    model.init_weights()
+    model = model.to(torch.bfloat16).eval()
+    cfg = model.config
+    log(f"case config-4 workload: {cfg.n_layer} layers, width {cfg.n_embd}, bf16 eval, B={B} T={T}, "
+        f"split at {T1}")
+    g = torch.Generator().manual_seed(44)
+    idx = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
+    with torch.no_grad():
+        full = model(idx)
+        first, st = model(idx[:, :T1], return_state=True)
+        second = model(idx[:, T1:], state=st)
+    torch.cuda.synchronize()
+    assert full.shape == (B, T, cfg.padded_vocab_size)
+    assert torch.isfinite(full).all(), "non-finite logits"
+    assert torch.isfinite(first).all() and torch.isfinite(second).all()
+    log(f"  logits: max |x| {full.float().abs().max().item():.3f}, std {full.float().std().item():.3f}")
+    _check("logits, prefill + continuation vs one pass", torch.cat([first, second], 1), full, 1e-2)
+    _check("logits of the second half", second, full[:, T1:], 1e-2)

@@ -1,13 +1,15 @@
 """The overlapped schedule of the memory-scan backward (kdn_mem_bwd with stage bits 0 and 1 in one
 call): with one chunk group the reverse state pass runs in two segments, and chunk-backward tasks of
-the first segment's chunks run on a second stream, in launches no wider than the CUs the pass leaves
-idle, while the pass continues; the remaining tasks run after the pass.
+the first segment's chunks run on a second stream while the second segment runs, in one launch that
+starts after a 3 us bounded wait (so the second segment's workgroups take the CUs the first one
+frees); the remaining tasks run at full width after the pass.
 
 The state gradient crosses the segment boundary in fp32 and every kernel computes what it computes
 in the serial schedule, so every output must be bit-identical to separate calls (reverse pass, then
 chunk backward), which the other memory-scan tests pin to the fp64 oracle.  Shapes have B*H large
-enough for one chunk group (checked): 33 chunks (8 in the first segment, 400 side tasks in 4
-launches) and the benchmark's 64 chunks (16; 768 side tasks in 7 launches), with a ragged last chunk,
+enough for one chunk group (checked): on 256 CUs, 33 chunks (7 in the first segment, 448 side tasks)
+and the benchmark's 64 chunks (13; 896 side tasks), as the library's plan_bwd_overlap sizes them for
+144 state workgroups and 112 idle CUs, with a ragged last chunk,
 a chunk taken by the exact path, a final-state cotangent and the initial-state gradient; iso (beta,
 bf16 dO) and diag (kappa, fp32 dO).
 """

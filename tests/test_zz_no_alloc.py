@@ -2,7 +2,9 @@
 through the C ABI: the same kernels on the same inputs, so beta, p_prev and the final precision are
 bit-identical.  Two calls in a row on the library's fixed workspace, the second with a smaller input
 (and the [B,H] precision mode), then a third identical to the first; a size beyond the fixed workspace
-is rejected on the host with KDN_ERR_ARG before any launch."""
+is rejected on the host with KDN_ERR_ARG before any launch.  Under HIP graph capture (after a first
+eager call on the device, which looks up the fixed array's address): replays, with eager calls of
+other sizes on the same array between them, are bit-identical to ``kdn_iso_gain_fwd``."""
 import pytest
 import torch
 import torch.nn.functional as F
@@ -71,3 +73,35 @@ def test_noalloc_gain_rejects_sizes_beyond_its_workspace():
     got = _run("kdn_iso_gain_fwd_noalloc", B, T, H, xs, 0, 1.0, dev)
     for x, y in zip(got, want):
         assert torch.equal(x, y)
+
+
+def test_noalloc_gain_under_graph_capture():
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import _lib
+    B, T, H, s = 4, 4096, 18, 1.0
+    log(f"case noalloc iso gain captured in a HIP graph B={B} T={T} H={H}, 3 replays")
+    xs = _inputs(B, T, H, 7, dev, 0)
+    want = _run("kdn_iso_gain_fwd", B, T, H, xs, 0, s, dev)
+    _run("kdn_iso_gain_fwd_noalloc", B, T, H, xs, 0, s, dev)  # first call on the device: outside capture
+    a, omega, r, mu = xs
+    outs = [torch.empty((B, T, H), device=dev), torch.empty((B, T, H), device=dev), torch.empty((B, H), device=dev)]
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            _lib.call("kdn_iso_gain_fwd_noalloc", _lib.ptr(a), _lib.ptr(omega), _lib.ptr(r), _lib.ptr(mu), 0, B, T,
+                      H, s, _lib.ptr(outs[0]), _lib.ptr(outs[1]), _lib.ptr(outs[2]), _lib.stream_of(a))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    other = _inputs(2, 300, 5, 8, dev, 1)
+    for rep in range(3):
+        for x in outs:
+            x.fill_(float("nan"))
+        # an eager call of another size on the same fixed array between replays
+        _run("kdn_iso_gain_fwd_noalloc", 2, 300, 5, other, 1, 0.5, dev)
+        graph.replay()
+        torch.cuda.synchronize()
+        for n, x, y in zip(("beta", "p_prev", "final precision"), outs, want):
+            assert torch.equal(x, y), f"replay {rep} {n}: max diff {float((x - y).abs().max()):.3e}"
+        log(f"  replay {rep}: bit-identical")
