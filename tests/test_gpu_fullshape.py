@@ -18,8 +18,9 @@
   fp32 eval mode, against the oracle GPT: logits and gradients at 2e-2, at T = 256 (fp64 oracle,
   tokenwise memory) and at the config's T = 4096 (64 chunks per head inside the model; fp32 oracle
   with the WY-chunked memory, which equals the tokenwise form to rounding on the CPU).
-* Config 4's workload itself: the whole 18-layer iso_kdn_1.3B in bf16 (eval) at B1 T4096.  Its logits
-  are finite, and one pass equals a 2048-token prefill continued from the 18 layer states (1e-2).
+* Config 4's workload itself: the whole 18-layer iso_kdn_1.3B (eval) at B1 T4096: one pass against a
+  2048-token prefill continued from the 18 layer states, with fp32 and with bf16 weights; the bars
+  sit above the random-init stack's own rounding-noise amplification (the test's docstring).
 """
 import math
 import pathlib
@@ -241,9 +242,18 @@ def test_config4_full_width_two_layers_match_oracle(T):
 
 def test_config4_full_model_prefill_continuation():
     """The config-4 workload (model.py:95-161, config.py:137-160): all 18 layers of the random-init
-    iso_kdn_1.3B in bf16, eval, B1 T4096.  The logits are finite, and the one-pass forward equals a
-    2048-token prefill whose 18 layer states (short-convolution tails, memory, precision) carry into
-    the second 2048 tokens."""
+    iso_kdn_1.3B at B1 T4096, eval, one pass against a 2048-token prefill whose 18 layer states
+    (short-convolution tails, memory, precision) carry into the second 2048 tokens.
+
+    The random-init 18-layer stack amplifies last-bit differences (the projections' GEMMs at
+    M = 4096 against M = 2048, the state pass's chunk-group plan at T = 4096 against T = 2048, then
+    the bf16 rounding of q, k, v at the scan's boundary): with fp32 weights the two runs agree to
+    about 1% of the largest logit, and the bf16 model's one pass already differs from the fp32 model
+    by about 10%, at its first token, where no state is carried at all.  So the bars are:
+      * fp32 weights: split against one pass at 2e-2; layer 0's carried memory and precision (its
+        input is the embedding, with no amplification in front of it) at 1e-3;
+      * bf16 weights (the workload): finite logits, and the split run no further from the fp32
+        model's one pass than the bf16 one pass is (1.25x, plus 1e-3)."""
     dev = gpu_or_skip()
     from lit_gpt.model import GPT
     B, T, T1 = 1, 4096, 2048
@@ -251,20 +261,34 @@ def test_config4_full_model_prefill_continuation():
     with torch.device(dev):
         model = GPT.from_name("iso_kdn_1.3B")
     model.init_weights()
-    model = model.to(torch.bfloat16).eval()
+    model = model.eval()
     cfg = model.config
-    log(f"case config-4 workload: {cfg.n_layer} layers, width {cfg.n_embd}, bf16 eval, B={B} T={T}, "
-        f"split at {T1}")
+    log(f"case config-4 workload: {cfg.n_layer} layers, width {cfg.n_embd}, B={B} T={T}, split at {T1}")
     g = torch.Generator().manual_seed(44)
     idx = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(dev)
-    with torch.no_grad():
-        full = model(idx)
-        first, st = model(idx[:, :T1], return_state=True)
-        second = model(idx[:, T1:], state=st)
-    torch.cuda.synchronize()
-    assert full.shape == (B, T, cfg.padded_vocab_size)
-    assert torch.isfinite(full).all(), "non-finite logits"
-    assert torch.isfinite(first).all() and torch.isfinite(second).all()
-    log(f"  logits: max |x| {full.float().abs().max().item():.3f}, std {full.float().std().item():.3f}")
-    _check("logits, prefill + continuation vs one pass", torch.cat([first, second], 1), full, 1e-2)
-    _check("logits of the second half", second, full[:, T1:], 1e-2)
+
+    def run():
+        with torch.no_grad():
+            full, st_full = model(idx, return_state=True)
+            first, st = model(idx[:, :T1], return_state=True)
+            second, st_split = model(idx[:, T1:], state=st, return_state=True)
+        torch.cuda.synchronize()
+        assert full.shape == (B, T, cfg.padded_vocab_size)
+        for x in (full, first, second):
+            assert torch.isfinite(x).all(), "non-finite logits"
+        return full.float(), torch.cat([first, second], 1).float(), st_full, st_split
+
+    f_full, f_split, st_full, st_split = run()
+    log(f"  fp32 weights: logits max |x| {f_full.abs().max().item():.3f}, std {f_full.std().item():.3f}")
+    _check("fp32: logits, prefill + continuation vs one pass", f_split, f_full, 2e-2)
+    _check("fp32: layer-0 memory after T tokens, carried vs one pass", st_split[0].memory, st_full[0].memory, 1e-3)
+    _check("fp32: layer-0 precision after T tokens, carried vs one pass", st_split[0].precision,
+           st_full[0].precision, 1e-3)
+    del st_full, st_split
+    model = model.to(torch.bfloat16)
+    b_full, b_split, _, _ = run()
+    e_one = rel(b_full, f_full)
+    e_split = rel(b_split, f_full)
+    log(f"  bf16 weights: one pass vs the fp32 model {e_one:.3e}; split vs the fp32 model {e_split:.3e}; "
+        f"split vs one pass {rel(b_split, b_full):.3e}")
+    assert e_split <= 1.25 * e_one + 1e-3, f"bf16 split {e_split:.3e} vs one pass {e_one:.3e} (from fp32)"
