@@ -39,6 +39,22 @@ __device__ __forceinline__ f32x4 mma2b(uint4 a, uint4 bh, uint4 bl, f32x4 c) {
   c = mfma(a, bl, c);
   return c;
 }
+// a*b where each operand is split (hi + lo, AL / BL) or exact in bf16 (hi only): hi*hi, hi*lo, lo*hi
+// in the order of mma3, dropping the terms of an absent lo half.
+template <bool AL, bool BL>
+__device__ __forceinline__ f32x4 mmx(uint4 ah, uint4 al, uint4 bh, uint4 bl, f32x4 c) {
+  c = mfma(ah, bh, c);
+  if constexpr (BL) c = mfma(ah, bl, c);
+  if constexpr (AL) c = mfma(al, bh, c);
+  return c;
+}
+// a staged fragment; without LO the tensor was staged as its bf16 values alone (lo = 0)
+template <bool LO>
+__device__ __forceinline__ void afragx(const bf16_t* buf, int tile, int lane, uint4& hi, uint4& lo) {
+  hi = *reinterpret_cast<const uint4*>(buf + tile * TILE + lane * 8);
+  if constexpr (LO) lo = *reinterpret_cast<const uint4*>(buf + tile * TILE + 512 + lane * 8);
+  else lo = uint4{0u, 0u, 0u, 0u};
+}
 
 // Lower 16x16 tiles (I, J), J <= I, 2-bit packed: 0:(0,0) 1:(1,1) 2:(2,2) 3:(3,3) 4:(1,0)
 // 5:(2,1) 6:(3,2) 7:(2,0) 8:(3,1) 9:(3,0); upper tiles (0,1) (0,2) (0,3) (1,2) (1,3) (2,3).
@@ -86,10 +102,10 @@ __device__ __forceinline__ int lower_tile_index(int I, int J) {
 // Chunks flagged by the forward store the products (dQg, dW, dKf, dM, dgl) for the exact kernels
 // and stop after them.
 // ---------------------------------------------------------------------------------------------
-template <int K, int V, bool ISO, typename TDO>
+template <int K, int V, bool ISO, typename TDO, int HM>
 __device__ __forceinline__ void chunk_bwd_task(
-    int task, const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
-    const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
+    int task, const void* __restrict__ hbuf, const void* __restrict__ dhbuf, const void* __restrict__ Dl,
+    const void* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
     const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const float* __restrict__ gc, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, int T, int H,
@@ -97,6 +113,13 @@ __device__ __forceinline__ void chunk_bwd_task(
     float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, float* __restrict__ xQg,
     float* __restrict__ xW, float* __restrict__ xKf, float* __restrict__ xM, float* __restrict__ xgl) {
   constexpr bool DO_BF16 = sizeof(TDO) == 2;
+  // HM: which of h, dh, delta, d delta were stored in bf16 (kdn_state::HB_*; the recurrences ran in
+  // fp32 and rounded those copies once).  A bf16 operand enters a product without a lo half: one
+  // MFMA against another bf16 operand, two against a split fp32 one.
+  constexpr bool LH = !(HM & kdn_state::HB_H), LDH = !(HM & kdn_state::HB_DH);  // fp32 (split) copies
+  constexpr bool LD = !(HM & kdn_state::HB_D), LDD = !(HM & kdn_state::HB_DD);
+  constexpr bool LO_ = !DO_BF16;
+  constexpr int EH = LH ? 4 : 2, EDH = LDH ? 4 : 2, ED = LD ? 4 : 2, EDD = LDD ? 4 : 2;  // bytes per element
   constexpr int NW = 8;
   constexpr int VB = V / 32;        // k-blocks of the V contraction
   constexpr int NIT = K / 16;       // channel tiles (waves 0 .. NIT-1 own one each)
@@ -138,19 +161,29 @@ __device__ __forceinline__ void chunk_bwd_task(
   }
 
   // ================================ loads ================================
-  const bufrsrc rD = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);  // rows past L read 0
-  const bufrsrc rdD = make_buf(dDl + ((int64_t)bh * T + t0) * V, L * V * 4);
+  const int64_t row0 = ((int64_t)bh * T + t0) * V;
+  const bufrsrc rD = make_buf(reinterpret_cast<const char*>(Dl) + row0 * ED, L * V * ED);  // rows past L read 0
+  const bufrsrc rdD = make_buf(reinterpret_cast<const char*>(dDl) + row0 * EDD, L * V * EDD);
   const bufrsrc rO = make_buf(dO + (((int64_t)b * T + t0) * H + h) * V, ((L - 1) * H + 1) * V * sizeof(TDO));
   float4 sr_D[SU][2], sr_dD[SU][2];
+  u32x4 sr_D16[SU], sr_dD16[SU];
   u32x4 sr_O[SU][DO_BF16 ? 1 : 2];
 #pragma unroll
   for (int u = 0; u < SU; ++u) {  // unit e: 16-row block, k-block, fragment lane
     const int e = tid + 512 * u, blk = e / (VB * 64), kb = (e / 64) % VB, sl = e & 63;
     const uint32_t c = (uint32_t)(16 * blk + (sl & 15)), v0 = (uint32_t)(32 * kb + 8 * (sl >> 4));
-    sr_D[u][0] = buf_ld4(rD, (c * V + v0) * 4);
-    sr_D[u][1] = buf_ld4(rD, (c * V + v0) * 4 + 16);
-    sr_dD[u][0] = buf_ld4(rdD, (c * V + v0) * 4);
-    sr_dD[u][1] = buf_ld4(rdD, (c * V + v0) * 4 + 16);
+    if constexpr (LD) {
+      sr_D[u][0] = buf_ld4(rD, (c * V + v0) * 4);
+      sr_D[u][1] = buf_ld4(rD, (c * V + v0) * 4 + 16);
+    } else {
+      sr_D16[u] = __builtin_amdgcn_raw_buffer_load_b128(rD, (c * V + v0) * 2, 0, 0);
+    }
+    if constexpr (LDD) {
+      sr_dD[u][0] = buf_ld4(rdD, (c * V + v0) * 4);
+      sr_dD[u][1] = buf_ld4(rdD, (c * V + v0) * 4 + 16);
+    } else {
+      sr_dD16[u] = __builtin_amdgcn_raw_buffer_load_b128(rdD, (c * V + v0) * 2, 0, 0);
+    }
     if constexpr (DO_BF16) {
       sr_O[u][0] = __builtin_amdgcn_raw_buffer_load_b128(rO, (c * H * V + v0) * 2, 0, 0);
     } else {
@@ -159,17 +192,20 @@ __device__ __forceinline__ void chunk_bwd_task(
     }
   }
   // this wave's rows of h and dh (row i = 16 it + r16, v = 32 kb + 8 g4 .. + 7) and the g_last factor
-  const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
-  const bufrsrc rdh = make_buf(dhbuf + chunk * K * V, K * V * 4);
+  const bufrsrc rh = make_buf(reinterpret_cast<const char*>(hbuf) + chunk * K * V * EH, K * V * EH);
+  const bufrsrc rdh = make_buf(reinterpret_cast<const char*>(dhbuf) + chunk * K * V * EDH, K * V * EDH);
   float hv[VB][8], dhv[VB][8];
+  u32x4 hr[VB], dhr[VB];  // bf16 copies: the rows are the MFMA fragments themselves
   float gl_i = 0.f;
   if (own_k) {
     const int i = 16 * it + r16;
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb) {
       const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
-      kdn_intra::ld8(rh, e * 4, hv[kb]);
-      kdn_intra::ld8(rdh, e * 4, dhv[kb]);
+      if constexpr (LH) kdn_intra::ld8(rh, e * 4, hv[kb]);
+      else hr[kb] = __builtin_amdgcn_raw_buffer_load_b128(rh, e * 2, 0, 0);
+      if constexpr (LDH) kdn_intra::ld8(rdh, e * 4, dhv[kb]);
+      else dhr[kb] = __builtin_amdgcn_raw_buffer_load_b128(rdh, e * 2, 0, 0);
     }
     gl_i = buf_ld(make_buf(gc + (((int64_t)b * T + t0 + L - 1) * H + h) * K, K * 4), i * 4);
   }
@@ -228,8 +264,11 @@ __device__ __forceinline__ void chunk_bwd_task(
       *reinterpret_cast<uint4*>(dst + off) = hi;
       *reinterpret_cast<uint4*>(dst + off + 512) = lo;
     };
-    put8(sD, sr_D[u][0], sr_D[u][1]);
-    put8(sdD, sr_dD[u][0], sr_dD[u][1]);
+    // a bf16 copy is staged as its values alone (the lo half stays unused)
+    if constexpr (LD) put8(sD, sr_D[u][0], sr_D[u][1]);
+    else *reinterpret_cast<uint4*>(sD + off) = __builtin_bit_cast(uint4, sr_D16[u]);
+    if constexpr (LDD) put8(sdD, sr_dD[u][0], sr_dD[u][1]);
+    else *reinterpret_cast<uint4*>(sdD + off) = __builtin_bit_cast(uint4, sr_dD16[u]);
     if constexpr (DO_BF16)
       *reinterpret_cast<uint4*>(sO + off) = uint4{sr_O[u][0].x, sr_O[u][0].y, sr_O[u][0].z, sr_O[u][0].w};
     else
@@ -257,31 +296,34 @@ __device__ __forceinline__ void chunk_bwd_task(
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl) aQ[tl] = aW[tl] = aK[tl] = zero4();
   if (own_k) {
-    uint4 fh[VB], fl[VB];
+    uint4 fh[VB], fl[VB];  // h (split, or its bf16 values)
 #pragma unroll
-    for (int kb = 0; kb < VB; ++kb) split8(hv[kb], fh[kb], fl[kb]);
+    for (int kb = 0; kb < VB; ++kb) {
+      if constexpr (LH) split8(hv[kb], fh[kb], fl[kb]);
+      else fh[kb] = __builtin_bit_cast(uint4, hr[kb]), fl[kb] = uint4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb)
 #pragma unroll
       for (int tl = 0; tl < 4; ++tl) {
-        if constexpr (DO_BF16) {
-          const uint4 ob = *reinterpret_cast<const uint4*>(sO + tl * RB + kb * TILE + lane * 8);
-          aQ[tl] = kdn_state::mma2(fh[kb], fl[kb], ob, aQ[tl]);
-        } else {
-          uint4 oh, ol;
-          afrag(sO + tl * RB, kb, lane, oh, ol);
-          aQ[tl] = mma3(fh[kb], fl[kb], oh, ol, aQ[tl]);
-        }
-        uint4 xh, xl;
-        afrag(sdD + tl * RB, kb, lane, xh, xl);
-        aW[tl] = mma3(xh, xl, fh[kb], fl[kb], aW[tl]);
+        uint4 oh, ol, xh, xl;
+        afragx<LO_>(sO + tl * RB, kb, lane, oh, ol);
+        aQ[tl] = mmx<LH, LO_>(fh[kb], fl[kb], oh, ol, aQ[tl]);
+        afragx<LDD>(sdD + tl * RB, kb, lane, xh, xl);
+        aW[tl] = mmx<LDD, LH>(xh, xl, fh[kb], fl[kb], aW[tl]);
       }
     float dot = 0.f;
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb) {
+      float hf[8], df[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dot += hv[kb][j] * dhv[kb][j];
-      split8(dhv[kb], fh[kb], fl[kb]);
+      for (int j = 0; j < 8; ++j) hf[j] = hv[kb][j], df[j] = dhv[kb][j];
+      if constexpr (!LH) kdn_intra::unpack8(hr[kb], hf);
+      if constexpr (!LDH) kdn_intra::unpack8(dhr[kb], df);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dot += hf[j] * df[j];
+      if constexpr (LDH) split8(dhv[kb], fh[kb], fl[kb]);  // fh, fl: dh from here on
+      else fh[kb] = __builtin_bit_cast(uint4, dhr[kb]), fl[kb] = uint4{0u, 0u, 0u, 0u};
     }
     dot += __shfl_xor(dot, 16, 64);
     dot += __shfl_xor(dot, 32, 64);
@@ -291,8 +333,8 @@ __device__ __forceinline__ void chunk_bwd_task(
 #pragma unroll
       for (int tl = 0; tl < 4; ++tl) {
         uint4 xh, xl;
-        afrag(sD + tl * RB, kb, lane, xh, xl);
-        aK[tl] = mma3(fh[kb], fl[kb], xh, xl, aK[tl]);
+        afragx<LD>(sD + tl * RB, kb, lane, xh, xl);
+        aK[tl] = mmx<LDH, LD>(fh[kb], fl[kb], xh, xl, aK[tl]);
       }
   }
   // dM tiles (c-block I, s-block J) = lower(dO delta^T) for lower tiles w and w + 8: mt lane -> column
@@ -308,18 +350,11 @@ __device__ __forceinline__ void chunk_bwd_task(
     lower_tile(t, I, J);
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb) {
-      uint4 xh, xl;
-      afrag(sD + J * RB, kb, lane, xh, xl);
-      if constexpr (DO_BF16) {
-        const uint4 ob = *reinterpret_cast<const uint4*>(sO + I * RB + kb * TILE + lane * 8);
-        mt[x] = mma2b(ob, xh, xl, mt[x]);
-        mtT[x] = kdn_state::mma2(xh, xl, ob, mtT[x]);
-      } else {
-        uint4 oh, ol;
-        afrag(sO + I * RB, kb, lane, oh, ol);
-        mt[x] = mma3(oh, ol, xh, xl, mt[x]);
-        mtT[x] = mma3(xh, xl, oh, ol, mtT[x]);
-      }
+      uint4 xh, xl, oh, ol;
+      afragx<LD>(sD + J * RB, kb, lane, xh, xl);
+      afragx<LO_>(sO + I * RB, kb, lane, oh, ol);
+      mt[x] = mmx<LO_, LD>(oh, ol, xh, xl, mt[x]);
+      mtT[x] = mmx<LD, LO_>(xh, xl, oh, ol, mtT[x]);
     }
     if (I == J) {
 #pragma unroll
@@ -385,7 +420,17 @@ __device__ __forceinline__ void chunk_bwd_task(
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     uint4 xh0, xl0, xh1, xl1;
-    {
+    if constexpr (!LDD) {  // bf16 d delta: the fragment is the raw values
+      uint32_t xr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = 32 * kb + (j < 4 ? 4 * g4 + j : 16 + 4 * g4 + j - 4);
+        xr[j] = own_v ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rdD, ((uint32_t)c * V + 16 * w + r16) * 2, 0, 0)
+                      : 0u;
+      }
+      xh0 = uint4{xr[0] | (xr[1] << 16), xr[2] | (xr[3] << 16), xr[4] | (xr[5] << 16), xr[6] | (xr[7] << 16)};
+      xl0 = uint4{0u, 0u, 0u, 0u};
+    } else {
       float xv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -406,7 +451,7 @@ __device__ __forceinline__ void chunk_bwd_task(
       const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
       uint4 ah, al;
       split8(av, ah, al);
-      Yt[0][J] = mma3(xh0, xl0, ah, al, Yt[0][J]);
+      Yt[0][J] = mmx<LDD, true>(xh0, xl0, ah, al, Yt[0][J]);
       Yt[1][J] = mma3(xh1, xl1, ah, al, Yt[1][J]);
     }
   }
@@ -802,17 +847,17 @@ __device__ __forceinline__ void chunk_bwd_task(
 }
 
 // One workgroup per task: tasks task0 .. task0 + gridDim.x - 1.
-template <int K, int V, bool ISO, typename TDO>
+template <int K, int V, bool ISO, typename TDO, int HM>
 __global__ __launch_bounds__(512, 1) void chunk_bwd_kernel(
-    const float* __restrict__ hbuf, const float* __restrict__ dhbuf, const float* __restrict__ Dl,
-    const float* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
+    const void* __restrict__ hbuf, const void* __restrict__ dhbuf, const void* __restrict__ Dl,
+    const void* __restrict__ dDl, const TDO* __restrict__ dO, const float* __restrict__ At,
     const float* __restrict__ U, const float* __restrict__ W, const int* __restrict__ flags,
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const float* __restrict__ gc, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, int T, int H,
     int NT, int BH, int task0, float scale, bf16_t* __restrict__ dv, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk,
     float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, float* __restrict__ xQg,
     float* __restrict__ xW, float* __restrict__ xKf, float* __restrict__ xM, float* __restrict__ xgl) {
-  chunk_bwd_task<K, V, ISO, TDO>(task0 + (int)blockIdx.x, hbuf, dhbuf, Dl, dDl, dO, At, U, W, flags, q, k, kap, gc,
+  chunk_bwd_task<K, V, ISO, TDO, HM>(task0 + (int)blockIdx.x, hbuf, dhbuf, Dl, dDl, dO, At, U, W, flags, q, k, kap, gc,
                                  q_rstd, k_rstd, T, H, NT, BH, scale, dv, dq, dk, dkap, dbeta, dg, xQg, xW, xKf, xM,
                                  xgl);
 }

@@ -402,7 +402,7 @@ __device__ void bwd_solve_exact_chunk(
     const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, bf16_t* __restrict__ dv, float* __restrict__ dKg,
-    float* __restrict__ dNg, int n, int bh, const float* __restrict__ k_rstd) {
+    float* __restrict__ dNg, int n, int bh, const float* __restrict__ k_rstd, bool dd16) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // phase 1: sK | sA | sG (3 x C x KP); phase 2 (after the solve) reuses it as sX | sUW (2 x C x XP)
@@ -435,7 +435,10 @@ __device__ void bwd_solve_exact_chunk(
       for (int r = 0; r < 16; ++r) {
         const int c = 16 * I + r;
         float x = 0.f;
-        if (c < L) x = isV ? dDl[bht(bh, t0 + c, T, V) + col] : dWg[bht(bh, t0 + c, T, K) + col];
+        if (c < L)
+          x = !isV ? dWg[bht(bh, t0 + c, T, K) + col]
+              : dd16 ? bf2f(reinterpret_cast<const bf16_t*>(dDl)[bht(bh, t0 + c, T, V) + col])
+                     : dDl[bht(bh, t0 + c, T, V) + col];
         acc[r] = x;
       }
 #pragma unroll 1
@@ -497,12 +500,13 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_exact_kernel(
     const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, int NB, const int* __restrict__ flags, bf16_t* __restrict__ dv,
-    float* __restrict__ dKg, float* __restrict__ dNg, const float* __restrict__ k_rstd) {
+    float* __restrict__ dKg, float* __restrict__ dNg, const float* __restrict__ k_rstd, bool dd16) {
   if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
-    bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, lin % NT, lin / NT, k_rstd);
+    bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, lin % NT, lin / NT, k_rstd,
+                                     dd16);
   }
 }
 
@@ -771,6 +775,27 @@ inline int64_t group_floats(int64_t BH, GroupCount gc, int K, int V) {
 }
 inline int64_t round64(int64_t x) { return (x + 63) / 64 * 64; }
 
+// Precision of the per-chunk copies only the backward reads (the forward pass's h and delta, the
+// reverse pass's dh and d delta; kdn_state::HB_* bits, set = bf16).  The isotropic scan stores h and dh
+// in bf16 (its reference's backward keeps all four in the input dtype: FLA's chunk_gated_delta_rule
+// allocates h, v_new, dh and dv2 like k): half the bytes of the two largest copies, written by the
+// state passes and read by the chunk backward, whose products with them take one or two bf16 MFMAs
+// instead of three.  delta and d delta stay fp32: in bf16 they moved the parameter gradients that sum
+// over every token with heavy cancellation (dA_log, the omega / r biases) by up to 1e-2 of their size
+// at B4 T4096 H18, against 4e-4 with bf16 h and dh alone.  The diagonal scan keeps fp32 (its reference
+// kernel keeps an fp32 h), and so does a scan whose state passes run in chunk groups (few B*H streams),
+// whose first group's chunk-parallel readout reads the forward's h and delta.  The recurrences
+// themselves and every output stay as before; the forward and the backward take the same decision from
+// the shape.
+constexpr int kIsoHalfCopies = kdn_state::HB_H | kdn_state::HB_DH;
+inline int half_copies(int iso, GroupCount gc) { return iso && gc.NG == 1 ? kIsoHalfCopies : 0; }
+// Calls f with the copies' precision mask as a compile-time constant.
+template <typename F>
+inline void with_copy_mask(int hm, F f) {
+  if (hm == kIsoHalfCopies) f(std::integral_constant<int, kIsoHalfCopies>{});
+  else f(std::integral_constant<int, 0>{});
+}
+
 // saved-buffer layout (floats), TT = B*H*T, NB = B*H*NT
 struct MemLayout {
   int64_t U, W, Kf, Qg, M, A, h, D, flags, grp, total;
@@ -925,6 +950,7 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   float *U = saved + lay.U, *W = saved + lay.W, *Kf = saved + lay.Kf, *Qg = saved + lay.Qg, *M = saved + lay.M,
         *A = saved + lay.A, *hb = saved + lay.h, *D = saved + lay.D;
   int* flags = reinterpret_cast<int*>(saved + lay.flags);
+  const int hm = half_copies(iso, lay.gc);
   // bit 3 (stages >= 0): no backward follows, so A^T and, where the readout is fused, h and delta
   // are not written
   const bool infer = stages >= 0 && (stages & 8) != 0;
@@ -950,30 +976,36 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
 #undef KDN_INTRA
     KDN_CHECK_LAUNCH();
   }
-  auto launch_ro = [&](dim3 grid, const kdn_state::GroupPlan& P, float* hstore, float* dstore) {
+  auto launch_ro = [&](dim3 grid, const kdn_state::GroupPlan& P, float* hstore, float* dstore, int mask) {
     const dim3 bs(2 * kdn_state::state_threads(V));
-    if (o_bf16)
-      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t, true>), grid, bs, 0, stream, U, W, Kf, gc, h0, T,
-                         H, NT, B * H, hstore, dstore, ht, P, Qg, M, (bf16_t*)o);
-    else
-      hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, true>), grid, bs, 0, stream, U, W, Kf, gc, h0, T,
-                         H, NT, B * H, hstore, dstore, ht, P, Qg, M, (float*)o);
+    with_copy_mask(mask, [&](auto hmc) {
+      constexpr int HM = decltype(hmc)::value;
+      if (o_bf16)
+        hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t, true, HM>), grid, bs, 0, stream, U, W, Kf, gc,
+                           h0, T, H, NT, B * H, hstore, dstore, ht, P, Qg, M, (bf16_t*)o);
+      else
+        hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, true, HM>), grid, bs, 0, stream, U, W, Kf, gc, h0,
+                           T, H, NT, B * H, hstore, dstore, ht, P, Qg, M, (float*)o);
+    });
   };
   auto launch_readout = [&](int NR) {  // chunk-parallel readout O = Qg h + M delta of the first NR chunks
     const int NCH = NR * B * H;        // chunk-heads; with two V halves the grid is padded to pairs of 8
     const dim3 gr(V / 64 == 2 ? 16 * cdiv(NCH, 8) : NCH);
-    if (o_bf16)
-      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, bf16_t>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
-                         NR, B * H, (bf16_t*)o);
-    else
-      hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, float>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H, NT,
-                         NR, B * H, (float*)o);
+    with_copy_mask(hm, [&](auto hmc) {
+      constexpr int HM = decltype(hmc)::value;
+      if (o_bf16)
+        hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, bf16_t, HM>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H,
+                           NT, NR, B * H, (bf16_t*)o);
+      else
+        hipLaunchKernelGGL((kdn_state::readout_kernel<K, V, float, HM>), gr, dim3(256), 0, stream, Qg, M, hb, D, T, H,
+                           NT, NR, B * H, (float*)o);
+    });
   };
   if ((stages & 6) == 6) {  // state pass with the readout fused
     const GroupCount gcnt = lay.gc;
     if (gcnt.NG == 1) {
       launch_ro(dim3(B * H * (V / kdn_state::state_cols(V))), kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr},
-                infer ? nullptr : hb, infer ? nullptr : D);
+                infer ? nullptr : hb, infer ? nullptr : D, hm);
       KDN_CHECK_LAUNCH();
       return 0;
     }
@@ -991,7 +1023,7 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
       KDN_CHECK_LAUNCH();
     }
     P.pass = 1;
-    launch_ro(dim3(B * H * (gcnt.NG - 1) * NV), P, infer ? nullptr : hb, infer ? nullptr : D);
+    launch_ro(dim3(B * H * (gcnt.NG - 1) * NV), P, infer ? nullptr : hb, infer ? nullptr : D, 0);
     KDN_CHECK_LAUNCH();
     launch_readout(gcnt.m);
     KDN_CHECK_LAUNCH();
@@ -999,11 +1031,13 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   }
   if (stages & 2) {  // serial state pass (one- or two-level): h per chunk, delta, final state
     const dim3 bs(kdn_state::state_threads(V));
-    const int rc = run_state_pass<K, V>(B * H, lay.gc, saved + lay.grp, false, stream,
-                                        [&](dim3 grid, const kdn_state::GroupPlan& P) {
-                                          hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V>), grid, bs, 0, stream, U,
-                                                             W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht, P);
-                                        });
+    const int rc = run_state_pass<K, V>(
+        B * H, lay.gc, saved + lay.grp, false, stream, [&](dim3 grid, const kdn_state::GroupPlan& P) {
+          with_copy_mask(hm, [&](auto hmc) {
+            hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, false, decltype(hmc)::value>), grid, bs, 0,
+                               stream, U, W, Kf, gc, h0, T, H, NT, B * H, hb, D, ht, P);
+          });
+        });
     if (rc) return rc;
   }
   if (stages & 4) {  // chunk-parallel readout O = Qg h + M delta of every chunk
@@ -1026,24 +1060,27 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   const int* flags = reinterpret_cast<const int*>(saved + lay.flags);
   float *dh = work + bl.dh, *dD = work + bl.dD, *dQg = work + bl.dQg, *dW = work + bl.dW, *dKf = work + bl.dKf,
         *dM = work + bl.dM, *dgl = work + bl.dgl, *dKg = work + bl.dKg, *dN = work + bl.dN;
+  const int hm = half_copies(iso, bl.gc);
   constexpr int NV = V / kdn_state::state_cols(V);
   const dim3 bs(2 * kdn_state::state_threads(V));  // helper waves take M^T dO and Qg^T dO off the chain
   auto launch_state = [&](dim3 grid, const kdn_state::GroupPlan& P, const float* dS_in, float* dS_out,
                           hipStream_t st) {
-    hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO, true>), grid, bs, 0, st, M, Kf, Qg, W, gc, dO, dS_in,
-                       T, H, NT, B * H, dh, dD, dS_out, P);
+    with_copy_mask(hm, [&](auto hmc) {
+      hipLaunchKernelGGL((kdn_state::state_bwd_kernel<K, V, TDO, true, decltype(hmc)::value>), grid, bs, 0, st, M, Kf,
+                         Qg, W, gc, dO, dS_in, T, H, NT, B * H, dh, dD, dS_out, P);
+    });
   };
   // every chunk's products with h / dh; the solves and gradients of the unflagged ones: the
   // chunk-head tasks task0 .. task_end - 1 (order of chunk_bwd_task: last chunks first)
   auto launch_chunk = [&](int task0, int task_end, hipStream_t st) {
-    if (iso)
-      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, true, TDO>), dim3(task_end - task0), dim3(512), 0, st, hb,
-                         dh, D, dD, dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, B * H, task0, scale,
-                         dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf, dM, dgl);
-    else
-      hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, false, TDO>), dim3(task_end - task0), dim3(512), 0, st, hb,
-                         dh, D, dD, dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, B * H, task0, scale,
-                         dv, dq, dk, dkap, dbeta, dg, dQg, dW, dKf, dM, dgl);
+#define KDN_CHUNK_BWD(ISO_, HB_)                                                                                    \
+  hipLaunchKernelGGL((kdn_bwd::chunk_bwd_kernel<K, V, ISO_, TDO, HB_>), dim3(task_end - task0), dim3(512), 0, st, hb, \
+                     dh, D, dD, dO, A, U, W, flags, q, k, kap, gc, q_rstd, k_rstd, T, H, NT, B * H, task0, scale, dv, \
+                     dq, dk, dkap, dbeta, dg, dQg, dW, dKf, dM, dgl)
+    if (iso && hm == kIsoHalfCopies) KDN_CHUNK_BWD(true, kIsoHalfCopies);
+    else if (iso) KDN_CHUNK_BWD(true, 0);
+    else KDN_CHUNK_BWD(false, 0);
+#undef KDN_CHUNK_BWD
   };
   const int tasks = NT * B * H;
   bool overlapped = false;
@@ -1092,10 +1129,10 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     const int NB = B * H * NT, gx = min(NB, 512);
     if (iso)
       hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, true>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD, dW,
-                         U, W, T, H, NT, NB, flags, dv, dKg, dN, k_rstd);
+                         U, W, T, H, NT, NB, flags, dv, dKg, dN, k_rstd, (hm & kdn_state::HB_DD) != 0);
     else
       hipLaunchKernelGGL((mem_bwd_solve_exact_kernel<K, V, false>), dim3(gx), dim3(256), 0, stream, k, kap, gc, dD,
-                         dW, U, W, T, H, NT, NB, flags, dv, dKg, dN, k_rstd);
+                         dW, U, W, T, H, NT, NB, flags, dv, dKg, dN, k_rstd, (hm & kdn_state::HB_DD) != 0);
     KDN_CHECK_LAUNCH();
   }
   if (stages & 8) {  // the exact path's gradients

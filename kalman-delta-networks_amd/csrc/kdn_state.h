@@ -149,6 +149,25 @@ __device__ __forceinline__ void st_rows4(bufrsrc r, uint32_t vbase, uint32_t row
 __device__ __forceinline__ bufrsrc rows_from(const float* p, int r0, int L, int D) {
   return make_buf(p + (int64_t)r0 * D, (uint32_t)(L > r0 ? (L - r0) * D * 4 : 0));
 }
+// The same four values rounded to bf16 (round to nearest even), into a bf16 block.
+__device__ __forceinline__ void st_rows4_bf16(bufrsrc r, uint32_t vbase, uint32_t row_bytes, const f32x4& x) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b16(f2bf(x[j]), r, vbase + j * row_bytes, 0, 0);
+}
+__device__ __forceinline__ bufrsrc rows_from_bf16(const void* p, int r0, int L, int D) {
+  return make_buf(reinterpret_cast<const bf16_t*>(p) + (int64_t)r0 * D, (uint32_t)(L > r0 ? (L - r0) * D * 2 : 0));
+}
+// A lane's 4 D-layout values of 16-row tile `tile` (rows 4 g4 + j of column col) of the row-major
+// [rows][D] block whose element e0 is the block's first (fp32, or bf16 with B16; rows past L dropped).
+template <bool B16>
+__device__ __forceinline__ void st_tile4(void* p, int64_t e0, int tile, int L, int D, int g4, int col,
+                                         const f32x4& x) {
+  if constexpr (B16)
+    st_rows4_bf16(rows_from_bf16(reinterpret_cast<bf16_t*>(p) + e0, 16 * tile, L, D), (4 * g4 * D + col) * 2, D * 2,
+                  x);
+  else
+    st_rows4(rows_from(reinterpret_cast<float*>(p) + e0, 16 * tile, L, D), (4 * g4 * D + col) * 4, D * 4, x);
+}
 
 // A sequence of NS fragment-read + MFMA steps with the reads issued LA steps ahead, so the
 // LDS latency of step s+LA overlaps the MFMAs of step s.  rd(s, hi, lo) reads step s's A
@@ -205,6 +224,12 @@ struct GroupPlan {
   // and leaving into ht (dh0); a sequence split into segments runs as consecutive such passes
   int c0 = 0, c1 = 0;
 };
+
+// Precision of the per-chunk copies only the backward (and a separate readout) reads, as a bit mask
+// (kernel template argument): the forward pass's h (bit 0) and delta (bit 2), the reverse pass's dh
+// (bit 1) and d delta (bit 3); a set bit stores the copy in bf16 (rounded once), a clear bit in fp32.
+// The recurrences themselves stay fp32 on chip.
+enum : int { HB_H = 1, HB_DH = 2, HB_D = 4, HB_DD = 8 };
 __device__ __forceinline__ void plan_range(const GroupPlan& P, int g, int NT, int& n0, int& n1) {
   if (P.NG == 1) {
     n0 = P.c0;
@@ -264,7 +289,7 @@ __device__ __forceinline__ bool group_task(const GroupPlan& P, int BH, int& bh, 
 // HBM one chunk ahead, straight into registers) and store o.  That drops readout_kernel and its
 // re-reads of h and delta, and keeps the readout's MFMAs and stores off the serial chain, which only
 // pays for the fragment stores.  Both wave groups run the same barrier sequence.
-template <int K, int V, typename TO = float, bool RO = false>
+template <int K, int V, typename TO = float, bool RO = false, int HM = 0>
 __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 1 : 2) void state_fwd_kernel(
     const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ Kf,
     const float* __restrict__ gc, const float* __restrict__ h0, int T, int H, int NT, int BH,
@@ -424,9 +449,9 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
   for (int n = n0; n < n1; ++n) {
     const int t0 = n * C, L = min(C, T - t0);
     if (real && hbuf) {  // (no h, delta stores when the readout is fused and no backward follows)
-      const float* hb = hbuf + ((int64_t)bh * NT + n) * K * V;
+      const int64_t e0 = ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
-      for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, S[ib]);
+      for (int ib = 0; ib < ST; ++ib) st_tile4<(HM & HB_H) != 0>(hbuf, e0, ib, K, V, g4, col, S[ib]);
     }
 
     // ---- phase 1: delta = U - W S   (reads sW; fills sK with chunk n; loads W of chunk n+1)
@@ -454,10 +479,10 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
 #pragma unroll
         for (int j = 0; j < 4; ++j) D[cb][j] = cU[cb][j] - D[cb][j];
       if (real && Dl) {
-        const float* dl = Dl + row_bht(bh, t0, T, V);
+        const int64_t e0 = row_bht(bh, t0, T, V);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
-          st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, D[cb]);  // rows past L dropped
+          st_tile4<(HM & HB_D) != 0>(Dl, e0, cb, L, V, g4, col, D[cb]);  // rows past L dropped
       }
       if constexpr (RO) {  // publish the B fragments of h_n (multiplied with W above) and delta_n
 #pragma unroll
@@ -529,7 +554,7 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
 // B operands Qg^T and M^T are rows of Qg and M, loaded straight into registers by the wave that
 // owns those 16 chunk rows.  Fragment k order is natural (slot j of lane group g <-> k = 8 g + j).
 // ===========================================================================
-template <int K, int V, typename TO>
+template <int K, int V, typename TO, int HM = 0>
 __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict__ Qg, const float* __restrict__ Mg,
                                                          const float* __restrict__ hbuf, const float* __restrict__ Dl,
                                                          int T, int H, int NT, int NR, int BH, TO* __restrict__ out) {
@@ -568,15 +593,28 @@ __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict
   // so a lane holds 4 consecutive rows of one column: 4 consecutive fragment slots of one lane,
   // written as 8 bytes of hi and 8 of lo
   {
-    const bufrsrc rh = make_buf(hbuf + chunk * K * V, K * V * 4);
-    const bufrsrc rd = make_buf(Dl + ((int64_t)bh * T + t0) * V, L * V * 4);  // rows past L read 0
+    constexpr int EH = (HM & HB_H) ? 2 : 4, ED = (HM & HB_D) ? 2 : 4;  // bytes per stored element
+    const bufrsrc rh = make_buf(reinterpret_cast<const char*>(hbuf) + chunk * K * V * EH, K * V * EH);
+    const bufrsrc rd = make_buf(reinterpret_cast<const char*>(Dl) + ((int64_t)bh * T + t0) * V * ED,
+                                L * V * ED);  // rows past L read 0
     constexpr int HU = K / 16, DU = C / 16;  // 4-row blocks per wave
     const int qr = lane & 3, vq = 4 * (lane >> 2), vc = vq + qr;  // after the transpose: column vc
     float4 hx[HU], dx[DU];
+    auto ld4h = [&](bufrsrc r, uint32_t e, auto b16) {  // 4 consecutive elements of either precision
+      if constexpr (!decltype(b16)::value) {
+        return buf_ld4(r, e * 4);
+      } else {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, e * 2, 0, 0);
+        return float4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                      __uint_as_float(v.y & 0xffff0000u)};
+      }
+    };
 #pragma unroll
-    for (int u = 0; u < HU; ++u) hx[u] = buf_ld4(rh, ((4 * (w + 4 * u) + qr) * V + v0 + vq) * 4);
+    for (int u = 0; u < HU; ++u)
+      hx[u] = ld4h(rh, (4 * (w + 4 * u) + qr) * V + v0 + vq, std::integral_constant<bool, (HM & HB_H) != 0>{});
 #pragma unroll
-    for (int u = 0; u < DU; ++u) dx[u] = buf_ld4(rd, ((4 * (w + 4 * u) + qr) * V + v0 + vq) * 4);
+    for (int u = 0; u < DU; ++u)
+      dx[u] = ld4h(rd, (4 * (w + 4 * u) + qr) * V + v0 + vq, std::integral_constant<bool, (HM & HB_D) != 0>{});
     auto put = [&](bf16_t* buf, int nkb, int r0, const float4& x) {  // rows r0 .. r0+3 of column vc
       const float4 y = quad_transpose(x, qr);
       const int tile = (vc >> 4) * nkb + (r0 >> 5), ln = (vc & 15) + 16 * ((r0 & 31) >> 3);
@@ -653,7 +691,7 @@ __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict
 // waves then stage only Kf and W^T and issue 32 split products per chunk instead of 56.  Both wave
 // groups run the same barrier sequence: two in the prologue, two per chunk.
 // ===========================================================================
-template <int K, int V, typename TDO, bool HW = false>
+template <int K, int V, typename TDO, bool HW = false, int HM = 0>
 __global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void state_bwd_kernel(
     const float* __restrict__ Mg, const float* __restrict__ Kf, const float* __restrict__ Qg,
     const float* __restrict__ W, const float* __restrict__ gc, const TDO* __restrict__ dO,
@@ -922,9 +960,9 @@ __global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void 
   for (int n = n1 - 1; n >= n0; --n) {
     const int t0 = n * C, L = min(C, T - t0);
     if (real) {
-      const float* hb = dhbuf + ((int64_t)bh * NT + n) * K * V;
+      const int64_t e0 = ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
-      for (int ib = 0; ib < ST; ++ib) st_rows4(rows_from(hb, 16 * ib, K, V), (4 * g4 * V + col) * 4, V * 4, dS[ib]);
+      for (int ib = 0; ib < ST; ++ib) st_tile4<(HM & HB_DH) != 0>(dhbuf, e0, ib, K, V, g4, col, dS[ib]);
     }
 
     // dO of this chunk as B fragments (k = c), kept for both phases
@@ -973,10 +1011,10 @@ __global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void 
             });
       }
       if (real) {
-        const float* dl = dDl + row_bht(bh, t0, T, V);
+        const int64_t e0 = row_bht(bh, t0, T, V);
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
-          st_rows4(rows_from(dl, 16 * cb, L, V), (4 * g4 * V + col) * 4, V * 4, dD[cb]);  // rows past L dropped
+          st_tile4<(HM & HB_DD) != 0>(dDl, e0, cb, L, V, g4, col, dD[cb]);  // rows past L dropped
       }
     }
     __syncthreads();

@@ -3,7 +3,10 @@ against the CPU oracle's tokenwise recurrence in fp64 with autograd gradients.
 
 Inputs are exactly representable at the HIP boundary (bf16 q, k, v; fp32 kappa/beta and
 gate), so the only differences are the kernel's fp32 arithmetic and the bf16 rounding of
-the dq, dk, dv outputs (which the reference also emits in bf16).
+the dq, dk, dv outputs (which the reference also emits in bf16).  The isotropic scan with its
+state passes in one chunk group (kdn_mem_state_groups == 1) also keeps the per-chunk states and
+state gradients its backward reads (h, dh) in bf16, as its reference's backward does, so its fp32
+gradients (dgate, dbeta) are held to 5e-3 instead of 1e-3 (measured <= 1.8e-3).
 """
 import math
 
@@ -17,6 +20,16 @@ pytestmark = pytest.mark.gpu
 CHUNK = 64
 TOL_F32 = 2e-4   # fp32 outputs / gradients (o, dkappa, dbeta, dg, states)
 TOL_BF16 = 1e-2  # bf16 gradient outputs (dq, dk, dv): 2^-8 rounding
+
+
+def _tol_grad(iso, q, v):
+    """Bar of the fp32 gradients (dgate, dkappa / dbeta): 5 TOL_F32, or 5e-3 where the isotropic scan
+    keeps its backward's per-chunk h and dh copies in bf16 (one chunk group)."""
+    from lit_gpt.kdn_ops import _memscan
+    B, T, H, K = q.shape
+    if iso and _memscan.state_groups(B, T, H, K, v.shape[-1]) == 1:
+        return 5e-3
+    return TOL_F32 * 5
 
 
 def _oracle(q, k, v, ell, kap, do, *, iso, scale, h0=None, dS=None):
@@ -96,8 +109,8 @@ def test_memory_scan_matches_oracle(variant, B, T, H, K, V):
     _check("dq", dq, g_ref[0], TOL_BF16)
     _check("dk", dkk, g_ref[1], TOL_BF16)
     _check("dv", dv, g_ref[2], TOL_BF16)
-    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
-    _check("dbeta" if iso else "dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("dgate", dell, g_ref[3], _tol_grad(iso, q, v))
+    _check("dbeta" if iso else "dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
 
 
 @pytest.mark.parametrize("variant", ["iso", "diag"])
@@ -118,8 +131,8 @@ def test_memory_scan_state_carry(variant):
     _check("dq", dq, g_ref[0], TOL_BF16)
     _check("dk", dkk, g_ref[1], TOL_BF16)
     _check("dv", dv, g_ref[2], TOL_BF16)
-    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
-    _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("dgate", dell, g_ref[3], _tol_grad(iso, q, v))
+    _check("dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
     _check("d initial state", dh0, g_ref[5], TOL_F32)
 
 
@@ -140,8 +153,8 @@ def test_memory_scan_extreme_decay_exact_path(variant):
     _check("dq", dq, g_ref[0], TOL_BF16)
     _check("dk", dkk, g_ref[1], TOL_BF16)
     _check("dv", dv, g_ref[2], TOL_BF16)
-    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
-    _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("dgate", dell, g_ref[3], _tol_grad(iso, q, v))
+    _check("dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
 
 
 @pytest.mark.parametrize("variant", ["iso", "diag"])
@@ -163,8 +176,8 @@ def test_memory_scan_mixed_anchor_and_exact_chunks(variant):
     _check("dq", dq, g_ref[0], TOL_BF16)
     _check("dk", dkk, g_ref[1], TOL_BF16)
     _check("dv", dv, g_ref[2], TOL_BF16)
-    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
-    _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("dgate", dell, g_ref[3], _tol_grad(iso, q, v))
+    _check("dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
 
 
 @pytest.mark.parametrize("variant", ["iso", "diag"])
@@ -189,8 +202,8 @@ def test_memory_scan_large_decay_block_anchors(variant, ell_mean, ell_std, shape
     _check("dq", dq, g_ref[0], TOL_BF16)
     _check("dk", dkk, g_ref[1], TOL_BF16)
     _check("dv", dv, g_ref[2], TOL_BF16)
-    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
-    _check("dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("dgate", dell, g_ref[3], _tol_grad(iso, q, v))
+    _check("dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
 
 
 def test_diag_bf16_output_equals_fp32_output_cast():
@@ -249,6 +262,6 @@ def test_memory_scan_grouped_state_passes(variant, B, T, H, K, V):
     _check("dq", dq, g_ref[0], TOL_BF16)
     _check("dk", dkk, g_ref[1], TOL_BF16)
     _check("dv", dv, g_ref[2], TOL_BF16)
-    _check("dgate", dell, g_ref[3], TOL_F32 * 5)
-    _check("dbeta" if iso else "dkappa", dkap, g_ref[4], TOL_F32 * 5)
+    _check("dgate", dell, g_ref[3], _tol_grad(iso, q, v))
+    _check("dbeta" if iso else "dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
     _check("d initial state", dh0, g_ref[5], TOL_F32)
