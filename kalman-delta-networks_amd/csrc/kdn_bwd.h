@@ -201,11 +201,12 @@ __device__ __forceinline__ void chunk_bwd_task(
     const int i = 16 * it + r16;
 #pragma unroll
     for (int kb = 0; kb < VB; ++kb) {
-      const uint32_t e = (uint32_t)(i * V + 32 * kb + 8 * g4);
-      if constexpr (LH) kdn_intra::ld8(rh, e * 4, hv[kb]);
-      else hr[kb] = __builtin_amdgcn_raw_buffer_load_b128(rh, e * 2, 0, 0);
-      if constexpr (LDH) kdn_intra::ld8(rdh, e * 4, dhv[kb]);
-      else dhr[kb] = __builtin_amdgcn_raw_buffer_load_b128(rdh, e * 2, 0, 0);
+      // the state passes' tiled layout (kdn_state::hb_off): 8 consecutive columns are contiguous
+      const uint32_t et = kdn_state::hb_off<K>(i, 32 * kb + 8 * g4);
+      if constexpr (LH) kdn_intra::ld8(rh, et * 4, hv[kb]);
+      else hr[kb] = __builtin_amdgcn_raw_buffer_load_b128(rh, et * 2, 0, 0);
+      if constexpr (LDH) kdn_intra::ld8(rdh, et * 4, dhv[kb]);
+      else dhr[kb] = __builtin_amdgcn_raw_buffer_load_b128(rdh, et * 2, 0, 0);
     }
     gl_i = buf_ld(make_buf(gc + (((int64_t)b * T + t0 + L - 1) * H + h) * K, K * 4), i * 4);
   }

@@ -157,6 +157,33 @@ __device__ __forceinline__ void st_rows4_bf16(bufrsrc r, uint32_t vbase, uint32_
 __device__ __forceinline__ bufrsrc rows_from_bf16(const void* p, int r0, int L, int D) {
   return make_buf(reinterpret_cast<const bf16_t*>(p) + (int64_t)r0 * D, (uint32_t)(L > r0 ? (L - r0) * D * 2 : 0));
 }
+// Layout of a per-chunk state copy [K][V] (h, dh; only the chunk backward and the readout read them):
+// 16-column blocks, within one the 16-row tiles, within a tile the rows in the order
+// (i % 4, (i / 4) % 4), 16 columns each.  A state wave's lane (g4, c16) holds rows 16 ib + 4 g4 + j of
+// one column, so each of its 4 stores per tile writes 64 consecutive elements (256 bytes in fp32, 128
+// in bf16; in a row-major layout a wave's 16 columns are 64- or 32-byte pieces of 4 rows); 8
+// consecutive columns of a row, which the chunk backward loads, stay contiguous.
+template <int K>
+__device__ __forceinline__ uint32_t hb_off(int i, int v) {
+  return ((((uint32_t)(v >> 4) * (K / 16) + (uint32_t)(i >> 4)) * 4 + (uint32_t)(i & 3)) * 4 + (uint32_t)((i >> 2) & 3)) *
+             16 + (uint32_t)(v & 15);
+}
+// A lane's 4 D-layout values (rows 16 ib + 4 g4 + j of column col) of one chunk's [K][V] state block
+// at element e0 of p (fp32, or bf16 with B16), in the hb_off layout.
+template <int K, int V, bool B16>
+__device__ __forceinline__ void st_state4(void* p, int64_t e0, int ib, int g4, int col, const f32x4& x) {
+  if constexpr (B16) {
+    const bufrsrc r = make_buf(reinterpret_cast<bf16_t*>(p) + e0, K * V * 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_buffer_store_b16(f2bf(x[j]), r, hb_off<K>(16 * ib + 4 * g4 + j, col) * 2, 0, 0);
+  } else {
+    const bufrsrc r = make_buf(reinterpret_cast<float*>(p) + e0, K * V * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x[j]), r, hb_off<K>(16 * ib + 4 * g4 + j, col) * 4, 0, 0);
+  }
+}
 // A lane's 4 D-layout values of 16-row tile `tile` (rows 4 g4 + j of column col) of the row-major
 // [rows][D] block whose element e0 is the block's first (fp32, or bf16 with B16; rows past L dropped).
 template <bool B16>
@@ -451,7 +478,7 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
     if (real && hbuf) {  // (no h, delta stores when the readout is fused and no backward follows)
       const int64_t e0 = ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
-      for (int ib = 0; ib < ST; ++ib) st_tile4<(HM & HB_H) != 0>(hbuf, e0, ib, K, V, g4, col, S[ib]);
+      for (int ib = 0; ib < ST; ++ib) st_state4<K, V, (HM & HB_H) != 0>(hbuf, e0, ib, g4, col, S[ib]);
     }
 
     // ---- phase 1: delta = U - W S   (reads sW; fills sK with chunk n; loads W of chunk n+1)
@@ -610,8 +637,10 @@ __global__ __launch_bounds__(256, 3) void readout_kernel(const float* __restrict
       }
     };
 #pragma unroll
-    for (int u = 0; u < HU; ++u)
-      hx[u] = ld4h(rh, (4 * (w + 4 * u) + qr) * V + v0 + vq, std::integral_constant<bool, (HM & HB_H) != 0>{});
+    for (int u = 0; u < HU; ++u) {
+      const int hi = 4 * (w + 4 * u) + qr, hv = v0 + vq;
+      hx[u] = ld4h(rh, hb_off<K>(hi, hv), std::integral_constant<bool, (HM & HB_H) != 0>{});
+    }
 #pragma unroll
     for (int u = 0; u < DU; ++u)
       dx[u] = ld4h(rd, (4 * (w + 4 * u) + qr) * V + v0 + vq, std::integral_constant<bool, (HM & HB_D) != 0>{});
@@ -962,7 +991,7 @@ __global__ __launch_bounds__(HW ? 2 * state_threads(V) : state_threads(V)) void 
     if (real) {
       const int64_t e0 = ((int64_t)bh * NT + n) * K * V;
 #pragma unroll
-      for (int ib = 0; ib < ST; ++ib) st_tile4<(HM & HB_DH) != 0>(dhbuf, e0, ib, K, V, g4, col, dS[ib]);
+      for (int ib = 0; ib < ST; ++ib) st_state4<K, V, (HM & HB_DH) != 0>(dhbuf, e0, ib, g4, col, dS[ib]);
     }
 
     // dO of this chunk as B fragments (k = c), kept for both phases
