@@ -37,6 +37,18 @@ __device__ __forceinline__ Map2 map_mul(const Map2& a, const Map2& b) {
   return c;
 }
 __device__ __forceinline__ float mobius(const Map2& m, float p) { return (m.m0 * p + m.m1) / (m.m2 * p + m.m3); }
+// The same with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of the IEEE division sequence: the
+// isotropic gain's passes are chains of dependent map products, and a Mobius map is invariant under a
+// common factor, so the renormalisation needs no exact reciprocal.
+__device__ __forceinline__ Map2 map_mul_r(const Map2& a, const Map2& b) {
+  Map2 c{a.m0 * b.m0 + a.m1 * b.m2, a.m0 * b.m1 + a.m1 * b.m3, a.m2 * b.m0 + a.m3 * b.m2,
+         a.m2 * b.m1 + a.m3 * b.m3};
+  const float s = fmaxf(fmaxf(fabsf(c.m0), fabsf(c.m1)), fmaxf(fabsf(c.m2), fabsf(c.m3)));
+  const float inv = frcp(fmaxf(s, 1e-30f));
+  c.m0 *= inv; c.m1 *= inv; c.m2 *= inv; c.m3 *= inv;
+  return c;
+}
+__device__ __forceinline__ float mobius_r(const Map2& m, float p) { return (m.m0 * p + m.m1) * frcp(m.m2 * p + m.m3); }
 __device__ __forceinline__ Map2 shfl_up_map(const Map2& m, int d) {
   return Map2{__shfl_up(m.m0, d, 64), __shfl_up(m.m1, d, 64), __shfl_up(m.m2, d, 64), __shfl_up(m.m3, d, 64)};
 }
@@ -87,13 +99,13 @@ __global__ __launch_bounds__(256) void iso_gain_map_kernel(const float* __restri
   for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
     const int h = hq / kIsoSub, q = hq % kIsoSub;
     Map2 M = map_identity();
-    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
+    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul_r(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
     sub[hq] = M;
   }
   __syncthreads();
   for (int h = threadIdx.x; h < H; h += blockDim.x) {
     Map2 M = sub[kIsoSub * h];
-    for (int q = 1; q < kIsoSub; ++q) M = map_mul(sub[kIsoSub * h + q], M);
+    for (int q = 1; q < kIsoSub; ++q) M = map_mul_r(sub[kIsoSub * h + q], M);
     maps[((int64_t)b * H + h) * NC + n] = float4{M.m0, M.m1, M.m2, M.m3};
   }
 }
@@ -117,13 +129,13 @@ __global__ __launch_bounds__(64) void iso_gain_carry_kernel(const float4* __rest
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const Map2 prev = shfl_up_map(M, d);
-      if (lane >= d) M = map_mul(M, prev);
+      if (lane >= d) M = map_mul_r(M, prev);
     }
     Map2 E = shfl_up_map(M, 1);
     if (lane == 0) E = map_identity();
-    if (c < NC) carry[(int64_t)bh * NC + c] = mobius(E, p);
+    if (c < NC) carry[(int64_t)bh * NC + c] = mobius_r(E, p);
     const Map2 tot{__shfl(M.m0, 63, 64), __shfl(M.m1, 63, 64), __shfl(M.m2, 63, 64), __shfl(M.m3, 63, 64)};
-    p = mobius(tot, p);
+    p = mobius_r(tot, p);
   }
   if (final_precision && lane == 0) final_precision[bh] = 1.f / p;
 }
@@ -146,22 +158,22 @@ __global__ __launch_bounds__(256) void iso_gain_emit_kernel(const float* __restr
   for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
     const int h = hq / kIsoSub, q = hq % kIsoSub;
     Map2 M = map_identity();
-    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
+    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul_r(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
     sub[hq] = M;
   }
   __syncthreads();
   for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
     const int h = hq / kIsoSub, q = hq % kIsoSub;
     Map2 E = map_identity();
-    for (int q2 = 0; q2 < q; ++q2) E = map_mul(sub[kIsoSub * h + q2], E);
-    float p = mobius(E, carry[((int64_t)b * H + h) * NC + n]);
+    for (int q2 = 0; q2 < q; ++q2) E = map_mul_r(sub[kIsoSub * h + q2], E);
+    float p = mobius_r(E, carry[((int64_t)b * H + h) * NC + n]);
     for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) {
       const float at = sa[t * H + h], wt = sw[t * H + h], rt = sr[t * H + h];
       spp[t * H + h] = p;
       const float z = at * p + wt;
-      const float g = z / (rt + z);
+      const float g = z * frcp(rt + z);
       sbeta[t * H + h] = g;
-      p = unit_scale ? rt * g : rt * z / (rt + s * z);
+      p = unit_scale ? rt * g : rt * z * frcp(rt + s * z);
     }
   }
   __syncthreads();
@@ -173,7 +185,7 @@ __global__ __launch_bounds__(256) void iso_gain_emit_kernel(const float* __restr
 __device__ __forceinline__ float2 aff_compose(float2 f, float2 g) { return float2{f.x * g.x, f.x * g.y + f.y}; }
 __device__ __forceinline__ float2 token_aff(float at, float wt, float rt, float dl, float pp, float s) {
   const float z = at * pp + wt;
-  const float ig = 1.f / (rt + z), ip = 1.f / (rt + s * z);
+  const float ig = frcp(rt + z), ip = frcp(rt + s * z);
   return float2{at * rt * rt * ip * ip, at * dl * rt * ig * ig};
 }
 
@@ -299,14 +311,14 @@ __global__ __launch_bounds__(256) void iso_gain_bwd_emit_kernel(
       const int e = t * H + h;
       const float at = sa[e], wt = sw[e], rt = sr[e], dl = sd[e], pp = sp[e];
       const float z = at * pp + wt;
-      const float ig = 1.f / (rt + z);
+      const float ig = frcp(rt + z);
       const float ig2 = ig * ig;
       float zbar, drt;
       if (unit_scale) {
         zbar = (dl + rt * lam) * rt * ig2;
         drt = z * (lam * z - dl) * ig2;
       } else {
-        const float ip = 1.f / (rt + s * z);
+        const float ip = frcp(rt + s * z);
         const float ip2 = ip * ip;
         zbar = dl * rt * ig2 + lam * rt * rt * ip2;
         drt = -dl * z * ig2 + lam * s * z * z * ip2;
