@@ -48,16 +48,18 @@ def mfma_peak(tag: str) -> float:
     return FP32_PEAK_TFLOPS if MFMA_PATH.get(tag, "f32") == "f32" else BF16_PEAK_TFLOPS / 3.0
 
 
-def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int, infer: bool = False):
+def kernel_counts(variant: str, B: int, T: int, H: int, K: int, V: int, infer: bool = False,
+                  half_states: bool = False):
     """Algorithmic HBM bytes and FLOPs per launch of each kernel (inputs read once, outputs
     written once, no recompute).  N = B*T*H token-heads; per-token-head figures times N.  With
     ``infer`` (no backward follows) the forward kernels skip what only the backward reads: A^T, and
-    h and delta of the fused state pass."""
+    h and delta of the fused state pass.  ``half_states``: the per-chunk state copies h and dh the
+    backward reads are bf16 (the isotropic scan with one chunk group)."""
     N = B * T * H
     kap_in = 4 * K if variant == "diag" else 4           # kappa fp32 [K] or beta fp32
     dkap_out = 4 * K if variant == "diag" else 4
     do_b = 4 * V if variant == "diag" else 2 * V         # diag output cotangent is fp32
-    h_b = 4 * K * V / C                                   # one fp32 state per chunk
+    h_b = (2 if half_states else 4) * K * V / C           # one state copy per chunk
     mm = C * C / C * 4                                    # one fp32 C x C matrix per chunk
     per = {
         # q,k,v bf16 + kappa + g fp32 -> U, W, Kf, Qg fp32 + M, A^T (the inverse, saved)
@@ -168,7 +170,7 @@ def op_roofline(variant: str, ms: float, B: int, T: int, H: int, K: int):
 def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K: int):
     import torch
 
-    from lit_gpt.kdn_ops import _lib
+    from lit_gpt.kdn_ops import _lib, _memscan
     from lit_gpt.kdn_ops.scan import diag_kdn_scan, iso_kdn_scan
     from lit_gpt.kdn_ops.synthetic import GRAD_KEYS, make_inputs
 
@@ -199,7 +201,8 @@ def run_variant(variant: str, steps: int, warmup: int, B: int, T: int, H: int, K
             step()
         torch.cuda.synchronize()
     kernel_ms = {tag: timer.mean_ms(tag) for tag in timer.tags()}
-    counts = kernel_counts(variant, B, T, H, K, K)
+    half = variant == "iso" and _memscan.state_groups(B, T, H, K, K) == 1
+    counts = kernel_counts(variant, B, T, H, K, K, half_states=half)
     counts.update(frontend_counts(variant, B, T, H, K))
     per_kernel = {}
     for tag, (nbytes, flops) in counts.items():
