@@ -1228,21 +1228,17 @@ __global__ __launch_bounds__(256) void diag_front_emit_kernel(FrontArgs<TX> a, c
 }
 
 // The backward passes need p_{t-1}, the precision entering each token, in reverse token order.  The
-// forward's emit pass saved the precision entering every even token of each tile (pe); a tile loads
-// its kVecChunk / 2 values into LDS (float4 per thread, 8 KB per wave), and the reverse pass takes
-// the tokens in pairs (2q + 1, 2q) and re-derives the odd token's entry value with one forward step
-// of token 2q, whose inputs it computes anyway.
+// forward's emit pass saved the precision entering every even token of each tile (pe); the reverse pass
+// takes the tokens in pairs (2q + 1, 2q), loads the pair's saved value with the pair's other inputs
+// (float4 per thread) and re-derives the odd token's entry value with one forward step of token 2q,
+// whose inputs it computes anyway.  (Staged in LDS for the whole tile, the values took 32 KB per
+// workgroup, which held the passes to five workgroups per CU.)
 __device__ __forceinline__ float4 f4(const float* x) { return float4{x[0], x[1], x[2], x[3]}; }
 __device__ __forceinline__ void unf4(float4 v, float* x) { x[0] = v.x, x[1] = v.y, x[2] = v.z, x[3] = v.w; }
-
-__device__ __forceinline__ void front_pe_load(const float* __restrict__ pe, const GainTile& g, int H, int NV, int K,
-                                              float4 (*lp)[256]) {
-  const int np = (g.t1 - g.t0 + 1) >> 1;
+// this thread's saved entry precisions of token pair q of its tile
+__device__ __forceinline__ float4 front_pe(const float* __restrict__ pe, const GainTile& g, int H, int NV, int K, int q) {
   const uint32_t tile = ((uint32_t)g.b * H + g.h) * NV + g.nt;
-#pragma unroll
-  for (int q = 0; q < kPairs; ++q)
-    if (q < np)
-      lp[q][threadIdx.x] = *reinterpret_cast<const float4*>(off32(pe, (tile * kPairs + q) * (uint32_t)K + g.i0));
+  return *reinterpret_cast<const float4*>(off32(pe, (tile * kPairs + q) * (uint32_t)K + g.i0));
 }
 
 // Backward map (reverse over the tile): the affine adjoint map (A, B) per channel, the per-token
@@ -1254,14 +1250,12 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
                                                                  const float* __restrict__ dG, float* __restrict__ ab,
                                                                  float* __restrict__ tdg, float* __restrict__ Gsave,
                                                                  float* __restrict__ Dsave) {
-  __shared__ float4 lp[kPairs][256];
   const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
   if (!g.ok) return;
   const int tpt = a.K / kCPT, L = g.t1 - g.t0;
   const float rate = __expf(a.A_log[g.h]);
   float bias[kCPT];
   ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
-  front_pe_load(pe, g, a.H, a.NV, a.K, lp);
   float Aacc[kCPT], Bacc[kCPT], sg[kCPT];
 #pragma unroll
   for (int j = 0; j < kCPT; ++j) Aacc[j] = 1.f, Bacc[j] = 0.f, sg[j] = 0.f;
@@ -1269,6 +1263,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
   for (int q = (L - 1) >> 1; q >= 0; --q) {
     FrontRaw<TX> raw[2];
     float dk_[2][kCPT], dg_[2][kCPT];
+    const float4 pe_q = front_pe(pe, g, a.H, a.NV, a.K, q);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {  // u = 0: token 2q + 1, u = 1: token 2q
       const uint32_t row = front_row(g, a.T, a.H, g.t0 + min(2 * q + 1 - u, L - 1));
@@ -1281,7 +1276,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_map_kernel(FrontArgs<TX> a
     float pp[2][kCPT];
 #pragma unroll
     for (int u = 0; u < 2; ++u) front_tok<false>(raw[u], rate, bias, tk[u], unused);
-    unf4(lp[q][threadIdx.x], pp[1]);
+    unf4(pe_q, pp[1]);
     front_step(pp[1], tk[1], a.s, pp[0]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -1335,14 +1330,12 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
     const float* __restrict__ prec0, int prec_mode, TX* __restrict__ dk, bf16_t* __restrict__ df,
     bf16_t* __restrict__ dz, bf16_t* __restrict__ dy, float* __restrict__ part_A, float* __restrict__ part_dt,
     float* __restrict__ dprec_part) {
-  __shared__ float4 lp[kPairs][256];
   const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
   if (!g.ok) return;
   const int tpt = a.K / kCPT, L = g.t1 - g.t0;
   const float rate = __expf(a.A_log[g.h]);
   float bias[kCPT];
   ldcf(a.dt_bias + g.h * a.K + g.i0, bias);
-  front_pe_load(pe, g, a.H, a.NV, a.K, lp);
   const uint32_t sb = ((uint32_t)g.b * a.H + g.h) * a.NV;
   float lam[kCPT], accg[kCPT], ddt[kCPT], dA = 0.f;
   ldcf(off32(lcarry, (sb + g.nt) * (uint32_t)a.K + g.i0), lam);
@@ -1360,6 +1353,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
     FrontRaw<TX> raw[2];
     float dk_[2][kCPT], dg_[2][kCPT], Gv[2], Dv[2];
     Bf4 dkm[2];
+    const float4 pe_q = front_pe(pe, g, a.H, a.NV, a.K, q);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {  // u = 0: token 2q + 1, u = 1: token 2q
       const uint32_t row = front_row(g, a.T, a.H, g.t0 + min(2 * q + 1 - u, L - 1));
@@ -1375,7 +1369,7 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
     float pp[2][kCPT];
 #pragma unroll
     for (int u = 0; u < 2; ++u) front_tok<true>(raw[u], rate, bias, tk[u], sgm[u]);
-    unf4(lp[q][threadIdx.x], pp[1]);
+    unf4(pe_q, pp[1]);
     front_step(pp[1], tk[1], a.s, pp[0]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
