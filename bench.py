@@ -96,6 +96,14 @@ def frontend_counts(variant: str, B: int, T: int, H: int, K: int):
     E = N * K
     if variant == "iso":
         per = {
+            # the scan's gate -> gain runs fused (lit_gpt/kdn_ops/iso_kdn_chunk.py iso_kdn_front):
+            # g_raw bf16, omega|r raw bf16 -> g_cumsum f32, a, omega, r, beta, p_prev f32 (a, omega, r, p_prev
+            # saved for the backward)
+            "iso_front_fwd": 6 * E + 28 * N,
+            # g_raw, omega|r raw, dg f32, dbeta, a, omega, r, p_prev -> dg_raw bf16, d omega|r raw bf16
+            # (the cotangents of a, omega, r stay on chip)
+            "iso_front_bwd": 8 * E + 28 * N,
+            # the two ops called separately:
             # g_raw bf16, omega|r raw bf16 -> g_cumsum f32, a, omega, r f32
             "iso_gate_fwd": 6 * E + 16 * N,
             # g_raw, omega|r raw, dg f32, da, domega, dr -> dg_raw bf16, d omega|r raw bf16

@@ -91,6 +91,36 @@ int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const f
                      float* domega, float* dr, float* d_initial_precision, void* workspace, size_t workspace_bytes,
                      hipStream_t stream);
 
+/* ---------------------------------------------------------------- fused iso front */
+/* kdn_iso_gate_fwd -> kdn_iso_gain_fwd (and their backwards) as the iso layer composes them
+ * (lit_gpt/iso_kdn.py:277-304 over iso_kdn_chunk.py:1317-1392, 1896-1962), chunk 64; no single
+ * counterpart in the reference, whose two ops it replaces with the same results.  The gain's prior is
+ * the gate's mu unless initial_precision is given ([H] for prec_mode 0, [B,H] for prec_mode 1).
+ * Forward: the gate's kernel also writes each chunk's gain map; one gain kernel carries them.  a,
+ * omega, r, mu are written (the backward reads them); p_prev and final_precision are nullable.
+ * Backward: the gain's reverse chunk maps, then the gate's backward kernel runs the gain's backward
+ * per chunk (the a/omega/r cotangents stay on chip).  dbeta is required, dg_pre and
+ * d_final_precision (which needs final_precision) are nullable; any gradient output may be NULL.
+ * dmu_param is zero when initial_precision is given; d_initial_precision has its shape.  Inputs the
+ * vector kernels cannot take (K not tiling the workgroup, unaligned rows) run the two ops' kernels one
+ * after the other, same results.  B * T == 0 is the caller's (the forward writes mu only). */
+size_t kdn_iso_front_workspace_size(int B, int T, int H, int K);
+int kdn_iso_front_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                      int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                      const float* dt_bias, const float* mu_param, float omega_min, float r_min,
+                      const float* initial_precision, int prec_mode, int B, int T, int H, int K, float posterior_scale,
+                      float* g_cumsum, float* a, float* omega, float* r, float* mu, float* beta, float* p_prev,
+                      float* final_precision, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int kdn_iso_front_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                      int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                      const float* dt_bias, const float* mu_param, const float* initial_precision, int prec_mode,
+                      const float* a, const float* omega, const float* r, const float* mu, const float* p_prev,
+                      const float* final_precision, const float* dg_pre, const float* dbeta,
+                      const float* d_final_precision, int B, int T, int H, int K, float posterior_scale, void* dg_raw,
+                      void* domega_r_raw, float* dA_log, float* ddt_bias, float* domega_bias, float* dr_bias,
+                      float* dmu_param, float* d_initial_precision, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
 /* ---------------------------------------------------------------- row norms */
 /* FLA l2norm_fwd / l2norm_bwd used inside _ChunkKDAPrecumsumFunction (iso_kdn_chunk.py:2203-2204,
  * 2229-2230): y = x * rsqrt(sum x^2 + eps), rstd [rows]. */

@@ -193,9 +193,9 @@ __global__ __launch_bounds__(256) void reduce_partials_vec_kernel(const float* _
 }
 
 // Several partial reductions (each as reduce_partials_vec_kernel with one segment, same summation order)
-// and the prior-precision VJP dmu_param = dmu * sigmoid(mu_param) in one launch: workgroup b serves
-// the segment whose block range holds it (64 outputs per workgroup); the workgroups past the last
-// segment form dmu_param.  The launches this replaces were each a few microseconds of dispatch.
+// and the prior-precision VJP in one launch: workgroup b serves the segment whose block range holds it
+// (64 outputs per workgroup); the workgroups past the last segment form the VJP.  The launches this
+// replaces were each a few microseconds of dispatch.
 struct PartSeg {
   const float* part;
   int64_t stride;
@@ -205,15 +205,21 @@ struct PartSeg {
 struct PartSegs {
   PartSeg seg[4];
   int nseg;
-  const float* mu_param;  // dmu_param = dmu * sigmoid(mu_param) over H entries when dmu_param != null
-  const float* dmu;       // (null: dmu = 0)
+  // The prior precision's cotangent over H entries: d = dmu (null: 0) plus, with rows_to_param,
+  // rows = sum over b < nrows of dmu_rows[b * H + h] (per batch row values, summed in order of b).
+  // dmu_param = d * sigmoid(mu_param) when dmu_param != null; dmu_sum = rows when dmu_sum != null.
+  const float* mu_param;
+  const float* dmu;
+  const float* dmu_rows;
+  int nrows, rows_to_param;
   int H;
   float* dmu_param;
+  float* dmu_sum;
 };
 inline int part_segs_blocks(const PartSegs& P) {
   int nb = 0;
   for (int i = 0; i < P.nseg; ++i) nb += (P.seg[i].n + 63) / 64;
-  return nb + (P.dmu_param ? (P.H + 255) / 256 : 0);
+  return nb + ((P.dmu_param || P.dmu_sum) ? (P.H + 255) / 256 : 0);
 }
 __global__ __launch_bounds__(256) void reduce_partials_multi_kernel(PartSegs P, int NP) {
   __shared__ float s[4][64];
@@ -226,8 +232,11 @@ __global__ __launch_bounds__(256) void reduce_partials_multi_kernel(PartSegs P, 
   if (i == P.nseg) {  // the prior-precision VJP
     const int hh = blk * 256 + threadIdx.x;
     if (hh < P.H) {
-      const float x = P.mu_param[hh];
-      P.dmu_param[hh] = P.dmu ? P.dmu[hh] * sigmoidf(x) : 0.f;
+      float rows = 0.f;
+      for (int bb = 0; bb < P.nrows; ++bb) rows += P.dmu_rows[(int64_t)bb * P.H + hh];
+      const float d = (P.dmu ? P.dmu[hh] : 0.f) + (P.rows_to_param ? rows : 0.f);
+      if (P.dmu_param) P.dmu_param[hh] = d * sigmoidf(P.mu_param[hh]);
+      if (P.dmu_sum) P.dmu_sum[hh] = rows;
     }
     return;
   }

@@ -7,6 +7,7 @@
 //   diag norm     lit_gpt/kdn_ops/diag_kdn_chunk.py:193-353
 //   FLA l2norm    iso_kdn_chunk.py:2203-2204,2229-2230 (x * rsqrt(sum x^2 + eps))
 #include "kdn_common.h"
+#include "kdn_iso_gain.h"
 #include "../../include/kdn.h"
 
 namespace {
@@ -142,15 +143,19 @@ __device__ __forceinline__ void store8<float>(float* p, const float* f) {
   reinterpret_cast<float4*>(p)[1] = float4{f[4], f[5], f[6], f[7]};
 }
 
-// grid (H * B * NT) with the head fastest, block 256.
-template <typename TG, typename TO>
+// grid (H * B * NT) with the head fastest, block 256.  With MAPS (chunk = 64, the fused front) the
+// workgroup also writes its chunk's gain map gain_maps[(b * H + h) * NT + nt] (posterior scale gain_s)
+// from the a, omega, r it has just produced.
+template <typename TG, typename TO, bool MAPS>
 __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
     const float* __restrict__ omega_bias, const float* __restrict__ r_bias, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const float* __restrict__ mu_param, float omega_min, float r_min,
     int T, int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ a_out,
-    float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out) {
+    float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out,
+    float4* __restrict__ gain_maps, float gain_s) {
   __shared__ float s_tot[256 * 8];  // [tg][K] group totals (TG * K = 2048)
+  __shared__ float s_ga[MAPS ? kIsoChunk : 1];  // MAPS: a of each token
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
   const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
   const int cg = tid % CG, tg = tid / CG, i0 = 8 * cg;
@@ -169,10 +174,11 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     const int t = min(tg * TPG + u, L - 1);
     load8<TG>(g_raw + (((int64_t)b * T + t0 + t) * H + h) * K + i0, xr[u]);
   }
+  const float om_t = omega_min + fsoftplus(or_t + omega_bias[h]), r_t = r_min + fsoftplus(rr_t + r_bias[h]);
   if (tid < L) {
     const int64_t o = ((int64_t)b * T + t0 + tid) * H + h;
-    omega_out[o] = omega_min + fsoftplus(or_t + omega_bias[h]);
-    r_out[o] = r_min + fsoftplus(rr_t + r_bias[h]);
+    omega_out[o] = om_t;
+    r_out[o] = r_t;
   }
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float pre[4][8];  // local inclusive prefix per token (TPG <= 4 when K >= 64 and chunk <= 64)
@@ -212,20 +218,34 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     // a = mean over channels of e^{2g}: reduce over the CG consecutive lanes of this token group
     float s = e2[u];
     for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
-    if (cg == 0 && u < TPG && t < L) a_out[((int64_t)b * T + t0 + t) * H + h] = s * (1.f / (float)K);  // K is a power of two: exact
+    if (cg == 0 && u < TPG && t < L) {
+      const float at = s * (1.f / (float)K);  // K is a power of two: exact
+      a_out[((int64_t)b * T + t0 + t) * H + h] = at;
+      if (MAPS) s_ga[t] = at;
+    }
   }
   if (blockIdx.x < H && tid == 0) mu_out[h] = 0.1f + fsoftplus(mu_param[h]);
+  if (MAPS) {
+    __syncthreads();
+    if (tid < kIsoChunk) {  // wave 0, lane = token
+      const Map2 M = wave_chunk_map(tid < L ? token_map(s_ga[tid], om_t, r_t, gain_s) : map_identity());
+      if (tid == 0) gain_maps[((int64_t)b * H + h) * NT + nt] = float4{M.m0, M.m1, M.m2, M.m3};
+    }
+  }
 }
 
 // grid (H * B * NT) with the head fastest, block 256.  Per-block partials as in iso_gate_bwd_kernel.
-template <typename TG, typename TO>
+// With GAIN (chunk = 64, the fused front) the cotangents of a, omega, r are not inputs: wave 0 runs the
+// gain's backward over this chunk of (b, h) from G (reverse chunk maps, the gain's saved state) and
+// hands each token's to the gate's math below.
+template <typename TG, typename TO, bool GAIN>
 __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     const TG* __restrict__ g_raw, const TO* __restrict__ orr, int64_t orr_sb, int64_t orr_st,
     const float* __restrict__ omega_bias, const float* __restrict__ r_bias, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const float* __restrict__ dg_pre, const float* __restrict__ da,
     const float* __restrict__ domega, const float* __restrict__ dr, int T, int H, int K, int chunk, int NT,
     TG* __restrict__ dg_raw, TO* __restrict__ dorr, float* __restrict__ part_A, float* __restrict__ part_dt,
-    float* __restrict__ part_bias) {
+    float* __restrict__ part_bias, IsoGainBwdArgs G) {
   __shared__ float s_tot[256 * 8];
   __shared__ float s_da[256];
   __shared__ float red[16];
@@ -240,9 +260,13 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
   // per-token scalars: thread tid owns token tid (chunk <= 256; loads clamped to the chunk, only
   // tid < L is used), so each is loaded once rather than by every channel group
   const int64_t srow = ((int64_t)b * T + t0 + min(tid, L - 1)) * H + h;
-  const float da_t = da ? da[srow] : 0.f;
-  const float do_t = domega ? domega[srow] : 0.f;
-  const float dr_t = dr ? dr[srow] : 0.f;
+  float da_t = 0.f, do_t = 0.f, dr_t = 0.f;
+  if (!GAIN) {
+    da_t = da ? da[srow] : 0.f;
+    do_t = domega ? domega[srow] : 0.f;
+    dr_t = dr ? dr[srow] : 0.f;
+  }
+  const bool has_da = GAIN || da, has_do = GAIN || domega, has_dr = GAIN || dr;  // GAIN: all present
   const int64_t sro = (int64_t)b * orr_sb + (int64_t)(t0 + min(tid, L - 1)) * orr_st + h;
   const float or_t = ld(orr, sro), rr_t = ld(orr, sro + H);
   // every vector load of this thread's tokens goes out first (rows clamped to the chunk; the
@@ -255,6 +279,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     if (dg_pre) load8<float>(dg_pre + row * K + i0, dgr_in[u]);
     load8<TG>(g_raw + row * K + i0, xr[u]);
   }
+  if (GAIN && tid < kIsoChunk) iso_gain_bwd_chunk(G, b, nt, h, T, H, L, da_t, do_t, dr_t);
   s_da[tid] = da_t * (2.f / (float)K);
   // local suffix sums of dg_pre over this thread's tokens (last token first)
   float dgp[4][8], acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -296,7 +321,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
         fsoftplus_sigmoid(xb, sp, sg);
         const float g = -rate * sp;
         float dgl = dg_pre ? off[j] + dgp[u][j] : 0.f;
-        if (da) dgl += dau * fexp(2.f * g);
+        if (has_da) dgl += dau * fexp(2.f * g);
         dgr[j] = dgl * (-rate) * sg;
         dA_term += dgl * g;
         ddt[j] += dgr[j];
@@ -305,8 +330,8 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     }
   }
   if (tid < L) {  // the per-token omega / r terms of token tid
-    const float ob = domega ? do_t * fsigmoid(or_t + omega_bias[h]) : 0.f;
-    const float rb = dr ? dr_t * fsigmoid(rr_t + r_bias[h]) : 0.f;
+    const float ob = has_do ? do_t * fsigmoid(or_t + omega_bias[h]) : 0.f;
+    const float rb = has_dr ? dr_t * fsigmoid(rr_t + r_bias[h]) : 0.f;
     dob = ob;
     drb = rb;
     if (dorr) {
@@ -884,6 +909,31 @@ inline bool gate_vec_ok(int K, int chunk) {  // the vector kernels also give eac
 // Row kernels: K/8 lanes per row, 8 elements per lane (K/8 a power of two dividing 64).
 inline bool row_vec_ok(int K) { return K % 8 == 0 && K <= 512 && 64 % (K / 8) == 0; }
 
+// The fused iso front's workspace parts (see kdn_iso_front_workspace_size).
+struct IsoFrontWs {
+  float* gate;
+  size_t gate_bytes;
+  void* gain;
+  size_t gain_bytes;
+  float* rows;
+  float* grads;
+};
+inline size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline IsoFrontWs iso_front_ws(void* ws, int B, int T, int H, int K) {
+  IsoFrontWs w;
+  char* p = (char*)ws;
+  w.gate = (float*)p;
+  w.gate_bytes = kdn_iso_gate_bwd_workspace_size(B, T, H, K, kIsoChunk);
+  p += al256(w.gate_bytes);
+  w.gain = p;
+  w.gain_bytes = kdn_iso_gain_workspace_size(B, T, H);
+  p += al256(w.gain_bytes);
+  w.rows = (float*)p;
+  p += al256((size_t)B * H * sizeof(float));
+  w.grads = (float*)p;
+  return w;
+}
+
 // ============================================================================
 // C ABI
 // ============================================================================
@@ -910,10 +960,14 @@ int kdn_iso_gate_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   dim3 grid(H * B * NT);
   const bool vec = gate_vec_ok(K, chunk) && aligned16(g_raw) && aligned16(g_cumsum) && aligned16(dt_bias);
 #define KDN_GATE_FWD(TG, TO)                                                                                     \
-  hipLaunchKernelGGL((vec ? iso_gate_fwd_vec_kernel<TG, TO> : iso_gate_fwd_kernel<TG, TO>), grid, dim3(256), 0,  \
-                     stream, (const TG*)g_raw,                                                                    \
-                     (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
-                     mu_param, omega_min, r_min, T, H, K, chunk, NT, g_cumsum, a, omega, r, mu)
+  if (vec)                                                                                                       \
+    hipLaunchKernelGGL((iso_gate_fwd_vec_kernel<TG, TO, false>), grid, dim3(256), 0, stream, (const TG*)g_raw,    \
+                       (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,   \
+                       mu_param, omega_min, r_min, T, H, K, chunk, NT, g_cumsum, a, omega, r, mu, nullptr, 0.f); \
+  else                                                                                                           \
+    hipLaunchKernelGGL((iso_gate_fwd_kernel<TG, TO>), grid, dim3(256), 0, stream, (const TG*)g_raw,              \
+                       (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,   \
+                       mu_param, omega_min, r_min, T, H, K, chunk, NT, g_cumsum, a, omega, r, mu)
   if (g_raw_bf16 && orr_bf16) KDN_GATE_FWD(bf16_t, bf16_t);
   else if (g_raw_bf16) KDN_GATE_FWD(bf16_t, float);
   else if (orr_bf16) KDN_GATE_FWD(float, bf16_t);
@@ -941,12 +995,18 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   const bool vec = gate_vec_ok(K, chunk) && aligned16(g_raw) && aligned16(dg_pre) && aligned16(dg_raw) &&
                    aligned16(dt_bias);
 #define KDN_GATE_BWD(TG, TO)                                                                                     \
-  hipLaunchKernelGGL((vec ? iso_gate_bwd_vec_kernel<TG, TO> : iso_gate_bwd_kernel<TG, TO>), grid, dim3(256), 0,  \
-                     stream, (const TG*)g_raw,                                                                    \
-                     (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
-                     dg_pre, da, domega, dr, T, H, K, chunk, NT, (TG*)dg_raw, (TO*)domega_r_raw,                 \
-                     dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr,                                    \
-                     (domega_bias || dr_bias) ? part_bias : nullptr)
+  if (vec)                                                                                                       \
+    hipLaunchKernelGGL((iso_gate_bwd_vec_kernel<TG, TO, false>), grid, dim3(256), 0, stream, (const TG*)g_raw,    \
+                       (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,   \
+                       dg_pre, da, domega, dr, T, H, K, chunk, NT, (TG*)dg_raw, (TO*)domega_r_raw,               \
+                       dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr,                                  \
+                       (domega_bias || dr_bias) ? part_bias : nullptr, IsoGainBwdArgs{});                        \
+  else                                                                                                           \
+    hipLaunchKernelGGL((iso_gate_bwd_kernel<TG, TO>), grid, dim3(256), 0, stream, (const TG*)g_raw,              \
+                       (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,   \
+                       dg_pre, da, domega, dr, T, H, K, chunk, NT, (TG*)dg_raw, (TO*)domega_r_raw,               \
+                       dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr,                                  \
+                       (domega_bias || dr_bias) ? part_bias : nullptr)
   if (g_raw_bf16 && orr_bf16) KDN_GATE_BWD(bf16_t, bf16_t);
   else if (g_raw_bf16) KDN_GATE_BWD(bf16_t, float);
   else if (orr_bf16) KDN_GATE_BWD(float, bf16_t);
@@ -964,6 +1024,135 @@ int kdn_iso_gate_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw,
   P.dmu = dmu;
   P.H = H;
   P.dmu_param = dmu_param;
+  const int nblk = part_segs_blocks(P);
+  if (nblk > 0) hipLaunchKernelGGL(reduce_partials_multi_kernel, dim3(nblk), dim3(256), 0, stream, P, NP);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+// ---------------------------------------------------------------- fused iso front
+// The gate and the gain as the layer composes them.  Workspace: the gate backward's partials, the gain's
+// workspace (the fused path's chunk maps), per-row prior cotangents [B*H], and the unfused path's
+// a / omega / r cotangents [3][B,T,H] plus a prior cotangent [H]; each part 256-byte aligned.
+
+size_t kdn_iso_front_workspace_size(int B, int T, int H, int K) {
+  if (B <= 0 || T <= 0 || H <= 0 || K <= 0) return 0;
+  return al256(kdn_iso_gate_bwd_workspace_size(B, T, H, K, kIsoChunk)) + al256(kdn_iso_gain_workspace_size(B, T, H)) +
+         al256((size_t)B * H * sizeof(float)) + al256(((size_t)3 * B * T * H + H) * sizeof(float));
+}
+
+int kdn_iso_front_fwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                      int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                      const float* dt_bias, const float* mu_param, float omega_min, float r_min,
+                      const float* initial_precision, int prec_mode, int B, int T, int H, int K, float posterior_scale,
+                      float* g_cumsum, float* a, float* omega, float* r, float* mu, float* beta, float* p_prev,
+                      float* final_precision, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (K <= 0 || K > 256 || B < 0 || T < 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
+  if ((prec_mode != 0 && prec_mode != 1) || (prec_mode == 1 && !initial_precision)) return KDN_ERR_ARG;
+  if (!a || !omega || !r || !mu || !beta) return KDN_ERR_ARG;
+  if (B == 0 || T == 0)  // mu only (the final precision of an empty sequence is the initial one: the caller's)
+    return kdn_iso_gate_fwd(g_raw, g_raw_bf16, omega_r_raw, orr_bf16, orr_stride_b, orr_stride_t, omega_bias, r_bias,
+                            A_log, dt_bias, mu_param, omega_min, r_min, B, T, H, K, kIsoChunk, g_cumsum, a, omega, r,
+                            mu, stream);
+  if (workspace_bytes < kdn_iso_front_workspace_size(B, T, H, K)) return KDN_ERR_ARG;
+  const IsoFrontWs ws = iso_front_ws(workspace, B, T, H, K);
+  const float* prior = initial_precision ? initial_precision : mu;
+  const bool vec = gate_vec_ok(K, kIsoChunk) && aligned16(g_raw) && aligned16(g_cumsum) && aligned16(dt_bias);
+  if (!vec) {  // the two ops one after the other
+    const int rc = kdn_iso_gate_fwd(g_raw, g_raw_bf16, omega_r_raw, orr_bf16, orr_stride_b, orr_stride_t, omega_bias,
+                                    r_bias, A_log, dt_bias, mu_param, omega_min, r_min, B, T, H, K, kIsoChunk,
+                                    g_cumsum, a, omega, r, mu, stream);
+    if (rc != 0) return rc;
+    return kdn_iso_gain_fwd(a, omega, r, prior, prec_mode, B, T, H, posterior_scale, beta, p_prev, final_precision,
+                            ws.gain, ws.gain_bytes, stream);
+  }
+  const int NC = cdiv(T, kIsoChunk);
+  float4* maps = (float4*)ws.gain;
+  dim3 grid(H * B * NC);
+#define KDN_FRONT_FWD(TG, TO)                                                                                    \
+  hipLaunchKernelGGL((iso_gate_fwd_vec_kernel<TG, TO, true>), grid, dim3(256), 0, stream, (const TG*)g_raw,      \
+                     (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
+                     mu_param, omega_min, r_min, T, H, K, kIsoChunk, NC, g_cumsum, a, omega, r, mu, maps,       \
+                     posterior_scale)
+  if (g_raw_bf16 && orr_bf16) KDN_FRONT_FWD(bf16_t, bf16_t);
+  else if (g_raw_bf16) KDN_FRONT_FWD(bf16_t, float);
+  else if (orr_bf16) KDN_FRONT_FWD(float, bf16_t);
+  else KDN_FRONT_FWD(float, float);
+#undef KDN_FRONT_FWD
+  launch_iso_gain_emit(a, omega, r, maps, prior, prec_mode, B, T, H, NC, posterior_scale, beta, p_prev,
+                       final_precision, stream);
+  KDN_CHECK_LAUNCH();
+  return 0;
+}
+
+int kdn_iso_front_bwd(const void* g_raw, int g_raw_bf16, const void* omega_r_raw, int orr_bf16, int64_t orr_stride_b,
+                      int64_t orr_stride_t, const float* omega_bias, const float* r_bias, const float* A_log,
+                      const float* dt_bias, const float* mu_param, const float* initial_precision, int prec_mode,
+                      const float* a, const float* omega, const float* r, const float* mu, const float* p_prev,
+                      const float* final_precision, const float* dg_pre, const float* dbeta,
+                      const float* d_final_precision, int B, int T, int H, int K, float posterior_scale, void* dg_raw,
+                      void* domega_r_raw, float* dA_log, float* ddt_bias, float* domega_bias, float* dr_bias,
+                      float* dmu_param, float* d_initial_precision, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
+  if (K <= 0 || K > 256 || B <= 0 || T <= 0 || H <= 0 || H > 96 || !(posterior_scale > 0.f)) return KDN_ERR_ARG;
+  if ((prec_mode != 0 && prec_mode != 1) || (prec_mode == 1 && !initial_precision)) return KDN_ERR_ARG;
+  if (!a || !omega || !r || !mu || !p_prev || !dbeta || (d_final_precision && !final_precision)) return KDN_ERR_ARG;
+  if (workspace_bytes < kdn_iso_front_workspace_size(B, T, H, K)) return KDN_ERR_ARG;
+  const IsoFrontWs ws = iso_front_ws(workspace, B, T, H, K);
+  const float* prior = initial_precision ? initial_precision : mu;
+  const bool vec = gate_vec_ok(K, kIsoChunk) && aligned16(g_raw) && aligned16(dg_pre) && aligned16(dg_raw) &&
+                   aligned16(dt_bias);
+  if (!vec) {  // the gain's backward into the workspace, then the gate's
+    const int64_t n = (int64_t)B * T * H;
+    float *gda = ws.grads, *gdo = gda + n, *gdr = gdo + n, *gdmu = gdr + n;
+    int rc = kdn_iso_gain_bwd(a, omega, r, prior, prec_mode, dbeta, p_prev, final_precision, d_final_precision, B, T,
+                              H, posterior_scale, gda, gdo, gdr, initial_precision ? d_initial_precision : gdmu,
+                              ws.gain, ws.gain_bytes, stream);
+    if (rc != 0) return rc;
+    return kdn_iso_gate_bwd(g_raw, g_raw_bf16, omega_r_raw, orr_bf16, orr_stride_b, orr_stride_t, omega_bias, r_bias,
+                            A_log, dt_bias, mu_param, dg_pre, gda, gdo, gdr, initial_precision ? nullptr : gdmu, B, T,
+                            H, K, kIsoChunk, dg_raw, domega_r_raw, dA_log, ddt_bias, domega_bias, dr_bias, dmu_param,
+                            ws.gate, ws.gate_bytes, stream);
+  }
+  const int NC = cdiv(T, kIsoChunk), NP = B * NC;
+  float2* maps = (float2*)ws.gain;
+  launch_iso_gain_bwd_map(a, omega, r, dbeta, p_prev, B, T, H, NC, posterior_scale, maps, stream);
+  // per-row prior cotangents: the [B,H] initial precision's own (prec_mode 1), else rows summed below
+  float* rows = nullptr;
+  if (prec_mode == 1) rows = d_initial_precision;
+  else if (initial_precision ? d_initial_precision != nullptr : dmu_param != nullptr) rows = ws.rows;
+  const IsoGainBwdArgs G{maps, a, omega, r, dbeta, p_prev, final_precision, d_final_precision, prior, rows,
+                         prec_mode, NC, posterior_scale == 1.f ? 1 : 0, posterior_scale};
+  float* part_A = ws.gate;
+  float* part_dt = part_A + (int64_t)NP * H;
+  float* part_bias = part_dt + (int64_t)NP * H * K;
+  dim3 grid(H * NP);  // head fastest
+#define KDN_FRONT_BWD(TG, TO)                                                                                    \
+  hipLaunchKernelGGL((iso_gate_bwd_vec_kernel<TG, TO, true>), grid, dim3(256), 0, stream, (const TG*)g_raw,      \
+                     (const TO*)omega_r_raw, orr_stride_b, orr_stride_t, omega_bias, r_bias, A_log, dt_bias,     \
+                     dg_pre, nullptr, nullptr, nullptr, T, H, K, kIsoChunk, NC, (TG*)dg_raw, (TO*)domega_r_raw,  \
+                     dA_log ? part_A : nullptr, ddt_bias ? part_dt : nullptr,                                    \
+                     (domega_bias || dr_bias) ? part_bias : nullptr, G)
+  if (g_raw_bf16 && orr_bf16) KDN_FRONT_BWD(bf16_t, bf16_t);
+  else if (g_raw_bf16) KDN_FRONT_BWD(bf16_t, float);
+  else if (orr_bf16) KDN_FRONT_BWD(float, bf16_t);
+  else KDN_FRONT_BWD(float, float);
+#undef KDN_FRONT_BWD
+  KDN_CHECK_LAUNCH();
+  PartSegs P{};
+  if (dA_log) P.seg[P.nseg++] = PartSeg{part_A, (int64_t)H, H, dA_log};
+  if (ddt_bias) P.seg[P.nseg++] = PartSeg{part_dt, (int64_t)H * K, H * K, ddt_bias};
+  if (domega_bias) P.seg[P.nseg++] = PartSeg{part_bias, (int64_t)2 * H, H, domega_bias};
+  if (dr_bias) P.seg[P.nseg++] = PartSeg{part_bias + H, (int64_t)2 * H, H, dr_bias};
+  P.mu_param = mu_param;
+  P.H = H;
+  P.dmu_param = dmu_param;  // the gain's prior is mu only without an initial precision (else zero)
+  if (prec_mode == 0 && rows) {
+    P.dmu_rows = rows;
+    P.nrows = B;
+    P.rows_to_param = initial_precision ? 0 : 1;
+    P.dmu_sum = initial_precision ? d_initial_precision : nullptr;
+  }
   const int nblk = part_segs_blocks(P);
   if (nblk > 0) hipLaunchKernelGGL(reduce_partials_multi_kernel, dim3(nblk), dim3(256), 0, stream, P, NP);
   KDN_CHECK_LAUNCH();

@@ -18,70 +18,17 @@
 #include <mutex>
 
 #include "kdn_common.h"
+#include "kdn_iso_gain.h"
 #include "../../include/kdn.h"
 
 namespace {
 
 // ----------------------------------------------------------------------------
-// 2x2 map helpers (row-major m0 m1 / m2 m3).  compose(a, b) = a * b (b applied first).
+// iso gain, standalone entry points: map / emit forward, map / carry / emit backward over 64-token
+// chunks (the emit forward and the backward map are shared with the fused front, kdn_iso_gain.h).
+// Workspace (5 floats per (b, h, chunk)): forward maps [B*H][NC] x 4 floats; backward maps [B*H][NC] x 2
+// floats, then lambda after each chunk [B*H][NC].
 // ----------------------------------------------------------------------------
-struct Map2 {
-  float m0, m1, m2, m3;
-};
-__device__ __forceinline__ Map2 map_mul(const Map2& a, const Map2& b) {
-  Map2 c{a.m0 * b.m0 + a.m1 * b.m2, a.m0 * b.m1 + a.m1 * b.m3, a.m2 * b.m0 + a.m3 * b.m2,
-         a.m2 * b.m1 + a.m3 * b.m3};
-  const float s = fmaxf(fmaxf(fabsf(c.m0), fabsf(c.m1)), fmaxf(fabsf(c.m2), fabsf(c.m3)));
-  const float inv = 1.f / fmaxf(s, 1e-30f);
-  c.m0 *= inv; c.m1 *= inv; c.m2 *= inv; c.m3 *= inv;
-  return c;
-}
-__device__ __forceinline__ float mobius(const Map2& m, float p) { return (m.m0 * p + m.m1) / (m.m2 * p + m.m3); }
-// The same with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of the IEEE division sequence: the
-// isotropic gain's passes are chains of dependent map products, and a Mobius map is invariant under a
-// common factor, so the renormalisation needs no exact reciprocal.
-__device__ __forceinline__ Map2 map_mul_r(const Map2& a, const Map2& b) {
-  Map2 c{a.m0 * b.m0 + a.m1 * b.m2, a.m0 * b.m1 + a.m1 * b.m3, a.m2 * b.m0 + a.m3 * b.m2,
-         a.m2 * b.m1 + a.m3 * b.m3};
-  const float s = fmaxf(fmaxf(fabsf(c.m0), fabsf(c.m1)), fmaxf(fabsf(c.m2), fabsf(c.m3)));
-  const float inv = frcp(fmaxf(s, 1e-30f));
-  c.m0 *= inv; c.m1 *= inv; c.m2 *= inv; c.m3 *= inv;
-  return c;
-}
-__device__ __forceinline__ float mobius_r(const Map2& m, float p) { return (m.m0 * p + m.m1) * frcp(m.m2 * p + m.m3); }
-__device__ __forceinline__ Map2 shfl_up_map(const Map2& m, int d) {
-  return Map2{__shfl_up(m.m0, d, 64), __shfl_up(m.m1, d, 64), __shfl_up(m.m2, d, 64), __shfl_up(m.m3, d, 64)};
-}
-
-// ----------------------------------------------------------------------------
-// iso gain: chunked map / carry / emit over 64-token chunks.  a, omega, r, beta, p_prev are
-// [B,T,H] (heads interleaved), so the map and emit kernels stage a chunk's contiguous
-// [64][H] tile in LDS; four threads per head compose or replay 16 tokens each.  The carry
-// kernel scans one (b, h) stream's chunk maps with a wave (64 chunks per step).
-//   forward map of a token:  p -> (r a p + r w) / (s a p + r + s w)       (p' = r z / (r + s z))
-//   backward (reverse):      lambda_{t-1} = A_t lambda_t + B_t,
-//                            A_t = a r^2 / (r + s z)^2,  B_t = a dbeta r / (r + z)^2
-// Workspace: maps [B*H][NC] x 4 floats, then per-chunk carries [B*H][NC].
-// ----------------------------------------------------------------------------
-constexpr int kIsoChunk = 64;
-constexpr int kIsoSub = 4;  // threads per head in a chunk (16 tokens each)
-
-__device__ __forceinline__ Map2 map_identity() { return Map2{1.f, 0.f, 0.f, 1.f}; }
-__device__ __forceinline__ Map2 token_map(float at, float wt, float rt, float s) {
-  return Map2{rt * at, rt * wt, s * at, rt + s * wt};
-}
-
-// Stage rows [t0, t0 + L) of a [B,T,H] array into LDS tile[t][h] (coalesced).
-__device__ __forceinline__ void stage_bth(const float* __restrict__ x, int b, int T, int H, int t0, int L,
-                                          float* tile) {
-  const int64_t base = ((int64_t)b * T + t0) * H;
-  for (int e = threadIdx.x; e < L * H; e += blockDim.x) tile[e] = x[base + e];
-}
-__device__ __forceinline__ void store_bth(float* __restrict__ x, int b, int T, int H, int t0, int L,
-                                          const float* tile) {
-  const int64_t base = ((int64_t)b * T + t0) * H;
-  for (int e = threadIdx.x; e < L * H; e += blockDim.x) x[base + e] = tile[e];
-}
 
 // grid (NC, B), block 256, dynamic LDS 3 * 64 * H floats + 4 * H maps.
 __global__ __launch_bounds__(256) void iso_gain_map_kernel(const float* __restrict__ a, const float* __restrict__ omega,
@@ -91,15 +38,14 @@ __global__ __launch_bounds__(256) void iso_gain_map_kernel(const float* __restri
   float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H;
   Map2* sub = reinterpret_cast<Map2*>(sm + 3 * kIsoChunk * H);
   const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
-  stage_bth(a, b, T, H, t0, L, sa);
-  stage_bth(omega, b, T, H, t0, L, sw);
-  stage_bth(r, b, T, H, t0, L, sr);
+  stage_bth_n<3>({a, omega, r}, b, T, H, t0, L, sa);
   __syncthreads();
   constexpr int SL = kIsoChunk / kIsoSub;
   for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
     const int h = hq / kIsoSub, q = hq % kIsoSub;
     Map2 M = map_identity();
-    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul_r(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
+    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t)
+      M = map_mul_r(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
     sub[hq] = M;
   }
   __syncthreads();
@@ -107,121 +53,6 @@ __global__ __launch_bounds__(256) void iso_gain_map_kernel(const float* __restri
     Map2 M = sub[kIsoSub * h];
     for (int q = 1; q < kIsoSub; ++q) M = map_mul_r(sub[kIsoSub * h + q], M);
     maps[((int64_t)b * H + h) * NC + n] = float4{M.m0, M.m1, M.m2, M.m3};
-  }
-}
-
-// grid (B*H), block 64: p at each chunk start (carry) and the final precision.  The initial
-// precision mu is per head ([H], prec_mode 0) or per batch row and head ([B,H], prec_mode 1: the
-// final precision of an earlier segment of the same sequences).
-__global__ __launch_bounds__(64) void iso_gain_carry_kernel(const float4* __restrict__ maps,
-                                                            const float* __restrict__ mu, int prec_mode, int H,
-                                                            int NC, float* __restrict__ carry,
-                                                            float* __restrict__ final_precision) {
-  const int bh = blockIdx.x, h = bh % H, lane = threadIdx.x;
-  float p = 1.f / mu[prec_mode ? bh : h];
-  for (int c0 = 0; c0 < NC; c0 += 64) {
-    const int c = c0 + lane;
-    Map2 M = map_identity();
-    if (c < NC) {
-      const float4 m = maps[(int64_t)bh * NC + c];
-      M = Map2{m.x, m.y, m.z, m.w};
-    }
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const Map2 prev = shfl_up_map(M, d);
-      if (lane >= d) M = map_mul_r(M, prev);
-    }
-    Map2 E = shfl_up_map(M, 1);
-    if (lane == 0) E = map_identity();
-    if (c < NC) carry[(int64_t)bh * NC + c] = mobius_r(E, p);
-    const Map2 tot{__shfl(M.m0, 63, 64), __shfl(M.m1, 63, 64), __shfl(M.m2, 63, 64), __shfl(M.m3, 63, 64)};
-    p = mobius_r(tot, p);
-  }
-  if (final_precision && lane == 0) final_precision[bh] = 1.f / p;
-}
-
-// grid (NC, B), block 256, dynamic LDS 5 * 64 * H floats + 4 * H maps.
-__global__ __launch_bounds__(256) void iso_gain_emit_kernel(const float* __restrict__ a, const float* __restrict__ omega,
-                                                            const float* __restrict__ r, int B, int T, int H, int NC,
-                                                            float s, int unit_scale, const float* __restrict__ carry,
-                                                            float* __restrict__ beta, float* __restrict__ p_prev) {
-  extern __shared__ float sm[];
-  float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H, *sbeta = sm + 3 * kIsoChunk * H,
-        *spp = sm + 4 * kIsoChunk * H;
-  Map2* sub = reinterpret_cast<Map2*>(sm + 5 * kIsoChunk * H);
-  const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
-  stage_bth(a, b, T, H, t0, L, sa);
-  stage_bth(omega, b, T, H, t0, L, sw);
-  stage_bth(r, b, T, H, t0, L, sr);
-  __syncthreads();
-  constexpr int SL = kIsoChunk / kIsoSub;
-  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
-    const int h = hq / kIsoSub, q = hq % kIsoSub;
-    Map2 M = map_identity();
-    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) M = map_mul_r(token_map(sa[t * H + h], sw[t * H + h], sr[t * H + h], s), M);
-    sub[hq] = M;
-  }
-  __syncthreads();
-  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
-    const int h = hq / kIsoSub, q = hq % kIsoSub;
-    Map2 E = map_identity();
-    for (int q2 = 0; q2 < q; ++q2) E = map_mul_r(sub[kIsoSub * h + q2], E);
-    float p = mobius_r(E, carry[((int64_t)b * H + h) * NC + n]);
-    for (int t = q * SL; t < min(L, (q + 1) * SL); ++t) {
-      const float at = sa[t * H + h], wt = sw[t * H + h], rt = sr[t * H + h];
-      spp[t * H + h] = p;
-      const float z = at * p + wt;
-      const float g = z * frcp(rt + z);
-      sbeta[t * H + h] = g;
-      p = unit_scale ? rt * g : rt * z * frcp(rt + s * z);
-    }
-  }
-  __syncthreads();
-  store_bth(beta, b, T, H, t0, L, sbeta);
-  if (p_prev) store_bth(p_prev, b, T, H, t0, L, spp);
-}
-
-// Affine maps x -> A x + B of the reverse recurrence; compose(f, g) = f o g (g applied first).
-__device__ __forceinline__ float2 aff_compose(float2 f, float2 g) { return float2{f.x * g.x, f.x * g.y + f.y}; }
-__device__ __forceinline__ float2 token_aff(float at, float wt, float rt, float dl, float pp, float s) {
-  const float z = at * pp + wt;
-  const float ig = frcp(rt + z), ip = frcp(rt + s * z);
-  return float2{at * rt * rt * ip * ip, at * dl * rt * ig * ig};
-}
-
-// grid (NC, B), block 256, dynamic LDS 5 * 64 * H floats + 2 * 4 * H.
-__global__ __launch_bounds__(256) void iso_gain_bwd_map_kernel(const float* __restrict__ a,
-                                                               const float* __restrict__ omega,
-                                                               const float* __restrict__ r,
-                                                               const float* __restrict__ dbeta,
-                                                               const float* __restrict__ p_prev, int T, int H, int NC,
-                                                               float s, float2* __restrict__ maps) {
-  extern __shared__ float sm[];
-  float *sa = sm, *sw = sm + kIsoChunk * H, *sr = sm + 2 * kIsoChunk * H, *sd = sm + 3 * kIsoChunk * H,
-        *sp = sm + 4 * kIsoChunk * H;
-  float2* sub = reinterpret_cast<float2*>(sm + 5 * kIsoChunk * H);
-  const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
-  stage_bth(a, b, T, H, t0, L, sa);
-  stage_bth(omega, b, T, H, t0, L, sw);
-  stage_bth(r, b, T, H, t0, L, sr);
-  stage_bth(dbeta, b, T, H, t0, L, sd);
-  stage_bth(p_prev, b, T, H, t0, L, sp);
-  __syncthreads();
-  constexpr int SL = kIsoChunk / kIsoSub;
-  for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
-    const int h = hq / kIsoSub, q = hq % kIsoSub;
-    float2 F{1.f, 0.f};  // lambda before the sub-segment from lambda after it
-    for (int t = min(L, (q + 1) * SL) - 1; t >= q * SL; --t) {
-      const int e = t * H + h;
-      F = aff_compose(token_aff(sa[e], sw[e], sr[e], sd[e], sp[e], s), F);  // earlier token applied after
-    }
-    sub[hq] = F;
-  }
-  __syncthreads();
-  for (int h = threadIdx.x; h < H; h += blockDim.x) {
-    float2 F = sub[kIsoSub * h + kIsoSub - 1];
-    for (int q = kIsoSub - 2; q >= 0; --q) F = aff_compose(sub[kIsoSub * h + q], F);
-    maps[((int64_t)b * H + h) * NC + n] = F;
   }
 }
 
@@ -283,11 +114,7 @@ __global__ __launch_bounds__(256) void iso_gain_bwd_emit_kernel(
         *orr = sm + 7 * kIsoChunk * H;
   float2* sub = reinterpret_cast<float2*>(sm + 8 * kIsoChunk * H);
   const int n = blockIdx.x, b = blockIdx.y, t0 = n * kIsoChunk, L = min(kIsoChunk, T - t0);
-  stage_bth(a, b, T, H, t0, L, sa);
-  stage_bth(omega, b, T, H, t0, L, sw);
-  stage_bth(r, b, T, H, t0, L, sr);
-  stage_bth(dbeta, b, T, H, t0, L, sd);
-  stage_bth(p_prev, b, T, H, t0, L, sp);
+  stage_bth_n<5>({a, omega, r, dbeta, p_prev}, b, T, H, t0, L, sa);
   __syncthreads();
   constexpr int SL = kIsoChunk / kIsoSub;
   for (int hq = threadIdx.x; hq < kIsoSub * H; hq += blockDim.x) {
@@ -309,24 +136,7 @@ __global__ __launch_bounds__(256) void iso_gain_bwd_emit_kernel(
     }
     for (int t = min(L, (q + 1) * SL) - 1; t >= q * SL; --t) {
       const int e = t * H + h;
-      const float at = sa[e], wt = sw[e], rt = sr[e], dl = sd[e], pp = sp[e];
-      const float z = at * pp + wt;
-      const float ig = frcp(rt + z);
-      const float ig2 = ig * ig;
-      float zbar, drt;
-      if (unit_scale) {
-        zbar = (dl + rt * lam) * rt * ig2;
-        drt = z * (lam * z - dl) * ig2;
-      } else {
-        const float ip = frcp(rt + s * z);
-        const float ip2 = ip * ip;
-        zbar = dl * rt * ig2 + lam * rt * rt * ip2;
-        drt = -dl * z * ig2 + lam * s * z * z * ip2;
-      }
-      oa[e] = zbar * pp;
-      ow[e] = zbar;
-      orr[e] = drt;
-      lam = at * zbar;
+      lam = token_grad(sa[e], sw[e], sr[e], sd[e], sp[e], lam, s, unit_scale != 0, oa[e], ow[e], orr[e]);
     }
   }
   __syncthreads();
@@ -1507,16 +1317,12 @@ int kdn_iso_gain_fwd(const float* a, const float* omega, const float* r, const f
   if (workspace_bytes < kdn_iso_gain_workspace_size(B, T, H)) return KDN_ERR_ARG;
   const int NC = cdiv(T, kIsoChunk);
   float4* maps = (float4*)workspace;
-  float* carry = (float*)(maps + (int64_t)B * H * NC);
   const int unit = posterior_scale == 1.f ? 1 : 0;
   const size_t lds_map = (size_t)(3 * kIsoChunk * H + 4 * kIsoSub * H) * sizeof(float);
-  const size_t lds_emit = (size_t)(5 * kIsoChunk * H + 4 * kIsoSub * H) * sizeof(float);
   hipLaunchKernelGGL(iso_gain_map_kernel, dim3(NC, B), dim3(256), lds_map, stream, a, omega, r, T, H, NC,
                      posterior_scale, maps);
-  hipLaunchKernelGGL(iso_gain_carry_kernel, dim3(B * H), dim3(64), 0, stream, maps, initial_precision, prec_mode, H,
-                     NC, carry, final_precision);
-  hipLaunchKernelGGL(iso_gain_emit_kernel, dim3(NC, B), dim3(256), lds_emit, stream, a, omega, r, B, T, H, NC,
-                     posterior_scale, unit, carry, beta, p_prev);
+  launch_iso_gain_emit(a, omega, r, maps, initial_precision, prec_mode, B, T, H, NC, posterior_scale, beta, p_prev,
+                       final_precision, stream);
   KDN_CHECK_LAUNCH();
   return 0;
 }
@@ -1558,11 +1364,9 @@ int kdn_iso_gain_bwd(const float* a, const float* omega, const float* r, const f
   float2* maps = (float2*)workspace;
   float* carry = (float*)(maps + (int64_t)B * H * NC);
   const int unit = posterior_scale == 1.f ? 1 : 0;
-  const size_t lds_map = (size_t)(5 * kIsoChunk * H + 2 * kIsoSub * H) * sizeof(float);
   const size_t lds_emit = (size_t)(8 * kIsoChunk * H + 2 * kIsoSub * H) * sizeof(float);
   const int GB = B < 16 ? B : 16;
-  hipLaunchKernelGGL(iso_gain_bwd_map_kernel, dim3(NC, B), dim3(256), lds_map, stream, a, omega, r, dbeta, p_prev, T,
-                     H, NC, posterior_scale, maps);
+  launch_iso_gain_bwd_map(a, omega, r, dbeta, p_prev, B, T, H, NC, posterior_scale, maps, stream);
   hipLaunchKernelGGL(iso_gain_bwd_carry_kernel, dim3(H), dim3(64 * GB), 0, stream, maps, initial_precision, prec_mode,
                      B, H, NC, final_precision, d_final_precision, carry, d_initial_precision);
   hipLaunchKernelGGL(iso_gain_bwd_emit_kernel, dim3(NC, B), dim3(256), lds_emit, stream, a, omega, r, dbeta, p_prev, T,

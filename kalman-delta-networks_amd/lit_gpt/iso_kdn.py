@@ -21,7 +21,7 @@ from torch import nn
 
 from ._inference import as_f32, linear, packed_weight, use_packed
 from .kdn_ops.gated_norm import FusedRMSNormGated
-from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
+from .kdn_ops.iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_front
 from .kdn_ops.short_conv import qkv_causal_conv1d, short_conv_step
 from .kdn_ops.step import kdn_kalman_step
 from .kdn_state import CONV_TAIL, carry_state, check_state, conv_input_with_tail
@@ -217,18 +217,18 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
         q, k = q.reshape(B, T, H, K), k.reshape(B, T, H, K)
         v = v.reshape(B, T, H, self.head_v_dim)
         g_raw = g_raw.view(B, T, H, K)
-        g_cumsum, a, omega, r, initial_precision = _iso_kdn_gate_precumsum_paired(
-            g_raw, omega_r_raw, as_f32(self, "omega_bias", self.omega_proj.bias), as_f32(self, "r_bias", self.r_proj.bias),
-            as_f32(self, "A_log", self.A_log), as_f32(self, "dt_bias", self.dt_bias),
-            as_f32(self, "mu_param", self.initial_precision_param), self.omega_min, self.r_min)
+        gate_args = (g_raw, omega_r_raw, as_f32(self, "omega_bias", self.omega_proj.bias),
+                     as_f32(self, "r_bias", self.r_proj.bias), as_f32(self, "A_log", self.A_log),
+                     as_f32(self, "dt_bias", self.dt_bias), as_f32(self, "mu_param", self.initial_precision_param),
+                     self.omega_min, self.r_min)
         new_state = None
-        if not stateful:
-            gain = iso_kdn_gain(a, omega, r, initial_precision, head_dim=K, out_dtype=torch.float32,
-                                info_scale=self.info_scale)
+        if not stateful:  # gate -> gain fused (the reference's two ops, same results)
+            g_cumsum, gain = iso_kdn_front(*gate_args, head_dim=K, info_scale=self.info_scale)
             output = _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain)
         else:
-            prec0 = state.precision if state is not None else initial_precision
             if T == 1 and not torch.is_grad_enabled():  # gain and memory of one token in one launch
+                g_cumsum, a, omega, r, initial_precision = _iso_kdn_gate_precumsum_paired(*gate_args)
+                prec0 = state.precision if state is not None else initial_precision
                 inplace = state is not None and state.inplace
                 if state is None:
                     memory = torch.zeros(B, H, K, self.head_v_dim, device=q.device, dtype=torch.float32)
@@ -239,8 +239,9 @@ class IsotropicKalmanDeltaNetwork(nn.Module):
                     omega=omega, r=r, info_scale=self.info_scale,
                     precision_out=state.precision_scratch() if inplace else None)
             else:
-                gain, precision = iso_kdn_gain(a, omega, r, prec0, head_dim=K, out_dtype=torch.float32,
-                                               info_scale=self.info_scale, output_final_state=True)
+                g_cumsum, gain, precision = iso_kdn_front(
+                    *gate_args, head_dim=K, info_scale=self.info_scale,
+                    initial_precision=state.precision if state is not None else None, output_final_state=True)
                 output, memory = _chunk_kda_precumsum_paired(
                     q=q, k=k, v=v, g_cumsum=g_cumsum, beta=gain,
                     initial_state=state.memory if state is not None else None, output_final_state=True)

@@ -23,6 +23,9 @@ _SIGS = {
     "kdn_iso_gain_fwd": "ppppiiiifppppzs",
     "kdn_iso_gain_fwd_noalloc": "ppppiiiifppps",
     "kdn_iso_gain_bwd": "ppppippppiiifpppppzs",
+    "kdn_iso_front_workspace_size": "iiii",
+    "kdn_iso_front_fwd": "pipill" "ppppp" "ff" "pi" "iiii" "f" "pppppppp" "pzs",
+    "kdn_iso_front_bwd": "pipill" "pppppp" "i" "ppppppppp" "iiii" "f" "pppppppp" "pzs",
     "kdn_l2norm_fwd": "pilifpips",
     "kdn_l2norm_bwd": "pippilips",
     "kdn_diag_norm_fwd": "ppilippppps",
@@ -59,7 +62,8 @@ _SIGS = {
     "kdn_rms_norm_gated_bwd_workspace_size": "li",
     "kdn_rms_norm_gated_bwd": "pipipippliippppzs",
 }
-_SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_iso_gain_workspace_size", "kdn_diag_frontend_bwd_workspace_size",
+_SIZE_FNS = {"kdn_iso_gate_bwd_workspace_size", "kdn_iso_gain_workspace_size", "kdn_iso_front_workspace_size",
+             "kdn_diag_frontend_bwd_workspace_size",
              "kdn_diag_gain_workspace_size", "kdn_diag_front_saved_size",
              "kdn_diag_front_workspace_size", "kdn_mem_saved_size", "kdn_mem_bwd_workspace_size",
              "kdn_short_conv_bwd_workspace_size", "kdn_rms_norm_gated_bwd_workspace_size",

@@ -9,7 +9,8 @@ Drop-in for the hot-path entry points of the reference module
 * ``qkv_causal_conv1d``               (reference :468-478; implemented in ``short_conv.py``)
 
 with the same argument order, dtypes, return tuples, autograd.Function structure and
-Python-side errors.  All arithmetic runs in the HIP library (``libkdn_hip.so``); there is
+Python-side errors.  ``iso_kdn_front`` is the first two as the layer composes them, fused
+(same results; no counterpart in the reference).  All arithmetic runs in the HIP library (``libkdn_hip.so``); there is
 no PyTorch or CPU fallback.  The packed projections of the reference module (plain GEMMs,
 iso_kdn_chunk.py:480-729) are not part of this package.
 """
@@ -206,6 +207,23 @@ def _require_same_cuda_device(a, *named_tensors):
     return device
 
 
+def _posterior_scale(head_dim, info_scale):
+    """s = info_scale / head_dim with the reference's checks (iso_kdn_chunk.py:2002-2020)."""
+    if isinstance(head_dim, bool) or not isinstance(head_dim, int):
+        raise TypeError(f"head_dim must be a positive int, got {type(head_dim).__name__}")
+    if head_dim <= 0:
+        raise ValueError(f"head_dim must be positive, got {head_dim}")
+    if info_scale is None:
+        resolved = float(head_dim)
+    else:
+        if isinstance(info_scale, bool) or not isinstance(info_scale, Real):
+            raise TypeError(f"info_scale must be a positive finite real, got {type(info_scale).__name__}")
+        resolved = float(info_scale)
+        if not math.isfinite(resolved) or resolved <= 0:
+            raise ValueError(f"info_scale must be positive and finite, got {info_scale!r}")
+    return resolved / float(head_dim)
+
+
 def _iso_kdn_gain_forward(a, omega, r, initial_precision, *, out_dtype, save_state, posterior_scale,
                           output_final_state=False):
     """Returns (beta, p_prev or None, final_precision [B,H] or None).  ``initial_precision`` is
@@ -315,26 +333,131 @@ def iso_kdn_gain(a, omega, r, initial_precision, *, head_dim, out_dtype=None, in
         raise ValueError(f"initial_precision must have shape [{H}] or [{B},{H}], "
                          f"got {tuple(initial_precision.shape)}")
     _require_same_cuda_device(a, ("omega", omega), ("r", r), ("initial_precision", initial_precision))
-    if isinstance(head_dim, bool) or not isinstance(head_dim, int):
-        raise TypeError(f"head_dim must be a positive int, got {type(head_dim).__name__}")
-    if head_dim <= 0:
-        raise ValueError(f"head_dim must be positive, got {head_dim}")
     if out_dtype is None:
         out_dtype = torch.float32
-    if info_scale is None:
-        resolved = float(head_dim)
-    else:
-        if isinstance(info_scale, bool) or not isinstance(info_scale, Real):
-            raise TypeError(f"info_scale must be a positive finite real, got {type(info_scale).__name__}")
-        resolved = float(info_scale)
-        if not math.isfinite(resolved) or resolved <= 0:
-            raise ValueError(f"info_scale must be positive and finite, got {info_scale!r}")
-    posterior_scale = resolved / float(head_dim)
+    posterior_scale = _posterior_scale(head_dim, info_scale)
     needs_backward = torch.is_grad_enabled() and any(
         t.requires_grad for t in (a, omega, r, initial_precision))
     return _IsoKDNGainFunction.apply(a.float().contiguous(), omega.float().contiguous(), r.float().contiguous(),
                                      initial_precision.float().contiguous(), out_dtype, posterior_scale,
                                      needs_backward, bool(output_final_state))
+
+
+# ---------------------------------------------------------------------------
+# Fused front: gate frontend -> scalar gain
+# ---------------------------------------------------------------------------
+
+class _IsoKDNFrontFunction(torch.autograd.Function):
+    """``_iso_kdn_gate_precumsum_paired`` -> ``iso_kdn_gain`` (reference iso_kdn_chunk.py:1317-1392,
+    1896-1962, composed as lit_gpt/iso_kdn.py:277-304) as one op.  Forward: the gate's kernel also
+    writes each 64-token chunk's gain map, and one gain kernel carries them; backward: the gain's
+    reverse chunk maps, then the gate's backward kernel runs the gain's per-chunk backward itself, so
+    the cotangents of a, omega, r never reach memory.  Returns (g_cumsum, beta[, final_precision])."""
+
+    @staticmethod
+    def forward(ctx, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu_param, initial_precision,
+                omega_min, r_min, posterior_scale, needs_backward, output_final_state):
+        B, T, H, K = g_raw.shape
+        dev = g_raw.device
+        g_cumsum = torch.empty((B, T, H, K), device=dev, dtype=torch.float32)
+        a = torch.empty((B, T, H), device=dev, dtype=torch.float32)
+        omega = torch.empty_like(a)
+        r = torch.empty_like(a)
+        beta = torch.empty_like(a)
+        mu = torch.empty((H,), device=dev, dtype=torch.float32)
+        p_prev = torch.empty_like(a) if needs_backward else None
+        fprec = torch.empty((B, H), device=dev, dtype=torch.float32) if output_final_state else None
+        prec_mode = 0 if initial_precision is None or initial_precision.ndim == 1 else 1
+        ws_bytes = _lib.size("kdn_iso_front_workspace_size", B, T, H, K)
+        ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+        with torch.cuda.device(dev):
+            _lib.call("kdn_iso_front_fwd", _lib.ptr(g_raw), _lib.is_bf16(g_raw), _lib.ptr(omega_r_raw),
+                      _lib.is_bf16(omega_r_raw), omega_r_raw.stride(0), omega_r_raw.stride(1),
+                      _lib.ptr(omega_bias), _lib.ptr(r_bias), _lib.ptr(A_log), _lib.ptr(dt_bias),
+                      _lib.ptr(mu_param), float(omega_min), float(r_min), _lib.ptr(initial_precision), prec_mode,
+                      B, T, H, K, float(posterior_scale), _lib.ptr(g_cumsum), _lib.ptr(a), _lib.ptr(omega),
+                      _lib.ptr(r), _lib.ptr(mu), _lib.ptr(beta), _lib.ptr(p_prev), _lib.ptr(fprec), _lib.ptr(ws),
+                      ws_bytes, _lib.stream_of(g_raw))
+        ctx.posterior_scale = posterior_scale
+        ctx.has_saved_state = needs_backward
+        if needs_backward:
+            ctx.save_for_backward(g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu_param,
+                                  initial_precision, a, omega, r, mu, p_prev, fprec)
+        ctx.set_materialize_grads(False)
+        return (g_cumsum, beta, fprec) if output_final_state else (g_cumsum, beta)
+
+    @staticmethod
+    def backward(ctx, d_g_cumsum, d_beta, d_final_precision=None):
+        if not ctx.has_saved_state:
+            raise RuntimeError("Isotropic KDN front backward called after a no-save forward")
+        (g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, mu_param, initial_precision, a, omega, r, mu,
+         p_prev, fprec) = ctx.saved_tensors
+        B, T, H, K = g_raw.shape
+        dev = g_raw.device
+        needs = ctx.needs_input_grad
+        prec_mode = 0 if initial_precision is None or initial_precision.ndim == 1 else 1
+        dg_pre = d_g_cumsum.float().contiguous() if d_g_cumsum is not None else None
+        dbeta = torch.zeros_like(a) if d_beta is None else d_beta.float().contiguous()
+        dfp = d_final_precision.float().contiguous() if d_final_precision is not None else None
+        dg_raw = torch.empty_like(g_raw) if needs[0] else None
+        domega_r_raw = (torch.empty(omega_r_raw.shape, device=dev, dtype=omega_r_raw.dtype)
+                        if needs[1] else None)
+        domega_bias = torch.empty((H,), device=dev, dtype=torch.float32) if needs[2] else None
+        dr_bias = torch.empty((H,), device=dev, dtype=torch.float32) if needs[3] else None
+        dA_log = torch.empty((H,), device=dev, dtype=torch.float32) if needs[4] else None
+        ddt_bias = torch.empty((H * K,), device=dev, dtype=torch.float32) if needs[5] else None
+        dmu = torch.empty((H,), device=dev, dtype=torch.float32) if needs[6] else None
+        dinit = (torch.empty_like(initial_precision) if initial_precision is not None and needs[7] else None)
+        ws_bytes = _lib.size("kdn_iso_front_workspace_size", B, T, H, K)
+        ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+        with torch.cuda.device(dev):
+            _lib.call("kdn_iso_front_bwd", _lib.ptr(g_raw), _lib.is_bf16(g_raw), _lib.ptr(omega_r_raw),
+                      _lib.is_bf16(omega_r_raw), omega_r_raw.stride(0), omega_r_raw.stride(1),
+                      _lib.ptr(omega_bias), _lib.ptr(r_bias), _lib.ptr(A_log), _lib.ptr(dt_bias),
+                      _lib.ptr(mu_param), _lib.ptr(initial_precision), prec_mode, _lib.ptr(a), _lib.ptr(omega),
+                      _lib.ptr(r), _lib.ptr(mu), _lib.ptr(p_prev), _lib.ptr(fprec if dfp is not None else None),
+                      _lib.ptr(dg_pre), _lib.ptr(dbeta), _lib.ptr(dfp), B, T, H, K, float(ctx.posterior_scale),
+                      _lib.ptr(dg_raw), _lib.ptr(domega_r_raw), _lib.ptr(dA_log), _lib.ptr(ddt_bias),
+                      _lib.ptr(domega_bias), _lib.ptr(dr_bias), _lib.ptr(dmu), _lib.ptr(dinit), _lib.ptr(ws),
+                      ws_bytes, _lib.stream_of(g_raw))
+        return (dg_raw, domega_r_raw, domega_bias, dr_bias, dA_log, ddt_bias, dmu, dinit,
+                None, None, None, None, None)
+
+
+@torch.compiler.disable
+def iso_kdn_front(g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param, omega_min,
+                  r_min, *, head_dim, info_scale=None, initial_precision=None, output_final_state=False):
+    """``_iso_kdn_gate_precumsum_paired`` -> ``iso_kdn_gain`` as the iso layer composes them (reference
+    lit_gpt/iso_kdn.py:277-304), fused: returns ``(g_cumsum, beta)`` (plus ``final_precision`` [B,H]
+    with ``output_final_state``), equal to the two ops' outputs with ``out_dtype=torch.float32``.  The
+    gain's prior precision is the gate's ``0.1 + softplus(initial_precision_param)`` unless
+    ``initial_precision`` ([H] or [B,H], state continuation) is given.  ``g_cumsum`` keeps the gate's
+    contract: its one consumer is ``_chunk_kda_precumsum_paired``.  Same argument checks and errors as
+    the two ops."""
+    B, T, H, K = _validate_iso_gate_inputs(g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias,
+                                           initial_precision_param, omega_min, r_min)
+    if initial_precision is not None:
+        if not isinstance(initial_precision, torch.Tensor):
+            raise TypeError("initial_precision must be a torch.Tensor")
+        if initial_precision.shape not in ((H,), (B, H)):
+            raise ValueError(f"initial_precision must have shape [{H}] or [{B},{H}], "
+                             f"got {tuple(initial_precision.shape)}")
+        _require_same_cuda_device(g_raw, ("initial_precision", initial_precision))
+    posterior_scale = _posterior_scale(head_dim, info_scale)
+    if B == 0 or T == 0:  # nothing to fuse: the two ops
+        g_cumsum, a, omega, r, mu = _iso_kdn_gate_precumsum_paired(
+            g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param, omega_min, r_min)
+        out = iso_kdn_gain(a, omega, r, mu if initial_precision is None else initial_precision, head_dim=head_dim,
+                           out_dtype=torch.float32, info_scale=info_scale, output_final_state=output_final_state)
+        return (g_cumsum, *out) if output_final_state else (g_cumsum, out)
+    init = initial_precision.float().contiguous() if initial_precision is not None else None
+    needs_backward = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad
+        for t in (g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param, init))
+    return _IsoKDNFrontFunction.apply(
+        g_raw.contiguous(), omega_r_raw, omega_bias.contiguous(), r_bias.contiguous(), A_log.contiguous(),
+        dt_bias.contiguous(), initial_precision_param.contiguous(), init, float(omega_min), float(r_min),
+        posterior_scale, needs_backward, bool(output_final_state))
 
 
 # ---------------------------------------------------------------------------

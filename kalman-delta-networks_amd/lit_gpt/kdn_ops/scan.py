@@ -1,27 +1,25 @@
 """The KDN mixer scan: the kdn_ops calls of one layer, composed as the reference layers do.
 
 ``iso_kdn_scan`` follows lit_gpt/iso_kdn.py:277-304 (gate frontend -> scalar gain ->
-chunked memory scan with in-op q/k normalisation); ``diag_kdn_scan`` follows
+chunked memory scan with in-op q/k normalisation), with the first two as one fused op
+(``iso_kdn_front``); ``diag_kdn_scan`` follows
 lit_gpt/diag_kdn.py:315-345 (q/k normalisation -> frontend -> vector gain -> memory scan,
 output materialised at v's dtype), with the first three as one fused op (``diag_kdn_front``).  Projections, short convolutions and the gated output
 norm of the layers are not part of the scan.
 """
 from __future__ import annotations
 
-import torch
-
 from .diag_kdn_chunk import _chunk_kalman_as, diag_kdn_front
-from .iso_kdn_chunk import _chunk_kda_precumsum_paired, _iso_kdn_gate_precumsum_paired, iso_kdn_gain
+from .iso_kdn_chunk import _chunk_kda_precumsum_paired, iso_kdn_front
 
 
 def iso_kdn_scan(q, k, v, g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param,
                  *, omega_min: float = 0.0, r_min: float = 0.01, info_scale: float | None = None):
     """q, k, v, g_raw [B,T,H,d]; omega_r_raw [B,T,2H]; dt_bias [H*K]; returns o [B,T,H,V]."""
     K = q.shape[-1]
-    g_cumsum, a, omega, r, mu = _iso_kdn_gate_precumsum_paired(
-        g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param, omega_min, r_min)
-    beta = iso_kdn_gain(a, omega, r, mu, head_dim=K, out_dtype=torch.float32,
-                        info_scale=float(K) if info_scale is None else info_scale)
+    # gate -> gain as one fused op (same results as the two reference ops)
+    g_cumsum, beta = iso_kdn_front(g_raw, omega_r_raw, omega_bias, r_bias, A_log, dt_bias, initial_precision_param,
+                                   omega_min, r_min, head_dim=K, info_scale=float(K) if info_scale is None else info_scale)
     return _chunk_kda_precumsum_paired(q=q, k=k, v=v, g_cumsum=g_cumsum, beta=beta)
 
 
