@@ -5,12 +5,13 @@
  * on; it allocates no device memory (the caller passes outputs and workspaces, sized by the
  * *_size() queries) and returns 0 on success, KDN_ERR_ARG (-1) on a rejected argument,
  * or a positive hipError_t value from the launch.  Every entry point launches only on
- * `stream` and keeps no state between calls, with one exception: kdn_mem_bwd called with its
- * stage bits 0 and 1 together may use its overlapped schedule, which also launches on a stream
- * of the library's own and keeps that stream, two events and a mutex per device for the
- * life of the process (its declaration below says when and how; calling the two stages
- * separately keeps to `stream` alone).  kdn_iso_gain_fwd_noalloc keeps a fixed device
- * array per GPU.  Tensors are dense row-major:
+ * `stream` and keeps no state between calls, with two exceptions that share one side stream:
+ * kdn_mem_fwd called with its stage bits 0, 1 and 2 together and kdn_mem_bwd called with its
+ * stage bits 0 and 1 together may use their overlapped schedules, which also launch on a stream
+ * of the library's own and keep that stream, two events and a mutex per device for the life of
+ * the process (their declarations below say when and how; calling the stages separately keeps to
+ * `stream` alone).  kdn_iso_gain_fwd_noalloc keeps a fixed device array per GPU.  Tensors are
+ * dense row-major:
  *   [B,T,H,D]  token-major with heads interleaved (the reference layout),
  *   bf16 arguments are raw uint16_t bit patterns.
  * Dtype flags (*_bf16) select bf16 (1) or fp32 (0) for arguments typed void*.
@@ -223,7 +224,14 @@ size_t kdn_mem_bwd_workspace_size(int B, int T, int H, int K, int V);
  * initial_memory / output_final_state, iso_kdn_naive.py:376-440).  `saved` receives the
  * intermediates the backward consumes (kdn_mem_saved_size bytes).  `stages` selects kernels
  * (bit 0 intra-chunk WY build, bit 1 serial state pass, bit 2 readout o; -1 = all) so that a
- * caller can launch and time them one at a time; the stages must run in this order.  Bits 1 and 2
+ * caller can launch and time them one at a time; the stages must run in this order.  Bits 0, 1 and
+ * 2 in one call with one chunk group (kdn_mem_state_groups == 1) take the overlapped schedule when B*H*V/64
+ * leaves at least 32 CUs idle: the sequence runs in two chunk ranges, the second range's intra-chunk
+ * build on the library's side stream beside the first range's state pass (made on the first such call
+ * outside HIP graph capture; a captured call before that runs the stages in order on `stream`); the
+ * side stream waits for `stream`'s earlier work and `stream` for the side build before the second
+ * range's pass (an event each; under capture a fork and a join of the graph); the state crosses the
+ * ranges in fp32 through `saved`, so every output is bit-identical to the stages in order.  Bits 1 and 2
  * in one call run the state pass with the readout fused.  Bit 3 (with stages >= 0) declares that
  * no backward follows (inference, as under torch.no_grad): the intermediates only the backward
  * reads are then not written, and `saved` is scratch for this call alone.  A caller that keeps no

@@ -260,14 +260,14 @@ __device__ __forceinline__ float row_rstd(const u32x4 (&raw)[KB]) {
   return l2n_rstd(l2n_tree<KB>(t));
 }
 
-// grid (NT, B*H), block 256.
+// grid (chunks, B*H), block 256: chunks n0 .. n0 + gridDim.x - 1 of every head.
 template <int K, int V, bool ISO, bool NORM = false>
 __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
     float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd = nullptr,
-    float* __restrict__ k_rstd = nullptr) {
+    float* __restrict__ k_rstd = nullptr, int n0 = 0) {
   constexpr int KB = K / 32;
   // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
   float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand rows [s][col], pitch XR
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int n = n0 + blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;  // chunks n0 + gridDim.x
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
 
@@ -430,14 +430,15 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   intra_solve_emit<K, V, NORM>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid, sRk);
 }
 
-// grid (NT, B*H), block 256; a workgroup whose chunk intra_fwd_kernel did not flag exits at once.
+// grid (chunks, B*H), block 256 (chunks n0 ..); a workgroup whose chunk intra_fwd_kernel did not flag exits at
+// once.
 template <int K, int V, bool ISO, bool NORM = false>
 __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
     float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd = nullptr,
-    float* __restrict__ k_rstd = nullptr) {
+    float* __restrict__ k_rstd = nullptr, int n0 = 0) {
   constexpr int KB = K / 32;
   // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
   constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   __shared__ float sSpan[4];
   __shared__ __attribute__((aligned(16))) float sMid[4 * K];  // block anchors m_J per channel
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int n = n0 + blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;  // chunks n0 + gridDim.x
   const int64_t lin = (int64_t)bh * NT + n;
   if (flags[lin] == 0) return;  // handled by intra_fwd_kernel
   const int t0 = n * C, L = min(C, T - t0);

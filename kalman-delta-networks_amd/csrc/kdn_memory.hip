@@ -376,19 +376,24 @@ __device__ __forceinline__ bool any_flagged(const int* __restrict__ flags, int N
   return __syncthreads_or(any) != 0;
 }
 
+// Chunks n0 .. n1 - 1 of every head (the forward's schedule may build a sequence in two ranges).
 template <int K, int V, bool ISO>
 __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
-    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, int NB, float scale,
-    float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
+    const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, int BH, int n0, int n1,
+    float scale, float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
     float* __restrict__ Mg, float* __restrict__ Ag, const int* __restrict__ flags, float* __restrict__ q_rstd,
     float* __restrict__ k_rstd) {
-  if (!any_flagged(flags, NB)) return;
-  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
-    if (flags[lin] == 0) continue;
+  const int len = n1 - n0, N = BH * len;
+  int any = 0;
+  for (int i = blockIdx.x + threadIdx.x * gridDim.x; i < N; i += blockDim.x * gridDim.x)
+    any |= flags[(int64_t)(i / len) * NT + n0 + i % len];
+  if (__syncthreads_or(any) == 0) return;
+  for (int i = blockIdx.x; i < N; i += gridDim.x) {
+    const int bh = i / len, n = n0 + i % len;
+    if (flags[(int64_t)bh * NT + n] == 0) continue;
     __syncthreads();  // LDS of the previous chunk is dead
-    intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, lin % NT, lin / NT,
-                                     q_rstd, k_rstd);
+    intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, n, bh, q_rstd, k_rstd);
   }
 }
 
@@ -798,7 +803,7 @@ inline void with_copy_mask(int hm, F f) {
 
 // saved-buffer layout (floats), TT = B*H*T, NB = B*H*NT
 struct MemLayout {
-  int64_t U, W, Kf, Qg, M, A, h, D, flags, grp, total;
+  int64_t U, W, Kf, Qg, M, A, h, D, flags, grp, mid, total;
   GroupCount gc;
   MemLayout(int B, int T, int H, int K, int V) {
     const int64_t TT = (int64_t)B * H * T, NB = (int64_t)B * H * cdiv(T, C);
@@ -813,7 +818,8 @@ struct MemLayout {
     D = h + NB * K * V;
     flags = D + TT * V;  // NB ints: chunk taken by the exact intra-chunk path
     grp = round64(flags + NB);  // the forward state pass's group buffers (dead after the forward)
-    total = grp + group_floats((int64_t)B * H, gc, K, V);
+    mid = grp + group_floats((int64_t)B * H, gc, K, V);  // the overlapped forward's carried state
+    total = mid + (int64_t)B * H * K * V;
   }
 };
 struct BwdLayout {
@@ -862,6 +868,20 @@ inline BwdOverlap plan_bwd_overlap(int BH, int NT, int NV, GroupCount gc, int cu
   o.side_tasks = min(m1 * BH, iters * idle);
   return o;
 }
+// Overlapped schedule of the forward (one call with the intra-chunk build and the state pass): the build
+// of the first m1 chunks, then their state pass beside the build of the rest on a second stream, then
+// the rest's pass (see mem_fwd_impl).  The pass holds B*H*V/64 CUs; the side build's workgroups (three
+// per CU, each lasting about kBuildSteps chunk steps of the pass: the diagonal build is ~15% longer) take
+// the `idle` ones, so m1 balances the first range's pass against the second range's build there.
+// Measured at B4 T4096 H18 (m1 swept 30 .. 45): best at 39 (isotropic) and 42 (diagonal).
+constexpr float kBuildStepsIso = 7.3f, kBuildStepsDiag = 9.0f;
+inline int plan_fwd_overlap(int BH, int NT, int NV, int cus, bool iso) {
+  const int idle = cus - BH * NV;
+  if (idle < 32 || NT < 8) return 0;
+  const float r = BH * (iso ? kBuildStepsIso : kBuildStepsDiag) / (3.f * idle);
+  return max(1, min(NT - 1, (int)lrintf(NT * r / (1.f + r))));
+}
+
 // One wave that returns after `ticks` of the constant 100 MHz clock (bounded wait, no memory access).
 __global__ void side_delay_kernel(unsigned ticks) {
   const uint64_t t0 = wall_clock64();
@@ -955,39 +975,78 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   // are not written
   const bool infer = stages >= 0 && (stages & 8) != 0;
   float* Asave = infer ? nullptr : A;
-  dim3 gchunk(NT, B * H);
-  if (stages & 1) {
-    const int NB = B * H * NT, gx = min(NB, 512);
+  // the intra-chunk build of chunks n0 .. n1 - 1 on stream s: the single-anchor kernel, the block-anchor
+  // kernel for the chunks it flagged, the exact kernel for those the block kernel left flagged
+  auto launch_intra = [&](int n0, int n1, hipStream_t s) {
+    const dim3 gchunk(n1 - n0, B * H);
+    const int gx = min(B * H * (n1 - n0), 512);
     // the in-op L2 norm (q_rstd given) is a template variant: its row loads would otherwise cost the
     // plain kernels registers
-#define KDN_INTRA(ISO_, NORM_)                                                                                       \
-  do {                                                                                                               \
-    hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, stream, q, k, kap, v, \
-                       gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                          \
-    hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, stream, q, k,   \
-                       kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                  \
-    hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, ISO_>), dim3(gx), dim3(256), 0, stream, q, k, kap, v, gc, T, \
-                       H, NT, NB, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                             \
+#define KDN_INTRA(ISO_, NORM_)                                                                                         \
+  do {                                                                                                                 \
+    hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, s, q, k, kap, v, gc, T, \
+                       H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd, n0);                               \
+    hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, s, q, k, kap, v,  \
+                       gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd, n0);                        \
+    hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, ISO_>), dim3(gx), dim3(256), 0, s, q, k, kap, v, gc, T, H, NT, \
+                       B * H, n0, n1, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                          \
   } while (0)
     if (iso && q_rstd) KDN_INTRA(true, true);
     else if (iso) KDN_INTRA(true, false);
     else if (q_rstd) KDN_INTRA(false, true);
     else KDN_INTRA(false, false);
 #undef KDN_INTRA
-    KDN_CHECK_LAUNCH();
-  }
-  auto launch_ro = [&](dim3 grid, const kdn_state::GroupPlan& P, float* hstore, float* dstore, int mask) {
+  };
+  auto launch_ro = [&](dim3 grid, const kdn_state::GroupPlan& P, float* hstore, float* dstore, int mask,
+                       const float* hin, float* hout) {
     const dim3 bs(2 * kdn_state::state_threads(V));
     with_copy_mask(mask, [&](auto hmc) {
       constexpr int HM = decltype(hmc)::value;
       if (o_bf16)
         hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, bf16_t, true, HM>), grid, bs, 0, stream, U, W, Kf, gc,
-                           h0, T, H, NT, B * H, hstore, dstore, ht, P, Qg, M, (bf16_t*)o);
+                           hin, T, H, NT, B * H, hstore, dstore, hout, P, Qg, M, (bf16_t*)o);
       else
-        hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, true, HM>), grid, bs, 0, stream, U, W, Kf, gc, h0,
-                           T, H, NT, B * H, hstore, dstore, ht, P, Qg, M, (float*)o);
+        hipLaunchKernelGGL((kdn_state::state_fwd_kernel<K, V, float, true, HM>), grid, bs, 0, stream, U, W, Kf, gc,
+                           hin, T, H, NT, B * H, hstore, dstore, hout, P, Qg, M, (float*)o);
     });
   };
+  // Overlapped schedule (bits 0, 1 and 2 in one call, one chunk group): the state pass (with the readout
+  // fused) occupies B*H*V/64 CUs, one workgroup each, and leaves the rest idle.  The sequence runs in two
+  // chunk ranges: the build of the first m1 chunks, then that range's state pass on `stream` while the
+  // second range's build runs on the side stream, then the second range's pass from the carried state
+  // (saved + mid, fp32: the same state the single pass holds, so every output is bit-identical).
+  if ((stages & 7) == 7 && lay.gc.NG == 1) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return KDN_ERR_ARG;
+    if (cap == hipStreamCaptureStatusNone || side_ready()) {
+      std::lock_guard<std::mutex> lock(g_side_mu);
+      SideQueue* sq = nullptr;
+      int rc = side_queue(&sq);
+      if (rc) return rc;
+      const int m1 = plan_fwd_overlap(B * H, NT, V / kdn_state::state_cols(V), sq->cus, iso != 0);
+      if (m1 > 0) {
+        const dim3 grid(B * H * (V / kdn_state::state_cols(V)));
+        float* mid = saved + lay.mid;
+        launch_intra(0, m1, stream);
+        KDN_CHECK_LAUNCH();
+        if ((rc = stream_wait(sq->s, stream, sq->ev[0]))) return rc;
+        launch_intra(m1, NT, sq->s);
+        KDN_CHECK_LAUNCH();
+        launch_ro(grid, kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr, 0, m1}, infer ? nullptr : hb,
+                  infer ? nullptr : D, hm, h0, mid);
+        KDN_CHECK_LAUNCH();
+        if ((rc = stream_wait(stream, sq->s, sq->ev[1]))) return rc;
+        launch_ro(grid, kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr, m1, NT}, infer ? nullptr : hb,
+                  infer ? nullptr : D, hm, mid, ht);
+        KDN_CHECK_LAUNCH();
+        return 0;
+      }
+    }
+  }
+  if (stages & 1) {
+    launch_intra(0, NT, stream);
+    KDN_CHECK_LAUNCH();
+  }
   auto launch_readout = [&](int NR) {  // chunk-parallel readout O = Qg h + M delta of the first NR chunks
     const int NCH = NR * B * H;        // chunk-heads; with two V halves the grid is padded to pairs of 8
     const dim3 gr(V / 64 == 2 ? 16 * cdiv(NCH, 8) : NCH);
@@ -1005,7 +1064,7 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
     const GroupCount gcnt = lay.gc;
     if (gcnt.NG == 1) {
       launch_ro(dim3(B * H * (V / kdn_state::state_cols(V))), kdn_state::GroupPlan{1, NT, 0, nullptr, nullptr},
-                infer ? nullptr : hb, infer ? nullptr : D, hm);
+                infer ? nullptr : hb, infer ? nullptr : D, hm, h0, ht);
       KDN_CHECK_LAUNCH();
       return 0;
     }
@@ -1023,7 +1082,7 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
       KDN_CHECK_LAUNCH();
     }
     P.pass = 1;
-    launch_ro(dim3(B * H * (gcnt.NG - 1) * NV), P, infer ? nullptr : hb, infer ? nullptr : D, 0);
+    launch_ro(dim3(B * H * (gcnt.NG - 1) * NV), P, infer ? nullptr : hb, infer ? nullptr : D, 0, h0, ht);
     KDN_CHECK_LAUNCH();
     launch_readout(gcnt.m);
     KDN_CHECK_LAUNCH();

@@ -14,6 +14,9 @@ from . import _lib
 # bits 1 | 2 in one call: the state pass with the readout fused (with chunk groups, fused into the
 # groups that start from their true state; the first group's readout follows in the same call)
 FWD_STAGES = ((1, "mem_intra_fwd"), (6, "mem_state_readout_fwd"))
+# bits 0 | 1 | 2 in one call: with one chunk group the sequence runs in two chunk ranges, the second
+# range's intra-chunk build on a second stream beside the first range's state pass (same results)
+FWD_STAGES_OVERLAP = ((7, "mem_fwd_overlap"),)
 NO_BACKWARD = 8  # stage bit: no backward follows, intermediates only the backward reads are not written
 
 
@@ -61,13 +64,17 @@ def backward_mode() -> str:
 
 
 def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initial_state=None,
-            output_final_state=False, out_dtype=torch.float32, need_backward=True, q_rstd=None, k_rstd=None):
+            output_final_state=False, out_dtype=torch.float32, need_backward=True, q_rstd=None, k_rstd=None,
+            overlap=None):
     """q, k, v bf16 [B,T,H,*]; kappa [B,T,H,K] f32 (diag) or beta [B,T,H] f32 (iso).
     Returns (o, saved, final_state or None); with ``need_backward=False`` saved is not usable by
     mem_bwd (the intermediates only the backward reads are skipped).
 
     With ``q_rstd`` / ``k_rstd`` (f32 [B,T,H] outputs, the in-op L2 norm) q and k are the raw inputs:
-    the scan normalises their rows as kdn_l2norm_fwd would and writes the rows' rstd for mem_bwd."""
+    the scan normalises their rows as kdn_l2norm_fwd would and writes the rows' rstd for mem_bwd.
+
+    ``overlap`` (default: unless a KernelTimer is timing each kernel) launches the intra-chunk build and
+    the state pass in one call, which overlaps them where the shape allows."""
     B, T, H, K = q.shape
     V = v.shape[-1]
     dev = q.device
@@ -77,7 +84,9 @@ def mem_fwd(q, k, kappa_or_beta, iso: bool, v, g_cumsum, scale: float, *, initia
     h0 = initial_state.float().contiguous() if initial_state is not None else None
     stream = _lib.stream_of(q)
     extra = 0 if need_backward else NO_BACKWARD
-    for bit, tag in FWD_STAGES:
+    if overlap is None:
+        overlap = DEFAULT_OVERLAP and not _lib.timing()
+    for bit, tag in (FWD_STAGES_OVERLAP if overlap else FWD_STAGES):
         _lib.call("kdn_mem_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(kappa_or_beta), int(iso), _lib.ptr(v),
                   _lib.ptr(g_cumsum), B, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(saved), saved.numel(),
                   _lib.ptr(ht), _lib.ptr(o), _lib.is_bf16(o), _lib.ptr(q_rstd), _lib.ptr(k_rstd), bit | extra,

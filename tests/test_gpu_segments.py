@@ -12,6 +12,12 @@ and the benchmark's 64 chunks (13; 896 side tasks), as the library's plan_bwd_ov
 144 state workgroups and 112 idle CUs, with a ragged last chunk,
 a chunk taken by the exact path, a final-state cotangent and the initial-state gradient; iso (beta,
 bf16 dO) and diag (kappa, fp32 dO).
+
+The forward has the same kind of schedule (kdn_mem_fwd with stage bits 0, 1 and 2 in one call): the
+intra-chunk build of the first chunk range, then that range's state pass beside the second range's
+build on the second stream, then the second range's pass from the state carried in fp32.  Its output,
+final state and every intermediate the backward reads must equal the separate calls' bit for bit, with
+and without an initial state, for training and for a no-backward forward, and under graph capture.
 """
 import pytest
 import torch
@@ -104,6 +110,78 @@ def test_overlapped_backward_under_graph_capture():
         torch.cuda.synchronize()
         assert torch.isfinite(noise)
         for name, a, b, c in zip(names, eager, out, again):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager call"
+            assert torch.equal(a, c), f"{name}: eager call {rep} differs"
+    log("  replays bit-identical")
+
+
+@pytest.mark.parametrize("B,T,H,variant,extreme", [
+    (2, 2048 + 37, 36, "iso", True),   # 33 chunks, a ragged last chunk, a chunk for the exact path
+    (4, 4096, 18, "iso", False),       # the benchmark shape
+    (4, 4096, 18, "diag", True),
+])
+def test_overlapped_forward_is_bit_identical(B, T, H, variant, extreme):
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import _memscan
+    K = V = 128
+    diag = variant == "diag"
+    assert _memscan.state_groups(B, T, H, K, V) == 1, "shape must run one chunk group"
+    log(f"case overlapped-fwd {variant} B={B} T={T} H={H} extreme={extreme}")
+    q, k, v, G, kap, do, dht = _inputs(dev, 5 + T + H, B, T, H, K, V, diag, extreme)
+    h0 = 0.5 * dht
+    scale = K ** -0.5
+    out_dtype = torch.float32 if diag else torch.bfloat16
+    names = ("dq", "dk", "dv", "dkappa" if diag else "dbeta", "dg", "d initial state")
+    for init in (None, h0):
+        for need_backward in (True, False):
+            runs = [_memscan.mem_fwd(q, k, kap, not diag, v, G, scale, initial_state=init, output_final_state=True,
+                                     out_dtype=out_dtype, need_backward=need_backward, overlap=ov)
+                    for ov in (False, True, True)]  # twice overlapped: the side stream's events are reused
+            # what the backward reads of each forward's saved intermediates: its gradients (serial schedule)
+            grads = [_memscan.mem_bwd(q, k, kap, not diag, v, G, s, scale, do, d_final_state=dht,
+                                      need_initial_state_grad=True, overlap=False) for _, s, _ in runs] \
+                if need_backward else None
+            torch.cuda.synchronize()
+            o0, _, f0 = runs[0]
+            assert torch.isfinite(o0.float()).all() and torch.isfinite(f0).all()
+            for i, (o, _, f) in enumerate(runs[1:], 1):
+                assert torch.equal(o, o0), "output differs from the serial schedule"
+                assert torch.equal(f, f0), "final state differs from the serial schedule"
+                if grads is not None:
+                    for name, a, b in zip(names, grads[0], grads[i]):
+                        assert torch.equal(a, b), f"{name} from the overlapped forward's saved state differs"
+    log("  bit-identical")
+
+
+def test_overlapped_forward_under_graph_capture():
+    """The overlapped forward captured into a HIP graph: every replay, with eager work and
+    synchronisations between them, equals the eager call bit for bit."""
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import _memscan
+    B, T, H, K = 4, 4096, 18, 128
+    assert _memscan.state_groups(B, T, H, K, K) == 1
+    log(f"case overlapped-fwd graph capture iso B={B} T={T} H={H}")
+    q, k, v, G, kap, _do, dht = _inputs(dev, 9, B, T, H, K, K, False, False)
+    scale = K ** -0.5
+    call = lambda: _memscan.mem_fwd(q, k, kap, True, v, G, scale, initial_state=dht,  # noqa: E731
+                                    output_final_state=True, out_dtype=torch.bfloat16, overlap=True)
+    eager = call()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call()
+    for rep in range(3):
+        noise = torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+        again = call()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        for name, a, b, c in zip(("o", "final state"), eager[::2], out[::2], again[::2]):
             assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager call"
             assert torch.equal(a, c), f"{name}: eager call {rep} differs"
     log("  replays bit-identical")
