@@ -8,8 +8,9 @@
 // N and M are K-contractions of factored operands (bf16x3 MFMA); the decay 2^{G_c - G_s} is split
 // at an anchor so neither factor overflows.  A^T is saved for the backward.
 //
-// intra_fwd_kernel (every chunk): one anchor per chunk, the first row,
-//   Lk = k 2^{G - G_0},  Lq = scale q 2^{G - G_0},  R = kappa 2^{G_0 - G}  (R <= 2^span);
+// intra_fwd_kernel (every chunk): one anchor per chunk and channel, the midpoint of the chunk's gate
+//   range m = (G_0 + G_{L-1}) / 2, so |G - m| <= span / 2 on every row:
+//   Lk = k 2^{G - m},  Lq = scale q 2^{G - m},  R = kappa 2^{m - G}  (each <= 2^{span/2} times k, q, kappa);
 //   a chunk whose span max_i (G_0 - G_{L-1})_i exceeds kAnchorSpanMax is flagged (flags = 1).
 // intra_fwd_block_kernel (the flagged chunks): one anchor per 16-token block J,
 //   m_J = (G_{16J} + G_{16J+15})/2 per channel (rows clamped), so |G - m_J| <= span_J / 2 inside
@@ -18,8 +19,9 @@
 //   Lq likewise.  A chunk handled here gets flags = 0; one with a block span past kBlockSpanMax
 //   (the masked upper-triangle products of a diagonal block reach 2^span) stays flagged for the
 //   exact per-block kernel, which runs last.
-// Random-init and trained models decay fast enough (up to ~e^-4 per token and channel) that most
-// of their chunks take the block kernel; slow-decay inputs stay on the single-anchor kernel.
+// A random-init 1.3B model decays by up to ~e^-2 per token in its fastest channels on average (chunk
+// spans up to ~170), which the midpoint anchor covers; faster decay (trained models reach ~e^-4 per
+// token, spans ~370) takes the block kernel.
 //
 // Layout of work: wave w owns row block I = w (16 rows) for the N / M build, keeping its k / q
 // factors in registers and publishing its R fragments (and block anchors) to LDS; the U / W
@@ -41,7 +43,9 @@ using kdn_state::split2;
 using kdn_state::TILE;
 using kdn_state::zero4;
 
-constexpr float kAnchorSpanMax = 100.f;  // base 2, one anchor per chunk: R <= 2^100 stays far inside fp32
+// base 2, one midpoint anchor per chunk and channel: every factor stays <= 2^100, far inside fp32 (the
+// masked products above the diagonal may overflow; they are discarded by a select, never multiplied)
+constexpr float kAnchorSpanMax = 200.f;
 constexpr float kBlockSpanMax = 120.f;   // base 2, per 16-token block: every product stays below 2^120
 constexpr int AP = C + 1;                // LDS row stride of the fp32 N and A tiles
 constexpr int XR = 128 + 4;              // LDS row stride of the staged [s][column] operands (<= 128 columns)
@@ -325,9 +329,10 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   }
   if (tid == 0) flags[(int64_t)bh * NT + n] = 0;
 
-  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels
+  // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels.
+  // Rows past L read zero k, q, kappa and repeat the gate of row L-1, so every factor is bounded.
   const int c = 16 * w + r16;
-  const uint32_t crow = (uint32_t)(c * H);
+  const uint32_t crow = (uint32_t)(c * H), grow = (uint32_t)(min(c, L - 1) * H);
   uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
   const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
   // with the in-op L2 norm (NORM) q, k are raw: this workgroup normalises its rows
@@ -358,7 +363,7 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     }
     const float* g0 = NORM ? g0x : g0s[kb];
     const float* gl = NORM ? glx : gls[kb];
-    ld8(rG, (crow * K + i0) * 4, gcv);
+    ld8(rG, (grow * K + i0) * 4, gcv);
     if constexpr (NORM) {
       unpack8(kraw[kb], kv);
       unpack8(qraw[kb], qv);
@@ -382,10 +387,11 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     float lk[8], lq[8], rr[8], kf[8], qg[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float e = fexp2(gcv[j] - g0[j]);
+      const float mid = 0.5f * (g0[j] + gl[j]);
+      const float e = fexp2(gcv[j] - mid);
       lk[j] = kv[j] * e;
       lq[j] = scale * qv[j] * e;
-      rr[j] = av[j] * fexp2(g0[j] - gcv[j]);
+      rr[j] = av[j] * fexp2(mid - gcv[j]);
       kf[j] = av[j] * fexp2(gl[j] - gcv[j]);
       qg[j] = scale * qv[j] * fexp2(gcv[j]);
     }

@@ -569,12 +569,15 @@ def swiglu(x, w1, w2, w3, amp: bool = False):
     return linear(amp_round(amp_round(F.silu(a), amp) * b, amp), w3, amp=amp)
 
 
-def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp=False, chunked=False):
+def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp=False, chunked=False,
+              scan_bf16=False):
     """IsotropicKalmanDeltaNetwork.forward (iso_kdn.py:262-314) on a state dict ``p`` of the
     layer (reference parameter names): packed q|k|v projection + per-group SiLU short
     convolution; [f0 | omega | r] packed projection, f_proj[1] on the f0 slice; iso_mixer;
     sigmoid-gated RMS norm against g_proj(x); o_proj.  ``chunked`` runs the mixer's memory in the
-    WY chunk form (equal to the tokenwise form to rounding; faster at long T)."""
+    WY chunk form (equal to the tokenwise form to rounding; faster at long T).  ``scan_bf16`` rounds
+    the normalised q, k and v to bf16 at the memory scan's boundary, for a model whose scan takes bf16
+    operands from fp32 inputs (the HIP scan does; under autocast, ``amp``, they are bf16 already)."""
     H = p["A_log"].shape[0]
     Dm = p["qkv_pack.projection_weight"].shape[0] // 3
     K = Dm // H
@@ -586,10 +589,11 @@ def iso_layer(p, x, *, eps=1e-5, omega_min=0.0, r_min=0.01, info_scale=None, amp
     packed = linear(x, p["f_omega_r_proj.weight"], amp=amp)
     f_hidden, omega_r_raw = packed[..., :K], packed[..., K:]
     g_raw = linear(f_hidden, p["f_proj.1.weight"], amp=amp)
+    v = amp_round(v, scan_bf16)
     o = iso_mixer(q.view(B, T, H, K), k.view(B, T, H, K), v.view(B, T, H, K), g_raw.view(B, T, H, K),
                   omega_r_raw, p["omega_proj.bias"], p["r_proj.bias"], p["A_log"], p["dt_bias"],
                   p["initial_precision_param"], omega_min=omega_min, r_min=r_min, info_scale=info_scale,
-                  round_qk=amp, chunked=chunked)
+                  round_qk=amp or scan_bf16, chunked=chunked)
     o = amp_round(o, amp)
     gate = linear(linear(x, p["g_proj.0.weight"], amp=amp), p["g_proj.1.weight"], p["g_proj.1.bias"], amp=amp)
     y = amp_round(rms_norm_gated(o, gate.view(B, T, H, K), p["o_norm.weight"], eps, "sigmoid"), amp)

@@ -180,20 +180,44 @@ def test_memory_scan_mixed_anchor_and_exact_chunks(variant):
     _check("dkappa", dkap, g_ref[4], _tol_grad(iso, q, v))
 
 
+SPAN_ANCHOR = 200.0  # base 2: one midpoint anchor per chunk and channel up to this chunk span
+SPAN_BLOCK = 120.0   # base 2: per-16-token block anchors up to this block span
+
+
+def _decay_spans(ell):
+    """Base-2 decay spans max_i (G_first - G_last)_i of every full 64-token chunk and of every
+    16-token block in it ([B,T,H,K] natural-log gate)."""
+    B, T, H, K = ell.shape
+    nf = T // CHUNK
+    G = chunk_prefix_base2(ell[:, :nf * CHUNK], CHUNK).reshape(B, nf, CHUNK, H, K)
+    chunk = (G[:, :, 0] - G[:, :, -1]).amax(-1)
+    Gb = G.reshape(B, nf, 4, 16, H, K)
+    block = (Gb[:, :, :, 0] - Gb[:, :, :, -1]).amax(-1)
+    return chunk, block
+
+
 @pytest.mark.parametrize("variant", ["iso", "diag"])
-@pytest.mark.parametrize("ell_mean,ell_std,shape", [(-1.5, 0.8, (1, 200, 2, 128, 128)),
-                                                    (-4.0, 0.3, (1, 200, 2, 128, 128)),
-                                                    (-2.0, 0.5, (2, 130, 2, 64, 64))])
-def test_memory_scan_large_decay_block_anchors(variant, ell_mean, ell_std, shape):
-    """Per-token decays of e^-1.5 to e^-4 (a 64-token chunk spans ~140 to ~370 in base 2), the range
-    a randomly initialised 1.3B model produces: far outside one anchor per chunk, inside the
-    per-16-token block anchors (block spans <= ~100), so the MFMA block-anchor kernels must match
-    the oracle, at d = 128 and d = 64 with a partial last chunk."""
+@pytest.mark.parametrize("ell_mean,ell_std,shape,cover", [(-1.5, 0.8, (1, 200, 2, 128, 128), "midpoint"),
+                                                          (-4.0, 0.3, (1, 200, 2, 128, 128), "block"),
+                                                          (-2.05, 0.5, (2, 130, 2, 64, 64), "both"),
+                                                          (-3.5, 0.3, (2, 130, 2, 64, 64), "block")])
+def test_memory_scan_large_decay_block_anchors(variant, ell_mean, ell_std, shape, cover):
+    """Per-token decays of e^-1.5 to e^-4 (a 64-token chunk spans ~140 to ~370 in base 2; a randomly
+    initialised 1.3B model spans up to ~170, trained models more), at d = 128 and d = 64 with a partial
+    last chunk, against the oracle.  Each case states which MFMA path its full chunks take, checked on
+    its inputs: "midpoint" (spans past 100, where a first-row anchor would overflow, and within the
+    midpoint anchor's 200), "block" (spans past 200, block spans within 120: the per-16-token
+    block-anchor kernel), "both" (chunks of each kind in one launch)."""
     dev = gpu_or_skip()
     B, T, H, K, V = shape
-    log(f"case memory large decay {variant} ell~N({ell_mean},{ell_std}) B={B} T={T} H={H} K={K} V={V}")
+    log(f"case memory large decay {variant} ell~N({ell_mean},{ell_std}) B={B} T={T} H={H} K={K} V={V} {cover}")
     iso = variant == "iso"
     q, k, v, ell, kap, do = memory_inputs(41, B, T, H, K, V, diag=not iso, ell_mean=ell_mean, ell_std=ell_std)
+    spans, blocks = _decay_spans(ell)
+    mid = (spans > 100.0) & (spans <= SPAN_ANCHOR)
+    blk = spans > SPAN_ANCHOR
+    assert (spans > 100.0).all() and bool(blocks.amax() <= SPAN_BLOCK), (spans, blocks.amax())
+    assert {"midpoint": mid.all(), "block": blk.all(), "both": mid.any() and blk.any()}[cover], spans
     scale = K ** -0.5
     o_ref, _, g_ref = _oracle(q, k, v, ell, kap, do, iso=iso, scale=scale)
     o, _, dq, dkk, dv, dell, dkap, _ = _gpu(q, k, v, ell, kap, do, iso=iso, scale=scale, dev=dev)
