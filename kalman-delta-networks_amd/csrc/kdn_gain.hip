@@ -942,9 +942,10 @@ __device__ __forceinline__ void map_renorm(Map2& c) {
 
 // Forward map: per channel the tile's composite Mobius map, and the tile's sum of clamped log-decays.
 template <typename TX>
-__global__ __launch_bounds__(256) void diag_front_map_kernel(FrontArgs<TX> a, float* __restrict__ maps,
+// 8 workgroups (waves per SIMD) per CU: the pass hides its loads' latency with waves, 2 tokens in flight each
+__global__ __launch_bounds__(256, 8) void diag_front_map_kernel(FrontArgs<TX> a, float* __restrict__ maps,
                                                              float* __restrict__ tsum) {
-  constexpr int NB = 4;
+  constexpr int NB = 2;
   const GainTile g = gain_tile(a.B, a.T, a.H, a.K, a.NV);
   if (!g.ok) return;
   const float rate = __expf(a.A_log[g.h]);
@@ -953,21 +954,32 @@ __global__ __launch_bounds__(256) void diag_front_map_kernel(FrontArgs<TX> a, fl
   Map2 M[kCPT];
 #pragma unroll
   for (int j = 0; j < kCPT; ++j) M[j] = Map2{1.f, 0.f, 0.f, 1.f}, es[j] = 0.f;
+  // one token's step: its log-decay into the tile sum, its map onto the composite
+  auto step = [&](const FrontRaw<TX>& raw) {
+    FrontTok tk;
+    FrontSig unused;
+    front_tok<false>(raw, rate, bias, tk, unused);
+#pragma unroll
+    for (int j = 0; j < kCPT; ++j) {
+      es[j] += ell_mem(tk.ell[j], tk.al[j]);
+      const float a2 = tk.al[j] * tk.al[j], uu = a.s * tk.kt[j] * tk.kt[j] * tk.ir;
+      M[j] = map_mul_raw(Map2{a2, tk.wt[j], uu * a2, 1.f + uu * tk.wt[j]}, M[j]);
+    }
+  };
   for (int t = g.t0; t < g.t1; t += NB) {
     FrontRaw<TX> raw[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) front_load(a, front_row(g, a.T, a.H, min(t + u, g.t1 - 1)), g.i0, raw[u]);
+    if (t + NB <= g.t1) {
+      // every token of the group is in the tile: no per-token condition, so the compiler keeps the
+      // NB tokens' loads in flight together instead of sinking each into its token's branch
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      if (t + u >= g.t1) break;
-      FrontTok tk;
-      FrontSig unused;
-      front_tok<false>(raw[u], rate, bias, tk, unused);
+      for (int u = 0; u < NB; ++u) step(raw[u]);
+    } else {
 #pragma unroll
-      for (int j = 0; j < kCPT; ++j) {
-        es[j] += ell_mem(tk.ell[j], tk.al[j]);
-        const float a2 = tk.al[j] * tk.al[j], uu = a.s * tk.kt[j] * tk.kt[j] * tk.ir;
-        M[j] = map_mul_raw(Map2{a2, tk.wt[j], uu * a2, 1.f + uu * tk.wt[j]}, M[j]);
+      for (int u = 0; u < NB; ++u) {
+        if (t + u >= g.t1) break;
+        step(raw[u]);
       }
     }
 #pragma unroll
