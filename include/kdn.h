@@ -15,6 +15,9 @@
  *   [B,T,H,D]  token-major with heads interleaved (the reference layout),
  *   bf16 arguments are raw uint16_t bit patterns.
  * Dtype flags (*_bf16) select bf16 (1) or fp32 (0) for arguments typed void*.
+ * A pointer argument that a declaration does not call optional or nullable must address a device
+ * buffer of the documented shape: the library checks sizes, flags and workspace lengths, not the
+ * validity of such pointers.
  * g_cumsum is the base-2, chunk-local inclusive prefix of the per-channel log-gate; its
  * chunk length is kdn_mem_chunk_size() (64) for both variants, and it has exactly one
  * consumer (the memory scan), whose backward returns the gate cotangent in natural-log
