@@ -252,6 +252,30 @@ __device__ __forceinline__ void chunk_bwd_task(
   auto qk_lds = [&](int x, int c, int ch) -> const unsigned char* {
     return sQK + x * QK_T + (c >> 2) * QK_S + (c & 3) * (K * 2) + ch * 2;
   };
+  // Isotropic variant, K = 128: the chunk's gate rows G (fp32) for the gradient phase go to LDS the same way,
+  // issued with the k, q rows' slot: one instruction moves 64 lanes x 16 B = 2 rows of 512 B, and row c sits at
+  // (c / 2) * G_S + (c % 2) * 512 bytes.  The 32-byte gap after each pair puts the rows 4 apart, which one
+  // gradient-phase read gathers, on different banks.  Rows past L read 0; the reads clamp to row L - 1.
+  constexpr bool G_LDS = K == 128 && ISO;
+  constexpr int G_S = 2 * K * 4 + 32, G_T = (C / 2) * G_S;
+  __shared__ __attribute__((aligned(16))) unsigned char sGr[G_LDS ? G_T : 16];
+  auto issue_g = [&]() {
+    if constexpr (G_LDS) {
+      if (!flagged) {
+        const bufrsrc rg = make_buf(gc + in_row0 * K, rows_in * K * 4);
+        const int wu = __builtin_amdgcn_readfirstlane(w);
+#pragma unroll
+        for (int gi = 0; gi < C / 2 / NW; ++gi) {  // wave w: row pairs NW gi + w
+          const int pr = NW * gi + wu, c = 2 * pr + (lane >> 5);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (__attribute__((address_space(3))) void*)(sGr + pr * G_S), 16,
+                                                   (uint32_t)((c * H * K + 4 * (lane & 31)) * 4), 0, 0, 0);
+        }
+      }
+    }
+  };
+  auto g_lds = [&](int c, int ch) -> const float* {
+    return reinterpret_cast<const float*>(sGr + (c >> 1) * G_S + (c & 1) * (K * 4) + ch * 4);
+  };
 
   // ---- phase-1 fragments into LDS
 #pragma unroll
@@ -293,6 +317,7 @@ __device__ __forceinline__ void chunk_bwd_task(
     }
   }
   issue_qk();  // after phase 1's operands, like the U / W rows
+  issue_g();
   f32x4 aQ[4], aW[4], aK[4];  // dQg^T (rows i, cols c), d delta h^T (rows c, cols i), dKf^T
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl) aQ[tl] = aW[tl] = aK[tl] = zero4();
@@ -574,7 +599,7 @@ __device__ __forceinline__ void chunk_bwd_task(
     kdn_state::put_unit(sF + FR, foff(16 * I + r16, 16 * J + 4 * g4), a[0], a[1], a[2], a[3]);
     kdn_state::put_unit(sF + 3 * FR, foff(16 * J + r16, 16 * I + 4 * g4), at[0], at[1], at[2], at[3]);
   }
-  if constexpr (QK_LDS) __builtin_amdgcn_s_waitcnt(0);  // this wave's k, q rows have reached LDS
+  if constexpr (QK_LDS || G_LDS) __builtin_amdgcn_s_waitcnt(0);  // this wave's k, q or G rows have reached LDS
   __syncthreads();
 
   // ================================ gradient phase ================================
@@ -611,7 +636,8 @@ __device__ __forceinline__ void chunk_bwd_task(
         qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
       }
       av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);
-      Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
+      if constexpr (G_LDS) Gv[p] = *g_lds(min(c, L - 1), i);
+      else Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
     }
     __builtin_amdgcn_sched_barrier(0);
     float mA[4];  // block anchors m_J = (G_{16J} + G_{16J+15}) / 2 of this lane's channel
@@ -631,7 +657,8 @@ __device__ __forceinline__ void chunk_bwd_task(
       Qown[p] = scale * qvp * e;
       Rown[p] = (ISO ? av[p] * kvp : av[p]) * frcp(e);
     }
-    const float4 glv = buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
+    const float4 glv = G_LDS ? *reinterpret_cast<const float4*>(g_lds(L - 1, i0))
+                             : buf_ld4(rG, ((uint32_t)((L - 1) * H) * K + i0) * 4);
     u32x2 kq4[4], qq4[4];
     float4 kap4[4], G4[4];
 #pragma unroll
@@ -650,7 +677,8 @@ __device__ __forceinline__ void chunk_bwd_task(
       } else {
         kap4[tl] = buf_ld4(rkap, o * 4);
       }
-      G4[tl] = buf_ld4(rG, ((uint32_t)(min(16 * tl + r16, L - 1) * H) * K + i0) * 4);
+      G4[tl] = G_LDS ? *reinterpret_cast<const float4*>(g_lds(min(16 * tl + r16, L - 1), i0))
+                     : buf_ld4(rG, ((uint32_t)(min(16 * tl + r16, L - 1) * H) * K + i0) * 4);
     }
     float colpart[4] = {0.f, 0.f, 0.f, 0.f};
     float4 dg_last = float4{0.f, 0.f, 0.f, 0.f};
