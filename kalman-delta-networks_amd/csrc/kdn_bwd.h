@@ -140,6 +140,7 @@ __device__ __forceinline__ void chunk_bwd_task(
   __shared__ float sBeta[NW * C];
   __shared__ float sDot[2][NW][C];  // in-op L2 norm: per-wave partial row dots y . dy of q and k
   __shared__ float sRs[2][C];       // ... and the rows' rstd of q and k (their raw values in memory)
+  __shared__ float sBt[ISO ? C : 1];  // iso: the rows' beta (0 past L), for the gradient phase
   bf16_t* sO = reinterpret_cast<bf16_t*>(smem);  // phase 1: dO, delta, d delta row fragments
   bf16_t* sD = sO + 4 * RB;
   bf16_t* sdD = sD + 4 * RB;
@@ -158,6 +159,10 @@ __device__ __forceinline__ void chunk_bwd_task(
   if (q_rstd && tid < 2 * C) {  // read in the gradient phase, after phase 1's barriers
     const int c = tid & 63;
     sRs[tid >> 6][c] = c < L ? ((tid >> 6) ? k_rstd : q_rstd)[((int64_t)b * T + t0 + c) * H + h] : 0.f;
+  }
+  if (ISO && tid >= 2 * C && tid < 3 * C) {  // read in the gradient phase, after phase 1's barriers
+    const int c = tid - 2 * C;
+    sBt[ISO ? c : 0] = c < L ? kap[((int64_t)b * T + t0 + c) * H + h] : 0.f;
   }
 
   // ================================ loads ================================
@@ -635,7 +640,7 @@ __device__ __forceinline__ void chunk_bwd_task(
         kraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rk, o * 2, 0, 0);
         qraw[p] = __builtin_amdgcn_raw_buffer_load_b16(rq, o * 2, 0, 0);
       }
-      av[p] = ISO ? buf_ld(rkap, crow * 4) : buf_ld(rkap, o * 4);
+      av[p] = ISO ? sBt[ISO ? c : 0] : buf_ld(rkap, o * 4);
       if constexpr (G_LDS) Gv[p] = *g_lds(min(c, L - 1), i);
       else Gv[p] = buf_ld(rG, ((uint32_t)(min(c, L - 1) * H) * K + i) * 4);
     }
@@ -672,7 +677,7 @@ __device__ __forceinline__ void chunk_bwd_task(
         qq4[tl] = __builtin_amdgcn_raw_buffer_load_b64(rq, o * 2, 0, 0);
       }
       if (ISO) {
-        const float be = buf_ld(rkap, c * H * 4);
+        const float be = sBt[ISO ? c : 0];
         kap4[tl] = float4{be, be, be, be};
       } else {
         kap4[tl] = buf_ld4(rkap, o * 4);
