@@ -451,24 +451,22 @@ __device__ __forceinline__ void chunk_bwd_task(
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     uint4 xh0, xl0, xh1, xl1;
-    if constexpr (!LDD) {  // bf16 d delta: the fragment is the raw values
-      uint32_t xr[8];
+    {
+      // d delta from phase 1's staged fragments (still intact: the partials overwrite them only after the barrier
+      // that ends the solve's reads): element (c, v) of the [rows c][k = v] fragments, its bf16 hi and lo halves,
+      // the split of the same value this column needs (a bf16 copy has no lo half)
+      const uint16_t* f16 = reinterpret_cast<const uint16_t*>(sdD);
+      const int v = 16 * w + r16;
+      uint32_t xr[8], xq[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int c = 32 * kb + (j < 4 ? 4 * g4 + j : 16 + 4 * g4 + j - 4);
-        xr[j] = own_v ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rdD, ((uint32_t)c * V + 16 * w + r16) * 2, 0, 0)
-                      : 0u;
+        const int off = (c >> 4) * RB + (v >> 5) * TILE + ((c & 15) + 16 * ((v & 31) >> 3)) * 8 + (v & 7);
+        xr[j] = own_v ? (uint32_t)f16[off] : 0u;
+        xq[j] = own_v && LDD ? (uint32_t)f16[off + 512] : 0u;
       }
       xh0 = uint4{xr[0] | (xr[1] << 16), xr[2] | (xr[3] << 16), xr[4] | (xr[5] << 16), xr[6] | (xr[7] << 16)};
-      xl0 = uint4{0u, 0u, 0u, 0u};
-    } else {
-      float xv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int c = 32 * kb + (j < 4 ? 4 * g4 + j : 16 + 4 * g4 + j - 4);
-        xv[j] = own_v ? buf_ld(rdD, ((uint32_t)c * V + 16 * w + r16) * 4) : 0.f;
-      }
-      split8(xv, xh0, xl0);
+      xl0 = uint4{xq[0] | (xq[1] << 16), xq[2] | (xq[3] << 16), xq[4] | (xq[5] << 16), xq[6] | (xq[7] << 16)};
     }
     {
       const f32x4 t0_ = -aW[2 * kb], t1_ = -aW[2 * kb + 1];  // zero for waves without a channel tile
