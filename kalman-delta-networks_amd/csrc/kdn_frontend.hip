@@ -143,6 +143,36 @@ __device__ __forceinline__ void store8<float>(float* p, const float* f) {
   reinterpret_cast<float4*>(p)[1] = float4{f[4], f[5], f[6], f[7]};
 }
 
+// s_tot [TGN][K] holds each token group's per-channel totals; replace them in place by the exclusive
+// prefix over the groups (forward: the earlier groups' sum, taken in group order, as a left fold from 0) or
+// suffix (backward: the later groups' sum, accumulated from the last group down).  One thread per channel
+// walks the groups, so the reads and writes are consecutive words; the caller's barriers order the
+// writes of the totals before this and the reads of the prefixes after.
+__device__ __forceinline__ void group_prefix_excl(float* s_tot, int K, int TGN, int tid) {
+  if (tid < K) {
+    float run = 0.f;
+#pragma unroll 8
+    for (int q = 0; q < TGN; ++q) {
+      const float x = s_tot[q * K + tid];
+      s_tot[q * K + tid] = run;
+      run += x;
+    }
+  }
+  __syncthreads();
+}
+__device__ __forceinline__ void group_suffix_excl(float* s_tot, int K, int TGN, int tid) {
+  if (tid < K) {
+    float run = 0.f;
+#pragma unroll 8
+    for (int q = TGN - 1; q >= 0; --q) {
+      const float x = s_tot[q * K + tid];
+      s_tot[q * K + tid] = run;
+      run += x;
+    }
+  }
+  __syncthreads();
+}
+
 // grid (H * B * NT) with the head fastest, block 256.  With MAPS (chunk = 64, the fused front) the
 // workgroup also writes its chunk's gain map gain_maps[(b * H + h) * NT + nt] (posterior scale gain_s)
 // from the a, omega, r it has just produced.
@@ -154,7 +184,7 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     int T, int H, int K, int chunk, int NT, float* __restrict__ g_cumsum, float* __restrict__ a_out,
     float* __restrict__ omega_out, float* __restrict__ r_out, float* __restrict__ mu_out,
     float4* __restrict__ gain_maps, float gain_s) {
-  __shared__ float s_tot[256 * 8];  // [tg][K] group totals (TG * K = 2048)
+  __shared__ __attribute__((aligned(16))) float s_tot[256 * 8];  // [tg][K] group totals (TG * K = 2048)
   __shared__ float s_ga[MAPS ? kIsoChunk : 1];  // MAPS: a of each token
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
   const int h = blockIdx.x % H, b = blockIdx.x / H / NT, nt = blockIdx.x / H % NT, tid = threadIdx.x;
@@ -202,10 +232,9 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = acc[j];
   }
   __syncthreads();
+  group_prefix_excl(s_tot, K, TGN, tid);
   float off[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < tg; ++q)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) off[j] += s_tot[q * K + i0 + j];
+  if (tg < TGN) load8<float>(s_tot + tg * K + i0, off);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int t = tg * TPG + u;
@@ -217,7 +246,11 @@ __global__ __launch_bounds__(256) void iso_gate_fwd_vec_kernel(
     }
     // a = mean over channels of e^{2g}: reduce over the CG consecutive lanes of this token group
     float s = e2[u];
-    for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
+    if (CG == 16) {
+      s = row16_sum(s);  // the same butterfly on DPP
+    } else {
+      for (int o = 1; o < CG; o <<= 1) s += __shfl_xor(s, o, 64);
+    }
     if (cg == 0 && u < TPG && t < L) {
       const float at = s * (1.f / (float)K);  // K is a power of two: exact
       a_out[((int64_t)b * T + t0 + t) * H + h] = at;
@@ -246,7 +279,7 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     const float* __restrict__ domega, const float* __restrict__ dr, int T, int H, int K, int chunk, int NT,
     TG* __restrict__ dg_raw, TO* __restrict__ dorr, float* __restrict__ part_A, float* __restrict__ part_dt,
     float* __restrict__ part_bias, IsoGainBwdArgs G) {
-  __shared__ float s_tot[256 * 8];
+  __shared__ __attribute__((aligned(16))) float s_tot[256 * 8];
   __shared__ float s_da[256];
   __shared__ float red[16];
   const int CG = K / 8, TGN = 256 / CG, TPG = (chunk + TGN - 1) / TGN;
@@ -301,10 +334,9 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     for (int j = 0; j < 8; ++j) s_tot[tg * K + i0 + j] = acc[j];
   }
   __syncthreads();
+  group_suffix_excl(s_tot, K, TGN, tid);
   float off[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int q = tg + 1; q < TGN; ++q)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) off[j] += s_tot[q * K + i0 + j];
+  if (tg < TGN) load8<float>(s_tot + tg * K + i0, off);
   __syncthreads();  // s_tot is reused for the per-channel ddt partials below
   float ddt[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, dA_term = 0.f, dob = 0.f, drb = 0.f;
 #pragma unroll
@@ -351,13 +383,27 @@ __global__ __launch_bounds__(256) void iso_gate_bwd_vec_kernel(
     for (int q = 0; q < TGN; ++q) sdt += s_tot[q * K + tid];
     part_dt[((int64_t)p * H + h) * K + tid] = sdt;
   }
-  const float sA = block_sum(dA_term, red);
-  if (part_A && tid == 0) part_A[(int64_t)p * H + h] = sA;
-  const float sO = block_sum(dob, red);
-  const float sR = block_sum(drb, red);
-  if (part_bias && tid == 0) {
-    part_bias[(int64_t)p * 2 * H + h] = sO;
-    part_bias[(int64_t)p * 2 * H + H + h] = sR;
+  // the three block sums share one exchange: each wave's sums (xor butterflies), then the waves' in
+  // order, as block_sum forms each
+  const float wA = wave_sum(dA_term), wO = wave_sum(dob), wR = wave_sum(drb);
+  if ((tid & 63) == 0) {
+    red[3 * (tid >> 6)] = wA;
+    red[3 * (tid >> 6) + 1] = wO;
+    red[3 * (tid >> 6) + 2] = wR;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sA = 0.f, sO = 0.f, sR = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      sA += red[3 * i];
+      sO += red[3 * i + 1];
+      sR += red[3 * i + 2];
+    }
+    if (part_A) part_A[(int64_t)p * H + h] = sA;
+    if (part_bias) {
+      part_bias[(int64_t)p * 2 * H + h] = sO;
+      part_bias[(int64_t)p * 2 * H + H + h] = sR;
+    }
   }
 }
 
