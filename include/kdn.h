@@ -261,6 +261,9 @@ int kdn_mem_fwd(const uint16_t* q, const uint16_t* k, const float* kappa_or_beta
  * kernel (kdn_l2norm_bwd takes the bf16-rounded dy instead; the two agree to bf16 rounding).
  * `stages`: bit 0 reverse state pass, bit 1 the chunk-parallel backward, bits 2 and 3 the exact
  * path's solves and gradients for the chunks outside the factored range (-1 = all, in this order).
+ * Bits 2 and 3 in one call run as one launch (each such chunk's solves, gradients and, with q_rstd, the
+ * norm's backward of its rows in one workgroup), bit-identical to a call with bit 2 and then one with
+ * bit 3.
  * Bits 0 and 1 in one call, with one chunk group (kdn_mem_state_groups == 1), at least 16 chunks
  * and at least 32 CUs the pass leaves idle (the overlapped schedule): the reverse pass runs in two
  * segments, and chunk-backward work of the first segment's chunks runs beside the second on a

@@ -400,22 +400,32 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
 // ===========================================================================
 // Backward: transposed triangular solves and dN.
 // ===========================================================================
+// LDS bytes of the two exact backward steps (their arrays are carved from a caller's 16-byte aligned pool,
+// so one kernel can run both on the same bytes).  Every array size is a multiple of 4 floats.
+template <int K, int V>
+struct ExactLds {
+  static constexpr int KP = K + 4, XP = V + K + 4, P1 = 3 * C * KP, P2 = 2 * C * XP, R1 = P1 > P2 ? P1 : P2;
+  static constexpr int KQ = K + 8;  // QKStride<K, bf16_t>
+  static constexpr int solve = (R1 + C * NS + 4) * 4;
+  static constexpr int contrib = 2 * C * KQ * 2 + (2 * C * KP + 2 * C * NS + 4 + 5 * K + C * (K / 16)) * 4;
+  static constexpr int both = solve > contrib ? solve : contrib;
+};
+
 // Exact path for one chunk (rebuilds N with per-block anchors, scalar back substitution); runs
-// only for the chunks the forward flagged as outside the single-anchor range.
+// only for the chunks the forward flagged as outside the single-anchor range.  lds: ExactLds::solve bytes.
 template <int K, int V, bool ISO>
 __device__ void bwd_solve_exact_chunk(
     const bf16_t* __restrict__ k, const float* __restrict__ kap, const float* __restrict__ gc,
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, bf16_t* __restrict__ dv, float* __restrict__ dKg,
-    float* __restrict__ dNg, int n, int bh, const float* __restrict__ k_rstd, bool dd16) {
+    float* __restrict__ dNg, int n, int bh, const float* __restrict__ k_rstd, bool dd16, unsigned char* lds) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // phase 1: sK | sA | sG (3 x C x KP); phase 2 (after the solve) reuses it as sX | sUW (2 x C x XP)
-  constexpr int P1 = 3 * C * KP, P2 = 2 * C * XP;
-  constexpr int R1 = P1 > P2 ? P1 : P2;
-  __shared__ __attribute__((aligned(16))) float sBuf[R1];
-  __shared__ __attribute__((aligned(16))) float sN[C * NS];
-  __shared__ float sSpan[4];
+  constexpr int R1 = ExactLds<K, V>::R1;
+  float* sBuf = reinterpret_cast<float*>(lds);
+  float* sN = sBuf + R1;
+  float* sSpan = sN + C * NS;
   float* sK = sBuf;
   float* sA = sBuf + C * KP;
   float* sG = sBuf + 2 * C * KP;
@@ -506,12 +516,13 @@ __global__ __launch_bounds__(256) void mem_bwd_solve_exact_kernel(
     const float* __restrict__ dDl, const float* __restrict__ dWg, const float* __restrict__ U,
     const float* __restrict__ W, int T, int H, int NT, int NB, const int* __restrict__ flags, bf16_t* __restrict__ dv,
     float* __restrict__ dKg, float* __restrict__ dNg, const float* __restrict__ k_rstd, bool dd16) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[ExactLds<K, V>::solve];
   if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
     bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, lin % NT, lin / NT, k_rstd,
-                                     dd16);
+                                     dd16, lds);
   }
 }
 
@@ -528,17 +539,22 @@ __device__ void bwd_contrib_exact_chunk(
     const float* __restrict__ dQg, const float* __restrict__ dKg, const float* __restrict__ dKf,
     const float* __restrict__ dgl, int T, int H, int NT, float scale, bf16_t* __restrict__ dq,
     bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta, float* __restrict__ dg, int n,
-    int bh, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd) {
+    int bh, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, unsigned char* lds) {
   constexpr int KP = K + 4;
   constexpr int NCT = K / 16;  // channel tiles
   constexpr int KQ = QKStride<K, bf16_t>::value;
-  __shared__ __attribute__((aligned(16))) bf16_t sQ[C * KQ], sK[C * KQ];  // bf16 inputs are exact in bf16
-  __shared__ __attribute__((aligned(16))) float sA[C * KP], sG[C * KP];
-  __shared__ __attribute__((aligned(16))) float sDN[C * NS], sDM[C * NS];
-  __shared__ float sSpan[4];
-  __shared__ float sColPart[4 * K];     // per row block partial of sum_c dKf kappa e^{g_last - g}
-  __shared__ float sDgLast[K];          // dg of row L-1 before the g_last terms
-  __shared__ float sBetaPart[C * NCT];  // iso: per (row, channel tile) partial of sum_i dkappa k
+  static_assert(KQ == ExactLds<K, V>::KQ, "staged q / k stride");
+  // lds: ExactLds::contrib bytes
+  bf16_t* sQ = reinterpret_cast<bf16_t*>(lds);  // bf16 inputs are exact in bf16
+  bf16_t* sK = sQ + C * KQ;
+  float* sA = reinterpret_cast<float*>(sK + C * KQ);
+  float* sG = sA + C * KP;
+  float* sDN = sG + C * KP;
+  float* sDM = sDN + C * NS;
+  float* sSpan = sDM + C * NS;
+  float* sColPart = sSpan + 4;          // per row block partial of sum_c dKf kappa e^{g_last - g}
+  float* sDgLast = sColPart + 4 * K;    // dg of row L-1 before the g_last terms
+  float* sBetaPart = sDgLast + K;       // iso: per (row, channel tile) partial of sum_i dkappa k
   const int b = bh / H, h = bh % H;
   const int t0 = n * C, L = min(C, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -694,12 +710,13 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
     const float* __restrict__ dgl, int T, int H, int NT, int NB, const int* __restrict__ flags, float scale,
     bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap, float* __restrict__ dbeta,
     float* __restrict__ dg, const float* __restrict__ q_rstd, const float* __restrict__ k_rstd) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[ExactLds<K, V>::contrib];
   if (!any_flagged(flags, NB)) return;
   for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
     if (flags[lin] == 0) continue;
     __syncthreads();
     bwd_contrib_exact_chunk<K, V, ISO>(q, k, kap, gc, dNg, dMg, dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap,
-                                       dbeta, dg, lin % NT, lin / NT, q_rstd, k_rstd);
+                                       dbeta, dg, lin % NT, lin / NT, q_rstd, k_rstd, lds);
   }
 }
 
@@ -708,16 +725,13 @@ __global__ __launch_bounds__(256) void mem_bwd_contrib_exact_kernel(
 // in place.
 // One wave per row (K / 64 elements per lane); a row is read whole before it is written.
 template <int K>
-__global__ __launch_bounds__(256) void l2norm_bwd_flagged_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ q_rstd,
-    const float* __restrict__ k_rstd, int T, int H, int NT, int NB, const int* __restrict__ flags,
-    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk) {
+__device__ void l2norm_bwd_chunk_rows(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                      const float* __restrict__ q_rstd, const float* __restrict__ k_rstd, int T,
+                                      int H, int n, int bh, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk) {
   constexpr int PL = K / 64;
-  if (!any_flagged(flags, NB)) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
-    if (flags[lin] == 0) continue;
-    const int n = lin % NT, bh = lin / NT, b = bh / H, h = bh % H;
+  {
+    const int b = bh / H, h = bh % H;
     const int t0 = n * C, L = min(C, T - t0);
     for (int r = w; r < 2 * L; r += 4) {
       const bool isq = r < L;
@@ -736,6 +750,47 @@ __global__ __launch_bounds__(256) void l2norm_bwd_flagged_kernel(
       dot = wave_sum(dot);
 #pragma unroll
       for (int j = 0; j < PL; ++j) d[row * K + lane + 64 * j] = f2bf(rs * (g[j] - y[j] * dot));
+    }
+  }
+}
+template <int K>
+__global__ __launch_bounds__(256) void l2norm_bwd_flagged_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ q_rstd,
+    const float* __restrict__ k_rstd, int T, int H, int NT, int NB, const int* __restrict__ flags,
+    bf16_t* __restrict__ dq, bf16_t* __restrict__ dk) {
+  if (!any_flagged(flags, NB)) return;
+  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x)
+    if (flags[lin] != 0) l2norm_bwd_chunk_rows<K>(q, k, q_rstd, k_rstd, T, H, lin % NT, lin / NT, dq, dk);
+}
+
+// The whole exact backward of each flagged chunk in one workgroup: the solves (dv, dKg, dN), then the
+// gradients from them, then (in-op norm) the norm's backward of its q, k rows.  Each step reads only what
+// the previous ones wrote for the same chunk; the barrier between steps orders those global writes before
+// the next step's reads (the workgroup's waves share one CU's caches), and the steps' LDS arrays share one
+// pool.  One launch instead of the two or three a call with both exact stages would make.
+template <int K, int V, bool ISO>
+__global__ __launch_bounds__(256) void mem_bwd_exact_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
+    const float* __restrict__ gc, const float* __restrict__ dDl, const float* __restrict__ dWg,
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ dMg,
+    const float* __restrict__ dQg, const float* __restrict__ dKf, const float* __restrict__ dgl, int T, int H, int NT,
+    int NB, const int* __restrict__ flags, float scale, bf16_t* __restrict__ dv, float* __restrict__ dKg,
+    float* __restrict__ dNg, bf16_t* __restrict__ dq, bf16_t* __restrict__ dk, float* __restrict__ dkap,
+    float* __restrict__ dbeta, float* __restrict__ dg, const float* __restrict__ q_rstd,
+    const float* __restrict__ k_rstd, bool dd16) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[ExactLds<K, V>::both];
+  if (!any_flagged(flags, NB)) return;
+  for (int lin = blockIdx.x; lin < NB; lin += gridDim.x) {
+    if (flags[lin] == 0) continue;
+    const int n = lin % NT, bh = lin / NT;
+    __syncthreads();
+    bwd_solve_exact_chunk<K, V, ISO>(k, kap, gc, dDl, dWg, U, W, T, H, NT, dv, dKg, dNg, n, bh, k_rstd, dd16, lds);
+    __syncthreads();
+    bwd_contrib_exact_chunk<K, V, ISO>(q, k, kap, gc, dNg, dMg, dQg, dKg, dKf, dgl, T, H, NT, scale, dq, dk, dkap,
+                                       dbeta, dg, n, bh, q_rstd, k_rstd, lds);
+    if (q_rstd) {
+      __syncthreads();
+      l2norm_bwd_chunk_rows<K>(q, k, q_rstd, k_rstd, T, H, n, bh, dq, dk);
     }
   }
 }
@@ -1183,6 +1238,18 @@ int mem_bwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   if (!overlapped && (stages & 2)) {
     launch_chunk(0, tasks, stream);
     KDN_CHECK_LAUNCH();
+  }
+  if ((stages & 12) == 12) {  // both exact stages: one launch runs each flagged chunk's solves, gradients and norm
+    const int NB = B * H * NT, gx = min(NB, 256);  // one workgroup per CU fits (its LDS)
+#define KDN_EXACT(ISO_)                                                                                               \
+  hipLaunchKernelGGL((mem_bwd_exact_kernel<K, V, ISO_>), dim3(gx), dim3(256), 0, stream, q, k, kap, gc, dD, dW, U, W, \
+                     dM, dQg, dKf, dgl, T, H, NT, NB, flags, scale, dv, dKg, dN, dq, dk, dkap, dbeta, dg, q_rstd,      \
+                     k_rstd, (hm & kdn_state::HB_DD) != 0)
+    if (iso) KDN_EXACT(true);
+    else KDN_EXACT(false);
+#undef KDN_EXACT
+    KDN_CHECK_LAUNCH();
+    return 0;
   }
   if (stages & 4) {  // the chunks left to the exact path: transposed solves into dv, dKg, dN
     const int NB = B * H * NT, gx = min(NB, 512);

@@ -185,3 +185,39 @@ def test_overlapped_forward_under_graph_capture():
             assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager call"
             assert torch.equal(a, c), f"{name}: eager call {rep} differs"
     log("  replays bit-identical")
+
+
+@pytest.mark.parametrize("variant,norm", [("iso", True), ("iso", False), ("diag", False)])
+def test_exact_stages_in_one_launch_equal_separate_calls(variant, norm, monkeypatch):
+    """kdn_mem_bwd with stage bits 2 and 3 in one call runs each flagged chunk's exact solves, its exact
+    gradients and (with the in-op L2 norm) the norm's backward of its q, k rows in one launch; separate
+    calls (bit 2, then bit 3) run them as separate kernels.  On inputs with a chunk taken by the exact
+    path (a ragged last chunk too) every gradient must be bit-identical."""
+    dev = gpu_or_skip()
+    from lit_gpt.kdn_ops import _memscan
+    B, T, H, K = 2, 2048 + 37, 3, 128
+    diag = variant == "diag"
+    log(f"case exact stages one launch vs separate {variant} norm={norm} B={B} T={T} H={H}")
+    q, k, v, G, kap, do, dht = _inputs(dev, 77, B, T, H, K, K, diag, True)
+    rs = {}
+    if norm:  # raw rows the op normalises itself
+        q, k = (2.5 * q.float()).bfloat16(), (0.75 * k.float()).bfloat16()
+        rs = {"q_rstd": torch.empty(B, T, H, device=dev), "k_rstd": torch.empty(B, T, H, device=dev)}
+    scale = K ** -0.5
+    _, saved, _ = _memscan.mem_fwd(q, k, kap, not diag, v, G, scale, output_final_state=True,
+                                   out_dtype=torch.float32 if diag else torch.bfloat16, **rs)
+
+    def run():
+        return _memscan.mem_bwd(q, k, kap, not diag, v, G, saved, scale, do, d_final_state=dht,
+                                need_initial_state_grad=True, overlap=False, **rs)
+
+    one = run()
+    monkeypatch.setattr(_memscan, "BWD_STAGES", ((1, "mem_state_bwd"), (2, "mem_bwd_chunk"),
+                                                 (4, "mem_bwd_solve_exact"), (8, "mem_bwd_contrib_exact")))
+    separate = run()
+    torch.cuda.synchronize()
+    names = ("dq", "dk", "dv", "dkappa" if diag else "dbeta", "dg", "d initial state")
+    for name, a, b in zip(names, one, separate):
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(a, b), f"{name}: one launch differs from the separate exact stages"
+    log("  bit-identical")
