@@ -192,10 +192,11 @@ __global__ __launch_bounds__(256) void reduce_partials_vec_kernel(const float* _
   if (st4 == 0 && j < n) out[(int64_t)blockIdx.y * n + j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
 }
 
-// Several partial reductions (each as reduce_partials_vec_kernel with one segment, same summation order)
-// and the prior-precision VJP in one launch: workgroup b serves the segment whose block range holds it
-// (64 outputs per workgroup); the workgroups past the last segment form the VJP.  The launches this
-// replaces were each a few microseconds of dispatch.
+// Several partial reductions (each as reduce_partials_vec_kernel, same summation order) and the
+// prior-precision VJP in one launch: workgroup x serves the reduction whose block range holds it (64
+// outputs per workgroup); the workgroups past the last one form the VJP.  grid (blocks, S): as in
+// reduce_partials_vec_kernel, row segment y sums rows [NP y / S, NP (y + 1) / S) into out[y * n + j] (the
+// VJP runs in segment 0).  The launches this replaces were each a few microseconds of dispatch.
 struct PartSeg {
   const float* part;
   int64_t stride;
@@ -230,6 +231,7 @@ __global__ __launch_bounds__(256) void reduce_partials_multi_kernel(PartSegs P, 
     blk -= nb;
   }
   if (i == P.nseg) {  // the prior-precision VJP
+    if (blockIdx.y != 0) return;
     const int hh = blk * 256 + threadIdx.x;
     if (hh < P.H) {
       float rows = 0.f;
@@ -242,18 +244,19 @@ __global__ __launch_bounds__(256) void reduce_partials_multi_kernel(PartSegs P, 
   }
   const PartSeg g = P.seg[i];
   const int jj = threadIdx.x & 63, st4 = threadIdx.x >> 6, j = blk * 64 + jj;
+  const int p0 = (int)((int64_t)NP * blockIdx.y / gridDim.y), p1 = (int)((int64_t)NP * (blockIdx.y + 1) / gridDim.y);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (j < g.n) {
-    int pp = st4;
-    for (; pp + 28 < NP; pp += 32) {
+    int pp = p0 + st4;
+    for (; pp + 28 < p1; pp += 32) {
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] += g.part[(int64_t)(pp + 4 * q) * g.stride + j];
     }
-    for (; pp < NP; pp += 4) acc[0] += g.part[(int64_t)pp * g.stride + j];
+    for (; pp < p1; pp += 4) acc[0] += g.part[(int64_t)pp * g.stride + j];
   }
   s[st4][jj] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (st4 == 0 && j < g.n) g.out[j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
+  if (st4 == 0 && j < g.n) g.out[(int64_t)blockIdx.y * g.n + j] = (s[0][jj] + s[1][jj]) + (s[2][jj] + s[3][jj]);
 }
 }  // namespace
 

@@ -1269,16 +1269,6 @@ __global__ __launch_bounds__(256) void diag_front_bwd_emit_kernel(
   }
 }
 
-// d mu_param = sigmoid(mu_param) * sum_b part[b, h]   (or d prior [H] = sum_b part[b, h] when mu_param is null)
-__global__ void front_dmu_kernel(const float* __restrict__ part, const float* __restrict__ mu_param, int B, int H,
-                                 float* __restrict__ out) {
-  const int h = blockIdx.x * blockDim.x + threadIdx.x;
-  if (h >= H) return;
-  float s = 0.f;
-  for (int b = 0; b < B; ++b) s += part[(int64_t)b * H + h];
-  out[h] = mu_param ? s * sigmoidf(mu_param[h]) : s;
-}
-
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // Fixed device workspace of kdn_iso_gain_fwd_noalloc (the per-chunk maps and carries of the iso gain),
 // for callers that cannot allocate.  Each GPU the library runs on holds its own copy until the process
@@ -1505,7 +1495,7 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
 // ---------------------------------------------------------------- fused diag frontend + gain
 namespace {
 struct FrontLayout {  // float offsets into the workspace (each 64-float aligned)
-  int64_t maps, tsum, carry, grp, ab, lcarry, tdg, G, D, partA, partdt, dpart, seg, total;
+  int64_t maps, tsum, carry, grp, ab, lcarry, tdg, G, D, partA, partdt, dpart, seg, segA, total;
 };
 inline int64_t al64(int64_t x) { return (x + 63) / 64 * 64; }
 constexpr int kFrontReduceSegments = 32;
@@ -1540,6 +1530,7 @@ FrontLayout front_layout(int B, int T, int H, int K) {
   L.partdt = o; o += al64(BHK * NV);
   L.dpart = o; o += al64((int64_t)B * H);
   L.seg = o; o += al64((int64_t)kFrontReduceSegments * H * K);
+  L.segA = o; o += al64((int64_t)kFrontReduceSegments * H);
   L.total = o;
   return L;
 }
@@ -1651,22 +1642,38 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
                        (bf16_t*)d_r + b0 * er, dA_log ? ws + L.partA + (int64_t)b0 * NV * a.H : nullptr,
                        ddt_bias ? ws + L.partdt + b0 * ev : nullptr, dprec_out ? dprec_out + b0 * ep : nullptr);
   }
-  const int NP = a.B * NV;
-  if (dA_log)
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv(a.H, 64)), dim3(256), 0, stream, ws + L.partA, NP,
-                       (int64_t)a.H, a.H, dA_log);
-  if (ddt_bias) {  // B*NV partial rows of H*K: segments first, then the segment sums
-    const int S = std::max(1, std::min(kFrontReduceSegments, NP / 64));
-    float* seg = ws + L.seg;
-    hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv((int64_t)a.H * a.K, 64), S), dim3(256), 0, stream,
-                       ws + L.partdt, NP, (int64_t)a.H * a.K, a.H * a.K, S > 1 ? seg : ddt_bias);
-    if (S > 1)
-      hipLaunchKernelGGL(reduce_partials_vec_kernel, dim3(cdiv((int64_t)a.H * a.K, 64)), dim3(256), 0, stream, seg,
-                         S, (int64_t)a.H * a.K, a.H * a.K, ddt_bias);
+  // dA_log [H] and d dt_bias [H K] from the B*NV partial rows, in row segments (S launches' worth of
+  // workgroups) and then the segment sums, and the prior's VJP (sum over b of the per-row cotangents) with
+  // the second: two launches
+  const int NP = a.B * NV, HK = a.H * a.K;
+  const int S = std::max(1, std::min(kFrontReduceSegments, NP / 64));
+  PartSegs fin{};
+  auto add = [](PartSegs& P, const float* part, int n, float* out) { P.seg[P.nseg++] = PartSeg{part, n, n, out}; };
+  if (S > 1) {
+    PartSegs rows{};
+    if (dA_log) add(rows, ws + L.partA, a.H, ws + L.segA);
+    if (ddt_bias) add(rows, ws + L.partdt, HK, ws + L.seg);
+    if (rows.nseg > 0)
+      hipLaunchKernelGGL(reduce_partials_multi_kernel, dim3(part_segs_blocks(rows), S), dim3(256), 0, stream, rows,
+                         NP);
+    if (dA_log) add(fin, ws + L.segA, a.H, dA_log);
+    if (ddt_bias) add(fin, ws + L.seg, HK, ddt_bias);
+  } else {
+    if (dA_log) add(fin, ws + L.partA, a.H, dA_log);
+    if (ddt_bias) add(fin, ws + L.partdt, HK, ddt_bias);
   }
-  if (want_prec && prec_mode != 1)
-    hipLaunchKernelGGL(front_dmu_kernel, dim3(cdiv(a.H, 64)), dim3(64), 0, stream, ws + L.dpart,
-                       d_mu_param ? mu_param : nullptr, a.B, a.H, d_mu_param ? d_mu_param : d_prec);
+  if (want_prec && prec_mode != 1) {  // d mu_param = sigmoid(mu_param) sum_b part (or the [H] prior's sum)
+    fin.mu_param = mu_param;
+    fin.dmu_rows = ws + L.dpart;
+    fin.nrows = a.B;
+    fin.rows_to_param = 1;
+    fin.H = a.H;
+    if (d_mu_param) fin.dmu_param = d_mu_param;
+    else fin.dmu_sum = d_prec;
+  }
+  const int nfin = part_segs_blocks(fin);
+  if (nfin > 0)
+    hipLaunchKernelGGL(reduce_partials_multi_kernel, dim3(nfin), dim3(256), 0, stream, fin, S > 1 ? S : NP);
   KDN_CHECK_LAUNCH();
   return 0;
 }
