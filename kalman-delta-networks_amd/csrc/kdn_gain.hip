@@ -629,9 +629,10 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_carry_v_kernel(const float2
 }
 
 // Two-level carries for long streams.  A (b, h) stream of NT chunk maps per channel is cut into
-// groups of kCarryGroup chunks: the groups' composite maps are formed in parallel (group_map), the
-// serial carry kernel runs over the NG composites only, and every group then replays its own chunk
-// maps from its start value (group_fill).  The serial depth drops from NT to NG + 2 kCarryGroup steps.
+// groups of kCarryGroup chunks: the groups' composite maps are formed in parallel (group_map), and every
+// group then carries the stream's start value through the composites before it and replays its own chunk
+// maps from there (group_fill), so no launch runs the serial carry over the composites.  The serial depth
+// drops from NT to NG + 2 kCarryGroup steps.
 // Forward maps are 2x2 Mobius maps on p (composed with max-abs renormalisation); backward maps are
 // affine, lambda <- A lambda + B, applied from the last chunk down.
 constexpr int kCarryGroup = 32;
@@ -651,15 +652,32 @@ __global__ __launch_bounds__(256) void diag_gain_group_map_kernel(const float4* 
   }
   gmaps[((int64_t)bh * NG + gi) * K + i] = float4{M.m0, M.m1, M.m2, M.m3};
 }
-// grid (B*H, NG), block K: per-chunk carries (p entering each chunk) of group g from its start value
+// grid (B*H, NG), block K: per-chunk carries (p entering each chunk) of group g.  Its start value is the
+// prior's precision carried through the composites of groups 0 .. g-1, which each workgroup applies itself
+// in order with the serial carry's arithmetic (diag_gain_carry_v_kernel over the composites gives the same
+// values); the last group's workgroup also writes the final precision from its own composite.
 __global__ __launch_bounds__(256) void diag_gain_group_fill_kernel(const float4* __restrict__ maps,
-                                                                   const float* __restrict__ gstart, int K, int NT,
-                                                                   int NG, float* __restrict__ carry) {
+                                                                   const float4* __restrict__ gmaps,
+                                                                   const float* __restrict__ prec0, int prec_mode,
+                                                                   int H, int K, int NT, int NG,
+                                                                   float* __restrict__ carry,
+                                                                   float* __restrict__ final_prec) {
   const int bh = blockIdx.x, gi = blockIdx.y, i = threadIdx.x;
   if (i >= K) return;
   const int64_t cb = (int64_t)bh * NT;
   const int n0 = gi * kCarryGroup, n1 = min(NT, n0 + kCarryGroup);
-  float p = gstart[((int64_t)bh * NG + gi) * K + i];
+  float p = 1.f / prior_precision(prec0, prec_mode, bh / H, bh % H, H, K, i);
+  const float4* gm = gmaps + (int64_t)bh * NG * K + i;
+#pragma unroll 8
+  for (int g = 0; g < gi; ++g) {
+    const float4 m = gm[(int64_t)g * K];
+    p = (m.x * p + m.y) / (m.z * p + m.w);
+  }
+  if (final_prec && gi == NG - 1) {
+    const float4 m = gm[(int64_t)gi * K];
+    const float pf = (m.x * p + m.y) / (m.z * p + m.w);
+    final_prec[(int64_t)bh * K + i] = 1.f / pf;
+  }
 #pragma unroll 8
   for (int n = n0; n < n1; ++n) {
     const float4 m = maps[(cb + n) * K + i];
@@ -683,15 +701,30 @@ __global__ __launch_bounds__(256) void diag_gain_bwd_group_map_kernel(const floa
   }
   gab[((int64_t)bh * NG + gi) * K + i] = float2{A, Bc};
 }
-// grid (B*H, NG), block K: per-chunk adjoint carries of group g from lambda leaving the group
+// grid (B*H, NG), block K: per-chunk adjoint carries of group g from lambda leaving the group: the final
+// precision's cotangent carried through the composites of groups NG-1 .. g+1, which each workgroup applies
+// itself in that order with the serial carry's arithmetic (diag_gain_bwd_carry_v_kernel over the composites
+// gives the same values).
 __global__ __launch_bounds__(256) void diag_gain_bwd_group_fill_kernel(const float2* __restrict__ ab,
-                                                                       const float* __restrict__ gend, int K, int NT,
-                                                                       int NG, float* __restrict__ carry) {
+                                                                       const float2* __restrict__ gab,
+                                                                       const float* __restrict__ d_final_prec,
+                                                                       const float* __restrict__ final_prec, int K,
+                                                                       int NT, int NG, float* __restrict__ carry) {
   const int bh = blockIdx.x, gi = blockIdx.y, i = threadIdx.x;
   if (i >= K) return;
   const int64_t cb = (int64_t)bh * NT;
   const int n0 = gi * kCarryGroup, n1 = min(NT, n0 + kCarryGroup);
-  float lam = gend[((int64_t)bh * NG + gi) * K + i];
+  float lam = 0.f;
+  if (d_final_prec) {
+    const float c = final_prec[(int64_t)bh * K + i];
+    lam = -d_final_prec[(int64_t)bh * K + i] * c * c;
+  }
+  const float2* gm = gab + (int64_t)bh * NG * K + i;
+#pragma unroll 8
+  for (int g = NG - 1; g > gi; --g) {
+    const float2 m = gm[(int64_t)g * K];
+    lam = m.x * lam + m.y;
+  }
 #pragma unroll 8
   for (int n = n1 - 1; n >= n0; --n) {
     const float2 m = ab[(cb + n) * K + i];
@@ -1405,13 +1438,10 @@ int kdn_diag_gain_fwd(const float* k, const float* alpha, const float* omega, co
       const int NG = cdiv(NV, kCarryGroup);
       float* grp = maps + (int64_t)B * H * NV * K * 5 + (int64_t)B * H * K;
       float4* gmaps = reinterpret_cast<float4*>(grp);
-      float* gstart = grp + (int64_t)B * H * NG * K * 4;
       hipLaunchKernelGGL(diag_gain_group_map_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float4*)maps, K, NV,
                          NG, gmaps);
-      hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)gmaps,
-                         initial_precision, prec_mode, H, K, NG, gstart, final_precision);
       hipLaunchKernelGGL(diag_gain_group_fill_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float4*)maps,
-                         gstart, K, NV, NG, carry_v);
+                         (const float4*)gmaps, initial_precision, prec_mode, H, K, NV, NG, carry_v, final_precision);
     } else {
       hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float4*)maps,
                          initial_precision, prec_mode, H, K, NV, carry_v, final_precision);
@@ -1460,13 +1490,10 @@ int kdn_diag_gain_bwd(const float* k, const float* alpha, const float* omega, co
       const int NG = cdiv(NV, kCarryGroup);
       float* grp = ab + (int64_t)B * H * NV * K * 5 + (int64_t)B * H * K;
       float2* gab = reinterpret_cast<float2*>(grp);
-      float* gend = grp + (int64_t)B * H * NG * K * 4;
       hipLaunchKernelGGL(diag_gain_bwd_group_map_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float2*)ab, K,
                          NV, NG, gab);
-      hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)gab,
-                         d_final_precision, final_precision, H, K, NG, gend);
       hipLaunchKernelGGL(diag_gain_bwd_group_fill_kernel, dim3(B * H, NG), dim3(bs), 0, stream, (const float2*)ab,
-                         gend, K, NV, NG, carry_v);
+                         (const float2*)gab, d_final_precision, final_precision, K, NV, NG, carry_v);
     } else {
       hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(B * H), dim3(bs), 0, stream, (const float2*)ab,
                          d_final_precision, final_precision, H, K, NV, carry_v);
@@ -1572,13 +1599,10 @@ int front_fwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   if (NV > 2 * kCarryGroup) {  // two-level carry
     const int NG = cdiv(NV, kCarryGroup);
     float4* gmaps = reinterpret_cast<float4*>(ws + L.grp);
-    float* gstart = ws + L.grp + (int64_t)a.B * a.H * NG * a.K * 4;
     hipLaunchKernelGGL(diag_gain_group_map_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float4*)maps, a.K,
                        NV, NG, gmaps);
-    hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float4*)gmaps, prec0,
-                       prec_mode, a.H, a.K, NG, gstart, final_precision);
     hipLaunchKernelGGL(diag_gain_group_fill_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float4*)maps,
-                       gstart, a.K, NV, NG, carry);
+                       (const float4*)gmaps, prec0, prec_mode, a.H, a.K, NV, NG, carry, final_precision);
   } else {
     hipLaunchKernelGGL(diag_gain_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float4*)maps, prec0,
                        prec_mode, a.H, a.K, NV, carry, final_precision);
@@ -1617,13 +1641,10 @@ int front_bwd(const FrontArgs<TX>& a, const float* mu_param, const float* prec0,
   if (NV > 2 * kCarryGroup) {  // two-level carry
     const int NG = cdiv(NV, kCarryGroup);
     float2* gab = reinterpret_cast<float2*>(ws + L.grp);
-    float* gend = ws + L.grp + (int64_t)a.B * a.H * NG * a.K * 2;
     hipLaunchKernelGGL(diag_gain_bwd_group_map_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float2*)ab,
                        a.K, NV, NG, gab);
-    hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float2*)gab,
-                       d_final_precision, final_precision, a.H, a.K, NG, gend);
     hipLaunchKernelGGL(diag_gain_bwd_group_fill_kernel, dim3(a.B * a.H, NG), dim3(bs), 0, stream, (const float2*)ab,
-                       gend, a.K, NV, NG, lcarry);
+                       (const float2*)gab, d_final_precision, final_precision, a.K, NV, NG, lcarry);
   } else {
     hipLaunchKernelGGL(diag_gain_bwd_carry_v_kernel, dim3(a.B * a.H), dim3(bs), 0, stream, (const float2*)ab,
                        d_final_precision, final_precision, a.H, a.K, NV, lcarry);
