@@ -12,13 +12,13 @@
 //   range m = (G_0 + G_{L-1}) / 2, so |G - m| <= span / 2 on every row:
 //   Lk = k 2^{G - m},  Lq = scale q 2^{G - m},  R = kappa 2^{m - G}  (each <= 2^{span/2} times k, q, kappa);
 //   a chunk whose span max_i (G_0 - G_{L-1})_i exceeds kAnchorSpanMax is flagged (flags = 1).
-// intra_fwd_block_kernel (the flagged chunks): one anchor per 16-token block J,
+// intra_fwd_block_chunk (each flagged chunk, in one launch with the exact path): one anchor per 16-token block J,
 //   m_J = (G_{16J} + G_{16J+15})/2 per channel (rows clamped), so |G - m_J| <= span_J / 2 inside
 //   the block.  For s in block J and c in block I >= J, 2^{G_c - G_s} = (2^{G_c - m_J}) (2^{m_J - G_s}):
 //   R_J = kappa 2^{m_J - G} (published per block),  Lk_IJ = k 2^{G - m_I} 2^{m_I - m_J}  (<= 1 for J < I),
 //   Lq likewise.  A chunk handled here gets flags = 0; one with a block span past kBlockSpanMax
 //   (the masked upper-triangle products of a diagonal block reach 2^span) stays flagged for the
-//   exact per-block kernel, which runs last.
+//   exact per-block path, which the same workgroup then runs.
 // A random-init 1.3B model decays by up to ~e^-2 per token in its fastest channels on average (chunk
 // spans up to ~170), which the midpoint anchor covers; faster decay (trained models reach ~e^-4 per
 // token, spans ~370) takes the block kernel.
@@ -436,34 +436,43 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   intra_solve_emit<K, V, NORM>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid, sRk);
 }
 
-// grid (chunks, B*H), block 256 (chunks n0 ..); a workgroup whose chunk intra_fwd_kernel did not flag exits at
-// once.
-template <int K, int V, bool ISO, bool NORM = false>
-__global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
+// LDS of the block-anchor path for one chunk (intra_fwd_block_chunk), carved from a caller's 16-byte aligned
+// pool: [R fragments | A] then N, the U/W stage reusing the whole buffer; the k rstd of the rows; the block
+// spans; the block anchors.
+template <int K, int V>
+struct BlockLds {
+  static constexpr int KB = K / 32, RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
+  static constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
+  static constexpr int SBYTES = RABYTES + C * AP * 4 > C * XR * 4 ? RABYTES + C * AP * 4 : C * XR * 4;
+  static constexpr int bytes = SBYTES + C * 4 + 16 + 4 * K * 4;
+  static_assert(SBYTES % 16 == 0, "16-byte arrays");
+};
+
+// The block-anchor path for one chunk intra_fwd_kernel flagged (block 256; lds: BlockLds<K, V>::bytes).
+// Returns false, leaving the chunk flagged, when a 16-token block spans more than kBlockSpanMax (the exact
+// path takes it); otherwise writes the chunk's outputs and clears its flag.
+template <int K, int V, bool ISO, bool NORM>
+__device__ __forceinline__ bool intra_fwd_block_chunk(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd = nullptr,
-    float* __restrict__ k_rstd = nullptr, int n0 = 0) {
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd,
+    float* __restrict__ k_rstd, int n, int bh, unsigned char* lds) {
   constexpr int KB = K / 32;
-  // R fragments [s-tile][kb] until the N / M build, then A [c][s] in the same bytes
-  constexpr int RBYTES = (C / 16) * KB * TILE * 2, ABYTES = C * AP * 4;
-  constexpr int RABYTES = RBYTES > ABYTES ? RBYTES : ABYTES;
-  // [R fragments | A] then N [c][s]; the U/W stage reuses the whole buffer for its operand staging
-  constexpr int SBYTES = RABYTES + C * AP * 4 > C * XR * 4 ? RABYTES + C * AP * 4 : C * XR * 4;
+  using Lds = BlockLds<K, V>;
+  constexpr int RABYTES = Lds::RABYTES;
   static_assert(V <= 128 && K <= 128, "operand staging holds up to 128 columns");
-  __shared__ __attribute__((aligned(16))) unsigned char sbuf[SBYTES];
-  __shared__ float sRk[C];  // in-op L2 norm: the rows' k rstd for the W stage
+  unsigned char* sbuf = lds;
+  float* sRk = reinterpret_cast<float*>(lds + Lds::SBYTES);  // in-op L2 norm: the rows' k rstd for the W stage
   bf16_t* sR = reinterpret_cast<bf16_t*>(sbuf);
   float* sA = reinterpret_cast<float*>(sbuf);
   float* sN = reinterpret_cast<float*>(sbuf + RABYTES);
   float* sX = reinterpret_cast<float*>(sbuf);  // U/W stage: operand rows [s][col], pitch XR
-  __shared__ float sSpan[4];
-  __shared__ __attribute__((aligned(16))) float sMid[4 * K];  // block anchors m_J per channel
+  float* sSpan = sRk + C;
+  float* sMid = sSpan + 4;  // block anchors m_J per channel
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
-  const int n = n0 + blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H;  // chunks n0 + gridDim.x
+  const int b = bh / H, h = bh % H;
   const int64_t lin = (int64_t)bh * NT + n;
-  if (flags[lin] == 0) return;  // handled by intra_fwd_kernel
   const int t0 = n * C, L = min(C, T - t0);
 
   // [B,T,H,D] inputs: row c of this chunk at ((b*T + t0 + c)*H + h)*D
@@ -500,7 +509,7 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
   }
   __syncthreads();
   const float cspan = fmaxf(fmaxf(sSpan[0], sSpan[1]), fmaxf(sSpan[2], sSpan[3]));
-  if (!(cspan <= kBlockSpanMax)) return;  // left flagged: the exact kernel takes this chunk
+  if (!(cspan <= kBlockSpanMax)) return false;  // left flagged: the exact path takes this chunk
 
   // ---- 1. per-row factors: wave w owns rows 16w + r16; lanes hold 8 consecutive channels.
   // Rows past L read zero k, q, kappa and repeat the gate of row L-1, so every factor is bounded.
@@ -617,6 +626,7 @@ __global__ __launch_bounds__(256, 2) void intra_fwd_block_kernel(
 
   intra_solve_emit<K, V, NORM>(sA, sN, sX, An, rv, rk, rG, rU, rW, H, tid, sRk);
   if (tid == 0) flags[lin] = 0;
+  return true;
 }
 
 }  // namespace kdn_intra

@@ -283,21 +283,28 @@ __device__ void build_NM(const float* sQ, const float* sK, const float* sA, cons
 // ===========================================================================
 // Exact path for one chunk (per-block decay anchors, per-element diagonal blocks when a
 // block's span exceeds kSpanMax, scalar forward substitution).  Runs only for the chunks the
-// MFMA kernel (kdn_intra.h) flags as outside its single-anchor range.
+// MFMA kernels (kdn_intra.h) leave flagged: a 16-token block spans more than their block-anchor range.
+// lds: ExactFwdLds<K, V>::bytes of a caller's 16-byte aligned pool.
+template <int K, int V>
+struct ExactFwdLds {
+  static constexpr int KP = K + 4, XP = V + K + 4;
+  static constexpr int OFF2 = (2 * C * KP > C * XP) ? 2 * C * KP : C * XP;
+  static constexpr int bytes = (OFF2 + 2 * C * KP + C * NS + 4) * 4;
+};
 template <int K, int V, bool ISO>
 __device__ void intra_fwd_exact_chunk(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, float scale,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
     float* __restrict__ Mg, float* __restrict__ Ag, int n, int bh, float* __restrict__ q_rstd,
-    float* __restrict__ k_rstd) {
+    float* __restrict__ k_rstd, unsigned char* lds) {
   constexpr int KP = K + 4;
   constexpr int XP = V + K + 4;
   // sQ | sA are dead after Kf / Qg are written and are then reused for the solve's sX [C][XP]
-  constexpr int OFF2 = (2 * C * KP > C * XP) ? 2 * C * KP : C * XP;
-  __shared__ __attribute__((aligned(16))) float sBuf[OFF2 + 2 * C * KP];
-  __shared__ __attribute__((aligned(16))) float sN[C * NS];  // transposed: sN[s * NS + c] = N[c][s]
-  __shared__ float sSpan[4];
+  constexpr int OFF2 = ExactFwdLds<K, V>::OFF2;
+  float* sBuf = reinterpret_cast<float*>(lds);
+  float* sN = sBuf + OFF2 + 2 * C * KP;  // transposed: sN[s * NS + c] = N[c][s]
+  float* sSpan = sN + C * NS;
   float* sQ = sBuf;
   float* sA = sBuf + C * KP;
   float* sK = sBuf + OFF2;
@@ -376,14 +383,20 @@ __device__ __forceinline__ bool any_flagged(const int* __restrict__ flags, int N
   return __syncthreads_or(any) != 0;
 }
 
-// Chunks n0 .. n1 - 1 of every head (the forward's schedule may build a sequence in two ranges).
-template <int K, int V, bool ISO>
-__global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
+// The chunks intra_fwd_kernel flagged, of chunks n0 .. n1 - 1 of every head (the forward's schedule may build a
+// sequence in two ranges), grid-stride (i = blockIdx.x, + gridDim.x, ...: head i / len, chunk n0 + i % len).
+// Each flagged chunk takes the block-anchor path, and the exact path when that leaves it flagged, in the same
+// workgroup; the two paths' LDS arrays share one pool (one workgroup per CU).  A workgroup first loads all its
+// chunks' flags at once and exits when none is set.  One launch for both paths.
+template <int K, int V, bool ISO, bool NORM>
+__global__ __launch_bounds__(256) void intra_fwd_flagged_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const float* __restrict__ kap,
     const bf16_t* __restrict__ v, const float* __restrict__ gc, int T, int H, int NT, int BH, int n0, int n1,
     float scale, float* __restrict__ U, float* __restrict__ W, float* __restrict__ Kf, float* __restrict__ Qg,
-    float* __restrict__ Mg, float* __restrict__ Ag, const int* __restrict__ flags, float* __restrict__ q_rstd,
+    float* __restrict__ Mg, float* __restrict__ Ag, int* __restrict__ flags, float* __restrict__ q_rstd,
     float* __restrict__ k_rstd) {
+  constexpr int LB = kdn_intra::BlockLds<K, V>::bytes, LE = ExactFwdLds<K, V>::bytes;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LB > LE ? LB : LE];
   const int len = n1 - n0, N = BH * len;
   int any = 0;
   for (int i = blockIdx.x + threadIdx.x * gridDim.x; i < N; i += blockDim.x * gridDim.x)
@@ -393,7 +406,12 @@ __global__ __launch_bounds__(256) void mem_intra_fwd_exact_kernel(
     const int bh = i / len, n = n0 + i % len;
     if (flags[(int64_t)bh * NT + n] == 0) continue;
     __syncthreads();  // LDS of the previous chunk is dead
-    intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, n, bh, q_rstd, k_rstd);
+    if (!kdn_intra::intra_fwd_block_chunk<K, V, ISO, NORM>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag,
+                                                           flags, q_rstd, k_rstd, n, bh, lds)) {
+      __syncthreads();  // the block path's span reads are done
+      intra_fwd_exact_chunk<K, V, ISO>(q, k, kap, v, gc, T, H, NT, scale, U, W, Kf, Qg, Mg, Ag, n, bh, q_rstd, k_rstd,
+                                       lds);
+    }
   }
 }
 
@@ -1030,21 +1048,19 @@ int mem_fwd_impl(const bf16_t* q, const bf16_t* k, const float* kap, int iso, co
   // are not written
   const bool infer = stages >= 0 && (stages & 8) != 0;
   float* Asave = infer ? nullptr : A;
-  // the intra-chunk build of chunks n0 .. n1 - 1 on stream s: the single-anchor kernel, the block-anchor
-  // kernel for the chunks it flagged, the exact kernel for those the block kernel left flagged
+  // the intra-chunk build of chunks n0 .. n1 - 1 on stream s: the single-anchor kernel, then one launch for the
+  // chunks it flagged (the block-anchor path, and the exact path for those it leaves flagged)
   auto launch_intra = [&](int n0, int n1, hipStream_t s) {
     const dim3 gchunk(n1 - n0, B * H);
-    const int gx = min(B * H * (n1 - n0), 512);
+    const int gx = min(B * H * (n1 - n0), 256);  // one workgroup per CU fits (its LDS)
     // the in-op L2 norm (q_rstd given) is a template variant: its row loads would otherwise cost the
     // plain kernels registers
 #define KDN_INTRA(ISO_, NORM_)                                                                                         \
   do {                                                                                                                 \
     hipLaunchKernelGGL((kdn_intra::intra_fwd_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, s, q, k, kap, v, gc, T, \
                        H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd, n0);                               \
-    hipLaunchKernelGGL((kdn_intra::intra_fwd_block_kernel<K, V, ISO_, NORM_>), gchunk, dim3(256), 0, s, q, k, kap, v,  \
-                       gc, T, H, NT, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd, n0);                        \
-    hipLaunchKernelGGL((mem_intra_fwd_exact_kernel<K, V, ISO_>), dim3(gx), dim3(256), 0, s, q, k, kap, v, gc, T, H, NT, \
-                       B * H, n0, n1, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                          \
+    hipLaunchKernelGGL((intra_fwd_flagged_kernel<K, V, ISO_, NORM_>), dim3(gx), dim3(256), 0, s, q, k, kap, v, gc, T,  \
+                       H, NT, B * H, n0, n1, scale, U, W, Kf, Qg, M, Asave, flags, q_rstd, k_rstd);                  \
   } while (0)
     if (iso && q_rstd) KDN_INTRA(true, true);
     else if (iso) KDN_INTRA(true, false);
