@@ -36,7 +36,8 @@ C = 64
 OP_BYTES = {"iso": lambda d: (6 * d + 4 * d + 8 + 2 * d) + (22 * d + 16),
             "diag": lambda d: (6 * d + 4 * d + 4 * d + 4 + 2 * d) + (30 * d + 8)}
 OP_FWD_BYTES = {"diag": lambda d: 6 * d + 4 * d + 4 * d + 4 + 2 * d}
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "kdn_traffic.json")
+# calibrated counter traffic per variant (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script)
+TRAFFIC_FILES = [os.path.join(ROOT, "profiles", f) for f in ("kdn_traffic.json", "kdn_traffic_diag.json")]
 
 # MFMA path of each kernel: "f32" = fp32 MFMA; "bf16x3" = fp32-grade products as three bf16
 # MFMAs (hi*hi + hi*lo + lo*hi), whose ceiling is the bf16 peak / 3 in algorithmic FLOP/s.
@@ -143,14 +144,15 @@ S8D_BYTES = {"mem_bwd_chunk": {"iso": lambda d: 22 * d + 16, "diag": lambda d: 3
                                        "diag": lambda d: 16 * d + 4 * d * d / C}}
 
 
-def headline_roofline(variant: str, tag: str, kern: dict, B: int, T: int, H: int, K: int, traffic):
+def headline_roofline(variant: str, tag: str, kern: dict, B: int, T: int, H: int, K: int, traffic=(None, None)):
     """The dominant kernel against MI355X's HBM peak, priced on the scope's algorithmic bytes for it
     (S8D_BYTES per token-head times B*T*H) over its mean event-timed duration; the figure on this
     decomposition's own bytes (kernel_counts) is kept beside it."""
     t = kern["ms"] * 1e-3
     per = S8D_BYTES.get(tag, {}).get(variant)
-    out = {"kernel": tag, "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "traffic": traffic,
-           "traffic_source": (os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None),
+    nbytes_traffic, source = traffic
+    out = {"kernel": tag, "bound": "hbm", "peak": HBM_PEAK_GBS, "unit": "GB/s", "traffic": nbytes_traffic,
+           "traffic_source": (os.path.relpath(source, ROOT) if source is not None else None),
            "kernel_ms": kern["ms"]}
     if per is not None:
         nbytes = per(K) * B * T * H
@@ -599,17 +601,18 @@ def cpu_baseline_config3(T: int, K: int, B: int, H: int):
 
 
 def measured_traffic(kernel: str, config: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            rec = json.load(f)
-    except (OSError, ValueError):
-        return None
-    k = rec.get("kernels", {}).get(kernel)
-    if rec.get("config") != config or not k:
-        return None
-    return int(k["fetch_bytes"] + k["write_bytes"])
+    """(HBM bytes per launch of `kernel`, the file they come from) from the committed rocprofv3 --pmc summary
+    whose config is `config` (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or (None, None)."""
+    for path in TRAFFIC_FILES:
+        try:
+            with open(path) as f:
+                rec = json.load(f)
+        except (OSError, ValueError):
+            continue
+        k = rec.get("kernels", {}).get(kernel)
+        if rec.get("config") == config and k:
+            return int(k["fetch_bytes"] + k["write_bytes"]), path
+    return None, None
 
 
 def calib_copy(mib: int):
@@ -695,7 +698,7 @@ def main():
         print(json.dumps({"metric": METRIC, "value": round(res["tokens_per_s"], 1), "unit": "tokens/s",
                           "ms_per_step": round(res["ms_per_step"], 4), "steps": args.steps, "warmup": args.warmup,
                           "roofline": headline_roofline(main_v, res["dominant"], res["kernels"][res["dominant"]],
-                                                        B, T, H, K, None),
+                                                        B, T, H, K),
                           "op_roofline": op_roofline(main_v, res["ms_per_step"], B, T, H, K),
                           "kernels": res["kernels"]}), flush=True)
         return
@@ -726,8 +729,9 @@ def main():
                                   "ms_per_step": round(res_other["ms_per_step"], 4),
                                   "op_roofline": op_roofline(other, res_other["ms_per_step"], B, T, H, K),
                                   "roofline": headline_roofline(other, res_other["dominant"],
-                                                                res_other["kernels"][res_other["dominant"]],
-                                                                B, T, H, K, None),
+                                                                res_other["kernels"][res_other["dominant"]], B, T, H,
+                                                                K, measured_traffic(res_other["dominant"],
+                                                                                    f"{other} B{B} T{T} H{H} d{K}")),
                                   "dominant": res_other["dominant"],
                                   "kernels": res_other["kernels"]},
                  "layer_frontends": {"workload": "packed q|k|v short conv + SiLU and sigmoid-gated RMS norm, "
