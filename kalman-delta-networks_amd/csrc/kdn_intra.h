@@ -91,6 +91,13 @@ __device__ __forceinline__ void st8(bufrsrc r, uint32_t off, const float* f) {
                                                __float_as_uint(f[7])},
                                          r, off + 16, 0, 0);
 }
+// Orders one wave's LDS accesses around a cross-lane exchange: the LDS unit serves a wave's
+// instructions in issue order, so only the compiler's reordering has to be fenced off.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Stages after the N / M build, shared by both kernels: the inverse A = (I + N)^{-1} from sN, A^T
 // saved to An, then U = A V and W = A (k 2^G) (rows past L dropped by the output descriptors).
@@ -335,6 +342,12 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
   const uint32_t crow = (uint32_t)(c * H), grow = (uint32_t)(min(c, L - 1) * H);
   uint4 lkh[KB], lkl[KB], lqh[KB], lql[KB];
   const float beta = ISO ? buf_ld(rkap, crow * 4) : 0.f;
+  // Kf and Qg leave through this wave's slice of the N tile's bytes (unused until stage 2): a lane's 8
+  // channels lie 32 bytes from the next lane's, so a direct store covers 16 rows in 16-byte pieces;
+  // regrouped, each store writes 8 whole 128-byte row segments.  Slice: [Kf | Qg][16 rows][32 channels],
+  // 16-byte quad q of row r at slot q ^ (r & 7).
+  static_assert(4 * 2 * 16 * 32 * 4 <= C * AP * 4, "Kf / Qg staging fits the N tile");
+  float* sKQ = sN + w * (2 * 16 * 32);
   // with the in-op L2 norm (NORM) q, k are raw: this workgroup normalises its rows
   float rsq = 1.f, rsk = 1.f;
   u32x4 kraw[KB], qraw[KB];
@@ -401,10 +414,26 @@ __global__ __launch_bounds__(256, 3) void intra_fwd_kernel(
     split8(rr, rh, rl);
     *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + lane * 8) = rh;
     *reinterpret_cast<uint4*>(sR + (w * KB + kb) * TILE + 512 + lane * 8) = rl;
-    st8(rKf, ((uint32_t)c * K + i0) * 4, kf);
-    st8(rQg, ((uint32_t)c * K + i0) * 4, qg);
+    wave_lds_sync();  // the previous column block's reads are issued before these writes
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      float* slot = sKQ + r16 * 32 + (((2 * g4 + hf) ^ (r16 & 7)) * 4);
+      *reinterpret_cast<float4*>(slot) = float4{kf[4 * hf], kf[4 * hf + 1], kf[4 * hf + 2], kf[4 * hf + 3]};
+      *reinterpret_cast<float4*>(slot + 512) = float4{qg[4 * hf], qg[4 * hf + 1], qg[4 * hf + 2], qg[4 * hf + 3]};
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int rr = (lane >> 3) + 8 * hh, qd = lane & 7;
+      const float* slot = sKQ + rr * 32 + ((qd ^ (rr & 7)) * 4);
+      const uint32_t off = ((uint32_t)(16 * w + rr) * K + 32 * kb + 4 * qd) * 4;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const float4*>(slot)),
+                                             rKf, off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(u32x4, *reinterpret_cast<const float4*>(slot + 512)), rQg, off, 0, 0);
+    }
   }
-  __syncthreads();  // R fragments of every row block
+  __syncthreads();  // R fragments of every row block; the N tile's bytes are free again
 
   // ---- 2. N and M tiles of row block I = w
   const bufrsrc rM = make_buf(Mn, C * C * 4);
