@@ -39,6 +39,7 @@ using kdn_state::C;
 using kdn_state::mfma;
 using kdn_state::mma2;
 using kdn_state::mma3;
+using kdn_state::wave_lds_sync;
 using kdn_state::split2;
 using kdn_state::TILE;
 using kdn_state::zero4;
@@ -90,13 +91,6 @@ __device__ __forceinline__ void st8(bufrsrc r, uint32_t off, const float* f) {
   __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]),
                                                __float_as_uint(f[7])},
                                          r, off + 16, 0, 0);
-}
-// Orders one wave's LDS accesses around a cross-lane exchange: the LDS unit serves a wave's
-// instructions in issue order, so only the compiler's reordering has to be fenced off.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Stages after the N / M build, shared by both kernels: the inverse A = (I + N)^{-1} from sN, A^T

@@ -98,6 +98,13 @@ __device__ __forceinline__ float4 quad_transpose(const float4& x, int r) {
   }
   return float4{a0, a1, a2, a3};
 }
+// Orders one wave's LDS accesses around a cross-lane exchange: the LDS unit serves a wave's
+// instructions in issue order, so only the compiler's reordering has to be fenced off.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 // 8 floats -> split hi/lo fragment (slot j <- x[j])
 __device__ __forceinline__ void split8v(const float* x, uint4& hi, uint4& lo) {
   split2(x[0], x[1], hi.x, lo.x);
@@ -333,6 +340,10 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
   // RO: B fragments of h_n ([wave][kb][hi, lo][lane], K / 32 k-blocks) then of delta_n (2 k-blocks)
   constexpr int NHF = 4 * KB * 2 * 64, NDF = 4 * 2 * 2 * 64;
   __shared__ __attribute__((aligned(16))) uint4 sHD[RO ? NHF + NDF : 1];
+  // RO: each readout wave's 16 output rows, regrouped so that every store writes whole row segments
+  constexpr int ROWB = COLS * (int)sizeof(TO), QPR = ROWB / 16, RPI = 1024 / ROWB;
+  static_assert(ROWB % 128 == 0 && RPI <= 16, "readout rows of 8 or more 16-byte quads");
+  __shared__ __attribute__((aligned(16))) uint4 sO[RO ? 4 * 16 * QPR : 1];
   int bh, vs, g;
   bool real, phi;
   if (!group_task<V, K, false>(P, BH, bh, vs, g, real, phi)) return;
@@ -381,6 +392,8 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
         __syncthreads();  // end of phase 1: h_n and delta_n fragments published
         const bufrsrc ro = make_buf(out + row_bthk(b, t0, h, T, H, V), (uint32_t)((L - 1) * H + 1) * V * sizeof(TO));
         const int qr = lane & 3;
+        // this wave's rows; the barriers of each chunk separate the last chunk's reads from these writes
+        unsigned char* sOw = reinterpret_cast<unsigned char*>(sO) + rw * 16 * ROWB;
 #pragma unroll
         for (int sw = 0; sw < 4; ++sw) {  // the 16 columns of state wave sw (four independent chains)
           f32x4 O = zero4();
@@ -395,17 +408,26 @@ __global__ __launch_bounds__(RO ? 2 * state_threads(V) : state_threads(V), RO ? 
             const uint4 dh2 = sHD[NHF + ((sw * 2 + kb) * 2) * 64 + lane], dl2 = sHD[NHF + ((sw * 2 + kb) * 2 + 1) * 64 + lane];
             O = mma3(mh[kb], ml[kb], dh2, dl2, O);
           }
-          // lane (column 4 q + r, rows 4 g4 ..) -> quad transpose -> row 4 g4 + r, columns 4 q .. 4 q + 3
+          // lane (column 4 q + r, rows 4 g4 ..) -> quad transpose -> row 4 g4 + r, columns 4 q .. 4 q + 3,
+          // into this wave's LDS rows (16-byte quad j of row r at slot j ^ (r & 7))
           const float4 y = quad_transpose(float4{O[0], O[1], O[2], O[3]}, qr);
-          const uint32_t e = (uint32_t)((16 * rw + 4 * g4 + qr) * H) * V +
-                             (uint32_t)(vs * COLS + 16 * sw + 4 * ((lane & 15) >> 2));  // rows past L dropped
+          const int r = 4 * g4 + qr, cb = (16 * sw + 4 * ((lane & 15) >> 2)) * (int)sizeof(TO);
+          unsigned char* dst = sOw + r * ROWB + (((cb >> 4) ^ (r & 7)) << 4) + (cb & 15);
           if constexpr (sizeof(TO) == 2) {
-            __builtin_amdgcn_raw_buffer_store_b64(
-                u32x2{(uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16), (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16)},
-                ro, e * 2, 0, 0);
+            *reinterpret_cast<u32x2*>(dst) =
+                u32x2{(uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16), (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16)};
           } else {
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, e * 4, 0, 0);
+            *reinterpret_cast<float4*>(dst) = y;
           }
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int hh = 0; hh < 16 / RPI; ++hh) {  // RPI whole rows of COLS columns per store
+          const int rr = lane / QPR + RPI * hh, qd = lane % QPR;
+          const u32x4 x = *reinterpret_cast<const u32x4*>(sOw + rr * ROWB + ((qd ^ (rr & 7)) << 4));
+          const uint32_t eb =
+              ((uint32_t)((16 * rw + rr) * H) * V + (uint32_t)(vs * COLS)) * (uint32_t)sizeof(TO) + 16 * qd;
+          __builtin_amdgcn_raw_buffer_store_b128(x, ro, eb, 0, 0);  // rows past L dropped
         }
         __syncthreads();  // end of phase 2: the fragments may be overwritten
       }
